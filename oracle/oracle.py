@@ -1,0 +1,347 @@
+"""ctypes binding of the oracle (oracle/_build/liboracle.so) and of the reference compiled from its
+own sources (oracle/_ref/libsardyne_ref.so). TEST INFRASTRUCTURE ONLY: imported by tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg, always as the checker or the CPU
+baseline, never by the product package.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+ORACLE_LIB = HERE / "_build" / "liboracle.so"
+REF_LIB = HERE / "_ref" / "libsardyne_ref.so"
+
+F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q6_K, Q8_K, BF16 = 0, 1, 2, 6, 8, 12, 14, 15, 30
+QK = {F32: 1, F16: 1, BF16: 1, Q8_0: 32, Q4_0: 32, Q5_0: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256}
+BLOCK_BYTES = {F32: 4, F16: 2, BF16: 2, Q8_0: 34, Q4_0: 18, Q5_0: 22, Q4_K: 144, Q6_K: 210, Q8_K: 292}
+VEC_DOT = {Q8_0: Q8_0, Q4_0: Q8_0, Q5_0: Q8_0, Q4_K: Q8_K, Q6_K: Q8_K}
+NAMES = {"F32": F32, "F16": F16, "BF16": BF16, "Q8_0": Q8_0, "Q4_0": Q4_0, "Q5_0": Q5_0, "Q4_K": Q4_K,
+         "Q6_K": Q6_K, "Q8_K": Q8_K}
+
+_vp, _i32, _f = ctypes.c_void_p, ctypes.c_int32, ctypes.c_float
+
+
+class Info(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("n_vocab", "dim", "n_layer", "n_head", "n_kv_head", "head_dim",
+                                                "ffn_dim", "max_pos")] + \
+               [("norm_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)] + \
+               [(n, ctypes.c_int32) for n in ("rope_interleaved", "qkv_bias", "tied_embeddings", "qk_norm",
+                                                "n_expert", "n_expert_used", "ffn_exp_dim")]
+
+
+class Tensor(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("type", ctypes.c_int32)]
+
+
+class Layer(ctypes.Structure):
+    _fields_ = [(n, Tensor) for n in ("attn_norm", "ffn_norm", "bq", "bk", "bv", "q_norm", "k_norm", "wq", "wk",
+                                       "wv", "wo", "gate", "up", "down", "gate_inp")]
+
+
+_SIG = {
+    "orc_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+    "orc_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+    "orc_f16_to_f32_n": (None, [_vp, _vp, ctypes.c_size_t]),
+    "orc_row_size": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
+    "orc_row_to_f32": (None, [_vp, ctypes.c_int, _vp, ctypes.c_size_t]),
+    "orc_quantize_rows": (None, [ctypes.c_int, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "orc_dot_scalar": (ctypes.c_float, [ctypes.c_int, _vp, _vp, ctypes.c_int]),
+    "orc_dot_avx2": (ctypes.c_float, [ctypes.c_int, _vp, _vp, ctypes.c_int]),
+    "orc_matmul_q_rows": (None, [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                 ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "orc_matmul_rows": (None, [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                               ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "orc_dot_f32": (ctypes.c_float, [_vp, _vp, ctypes.c_int, ctypes.c_int]),
+    "orc_axpy": (None, [_vp, ctypes.c_float, _vp, ctypes.c_int, ctypes.c_int]),
+    "orc_rmsnorm": (None, [_vp, _vp, _vp, ctypes.c_int, ctypes.c_float]),
+    "orc_softmax": (None, [_vp, ctypes.c_int]),
+    "orc_silu_mul": (None, [_vp, _vp, ctypes.c_int]),
+    "orc_rope_table": (None, [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_float]),
+    "orc_rope": (None, [_vp, ctypes.c_int, ctypes.c_int, _vp, _vp, ctypes.c_int]),
+    "orc_attention": (None, [_vp, _vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                             ctypes.c_int, _vp, ctypes.c_int]),
+    "orc_model_new": (_vp, [ctypes.POINTER(Info), Tensor, Tensor, Tensor, ctypes.POINTER(Layer)]),
+    "orc_model_free": (None, [_vp]),
+    "orc_ctx_new": (_vp, [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "orc_ctx_free": (None, [_vp]),
+    "orc_eval": (ctypes.c_int, [_vp, _vp, ctypes.c_int]),
+    "orc_logits": (ctypes.POINTER(ctypes.c_float), [_vp]),
+    "orc_n_logits": (ctypes.c_int, [_vp]),
+    "orc_n_past": (ctypes.c_int, [_vp]),
+    "orc_reset": (None, [_vp]),
+    "orc_truncate": (ctypes.c_int, [_vp, ctypes.c_int]),
+    "orc_last_topk": (ctypes.POINTER(ctypes.c_int32), [_vp]),
+}
+
+_lib = None
+
+
+def available() -> bool:
+    return ORACLE_LIB.exists()
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not ORACLE_LIB.exists():
+            raise OSError(f"{ORACLE_LIB} missing: run `make -C oracle`")
+        h = ctypes.CDLL(str(ORACLE_LIB))
+        for name, (res, args) in _SIG.items():
+            fn = getattr(h, name)
+            fn.restype, fn.argtypes = res, args
+        _lib = h
+    return _lib
+
+
+def ref_available() -> bool:
+    return REF_LIB.exists()
+
+
+_ref = None
+
+
+def ref_lib():
+    """The reference's own op_* / engine_* entry points (same signatures as the product ABI)."""
+    global _ref
+    if _ref is None:
+        if not REF_LIB.exists():
+            raise OSError(f"{REF_LIB} missing: run `make -C oracle ref` where the reference sources exist")
+        h = ctypes.CDLL(str(REF_LIB))
+        sig = {
+            "op_set_simd": (ctypes.c_int, [ctypes.c_int]),
+            "op_row_to_f32": (None, [_vp, ctypes.c_int, _vp, ctypes.c_size_t]),
+            "op_quantize_rows": (None, [ctypes.c_int, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+            "op_matmul_q_rows": (None, [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int]),
+            "op_vec_dot_q": (ctypes.c_float, [ctypes.c_int, _vp, _vp, ctypes.c_int]),
+            "op_matmul_rows": (None, [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int]),
+            "op_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+            "op_f16_to_f32_n": (None, [_vp, _vp, ctypes.c_size_t]),
+            "op_rmsnorm": (None, [_vp, _vp, _vp, ctypes.c_int, ctypes.c_float]),
+            "op_softmax": (None, [_vp, ctypes.c_int]),
+            "op_silu_mul": (None, [_vp, _vp, ctypes.c_int]),
+            "op_rope_table": (None, [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_float]),
+            "op_rope": (None, [_vp, ctypes.c_int, ctypes.c_int, _vp, _vp, ctypes.c_int]),
+            "op_attention": (None, [_vp, _vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int, _vp]),
+            "op_dot_f32": (ctypes.c_float, [_vp, _vp, ctypes.c_int]),
+            "op_axpy": (None, [_vp, ctypes.c_float, _vp, ctypes.c_int]),
+            "engine_model_load": (_vp, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
+            "engine_model_free": (None, [_vp]),
+            "engine_ctx_new": (_vp, [_vp, _i32, _i32, _i32, _i32, ctypes.c_char_p, ctypes.c_size_t]),
+            "engine_ctx_free": (None, [_vp]),
+            "engine_eval": (ctypes.c_int, [_vp, ctypes.POINTER(_i32), _i32]),
+            "engine_logits": (ctypes.POINTER(ctypes.c_float), [_vp]),
+            "engine_n_logits": (_i32, [_vp]),
+            "engine_last_error": (ctypes.c_char_p, [_vp]),
+            "engine_reset": (None, [_vp]),
+            "engine_ctx_n_threads": (_i32, [_vp]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(h, name)
+            fn.restype, fn.argtypes = res, args
+        _ref = h
+    return _ref
+
+
+def ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+# ---------------------------------------------------------------- kernel helpers
+
+def row_size(t: int, n: int) -> int:
+    return n // QK[t] * BLOCK_BYTES[t]
+
+
+def dequant(raw: np.ndarray, t: int, n: int, use_ref=False) -> np.ndarray:
+    raw = np.ascontiguousarray(raw).view(np.uint8)
+    out = np.empty(n, np.float32)
+    if use_ref:
+        ref_lib().op_row_to_f32(ptr(raw), t, ptr(out), n)
+    else:
+        lib().orc_row_to_f32(ptr(raw), t, ptr(out), n)
+    return out
+
+
+def quantize(x: np.ndarray, vt: int, use_ref=False) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    x2 = x.reshape(-1, x.shape[-1])
+    n_tok, n_in = x2.shape
+    out = np.zeros(row_size(vt, n_in) * n_tok, np.uint8)
+    if use_ref:
+        ref_lib().op_quantize_rows(vt, ptr(x2), ptr(out), n_in, 0, n_tok)
+    else:
+        lib().orc_quantize_rows(vt, ptr(x2), ptr(out), n_in, 0, n_tok)
+    return out.reshape(n_tok, -1)
+
+
+def matmul_q(w: np.ndarray, wt: int, xq: np.ndarray, n_in: int, simd: int = 1, use_ref=False) -> np.ndarray:
+    """out[t][j] = row j of w (raw blocks) · quantized activation row t."""
+    w = np.ascontiguousarray(w).view(np.uint8)
+    xq = np.ascontiguousarray(xq).view(np.uint8)
+    n_out = w.size // row_size(wt, n_in)
+    n_tok = xq.size // row_size(VEC_DOT[wt], n_in)
+    out = np.empty((n_tok, n_out), np.float32)
+    if use_ref:
+        r = ref_lib()
+        r.op_set_simd(simd)
+        r.op_matmul_q_rows(ptr(out), ptr(xq), ptr(w), wt, n_tok, n_in, n_out, 0, n_out)
+        r.op_set_simd(1)
+    else:
+        lib().orc_matmul_q_rows(ptr(out), ptr(xq), ptr(w), wt, n_tok, n_in, n_out, 0, n_out, simd)
+    return out
+
+
+# ---------------------------------------------------------------- model forward
+
+def gguf_model(path, lib_=None):
+    """Build an oracle model from a GGUF file (tensor bytes read through a memory map).
+    Returns (handle, keepalive) — keep ``keepalive`` referenced while the model is used."""
+    from sardyne_amd.gguf_synth import read_tensors
+    meta, tensors, data_off, _ = read_tensors(path)
+    mm = np.memmap(path, np.uint8, mode="r")
+    base = mm.ctypes.data + data_off
+    arch = meta["general.architecture"]
+    g = lambda k, d=None: meta.get(f"{arch}.{k}", d)
+
+    def T(name):
+        if name not in tensors:
+            return Tensor(None, 0)
+        ne, tid, off = tensors[name]
+        return Tensor(base + off, tid)
+
+    info = Info()
+    emb_ne = tensors["token_embd.weight"][0]
+    info.n_vocab, info.dim, info.n_layer = emb_ne[1], g("embedding_length"), g("block_count")
+    info.n_head = g("attention.head_count")
+    info.n_kv_head = g("attention.head_count_kv", info.n_head)
+    info.head_dim = g("attention.key_length", info.dim // info.n_head)
+    info.ffn_dim = g("feed_forward_length")
+    info.max_pos = g("context_length", 2048)
+    info.norm_eps = g("attention.layer_norm_rms_epsilon")
+    info.rope_theta = g("rope.freq_base", 10000.0)
+    info.rope_interleaved = 1 if arch == "llama" else 0
+    info.qkv_bias = 1 if "blk.0.attn_q.bias" in tensors else 0
+    info.tied_embeddings = 0 if "output.weight" in tensors else 1
+    info.qk_norm = 1 if "blk.0.attn_q_norm.weight" in tensors else 0
+    if arch == "qwen3moe":
+        info.n_expert = g("expert_count")
+        info.n_expert_used = g("expert_used_count")
+        info.ffn_exp_dim = g("expert_feed_forward_length", info.ffn_dim // info.n_expert_used)
+    layers = (Layer * info.n_layer)()
+    for l in range(info.n_layer):
+        p = f"blk.{l}."
+        L = layers[l]
+        L.attn_norm, L.ffn_norm = T(p + "attn_norm.weight"), T(p + "ffn_norm.weight")
+        L.bq, L.bk, L.bv = T(p + "attn_q.bias"), T(p + "attn_k.bias"), T(p + "attn_v.bias")
+        L.q_norm, L.k_norm = T(p + "attn_q_norm.weight"), T(p + "attn_k_norm.weight")
+        L.wq, L.wk, L.wv, L.wo = T(p + "attn_q.weight"), T(p + "attn_k.weight"), T(p + "attn_v.weight"), \
+            T(p + "attn_output.weight")
+        if info.n_expert:
+            L.gate, L.up, L.down = T(p + "ffn_gate_exps.weight"), T(p + "ffn_up_exps.weight"), \
+                T(p + "ffn_down_exps.weight")
+            L.gate_inp = T(p + "ffn_gate_inp.weight")
+        else:
+            L.gate, L.up, L.down = T(p + "ffn_gate.weight"), T(p + "ffn_up.weight"), T(p + "ffn_down.weight")
+    lb = lib_ or lib()
+    h = lb.orc_model_new(ctypes.byref(info), T("token_embd.weight"), T("output_norm.weight"),
+                         T("output.weight"), layers)
+    return h, (mm, layers, info)
+
+
+class OracleContext:
+    """Oracle counterpart of the engine context: eval() returns logits like the reference runtime."""
+
+    def __init__(self, path, max_seq, n_batch=64, logits_all=False, simd=1):
+        self.lib = lib()
+        self.model, self._keep = gguf_model(path)
+        self.info = self._keep[2]
+        self.h = self.lib.orc_ctx_new(self.model, max_seq, n_batch, int(logits_all), simd)
+        if not self.h:
+            raise ValueError("oracle context rejected")
+        self.logits_all = logits_all
+        self.n_batch = n_batch
+
+    def eval(self, tokens):
+        toks = np.ascontiguousarray(np.asarray(tokens, np.int32).reshape(-1))
+        step = self.n_batch if self.logits_all else toks.size
+        outs = []
+        for i in range(0, toks.size, step):
+            part = np.ascontiguousarray(toks[i:i + step])
+            if self.lib.orc_eval(self.h, ptr(part), part.size) != 0:
+                raise ValueError("oracle eval rejected")
+            n = self.lib.orc_n_logits(self.h)
+            outs.append(np.ctypeslib.as_array(self.lib.orc_logits(self.h), shape=(n, self.info.n_vocab)).copy())
+        out = np.concatenate(outs)
+        return out if self.logits_all else out[-1]
+
+    def last_topk(self, n_tok):
+        k = self.info.n_expert_used
+        a = np.ctypeslib.as_array(self.lib.orc_last_topk(self.h), shape=(self.info.n_layer * n_tok * k,))
+        return a.reshape(self.info.n_layer, n_tok, k).copy()
+
+    @property
+    def n_past(self):
+        return self.lib.orc_n_past(self.h)
+
+    def reset(self):
+        self.lib.orc_reset(self.h)
+
+    def __del__(self):
+        try:
+            if self.h:
+                self.lib.orc_ctx_free(self.h)
+                self.h = None
+            if self.model:
+                self.lib.orc_model_free(self.model)
+                self.model = None
+        except Exception:
+            pass
+
+
+class RefEngine:
+    """The reference engine compiled from its sources (oracle/_ref): same eval() interface."""
+
+    def __init__(self, path, max_seq, n_batch=64, logits_all=False, n_threads=0):
+        self.lib = ref_lib()
+        err = ctypes.create_string_buffer(512)
+        self.model = self.lib.engine_model_load(str(path).encode(), err, len(err))
+        if not self.model:
+            raise ValueError(err.value.decode())
+        self.h = self.lib.engine_ctx_new(self.model, max_seq, n_batch, int(logits_all), n_threads, err, len(err))
+        if not self.h:
+            raise ValueError(err.value.decode())
+        from sardyne_amd.gguf_synth import read_tensors
+        self.n_vocab = read_tensors(path)[1]["token_embd.weight"][0][1]
+        self.logits_all, self.n_batch = logits_all, n_batch
+        self.n_threads = self.lib.engine_ctx_n_threads(self.h)
+
+    def eval(self, tokens):
+        toks = np.ascontiguousarray(np.asarray(tokens, np.int32).reshape(-1))
+        step = self.n_batch if self.logits_all else toks.size
+        outs = []
+        for i in range(0, toks.size, step):
+            part = np.ascontiguousarray(toks[i:i + step])
+            if self.lib.engine_eval(self.h, part.ctypes.data_as(ctypes.POINTER(_i32)), part.size) != 0:
+                raise ValueError(self.lib.engine_last_error(self.h).decode())
+            n = self.lib.engine_n_logits(self.h)
+            outs.append(np.ctypeslib.as_array(self.lib.engine_logits(self.h), shape=(n, self.n_vocab)).copy())
+        out = np.concatenate(outs)
+        return out if self.logits_all else out[-1]
+
+    def reset(self):
+        self.lib.engine_reset(self.h)
+
+    def __del__(self):
+        try:
+            self.lib.engine_ctx_free(self.h)
+            self.lib.engine_model_free(self.model)
+        except Exception:
+            pass
