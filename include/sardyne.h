@@ -1,0 +1,157 @@
+/* Public C ABI of libsardyne.so (MI355X build).
+ *
+ * The declarations below are the drop-in boundary: the same symbols, signatures, struct layouts,
+ * ownership and error conventions as the reference's libsardyne.so, so that its ctypes layer
+ * (sardyne/capi.py:33-102) binds this library unchanged. Each group cites the reference
+ * declaration it replaces. Computation behind engine_* and op_* runs on the GPU (gfx950); there is
+ * no CPU compute path in this library.
+ */
+#ifndef SARDYNE_H
+#define SARDYNE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ engine (csrc/engine.h:17-72) */
+
+typedef struct engine_model engine_model;
+typedef struct engine_ctx engine_ctx;
+
+/* Field order and types of csrc/engine.h:24-40 (mirrored by sardyne/capi.py:55-60). */
+typedef struct {
+    int32_t n_vocab;
+    int32_t dim;
+    int32_t n_layer;
+    int32_t n_head;
+    int32_t n_kv_head;
+    int32_t head_dim;
+    int32_t ffn_dim;
+    int32_t max_pos;
+    float norm_eps;
+    float rope_theta;
+    int32_t rope_interleaved; /* 1: pairs (2i, 2i+1) ("llama"); 0: pairs (i, i + head_dim/2) (qwen2/qwen3) */
+    int32_t qkv_bias;
+    int32_t tied_embeddings;
+    int32_t qk_norm;
+    int32_t n_expert, n_expert_used, ffn_exp_dim;
+} engine_model_info;
+
+/* csrc/engine.h:44-45 */
+const char *engine_version(void);
+void engine_add_f32(const float *a, const float *b, float *out, size_t n);
+
+/* csrc/engine.h:49-51. Loads a llama / qwen2 / qwen3 / qwen3moe GGUF and uploads every weight to
+ * device memory (all experts resident). NULL on error, with the reason in err. */
+engine_model *engine_model_load(const char *path, char *err, size_t err_len);
+void engine_model_free(engine_model *m);
+void engine_model_get_info(const engine_model *m, engine_model_info *out);
+
+/* csrc/engine.h:57-60. n_threads is validated (0..256) and reported back; results never depend on
+ * it. The KV cache and activations live in device memory. */
+engine_ctx *engine_ctx_new(const engine_model *m, int32_t max_seq, int32_t n_batch, int32_t logits_all,
+                           int32_t n_threads, char *err, size_t err_len);
+int32_t engine_ctx_n_threads(const engine_ctx *c);
+void engine_ctx_free(engine_ctx *c);
+
+/* csrc/engine.h:65-72. engine_eval returns 0, or -1 with the reason in engine_last_error and the
+ * context unchanged. engine_logits points into host memory owned by the context, valid until the
+ * next call. */
+int engine_eval(engine_ctx *c, const int32_t *tokens, int32_t n);
+const float *engine_logits(const engine_ctx *c);
+int32_t engine_n_logits(const engine_ctx *c);
+int32_t engine_n_past(const engine_ctx *c);
+void engine_reset(engine_ctx *c);
+int engine_truncate(engine_ctx *c, int32_t n);
+const char *engine_last_error(const engine_ctx *c);
+
+/* ------------------------------------------------------------------ GGUF (csrc/gguf.h:22-84) */
+
+enum gguf_value_type {
+    GGUF_TYPE_UINT8 = 0, GGUF_TYPE_INT8 = 1, GGUF_TYPE_UINT16 = 2, GGUF_TYPE_INT16 = 3, GGUF_TYPE_UINT32 = 4,
+    GGUF_TYPE_INT32 = 5, GGUF_TYPE_FLOAT32 = 6, GGUF_TYPE_BOOL = 7, GGUF_TYPE_STRING = 8, GGUF_TYPE_ARRAY = 9,
+    GGUF_TYPE_UINT64 = 10, GGUF_TYPE_INT64 = 11, GGUF_TYPE_FLOAT64 = 12,
+};
+#define GGUF_MAX_DIMS 4
+
+/* csrc/gguf.h:40-48 (sardyne/capi.py:22-25) */
+typedef struct {
+    const char *name;
+    uint32_t n_dims;
+    uint32_t type;
+    uint64_t ne[GGUF_MAX_DIMS];
+    uint64_t offset;
+    uint64_t nbytes;
+    const void *data;
+} gguf_tensor;
+
+/* csrc/gguf.h:50-57 (sardyne/capi.py:28-30) */
+typedef struct {
+    const char *key;
+    uint32_t type;
+    uint32_t arr_type;
+    uint64_t n;
+    const uint8_t *ptr;
+    uint64_t *str_pos;
+} gguf_kv;
+
+typedef struct gguf_file gguf_file;
+
+gguf_file *gguf_open(const char *path, char *err, size_t err_len);
+void gguf_close(gguf_file *f);
+void gguf_prefetch(const void *p, size_t n);
+uint32_t gguf_version(const gguf_file *f);
+uint32_t gguf_alignment(const gguf_file *f);
+uint64_t gguf_data_offset(const gguf_file *f);
+uint64_t gguf_n_kv(const gguf_file *f);
+uint64_t gguf_n_tensors(const gguf_file *f);
+const gguf_kv *gguf_get_kv(const gguf_file *f, uint64_t i);
+int64_t gguf_find_kv(const gguf_file *f, const char *key);
+const gguf_tensor *gguf_get_tensor(const gguf_file *f, uint64_t i);
+int64_t gguf_find_tensor(const gguf_file *f, const char *name);
+int gguf_kv_get_u64(const gguf_file *f, int64_t i, uint64_t *out);
+int gguf_kv_get_f64(const gguf_file *f, int64_t i, double *out);
+const char *gguf_kv_get_str(const gguf_file *f, int64_t i, uint64_t *len);
+const char *gguf_kv_get_arr_str(const gguf_file *f, int64_t i, uint64_t j, uint64_t *len);
+const char *gguf_type_name(uint32_t ggml_type);
+
+/* ------------------------------------------------------------------ kernels (csrc/ops.h:21-74)
+ * Host-pointer entry points used by kernel-level tests. Each call copies its operands to the GPU,
+ * runs the gfx950 kernel and copies the result back. */
+
+enum { OP_F32 = 0, OP_F16 = 1, OP_Q4_0 = 2, OP_Q5_0 = 6, OP_Q8_0 = 8, OP_Q4_K = 12, OP_Q6_K = 14,
+       OP_Q8_K = 15, OP_BF16 = 30 };
+
+/* csrc/ops.h:25-26. The reference selects scalar or AVX2 CPU kernels. Here op_set_simd records the
+ * request and op_simd reports it (1 by default); the GPU kernels are the same either way, and
+ * their Q4_K/Q6_K results equal both of the reference's kernel sets, which agree bit for bit. */
+int op_simd(void);
+int op_set_simd(int enable);
+void op_f16_to_f32_n(const uint16_t *x, float *out, size_t n);                     /* csrc/ops.h:36 */
+void op_matmul_rows(float *out, const float *x, const void *w, int wtype, int n_tok, int n_in, int n_out,
+                    int row0, int row1);                                          /* csrc/ops.h:42-43 */
+float op_dot_f32(const float *a, const float *b, int n);                          /* csrc/ops.h:55 */
+uint16_t op_f32_to_f16(float f);                                                  /* csrc/ops.h:35 */
+void op_row_to_f32(const void *row, int type, float *out, size_t n);              /* csrc/ops.h:37 */
+size_t op_row_size(int type, int n);                                              /* csrc/ops.h:30 */
+void op_quantize_rows(int vtype, const float *x, void *xq, int n_in, int t0, int t1); /* csrc/ops.h:49 */
+void op_matmul_q_rows(float *out, const void *xq, const void *w, int wtype, int n_tok, int n_in, int n_out,
+                      int row0, int row1);                                        /* csrc/ops.h:50-51 */
+float op_vec_dot_q(int wtype, const void *w, const void *xq, int n);             /* csrc/ops.h:52 */
+void op_axpy(float *y, float a, const float *x, int n);                           /* csrc/ops.h:56 */
+void op_matmul(float *out, const float *x, const void *w, int wtype, int n_tok, int n_in, int n_out); /* :45 */
+void op_rmsnorm(float *out, const float *x, const float *w, int n, float eps);    /* csrc/ops.h:58 */
+void op_softmax(float *x, int n);                                                 /* csrc/ops.h:59 */
+void op_silu_mul(float *gate, const float *up, int n);                            /* csrc/ops.h:60 */
+void op_rope_table(float *cos_out, float *sin_out, int n_pos, int head_dim, float theta); /* csrc/ops.h:63 */
+void op_rope(float *x, int n_heads, int head_dim, const float *cos, const float *sin, int interleaved); /* :66 */
+void op_attention(float *out, const float *q, const float *k_cache, const float *v_cache, int n_head,
+                  int n_kv_head, int head_dim, int n_kv, int stride, float *scores); /* csrc/ops.h:73-74 */
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,214 @@
+/* Device forward pass: the layer sequence of the reference forward (csrc/model_llama.c:757-832)
+ * issued as gfx950 kernels on the context's stream.
+ *
+ *   embedding rows (dequant gather) -> per layer: RMSNorm -> Q/K/V matvec (+bias) -> q/k norm,
+ *   RoPE, KV-cache write -> GQA attention -> O matvec + residual -> RMSNorm -> gate/up matvec ->
+ *   SiLU·mul -> down matvec + residual (or the MoE block) -> final RMSNorm -> output matvec.
+ *
+ * Quantized matrices read activations quantized once per input (Q8_K for K-quants, Q8_0 for the
+ * 32-element types), as csrc/model_llama.c:592-611 does.
+ */
+#define _POSIX_C_SOURCE 200809L
+#include <stdlib.h>
+#include <string.h>
+
+#include "sdy_engine.h"
+#include "sdy_ops.h"
+#include "sdy_shim.h"
+
+#define TRY(call)             \
+    do {                      \
+        int rc_ = (call);     \
+        if (rc_) return rc_;  \
+    } while (0)
+
+static int vec_dot_type(int wtype) {
+    if (wtype == SDY_Q8_0 || wtype == SDY_Q4_0 || wtype == SDY_Q5_0) return SDY_Q8_0;
+    if (wtype == SDY_Q4_K || wtype == SDY_Q6_K) return SDY_Q8_K;
+    return SDY_F32;
+}
+
+
+static int dalloc(void **p, size_t n) { return sdy_malloc(p, n ? n : 64); }
+
+int sdy_engine_alloc(engine_ctx *c) {
+    const engine_model_info *in = &c->m->info;
+    size_t B = (size_t)c->n_batch, S = (size_t)c->max_seq, hd = (size_t)in->head_dim;
+    size_t q_dim = (size_t)in->n_head * hd, kv_dim = (size_t)in->n_kv_head * hd;
+    size_t kv = (size_t)in->n_layer * in->n_kv_head * S * hd;
+    size_t ffn = (size_t)(in->n_expert ? in->ffn_exp_dim : in->ffn_dim);
+    size_t max_in = (size_t)in->dim > q_dim ? (size_t)in->dim : q_dim;
+    if (ffn > max_in) max_in = ffn;
+    size_t logit_rows = c->logits_all ? B : 1;
+    TRY(dalloc((void **)&c->k_cache, kv * 4));
+    TRY(dalloc((void **)&c->v_cache, kv * 4));
+    TRY(dalloc((void **)&c->rope_cos, S * hd / 2 * 4));
+    TRY(dalloc((void **)&c->rope_sin, S * hd / 2 * 4));
+    TRY(dalloc((void **)&c->x, B * in->dim * 4));
+    TRY(dalloc((void **)&c->xb, B * in->dim * 4));
+    TRY(dalloc((void **)&c->q, B * q_dim * 4));
+    TRY(dalloc((void **)&c->k, B * kv_dim * 4));
+    TRY(dalloc((void **)&c->v, B * kv_dim * 4));
+    TRY(dalloc((void **)&c->att, B * q_dim * 4));
+    TRY(dalloc((void **)&c->hb, B * ffn * 4));
+    TRY(dalloc((void **)&c->hb2, B * ffn * 4));
+    TRY(dalloc((void **)&c->logits_dev, logit_rows * in->n_vocab * 4));
+    TRY(dalloc((void **)&c->part, sdy_attn_part_floats((int)B, in->n_head, in->head_dim, (int)S) * 4));
+    TRY(dalloc(&c->xq[0], B * ((max_in + 31) / 32 * 34)));
+    TRY(dalloc(&c->xq[1], B * ((max_in + 255) / 256 * 292)));
+    TRY(dalloc((void **)&c->tok_dev, B * 4));
+    TRY(sdy_host_alloc((void **)&c->tok_host, B * 4));
+    if (in->n_expert) {
+        size_t chosen = B * in->n_expert_used;
+        TRY(dalloc((void **)&c->moe_probs, B * in->n_expert * 4));
+        TRY(dalloc((void **)&c->moe_w, chosen * 4));
+        TRY(dalloc((void **)&c->moe_top, chosen * 4));
+        TRY(dalloc((void **)&c->moe_x, B * in->dim * 4));
+        TRY(dalloc((void **)&c->moe_y, B * in->dim * 4));
+        TRY(dalloc((void **)&c->moe_sum, B * in->dim * 4));
+        TRY(dalloc((void **)&c->moe_gidx, chosen * 4));
+        TRY(dalloc((void **)&c->moe_gw, chosen * 4));
+        TRY(sdy_host_alloc((void **)&c->moe_top_host, chosen * 4));
+        TRY(sdy_host_alloc((void **)&c->moe_w_host, chosen * 4));
+        TRY(sdy_host_alloc((void **)&c->moe_gidx_host, chosen * 4));
+        TRY(sdy_host_alloc((void **)&c->moe_gw_host, chosen * 4));
+    }
+    TRY(sdy_rope_table(c->rope_cos, c->rope_sin, c->max_seq, in->head_dim, in->rope_theta, c->st));
+    TRY(sdy_memset(c->k_cache, 0, kv * 4, c->st));
+    TRY(sdy_memset(c->v_cache, 0, kv * 4, c->st));
+    return sdy_sync(c->st);
+}
+
+void sdy_engine_release(engine_ctx *c) {
+    void *dev[] = {c->k_cache, c->v_cache, c->rope_cos, c->rope_sin, c->x, c->xb, c->q, c->k, c->v, c->att, c->hb,
+                   c->hb2, c->logits_dev, c->part, c->xq[0], c->xq[1], c->tok_dev, c->moe_probs, c->moe_w,
+                   c->moe_top, c->moe_x, c->moe_y, c->moe_sum, c->moe_gidx, c->moe_gw};
+    for (size_t i = 0; i < sizeof dev / sizeof *dev; i++) sdy_free(dev[i]);
+    void *host[] = {c->tok_host, c->moe_top_host, c->moe_w_host, c->moe_gidx_host, c->moe_gw_host};
+    for (size_t i = 0; i < sizeof host / sizeof *host; i++) sdy_host_free(host[i]);
+}
+
+/* out[t][row] = W . x[t] for n_tok rows of x; new_input = 1 when x changed since the last call
+ * (the quantized copy of x is then rebuilt), as matmul() in csrc/model_llama.c:592-611. */
+static int mm(engine_ctx *c, float *out, const float *x, const dmat *w, int n_tok, const float *bias,
+              const float *resid, int new_input) {
+    if (new_input) c->xq_src[0] = c->xq_src[1] = NULL;
+    sdy_mv_args a;
+    memset(&a, 0, sizeof a);
+    a.n_tok = n_tok;
+    a.out = out;
+    a.out_stride = w->n_out;
+    a.bias = bias;
+    a.resid = resid;
+    a.row0 = 0;
+    a.row1 = w->n_out;
+    int vt = vec_dot_type(w->type);
+    if (vt == SDY_F32) {
+        a.x = x;
+    } else {
+        int s = vt == SDY_Q8_0 ? 0 : 1;
+        if (c->xq_src[s] != x || c->xq_n_tok[s] != n_tok || c->xq_n_in[s] != w->n_in) {
+            TRY(sdy_quantize(vt, x, c->xq[s], w->n_in, n_tok, c->st));
+            c->xq_src[s] = x;
+            c->xq_n_tok[s] = n_tok;
+            c->xq_n_in[s] = w->n_in;
+        }
+        a.xq = c->xq[s];
+    }
+    return sdy_matvec(&w->m, &a, c->st);
+}
+
+/* One expert's slice of a stacked [n_expert][n_out][n_in] tensor. */
+static dmat expert(const dmat *w, int e) {
+    dmat d = *w;
+    d.m = sdy_mat_rows(&w->m, (long)e * w->n_out, w->n_out);
+    return d;
+}
+
+int sdy_gather_rows(const float *src, const int32_t *idx, int n, int dim, float *dst, sdy_stream s);
+int sdy_scatter_axpy(float *dst, const int32_t *idx, const float *w, const float *src, int n, int dim, sdy_stream s);
+
+/* moe_ffn (csrc/model_llama.c:724-751): router, top-k on the device; the (token, slot) pairs are
+ * grouped by expert on the host after one small copy, then each chosen expert runs gate/up/down
+ * over its tokens and the weighted outputs are accumulated per token in ascending expert order. */
+static int moe(engine_ctx *c, const dlayer *L, int n) {
+    const engine_model_info *in = &c->m->info;
+    const int dim = in->dim, fe = in->ffn_exp_dim, ne = in->n_expert, k = in->n_expert_used, total = n * k;
+    TRY(mm(c, c->moe_probs, c->xb, &L->gate_inp, n, NULL, NULL, 1));
+    TRY(sdy_moe_route(c->moe_probs, n, ne, k, c->moe_top, c->moe_w, c->st));
+    TRY(sdy_d2h(c->moe_top_host, c->moe_top, (size_t)total * 4, c->st));
+    TRY(sdy_d2h(c->moe_w_host, c->moe_w, (size_t)total * 4, c->st));
+    TRY(sdy_memset(c->moe_sum, 0, (size_t)n * dim * 4, c->st));
+    TRY(sdy_sync(c->st));
+    int *count = calloc((size_t)ne + 1, sizeof(int));
+    if (!count) return -1;
+    for (int i = 0; i < total; i++) count[c->moe_top_host[i] + 1]++;
+    for (int e = 0; e < ne; e++) count[e + 1] += count[e];
+    for (int i = 0; i < total; i++) {
+        int slot = count[c->moe_top_host[i]]++;
+        c->moe_gidx_host[slot] = i / k;
+        c->moe_gw_host[slot] = c->moe_w_host[i];
+    }
+    memmove(count + 1, count, (size_t)ne * sizeof(int));
+    count[0] = 0;
+    int rc = sdy_h2d(c->moe_gidx, c->moe_gidx_host, (size_t)total * 4, c->st);
+    if (!rc) rc = sdy_h2d(c->moe_gw, c->moe_gw_host, (size_t)total * 4, c->st);
+    for (int e = 0; e < ne && !rc; e++) {
+        int first = count[e], m = count[e + 1] - first;
+        if (!m) continue;
+        dmat g = expert(&L->gate, e), u = expert(&L->up, e), d = expert(&L->down, e);
+        if ((rc = sdy_gather_rows(c->xb, c->moe_gidx + first, m, dim, c->moe_x, c->st))) break;
+        if ((rc = mm(c, c->hb, c->moe_x, &g, m, NULL, NULL, 1))) break;
+        if ((rc = mm(c, c->hb2, c->moe_x, &u, m, NULL, NULL, 0))) break;
+        if ((rc = sdy_silu_mul(c->hb, c->hb2, (long)m * fe, c->st))) break;
+        if ((rc = mm(c, c->moe_y, c->hb, &d, m, NULL, NULL, 1))) break;
+        rc = sdy_scatter_axpy(c->moe_sum, c->moe_gidx + first, c->moe_gw + first, c->moe_y, m, dim, c->st);
+    }
+    free(count);
+    if (!rc) rc = sdy_sync(c->st); /* the pinned index buffers are reused by the next layer */
+    return rc;
+}
+
+int sdy_engine_forward(engine_ctx *c, const int32_t *tokens, int n, int out_rows) {
+    const engine_model *m = c->m;
+    const engine_model_info *in = &m->info;
+    const int dim = in->dim, hd = in->head_dim, q_dim = in->n_head * hd, kv_dim = in->n_kv_head * hd;
+    const int pos0 = c->n_past;
+    const long head_stride = (long)c->max_seq * hd, layer_stride = (long)in->n_kv_head * head_stride;
+    memcpy(c->tok_host, tokens, (size_t)n * 4);
+    TRY(sdy_h2d(c->tok_dev, c->tok_host, (size_t)n * 4, c->st));
+    TRY(sdy_dequant_gather(&m->tok_embd.m, c->tok_dev, n, c->x, c->st));
+    for (int l = 0; l < in->n_layer; l++) {
+        const dlayer *L = &m->layers[l];
+        float *kc = c->k_cache + l * layer_stride, *vc = c->v_cache + l * layer_stride;
+        TRY(sdy_rmsnorm(c->x, L->attn_norm, c->xb, dim, in->norm_eps, n, dim, dim, c->st));
+        TRY(mm(c, c->q, c->xb, &L->wq, n, L->bq, NULL, 1));
+        TRY(mm(c, c->k, c->xb, &L->wk, n, L->bk, NULL, 0));
+        TRY(mm(c, c->v, c->xb, &L->wv, n, L->bv, NULL, 0));
+        TRY(sdy_qk_rope_kv(c->q, c->k, c->v, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos, c->rope_sin, pos0, n,
+                           in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc, vc, head_stride, c->st));
+        TRY(sdy_attention(c->q, kc, vc, n, in->n_head, in->n_kv_head, hd, pos0 + 1, head_stride, q_dim, c->part,
+                          c->att, q_dim, c->st));
+        TRY(mm(c, c->x, c->att, &L->wo, n, NULL, c->x, 1));
+        TRY(sdy_rmsnorm(c->x, L->ffn_norm, c->xb, dim, in->norm_eps, n, dim, dim, c->st));
+        if (in->n_expert) {
+            TRY(moe(c, L, n));
+            TRY(sdy_add(c->x, c->moe_sum, c->x, (long)n * dim, c->st));
+        } else {
+            TRY(mm(c, c->hb, c->xb, &L->gate, n, NULL, NULL, 1));
+            TRY(mm(c, c->hb2, c->xb, &L->up, n, NULL, NULL, 0));
+            TRY(sdy_silu_mul(c->hb, c->hb2, (long)n * in->ffn_dim, c->st));
+            TRY(mm(c, c->x, c->hb, &L->down, n, NULL, c->x, 1));
+        }
+        (void)kv_dim;
+    }
+    if (out_rows > 0) {
+        const float *xs = c->x + (size_t)(n - out_rows) * dim;
+        TRY(sdy_rmsnorm(xs, m->output_norm, c->xb, dim, in->norm_eps, out_rows, dim, dim, c->st));
+        TRY(mm(c, c->logits_dev, c->xb, &m->output, out_rows, NULL, NULL, 1));
+        TRY(sdy_d2h(c->logits, c->logits_dev, (size_t)out_rows * in->n_vocab * 4, c->st));
+    }
+    TRY(sdy_sync(c->st));
+    c->n_past += n;
+    return 0;
+}

@@ -1,0 +1,928 @@
+// gfx950 kernels of the quantized-weight path: device weight layout (repack), dequantisation,
+// activation quantisers and the decode / small-batch matvec.
+//
+// Device weight layout. Every quantized matrix is split into "planes" so that each lane of a
+// wave64 reads its share of a row with one 16-byte load per plane and the 64 lanes of a load
+// instruction cover 1 KiB of contiguous HBM. The unit of work is a 64-element slice of a row
+// ("unit"; 4 units per 256-element K-quant super-block, 2 blocks per unit for the 32-element
+// types). Plane p of a matrix is [n_rows][per-row bytes] and the byte count of all planes
+// together equals the GGUF size (plus padding of odd 32-element blocks), so HBM traffic is the
+// format's own bytes:
+//
+//   Q4_K  QA: qs[32j..32j+16) of sub-block pair j (16 B/unit)   QB: qs[32j+16..32j+32) (16 B/unit)
+//         H : d, dmin, scales[12] as stored (16 B/super-block)
+//   Q6_K  N0, N1: 32 bytes/unit of low nibbles; byte i holds element i (low) and i+32 (high)
+//         HB: 16 bytes/unit; byte i holds the two high bits of elements i, i+16, i+32, i+48
+//         SC: scales[16] as stored (16 B/super-block)   D: f16 d (2 B/super-block)
+//         The six-bit values are the stored ones, only their bits are regrouped per unit.
+//   Q8_0  Q0..Q3: the 64 int8 quants of blocks 2u, 2u+1 (16 B each)   D: both f16 scales (4 B/unit)
+//   Q4_0  P0, P1: qs of blocks 2u, 2u+1   D: 4 B/unit
+//   Q5_0  P0, P1: qs   QH: qh of both blocks (8 B/unit)   D: 4 B/unit
+//
+// Numerics (the reference's csrc/quant.c:191-235 and csrc/quant.h:84-91): integer parts of a
+// super-block are exact int32 sums (v_dot4c_i32_i8 + quad reduction), and the fp32 combine
+// acc + (yd*d*isum - yd*dmin*msum) runs in super-block order with contraction disabled, so the
+// Q4_K / Q6_K matvec reproduces the reference's float result bit for bit. Q8_0/Q4_0/Q5_0 blocks
+// contribute (float)isum*(dw*dx) as the reference's scalar kernel does; two blocks of a unit are
+// summed first, then units in order (the reference's AVX2 order differs again; parity for these
+// types is by tolerance).
+#include "sdy_device.h"
+#include "sdy_shim.h"
+#include "sdy_internal.h"
+
+namespace {
+
+constexpr int WAVES = 4;  // waves per workgroup of the matvec
+constexpr int THREADS = 64 * WAVES;
+
+struct Planes {
+    const uint8_t *p[5];
+    int n_in, T, nb;  // elements per row, units per row, 32/256-element blocks per row
+};
+
+SDY_DEV uint4 ld16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+SDY_DEV uint32_t ld4(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
+
+// ------------------------------------------------------------------------------------ repack
+
+template <int WT>
+__global__ void k_repack(const uint8_t *__restrict__ src, size_t src_row, Planes P, uint8_t *const *dst,
+                         long n_rows) {
+    long gid = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    long row = gid / P.T;
+    int u = (int)(gid - row * P.T);
+    if (row >= n_rows) return;
+    const uint8_t *r = src + row * src_row;
+    if constexpr (WT == SDY_Q4_K) {
+        int s = u >> 2, j = u & 3;
+        const uint8_t *sb = r + 144 * s;
+        uint8_t *qa = dst[0] + (row * P.T + u) * 16, *qb = dst[1] + (row * P.T + u) * 16;
+        for (int i = 0; i < 16; i++) {
+            qa[i] = sb[16 + 32 * j + i];
+            qb[i] = sb[16 + 32 * j + 16 + i];
+        }
+        if (j == 0) {
+            uint8_t *h = dst[2] + (row * P.nb + s) * 16;
+            for (int i = 0; i < 16; i++) h[i] = sb[i];
+        }
+    } else if constexpr (WT == SDY_Q6_K) {
+        int s = u >> 2, j = u & 3;
+        const uint8_t *sb = r + 210 * s;
+        // six-bit value of super-block element e (csrc/quant.c:62-75)
+        auto lo4 = [&](int e) -> int {
+            int half = e >> 7, ee = e & 127, l = ee & 31, k = ee >> 5;
+            int b = sb[64 * half + l + ((k & 1) ? 32 : 0)];
+            return (k >= 2) ? (b >> 4) : (b & 15);
+        };
+        auto hi2 = [&](int e) -> int {
+            int half = e >> 7, ee = e & 127, l = ee & 31, k = ee >> 5;
+            return (sb[128 + 32 * half + l] >> (2 * k)) & 3;
+        };
+        int base = 64 * j;
+        uint8_t *n0 = dst[0] + (row * P.T + u) * 16, *n1 = dst[1] + (row * P.T + u) * 16;
+        uint8_t *hb = dst[2] + (row * P.T + u) * 16;
+        for (int i = 0; i < 32; i++) {
+            uint8_t v = (uint8_t)(lo4(base + i) | (lo4(base + i + 32) << 4));
+            if (i < 16) n0[i] = v;
+            else n1[i - 16] = v;
+        }
+        for (int i = 0; i < 16; i++) {
+            int v = 0;
+            for (int k = 0; k < 4; k++) v |= hi2(base + i + 16 * k) << (2 * k);
+            hb[i] = (uint8_t)v;
+        }
+        if (j == 0) {
+            uint8_t *sc = dst[3] + (row * P.nb + s) * 16;
+            for (int i = 0; i < 16; i++) sc[i] = sb[192 + i];
+            uint8_t *d = dst[4] + (row * P.nb + s) * 2;
+            d[0] = sb[208];
+            d[1] = sb[209];
+        }
+    } else {
+        // 32-element types: blocks 2u and 2u+1 (the second may be absent when the row has an odd
+        // number of blocks: zero quants and zero scale).
+        constexpr int BB = WT == SDY_Q8_0 ? 34 : WT == SDY_Q4_0 ? 18 : 22;
+        constexpr int QOFF = WT == SDY_Q8_0 ? 2 : WT == SDY_Q4_0 ? 2 : 6;
+        uint8_t *d = dst[4] + (row * P.T + u) * 4;
+        for (int h = 0; h < 2; h++) {
+            int b = 2 * u + h;
+            bool ok = b < P.nb;
+            const uint8_t *blk = r + (size_t)BB * (ok ? b : 0);
+            d[2 * h] = ok ? blk[0] : 0;
+            d[2 * h + 1] = ok ? blk[1] : 0;
+            if constexpr (WT == SDY_Q8_0) {
+                uint8_t *q0 = dst[2 * h] + (row * P.T + u) * 16, *q1 = dst[2 * h + 1] + (row * P.T + u) * 16;
+                for (int i = 0; i < 16; i++) {
+                    q0[i] = ok ? blk[QOFF + i] : 0;
+                    q1[i] = ok ? blk[QOFF + 16 + i] : 0;
+                }
+            } else {
+                uint8_t *q = dst[h] + (row * P.T + u) * 16;
+                for (int i = 0; i < 16; i++) q[i] = ok ? blk[QOFF + i] : 0;
+                if constexpr (WT == SDY_Q5_0) {
+                    uint8_t *qh = dst[2] + (row * P.T + u) * 8 + 4 * h;
+                    for (int i = 0; i < 4; i++) qh[i] = ok ? blk[2 + i] : 0;
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------ dequant
+
+// Six-bit scale (is_min = 0) or min (is_min = 1) of Q4_K sub-block k from the 12 scale bytes
+// (csrc/quant.h:72-80).
+SDY_DEV int q4k_scale(const uint8_t *s, int k, int is_min) {
+    if (k < 4) return s[k + 4 * is_min] & 63;
+    return is_min ? ((s[k + 4] >> 4) | ((s[k] >> 6) << 4)) : ((s[k + 4] & 15) | ((s[k - 4] >> 6) << 4));
+}
+
+template <int WT>
+__global__ void k_dequant(Planes P, const int32_t *__restrict__ idx, long r0, long n, float *__restrict__ out) {
+    long gid = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    long i = gid / P.T;
+    int u = (int)(gid - i * P.T);
+    if (i >= n) return;
+    long row = idx ? (long)idx[i] : r0 + i;
+    float *o = out + i * P.n_in + 64 * u;
+    int n_el = P.n_in - 64 * u < 64 ? P.n_in - 64 * u : 64;
+    if constexpr (WT == SDY_Q4_K) {
+        int s = u >> 2, j = u & 3;
+        uint8_t qa[16], qb[16], h[16];
+        *reinterpret_cast<uint4 *>(qa) = ld16(P.p[0] + (row * P.T + u) * 16);
+        *reinterpret_cast<uint4 *>(qb) = ld16(P.p[1] + (row * P.T + u) * 16);
+        *reinterpret_cast<uint4 *>(h) = ld16(P.p[2] + (row * P.nb + s) * 16);
+        float d = sdy_h2f((uint16_t)(h[0] | (h[1] << 8))), dmin = sdy_h2f((uint16_t)(h[2] | (h[3] << 8)));
+        for (int half = 0; half < 2; half++) {
+            int k = 2 * j + half;
+            float d1 = d * (float)q4k_scale(h + 4, k, 0);
+            float m1 = dmin * (float)q4k_scale(h + 4, k, 1);
+            for (int l = 0; l < 32; l++) {
+                int b = l < 16 ? qa[l] : qb[l - 16];
+                int q = half ? (b >> 4) : (b & 15);
+                float p = d1 * (float)q;
+                o[32 * half + l] = p - m1;
+            }
+        }
+    } else if constexpr (WT == SDY_Q6_K) {
+        int s = u >> 2, j = u & 3;
+        uint8_t nb8[32], hb[16];
+        *reinterpret_cast<uint4 *>(nb8) = ld16(P.p[0] + (row * P.T + u) * 16);
+        *reinterpret_cast<uint4 *>(nb8 + 16) = ld16(P.p[1] + (row * P.T + u) * 16);
+        *reinterpret_cast<uint4 *>(hb) = ld16(P.p[2] + (row * P.T + u) * 16);
+        const int8_t *sc = reinterpret_cast<const int8_t *>(P.p[3] + (row * P.nb + s) * 16);
+        const uint8_t *dp = P.p[4] + (row * P.nb + s) * 2;
+        float d = sdy_h2f((uint16_t)(dp[0] | (dp[1] << 8)));
+        for (int e = 0; e < 64; e++) {
+            int lo = e < 32 ? (nb8[e] & 15) : (nb8[e - 32] >> 4);
+            int hi = (hb[e & 15] >> (2 * (e >> 4))) & 3;
+            int v = (lo | (hi << 4)) - 32;
+            float ds = d * (float)sc[4 * j + (e >> 4)];
+            o[e] = ds * (float)v;
+        }
+    } else {
+        const uint8_t *dd = P.p[4] + (row * P.T + u) * 4;
+        for (int e = 0; e < n_el; e++) {
+            int h = e >> 5, i = e & 31;
+            float d = sdy_h2f((uint16_t)(dd[2 * h] | (dd[2 * h + 1] << 8)));
+            int v;
+            if constexpr (WT == SDY_Q8_0) {
+                const uint8_t *q = P.p[2 * h + (i >> 4)] + (row * P.T + u) * 16;
+                v = (int8_t)q[i & 15];
+            } else {
+                const uint8_t *q = P.p[h] + (row * P.T + u) * 16;
+                int nib = i < 16 ? (q[i] & 15) : (q[i - 16] >> 4);
+                if constexpr (WT == SDY_Q4_0) {
+                    v = nib - 8;
+                } else {
+                    uint32_t qh = ld4(P.p[2] + (row * P.T + u) * 8 + 4 * h);
+                    v = (nib | (int)(((qh >> i) & 1u) << 4)) - 16;
+                }
+            }
+            o[e] = (float)v * d;
+        }
+    }
+}
+
+template <int WT>
+__global__ void k_dequant_float(const uint8_t *__restrict__ w, int n_in, const int32_t *__restrict__ idx, long r0,
+                                long n, float *__restrict__ out) {
+    long gid = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    long i = gid / n_in;
+    int e = (int)(gid - i * n_in);
+    if (i >= n) return;
+    long row = idx ? (long)idx[i] : r0 + i;
+    float v;
+    if constexpr (WT == SDY_F32) v = reinterpret_cast<const float *>(w)[row * n_in + e];
+    else if constexpr (WT == SDY_F16) v = sdy_h2f(reinterpret_cast<const uint16_t *>(w)[row * n_in + e]);
+    else v = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(w)[row * n_in + e] << 16);
+    out[i * n_in + e] = v;
+}
+
+// ------------------------------------------------------------------------ activation quantisers
+
+// Q8_K (csrc/quant.c:118-144): one wave per 256-element block, lane l holds elements 4l..4l+3.
+__global__ void k_quant_q8k(const float *__restrict__ x, uint8_t *__restrict__ out, int n_in) {
+    const int nb = n_in / 256, s = blockIdx.x, t = blockIdx.y, l = threadIdx.x;
+    const float *xb = x + (size_t)t * n_in + 256 * s;
+    uint8_t *ob = out + ((size_t)t * nb + s) * 292;
+    float4 v = *reinterpret_cast<const float4 *>(xb + 4 * l);
+    float xs[4] = {v.x, v.y, v.z, v.w};
+    float best = 0.0f;
+    int bi = 0x7fffffff;
+    for (int e = 0; e < 4; e++)
+        if (fabsf(xs[e]) > best) {
+            best = fabsf(xs[e]);
+            bi = 4 * l + e;
+        }
+    for (int off = 32; off >= 1; off >>= 1) {
+        float ob_ = __shfl_xor(best, off);
+        int oi = __shfl_xor(bi, off);
+        if (ob_ > best || (ob_ == best && oi < bi)) {
+            best = ob_;
+            bi = oi;
+        }
+    }
+    if (best == 0.0f) {  // all-zero block: zero bytes (d, qs and bsums)
+        *reinterpret_cast<uint32_t *>(ob + 4 + 4 * l) = 0u;
+        if (l == 0) *reinterpret_cast<uint32_t *>(ob) = 0u;
+        if (l < 8) *reinterpret_cast<uint32_t *>(ob + 260 + 4 * l) = 0u;
+        return;
+    }
+    float vmax = xb[bi];
+    float iscale = -127.0f / vmax;
+    uint32_t packed = 0;
+    int lsum = 0;
+    for (int e = 0; e < 4; e++) {
+        int q = sdy_nearest_int(iscale * xs[e]);
+        q = q < 127 ? q : 127;
+        lsum += (int8_t)q;
+        packed |= (uint32_t)(uint8_t)(int8_t)q << (8 * e);
+    }
+    *reinterpret_cast<uint32_t *>(ob + 4 + 4 * l) = packed;
+    int gsum = sdy_quad_sum(lsum);  // group of 16 = lanes 4g..4g+3
+    if ((l & 3) == 0) *reinterpret_cast<int16_t *>(ob + 260 + 2 * (l >> 2)) = (int16_t)gsum;
+    if (l == 0) *reinterpret_cast<float *>(ob) = 1.0f / iscale;
+}
+
+// Q8_0 (csrc/quant.c:98-108): one wave per two 32-element blocks, one element per lane.
+__global__ void k_quant_q8_0(const float *__restrict__ x, uint8_t *__restrict__ out, int n_in) {
+    const int nblk = n_in / 32, t = blockIdx.y, l = threadIdx.x & 31;
+    const int b = 2 * blockIdx.x + (threadIdx.x >> 5);
+    if (b >= nblk) return;  // uniform per half-wave
+    float xv = x[(size_t)t * n_in + 32 * b + l];
+    float amax = fabsf(xv);
+    for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    float d = amax / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint8_t *ob = out + ((size_t)t * nblk + b) * 34;
+    ob[2 + l] = (uint8_t)(int8_t)roundf(xv * id);
+    if (l == 0) {
+        uint16_t h = sdy_f2h(d);
+        ob[0] = (uint8_t)(h & 255);
+        ob[1] = (uint8_t)(h >> 8);
+    }
+}
+
+// ------------------------------------------------------------------------------------ matvec
+
+// LDS layout of the staged activations of MT tokens (T units per row):
+//   Y  [MT][4][T] x 16 B   y bytes of unit u, 16-byte chunk q (conflict-free ds_read_b128)
+//   K-quants: BS [MT][T] x 8 B (bsums 4j..4j+3 of the unit)   YD [MT][nb] floats (Q8_K d)
+//   32-element types: DX [MT][T] x 8 B (two f32 scales)   SY [MT][T] x 8 B (two int sums of y)
+struct MvArgs {
+    Planes P;
+    const uint8_t *xq;
+    int n_tok;
+    float *out;
+    long out_stride;
+    const float *bias, *resid;
+    long row0, row1;
+    int rb;      // rows per wave batch (rb * T is a multiple of 64)
+    int nterm;   // f32 terms per row and token (super-blocks or units)
+};
+
+constexpr bool is_k(int wt) { return wt == SDY_Q4_K || wt == SDY_Q6_K; }
+
+template <int WT, int MT>
+__device__ void stage_acts(const MvArgs &a, uint8_t *lds) {
+    const int T = a.P.T, nb = a.P.nb, tid = threadIdx.x;
+    const int n_tok = a.n_tok;
+    if constexpr (is_k(WT)) {
+        // Q8_K rows: nb blocks of 292 B; y starts 4 bytes into a block (dword aligned)
+        for (int i = tid; i < n_tok * T * 16; i += THREADS) {
+            int m = i / (T * 16), r = i - m * T * 16, u = r >> 4, w = r & 15;
+            const uint8_t *src = a.xq + ((size_t)m * nb + (u >> 2)) * 292 + 4 + 64 * (u & 3) + 4 * w;
+            *reinterpret_cast<uint32_t *>(lds + ((m * 4 + (w >> 2)) * T + u) * 16 + 4 * (w & 3)) = ld4(src);
+        }
+        uint8_t *bs = lds + MT * 4 * T * 16;
+        for (int i = tid; i < n_tok * T; i += THREADS) {
+            int m = i / T, u = i - m * T;
+            const uint8_t *src = a.xq + ((size_t)m * nb + (u >> 2)) * 292 + 260 + 8 * (u & 3);
+            *reinterpret_cast<uint2 *>(bs + (m * T + u) * 8) = make_uint2(ld4(src), ld4(src + 4));
+        }
+        float *yd = reinterpret_cast<float *>(bs + MT * T * 8);
+        for (int i = tid; i < n_tok * nb; i += THREADS)
+            yd[i] = *reinterpret_cast<const float *>(a.xq + (size_t)i * 292);
+    } else {
+        // Q8_0 rows: nb blocks of 34 B (2-byte aligned); unit u = blocks 2u, 2u+1 (the second may
+        // be missing: zeros)
+        for (int i = tid; i < n_tok * T * 16; i += THREADS) {
+            int m = i / (T * 16), r = i - m * T * 16, u = r >> 4, w = r & 15;
+            int b = 2 * u + (w >> 3);
+            uint32_t v = 0;
+            if (b < nb) {
+                const uint16_t *src =
+                    reinterpret_cast<const uint16_t *>(a.xq + ((size_t)m * nb + b) * 34 + 2 + 4 * (w & 7));
+                v = (uint32_t)src[0] | ((uint32_t)src[1] << 16);
+            }
+            *reinterpret_cast<uint32_t *>(lds + ((m * 4 + (w >> 2)) * T + u) * 16 + 4 * (w & 3)) = v;
+        }
+        float *dx = reinterpret_cast<float *>(lds + MT * 4 * T * 16);
+        int *sy = reinterpret_cast<int *>(dx + MT * T * 2);
+        for (int i = tid; i < n_tok * T * 2; i += THREADS) {
+            int m = i / (T * 2), r = i - m * T * 2;  // r = 2u + h = block index
+            float dv = 0.0f;
+            int s = 0;
+            if (r < nb) {
+                const uint8_t *blk = a.xq + ((size_t)m * nb + r) * 34;
+                dv = sdy_h2f((uint16_t)(blk[0] | (blk[1] << 8)));
+                for (int e = 0; e < 32; e++) s += (int8_t)blk[2 + e];
+            }
+            dx[m * T * 2 + r] = dv;
+            sy[m * T * 2 + r] = s;
+        }
+    }
+}
+
+template <int WT>
+struct WRegs {
+    uint4 a, b, c, e;
+    uint32_t f, g;
+};
+
+template <int WT>
+SDY_DEV void load_w(const Planes &P, long row, int u, WRegs<WT> &r) {
+    const size_t ou = ((size_t)row * P.T + u) * 16;
+    if constexpr (WT == SDY_Q4_K) {
+        r.a = ld16(P.p[0] + ou);
+        r.b = ld16(P.p[1] + ou);
+        r.c = ld16(P.p[2] + ((size_t)row * P.nb + (u >> 2)) * 16);
+    } else if constexpr (WT == SDY_Q6_K) {
+        const size_t os = (size_t)row * P.nb + (u >> 2);
+        r.a = ld16(P.p[0] + ou);
+        r.b = ld16(P.p[1] + ou);
+        r.c = ld16(P.p[2] + ou);
+        r.f = ld4(P.p[3] + os * 16 + 4 * (u & 3));
+        r.g = *reinterpret_cast<const uint16_t *>(P.p[4] + os * 2);
+    } else if constexpr (WT == SDY_Q8_0) {
+        r.a = ld16(P.p[0] + ou);
+        r.b = ld16(P.p[1] + ou);
+        r.c = ld16(P.p[2] + ou);
+        r.e = ld16(P.p[3] + ou);
+        r.f = ld4(P.p[4] + ((size_t)row * P.T + u) * 4);
+    } else {
+        r.a = ld16(P.p[0] + ou);
+        r.b = ld16(P.p[1] + ou);
+        r.f = ld4(P.p[4] + ((size_t)row * P.T + u) * 4);
+        if constexpr (WT == SDY_Q5_0) {
+            const uint8_t *q = P.p[2] + ((size_t)row * P.T + u) * 8;
+            r.c.x = ld4(q);
+            r.c.y = ld4(q + 4);
+        }
+    }
+}
+
+SDY_DEV uint32_t w4(const uint4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+
+// One unit of one token: K-quants return the lane's integer parts (isum, msum), the 32-element
+// types return the unit's f32 term directly.
+template <int WT>
+SDY_DEV void unit_dot(const WRegs<WT> &r, const uint4 *Y, const uint8_t *aux, int u, int &isum, int &msum,
+                      float &term, const float *dxp, const int *syp) {
+    constexpr uint32_t LO = 0x0F0F0F0Fu;
+    if constexpr (WT == SDY_Q4_K) {
+        int slo = 0, shi = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            uint32_t qa = w4(r.a, w), qb = w4(r.b, w);
+            slo = sdy_dot4((int)(qa & LO), (int)w4(Y[0], w), slo);
+            slo = sdy_dot4((int)(qb & LO), (int)w4(Y[1], w), slo);
+            shi = sdy_dot4((int)((qa >> 4) & LO), (int)w4(Y[2], w), shi);
+            shi = sdy_dot4((int)((qb >> 4) & LO), (int)w4(Y[3], w), shi);
+        }
+        const int j = u & 3, k0 = 2 * j, k1 = 2 * j + 1;
+        const uint8_t *sc = reinterpret_cast<const uint8_t *>(&r.c) + 4;
+        int sc0 = q4k_scale(sc, k0, 0), sc1 = q4k_scale(sc, k1, 0);
+        int m0 = q4k_scale(sc, k0, 1), m1 = q4k_scale(sc, k1, 1);
+        const int16_t *bs = reinterpret_cast<const int16_t *>(aux);
+        isum = sc0 * slo + sc1 * shi;
+        msum = m0 * ((int)bs[0] + (int)bs[1]) + m1 * ((int)bs[2] + (int)bs[3]);
+    } else if constexpr (WT == SDY_Q6_K) {
+        const int16_t *bs = reinterpret_cast<const int16_t *>(aux);
+        int acc0 = -32 * bs[0], acc1 = -32 * bs[1], acc2 = -32 * bs[2], acc3 = -32 * bs[3];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            uint32_t n0 = w4(r.a, w), n1 = w4(r.b, w), h = w4(r.c, w);
+            uint32_t e0 = (n0 & LO) | ((h & 0x03030303u) << 4);
+            uint32_t e1 = (n1 & LO) | (((h >> 2) & 0x03030303u) << 4);
+            uint32_t e2 = ((n0 >> 4) & LO) | (((h >> 4) & 0x03030303u) << 4);
+            uint32_t e3 = ((n1 >> 4) & LO) | (((h >> 6) & 0x03030303u) << 4);
+            acc0 = sdy_dot4((int)e0, (int)w4(Y[0], w), acc0);
+            acc1 = sdy_dot4((int)e1, (int)w4(Y[1], w), acc1);
+            acc2 = sdy_dot4((int)e2, (int)w4(Y[2], w), acc2);
+            acc3 = sdy_dot4((int)e3, (int)w4(Y[3], w), acc3);
+        }
+        int s0 = (int)(int8_t)(r.f & 255u), s1 = (int)(int8_t)((r.f >> 8) & 255u);
+        int s2 = (int)(int8_t)((r.f >> 16) & 255u), s3 = (int)(int8_t)(r.f >> 24);
+        isum = s0 * acc0 + s1 * acc1 + s2 * acc2 + s3 * acc3;
+        msum = 0;
+    } else {
+        int s[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            int acc = 0;
+            if constexpr (WT == SDY_Q8_0) {
+                const uint4 &qa = h ? r.c : r.a, &qb = h ? r.e : r.b;
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    acc = sdy_dot4((int)w4(qa, w), (int)w4(Y[2 * h], w), acc);
+                    acc = sdy_dot4((int)w4(qb, w), (int)w4(Y[2 * h + 1], w), acc);
+                }
+            } else {
+                const uint4 &q = h ? r.b : r.a;
+                uint32_t qh = h ? r.c.y : r.c.x;
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    uint32_t lo = w4(q, w) & LO, hi = (w4(q, w) >> 4) & LO;
+                    if constexpr (WT == SDY_Q5_0) {
+                        lo |= sdy_spread4(qh >> (4 * w));
+                        hi |= sdy_spread4(qh >> (16 + 4 * w));
+                    }
+                    acc = sdy_dot4((int)lo, (int)w4(Y[2 * h], w), acc);
+                    acc = sdy_dot4((int)hi, (int)w4(Y[2 * h + 1], w), acc);
+                }
+                acc -= (WT == SDY_Q4_0 ? 8 : 16) * syp[h];
+            }
+            s[h] = acc;
+        }
+        float dw0 = sdy_h2f((uint16_t)(r.f & 0xFFFFu)), dw1 = sdy_h2f((uint16_t)(r.f >> 16));
+        float f0 = dw0 * dxp[0], f1 = dw1 * dxp[1];
+        float t0 = (float)s[0] * f0, t1 = (float)s[1] * f1;
+        term = t0 + t1;
+        isum = msum = 0;
+    }
+}
+
+template <int WT, int MT>
+__global__ __launch_bounds__(THREADS) void k_matvec(MvArgs a) {
+    extern __shared__ uint8_t lds[];
+    const int T = a.P.T, nb = a.P.nb;
+    stage_acts<WT, MT>(a, lds);
+    __syncthreads();
+    const size_t y_bytes = (size_t)MT * 4 * T * 16;
+    const uint8_t *aux_base = lds + y_bytes;  // BS (K) or DX (32-element types)
+    const float *yd = reinterpret_cast<const float *>(lds + y_bytes + (size_t)MT * T * 8);
+    const int *sy = reinterpret_cast<const int *>(lds + y_bytes + (size_t)MT * T * 8);
+    const size_t act_bytes = y_bytes + (size_t)MT * T * 16;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float *terms = reinterpret_cast<float *>(lds + act_bytes) + (size_t)wave * a.rb * MT * a.nterm;
+
+    const int rb = a.rb, tasks = rb * T, n_it = tasks / 64;
+    const long n_rows = a.row1 - a.row0;
+    const long n_batches = (n_rows + rb - 1) / rb;
+    for (long bt = (long)blockIdx.x * WAVES + wave; bt < n_batches; bt += (long)gridDim.x * WAVES) {
+        const long rbase = a.row0 + bt * rb;
+        WRegs<WT> cur, nxt;
+        auto task_row = [&](int it, int &rl, int &u) {
+            int task = it * 64 + lane;
+            rl = task / T;
+            u = task - rl * T;
+        };
+        int rl, u;
+        task_row(0, rl, u);
+        load_w<WT>(a.P, rbase + rl < a.row1 ? rbase + rl : rbase, u, cur);
+        for (int it = 0; it < n_it; it++) {
+            int rl_c = rl, u_c = u;
+            if (it + 1 < n_it) {
+                task_row(it + 1, rl, u);
+                load_w<WT>(a.P, rbase + rl < a.row1 ? rbase + rl : rbase, u, nxt);
+            }
+            const bool valid = rbase + rl_c < a.row1;
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                if (m >= a.n_tok) break;
+                uint4 Y[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    Y[q] = *reinterpret_cast<const uint4 *>(lds + ((m * 4 + q) * T + u_c) * 16);
+                int isum, msum;
+                float term;
+                if constexpr (is_k(WT)) {
+                    unit_dot<WT>(cur, Y, aux_base + (m * T + u_c) * 8, u_c, isum, msum, term, nullptr, nullptr);
+                    isum = sdy_quad_sum(isum);
+                    if constexpr (WT == SDY_Q4_K) msum = sdy_quad_sum(msum);
+                    if ((u_c & 3) == 0 && valid) {
+                        const int s = u_c >> 2;
+                        const float ydv = yd[m * nb + s];
+                        float t;
+                        if constexpr (WT == SDY_Q4_K) {
+                            float d = sdy_h2f((uint16_t)(cur.c.x & 0xFFFFu)), dmin = sdy_h2f((uint16_t)(cur.c.x >> 16));
+                            float dall = ydv * d, dmn = ydv * dmin;
+                            float t1 = dall * (float)isum, t2 = dmn * (float)msum;
+                            t = t1 - t2;
+                        } else {
+                            float d = sdy_h2f((uint16_t)cur.g);
+                            float ydd = ydv * d;
+                            t = ydd * (float)isum;
+                        }
+                        terms[(rl_c * MT + m) * a.nterm + s] = t;
+                    }
+                } else {
+                    const float *dxp = reinterpret_cast<const float *>(aux_base) + (m * T + u_c) * 2;
+                    unit_dot<WT>(cur, Y, nullptr, u_c, isum, msum, term, dxp, sy + (m * T + u_c) * 2);
+                    if (valid) terms[(rl_c * MT + m) * a.nterm + u_c] = term;
+                }
+            }
+            cur = nxt;
+        }
+        sdy_wave_sync();
+        // phase 2: each lane sums the terms of one (row, token) in block order
+        for (int i = lane; i < rb * a.n_tok; i += 64) {
+            int r = i / a.n_tok, m = i - r * a.n_tok;
+            long row = rbase + r;
+            if (row >= a.row1) continue;
+            const float *tp = terms + (r * MT + m) * a.nterm;
+            float acc = 0.0f;
+            for (int s = 0; s < a.nterm; s++) acc = acc + tp[s];
+            if (a.bias) acc = acc + a.bias[row];
+            float *o = a.out + (size_t)m * a.out_stride + row;
+            if (a.resid) acc = a.resid[(size_t)m * a.out_stride + row] + acc;
+            *o = acc;
+        }
+        sdy_wave_sync();
+    }
+}
+
+// ------------------------------------------------------------------ float-weight matvec (F32/F16/BF16)
+
+template <int WT>
+SDY_DEV float welem(const uint8_t *w, size_t i) {
+    if constexpr (WT == SDY_F32) return reinterpret_cast<const float *>(w)[i];
+    else if constexpr (WT == SDY_F16) return sdy_h2f(reinterpret_cast<const uint16_t *>(w)[i]);
+    else return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(w)[i] << 16);
+}
+
+// One wave per (row, token): lane l accumulates elements l, l+64, ... with fused multiply-adds,
+// then a fixed xor-butterfly reduction. Deterministic; parity with the reference is by tolerance.
+template <int WT>
+__global__ __launch_bounds__(THREADS) void k_matvec_float(const uint8_t *__restrict__ w, int n_in, const float *__restrict__ x,
+                                                          int n_tok, float *out, long out_stride, const float *bias,
+                                                          const float *resid, long row0, long row1) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const long n = (row1 - row0) * n_tok;
+    for (long i = (long)blockIdx.x * WAVES + wave; i < n; i += (long)gridDim.x * WAVES) {
+        long row = row0 + i / n_tok;
+        int t = (int)(i % n_tok);
+        const uint8_t *wr = w + (size_t)row * n_in * (WT == SDY_F32 ? 4 : 2);
+        const float *xr = x + (size_t)t * n_in;
+        float acc = 0.0f;
+        for (int e = lane; e < n_in; e += 64) acc = fmaf(welem<WT>(wr, e), xr[e], acc);
+        for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off);
+        if (lane == 0) {
+            if (bias) acc = acc + bias[row];
+            if (resid) acc = resid[(size_t)t * out_stride + row] + acc;
+            out[(size_t)t * out_stride + row] = acc;
+        }
+    }
+}
+
+}  // namespace
+
+// =============================================================================== host launchers
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static int n_units(int type, int n_in) {
+    if (type == SDY_Q4_K || type == SDY_Q6_K) return n_in / 64;
+    return (n_in + 63) / 64;
+}
+
+static int n_blocks(int type, int n_in) {
+    if (type == SDY_Q4_K || type == SDY_Q6_K) return n_in / 256;
+    return n_in / 32;
+}
+
+// per-row bytes of each plane
+static void plane_row_bytes(int type, int n_in, size_t pb[5]) {
+    int T = n_units(type, n_in), nb = n_blocks(type, n_in);
+    for (int i = 0; i < 5; i++) pb[i] = 0;
+    switch (type) {
+    case SDY_Q4_K: pb[0] = pb[1] = 16u * T; pb[2] = 16u * nb; break;
+    case SDY_Q6_K: pb[0] = pb[1] = pb[2] = 16u * T; pb[3] = 16u * nb; pb[4] = 2u * nb; break;
+    case SDY_Q8_0: pb[0] = pb[1] = pb[2] = pb[3] = 16u * T; pb[4] = 4u * T; break;
+    case SDY_Q4_0: pb[0] = pb[1] = 16u * T; pb[4] = 4u * T; break;
+    case SDY_Q5_0: pb[0] = pb[1] = 16u * T; pb[2] = 8u * T; pb[4] = 4u * T; break;
+    case SDY_F32: pb[0] = 4u * n_in; break;
+    case SDY_F16: case SDY_BF16: pb[0] = 2u * n_in; break;
+    default: break;
+    }
+}
+
+static bool type_ok(int type) {
+    switch (type) {
+    case SDY_F32: case SDY_F16: case SDY_BF16: case SDY_Q8_0: case SDY_Q4_0: case SDY_Q5_0: case SDY_Q4_K:
+    case SDY_Q6_K: return true;
+    default: return false;
+    }
+}
+
+static bool is_float_type(int type) { return type == SDY_F32 || type == SDY_F16 || type == SDY_BF16; }
+
+size_t sdy_raw_row_bytes(int type, int n_in) {
+    switch (type) {
+    case SDY_F32: return 4u * n_in;
+    case SDY_F16: case SDY_BF16: return 2u * n_in;
+    case SDY_Q8_0: return (size_t)(n_in / 32) * 34;
+    case SDY_Q4_0: return (size_t)(n_in / 32) * 18;
+    case SDY_Q5_0: return (size_t)(n_in / 32) * 22;
+    case SDY_Q4_K: return (size_t)(n_in / 256) * 144;
+    case SDY_Q6_K: return (size_t)(n_in / 256) * 210;
+    case SDY_Q8_K: return (size_t)(n_in / 256) * 292;
+    default: return 0;
+    }
+}
+
+extern "C" size_t sdy_mat_bytes(int type, int n_in, long n_rows) {
+    size_t pb[5], tot = 0;
+    plane_row_bytes(type, n_in, pb);
+    for (int i = 0; i < 5; i++)
+        if (pb[i]) tot += align256(pb[i] * (size_t)n_rows);
+    return tot;
+}
+
+static Planes planes_of(const sdy_mat *m) {
+    Planes P;
+    for (int i = 0; i < 5; i++) P.p[i] = (const uint8_t *)m->base + m->plane_off[i];
+    P.n_in = m->n_in;
+    P.T = m->n_units;
+    P.nb = n_blocks(m->type, m->n_in);
+    return P;
+}
+
+static int check_shape(int type, int n_in, long n_rows) {
+    if (!type_ok(type)) return sdy_fail(-1, "weight type %d not supported on the GPU path", type);
+    if (n_in <= 0 || n_rows <= 0) return sdy_fail(-1, "empty matrix (%d x %ld)", n_in, n_rows);
+    if ((type == SDY_Q4_K || type == SDY_Q6_K) && n_in % 256)
+        return sdy_fail(-1, "K-quant rows must be a multiple of 256 (got %d)", n_in);
+    if ((type == SDY_Q8_0 || type == SDY_Q4_0 || type == SDY_Q5_0) && n_in % 32)
+        return sdy_fail(-1, "32-element block rows must be a multiple of 32 (got %d)", n_in);
+    return 0;
+}
+
+extern "C" int sdy_mat_from_device(sdy_mat *m, int type, int n_in, long n_rows, const void *dev_raw, sdy_stream s) {
+    int rc = check_shape(type, n_in, n_rows);
+    if (rc) return rc;
+    memset(m, 0, sizeof(*m));
+    m->type = type;
+    m->n_in = n_in;
+    m->n_rows = n_rows;
+    m->n_units = n_units(type, n_in);
+    m->bytes = sdy_mat_bytes(type, n_in, n_rows);
+    if ((rc = sdy_malloc(&m->base, m->bytes))) return rc;
+    size_t pb[5], off = 0;
+    plane_row_bytes(type, n_in, pb);
+    for (int i = 0; i < 5; i++) {
+        m->plane_off[i] = off;
+        if (pb[i]) off += align256(pb[i] * (size_t)n_rows);
+    }
+    hipStream_t st = (hipStream_t)s;
+    if (is_float_type(type)) return sdy_d2d(m->base, dev_raw, pb[0] * n_rows, s);
+    uint8_t *dst_h[5];
+    for (int i = 0; i < 5; i++) dst_h[i] = (uint8_t *)m->base + m->plane_off[i];
+    uint8_t **dst_d = nullptr;
+    if ((rc = sdy_malloc((void **)&dst_d, sizeof(dst_h)))) return rc;
+    if ((rc = sdy_h2d(dst_d, dst_h, sizeof(dst_h), s))) return rc;
+    Planes P = planes_of(m);
+    long total = n_rows * (long)m->n_units;
+    dim3 grid((unsigned)((total + 255) / 256)), block(256);
+    size_t src_row = sdy_raw_row_bytes(type, n_in);
+    const uint8_t *src = (const uint8_t *)dev_raw;
+    switch (type) {
+    case SDY_Q4_K: hipLaunchKernelGGL(k_repack<SDY_Q4_K>, grid, block, 0, st, src, src_row, P, dst_d, n_rows); break;
+    case SDY_Q6_K: hipLaunchKernelGGL(k_repack<SDY_Q6_K>, grid, block, 0, st, src, src_row, P, dst_d, n_rows); break;
+    case SDY_Q8_0: hipLaunchKernelGGL(k_repack<SDY_Q8_0>, grid, block, 0, st, src, src_row, P, dst_d, n_rows); break;
+    case SDY_Q4_0: hipLaunchKernelGGL(k_repack<SDY_Q4_0>, grid, block, 0, st, src, src_row, P, dst_d, n_rows); break;
+    case SDY_Q5_0: hipLaunchKernelGGL(k_repack<SDY_Q5_0>, grid, block, 0, st, src, src_row, P, dst_d, n_rows); break;
+    }
+    if ((rc = sdy_check_launch("repack"))) return rc;
+    if ((rc = sdy_sync(s))) return rc;
+    return sdy_free(dst_d);
+}
+
+extern "C" int sdy_mat_upload(sdy_mat *m, int type, int n_in, long n_rows, const void *host_raw, sdy_stream s) {
+    int rc = check_shape(type, n_in, n_rows);
+    if (rc) return rc;
+    size_t raw = sdy_raw_row_bytes(type, n_in) * (size_t)n_rows;
+    void *tmp = nullptr;
+    if ((rc = sdy_malloc(&tmp, raw))) return rc;
+    if ((rc = sdy_h2d(tmp, host_raw, raw, s)) || (rc = sdy_mat_from_device(m, type, n_in, n_rows, tmp, s))) {
+        sdy_free(tmp);
+        return rc;
+    }
+    if ((rc = sdy_sync(s))) return rc;
+    return sdy_free(tmp);
+}
+
+extern "C" int sdy_mat_free(sdy_mat *m) {
+    if (!m || !m->base) return 0;
+    int rc = sdy_free(m->base);
+    m->base = nullptr;
+    return rc;
+}
+
+extern "C" sdy_mat sdy_mat_rows(const sdy_mat *m, long r0, long n) {
+    // A view: plane pointers advanced by r0 rows. Planes are per-row arrays, so the view keeps the
+    // same base with shifted offsets.
+    sdy_mat v = *m;
+    size_t pb[5];
+    plane_row_bytes(m->type, m->n_in, pb);
+    for (int i = 0; i < 5; i++) v.plane_off[i] = m->plane_off[i] + pb[i] * (size_t)r0;
+    v.n_rows = n;
+    return v;
+}
+
+static int dequant_impl(const sdy_mat *m, const int32_t *idx, long r0, long n, float *out, sdy_stream s) {
+    hipStream_t st = (hipStream_t)s;
+    if (n <= 0) return 0;
+    if (is_float_type(m->type)) {
+        long total = n * (long)m->n_in;
+        dim3 grid((unsigned)((total + 255) / 256));
+        const uint8_t *w = (const uint8_t *)m->base + m->plane_off[0];
+        switch (m->type) {
+        case SDY_F32: hipLaunchKernelGGL(k_dequant_float<SDY_F32>, grid, dim3(256), 0, st, w, m->n_in, idx, r0, n, out); break;
+        case SDY_F16: hipLaunchKernelGGL(k_dequant_float<SDY_F16>, grid, dim3(256), 0, st, w, m->n_in, idx, r0, n, out); break;
+        default: hipLaunchKernelGGL(k_dequant_float<SDY_BF16>, grid, dim3(256), 0, st, w, m->n_in, idx, r0, n, out); break;
+        }
+        return sdy_check_launch("dequant_float");
+    }
+    Planes P = planes_of(m);
+    long total = n * (long)P.T;
+    dim3 grid((unsigned)((total + 127) / 128)), block(128);
+    switch (m->type) {
+    case SDY_Q4_K: hipLaunchKernelGGL(k_dequant<SDY_Q4_K>, grid, block, 0, st, P, idx, r0, n, out); break;
+    case SDY_Q6_K: hipLaunchKernelGGL(k_dequant<SDY_Q6_K>, grid, block, 0, st, P, idx, r0, n, out); break;
+    case SDY_Q8_0: hipLaunchKernelGGL(k_dequant<SDY_Q8_0>, grid, block, 0, st, P, idx, r0, n, out); break;
+    case SDY_Q4_0: hipLaunchKernelGGL(k_dequant<SDY_Q4_0>, grid, block, 0, st, P, idx, r0, n, out); break;
+    case SDY_Q5_0: hipLaunchKernelGGL(k_dequant<SDY_Q5_0>, grid, block, 0, st, P, idx, r0, n, out); break;
+    default: return sdy_fail(-1, "dequant: type %d", m->type);
+    }
+    return sdy_check_launch("dequant");
+}
+
+extern "C" int sdy_dequant_rows(const sdy_mat *m, long r0, long n, float *out, sdy_stream s) {
+    if (r0 < 0 || r0 + n > m->n_rows) return sdy_fail(-1, "dequant rows [%ld, %ld) outside %ld rows", r0, r0 + n, m->n_rows);
+    return dequant_impl(m, nullptr, r0, n, out, s);
+}
+
+extern "C" int sdy_dequant_gather(const sdy_mat *m, const int32_t *idx, int n, float *out, sdy_stream s) {
+    return dequant_impl(m, idx, 0, n, out, s);
+}
+
+extern "C" int sdy_quantize(int vtype, const float *x, void *xq, int n_in, int n_tok, sdy_stream s) {
+    hipStream_t st = (hipStream_t)s;
+    if (n_tok <= 0) return 0;
+    if (vtype == SDY_Q8_K) {
+        if (n_in % 256) return sdy_fail(-1, "Q8_K rows must be a multiple of 256 (got %d)", n_in);
+        hipLaunchKernelGGL(k_quant_q8k, dim3(n_in / 256, n_tok), dim3(64), 0, st, x, (uint8_t *)xq, n_in);
+        return sdy_check_launch("quant_q8k");
+    }
+    if (vtype == SDY_Q8_0) {
+        if (n_in % 32) return sdy_fail(-1, "Q8_0 rows must be a multiple of 32 (got %d)", n_in);
+        int nblk = n_in / 32;
+        hipLaunchKernelGGL(k_quant_q8_0, dim3((nblk + 1) / 2, n_tok), dim3(64), 0, st, x, (uint8_t *)xq, n_in);
+        return sdy_check_launch("quant_q8_0");
+    }
+    return sdy_fail(-1, "activation type %d", vtype);
+}
+
+static int g_n_cu = 0;
+
+static int rows_per_batch(int T) {
+    int g = 1;
+    while (g < 64 && T % (2 * g) == 0) g *= 2;  // gcd(T, 64)
+    int rb_unit = 64 / g;                        // rb * T must be a multiple of 64
+    return rb_unit > 16 ? rb_unit : 16;
+}
+
+// LDS bytes of k_matvec: staged activations of MT tokens plus the per-wave term buffers.
+static size_t mv_lds_bytes(int wt, int T, int nb, int MT) {
+    int nterm = is_k(wt) ? nb : T;
+    return (size_t)MT * 4 * T * 16 + (size_t)MT * T * 16 + (size_t)WAVES * rows_per_batch(T) * MT * nterm * 4;
+}
+
+constexpr size_t LDS_MAX = 160 * 1024;
+
+template <int WT, int MT>
+static int launch_mv(const sdy_mat *m, const sdy_mv_args *a, int n_tok, const uint8_t *xq, float *out,
+                     const float *resid, hipStream_t st) {
+    MvArgs A;
+    A.P = planes_of(m);
+    A.xq = xq;
+    A.n_tok = n_tok;
+    A.out = out;
+    A.out_stride = a->out_stride;
+    A.bias = a->bias;
+    A.resid = resid;
+    A.row0 = a->row0;
+    A.row1 = a->row1;
+    A.rb = rows_per_batch(A.P.T);
+    A.nterm = is_k(WT) ? A.P.nb : A.P.T;
+    size_t lds = mv_lds_bytes(WT, A.P.T, A.P.nb, MT);
+    if (lds > LDS_MAX) return sdy_fail(-1, "matvec: %zu bytes of LDS needed (n_in %d, %d tokens)", lds, m->n_in, MT);
+    long n_rows = a->row1 - a->row0;
+    long n_batches = (n_rows + A.rb - 1) / A.rb;
+    long wgs = (n_batches + WAVES - 1) / WAVES;
+    int per_cu = (int)(LDS_MAX / lds);
+    per_cu = per_cu < 1 ? 1 : per_cu > 8 ? 8 : per_cu;
+    long cap = (long)(g_n_cu ? g_n_cu : 256) * per_cu;
+    if (wgs > cap) wgs = cap;
+    static bool big_lds = false;
+    if (lds > 64 * 1024 && !big_lds) {
+        (void)hipFuncSetAttribute((const void *)k_matvec<WT, MT>, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_MAX);
+        big_lds = true;
+    }
+    hipLaunchKernelGGL((k_matvec<WT, MT>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
+    return sdy_check_launch("matvec");
+}
+
+template <int WT>
+static int mv_type(const sdy_mat *m, const sdy_mv_args *a, hipStream_t st) {
+    size_t xrow = sdy_raw_row_bytes(is_k(WT) ? SDY_Q8_K : SDY_Q8_0, m->n_in);
+    const int T = m->n_units, nb = n_blocks(WT, m->n_in);
+    // largest token capacity (8, 4, 2, 1) whose LDS fits; tokens are processed in chunks of it
+    int cap = 8;
+    while (cap > 1 && mv_lds_bytes(WT, T, nb, cap) > LDS_MAX) cap /= 2;
+    for (int t0 = 0; t0 < a->n_tok;) {
+        int n = a->n_tok - t0 < cap ? a->n_tok - t0 : cap;
+        const uint8_t *xq = (const uint8_t *)a->xq + xrow * t0;
+        float *out = a->out + a->out_stride * t0;
+        const float *resid = a->resid ? a->resid + a->out_stride * t0 : nullptr;
+        int rc;  // the smallest token capacity that holds n
+        if (n > 4) rc = launch_mv<WT, 8>(m, a, n, xq, out, resid, st);
+        else if (n > 2) rc = launch_mv<WT, 4>(m, a, n, xq, out, resid, st);
+        else if (n == 2) rc = launch_mv<WT, 2>(m, a, n, xq, out, resid, st);
+        else rc = launch_mv<WT, 1>(m, a, 1, xq, out, resid, st);
+        if (rc) return rc;
+        t0 += n;
+    }
+    return 0;
+}
+
+extern "C" int sdy_matvec(const sdy_mat *m, const sdy_mv_args *a, sdy_stream s) {
+    hipStream_t st = (hipStream_t)s;
+    if (a->row0 < 0 || a->row1 > m->n_rows || a->row0 > a->row1)
+        return sdy_fail(-1, "matvec rows [%ld, %ld) outside %ld", a->row0, a->row1, m->n_rows);
+    if (a->row0 == a->row1 || a->n_tok <= 0) return 0;
+    if (!g_n_cu) {
+        int n_cu = 0;
+        size_t mem = 0;
+        sdy_device_info(&n_cu, &mem);
+        g_n_cu = n_cu;
+    }
+    switch (m->type) {
+    case SDY_Q4_K: return mv_type<SDY_Q4_K>(m, a, st);
+    case SDY_Q6_K: return mv_type<SDY_Q6_K>(m, a, st);
+    case SDY_Q8_0: return mv_type<SDY_Q8_0>(m, a, st);
+    case SDY_Q4_0: return mv_type<SDY_Q4_0>(m, a, st);
+    case SDY_Q5_0: return mv_type<SDY_Q5_0>(m, a, st);
+    case SDY_F32: case SDY_F16: case SDY_BF16:
+        return sdy_matvec_float(m->type, (const uint8_t *)m->base + m->plane_off[0], m->n_in, a, s);
+    default: return sdy_fail(-1, "matvec: type %d", m->type);
+    }
+}
+
+extern "C" int sdy_matvec_float(int wtype, const void *w, int n_in, const sdy_mv_args *a, sdy_stream s) {
+    hipStream_t st = (hipStream_t)s;
+    long n = (a->row1 - a->row0) * (long)a->n_tok;
+    if (n <= 0) return 0;
+    long wgs = (n + WAVES - 1) / WAVES;
+    if (wgs > 4096) wgs = 4096;
+    const uint8_t *wp = (const uint8_t *)w;
+    switch (wtype) {
+    case SDY_F32:
+        hipLaunchKernelGGL(k_matvec_float<SDY_F32>, dim3((unsigned)wgs), dim3(THREADS), 0, st, wp, n_in, a->x, a->n_tok,
+                           a->out, a->out_stride, a->bias, a->resid, a->row0, a->row1);
+        break;
+    case SDY_F16:
+        hipLaunchKernelGGL(k_matvec_float<SDY_F16>, dim3((unsigned)wgs), dim3(THREADS), 0, st, wp, n_in, a->x, a->n_tok,
+                           a->out, a->out_stride, a->bias, a->resid, a->row0, a->row1);
+        break;
+    case SDY_BF16:
+        hipLaunchKernelGGL(k_matvec_float<SDY_BF16>, dim3((unsigned)wgs), dim3(THREADS), 0, st, wp, n_in, a->x, a->n_tok,
+                           a->out, a->out_stride, a->bias, a->resid, a->row0, a->row1);
+        break;
+    default: return sdy_fail(-1, "float matvec: type %d", wtype);
+    }
+    return sdy_check_launch("matvec_float");
+}

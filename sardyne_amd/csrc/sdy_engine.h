@@ -1,0 +1,52 @@
+/* Engine state shared by engine.c (ABI, loading, validation) and forward.c (device forward). */
+#ifndef SDY_ENGINE_H
+#define SDY_ENGINE_H
+#include <stdint.h>
+
+#include "sardyne.h"
+#include "sdy_shim.h"
+
+typedef struct {
+    sdy_mat m;  /* device layout; experts stacked as n_expert * n_out rows */
+    int type, n_in, n_out;
+} dmat;
+
+typedef struct {
+    float *attn_norm, *ffn_norm, *bq, *bk, *bv, *q_norm, *k_norm; /* f32, device */
+    dmat wq, wk, wv, wo, gate, up, down, gate_inp;
+} dlayer;
+
+struct engine_model {
+    gguf_file *gf;
+    engine_model_info info;
+    dmat tok_embd, output;
+    float *output_norm;
+    dlayer *layers;
+    float *vectors, *vec_cursor; /* one device allocation for every f32 vector */
+    sdy_stream st;
+    size_t device_bytes;
+};
+
+struct engine_ctx {
+    const engine_model *m;
+    int max_seq, n_batch, logits_all, n_past, n_logits, n_threads;
+    sdy_stream st;
+    float *logits; /* host (pinned), [n_logits][n_vocab] */
+    /* device state */
+    float *k_cache, *v_cache, *rope_cos, *rope_sin;
+    float *x, *xb, *q, *k, *v, *att, *hb, *hb2, *logits_dev, *part;
+    void *xq[2];                /* quantized activations: [0] Q8_0, [1] Q8_K */
+    const float *xq_src[2];
+    int xq_n_tok[2], xq_n_in[2];
+    int32_t *tok_dev, *tok_host;
+    /* MoE */
+    float *moe_probs, *moe_w, *moe_x, *moe_y, *moe_sum, *moe_gw;
+    int32_t *moe_top, *moe_gidx, *moe_top_host, *moe_gidx_host;
+    float *moe_w_host, *moe_gw_host;
+    char err[256];
+};
+
+int sdy_engine_alloc(engine_ctx *c);
+void sdy_engine_release(engine_ctx *c);
+int sdy_engine_forward(engine_ctx *c, const int32_t *tokens, int n, int out_rows);
+#endif

@@ -1,0 +1,17 @@
+// Internal helpers shared by the HIP translation units of the shim (not part of any ABI).
+#pragma once
+#include <stddef.h>
+#include <string.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+/* Records a formatted error for sdy_last_error() and returns rc. */
+int sdy_fail(int rc, const char *fmt, ...);
+/* Turns a pending kernel-launch error into an sdy error. */
+int sdy_check_launch(const char *what);
+/* Bytes of one row in the GGUF layout. */
+size_t sdy_raw_row_bytes(int type, int n_in);
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,36 @@
+/* Launchers of the float-side kernels (ops_kernels.hip). Internal to the library. */
+#ifndef SDY_OPS_H
+#define SDY_OPS_H
+#include <stddef.h>
+#include <stdint.h>
+
+#include "sdy_shim.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+int sdy_rmsnorm(const float *x, const float *w, float *out, int n, float eps, int n_rows, long x_stride,
+                long out_stride, sdy_stream s);
+int sdy_qk_rope_kv(float *q, float *k, const float *v, const float *qn, const float *kn, float eps,
+                   const float *rope_cos, const float *rope_sin, int pos0, int n_tok, int n_head, int n_kv_head, int hd,
+                   int interleaved, float *k_cache, float *v_cache, long head_stride, sdy_stream s);
+size_t sdy_attn_part_floats(int n_tok, int n_head, int hd, int max_kv);
+int sdy_attention(const float *q, const float *k_cache, const float *v_cache, int n_tok, int n_head, int n_kv_head,
+                  int hd, int n_kv0, long head_stride, long q_stride, float *part, float *out, long out_stride,
+                  sdy_stream s);
+int sdy_silu_mul(float *gate, const float *up, long n, sdy_stream s);
+int sdy_add(const float *a, const float *b, float *out, long n, sdy_stream s);
+int sdy_axpy(float *y, float a, const float *x, long n, sdy_stream s);
+int sdy_dot(const float *a, const float *b, int n, float *out, sdy_stream s);
+int sdy_f16_to_f32(const uint16_t *x, float *out, long n, sdy_stream s);
+int sdy_f32_to_f16(const float *x, uint16_t *out, long n, sdy_stream s);
+int sdy_softmax(float *x, int n, int n_rows, long stride, sdy_stream s);
+int sdy_rope_table(float *cos_out, float *sin_out, int n_pos, int hd, float theta, sdy_stream s);
+int sdy_rope(float *x, int n_heads, int hd, const float *cs, const float *sn, int interleaved, sdy_stream s);
+int sdy_moe_route(float *probs, int n_tok, int n_expert, int k, int32_t *top, float *wts, sdy_stream s);
+int sdy_moe_combine(const float *y, const int32_t *top, const float *wts, int n_tok, int k, int dim, float *out,
+                    const float *resid, sdy_stream s);
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,169 @@
+// Device management for the C host: device selection, allocations, copies, streams.
+// Errors are reported as negative return codes with a per-thread message (sdy_last_error).
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "sdy_internal.h"
+#include "sdy_shim.h"
+
+static thread_local char g_err[512];
+static int g_inited = 0;
+static int g_n_cu = 0;
+static size_t g_mem = 0;
+
+extern "C" const char *sdy_last_error(void) { return g_err; }
+
+extern "C" int sdy_fail(int rc, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return rc;
+}
+
+static int hip_fail(hipError_t e, const char *what) {
+    return sdy_fail(-2, "%s: %s (%s)", what, hipGetErrorString(e), hipGetErrorName(e));
+}
+
+#define HIPCK(call, what)                                   \
+    do {                                                    \
+        hipError_t e_ = (call);                             \
+        if (e_ != hipSuccess) return hip_fail(e_, what);    \
+    } while (0)
+
+extern "C" int sdy_check_launch(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, what);
+    return 0;
+}
+
+extern "C" int sdy_init(void) {
+    if (g_inited) return 0;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n < 1)
+        return sdy_fail(-3, "no HIP device available (%s): this library computes on an MI355X (gfx950) GPU",
+                        e != hipSuccess ? hipGetErrorString(e) : "0 devices");
+    HIPCK(hipSetDevice(0), "hipSetDevice");
+    hipDeviceProp_t p;
+    HIPCK(hipGetDeviceProperties(&p, 0), "hipGetDeviceProperties");
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return sdy_fail(-3, "device 0 is %s; the kernels are built for gfx950 only", p.gcnArchName);
+    g_n_cu = p.multiProcessorCount;
+    g_mem = p.totalGlobalMem;
+    g_inited = 1;
+    return 0;
+}
+
+extern "C" int sdy_device_info(int *n_cu, size_t *mem_total) {
+    int rc = sdy_init();
+    if (rc) return rc;
+    if (n_cu) *n_cu = g_n_cu;
+    if (mem_total) *mem_total = g_mem;
+    return 0;
+}
+
+extern "C" int sdy_malloc(void **p, size_t n) {
+    int rc = sdy_init();
+    if (rc) return rc;
+    *p = nullptr;
+    if (n == 0) n = 256;
+    hipError_t e = hipMalloc(p, n);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return sdy_fail(-4, "device allocation of %.1f MB failed: %s", n / 1e6, hipGetErrorString(e));
+    }
+    return 0;
+}
+
+extern "C" int sdy_free(void *p) {
+    if (!p) return 0;
+    HIPCK(hipFree(p), "hipFree");
+    return 0;
+}
+
+extern "C" int sdy_host_alloc(void **p, size_t n) {
+    int rc = sdy_init();
+    if (rc) return rc;
+    HIPCK(hipHostMalloc(p, n ? n : 64, hipHostMallocDefault), "hipHostMalloc");
+    return 0;
+}
+
+extern "C" int sdy_host_free(void *p) {
+    if (!p) return 0;
+    HIPCK(hipHostFree(p), "hipHostFree");
+    return 0;
+}
+
+extern "C" int sdy_h2d(void *dst, const void *src, size_t n, sdy_stream s) {
+    if (!n) return 0;
+    HIPCK(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, (hipStream_t)s), "copy to device");
+    return 0;
+}
+
+extern "C" int sdy_d2h(void *dst, const void *src, size_t n, sdy_stream s) {
+    if (!n) return 0;
+    HIPCK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, (hipStream_t)s), "copy to host");
+    return 0;
+}
+
+extern "C" int sdy_d2d(void *dst, const void *src, size_t n, sdy_stream s) {
+    if (!n) return 0;
+    HIPCK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, (hipStream_t)s), "device copy");
+    return 0;
+}
+
+extern "C" int sdy_memset(void *p, int v, size_t n, sdy_stream s) {
+    if (!n) return 0;
+    HIPCK(hipMemsetAsync(p, v, n, (hipStream_t)s), "memset");
+    return 0;
+}
+
+extern "C" int sdy_sync(sdy_stream s) {
+    HIPCK(hipStreamSynchronize((hipStream_t)s), "stream synchronize");
+    return 0;
+}
+
+extern "C" int sdy_stream_new(sdy_stream *s) {
+    int rc = sdy_init();
+    if (rc) return rc;
+    hipStream_t st;
+    HIPCK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "hipStreamCreate");
+    *s = (sdy_stream)st;
+    return 0;
+}
+
+extern "C" int sdy_stream_free(sdy_stream s) {
+    if (!s) return 0;
+    HIPCK(hipStreamDestroy((hipStream_t)s), "hipStreamDestroy");
+    return 0;
+}
+
+// ---- events (timing on a given stream)
+extern "C" int sdy_event_new(void **ev) {
+    int rc = sdy_init();
+    if (rc) return rc;
+    hipEvent_t e;
+    HIPCK(hipEventCreate(&e), "hipEventCreate");
+    *ev = (void *)e;
+    return 0;
+}
+
+extern "C" int sdy_event_record(void *ev, sdy_stream s) {
+    HIPCK(hipEventRecord((hipEvent_t)ev, (hipStream_t)s), "hipEventRecord");
+    return 0;
+}
+
+extern "C" int sdy_event_elapsed(float *ms, void *e0, void *e1) {
+    HIPCK(hipEventSynchronize((hipEvent_t)e1), "hipEventSynchronize");
+    HIPCK(hipEventElapsedTime(ms, (hipEvent_t)e0, (hipEvent_t)e1), "hipEventElapsedTime");
+    return 0;
+}
+
+extern "C" int sdy_event_free(void *ev) {
+    if (!ev) return 0;
+    HIPCK(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy");
+    return 0;
+}

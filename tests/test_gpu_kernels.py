@@ -1,0 +1,271 @@
+"""GPU kernels against the oracle (oracle/, a CPU restatement of the reference pinned to the
+compiled reference): dequantisation and activation quantisation bit/byte-exact, K-quant matvec
+bit-exact, 32-element-block matvec within rel 1e-5, float kernels within the tolerances of the
+reference's own tests (tests/test_runtime.py:100-152, tests/test_quant.py:120-205).
+
+Every test calls the C ABI of build/libsardyne.so (op_* host entry points or the sdy_* device
+entry points)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle as O
+from sardyne_amd import capi
+from sardyne_amd.gguf_synth import random_blocks
+
+pytestmark = pytest.mark.gpu
+
+TYPES = {"Q8_0": O.Q8_0, "Q4_0": O.Q4_0, "Q5_0": O.Q5_0, "Q4_K": O.Q4_K, "Q6_K": O.Q6_K}
+
+
+def lib():
+    return capi.lib()
+
+
+def ptr(a):
+    return a.ctypes.data
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def ref_blocks(kind, n_blocks, seed):
+    """The reference's test generator distribution (tests/test_quant.py:24-36): uniform bytes, f16
+    scales U(1e-4, 1e-2), Q6_K int8 scales in [-60, 60)."""
+    rng = np.random.default_rng(seed)
+    size = O.BLOCK_BYTES[TYPES[kind]]
+    b = rng.integers(0, 256, (n_blocks, size), dtype=np.uint8)
+    scale = lambda: rng.uniform(1e-4, 1e-2, n_blocks).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    if kind in ("Q8_0", "Q4_0", "Q5_0"):
+        b[:, 0:2] = scale()
+    elif kind == "Q4_K":
+        b[:, 0:2], b[:, 2:4] = scale(), scale()
+    elif kind == "Q6_K":
+        b[:, 208:210] = scale()
+        b[:, 192:208] = rng.integers(-60, 60, (n_blocks, 16)).astype(np.int8).view(np.uint8)
+    return b
+
+
+def test_f16_to_f32_all_values():
+    h = np.arange(1 << 16, dtype=np.uint16)
+    out = np.empty(1 << 16, np.float32)
+    lib().op_f16_to_f32_n(ptr(h), ptr(out), h.size)
+    exp = np.empty_like(out)
+    O.lib().orc_f16_to_f32_n(ptr(h), ptr(exp), h.size)
+    nan = np.isnan(exp)
+    assert np.array_equal(np.isnan(out), nan)
+    assert np.array_equal(bits(out)[~nan], bits(exp)[~nan])
+
+
+def test_f32_to_f16_edge_values():
+    rng = np.random.default_rng(3)
+    v = (rng.standard_normal(200) * 10.0 ** rng.integers(-9, 6, 200)).astype(np.float32)
+    v = np.concatenate([v, np.array([65504, 65519, 65520, 7e4, 6e-8, 3e-8, 2.98e-8, 0, -0.0, 5.96e-8, np.inf,
+                                     -np.inf, 1e-45, -3.1e-5], np.float32)])
+    got = np.array([lib().op_f32_to_f16(float(x)) for x in v], np.uint16)
+    exp = np.array([O.lib().orc_f32_to_f16(float(x)) for x in v], np.uint16)
+    assert np.array_equal(got, exp)
+
+
+@pytest.mark.parametrize("kind", list(TYPES))
+@pytest.mark.parametrize("gen", ["reference", "workload"])
+def test_dequant_bit_exact(kind, gen):
+    t = TYPES[kind]
+    n = 2048
+    nb = n // O.QK[t]
+    raw = ref_blocks(kind, nb, 4) if gen == "reference" else random_blocks(kind, nb, np.random.default_rng(4))
+    raw = np.ascontiguousarray(raw).reshape(-1)
+    out = np.empty(n, np.float32)
+    lib().op_row_to_f32(ptr(raw), t, ptr(out), n)
+    assert np.array_equal(bits(out), bits(O.dequant(raw, t, n)))
+
+
+@pytest.mark.parametrize("vt", [O.Q8_0, O.Q8_K], ids=["Q8_0", "Q8_K"])
+def test_activation_quantization_byte_exact(vt):
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((5, 512)) * np.array([[1e-3], [1.0], [300.0], [1.0], [1e-30]])).astype(np.float32)
+    x[1, :256] = 0  # all-zero block
+    x[2, 7] = 1e4  # one dominant value
+    x[3, 10], x[3, 20] = -4.0, 4.0  # equal magnitudes: the first one sets the sign
+    x[3, 300] = 2.5
+    n_rows, n = x.shape
+    out = np.zeros(O.row_size(vt, n) * n_rows, np.uint8)
+    lib().op_quantize_rows(vt, ptr(x), ptr(out), n, 0, n_rows)
+    assert out.tobytes() == O.quantize(x, vt).tobytes()
+
+
+def _matvec_case(kind, n_in, n_out, n_tok, seed, gen="workload"):
+    t = TYPES[kind]
+    nb = n_out * n_in // O.QK[t]
+    if gen == "workload":
+        w = random_blocks(kind, nb, np.random.default_rng(seed)).reshape(n_out, -1)
+    else:
+        w = ref_blocks(kind, nb, seed).reshape(n_out, -1)
+    x = np.random.default_rng(seed + 1).standard_normal((n_tok, n_in)).astype(np.float32)
+    xq = O.quantize(x, O.VEC_DOT[t])
+    return t, w, xq
+
+
+@pytest.mark.parametrize("kind", list(TYPES))
+@pytest.mark.parametrize("n_in,n_out,n_tok", [(256, 13, 1), (512, 13, 3), (2048, 37, 1), (768, 20, 5),
+                                              (11008, 9, 2), (4096, 16, 9), (2048, 64, 8)])
+def test_matvec_vs_oracle(kind, n_in, n_out, n_tok):
+    if kind in ("Q8_0", "Q4_0", "Q5_0") and n_in % 32:
+        pytest.skip("row not a whole number of blocks")
+    t, w, xq = _matvec_case(kind, n_in, n_out, n_tok, seed=n_in + n_out)
+    out = np.full((n_tok, n_out), np.nan, np.float32)
+    lib().op_matmul_q_rows(ptr(out), ptr(xq), ptr(w), t, n_tok, n_in, n_out, 0, n_out)
+    if t in (O.Q4_K, O.Q6_K):
+        # integer super-block sums and the reference's f32 combine order: identical bits
+        exp = O.matmul_q(w, t, xq, n_in, simd=1)
+        assert np.array_equal(bits(out), bits(exp))
+    else:
+        exp = O.matmul_q(w, t, xq, n_in, simd=0)
+        np.testing.assert_allclose(out, exp, rtol=1e-5, atol=1e-5 * float(np.abs(exp).max()))
+        exp2 = O.matmul_q(w, t, xq, n_in, simd=1)
+        np.testing.assert_allclose(out, exp2, rtol=1e-5, atol=1e-5 * float(np.abs(exp).max()))
+
+
+@pytest.mark.parametrize("kind", list(TYPES))
+def test_matvec_row_ranges(kind):
+    n_in, n_out, n_tok = 512, 13, 3
+    t, w, xq = _matvec_case(kind, n_in, n_out, n_tok, seed=10, gen="reference")
+    full = np.empty((n_tok, n_out), np.float32)
+    lib().op_matmul_q_rows(ptr(full), ptr(xq), ptr(w), t, n_tok, n_in, n_out, 0, n_out)
+    parts = np.full_like(full, np.nan)
+    for r0, r1 in [(0, 5), (5, 6), (6, n_out)]:
+        lib().op_matmul_q_rows(ptr(parts), ptr(xq), ptr(w), t, n_tok, n_in, n_out, r0, r1)
+    assert np.array_equal(bits(parts), bits(full))
+
+
+@pytest.mark.parametrize("kind", list(TYPES))
+def test_vec_dot(kind):
+    t = TYPES[kind]
+    n = 1024
+    w = ref_blocks(kind, n // O.QK[t], 6).reshape(-1)
+    x = np.random.default_rng(7).standard_normal(n).astype(np.float32)
+    xq = O.quantize(x, O.VEC_DOT[t]).reshape(-1)
+    got = lib().op_vec_dot_q(t, ptr(w), ptr(xq), n)
+    exp = float(O.matmul_q(w, t, xq, n, simd=0)[0, 0])
+    assert got == pytest.approx(exp, rel=1e-5, abs=1e-5)
+    wd = O.dequant(w, t, n).astype(np.float64)
+    assert abs(got - float(wd @ x)) <= 0.01 * float(np.linalg.norm(wd) * np.linalg.norm(x))
+
+
+def test_matvec_device_api_deterministic():
+    """Same inputs, two launches, identical bits; also checks the device-resident entry points."""
+    t = O.Q6_K
+    n_in, n_out = 2048, 1000
+    w = random_blocks("Q6_K", n_out * n_in // 256, np.random.default_rng(1)).reshape(n_out, -1)
+    x = np.random.default_rng(2).standard_normal(n_in).astype(np.float32)
+    L = lib()
+    m = capi.DeviceMatrix(t, n_in, n_out, w)
+    dx = capi.DeviceBuffer.from_array(x)
+    dq = capi.DeviceBuffer(O.row_size(O.Q8_K, n_in))
+    dout = capi.DeviceBuffer(n_out * 4)
+    capi.check(L.sdy_quantize(O.Q8_K, dx.ptr, dq.ptr, n_in, 1, None))
+    a = capi.SdyMvArgs(xq=dq.ptr, n_tok=1, out=dout.ptr, out_stride=n_out, row0=0, row1=n_out)
+    capi.check(L.sdy_matvec(ctypes.byref(m.m), ctypes.byref(a), None))
+    y1 = dout.to_array(np.float32, n_out)
+    capi.check(L.sdy_matvec(ctypes.byref(m.m), ctypes.byref(a), None))
+    y2 = dout.to_array(np.float32, n_out)
+    assert np.array_equal(bits(y1), bits(y2))
+    exp = O.matmul_q(w, t, O.quantize(x, O.Q8_K), n_in)[0]
+    assert np.array_equal(bits(y1), bits(exp))
+
+
+@pytest.mark.parametrize("wtype", [O.F32, O.F16, O.BF16], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("n_tok", [1, 3, 4, 9])
+@pytest.mark.parametrize("n_in", [67, 96])
+def test_float_matmul(wtype, n_tok, n_in):
+    rng = np.random.default_rng(0)
+    n_out = 45
+    x = rng.standard_normal((n_tok, n_in)).astype(np.float32)
+    w32 = rng.standard_normal((n_out, n_in)).astype(np.float32)
+    if wtype == O.F16:
+        w = w32.astype(np.float16)
+        w_ref = w.astype(np.float32)
+    elif wtype == O.BF16:
+        b = w32.view(np.uint32)
+        w = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+        w_ref = (w.astype(np.uint32) << 16).view(np.float32)
+    else:
+        w, w_ref = w32, w32
+    w = np.ascontiguousarray(w)
+    out = np.empty((n_tok, n_out), np.float32)
+    lib().op_matmul(ptr(out), ptr(x), ptr(w), wtype, n_tok, n_in, n_out)
+    np.testing.assert_allclose(out, x @ w_ref.T, rtol=1e-5, atol=1e-5)
+    parts = np.full_like(out, np.nan)
+    for r0, r1 in [(0, 10), (10, 30), (30, n_out)]:
+        lib().op_matmul_rows(ptr(parts), ptr(x), ptr(w), wtype, n_tok, n_in, n_out, r0, r1)
+    assert np.array_equal(bits(parts), bits(out))
+
+
+def test_rmsnorm_softmax_silu():
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(300) * 5).astype(np.float32)
+    w = rng.standard_normal(300).astype(np.float32)
+    out = np.empty_like(x)
+    lib().op_rmsnorm(ptr(out), ptr(x), ptr(w), x.size, 1e-5)
+    exp = np.empty_like(x)
+    O.lib().orc_rmsnorm(ptr(exp), ptr(x), ptr(w), x.size, 1e-5)
+    assert np.array_equal(bits(out), bits(exp))  # double sum, one float rounding: same bits
+    s = np.array([1000.0, 1001.0, -50.0, 3.0], np.float32)
+    e = s.copy()
+    O.lib().orc_softmax(ptr(e), e.size)
+    lib().op_softmax(ptr(s), s.size)
+    np.testing.assert_allclose(s, e, rtol=1e-6)
+    g = np.array([-100.0, -1.0, 0.0, 2.0, 50.0], np.float32)
+    up = np.array([3.0, 2.0, 1.0, -1.0, 0.5], np.float32)
+    e = g.copy()
+    O.lib().orc_silu_mul(ptr(e), ptr(up), g.size)
+    lib().op_silu_mul(ptr(g), ptr(up), g.size)
+    np.testing.assert_allclose(g, e, rtol=1e-6, atol=1e-30)
+
+
+@pytest.mark.parametrize("interleaved", [0, 1], ids=["neox", "interleaved"])
+def test_rope(interleaved):
+    n_pos, hd, n_heads, theta = 40, 16, 3, 10000.0
+    cos, sin = np.empty((n_pos, hd // 2), np.float32), np.empty((n_pos, hd // 2), np.float32)
+    lib().op_rope_table(ptr(cos), ptr(sin), n_pos, hd, theta)
+    ec, es = np.empty_like(cos), np.empty_like(sin)
+    O.lib().orc_rope_table(ptr(ec), ptr(es), n_pos, hd, theta)
+    np.testing.assert_allclose(cos, ec, atol=1e-7)
+    np.testing.assert_allclose(sin, es, atol=1e-7)
+    x = np.random.default_rng(2).standard_normal((n_heads, hd)).astype(np.float32)
+    e = x.copy()
+    rc, rs = np.ascontiguousarray(ec[33]), np.ascontiguousarray(es[33])
+    O.lib().orc_rope(ptr(e), n_heads, hd, ptr(rc), ptr(rs), interleaved)
+    lib().op_rope(ptr(x), n_heads, hd, ptr(rc), ptr(rs), interleaved)
+    assert np.array_equal(bits(x), bits(e))
+
+
+@pytest.mark.parametrize("n_kv", [1, 13, 64, 65, 200])
+def test_attention_gqa(n_kv):
+    rng = np.random.default_rng(3)
+    n_head, n_kv_head, hd, stride = 6, 2, 8, 256
+    q = rng.standard_normal((n_head, hd)).astype(np.float32)
+    kc = rng.standard_normal((n_kv_head, stride, hd)).astype(np.float32)
+    vc = rng.standard_normal((n_kv_head, stride, hd)).astype(np.float32)
+    out = np.empty_like(q)
+    scores = np.empty(stride, np.float32)
+    lib().op_attention(ptr(out), ptr(q), ptr(kc), ptr(vc), n_head, n_kv_head, hd, n_kv, stride, ptr(scores))
+    exp = np.empty_like(q)
+    O.lib().orc_attention(ptr(exp), ptr(q), ptr(kc), ptr(vc), n_head, n_kv_head, hd, n_kv, stride, ptr(scores), 1)
+    np.testing.assert_allclose(out, exp, rtol=1e-5, atol=1e-6)
+
+
+def test_dot_axpy_add():
+    rng = np.random.default_rng(4)
+    for n in (1, 7, 8, 64, 100):
+        a, b = rng.standard_normal((2, n)).astype(np.float32)
+        assert lib().op_dot_f32(ptr(a), ptr(b), n) == pytest.approx(float(a.astype(np.float64) @ b), rel=1e-5, abs=1e-5)
+        y = rng.standard_normal(n).astype(np.float32)
+        expected = y + np.float32(0.5) * a
+        lib().op_axpy(ptr(y), 0.5, ptr(a), n)
+        np.testing.assert_allclose(y, expected, rtol=1e-6, atol=1e-6)
+    a = rng.standard_normal(1023).astype(np.float32)
+    b = rng.standard_normal(1023).astype(np.float32)
+    np.testing.assert_array_equal(capi.add(a, b), a + b)
