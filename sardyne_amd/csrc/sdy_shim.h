@@ -37,6 +37,8 @@ int sdy_event_new(void **ev);
 int sdy_event_record(void *ev, sdy_stream s);
 int sdy_event_elapsed(float *ms, void *e0, void *e1); /* waits for e1 */
 int sdy_event_free(void *ev);
+/* reads every byte of buf once (HBM bandwidth probe); sink: 4 bytes of device memory */
+int sdy_membw_read(const void *buf, size_t bytes, void *sink, sdy_stream s);
 
 /* ---- weight matrices in the device layout (planes, see quant_kernels.hip) */
 typedef struct {

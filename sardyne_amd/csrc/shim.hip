@@ -167,3 +167,21 @@ extern "C" int sdy_event_free(void *ev) {
     HIPCK(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy");
     return 0;
 }
+
+// ---- HBM read-bandwidth probe: every byte of buf read once with 16-byte loads (a grid-stride
+// sweep), an XOR of the data kept live so the loads are not removed.
+__global__ void k_membw_read(const uint4 *__restrict__ p, size_t n16, unsigned *sink) {
+    size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x, stride = (size_t)gridDim.x * blockDim.x;
+    unsigned acc = 0;
+    for (; i < n16; i += stride) {
+        uint4 v = p[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+extern "C" int sdy_membw_read(const void *buf, size_t bytes, void *sink, sdy_stream s) {
+    hipLaunchKernelGGL(k_membw_read, dim3(2048), dim3(256), 0, (hipStream_t)s, (const uint4 *)buf, bytes / 16,
+                       (unsigned *)sink);
+    return sdy_check_launch("membw_read");
+}

@@ -173,6 +173,7 @@ class ModelSpec:
     router_std: float = 0.02
     norm_value: float = 1.0
     bias_std: float = 0.02
+    type_fn: object = None  # optional name -> weight type override for quantized matrices
 
 
 def qwen25_3b(n_layer=36) -> ModelSpec:
@@ -227,6 +228,17 @@ def write_model(path, spec: ModelSpec, seed: int = 0) -> Path:
         return s[0]
 
     norm = lambda n: np.full(n, spec.norm_value, np.float32)
+    orig_add = b.add_tensor
+
+    def add_matrix(name, ne, tname, produce):
+        t = spec.type_fn(name) if spec.type_fn else None
+        if t and t != tname and tname not in ("F32", "F16", "BF16"):
+            n_out = int(np.prod(ne[1:]))
+            produce = _matrix_producer(t, n_out, ne[0], nxt())
+            tname = t
+        orig_add(name, ne, tname, produce)
+
+    b.add_tensor = add_matrix
     b.add_tensor("token_embd.weight", (dim, spec.n_vocab), spec.t_embd,
                  _matrix_producer(spec.t_embd, spec.n_vocab, dim, nxt()))
     b.add_array("output_norm.weight", norm(dim))

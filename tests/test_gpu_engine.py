@@ -1,0 +1,137 @@
+"""The GPU engine (engine_* of build/libsardyne.so) against the oracle forward (oracle/orc_model.c,
+bit-exact with the compiled reference) on small synthetic GGUF models, following the reference's
+runtime and MoE tests (tests/test_runtime.py:180-283, tests/test_moe.py:274-406)."""
+import numpy as np
+import pytest
+
+import oracle as O
+from sardyne_amd.gguf_synth import ModelSpec, write_model
+from sardyne_amd.runtime import Context, Model, generate
+
+pytestmark = pytest.mark.gpu
+
+TOKENS = [3, 14, 15, 9, 26, 5, 35, 8, 2, 7, 1, 60]
+
+
+def kquant_moe_types(name):
+    """The mix of a published Q4_K_M MoE file (tests/test_moe.py:265-271): K-quants where rows allow,
+    Q5_0 for ffn_down."""
+    if "ffn_down" in name:
+        return "Q5_0"
+    return "Q6_K" if "ffn_up" in name or "attn_output" in name else "Q4_K"
+
+
+SPECS = {
+    "qwen2-kquant": ModelSpec(n_vocab=300, dim=256, n_layer=2, n_head=4, n_kv_head=2, head_dim=64, ffn_dim=512,
+                              context=64),
+    "qwen2-q0": ModelSpec(n_vocab=300, dim=256, n_layer=2, n_head=4, n_kv_head=2, head_dim=64, ffn_dim=512,
+                          context=64, t_default="Q8_0", t_attn_v="Q4_0", t_ffn_down="Q5_0", t_output="Q8_0",
+                          t_embd="Q4_0"),
+    "llama-kquant": ModelSpec(arch="llama", n_vocab=300, dim=256, n_layer=2, n_head=4, n_kv_head=4, head_dim=64,
+                              ffn_dim=512, context=64, qkv_bias=False, tied=True, t_embd="Q6_K"),
+    "qwen3-q8": ModelSpec(arch="qwen3", n_vocab=300, dim=128, n_layer=2, n_head=4, n_kv_head=2, head_dim=32,
+                          ffn_dim=192, context=64, qkv_bias=False, qk_norm=True, t_default="Q8_0", t_attn_v="Q8_0",
+                          t_ffn_down="Q8_0", t_output="Q8_0", t_embd="Q8_0"),
+    "moe-kquant": ModelSpec(arch="qwen3moe", n_vocab=300, dim=256, n_layer=2, n_head=4, n_kv_head=2, head_dim=64,
+                            ffn_dim=480, context=64, n_expert=8, n_expert_used=3, ffn_exp_dim=160, qkv_bias=False,
+                            qk_norm=True, router_std=0.3, type_fn=kquant_moe_types, t_output="Q8_0", t_embd="Q8_0"),
+    "moe-128x8": ModelSpec(arch="qwen3moe", n_vocab=300, dim=256, n_layer=2, n_head=4, n_kv_head=2, head_dim=64,
+                           ffn_dim=2048, context=64, n_expert=128, n_expert_used=8, ffn_exp_dim=256, qkv_bias=False,
+                           qk_norm=True, router_std=0.3),
+}
+
+
+@pytest.fixture(scope="module", params=sorted(SPECS))
+def model_path(request, tmp_path_factory):
+    path = tmp_path_factory.mktemp(request.param) / "m.gguf"
+    write_model(path, SPECS[request.param], seed=11)
+    return path
+
+
+def assert_close(got, ref):
+    # random quantized blocks give large logits: the tolerance follows their scale
+    # (tests/test_moe.py:297-299 of the reference)
+    np.testing.assert_allclose(got, ref, atol=1e-4 * max(1.0, float(np.abs(ref).max())), rtol=0)
+
+
+def test_forward_matches_oracle(model_path):
+    ref = O.OracleContext(model_path, 32, n_batch=len(TOKENS), logits_all=True).eval(TOKENS)
+    got = Context(Model(model_path), max_seq=32, n_batch=len(TOKENS), logits_all=True).eval(TOKENS)
+    assert_close(got, ref)
+    assert np.mean(got.argmax(-1) == ref.argmax(-1)) == 1.0
+
+
+def test_kv_cache_and_batching(model_path):
+    model = Model(model_path)
+    full = Context(model, max_seq=32, n_batch=len(TOKENS), logits_all=True).eval(TOKENS)
+    chunked = Context(model, max_seq=32, n_batch=5, logits_all=True).eval(TOKENS)
+    assert_close(chunked, full)
+    ctx = Context(model, max_seq=32, n_batch=4)
+    assert_close(ctx.eval(TOKENS[:7]), full[6])
+    for i, t in enumerate(TOKENS[7:], start=7):
+        assert_close(ctx.eval([t]), full[i])
+    assert ctx.n_past == len(TOKENS)
+    ctx.reset()
+    assert ctx.n_past == 0
+    assert_close(ctx.eval(TOKENS), full[-1])
+
+
+def test_deterministic(model_path):
+    model = Model(model_path)
+    a = Context(model, max_seq=32, n_batch=len(TOKENS), logits_all=True).eval(TOKENS)
+    b = Context(model, max_seq=32, n_batch=len(TOKENS), logits_all=True, n_threads=7).eval(TOKENS)
+    assert np.array_equal(a, b)
+
+
+def test_generate_matches_oracle(model_path):
+    ref = O.OracleContext(model_path, 32, n_batch=64)
+    toks, out = list(TOKENS[:4]), []
+    logits = ref.eval(toks)
+    for _ in range(12):
+        nxt = int(np.argmax(logits))
+        out.append(nxt)
+        logits = ref.eval([nxt])
+    assert generate(Context(Model(model_path), max_seq=32), TOKENS[:4], 12) == out
+
+
+def test_truncate(model_path):
+    model = Model(model_path)
+    full = Context(model, max_seq=32, n_batch=len(TOKENS), logits_all=True).eval(TOKENS)
+    ctx = Context(model, max_seq=32, n_batch=4)
+    ctx.eval(TOKENS[:7])
+    ctx.truncate(3)
+    assert ctx.n_past == 3
+    ctx.eval([60, 61])
+    ctx.truncate(3)
+    assert_close(ctx.eval(TOKENS[3:]), full[-1])
+    for bad in (-1, len(TOKENS) + 1):
+        with pytest.raises(ValueError, match="posizione"):
+            ctx.truncate(bad)
+
+
+def test_errors_leave_context_unchanged(model_path):
+    model = Model(model_path)
+    ctx = Context(model, max_seq=8, n_batch=4)
+    ctx.eval([1, 2, 3])
+    for bad, msg in [([1] * 6, "contesto pieno"), ([300], "vocabolario"), ([-1], "vocabolario"), ([], "nessun")]:
+        with pytest.raises(ValueError, match=msg):
+            ctx.eval(bad)
+        assert ctx.n_past == 3
+    with pytest.raises(ValueError, match="n_batch"):
+        Context(model, max_seq=8, n_batch=0)
+    with pytest.raises(ValueError, match="max_seq"):
+        Context(model, max_seq=0)
+    with pytest.raises(ValueError, match="n_threads"):
+        Context(model, max_seq=8, n_threads=-1)
+    all_ctx = Context(model, max_seq=16, n_batch=2, logits_all=True)
+    assert all_ctx.eval([1, 2, 3, 4, 5]).shape == (5, model.info.n_vocab)
+
+
+def test_info(model_path):
+    from sardyne_amd.gguf_synth import read_tensors
+    meta, tensors, _, _ = read_tensors(model_path)
+    i = Model(model_path).info
+    arch = meta["general.architecture"]
+    assert i.dim == meta[f"{arch}.embedding_length"] and i.n_layer == meta[f"{arch}.block_count"]
+    assert i.n_vocab == tensors["token_embd.weight"][0][1]
+    assert bool(i.tied_embeddings) == ("output.weight" not in tensors)
