@@ -260,14 +260,86 @@ def bench_matvec(args, wt, n_out, n_in, n_copies, stacked):
     return line
 
 
+# ---------------------------------------------------------------- decode workloads
+
+def bench_decode(args, spec, ctx_len, n_decode, label):
+    """Decode tok/s after a ctx_len-token context at batch 1 (the method of the reference's
+    bench/bench_decode.py:39-48: n_decode / wall time of the decode loop). Token ids are uniform
+    over the vocabulary (seeded) and fed teacher-forced, so the GPU and the CPU reference see the
+    same sequence and their logits are compared step by step."""
+    from sardyne_amd.gguf_synth import write_model
+    from sardyne_amd.runtime import Context, Model
+    tmpdir = Path(os.environ.get("SARDYNE_BENCH_DIR", "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()))
+    path = tmpdir / f"sardyne_bench_{label}.gguf"
+    t0 = time.perf_counter()
+    write_model(path, spec, seed=0)
+    log(f"[bench] wrote {path} ({path.stat().st_size / 1e9:.2f} GB) in {time.perf_counter() - t0:.1f}s")
+    rng = np.random.default_rng(0)
+    toks = rng.integers(0, spec.n_vocab, ctx_len + n_decode).astype(np.int32)
+    try:
+        t0 = time.perf_counter()
+        model = Model(path)
+        log(f"[bench] GPU model load {time.perf_counter() - t0:.1f}s")
+        ctx = Context(model, max_seq=ctx_len + n_decode + 1, n_batch=args.n_batch)
+        t0 = time.perf_counter()
+        ctx.eval(toks[:ctx_len])
+        t_prefill = time.perf_counter() - t0
+        gpu_logits = []
+        t0 = time.perf_counter()
+        for i in range(n_decode):
+            gpu_logits.append(ctx.eval([int(toks[ctx_len + i])]))
+        t_dec = time.perf_counter() - t0
+        gpu_tok_s = n_decode / t_dec
+        log(f"[bench] GPU prefill {ctx_len} tok in {t_prefill:.3f}s, decode {gpu_tok_s:.1f} tok/s")
+        del ctx, model
+    finally:
+        pass
+    cpu = None
+    parity = {}
+    if args.cpu_seconds > 0:
+        try:
+            import oracle as O
+            if O.ref_available():
+                n_cpu = os.cpu_count() or 1
+                eng = O.RefEngine(path, ctx_len + n_decode + 1, n_batch=64, n_threads=0)
+                t0 = time.perf_counter()
+                eng.eval(toks[:ctx_len])
+                t_pre_cpu = time.perf_counter() - t0
+                n_cpu_steps, cpu_logits = 0, []
+                t0 = time.perf_counter()
+                while n_cpu_steps < n_decode and (time.perf_counter() - t0 < args.cpu_seconds or n_cpu_steps < 4):
+                    cpu_logits.append(eng.eval([int(toks[ctx_len + n_cpu_steps])]))
+                    n_cpu_steps += 1
+                t_cpu = time.perf_counter() - t0
+                cpu = {"value": round(n_cpu_steps / t_cpu, 3), "unit": "tok/s", "cores": eng.n_threads,
+                       "kind": "reference",
+                       "sample": f"reference engine, {n_cpu_steps} decode steps after a {ctx_len}-token prefill "
+                                 f"(prefill {ctx_len / t_pre_cpu:.1f} tok/s, n_batch 64), {host_cpu_model()}"}
+                g = np.stack(gpu_logits[:n_cpu_steps])
+                c = np.stack(cpu_logits)
+                maxabs = float(np.abs(g - c).max())
+                parity = {"steps_compared": n_cpu_steps, "logits_max_abs": maxabs,
+                          "logits_max_abs_over_max_ref": maxabs / float(np.abs(c).max()),
+                          "greedy_argmax_agreement": float(np.mean(g.argmax(-1) == c.argmax(-1)))}
+        except Exception as ex:
+            cpu = {"error": str(ex)}
+    try:
+        path.unlink()
+    except OSError:
+        pass
+    return gpu_tok_s, t_prefill, cpu, parity
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="q6k_head",
-                    choices=["q6k_head", "q8_0_head", "q4k_matvec"])
+                    choices=["q6k_head", "q8_0_head", "q4k_matvec", "decode_3b"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--n-batch", type=int, default=512, help="GPU prefill chunk (decode workloads)")
+    ap.add_argument("--layers", type=int, default=0, help="override the layer count (smoke runs only)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -278,8 +350,30 @@ def main():
         line = bench_matvec(args, Q6_K, 151936, 2048, 8, stacked=False)
     elif args.workload == "q8_0_head":
         line = bench_matvec(args, Q8_0, 151936, 2048, 8, stacked=False)
-    else:
+    elif args.workload == "q4k_matvec":
         line = bench_matvec(args, Q4_K, 2048, 2048, 448, stacked=True)
+    else:
+        from sardyne_amd.gguf_synth import qwen25_3b
+        spec = qwen25_3b(args.layers or 36)
+        n_dec = max(args.steps, 8)
+        tok_s, t_pre, cpu, parity = bench_decode(args, spec, 512, n_dec, "qwen25_3b")
+        w_bytes = 2031000704  # weights read per token (see the roofline note in the design)
+        kv_mean = 73728 * (512 + n_dec / 2)
+        line = {"metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": n_dec,
+                "warmup": 0, "ms_per_step": round(1e3 / tok_s, 4), "higher_is_better": True, "scaling": "weak",
+                "vs_baseline": None, "dtype": "int8 activations x Q4_K/Q6_K weights, f32 elsewhere",
+                "data": "synthetic (random-init Q4_K_M weights, uniform token ids)",
+                "config": {"workload": f"Qwen2.5-3B-shaped Q4_K_M decode, batch 1, {n_dec} tokens after a "
+                                       f"512-token context", "n_layer": spec.n_layer, "dim": spec.dim,
+                           "heads": f"{spec.n_head}/{spec.n_kv_head}", "ffn": spec.ffn_dim, "vocab": spec.n_vocab},
+                "prefill_512_s": round(t_pre, 4),
+                "roofline": {"bound": "hbm", "achieved": round((w_bytes + kv_mean) * tok_s / 1e9, 1),
+                             "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                             "frac": round((w_bytes + kv_mean) * tok_s / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                             "kernel": "whole decode step (weights + mean KV bytes per token)"},
+                "cpu_baseline": cpu, "parity": parity}
+        if cpu and "value" in cpu:
+            line["gpu_over_cpu"] = round(tok_s / cpu["value"], 1)
     print(json.dumps(line), flush=True)
 
 

@@ -42,6 +42,16 @@ struct Planes {
 
 SDY_DEV uint4 ld16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 SDY_DEV uint32_t ld4(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
+// Weight loads: every weight byte is read once per matvec, so full-line plane loads are issued
+// non-temporal (streamed past the caches). Sub-line planes that neighbouring waves share (the
+// Q6_K d plane: 32 bytes per iteration) keep normal loads so the line is fetched once.
+typedef unsigned int sdy_u32x4 __attribute__((ext_vector_type(4)));
+SDY_DEV uint4 ldw16(const uint8_t *p) {
+    sdy_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const sdy_u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+SDY_DEV uint32_t ldw4(const uint8_t *p) { return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p)); }
+SDY_DEV uint16_t ldw2(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
 
 // ------------------------------------------------------------------------------------ repack
 
@@ -290,6 +300,15 @@ __global__ void k_quant_q8_0(const float *__restrict__ x, uint8_t *__restrict__ 
 //   Y  [MT][4][T] x 16 B   y bytes of unit u, 16-byte chunk q (conflict-free ds_read_b128)
 //   K-quants: BS [MT][T] x 8 B (bsums 4j..4j+3 of the unit)   YD [MT][nb] floats (Q8_K d)
 //   32-element types: DX [MT][T] x 8 B (two f32 scales)   SY [MT][T] x 8 B (two int sums of y)
+// followed by one term buffer per wave: [rb rows][MT tokens][nterm] floats.
+//
+// Work decomposition. Rows are cut into batches of rb rows; the (row, unit) tasks of a batch are
+// spread over ceil(rb*T/64) wave iterations (64 lanes, one unit each; a last partial iteration
+// leaves lanes idle). Each wave owns one contiguous, balanced range of batches and walks it as one
+// flat sequence of iterations, loading the weights of the next iteration while it computes the
+// current one, across batch boundaries. At the end of a batch the wave sums the terms of each
+// (row, token) in block order (phase 2). rb is the smallest row count with at least 64 tasks, so
+// small matrices still spread over every CU.
 struct MvArgs {
     Planes P;
     const uint8_t *xq;
@@ -298,8 +317,10 @@ struct MvArgs {
     long out_stride;
     const float *bias, *resid;
     long row0, row1;
-    int rb;      // rows per wave batch (rb * T is a multiple of 64)
+    int rb;      // rows per batch
+    int ipb;     // wave iterations per batch = ceil(rb * T / 64)
     int nterm;   // f32 terms per row and token (super-blocks or units)
+    int q64, r64;  // 64 / T and 64 % T: advance of a lane's (row, unit) per iteration
 };
 
 constexpr bool is_k(int wt) { return wt == SDY_Q4_K || wt == SDY_Q6_K; }
@@ -361,45 +382,65 @@ struct WRegs {
     uint32_t f, g;
 };
 
+// Loads one unit of one row (row and unit given as indices into the planes).
 template <int WT>
-SDY_DEV void load_w(const Planes &P, long row, int u, WRegs<WT> &r) {
-    const size_t ou = ((size_t)row * P.T + u) * 16;
+SDY_DEV void load_w(const Planes &P, uint32_t row, uint32_t u, WRegs<WT> &r) {
+    const uint32_t ou = (row * (uint32_t)P.T + u) * 16u;
     if constexpr (WT == SDY_Q4_K) {
-        r.a = ld16(P.p[0] + ou);
-        r.b = ld16(P.p[1] + ou);
-        r.c = ld16(P.p[2] + ((size_t)row * P.nb + (u >> 2)) * 16);
+        r.a = ldw16(P.p[0] + ou);
+        r.b = ldw16(P.p[1] + ou);
+        r.c = ldw16(P.p[2] + (row * (uint32_t)P.nb + (u >> 2)) * 16u);
     } else if constexpr (WT == SDY_Q6_K) {
-        const size_t os = (size_t)row * P.nb + (u >> 2);
-        r.a = ld16(P.p[0] + ou);
-        r.b = ld16(P.p[1] + ou);
-        r.c = ld16(P.p[2] + ou);
-        r.f = ld4(P.p[3] + os * 16 + 4 * (u & 3));
-        r.g = *reinterpret_cast<const uint16_t *>(P.p[4] + os * 2);
+        const uint32_t os = row * (uint32_t)P.nb + (u >> 2);
+        r.a = ldw16(P.p[0] + ou);
+        r.b = ldw16(P.p[1] + ou);
+        r.c = ldw16(P.p[2] + ou);
+        r.f = ldw4(P.p[3] + os * 16u + 4u * (u & 3u));
+        r.g = ldw2(P.p[4] + os * 2u);
     } else if constexpr (WT == SDY_Q8_0) {
-        r.a = ld16(P.p[0] + ou);
-        r.b = ld16(P.p[1] + ou);
-        r.c = ld16(P.p[2] + ou);
-        r.e = ld16(P.p[3] + ou);
-        r.f = ld4(P.p[4] + ((size_t)row * P.T + u) * 4);
+        r.a = ldw16(P.p[0] + ou);
+        r.b = ldw16(P.p[1] + ou);
+        r.c = ldw16(P.p[2] + ou);
+        r.e = ldw16(P.p[3] + ou);
+        r.f = ldw4(P.p[4] + (row * (uint32_t)P.T + u) * 4u);
     } else {
-        r.a = ld16(P.p[0] + ou);
-        r.b = ld16(P.p[1] + ou);
-        r.f = ld4(P.p[4] + ((size_t)row * P.T + u) * 4);
+        r.a = ldw16(P.p[0] + ou);
+        r.b = ldw16(P.p[1] + ou);
+        r.f = ldw4(P.p[4] + (row * (uint32_t)P.T + u) * 4u);
         if constexpr (WT == SDY_Q5_0) {
-            const uint8_t *q = P.p[2] + ((size_t)row * P.T + u) * 8;
-            r.c.x = ld4(q);
-            r.c.y = ld4(q + 4);
+            const uint8_t *q = P.p[2] + (row * (uint32_t)P.T + u) * 8u;
+            r.c.x = ldw4(q);
+            r.c.y = ldw4(q + 4);
         }
     }
 }
 
 SDY_DEV uint32_t w4(const uint4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
+// Scales and mins of the Q4_K sub-block pair (2j, 2j+1) from the 12 scale bytes held in the
+// dwords A (bytes 0-3), B (4-7), C (8-11) (csrc/quant.h:72-80), with shifts and masks only.
+SDY_DEV void q4k_pair(uint32_t A, uint32_t B, uint32_t C, int j, int &sc0, int &sc1, int &m0, int &m1) {
+    const uint32_t sh = (j & 1) ? 16u : 0u;
+    const uint32_t a = (A >> sh) & 0xFFFFu, b = (B >> sh) & 0xFFFFu, c = (C >> sh) & 0xFFFFu;
+    uint32_t sc, m;
+    if (j < 2) {
+        sc = a & 0x3F3Fu;
+        m = b & 0x3F3Fu;
+    } else {
+        sc = (c & 0x0F0Fu) | ((a >> 2) & 0x3030u);
+        m = ((c >> 4) & 0x0F0Fu) | ((b >> 2) & 0x3030u);
+    }
+    sc0 = (int)(sc & 255u);
+    sc1 = (int)(sc >> 8);
+    m0 = (int)(m & 255u);
+    m1 = (int)(m >> 8);
+}
+
 // One unit of one token: K-quants return the lane's integer parts (isum, msum), the 32-element
 // types return the unit's f32 term directly.
 template <int WT>
-SDY_DEV void unit_dot(const WRegs<WT> &r, const uint4 *Y, const uint8_t *aux, int u, int &isum, int &msum,
-                      float &term, const float *dxp, const int *syp) {
+SDY_DEV void unit_dot(const WRegs<WT> &r, const uint4 *Y, uint2 bsp, int u, int &isum, int &msum, float &term,
+                      float2 dxp, int2 syp) {
     constexpr uint32_t LO = 0x0F0F0F0Fu;
     if constexpr (WT == SDY_Q4_K) {
         int slo = 0, shi = 0;
@@ -411,16 +452,15 @@ SDY_DEV void unit_dot(const WRegs<WT> &r, const uint4 *Y, const uint8_t *aux, in
             shi = sdy_dot4((int)((qa >> 4) & LO), (int)w4(Y[2], w), shi);
             shi = sdy_dot4((int)((qb >> 4) & LO), (int)w4(Y[3], w), shi);
         }
-        const int j = u & 3, k0 = 2 * j, k1 = 2 * j + 1;
-        const uint8_t *sc = reinterpret_cast<const uint8_t *>(&r.c) + 4;
-        int sc0 = q4k_scale(sc, k0, 0), sc1 = q4k_scale(sc, k1, 0);
-        int m0 = q4k_scale(sc, k0, 1), m1 = q4k_scale(sc, k1, 1);
-        const int16_t *bs = reinterpret_cast<const int16_t *>(aux);
+        int sc0, sc1, m0, m1;
+        q4k_pair(r.c.y, r.c.z, r.c.w, u & 3, sc0, sc1, m0, m1);
+        const int b0 = (int)(int16_t)(bsp.x & 0xFFFFu), b1 = (int)(int16_t)(bsp.x >> 16);
+        const int b2 = (int)(int16_t)(bsp.y & 0xFFFFu), b3 = (int)(int16_t)(bsp.y >> 16);
         isum = sc0 * slo + sc1 * shi;
-        msum = m0 * ((int)bs[0] + (int)bs[1]) + m1 * ((int)bs[2] + (int)bs[3]);
+        msum = m0 * (b0 + b1) + m1 * (b2 + b3);
     } else if constexpr (WT == SDY_Q6_K) {
-        const int16_t *bs = reinterpret_cast<const int16_t *>(aux);
-        int acc0 = -32 * bs[0], acc1 = -32 * bs[1], acc2 = -32 * bs[2], acc3 = -32 * bs[3];
+        int acc0 = -32 * (int)(int16_t)(bsp.x & 0xFFFFu), acc1 = -32 * (int)(int16_t)(bsp.x >> 16);
+        int acc2 = -32 * (int)(int16_t)(bsp.y & 0xFFFFu), acc3 = -32 * (int)(int16_t)(bsp.y >> 16);
 #pragma unroll
         for (int w = 0; w < 4; w++) {
             uint32_t n0 = w4(r.a, w), n1 = w4(r.b, w), h = w4(r.c, w);
@@ -462,19 +502,21 @@ SDY_DEV void unit_dot(const WRegs<WT> &r, const uint4 *Y, const uint8_t *aux, in
                     acc = sdy_dot4((int)lo, (int)w4(Y[2 * h], w), acc);
                     acc = sdy_dot4((int)hi, (int)w4(Y[2 * h + 1], w), acc);
                 }
-                acc -= (WT == SDY_Q4_0 ? 8 : 16) * syp[h];
+                acc -= (WT == SDY_Q4_0 ? 8 : 16) * (h ? syp.y : syp.x);
             }
             s[h] = acc;
         }
         float dw0 = sdy_h2f((uint16_t)(r.f & 0xFFFFu)), dw1 = sdy_h2f((uint16_t)(r.f >> 16));
-        float f0 = dw0 * dxp[0], f1 = dw1 * dxp[1];
+        float f0 = dw0 * dxp.x, f1 = dw1 * dxp.y;
         float t0 = (float)s[0] * f0, t1 = (float)s[1] * f1;
         term = t0 + t1;
         isum = msum = 0;
     }
 }
 
-template <int WT, int MT>
+// YREG: every lane keeps the same unit for the whole kernel (64 % T == 0, one token), so its
+// activation slice lives in registers instead of being re-read from LDS.
+template <int WT, int MT, bool YREG>
 __global__ __launch_bounds__(THREADS) void k_matvec(MvArgs a) {
     extern __shared__ uint8_t lds[];
     const int T = a.P.T, nb = a.P.nb;
@@ -488,79 +530,236 @@ __global__ __launch_bounds__(THREADS) void k_matvec(MvArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     float *terms = reinterpret_cast<float *>(lds + act_bytes) + (size_t)wave * a.rb * MT * a.nterm;
 
-    const int rb = a.rb, tasks = rb * T, n_it = tasks / 64;
+    const int rb = a.rb, ipb = a.ipb, tasks = rb * T;
     const long n_rows = a.row1 - a.row0;
     const long n_batches = (n_rows + rb - 1) / rb;
-    for (long bt = (long)blockIdx.x * WAVES + wave; bt < n_batches; bt += (long)gridDim.x * WAVES) {
-        const long rbase = a.row0 + bt * rb;
-        WRegs<WT> cur, nxt;
-        auto task_row = [&](int it, int &rl, int &u) {
-            int task = it * 64 + lane;
-            rl = task / T;
-            u = task - rl * T;
-        };
-        int rl, u;
-        task_row(0, rl, u);
-        load_w<WT>(a.P, rbase + rl < a.row1 ? rbase + rl : rbase, u, cur);
-        for (int it = 0; it < n_it; it++) {
-            int rl_c = rl, u_c = u;
-            if (it + 1 < n_it) {
-                task_row(it + 1, rl, u);
-                load_w<WT>(a.P, rbase + rl < a.row1 ? rbase + rl : rbase, u, nxt);
+    const long n_waves = (long)gridDim.x * WAVES, wid = (long)blockIdx.x * WAVES + wave;
+    const long b_begin = n_batches * wid / n_waves, b_end = n_batches * (wid + 1) / n_waves;
+    if (b_begin >= b_end) return;
+    const int rl0 = lane / T, u0 = lane - rl0 * T;  // lane's (row, unit) in the first iteration of a batch
+
+    uint4 Yr[4];
+    uint2 bsr = make_uint2(0u, 0u);
+    if constexpr (YREG) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) Yr[q] = *reinterpret_cast<const uint4 *>(lds + (q * T + u0) * 16);
+        if constexpr (is_k(WT)) bsr = *reinterpret_cast<const uint2 *>(aux_base + u0 * 8);
+    }
+
+    // the lane's task in (batch b, iteration i): rl, u; validity: task < tasks and row < row1
+    long b = b_begin;
+    int it = 0, rl = rl0, u = u0;
+    auto row_of = [&](long bb, int rr) -> long { return a.row0 + bb * rb + rr; };
+    auto lane_ok = [&](long bb, int itx, int rr) -> bool {
+        return itx * 64 + lane < tasks && row_of(bb, rr) < a.row1;
+    };
+    WRegs<WT> cur, nxt;
+    {
+        long row = lane_ok(b, it, rl) ? row_of(b, rl) : a.row0;
+        load_w<WT>(a.P, (uint32_t)(row - 0), (uint32_t)(lane_ok(b, it, rl) ? u : 0), cur);
+    }
+    for (;;) {
+        // advance a copy of the position to the next iteration and prefetch it
+        long nb_ = b;
+        int nit = it + 1, nrl = rl + a.q64, nu = u + a.r64;
+        if (nu >= T) {
+            nu -= T;
+            nrl++;
+        }
+        if (nit == ipb) {
+            nit = 0;
+            nb_ = b + 1;
+            nrl = rl0;
+            nu = u0;
+        }
+        const bool more = nb_ < b_end;
+        if (more) {
+            const bool ok = lane_ok(nb_, nit, nrl);
+            load_w<WT>(a.P, (uint32_t)(ok ? row_of(nb_, nrl) : a.row0), (uint32_t)(ok ? nu : 0), nxt);
+        }
+        const bool valid = lane_ok(b, it, rl);
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            if (m >= a.n_tok) break;
+            uint4 Y[4];
+            uint2 bsp = bsr;
+            if constexpr (YREG) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) Y[q] = Yr[q];
+            } else {
+                const int uu = valid ? u : 0;
+#pragma unroll
+                for (int q = 0; q < 4; q++) Y[q] = *reinterpret_cast<const uint4 *>(lds + ((m * 4 + q) * T + uu) * 16);
+                if constexpr (is_k(WT)) bsp = *reinterpret_cast<const uint2 *>(aux_base + (m * T + uu) * 8);
             }
-            const bool valid = rbase + rl_c < a.row1;
-#pragma unroll
-            for (int m = 0; m < MT; m++) {
-                if (m >= a.n_tok) break;
-                uint4 Y[4];
-#pragma unroll
-                for (int q = 0; q < 4; q++)
-                    Y[q] = *reinterpret_cast<const uint4 *>(lds + ((m * 4 + q) * T + u_c) * 16);
-                int isum, msum;
-                float term;
-                if constexpr (is_k(WT)) {
-                    unit_dot<WT>(cur, Y, aux_base + (m * T + u_c) * 8, u_c, isum, msum, term, nullptr, nullptr);
-                    isum = sdy_quad_sum(isum);
-                    if constexpr (WT == SDY_Q4_K) msum = sdy_quad_sum(msum);
-                    if ((u_c & 3) == 0 && valid) {
-                        const int s = u_c >> 2;
-                        const float ydv = yd[m * nb + s];
-                        float t;
-                        if constexpr (WT == SDY_Q4_K) {
-                            float d = sdy_h2f((uint16_t)(cur.c.x & 0xFFFFu)), dmin = sdy_h2f((uint16_t)(cur.c.x >> 16));
-                            float dall = ydv * d, dmn = ydv * dmin;
-                            float t1 = dall * (float)isum, t2 = dmn * (float)msum;
-                            t = t1 - t2;
-                        } else {
-                            float d = sdy_h2f((uint16_t)cur.g);
-                            float ydd = ydv * d;
-                            t = ydd * (float)isum;
-                        }
-                        terms[(rl_c * MT + m) * a.nterm + s] = t;
+            int isum, msum;
+            float term;
+            if constexpr (is_k(WT)) {
+                unit_dot<WT>(cur, Y, bsp, u, isum, msum, term, make_float2(0.f, 0.f), make_int2(0, 0));
+                isum = sdy_quad_sum(isum);
+                if constexpr (WT == SDY_Q4_K) msum = sdy_quad_sum(msum);
+                if ((u & 3) == 0 && valid) {
+                    const int s = u >> 2;
+                    const float ydv = yd[m * nb + s];
+                    float t;
+                    if constexpr (WT == SDY_Q4_K) {
+                        float d = sdy_h2f((uint16_t)(cur.c.x & 0xFFFFu)), dmin = sdy_h2f((uint16_t)(cur.c.x >> 16));
+                        float dall = ydv * d, dmn = ydv * dmin;
+                        float t1 = dall * (float)isum, t2 = dmn * (float)msum;
+                        t = t1 - t2;
+                    } else {
+                        float d = sdy_h2f((uint16_t)cur.g);
+                        float ydd = ydv * d;
+                        t = ydd * (float)isum;
                     }
-                } else {
-                    const float *dxp = reinterpret_cast<const float *>(aux_base) + (m * T + u_c) * 2;
-                    unit_dot<WT>(cur, Y, nullptr, u_c, isum, msum, term, dxp, sy + (m * T + u_c) * 2);
-                    if (valid) terms[(rl_c * MT + m) * a.nterm + u_c] = term;
+                    terms[(rl * MT + m) * a.nterm + s] = t;
+                }
+            } else {
+                const int uu = valid ? u : 0;
+                const float2 dxp = *reinterpret_cast<const float2 *>(aux_base + (m * T + uu) * 8);
+                const int2 syp = *reinterpret_cast<const int2 *>(sy + (m * T + uu) * 2);
+                unit_dot<WT>(cur, Y, make_uint2(0u, 0u), u, isum, msum, term, dxp, syp);
+                if (valid) terms[(rl * MT + m) * a.nterm + u] = term;
+            }
+        }
+        if (it + 1 == ipb) {
+            // end of batch b: each lane sums the terms of one (row, token) in block order
+            sdy_wave_sync();
+            for (int i = lane; i < rb * a.n_tok; i += 64) {
+                int r = i / a.n_tok, m = i - r * a.n_tok;
+                long row = row_of(b, r);
+                if (row >= a.row1) continue;
+                const float *tp = terms + (r * MT + m) * a.nterm;
+                float acc = 0.0f;
+                for (int s = 0; s < a.nterm; s++) acc = acc + tp[s];
+                if (a.bias) acc = acc + a.bias[row];
+                if (a.resid) acc = a.resid[(size_t)m * a.out_stride + row] + acc;
+                a.out[(size_t)m * a.out_stride + row] = acc;
+            }
+            sdy_wave_sync();
+        }
+        if (!more) break;
+        b = nb_;
+        it = nit;
+        rl = nrl;
+        u = nu;
+        cur = nxt;
+    }
+}
+
+// Row-in-lanes variant (64 % T == 0): an iteration covers 64/T whole rows, lane = (row rl, unit u)
+// for the whole kernel. After the quad reduction the super-block terms of a row sit in lanes
+// rl*T + 4s; the row sum folds them in block order with lane shuffles (the reference's sequential
+// f32 order), so no LDS round trip is needed. 32-element types sum their unit terms with a fixed
+// butterfly over the row's T lanes. Each wave walks one contiguous, balanced range of iterations
+// and loads the next iteration's weights while it computes the current one.
+template <int WT, int MT, bool YREG>
+__global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
+    extern __shared__ uint8_t lds[];
+    const int T = a.P.T, nb = a.P.nb;
+    stage_acts<WT, MT>(a, lds);
+    __syncthreads();
+    const size_t y_bytes = (size_t)MT * 4 * T * 16;
+    const uint8_t *aux_base = lds + y_bytes;
+    const float *yd = reinterpret_cast<const float *>(lds + y_bytes + (size_t)MT * T * 8);
+    const int *sy = reinterpret_cast<const int *>(lds + y_bytes + (size_t)MT * T * 8);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rpi = 64 / T;  // rows per iteration
+    const int rl = lane / T, u = lane - rl * T;
+    const long n_rows = a.row1 - a.row0;
+    const long n_it = (n_rows + rpi - 1) / rpi;
+    // Workgroups are dealt round-robin over the 8 XCDs; renumber them so that consecutive work
+    // (neighbouring rows) stays on one XCD and its L2.
+    const long G = gridDim.x, bx = blockIdx.x;
+    const long vblk = (G % 8 == 0) ? (bx % 8) * (G / 8) + bx / 8 : bx;  // a bijection of [0, G)
+    const long n_waves = G * WAVES, wid = vblk * WAVES + wave;
+    // grid-stride: at any moment the waves of the grid read neighbouring rows, so the whole GPU
+    // sweeps each plane front to back
+    if (wid >= n_it) return;
+
+    uint4 Yr[4];
+    uint2 bsr = make_uint2(0u, 0u);
+    float2 dxr = make_float2(0.f, 0.f);
+    int2 syr = make_int2(0, 0);
+    if constexpr (YREG) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) Yr[q] = *reinterpret_cast<const uint4 *>(lds + (q * T + u) * 16);
+        if constexpr (is_k(WT)) bsr = *reinterpret_cast<const uint2 *>(aux_base + u * 8);
+        else {
+            dxr = *reinterpret_cast<const float2 *>(aux_base + u * 8);
+            syr = *reinterpret_cast<const int2 *>(sy + u * 2);
+        }
+    }
+    auto row_at = [&](long itx) -> long { return a.row0 + itx * rpi + rl; };
+    auto load_it = [&](long itx, WRegs<WT> &r) {
+        long rr = row_at(itx);
+        load_w<WT>(a.P, (uint32_t)(rr < a.row1 ? rr : a.row0), (uint32_t)u, r);
+    };
+    auto body = [&](const WRegs<WT> &cur, long itx) {
+        const long row = row_at(itx);
+        const bool valid = row < a.row1;
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            if (m >= a.n_tok) break;
+            uint4 Y[4];
+            uint2 bsp = bsr;
+            float2 dxp = dxr;
+            int2 syp = syr;
+            if constexpr (YREG) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) Y[q] = Yr[q];
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) Y[q] = *reinterpret_cast<const uint4 *>(lds + ((m * 4 + q) * T + u) * 16);
+                if constexpr (is_k(WT)) bsp = *reinterpret_cast<const uint2 *>(aux_base + (m * T + u) * 8);
+                else {
+                    dxp = *reinterpret_cast<const float2 *>(aux_base + (m * T + u) * 8);
+                    syp = *reinterpret_cast<const int2 *>(sy + (m * T + u) * 2);
                 }
             }
-            cur = nxt;
+            int isum, msum;
+            float term = 0.0f;
+            unit_dot<WT>(cur, Y, bsp, u, isum, msum, term, dxp, syp);
+            float acc;
+            if constexpr (is_k(WT)) {
+                isum = sdy_quad_sum(isum);
+                if constexpr (WT == SDY_Q4_K) msum = sdy_quad_sum(msum);
+                const float ydv = yd[m * nb + (u >> 2)];
+                if constexpr (WT == SDY_Q4_K) {
+                    float d = sdy_h2f((uint16_t)(cur.c.x & 0xFFFFu)), dmin = sdy_h2f((uint16_t)(cur.c.x >> 16));
+                    float dall = ydv * d, dmn = ydv * dmin;
+                    float t1 = dall * (float)isum, t2 = dmn * (float)msum;
+                    term = t1 - t2;
+                } else {
+                    float d = sdy_h2f((uint16_t)cur.g);
+                    float ydd = ydv * d;
+                    term = ydd * (float)isum;
+                }
+                // sequential fold over the row's super-blocks: lane rl*T reads lanes rl*T + 4s
+                acc = term;
+                const int nsb = T >> 2;
+                for (int s = 1; s < nsb; s++) acc = acc + __shfl(term, lane + 4 * s);
+            } else {
+                acc = term;
+                for (int off = 1; off < T; off <<= 1) acc = acc + __shfl_xor(acc, off);
+            }
+            if (u == 0 && valid) {
+                if (a.bias) acc = acc + a.bias[row];
+                if (a.resid) acc = a.resid[(size_t)m * a.out_stride + row] + acc;
+                a.out[(size_t)m * a.out_stride + row] = acc;
+            }
         }
-        sdy_wave_sync();
-        // phase 2: each lane sums the terms of one (row, token) in block order
-        for (int i = lane; i < rb * a.n_tok; i += 64) {
-            int r = i / a.n_tok, m = i - r * a.n_tok;
-            long row = rbase + r;
-            if (row >= a.row1) continue;
-            const float *tp = terms + (r * MT + m) * a.nterm;
-            float acc = 0.0f;
-            for (int s = 0; s < a.nterm; s++) acc = acc + tp[s];
-            if (a.bias) acc = acc + a.bias[row];
-            float *o = a.out + (size_t)m * a.out_stride + row;
-            if (a.resid) acc = a.resid[(size_t)m * a.out_stride + row] + acc;
-            *o = acc;
-        }
-        sdy_wave_sync();
+    };
+    // ping-pong register buffers: the loads of one iteration stay in flight while the other computes
+    WRegs<WT> A, B;
+    const long S = n_waves;
+    load_it(wid, A);
+    for (long itx = wid; itx < n_it; itx += 2 * S) {
+        if (itx + S < n_it) load_it(itx + S, B);
+        body(A, itx);
+        if (itx + S >= n_it) break;
+        if (itx + 2 * S < n_it) load_it(itx + 2 * S, A);
+        body(B, itx + S);
     }
 }
 
@@ -808,11 +1007,16 @@ extern "C" int sdy_quantize(int vtype, const float *x, void *xq, int n_in, int n
 
 static int g_n_cu = 0;
 
+// Rows per batch: the smallest count giving at least 64 (row, unit) tasks with little idle-lane
+// waste, so that small matrices spread over many waves; long rows (T >= 64) take one row per batch.
 static int rows_per_batch(int T) {
-    int g = 1;
-    while (g < 64 && T % (2 * g) == 0) g *= 2;  // gcd(T, 64)
-    int rb_unit = 64 / g;                        // rb * T must be a multiple of 64
-    return rb_unit > 16 ? rb_unit : 16;
+    if (T >= 64) return 1;
+    if (64 % T == 0) return 64 / T;
+    for (int rb = (64 + T - 1) / T; rb < 64; rb++) {
+        int tasks = rb * T, its = (tasks + 63) / 64;
+        if (its * 64 - tasks <= its * 8) return rb;  // at most 1/8 of the lanes idle
+    }
+    return 64;
 }
 
 // LDS bytes of k_matvec: staged activations of MT tokens plus the per-wave term buffers.
@@ -822,6 +1026,49 @@ static size_t mv_lds_bytes(int wt, int T, int nb, int MT) {
 }
 
 constexpr size_t LDS_MAX = 160 * 1024;
+
+template <int WT, int MT, bool YREG>
+static int launch_mv_k(MvArgs &A, size_t lds, hipStream_t st) {
+    static int per_cu = 0;  // resident workgroups per CU for this instantiation (at this LDS size)
+    static size_t per_cu_lds = 0;
+    const void *fn = (const void *)k_matvec<WT, MT, YREG>;
+    if (per_cu == 0 || per_cu_lds != lds) {
+        if (lds > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_MAX);
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, THREADS, lds) != hipSuccess || n < 1) n = 1;
+        per_cu = n;
+        per_cu_lds = lds;
+    }
+    long n_rows = A.row1 - A.row0;
+    long n_batches = (n_rows + A.rb - 1) / A.rb;
+    long wgs = (n_batches + WAVES - 1) / WAVES;
+    long cap = (long)(g_n_cu ? g_n_cu : 256) * per_cu;
+    if (wgs > cap) wgs = cap;
+    hipLaunchKernelGGL((k_matvec<WT, MT, YREG>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
+    return sdy_check_launch("matvec");
+}
+
+static size_t mv_lds_bytes_rl(int T, int MT) { return (size_t)MT * 4 * T * 16 + (size_t)MT * T * 16; }
+
+template <int WT, int MT, bool YREG>
+static int launch_mv_rl(MvArgs &A, size_t lds, hipStream_t st) {
+    static int per_cu = 0;
+    static size_t per_cu_lds = 0;
+    const void *fn = (const void *)k_matvec_rl<WT, MT, YREG>;
+    if (per_cu == 0 || per_cu_lds != lds) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, THREADS, lds) != hipSuccess || n < 1) n = 1;
+        per_cu = n;
+        per_cu_lds = lds;
+    }
+    const int rpi = 64 / A.P.T;
+    long n_it = (A.row1 - A.row0 + rpi - 1) / rpi;
+    long wgs = (n_it + WAVES - 1) / WAVES;
+    long cap = (long)(g_n_cu ? g_n_cu : 256) * per_cu;
+    if (wgs > cap) wgs = cap;
+    hipLaunchKernelGGL((k_matvec_rl<WT, MT, YREG>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
+    return sdy_check_launch("matvec");
+}
 
 template <int WT, int MT>
 static int launch_mv(const sdy_mat *m, const sdy_mv_args *a, int n_tok, const uint8_t *xq, float *out,
@@ -836,24 +1083,20 @@ static int launch_mv(const sdy_mat *m, const sdy_mv_args *a, int n_tok, const ui
     A.resid = resid;
     A.row0 = a->row0;
     A.row1 = a->row1;
-    A.rb = rows_per_batch(A.P.T);
-    A.nterm = is_k(WT) ? A.P.nb : A.P.T;
-    size_t lds = mv_lds_bytes(WT, A.P.T, A.P.nb, MT);
+    const int T = A.P.T;
+    A.rb = rows_per_batch(T);
+    A.ipb = (A.rb * T + 63) / 64;
+    A.q64 = 64 / T;
+    A.r64 = 64 % T;
+    A.nterm = is_k(WT) ? A.P.nb : T;
+    size_t lds = mv_lds_bytes(WT, T, A.P.nb, MT);
     if (lds > LDS_MAX) return sdy_fail(-1, "matvec: %zu bytes of LDS needed (n_in %d, %d tokens)", lds, m->n_in, MT);
-    long n_rows = a->row1 - a->row0;
-    long n_batches = (n_rows + A.rb - 1) / A.rb;
-    long wgs = (n_batches + WAVES - 1) / WAVES;
-    int per_cu = (int)(LDS_MAX / lds);
-    per_cu = per_cu < 1 ? 1 : per_cu > 8 ? 8 : per_cu;
-    long cap = (long)(g_n_cu ? g_n_cu : 256) * per_cu;
-    if (wgs > cap) wgs = cap;
-    static bool big_lds = false;
-    if (lds > 64 * 1024 && !big_lds) {
-        (void)hipFuncSetAttribute((const void *)k_matvec<WT, MT>, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_MAX);
-        big_lds = true;
+    if (T <= 64 && 64 % T == 0) {
+        lds = mv_lds_bytes_rl(T, MT);
+        if (MT == 1) return launch_mv_rl<WT, MT, true>(A, lds, st);
+        return launch_mv_rl<WT, MT, false>(A, lds, st);
     }
-    hipLaunchKernelGGL((k_matvec<WT, MT>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
-    return sdy_check_launch("matvec");
+    return launch_mv_k<WT, MT, false>(A, lds, st);
 }
 
 template <int WT>
