@@ -69,6 +69,42 @@ class Events:
         return ms.value
 
 
+def per_launch_ms(stream, launch, n):
+    """Average duration (ms) of n launches, each bracketed by its own pair of HIP events recorded
+    on `stream` (the stream the kernel runs on)."""
+    L = capi.lib()
+    evs = []
+    for _ in range(2 * n):
+        e = ctypes.c_void_p()
+        capi.check(L.sdy_event_new(ctypes.byref(e)))
+        evs.append(e)
+    for i in range(n):
+        capi.check(L.sdy_event_record(evs[2 * i], stream))
+        launch(i)
+        capi.check(L.sdy_event_record(evs[2 * i + 1], stream))
+    total = 0.0
+    ms = ctypes.c_float()
+    for i in range(n):
+        capi.check(L.sdy_event_elapsed(ctypes.byref(ms), evs[2 * i], evs[2 * i + 1]))
+        total += ms.value
+    for e in evs:
+        capi.check(L.sdy_event_free(e))
+    return total / n
+
+
+def profiled_traffic(name):
+    """HBM bytes per launch of a kernel, from the PMC summary committed under profiles/
+    (FETCH_SIZE and WRITE_SIZE scaled by copy-kernel calibration); None when absent."""
+    p = ROOT / "profiles" / name
+    try:
+        for line in p.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def membw_probe(stream, gib=4):
     L = capi.lib()
     n = gib << 30
@@ -212,14 +248,14 @@ def bench_matvec(args, wt, n_out, n_in, n_copies, stacked):
     units = n_copies if stacked else 1
     value = algo_bytes * units / (ms_step * 1e-3) / 1e9
 
-    # dominant kernel alone (matvec launches back to back on the same stream)
+    # dominant kernel alone: each launch bracketed by its own event pair on the kernel's stream,
+    # so the average is the launch duration without the gaps between dispatches
     for i in range(3):
         matvec_only(i)
-    ev.start()
-    for i in range(args.steps):
-        matvec_only(i)
-    ms_k = ev.stop_ms() / args.steps
-    achieved = w_bytes * units / (ms_k * 1e-3) / 1e9 + (n_in * 4 + n_out * 4 * units) / (ms_k * 1e-3) / 1e9
+    ms_k = per_launch_ms(st, matvec_only, args.steps)
+    algo_launch = w_bytes * units + n_in * 4 + n_out * 4 * units
+    achieved = algo_launch / (ms_k * 1e-3) / 1e9
+    traffic = profiled_traffic(f"k_matvec_{name.lower()}_{'stacked' if stacked else 'head'}.md")
     achievable = membw_probe(st)
 
     # CPU baseline: the reference's code on this host (all online CPUs, and 1 thread)
@@ -252,8 +288,9 @@ def bench_matvec(args, wt, n_out, n_in, n_copies, stacked):
             "config": cfg, "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2),
             "achievable_hbm_GBps": round(achievable, 1),
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                         "kernel": f"k_matvec<{name}>", "kernel_avg_us": round(ms_k * 1e3, 3)},
+                         "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                         "kernel": f"k_matvec<{name}>", "kernel_avg_us": round(ms_k * 1e3, 3),
+                         "algorithmic_bytes_per_launch": algo_launch},
             "cpu_baseline": cpu, "parity": parity}
     if cpu and "value" in cpu:
         line["gpu_over_cpu"] = round(value / cpu["value"], 1)
