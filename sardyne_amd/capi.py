@@ -108,7 +108,8 @@ class SdyMat(ctypes.Structure):
 
 class SdyMvArgs(ctypes.Structure):
     _fields_ = [("xq", _vp), ("x", _vp), ("n_tok", _int), ("out", _vp), ("out_stride", ctypes.c_long),
-                ("bias", _vp), ("resid", _vp), ("row0", ctypes.c_long), ("row1", ctypes.c_long)]
+                ("bias", _vp), ("resid", _vp), ("row0", ctypes.c_long), ("row1", ctypes.c_long),
+                ("epilogue", _int)]
 
 
 _DEVICE_SIGNATURES = {
@@ -136,7 +137,14 @@ _DEVICE_SIGNATURES = {
     "sdy_dequant_rows": (_int, [ctypes.POINTER(SdyMat), ctypes.c_long, ctypes.c_long, _vp, _vp]),
     "sdy_quantize": (_int, [_int, _vp, _vp, _int, _int, _vp]),
     "sdy_matvec": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp]),
+    "sdy_mat_alloc": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long]),
+    "sdy_mat_upload_map": (_int, [ctypes.POINTER(SdyMat), ctypes.c_long, ctypes.c_long, ctypes.c_long,
+                                  ctypes.c_long, ctypes.c_long, _vp, _vp]),
+    "sdy_rmsnorm": (_int, [_vp, _vp, _vp, _int, ctypes.c_float, _int, ctypes.c_long, ctypes.c_long, _vp]),
+    "sdy_norm_quant": (_int, [_vp, _vp, ctypes.c_float, _int, _int, _vp, _int, _vp, _vp]),
 }
+
+EPI_NONE, EPI_SWIGLU = 0, 1
 
 
 def lib_path() -> pathlib.Path:

@@ -211,33 +211,118 @@ static int sdy_err(char *err, size_t err_len, const char *what) {
     return -1;
 }
 
-/* [n_expert][n_out][n_in] (n_expert = 0: a matrix [n_out][n_in]) of a supported type, uploaded. */
-static int get_tensor(engine_model *m, const char *name, int n_in, int n_out, int n_expert, dmat *out, char *err,
-                      size_t err_len) {
+/* Descriptor of a [n_expert][n_out][n_in] tensor (n_expert = 0: a matrix [n_out][n_in]) of a
+ * supported type, or NULL with the reason in err. */
+static const gguf_tensor *check_tensor(engine_model *m, const char *name, int n_in, int n_out, int n_expert, char *err,
+                                       size_t err_len) {
     const gguf_tensor *t = find(m->gf, name);
     if (!t) {
         set_err(err, err_len, "tensore mancante: %s", name);
-        return -1;
+        return NULL;
     }
     if (t->n_dims != (n_expert ? 3u : 2u) || t->ne[0] != (uint64_t)n_in || t->ne[1] != (uint64_t)n_out ||
         (n_expert && t->ne[2] != (uint64_t)n_expert)) {
         set_err(err, err_len, "%s: dimensioni [%llu, %llu, %llu], attese [%d, %d, %d]", name,
                 (unsigned long long)t->ne[0], (unsigned long long)t->ne[1], (unsigned long long)t->ne[2], n_in, n_out,
                 n_expert ? n_expert : 1);
-        return -1;
+        return NULL;
     }
     if (!type_supported(t->type)) {
         set_err(err, err_len,
                 "%s: tipo %s non supportato dal runtime (supportati: F32, F16, BF16, Q8_0, Q4_0, Q5_0, Q4_K, Q6_K)",
                 name, gguf_type_name(t->type));
-        return -1;
+        return NULL;
     }
+    return t;
+}
+
+static void set_dmat(dmat *d, int type, int n_in, int n_out) {
+    d->type = type;
+    d->n_in = n_in;
+    d->n_out = n_out;
+}
+
+static int get_tensor(engine_model *m, const char *name, int n_in, int n_out, int n_expert, dmat *out, char *err,
+                      size_t err_len) {
+    const gguf_tensor *t = check_tensor(m, name, n_in, n_out, n_expert, err, err_len);
+    if (!t) return -1;
     if (sdy_mat_upload(&out->m, (int)t->type, n_in, (long)n_out * (n_expert ? n_expert : 1), t->data, m->st))
         return sdy_err(err, err_len, name);
-    out->type = (int)t->type;
-    out->n_in = n_in;
-    out->n_out = n_out;
+    set_dmat(out, (int)t->type, n_in, n_out);
     m->device_bytes += out->m.bytes;
+    return 0;
+}
+
+static int is_quant(uint32_t t) { return t != OP_F32 && t != OP_F16 && t != OP_BF16; }
+
+/* Row view of a fused matrix. */
+static dmat view(const dmat *w, long r0, int n_out) {
+    dmat d = *w;
+    d.m = sdy_mat_rows(&w->m, r0, n_out);
+    d.n_out = n_out;
+    return d;
+}
+
+/* wq, wk, wv. When wq and wk (and wv) have one type they are stored as one matrix whose row ranges
+ * are wq, wk (, wv), so that a single matvec computes them together. */
+static int get_qkv(engine_model *m, int l, dlayer *L, char *err, size_t err_len) {
+    const engine_model_info *in = &m->info;
+    const int dim = in->dim, q_dim = in->n_head * in->head_dim, kv_dim = in->n_kv_head * in->head_dim;
+    char nq[64], nk[64], nv[64];
+    snprintf(nq, sizeof nq, "blk.%d.attn_q.weight", l);
+    snprintf(nk, sizeof nk, "blk.%d.attn_k.weight", l);
+    snprintf(nv, sizeof nv, "blk.%d.attn_v.weight", l);
+    const gguf_tensor *tq = check_tensor(m, nq, dim, q_dim, 0, err, err_len);
+    const gguf_tensor *tk = tq ? check_tensor(m, nk, dim, kv_dim, 0, err, err_len) : NULL;
+    const gguf_tensor *tv = tk ? check_tensor(m, nv, dim, kv_dim, 0, err, err_len) : NULL;
+    if (!tv) return -1;
+    if (tq->type != tk->type) {
+        L->qkv_parts = 0;
+        return get_tensor(m, nq, dim, q_dim, 0, &L->wq, err, err_len) ||
+               get_tensor(m, nk, dim, kv_dim, 0, &L->wk, err, err_len) ||
+               get_tensor(m, nv, dim, kv_dim, 0, &L->wv, err, err_len) ? -1 : 0;
+    }
+    const int parts = tv->type == tq->type ? 3 : 2;
+    const long rows = (long)q_dim + kv_dim + (parts == 3 ? kv_dim : 0);
+    if (sdy_mat_alloc(&L->wqkv.m, (int)tq->type, dim, rows)) return sdy_err(err, err_len, nq);
+    set_dmat(&L->wqkv, (int)tq->type, dim, (int)rows);
+    L->qkv_parts = parts;
+    m->device_bytes += L->wqkv.m.bytes;
+    if (sdy_mat_upload_rows(&L->wqkv.m, 0, 1, q_dim, tq->data, m->st)) return sdy_err(err, err_len, nq);
+    if (sdy_mat_upload_rows(&L->wqkv.m, q_dim, 1, kv_dim, tk->data, m->st)) return sdy_err(err, err_len, nk);
+    L->wq = view(&L->wqkv, 0, q_dim);
+    L->wk = view(&L->wqkv, q_dim, kv_dim);
+    if (parts == 3) {
+        if (sdy_mat_upload_rows(&L->wqkv.m, q_dim + kv_dim, 1, kv_dim, tv->data, m->st))
+            return sdy_err(err, err_len, nv);
+        L->wv = view(&L->wqkv, q_dim + kv_dim, kv_dim);
+        return 0;
+    }
+    return get_tensor(m, nv, dim, kv_dim, 0, &L->wv, err, err_len);
+}
+
+/* gate and up ([n_expert][ffn][dim]). With one quantized type they are stored interleaved, row
+ * 2i = gate i and row 2i+1 = up i (per expert), for the SwiGLU matvec epilogue. */
+static int get_gate_up(engine_model *m, int l, dlayer *L, int ffn, int n_expert, char *err, size_t err_len) {
+    const int dim = m->info.dim;
+    char ng[64], nu[64];
+    snprintf(ng, sizeof ng, n_expert ? "blk.%d.ffn_gate_exps.weight" : "blk.%d.ffn_gate.weight", l);
+    snprintf(nu, sizeof nu, n_expert ? "blk.%d.ffn_up_exps.weight" : "blk.%d.ffn_up.weight", l);
+    const gguf_tensor *tg = check_tensor(m, ng, dim, ffn, n_expert, err, err_len);
+    const gguf_tensor *tu = tg ? check_tensor(m, nu, dim, ffn, n_expert, err, err_len) : NULL;
+    if (!tu) return -1;
+    if (tg->type != tu->type || !is_quant(tg->type)) {
+        L->gu_fused = 0;
+        return get_tensor(m, ng, dim, ffn, n_expert, &L->gate, err, err_len) ||
+               get_tensor(m, nu, dim, ffn, n_expert, &L->up, err, err_len) ? -1 : 0;
+    }
+    const long ne = n_expert ? n_expert : 1, n = ne * ffn;
+    if (sdy_mat_alloc(&L->gate_up.m, (int)tg->type, dim, 2 * n)) return sdy_err(err, err_len, ng);
+    set_dmat(&L->gate_up, (int)tg->type, dim, 2 * ffn);
+    L->gu_fused = 1;
+    m->device_bytes += L->gate_up.m.bytes;
+    if (sdy_mat_upload_map(&L->gate_up.m, 0, n, 2, ffn, 2L * ffn, tg->data, m->st)) return sdy_err(err, err_len, ng);
+    if (sdy_mat_upload_map(&L->gate_up.m, 1, n, 2, ffn, 2L * ffn, tu->data, m->st)) return sdy_err(err, err_len, nu);
     return 0;
 }
 
@@ -275,7 +360,11 @@ void engine_model_free(engine_model *m) {
     if (m->layers) {
         for (int l = 0; l < m->info.n_layer; l++) {
             dlayer *L = &m->layers[l];
-            dmat *mats[] = {&L->wq, &L->wk, &L->wv, &L->wo, &L->gate, &L->up, &L->down, &L->gate_inp};
+            /* row views of wqkv share its allocation */
+            if (L->qkv_parts < 2) sdy_mat_free(&L->wq.m);
+            if (L->qkv_parts < 2) sdy_mat_free(&L->wk.m);
+            if (L->qkv_parts < 3) sdy_mat_free(&L->wv.m);
+            dmat *mats[] = {&L->wqkv, &L->wo, &L->gate, &L->up, &L->gate_up, &L->down, &L->gate_inp};
             for (size_t i = 0; i < sizeof mats / sizeof *mats; i++) sdy_mat_free(&mats[i]->m);
         }
         free(m->layers);
@@ -329,21 +418,16 @@ engine_model *engine_model_load(const char *path, char *err, size_t err_len) {
         char name[64];
 #define NAME(suffix) (snprintf(name, sizeof name, "blk.%d." suffix, l), name)
         if (get_vector(m, NAME("attn_norm.weight"), dim, &L->attn_norm, err, err_len) ||
-            get_vector(m, NAME("ffn_norm.weight"), dim, &L->ffn_norm, err, err_len) ||
-            get_tensor(m, NAME("attn_q.weight"), dim, q_dim, 0, &L->wq, err, err_len) ||
-            get_tensor(m, NAME("attn_k.weight"), dim, kv_dim, 0, &L->wk, err, err_len) ||
-            get_tensor(m, NAME("attn_v.weight"), dim, kv_dim, 0, &L->wv, err, err_len) ||
+            get_vector(m, NAME("ffn_norm.weight"), dim, &L->ffn_norm, err, err_len) || get_qkv(m, l, L, err, err_len) ||
             get_tensor(m, NAME("attn_output.weight"), q_dim, dim, 0, &L->wo, err, err_len))
             goto fail;
         if (in->n_expert) {
             int ne = in->n_expert, fe = in->ffn_exp_dim;
             if (get_tensor(m, NAME("ffn_gate_inp.weight"), dim, ne, 0, &L->gate_inp, err, err_len) ||
-                get_tensor(m, NAME("ffn_gate_exps.weight"), dim, fe, ne, &L->gate, err, err_len) ||
-                get_tensor(m, NAME("ffn_up_exps.weight"), dim, fe, ne, &L->up, err, err_len) ||
+                get_gate_up(m, l, L, fe, ne, err, err_len) ||
                 get_tensor(m, NAME("ffn_down_exps.weight"), fe, dim, ne, &L->down, err, err_len))
                 goto fail;
-        } else if (get_tensor(m, NAME("ffn_gate.weight"), dim, in->ffn_dim, 0, &L->gate, err, err_len) ||
-                   get_tensor(m, NAME("ffn_up.weight"), dim, in->ffn_dim, 0, &L->up, err, err_len) ||
+        } else if (get_gate_up(m, l, L, in->ffn_dim, 0, err, err_len) ||
                    get_tensor(m, NAME("ffn_down.weight"), in->ffn_dim, dim, 0, &L->down, err, err_len)) {
             goto fail;
         }
@@ -415,6 +499,10 @@ engine_ctx *engine_ctx_new(const engine_model *m, int32_t max_seq, int32_t n_bat
         engine_ctx_free(c);
         return NULL;
     }
+    /* SARDYNE_NO_FUSED_DECODE / SARDYNE_NO_GRAPH: run one-token steps with the unfused kernels, or
+       without recording them (the results are the same; used to compare the paths) */
+    c->decode_fused = !getenv("SARDYNE_NO_FUSED_DECODE") && sdy_engine_decode_fused_ok(c);
+    c->use_graph = c->decode_fused && !getenv("SARDYNE_NO_GRAPH");
     return c;
 }
 

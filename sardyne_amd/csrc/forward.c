@@ -58,6 +58,11 @@ int sdy_engine_alloc(engine_ctx *c) {
     TRY(dalloc(&c->xq[1], B * ((max_in + 255) / 256 * 292)));
     TRY(dalloc((void **)&c->tok_dev, B * 4));
     TRY(sdy_host_alloc((void **)&c->tok_host, B * 4));
+    TRY(dalloc((void **)&c->qkv, (q_dim + 2 * kv_dim) * 4));
+    TRY(dalloc((void **)&c->step_dev, 2 * 4));
+    TRY(sdy_host_alloc((void **)&c->step_host, 2 * 4));
+    TRY(dalloc((void **)&c->att_counter, 64));
+    TRY(sdy_memset(c->att_counter, 0, 64, c->st));
     if (in->n_expert) {
         size_t chosen = B * in->n_expert_used;
         TRY(dalloc((void **)&c->moe_probs, B * in->n_expert * 4));
@@ -80,24 +85,28 @@ int sdy_engine_alloc(engine_ctx *c) {
 }
 
 void sdy_engine_release(engine_ctx *c) {
+    if (c->graph) sdy_graph_free(c->graph);
+    c->graph = NULL;
     void *dev[] = {c->k_cache, c->v_cache, c->rope_cos, c->rope_sin, c->x, c->xb, c->q, c->k, c->v, c->att, c->hb,
                    c->hb2, c->logits_dev, c->part, c->xq[0], c->xq[1], c->tok_dev, c->moe_probs, c->moe_w,
-                   c->moe_top, c->moe_x, c->moe_y, c->moe_sum, c->moe_gidx, c->moe_gw};
+                   c->moe_top, c->moe_x, c->moe_y, c->moe_sum, c->moe_gidx, c->moe_gw, c->qkv, c->step_dev,
+                   c->att_counter};
     for (size_t i = 0; i < sizeof dev / sizeof *dev; i++) sdy_free(dev[i]);
-    void *host[] = {c->tok_host, c->moe_top_host, c->moe_w_host, c->moe_gidx_host, c->moe_gw_host};
+    void *host[] = {c->tok_host, c->moe_top_host, c->moe_w_host, c->moe_gidx_host, c->moe_gw_host, c->step_host};
     for (size_t i = 0; i < sizeof host / sizeof *host; i++) sdy_host_free(host[i]);
 }
 
 /* out[t][row] = W . x[t] for n_tok rows of x; new_input = 1 when x changed since the last call
  * (the quantized copy of x is then rebuilt), as matmul() in csrc/model_llama.c:592-611. */
-static int mm(engine_ctx *c, float *out, const float *x, const dmat *w, int n_tok, const float *bias,
-              const float *resid, int new_input) {
+static int mm_epi(engine_ctx *c, float *out, const float *x, const dmat *w, int n_tok, const float *bias,
+                  const float *resid, int new_input, int epilogue) {
     if (new_input) c->xq_src[0] = c->xq_src[1] = NULL;
     sdy_mv_args a;
     memset(&a, 0, sizeof a);
     a.n_tok = n_tok;
     a.out = out;
-    a.out_stride = w->n_out;
+    a.out_stride = epilogue == SDY_EPI_SWIGLU ? w->n_out / 2 : w->n_out;
+    a.epilogue = epilogue;
     a.bias = bias;
     a.resid = resid;
     a.row0 = 0;
@@ -118,7 +127,37 @@ static int mm(engine_ctx *c, float *out, const float *x, const dmat *w, int n_to
     return sdy_matvec(&w->m, &a, c->st);
 }
 
-/* One expert's slice of a stacked [n_expert][n_out][n_in] tensor. */
+static int mm(engine_ctx *c, float *out, const float *x, const dmat *w, int n_tok, const float *bias,
+              const float *resid, int new_input) {
+    return mm_epi(c, out, x, w, n_tok, bias, resid, new_input, SDY_EPI_NONE);
+}
+
+/* xb = RMSNorm(x) * wn for n rows, quantized for the matrix `next` in the same launch; the copy
+ * is registered in the activation-quantisation cache, so mm(next, xb, new_input = 0) reuses it. */
+static int norm_for(engine_ctx *c, const float *x, const float *wn, const dmat *next, int n) {
+    const engine_model_info *in = &c->m->info;
+    const int vt = vec_dot_type(next->type);
+    c->xq_src[0] = c->xq_src[1] = NULL;
+    if (vt == SDY_F32) return sdy_norm_quant(x, wn, in->norm_eps, in->dim, n, c->xb, SDY_F32, NULL, c->st);
+    const int s = vt == SDY_Q8_0 ? 0 : 1;
+    TRY(sdy_norm_quant(x, wn, in->norm_eps, in->dim, n, c->xb, vt, c->xq[s], c->st));
+    c->xq_src[s] = c->xb;
+    c->xq_n_tok[s] = n;
+    c->xq_n_in[s] = in->dim;
+    return 0;
+}
+
+/* hb[t][i] = silu(gate_i . x) * (up_i . x) for n rows of x (gate/up fused and interleaved, or apart). */
+static int ffn_gate_up(engine_ctx *c, const float *x, int n, int new_input, const dmat *gate_up, const dmat *gate,
+                       const dmat *up, int ffn) {
+    if (gate_up) return mm_epi(c, c->hb, x, gate_up, n, NULL, NULL, new_input, SDY_EPI_SWIGLU);
+    TRY(mm(c, c->hb, x, gate, n, NULL, NULL, new_input));
+    TRY(mm(c, c->hb2, x, up, n, NULL, NULL, 0));
+    return sdy_silu_mul(c->hb, c->hb2, (long)n * ffn, c->st);
+}
+
+/* One expert's slice of a stacked [n_expert][n_out][n_in] tensor (rows_per_expert = n_out, or
+ * 2 * n_out for the interleaved gate|up tensor). */
 static dmat expert(const dmat *w, int e) {
     dmat d = *w;
     d.m = sdy_mat_rows(&w->m, (long)e * w->n_out, w->n_out);
@@ -134,7 +173,7 @@ int sdy_scatter_axpy(float *dst, const int32_t *idx, const float *w, const float
 static int moe(engine_ctx *c, const dlayer *L, int n) {
     const engine_model_info *in = &c->m->info;
     const int dim = in->dim, fe = in->ffn_exp_dim, ne = in->n_expert, k = in->n_expert_used, total = n * k;
-    TRY(mm(c, c->moe_probs, c->xb, &L->gate_inp, n, NULL, NULL, 1));
+    TRY(mm(c, c->moe_probs, c->xb, &L->gate_inp, n, NULL, NULL, 0));
     TRY(sdy_moe_route(c->moe_probs, n, ne, k, c->moe_top, c->moe_w, c->st));
     TRY(sdy_d2h(c->moe_top_host, c->moe_top, (size_t)total * 4, c->st));
     TRY(sdy_d2h(c->moe_w_host, c->moe_w, (size_t)total * 4, c->st));
@@ -156,11 +195,16 @@ static int moe(engine_ctx *c, const dlayer *L, int n) {
     for (int e = 0; e < ne && !rc; e++) {
         int first = count[e], m = count[e + 1] - first;
         if (!m) continue;
-        dmat g = expert(&L->gate, e), u = expert(&L->up, e), d = expert(&L->down, e);
         if ((rc = sdy_gather_rows(c->xb, c->moe_gidx + first, m, dim, c->moe_x, c->st))) break;
-        if ((rc = mm(c, c->hb, c->moe_x, &g, m, NULL, NULL, 1))) break;
-        if ((rc = mm(c, c->hb2, c->moe_x, &u, m, NULL, NULL, 0))) break;
-        if ((rc = sdy_silu_mul(c->hb, c->hb2, (long)m * fe, c->st))) break;
+        if (L->gu_fused) {
+            dmat gu = expert(&L->gate_up, e);
+            rc = ffn_gate_up(c, c->moe_x, m, 1, &gu, NULL, NULL, fe);
+        } else {
+            dmat g = expert(&L->gate, e), u = expert(&L->up, e);
+            rc = ffn_gate_up(c, c->moe_x, m, 1, NULL, &g, &u, fe);
+        }
+        if (rc) break;
+        dmat d = expert(&L->down, e);
         if ((rc = mm(c, c->moe_y, c->hb, &d, m, NULL, NULL, 1))) break;
         rc = sdy_scatter_axpy(c->moe_sum, c->moe_gidx + first, c->moe_gw + first, c->moe_y, m, dim, c->st);
     }
@@ -169,45 +213,116 @@ static int moe(engine_ctx *c, const dlayer *L, int n) {
     return rc;
 }
 
-int sdy_engine_forward(engine_ctx *c, const int32_t *tokens, int n, int out_rows) {
+/* Whether the one-token step can use the fused decode kernels (and be recorded as a graph). */
+int sdy_engine_decode_fused_ok(const engine_ctx *c) {
+    const engine_model_info *in = &c->m->info;
+    return sdy_attn_decode_ok(in->n_head, in->n_kv_head, in->head_dim, c->max_seq);
+}
+
+/* The layers and the head for n tokens at positions n_past.. (kernels only: no host copies or
+ * synchronisation, so that the one-token step can be recorded as a graph). decode: the fused
+ * one-token kernels, with the token and its position read from step_dev. */
+static int layers(engine_ctx *c, int n, int out_rows, int decode) {
     const engine_model *m = c->m;
     const engine_model_info *in = &m->info;
     const int dim = in->dim, hd = in->head_dim, q_dim = in->n_head * hd, kv_dim = in->n_kv_head * hd;
     const int pos0 = c->n_past;
     const long head_stride = (long)c->max_seq * hd, layer_stride = (long)in->n_kv_head * head_stride;
-    memcpy(c->tok_host, tokens, (size_t)n * 4);
-    TRY(sdy_h2d(c->tok_dev, c->tok_host, (size_t)n * 4, c->st));
-    TRY(sdy_dequant_gather(&m->tok_embd.m, c->tok_dev, n, c->x, c->st));
+    TRY(sdy_dequant_gather(&m->tok_embd.m, decode ? c->step_dev : c->tok_dev, n, c->x, c->st));
     for (int l = 0; l < in->n_layer; l++) {
         const dlayer *L = &m->layers[l];
         float *kc = c->k_cache + l * layer_stride, *vc = c->v_cache + l * layer_stride;
-        TRY(sdy_rmsnorm(c->x, L->attn_norm, c->xb, dim, in->norm_eps, n, dim, dim, c->st));
-        TRY(mm(c, c->q, c->xb, &L->wq, n, L->bq, NULL, 1));
-        TRY(mm(c, c->k, c->xb, &L->wk, n, L->bk, NULL, 0));
-        TRY(mm(c, c->v, c->xb, &L->wv, n, L->bv, NULL, 0));
-        TRY(sdy_qk_rope_kv(c->q, c->k, c->v, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos, c->rope_sin, pos0, n,
-                           in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc, vc, head_stride, c->st));
-        TRY(sdy_attention(c->q, kc, vc, n, in->n_head, in->n_kv_head, hd, pos0 + 1, head_stride, q_dim, c->part,
-                          c->att, q_dim, c->st));
-        TRY(mm(c, c->x, c->att, &L->wo, n, NULL, c->x, 1));
-        TRY(sdy_rmsnorm(c->x, L->ffn_norm, c->xb, dim, in->norm_eps, n, dim, dim, c->st));
+        if (decode) {
+            /* q | k | v of the token, contiguous in c->qkv */
+            float *q = c->qkv, *k = q + q_dim, *v = k + kv_dim;
+            const int bias_fused = !in->qkv_bias ||
+                                   (L->bk == L->bq + q_dim && (L->qkv_parts < 3 || L->bv == L->bk + kv_dim));
+            TRY(norm_for(c, c->x, L->attn_norm, L->qkv_parts >= 2 ? &L->wqkv : &L->wq, 1));
+            if (L->qkv_parts >= 2 && bias_fused) {
+                TRY(mm(c, q, c->xb, &L->wqkv, 1, L->bq, NULL, 0));
+                if (L->qkv_parts == 2) TRY(mm(c, v, c->xb, &L->wv, 1, L->bv, NULL, 0));
+            } else {
+                TRY(mm(c, q, c->xb, &L->wq, 1, L->bq, NULL, 0));
+                TRY(mm(c, k, c->xb, &L->wk, 1, L->bk, NULL, 0));
+                TRY(mm(c, v, c->xb, &L->wv, 1, L->bv, NULL, 0));
+            }
+            TRY(sdy_attn_decode(q, k, v, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos, c->rope_sin, c->step_dev,
+                                in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc, vc, head_stride, c->max_seq,
+                                c->part, c->st));
+            /* merge (and, for K-quant wo, quantise in the same launch); mm then reuses the Q8_K row */
+            const int q8k = vec_dot_type(L->wo.type) == SDY_Q8_K &&
+                            sdy_attn_merge1_q8k_ok(in->n_head, hd, c->max_seq);
+            TRY(sdy_attn_merge1(c->part, c->step_dev, in->n_head, hd, c->max_seq, c->att, q8k ? c->xq[1] : NULL,
+                                c->st));
+            c->xq_src[0] = c->xq_src[1] = NULL;
+            if (q8k) {
+                c->xq_src[1] = c->att;
+                c->xq_n_tok[1] = 1;
+                c->xq_n_in[1] = q_dim;
+            }
+            TRY(mm(c, c->x, c->att, &L->wo, 1, NULL, c->x, 0));
+        } else {
+            TRY(norm_for(c, c->x, L->attn_norm, L->qkv_parts >= 2 ? &L->wqkv : &L->wq, n));
+            TRY(mm(c, c->q, c->xb, &L->wq, n, L->bq, NULL, 0));
+            TRY(mm(c, c->k, c->xb, &L->wk, n, L->bk, NULL, 0));
+            TRY(mm(c, c->v, c->xb, &L->wv, n, L->bv, NULL, 0));
+            TRY(sdy_qk_rope_kv(c->q, c->k, c->v, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos, c->rope_sin, pos0,
+                               n, in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc, vc, head_stride, c->st));
+            TRY(sdy_attention(c->q, kc, vc, n, in->n_head, in->n_kv_head, hd, pos0 + 1, head_stride, q_dim, c->part,
+                              c->att, q_dim, c->st));
+            TRY(mm(c, c->x, c->att, &L->wo, n, NULL, c->x, 1));
+        }
         if (in->n_expert) {
+            TRY(norm_for(c, c->x, L->ffn_norm, &L->gate_inp, n));
             TRY(moe(c, L, n));
             TRY(sdy_add(c->x, c->moe_sum, c->x, (long)n * dim, c->st));
         } else {
-            TRY(mm(c, c->hb, c->xb, &L->gate, n, NULL, NULL, 1));
-            TRY(mm(c, c->hb2, c->xb, &L->up, n, NULL, NULL, 0));
-            TRY(sdy_silu_mul(c->hb, c->hb2, (long)n * in->ffn_dim, c->st));
+            TRY(norm_for(c, c->x, L->ffn_norm, L->gu_fused ? &L->gate_up : &L->gate, n));
+            TRY(ffn_gate_up(c, c->xb, n, 0, L->gu_fused ? &L->gate_up : NULL, &L->gate, &L->up, in->ffn_dim));
             TRY(mm(c, c->x, c->hb, &L->down, n, NULL, c->x, 1));
         }
-        (void)kv_dim;
     }
     if (out_rows > 0) {
         const float *xs = c->x + (size_t)(n - out_rows) * dim;
-        TRY(sdy_rmsnorm(xs, m->output_norm, c->xb, dim, in->norm_eps, out_rows, dim, dim, c->st));
-        TRY(mm(c, c->logits_dev, c->xb, &m->output, out_rows, NULL, NULL, 1));
-        TRY(sdy_d2h(c->logits, c->logits_dev, (size_t)out_rows * in->n_vocab * 4, c->st));
+        TRY(norm_for(c, xs, m->output_norm, &m->output, out_rows));
+        TRY(mm(c, c->logits_dev, c->xb, &m->output, out_rows, NULL, NULL, 0));
     }
+    return 0;
+}
+
+int sdy_engine_forward(engine_ctx *c, const int32_t *tokens, int n, int out_rows) {
+    const engine_model_info *in = &c->m->info;
+    const int decode = n == 1 && c->decode_fused;
+    if (decode) {
+        c->step_host[0] = tokens[0];
+        c->step_host[1] = c->n_past;
+        TRY(sdy_h2d(c->step_dev, c->step_host, 2 * 4, c->st));
+        /* the first one-token step runs eagerly (it settles every lazily configured kernel); the
+           second is recorded as a graph that later steps replay */
+        if (c->graph_ok == 0 && c->use_graph && c->n_decode >= 1 && !in->n_expert) {
+            TRY(sdy_graph_begin(c->st));
+            int rc = layers(c, 1, out_rows, 1);
+            if (rc) {
+                sdy_graph_abort(c->st);
+                c->graph_ok = -1;
+                return rc;
+            }
+            if (sdy_graph_end(c->st, &c->graph)) {
+                c->graph = NULL;
+                c->graph_ok = -1; /* not recordable here: keep running eagerly */
+            } else {
+                c->graph_ok = 1;
+            }
+        }
+        if (c->graph_ok == 1 && out_rows == 1) TRY(sdy_graph_launch(c->graph, c->st));
+        else TRY(layers(c, 1, out_rows, 1));
+        c->n_decode++;
+    } else {
+        memcpy(c->tok_host, tokens, (size_t)n * 4);
+        TRY(sdy_h2d(c->tok_dev, c->tok_host, (size_t)n * 4, c->st));
+        TRY(layers(c, n, out_rows, 0));
+    }
+    if (out_rows > 0) TRY(sdy_d2h(c->logits, c->logits_dev, (size_t)out_rows * in->n_vocab * 4, c->st));
     TRY(sdy_sync(c->st));
     c->n_past += n;
     return 0;

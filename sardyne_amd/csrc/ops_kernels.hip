@@ -1,6 +1,6 @@
 // gfx950 kernels for the float side of the forward pass: RMSNorm, softmax, SiLU·mul, RoPE table
-// and rotation, GQA attention (split over positions, deterministic two-pass combine), MoE router
-// (softmax + top-k) and the small elementwise ops of the kernel-level ABI.
+// and rotation, MoE router (softmax + top-k) and the small elementwise ops of the kernel-level ABI
+// (attention: attn_kernels.hip).
 //
 // Numerics follow the reference (csrc/ops.c:456-533, csrc/model_llama.c:653-666) where it matters
 // for parity: RMSNorm and softmax sum in double and round the scale once, RoPE angles are computed
@@ -8,6 +8,7 @@
 // sum. Reductions use fixed trees, so every result is reproducible run to run.
 #include "sdy_device.h"
 #include "sdy_internal.h"
+#include "sdy_norm_dev.h"
 #include "sdy_ops.h"
 #include "sdy_shim.h"
 
@@ -37,161 +38,17 @@ SDY_DEV float block_reduce_max(float v, float *sh) {
 }
 
 // out[r] = x[r] * (1/sqrt(mean(x[r]^2) + eps)) * w, one 256-thread block per row
-// (csrc/ops.c:456-461: sum of squares in double, scale rounded to float once).
+// (csrc/ops.c:346-351: sum of squares in double, scale rounded to float once).
 __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, float *out,
                                                  int n, float eps, long x_stride, long out_stride) {
     __shared__ double sh[4];
     const float *xr = x + blockIdx.x * x_stride;
     float *o = out + blockIdx.x * out_stride;
-    double ss = 0.0;
-    for (int i = threadIdx.x; i < n; i += 256) ss += (double)xr[i] * (double)xr[i];
-    ss = block_reduce_sum(ss, sh);
-    float scale = (float)(1.0 / sqrt(ss / (double)n + (double)eps));
+    const double ss = sdy_row_sumsq<0>(xr, n, nullptr, sh);
+    const float scale = (float)(1.0 / sqrt(ss / (double)n + (double)eps));
     for (int i = threadIdx.x; i < n; i += 256) {
         float t = xr[i] * scale;
         o[i] = t * w[i];
-    }
-}
-
-// Per-head RMSNorm of q and k (qwen3 q/k norm), then RoPE, then K and V written into the cache.
-// Grid: (n_tok, n_head + n_kv_head), block 64 threads (head_dim <= 512).
-__global__ __launch_bounds__(64) void k_qk_rope_kv(float *q, float *k, const float *v, const float *qn, const float *kn,
-                                                   float eps, const float *rope_cos, const float *rope_sin, int pos0,
-                                                   int n_head, int n_kv_head, int hd, int interleaved, float *k_cache,
-                                                   float *v_cache, long head_stride) {
-    __shared__ float buf[512];
-    __shared__ double shd[1];
-    const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
-    const bool is_q = h < n_head;
-    const int hh = is_q ? h : h - n_head;
-    float *vec = is_q ? q + ((size_t)t * n_head + hh) * hd : k + ((size_t)t * n_kv_head + hh) * hd;
-    const float *nw = is_q ? qn : kn;
-    for (int i = lane; i < hd; i += 64) buf[i] = vec[i];
-    __syncthreads();
-    if (nw) {
-        double ss = 0.0;
-        for (int i = lane; i < hd; i += 64) ss += (double)buf[i] * (double)buf[i];
-        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-        float scale = (float)(1.0 / sqrt(ss / (double)hd + (double)eps));
-        for (int i = lane; i < hd; i += 64) {
-            float tt = buf[i] * scale;
-            buf[i] = tt * nw[i];
-        }
-        __syncthreads();
-    }
-    (void)shd;
-    const int half = hd / 2, pos = pos0 + t;
-    const float *cs = rope_cos + (size_t)pos * half, *sn = rope_sin + (size_t)pos * half;
-    for (int i = lane; i < half; i += 64) {
-        int ia = interleaved ? 2 * i : i, ib = interleaved ? 2 * i + 1 : i + half;
-        float a = buf[ia], b = buf[ib];
-        float ac = a * cs[i], bs = b * sn[i], as = a * sn[i], bc = b * cs[i];
-        buf[ia] = ac - bs;
-        buf[ib] = as + bc;
-    }
-    __syncthreads();
-    for (int i = lane; i < hd; i += 64) vec[i] = buf[i];
-    if (!is_q && k_cache) {
-        float *kc = k_cache + hh * head_stride + (size_t)pos * hd;
-        float *vc = v_cache + hh * head_stride + (size_t)pos * hd;
-        const float *vv = v + ((size_t)t * n_kv_head + hh) * hd;
-        for (int i = lane; i < hd; i += 64) {
-            kc[i] = buf[i];
-            vc[i] = vv[i];
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------------- attention
-// Pass 1: block (chunk c, kv head g, token t) scores positions [c*CH, min((c+1)*CH, n_kv(t))) for
-// the n_rep query heads of g: K/V chunk staged in LDS once, then per head the chunk max, the sum
-// of exp, and the exp-weighted sum of V. Pass 2 merges the chunks of each (token, head) in chunk
-// order. n_kv(t) = n_kv0 + t (causal mask: token t sees positions 0..pos0+t).
-constexpr int ATT_CH = 64;
-
-__global__ __launch_bounds__(256) void k_attn_partial(const float *__restrict__ q, const float *__restrict__ k_cache,
-                                                      const float *__restrict__ v_cache, int n_head, int n_kv_head,
-                                                      int hd, int n_kv0, long head_stride, long q_stride,
-                                                      float *__restrict__ part, int n_chunk_max, float scale) {
-    extern __shared__ float sm[];
-    const int c = blockIdx.x, g = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
-    const int n_kv = n_kv0 + t, p0 = c * ATT_CH;
-    if (p0 >= n_kv) return;
-    const int np = n_kv - p0 < ATT_CH ? n_kv - p0 : ATT_CH;
-    const int n_rep = n_head / n_kv_head, kstride = hd + 1;
-    float *ks = sm;                        // [ATT_CH][hd+1]
-    float *vs = ks + ATT_CH * kstride;     // [ATT_CH][hd]
-    float *qs = vs + ATT_CH * hd;          // [n_rep][hd]
-    float *ps = qs + n_rep * hd;           // [n_rep][ATT_CH]
-    const float *kg = k_cache + g * head_stride + (size_t)p0 * hd;
-    const float *vg = v_cache + g * head_stride + (size_t)p0 * hd;
-    for (int i = tid; i < np * hd; i += 256) {
-        int p = i / hd, d = i - p * hd;
-        ks[p * kstride + d] = kg[i];
-        vs[i] = vg[i];
-    }
-    for (int i = tid; i < n_rep * hd; i += 256) qs[i] = q[(size_t)t * q_stride + (size_t)g * n_rep * hd + i];
-    __syncthreads();
-    // scores: one (head, position) pair per thread and step
-    for (int i = tid; i < n_rep * ATT_CH; i += 256) {
-        int r = i / ATT_CH, p = i - r * ATT_CH;
-        float s = -INFINITY;
-        if (p < np) {
-            const float *qq = qs + r * hd, *kk = ks + p * kstride;
-            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-            int d = 0;
-            for (; d + 4 <= hd; d += 4) {
-                a0 = fmaf(qq[d], kk[d], a0);
-                a1 = fmaf(qq[d + 1], kk[d + 1], a1);
-                a2 = fmaf(qq[d + 2], kk[d + 2], a2);
-                a3 = fmaf(qq[d + 3], kk[d + 3], a3);
-            }
-            for (; d < hd; d++) a0 = fmaf(qq[d], kk[d], a0);
-            s = ((a0 + a1) + (a2 + a3)) * scale;
-        }
-        ps[i] = s;
-    }
-    __syncthreads();
-    // per head: chunk max, exp, sum (one wave per head in turn)
-    const int wave = tid >> 6, lane = tid & 63;
-    for (int r = wave; r < n_rep; r += 4) {
-        float m = ps[r * ATT_CH + lane];  // ATT_CH == 64: one position per lane
-        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        float e = lane < np ? expf(ps[r * ATT_CH + lane] - m) : 0.0f;
-        ps[r * ATT_CH + lane] = e;
-        float l = e;
-        for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off);
-        if (lane == 0) {
-            float *pp = part + (((size_t)t * n_head + g * n_rep + r) * n_chunk_max + c) * (hd + 2);
-            pp[0] = m;
-            pp[1] = l;
-        }
-    }
-    __syncthreads();
-    // o[r][d] = sum_p e[r][p] * v[p][d]
-    for (int i = tid; i < n_rep * hd; i += 256) {
-        int r = i / hd, d = i - r * hd;
-        const float *pr = ps + r * ATT_CH;
-        float a = 0.0f;
-        for (int p = 0; p < np; p++) a = fmaf(pr[p], vs[p * hd + d], a);
-        part[(((size_t)t * n_head + g * n_rep + r) * n_chunk_max + c) * (hd + 2) + 2 + d] = a;
-    }
-}
-
-// Pass 2: one block per (head, token); merges the chunks in order.
-__global__ __launch_bounds__(128) void k_attn_combine(const float *__restrict__ part, int n_head, int hd, int n_kv0,
-                                                      int n_chunk_max, float *__restrict__ out, long out_stride) {
-    const int h = blockIdx.x, t = blockIdx.y;
-    const int n_kv = n_kv0 + t, nc = (n_kv + ATT_CH - 1) / ATT_CH;
-    const float *pp = part + ((size_t)t * n_head + h) * n_chunk_max * (hd + 2);
-    float M = -INFINITY;
-    for (int c = 0; c < nc; c++) M = fmaxf(M, pp[c * (hd + 2)]);
-    float L = 0.0f;
-    for (int c = 0; c < nc; c++) L = L + pp[c * (hd + 2) + 1] * expf(pp[c * (hd + 2)] - M);
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-        float a = 0.0f;
-        for (int c = 0; c < nc; c++) a = fmaf(pp[c * (hd + 2) + 2 + d], expf(pp[c * (hd + 2)] - M), a);
-        out[(size_t)t * out_stride + (size_t)h * hd + d] = a / L;
     }
 }
 
@@ -390,46 +247,6 @@ extern "C" int sdy_rmsnorm(const float *x, const float *w, float *out, int n, fl
     if (n_rows <= 0) return 0;
     hipLaunchKernelGGL(k_rmsnorm, dim3(n_rows), dim3(256), 0, (hipStream_t)s, x, w, out, n, eps, x_stride, out_stride);
     return sdy_check_launch("rmsnorm");
-}
-
-extern "C" int sdy_qk_rope_kv(float *q, float *k, const float *v, const float *qn, const float *kn, float eps,
-                              const float *rope_cos, const float *rope_sin, int pos0, int n_tok, int n_head,
-                              int n_kv_head, int hd, int interleaved, float *k_cache, float *v_cache,
-                              long head_stride, sdy_stream s) {
-    if (hd > 512) return sdy_fail(-1, "head_dim %d above 512", hd);
-    hipLaunchKernelGGL(k_qk_rope_kv, dim3(n_tok, n_head + n_kv_head), dim3(64), 0, (hipStream_t)s, q, k, v, qn, kn, eps,
-                       rope_cos, rope_sin, pos0, n_head, n_kv_head, hd, interleaved, k_cache, v_cache, head_stride);
-    return sdy_check_launch("qk_rope_kv");
-}
-
-extern "C" size_t sdy_attn_part_floats(int n_tok, int n_head, int hd, int max_kv) {
-    int nc = (max_kv + ATT_CH - 1) / ATT_CH;
-    return (size_t)n_tok * n_head * nc * (hd + 2);
-}
-
-extern "C" int sdy_attention(const float *q, const float *k_cache, const float *v_cache, int n_tok, int n_head,
-                             int n_kv_head, int hd, int n_kv0, long head_stride, long q_stride, float *part,
-                             float *out, long out_stride, sdy_stream s) {
-    hipStream_t st = (hipStream_t)s;
-    if (n_tok <= 0) return 0;
-    const int n_rep = n_head / n_kv_head;
-    const int n_kv_max = n_kv0 + n_tok - 1;
-    const int nc = (n_kv_max + ATT_CH - 1) / ATT_CH;
-    size_t lds = sizeof(float) * ((size_t)ATT_CH * (hd + 1) + (size_t)ATT_CH * hd + (size_t)n_rep * hd +
-                                  (size_t)n_rep * ATT_CH);
-    if (lds > 160 * 1024) return sdy_fail(-1, "attention: %zu bytes of LDS (head_dim %d, %d heads per KV head)", lds, hd, n_rep);
-    static int attr_set = 0;
-    if (lds > 64 * 1024 && !attr_set) {
-        (void)hipFuncSetAttribute((const void *)k_attn_partial, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        attr_set = 1;
-    }
-    float scale = 1.0f / sqrtf((float)hd);
-    hipLaunchKernelGGL(k_attn_partial, dim3(nc, n_kv_head, n_tok), dim3(256), lds, st, q, k_cache, v_cache, n_head,
-                       n_kv_head, hd, n_kv0, head_stride, q_stride, part, nc, scale);
-    int rc = sdy_check_launch("attention");
-    if (rc) return rc;
-    hipLaunchKernelGGL(k_attn_combine, dim3(n_head, n_tok), dim3(128), 0, st, part, n_head, hd, n_kv0, nc, out, out_stride);
-    return sdy_check_launch("attention_combine");
 }
 
 extern "C" int sdy_silu_mul(float *gate, const float *up, long n, sdy_stream s) {

@@ -29,6 +29,7 @@
 #include "sdy_device.h"
 #include "sdy_shim.h"
 #include "sdy_internal.h"
+#include "sdy_quant_dev.h"
 
 namespace {
 
@@ -55,14 +56,21 @@ SDY_DEV uint16_t ldw2(const uint8_t *p) { return *reinterpret_cast<const uint16_
 
 // ------------------------------------------------------------------------------------ repack
 
+// Row map of an upload: source row i goes to destination row (i / grp) * gstride + (i % grp) * step
+// of the planes in dst (step 2 interleaves two matrices; grp/gstride repeat that per expert).
+struct RowMap {
+    long step, grp, gstride;
+};
+
 template <int WT>
 __global__ void k_repack(const uint8_t *__restrict__ src, size_t src_row, Planes P, uint8_t *const *dst,
-                         long n_rows) {
+                         long n_rows, RowMap map) {
     long gid = blockIdx.x * (long)blockDim.x + threadIdx.x;
-    long row = gid / P.T;
-    int u = (int)(gid - row * P.T);
-    if (row >= n_rows) return;
-    const uint8_t *r = src + row * src_row;
+    long srow = gid / P.T;
+    int u = (int)(gid - srow * P.T);
+    if (srow >= n_rows) return;
+    const uint8_t *r = src + srow * src_row;
+    const long row = (srow / map.grp) * map.gstride + (srow % map.grp) * map.step;
     if constexpr (WT == SDY_Q4_K) {
         int s = u >> 2, j = u & 3;
         const uint8_t *sb = r + 144 * s;
@@ -234,45 +242,9 @@ __global__ void k_dequant_float(const uint8_t *__restrict__ w, int n_in, const i
 // Q8_K (csrc/quant.c:118-144): one wave per 256-element block, lane l holds elements 4l..4l+3.
 __global__ void k_quant_q8k(const float *__restrict__ x, uint8_t *__restrict__ out, int n_in) {
     const int nb = n_in / 256, s = blockIdx.x, t = blockIdx.y, l = threadIdx.x;
-    const float *xb = x + (size_t)t * n_in + 256 * s;
-    uint8_t *ob = out + ((size_t)t * nb + s) * 292;
-    float4 v = *reinterpret_cast<const float4 *>(xb + 4 * l);
-    float xs[4] = {v.x, v.y, v.z, v.w};
-    float best = 0.0f;
-    int bi = 0x7fffffff;
-    for (int e = 0; e < 4; e++)
-        if (fabsf(xs[e]) > best) {
-            best = fabsf(xs[e]);
-            bi = 4 * l + e;
-        }
-    for (int off = 32; off >= 1; off >>= 1) {
-        float ob_ = __shfl_xor(best, off);
-        int oi = __shfl_xor(bi, off);
-        if (ob_ > best || (ob_ == best && oi < bi)) {
-            best = ob_;
-            bi = oi;
-        }
-    }
-    if (best == 0.0f) {  // all-zero block: zero bytes (d, qs and bsums)
-        *reinterpret_cast<uint32_t *>(ob + 4 + 4 * l) = 0u;
-        if (l == 0) *reinterpret_cast<uint32_t *>(ob) = 0u;
-        if (l < 8) *reinterpret_cast<uint32_t *>(ob + 260 + 4 * l) = 0u;
-        return;
-    }
-    float vmax = xb[bi];
-    float iscale = -127.0f / vmax;
-    uint32_t packed = 0;
-    int lsum = 0;
-    for (int e = 0; e < 4; e++) {
-        int q = sdy_nearest_int(iscale * xs[e]);
-        q = q < 127 ? q : 127;
-        lsum += (int8_t)q;
-        packed |= (uint32_t)(uint8_t)(int8_t)q << (8 * e);
-    }
-    *reinterpret_cast<uint32_t *>(ob + 4 + 4 * l) = packed;
-    int gsum = sdy_quad_sum(lsum);  // group of 16 = lanes 4g..4g+3
-    if ((l & 3) == 0) *reinterpret_cast<int16_t *>(ob + 260 + 2 * (l >> 2)) = (int16_t)gsum;
-    if (l == 0) *reinterpret_cast<float *>(ob) = 1.0f / iscale;
+    const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)t * n_in + 256 * s + 4 * l);
+    const float xs[4] = {v.x, v.y, v.z, v.w};
+    sdy_q8k_block(xs, l, out + ((size_t)t * nb + s) * 292);
 }
 
 // Q8_0 (csrc/quant.c:98-108): one wave per two 32-element blocks, one element per lane.
@@ -280,18 +252,7 @@ __global__ void k_quant_q8_0(const float *__restrict__ x, uint8_t *__restrict__ 
     const int nblk = n_in / 32, t = blockIdx.y, l = threadIdx.x & 31;
     const int b = 2 * blockIdx.x + (threadIdx.x >> 5);
     if (b >= nblk) return;  // uniform per half-wave
-    float xv = x[(size_t)t * n_in + 32 * b + l];
-    float amax = fabsf(xv);
-    for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-    float d = amax / 127.0f;
-    float id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint8_t *ob = out + ((size_t)t * nblk + b) * 34;
-    ob[2 + l] = (uint8_t)(int8_t)roundf(xv * id);
-    if (l == 0) {
-        uint16_t h = sdy_f2h(d);
-        ob[0] = (uint8_t)(h & 255);
-        ob[1] = (uint8_t)(h >> 8);
-    }
+    sdy_q8_0_block(x[(size_t)t * n_in + 32 * b + l], l, out + ((size_t)t * nblk + b) * 34);
 }
 
 // ------------------------------------------------------------------------------------ matvec
@@ -321,6 +282,7 @@ struct MvArgs {
     int ipb;     // wave iterations per batch = ceil(rb * T / 64)
     int nterm;   // f32 terms per row and token (super-blocks or units)
     int q64, r64;  // 64 / T and 64 % T: advance of a lane's (row, unit) per iteration
+    int swiglu;    // rows (2i, 2i+1) are (gate, up) of output i: out[i] = silu(gate) * up
 };
 
 constexpr bool is_k(int wt) { return wt == SDY_Q4_K || wt == SDY_Q6_K; }
@@ -330,11 +292,25 @@ __device__ void stage_acts(const MvArgs &a, uint8_t *lds) {
     const int T = a.P.T, nb = a.P.nb, tid = threadIdx.x;
     const int n_tok = a.n_tok;
     if constexpr (is_k(WT)) {
-        // Q8_K rows: nb blocks of 292 B; y starts 4 bytes into a block (dword aligned)
-        for (int i = tid; i < n_tok * T * 16; i += THREADS) {
-            int m = i / (T * 16), r = i - m * T * 16, u = r >> 4, w = r & 15;
-            const uint8_t *src = a.xq + ((size_t)m * nb + (u >> 2)) * 292 + 4 + 64 * (u & 3) + 4 * w;
-            *reinterpret_cast<uint32_t *>(lds + ((m * 4 + (w >> 2)) * T + u) * 16 + 4 * (w & 3)) = ld4(src);
+        // Q8_K rows: nb blocks of 292 B; y starts 4 bytes into a block (dword aligned). The loads of
+        // 8 rounds go out before their LDS stores (clamped indices: no conditional load).
+        const int n_words = n_tok * T * 16;
+        for (int i0 = tid; i0 < n_words; i0 += 8 * THREADS) {
+            uint32_t v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = i0 + j * THREADS < n_words ? i0 + j * THREADS : n_words - 1;
+                const int m = i / (T * 16), r = i - m * T * 16, u = r >> 4, w = r & 15;
+                v[j] = ld4(a.xq + ((size_t)m * nb + (u >> 2)) * 292 + 4 + 64 * (u & 3) + 4 * w);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = i0 + j * THREADS;
+                if (i < n_words) {
+                    const int m = i / (T * 16), r = i - m * T * 16, u = r >> 4, w = r & 15;
+                    *reinterpret_cast<uint32_t *>(lds + ((m * 4 + (w >> 2)) * T + u) * 16 + 4 * (w & 3)) = v[j];
+                }
+            }
         }
         uint8_t *bs = lds + MT * 4 * T * 16;
         for (int i = tid; i < n_tok * T; i += THREADS) {
@@ -520,8 +496,6 @@ template <int WT, int MT, bool YREG>
 __global__ __launch_bounds__(THREADS) void k_matvec(MvArgs a) {
     extern __shared__ uint8_t lds[];
     const int T = a.P.T, nb = a.P.nb;
-    stage_acts<WT, MT>(a, lds);
-    __syncthreads();
     const size_t y_bytes = (size_t)MT * 4 * T * 16;
     const uint8_t *aux_base = lds + y_bytes;  // BS (K) or DX (32-element types)
     const float *yd = reinterpret_cast<const float *>(lds + y_bytes + (size_t)MT * T * 8);
@@ -535,8 +509,25 @@ __global__ __launch_bounds__(THREADS) void k_matvec(MvArgs a) {
     const long n_batches = (n_rows + rb - 1) / rb;
     const long n_waves = (long)gridDim.x * WAVES, wid = (long)blockIdx.x * WAVES + wave;
     const long b_begin = n_batches * wid / n_waves, b_end = n_batches * (wid + 1) / n_waves;
-    if (b_begin >= b_end) return;
     const int rl0 = lane / T, u0 = lane - rl0 * T;  // lane's (row, unit) in the first iteration of a batch
+
+    // the lane's task in (batch b, iteration i): rl, u; validity: task < tasks and row < row1
+    long b = b_begin;
+    int it = 0, rl = rl0, u = u0;
+    auto row_of = [&](long bb, int rr) -> long { return a.row0 + bb * rb + rr; };
+    auto lane_ok = [&](long bb, int itx, int rr) -> bool {
+        return itx * 64 + lane < tasks && row_of(bb, rr) < a.row1;
+    };
+    // the first weight loads are issued before the activations are staged, so that the two
+    // memory latencies overlap
+    WRegs<WT> cur, nxt;
+    if (b_begin < b_end) {
+        long row = lane_ok(b, it, rl) ? row_of(b, rl) : a.row0;
+        load_w<WT>(a.P, (uint32_t)(row - 0), (uint32_t)(lane_ok(b, it, rl) ? u : 0), cur);
+    }
+    stage_acts<WT, MT>(a, lds);
+    __syncthreads();
+    if (b_begin >= b_end) return;
 
     uint4 Yr[4];
     uint2 bsr = make_uint2(0u, 0u);
@@ -546,18 +537,6 @@ __global__ __launch_bounds__(THREADS) void k_matvec(MvArgs a) {
         if constexpr (is_k(WT)) bsr = *reinterpret_cast<const uint2 *>(aux_base + u0 * 8);
     }
 
-    // the lane's task in (batch b, iteration i): rl, u; validity: task < tasks and row < row1
-    long b = b_begin;
-    int it = 0, rl = rl0, u = u0;
-    auto row_of = [&](long bb, int rr) -> long { return a.row0 + bb * rb + rr; };
-    auto lane_ok = [&](long bb, int itx, int rr) -> bool {
-        return itx * 64 + lane < tasks && row_of(bb, rr) < a.row1;
-    };
-    WRegs<WT> cur, nxt;
-    {
-        long row = lane_ok(b, it, rl) ? row_of(b, rl) : a.row0;
-        load_w<WT>(a.P, (uint32_t)(row - 0), (uint32_t)(lane_ok(b, it, rl) ? u : 0), cur);
-    }
     for (;;) {
         // advance a copy of the position to the next iteration and prefetch it
         long nb_ = b;
@@ -625,16 +604,32 @@ __global__ __launch_bounds__(THREADS) void k_matvec(MvArgs a) {
         if (it + 1 == ipb) {
             // end of batch b: each lane sums the terms of one (row, token) in block order
             sdy_wave_sync();
-            for (int i = lane; i < rb * a.n_tok; i += 64) {
-                int r = i / a.n_tok, m = i - r * a.n_tok;
-                long row = row_of(b, r);
-                if (row >= a.row1) continue;
-                const float *tp = terms + (r * MT + m) * a.nterm;
-                float acc = 0.0f;
-                for (int s = 0; s < a.nterm; s++) acc = acc + tp[s];
-                if (a.bias) acc = acc + a.bias[row];
-                if (a.resid) acc = a.resid[(size_t)m * a.out_stride + row] + acc;
-                a.out[(size_t)m * a.out_stride + row] = acc;
+            if (a.swiglu) {
+                // rb is even and batches start at even rows: each (gate, up) pair is in this batch
+                for (int i = lane; i < (rb >> 1) * a.n_tok; i += 64) {
+                    int r = 2 * (i / a.n_tok), m = i - (r >> 1) * a.n_tok;
+                    long row = row_of(b, r);
+                    if (row >= a.row1) continue;
+                    const float *tg = terms + (r * MT + m) * a.nterm, *tu = terms + ((r + 1) * MT + m) * a.nterm;
+                    float g = 0.0f, up = 0.0f;
+                    for (int s = 0; s < a.nterm; s++) {
+                        g = g + tg[s];
+                        up = up + tu[s];
+                    }
+                    a.out[(size_t)m * a.out_stride + ((row - a.row0) >> 1)] = sdy_silu_mul1(g, up);
+                }
+            } else {
+                for (int i = lane; i < rb * a.n_tok; i += 64) {
+                    int r = i / a.n_tok, m = i - r * a.n_tok;
+                    long row = row_of(b, r);
+                    if (row >= a.row1) continue;
+                    const float *tp = terms + (r * MT + m) * a.nterm;
+                    float acc = 0.0f;
+                    for (int s = 0; s < a.nterm; s++) acc = acc + tp[s];
+                    if (a.bias) acc = acc + a.bias[row];
+                    if (a.resid) acc = a.resid[(size_t)m * a.out_stride + row] + acc;
+                    a.out[(size_t)m * a.out_stride + row] = acc;
+                }
             }
             sdy_wave_sync();
         }
@@ -656,9 +651,10 @@ __global__ __launch_bounds__(THREADS) void k_matvec(MvArgs a) {
 template <int WT, int MT, bool YREG>
 __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
     extern __shared__ uint8_t lds[];
+    // One token of Q8_K activations in memory: every lane reads the 64 activation bytes of its unit
+    // (and the unit's bsums and block scale) straight into registers; no LDS staging, no barrier.
+    constexpr bool DIRECT = YREG && is_k(WT) && MT == 1;
     const int T = a.P.T, nb = a.P.nb;
-    stage_acts<WT, MT>(a, lds);
-    __syncthreads();
     const size_t y_bytes = (size_t)MT * 4 * T * 16;
     const uint8_t *aux_base = lds + y_bytes;
     const float *yd = reinterpret_cast<const float *>(lds + y_bytes + (size_t)MT * T * 8);
@@ -675,26 +671,44 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
     const long n_waves = G * WAVES, wid = vblk * WAVES + wave;
     // grid-stride: at any moment the waves of the grid read neighbouring rows, so the whole GPU
     // sweeps each plane front to back
-    if (wid >= n_it) return;
-
-    uint4 Yr[4];
-    uint2 bsr = make_uint2(0u, 0u);
-    float2 dxr = make_float2(0.f, 0.f);
-    int2 syr = make_int2(0, 0);
-    if constexpr (YREG) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) Yr[q] = *reinterpret_cast<const uint4 *>(lds + (q * T + u) * 16);
-        if constexpr (is_k(WT)) bsr = *reinterpret_cast<const uint2 *>(aux_base + u * 8);
-        else {
-            dxr = *reinterpret_cast<const float2 *>(aux_base + u * 8);
-            syr = *reinterpret_cast<const int2 *>(sy + u * 2);
-        }
-    }
     auto row_at = [&](long itx) -> long { return a.row0 + itx * rpi + rl; };
     auto load_it = [&](long itx, WRegs<WT> &r) {
         long rr = row_at(itx);
         load_w<WT>(a.P, (uint32_t)(rr < a.row1 ? rr : a.row0), (uint32_t)u, r);
     };
+    // the first weight loads go out before anything else, so their latency overlaps the
+    // activation loads
+    WRegs<WT> A, B;
+    if (wid < n_it) load_it(wid, A);
+
+    uint4 Yr[4];
+    uint2 bsr = make_uint2(0u, 0u);
+    float2 dxr = make_float2(0.f, 0.f);
+    int2 syr = make_int2(0, 0);
+    float ydr = 0.0f;
+    if constexpr (DIRECT) {
+        if (wid >= n_it) return;
+        const uint8_t *blk = a.xq + (size_t)(u >> 2) * 292;
+        const uint8_t *yb = blk + 4 + 64 * (u & 3);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            Yr[q] = make_uint4(ld4(yb + 16 * q), ld4(yb + 16 * q + 4), ld4(yb + 16 * q + 8), ld4(yb + 16 * q + 12));
+        bsr = make_uint2(ld4(blk + 260 + 8 * (u & 3)), ld4(blk + 264 + 8 * (u & 3)));
+        ydr = *reinterpret_cast<const float *>(blk);
+    } else {
+        stage_acts<WT, MT>(a, lds);
+        __syncthreads();
+        if (wid >= n_it) return;
+        if constexpr (YREG) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) Yr[q] = *reinterpret_cast<const uint4 *>(lds + (q * T + u) * 16);
+            if constexpr (is_k(WT)) bsr = *reinterpret_cast<const uint2 *>(aux_base + u * 8);
+            else {
+                dxr = *reinterpret_cast<const float2 *>(aux_base + u * 8);
+                syr = *reinterpret_cast<const int2 *>(sy + u * 2);
+            }
+        }
+    }
     auto body = [&](const WRegs<WT> &cur, long itx) {
         const long row = row_at(itx);
         const bool valid = row < a.row1;
@@ -724,7 +738,7 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
             if constexpr (is_k(WT)) {
                 isum = sdy_quad_sum(isum);
                 if constexpr (WT == SDY_Q4_K) msum = sdy_quad_sum(msum);
-                const float ydv = yd[m * nb + (u >> 2)];
+                const float ydv = DIRECT ? ydr : yd[m * nb + (u >> 2)];
                 if constexpr (WT == SDY_Q4_K) {
                     float d = sdy_h2f((uint16_t)(cur.c.x & 0xFFFFu)), dmin = sdy_h2f((uint16_t)(cur.c.x >> 16));
                     float dall = ydv * d, dmn = ydv * dmin;
@@ -735,15 +749,21 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
                     float ydd = ydv * d;
                     term = ydd * (float)isum;
                 }
-                // sequential fold over the row's super-blocks: lane rl*T reads lanes rl*T + 4s
-                acc = term;
+                // sequential fold over the row's super-blocks (lane rl*T reads lanes rl*T + 4s), from
+                // the reference's initial 0.0f
+                acc = 0.0f + term;
                 const int nsb = T >> 2;
                 for (int s = 1; s < nsb; s++) acc = acc + __shfl(term, lane + 4 * s);
             } else {
                 acc = term;
                 for (int off = 1; off < T; off <<= 1) acc = acc + __shfl_xor(acc, off);
             }
-            if (u == 0 && valid) {
+            if (a.swiglu) {
+                // rows per iteration is even and row0 is even: lane (rl+1)*T holds the up row
+                const float up = __shfl(acc, (lane + T) & 63);
+                if (u == 0 && (rl & 1) == 0 && valid)
+                    a.out[(size_t)m * a.out_stride + ((row - a.row0) >> 1)] = sdy_silu_mul1(acc, up);
+            } else if (u == 0 && valid) {
                 if (a.bias) acc = acc + a.bias[row];
                 if (a.resid) acc = a.resid[(size_t)m * a.out_stride + row] + acc;
                 a.out[(size_t)m * a.out_stride + row] = acc;
@@ -751,15 +771,94 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
         }
     };
     // ping-pong register buffers: the loads of one iteration stay in flight while the other computes
-    WRegs<WT> A, B;
     const long S = n_waves;
-    load_it(wid, A);
     for (long itx = wid; itx < n_it; itx += 2 * S) {
         if (itx + S < n_it) load_it(itx + S, B);
         body(A, itx);
         if (itx + S >= n_it) break;
         if (itx + 2 * S < n_it) load_it(itx + 2 * S, A);
         body(B, itx + S);
+    }
+}
+
+// Long rows, one token (K-quants with T > 64 units or T not dividing 64, e.g. n_in = 11008 with
+// 172 units): a wave owns whole rows, lane l handles units l, l + 64, ..., l + 64 (NI - 1) of a row.
+// After the quad reduction the term of super-block s = 16k + q sits in lane 4q of pass k, and the
+// row sum folds the terms in super-block order with lane reads (the reference's sequential f32
+// order). Activations are staged in LDS. Each wave walks its rows one at a time; its first row's
+// weights are requested before the activations are staged.
+template <int WT, int NI>
+__global__ __launch_bounds__(THREADS) void k_matvec_lr(MvArgs a) {
+    extern __shared__ uint8_t lds[];
+    const int T = a.P.T, nb = a.P.nb;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const long n_rows = a.row1 - a.row0;
+    const long G = gridDim.x, bx = blockIdx.x;
+    const long vblk = (G % 8 == 0) ? (bx % 8) * (G / 8) + bx / 8 : bx;  // XCD-aware renumbering
+    const long S = G * WAVES, wid = vblk * WAVES + wave;
+    auto load_row = [&](long r, WRegs<WT> (&R)[NI]) {
+#pragma unroll
+        for (int k = 0; k < NI; k++) {
+            const int u = 64 * k + lane;
+            load_w<WT>(a.P, (uint32_t)(a.row0 + r), (uint32_t)(u < T ? u : 0), R[k]);
+        }
+    };
+    WRegs<WT> A[NI];
+    if (wid < n_rows) load_row(wid, A);
+    stage_acts<WT, 1>(a, lds);
+    __syncthreads();
+    if (wid >= n_rows) return;
+    const uint8_t *aux = lds + (size_t)4 * T * 16;
+    const float *yd = reinterpret_cast<const float *>(aux + (size_t)T * 8);
+    auto body = [&](const WRegs<WT> (&R)[NI], long r) {
+        float term[NI];
+#pragma unroll
+        for (int k = 0; k < NI; k++) {
+            const int u = 64 * k + lane, uu = u < T ? u : 0;
+            uint4 Y[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) Y[q] = *reinterpret_cast<const uint4 *>(lds + (q * T + uu) * 16);
+            const uint2 bsp = *reinterpret_cast<const uint2 *>(aux + uu * 8);
+            int isum, msum;
+            float dummy = 0.0f;
+            unit_dot<WT>(R[k], Y, bsp, uu, isum, msum, dummy, make_float2(0.f, 0.f), make_int2(0, 0));
+            isum = sdy_quad_sum(isum);
+            if constexpr (WT == SDY_Q4_K) msum = sdy_quad_sum(msum);
+            const float ydv = yd[uu >> 2];
+            if constexpr (WT == SDY_Q4_K) {
+                float d = sdy_h2f((uint16_t)(R[k].c.x & 0xFFFFu)), dmin = sdy_h2f((uint16_t)(R[k].c.x >> 16));
+                float dall = ydv * d, dmn = ydv * dmin;
+                float t1 = dall * (float)isum, t2 = dmn * (float)msum;
+                term[k] = t1 - t2;
+            } else {
+                float d = sdy_h2f((uint16_t)R[k].g);
+                float ydd = ydv * d;
+                term[k] = ydd * (float)isum;
+            }
+        }
+        // fold in super-block order: super-block 16k + q is in lane 4q of pass k
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NI; k++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int sb = 16 * k + q;
+                if (sb < nb) {
+                    const float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(term[k]), 4 * q));
+                    acc = acc + t;
+                }
+            }
+        if (lane == 0) {
+            const long row = a.row0 + r;
+            if (a.bias) acc = acc + a.bias[row];
+            if (a.resid) acc = a.resid[row] + acc;
+            a.out[row] = acc;
+        }
+    };
+    // one row in registers per wave: the waves resident on a SIMD overlap each other's loads
+    for (long r = wid; r < n_rows; r += S) {
+        body(A, r);
+        if (r + S < n_rows) load_row(r + S, A);
     }
 }
 
@@ -801,6 +900,8 @@ __global__ __launch_bounds__(THREADS) void k_matvec_float(const uint8_t *__restr
 // =============================================================================== host launchers
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+
 
 static int n_units(int type, int n_in) {
     if (type == SDY_Q4_K || type == SDY_Q6_K) return n_in / 64;
@@ -879,7 +980,7 @@ static int check_shape(int type, int n_in, long n_rows) {
     return 0;
 }
 
-extern "C" int sdy_mat_from_device(sdy_mat *m, int type, int n_in, long n_rows, const void *dev_raw, sdy_stream s) {
+extern "C" int sdy_mat_alloc(sdy_mat *m, int type, int n_in, long n_rows) {
     int rc = check_shape(type, n_in, n_rows);
     if (rc) return rc;
     memset(m, 0, sizeof(*m));
@@ -895,42 +996,82 @@ extern "C" int sdy_mat_from_device(sdy_mat *m, int type, int n_in, long n_rows, 
         m->plane_off[i] = off;
         if (pb[i]) off += align256(pb[i] * (size_t)n_rows);
     }
+    return 0;
+}
+
+// Repacks n raw GGUF-layout rows (device memory) into rows r0 + map(i) of m (RowMap above).
+static int repack_rows(sdy_mat *m, long r0, RowMap map, long n, const void *dev_raw, sdy_stream s) {
     hipStream_t st = (hipStream_t)s;
-    if (is_float_type(type)) return sdy_d2d(m->base, dev_raw, pb[0] * n_rows, s);
+    const int type = m->type;
+    const size_t src_row = sdy_raw_row_bytes(type, m->n_in);
+    if (is_float_type(type)) {
+        if (map.step != 1 || map.gstride != 0)
+            return sdy_fail(-1, "interleaved layouts are for quantized types");
+        return sdy_d2d((uint8_t *)m->base + m->plane_off[0] + src_row * r0, dev_raw, src_row * n, s);
+    }
+    size_t pb[5];
+    plane_row_bytes(type, m->n_in, pb);
     uint8_t *dst_h[5];
-    for (int i = 0; i < 5; i++) dst_h[i] = (uint8_t *)m->base + m->plane_off[i];
+    for (int i = 0; i < 5; i++) dst_h[i] = (uint8_t *)m->base + m->plane_off[i] + pb[i] * (size_t)r0;
     uint8_t **dst_d = nullptr;
+    int rc;
     if ((rc = sdy_malloc((void **)&dst_d, sizeof(dst_h)))) return rc;
-    if ((rc = sdy_h2d(dst_d, dst_h, sizeof(dst_h), s))) return rc;
+    if ((rc = sdy_h2d(dst_d, dst_h, sizeof(dst_h), s))) {
+        sdy_free(dst_d);
+        return rc;
+    }
     Planes P = planes_of(m);
-    long total = n_rows * (long)m->n_units;
+    long total = n * (long)m->n_units;
     dim3 grid((unsigned)((total + 255) / 256)), block(256);
-    size_t src_row = sdy_raw_row_bytes(type, n_in);
     const uint8_t *src = (const uint8_t *)dev_raw;
     switch (type) {
-    case SDY_Q4_K: hipLaunchKernelGGL(k_repack<SDY_Q4_K>, grid, block, 0, st, src, src_row, P, dst_d, n_rows); break;
-    case SDY_Q6_K: hipLaunchKernelGGL(k_repack<SDY_Q6_K>, grid, block, 0, st, src, src_row, P, dst_d, n_rows); break;
-    case SDY_Q8_0: hipLaunchKernelGGL(k_repack<SDY_Q8_0>, grid, block, 0, st, src, src_row, P, dst_d, n_rows); break;
-    case SDY_Q4_0: hipLaunchKernelGGL(k_repack<SDY_Q4_0>, grid, block, 0, st, src, src_row, P, dst_d, n_rows); break;
-    case SDY_Q5_0: hipLaunchKernelGGL(k_repack<SDY_Q5_0>, grid, block, 0, st, src, src_row, P, dst_d, n_rows); break;
+    case SDY_Q4_K: hipLaunchKernelGGL(k_repack<SDY_Q4_K>, grid, block, 0, st, src, src_row, P, dst_d, n, map); break;
+    case SDY_Q6_K: hipLaunchKernelGGL(k_repack<SDY_Q6_K>, grid, block, 0, st, src, src_row, P, dst_d, n, map); break;
+    case SDY_Q8_0: hipLaunchKernelGGL(k_repack<SDY_Q8_0>, grid, block, 0, st, src, src_row, P, dst_d, n, map); break;
+    case SDY_Q4_0: hipLaunchKernelGGL(k_repack<SDY_Q4_0>, grid, block, 0, st, src, src_row, P, dst_d, n, map); break;
+    case SDY_Q5_0: hipLaunchKernelGGL(k_repack<SDY_Q5_0>, grid, block, 0, st, src, src_row, P, dst_d, n, map); break;
     }
-    if ((rc = sdy_check_launch("repack"))) return rc;
-    if ((rc = sdy_sync(s))) return rc;
+    if ((rc = sdy_check_launch("repack")) || (rc = sdy_sync(s))) {
+        sdy_free(dst_d);
+        return rc;
+    }
     return sdy_free(dst_d);
 }
 
-extern "C" int sdy_mat_upload(sdy_mat *m, int type, int n_in, long n_rows, const void *host_raw, sdy_stream s) {
-    int rc = check_shape(type, n_in, n_rows);
+extern "C" int sdy_mat_from_device(sdy_mat *m, int type, int n_in, long n_rows, const void *dev_raw, sdy_stream s) {
+    int rc = sdy_mat_alloc(m, type, n_in, n_rows);
     if (rc) return rc;
-    size_t raw = sdy_raw_row_bytes(type, n_in) * (size_t)n_rows;
+    if ((rc = repack_rows(m, 0, RowMap{1, n_rows, 0}, n_rows, dev_raw, s))) sdy_mat_free(m);
+    return rc;
+}
+
+extern "C" int sdy_mat_upload_map(sdy_mat *m, long r0, long n, long step, long grp, long gstride,
+                                  const void *host_raw, sdy_stream s) {
+    if (n < 0 || r0 < 0 || step < 1 || grp < 1 || gstride < 0) return sdy_fail(-1, "upload: bad row map");
+    if (n == 0) return 0;
+    const long last = r0 + ((n - 1) / grp) * gstride + ((n - 1) % grp) * step;
+    const long span = r0 + ((n - 1) / grp) * gstride + (grp - 1 < n - 1 ? grp - 1 : n - 1) * step;
+    if (last >= m->n_rows || span >= m->n_rows)
+        return sdy_fail(-1, "upload of %ld rows from row %ld (step %ld) outside %ld rows", n, r0, step, m->n_rows);
+    size_t raw = sdy_raw_row_bytes(m->type, m->n_in) * (size_t)n;
     void *tmp = nullptr;
+    int rc;
     if ((rc = sdy_malloc(&tmp, raw))) return rc;
-    if ((rc = sdy_h2d(tmp, host_raw, raw, s)) || (rc = sdy_mat_from_device(m, type, n_in, n_rows, tmp, s))) {
-        sdy_free(tmp);
-        return rc;
-    }
-    if ((rc = sdy_sync(s))) return rc;
-    return sdy_free(tmp);
+    if (!(rc = sdy_h2d(tmp, host_raw, raw, s))) rc = repack_rows(m, r0, RowMap{step, grp, gstride}, n, tmp, s);
+    if (!rc) rc = sdy_sync(s);
+    sdy_free(tmp);
+    return rc;
+}
+
+extern "C" int sdy_mat_upload_rows(sdy_mat *m, long r0, long step, long n, const void *host_raw, sdy_stream s) {
+    return sdy_mat_upload_map(m, r0, n, step, n > 0 ? n : 1, 0, host_raw, s);
+}
+
+extern "C" int sdy_mat_upload(sdy_mat *m, int type, int n_in, long n_rows, const void *host_raw, sdy_stream s) {
+    int rc = sdy_mat_alloc(m, type, n_in, n_rows);
+    if (rc) return rc;
+    if ((rc = sdy_mat_upload_rows(m, 0, 1, n_rows, host_raw, s))) sdy_mat_free(m);
+    return rc;
 }
 
 extern "C" int sdy_mat_free(sdy_mat *m) {
@@ -1009,20 +1150,27 @@ static int g_n_cu = 0;
 
 // Rows per batch: the smallest count giving at least 64 (row, unit) tasks with little idle-lane
 // waste, so that small matrices spread over many waves; long rows (T >= 64) take one row per batch.
-static int rows_per_batch(int T) {
-    if (T >= 64) return 1;
-    if (64 % T == 0) return 64 / T;
-    for (int rb = (64 + T - 1) / T; rb < 64; rb++) {
-        int tasks = rb * T, its = (tasks + 63) / 64;
-        if (its * 64 - tasks <= its * 8) return rb;  // at most 1/8 of the lanes idle
-    }
-    return 64;
+// With the SwiGLU epilogue the count is rounded up to even, so that a (gate, up) pair of rows
+// never straddles two batches.
+static int rows_per_batch(int T, bool swiglu) {
+    int rb = 64;
+    if (T >= 64) rb = 1;
+    else if (64 % T == 0) rb = 64 / T;
+    else
+        for (int r = (64 + T - 1) / T; r < 64; r++) {
+            int tasks = r * T, its = (tasks + 63) / 64;
+            if (its * 64 - tasks <= its * 8) {  // at most 1/8 of the lanes idle
+                rb = r;
+                break;
+            }
+        }
+    return swiglu ? (rb + 1) & ~1 : rb;
 }
 
 // LDS bytes of k_matvec: staged activations of MT tokens plus the per-wave term buffers.
-static size_t mv_lds_bytes(int wt, int T, int nb, int MT) {
+static size_t mv_lds_bytes(int wt, int T, int nb, int MT, int rb) {
     int nterm = is_k(wt) ? nb : T;
-    return (size_t)MT * 4 * T * 16 + (size_t)MT * T * 16 + (size_t)WAVES * rows_per_batch(T) * MT * nterm * 4;
+    return (size_t)MT * 4 * T * 16 + (size_t)MT * T * 16 + (size_t)WAVES * rb * MT * nterm * 4;
 }
 
 constexpr size_t LDS_MAX = 160 * 1024;
@@ -1030,10 +1178,11 @@ constexpr size_t LDS_MAX = 160 * 1024;
 template <int WT, int MT, bool YREG>
 static int launch_mv_k(MvArgs &A, size_t lds, hipStream_t st) {
     static int per_cu = 0;  // resident workgroups per CU for this instantiation (at this LDS size)
-    static size_t per_cu_lds = 0;
+    static size_t per_cu_lds = 0, granted = 0;
     const void *fn = (const void *)k_matvec<WT, MT, YREG>;
+    int rc = sdy_lds_limit(fn, lds, &granted);
+    if (rc) return rc;
     if (per_cu == 0 || per_cu_lds != lds) {
-        if (lds > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_MAX);
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, THREADS, lds) != hipSuccess || n < 1) n = 1;
         per_cu = n;
@@ -1070,6 +1219,40 @@ static int launch_mv_rl(MvArgs &A, size_t lds, hipStream_t st) {
     return sdy_check_launch("matvec");
 }
 
+template <int WT, int NI>
+static int launch_mv_lr_ni(MvArgs &A, size_t lds, hipStream_t st) {
+    static int per_cu = 0;
+    static size_t per_cu_lds = 0, granted = 0;
+    const void *fn = (const void *)k_matvec_lr<WT, NI>;
+    int rc = sdy_lds_limit(fn, lds, &granted);
+    if (rc) return rc;
+    if (per_cu == 0 || per_cu_lds != lds) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, THREADS, lds) != hipSuccess || n < 1) n = 1;
+        per_cu = n;
+        per_cu_lds = lds;
+    }
+    long wgs = (A.row1 - A.row0 + WAVES - 1) / WAVES;
+    long cap = (long)(g_n_cu ? g_n_cu : 256) * per_cu;
+    if (wgs > cap) wgs = cap;
+    hipLaunchKernelGGL((k_matvec_lr<WT, NI>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
+    return sdy_check_launch("matvec");
+}
+
+// one token, long rows: NI = ceil(T / 64) passes per row
+template <int WT>
+static int launch_mv_lr(MvArgs &A, size_t lds, hipStream_t st) {
+    switch ((A.P.T + 63) / 64) {
+    case 1: return launch_mv_lr_ni<WT, 1>(A, lds, st);
+    case 2: return launch_mv_lr_ni<WT, 2>(A, lds, st);
+    case 3: return launch_mv_lr_ni<WT, 3>(A, lds, st);
+    case 4: return launch_mv_lr_ni<WT, 4>(A, lds, st);
+    case 5: return launch_mv_lr_ni<WT, 5>(A, lds, st);
+    case 6: return launch_mv_lr_ni<WT, 6>(A, lds, st);
+    default: return sdy_fail(-1, "matvec: rows of %d elements are above the one-token kernel's 24576", A.P.n_in);
+    }
+}
+
 template <int WT, int MT>
 static int launch_mv(const sdy_mat *m, const sdy_mv_args *a, int n_tok, const uint8_t *xq, float *out,
                      const float *resid, hipStream_t st) {
@@ -1084,18 +1267,21 @@ static int launch_mv(const sdy_mat *m, const sdy_mv_args *a, int n_tok, const ui
     A.row0 = a->row0;
     A.row1 = a->row1;
     const int T = A.P.T;
-    A.rb = rows_per_batch(T);
+    A.swiglu = a->epilogue == SDY_EPI_SWIGLU;
+    A.rb = rows_per_batch(T, A.swiglu);
     A.ipb = (A.rb * T + 63) / 64;
     A.q64 = 64 / T;
     A.r64 = 64 % T;
     A.nterm = is_k(WT) ? A.P.nb : T;
-    size_t lds = mv_lds_bytes(WT, T, A.P.nb, MT);
+    size_t lds = mv_lds_bytes(WT, T, A.P.nb, MT, A.rb);
     if (lds > LDS_MAX) return sdy_fail(-1, "matvec: %zu bytes of LDS needed (n_in %d, %d tokens)", lds, m->n_in, MT);
-    if (T <= 64 && 64 % T == 0) {
-        lds = mv_lds_bytes_rl(T, MT);
+    if (T <= 64 && 64 % T == 0 && (!A.swiglu || (64 / T) % 2 == 0)) {
+        lds = (MT == 1 && is_k(WT)) ? 0 : mv_lds_bytes_rl(T, MT);  // one K-quant token: no staging
         if (MT == 1) return launch_mv_rl<WT, MT, true>(A, lds, st);
         return launch_mv_rl<WT, MT, false>(A, lds, st);
     }
+    if constexpr (MT == 1 && is_k(WT))
+        if (!A.swiglu) return launch_mv_lr<WT>(A, mv_lds_bytes_rl(T, 1), st);
     return launch_mv_k<WT, MT, false>(A, lds, st);
 }
 
@@ -1104,8 +1290,9 @@ static int mv_type(const sdy_mat *m, const sdy_mv_args *a, hipStream_t st) {
     size_t xrow = sdy_raw_row_bytes(is_k(WT) ? SDY_Q8_K : SDY_Q8_0, m->n_in);
     const int T = m->n_units, nb = n_blocks(WT, m->n_in);
     // largest token capacity (8, 4, 2, 1) whose LDS fits; tokens are processed in chunks of it
+    const int rb = rows_per_batch(T, a->epilogue == SDY_EPI_SWIGLU);
     int cap = 8;
-    while (cap > 1 && mv_lds_bytes(WT, T, nb, cap) > LDS_MAX) cap /= 2;
+    while (cap > 1 && mv_lds_bytes(WT, T, nb, cap, rb) > LDS_MAX) cap /= 2;
     for (int t0 = 0; t0 < a->n_tok;) {
         int n = a->n_tok - t0 < cap ? a->n_tok - t0 : cap;
         const uint8_t *xq = (const uint8_t *)a->xq + xrow * t0;
@@ -1127,6 +1314,11 @@ extern "C" int sdy_matvec(const sdy_mat *m, const sdy_mv_args *a, sdy_stream s) 
     if (a->row0 < 0 || a->row1 > m->n_rows || a->row0 > a->row1)
         return sdy_fail(-1, "matvec rows [%ld, %ld) outside %ld", a->row0, a->row1, m->n_rows);
     if (a->row0 == a->row1 || a->n_tok <= 0) return 0;
+    if (a->epilogue == SDY_EPI_SWIGLU && (((a->row1 - a->row0) | a->row0) & 1 || a->bias || a->resid))
+        return sdy_fail(-1, "matvec: the SwiGLU epilogue needs an even row range starting at an even row, no bias "
+                            "and no residual");
+    if (a->epilogue == SDY_EPI_SWIGLU && (m->type == SDY_F32 || m->type == SDY_F16 || m->type == SDY_BF16))
+        return sdy_fail(-1, "matvec: the SwiGLU epilogue is for quantized weights");
     if (!g_n_cu) {
         int n_cu = 0;
         size_t mem = 0;

@@ -14,6 +14,14 @@ typedef struct {
 typedef struct {
     float *attn_norm, *ffn_norm, *bq, *bk, *bv, *q_norm, *k_norm; /* f32, device */
     dmat wq, wk, wv, wo, gate, up, down, gate_inp;
+    /* wq|wk (qkv_parts 2) or wq|wk|wv (3) of one type stored as one matrix; wq, wk (and wv) are
+       then row views of it, and bq|bk|bv are contiguous */
+    dmat wqkv;
+    int qkv_parts;
+    /* gate and up of one quantized type stored interleaved (row 2i = gate i, row 2i+1 = up i; per
+       expert for MoE): used with the SwiGLU matvec epilogue; gate and up are then unset */
+    dmat gate_up;
+    int gu_fused;
 } dlayer;
 
 struct engine_model {
@@ -39,6 +47,16 @@ struct engine_ctx {
     const float *xq_src[2];
     int xq_n_tok[2], xq_n_in[2];
     int32_t *tok_dev, *tok_host;
+    /* one-token decode: step_dev = {token, position} read by the kernels, so the recorded graph
+       replays for every position */
+    int32_t *step_dev, *step_host;
+    int32_t *att_counter;       /* arrival counter of the fused decode attention (kept at 0) */
+    void *graph;                /* recorded one-token decode step (NULL until recorded) */
+    int graph_ok;               /* 0: not tried, 1: recorded, -1: recording failed (run eagerly) */
+    int n_decode;               /* one-token evals so far (the first runs eagerly) */
+    int decode_fused;           /* one-token steps use the fused decode kernels */
+    int use_graph;              /* one-token steps are recorded once and replayed */
+    float *qkv;                 /* q | k | v of one token */
     /* MoE */
     float *moe_probs, *moe_w, *moe_x, *moe_y, *moe_sum, *moe_gw;
     int32_t *moe_top, *moe_gidx, *moe_top_host, *moe_gidx_host;
@@ -49,4 +67,5 @@ struct engine_ctx {
 int sdy_engine_alloc(engine_ctx *c);
 void sdy_engine_release(engine_ctx *c);
 int sdy_engine_forward(engine_ctx *c, const int32_t *tokens, int n, int out_rows);
+int sdy_engine_decode_fused_ok(const engine_ctx *c);
 #endif

@@ -10,6 +10,8 @@ extern "C" {
 int sdy_fail(int rc, const char *fmt, ...);
 /* Turns a pending kernel-launch error into an sdy error. */
 int sdy_check_launch(const char *what);
+/* Raises kernel fn's dynamic-LDS limit to `bytes` if *granted (per call site) is below it. */
+int sdy_lds_limit(const void *fn, size_t bytes, size_t *granted);
 /* Bytes of one row in the GGUF layout. */
 size_t sdy_raw_row_bytes(int type, int n_in);
 #ifdef __cplusplus

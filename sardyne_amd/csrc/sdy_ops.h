@@ -30,6 +30,25 @@ int sdy_rope(float *x, int n_heads, int hd, const float *cs, const float *sn, in
 int sdy_moe_route(float *probs, int n_tok, int n_expert, int k, int32_t *top, float *wts, sdy_stream s);
 int sdy_moe_combine(const float *y, const int32_t *top, const float *wts, int n_tok, int k, int dim, float *out,
                     const float *resid, sdy_stream s);
+/* RMSNorm of n_rows rows of n floats, then the activation quantiser vtype (SDY_Q8_K / SDY_Q8_0)
+ * into xq, or vtype SDY_F32: normalise only. xb receives the f32 rows (may be NULL when
+ * quantising). Bytes equal sdy_rmsnorm followed by sdy_quantize. */
+int sdy_norm_quant(const float *x, const float *w, float eps, int n, int n_rows, float *xb, int vtype, void *xq,
+                   sdy_stream s);
+/* One-token decode attention: q/k norm + RoPE + KV write at position step_dev[1], and the split
+ * attention over positions 0..step_dev[1] as partial records in part (n_head heads x
+ * sdy_attn_decode_chunks(max_seq) chunks), merged by sdy_attn_merge1. */
+int sdy_attn_decode_ok(int n_head, int n_kv_head, int hd, int max_seq);
+size_t sdy_attn_decode_chunks(int max_seq);
+int sdy_attn_decode(const float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
+                    float eps, const float *rope_cos, const float *rope_sin, const int32_t *step_dev, int n_head,
+                    int n_kv_head, int hd, int interleaved, float *k_cache, float *v_cache, long head_stride,
+                    int max_seq, float *part, sdy_stream s);
+/* out (f32, n_head * hd) = the merge of one token's records; with xq_q8k also its Q8_K row (when
+ * sdy_attn_merge1_q8k_ok), in the same launch. */
+int sdy_attn_merge1(const float *part, const int32_t *step_dev, int n_head, int hd, int max_seq, float *out,
+                    void *xq_q8k, sdy_stream s);
+int sdy_attn_merge1_q8k_ok(int n_head, int hd, int max_seq);
 #ifdef __cplusplus
 }
 #endif

@@ -37,6 +37,12 @@ int sdy_event_new(void **ev);
 int sdy_event_record(void *ev, sdy_stream s);
 int sdy_event_elapsed(float *ms, void *e0, void *e1); /* waits for e1 */
 int sdy_event_free(void *ev);
+/* stream capture into a replayable graph (hipGraph): begin, issue kernels on s, end */
+int sdy_graph_begin(sdy_stream s);
+int sdy_graph_end(sdy_stream s, void **exec);
+void sdy_graph_abort(sdy_stream s);
+int sdy_graph_launch(void *exec, sdy_stream s);
+int sdy_graph_free(void *exec);
 /* reads every byte of buf once (HBM bandwidth probe); sink: 4 bytes of device memory */
 int sdy_membw_read(const void *buf, size_t bytes, void *sink, sdy_stream s);
 
@@ -53,10 +59,17 @@ typedef struct {
 
 /* Bytes of the device layout for a matrix. */
 size_t sdy_mat_bytes(int type, int n_in, long n_rows);
-/* Upload raw GGUF-layout rows from host memory and repack them on the device. `staging` is a
- * device buffer of at least min(raw bytes, staging_bytes) bytes reused for chunked uploads; pass
- * NULL to let the function allocate one. */
+/* Upload raw GGUF-layout rows from host memory and repack them on the device. */
 int sdy_mat_upload(sdy_mat *m, int type, int n_in, long n_rows, const void *host_raw, sdy_stream s);
+/* Allocate a matrix in the device layout (contents undefined until rows are uploaded). */
+int sdy_mat_alloc(sdy_mat *m, int type, int n_in, long n_rows);
+/* Upload n raw rows from host memory into rows r0, r0 + step, ... of an allocated matrix: step 1
+ * fills a range (concatenated matrices), step 2 interleaves two matrices row by row. */
+int sdy_mat_upload_rows(sdy_mat *m, long r0, long step, long n, const void *host_raw, sdy_stream s);
+/* General form: source row i goes to row r0 + (i / grp) * gstride + (i % grp) * step (per-expert
+ * interleaving: grp = rows per expert, gstride = destination rows per expert, step 2). */
+int sdy_mat_upload_map(sdy_mat *m, long r0, long n, long step, long grp, long gstride, const void *host_raw,
+                       sdy_stream s);
 /* Same, from raw rows already in device memory. */
 int sdy_mat_from_device(sdy_mat *m, int type, int n_in, long n_rows, const void *dev_raw, sdy_stream s);
 int sdy_mat_free(sdy_mat *m);
@@ -80,7 +93,10 @@ typedef struct {
     const float *bias;   /* optional, out += bias[row] */
     const float *resid;  /* optional, out = resid[t * out_stride + row] + result */
     long row0, row1;     /* rows computed */
+    int epilogue;        /* SDY_EPI_NONE, or SDY_EPI_SWIGLU: rows (2i, 2i+1) of [row0, row1) are the gate and
+                            up rows of output i, out[t * out_stride + i] = silu(gate) * up */
 } sdy_mv_args;
+enum { SDY_EPI_NONE = 0, SDY_EPI_SWIGLU = 1 };
 /* out = W · x for rows [row0, row1) and n_tok tokens. */
 int sdy_matvec(const sdy_mat *m, const sdy_mv_args *a, sdy_stream s);
 

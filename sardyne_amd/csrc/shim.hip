@@ -39,6 +39,19 @@ extern "C" int sdy_check_launch(const char *what) {
     return 0;
 }
 
+// Raises the dynamic-LDS limit of kernel fn to `bytes` when *granted is below it (the limit counts
+// dynamic bytes only; a kernel's static LDS comes on top, so the request is exact, not the maximum).
+extern "C" int sdy_lds_limit(const void *fn, size_t bytes, size_t *granted) {
+    if (bytes <= 64 * 1024 || bytes <= *granted) return 0;
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return sdy_fail(-2, "dynamic LDS of %zu bytes refused: %s", bytes, hipGetErrorString(e));
+    }
+    *granted = bytes;
+    return 0;
+}
+
 extern "C" int sdy_init(void) {
     if (g_inited) return 0;
     int n = 0;
@@ -165,6 +178,42 @@ extern "C" int sdy_event_elapsed(float *ms, void *e0, void *e1) {
 extern "C" int sdy_event_free(void *ev) {
     if (!ev) return 0;
     HIPCK(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy");
+    return 0;
+}
+
+// ---- graphs: the kernels issued on a stream between begin and end are recorded once and
+// replayed with one launch. Relaxed capture mode: other threads may keep using HIP meanwhile.
+extern "C" int sdy_graph_begin(sdy_stream s) {
+    HIPCK(hipStreamBeginCapture((hipStream_t)s, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
+    return 0;
+}
+
+extern "C" int sdy_graph_end(sdy_stream s, void **exec) {
+    hipGraph_t g = nullptr;
+    HIPCK(hipStreamEndCapture((hipStream_t)s, &g), "hipStreamEndCapture");
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    *exec = (void *)ge;
+    return 0;
+}
+
+// Ends a capture that failed part-way; the partial graph is discarded.
+extern "C" void sdy_graph_abort(sdy_stream s) {
+    hipGraph_t g = nullptr;
+    if (hipStreamEndCapture((hipStream_t)s, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+    (void)hipGetLastError();
+}
+
+extern "C" int sdy_graph_launch(void *exec, sdy_stream s) {
+    HIPCK(hipGraphLaunch((hipGraphExec_t)exec, (hipStream_t)s), "hipGraphLaunch");
+    return 0;
+}
+
+extern "C" int sdy_graph_free(void *exec) {
+    if (!exec) return 0;
+    HIPCK(hipGraphExecDestroy((hipGraphExec_t)exec), "hipGraphExecDestroy");
     return 0;
 }
 

@@ -269,3 +269,79 @@ def test_dot_axpy_add():
     a = rng.standard_normal(1023).astype(np.float32)
     b = rng.standard_normal(1023).astype(np.float32)
     np.testing.assert_array_equal(capi.add(a, b), a + b)
+
+
+@pytest.mark.parametrize("vt,n,n_rows", [(O.Q8_K, 2048, 1), (O.Q8_K, 4096, 3), (O.Q8_0, 2048, 2), (O.Q8_0, 96, 1),
+                                         (O.F32, 200, 2)], ids=["q8k", "q8k-3rows", "q8_0", "q8_0-odd", "f32"])
+def test_norm_quant_equals_rmsnorm_then_quantize(vt, n, n_rows):
+    """The fused RMSNorm + activation quantiser writes the bytes of the two separate kernels, and
+    those equal the oracle's rmsnorm followed by the reference quantiser."""
+    L = lib()
+    rng = np.random.default_rng(n + n_rows)
+    x = (rng.standard_normal((n_rows, n)) * 3).astype(np.float32)
+    x[0, 5] = 40.0  # a dominant element
+    w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    dx, dw = capi.DeviceBuffer.from_array(x), capi.DeviceBuffer.from_array(w)
+    db1, db2 = capi.DeviceBuffer(x.nbytes), capi.DeviceBuffer(x.nbytes)
+    qbytes = O.row_size(vt, n) * n_rows if vt != O.F32 else 64
+    dq1, dq2 = capi.DeviceBuffer(qbytes), capi.DeviceBuffer(qbytes)
+    capi.check(L.sdy_rmsnorm(dx.ptr, dw.ptr, db1.ptr, n, 1e-6, n_rows, n, n, None))
+    if vt != O.F32:
+        capi.check(L.sdy_quantize(vt, db1.ptr, dq1.ptr, n, n_rows, None))
+    capi.check(L.sdy_norm_quant(dx.ptr, dw.ptr, 1e-6, n, n_rows, db2.ptr, vt, dq2.ptr if vt != O.F32 else None, None))
+    xb1, xb2 = db1.to_array(np.float32, (n_rows, n)), db2.to_array(np.float32, (n_rows, n))
+    assert np.array_equal(bits(xb1), bits(xb2))
+    exp = np.empty_like(x)
+    for r in range(n_rows):
+        O.lib().orc_rmsnorm(ptr(exp[r]), ptr(x[r]), ptr(w), n, 1e-6)
+    assert np.array_equal(bits(xb2), bits(exp))
+    if vt != O.F32:
+        q1, q2 = dq1.to_array(np.uint8, qbytes), dq2.to_array(np.uint8, qbytes)
+        assert np.array_equal(q1, q2)
+        assert np.array_equal(q2, O.quantize(exp, vt).reshape(-1))
+
+
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K", "Q8_0", "Q5_0"])
+@pytest.mark.parametrize("n_in,ffn,n_tok", [(2048, 96, 1), (1024, 40, 3), (11008, 8, 2), (768, 20, 1)])
+def test_swiglu_epilogue(kind, n_in, ffn, n_tok):
+    """gate and up uploaded interleaved (row 2i = gate i, 2i+1 = up i) and multiplied with the
+    SwiGLU epilogue give silu(gate.x) * (up.x) with the bits of the separate matvecs followed by
+    the SiLU kernel; the matvecs themselves are checked against the oracle."""
+    if kind in ("Q8_0", "Q5_0") and n_in % 32:
+        pytest.skip("row not a whole number of blocks")
+    t = TYPES[kind]
+    L = lib()
+    rng = np.random.default_rng(n_in + ffn)
+    nb = ffn * n_in // O.QK[t]
+    g = random_blocks(kind, nb, rng).reshape(ffn, -1)
+    u = random_blocks(kind, nb, rng).reshape(ffn, -1)
+    x = rng.standard_normal((n_tok, n_in)).astype(np.float32)
+    xq = O.quantize(x, O.VEC_DOT[t])
+    m = capi.SdyMat()
+    capi.check(L.sdy_mat_alloc(ctypes.byref(m), t, n_in, 2 * ffn))
+    capi.check(L.sdy_mat_upload_map(ctypes.byref(m), 0, ffn, 2, ffn, 0, ptr(g), None))
+    capi.check(L.sdy_mat_upload_map(ctypes.byref(m), 1, ffn, 2, ffn, 0, ptr(u), None))
+    dq = capi.DeviceBuffer.from_array(xq)
+    dout = capi.DeviceBuffer(n_tok * ffn * 4)
+    a = capi.SdyMvArgs(xq=dq.ptr, n_tok=n_tok, out=dout.ptr, out_stride=ffn, row0=0, row1=2 * ffn,
+                       epilogue=capi.EPI_SWIGLU)
+    capi.check(L.sdy_matvec(ctypes.byref(m), ctypes.byref(a), None))
+    got = dout.to_array(np.float32, (n_tok, ffn))
+    # separate path: both halves through the plain matvec, then the SiLU kernel
+    gm, um = capi.DeviceMatrix(t, n_in, ffn, g), capi.DeviceMatrix(t, n_in, ffn, u)
+    dg, du = capi.DeviceBuffer(n_tok * ffn * 4), capi.DeviceBuffer(n_tok * ffn * 4)
+    for mat, buf in ((gm, dg), (um, du)):
+        a2 = capi.SdyMvArgs(xq=dq.ptr, n_tok=n_tok, out=buf.ptr, out_stride=ffn, row0=0, row1=ffn)
+        capi.check(L.sdy_matvec(ctypes.byref(mat.m), ctypes.byref(a2), None))
+    yg, yu = dg.to_array(np.float32, (n_tok, ffn)), du.to_array(np.float32, (n_tok, ffn))
+    hg = yg.copy()
+    L.op_silu_mul(ptr(hg), ptr(yu), hg.size)
+    assert np.array_equal(bits(got), bits(hg))
+    simd = 1 if t in (O.Q4_K, O.Q6_K) else 0
+    eg, eu = O.matmul_q(g, t, xq, n_in, simd=simd), O.matmul_q(u, t, xq, n_in, simd=simd)
+    if t in (O.Q4_K, O.Q6_K):
+        assert np.array_equal(bits(yg), bits(eg)) and np.array_equal(bits(yu), bits(eu))
+    exp = eg.copy()
+    O.lib().orc_silu_mul(ptr(exp), ptr(eu), exp.size)
+    np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * float(np.abs(exp).max()))
+    L.sdy_mat_free(ctypes.byref(m))
