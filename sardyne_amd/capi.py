@@ -103,7 +103,7 @@ _SIGNATURES = {
 class SdyMat(ctypes.Structure):
     """Device-layout matrix descriptor (sdy_mat in sardyne_amd/csrc/sdy_shim.h)."""
     _fields_ = [("base", _vp), ("bytes", _sz), ("type", _int), ("n_in", _int), ("n_rows", ctypes.c_long),
-                ("n_units", _int), ("plane_off", _sz * 5)]
+                ("n_units", _int), ("plane_off", _sz * 5), ("gemm_ok", _int)]
 
 
 class SdyMvArgs(ctypes.Structure):
@@ -142,6 +142,9 @@ _DEVICE_SIGNATURES = {
                                   ctypes.c_long, ctypes.c_long, _vp, _vp]),
     "sdy_rmsnorm": (_int, [_vp, _vp, _vp, _int, ctypes.c_float, _int, ctypes.c_long, ctypes.c_long, _vp]),
     "sdy_norm_quant": (_int, [_vp, _vp, ctypes.c_float, _int, _int, _vp, _int, _vp, _vp]),
+    "sdy_gemm_ok": (_int, [ctypes.POINTER(SdyMat), _int]),
+    "sdy_gemm_ws_bytes": (_sz, [_int, _int]),
+    "sdy_gemm": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp, _vp]),
 }
 
 EPI_NONE, EPI_SWIGLU = 0, 1

@@ -31,6 +31,9 @@ static int vec_dot_type(int wtype) {
 
 static int dalloc(void **p, size_t n) { return sdy_malloc(p, n ? n : 64); }
 
+/* Token count from which quantized matrices go through the MFMA GEMM instead of the matvec. */
+#define GEMM_MIN_TOKENS 16
+
 int sdy_engine_alloc(engine_ctx *c) {
     const engine_model_info *in = &c->m->info;
     size_t B = (size_t)c->n_batch, S = (size_t)c->max_seq, hd = (size_t)in->head_dim;
@@ -61,8 +64,7 @@ int sdy_engine_alloc(engine_ctx *c) {
     TRY(dalloc((void **)&c->qkv, (q_dim + 2 * kv_dim) * 4));
     TRY(dalloc((void **)&c->step_dev, 2 * 4));
     TRY(sdy_host_alloc((void **)&c->step_host, 2 * 4));
-    TRY(dalloc((void **)&c->att_counter, 64));
-    TRY(sdy_memset(c->att_counter, 0, 64, c->st));
+    TRY(dalloc(&c->gemm_ws, sdy_gemm_ws_bytes((int)B, (int)max_in)));
     if (in->n_expert) {
         size_t chosen = B * in->n_expert_used;
         TRY(dalloc((void **)&c->moe_probs, B * in->n_expert * 4));
@@ -90,7 +92,7 @@ void sdy_engine_release(engine_ctx *c) {
     void *dev[] = {c->k_cache, c->v_cache, c->rope_cos, c->rope_sin, c->x, c->xb, c->q, c->k, c->v, c->att, c->hb,
                    c->hb2, c->logits_dev, c->part, c->xq[0], c->xq[1], c->tok_dev, c->moe_probs, c->moe_w,
                    c->moe_top, c->moe_x, c->moe_y, c->moe_sum, c->moe_gidx, c->moe_gw, c->qkv, c->step_dev,
-                   c->att_counter};
+                   c->gemm_ws};
     for (size_t i = 0; i < sizeof dev / sizeof *dev; i++) sdy_free(dev[i]);
     void *host[] = {c->tok_host, c->moe_top_host, c->moe_w_host, c->moe_gidx_host, c->moe_gw_host, c->step_host};
     for (size_t i = 0; i < sizeof host / sizeof *host; i++) sdy_host_free(host[i]);
@@ -123,6 +125,8 @@ static int mm_epi(engine_ctx *c, float *out, const float *x, const dmat *w, int 
             c->xq_n_in[s] = w->n_in;
         }
         a.xq = c->xq[s];
+        /* many tokens of a K-quant matrix: the MFMA GEMM (same bits as the matvec) */
+        if (n_tok >= GEMM_MIN_TOKENS && sdy_gemm_ok(&w->m, n_tok)) return sdy_gemm(&w->m, &a, c->gemm_ws, c->st);
     }
     return sdy_matvec(&w->m, &a, c->st);
 }

@@ -1,0 +1,363 @@
+// Quantized-weight GEMM for prefill (many tokens) on gfx950 MFMA, bit-exact with the reference's
+// integer-dot path (csrc/quant.c:191-235, csrc/quant.h:84-91; the reference's 4-token micro-kernels
+// csrc/quant_avx2.c:290-385 give the same bits as its one-token dots).
+//
+// Per 256-element super-block the reference computes an exact integer isum = sum_k (sc_g q_k) y_k
+// (and for Q4_K msum = sum_j m_j bsum_j), then combines acc + (yd*d*isum - yd*dmin*msum) in f32.
+// Here every wave dequantises its weight fragments in registers as f16 w' = sc * q (Q4_K) or
+// sc * (q - 32) (Q6_K) — exact small integers — and multiplies them with the Q8_K activations as
+// f16 (exact int8 values) on v_mfma_f32_32x32x16_f16, accumulating one super-block at a time in
+// f32. The products are exact and every partial sum stays below 2^24 when
+// 127 * sum_k |w'_k| < 2^24 for each row and super-block (checked when the matrix is uploaded;
+// matrices that fail it take the matvec path), so the accumulator holds isum exactly. The Q4_K
+// min term is one more MFMA of the mins against the 16-element bsums. The f32 combine then follows
+// the reference's expression and super-block order, so each output has the reference's bits.
+//
+// Tiling: a wave owns 32 rows x 32*NT tokens (NT MFMA tiles sharing its dequantised weight
+// fragments); a workgroup is 4 waves on 4 consecutive row tiles, so they read the same activation
+// fragments (L1 hits). The activations are expanded once per call to f16 (k_gemm_prep).
+#include "sdy_device.h"
+#include "sdy_internal.h"
+#include "sdy_quant_dev.h"
+#include "sdy_shim.h"
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+struct GemmArgs {
+    const uint8_t *p[5];  // weight planes (quant_kernels.hip layout)
+    int n_in, T, nb;      // elements, 64-element units and super-blocks per row
+    long row0, n_rows;    // rows row0 .. row0 + n_rows of the planes
+    int n_tok;
+    const _Float16 *y16;  // [n_tok][n_in] activations (the Q8_K int8 values)
+    const float *yd;      // [n_tok][nb] Q8_K scales
+    const _Float16 *bs16; // [n_tok][nb][16] Q8_K bsums
+    float *out;
+    long out_stride;
+    const float *bias, *resid;
+    int swiglu;
+};
+
+SDY_DEV u32x2 ld8(const uint8_t *p) { return *reinterpret_cast<const u32x2 *>(p); }
+
+// f16 pairs (1024 + b0, 1024 + b1) from byte lanes 0,1 (sel lo) or 2,3 (hi) of v: the magic
+// exponent 0x64 put above each byte by v_perm_b32.
+SDY_DEV uint32_t magic_lo(uint32_t v) { return __builtin_amdgcn_perm(0x64646464u, v, 0x05010400u); }
+SDY_DEV uint32_t magic_hi(uint32_t v) { return __builtin_amdgcn_perm(0x64646464u, v, 0x05030402u); }
+
+SDY_DEV half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
+SDY_DEV uint32_t as_u(half2v v) { return __builtin_bit_cast(uint32_t, v); }
+
+// 8 small unsigned integers (one per byte of n.x, n.y) times sc as f16: ((1024 + q) - 1024) * sc,
+// every step exact (q <= 63, |q * sc| <= 2048).
+SDY_DEV half8 frag_scaled(u32x2 n, half2v off, half2v sc2) {
+    half8 r;
+    const uint32_t w[4] = {magic_lo(n.x), magic_hi(n.x), magic_lo(n.y), magic_hi(n.y)};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const half2v t = (as_h2(w[i]) + off) * sc2;
+        r[2 * i] = t[0];
+        r[2 * i + 1] = t[1];
+    }
+    return r;
+}
+
+template <int WT>
+SDY_DEV void load_unit(const GemmArgs &g, long row, int u, int h, u32x2 (&q)[3]) {
+    const size_t ou = ((size_t)row * g.T + u) * 16 + 8 * h;
+    if constexpr (WT == SDY_Q4_K) {
+        q[0] = ld8(g.p[0] + ou);  // QA
+        q[1] = ld8(g.p[1] + ou);  // QB
+    } else {
+        q[0] = ld8(g.p[0] + ou);  // N0
+        q[1] = ld8(g.p[1] + ou);  // N1
+        q[2] = ld8(g.p[2] + ou);  // HB
+    }
+}
+
+template <int WT, int NT>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, lr = lane & 31;
+    const long rt = (long)blockIdx.x * 128 + 32 * wave;  // first row of the wave's tile
+    if (rt >= g.n_rows) return;
+    const int t0 = blockIdx.y * 32 * NT;
+    const long ra = g.row0 + (rt + lr < g.n_rows ? rt + lr : g.n_rows - 1);  // this lane's A row
+    int tb[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int t = t0 + 32 * nt + lr;
+        tb[nt] = t < g.n_tok ? t : g.n_tok - 1;
+    }
+    float acc[NT][16];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[nt][r] = 0.0f;
+    const half2v off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const half2v off6 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+
+    for (int sb = 0; sb < g.nb; sb++) {
+        // scales of this lane's A row
+        int sc[16];
+        int mn[8];
+        if constexpr (WT == SDY_Q4_K) {
+            const u32x4 hd = *reinterpret_cast<const u32x4 *>(g.p[2] + ((size_t)ra * g.nb + sb) * 16);
+            const uint32_t A = hd.y, B = hd.z, C = hd.w;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                sc[j] = (A >> (8 * j)) & 63;
+                mn[j] = (B >> (8 * j)) & 63;
+                sc[j + 4] = ((C >> (8 * j)) & 15) | (((A >> (8 * j + 6)) & 3) << 4);
+                mn[j + 4] = ((C >> (8 * j + 4)) & 15) | (((B >> (8 * j + 6)) & 3) << 4);
+            }
+        } else {
+            const u32x4 s4 = *reinterpret_cast<const u32x4 *>(g.p[3] + ((size_t)ra * g.nb + sb) * 16);
+#pragma unroll
+            for (int j = 0; j < 16; j++) sc[j] = (int)(int8_t)((s4[j >> 2] >> (8 * (j & 3))) & 255u);
+        }
+        float16v isum[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) isum[nt] = float16v{};
+#pragma unroll
+        for (int un = 0; un < 4; un++) {
+            u32x2 q[3];
+            load_unit<WT>(g, ra, 4 * sb + un, h, q);
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                half8 a;
+                if constexpr (WT == SDY_Q4_K) {
+                    // s: 0 QA low, 1 QB low (sub-block 2un), 2 QA high, 3 QB high (sub-block 2un + 1)
+                    const u32x2 src = (s & 1) ? q[1] : q[0];
+                    const u32x2 nib = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
+                    const _Float16 f = (_Float16)(float)sc[2 * un + (s >> 1)];
+                    a = frag_scaled(nib, off, half2v{f, f});
+                } else {
+                    // s: 0 N0 low, 1 N1 low, 2 N0 high, 3 N1 high; high bits from HB >> 2s; group 4un + s
+                    const u32x2 src = (s & 1) ? q[1] : q[0];
+                    const u32x2 lo = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
+                    const u32x2 hi = ((q[2] >> (unsigned)(2 * s)) & 0x03030303u) << 4u;
+                    const _Float16 f = (_Float16)(float)sc[4 * un + s];
+                    a = frag_scaled(lo | hi, off6, half2v{f, f});
+                }
+                const int k = sb * 256 + 64 * un + 16 * s + 8 * h;
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    const half8 b = *reinterpret_cast<const half8 *>(g.y16 + (size_t)tb[nt] * g.n_in + k);
+                    isum[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, isum[nt], 0, 0, 0);
+                }
+            }
+        }
+        float16v msum[NT];
+        if constexpr (WT == SDY_Q4_K) {
+            half8 a2;
+#pragma unroll
+            for (int e = 0; e < 8; e++) a2[e] = (_Float16)(float)mn[4 * h + (e >> 1)];
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const half8 b2 = *reinterpret_cast<const half8 *>(g.bs16 + ((size_t)tb[nt] * g.nb + sb) * 16 + 8 * h);
+                msum[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b2, float16v{}, 0, 0, 0);
+            }
+        }
+        // combine in the reference's order: acc + (yd*d*isum - yd*dmin*msum)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const long ri = rt + 8 * (r >> 2) + 4 * h + (r & 3);
+            const long row = g.row0 + (ri < g.n_rows ? ri : g.n_rows - 1);
+            float d, dmin = 0.0f;
+            if constexpr (WT == SDY_Q4_K) {
+                const uint32_t dd = *reinterpret_cast<const uint32_t *>(g.p[2] + ((size_t)row * g.nb + sb) * 16);
+                d = sdy_h2f((uint16_t)(dd & 0xFFFFu));
+                dmin = sdy_h2f((uint16_t)(dd >> 16));
+            } else {
+                d = sdy_h2f(*reinterpret_cast<const uint16_t *>(g.p[4] + ((size_t)row * g.nb + sb) * 2));
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const float ydv = g.yd[(size_t)tb[nt] * g.nb + sb];
+                if constexpr (WT == SDY_Q4_K) {
+                    const float dall = ydv * d, dmn = ydv * dmin;
+                    const float t1 = dall * isum[nt][r], t2 = dmn * msum[nt][r];
+                    acc[nt][r] = acc[nt][r] + (t1 - t2);
+                } else {
+                    const float ydd = ydv * d;
+                    acc[nt][r] = acc[nt][r] + ydd * isum[nt][r];
+                }
+            }
+        }
+    }
+    // store (bias, residual, or the SwiGLU pair of rows 2i, 2i+1 held by this lane)
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int tok = t0 + 32 * nt + lr;
+        if (tok >= g.n_tok) continue;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const long ri = rt + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (ri >= g.n_rows) continue;
+            const long row = g.row0 + ri;
+            if (g.swiglu) {
+                if ((r & 1) == 0) g.out[(size_t)tok * g.out_stride + (ri >> 1)] = sdy_silu_mul1(acc[nt][r], acc[nt][r + 1]);
+            } else {
+                float v = acc[nt][r];
+                if (g.bias) v = v + g.bias[row];
+                if (g.resid) v = g.resid[(size_t)tok * g.out_stride + row] + v;
+                g.out[(size_t)tok * g.out_stride + row] = v;
+            }
+        }
+    }
+}
+
+// Q8_K rows -> f16 values, f32 scales and f16 bsums for the GEMM. Grid (nb, n_tok), 64 threads.
+__global__ __launch_bounds__(64) void k_gemm_prep(const uint8_t *__restrict__ xq, int nb, _Float16 *__restrict__ y16,
+                                                  float *__restrict__ yd, _Float16 *__restrict__ bs16) {
+    const int sb = blockIdx.x, t = blockIdx.y, l = threadIdx.x;
+    const uint8_t *blk = xq + ((size_t)t * nb + sb) * 292;
+    const uint32_t v = *reinterpret_cast<const uint32_t *>(blk + 4 + 4 * l);
+    _Float16 *o = y16 + (size_t)t * nb * 256 + 256 * sb + 4 * l;
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[e] = (_Float16)(float)(int8_t)((v >> (8 * e)) & 255u);
+    if (l < 16) bs16[((size_t)t * nb + sb) * 16 + l] = (_Float16)(float)reinterpret_cast<const int16_t *>(blk + 260)[l];
+    if (l == 0) yd[(size_t)t * nb + sb] = *reinterpret_cast<const float *>(blk);
+}
+
+// Exactness check of a K-quant matrix for the GEMM: flags a row super-block whose
+// 127 * sum |w'| reaches 2^24 or (Q6_K) whose |sc * (q - 32)| exceeds 2048. One thread per
+// (row, super-block) of rows [0, n_rows) of the planes.
+template <int WT>
+__global__ void k_gemm_check(GemmArgs g, int *bad) {
+    const long gid = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    const long row = gid / g.nb;
+    const int sb = (int)(gid - row * g.nb);
+    if (row >= g.n_rows) return;
+    long sum = 0;
+    int over = 0;
+    if constexpr (WT == SDY_Q4_K) {
+        const uint8_t *hd = g.p[2] + ((size_t)row * g.nb + sb) * 16 + 4;
+        for (int u = 0; u < 4; u++)
+            for (int half = 0; half < 2; half++) {
+                const uint8_t *qp = g.p[half] + ((size_t)row * g.T + 4 * sb + u) * 16;
+                const int j0 = 2 * u, j1 = 2 * u + 1;
+                const int s0 = j0 < 4 ? hd[j0] & 63 : (hd[j0 + 4] & 15) | ((hd[j0 - 4] >> 6) << 4);
+                const int s1 = j1 < 4 ? hd[j1] & 63 : (hd[j1 + 4] & 15) | ((hd[j1 - 4] >> 6) << 4);
+                for (int i = 0; i < 16; i++) sum += (long)s0 * (qp[i] & 15) + (long)s1 * (qp[i] >> 4);
+            }
+    } else {
+        const int8_t *scs = reinterpret_cast<const int8_t *>(g.p[3] + ((size_t)row * g.nb + sb) * 16);
+        for (int u = 0; u < 4; u++) {
+            const size_t ou = ((size_t)row * g.T + 4 * sb + u) * 16;
+            for (int e = 0; e < 64; e++) {
+                const int lo = e < 32 ? (g.p[e < 16 ? 0 : 1][ou + (e & 15)] & 15) : (g.p[e < 48 ? 0 : 1][ou + (e & 15)] >> 4);
+                const int hi = (g.p[2][ou + (e & 15)] >> (2 * (e >> 4))) & 3;
+                const int w = scs[4 * u + (e >> 4)] * ((lo | (hi << 4)) - 32);
+                const int aw = w < 0 ? -w : w;
+                if (aw > 2048) over = 1;
+                sum += aw;
+            }
+        }
+    }
+    if (over || 127 * sum >= (1L << 24)) atomicOr(bad, 1);
+}
+
+}  // namespace
+
+// =============================================================================== host
+
+static GemmArgs gemm_args(const sdy_mat *m) {
+    GemmArgs g;
+    memset(&g, 0, sizeof(g));
+    for (int i = 0; i < 5; i++) g.p[i] = (const uint8_t *)m->base + m->plane_off[i];
+    g.n_in = m->n_in;
+    g.T = m->n_units;
+    g.nb = m->n_in / 256;
+    g.n_rows = m->n_rows;
+    return g;
+}
+
+// Flags (bad = 1) rows [r0, r0 + n) of m that the GEMM cannot multiply exactly. Synchronous.
+extern "C" int sdy_gemm_check_rows(const sdy_mat *m, long r0, long n, int *bad_host, sdy_stream s) {
+    *bad_host = 1;
+    if (m->type != SDY_Q4_K && m->type != SDY_Q6_K) return 0;
+    sdy_mat v = sdy_mat_rows(m, r0, n);
+    GemmArgs g = gemm_args(&v);
+    int *bad = nullptr, rc;
+    if ((rc = sdy_malloc((void **)&bad, sizeof(int)))) return rc;
+    if ((rc = sdy_memset(bad, 0, sizeof(int), s))) {
+        sdy_free(bad);
+        return rc;
+    }
+    const long total = n * (long)g.nb;
+    dim3 grid((unsigned)((total + 255) / 256));
+    if (m->type == SDY_Q4_K) hipLaunchKernelGGL(k_gemm_check<SDY_Q4_K>, grid, dim3(256), 0, (hipStream_t)s, g, bad);
+    else hipLaunchKernelGGL(k_gemm_check<SDY_Q6_K>, grid, dim3(256), 0, (hipStream_t)s, g, bad);
+    if (!(rc = sdy_check_launch("gemm_check")) && !(rc = sdy_d2h(bad_host, bad, sizeof(int), s))) rc = sdy_sync(s);
+    sdy_free(bad);
+    return rc;
+}
+
+extern "C" size_t sdy_gemm_ws_bytes(int n_tok, int n_in) {
+    const size_t nb = (size_t)n_in / 256;
+    return (size_t)n_tok * n_in * 2 + (size_t)n_tok * nb * 4 + (size_t)n_tok * nb * 32 + 3 * 256;
+}
+
+extern "C" int sdy_gemm_ok(const sdy_mat *m, int n_tok) {
+    return (m->type == SDY_Q4_K || m->type == SDY_Q6_K) && m->gemm_ok && n_tok >= 2;
+}
+
+template <int WT, int NT>
+static int launch_gemm(GemmArgs &g, hipStream_t st) {
+    const long row_tiles = (g.n_rows + 127) / 128;
+    const int tok_groups = (g.n_tok + 32 * NT - 1) / (32 * NT);
+    hipLaunchKernelGGL((k_gemm<WT, NT>), dim3((unsigned)row_tiles, (unsigned)tok_groups), dim3(256), 0, st, g);
+    return sdy_check_launch("gemm");
+}
+
+template <int WT>
+static int gemm_type(GemmArgs &g, hipStream_t st) {
+    // token tiles per wave: the largest of 4, 2, 1 that still gives a few waves per SIMD
+    const long waves_at = [&](int nt) { return (g.n_rows + 31) / 32 * ((g.n_tok + 32 * nt - 1) / (32 * nt)); }(4);
+    int n_cu = 256;
+    size_t mem = 0;
+    sdy_device_info(&n_cu, &mem);
+    if (waves_at >= 4L * n_cu && g.n_tok > 64) return launch_gemm<WT, 4>(g, st);
+    if (g.n_tok > 32) return launch_gemm<WT, 2>(g, st);
+    return launch_gemm<WT, 1>(g, st);
+}
+
+// out[t][row] for rows [a->row0, a->row1) and a->n_tok tokens of Q8_K activations a->xq, through
+// the MFMA GEMM; ws: sdy_gemm_ws_bytes(n_tok, n_in) bytes of device scratch.
+extern "C" int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_stream s) {
+    hipStream_t st = (hipStream_t)s;
+    if (!sdy_gemm_ok(m, a->n_tok)) return sdy_fail(-1, "gemm: matrix not eligible (type %d)", m->type);
+    if (a->row0 < 0 || a->row1 > m->n_rows || a->row0 > a->row1)
+        return sdy_fail(-1, "gemm rows [%ld, %ld) outside %ld", a->row0, a->row1, m->n_rows);
+    if (a->row0 == a->row1) return 0;
+    if (a->epilogue == SDY_EPI_SWIGLU && (((a->row1 - a->row0) | a->row0) & 1 || a->bias || a->resid))
+        return sdy_fail(-1, "gemm: the SwiGLU epilogue needs an even row range from an even row, no bias, no residual");
+    GemmArgs g = gemm_args(m);
+    const int nb = g.nb, n_tok = a->n_tok;
+    uint8_t *w = (uint8_t *)ws;
+    g.y16 = (const _Float16 *)w;
+    w += ((size_t)n_tok * g.n_in * 2 + 255) & ~(size_t)255;
+    g.yd = (const float *)w;
+    w += ((size_t)n_tok * nb * 4 + 255) & ~(size_t)255;
+    g.bs16 = (const _Float16 *)w;
+    hipLaunchKernelGGL(k_gemm_prep, dim3(nb, n_tok), dim3(64), 0, st, (const uint8_t *)a->xq, nb, (_Float16 *)g.y16,
+                       (float *)g.yd, (_Float16 *)g.bs16);
+    int rc = sdy_check_launch("gemm_prep");
+    if (rc) return rc;
+    g.row0 = a->row0;
+    g.n_rows = a->row1 - a->row0;
+    g.n_tok = n_tok;
+    g.out = a->out;
+    g.out_stride = a->out_stride;
+    g.bias = a->bias;
+    g.resid = a->resid;
+    g.swiglu = a->epilogue == SDY_EPI_SWIGLU;
+    // with a row range the outputs are indexed by row - row0 only for SwiGLU (as in the matvec)
+    return m->type == SDY_Q4_K ? gemm_type<SDY_Q4_K>(g, st) : gemm_type<SDY_Q6_K>(g, st);
+}

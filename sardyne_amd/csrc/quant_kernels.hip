@@ -996,6 +996,10 @@ extern "C" int sdy_mat_alloc(sdy_mat *m, int type, int n_in, long n_rows) {
         m->plane_off[i] = off;
         if (pb[i]) off += align256(pb[i] * (size_t)n_rows);
     }
+    // zero rows pass the GEMM check, so a matrix filled in several uploads is checked piecewise
+    m->gemm_ok = type == SDY_Q4_K || type == SDY_Q6_K;
+    // (completed before returning: the uploads run on other, non-blocking streams)
+    if (m->gemm_ok && ((rc = sdy_memset(m->base, 0, m->bytes, nullptr)) || (rc = sdy_sync(nullptr)))) return rc;
     return 0;
 }
 
@@ -1041,8 +1045,16 @@ static int repack_rows(sdy_mat *m, long r0, RowMap map, long n, const void *dev_
 extern "C" int sdy_mat_from_device(sdy_mat *m, int type, int n_in, long n_rows, const void *dev_raw, sdy_stream s) {
     int rc = sdy_mat_alloc(m, type, n_in, n_rows);
     if (rc) return rc;
-    if ((rc = repack_rows(m, 0, RowMap{1, n_rows, 0}, n_rows, dev_raw, s))) sdy_mat_free(m);
-    return rc;
+    if ((rc = repack_rows(m, 0, RowMap{1, n_rows, 0}, n_rows, dev_raw, s))) {
+        sdy_mat_free(m);
+        return rc;
+    }
+    if (m->gemm_ok) {
+        int bad = 1;
+        if ((rc = sdy_gemm_check_rows(m, 0, n_rows, &bad, s))) return rc;
+        if (bad) m->gemm_ok = 0;
+    }
+    return 0;
 }
 
 extern "C" int sdy_mat_upload_map(sdy_mat *m, long r0, long n, long step, long grp, long gstride,
@@ -1060,6 +1072,11 @@ extern "C" int sdy_mat_upload_map(sdy_mat *m, long r0, long n, long step, long g
     if (!(rc = sdy_h2d(tmp, host_raw, raw, s))) rc = repack_rows(m, r0, RowMap{step, grp, gstride}, n, tmp, s);
     if (!rc) rc = sdy_sync(s);
     sdy_free(tmp);
+    if (!rc && m->gemm_ok) {
+        int bad = 1;
+        rc = sdy_gemm_check_rows(m, r0, span - r0 + 1, &bad, s);
+        if (!rc && bad) m->gemm_ok = 0;
+    }
     return rc;
 }
 

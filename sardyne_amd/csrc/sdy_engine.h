@@ -50,13 +50,13 @@ struct engine_ctx {
     /* one-token decode: step_dev = {token, position} read by the kernels, so the recorded graph
        replays for every position */
     int32_t *step_dev, *step_host;
-    int32_t *att_counter;       /* arrival counter of the fused decode attention (kept at 0) */
     void *graph;                /* recorded one-token decode step (NULL until recorded) */
     int graph_ok;               /* 0: not tried, 1: recorded, -1: recording failed (run eagerly) */
     int n_decode;               /* one-token evals so far (the first runs eagerly) */
     int decode_fused;           /* one-token steps use the fused decode kernels */
     int use_graph;              /* one-token steps are recorded once and replayed */
     float *qkv;                 /* q | k | v of one token */
+    void *gemm_ws;              /* scratch of the prefill GEMM (f16 activations of n_batch rows) */
     /* MoE */
     float *moe_probs, *moe_w, *moe_x, *moe_y, *moe_sum, *moe_gw;
     int32_t *moe_top, *moe_gidx, *moe_top_host, *moe_gidx_host;

@@ -55,6 +55,7 @@ typedef struct {
     long n_rows;    /* rows (experts stacked: n_expert * n_out) */
     int n_units;    /* 64-element units per row (quantized types) */
     size_t plane_off[5];
+    int gemm_ok;    /* K-quant rows the MFMA GEMM multiplies exactly (every row passes its check) */
 } sdy_mat;
 
 /* Bytes of the device layout for a matrix. */
@@ -99,6 +100,15 @@ typedef struct {
 enum { SDY_EPI_NONE = 0, SDY_EPI_SWIGLU = 1 };
 /* out = W · x for rows [row0, row1) and n_tok tokens. */
 int sdy_matvec(const sdy_mat *m, const sdy_mv_args *a, sdy_stream s);
+
+/* The prefill GEMM (gemm_kernels.hip): the same outputs as sdy_matvec (bit for bit) for
+ * n_tok >= 2 tokens of Q8_K activations a->xq on Q4_K / Q6_K matrices with gemm_ok, through
+ * MFMA. ws: sdy_gemm_ws_bytes(n_tok, n_in) bytes of device scratch. */
+int sdy_gemm_ok(const sdy_mat *m, int n_tok);
+size_t sdy_gemm_ws_bytes(int n_tok, int n_in);
+int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_stream s);
+/* Exactness check of rows [r0, r0 + n) of m for the GEMM: *bad_host = 1 when some row fails. */
+int sdy_gemm_check_rows(const sdy_mat *m, long r0, long n, int *bad_host, sdy_stream s);
 
 /* raw float-weight matrices (F32/F16/BF16, GGUF row-major layout kept as is) */
 int sdy_matvec_float(int wtype, const void *w, int n_in, const sdy_mv_args *a, sdy_stream s);

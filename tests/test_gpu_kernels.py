@@ -345,3 +345,73 @@ def test_swiglu_epilogue(kind, n_in, ffn, n_tok):
     O.lib().orc_silu_mul(ptr(exp), ptr(eu), exp.size)
     np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * float(np.abs(exp).max()))
     L.sdy_mat_free(ctypes.byref(m))
+
+
+def _gemm_case(kind, n_in, n_out, n_tok, seed, gen="workload"):
+    t = TYPES[kind]
+    rng = np.random.default_rng(seed)
+    nb = n_out * n_in // O.QK[t]
+    w = (random_blocks(kind, nb, rng) if gen == "workload" else ref_blocks(kind, nb, seed)).reshape(n_out, -1)
+    x = np.random.default_rng(seed + 1).standard_normal((n_tok, n_in)).astype(np.float32)
+    return t, w, O.quantize(x, O.Q8_K)
+
+
+def _gemm_run(t, w, xq, n_in, n_out, n_tok, row0=0, row1=None, bias=None, resid=None, epilogue=0):
+    L = lib()
+    row1 = n_out if row1 is None else row1
+    m = capi.DeviceMatrix(t, n_in, n_out, w)
+    assert L.sdy_gemm_ok(ctypes.byref(m.m), n_tok), "matrix failed the GEMM exactness check"
+    out_cols = (row1 - row0) // 2 if epilogue else n_out
+    dq = capi.DeviceBuffer.from_array(xq)
+    dout = capi.DeviceBuffer.from_array(np.full((n_tok, out_cols), np.nan, np.float32))
+    ws = capi.DeviceBuffer(L.sdy_gemm_ws_bytes(n_tok, n_in))
+    db = capi.DeviceBuffer.from_array(bias) if bias is not None else None
+    dr = capi.DeviceBuffer.from_array(resid) if resid is not None else None
+    a = capi.SdyMvArgs(xq=dq.ptr, n_tok=n_tok, out=dout.ptr, out_stride=out_cols, row0=row0, row1=row1,
+                       bias=db.ptr if db else None, resid=dr.ptr if dr else None, epilogue=epilogue)
+    capi.check(L.sdy_gemm(ctypes.byref(m.m), ctypes.byref(a), ws.ptr, None))
+    return dout.to_array(np.float32, (n_tok, out_cols))
+
+
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("n_in,n_out,n_tok", [(256, 40, 16), (2048, 128, 33), (2048, 300, 64), (768, 96, 100),
+                                              (11008, 64, 20), (4096, 200, 200), (2048, 37, 129)])
+def test_gemm_bit_exact(kind, n_in, n_out, n_tok):
+    """The MFMA prefill GEMM gives the reference's bits (integer super-block dots, f32 combine in
+    super-block order) for every token and row, including partial row and token tiles."""
+    t, w, xq = _gemm_case(kind, n_in, n_out, n_tok, seed=n_in + n_out + n_tok)
+    got = _gemm_run(t, w, xq, n_in, n_out, n_tok)
+    exp = O.matmul_q(w, t, xq, n_in, simd=1)
+    assert np.array_equal(bits(got), bits(exp))
+
+
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
+def test_gemm_bias_resid_rows_swiglu(kind):
+    n_in, n_out, n_tok = 512, 96, 40
+    t, w, xq = _gemm_case(kind, n_in, n_out, n_tok, seed=7)
+    exp = O.matmul_q(w, t, xq, n_in, simd=1)
+    rng = np.random.default_rng(8)
+    bias = rng.standard_normal(n_out).astype(np.float32)
+    resid = rng.standard_normal((n_tok, n_out)).astype(np.float32)
+    got = _gemm_run(t, w, xq, n_in, n_out, n_tok, bias=bias, resid=resid)
+    assert np.array_equal(bits(got), bits(resid + (exp + bias)))
+    part = _gemm_run(t, w, xq, n_in, n_out, n_tok, row0=32, row1=70)
+    assert np.array_equal(bits(part[:, 32:70]), bits(exp[:, 32:70]))
+    # SwiGLU over rows (2i, 2i+1)
+    sw = _gemm_run(t, w, xq, n_in, n_out, n_tok, epilogue=capi.EPI_SWIGLU)
+    g, u = exp[:, 0::2].copy(), exp[:, 1::2].copy()
+    lib().op_silu_mul(ptr(g), ptr(u), g.size)
+    assert np.array_equal(bits(sw), bits(g))
+
+
+def test_gemm_exactness_check_rejects_overflowing_rows():
+    """Q6_K rows whose scaled values exceed what f16 holds exactly are flagged (they take the
+    matvec path); ordinary rows are accepted."""
+    L = lib()
+    w = random_blocks("Q6_K", 8 * 4, np.random.default_rng(3)).reshape(8, -1)
+    ok = capi.DeviceMatrix(O.Q6_K, 1024, 8, w)
+    assert L.sdy_gemm_ok(ctypes.byref(ok.m), 32)
+    w2 = w.copy().reshape(-1, 210)
+    w2[5, 192:208] = np.uint8(0x80)  # scales -128: |-128 * (q - 32)| reaches 4096
+    bad = capi.DeviceMatrix(O.Q6_K, 1024, 8, w2.reshape(8, -1))
+    assert not L.sdy_gemm_ok(ctypes.byref(bad.m), 32)
