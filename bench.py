@@ -7,7 +7,8 @@ step streams its weights from HBM. value = algorithmic bytes per step / step tim
 
 Other workloads (--workload): q8_0_head (the Q8_0 matvec of the same shape), q4k_matvec (2048 x
 2048 Q4_K, measured as one launch over 448 stacked copies), decode_3b (Qwen2.5-3B-shaped Q4_K_M
-decode tok/s after a 512-token context), decode_moe (Qwen3-30B-A3B-shaped decode).
+decode tok/s after a 512-token context), decode_moe (Qwen3-30B-A3B-shaped MoE decode after a
+1024-token context), prefill_3b (one 512-token prompt through the Qwen2.5-3B-shaped model).
 
 Every line carries:
   roofline      the dominant kernel's algorithmic bytes / its average duration (HIP events on the
@@ -299,18 +300,50 @@ def bench_matvec(args, wt, n_out, n_in, n_copies, stacked):
 
 # ---------------------------------------------------------------- decode workloads
 
-def bench_decode(args, spec, ctx_len, n_decode, label):
-    """Decode tok/s after a ctx_len-token context at batch 1 (the method of the reference's
-    bench/bench_decode.py:39-48: n_decode / wall time of the decode loop). Token ids are uniform
-    over the vocabulary (seeded) and fed teacher-forced, so the GPU and the CPU reference see the
-    same sequence and their logits are compared step by step."""
+def decode_weight_bytes(spec):
+    """Weight bytes one decode token reads: per layer the attention matrices, norms and biases, the
+    dense FFN or the router plus the k chosen experts' gate/up/down; then the final norm, the output
+    head (the tied embedding when there is none) and one embedding row."""
+    from sardyne_amd.gguf_synth import row_bytes
+    dim, hd = spec.dim, spec.head_dim
+    q_dim, kv_dim = spec.n_head * hd, spec.n_kv_head * hd
+    td = spec.t_default
+    layer = (q_dim * row_bytes(td, dim) + kv_dim * row_bytes(td, dim) + kv_dim * row_bytes(spec.t_attn_v, dim)
+             + dim * row_bytes(td, q_dim) + 2 * dim * 4)
+    if spec.qkv_bias:
+        layer += (q_dim + 2 * kv_dim) * 4
+    if spec.qk_norm:
+        layer += 2 * hd * 4
+    if spec.n_expert:
+        fe = spec.ffn_exp_dim
+        layer += spec.n_expert * dim * 4 + spec.n_expert_used * (
+            2 * fe * row_bytes(td, dim) + dim * row_bytes(spec.t_ffn_down, fe))
+    else:
+        layer += 2 * spec.ffn_dim * row_bytes(td, dim) + dim * row_bytes(spec.t_ffn_down, spec.ffn_dim)
+    head = spec.n_vocab * row_bytes(spec.t_embd if spec.tied else spec.t_output, dim)
+    return spec.n_layer * layer + head + dim * 4 + row_bytes(spec.t_embd, dim)
+
+
+def kv_bytes_per_position(spec):
+    return 2 * spec.n_layer * spec.n_kv_head * spec.head_dim * 4
+
+
+def write_bench_model(spec, label):
     from sardyne_amd.gguf_synth import write_model
-    from sardyne_amd.runtime import Context, Model
     tmpdir = Path(os.environ.get("SARDYNE_BENCH_DIR", "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()))
     path = tmpdir / f"sardyne_bench_{label}.gguf"
     t0 = time.perf_counter()
     write_model(path, spec, seed=0)
     log(f"[bench] wrote {path} ({path.stat().st_size / 1e9:.2f} GB) in {time.perf_counter() - t0:.1f}s")
+    return path
+
+def bench_decode(args, spec, ctx_len, n_decode, label):
+    """Decode tok/s after a ctx_len-token context at batch 1 (the method of the reference's
+    bench/bench_decode.py:39-48: n_decode / wall time of the decode loop). Token ids are uniform
+    over the vocabulary (seeded) and fed teacher-forced, so the GPU and the CPU reference see the
+    same sequence and their logits are compared step by step."""
+    from sardyne_amd.runtime import Context, Model
+    path = write_bench_model(spec, label)
     rng = np.random.default_rng(0)
     toks = rng.integers(0, spec.n_vocab, ctx_len + n_decode).astype(np.int32)
     try:
@@ -367,13 +400,145 @@ def bench_decode(args, spec, ctx_len, n_decode, label):
     return gpu_tok_s, t_prefill, cpu, parity
 
 
+def decode_line(args, spec, label, ctx_len, desc):
+    n_dec = max(args.steps, 8)
+    tok_s, t_pre, cpu, parity = bench_decode(args, spec, ctx_len, n_dec, label)
+    w_bytes = decode_weight_bytes(spec)
+    kv_mean = kv_bytes_per_position(spec) * (ctx_len + n_dec / 2)
+    gbps = (w_bytes + kv_mean) * tok_s / 1e9
+    cfg = {"workload": f"{desc} decode, batch 1, {n_dec} tokens after a {ctx_len}-token context",
+           "n_layer": spec.n_layer, "dim": spec.dim, "heads": f"{spec.n_head}/{spec.n_kv_head}",
+           "vocab": spec.n_vocab, "weight_bytes_per_token": w_bytes, "mean_kv_bytes_per_token": int(kv_mean)}
+    if spec.n_expert:
+        cfg.update({"experts": f"{spec.n_expert} (top-{spec.n_expert_used})", "expert_ffn": spec.ffn_exp_dim})
+    else:
+        cfg["ffn"] = spec.ffn_dim
+    line = {"metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": n_dec,
+            "warmup": 0, "ms_per_step": round(1e3 / tok_s, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "int8 activations x Q4_K/Q6_K weights, f32 elsewhere",
+            "data": "synthetic (random-init Q4_K_M weights, uniform token ids)", "config": cfg,
+            f"prefill_{ctx_len}_s": round(t_pre, 4),
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "kernel": "whole decode step (weights + mean KV bytes per token)"},
+            "cpu_baseline": cpu, "parity": parity}
+    if cpu and "value" in cpu:
+        line["gpu_over_cpu"] = round(tok_s / cpu["value"], 1)
+    return line
+
+
+def prefill_flops(spec, n):
+    """GEMM flops of an n-token prefill (2 n x matrix parameters, head for the last token only)
+    plus the causal attention's QK and PV flops."""
+    dim, hd = spec.dim, spec.head_dim
+    q_dim, kv_dim = spec.n_head * hd, spec.n_kv_head * hd
+    params = dim * q_dim * 2 + dim * kv_dim * 2 + 3 * dim * spec.ffn_dim
+    attn = spec.n_layer * spec.n_head * 2 * 2 * hd * (n * (n + 1) // 2)
+    return 2 * n * params * spec.n_layer + 2 * spec.n_vocab * dim + attn
+
+
+def gemm_gate_up_ms(spec, n_tok, reps):
+    """The prefill's dominant kernel at its real shape: the interleaved gate|up Q4_K matrix
+    (2 ffn x dim) times n_tok Q8_K rows with the SwiGLU epilogue, each launch timed by its own
+    HIP event pair on the stream it runs on."""
+    L = capi.lib()
+    stream = ctypes.c_void_p()
+    capi.check(L.sdy_stream_new(ctypes.byref(stream)))
+    st = stream.value
+    rows, n_in = 2 * spec.ffn_dim, spec.dim
+    w = random_blocks("Q4_K", rows * n_in // 256, np.random.default_rng(3)).reshape(rows, -1)
+    m = capi.DeviceMatrix(Q4_K, n_in, rows, w, st)
+    if not L.sdy_gemm_ok(ctypes.byref(m.m), n_tok):
+        return None
+    x = np.random.default_rng(4).standard_normal((n_tok, n_in)).astype(np.float32)
+    dx = capi.DeviceBuffer.from_array(x, st)
+    dq = capi.DeviceBuffer(n_tok * row_size(Q8_K, n_in))
+    capi.check(L.sdy_quantize(Q8_K, dx.ptr, dq.ptr, n_in, n_tok, st))
+    ws = capi.DeviceBuffer(L.sdy_gemm_ws_bytes(n_tok, n_in))
+    dout = capi.DeviceBuffer(n_tok * spec.ffn_dim * 4)
+    a = capi.SdyMvArgs(xq=dq.ptr, n_tok=n_tok, out=dout.ptr, out_stride=spec.ffn_dim, row0=0, row1=rows,
+                       epilogue=capi.EPI_SWIGLU)
+
+    def launch(_):
+        capi.check(L.sdy_gemm(ctypes.byref(m.m), ctypes.byref(a), ws.ptr, st))
+
+    for i in range(3):
+        launch(i)
+    return per_launch_ms(st, launch, reps), 2.0 * rows * n_in * n_tok
+
+
+def prefill_line(args, spec, label, n_prompt, desc):
+    """Prefill tok/s of one n_prompt-token eval (n_batch = n_prompt), the median over --steps
+    fresh evals, with the whole prefill's MFMA utilisation and the dominant GEMM's roofline."""
+    from sardyne_amd.runtime import Context, Model
+    MFMA_PEAK = 2500.0  # TFLOP/s, dense f16/bf16
+    path = write_bench_model(spec, label)
+    toks = np.random.default_rng(0).integers(0, spec.n_vocab, n_prompt).astype(np.int32)
+    model = Model(path)
+    ctx = Context(model, max_seq=n_prompt + 1, n_batch=n_prompt)
+    for _ in range(max(1, args.warmup)):
+        ctx.reset()
+        gpu_logits = ctx.eval(toks)
+    times = []
+    for _ in range(args.steps):
+        ctx.reset()
+        t0 = time.perf_counter()
+        ctx.eval(toks)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    tok_s = n_prompt / t
+    log(f"[bench] GPU prefill {n_prompt} tok: {t * 1e3:.2f} ms median of {len(times)} ({tok_s:.0f} tok/s)")
+    del ctx, model
+    flops = prefill_flops(spec, n_prompt)
+    k = gemm_gate_up_ms(spec, n_prompt, args.steps)
+    roof = None
+    if k:
+        ms_k, fl = k
+        ach = fl / (ms_k * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": MFMA_PEAK, "unit": "TFLOP/s",
+                "frac": round(ach / MFMA_PEAK, 4), "traffic": None, "kernel": "k_gemm<Q4_K> (gate|up, SwiGLU)",
+                "kernel_avg_us": round(ms_k * 1e3, 2), "algorithmic_flops_per_launch": fl}
+    cpu, parity = None, {}
+    if args.cpu_seconds > 0:
+        try:
+            import oracle as O
+            if O.ref_available():
+                eng = O.RefEngine(path, n_prompt + 1, n_batch=n_prompt, n_threads=0)
+                t0 = time.perf_counter()
+                c = eng.eval(toks)
+                t_cpu = time.perf_counter() - t0
+                cpu = {"value": round(n_prompt / t_cpu, 3), "unit": "tok/s", "cores": eng.n_threads,
+                       "kind": "reference", "sample": f"reference engine, one {n_prompt}-token prefill "
+                                                      f"(n_batch {n_prompt}), {host_cpu_model()}"}
+                maxabs = float(np.abs(gpu_logits - c).max())
+                parity = {"logits_max_abs": maxabs, "logits_max_abs_over_max_ref": maxabs / float(np.abs(c).max()),
+                          "greedy_argmax_agreement": float(gpu_logits.argmax() == c.argmax())}
+        except Exception as ex:
+            cpu = {"error": str(ex)}
+    try:
+        path.unlink()
+    except OSError:
+        pass
+    line = {"metric": METRIC, "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(t * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "int8 activations x Q4_K/Q6_K weights on f16 MFMA (exact integer sums)",
+            "data": "synthetic (random-init Q4_K_M weights, uniform token ids)",
+            "config": {"workload": f"{desc} prefill, one {n_prompt}-token prompt", "n_layer": spec.n_layer,
+                       "dim": spec.dim, "ffn": spec.ffn_dim, "vocab": spec.n_vocab, "flops": flops},
+            "mfma_utilisation": round(flops / t / 1e12 / MFMA_PEAK, 4),
+            "roofline": roof, "cpu_baseline": cpu, "parity": parity}
+    if cpu and "value" in cpu:
+        line["gpu_over_cpu"] = round(tok_s / cpu["value"], 1)
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="q6k_head",
-                    choices=["q6k_head", "q8_0_head", "q4k_matvec", "decode_3b"])
+                    choices=["q6k_head", "q8_0_head", "q4k_matvec", "decode_3b", "decode_moe", "prefill_3b"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--n-batch", type=int, default=512, help="GPU prefill chunk (decode workloads)")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (smoke runs only)")
@@ -389,28 +554,16 @@ def main():
         line = bench_matvec(args, Q8_0, 151936, 2048, 8, stacked=False)
     elif args.workload == "q4k_matvec":
         line = bench_matvec(args, Q4_K, 2048, 2048, 448, stacked=True)
+    elif args.workload == "decode_3b":
+        from sardyne_amd.gguf_synth import qwen25_3b
+        line = decode_line(args, qwen25_3b(args.layers or 36), "qwen25_3b", 512, "Qwen2.5-3B-shaped Q4_K_M")
+    elif args.workload == "decode_moe":
+        from sardyne_amd.gguf_synth import qwen3_30b_a3b
+        line = decode_line(args, qwen3_30b_a3b(args.layers or 48), "qwen3_30b_a3b", 1024,
+                           "Qwen3-30B-A3B-shaped qwen3moe Q4_K_M (128 experts resident, top-8)")
     else:
         from sardyne_amd.gguf_synth import qwen25_3b
-        spec = qwen25_3b(args.layers or 36)
-        n_dec = max(args.steps, 8)
-        tok_s, t_pre, cpu, parity = bench_decode(args, spec, 512, n_dec, "qwen25_3b")
-        w_bytes = 2031000704  # weights read per token (see the roofline note in the design)
-        kv_mean = 73728 * (512 + n_dec / 2)
-        line = {"metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": n_dec,
-                "warmup": 0, "ms_per_step": round(1e3 / tok_s, 4), "higher_is_better": True, "scaling": "weak",
-                "vs_baseline": None, "dtype": "int8 activations x Q4_K/Q6_K weights, f32 elsewhere",
-                "data": "synthetic (random-init Q4_K_M weights, uniform token ids)",
-                "config": {"workload": f"Qwen2.5-3B-shaped Q4_K_M decode, batch 1, {n_dec} tokens after a "
-                                       f"512-token context", "n_layer": spec.n_layer, "dim": spec.dim,
-                           "heads": f"{spec.n_head}/{spec.n_kv_head}", "ffn": spec.ffn_dim, "vocab": spec.n_vocab},
-                "prefill_512_s": round(t_pre, 4),
-                "roofline": {"bound": "hbm", "achieved": round((w_bytes + kv_mean) * tok_s / 1e9, 1),
-                             "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                             "frac": round((w_bytes + kv_mean) * tok_s / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
-                             "kernel": "whole decode step (weights + mean KV bytes per token)"},
-                "cpu_baseline": cpu, "parity": parity}
-        if cpu and "value" in cpu:
-            line["gpu_over_cpu"] = round(tok_s / cpu["value"], 1)
+        line = prefill_line(args, qwen25_3b(args.layers or 36), "qwen25_3b", 512, "Qwen2.5-3B-shaped Q4_K_M")
     print(json.dumps(line), flush=True)
 
 

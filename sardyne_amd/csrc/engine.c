@@ -502,7 +502,9 @@ engine_ctx *engine_ctx_new(const engine_model *m, int32_t max_seq, int32_t n_bat
     /* SARDYNE_NO_FUSED_DECODE / SARDYNE_NO_GRAPH: run one-token steps with the unfused kernels, or
        without recording them (the results are the same; used to compare the paths) */
     c->decode_fused = !getenv("SARDYNE_NO_FUSED_DECODE") && sdy_engine_decode_fused_ok(c);
-    c->use_graph = c->decode_fused && !getenv("SARDYNE_NO_GRAPH");
+    /* SARDYNE_NO_DEVICE_MOE: one-token MoE blocks group their experts on the host, as prefill does */
+    c->moe_device = c->decode_fused && !getenv("SARDYNE_NO_DEVICE_MOE") && sdy_engine_moe_device_ok(c);
+    c->use_graph = c->decode_fused && (!m->info.n_expert || c->moe_device) && !getenv("SARDYNE_NO_GRAPH");
     return c;
 }
 

@@ -43,6 +43,8 @@ int sdy_engine_alloc(engine_ctx *c) {
     size_t max_in = (size_t)in->dim > q_dim ? (size_t)in->dim : q_dim;
     if (ffn > max_in) max_in = ffn;
     size_t logit_rows = c->logits_all ? B : 1;
+    /* rows of the FFN activations: n_batch tokens, or the k routed slots of one MoE token */
+    size_t BR = in->n_expert && (size_t)in->n_expert_used > B ? (size_t)in->n_expert_used : B;
     TRY(dalloc((void **)&c->k_cache, kv * 4));
     TRY(dalloc((void **)&c->v_cache, kv * 4));
     TRY(dalloc((void **)&c->rope_cos, S * hd / 2 * 4));
@@ -53,12 +55,12 @@ int sdy_engine_alloc(engine_ctx *c) {
     TRY(dalloc((void **)&c->k, B * kv_dim * 4));
     TRY(dalloc((void **)&c->v, B * kv_dim * 4));
     TRY(dalloc((void **)&c->att, B * q_dim * 4));
-    TRY(dalloc((void **)&c->hb, B * ffn * 4));
-    TRY(dalloc((void **)&c->hb2, B * ffn * 4));
+    TRY(dalloc((void **)&c->hb, BR * ffn * 4));
+    TRY(dalloc((void **)&c->hb2, BR * ffn * 4));
     TRY(dalloc((void **)&c->logits_dev, logit_rows * in->n_vocab * 4));
     TRY(dalloc((void **)&c->part, sdy_attn_part_floats((int)B, in->n_head, in->head_dim, (int)S) * 4));
-    TRY(dalloc(&c->xq[0], B * ((max_in + 31) / 32 * 34)));
-    TRY(dalloc(&c->xq[1], B * ((max_in + 255) / 256 * 292)));
+    TRY(dalloc(&c->xq[0], BR * ((max_in + 31) / 32 * 34)));
+    TRY(dalloc(&c->xq[1], BR * ((max_in + 255) / 256 * 292)));
     TRY(dalloc((void **)&c->tok_dev, B * 4));
     TRY(sdy_host_alloc((void **)&c->tok_host, B * 4));
     TRY(dalloc((void **)&c->qkv, (q_dim + 2 * kv_dim) * 4));
@@ -71,7 +73,7 @@ int sdy_engine_alloc(engine_ctx *c) {
         TRY(dalloc((void **)&c->moe_w, chosen * 4));
         TRY(dalloc((void **)&c->moe_top, chosen * 4));
         TRY(dalloc((void **)&c->moe_x, B * in->dim * 4));
-        TRY(dalloc((void **)&c->moe_y, B * in->dim * 4));
+        TRY(dalloc((void **)&c->moe_y, BR * in->dim * 4));
         TRY(dalloc((void **)&c->moe_sum, B * in->dim * 4));
         TRY(dalloc((void **)&c->moe_gidx, chosen * 4));
         TRY(dalloc((void **)&c->moe_gw, chosen * 4));
@@ -217,6 +219,70 @@ static int moe(engine_ctx *c, const dlayer *L, int n) {
     return rc;
 }
 
+/* The one-token MoE block on the device (csrc/model_llama.c:724-751 for one token): router
+ * matvec, softmax + top-k, the k chosen experts' gate|up (SwiGLU) and down as grouped matvecs
+ * indexed by the device-side top-k, then the weighted sum in ascending expert order plus the
+ * residual. No host round trip, so the step can be recorded as a graph. */
+static int moe_decode(engine_ctx *c, const dlayer *L) {
+    const engine_model_info *in = &c->m->info;
+    const int dim = in->dim, fe = in->ffn_exp_dim, ne = in->n_expert, k = in->n_expert_used;
+    TRY(norm_for(c, c->x, L->ffn_norm, L->gu_fused ? &L->gate_up : &L->gate, 1)); /* xb and its Q8_K row */
+    TRY(mm(c, c->moe_probs, c->xb, &L->gate_inp, 1, NULL, NULL, 0));
+    TRY(sdy_moe_route(c->moe_probs, 1, ne, k, c->moe_top, c->moe_w, c->st));
+    sdy_mv_args a;
+    memset(&a, 0, sizeof a);
+    a.n_tok = 1;
+    a.xq = c->xq[1];
+    a.out = c->hb;
+    a.out_stride = fe;
+    a.row0 = 0;
+    if (L->gu_fused) {
+        a.row1 = 2 * fe;
+        a.epilogue = SDY_EPI_SWIGLU;
+        TRY(sdy_matvec_grouped(&L->gate_up.m, &a, c->moe_top, k, 2L * fe, 0, fe, c->st));
+    } else {
+        a.row1 = fe;
+        TRY(sdy_matvec_grouped(&L->gate.m, &a, c->moe_top, k, fe, 0, fe, c->st));
+        a.out = c->hb2;
+        TRY(sdy_matvec_grouped(&L->up.m, &a, c->moe_top, k, fe, 0, fe, c->st));
+        TRY(sdy_silu_mul(c->hb, c->hb2, (long)k * fe, c->st));
+    }
+    /* the k SwiGLU rows, quantised for down (the Q8_K row of xb is no longer needed) */
+    c->xq_src[0] = c->xq_src[1] = NULL;
+    TRY(sdy_quantize(SDY_Q8_K, c->hb, c->xq[1], fe, k, c->st));
+    memset(&a, 0, sizeof a);
+    a.n_tok = 1;
+    a.xq = c->xq[1];
+    a.out = c->moe_y;
+    a.out_stride = dim;
+    a.row0 = 0;
+    a.row1 = dim;
+    TRY(sdy_matvec_grouped(&L->down.m, &a, c->moe_top, k, dim, (long)(fe / 256) * 292, dim, c->st));
+    return sdy_moe_combine(c->moe_y, c->moe_top, c->moe_w, 1, k, dim, c->x, c->x, c->st);
+}
+
+static int kquant_rows_le_4096(int type, int n_in) {
+    return (type == SDY_Q4_K || type == SDY_Q6_K) && n_in % 256 == 0 && n_in <= 4096;
+}
+
+/* Whether every MoE layer can take moe_decode: K-quant expert matrices with rows of at most 4096
+ * elements (the grouped matvec), an expert width that Q8_K blocks tile, an f32 router. */
+int sdy_engine_moe_device_ok(const engine_ctx *c) {
+    const engine_model *m = c->m;
+    const engine_model_info *in = &m->info;
+    if (!in->n_expert) return 0;
+    for (int l = 0; l < in->n_layer; l++) {
+        const dlayer *L = &m->layers[l];
+        if (L->gate_inp.type != SDY_F32 || !kquant_rows_le_4096(L->down.type, in->ffn_exp_dim)) return 0;
+        if (L->gu_fused) {
+            if (!kquant_rows_le_4096(L->gate_up.type, in->dim) || (64 / (in->dim / 64)) % 2) return 0;
+        } else if (!kquant_rows_le_4096(L->gate.type, in->dim) || !kquant_rows_le_4096(L->up.type, in->dim)) {
+            return 0;
+        }
+    }
+    return 1;
+}
+
 /* Whether the one-token step can use the fused decode kernels (and be recorded as a graph). */
 int sdy_engine_decode_fused_ok(const engine_ctx *c) {
     const engine_model_info *in = &c->m->info;
@@ -276,7 +342,9 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
                               c->att, q_dim, c->st));
             TRY(mm(c, c->x, c->att, &L->wo, n, NULL, c->x, 1));
         }
-        if (in->n_expert) {
+        if (in->n_expert && decode && c->moe_device) {
+            TRY(moe_decode(c, L));
+        } else if (in->n_expert) {
             TRY(norm_for(c, c->x, L->ffn_norm, &L->gate_inp, n));
             TRY(moe(c, L, n));
             TRY(sdy_add(c->x, c->moe_sum, c->x, (long)n * dim, c->st));
@@ -303,7 +371,7 @@ int sdy_engine_forward(engine_ctx *c, const int32_t *tokens, int n, int out_rows
         TRY(sdy_h2d(c->step_dev, c->step_host, 2 * 4, c->st));
         /* the first one-token step runs eagerly (it settles every lazily configured kernel); the
            second is recorded as a graph that later steps replay */
-        if (c->graph_ok == 0 && c->use_graph && c->n_decode >= 1 && !in->n_expert) {
+        if (c->graph_ok == 0 && c->use_graph && c->n_decode >= 1) {
             TRY(sdy_graph_begin(c->st));
             int rc = layers(c, 1, out_rows, 1);
             if (rc) {

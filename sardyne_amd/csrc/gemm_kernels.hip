@@ -102,12 +102,18 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     const half2v off6 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
 
     for (int sb = 0; sb < g.nb; sb++) {
-        // scales of this lane's A row
+        // this super-block's weights for the lane's A row, all requested up front
+        u32x2 q[4][3];
+#pragma unroll
+        for (int un = 0; un < 4; un++) load_unit<WT>(g, ra, 4 * sb + un, h, q[un]);
+        // scales of this lane's A row, and d (dmin) of that row (lanes 0..31 hold rows 0..31)
         int sc[16];
         int mn[8];
+        uint32_t dpair;
         if constexpr (WT == SDY_Q4_K) {
             const u32x4 hd = *reinterpret_cast<const u32x4 *>(g.p[2] + ((size_t)ra * g.nb + sb) * 16);
             const uint32_t A = hd.y, B = hd.z, C = hd.w;
+            dpair = hd.x;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 sc[j] = (A >> (8 * j)) & 63;
@@ -119,28 +125,27 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
             const u32x4 s4 = *reinterpret_cast<const u32x4 *>(g.p[3] + ((size_t)ra * g.nb + sb) * 16);
 #pragma unroll
             for (int j = 0; j < 16; j++) sc[j] = (int)(int8_t)((s4[j >> 2] >> (8 * (j & 3))) & 255u);
+            dpair = *reinterpret_cast<const uint16_t *>(g.p[4] + ((size_t)ra * g.nb + sb) * 2);
         }
         float16v isum[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) isum[nt] = float16v{};
 #pragma unroll
         for (int un = 0; un < 4; un++) {
-            u32x2 q[3];
-            load_unit<WT>(g, ra, 4 * sb + un, h, q);
 #pragma unroll
             for (int s = 0; s < 4; s++) {
                 half8 a;
                 if constexpr (WT == SDY_Q4_K) {
                     // s: 0 QA low, 1 QB low (sub-block 2un), 2 QA high, 3 QB high (sub-block 2un + 1)
-                    const u32x2 src = (s & 1) ? q[1] : q[0];
+                    const u32x2 src = (s & 1) ? q[un][1] : q[un][0];
                     const u32x2 nib = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
                     const _Float16 f = (_Float16)(float)sc[2 * un + (s >> 1)];
                     a = frag_scaled(nib, off, half2v{f, f});
                 } else {
                     // s: 0 N0 low, 1 N1 low, 2 N0 high, 3 N1 high; high bits from HB >> 2s; group 4un + s
-                    const u32x2 src = (s & 1) ? q[1] : q[0];
+                    const u32x2 src = (s & 1) ? q[un][1] : q[un][0];
                     const u32x2 lo = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
-                    const u32x2 hi = ((q[2] >> (unsigned)(2 * s)) & 0x03030303u) << 4u;
+                    const u32x2 hi = ((q[un][2] >> (unsigned)(2 * s)) & 0x03030303u) << 4u;
                     const _Float16 f = (_Float16)(float)sc[4 * un + s];
                     a = frag_scaled(lo | hi, off6, half2v{f, f});
                 }
@@ -166,16 +171,10 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
         // combine in the reference's order: acc + (yd*d*isum - yd*dmin*msum)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const long ri = rt + 8 * (r >> 2) + 4 * h + (r & 3);
-            const long row = g.row0 + (ri < g.n_rows ? ri : g.n_rows - 1);
-            float d, dmin = 0.0f;
-            if constexpr (WT == SDY_Q4_K) {
-                const uint32_t dd = *reinterpret_cast<const uint32_t *>(g.p[2] + ((size_t)row * g.nb + sb) * 16);
-                d = sdy_h2f((uint16_t)(dd & 0xFFFFu));
-                dmin = sdy_h2f((uint16_t)(dd >> 16));
-            } else {
-                d = sdy_h2f(*reinterpret_cast<const uint16_t *>(g.p[4] + ((size_t)row * g.nb + sb) * 2));
-            }
+            // D row 8(r/4) + 4h + r%4 of the tile is the A row of lane 8(r/4) + 4h + r%4
+            const uint32_t dd = (uint32_t)__shfl((int)dpair, 8 * (r >> 2) + 4 * h + (r & 3));
+            const float d = sdy_h2f((uint16_t)(dd & 0xFFFFu));
+            const float dmin = WT == SDY_Q4_K ? sdy_h2f((uint16_t)(dd >> 16)) : 0.0f;
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 const float ydv = g.yd[(size_t)tb[nt] * g.nb + sb];

@@ -195,6 +195,12 @@ __global__ __launch_bounds__(64) void k_moe_route(float *probs, int n_expert, in
     }
 }
 
+// One step of the reference's AVX2 axpy (csrc/ops_avx2.c:142-147) at element d of a dim-element
+// row: fused in the 8-lane body, a rounded product then a sum in the tail.
+SDY_DEV float axpy1(float acc, float w, float y, int d, int dim) {
+    return d < (dim & ~7) ? fmaf(w, y, acc) : acc + w * y;
+}
+
 // out[t] = sum over the k chosen experts, in ascending expert id, of w * y   (moe_ffn's axpy order
 // over experts, csrc/model_llama.c:734-750). y is [n_tok][k][dim] in top-k slot order.
 __global__ void k_moe_combine(const float *y, const int32_t *top, const float *wts, int k, int dim, float *out,
@@ -213,7 +219,7 @@ __global__ void k_moe_combine(const float *y, const int32_t *top, const float *w
                 best = j;
             }
         last = bid;
-        acc = fmaf(wts[(size_t)t * k + best], y[((size_t)t * k + best) * dim + d], acc);
+        acc = axpy1(acc, wts[(size_t)t * k + best], y[((size_t)t * k + best) * dim + d], d, dim);
     }
     out[(size_t)t * dim + d] = resid ? resid[(size_t)t * dim + d] + acc : acc;
 }
@@ -232,7 +238,7 @@ __global__ void k_scatter_axpy(float *dst, const int32_t *idx, const float *w, c
     int d = blockIdx.x * blockDim.x + threadIdx.x;
     if (d < dim) {
         float *o = dst + (size_t)idx[r] * dim + d;
-        *o = fmaf(w[r], src[(size_t)r * dim + d], *o);
+        *o = axpy1(*o, w[r], src[(size_t)r * dim + d], d, dim);
     }
 }
 

@@ -283,6 +283,14 @@ struct MvArgs {
     int nterm;   // f32 terms per row and token (super-blocks or units)
     int q64, r64;  // 64 / T and 64 % T: advance of a lane's (row, unit) per iteration
     int swiglu;    // rows (2i, 2i+1) are (gate, up) of output i: out[i] = silu(gate) * up
+    // Grouped one-token matvec (routed experts, k_matvec_rl with register activations only):
+    // blockIdx.y is a slot whose rows are those of expert slot_expert[slot] in a stack of
+    // n_slot_exp experts of slot_rows rows each; the slot's activation row starts xq_slot bytes and
+    // its output out_slot floats after slot 0's. slot_expert == null: an ordinary matvec.
+    const int32_t *slot_expert;
+    long slot_rows;
+    int n_slot_exp;
+    long xq_slot, out_slot;
 };
 
 constexpr bool is_k(int wt) { return wt == SDY_Q4_K || wt == SDY_Q6_K; }
@@ -642,12 +650,13 @@ __global__ __launch_bounds__(THREADS) void k_matvec(MvArgs a) {
     }
 }
 
-// Row-in-lanes variant (64 % T == 0): an iteration covers 64/T whole rows, lane = (row rl, unit u)
-// for the whole kernel. After the quad reduction the super-block terms of a row sit in lanes
+// Row-in-lanes variant: an iteration covers 64/T whole rows, lane = (row rl, unit u) for the whole
+// kernel (T <= 64; when T does not divide 64 — K-quants with one token only — lanes past
+// (64/T)*T idle). After the quad reduction the super-block terms of a row sit in lanes
 // rl*T + 4s; the row sum folds them in block order with lane shuffles (the reference's sequential
 // f32 order), so no LDS round trip is needed. 32-element types sum their unit terms with a fixed
-// butterfly over the row's T lanes. Each wave walks one contiguous, balanced range of iterations
-// and loads the next iteration's weights while it computes the current one.
+// butterfly over the row's T lanes (T a power of two). Waves stride over the iterations and load
+// the next iteration's weights while they compute the current one.
 template <int WT, int MT, bool YREG>
 __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
     extern __shared__ uint8_t lds[];
@@ -661,7 +670,21 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
     const int *sy = reinterpret_cast<const int *>(lds + y_bytes + (size_t)MT * T * 8);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rpi = 64 / T;  // rows per iteration
-    const int rl = lane / T, u = lane - rl * T;
+    const int rl_ = lane / T, u = lane - rl_ * T;
+    const bool lane_on = rl_ < rpi;   // spare lanes (T not dividing 64) shadow row 0 and store nothing
+    const int rl = lane_on ? rl_ : 0;
+    // grouped (routed-expert) launch: this workgroup's slot, its expert's first row, activation and output
+    long poff = 0;
+    const uint8_t *xq = a.xq;
+    float *out = a.out;
+    if (a.slot_expert) {
+        const int slot = blockIdx.y;
+        int e = a.slot_expert[slot];
+        e = e < 0 ? 0 : (e >= a.n_slot_exp ? a.n_slot_exp - 1 : e);
+        poff = (long)e * a.slot_rows;
+        xq += (size_t)slot * a.xq_slot;
+        out += (size_t)slot * a.out_slot;
+    }
     const long n_rows = a.row1 - a.row0;
     const long n_it = (n_rows + rpi - 1) / rpi;
     // Workgroups are dealt round-robin over the 8 XCDs; renumber them so that consecutive work
@@ -674,7 +697,7 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
     auto row_at = [&](long itx) -> long { return a.row0 + itx * rpi + rl; };
     auto load_it = [&](long itx, WRegs<WT> &r) {
         long rr = row_at(itx);
-        load_w<WT>(a.P, (uint32_t)(rr < a.row1 ? rr : a.row0), (uint32_t)u, r);
+        load_w<WT>(a.P, (uint32_t)((rr < a.row1 ? rr : a.row0) + poff), (uint32_t)u, r);
     };
     // the first weight loads go out before anything else, so their latency overlaps the
     // activation loads
@@ -688,7 +711,7 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
     float ydr = 0.0f;
     if constexpr (DIRECT) {
         if (wid >= n_it) return;
-        const uint8_t *blk = a.xq + (size_t)(u >> 2) * 292;
+        const uint8_t *blk = xq + (size_t)(u >> 2) * 292;
         const uint8_t *yb = blk + 4 + 64 * (u & 3);
 #pragma unroll
         for (int q = 0; q < 4; q++)
@@ -711,7 +734,7 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
     }
     auto body = [&](const WRegs<WT> &cur, long itx) {
         const long row = row_at(itx);
-        const bool valid = row < a.row1;
+        const bool valid = lane_on && row < a.row1;
 #pragma unroll
         for (int m = 0; m < MT; m++) {
             if (m >= a.n_tok) break;
@@ -762,11 +785,11 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
                 // rows per iteration is even and row0 is even: lane (rl+1)*T holds the up row
                 const float up = __shfl(acc, (lane + T) & 63);
                 if (u == 0 && (rl & 1) == 0 && valid)
-                    a.out[(size_t)m * a.out_stride + ((row - a.row0) >> 1)] = sdy_silu_mul1(acc, up);
+                    out[(size_t)m * a.out_stride + ((row - a.row0) >> 1)] = sdy_silu_mul1(acc, up);
             } else if (u == 0 && valid) {
                 if (a.bias) acc = acc + a.bias[row];
                 if (a.resid) acc = a.resid[(size_t)m * a.out_stride + row] + acc;
-                a.out[(size_t)m * a.out_stride + row] = acc;
+                out[(size_t)m * a.out_stride + row] = acc;
             }
         }
     };
@@ -1217,7 +1240,7 @@ static int launch_mv_k(MvArgs &A, size_t lds, hipStream_t st) {
 static size_t mv_lds_bytes_rl(int T, int MT) { return (size_t)MT * 4 * T * 16 + (size_t)MT * T * 16; }
 
 template <int WT, int MT, bool YREG>
-static int launch_mv_rl(MvArgs &A, size_t lds, hipStream_t st) {
+static int launch_mv_rl(MvArgs &A, size_t lds, hipStream_t st, int n_slot = 1) {
     static int per_cu = 0;
     static size_t per_cu_lds = 0;
     const void *fn = (const void *)k_matvec_rl<WT, MT, YREG>;
@@ -1230,9 +1253,10 @@ static int launch_mv_rl(MvArgs &A, size_t lds, hipStream_t st) {
     const int rpi = 64 / A.P.T;
     long n_it = (A.row1 - A.row0 + rpi - 1) / rpi;
     long wgs = (n_it + WAVES - 1) / WAVES;
-    long cap = (long)(g_n_cu ? g_n_cu : 256) * per_cu;
+    long cap = (long)(g_n_cu ? g_n_cu : 256) * per_cu / n_slot;
+    if (cap < 8) cap = 8;
     if (wgs > cap) wgs = cap;
-    hipLaunchKernelGGL((k_matvec_rl<WT, MT, YREG>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
+    hipLaunchKernelGGL((k_matvec_rl<WT, MT, YREG>), dim3((unsigned)wgs, (unsigned)n_slot), dim3(THREADS), lds, st, A);
     return sdy_check_launch("matvec");
 }
 
@@ -1273,7 +1297,7 @@ static int launch_mv_lr(MvArgs &A, size_t lds, hipStream_t st) {
 template <int WT, int MT>
 static int launch_mv(const sdy_mat *m, const sdy_mv_args *a, int n_tok, const uint8_t *xq, float *out,
                      const float *resid, hipStream_t st) {
-    MvArgs A;
+    MvArgs A = {};
     A.P = planes_of(m);
     A.xq = xq;
     A.n_tok = n_tok;
@@ -1297,6 +1321,10 @@ static int launch_mv(const sdy_mat *m, const sdy_mv_args *a, int n_tok, const ui
         if (MT == 1) return launch_mv_rl<WT, MT, true>(A, lds, st);
         return launch_mv_rl<WT, MT, false>(A, lds, st);
     }
+    // one K-quant token, T < 64 not dividing 64 (e.g. 768-element rows, T = 12): floor(64/T) rows per
+    // wave iteration
+    if constexpr (MT == 1 && is_k(WT))
+        if (T < 64 && (!A.swiglu || (64 / T) % 2 == 0)) return launch_mv_rl<WT, 1, true>(A, 0, st);
     if constexpr (MT == 1 && is_k(WT))
         if (!A.swiglu) return launch_mv_lr<WT>(A, mv_lds_bytes_rl(T, 1), st);
     return launch_mv_k<WT, MT, false>(A, lds, st);
@@ -1352,6 +1380,52 @@ extern "C" int sdy_matvec(const sdy_mat *m, const sdy_mv_args *a, sdy_stream s) 
         return sdy_matvec_float(m->type, (const uint8_t *)m->base + m->plane_off[0], m->n_in, a, s);
     default: return sdy_fail(-1, "matvec: type %d", m->type);
     }
+}
+
+template <int WT>
+static int mv_grouped(const sdy_mat *m, const sdy_mv_args *a, const int32_t *slot_expert, int n_slot, long slot_rows,
+                      long xq_slot, long out_slot, hipStream_t st) {
+    MvArgs A = {};
+    A.P = planes_of(m);
+    A.xq = (const uint8_t *)a->xq;
+    A.n_tok = 1;
+    A.out = a->out;
+    A.out_stride = a->out_stride;
+    A.row0 = a->row0;
+    A.row1 = a->row1;
+    A.swiglu = a->epilogue == SDY_EPI_SWIGLU;
+    A.slot_expert = slot_expert;
+    A.slot_rows = slot_rows;
+    A.n_slot_exp = (int)(m->n_rows / slot_rows);
+    A.xq_slot = xq_slot;
+    A.out_slot = out_slot;
+    return launch_mv_rl<WT, 1, true>(A, 0, st, n_slot);
+}
+
+extern "C" int sdy_matvec_grouped(const sdy_mat *m, const sdy_mv_args *a, const int32_t *slot_expert, int n_slot,
+                                  long slot_rows, long xq_slot, long out_slot, sdy_stream s) {
+    hipStream_t st = (hipStream_t)s;
+    if (m->type != SDY_Q4_K && m->type != SDY_Q6_K)
+        return sdy_fail(-1, "grouped matvec: K-quant weights only (type %d)", m->type);
+    if (a->n_tok != 1 || a->bias || a->resid) return sdy_fail(-1, "grouped matvec: one token, no bias or residual");
+    if (slot_rows <= 0 || m->n_rows % slot_rows)
+        return sdy_fail(-1, "grouped matvec: %ld rows are not a stack of %ld-row experts", m->n_rows, slot_rows);
+    if (a->row0 < 0 || a->row1 > slot_rows || a->row0 > a->row1)
+        return sdy_fail(-1, "grouped matvec rows [%ld, %ld) outside an expert's %ld", a->row0, a->row1, slot_rows);
+    if (n_slot < 1 || n_slot > 65535) return sdy_fail(-1, "grouped matvec: %d slots", n_slot);
+    const int T = m->n_units;
+    if (T > 64) return sdy_fail(-1, "grouped matvec: rows of %d elements above 4096", m->n_in);
+    if (a->epilogue == SDY_EPI_SWIGLU && ((64 / T) % 2 || ((a->row1 - a->row0) | a->row0) & 1))
+        return sdy_fail(-1, "grouped matvec: SwiGLU needs an even number of rows per iteration and an even row range");
+    if (a->row0 == a->row1) return 0;
+    if (!g_n_cu) {
+        int n_cu = 0;
+        size_t mem = 0;
+        sdy_device_info(&n_cu, &mem);
+        g_n_cu = n_cu;
+    }
+    if (m->type == SDY_Q4_K) return mv_grouped<SDY_Q4_K>(m, a, slot_expert, n_slot, slot_rows, xq_slot, out_slot, st);
+    return mv_grouped<SDY_Q6_K>(m, a, slot_expert, n_slot, slot_rows, xq_slot, out_slot, st);
 }
 
 extern "C" int sdy_matvec_float(int wtype, const void *w, int n_in, const sdy_mv_args *a, sdy_stream s) {

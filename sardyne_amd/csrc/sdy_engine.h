@@ -55,6 +55,8 @@ struct engine_ctx {
     int n_decode;               /* one-token evals so far (the first runs eagerly) */
     int decode_fused;           /* one-token steps use the fused decode kernels */
     int use_graph;              /* one-token steps are recorded once and replayed */
+    int moe_device;             /* one-token MoE blocks route, run their experts and combine on the
+                                   device (grouped matvec, no host round trip) */
     float *qkv;                 /* q | k | v of one token */
     void *gemm_ws;              /* scratch of the prefill GEMM (f16 activations of n_batch rows) */
     /* MoE */
@@ -68,4 +70,5 @@ int sdy_engine_alloc(engine_ctx *c);
 void sdy_engine_release(engine_ctx *c);
 int sdy_engine_forward(engine_ctx *c, const int32_t *tokens, int n, int out_rows);
 int sdy_engine_decode_fused_ok(const engine_ctx *c);
+int sdy_engine_moe_device_ok(const engine_ctx *c);
 #endif

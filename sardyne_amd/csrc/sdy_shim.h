@@ -100,6 +100,12 @@ typedef struct {
 enum { SDY_EPI_NONE = 0, SDY_EPI_SWIGLU = 1 };
 /* out = W · x for rows [row0, row1) and n_tok tokens. */
 int sdy_matvec(const sdy_mat *m, const sdy_mv_args *a, sdy_stream s);
+/* Grouped one-token matvec over routed experts: m stacks experts of slot_rows rows; for each of
+ * n_slot slots, rows [row0, row1) of expert slot_expert[slot] (device array) times the slot's
+ * Q8_K activation row (a->xq + slot * xq_slot bytes) go to a->out + slot * out_slot. Q4_K / Q6_K,
+ * rows of at most 4096 elements; the SwiGLU epilogue as in sdy_matvec. */
+int sdy_matvec_grouped(const sdy_mat *m, const sdy_mv_args *a, const int32_t *slot_expert, int n_slot,
+                       long slot_rows, long xq_slot, long out_slot, sdy_stream s);
 
 /* The prefill GEMM (gemm_kernels.hip): the same outputs as sdy_matvec (bit for bit) for
  * n_tok >= 2 tokens of Q8_K activations a->xq on Q4_K / Q6_K matrices with gemm_ok, through

@@ -39,6 +39,10 @@ SPECS = {
                             qk_norm=True, router_std=0.3, type_fn=kquant_moe_types, t_output="Q8_0", t_embd="Q8_0"),
     "qwen2-gqa8-hd128": ModelSpec(n_vocab=300, dim=256, n_layer=2, n_head=16, n_kv_head=2, head_dim=128,
                                   ffn_dim=512, context=256),
+    # expert FFN 768 as in Qwen3-30B-A3B: down rows of 12 K-quant units (not a divisor of 64)
+    "moe-16x4-ffn768": ModelSpec(arch="qwen3moe", n_vocab=300, dim=256, n_layer=2, n_head=4, n_kv_head=2,
+                                 head_dim=64, ffn_dim=2048, context=64, n_expert=16, n_expert_used=4,
+                                 ffn_exp_dim=768, qkv_bias=False, qk_norm=True, router_std=0.3),
     "moe-128x8": ModelSpec(arch="qwen3moe", n_vocab=300, dim=256, n_layer=2, n_head=4, n_kv_head=2, head_dim=64,
                            ffn_dim=2048, context=64, n_expert=128, n_expert_used=8, ffn_exp_dim=256, qkv_bias=False,
                            qk_norm=True, router_std=0.3),
@@ -167,8 +171,10 @@ def test_decode_paths_bit_identical(model_path):
     model = Model(model_path)
     fused_graph = _decode_run(model, {})
     fused_eager = _decode_run(model, {"SARDYNE_NO_GRAPH": "1"})
+    host_moe = _decode_run(model, {"SARDYNE_NO_DEVICE_MOE": "1"})
     unfused = _decode_run(model, {"SARDYNE_NO_FUSED_DECODE": "1"})
     assert np.array_equal(fused_graph.view(np.uint32), fused_eager.view(np.uint32))
+    assert np.array_equal(fused_graph.view(np.uint32), host_moe.view(np.uint32))
     assert np.array_equal(fused_graph.view(np.uint32), unfused.view(np.uint32))
     # the oracle's scalar kernels: its AVX2 Q8_0/Q4_0/Q5_0 order differs between one-token and
     # batched calls, and on this seed a resulting activation-quantisation flip moves one decode row

@@ -110,7 +110,8 @@ def _matvec_case(kind, n_in, n_out, n_tok, seed, gen="workload"):
 
 @pytest.mark.parametrize("kind", list(TYPES))
 @pytest.mark.parametrize("n_in,n_out,n_tok", [(256, 13, 1), (512, 13, 3), (2048, 37, 1), (768, 20, 5),
-                                              (11008, 9, 2), (4096, 16, 9), (2048, 64, 8)])
+                                              (11008, 9, 2), (4096, 16, 9), (2048, 64, 8), (768, 41, 1),
+                                              (1280, 23, 1), (2560, 7, 1)])
 def test_matvec_vs_oracle(kind, n_in, n_out, n_tok):
     if kind in ("Q8_0", "Q4_0", "Q5_0") and n_in % 32:
         pytest.skip("row not a whole number of blocks")
@@ -345,6 +346,70 @@ def test_swiglu_epilogue(kind, n_in, ffn, n_tok):
     O.lib().orc_silu_mul(ptr(exp), ptr(eu), exp.size)
     np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * float(np.abs(exp).max()))
     L.sdy_mat_free(ctypes.byref(m))
+
+
+@pytest.mark.parametrize("kind,n_in,e_rows,swiglu,rows", [
+    ("Q4_K", 2048, 96, True, None), ("Q6_K", 768, 200, False, None), ("Q4_K", 768, 64, False, (3, 61)),
+    ("Q6_K", 256, 40, True, None), ("Q4_K", 1280, 30, False, None), ("Q6_K", 4096, 16, False, None)])
+def test_grouped_matvec(kind, n_in, e_rows, swiglu, rows):
+    """The routed-expert grouped matvec: slot s computes rows of expert top[s] of a stacked
+    matrix with its own activation row (down) or one shared row (gate|up with SwiGLU), with the
+    bits of the plain matvec on that expert's rows, which are the oracle's."""
+    t = TYPES[kind]
+    L = lib()
+    n_exp = 12
+    top = np.array([7, 2, 11, 2, 0], np.int32)  # expert 2 twice, as two tokens' slots could
+    k = len(top)
+    rng = np.random.default_rng(n_in + e_rows)
+    w = random_blocks(kind, n_exp * e_rows * n_in // 256, rng).reshape(n_exp * e_rows, -1)
+    x = rng.standard_normal((1 if swiglu else k, n_in)).astype(np.float32)
+    xq = O.quantize(x, O.Q8_K)
+    xrow = O.row_size(O.Q8_K, n_in)
+    r0, r1 = rows or (0, e_rows)
+    n_out = (r1 - r0) // 2 if swiglu else e_rows
+    epi = capi.EPI_SWIGLU if swiglu else capi.EPI_NONE
+    m = capi.DeviceMatrix(t, n_in, n_exp * e_rows, w)
+    dq, dtop = capi.DeviceBuffer.from_array(xq), capi.DeviceBuffer.from_array(top)
+    dout = capi.DeviceBuffer.from_array(np.full((k, n_out), np.nan, np.float32))
+    a = capi.SdyMvArgs(xq=dq.ptr, n_tok=1, out=dout.ptr, out_stride=n_out, row0=r0, row1=r1, epilogue=epi)
+    capi.check(L.sdy_matvec_grouped(ctypes.byref(m.m), ctypes.byref(a), dtop.ptr, k, e_rows, 0 if swiglu else xrow,
+                                    n_out, None))
+    got = dout.to_array(np.float32, (k, n_out))
+    # the plain matvec writes out[row] for row in [row0, row1) (out[(row - row0) / 2] with SwiGLU)
+    n1 = n_out if swiglu else n_exp * e_rows
+    d1 = capi.DeviceBuffer.from_array(np.full(n1, np.nan, np.float32))
+    for s, e in enumerate(top):
+        xs = 0 if swiglu else s
+        a1 = capi.SdyMvArgs(xq=dq.ptr + xs * xrow, n_tok=1, out=d1.ptr, out_stride=n1, row0=e * e_rows + r0,
+                            row1=e * e_rows + r1, epilogue=epi)
+        capi.check(L.sdy_matvec(ctypes.byref(m.m), ctypes.byref(a1), None))
+        one = d1.to_array(np.float32, n1)
+        if swiglu:
+            assert np.array_equal(bits(got[s]), bits(one)), s
+        else:
+            assert np.array_equal(bits(got[s, r0:r1]), bits(one[e * e_rows + r0:e * e_rows + r1])), s
+            assert np.isnan(got[s, :r0]).all() and np.isnan(got[s, r1:]).all()
+            exp = O.matmul_q(w[e * e_rows + r0:e * e_rows + r1], t, xq[xs:xs + 1], n_in, simd=1)[0]
+            assert np.array_equal(bits(got[s, r0:r1]), bits(exp)), s
+    if swiglu:  # the gate and up rows of each slot through the oracle, then SiLU (libm expf: 1e-5)
+        for s, e in enumerate(top):
+            y = O.matmul_q(w[e * e_rows + r0:e * e_rows + r1], t, xq, n_in, simd=1)[0]
+            g, u = y[0::2].copy(), y[1::2].copy()
+            O.lib().orc_silu_mul(ptr(g), ptr(u), g.size)
+            np.testing.assert_allclose(got[s], g, rtol=1e-5, atol=1e-5 * float(np.abs(g).max()))
+
+
+def test_grouped_matvec_rejects_bad_shapes():
+    L = lib()
+    w = random_blocks("Q4_K", 4 * 10 * 2048 // 256, np.random.default_rng(0)).reshape(40, -1)
+    m = capi.DeviceMatrix(O.Q4_K, 2048, 40, w)
+    top = capi.DeviceBuffer.from_array(np.zeros(2, np.int32))
+    a = capi.SdyMvArgs(xq=None, n_tok=1, out=None, out_stride=10, row0=0, row1=10)
+    assert L.sdy_matvec_grouped(ctypes.byref(m.m), ctypes.byref(a), top.ptr, 2, 7, 0, 10, None) != 0  # 40 % 7
+    a.row1 = 11
+    assert L.sdy_matvec_grouped(ctypes.byref(m.m), ctypes.byref(a), top.ptr, 2, 10, 0, 10, None) != 0
+    a.row1, a.n_tok = 10, 2
+    assert L.sdy_matvec_grouped(ctypes.byref(m.m), ctypes.byref(a), top.ptr, 2, 10, 0, 10, None) != 0
 
 
 def _gemm_case(kind, n_in, n_out, n_tok, seed, gen="workload"):
