@@ -154,6 +154,12 @@ static int read_config(engine_model *m, char *err, size_t err_len) {
             set_err(err, err_len, "expert_used_count=%d oltre expert_count=%d", in->n_expert_used, in->n_expert);
             return -1;
         }
+        /* the device router keeps a token's expert probabilities in one wave's registers */
+        if (in->n_expert > 512 || in->n_expert_used < 1 || in->n_expert_used > 64) {
+            set_err(err, err_len, "expert_count=%d / expert_used_count=%d oltre i limiti del dispositivo (512 / 64)",
+                    in->n_expert, in->n_expert_used);
+            return -1;
+        }
         if ((v = meta_int(&mt, "expert_feed_forward_length", in->ffn_dim / in->n_expert_used)) <= 0) {
             if (v == 0) set_err(err, err_len, "dimensione degli esperti nulla");
             return -1;

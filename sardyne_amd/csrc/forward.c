@@ -270,7 +270,7 @@ static int kquant_rows_le_4096(int type, int n_in) {
 int sdy_engine_moe_device_ok(const engine_ctx *c) {
     const engine_model *m = c->m;
     const engine_model_info *in = &m->info;
-    if (!in->n_expert) return 0;
+    if (!in->n_expert || in->n_expert_used > 16) return 0; /* the combine sorts up to 16 slots in registers */
     for (int l = 0; l < in->n_layer; l++) {
         const dlayer *L = &m->layers[l];
         if (L->gate_inp.type != SDY_F32 || !kquant_rows_le_4096(L->down.type, in->ffn_exp_dim)) return 0;

@@ -141,57 +141,67 @@ __global__ void k_rope(float *x, int n_heads, int hd, const float *cs, const flo
 // One wave per token: softmax over the expert logits (max, expf, double sum, float reciprocal),
 // then top-k by repeated arg-max with ties to the lower index (the order moe_select produces,
 // csrc/model_llama.c:653-666) and weights renormalised by their sequential float sum.
-__global__ __launch_bounds__(64) void k_moe_route(float *probs, int n_expert, int k, int32_t *top, float *wts) {
+template <int NPL>  // experts held per lane: n_expert <= 64 * NPL
+__global__ __launch_bounds__(64) void k_moe_route(const float *logits, int n_expert, int k, int32_t *top,
+                                                  float *wts) {
     const int t = blockIdx.x, lane = threadIdx.x;
-    float *p = probs + (size_t)t * n_expert;
+    const float *p = logits + (size_t)t * n_expert;
+    float v[NPL];
     float m = -INFINITY;
-    for (int e = lane; e < n_expert; e += 64) m = fmaxf(m, p[e]);
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    double s = 0.0;
-    for (int e = lane; e < n_expert; e += 64) {
-        float v = expf(p[e] - m);
-        p[e] = v;
-        s += (double)v;
+#pragma unroll
+    for (int j = 0; j < NPL; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < n_expert ? p[e] : -INFINITY;
+        m = fmaxf(m, v[j]);
     }
-    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-    float inv = (float)(1.0 / s);
-    for (int e = lane; e < n_expert; e += 64) p[e] *= inv;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    // top-k
-    float chosen_sum = 0.0f;
-    int32_t *tt = top + (size_t)t * k;
-    uint32_t taken[4] = {0u, 0u, 0u, 0u};  // bitmask of taken experts per lane slot (n_expert <= 256)
-    for (int i = 0; i < k; i++) {
-        float best = -1.0f;
-        int bi = 0x7fffffff;
-        for (int e = lane, slot = 0; e < n_expert; e += 64, slot++) {
-            if (taken[slot >> 5] >> (slot & 31) & 1u) continue;
-            float v = p[e];
-            if (v > best || (v == best && e < bi)) {
-                best = v;
-                bi = e;
-            }
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    // op_softmax (csrc/ops.c:353-364): expf(x - max), the sum in double, times (float)(1 / sum).
+    // The probabilities stay in registers; -1 marks lanes past n_expert (never chosen).
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < NPL; j++)
+        if (lane + 64 * j < n_expert) {
+            v[j] = expf(v[j] - m);
+            s += (double)v[j];
         }
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    const float inv = (float)(1.0 / s);
+#pragma unroll
+    for (int j = 0; j < NPL; j++) v[j] = lane + 64 * j < n_expert ? v[j] * inv : -1.0f;
+    // moe_select (csrc/model_llama.c:653-666): k times the largest remaining probability, ties to
+    // the lowest expert; chosen ones are marked -2. The weights divide by the sum of the chosen
+    // probabilities taken in rank order.
+    float chosen_sum = 0.0f, my_p = 0.0f;
+    int my_e = 0;
+    for (int i = 0; i < k; i++) {
+        float best = -1.5f;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < NPL; j++)
+            if (v[j] > best) {  // own experts ascend with j: '>' keeps the lowest on ties
+                best = v[j];
+                bi = lane + 64 * j;
+            }
         for (int off = 32; off >= 1; off >>= 1) {
-            float ob = __shfl_xor(best, off);
-            int oi = __shfl_xor(bi, off);
+            const float ob = __shfl_xor(best, off);
+            const int oi = __shfl_xor(bi, off);
             if (ob > best || (ob == best && oi < bi)) {
                 best = ob;
                 bi = oi;
             }
         }
-        if ((bi & 63) == lane) {
-            int slot = bi >> 6;
-            taken[slot >> 5] |= 1u << (slot & 31);
+#pragma unroll
+        for (int j = 0; j < NPL; j++)
+            if (bi == lane + 64 * j) v[j] = -2.0f;
+        if (lane == i) {
+            my_p = best;
+            my_e = bi;
         }
-        if (lane == 0) tt[i] = bi;
         chosen_sum = chosen_sum + best;
     }
     if (lane < k) {
-        int e = tt[lane];
-        wts[(size_t)t * k + lane] = p[e] / chosen_sum;
+        top[(size_t)t * k + lane] = my_e;
+        wts[(size_t)t * k + lane] = my_p / chosen_sum;
     }
 }
 
@@ -202,28 +212,45 @@ SDY_DEV float axpy1(float acc, float w, float y, int d, int dim) {
 }
 
 // out[t] = sum over the k chosen experts, in ascending expert id, of w * y   (moe_ffn's axpy order
-// over experts, csrc/model_llama.c:734-750). y is [n_tok][k][dim] in top-k slot order.
+// over experts, csrc/model_llama.c:734-750), plus resid. y is [n_tok][k][dim] in top-k slot order.
+// The k (id, weight, value) triples of a token are sorted by id in registers (k <= KMAX).
+template <int KMAX>
 __global__ void k_moe_combine(const float *y, const int32_t *top, const float *wts, int k, int dim, float *out,
                               const float *resid) {
     const int t = blockIdx.y;
-    int d = blockIdx.x * blockDim.x + threadIdx.x;
-    if (d >= dim) return;
+    const int d0 = blockIdx.x * blockDim.x + threadIdx.x;
+    const int d = d0 < dim ? d0 : dim - 1;
     const int32_t *tt = top + (size_t)t * k;
-    float acc = 0.0f;
-    int last = -1;
-    for (int i = 0; i < k; i++) {  // visit slots in ascending expert id
-        int best = -1, bid = 0x7fffffff;
-        for (int j = 0; j < k; j++)
-            if (tt[j] > last && tt[j] < bid) {
-                bid = tt[j];
-                best = j;
-            }
-        last = bid;
-        acc = axpy1(acc, wts[(size_t)t * k + best], y[((size_t)t * k + best) * dim + d], d, dim);
+    int id[KMAX];
+    float w[KMAX], yv[KMAX];
+#pragma unroll
+    for (int i = 0; i < KMAX; i++) {
+        const int ii = i < k ? i : 0;
+        id[i] = i < k ? tt[ii] : 0x7fffffff;
+        w[i] = wts[(size_t)t * k + ii];
+        yv[i] = y[((size_t)t * k + ii) * dim + d];
     }
-    out[(size_t)t * dim + d] = resid ? resid[(size_t)t * dim + d] + acc : acc;
+#pragma unroll
+    for (int a = 0; a < KMAX; a++)
+#pragma unroll
+        for (int b = 0; b + 1 < KMAX - a; b++)
+            if (id[b] > id[b + 1]) {
+                const int ti = id[b];
+                id[b] = id[b + 1];
+                id[b + 1] = ti;
+                const float tw = w[b];
+                w[b] = w[b + 1];
+                w[b + 1] = tw;
+                const float ty = yv[b];
+                yv[b] = yv[b + 1];
+                yv[b + 1] = ty;
+            }
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KMAX; i++)
+        if (i < k) acc = axpy1(acc, w[i], yv[i], d, dim);
+    if (d0 < dim) out[(size_t)t * dim + d] = resid ? resid[(size_t)t * dim + d] + acc : acc;
 }
-
 
 // dst[r] = src[idx[r]] (rows of dim floats)
 __global__ void k_gather_rows(const float *src, const int32_t *idx, int dim, float *dst) {
@@ -311,16 +338,23 @@ extern "C" int sdy_rope(float *x, int n_heads, int hd, const float *cs, const fl
 }
 
 extern "C" int sdy_moe_route(float *probs, int n_tok, int n_expert, int k, int32_t *top, float *wts, sdy_stream s) {
-    if (n_expert > 8192) return sdy_fail(-1, "n_expert %d above 8192", n_expert);
-    if (k > 64) return sdy_fail(-1, "n_expert_used %d above 64", k);
-    hipLaunchKernelGGL(k_moe_route, dim3(n_tok), dim3(64), 0, (hipStream_t)s, probs, n_expert, k, top, wts);
+    if (n_expert > 512) return sdy_fail(-1, "n_expert %d above 512", n_expert);
+    if (k < 1 || k > n_expert || k > 64) return sdy_fail(-1, "n_expert_used %d (of %d experts)", k, n_expert);
+    hipStream_t st = (hipStream_t)s;
+    if (n_expert <= 64) hipLaunchKernelGGL(k_moe_route<1>, dim3(n_tok), dim3(64), 0, st, probs, n_expert, k, top, wts);
+    else if (n_expert <= 128) hipLaunchKernelGGL(k_moe_route<2>, dim3(n_tok), dim3(64), 0, st, probs, n_expert, k, top, wts);
+    else if (n_expert <= 256) hipLaunchKernelGGL(k_moe_route<4>, dim3(n_tok), dim3(64), 0, st, probs, n_expert, k, top, wts);
+    else hipLaunchKernelGGL(k_moe_route<8>, dim3(n_tok), dim3(64), 0, st, probs, n_expert, k, top, wts);
     return sdy_check_launch("moe_route");
 }
 
 extern "C" int sdy_moe_combine(const float *y, const int32_t *top, const float *wts, int n_tok, int k, int dim,
                                float *out, const float *resid, sdy_stream s) {
-    hipLaunchKernelGGL(k_moe_combine, dim3((dim + 255) / 256, n_tok), dim3(256), 0, (hipStream_t)s, y, top, wts, k, dim,
-                       out, resid);
+    hipStream_t st = (hipStream_t)s;
+    const dim3 grid((dim + 63) / 64, n_tok);
+    if (k < 1 || k > 16) return sdy_fail(-1, "moe_combine: %d experts per token (1..16)", k);
+    if (k <= 8) hipLaunchKernelGGL(k_moe_combine<8>, grid, dim3(64), 0, st, y, top, wts, k, dim, out, resid);
+    else hipLaunchKernelGGL(k_moe_combine<16>, grid, dim3(64), 0, st, y, top, wts, k, dim, out, resid);
     return sdy_check_launch("moe_combine");
 }
 

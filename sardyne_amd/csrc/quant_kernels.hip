@@ -894,8 +894,9 @@ SDY_DEV float welem(const uint8_t *w, size_t i) {
     else return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(w)[i] << 16);
 }
 
-// One wave per (row, token): lane l accumulates elements l, l+64, ... with fused multiply-adds,
-// then a fixed xor-butterfly reduction. Deterministic; parity with the reference is by tolerance.
+// One wave per (row, token): each lane accumulates its elements with fused multiply-adds in a
+// fixed order, then a fixed xor-butterfly reduction. Deterministic; parity with the reference is
+// by tolerance.
 template <int WT>
 __global__ __launch_bounds__(THREADS) void k_matvec_float(const uint8_t *__restrict__ w, int n_in, const float *__restrict__ x,
                                                           int n_tok, float *out, long out_stride, const float *bias,
@@ -908,7 +909,41 @@ __global__ __launch_bounds__(THREADS) void k_matvec_float(const uint8_t *__restr
         const uint8_t *wr = w + (size_t)row * n_in * (WT == SDY_F32 ? 4 : 2);
         const float *xr = x + (size_t)t * n_in;
         float acc = 0.0f;
-        for (int e = lane; e < n_in; e += 64) acc = fmaf(welem<WT>(wr, e), xr[e], acc);
+        if ((n_in & 3) == 0) {
+            // lane l takes elements 256c + 4l .. 256c + 4l + 3 of chunk c (one 16-byte f32 or 8-byte
+            // f16/bf16 load); 8 chunks' loads go out before their multiply-adds
+            const int n_chunk = (n_in + 255) / 256;
+            for (int c0 = 0; c0 < n_chunk; c0 += 8) {
+                float4 wv[8], xv[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    int e = 256 * (c0 + j) + 4 * lane;
+                    e = e < n_in ? e : 0;
+                    xv[j] = *reinterpret_cast<const float4 *>(xr + e);
+                    if constexpr (WT == SDY_F32) {
+                        wv[j] = *reinterpret_cast<const float4 *>(wr + 4 * (size_t)e);
+                    } else {
+                        const uint2 h = *reinterpret_cast<const uint2 *>(wr + 2 * (size_t)e);
+                        const uint16_t hv[4] = {(uint16_t)(h.x & 0xFFFFu), (uint16_t)(h.x >> 16),
+                                                (uint16_t)(h.y & 0xFFFFu), (uint16_t)(h.y >> 16)};
+                        wv[j] = make_float4(welem<WT>(reinterpret_cast<const uint8_t *>(hv), 0),
+                                            welem<WT>(reinterpret_cast<const uint8_t *>(hv), 1),
+                                            welem<WT>(reinterpret_cast<const uint8_t *>(hv), 2),
+                                            welem<WT>(reinterpret_cast<const uint8_t *>(hv), 3));
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    if (256 * (c0 + j) + 4 * lane < n_in) {
+                        acc = fmaf(wv[j].x, xv[j].x, acc);
+                        acc = fmaf(wv[j].y, xv[j].y, acc);
+                        acc = fmaf(wv[j].z, xv[j].z, acc);
+                        acc = fmaf(wv[j].w, xv[j].w, acc);
+                    }
+            }
+        } else {
+            for (int e = lane; e < n_in; e += 64) acc = fmaf(welem<WT>(wr, e), xr[e], acc);
+        }
         for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off);
         if (lane == 0) {
             if (bias) acc = acc + bias[row];

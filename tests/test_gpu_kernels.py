@@ -179,7 +179,7 @@ def test_matvec_device_api_deterministic():
 
 @pytest.mark.parametrize("wtype", [O.F32, O.F16, O.BF16], ids=["f32", "f16", "bf16"])
 @pytest.mark.parametrize("n_tok", [1, 3, 4, 9])
-@pytest.mark.parametrize("n_in", [67, 96])
+@pytest.mark.parametrize("n_in", [67, 96, 2048, 2340])
 def test_float_matmul(wtype, n_tok, n_in):
     rng = np.random.default_rng(0)
     n_out = 45
@@ -197,7 +197,12 @@ def test_float_matmul(wtype, n_tok, n_in):
     w = np.ascontiguousarray(w)
     out = np.empty((n_tok, n_out), np.float32)
     lib().op_matmul(ptr(out), ptr(x), ptr(w), wtype, n_tok, n_in, n_out)
-    np.testing.assert_allclose(out, x @ w_ref.T, rtol=1e-5, atol=1e-5)
+    exact = x.astype(np.float64) @ w_ref.T.astype(np.float64)
+    if n_in <= 96:  # the reference's own sizes and tolerance (tests/test_runtime.py:100-152)
+        np.testing.assert_allclose(out, x @ w_ref.T, rtol=1e-5, atol=1e-5)
+    else:  # long rows: the f32 error bound of n_in / 64 chained FMAs per lane and a 6-level tree
+        bound = (n_in / 64 + 8) * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(w_ref).T)
+        assert np.all(np.abs(out - exact) <= bound)
     parts = np.full_like(out, np.nan)
     for r0, r1 in [(0, 10), (10, 30), (30, n_out)]:
         lib().op_matmul_rows(ptr(parts), ptr(x), ptr(w), wtype, n_tok, n_in, n_out, r0, r1)
@@ -410,6 +415,46 @@ def test_grouped_matvec_rejects_bad_shapes():
     assert L.sdy_matvec_grouped(ctypes.byref(m.m), ctypes.byref(a), top.ptr, 2, 10, 0, 10, None) != 0
     a.row1, a.n_tok = 10, 2
     assert L.sdy_matvec_grouped(ctypes.byref(m.m), ctypes.byref(a), top.ptr, 2, 10, 0, 10, None) != 0
+
+
+@pytest.mark.parametrize("n_expert,k", [(128, 8), (60, 4), (256, 16), (512, 64), (8, 3)])
+def test_moe_route_and_combine(n_expert, k):
+    """Router softmax + top-k (ties to the lowest expert) and the weighted sum of the chosen experts'
+    outputs in ascending expert order, against the oracle's softmax, a stable sort and the oracle's
+    AVX2 axpy (fused in 8-lane steps, rounded product and sum in the tail: dim 2050)."""
+    L = lib()
+    n_tok, dim = 5, 2050
+    rng = np.random.default_rng(n_expert + k)
+    logits = (rng.standard_normal((n_tok, n_expert)) * 2).astype(np.float32)
+    logits[1, 1:min(n_expert, 40):3] = logits[1, 0]  # exact ties
+    logits[2, :] = 0.5                               # all equal: experts 0 .. k-1
+    dl = capi.DeviceBuffer.from_array(logits)
+    dtop, dw = capi.DeviceBuffer(n_tok * k * 4), capi.DeviceBuffer(n_tok * k * 4)
+    capi.check(L.sdy_moe_route(dl.ptr, n_tok, n_expert, k, dtop.ptr, dw.ptr, None))
+    top, w = dtop.to_array(np.int32, (n_tok, k)), dw.to_array(np.float32, (n_tok, k))
+    for t in range(n_tok):
+        p = logits[t].copy()
+        O.lib().orc_softmax(ptr(p), n_expert)
+        et = np.argsort(-p, kind="stable")[:k]
+        assert top[t].tolist() == et.tolist(), t
+        s = np.float32(0)
+        for e in et:
+            s = np.float32(s + p[e])
+        np.testing.assert_allclose(w[t], p[et] / s, rtol=2e-6)
+    if k > 16:
+        return
+    y = rng.standard_normal((n_tok, k, dim)).astype(np.float32)
+    resid = rng.standard_normal((n_tok, dim)).astype(np.float32)
+    dy, dr = capi.DeviceBuffer.from_array(y), capi.DeviceBuffer.from_array(resid)
+    dout = capi.DeviceBuffer(n_tok * dim * 4)
+    capi.check(L.sdy_moe_combine(dy.ptr, dtop.ptr, dw.ptr, n_tok, k, dim, dout.ptr, dr.ptr, None))
+    got = dout.to_array(np.float32, (n_tok, dim))
+    for t in range(n_tok):
+        acc = np.zeros(dim, np.float32)
+        for i in np.argsort(top[t]):
+            yi = np.ascontiguousarray(y[t, i])
+            O.lib().orc_axpy(ptr(acc), float(w[t, i]), ptr(yi), dim, 1)
+        assert np.array_equal(bits(got[t]), bits(resid[t] + acc)), t
 
 
 def _gemm_case(kind, n_in, n_out, n_tok, seed, gen="workload"):
