@@ -2,8 +2,9 @@
 into build/libsardyne.so. Run as ``python -m sardyne_amd.build``.
 
 HIP flags: contraction off and f16/f32 denormals kept (the dequantisation and the f32 combines
-must round exactly like the reference), correctly rounded f32 division/sqrt, and packed-FP32
-instructions disabled.
+must round exactly like the reference), correctly rounded f32 division/sqrt, packed-FP32
+instructions disabled, and MFMA results in ordinary VGPRs (the GEMM combines them with VALU
+instructions, which would otherwise first copy them out of the accumulation registers).
 """
 from __future__ import annotations
 
@@ -24,7 +25,7 @@ OBJ_DIR = OUT_DIR / "obj"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
              "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-gpu-flush-denormals-to-zero",
-             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form", "-Wall",
              f"-I{INCLUDE}", f"-I{CSRC}"]
 C_FLAGS = ["-std=c11", "-O2", "-fPIC", "-ffp-contract=off", "-Wall", "-Wextra", f"-I{INCLUDE}", f"-I{CSRC}",
            "-I/opt/rocm/include"]

@@ -16,6 +16,8 @@
 // Tiling: a wave owns 32 rows x 32*NT tokens (NT MFMA tiles sharing its dequantised weight
 // fragments); a workgroup is 4 waves on 4 consecutive row tiles, so they read the same activation
 // fragments (L1 hits). The activations are expanded once per call to f16 (k_gemm_prep).
+#include <stdlib.h>
+
 #include "sdy_device.h"
 #include "sdy_internal.h"
 #include "sdy_quant_dev.h"
@@ -31,6 +33,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 struct GemmArgs {
     const uint8_t *p[5];  // weight planes (quant_kernels.hip layout)
+    uint32_t psz[5];      // their sizes in bytes (bounds of the buffer resources)
     int n_in, T, nb;      // elements, 64-element units and super-blocks per row
     long row0, n_rows;    // rows row0 .. row0 + n_rows of the planes
     int n_tok;
@@ -51,6 +54,21 @@ SDY_DEV uint32_t magic_lo(uint32_t v) { return __builtin_amdgcn_perm(0x64646464u
 SDY_DEV uint32_t magic_hi(uint32_t v) { return __builtin_amdgcn_perm(0x64646464u, v, 0x05030402u); }
 
 SDY_DEV half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
+
+// 8 Q4_K quants q (one per byte of n.x, n.y) times sc as f16 with one fused multiply-add per
+// pair: (1024 + q) * sc - 1024 * sc. The exact result q * sc <= 945 is representable, so the single
+// rounding of the fma is exact (1024 * sc <= 64512 is exact too).
+SDY_DEV half8 frag_q4(u32x2 n, half2v sc2, half2v nsc2) {
+    half8 r;
+    const uint32_t w[4] = {magic_lo(n.x), magic_hi(n.x), magic_lo(n.y), magic_hi(n.y)};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const half2v t = __builtin_elementwise_fma(as_h2(w[i]), sc2, nsc2);
+        r[2 * i] = t[0];
+        r[2 * i + 1] = t[1];
+    }
+    return r;
+}
 SDY_DEV uint32_t as_u(half2v v) { return __builtin_bit_cast(uint32_t, v); }
 
 // 8 small unsigned integers (one per byte of n.x, n.y) times sc as f16: ((1024 + q) - 1024) * sc,
@@ -211,6 +229,539 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     }
 }
 
+// The weights of one super-block for one lane: its A row's quants for k-half h of the 4 units, the
+// scale record (Q4_K: d, dmin and the 12 packed scale/min bytes; Q6_K: the 16 int8 scales) and
+// the Q6_K d.
+struct SbRegs {
+    u32x2 q[4][3];
+    u32x4 hd;
+    uint32_t d6;
+};
+
+template <int WT>
+SDY_DEV void load_sb(const GemmArgs &g, long row, int sb, int h, SbRegs &r) {
+#pragma unroll
+    for (int un = 0; un < 4; un++) load_unit<WT>(g, row, 4 * sb + un, h, r.q[un]);
+    if constexpr (WT == SDY_Q4_K) {
+        r.hd = *reinterpret_cast<const u32x4 *>(g.p[2] + ((size_t)row * g.nb + sb) * 16);
+        r.d6 = 0;
+    } else {
+        r.hd = *reinterpret_cast<const u32x4 *>(g.p[3] + ((size_t)row * g.nb + sb) * 16);
+        r.d6 = *reinterpret_cast<const uint16_t *>(g.p[4] + ((size_t)row * g.nb + sb) * 2);
+    }
+}
+
+// LDS-staged GEMM. A workgroup of WM waves covers 32*MT*WM rows x 32*NT tokens; every wave owns
+// 32*MT rows (MT MFMA row tiles, dequantised in its registers from its own global loads) and all
+// the workgroup's tokens. The f16 activations of a super-block (32*NT tokens x 256 values) are
+// staged once per workgroup in LDS (rows padded to 528 bytes: the 16-byte fragment reads of 8
+// consecutive lanes fall in distinct banks), double-buffered: the loads of super-block s + 1
+// (activations into registers, then LDS; weights into registers) are in flight while s is
+// multiplied. One barrier per super-block. Integer sums and the f32 combine as in k_gemm.
+template <int WT, int MT, int NT, int WM>
+__global__ __launch_bounds__(64 * WM) void k_gemm2(GemmArgs g) {
+    constexpr int BN = 32 * NT, NTH = 64 * WM, ROWB = 528;
+    constexpr int BUF = BN * ROWB + BN * 4 + BN * 32;  // f16 rows, yd, 16 f16 bsums per token
+    constexpr int NCH = BN * 32 / NTH;                  // 16-byte activation chunks per thread
+    static_assert(BN <= NTH && (BN * 32) % NTH == 0, "tile");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, lr = lane & 31;
+    // Workgroups are dealt round-robin to the 8 XCDs in launch order. Renumber them so that the
+    // token tiles of a row tile run on one XCD at about the same time: its weights then come from
+    // HBM once into that XCD's L2 instead of once per token tile.
+    const int n_tt = gridDim.x;
+    const long n_rt = gridDim.y, L = (long)blockIdx.y * n_tt + blockIdx.x;
+    long rti, tti;
+    {
+        const long grp = 8L * n_tt;                     // 8 row tiles x all token tiles
+        const long full = n_rt / 8 * grp;               // workgroups in complete groups
+        if (L < full) {
+            const long gq = L / grp, w = L - gq * grp;  // w % 8: the XCD
+            rti = gq * 8 + (w & 7);
+            tti = w >> 3;
+        } else {                                        // the last, partial group: row-major
+            const long w = L - full;
+            rti = n_rt / 8 * 8 + w / n_tt;
+            tti = w - (w / n_tt) * n_tt;
+        }
+    }
+    const long rt = rti * (32 * MT * WM) + 32 * MT * wave;  // first row of the wave
+    const int t0 = (int)tti * BN;
+    long ra[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const long ri = rt + 32 * mt + lr;
+        ra[mt] = g.row0 + (ri < g.n_rows ? ri : g.n_rows - 1);
+    }
+    const int nb = g.nb;
+    auto tok_of = [&](int t) { return t0 + t < g.n_tok ? t0 + t : g.n_tok - 1; };
+    u32x4 bv[NCH];
+    float ydv = 0.0f;
+    u32x4 bs0 = {0u, 0u, 0u, 0u}, bs1 = {0u, 0u, 0u, 0u};
+    auto load_b = [&](int sb) {
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int q = tid + j * NTH;
+            bv[j] = *reinterpret_cast<const u32x4 *>(g.y16 + (size_t)tok_of(q >> 5) * g.n_in + 256 * sb + 8 * (q & 31));
+        }
+        if (tid < BN) {
+            const size_t tb = (size_t)tok_of(tid) * nb + sb;
+            ydv = g.yd[tb];
+            if constexpr (WT == SDY_Q4_K) {
+                bs0 = *reinterpret_cast<const u32x4 *>(g.bs16 + tb * 16);
+                bs1 = *reinterpret_cast<const u32x4 *>(g.bs16 + tb * 16 + 8);
+            }
+        }
+    };
+    auto store_b = [&](int buf) {
+        uint8_t *base = lds + buf * BUF;
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int q = tid + j * NTH;
+            *reinterpret_cast<u32x4 *>(base + (q >> 5) * ROWB + 16 * (q & 31)) = bv[j];
+        }
+        if (tid < BN) {
+            *reinterpret_cast<float *>(base + BN * ROWB + 4 * tid) = ydv;
+            if constexpr (WT == SDY_Q4_K) {
+                *reinterpret_cast<u32x4 *>(base + BN * ROWB + BN * 4 + 32 * tid) = bs0;
+                *reinterpret_cast<u32x4 *>(base + BN * ROWB + BN * 4 + 32 * tid + 16) = bs1;
+            }
+        }
+    };
+
+    float16v acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[mt][nt] = float16v{};
+    const half2v off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const half2v off6 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+
+    // weights two super-blocks ahead (A: current, An: next, Ann: requested in this iteration);
+    // activations one ahead (registers, then the other LDS buffer)
+    SbRegs A[MT], An[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        load_sb<WT>(g, ra[mt], 0, h, A[mt]);
+        load_sb<WT>(g, ra[mt], nb > 1 ? 1 : 0, h, An[mt]);
+    }
+    load_b(0);
+    store_b(0);
+    __syncthreads();
+
+    for (int sb = 0; sb < nb; sb++) {
+        const int cur = sb & 1;
+        const int nx = sb + 1 < nb ? sb + 1 : sb;   // the last iterations reload their own super-block
+        const int nx2 = sb + 2 < nb ? sb + 2 : nb - 1;
+        SbRegs Ann[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) load_sb<WT>(g, ra[mt], nx2, h, Ann[mt]);
+        load_b(nx);
+
+        const uint8_t *bbuf = lds + cur * BUF;
+        float16v isum[MT][NT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) isum[mt][nt] = float16v{};
+#pragma unroll
+        for (int un = 0; un < 4; un++) {
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                half8 a[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    if constexpr (WT == SDY_Q4_K) {
+                        // s: 0 QA low, 1 QB low (sub-block 2un), 2 QA high, 3 QB high (sub-block 2un + 1)
+                        const uint32_t Aw = A[mt].hd.y, Cw = A[mt].hd.w;
+                        const int j = 2 * un + (s >> 1);
+                        const int sc = j < 4 ? (int)((Aw >> (8 * j)) & 63)
+                                             : (int)(((Cw >> (8 * (j - 4))) & 15) | (((Aw >> (8 * (j - 4) + 6)) & 3) << 4));
+                        const u32x2 src = (s & 1) ? A[mt].q[un][1] : A[mt].q[un][0];
+                        const u32x2 nib = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
+                        const _Float16 f = (_Float16)(float)sc;
+                        a[mt] = frag_scaled(nib, off, half2v{f, f});
+                    } else {
+                        const int j = 4 * un + s;
+                        const int sc = (int)(int8_t)((A[mt].hd[j >> 2] >> (8 * (j & 3))) & 255u);
+                        const u32x2 src = (s & 1) ? A[mt].q[un][1] : A[mt].q[un][0];
+                        const u32x2 lo = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
+                        const u32x2 hi = ((A[mt].q[un][2] >> (unsigned)(2 * s)) & 0x03030303u) << 4u;
+                        const _Float16 f = (_Float16)(float)sc;
+                        a[mt] = frag_scaled(lo | hi, off6, half2v{f, f});
+                    }
+                }
+                const int koff = 2 * (64 * un + 16 * s + 8 * h);
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    const half8 b = *reinterpret_cast<const half8 *>(bbuf + (32 * nt + lr) * ROWB + koff);
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++)
+                        isum[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt], b, isum[mt][nt], 0, 0, 0);
+                }
+            }
+        }
+        // combine in the reference's order: acc + (yd*d*isum - yd*dmin*msum)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            float16v msum[NT];
+            if constexpr (WT == SDY_Q4_K) {
+                const uint32_t Aw = A[mt].hd.y, Bw = A[mt].hd.z, Cw = A[mt].hd.w;
+                half8 a2;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int j = 4 * h + (e >> 1);  // sub-block of 16-group 8h + e
+                    const int m = j < 4 ? (int)((Bw >> (8 * j)) & 63)
+                                        : (int)(((Cw >> (8 * (j - 4) + 4)) & 15) | (((Bw >> (8 * (j - 4) + 6)) & 3) << 4));
+                    a2[e] = (_Float16)(float)m;
+                }
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    const half8 b2 = *reinterpret_cast<const half8 *>(bbuf + BN * ROWB + BN * 4 + 32 * (32 * nt + lr) + 16 * h);
+                    msum[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b2, float16v{}, 0, 0, 0);
+                }
+            }
+            const uint32_t dpair = WT == SDY_Q4_K ? A[mt].hd.x : A[mt].d6;
+            float ydn[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) ydn[nt] = *reinterpret_cast<const float *>(bbuf + BN * ROWB + 4 * (32 * nt + lr));
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                // D row 8(r/4) + 4h + r%4 of the tile is the A row of lane 8(r/4) + 4h + r%4
+                const uint32_t dd = (uint32_t)__shfl((int)dpair, 8 * (r >> 2) + 4 * h + (r & 3));
+                const float d = sdy_h2f((uint16_t)(dd & 0xFFFFu));
+                const float dmin = WT == SDY_Q4_K ? sdy_h2f((uint16_t)(dd >> 16)) : 0.0f;
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    if constexpr (WT == SDY_Q4_K) {
+                        const float dall = ydn[nt] * d, dmn = ydn[nt] * dmin;
+                        const float t1 = dall * isum[mt][nt][r], t2 = dmn * msum[nt][r];
+                        acc[mt][nt][r] = acc[mt][nt][r] + (t1 - t2);
+                    } else {
+                        const float ydd = ydn[nt] * d;
+                        acc[mt][nt][r] = acc[mt][nt][r] + ydd * isum[mt][nt][r];
+                    }
+                }
+            }
+        }
+        store_b(cur ^ 1);
+        __syncthreads();
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            A[mt] = An[mt];
+            An[mt] = Ann[mt];
+        }
+    }
+    // store (bias, residual, or the SwiGLU pair of rows 2i, 2i+1 held by this lane)
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int tok = t0 + 32 * nt + lr;
+            if (tok >= g.n_tok) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const long ri = rt + 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (ri >= g.n_rows) continue;
+                const long row = g.row0 + ri;
+                if (g.swiglu) {
+                    if ((r & 1) == 0)
+                        g.out[(size_t)tok * g.out_stride + (ri >> 1)] = sdy_silu_mul1(acc[mt][nt][r], acc[mt][nt][r + 1]);
+                } else {
+                    float v = acc[mt][nt][r];
+                    if (g.bias) v = v + g.bias[row];
+                    if (g.resid) v = g.resid[(size_t)tok * g.out_stride + row] + v;
+                    g.out[(size_t)tok * g.out_stride + row] = v;
+                }
+            }
+        }
+}
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+SDY_DEV uint32_t lds_addr(const float *p) {
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) float *)p;
+}
+
+// Four 16-byte LDS reads at a, a + 32, a + 64, a + 96 and four at b, b + 32, ... as one asm block
+// that waits for them itself. The compiler then does not see LDS loads here: it would otherwise
+// make them wait for every activation DMA in flight (it cannot tell that they do not alias).
+SDY_DEV void lds_read8(uint32_t a, uint32_t b, f32x4 &a0, f32x4 &a1, f32x4 &a2, f32x4 &a3, f32x4 &b0, f32x4 &b1,
+                       f32x4 &b2, f32x4 &b3) {
+    __asm__ volatile(
+        "ds_read_b128 %0, %8\n"
+        "ds_read_b128 %1, %8 offset:32\n"
+        "ds_read_b128 %2, %8 offset:64\n"
+        "ds_read_b128 %3, %8 offset:96\n"
+        "ds_read_b128 %4, %9\n"
+        "ds_read_b128 %5, %9 offset:32\n"
+        "ds_read_b128 %6, %9 offset:64\n"
+        "ds_read_b128 %7, %9 offset:96\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(a0), "=&v"(a1), "=&v"(a2), "=&v"(a3), "=&v"(b0), "=&v"(b1), "=&v"(b2), "=&v"(b3)
+        : "v"(a), "v"(b)
+        : "memory");
+}
+
+SDY_DEV __amdgpu_buffer_rsrc_t plane_rsrc(const uint8_t *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)bytes, 0x00020000);
+}
+
+// The MFMA GEMM with the activations staged by LDS DMA. A workgroup of WM waves covers 32*MT*WM
+// rows x 32*NT tokens; each wave owns 32*MT rows (MT MFMA row tiles, dequantised in registers
+// from buffer loads whose per-super-block advance is a scalar offset) and shares the staged
+// activations of all the workgroup's tokens. Per super-block and stage the activations are
+// copied global -> LDS with global_load_lds (no registers): LDS chunk p (16 bytes) holds token
+// p / 32, chunk (p % 32) ^ (token % 8), so that the fragment reads of 8 consecutive lanes hit
+// distinct banks. Two stages: super-block s + 1 is in flight while s is multiplied; one
+// s_waitcnt + barrier per super-block. The per-row d (and dmin) are converted once per row into a
+// per-wave LDS table. Integer sums and the f32 combine as in k_gemm.
+template <int WT, int MT, int NT, int WM>
+__global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
+    constexpr int BN = 32 * NT, NTH = 64 * WM;
+    constexpr int YDN = BN < 64 ? 64 : BN;                  // yd slots (one DMA dword per lane)
+    constexpr int YDOFF = BN * 512, BSOFF = YDOFF + YDN * 4;
+    constexpr int BUF = BSOFF + BN * 32;                    // bytes of one stage
+    constexpr int NI = BN * 32 / NTH;                       // activation DMA chunks per lane per stage
+    static_assert((BN * 32) % NTH == 0 && NI >= 1, "tile");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, lr = lane & 31;
+    // token tiles of a row tile on one XCD (workgroups are dealt round-robin to the 8 XCDs)
+    const int n_tt = gridDim.x;
+    const long n_rt = gridDim.y, L = (long)blockIdx.y * n_tt + blockIdx.x;
+    long rti, tti;
+    {
+        const long grp = 8L * n_tt, full = n_rt / 8 * grp;
+        if (L < full) {
+            const long gq = L / grp, w = L - gq * grp;
+            rti = gq * 8 + (w & 7);
+            tti = w >> 3;
+        } else {
+            const long w = L - full;
+            rti = n_rt / 8 * 8 + w / n_tt;
+            tti = w - (w / n_tt) * n_tt;
+        }
+    }
+    const long rt = rti * (32 * MT * WM) + 32 * MT * wave;
+    const int t0 = (int)tti * BN;
+    const int nb = g.nb;
+    auto tok_of = [&](int t) { return t0 + t < g.n_tok ? t0 + t : g.n_tok - 1; };
+
+    // weight buffer resources and this lane's per-row offsets
+    __amdgpu_buffer_rsrc_t rq[3], rh, rd;
+#pragma unroll
+    for (int i = 0; i < 3; i++) rq[i] = plane_rsrc(g.p[i], g.psz[i]);
+    rh = plane_rsrc(g.p[WT == SDY_Q4_K ? 2 : 3], g.psz[WT == SDY_Q4_K ? 2 : 3]);
+    rd = plane_rsrc(g.p[4], g.psz[4]);
+    uint32_t oq[MT], oh[MT], od[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const long ri = rt + 32 * mt + lr;
+        const uint32_t row = (uint32_t)(g.row0 + (ri < g.n_rows ? ri : g.n_rows - 1));
+        oq[mt] = row * (uint32_t)g.T * 16u + 8u * (uint32_t)h;
+        oh[mt] = row * (uint32_t)nb * 16u;
+        od[mt] = row * (uint32_t)nb * 2u;
+    }
+    auto load_sb3 = [&](int sb, SbRegs (&R)[MT]) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+            for (int un = 0; un < 4; un++) {
+                const int so = (4 * sb + un) * 16;
+                R[mt].q[un][0] = __builtin_amdgcn_raw_buffer_load_b64(rq[0], oq[mt], so, 0);
+                R[mt].q[un][1] = __builtin_amdgcn_raw_buffer_load_b64(rq[1], oq[mt], so, 0);
+                if constexpr (WT == SDY_Q6_K) R[mt].q[un][2] = __builtin_amdgcn_raw_buffer_load_b64(rq[2], oq[mt], so, 0);
+            }
+            R[mt].hd = __builtin_amdgcn_raw_buffer_load_b128(rh, oh[mt], sb * 16, 0);
+            R[mt].d6 = WT == SDY_Q6_K ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rd, od[mt], sb * 2, 0) : 0u;
+        }
+    };
+    // activation stage of super-block sb into buffer buf (asynchronous; completes at s_waitcnt)
+    auto stage = [&](int sb, int buf) {
+        uint8_t *base = lds + buf * BUF;
+#pragma unroll
+        for (int j = 0; j < NI; j++) {
+            const int blk = j * WM + wave;  // 64-chunk block written by this wave instruction
+            const int p = blk * 64 + lane, t = p >> 5, c = (p & 31) ^ (t & 7);
+            __builtin_amdgcn_global_load_lds((const void *)(g.y16 + (size_t)tok_of(t) * g.n_in + 256 * sb + 8 * c),
+                                             (lds_ptr_t)(base + blk * 1024), 16, 0, 0);
+        }
+        if (wave == 0) {
+#pragma unroll
+            for (int i = 0; i < YDN / 64; i++)
+                __builtin_amdgcn_global_load_lds((const void *)(g.yd + (size_t)tok_of(64 * i + lane) * nb + sb),
+                                                 (lds_ptr_t)(base + YDOFF + 256 * i), 4, 0, 0);
+        }
+        if constexpr (WT == SDY_Q4_K) {
+            if (wave == (WM > 1 ? 1 : 0)) {
+#pragma unroll
+                for (int i = 0; i < BN / 32; i++)
+                    __builtin_amdgcn_global_load_lds(
+                        (const void *)(g.bs16 + ((size_t)tok_of(32 * i + (lane >> 1)) * nb + sb) * 16 + 8 * (lane & 1)),
+                        (lds_ptr_t)(base + BSOFF + 1024 * i), 16, 0, 0);
+            }
+        }
+    };
+    // the barrier's release fence waits for every load of the wave, the DMA of the stage included
+    auto wait_stage = [&]() { __syncthreads(); };
+
+    float16v acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[mt][nt] = float16v{};
+    const half2v off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const half2v off6 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+    // per-wave d[32 MT] then dmin[32 MT] as f32 (static LDS: a separate object from the DMA target,
+    // so its reads need not wait for the activation loads in flight)
+    __shared__ __align__(16) float dtab_all[WM * 64 * MT];
+    float *dtab = dtab_all + wave * (64 * MT);
+
+    SbRegs A[MT];
+    load_sb3(0, A);
+    stage(0, 0);
+    wait_stage();
+
+    for (int sb = 0; sb < nb; sb++) {
+        const int cur = sb & 1;
+        SbRegs An[MT];
+        load_sb3(sb + 1 < nb ? sb + 1 : sb, An);
+        if (sb + 1 < nb) stage(sb + 1, cur ^ 1);
+        // d (and dmin) of the wave's rows as f32
+        if (h == 0) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const uint32_t dp = WT == SDY_Q4_K ? A[mt].hd.x : A[mt].d6;
+                dtab[32 * mt + lr] = sdy_h2f((uint16_t)(dp & 0xFFFFu));
+                if constexpr (WT == SDY_Q4_K) dtab[32 * MT + 32 * mt + lr] = sdy_h2f((uint16_t)(dp >> 16));
+            }
+        }
+        const uint8_t *bbuf = lds + cur * BUF;
+        float16v isum[MT][NT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) isum[mt][nt] = float16v{};
+#pragma unroll
+        for (int un = 0; un < 4; un++) {
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                half8 a[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    if constexpr (WT == SDY_Q4_K) {
+                        const uint32_t Aw = A[mt].hd.y, Cw = A[mt].hd.w;
+                        const int j = 2 * un + (s >> 1);
+                        const int sc = j < 4 ? (int)((Aw >> (8 * j)) & 63)
+                                             : (int)(((Cw >> (8 * (j - 4))) & 15) | (((Aw >> (8 * (j - 4) + 6)) & 3) << 4));
+                        const u32x2 src = (s & 1) ? A[mt].q[un][1] : A[mt].q[un][0];
+                        const u32x2 nib = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
+                        const _Float16 f = (_Float16)(float)sc, nf = (_Float16)(float)(-1024 * sc);
+                        a[mt] = frag_q4(nib, half2v{f, f}, half2v{nf, nf});
+                    } else {
+                        const int j = 4 * un + s;
+                        const int sc = (int)(int8_t)((A[mt].hd[j >> 2] >> (8 * (j & 3))) & 255u);
+                        const u32x2 src = (s & 1) ? A[mt].q[un][1] : A[mt].q[un][0];
+                        const u32x2 lo = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
+                        const u32x2 hi = ((A[mt].q[un][2] >> (unsigned)(2 * s)) & 0x03030303u) << 4u;
+                        const _Float16 f = (_Float16)(float)sc;
+                        a[mt] = frag_scaled(lo | hi, off6, half2v{f, f});
+                    }
+                }
+                const int c = 8 * un + 2 * s + h;
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    const int t = 32 * nt + lr;
+                    const half8 b = *reinterpret_cast<const half8 *>(bbuf + 16 * (t * 32 + (c ^ (t & 7))));
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++)
+                        isum[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt], b, isum[mt][nt], 0, 0, 0);
+                }
+            }
+        }
+        // combine in the reference's order: acc + (yd*d*isum - yd*dmin*msum)
+        float ydn[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) ydn[nt] = *reinterpret_cast<const float *>(bbuf + YDOFF + 4 * (32 * nt + lr));
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            float16v msum[NT];
+            if constexpr (WT == SDY_Q4_K) {
+                const uint32_t Bw = A[mt].hd.z, Cw = A[mt].hd.w;
+                half8 a2;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int j = 4 * h + (e >> 1);  // sub-block of 16-group 8h + e
+                    const int m = j < 4 ? (int)((Bw >> (8 * j)) & 63)
+                                        : (int)(((Cw >> (8 * (j - 4) + 4)) & 15) | (((Bw >> (8 * (j - 4) + 6)) & 3) << 4));
+                    a2[e] = (_Float16)(float)m;
+                }
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    const half8 b2 = *reinterpret_cast<const half8 *>(bbuf + BSOFF + 32 * (32 * nt + lr) + 16 * h);
+                    msum[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b2, float16v{}, 0, 0, 0);
+                }
+            }
+            // rows 8q + 4h .. 8q + 4h + 3 of the tile (D registers 4q .. 4q + 3): d, then dmin
+            float dv[16], dm[16];
+            {
+                const uint32_t da = lds_addr(dtab + 32 * mt + 4 * h);
+                f32x4 d0, d1, d2, d3, m0, m1, m2, m3;
+                lds_read8(da, da + 4 * 32 * MT, d0, d1, d2, d3, m0, m1, m2, m3);
+                const f32x4 dq[4] = {d0, d1, d2, d3}, mq[4] = {m0, m1, m2, m3};
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        dv[4 * q + i] = dq[q][i];
+                        dm[4 * q + i] = WT == SDY_Q4_K ? mq[q][i] : 0.0f;
+                    }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    if constexpr (WT == SDY_Q4_K) {
+                        const float dall = ydn[nt] * dv[r], dmn = ydn[nt] * dm[r];
+                        const float t1 = dall * isum[mt][nt][r], t2 = dmn * msum[nt][r];
+                        acc[mt][nt][r] = acc[mt][nt][r] + (t1 - t2);
+                    } else {
+                        const float ydd = ydn[nt] * dv[r];
+                        acc[mt][nt][r] = acc[mt][nt][r] + ydd * isum[mt][nt][r];
+                    }
+                }
+            }
+        }
+        wait_stage();
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) A[mt] = An[mt];
+    }
+    // store (bias, residual, or the SwiGLU pair of rows 2i, 2i+1 held by this lane)
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int tok = t0 + 32 * nt + lr;
+            if (tok >= g.n_tok) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const long ri = rt + 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (ri >= g.n_rows) continue;
+                const long row = g.row0 + ri;
+                if (g.swiglu) {
+                    if ((r & 1) == 0)
+                        g.out[(size_t)tok * g.out_stride + (ri >> 1)] = sdy_silu_mul1(acc[mt][nt][r], acc[mt][nt][r + 1]);
+                } else {
+                    float v = acc[mt][nt][r];
+                    if (g.bias) v = v + g.bias[row];
+                    if (g.resid) v = g.resid[(size_t)tok * g.out_stride + row] + v;
+                    g.out[(size_t)tok * g.out_stride + row] = v;
+                }
+            }
+        }
+}
+
 // Q8_K rows -> f16 values, f32 scales and f16 bsums for the GEMM. Grid (nb, n_tok), 64 threads.
 __global__ __launch_bounds__(64) void k_gemm_prep(const uint8_t *__restrict__ xq, int nb, _Float16 *__restrict__ y16,
                                                   float *__restrict__ yd, _Float16 *__restrict__ bs16) {
@@ -274,6 +825,10 @@ static GemmArgs gemm_args(const sdy_mat *m) {
     g.T = m->n_units;
     g.nb = m->n_in / 256;
     g.n_rows = m->n_rows;
+    const size_t rows = (size_t)m->n_rows, unit = rows * g.T * 16, sbk = rows * g.nb;
+    const size_t sz[5] = {unit, unit, m->type == SDY_Q4_K ? sbk * 16 : unit, m->type == SDY_Q4_K ? 0 : sbk * 16,
+                          m->type == SDY_Q4_K ? 0 : sbk * 2};
+    for (int i = 0; i < 5; i++) g.psz[i] = sz[i] < 0xFFFFFFFFu ? (uint32_t)sz[i] : 0xFFFFFFFFu;
     return g;
 }
 
@@ -304,7 +859,9 @@ extern "C" size_t sdy_gemm_ws_bytes(int n_tok, int n_in) {
 }
 
 extern "C" int sdy_gemm_ok(const sdy_mat *m, int n_tok) {
-    return (m->type == SDY_Q4_K || m->type == SDY_Q6_K) && m->gemm_ok && n_tok >= 2;
+    // buffer resources address each plane with 32-bit offsets: planes below 4 GiB
+    return (m->type == SDY_Q4_K || m->type == SDY_Q6_K) && m->gemm_ok && n_tok >= 2 &&
+           (size_t)m->n_rows * m->n_units * 16 < 0xFFFFFFFFu;
 }
 
 template <int WT, int NT>
@@ -315,8 +872,57 @@ static int launch_gemm(GemmArgs &g, hipStream_t st) {
     return sdy_check_launch("gemm");
 }
 
+template <int WT, int MT, int NT, int WM>
+static int launch_gemm2(GemmArgs &g, hipStream_t st) {
+    constexpr int BN = 32 * NT, BM = 32 * MT * WM;
+    constexpr size_t lds = 2 * (size_t)(BN * 528 + BN * 4 + BN * 32);
+    static size_t granted = 0;
+    const void *fn = (const void *)k_gemm2<WT, MT, NT, WM>;
+    int rc = sdy_lds_limit(fn, lds, &granted);
+    if (rc) return rc;
+    const unsigned tok_tiles = (unsigned)((g.n_tok + BN - 1) / BN), row_tiles = (unsigned)((g.n_rows + BM - 1) / BM);
+    hipLaunchKernelGGL((k_gemm2<WT, MT, NT, WM>), dim3(tok_tiles, row_tiles), dim3(64 * WM), lds, st, g);
+    return sdy_check_launch("gemm");
+}
+
+template <int WT, int MT, int NT, int WM>
+static int launch_gemm3(GemmArgs &g, hipStream_t st) {
+    constexpr int BN = 32 * NT, BM = 32 * MT * WM, YDN = BN < 64 ? 64 : BN;
+    constexpr size_t lds = 2 * (size_t)(BN * 512 + YDN * 4 + BN * 32);
+    static size_t granted = 0;
+    const void *fn = (const void *)k_gemm3<WT, MT, NT, WM>;
+    int rc = sdy_lds_limit(fn, lds, &granted);
+    if (rc) return rc;
+    const unsigned tok_tiles = (unsigned)((g.n_tok + BN - 1) / BN), row_tiles = (unsigned)((g.n_rows + BM - 1) / BM);
+    hipLaunchKernelGGL((k_gemm3<WT, MT, NT, WM>), dim3(tok_tiles, row_tiles), dim3(64 * WM), lds, st, g);
+    return sdy_check_launch("gemm");
+}
+
 template <int WT>
 static int gemm_type(GemmArgs &g, hipStream_t st) {
+    // SARDYNE_GEMM_VARIANT picks one tile shape (tests and tuning); default: by shape
+    const char *ev = getenv("SARDYNE_GEMM_VARIANT");
+    const int variant = ev ? atoi(ev) : 1;
+    if (variant == 1) {
+        // 128-row workgroup tiles (4 waves of 32 rows); 64 tokens per tile when there are enough
+        // row tiles to fill the GPU twice over with them, else 32 (measured on the 2048- to
+        // 22016-row matrices of a 512-token prefill)
+        const long r128 = (g.n_rows + 127) / 128, t64 = (g.n_tok + 63) / 64;
+        if (r128 * t64 >= 1024) return launch_gemm3<WT, 1, 2, 4>(g, st);
+        return launch_gemm3<WT, 1, 1, 4>(g, st);
+    }
+    if (variant == 2) return launch_gemm2<WT, 2, 4, 4>(g, st);
+    if (variant == 3) return launch_gemm2<WT, 1, 4, 4>(g, st);
+    if (variant == 4) return launch_gemm2<WT, 1, 2, 4>(g, st);
+    if (variant == 5) return launch_gemm2<WT, 1, 2, 2>(g, st);
+    if (variant == 6) return launch_gemm2<WT, 2, 2, 4>(g, st);
+    if (variant == 11) return launch_gemm3<WT, 1, 4, 8>(g, st);
+    if (variant == 12) return launch_gemm3<WT, 1, 2, 4>(g, st);
+    if (variant == 13) return launch_gemm3<WT, 1, 2, 8>(g, st);
+    if (variant == 14) return launch_gemm3<WT, 1, 1, 4>(g, st);
+    if (variant == 15) return launch_gemm3<WT, 1, 4, 4>(g, st);
+    if (variant == 16) return launch_gemm3<WT, 2, 2, 4>(g, st);
+    // variant 0: the register-only kernel (activation fragments from global memory)
     // token tiles per wave: the largest of 4, 2, 1 that still gives a few waves per SIMD
     const long waves_at = [&](int nt) { return (g.n_rows + 31) / 32 * ((g.n_tok + 32 * nt - 1) / (32 * nt)); }(4);
     int n_cu = 256;

@@ -495,6 +495,19 @@ def test_gemm_bit_exact(kind, n_in, n_out, n_tok):
     assert np.array_equal(bits(got), bits(exp))
 
 
+@pytest.mark.parametrize("variant", ["0", "3", "4", "5", "6", "11", "12", "13", "14", "15", "16"])
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
+def test_gemm_tile_variants_bit_exact(kind, variant, monkeypatch):
+    """Every workgroup tile shape of the GEMM (forced through SARDYNE_GEMM_VARIANT) gives the
+    reference's bits, with partial row and token tiles."""
+    monkeypatch.setenv("SARDYNE_GEMM_VARIANT", variant)
+    for n_in, n_out, n_tok in [(2048, 300, 200), (768, 40, 17), (11008, 70, 130)]:
+        t, w, xq = _gemm_case(kind, n_in, n_out, n_tok, seed=n_in + n_out + n_tok + 1)
+        got = _gemm_run(t, w, xq, n_in, n_out, n_tok)
+        exp = O.matmul_q(w, t, xq, n_in, simd=1)
+        assert np.array_equal(bits(got), bits(exp)), (n_in, n_out, n_tok)
+
+
 @pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
 def test_gemm_bias_resid_rows_swiglu(kind):
     n_in, n_out, n_tok = 512, 96, 40
