@@ -1,10 +1,10 @@
 // gfx950 attention kernels (the reference's op_attention / attention_worker, csrc/ops.c:405-423 and
 // csrc/model_llama.c:619-640), over the f32 KV cache [n_kv_head][max_seq][head_dim] of a layer.
 //
-// Positions are cut into chunks of CH = 64. One workgroup handles one (chunk, KV head, token): it
-// stages the chunk's K and V in LDS with 16-byte loads, computes the scores of the n_rep query heads
-// that share the KV head, and writes per head the chunk maximum m, the sum l of exp(score - m) and
-// the exp-weighted sum o of V. A merge then combines the chunks of each (token, head) in chunk order:
+// Positions are cut into chunks of CH = 64. A workgroup stages a chunk's K and V in LDS with 16-byte
+// loads and, for each of its tokens, computes the scores of the n_rep query heads that share the KV
+// head and writes per head the chunk maximum m, the sum l of exp(score - m) and the exp-weighted
+// sum o of V. A merge then combines the chunks of each (token, head) in chunk order:
 // M = max m_c, e_c = exp(m_c - M), L = sum l_c e_c, out = (sum o_c e_c) / L. Every path (prefill,
 // the fused decode step, the host-pointer op_attention) uses these same functions, so they agree
 // bit for bit; the result differs from the reference's single softmax only by f32 rounding.
@@ -51,17 +51,29 @@ template <int NT>
 SDY_DEV void stage_kv(const ChunkLds &L, const float *kg, const float *vg, int np, int hd, int special,
                       const float *kspec, const float *vspec) {
     const int n4 = np * hd / 4, tid = threadIdx.x;
-    for (int i = tid; i < n4; i += NT) {
-        const int p = (4 * i) / hd, d = 4 * i - p * hd;
-        if (p == special) continue;
-        const float4 kv = reinterpret_cast<const float4 *>(kg)[i];
-        const float4 vv = reinterpret_cast<const float4 *>(vg)[i];
-        float *kr = L.ks + p * (hd + 1) + d;
-        kr[0] = kv.x;
-        kr[1] = kv.y;
-        kr[2] = kv.z;
-        kr[3] = kv.w;
-        *reinterpret_cast<float4 *>(L.vs + 4 * i) = vv;
+    // batches of 4 loads per thread go out before their LDS stores (clamped indices, no
+    // conditional load), so that their latencies overlap
+    for (int i0 = tid; i0 < n4; i0 += 4 * NT) {
+        float4 kv[4], vv[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = i0 + j * NT < n4 ? i0 + j * NT : i0;
+            kv[j] = reinterpret_cast<const float4 *>(kg)[i];
+            vv[j] = reinterpret_cast<const float4 *>(vg)[i];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = i0 + j * NT;
+            if (i >= n4) break;
+            const int p = (4 * i) / hd, d = 4 * i - p * hd;
+            if (p == special) continue;
+            float *kr = L.ks + p * (hd + 1) + d;
+            kr[0] = kv[j].x;
+            kr[1] = kv[j].y;
+            kr[2] = kv[j].z;
+            kr[3] = kv[j].w;
+            *reinterpret_cast<float4 *>(L.vs + 4 * i) = vv[j];
+        }
     }
     if (special >= 0 && special < np)
         for (int d = tid; d < hd; d += NT) {
@@ -126,25 +138,223 @@ SDY_DEV void chunk_attend(const ChunkLds &L, int n_rep, int hd, int np, float sc
 
 // ------------------------------------------------------------------ prefill: n tokens, two launches
 
-// Grid (n_chunk, n_kv_head, n_tok): token t attends to positions 0..n_kv0-1+t.
+// Grid (n_chunk, n_kv_head, ceil(n_tok / TB)): tokens tb*TB .. tb*TB + TB - 1, token t attending to
+// positions 0..n_kv0-1+t. The chunk's K and V are staged once for the workgroup's tokens (for the
+// last of them that reaches the chunk); each token then stages its queries and runs chunk_attend
+// over its own np positions, so every record has the bits of a workgroup for that token alone.
+constexpr int TB = 16;
 __global__ __launch_bounds__(256) void k_attn_partial(const float *__restrict__ q, const float *__restrict__ k_cache,
                                                       const float *__restrict__ v_cache, int n_head, int n_kv_head,
                                                       int hd, int n_kv0, long head_stride, long q_stride,
                                                       float *__restrict__ part, int n_tok, int n_chunk_max,
                                                       float scale) {
     extern __shared__ float sm[];
-    const int c = blockIdx.x, g = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
-    const int n_kv = n_kv0 + t, p0 = c * CH;
-    if (p0 >= n_kv) return;
-    const int np = n_kv - p0 < CH ? n_kv - p0 : CH;
+    const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    const int t0 = blockIdx.z * TB, t1 = t0 + TB < n_tok ? t0 + TB : n_tok;
+    const int p0 = c * CH;
+    const int n_kv_last = n_kv0 + t1 - 1;
+    if (p0 >= n_kv_last) return;  // no token of the block reaches this chunk
+    const int np_max = n_kv_last - p0 < CH ? n_kv_last - p0 : CH;
     const int n_rep = n_head / n_kv_head;
     const ChunkLds L = chunk_lds(sm, hd, n_rep);
-    stage_kv<256>(L, k_cache + g * head_stride + (size_t)p0 * hd, v_cache + g * head_stride + (size_t)p0 * hd, np, hd,
-                  -1, nullptr, nullptr);
-    for (int i = tid; i < n_rep * hd; i += 256) L.qs[i] = q[(size_t)t * q_stride + (size_t)g * n_rep * hd + i];
+    stage_kv<256>(L, k_cache + g * head_stride + (size_t)p0 * hd, v_cache + g * head_stride + (size_t)p0 * hd, np_max,
+                  hd, -1, nullptr, nullptr);
+    for (int t = t0 < (p0 + 1 - n_kv0) ? (p0 + 1 - n_kv0) : t0; t < t1; t++) {  // tokens that reach the chunk
+        const int n_kv = n_kv0 + t;
+        const int np = n_kv - p0 < CH ? n_kv - p0 : CH;
+        for (int i = tid; i < n_rep * hd; i += 256) L.qs[i] = q[(size_t)t * q_stride + (size_t)g * n_rep * hd + i];
+        __syncthreads();
+        chunk_attend<256>(L, n_rep, hd, np, scale, part, part + (size_t)n_tok * n_head * n_chunk_max * hd,
+                          ((size_t)t * n_head + g * n_rep) * n_chunk_max + c, n_chunk_max);
+    }
+}
+
+// Register-blocked prefill chunk: a workgroup takes R = 64 query rows (TBR = 64 / n_rep tokens x
+// the n_rep heads of KV head g) against the CH = 64 positions of chunk c. K is staged transposed
+// ([HD][64]), V as [64][HD], the scores / weights as [64][64]; the queries are read from global
+// memory (L1). Thread
+// (row group rg, column group cg) computes the scores of rows 4rg..4rg+3 x positions 4cg..4cg+3 and
+// then the weighted V of rows 4rg..4rg+3 x dims (HD/16)cg.. . Every sum has chunk_attend's order
+// (scores: four partial sums by d mod 4, then (a0 + a1) + (a2 + a3); weighted V: one chain over
+// the positions; weights past a row's own positions are exact zeros and leave the chain unchanged),
+// so the records are bit-identical to those of k_attn_partial. 80 KB of LDS: two workgroups, two
+// waves per SIMD, per CU (the register budget is set for that occupancy, so that the next operands
+// can be read while the current ones are multiplied). Token blocks are launched last first.
+template <int HD>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attn_prefill(const float *__restrict__ q, const float *__restrict__ k_cache,
+                                                      const float *__restrict__ v_cache, int n_head, int n_kv_head,
+                                                      int n_kv0, long head_stride, long q_stride,
+                                                      float *__restrict__ part, int n_tok, int n_chunk_max,
+                                                      float scale) {
+    constexpr int R = 64, DG = HD / 16;  // rows per workgroup, dims per thread in the weighted sum
+    extern __shared__ __align__(16) float sm[];
+    float *kT = sm;                // [HD][64]
+    float *vs = kT + HD * CH;      // [64][HD]
+    float *ps = vs + CH * HD;      // [R][64]
+    const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int n_rep = n_head / n_kv_head, tbr = R / n_rep;
+    // the last token blocks reach the most chunks: they are launched first
+    const int blk = (int)gridDim.z - 1 - (int)blockIdx.z;
+    const int t0 = blk * tbr, t1 = t0 + tbr < n_tok ? t0 + tbr : n_tok;
+    const int p0 = c * CH;
+    const int n_kv_last = n_kv0 + t1 - 1;
+    if (p0 >= n_kv_last) return;
+    const int np_max = n_kv_last - p0 < CH ? n_kv_last - p0 : CH;
+    // stage K transposed and V (positions past np_max as zeros), and the queries (rows past the
+    // last token repeat it)
+    // (each batch of 8 loads goes out before its LDS stores: unconditional, clamped addresses, so
+    // that their latencies overlap)
+    const float *kg = k_cache + g * head_stride + (size_t)p0 * HD, *vg = v_cache + g * head_stride + (size_t)p0 * HD;
+    constexpr int NV = CH * HD / 4 / 256;  // float4 of K (and of V) per thread
+    constexpr int NBT = NV < 8 ? NV : 8;   // per batch
+    static_assert(NV % NBT == 0, "batches");
+    for (int b0 = 0; b0 < NV; b0 += NBT) {
+        float4 kv[NBT], vv[NBT];
+#pragma unroll
+        for (int j = 0; j < NBT; j++) {
+            const int i = tid + 256 * (b0 + j);
+            const int pp = i % CH, d4 = i / CH;  // position fastest: conflict-free transposed writes
+            kv[j] = *reinterpret_cast<const float4 *>(kg + (size_t)(pp < np_max ? pp : 0) * HD + 4 * d4);
+            const int pv = (4 * i) / HD;
+            vv[j] = reinterpret_cast<const float4 *>(vg)[pv < np_max ? i : 0];
+        }
+#pragma unroll
+        for (int j = 0; j < NBT; j++) {
+            const int i = tid + 256 * (b0 + j);
+            const int pp = i % CH, d4 = i / CH, pv = (4 * i) / HD;
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 k4 = pp < np_max ? kv[j] : z;
+            kT[(4 * d4 + 0) * CH + pp] = k4.x;
+            kT[(4 * d4 + 1) * CH + pp] = k4.y;
+            kT[(4 * d4 + 2) * CH + pp] = k4.z;
+            kT[(4 * d4 + 3) * CH + pp] = k4.w;
+            reinterpret_cast<float4 *>(vs)[i] = pv < np_max ? vv[j] : z;
+        }
+    }
     __syncthreads();
-    chunk_attend<256>(L, n_rep, hd, np, scale, part, part + (size_t)n_tok * n_head * n_chunk_max * hd,
-                      ((size_t)t * n_head + g * n_rep) * n_chunk_max + c, n_chunk_max);
+    const int rg = tid >> 4, cg = tid & 15;
+    // the thread's 4 query rows, read from global memory (the 16 threads of a row group share them)
+    const float *qrow[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 4 * rg + i, tl = r / n_rep, jj = r - tl * n_rep;
+        const int t = t0 + tl < t1 ? t0 + tl : t1 - 1;
+        qrow[i] = q + (size_t)t * q_stride + (size_t)(g * n_rep + jj) * HD;
+    }
+    {
+        float a[4][4][4];  // [row][position][d mod 4]
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+#pragma unroll
+                for (int m = 0; m < 4; m++) a[i][k][m] = 0.0f;
+        // the next 4 dims' operands are read while the current ones are multiplied
+        float4 qn[4], kn[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) qn[i] = *reinterpret_cast<const float4 *>(qrow[i]);
+#pragma unroll
+        for (int m = 0; m < 4; m++) kn[m] = *reinterpret_cast<const float4 *>(kT + m * CH + 4 * cg);
+        for (int d = 0; d < HD; d += 4) {
+            float4 qv[4], kv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) qv[i] = qn[i];
+#pragma unroll
+            for (int m = 0; m < 4; m++) kv[m] = kn[m];
+            const int dn = d + 4 < HD ? d + 4 : d;
+#pragma unroll
+            for (int i = 0; i < 4; i++) qn[i] = *reinterpret_cast<const float4 *>(qrow[i] + dn);
+#pragma unroll
+            for (int m = 0; m < 4; m++) kn[m] = *reinterpret_cast<const float4 *>(kT + (dn + m) * CH + 4 * cg);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float qd[4] = {qv[i].x, qv[i].y, qv[i].z, qv[i].w};
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    const float kk[4] = {kv[m].x, kv[m].y, kv[m].z, kv[m].w};
+#pragma unroll
+                    for (int k = 0; k < 4; k++) a[i][k][m] = fmaf(qd[m], kk[k], a[i][k][m]);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float4 sc;
+            sc.x = ((a[i][0][0] + a[i][0][1]) + (a[i][0][2] + a[i][0][3])) * scale;
+            sc.y = ((a[i][1][0] + a[i][1][1]) + (a[i][1][2] + a[i][1][3])) * scale;
+            sc.z = ((a[i][2][0] + a[i][2][1]) + (a[i][2][2] + a[i][2][3])) * scale;
+            sc.w = ((a[i][3][0] + a[i][3][1]) + (a[i][3][2] + a[i][3][3])) * scale;
+            *reinterpret_cast<float4 *>(ps + (4 * rg + i) * CH + 4 * cg) = sc;
+        }
+    }
+    __syncthreads();
+    // softmax pieces per row (one wave per row, lane = position), as in chunk_attend
+    float *ml_base = part + (size_t)n_tok * n_head * n_chunk_max * HD;
+    for (int r = wave; r < R; r += 4) {
+        const int tl = r / n_rep, j = r - tl * n_rep, t = t0 + tl;
+        const int np = t < t1 ? (n_kv0 + t - p0 < CH ? n_kv0 + t - p0 : CH) : 0;
+        float e = 0.0f;
+        if (np > 0) {
+            const float sv = lane < np ? ps[r * CH + lane] : -INFINITY;
+            float m = sv;
+            for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+            e = lane < np ? expf(sv - m) : 0.0f;
+            float l = e;
+            for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off);
+            if (lane == 0) {
+                float *ml = ml_base + (((size_t)t * n_head + g * n_rep + j) * n_chunk_max + c) * 2;
+                ml[0] = m;
+                ml[1] = l;
+            }
+        }
+        ps[r * CH + lane] = e;
+    }
+    __syncthreads();
+    // weighted V: rows 4rg..4rg+3, dims DG*cg .. DG*cg + DG - 1, one chain over the positions
+    {
+        float o[4][DG];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int k = 0; k < DG; k++) o[i][k] = 0.0f;
+        // (the next position's weights and V are read while the current ones are multiplied)
+        float wn[4];
+        float4 vn[DG / 4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) wn[i] = ps[(4 * rg + i) * CH];
+#pragma unroll
+        for (int k = 0; k < DG / 4; k++) vn[k] = *reinterpret_cast<const float4 *>(vs + DG * cg + 4 * k);
+        for (int pp = 0; pp < np_max; pp++) {
+            float w[4];
+            float vv[DG];
+#pragma unroll
+            for (int i = 0; i < 4; i++) w[i] = wn[i];
+#pragma unroll
+            for (int k = 0; k < DG / 4; k++) {
+                vv[4 * k] = vn[k].x;
+                vv[4 * k + 1] = vn[k].y;
+                vv[4 * k + 2] = vn[k].z;
+                vv[4 * k + 3] = vn[k].w;
+            }
+            const int pn = pp + 1 < CH ? pp + 1 : pp;
+#pragma unroll
+            for (int i = 0; i < 4; i++) wn[i] = ps[(4 * rg + i) * CH + pn];
+#pragma unroll
+            for (int k = 0; k < DG / 4; k++) vn[k] = *reinterpret_cast<const float4 *>(vs + pn * HD + DG * cg + 4 * k);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int k = 0; k < DG; k++) o[i][k] = fmaf(w[i], vv[k], o[i][k]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = 4 * rg + i, tl = r / n_rep, j = r - tl * n_rep, t = t0 + tl;
+            if (t >= t1 || n_kv0 + t - p0 <= 0) continue;
+            float *ob = part + (((size_t)t * n_head + g * n_rep + j) * n_chunk_max + c) * HD + DG * cg;
+#pragma unroll
+            for (int k = 0; k < DG; k += 4) *reinterpret_cast<float4 *>(ob + k) = make_float4(o[i][k], o[i][k + 1], o[i][k + 2], o[i][k + 3]);
+        }
+    }
 }
 
 // Grid (n_head, n_tok), 128 threads.
@@ -364,8 +574,24 @@ extern "C" int sdy_attention(const float *q, const float *k_cache, const float *
     static size_t granted = 0;
     if ((rc = sdy_lds_limit((const void *)k_attn_partial, lds, &granted))) return rc;
     float scale = 1.0f / sqrtf((float)hd);
-    hipLaunchKernelGGL(k_attn_partial, dim3(nc, n_kv_head, n_tok), dim3(256), lds, st, q, k_cache, v_cache, n_head,
-                       n_kv_head, hd, n_kv0, head_stride, q_stride, part, n_tok, nc, scale);
+    if (n_tok >= 16 && 64 % n_rep == 0 && (hd == 64 || hd == 128)) {
+        // many tokens: the register-blocked chunk kernel (the same records, bit for bit)
+        const int tbr = 64 / n_rep;
+        const size_t lds2 = sizeof(float) * ((size_t)hd * CH * 2 + 64 * CH);
+        static size_t granted2[2] = {0, 0};
+        const void *fn = hd == 128 ? (const void *)k_attn_prefill<128> : (const void *)k_attn_prefill<64>;
+        if ((rc = sdy_lds_limit(fn, lds2, &granted2[hd == 128]))) return rc;
+        const dim3 grid(nc, n_kv_head, (n_tok + tbr - 1) / tbr);
+        if (hd == 128)
+            hipLaunchKernelGGL(k_attn_prefill<128>, grid, dim3(256), lds2, st, q, k_cache, v_cache, n_head, n_kv_head,
+                               n_kv0, head_stride, q_stride, part, n_tok, nc, scale);
+        else
+            hipLaunchKernelGGL(k_attn_prefill<64>, grid, dim3(256), lds2, st, q, k_cache, v_cache, n_head, n_kv_head,
+                               n_kv0, head_stride, q_stride, part, n_tok, nc, scale);
+    } else {
+        hipLaunchKernelGGL(k_attn_partial, dim3(nc, n_kv_head, (n_tok + TB - 1) / TB), dim3(256), lds, st, q, k_cache,
+                           v_cache, n_head, n_kv_head, hd, n_kv0, head_stride, q_stride, part, n_tok, nc, scale);
+    }
     if ((rc = sdy_check_launch("attention"))) return rc;
     hipLaunchKernelGGL(k_attn_combine, dim3(n_head, n_tok), dim3(128), 2 * nc * sizeof(float), st, part, n_head, hd,
                        n_kv0, n_tok, nc, out, out_stride);

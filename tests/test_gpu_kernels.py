@@ -457,6 +457,41 @@ def test_moe_route_and_combine(n_expert, k):
         assert np.array_equal(bits(got[t]), bits(resid[t] + acc)), t
 
 
+@pytest.mark.parametrize("n_head,n_kv_head,hd", [(16, 2, 128), (4, 2, 64), (32, 4, 128), (4, 4, 64), (6, 2, 64)])
+@pytest.mark.parametrize("n_tok,n_kv0", [(16, 1), (40, 70), (77, 3)])
+def test_prefill_attention_tokens_bit_identical(n_head, n_kv_head, hd, n_tok, n_kv0):
+    """Causal attention of n_tok tokens in one call (the register-blocked chunk kernel from 16
+    tokens on) gives the bits of one call per token, and follows a float64 softmax."""
+    L = lib()
+    rng = np.random.default_rng(n_head * 1000 + n_tok + hd)
+    max_seq = 160
+    q = rng.standard_normal((n_tok, n_head * hd)).astype(np.float32)
+    kc = rng.standard_normal((n_kv_head, max_seq, hd)).astype(np.float32)
+    vc = rng.standard_normal((n_kv_head, max_seq, hd)).astype(np.float32)
+    dq, dk, dv = capi.DeviceBuffer.from_array(q), capi.DeviceBuffer.from_array(kc), capi.DeviceBuffer.from_array(vc)
+    dpart = capi.DeviceBuffer(L.sdy_attn_part_floats(n_tok, n_head, hd, max_seq) * 4)
+    dout = capi.DeviceBuffer(n_tok * n_head * hd * 4)
+    q_dim = n_head * hd
+    capi.check(L.sdy_attention(dq.ptr, dk.ptr, dv.ptr, n_tok, n_head, n_kv_head, hd, n_kv0, max_seq * hd, q_dim,
+                               dpart.ptr, dout.ptr, q_dim, None))
+    got = dout.to_array(np.float32, (n_tok, q_dim))
+    one = np.empty_like(got)
+    d1 = capi.DeviceBuffer(q_dim * 4)
+    for t in range(n_tok):
+        capi.check(L.sdy_attention(dq.ptr + 4 * t * q_dim, dk.ptr, dv.ptr, 1, n_head, n_kv_head, hd, n_kv0 + t,
+                                   max_seq * hd, q_dim, dpart.ptr, d1.ptr, q_dim, None))
+        one[t] = d1.to_array(np.float32, q_dim)
+    assert np.array_equal(bits(got), bits(one))
+    n_rep = n_head // n_kv_head
+    for t in range(0, n_tok, 7):
+        for h in range(n_head):
+            kk, vv = kc[h // n_rep, :n_kv0 + t].astype(np.float64), vc[h // n_rep, :n_kv0 + t].astype(np.float64)
+            sc = kk @ q[t, h * hd:(h + 1) * hd].astype(np.float64) / np.sqrt(hd)
+            p = np.exp(sc - sc.max())
+            exp = (p / p.sum()) @ vv
+            np.testing.assert_allclose(got[t, h * hd:(h + 1) * hd], exp, rtol=1e-4, atol=1e-5)
+
+
 def _gemm_case(kind, n_in, n_out, n_tok, seed, gen="workload"):
     t = TYPES[kind]
     rng = np.random.default_rng(seed)
