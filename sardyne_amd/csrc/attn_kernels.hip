@@ -51,18 +51,19 @@ template <int NT>
 SDY_DEV void stage_kv(const ChunkLds &L, const float *kg, const float *vg, int np, int hd, int special,
                       const float *kspec, const float *vspec) {
     const int n4 = np * hd / 4, tid = threadIdx.x;
-    // batches of 4 loads per thread go out before their LDS stores (clamped indices, no
-    // conditional load), so that their latencies overlap
-    for (int i0 = tid; i0 < n4; i0 += 4 * NT) {
-        float4 kv[4], vv[4];
+    // batches of B loads per thread (a chunk of 64 x 128 floats is 2048 float4 of K and of V) go out
+    // before their LDS stores (clamped indices, no conditional load), so that their latencies overlap
+    constexpr int B = NT >= 1024 ? 2 : 4;
+    for (int i0 = tid; i0 < n4; i0 += B * NT) {
+        float4 kv[B], vv[B];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < B; j++) {
             const int i = i0 + j * NT < n4 ? i0 + j * NT : i0;
             kv[j] = reinterpret_cast<const float4 *>(kg)[i];
             vv[j] = reinterpret_cast<const float4 *>(vg)[i];
         }
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < B; j++) {
             const int i = i0 + j * NT;
             if (i >= n4) break;
             const int p = (4 * i) / hd, d = 4 * i - p * hd;
@@ -464,6 +465,17 @@ __global__ __launch_bounds__(DEC_NT) void k_attn_decode(AttnDecodeArgs a) {
     const bool has_pos = c == nch - 1;  // this chunk holds the new position
     const ChunkLds L = chunk_lds(sm, hd, n_rep);
     float *kp = L.ps + n_rep * CH;      // [hd]: normalised, rotated k of the new position
+    // 0. the chunk's K and V from the cache (a chunk is at most 2 float4 of each per thread): the
+    //    loads go out first and land while the queries are rotated
+    const float *kg = a.k_cache + g * a.head_stride + (size_t)p0 * hd, *vg = a.v_cache + g * a.head_stride + (size_t)p0 * hd;
+    const int n4 = np * hd / 4, tid = threadIdx.x;
+    float4 kv[2], vv[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int i = tid + j * DEC_NT < n4 ? tid + j * DEC_NT : 0;
+        kv[j] = reinterpret_cast<const float4 *>(kg)[i];
+        vv[j] = reinterpret_cast<const float4 *>(vg)[i];
+    }
     // 1. q heads of this group (and k of the new position): norm + RoPE in LDS
     const float *cs = a.rope_cos + (size_t)pos * (hd / 2), *sn = a.rope_sin + (size_t)pos * (hd / 2);
     const int tasks = n_rep + (has_pos ? 1 : 0);
@@ -485,9 +497,26 @@ __global__ __launch_bounds__(DEC_NT) void k_attn_decode(AttnDecodeArgs a) {
         }
     }
     __syncthreads();
-    // 2. the chunk (the new position from LDS / the raw v)
-    stage_kv<DEC_NT>(L, a.k_cache + g * a.head_stride + (size_t)p0 * hd, a.v_cache + g * a.head_stride + (size_t)p0 * hd,
-                     np, hd, has_pos ? pos - p0 : -1, kp, a.v + (size_t)g * hd);
+    // 2. the chunk into LDS (the new position from LDS / the raw v: its cache entry is written above)
+    const int special = has_pos ? pos - p0 : -1;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int i = tid + j * DEC_NT;
+        if (i >= n4) break;
+        const int p = (4 * i) / hd, d = 4 * i - p * hd;
+        if (p == special) continue;
+        float *kr = L.ks + p * (hd + 1) + d;
+        kr[0] = kv[j].x;
+        kr[1] = kv[j].y;
+        kr[2] = kv[j].z;
+        kr[3] = kv[j].w;
+        *reinterpret_cast<float4 *>(L.vs + 4 * i) = vv[j];
+    }
+    if (special >= 0)
+        for (int d = tid; d < hd; d += DEC_NT) {
+            L.ks[special * (hd + 1) + d] = kp[d];
+            L.vs[special * hd + d] = a.v[(size_t)g * hd + d];
+        }
     __syncthreads();
     chunk_attend<DEC_NT>(L, n_rep, hd, np, a.scale, a.part, a.part + (size_t)a.n_head * a.n_chunk_max * hd,
                          (size_t)g * n_rep * a.n_chunk_max + c, a.n_chunk_max);
@@ -604,7 +633,8 @@ static size_t attn_decode_lds(int n_head, int n_kv_head, int hd) {
 
 extern "C" int sdy_attn_decode_ok(int n_head, int n_kv_head, int hd, int max_seq) {
     (void)max_seq;
-    if (hd > 512 || hd % 4 || n_kv_head < 1 || n_head % n_kv_head || n_head > 64) return 0;
+    // a chunk's K and V are at most 2 float4 each per thread: CH * hd / 4 <= 2 * DEC_NT
+    if (hd > 128 || hd % 4 || n_kv_head < 1 || n_head % n_kv_head || n_head > 64) return 0;
     return attn_decode_lds(n_head, n_kv_head, hd) <= 160 * 1024;
 }
 

@@ -804,15 +804,14 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
     }
 }
 
-// Long rows, one token (K-quants with T > 64 units or T not dividing 64, e.g. n_in = 11008 with
-// 172 units): a wave owns whole rows, lane l handles units l, l + 64, ..., l + 64 (NI - 1) of a row.
-// After the quad reduction the term of super-block s = 16k + q sits in lane 4q of pass k, and the
-// row sum folds the terms in super-block order with lane reads (the reference's sequential f32
-// order). Activations are staged in LDS. Each wave walks its rows one at a time; its first row's
-// weights are requested before the activations are staged.
+// Long rows, one token (K-quants with T > 64 units, e.g. n_in = 11008 with 172 units): a wave owns
+// whole rows, lane l handles units l, l + 64, ..., l + 64 (NI - 1) of a row. After the quad
+// reduction the term of super-block s = 16k + q sits in lane 4q of pass k, and the row sum folds the
+// terms in super-block order with lane reads (the reference's sequential f32 order). Each lane keeps
+// the activations of its units in registers (read from memory with the first row's weights). Each
+// wave walks its rows one at a time.
 template <int WT, int NI>
 __global__ __launch_bounds__(THREADS) void k_matvec_lr(MvArgs a) {
-    extern __shared__ uint8_t lds[];
     const int T = a.P.T, nb = a.P.nb;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const long n_rows = a.row1 - a.row0;
@@ -827,27 +826,36 @@ __global__ __launch_bounds__(THREADS) void k_matvec_lr(MvArgs a) {
         }
     };
     WRegs<WT> A[NI];
-    if (wid < n_rows) load_row(wid, A);
-    stage_acts<WT, 1>(a, lds);
-    __syncthreads();
     if (wid >= n_rows) return;
-    const uint8_t *aux = lds + (size_t)4 * T * 16;
-    const float *yd = reinterpret_cast<const float *>(aux + (size_t)T * 8);
+    load_row(wid, A);
+    // the lane's activations (the 64 Q8_K bytes of its unit in each pass, their bsums and the block
+    // scale) straight from memory into registers, requested with the first row's weights: no LDS
+    // staging, no barrier
+    uint4 Yr[NI][4];
+    uint2 bsr[NI];
+    float ydr[NI];
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+        const int u = 64 * k + lane, uu = u < T ? u : 0;
+        const uint8_t *blk = a.xq + (size_t)(uu >> 2) * 292;
+        const uint8_t *yb = blk + 4 + 64 * (uu & 3);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            Yr[k][q] = make_uint4(ld4(yb + 16 * q), ld4(yb + 16 * q + 4), ld4(yb + 16 * q + 8), ld4(yb + 16 * q + 12));
+        bsr[k] = make_uint2(ld4(blk + 260 + 8 * (uu & 3)), ld4(blk + 264 + 8 * (uu & 3)));
+        ydr[k] = *reinterpret_cast<const float *>(blk);
+    }
     auto body = [&](const WRegs<WT> (&R)[NI], long r) {
         float term[NI];
 #pragma unroll
         for (int k = 0; k < NI; k++) {
             const int u = 64 * k + lane, uu = u < T ? u : 0;
-            uint4 Y[4];
-#pragma unroll
-            for (int q = 0; q < 4; q++) Y[q] = *reinterpret_cast<const uint4 *>(lds + (q * T + uu) * 16);
-            const uint2 bsp = *reinterpret_cast<const uint2 *>(aux + uu * 8);
             int isum, msum;
             float dummy = 0.0f;
-            unit_dot<WT>(R[k], Y, bsp, uu, isum, msum, dummy, make_float2(0.f, 0.f), make_int2(0, 0));
+            unit_dot<WT>(R[k], Yr[k], bsr[k], uu, isum, msum, dummy, make_float2(0.f, 0.f), make_int2(0, 0));
             isum = sdy_quad_sum(isum);
             if constexpr (WT == SDY_Q4_K) msum = sdy_quad_sum(msum);
-            const float ydv = yd[uu >> 2];
+            const float ydv = ydr[k];
             if constexpr (WT == SDY_Q4_K) {
                 float d = sdy_h2f((uint16_t)(R[k].c.x & 0xFFFFu)), dmin = sdy_h2f((uint16_t)(R[k].c.x >> 16));
                 float dall = ydv * d, dmn = ydv * dmin;
@@ -1361,7 +1369,7 @@ static int launch_mv(const sdy_mat *m, const sdy_mv_args *a, int n_tok, const ui
     if constexpr (MT == 1 && is_k(WT))
         if (T < 64 && (!A.swiglu || (64 / T) % 2 == 0)) return launch_mv_rl<WT, 1, true>(A, 0, st);
     if constexpr (MT == 1 && is_k(WT))
-        if (!A.swiglu) return launch_mv_lr<WT>(A, mv_lds_bytes_rl(T, 1), st);
+        if (!A.swiglu) return launch_mv_lr<WT>(A, 0, st);
     return launch_mv_k<WT, MT, false>(A, lds, st);
 }
 

@@ -111,7 +111,8 @@ def _matvec_case(kind, n_in, n_out, n_tok, seed, gen="workload"):
 @pytest.mark.parametrize("kind", list(TYPES))
 @pytest.mark.parametrize("n_in,n_out,n_tok", [(256, 13, 1), (512, 13, 3), (2048, 37, 1), (768, 20, 5),
                                               (11008, 9, 2), (4096, 16, 9), (2048, 64, 8), (768, 41, 1),
-                                              (1280, 23, 1), (2560, 7, 1)])
+                                              (1280, 23, 1), (2560, 7, 1), (11008, 33, 1), (8192, 20, 1),
+                                              (16384, 5, 1)])
 def test_matvec_vs_oracle(kind, n_in, n_out, n_tok):
     if kind in ("Q8_0", "Q4_0", "Q5_0") and n_in % 32:
         pytest.skip("row not a whole number of blocks")
