@@ -449,77 +449,124 @@ struct AttnDecodeArgs {
     float scale;
 };
 
-// Grid (n_chunk_max, n_kv_head), DEC_NT threads; chunks past the position exit at once. Writes the
-// partial records of every chunk; the merge happens in the consumer (the output projection's
-// activation prologue, or k_attn_merge1).
-constexpr int DEC_NT = 1024, DEC_W = DEC_NT / 64;
+// Grid (n_chunk_max, n_kv_head), DEC_NT threads (8 waves); chunks past the position exit at once.
+// Writes the partial records of every chunk; the merge is a separate launch (k_attn_merge1*).
+// The chunk's K and V loads go out first; meanwhile each wave normalises and rotates its query
+// heads (and one wave the new position's k, which it also writes to the cache). After one barrier
+// wave w takes heads w, w + 8, ...: lane p computes the score of position p with chunk_attend's
+// four partial sums (d mod 4), the wave forms m, l and the weights as chunk_attend does, and lane l
+// accumulates dims l, l + 64, ... of the weighted V over the positions in order (the weight of
+// position p read from lane p). The records are therefore those of chunk_attend, bit for bit.
+constexpr int DEC_NT = 512, DEC_W = DEC_NT / 64;
 
+template <int HD>
 __global__ __launch_bounds__(DEC_NT) void k_attn_decode(AttnDecodeArgs a) {
+    constexpr int KS = HD + 1;            // K row stride (odd: conflict-free reads by position)
+    constexpr int NV = CH * HD / 4 / DEC_NT;  // float4 of K (and of V) per thread
+    static_assert(NV >= 1 && NV * DEC_NT * 4 == CH * HD, "chunk");
     extern __shared__ float sm[];
-    const int c = blockIdx.x, g = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float *ks = sm;                       // [CH][HD + 1]
+    float *vs = ks + CH * KS;             // [CH][HD]
+    float *kp = vs + CH * HD;             // [HD]: normalised, rotated k of the new position
+    float *qs = kp + HD;                  // [n_rep][HD]
+    const int c = blockIdx.x, g = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
     const int pos = a.step[1], n_kv = pos + 1;
     const int nch = (n_kv + CH - 1) / CH;
     if (c >= nch) return;
-    const int hd = a.hd, n_rep = a.n_head / a.n_kv_head;
+    const int n_rep = a.n_head / a.n_kv_head;
     const int p0 = c * CH, np = n_kv - p0 < CH ? n_kv - p0 : CH;
     const bool has_pos = c == nch - 1;  // this chunk holds the new position
-    const ChunkLds L = chunk_lds(sm, hd, n_rep);
-    float *kp = L.ps + n_rep * CH;      // [hd]: normalised, rotated k of the new position
-    // 0. the chunk's K and V from the cache (a chunk is at most 2 float4 of each per thread): the
-    //    loads go out first and land while the queries are rotated
-    const float *kg = a.k_cache + g * a.head_stride + (size_t)p0 * hd, *vg = a.v_cache + g * a.head_stride + (size_t)p0 * hd;
-    const int n4 = np * hd / 4, tid = threadIdx.x;
-    float4 kv[2], vv[2];
+    // 0. the chunk's K and V from the cache (clamped indices: every load is unconditional)
+    const float *kg = a.k_cache + g * a.head_stride + (size_t)p0 * HD, *vg = a.v_cache + g * a.head_stride + (size_t)p0 * HD;
+    const int n4 = np * HD / 4;
+    float4 kv[NV], vv[NV];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < NV; j++) {
         const int i = tid + j * DEC_NT < n4 ? tid + j * DEC_NT : 0;
         kv[j] = reinterpret_cast<const float4 *>(kg)[i];
         vv[j] = reinterpret_cast<const float4 *>(vg)[i];
     }
     // 1. q heads of this group (and k of the new position): norm + RoPE in LDS
-    const float *cs = a.rope_cos + (size_t)pos * (hd / 2), *sn = a.rope_sin + (size_t)pos * (hd / 2);
+    const float *cs = a.rope_cos + (size_t)pos * (HD / 2), *sn = a.rope_sin + (size_t)pos * (HD / 2);
     const int tasks = n_rep + (has_pos ? 1 : 0);
     for (int r = wave; r < tasks; r += DEC_W) {
         const bool is_k = r == n_rep;
-        float *buf = is_k ? kp : L.qs + r * hd;
-        const float *src = is_k ? a.k + (size_t)g * hd : a.q + (size_t)(g * n_rep + r) * hd;
-        for (int i = lane; i < hd; i += 64) buf[i] = src[i];
+        float *buf = is_k ? kp : qs + r * HD;
+        const float *src = is_k ? a.k + (size_t)g * HD : a.q + (size_t)(g * n_rep + r) * HD;
+        for (int i = lane; i < HD; i += 64) buf[i] = src[i];
         sdy_wave_sync();
-        norm_rope_wave(buf, is_k ? a.k_norm : a.q_norm, a.eps, cs, sn, hd, a.interleaved, lane);
+        norm_rope_wave(buf, is_k ? a.k_norm : a.q_norm, a.eps, cs, sn, HD, a.interleaved, lane);
         if (is_k) {  // KV-cache write of the new position
-            float *kc = a.k_cache + g * a.head_stride + (size_t)pos * hd;
-            float *vc = a.v_cache + g * a.head_stride + (size_t)pos * hd;
-            const float *vv = a.v + (size_t)g * hd;
-            for (int i = lane; i < hd; i += 64) {
+            float *kc = a.k_cache + g * a.head_stride + (size_t)pos * HD;
+            float *vc = a.v_cache + g * a.head_stride + (size_t)pos * HD;
+            const float *vn = a.v + (size_t)g * HD;
+            for (int i = lane; i < HD; i += 64) {
                 kc[i] = buf[i];
-                vc[i] = vv[i];
+                vc[i] = vn[i];
             }
         }
     }
-    __syncthreads();
     // 2. the chunk into LDS (the new position from LDS / the raw v: its cache entry is written above)
     const int special = has_pos ? pos - p0 : -1;
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < NV; j++) {
         const int i = tid + j * DEC_NT;
         if (i >= n4) break;
-        const int p = (4 * i) / hd, d = 4 * i - p * hd;
+        const int p = (4 * i) / HD, d = 4 * i - p * HD;
         if (p == special) continue;
-        float *kr = L.ks + p * (hd + 1) + d;
+        float *kr = ks + p * KS + d;
         kr[0] = kv[j].x;
         kr[1] = kv[j].y;
         kr[2] = kv[j].z;
         kr[3] = kv[j].w;
-        *reinterpret_cast<float4 *>(L.vs + 4 * i) = vv[j];
+        *reinterpret_cast<float4 *>(vs + 4 * i) = vv[j];
     }
+    __syncthreads();  // (also orders the k of the new position in kp before its use below)
     if (special >= 0)
-        for (int d = tid; d < hd; d += DEC_NT) {
-            L.ks[special * (hd + 1) + d] = kp[d];
-            L.vs[special * hd + d] = a.v[(size_t)g * hd + d];
+        for (int d = tid; d < HD; d += DEC_NT) {
+            ks[special * KS + d] = kp[d];
+            vs[special * HD + d] = a.v[(size_t)g * HD + d];
         }
     __syncthreads();
-    chunk_attend<DEC_NT>(L, n_rep, hd, np, a.scale, a.part, a.part + (size_t)a.n_head * a.n_chunk_max * hd,
-                         (size_t)g * n_rep * a.n_chunk_max + c, a.n_chunk_max);
+    // 3. per head: scores (lane = position), weights, weighted V (lane = dims)
+    float *o_base = a.part, *ml_base = a.part + (size_t)a.n_head * a.n_chunk_max * HD;
+    for (int r = wave; r < n_rep; r += DEC_W) {
+        const float *qq = qs + r * HD;
+        float sc = -INFINITY;
+        if (lane < np) {
+            const float *kk = ks + lane * KS;
+            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll 8
+            for (int d = 0; d < HD; d += 4) {
+                const float4 q4 = *reinterpret_cast<const float4 *>(qq + d);
+                a0 = fmaf(q4.x, kk[d], a0);
+                a1 = fmaf(q4.y, kk[d + 1], a1);
+                a2 = fmaf(q4.z, kk[d + 2], a2);
+                a3 = fmaf(q4.w, kk[d + 3], a3);
+            }
+            sc = ((a0 + a1) + (a2 + a3)) * a.scale;
+        }
+        float m = sc;
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        const float e = lane < np ? expf(sc - m) : 0.0f;
+        float l = e;
+        for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off);
+        const size_t rec = (size_t)(g * n_rep + r) * a.n_chunk_max + c;
+        if (lane == 0) {
+            ml_base[rec * 2] = m;
+            ml_base[rec * 2 + 1] = l;
+        }
+        float acc[HD / 64];
+#pragma unroll
+        for (int k = 0; k < HD / 64; k++) acc[k] = 0.0f;
+        for (int p = 0; p < np; p++) {
+            const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), p));
+#pragma unroll
+            for (int k = 0; k < HD / 64; k++) acc[k] = fmaf(w, vs[p * HD + lane + 64 * k], acc[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < HD / 64; k++) o_base[rec * HD + lane + 64 * k] = acc[k];
+    }
 }
 
 // Merge of one token's partial records (position in step[1]) into out [n_head * hd], for output
@@ -628,13 +675,13 @@ extern "C" int sdy_attention(const float *q, const float *k_cache, const float *
 }
 
 static size_t attn_decode_lds(int n_head, int n_kv_head, int hd) {
-    return sizeof(float) * (chunk_lds_floats(hd, n_head / n_kv_head) + hd);
+    return sizeof(float) * ((size_t)CH * (hd + 1) + (size_t)CH * hd + hd + (size_t)(n_head / n_kv_head) * hd);
 }
 
 extern "C" int sdy_attn_decode_ok(int n_head, int n_kv_head, int hd, int max_seq) {
     (void)max_seq;
-    // a chunk's K and V are at most 2 float4 each per thread: CH * hd / 4 <= 2 * DEC_NT
-    if (hd > 128 || hd % 4 || n_kv_head < 1 || n_head % n_kv_head || n_head > 64) return 0;
+    // the decode kernel is built for head_dim 64 and 128
+    if ((hd != 64 && hd != 128) || n_kv_head < 1 || n_head % n_kv_head || n_head > 64) return 0;
     return attn_decode_lds(n_head, n_kv_head, hd) <= 160 * 1024;
 }
 
@@ -649,8 +696,9 @@ extern "C" int sdy_attn_decode(const float *q, const float *k, const float *v, c
         return sdy_fail(-1, "attn_decode: unsupported shape (%d heads, %d kv heads, head_dim %d)", n_head, n_kv_head,
                         hd);
     const size_t lds = attn_decode_lds(n_head, n_kv_head, hd);
-    static size_t granted = 0;
-    int rc = sdy_lds_limit((const void *)k_attn_decode, lds, &granted);
+    static size_t granted[2] = {0, 0};
+    const void *fn = hd == 128 ? (const void *)k_attn_decode<128> : (const void *)k_attn_decode<64>;
+    int rc = sdy_lds_limit(fn, lds, &granted[hd == 128]);
     if (rc) return rc;
     AttnDecodeArgs a;
     a.q = q;
@@ -672,7 +720,10 @@ extern "C" int sdy_attn_decode(const float *q, const float *k, const float *v, c
     a.part = part;
     a.n_chunk_max = (max_seq + CH - 1) / CH;
     a.scale = 1.0f / sqrtf((float)hd);
-    hipLaunchKernelGGL(k_attn_decode, dim3(a.n_chunk_max, n_kv_head), dim3(DEC_NT), lds, (hipStream_t)s, a);
+    if (hd == 128)
+        hipLaunchKernelGGL(k_attn_decode<128>, dim3(a.n_chunk_max, n_kv_head), dim3(DEC_NT), lds, (hipStream_t)s, a);
+    else
+        hipLaunchKernelGGL(k_attn_decode<64>, dim3(a.n_chunk_max, n_kv_head), dim3(DEC_NT), lds, (hipStream_t)s, a);
     return sdy_check_launch("attn_decode");
 }
 
