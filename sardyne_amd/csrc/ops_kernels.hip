@@ -156,12 +156,14 @@ __global__ __launch_bounds__(64) void k_moe_route(const float *logits, int n_exp
     }
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     // op_softmax (csrc/ops.c:353-364): expf(x - max), the sum in double, times (float)(1 / sum).
-    // The probabilities stay in registers; -1 marks lanes past n_expert (never chosen).
+    // expf is computed in double and rounded once (the correctly rounded value, as the host libm
+    // gives), so that near-equal router probabilities order as on the host. The probabilities stay
+    // in registers; -1 marks lanes past n_expert (never chosen).
     double s = 0.0;
 #pragma unroll
     for (int j = 0; j < NPL; j++)
         if (lane + 64 * j < n_expert) {
-            v[j] = expf(v[j] - m);
+            v[j] = (float)exp((double)(v[j] - m));
             s += (double)v[j];
         }
     for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);

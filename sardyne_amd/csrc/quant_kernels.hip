@@ -902,63 +902,122 @@ SDY_DEV float welem(const uint8_t *w, size_t i) {
     else return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(w)[i] << 16);
 }
 
-// One wave per (row, token): each lane accumulates its elements with fused multiply-adds in a
-// fixed order, then a fixed xor-butterfly reduction. Deterministic; parity with the reference is
-// by tolerance.
+// Float-weight matvec in the reference's AVX2 order (csrc/ops_avx2.c:61-134, as op_matmul_rows
+// splits the work): rows [row0, row1) in pairs from row0 and, with n_tok >= 4, tokens in groups of
+// four take block_2x4's order (one 8-lane FMA chain over 8-element steps per (row, token)); the other
+// (row, token) pairs take dot's order (four 8-lane chains over 32-element steps, then 8-element steps
+// into the first chain, the lane-wise (a0 + a1) + (a2 + a3)). Both then sum the 8 lanes as hsum does,
+// ((v0 + v4) + (v2 + v6)) + ((v1 + v5) + (v3 + v7)), and add the n_in % 8 tail one rounded product
+// at a time. The results are the reference's bits.
+
+// hsum of the 8 lanes of a group (lane l of the group holds v_l; the result is in every lane)
+SDY_DEV float hsum8_group(float v, int base) {
+    const float s0 = __shfl(v, base + 0), s1 = __shfl(v, base + 1), s2 = __shfl(v, base + 2), s3 = __shfl(v, base + 3);
+    const float s4 = __shfl(v, base + 4), s5 = __shfl(v, base + 5), s6 = __shfl(v, base + 6), s7 = __shfl(v, base + 7);
+    return ((s0 + s4) + (s2 + s6)) + ((s1 + s5) + (s3 + s7));
+}
+
 template <int WT>
-__global__ __launch_bounds__(THREADS) void k_matvec_float(const uint8_t *__restrict__ w, int n_in, const float *__restrict__ x,
-                                                          int n_tok, float *out, long out_stride, const float *bias,
-                                                          const float *resid, long row0, long row1) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const long n = (row1 - row0) * n_tok;
-    for (long i = (long)blockIdx.x * WAVES + wave; i < n; i += (long)gridDim.x * WAVES) {
-        long row = row0 + i / n_tok;
-        int t = (int)(i % n_tok);
-        const uint8_t *wr = w + (size_t)row * n_in * (WT == SDY_F32 ? 4 : 2);
-        const float *xr = x + (size_t)t * n_in;
-        float acc = 0.0f;
-        if ((n_in & 3) == 0) {
-            // lane l takes elements 256c + 4l .. 256c + 4l + 3 of chunk c (one 16-byte f32 or 8-byte
-            // f16/bf16 load); 8 chunks' loads go out before their multiply-adds
-            const int n_chunk = (n_in + 255) / 256;
-            for (int c0 = 0; c0 < n_chunk; c0 += 8) {
-                float4 wv[8], xv[8];
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    int e = 256 * (c0 + j) + 4 * lane;
-                    e = e < n_in ? e : 0;
-                    xv[j] = *reinterpret_cast<const float4 *>(xr + e);
-                    if constexpr (WT == SDY_F32) {
-                        wv[j] = *reinterpret_cast<const float4 *>(wr + 4 * (size_t)e);
-                    } else {
-                        const uint2 h = *reinterpret_cast<const uint2 *>(wr + 2 * (size_t)e);
-                        const uint16_t hv[4] = {(uint16_t)(h.x & 0xFFFFu), (uint16_t)(h.x >> 16),
-                                                (uint16_t)(h.y & 0xFFFFu), (uint16_t)(h.y >> 16)};
-                        wv[j] = make_float4(welem<WT>(reinterpret_cast<const uint8_t *>(hv), 0),
-                                            welem<WT>(reinterpret_cast<const uint8_t *>(hv), 1),
-                                            welem<WT>(reinterpret_cast<const uint8_t *>(hv), 2),
-                                            welem<WT>(reinterpret_cast<const uint8_t *>(hv), 3));
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < 8; j++)
-                    if (256 * (c0 + j) + 4 * lane < n_in) {
-                        acc = fmaf(wv[j].x, xv[j].x, acc);
-                        acc = fmaf(wv[j].y, xv[j].y, acc);
-                        acc = fmaf(wv[j].z, xv[j].z, acc);
-                        acc = fmaf(wv[j].w, xv[j].w, acc);
-                    }
-            }
-        } else {
-            for (int e = lane; e < n_in; e += 64) acc = fmaf(welem<WT>(wr, e), xr[e], acc);
-        }
-        for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off);
-        if (lane == 0) {
-            if (bias) acc = acc + bias[row];
-            if (resid) acc = resid[(size_t)t * out_stride + row] + acc;
-            out[(size_t)t * out_stride + row] = acc;
-        }
+SDY_DEV float float_tail(const uint8_t *wr, const float *xr, int n_in, float sum) {
+    for (int i = n_in & ~7; i < n_in; i++) {
+        const float p = xr[i] * welem<WT>(wr, i);
+        sum = sum + p;
     }
+    return sum;
+}
+
+template <int WT>
+SDY_DEV void float_store(float acc, long row, int t, float *out, long out_stride, const float *bias,
+                         const float *resid) {
+    if (bias) acc = acc + bias[row];
+    if (resid) acc = resid[(size_t)t * out_stride + row] + acc;
+    out[(size_t)t * out_stride + row] = acc;
+}
+
+// dot's order: one (row, token) per 32-lane half-wave. Items: with n_tok >= 4 the paired rows times
+// the tokens past the last group of four, then the unpaired last row times every token; with fewer
+// tokens every (row, token).
+template <int WT>
+__global__ __launch_bounds__(THREADS) void k_matvec_float_dot(const uint8_t *__restrict__ w, int n_in,
+                                                              const float *__restrict__ x, int n_tok, float *out,
+                                                              long out_stride, const float *bias, const float *resid,
+                                                              long row0, long row1) {
+    const int lane = threadIdx.x & 63, L = lane & 31, base = lane & 32;
+    const long n_rows = row1 - row0, n_pr = n_tok >= 4 ? (n_rows & ~1L) : 0;
+    const int n_gt = n_tok >= 4 ? (n_tok & ~3) : 0;
+    const long n_a = n_pr * (n_tok - n_gt), n_items = n_a + (n_rows - n_pr) * n_tok;
+    const long item = ((long)blockIdx.x * THREADS + threadIdx.x) >> 5;
+    if (item >= n_items) return;  // (uniform per half-wave)
+    long r;
+    int t;
+    if (item < n_a) {
+        r = item / (n_tok - n_gt);
+        t = n_gt + (int)(item - r * (n_tok - n_gt));
+    } else {
+        const long k = item - n_a;
+        r = n_pr + k / n_tok;
+        t = (int)(k % n_tok);
+    }
+    const long row = row0 + r;
+    const uint8_t *wr = w + (size_t)row * n_in * (WT == SDY_F32 ? 4 : 2);
+    const float *xr = x + (size_t)t * n_in;
+    float acc = 0.0f;
+    const int n32 = n_in & ~31, n8 = n_in & ~7;
+    int i = L;
+    for (; i + 32 * 7 < n32; i += 32 * 8) {  // 8 steps' loads first, then their chain in order
+        float wv[8], xv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            wv[j] = welem<WT>(wr, i + 32 * j);
+            xv[j] = xr[i + 32 * j];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc = fmaf(wv[j], xv[j], acc);
+    }
+    for (; i < n32; i += 32) acc = fmaf(welem<WT>(wr, i), xr[i], acc);
+    if (L < 8)
+        for (int i = n32 + L; i < n8; i += 8) acc = fmaf(welem<WT>(wr, i), xr[i], acc);
+    // lanes 0..7 of the half: v_l = (a0_l + a1_l) + (a2_l + a3_l)
+    const float a1 = __shfl(acc, base + ((L + 8) & 31)), a2 = __shfl(acc, base + ((L + 16) & 31)),
+                a3 = __shfl(acc, base + ((L + 24) & 31));
+    const float v = (acc + a1) + (a2 + a3);
+    float sum = hsum8_group(v, base);
+    if (L == 0) float_store<WT>(float_tail<WT>(wr, xr, n_in, sum), row, t, out, out_stride, bias, resid);
+}
+
+// block_2x4's order: one (row, token) per 8-lane group, for the paired rows times the tokens of the
+// groups of four (n_tok >= 4).
+template <int WT>
+__global__ __launch_bounds__(THREADS) void k_matvec_float_block(const uint8_t *__restrict__ w, int n_in,
+                                                                const float *__restrict__ x, int n_tok, float *out,
+                                                                long out_stride, const float *bias,
+                                                                const float *resid, long row0, long row1) {
+    const int lane = threadIdx.x & 63, l = lane & 7, base = lane & 56;
+    const long n_pr = (row1 - row0) & ~1L;
+    const int n_gt = n_tok & ~3;
+    const long item = ((long)blockIdx.x * THREADS + threadIdx.x) >> 3;
+    if (item >= n_pr * n_gt) return;  // (uniform per group)
+    const long r = item / n_gt;
+    const int t = (int)(item - r * n_gt);
+    const long row = row0 + r;
+    const uint8_t *wr = w + (size_t)row * n_in * (WT == SDY_F32 ? 4 : 2);
+    const float *xr = x + (size_t)t * n_in;
+    float acc = 0.0f;
+    const int n8 = n_in & ~7;
+    int i = l;
+    for (; i + 8 * 7 < n8; i += 8 * 8) {  // 8 steps' loads first, then their chain in order
+        float wv[8], xv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            wv[j] = welem<WT>(wr, i + 8 * j);
+            xv[j] = xr[i + 8 * j];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc = fmaf(wv[j], xv[j], acc);
+    }
+    for (; i < n8; i += 8) acc = fmaf(welem<WT>(wr, i), xr[i], acc);
+    const float sum = hsum8_group(acc, base);
+    if (l == 0) float_store<WT>(float_tail<WT>(wr, xr, n_in, sum), row, t, out, out_stride, bias, resid);
 }
 
 }  // namespace
@@ -1473,25 +1532,29 @@ extern "C" int sdy_matvec_grouped(const sdy_mat *m, const sdy_mv_args *a, const 
 
 extern "C" int sdy_matvec_float(int wtype, const void *w, int n_in, const sdy_mv_args *a, sdy_stream s) {
     hipStream_t st = (hipStream_t)s;
-    long n = (a->row1 - a->row0) * (long)a->n_tok;
-    if (n <= 0) return 0;
-    long wgs = (n + WAVES - 1) / WAVES;
-    if (wgs > 4096) wgs = 4096;
+    const long n_rows = a->row1 - a->row0;
+    if (n_rows <= 0 || a->n_tok <= 0) return 0;
+    const int n_tok = a->n_tok;
+    const long n_pr = n_tok >= 4 ? (n_rows & ~1L) : 0;
+    const int n_gt = n_tok >= 4 ? (n_tok & ~3) : 0;
+    const long n_block = n_pr * n_gt, n_dot = n_rows * n_tok - n_block;
     const uint8_t *wp = (const uint8_t *)w;
-    switch (wtype) {
-    case SDY_F32:
-        hipLaunchKernelGGL(k_matvec_float<SDY_F32>, dim3((unsigned)wgs), dim3(THREADS), 0, st, wp, n_in, a->x, a->n_tok,
-                           a->out, a->out_stride, a->bias, a->resid, a->row0, a->row1);
-        break;
-    case SDY_F16:
-        hipLaunchKernelGGL(k_matvec_float<SDY_F16>, dim3((unsigned)wgs), dim3(THREADS), 0, st, wp, n_in, a->x, a->n_tok,
-                           a->out, a->out_stride, a->bias, a->resid, a->row0, a->row1);
-        break;
-    case SDY_BF16:
-        hipLaunchKernelGGL(k_matvec_float<SDY_BF16>, dim3((unsigned)wgs), dim3(THREADS), 0, st, wp, n_in, a->x, a->n_tok,
-                           a->out, a->out_stride, a->bias, a->resid, a->row0, a->row1);
-        break;
-    default: return sdy_fail(-1, "float matvec: type %d", wtype);
+    if (wtype != SDY_F32 && wtype != SDY_F16 && wtype != SDY_BF16) return sdy_fail(-1, "float matvec: type %d", wtype);
+#define SDY_FLOAT_LAUNCH(KERNEL, N_ITEMS, PER_WAVE)                                                                  \
+    if ((N_ITEMS) > 0) {                                                                                             \
+        const dim3 grid((unsigned)(((N_ITEMS) + (PER_WAVE) * WAVES - 1) / ((PER_WAVE) * WAVES)));                    \
+        if (wtype == SDY_F32)                                                                                        \
+            hipLaunchKernelGGL(KERNEL<SDY_F32>, grid, dim3(THREADS), 0, st, wp, n_in, a->x, n_tok, a->out,            \
+                               a->out_stride, a->bias, a->resid, a->row0, a->row1);                                  \
+        else if (wtype == SDY_F16)                                                                                   \
+            hipLaunchKernelGGL(KERNEL<SDY_F16>, grid, dim3(THREADS), 0, st, wp, n_in, a->x, n_tok, a->out,            \
+                               a->out_stride, a->bias, a->resid, a->row0, a->row1);                                  \
+        else                                                                                                         \
+            hipLaunchKernelGGL(KERNEL<SDY_BF16>, grid, dim3(THREADS), 0, st, wp, n_in, a->x, n_tok, a->out,           \
+                               a->out_stride, a->bias, a->resid, a->row0, a->row1);                                  \
     }
+    SDY_FLOAT_LAUNCH(k_matvec_float_block, n_block, 8)
+    SDY_FLOAT_LAUNCH(k_matvec_float_dot, n_dot, 2)
+#undef SDY_FLOAT_LAUNCH
     return sdy_check_launch("matvec_float");
 }

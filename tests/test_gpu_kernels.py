@@ -418,6 +418,35 @@ def test_grouped_matvec_rejects_bad_shapes():
     assert L.sdy_matvec_grouped(ctypes.byref(m.m), ctypes.byref(a), top.ptr, 2, 10, 0, 10, None) != 0
 
 
+@pytest.mark.parametrize("wtype", [O.F32, O.F16, O.BF16], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("n_in,n_out,n_tok,r0,r1", [(2048, 128, 1, 0, 128), (2340, 45, 9, 0, 45),
+                                                  (67, 45, 4, 3, 42), (768, 33, 17, 0, 33), (96, 10, 3, 1, 10),
+                                                  (2048, 128, 1024, 0, 128)])
+def test_float_matmul_reference_order_bit_exact(wtype, n_in, n_out, n_tok, r0, r1):
+    """F32/F16/BF16 weights (the MoE router) in the reference's AVX2 order: block_2x4 for paired
+    rows x groups of four tokens, dot for the rest, with the hsum tree and the scalar tail; the
+    bits of the oracle's restatement of csrc/ops_avx2.c."""
+    rng = np.random.default_rng(n_in + n_tok + r0)
+    x = rng.standard_normal((n_tok, n_in)).astype(np.float32)
+    w32 = (rng.standard_normal((n_out, n_in)) * 0.02).astype(np.float32)
+    if wtype == O.F16:
+        w = w32.astype(np.float16)
+    elif wtype == O.BF16:
+        w = (w32.view(np.uint32) >> 16).astype(np.uint16)
+    else:
+        w = w32
+    w = np.ascontiguousarray(w)
+    L = lib()
+    dw, dx = capi.DeviceBuffer.from_array(w), capi.DeviceBuffer.from_array(x)
+    dout = capi.DeviceBuffer.from_array(np.full((n_tok, n_out), np.nan, np.float32))
+    a = capi.SdyMvArgs(x=dx.ptr, n_tok=n_tok, out=dout.ptr, out_stride=n_out, row0=r0, row1=r1)
+    capi.check(L.sdy_matvec_float(wtype, dw.ptr, n_in, ctypes.byref(a), None))
+    got = dout.to_array(np.float32, (n_tok, n_out))
+    exp = np.full((n_tok, n_out), np.nan, np.float32)
+    O.lib().orc_matmul_rows(ptr(exp), ptr(x), ptr(w), wtype, n_tok, n_in, n_out, r0, r1, 1)
+    assert np.array_equal(bits(got[:, r0:r1]), bits(exp[:, r0:r1]))
+
+
 @pytest.mark.parametrize("n_expert,k", [(128, 8), (60, 4), (256, 16), (512, 64), (8, 3)])
 def test_moe_route_and_combine(n_expert, k):
     """Router softmax + top-k (ties to the lowest expert) and the weighted sum of the chosen experts'
@@ -438,10 +467,20 @@ def test_moe_route_and_combine(n_expert, k):
         O.lib().orc_softmax(ptr(p), n_expert)
         et = np.argsort(-p, kind="stable")[:k]
         assert top[t].tolist() == et.tolist(), t
+        # the device takes expf correctly rounded (exp in double, one rounding); the sum in double is
+        # exact here, so the weights are reproduced bit for bit (the host libm's expf is within
+        # 0.502 ulp of the same value: 1e-6 against the oracle)
+        xm = logits[t] - logits[t].max()
+        pc = np.exp(xm.astype(np.float64)).astype(np.float32)
+        pc = pc * np.float32(1.0 / pc.astype(np.float64).sum())
+        sc = np.float32(0)
+        for e in et:
+            sc = np.float32(sc + pc[e])
+        assert np.array_equal(bits(w[t]), bits(pc[et] / sc)), t
         s = np.float32(0)
         for e in et:
             s = np.float32(s + p[e])
-        np.testing.assert_allclose(w[t], p[et] / s, rtol=2e-6)
+        np.testing.assert_allclose(w[t], p[et] / s, rtol=1e-6)
     if k > 16:
         return
     y = rng.standard_normal((n_tok, k, dim)).astype(np.float32)
