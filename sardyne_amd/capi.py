@@ -145,7 +145,7 @@ _DEVICE_SIGNATURES = {
                                   ctypes.c_long, ctypes.c_long, _vp, _vp]),
     "sdy_rmsnorm": (_int, [_vp, _vp, _vp, _int, ctypes.c_float, _int, ctypes.c_long, ctypes.c_long, _vp]),
     "sdy_norm_quant": (_int, [_vp, _vp, ctypes.c_float, _int, _int, _vp, _int, _vp, _vp]),
-    "sdy_attn_part_floats": (_sz, [_int, _int, _int, _int]),
+    "sdy_attn_scores_floats": (_sz, [_int, _int, _int]),
     "sdy_attention": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, ctypes.c_long, ctypes.c_long, _vp, _vp,
                              ctypes.c_long, _vp]),
     "sdy_moe_route": (_int, [_vp, _int, _int, _int, _vp, _vp, _vp]),

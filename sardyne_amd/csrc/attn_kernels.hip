@@ -1,385 +1,35 @@
-// gfx950 attention kernels (the reference's op_attention / attention_worker, csrc/ops.c:405-423 and
-// csrc/model_llama.c:619-640), over the f32 KV cache [n_kv_head][max_seq][head_dim] of a layer.
+// gfx950 attention (the reference's op_attention_head over attention_worker's (token, head) pairs,
+// csrc/ops.c:405-414 and csrc/model_llama.c:619-634) over the f32 KV cache
+// [n_kv_head][max_seq][head_dim] of a layer, with the reference's arithmetic step by step:
+//   score_j = dot(q, k_j) * (1 / sqrtf(head_dim)), dot in the AVX2 order of csrc/ops_avx2.c:61-74
+//     (four 8-lane FMA chains over 32-element steps, 8-element steps into the first chain, the
+//     lane-wise (a0 + a1) + (a2 + a3), the 8-lane tree ((v0 + v4) + (v2 + v6)) + ((v1 + v5) +
+//     (v3 + v7)), a scalar tail);
+//   op_softmax over every position of the token: the maximum, e_j = expf(score_j - max) (the host
+//     libm's expf, sdy_expf.h), their sum in double, the float reciprocal, p_j = e_j * inv;
+//   out = sum over the positions in order of axpy(p_j, v_j): one FMA chain per output element
+//     (head_dim % 8 == 0: AVX2 axpy fuses every element).
+// Only the double sum is taken in a different order (a tree): its rounding can move the float
+// reciprocal only when two double roundings straddle a float rounding boundary.
 //
-// Positions are cut into chunks of CH = 64. A workgroup stages a chunk's K and V in LDS with 16-byte
-// loads and, for each of its tokens, computes the scores of the n_rep query heads that share the KV
-// head and writes per head the chunk maximum m, the sum l of exp(score - m) and the exp-weighted
-// sum o of V. A merge then combines the chunks of each (token, head) in chunk order:
-// M = max m_c, e_c = exp(m_c - M), L = sum l_c e_c, out = (sum o_c e_c) / L. Every path (prefill,
-// the fused decode step, the host-pointer op_attention) uses these same functions, so they agree
-// bit for bit; the result differs from the reference's single softmax only by f32 rounding.
-//
-//   k_attn_partial + k_attn_combine   n tokens at positions n_kv0 - 1 + t (causal), two launches
-//   k_attn_decode                     one token at the position held in device memory: q/k norm,
-//                                     RoPE and the KV-cache write of that position, the chunks, and
-//                                     the merge (plus the quantisation for the next matvec) in the
-//                                     last workgroup to arrive
-//
-// Partial records: o [n_tok][n_head][n_chunk][hd] then (m, l) [n_tok][n_head][n_chunk][2].
+//   k_attn_scores<HD, DECODE>     scores of a 64-position chunk for a block of (token, head) pairs
+//                                 into scores [n_tok][n_head][max_kv]; the decode variant first
+//                                 normalises and rotates q and the new k and writes the new K/V
+//   k_attn_softmax_pv<HD, DECODE> softmax and weighted V of 256 / HD heads of one token (the decode
+//                                 variant also quantises the 256 outputs to a Q8_K block)
+//   k_attn_*_any                  the same for other head dims (runtime loops, scalar LDS reads)
 #include "sdy_device.h"
+#include "sdy_expf.h"
 #include "sdy_internal.h"
 #include "sdy_ops.h"
 #include "sdy_quant_dev.h"
-#include "sdy_attn_dev.h"
 #include "sdy_shim.h"
 
 namespace {
 
-constexpr int CH = 64;
-
-struct ChunkLds {
-    float *ks, *vs, *qs, *ps;  // K [CH][hd+1] (odd stride: conflict-free score reads), V [CH][hd],
-                               // q [n_rep][hd], scores / weights [n_rep][CH]
-};
-
-SDY_DEV ChunkLds chunk_lds(float *sm, int hd, int n_rep) {
-    ChunkLds L;
-    L.ks = sm;
-    L.vs = L.ks + CH * (hd + 1);
-    L.qs = L.vs + CH * hd;
-    L.ps = L.qs + n_rep * hd;
-    return L;
-}
-
-__host__ __device__ inline size_t chunk_lds_floats(int hd, int n_rep) {
-    return (size_t)CH * (hd + 1) + (size_t)CH * hd + (size_t)n_rep * hd + (size_t)n_rep * CH;
-}
-
-// K/V of positions [p0, p0 + np) into LDS, 16 bytes per load (hd % 4 == 0). Position `special`
-// (if in range) takes its K from kspec and its V from vspec instead of the cache.
-template <int NT>
-SDY_DEV void stage_kv(const ChunkLds &L, const float *kg, const float *vg, int np, int hd, int special,
-                      const float *kspec, const float *vspec) {
-    const int n4 = np * hd / 4, tid = threadIdx.x;
-    // batches of B loads per thread (a chunk of 64 x 128 floats is 2048 float4 of K and of V) go out
-    // before their LDS stores (clamped indices, no conditional load), so that their latencies overlap
-    constexpr int B = NT >= 1024 ? 2 : 4;
-    for (int i0 = tid; i0 < n4; i0 += B * NT) {
-        float4 kv[B], vv[B];
-#pragma unroll
-        for (int j = 0; j < B; j++) {
-            const int i = i0 + j * NT < n4 ? i0 + j * NT : i0;
-            kv[j] = reinterpret_cast<const float4 *>(kg)[i];
-            vv[j] = reinterpret_cast<const float4 *>(vg)[i];
-        }
-#pragma unroll
-        for (int j = 0; j < B; j++) {
-            const int i = i0 + j * NT;
-            if (i >= n4) break;
-            const int p = (4 * i) / hd, d = 4 * i - p * hd;
-            if (p == special) continue;
-            float *kr = L.ks + p * (hd + 1) + d;
-            kr[0] = kv[j].x;
-            kr[1] = kv[j].y;
-            kr[2] = kv[j].z;
-            kr[3] = kv[j].w;
-            *reinterpret_cast<float4 *>(L.vs + 4 * i) = vv[j];
-        }
-    }
-    if (special >= 0 && special < np)
-        for (int d = tid; d < hd; d += NT) {
-            L.ks[special * (hd + 1) + d] = kspec[d];
-            L.vs[special * hd + d] = vspec[d];
-        }
-}
-
-// Scores, chunk max / exp-sum and exp-weighted V of n_rep heads over np staged positions (LDS
-// staged and synchronised by the caller). Head r's records: o at o_base + (rec0 + r * rstride) * hd,
-// (m, l) at ml_base + (rec0 + r * rstride) * 2.
-template <int NT>
-SDY_DEV void chunk_attend(const ChunkLds &L, int n_rep, int hd, int np, float scale, float *o_base, float *ml_base,
-                          size_t rec0, int rstride) {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, kstride = hd + 1;
-    for (int i = tid; i < n_rep * CH; i += NT) {
-        const int r = i / CH, p = i - r * CH;
-        float sc = -INFINITY;
-        if (p < np) {
-            const float *qq = L.qs + r * hd, *kk = L.ks + p * kstride;
-            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-            for (int d = 0; d < hd; d += 4) {
-                a0 = fmaf(qq[d], kk[d], a0);
-                a1 = fmaf(qq[d + 1], kk[d + 1], a1);
-                a2 = fmaf(qq[d + 2], kk[d + 2], a2);
-                a3 = fmaf(qq[d + 3], kk[d + 3], a3);
-            }
-            sc = ((a0 + a1) + (a2 + a3)) * scale;
-        }
-        L.ps[i] = sc;
-    }
-    __syncthreads();
-    for (int r = wave; r < n_rep; r += NT / 64) {  // CH == 64: one position per lane
-        float m = L.ps[r * CH + lane];
-        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        const float e = lane < np ? expf(L.ps[r * CH + lane] - m) : 0.0f;
-        L.ps[r * CH + lane] = e;
-        float l = e;
-        for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off);
-        if (lane == 0) {
-            float *ml = ml_base + (rec0 + (size_t)r * rstride) * 2;
-            ml[0] = m;
-            ml[1] = l;
-        }
-    }
-    __syncthreads();
-    for (int i = tid; i < n_rep * hd / 4; i += NT) {
-        const int r = (4 * i) / hd, d = 4 * i - r * hd;
-        const float *pr = L.ps + r * CH;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int p = 0; p < np; p++) {
-            const float w = pr[p];
-            const float4 v = *reinterpret_cast<const float4 *>(L.vs + p * hd + d);
-            acc.x = fmaf(w, v.x, acc.x);
-            acc.y = fmaf(w, v.y, acc.y);
-            acc.z = fmaf(w, v.z, acc.z);
-            acc.w = fmaf(w, v.w, acc.w);
-        }
-        *reinterpret_cast<float4 *>(o_base + (rec0 + (size_t)r * rstride) * hd + d) = acc;
-    }
-}
-
-// ------------------------------------------------------------------ prefill: n tokens, two launches
-
-// Grid (n_chunk, n_kv_head, ceil(n_tok / TB)): tokens tb*TB .. tb*TB + TB - 1, token t attending to
-// positions 0..n_kv0-1+t. The chunk's K and V are staged once for the workgroup's tokens (for the
-// last of them that reaches the chunk); each token then stages its queries and runs chunk_attend
-// over its own np positions, so every record has the bits of a workgroup for that token alone.
-constexpr int TB = 16;
-__global__ __launch_bounds__(256) void k_attn_partial(const float *__restrict__ q, const float *__restrict__ k_cache,
-                                                      const float *__restrict__ v_cache, int n_head, int n_kv_head,
-                                                      int hd, int n_kv0, long head_stride, long q_stride,
-                                                      float *__restrict__ part, int n_tok, int n_chunk_max,
-                                                      float scale) {
-    extern __shared__ float sm[];
-    const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
-    const int t0 = blockIdx.z * TB, t1 = t0 + TB < n_tok ? t0 + TB : n_tok;
-    const int p0 = c * CH;
-    const int n_kv_last = n_kv0 + t1 - 1;
-    if (p0 >= n_kv_last) return;  // no token of the block reaches this chunk
-    const int np_max = n_kv_last - p0 < CH ? n_kv_last - p0 : CH;
-    const int n_rep = n_head / n_kv_head;
-    const ChunkLds L = chunk_lds(sm, hd, n_rep);
-    stage_kv<256>(L, k_cache + g * head_stride + (size_t)p0 * hd, v_cache + g * head_stride + (size_t)p0 * hd, np_max,
-                  hd, -1, nullptr, nullptr);
-    for (int t = t0 < (p0 + 1 - n_kv0) ? (p0 + 1 - n_kv0) : t0; t < t1; t++) {  // tokens that reach the chunk
-        const int n_kv = n_kv0 + t;
-        const int np = n_kv - p0 < CH ? n_kv - p0 : CH;
-        for (int i = tid; i < n_rep * hd; i += 256) L.qs[i] = q[(size_t)t * q_stride + (size_t)g * n_rep * hd + i];
-        __syncthreads();
-        chunk_attend<256>(L, n_rep, hd, np, scale, part, part + (size_t)n_tok * n_head * n_chunk_max * hd,
-                          ((size_t)t * n_head + g * n_rep) * n_chunk_max + c, n_chunk_max);
-    }
-}
-
-// Register-blocked prefill chunk: a workgroup takes R = 64 query rows (TBR = 64 / n_rep tokens x
-// the n_rep heads of KV head g) against the CH = 64 positions of chunk c. K is staged transposed
-// ([HD][64]), V as [64][HD], the scores / weights as [64][64]; the queries are read from global
-// memory (L1). Thread
-// (row group rg, column group cg) computes the scores of rows 4rg..4rg+3 x positions 4cg..4cg+3 and
-// then the weighted V of rows 4rg..4rg+3 x dims (HD/16)cg.. . Every sum has chunk_attend's order
-// (scores: four partial sums by d mod 4, then (a0 + a1) + (a2 + a3); weighted V: one chain over
-// the positions; weights past a row's own positions are exact zeros and leave the chain unchanged),
-// so the records are bit-identical to those of k_attn_partial. 80 KB of LDS: two workgroups, two
-// waves per SIMD, per CU (the register budget is set for that occupancy, so that the next operands
-// can be read while the current ones are multiplied). Token blocks are launched last first.
-template <int HD>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attn_prefill(const float *__restrict__ q, const float *__restrict__ k_cache,
-                                                      const float *__restrict__ v_cache, int n_head, int n_kv_head,
-                                                      int n_kv0, long head_stride, long q_stride,
-                                                      float *__restrict__ part, int n_tok, int n_chunk_max,
-                                                      float scale) {
-    constexpr int R = 64, DG = HD / 16;  // rows per workgroup, dims per thread in the weighted sum
-    extern __shared__ __align__(16) float sm[];
-    float *kT = sm;                // [HD][64]
-    float *vs = kT + HD * CH;      // [64][HD]
-    float *ps = vs + CH * HD;      // [R][64]
-    const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int n_rep = n_head / n_kv_head, tbr = R / n_rep;
-    // the last token blocks reach the most chunks: they are launched first
-    const int blk = (int)gridDim.z - 1 - (int)blockIdx.z;
-    const int t0 = blk * tbr, t1 = t0 + tbr < n_tok ? t0 + tbr : n_tok;
-    const int p0 = c * CH;
-    const int n_kv_last = n_kv0 + t1 - 1;
-    if (p0 >= n_kv_last) return;
-    const int np_max = n_kv_last - p0 < CH ? n_kv_last - p0 : CH;
-    // stage K transposed and V (positions past np_max as zeros), and the queries (rows past the
-    // last token repeat it)
-    // (each batch of 8 loads goes out before its LDS stores: unconditional, clamped addresses, so
-    // that their latencies overlap)
-    const float *kg = k_cache + g * head_stride + (size_t)p0 * HD, *vg = v_cache + g * head_stride + (size_t)p0 * HD;
-    constexpr int NV = CH * HD / 4 / 256;  // float4 of K (and of V) per thread
-    constexpr int NBT = NV < 8 ? NV : 8;   // per batch
-    static_assert(NV % NBT == 0, "batches");
-    for (int b0 = 0; b0 < NV; b0 += NBT) {
-        float4 kv[NBT], vv[NBT];
-#pragma unroll
-        for (int j = 0; j < NBT; j++) {
-            const int i = tid + 256 * (b0 + j);
-            const int pp = i % CH, d4 = i / CH;  // position fastest: conflict-free transposed writes
-            kv[j] = *reinterpret_cast<const float4 *>(kg + (size_t)(pp < np_max ? pp : 0) * HD + 4 * d4);
-            const int pv = (4 * i) / HD;
-            vv[j] = reinterpret_cast<const float4 *>(vg)[pv < np_max ? i : 0];
-        }
-#pragma unroll
-        for (int j = 0; j < NBT; j++) {
-            const int i = tid + 256 * (b0 + j);
-            const int pp = i % CH, d4 = i / CH, pv = (4 * i) / HD;
-            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 k4 = pp < np_max ? kv[j] : z;
-            kT[(4 * d4 + 0) * CH + pp] = k4.x;
-            kT[(4 * d4 + 1) * CH + pp] = k4.y;
-            kT[(4 * d4 + 2) * CH + pp] = k4.z;
-            kT[(4 * d4 + 3) * CH + pp] = k4.w;
-            reinterpret_cast<float4 *>(vs)[i] = pv < np_max ? vv[j] : z;
-        }
-    }
-    __syncthreads();
-    const int rg = tid >> 4, cg = tid & 15;
-    // the thread's 4 query rows, read from global memory (the 16 threads of a row group share them)
-    const float *qrow[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int r = 4 * rg + i, tl = r / n_rep, jj = r - tl * n_rep;
-        const int t = t0 + tl < t1 ? t0 + tl : t1 - 1;
-        qrow[i] = q + (size_t)t * q_stride + (size_t)(g * n_rep + jj) * HD;
-    }
-    {
-        float a[4][4][4];  // [row][position][d mod 4]
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int k = 0; k < 4; k++)
-#pragma unroll
-                for (int m = 0; m < 4; m++) a[i][k][m] = 0.0f;
-        // the next 4 dims' operands are read while the current ones are multiplied
-        float4 qn[4], kn[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) qn[i] = *reinterpret_cast<const float4 *>(qrow[i]);
-#pragma unroll
-        for (int m = 0; m < 4; m++) kn[m] = *reinterpret_cast<const float4 *>(kT + m * CH + 4 * cg);
-        for (int d = 0; d < HD; d += 4) {
-            float4 qv[4], kv[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) qv[i] = qn[i];
-#pragma unroll
-            for (int m = 0; m < 4; m++) kv[m] = kn[m];
-            const int dn = d + 4 < HD ? d + 4 : d;
-#pragma unroll
-            for (int i = 0; i < 4; i++) qn[i] = *reinterpret_cast<const float4 *>(qrow[i] + dn);
-#pragma unroll
-            for (int m = 0; m < 4; m++) kn[m] = *reinterpret_cast<const float4 *>(kT + (dn + m) * CH + 4 * cg);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float qd[4] = {qv[i].x, qv[i].y, qv[i].z, qv[i].w};
-#pragma unroll
-                for (int m = 0; m < 4; m++) {
-                    const float kk[4] = {kv[m].x, kv[m].y, kv[m].z, kv[m].w};
-#pragma unroll
-                    for (int k = 0; k < 4; k++) a[i][k][m] = fmaf(qd[m], kk[k], a[i][k][m]);
-                }
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float4 sc;
-            sc.x = ((a[i][0][0] + a[i][0][1]) + (a[i][0][2] + a[i][0][3])) * scale;
-            sc.y = ((a[i][1][0] + a[i][1][1]) + (a[i][1][2] + a[i][1][3])) * scale;
-            sc.z = ((a[i][2][0] + a[i][2][1]) + (a[i][2][2] + a[i][2][3])) * scale;
-            sc.w = ((a[i][3][0] + a[i][3][1]) + (a[i][3][2] + a[i][3][3])) * scale;
-            *reinterpret_cast<float4 *>(ps + (4 * rg + i) * CH + 4 * cg) = sc;
-        }
-    }
-    __syncthreads();
-    // softmax pieces per row (one wave per row, lane = position), as in chunk_attend
-    float *ml_base = part + (size_t)n_tok * n_head * n_chunk_max * HD;
-    for (int r = wave; r < R; r += 4) {
-        const int tl = r / n_rep, j = r - tl * n_rep, t = t0 + tl;
-        const int np = t < t1 ? (n_kv0 + t - p0 < CH ? n_kv0 + t - p0 : CH) : 0;
-        float e = 0.0f;
-        if (np > 0) {
-            const float sv = lane < np ? ps[r * CH + lane] : -INFINITY;
-            float m = sv;
-            for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-            e = lane < np ? expf(sv - m) : 0.0f;
-            float l = e;
-            for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off);
-            if (lane == 0) {
-                float *ml = ml_base + (((size_t)t * n_head + g * n_rep + j) * n_chunk_max + c) * 2;
-                ml[0] = m;
-                ml[1] = l;
-            }
-        }
-        ps[r * CH + lane] = e;
-    }
-    __syncthreads();
-    // weighted V: rows 4rg..4rg+3, dims DG*cg .. DG*cg + DG - 1, one chain over the positions
-    {
-        float o[4][DG];
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int k = 0; k < DG; k++) o[i][k] = 0.0f;
-        // (the next position's weights and V are read while the current ones are multiplied)
-        float wn[4];
-        float4 vn[DG / 4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) wn[i] = ps[(4 * rg + i) * CH];
-#pragma unroll
-        for (int k = 0; k < DG / 4; k++) vn[k] = *reinterpret_cast<const float4 *>(vs + DG * cg + 4 * k);
-        for (int pp = 0; pp < np_max; pp++) {
-            float w[4];
-            float vv[DG];
-#pragma unroll
-            for (int i = 0; i < 4; i++) w[i] = wn[i];
-#pragma unroll
-            for (int k = 0; k < DG / 4; k++) {
-                vv[4 * k] = vn[k].x;
-                vv[4 * k + 1] = vn[k].y;
-                vv[4 * k + 2] = vn[k].z;
-                vv[4 * k + 3] = vn[k].w;
-            }
-            const int pn = pp + 1 < CH ? pp + 1 : pp;
-#pragma unroll
-            for (int i = 0; i < 4; i++) wn[i] = ps[(4 * rg + i) * CH + pn];
-#pragma unroll
-            for (int k = 0; k < DG / 4; k++) vn[k] = *reinterpret_cast<const float4 *>(vs + pn * HD + DG * cg + 4 * k);
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int k = 0; k < DG; k++) o[i][k] = fmaf(w[i], vv[k], o[i][k]);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = 4 * rg + i, tl = r / n_rep, j = r - tl * n_rep, t = t0 + tl;
-            if (t >= t1 || n_kv0 + t - p0 <= 0) continue;
-            float *ob = part + (((size_t)t * n_head + g * n_rep + j) * n_chunk_max + c) * HD + DG * cg;
-#pragma unroll
-            for (int k = 0; k < DG; k += 4) *reinterpret_cast<float4 *>(ob + k) = make_float4(o[i][k], o[i][k + 1], o[i][k + 2], o[i][k + 3]);
-        }
-    }
-}
-
-// Grid (n_head, n_tok), 128 threads.
-__global__ __launch_bounds__(128) void k_attn_combine(const float *__restrict__ part, int n_head, int hd, int n_kv0,
-                                                      int n_tok, int n_chunk_max, float *__restrict__ out,
-                                                      long out_stride) {
-    extern __shared__ float e[];  // [n_chunk_max] weights, then [n_chunk_max] scratch
-    __shared__ float sL;
-    const int h = blockIdx.x, t = blockIdx.y;
-    const int n_kv = n_kv0 + t, nc = (n_kv + CH - 1) / CH;
-    const size_t rec0 = ((size_t)t * n_head + h) * n_chunk_max;
-    const float *o = part + rec0 * hd;
-    const float *ml = part + (size_t)n_tok * n_head * n_chunk_max * hd + rec0 * 2;
-    if (threadIdx.x < 64) {
-        const float L = merge_weights_wave(ml, nc, e, e + n_chunk_max, threadIdx.x);
-        if (threadIdx.x == 0) sL = L;
-    }
-    __syncthreads();
-    for (int d = 4 * threadIdx.x; d < hd; d += 4 * blockDim.x)
-        *reinterpret_cast<float4 *>(out + (size_t)t * out_stride + (size_t)h * hd + d) =
-            merge4(o, n_chunk_max, nc, hd, d, e, sL);
-}
-
-// ------------------------------------------------------------------ one-token decode, one launch
+constexpr int CH = 64;       // positions per scores workgroup (one per lane)
+constexpr int PAIRS = 64;    // (token, head) pairs per prefill scores workgroup
+constexpr int PW = 8192;     // weights held in LDS at a time by k_attn_softmax_pv (all its heads)
 
 // One wave: optional per-head RMSNorm (qwen3 q/k norm: double sum, one rounding of the scale) then
 // RoPE (pairs (i, i + hd/2), or (2i, 2i+1) when interleaved) of the hd-vector in buf (LDS).
@@ -435,194 +85,448 @@ __global__ __launch_bounds__(64) void k_qk_rope_kv(float *q, float *k, const flo
     }
 }
 
-struct AttnDecodeArgs {
-    const float *q, *k, *v;          // this token's projections: [n_head][hd], [n_kv_head][hd] x 2
-    const float *q_norm, *k_norm;    // per-head norm weights or null
+struct AttnArgs {
+    const float *q;                   // prefill: rotated queries [n_tok][q_stride]; decode: raw [n_head][HD]
+    const float *k, *v;               // decode: the token's raw k and v [n_kv_head][HD]
+    const float *q_norm, *k_norm;     // decode: per-head norm weights or null
     float eps;
     const float *rope_cos, *rope_sin;
-    const int32_t *step;             // step[1] = position of the token
-    int n_head, n_kv_head, hd, interleaved;
-    float *k_cache, *v_cache;        // this layer: [n_kv_head][max_seq][hd]
-    long head_stride;                // max_seq * hd
-    float *part;                     // partial records of one token
-    int n_chunk_max;
+    const int32_t *step;              // decode: step[1] = position of the token
+    int n_head, n_kv_head, n_kv0, n_tok, interleaved;
+    long q_stride;
+    float *k_cache, *v_cache;         // [n_kv_head][max_seq][HD]
+    long head_stride;                 // max_seq * HD
+    float *scores;                    // [n_tok][n_head][max_kv]
+    int max_kv;
     float scale;
+    float *out;                       // [n_tok][out_stride]
+    long out_stride;
+    uint8_t *xq;                      // decode: Q8_K row of out (or null)
 };
 
-// Grid (n_chunk_max, n_kv_head), DEC_NT threads (8 waves); chunks past the position exit at once.
-// Writes the partial records of every chunk; the merge is a separate launch (k_attn_merge1*).
-// The chunk's K and V loads go out first; meanwhile each wave normalises and rotates its query
-// heads (and one wave the new position's k, which it also writes to the cache). After one barrier
-// wave w takes heads w, w + 8, ...: lane p computes the score of position p with chunk_attend's
-// four partial sums (d mod 4), the wave forms m, l and the weights as chunk_attend does, and lane l
-// accumulates dims l, l + 64, ... of the weighted V over the positions in order (the weight of
-// position p read from lane p). The records are therefore those of chunk_attend, bit for bit.
-constexpr int DEC_NT = 512, DEC_W = DEC_NT / 64;
-
+// dot(q, k) in csrc/ops_avx2.c:61-74's order (x = q, w = k), both in LDS, q 16-byte aligned.
 template <int HD>
-__global__ __launch_bounds__(DEC_NT) void k_attn_decode(AttnDecodeArgs a) {
-    constexpr int KS = HD + 1;            // K row stride (odd: conflict-free reads by position)
-    constexpr int NV = CH * HD / 4 / DEC_NT;  // float4 of K (and of V) per thread
-    static_assert(NV >= 1 && NV * DEC_NT * 4 == CH * HD, "chunk");
-    extern __shared__ float sm[];
-    float *ks = sm;                       // [CH][HD + 1]
-    float *vs = ks + CH * KS;             // [CH][HD]
-    float *kp = vs + CH * HD;             // [HD]: normalised, rotated k of the new position
-    float *qs = kp + HD;                  // [n_rep][HD]
-    const int c = blockIdx.x, g = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
-    const int pos = a.step[1], n_kv = pos + 1;
-    const int nch = (n_kv + CH - 1) / CH;
-    if (c >= nch) return;
+SDY_DEV float dot_avx2_order(const float *q, const float *k) {
+    constexpr int N32 = HD / 32 * 32, N8 = HD / 8 * 8;
+    float a[4][8];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int l = 0; l < 8; l++) a[c][l] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N32; i += 32)
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float4 q0 = *reinterpret_cast<const float4 *>(q + i + 8 * c);
+            const float4 q1 = *reinterpret_cast<const float4 *>(q + i + 8 * c + 4);
+            const float4 k0 = *reinterpret_cast<const float4 *>(k + i + 8 * c);
+            const float4 k1 = *reinterpret_cast<const float4 *>(k + i + 8 * c + 4);
+            a[c][0] = fmaf(k0.x, q0.x, a[c][0]);
+            a[c][1] = fmaf(k0.y, q0.y, a[c][1]);
+            a[c][2] = fmaf(k0.z, q0.z, a[c][2]);
+            a[c][3] = fmaf(k0.w, q0.w, a[c][3]);
+            a[c][4] = fmaf(k1.x, q1.x, a[c][4]);
+            a[c][5] = fmaf(k1.y, q1.y, a[c][5]);
+            a[c][6] = fmaf(k1.z, q1.z, a[c][6]);
+            a[c][7] = fmaf(k1.w, q1.w, a[c][7]);
+        }
+#pragma unroll
+    for (int i = N32; i < N8; i += 8)
+#pragma unroll
+        for (int l = 0; l < 8; l++) a[0][l] = fmaf(k[i + l], q[i + l], a[0][l]);
+    float v[8];
+#pragma unroll
+    for (int l = 0; l < 8; l++) {
+        const float p = a[0][l] + a[1][l], r = a[2][l] + a[3][l];
+        v[l] = p + r;
+    }
+    float s = ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]));
+#pragma unroll
+    for (int i = N8; i < HD; i++) {
+        const float p = q[i] * k[i];
+        s = s + p;
+    }
+    return s;
+}
+
+// Grid (n_chunk, n_kv_head, token blocks), 256 threads. Prefill: the block's tokens are
+// PAIRS / n_rep consecutive tokens (queries already rotated, K/V already in the cache). Decode: one
+// token at position step[1]; every workgroup normalises and rotates the group's queries and the
+// new k in LDS, the workgroup of the last chunk writes the new K/V to the cache, and the new
+// position's K comes from LDS. Lane p of a wave computes the score of position p0 + p for one
+// (token, head) pair; the waves share the staged K chunk ([CH][HD + 4]: 16-byte rows, 8
+// consecutive rows in distinct banks).
+template <int HD, bool DECODE>
+__global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
+    constexpr int KS = HD + 4;
+    constexpr int NV = CH * HD / 4 / 256 > 0 ? CH * HD / 4 / 256 : 1;  // float4 of K per thread
+    extern __shared__ __align__(16) float sm[];
+    float *ks = sm;            // [CH][KS]
+    float *kp = ks + CH * KS;  // [HD]: the new position's rotated k (decode)
+    float *qs = kp + HD;       // [pairs][HD]
+    const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int n_rep = a.n_head / a.n_kv_head;
-    const int p0 = c * CH, np = n_kv - p0 < CH ? n_kv - p0 : CH;
-    const bool has_pos = c == nch - 1;  // this chunk holds the new position
-    // 0. the chunk's K and V from the cache (clamped indices: every load is unconditional)
-    const float *kg = a.k_cache + g * a.head_stride + (size_t)p0 * HD, *vg = a.v_cache + g * a.head_stride + (size_t)p0 * HD;
-    const int n4 = np * HD / 4;
-    float4 kv[NV], vv[NV];
+    int t0, t1, n_kv_last, pos = 0;
+    if constexpr (DECODE) {
+        pos = a.step[1];
+        t0 = 0;
+        t1 = 1;
+        n_kv_last = pos + 1;
+    } else {
+        const int tbs = PAIRS / n_rep > 0 ? PAIRS / n_rep : 1;
+        t0 = blockIdx.z * tbs;
+        t1 = t0 + tbs < a.n_tok ? t0 + tbs : a.n_tok;
+        n_kv_last = a.n_kv0 + t1 - 1;
+    }
+    const int p0 = c * CH;
+    if (p0 >= n_kv_last) return;
+    const int np_max = n_kv_last - p0 < CH ? n_kv_last - p0 : CH;
+    // K chunk loads first (clamped indices, unconditional)
+    const float *kg = a.k_cache + g * a.head_stride + (size_t)p0 * HD;
+    const int n4 = np_max * HD / 4;
+    float4 kv[NV];
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-        const int i = tid + j * DEC_NT < n4 ? tid + j * DEC_NT : 0;
+        const int i = tid + 256 * j < n4 ? tid + 256 * j : 0;
         kv[j] = reinterpret_cast<const float4 *>(kg)[i];
-        vv[j] = reinterpret_cast<const float4 *>(vg)[i];
     }
-    // 1. q heads of this group (and k of the new position): norm + RoPE in LDS
-    const float *cs = a.rope_cos + (size_t)pos * (HD / 2), *sn = a.rope_sin + (size_t)pos * (HD / 2);
-    const int tasks = n_rep + (has_pos ? 1 : 0);
-    for (int r = wave; r < tasks; r += DEC_W) {
-        const bool is_k = r == n_rep;
-        float *buf = is_k ? kp : qs + r * HD;
-        const float *src = is_k ? a.k + (size_t)g * HD : a.q + (size_t)(g * n_rep + r) * HD;
-        for (int i = lane; i < HD; i += 64) buf[i] = src[i];
-        sdy_wave_sync();
-        norm_rope_wave(buf, is_k ? a.k_norm : a.q_norm, a.eps, cs, sn, HD, a.interleaved, lane);
-        if (is_k) {  // KV-cache write of the new position
-            float *kc = a.k_cache + g * a.head_stride + (size_t)pos * HD;
-            float *vc = a.v_cache + g * a.head_stride + (size_t)pos * HD;
-            const float *vn = a.v + (size_t)g * HD;
-            for (int i = lane; i < HD; i += 64) {
-                kc[i] = buf[i];
-                vc[i] = vn[i];
+    const int n_pairs = (t1 - t0) * n_rep;
+    bool has_pos = false;
+    if constexpr (DECODE) {
+        // q heads of the group and the new k: norm + RoPE in LDS (one wave per vector)
+        has_pos = p0 + np_max == pos + 1;
+        const float *cs = a.rope_cos + (size_t)pos * (HD / 2), *sn = a.rope_sin + (size_t)pos * (HD / 2);
+        for (int r = wave; r <= n_rep; r += 4) {
+            const bool is_k = r == n_rep;
+            float *buf = is_k ? kp : qs + r * HD;
+            const float *src = is_k ? a.k + (size_t)g * HD : a.q + (size_t)(g * n_rep + r) * HD;
+            for (int i = lane; i < HD; i += 64) buf[i] = src[i];
+            sdy_wave_sync();
+            norm_rope_wave(buf, is_k ? a.k_norm : a.q_norm, a.eps, cs, sn, HD, a.interleaved, lane);
+            if (is_k && has_pos) {  // KV-cache write of the new position
+                float *kc = a.k_cache + g * a.head_stride + (size_t)pos * HD;
+                float *vc = a.v_cache + g * a.head_stride + (size_t)pos * HD;
+                const float *vn = a.v + (size_t)g * HD;
+                for (int i = lane; i < HD; i += 64) {
+                    kc[i] = buf[i];
+                    vc[i] = vn[i];
+                }
             }
         }
+    } else {
+        for (int i = tid; i < n_pairs * HD / 4; i += 256) {
+            const int pr = (4 * i) / HD, d = 4 * i - pr * HD;
+            const int tl = pr / n_rep, r = pr - tl * n_rep;
+            *reinterpret_cast<float4 *>(qs + pr * HD + d) = *reinterpret_cast<const float4 *>(
+                a.q + (size_t)(t0 + tl) * a.q_stride + (size_t)(g * n_rep + r) * HD + d);
+        }
     }
-    // 2. the chunk into LDS (the new position from LDS / the raw v: its cache entry is written above)
-    const int special = has_pos ? pos - p0 : -1;
+    const int special = DECODE && has_pos ? pos - p0 : -1;
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-        const int i = tid + j * DEC_NT;
+        const int i = tid + 256 * j;
         if (i >= n4) break;
         const int p = (4 * i) / HD, d = 4 * i - p * HD;
         if (p == special) continue;
-        float *kr = ks + p * KS + d;
-        kr[0] = kv[j].x;
-        kr[1] = kv[j].y;
-        kr[2] = kv[j].z;
-        kr[3] = kv[j].w;
-        *reinterpret_cast<float4 *>(vs + 4 * i) = vv[j];
+        *reinterpret_cast<float4 *>(ks + p * KS + d) = kv[j];
     }
-    __syncthreads();  // (also orders the k of the new position in kp before its use below)
-    if (special >= 0)
-        for (int d = tid; d < HD; d += DEC_NT) {
-            ks[special * KS + d] = kp[d];
-            vs[special * HD + d] = a.v[(size_t)g * HD + d];
-        }
     __syncthreads();
-    // 3. per head: scores (lane = position), weights, weighted V (lane = dims)
-    float *o_base = a.part, *ml_base = a.part + (size_t)a.n_head * a.n_chunk_max * HD;
-    for (int r = wave; r < n_rep; r += DEC_W) {
-        const float *qq = qs + r * HD;
-        float sc = -INFINITY;
+    if constexpr (DECODE) {
+        if (special >= 0)
+            for (int d = tid; d < HD; d += 256) ks[special * KS + d] = kp[d];
+        __syncthreads();
+    }
+    for (int pr = wave; pr < n_pairs; pr += 4) {
+        const int tl = pr / n_rep, r = pr - tl * n_rep, t = t0 + tl;
+        const int n_kv = DECODE ? pos + 1 : a.n_kv0 + t;
+        const int np = n_kv - p0 < CH ? n_kv - p0 : CH;
         if (lane < np) {
-            const float *kk = ks + lane * KS;
-            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll 8
-            for (int d = 0; d < HD; d += 4) {
-                const float4 q4 = *reinterpret_cast<const float4 *>(qq + d);
-                a0 = fmaf(q4.x, kk[d], a0);
-                a1 = fmaf(q4.y, kk[d + 1], a1);
-                a2 = fmaf(q4.z, kk[d + 2], a2);
-                a3 = fmaf(q4.w, kk[d + 3], a3);
+            const float s = dot_avx2_order<HD>(qs + pr * HD, ks + lane * KS) * a.scale;
+            a.scores[((size_t)t * a.n_head + g * n_rep + r) * a.max_kv + p0 + lane] = s;
+        }
+    }
+}
+
+// Grid (n_head * HD / 256, n_tok), 256 threads: thread (head h = h0 + tid / HD, element d = tid % HD).
+// Per head: max and the double sum of e_j over the token's positions (reductions across the head's
+// threads), then the weights in LDS (PW / HPB positions per head at a time) and out[d] = one FMA
+// chain over the positions in order. Decode: the 256 outputs (one Q8_K block) are also quantised to xq.
+template <int HD, bool DECODE>
+__global__ __launch_bounds__(256) void k_attn_softmax_pv(AttnArgs a) {
+    constexpr int HPB = 256 / HD, GW = HD < 64 ? HD : 64;  // heads per block, lanes per head in a wave
+    constexpr int PB = PW / HPB;                           // weights per head per pass
+    static_assert(HD * HPB == 256, "head_dim divides 256");
+    __shared__ float pw[HPB][PB];
+    __shared__ float redf[4];
+    __shared__ double redd[4];
+    __shared__ float obuf[256];
+    const int tid = threadIdx.x, hl = tid / HD, d = tid - hl * HD, wave = tid >> 6;
+    const int t = blockIdx.y;
+    // (a last, partial group of heads repeats the last head in its spare threads, which store nothing)
+    const int h_raw = blockIdx.x * HPB + hl, h = h_raw < a.n_head ? h_raw : a.n_head - 1;
+    const int n_rep = a.n_head / a.n_kv_head, g = h / n_rep;
+    const int n = DECODE ? a.step[1] + 1 : a.n_kv0 + t;
+    const float *row = a.scores + ((size_t)t * a.n_head + h) * a.max_kv;
+    // maximum over the head's positions
+    float m = -INFINITY;
+    for (int j = d; j < n; j += HD) m = fmaxf(m, row[j]);
+    for (int off = GW / 2; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if constexpr (HD > 64) {
+        if ((tid & 63) == 0) redf[wave] = m;
+        __syncthreads();
+        m = -INFINITY;
+        for (int w = 0; w < HD / 64; w++) m = fmaxf(m, redf[hl * (HD / 64) + w]);
+    }
+    // sum of expf(score - max) in double
+    double sum = 0.0;
+    for (int j = d; j < n; j += HD) sum += (double)sdy_expf(row[j] - m);
+    for (int off = GW / 2; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+    if constexpr (HD > 64) {
+        if ((tid & 63) == 0) redd[wave] = sum;
+        __syncthreads();
+        sum = 0.0;
+        for (int w = 0; w < HD / 64; w++) sum += redd[hl * (HD / 64) + w];
+    }
+    const float inv = (float)(1.0 / sum);
+    // weighted V, PB positions at a time
+    const float *vg = a.v_cache + g * a.head_stride + d;
+    float acc = 0.0f;
+    for (int jb = 0; jb < n; jb += PB) {
+        const int je = jb + PB < n ? jb + PB : n;
+        __syncthreads();
+        for (int j = jb + d; j < je; j += HD) pw[hl][j - jb] = sdy_expf(row[j] - m) * inv;
+        __syncthreads();
+        int j = jb;
+        for (; j + 8 <= je; j += 8) {
+            float vv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) vv[u] = vg[(size_t)(j + u) * HD];
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc = fmaf(pw[hl][j + u - jb], vv[u], acc);
+        }
+        for (; j < je; j++) acc = fmaf(pw[hl][j - jb], vg[(size_t)j * HD], acc);
+    }
+    if (h_raw < a.n_head) a.out[(size_t)t * a.out_stride + (size_t)h * HD + d] = acc;
+    if constexpr (DECODE) {
+        if (a.xq) {  // (n_head * HD is a multiple of 256 here: whole blocks)
+            obuf[tid] = acc;
+            __syncthreads();
+            if (wave == 0) {
+                const int lane = tid;
+                const float xs[4] = {obuf[4 * lane], obuf[4 * lane + 1], obuf[4 * lane + 2], obuf[4 * lane + 3]};
+                sdy_q8k_block(xs, lane, a.xq + (size_t)blockIdx.x * 292);
             }
-            sc = ((a0 + a1) + (a2 + a3)) * a.scale;
         }
-        float m = sc;
-        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        const float e = lane < np ? expf(sc - m) : 0.0f;
-        float l = e;
-        for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off);
-        const size_t rec = (size_t)(g * n_rep + r) * a.n_chunk_max + c;
-        if (lane == 0) {
-            ml_base[rec * 2] = m;
-            ml_base[rec * 2 + 1] = l;
-        }
-        float acc[HD / 64];
-#pragma unroll
-        for (int k = 0; k < HD / 64; k++) acc[k] = 0.0f;
-        for (int p = 0; p < np; p++) {
-            const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), p));
-#pragma unroll
-            for (int k = 0; k < HD / 64; k++) acc[k] = fmaf(w, vs[p * HD + lane + 64 * k], acc[k]);
-        }
-#pragma unroll
-        for (int k = 0; k < HD / 64; k++) o_base[rec * HD + lane + 64 * k] = acc[k];
     }
 }
 
-// Merge of one token's partial records (position in step[1]) into out [n_head * hd], for output
-// projections without an activation prologue. Grid n_head, one wave each.
-__global__ __launch_bounds__(64) void k_attn_merge1(const float *__restrict__ part, const int32_t *__restrict__ step,
-                                                    int n_head, int hd, int n_chunk_max, float *__restrict__ out) {
-    extern __shared__ float e[];  // [n_chunk_max] weights, [n_chunk_max] scratch
-    const int h = blockIdx.x, lane = threadIdx.x;
-    const int nch = (step[1] + 1 + CH - 1) / CH;
-    const float *ml = part + (size_t)n_head * n_chunk_max * hd + (size_t)h * n_chunk_max * 2;
-    const float L = merge_weights_wave(ml, nch, e, e + n_chunk_max, lane);
-    for (int d = 4 * lane; d < hd; d += 256)
-        *reinterpret_cast<float4 *>(out + (size_t)h * hd + d) =
-            merge4(part + (size_t)h * n_chunk_max * hd, n_chunk_max, nch, hd, d, e, L);
+// Any head_dim (hd % 4 == 0 is not required): the same arithmetic with runtime loops and scalar LDS
+// reads. Scores: as k_attn_scores (prefill or decode), K rows at an odd stride (hd | 1).
+SDY_DEV float dot_avx2_order_any(const float *q, const float *k, int hd) {
+    float a[4][8];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int l = 0; l < 8; l++) a[c][l] = 0.0f;
+    int i = 0;
+    for (; i + 32 <= hd; i += 32)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int l = 0; l < 8; l++) a[c][l] = fmaf(k[i + 8 * c + l], q[i + 8 * c + l], a[c][l]);
+    for (; i + 8 <= hd; i += 8)
+#pragma unroll
+        for (int l = 0; l < 8; l++) a[0][l] = fmaf(k[i + l], q[i + l], a[0][l]);
+    float v[8];
+#pragma unroll
+    for (int l = 0; l < 8; l++) {
+        const float p = a[0][l] + a[1][l], r = a[2][l] + a[3][l];
+        v[l] = p + r;
+    }
+    float s = ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]));
+    for (; i < hd; i++) {
+        const float p = q[i] * k[i];
+        s = s + p;
+    }
+    return s;
 }
 
-// Merge of one token's records into the Q8_K row of the output projection: one wave per 256-element
-// super-block (lane l: elements 4l..4l+3), the merge weights of the super-block's heads in LDS, the
-// merged values also written to out (f32).
-__global__ __launch_bounds__(64) void k_attn_merge1_q8k(const float *__restrict__ part,
-                                                        const int32_t *__restrict__ step, int n_head, int hd,
-                                                        int n_chunk_max, float *__restrict__ out,
-                                                        uint8_t *__restrict__ xq) {
-    extern __shared__ float sm[];  // per head of the super-block: [n_chunk_max] weights, [n_chunk_max] scratch
-    __shared__ float sL[64];
-    const int sb = blockIdx.x, lane = threadIdx.x;
-    const int nch = (step[1] + 1 + CH - 1) / CH;
-    const int h0 = 256 * sb / hd, h1 = (256 * sb + 255) / hd;
-    const float *ml = part + (size_t)n_head * n_chunk_max * hd;
-    for (int h = h0; h <= h1; h++) {
-        const float L = merge_weights_wave(ml + (size_t)h * n_chunk_max * 2, nch, sm + (h - h0) * 2 * n_chunk_max,
-                                           sm + (h - h0) * 2 * n_chunk_max + n_chunk_max, lane);
-        if (lane == 0) sL[h - h0] = L;
+template <bool DECODE>
+__global__ __launch_bounds__(256) void k_attn_scores_any(AttnArgs a, int hd) {
+    extern __shared__ __align__(16) float sm[];
+    const int KS = hd | 1;
+    float *ks = sm;            // [CH][KS]
+    float *kp = ks + CH * KS;  // [hd]
+    float *qs = kp + hd;       // [pairs][hd]
+    const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int n_rep = a.n_head / a.n_kv_head;
+    int t0, t1, n_kv_last, pos = 0;
+    if constexpr (DECODE) {
+        pos = a.step[1];
+        t0 = 0;
+        t1 = 1;
+        n_kv_last = pos + 1;
+    } else {
+        const int tbs = PAIRS / n_rep > 0 ? PAIRS / n_rep : 1;
+        t0 = blockIdx.z * tbs;
+        t1 = t0 + tbs < a.n_tok ? t0 + tbs : a.n_tok;
+        n_kv_last = a.n_kv0 + t1 - 1;
     }
-    sdy_wave_sync();
-    const int e0 = 256 * sb + 4 * lane, h = e0 / hd, d = e0 - h * hd;
-    const float4 v =
-        merge4(part + (size_t)h * n_chunk_max * hd, n_chunk_max, nch, hd, d, sm + (h - h0) * 2 * n_chunk_max, sL[h - h0]);
-    *reinterpret_cast<float4 *>(out + e0) = v;
-    const float xs[4] = {v.x, v.y, v.z, v.w};
-    sdy_q8k_block(xs, lane, xq + (size_t)sb * 292);
+    const int p0 = c * CH;
+    if (p0 >= n_kv_last) return;
+    const int np_max = n_kv_last - p0 < CH ? n_kv_last - p0 : CH;
+    const int n_pairs = (t1 - t0) * n_rep;
+    bool has_pos = false;
+    if constexpr (DECODE) {
+        has_pos = p0 + np_max == pos + 1;
+        const float *cs = a.rope_cos + (size_t)pos * (hd / 2), *sn = a.rope_sin + (size_t)pos * (hd / 2);
+        for (int r = wave; r <= n_rep; r += 4) {
+            const bool is_k = r == n_rep;
+            float *buf = is_k ? kp : qs + r * hd;
+            const float *src = is_k ? a.k + (size_t)g * hd : a.q + (size_t)(g * n_rep + r) * hd;
+            for (int i = lane; i < hd; i += 64) buf[i] = src[i];
+            sdy_wave_sync();
+            norm_rope_wave(buf, is_k ? a.k_norm : a.q_norm, a.eps, cs, sn, hd, a.interleaved, lane);
+            if (is_k && has_pos) {
+                float *kc = a.k_cache + g * a.head_stride + (size_t)pos * hd;
+                float *vc = a.v_cache + g * a.head_stride + (size_t)pos * hd;
+                for (int i = lane; i < hd; i += 64) {
+                    kc[i] = buf[i];
+                    vc[i] = a.v[(size_t)g * hd + i];
+                }
+            }
+        }
+    } else {
+        for (int i = tid; i < n_pairs * hd; i += 256) {
+            const int pr = i / hd, d = i - pr * hd, tl = pr / n_rep, r = pr - tl * n_rep;
+            qs[pr * hd + d] = a.q[(size_t)(t0 + tl) * a.q_stride + (size_t)(g * n_rep + r) * hd + d];
+        }
+    }
+    const int special = DECODE && has_pos ? pos - p0 : -1;
+    const float *kg = a.k_cache + g * a.head_stride + (size_t)p0 * hd;
+    for (int i = tid; i < np_max * hd; i += 256) {
+        const int p = i / hd, d = i - p * hd;
+        if (p != special) ks[p * KS + d] = kg[i];
+    }
+    __syncthreads();
+    if constexpr (DECODE) {
+        if (special >= 0)
+            for (int d = tid; d < hd; d += 256) ks[special * KS + d] = kp[d];
+        __syncthreads();
+    }
+    for (int pr = wave; pr < n_pairs; pr += 4) {
+        const int tl = pr / n_rep, r = pr - tl * n_rep, t = t0 + tl;
+        const int n_kv = DECODE ? pos + 1 : a.n_kv0 + t;
+        const int np = n_kv - p0 < CH ? n_kv - p0 : CH;
+        if (lane < np)
+            a.scores[((size_t)t * a.n_head + g * n_rep + r) * a.max_kv + p0 + lane] =
+                dot_avx2_order_any(qs + pr * hd, ks + lane * KS, hd) * a.scale;
+    }
+}
+
+// Softmax and weighted V of one head of one token per workgroup (256 threads; output elements
+// tid, tid + 256, ...), any head_dim. Decode: no Q8_K output (the caller quantises).
+template <bool DECODE>
+__global__ __launch_bounds__(256) void k_attn_softmax_pv_any(AttnArgs a, int hd) {
+    __shared__ float pw[PW];
+    __shared__ float redf[4];
+    __shared__ double redd[4];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h = blockIdx.x, t = blockIdx.y;
+    const int n_rep = a.n_head / a.n_kv_head, g = h / n_rep;
+    const int n = DECODE ? a.step[1] + 1 : a.n_kv0 + t;
+    const float *row = a.scores + ((size_t)t * a.n_head + h) * a.max_kv;
+    float m = -INFINITY;
+    for (int j = tid; j < n; j += 256) m = fmaxf(m, row[j]);
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if (lane == 0) redf[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
+    double sum = 0.0;
+    for (int j = tid; j < n; j += 256) sum += (double)sdy_expf(row[j] - m);
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+    if (lane == 0) redd[wave] = sum;
+    __syncthreads();
+    sum = (redd[0] + redd[1]) + (redd[2] + redd[3]);
+    const float inv = (float)(1.0 / sum);
+    const float *vg = a.v_cache + g * a.head_stride;
+    for (int d0 = 0; d0 < hd; d0 += 256) {
+        const int d = d0 + tid;
+        float acc = 0.0f;
+        for (int jb = 0; jb < n; jb += PW) {
+            const int je = jb + PW < n ? jb + PW : n;
+            __syncthreads();
+            for (int j = jb + tid; j < je; j += 256) pw[j - jb] = sdy_expf(row[j] - m) * inv;
+            __syncthreads();
+            if (d < hd)
+                for (int j = jb; j < je; j++) acc = fmaf(pw[j - jb], vg[(size_t)j * hd + d], acc);
+        }
+        if (d < hd) a.out[(size_t)t * a.out_stride + (size_t)h * hd + d] = acc;
+    }
 }
 
 }  // namespace
 
 // =============================================================================== launchers
 
-extern "C" size_t sdy_attn_part_floats(int n_tok, int n_head, int hd, int max_kv) {
-    int nc = (max_kv + CH - 1) / CH;
-    return (size_t)n_tok * n_head * nc * (hd + 2);
+extern "C" size_t sdy_attn_scores_floats(int n_tok, int n_head, int max_kv) {
+    return (size_t)n_tok * n_head * max_kv;
 }
 
-static int shape_ok(int n_head, int n_kv_head, int hd) {
-    if (hd > 512 || hd % 4 || n_kv_head < 1 || n_head % n_kv_head)
-        return sdy_fail(-1, "attention: head_dim %d / %d heads / %d kv heads not supported", hd, n_head, n_kv_head);
+static int head_dim_ok(int n_head, int n_kv_head, int hd) {
+    return hd >= 1 && hd <= 1024 && n_kv_head >= 1 && n_head % n_kv_head == 0 && n_head / n_kv_head <= PAIRS;
+}
+
+static int shape_fail(int n_head, int n_kv_head, int hd) {
+    return sdy_fail(-1, "attention: head_dim %d with %d heads / %d kv heads not supported (head_dim up to 1024, at "
+                        "most %d query heads per kv head)", hd, n_head, n_kv_head, PAIRS);
+}
+
+static size_t scores_lds(int hd, int n_pairs) {
+    return sizeof(float) * ((size_t)CH * (hd + 4) + hd + (size_t)n_pairs * hd);
+}
+
+template <int HD, bool DECODE>
+static int launch_attn(AttnArgs &A, int nc, int n_tblk, hipStream_t st) {
+    const int n_rep = A.n_head / A.n_kv_head;
+    const int n_pairs = DECODE ? n_rep : (PAIRS / n_rep > 0 ? PAIRS / n_rep : 1) * n_rep;
+    const size_t lds = scores_lds(HD, n_pairs);
+    static size_t granted = 0;
+    int rc = sdy_lds_limit((const void *)k_attn_scores<HD, DECODE>, lds, &granted);
+    if (rc) return rc;
+    hipLaunchKernelGGL((k_attn_scores<HD, DECODE>), dim3(nc, A.n_kv_head, n_tblk), dim3(256), lds, st, A);
+    if ((rc = sdy_check_launch("attention_scores"))) return rc;
+    hipLaunchKernelGGL((k_attn_softmax_pv<HD, DECODE>), dim3((A.n_head * HD + 255) / 256, DECODE ? 1 : A.n_tok), dim3(256),
+                       0, st, A);
+    return sdy_check_launch("attention_softmax_pv");
+}
+
+template <bool DECODE>
+static int launch_attn_any(AttnArgs &A, int hd, int nc, int n_tblk, hipStream_t st) {
+    const int n_rep = A.n_head / A.n_kv_head;
+    const int n_pairs = DECODE ? n_rep : (PAIRS / n_rep > 0 ? PAIRS / n_rep : 1) * n_rep;
+    const size_t lds = sizeof(float) * ((size_t)CH * (hd | 1) + hd + (size_t)n_pairs * hd);
+    if (lds > 160 * 1024) return sdy_fail(-1, "attention: head_dim %d needs %zu bytes of LDS", hd, lds);
+    static size_t granted = 0;
+    int rc = sdy_lds_limit((const void *)k_attn_scores_any<DECODE>, lds, &granted);
+    if (rc) return rc;
+    hipLaunchKernelGGL((k_attn_scores_any<DECODE>), dim3(nc, A.n_kv_head, n_tblk), dim3(256), lds, st, A, hd);
+    if ((rc = sdy_check_launch("attention_scores"))) return rc;
+    hipLaunchKernelGGL((k_attn_softmax_pv_any<DECODE>), dim3(A.n_head, DECODE ? 1 : A.n_tok), dim3(256), 0, st, A, hd);
+    if ((rc = sdy_check_launch("attention_softmax_pv"))) return rc;
+    if (DECODE && A.xq) return sdy_quantize(SDY_Q8_K, A.out, A.xq, A.n_head * hd, 1, (sdy_stream)st);
     return 0;
+}
+
+template <bool DECODE>
+static int attn_dispatch(AttnArgs &A, int hd, int nc, int n_tblk, hipStream_t st) {
+    switch (hd) {
+    case 32: return launch_attn<32, DECODE>(A, nc, n_tblk, st);
+    case 64: return launch_attn<64, DECODE>(A, nc, n_tblk, st);
+    case 128: return launch_attn<128, DECODE>(A, nc, n_tblk, st);
+    case 256: return launch_attn<256, DECODE>(A, nc, n_tblk, st);
+    default: return launch_attn_any<DECODE>(A, hd, nc, n_tblk, st);
+    }
 }
 
 extern "C" int sdy_qk_rope_kv(float *q, float *k, const float *v, const float *qn, const float *kn, float eps,
@@ -636,114 +540,64 @@ extern "C" int sdy_qk_rope_kv(float *q, float *k, const float *v, const float *q
 }
 
 extern "C" int sdy_attention(const float *q, const float *k_cache, const float *v_cache, int n_tok, int n_head,
-                             int n_kv_head, int hd, int n_kv0, long head_stride, long q_stride, float *part,
+                             int n_kv_head, int hd, int n_kv0, long head_stride, long q_stride, float *scores,
                              float *out, long out_stride, sdy_stream s) {
-    hipStream_t st = (hipStream_t)s;
     if (n_tok <= 0) return 0;
-    int rc = shape_ok(n_head, n_kv_head, hd);
-    if (rc) return rc;
-    const int n_rep = n_head / n_kv_head;
-    const int n_kv_max = n_kv0 + n_tok - 1;
-    const int nc = (n_kv_max + CH - 1) / CH;
-    const size_t lds = sizeof(float) * chunk_lds_floats(hd, n_rep);
-    if (lds > 160 * 1024) return sdy_fail(-1, "attention: %zu bytes of LDS (head_dim %d, %d heads per KV head)", lds, hd, n_rep);
-    static size_t granted = 0;
-    if ((rc = sdy_lds_limit((const void *)k_attn_partial, lds, &granted))) return rc;
-    float scale = 1.0f / sqrtf((float)hd);
-    if (n_tok >= 16 && 64 % n_rep == 0 && (hd == 64 || hd == 128)) {
-        // many tokens: the register-blocked chunk kernel (the same records, bit for bit)
-        const int tbr = 64 / n_rep;
-        const size_t lds2 = sizeof(float) * ((size_t)hd * CH * 2 + 64 * CH);
-        static size_t granted2[2] = {0, 0};
-        const void *fn = hd == 128 ? (const void *)k_attn_prefill<128> : (const void *)k_attn_prefill<64>;
-        if ((rc = sdy_lds_limit(fn, lds2, &granted2[hd == 128]))) return rc;
-        const dim3 grid(nc, n_kv_head, (n_tok + tbr - 1) / tbr);
-        if (hd == 128)
-            hipLaunchKernelGGL(k_attn_prefill<128>, grid, dim3(256), lds2, st, q, k_cache, v_cache, n_head, n_kv_head,
-                               n_kv0, head_stride, q_stride, part, n_tok, nc, scale);
-        else
-            hipLaunchKernelGGL(k_attn_prefill<64>, grid, dim3(256), lds2, st, q, k_cache, v_cache, n_head, n_kv_head,
-                               n_kv0, head_stride, q_stride, part, n_tok, nc, scale);
-    } else {
-        hipLaunchKernelGGL(k_attn_partial, dim3(nc, n_kv_head, (n_tok + TB - 1) / TB), dim3(256), lds, st, q, k_cache,
-                           v_cache, n_head, n_kv_head, hd, n_kv0, head_stride, q_stride, part, n_tok, nc, scale);
-    }
-    if ((rc = sdy_check_launch("attention"))) return rc;
-    hipLaunchKernelGGL(k_attn_combine, dim3(n_head, n_tok), dim3(128), 2 * nc * sizeof(float), st, part, n_head, hd,
-                       n_kv0, n_tok, nc, out, out_stride);
-    return sdy_check_launch("attention_combine");
-}
-
-static size_t attn_decode_lds(int n_head, int n_kv_head, int hd) {
-    return sizeof(float) * ((size_t)CH * (hd + 1) + (size_t)CH * hd + hd + (size_t)(n_head / n_kv_head) * hd);
+    if (!head_dim_ok(n_head, n_kv_head, hd)) return shape_fail(n_head, n_kv_head, hd);
+    AttnArgs A = {};
+    A.q = q;
+    A.n_head = n_head;
+    A.n_kv_head = n_kv_head;
+    A.n_kv0 = n_kv0;
+    A.n_tok = n_tok;
+    A.q_stride = q_stride;
+    A.k_cache = (float *)k_cache;
+    A.v_cache = (float *)v_cache;
+    A.head_stride = head_stride;
+    A.scores = scores;
+    A.max_kv = n_kv0 + n_tok - 1;
+    A.scale = 1.0f / sqrtf((float)hd);
+    A.out = out;
+    A.out_stride = out_stride;
+    const int n_rep = n_head / n_kv_head, tbs = PAIRS / n_rep > 0 ? PAIRS / n_rep : 1;
+    const int nc = (A.max_kv + CH - 1) / CH;
+    return attn_dispatch<false>(A, hd, nc, (n_tok + tbs - 1) / tbs, (hipStream_t)s);
 }
 
 extern "C" int sdy_attn_decode_ok(int n_head, int n_kv_head, int hd, int max_seq) {
     (void)max_seq;
-    // the decode kernel is built for head_dim 64 and 128
-    if ((hd != 64 && hd != 128) || n_kv_head < 1 || n_head % n_kv_head || n_head > 64) return 0;
-    return attn_decode_lds(n_head, n_kv_head, hd) <= 160 * 1024;
+    return head_dim_ok(n_head, n_kv_head, hd) && scores_lds(hd | 1, n_head / n_kv_head) <= 160 * 1024;
 }
-
-extern "C" size_t sdy_attn_decode_chunks(int max_seq) { return (size_t)((max_seq + CH - 1) / CH); }
 
 extern "C" int sdy_attn_decode(const float *q, const float *k, const float *v, const float *q_norm,
                                const float *k_norm, float eps, const float *rope_cos, const float *rope_sin,
                                const int32_t *step_dev, int n_head, int n_kv_head, int hd, int interleaved,
-                               float *k_cache, float *v_cache, long head_stride, int max_seq, float *part,
-                               sdy_stream s) {
-    if (!sdy_attn_decode_ok(n_head, n_kv_head, hd, max_seq))
-        return sdy_fail(-1, "attn_decode: unsupported shape (%d heads, %d kv heads, head_dim %d)", n_head, n_kv_head,
-                        hd);
-    const size_t lds = attn_decode_lds(n_head, n_kv_head, hd);
-    static size_t granted[2] = {0, 0};
-    const void *fn = hd == 128 ? (const void *)k_attn_decode<128> : (const void *)k_attn_decode<64>;
-    int rc = sdy_lds_limit(fn, lds, &granted[hd == 128]);
-    if (rc) return rc;
-    AttnDecodeArgs a;
-    a.q = q;
-    a.k = k;
-    a.v = v;
-    a.q_norm = q_norm;
-    a.k_norm = k_norm;
-    a.eps = eps;
-    a.rope_cos = rope_cos;
-    a.rope_sin = rope_sin;
-    a.step = step_dev;
-    a.n_head = n_head;
-    a.n_kv_head = n_kv_head;
-    a.hd = hd;
-    a.interleaved = interleaved;
-    a.k_cache = k_cache;
-    a.v_cache = v_cache;
-    a.head_stride = head_stride;
-    a.part = part;
-    a.n_chunk_max = (max_seq + CH - 1) / CH;
-    a.scale = 1.0f / sqrtf((float)hd);
-    if (hd == 128)
-        hipLaunchKernelGGL(k_attn_decode<128>, dim3(a.n_chunk_max, n_kv_head), dim3(DEC_NT), lds, (hipStream_t)s, a);
-    else
-        hipLaunchKernelGGL(k_attn_decode<64>, dim3(a.n_chunk_max, n_kv_head), dim3(DEC_NT), lds, (hipStream_t)s, a);
-    return sdy_check_launch("attn_decode");
-}
-
-extern "C" int sdy_attn_merge1(const float *part, const int32_t *step_dev, int n_head, int hd, int max_seq, float *out,
-                               void *xq_q8k, sdy_stream s) {
-    const int nchm = (max_seq + CH - 1) / CH;
-    const int n_out = n_head * hd, hps = (255 + hd - 1) / hd + 1;  // heads a super-block can touch
-    const size_t lds = (size_t)hps * 2 * nchm * sizeof(float);
-    if (xq_q8k && n_out % 256 == 0 && hps <= 64 && lds <= 64 * 1024) {
-        hipLaunchKernelGGL(k_attn_merge1_q8k, dim3(n_out / 256), dim3(64), lds, (hipStream_t)s, part, step_dev, n_head,
-                           hd, nchm, out, (uint8_t *)xq_q8k);
-        return sdy_check_launch("attn_merge1_q8k");
-    }
-    if (xq_q8k) return sdy_fail(-1, "attn_merge1: no Q8_K merge for %d heads of %d", n_head, hd);
-    hipLaunchKernelGGL(k_attn_merge1, dim3(n_head), dim3(64), 2 * nchm * sizeof(float), (hipStream_t)s, part, step_dev,
-                       n_head, hd, nchm, out);
-    return sdy_check_launch("attn_merge1");
-}
-
-extern "C" int sdy_attn_merge1_q8k_ok(int n_head, int hd, int max_seq) {
-    const int nchm = (max_seq + CH - 1) / CH, hps = (255 + hd - 1) / hd + 1;
-    return (n_head * hd) % 256 == 0 && (size_t)hps * 2 * nchm * sizeof(float) <= 64 * 1024;
+                               float *k_cache, float *v_cache, long head_stride, int max_seq, float *scores,
+                               float *out, void *xq_q8k, sdy_stream s) {
+    if (!sdy_attn_decode_ok(n_head, n_kv_head, hd, max_seq)) return shape_fail(n_head, n_kv_head, hd);
+    if (xq_q8k && (n_head * hd) % 256) return sdy_fail(-1, "attn_decode: %d outputs are not whole Q8_K blocks", n_head * hd);
+    AttnArgs A = {};
+    A.q = q;
+    A.k = k;
+    A.v = v;
+    A.q_norm = q_norm;
+    A.k_norm = k_norm;
+    A.eps = eps;
+    A.rope_cos = rope_cos;
+    A.rope_sin = rope_sin;
+    A.step = step_dev;
+    A.n_head = n_head;
+    A.n_kv_head = n_kv_head;
+    A.n_tok = 1;
+    A.interleaved = interleaved;
+    A.k_cache = k_cache;
+    A.v_cache = v_cache;
+    A.head_stride = head_stride;
+    A.scores = scores;
+    A.max_kv = max_seq;
+    A.scale = 1.0f / sqrtf((float)hd);
+    A.out = out;
+    A.out_stride = (long)n_head * hd;
+    A.xq = (uint8_t *)xq_q8k;
+    return attn_dispatch<true>(A, hd, (max_seq + CH - 1) / CH, 1, (hipStream_t)s);
 }

@@ -58,7 +58,7 @@ int sdy_engine_alloc(engine_ctx *c) {
     TRY(dalloc((void **)&c->hb, BR * ffn * 4));
     TRY(dalloc((void **)&c->hb2, BR * ffn * 4));
     TRY(dalloc((void **)&c->logits_dev, logit_rows * in->n_vocab * 4));
-    TRY(dalloc((void **)&c->part, sdy_attn_part_floats((int)B, in->n_head, in->head_dim, (int)S) * 4));
+    TRY(dalloc((void **)&c->part, sdy_attn_scores_floats((int)B, in->n_head, (int)S) * 4));
     TRY(dalloc(&c->xq[0], BR * ((max_in + 31) / 32 * 34)));
     TRY(dalloc(&c->xq[1], BR * ((max_in + 255) / 256 * 292)));
     TRY(dalloc((void **)&c->tok_dev, B * 4));
@@ -316,14 +316,11 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
                 TRY(mm(c, k, c->xb, &L->wk, 1, L->bk, NULL, 0));
                 TRY(mm(c, v, c->xb, &L->wv, 1, L->bv, NULL, 0));
             }
+            /* attention into att (and, for a K-quant wo, its Q8_K row: mm then reuses it) */
+            const int q8k = vec_dot_type(L->wo.type) == SDY_Q8_K;
             TRY(sdy_attn_decode(q, k, v, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos, c->rope_sin, c->step_dev,
                                 in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc, vc, head_stride, c->max_seq,
-                                c->part, c->st));
-            /* merge (and, for K-quant wo, quantise in the same launch); mm then reuses the Q8_K row */
-            const int q8k = vec_dot_type(L->wo.type) == SDY_Q8_K &&
-                            sdy_attn_merge1_q8k_ok(in->n_head, hd, c->max_seq);
-            TRY(sdy_attn_merge1(c->part, c->step_dev, in->n_head, hd, c->max_seq, c->att, q8k ? c->xq[1] : NULL,
-                                c->st));
+                                c->part, c->att, q8k ? c->xq[1] : NULL, c->st));
             c->xq_src[0] = c->xq_src[1] = NULL;
             if (q8k) {
                 c->xq_src[1] = c->att;

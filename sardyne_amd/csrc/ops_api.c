@@ -284,12 +284,12 @@ void op_rope(float *x, int n_heads, int head_dim, const float *cos, const float 
 
 void op_attention(float *out, const float *q, const float *k_cache, const float *v_cache, int n_head, int n_kv_head,
                   int head_dim, int n_kv, int stride, float *scores) {
-    (void)scores; /* the GPU kernel keeps its scores in LDS */
+    (void)scores; /* the GPU kernels keep their scores in device scratch */
     if (n_head <= 0 || n_kv <= 0) return;
     size_t qn = (size_t)n_head * head_dim, kvn = (size_t)n_kv_head * stride * head_dim;
     float *dq = dup_to_dev(q, qn * 4), *dk = dup_to_dev(k_cache, kvn * 4), *dv = dup_to_dev(v_cache, kvn * 4);
     float *dout = dalloc(qn * 4);
-    float *part = dalloc(sdy_attn_part_floats(1, n_head, head_dim, n_kv) * 4);
+    float *part = dalloc(sdy_attn_scores_floats(1, n_head, n_kv) * 4);
     CK(sdy_attention(dq, dk, dv, 1, n_head, n_kv_head, head_dim, n_kv, (long)stride * head_dim, (long)qn, part, dout,
                      (long)qn, stream()),
        "attention");

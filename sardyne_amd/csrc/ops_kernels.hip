@@ -7,6 +7,7 @@
 // in double, top-k keeps the lower expert index on ties and renormalises with a sequential float
 // sum. Reductions use fixed trees, so every result is reproducible run to run.
 #include "sdy_device.h"
+#include "sdy_expf.h"
 #include "sdy_internal.h"
 #include "sdy_norm_dev.h"
 #include "sdy_ops.h"
@@ -59,7 +60,7 @@ __global__ void k_silu_mul(float *gate, const float *up, long n) {
     long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
     if (i >= n) return;
     float g = gate[i];
-    float s = g / (1.0f + expf(-g));
+    float s = g / (1.0f + sdy_expf(-g));
     gate[i] = s * up[i];
 }
 
@@ -102,7 +103,7 @@ __global__ __launch_bounds__(256) void k_softmax(float *x, int n, long stride) {
     m = block_reduce_max(m, shf);
     double s = 0.0;
     for (int i = threadIdx.x; i < n; i += 256) {
-        float e = expf(r[i] - m);
+        float e = sdy_expf(r[i] - m);
         r[i] = e;
         s += (double)e;
     }
@@ -155,15 +156,14 @@ __global__ __launch_bounds__(64) void k_moe_route(const float *logits, int n_exp
         m = fmaxf(m, v[j]);
     }
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    // op_softmax (csrc/ops.c:353-364): expf(x - max), the sum in double, times (float)(1 / sum).
-    // expf is computed in double and rounded once (the correctly rounded value, as the host libm
-    // gives), so that near-equal router probabilities order as on the host. The probabilities stay
-    // in registers; -1 marks lanes past n_expert (never chosen).
+    // op_softmax (csrc/ops.c:353-364): expf(x - max) (the host libm's expf, bit for bit), the sum
+    // in double, times (float)(1 / sum). The probabilities stay in registers; -1 marks lanes past
+    // n_expert (never chosen).
     double s = 0.0;
 #pragma unroll
     for (int j = 0; j < NPL; j++)
         if (lane + 64 * j < n_expert) {
-            v[j] = (float)exp((double)(v[j] - m));
+            v[j] = sdy_expf(v[j] - m);
             s += (double)v[j];
         }
     for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);

@@ -14,9 +14,12 @@ int sdy_rmsnorm(const float *x, const float *w, float *out, int n, float eps, in
 int sdy_qk_rope_kv(float *q, float *k, const float *v, const float *qn, const float *kn, float eps,
                    const float *rope_cos, const float *rope_sin, int pos0, int n_tok, int n_head, int n_kv_head, int hd,
                    int interleaved, float *k_cache, float *v_cache, long head_stride, sdy_stream s);
-size_t sdy_attn_part_floats(int n_tok, int n_head, int hd, int max_kv);
+/* Causal attention of n_tok tokens at positions n_kv0 - 1 + t (q rotated, K/V in the cache) in the
+ * reference's arithmetic; scores: sdy_attn_scores_floats(n_tok, n_head, n_kv0 + n_tok - 1) floats of
+ * device scratch. head_dim 32, 64, 128 or 256. */
+size_t sdy_attn_scores_floats(int n_tok, int n_head, int max_kv);
 int sdy_attention(const float *q, const float *k_cache, const float *v_cache, int n_tok, int n_head, int n_kv_head,
-                  int hd, int n_kv0, long head_stride, long q_stride, float *part, float *out, long out_stride,
+                  int hd, int n_kv0, long head_stride, long q_stride, float *scores, float *out, long out_stride,
                   sdy_stream s);
 int sdy_silu_mul(float *gate, const float *up, long n, sdy_stream s);
 int sdy_add(const float *a, const float *b, float *out, long n, sdy_stream s);
@@ -35,20 +38,15 @@ int sdy_moe_combine(const float *y, const int32_t *top, const float *wts, int n_
  * quantising). Bytes equal sdy_rmsnorm followed by sdy_quantize. */
 int sdy_norm_quant(const float *x, const float *w, float eps, int n, int n_rows, float *xb, int vtype, void *xq,
                    sdy_stream s);
-/* One-token decode attention: q/k norm + RoPE + KV write at position step_dev[1], and the split
- * attention over positions 0..step_dev[1] as partial records in part (n_head heads x
- * sdy_attn_decode_chunks(max_seq) chunks), merged by sdy_attn_merge1. */
+/* One-token decode attention at the position held in step_dev[1] (read on the device, so that a
+ * recorded step replays for every position): q/k norm + RoPE, the KV-cache write of that position,
+ * the scores (scores: sdy_attn_scores_floats(1, n_head, max_seq) floats of scratch), the softmax and
+ * the weighted V into out (n_head * hd floats), and with xq_q8k also out's Q8_K row. */
 int sdy_attn_decode_ok(int n_head, int n_kv_head, int hd, int max_seq);
-size_t sdy_attn_decode_chunks(int max_seq);
 int sdy_attn_decode(const float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
                     float eps, const float *rope_cos, const float *rope_sin, const int32_t *step_dev, int n_head,
                     int n_kv_head, int hd, int interleaved, float *k_cache, float *v_cache, long head_stride,
-                    int max_seq, float *part, sdy_stream s);
-/* out (f32, n_head * hd) = the merge of one token's records; with xq_q8k also its Q8_K row (when
- * sdy_attn_merge1_q8k_ok), in the same launch. */
-int sdy_attn_merge1(const float *part, const int32_t *step_dev, int n_head, int hd, int max_seq, float *out,
-                    void *xq_q8k, sdy_stream s);
-int sdy_attn_merge1_q8k_ok(int n_head, int hd, int max_seq);
+                    int max_seq, float *scores, float *out, void *xq_q8k, sdy_stream s);
 #ifdef __cplusplus
 }
 #endif

@@ -2,6 +2,7 @@
 // decode kernels, so that every producer of a Q8_K / Q8_0 row writes the same bytes.
 #pragma once
 #include "sdy_device.h"
+#include "sdy_expf.h"
 
 // One 256-element Q8_K block (csrc/quant.c:118-144) held by a wave64, lane l holding elements
 // 4l..4l+3 in xs. The signed maximum is the first element of largest magnitude (strict '>' in
@@ -144,8 +145,8 @@ SDY_DEV void sdy_q8_0_block(float xv, int l, uint8_t *ob) {
     }
 }
 
-// SiLU(g) * u as the reference computes it (csrc/ops.c:366-371).
+// SiLU(g) * u as the reference computes it (csrc/ops.c:366-371), with the host libm's expf.
 SDY_DEV float sdy_silu_mul1(float g, float u) {
-    const float s = g / (1.0f + expf(-g));
+    const float s = g / (1.0f + sdy_expf(-g));
     return s * u;
 }

@@ -187,6 +187,26 @@ def test_decode_paths_bit_identical(model_path):
     assert_close(fused_graph, np.stack(exp))
 
 
+KQUANT_SPECS = ["qwen2-kquant", "llama-kquant", "qwen2-gqa8-hd128", "moe-128x8", "moe-16x4-ffn768"]
+
+
+@pytest.mark.parametrize("spec", KQUANT_SPECS)
+def test_logits_bit_identical_to_reference(spec, tmp_path):
+    """K-quant models (integer dots, the reference's f32 order for every float step: rmsnorm,
+    RoPE, the AVX2 attention dot, libm expf in the softmaxes and SiLU, in-order axpys, the AVX2 router
+    matvec): prefill and one-token logits have the bits of the oracle's AVX2 forward (itself the
+    compiled reference's, tests/test_oracle.py)."""
+    path = tmp_path / "m.gguf"
+    write_model(path, dataclasses.replace(SPECS[spec], context=160), seed=7)
+    toks = np.random.default_rng(8).integers(0, 300, 100).tolist()
+    ctx = Context(Model(path), max_seq=128, n_batch=32)
+    got = [ctx.eval(toks[:70])] + [ctx.eval([t]) for t in toks[70:100]]
+    ref = O.OracleContext(path, 128, n_batch=32, simd=1)
+    exp = [ref.eval(toks[:70])] + [ref.eval([t]) for t in toks[70:100]]
+    for i, (g, e) in enumerate(zip(got, exp)):
+        assert np.array_equal(g.view(np.uint32), e.view(np.uint32)), (i, float(np.abs(g - e).max()))
+
+
 @pytest.mark.parametrize("spec", ["qwen2-gqa8-hd128", "qwen2-kquant", "moe-kquant"])
 def test_long_context_decode(spec, tmp_path):
     """One-token steps over more than two 64-position attention chunks (the split attention and its

@@ -261,7 +261,8 @@ def test_attention_gqa(n_kv):
     lib().op_attention(ptr(out), ptr(q), ptr(kc), ptr(vc), n_head, n_kv_head, hd, n_kv, stride, ptr(scores))
     exp = np.empty_like(q)
     O.lib().orc_attention(ptr(exp), ptr(q), ptr(kc), ptr(vc), n_head, n_kv_head, hd, n_kv, stride, ptr(scores), 1)
-    np.testing.assert_allclose(out, exp, rtol=1e-5, atol=1e-6)
+    # the reference's arithmetic (AVX2 dot, libm expf, in-order axpy): the same bits
+    assert np.array_equal(bits(out), bits(exp))
 
 
 def test_dot_axpy_add():
@@ -497,11 +498,13 @@ def test_moe_route_and_combine(n_expert, k):
         assert np.array_equal(bits(got[t]), bits(resid[t] + acc)), t
 
 
-@pytest.mark.parametrize("n_head,n_kv_head,hd", [(16, 2, 128), (4, 2, 64), (32, 4, 128), (4, 4, 64), (6, 2, 64)])
+@pytest.mark.parametrize("n_head,n_kv_head,hd", [(16, 2, 128), (4, 2, 64), (32, 4, 128), (4, 4, 64), (6, 2, 64),
+                                             (4, 2, 32), (2, 1, 256), (6, 3, 80)])
 @pytest.mark.parametrize("n_tok,n_kv0", [(16, 1), (40, 70), (77, 3)])
 def test_prefill_attention_tokens_bit_identical(n_head, n_kv_head, hd, n_tok, n_kv0):
-    """Causal attention of n_tok tokens in one call (the register-blocked chunk kernel from 16
-    tokens on) gives the bits of one call per token, and follows a float64 softmax."""
+    """Causal attention of n_tok tokens in one call gives the bits of one call per token and those of
+    the oracle's op_attention_head (the reference's AVX2 dot, libm expf, in-order axpy), and follows a
+    float64 softmax."""
     L = lib()
     rng = np.random.default_rng(n_head * 1000 + n_tok + hd)
     max_seq = 160
@@ -509,7 +512,7 @@ def test_prefill_attention_tokens_bit_identical(n_head, n_kv_head, hd, n_tok, n_
     kc = rng.standard_normal((n_kv_head, max_seq, hd)).astype(np.float32)
     vc = rng.standard_normal((n_kv_head, max_seq, hd)).astype(np.float32)
     dq, dk, dv = capi.DeviceBuffer.from_array(q), capi.DeviceBuffer.from_array(kc), capi.DeviceBuffer.from_array(vc)
-    dpart = capi.DeviceBuffer(L.sdy_attn_part_floats(n_tok, n_head, hd, max_seq) * 4)
+    dpart = capi.DeviceBuffer(L.sdy_attn_scores_floats(n_tok, n_head, max_seq) * 4)
     dout = capi.DeviceBuffer(n_tok * n_head * hd * 4)
     q_dim = n_head * hd
     capi.check(L.sdy_attention(dq.ptr, dk.ptr, dv.ptr, n_tok, n_head, n_kv_head, hd, n_kv0, max_seq * hd, q_dim,
@@ -522,6 +525,13 @@ def test_prefill_attention_tokens_bit_identical(n_head, n_kv_head, hd, n_tok, n_
                                    max_seq * hd, q_dim, dpart.ptr, d1.ptr, q_dim, None))
         one[t] = d1.to_array(np.float32, q_dim)
     assert np.array_equal(bits(got), bits(one))
+    exp_o = np.empty((n_tok, q_dim), np.float32)
+    scores = np.empty(max_seq, np.float32)
+    for t in range(n_tok):
+        qt = np.ascontiguousarray(q[t])
+        O.lib().orc_attention(ptr(exp_o[t]), ptr(qt), ptr(kc), ptr(vc), n_head, n_kv_head, hd, n_kv0 + t, max_seq,
+                              ptr(scores), 1)
+    assert np.array_equal(bits(got), bits(exp_o))
     n_rep = n_head // n_kv_head
     for t in range(0, n_tok, 7):
         for h in range(n_head):
