@@ -31,6 +31,9 @@ constexpr int CH = 64;       // positions per scores workgroup (one per lane)
 constexpr int PAIRS = 64;    // (token, head) pairs per prefill scores workgroup
 constexpr int PW = 8192;     // weights held in LDS at a time by k_attn_softmax_pv (all its heads)
 
+// register arrays of 16-byte loads (an ext vector type: arrays of it stay in registers)
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 // One wave: optional per-head RMSNorm (qwen3 q/k norm: double sum, one rounding of the scale) then
 // RoPE (pairs (i, i + hd/2), or (2i, 2i+1) when interleaved) of the hd-vector in buf (LDS).
 SDY_DEV void norm_rope_wave(float *buf, const float *nw, float eps, const float *cs, const float *sn, int hd,
@@ -103,6 +106,67 @@ struct AttnArgs {
     long out_stride;
     uint8_t *xq;                      // decode: Q8_K row of out (or null)
 };
+
+// Maximum, and sum in double of expf(row[j] - m), over j = i0, i0 + stride, ... < n, eight loads in
+// flight at a time (clamped indices).
+SDY_DEV float row_max(const float *row, int i0, int stride, int n) {
+    float m = -INFINITY;
+    for (int j0 = i0; j0 < n; j0 += 8 * stride) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = j0 + u * stride;
+            v[u] = row[j < n ? j : n - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (j0 + u * stride < n) m = fmaxf(m, v[u]);
+    }
+    return m;
+}
+
+SDY_DEV double row_expsum(const float *row, int i0, int stride, int n, float m) {
+    double sum = 0.0;
+    for (int j0 = i0; j0 < n; j0 += 8 * stride) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = j0 + u * stride;
+            v[u] = row[j < n ? j : n - 1];
+        }
+        float e[8];  // every exponential first (clamped indices), so the table reads overlap
+#pragma unroll
+        for (int u = 0; u < 8; u++) e[u] = sdy_expf(v[u] - m);
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (j0 + u * stride < n) sum += (double)e[u];
+    }
+    return sum;
+}
+
+// dst[(j - j_base) * dst_stride] = expf(row[j] - m) * inv for j = i0, i0 + stride, ... < n
+SDY_DEV void row_weights(const float *row, int i0, int stride, int n, float m, float inv, float *dst, int j_base,
+                         int dst_stride) {
+    for (int j0 = i0; j0 < n; j0 += 8 * stride) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = j0 + u * stride;
+            v[u] = row[j < n ? j : n - 1];
+        }
+        float e[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) e[u] = sdy_expf(v[u] - m) * inv;
+        // all eight computed here, not sunk into the guarded stores one by one
+        asm volatile("" : "+v"(e[0]), "+v"(e[1]), "+v"(e[2]), "+v"(e[3]), "+v"(e[4]), "+v"(e[5]), "+v"(e[6]),
+                     "+v"(e[7]));
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = j0 + u * stride;
+            if (j < n) dst[(j - j_base) * dst_stride] = e[u];
+        }
+    }
+}
 
 // dot(q, k) in csrc/ops_avx2.c:61-74's order (x = q, w = k), both in LDS, q 16-byte aligned.
 template <int HD>
@@ -184,11 +248,11 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
     // K chunk loads first (clamped indices, unconditional)
     const float *kg = a.k_cache + g * a.head_stride + (size_t)p0 * HD;
     const int n4 = np_max * HD / 4;
-    float4 kv[NV];
+    f32x4 kv[NV];
 #pragma unroll
     for (int j = 0; j < NV; j++) {
         const int i = tid + 256 * j < n4 ? tid + 256 * j : 0;
-        kv[j] = reinterpret_cast<const float4 *>(kg)[i];
+        kv[j] = reinterpret_cast<const f32x4 *>(kg)[i];
     }
     const int n_pairs = (t1 - t0) * n_rep;
     bool has_pos = false;
@@ -228,7 +292,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
         if (i >= n4) break;
         const int p = (4 * i) / HD, d = 4 * i - p * HD;
         if (p == special) continue;
-        *reinterpret_cast<float4 *>(ks + p * KS + d) = kv[j];
+        *reinterpret_cast<f32x4 *>(ks + p * KS + d) = kv[j];
     }
     __syncthreads();
     if constexpr (DECODE) {
@@ -268,8 +332,7 @@ __global__ __launch_bounds__(256) void k_attn_softmax_pv(AttnArgs a) {
     const int n = DECODE ? a.step[1] + 1 : a.n_kv0 + t;
     const float *row = a.scores + ((size_t)t * a.n_head + h) * a.max_kv;
     // maximum over the head's positions
-    float m = -INFINITY;
-    for (int j = d; j < n; j += HD) m = fmaxf(m, row[j]);
+    float m = row_max(row, d, HD, n);
     for (int off = GW / 2; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     if constexpr (HD > 64) {
         if ((tid & 63) == 0) redf[wave] = m;
@@ -278,8 +341,7 @@ __global__ __launch_bounds__(256) void k_attn_softmax_pv(AttnArgs a) {
         for (int w = 0; w < HD / 64; w++) m = fmaxf(m, redf[hl * (HD / 64) + w]);
     }
     // sum of expf(score - max) in double
-    double sum = 0.0;
-    for (int j = d; j < n; j += HD) sum += (double)sdy_expf(row[j] - m);
+    double sum = row_expsum(row, d, HD, n, m);
     for (int off = GW / 2; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
     if constexpr (HD > 64) {
         if ((tid & 63) == 0) redd[wave] = sum;
@@ -294,7 +356,7 @@ __global__ __launch_bounds__(256) void k_attn_softmax_pv(AttnArgs a) {
     for (int jb = 0; jb < n; jb += PB) {
         const int je = jb + PB < n ? jb + PB : n;
         __syncthreads();
-        for (int j = jb + d; j < je; j += HD) pw[hl][j - jb] = sdy_expf(row[j] - m) * inv;
+        row_weights(row, jb + d, HD, je, m, inv, pw[hl], jb, 1);
         __syncthreads();
         int j = jb;
         for (; j + 8 <= je; j += 8) {
@@ -318,6 +380,91 @@ __global__ __launch_bounds__(256) void k_attn_softmax_pv(AttnArgs a) {
             }
         }
     }
+}
+
+// Decode softmax in place: one workgroup of 256 threads per query head turns the head's scores s_j
+// (j = 0..pos) into p_j = expf(s_j - m) * inv, m the maximum and inv = (float)(1 / sum expf(s_j - m))
+// with the sum in double. Each thread reads and rewrites only its own entries (j = tid mod 256).
+__global__ __launch_bounds__(256) void k_attn_decode_softmax(AttnArgs a) {
+    __shared__ float red_m[4];
+    __shared__ double red_s[4];
+    const int tid = threadIdx.x, wave = tid >> 6, n = a.step[1] + 1;
+    float *row = a.scores + (size_t)blockIdx.x * a.max_kv;
+    float m = row_max(row, tid, 256, n);
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((tid & 63) == 0) red_m[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+    double sum = row_expsum(row, tid, 256, n, m);
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+    if ((tid & 63) == 0) red_s[wave] = sum;
+    __syncthreads();
+    sum = (red_s[0] + red_s[1]) + (red_s[2] + red_s[3]);
+    row_weights(row, tid, 256, n, m, (float)(1.0 / sum), row, 0, 1);
+}
+
+// Decode weighted V: lane (r, d) of a wave owns dim d of query head r of HPW heads that share a KV
+// head and runs its FMA chain out = fma(p_j, v_j[d], out) over j = 0..pos in order (the reference's
+// in-order axpy). A wave covers DS = 64 / HPW consecutive dims; its loads of V row j read those DS
+// floats (each by HPW lanes) and its weight loads read four positions of each head at once. The
+// chains are latency-bound, so the grid is n_kv_head * (n_rep / HPW) * (HD / DS) one-wave workgroups
+// (one per CU), each with PF positions in flight in registers.
+template <int HD, int HPW, int PF>
+__global__ __launch_bounds__(64) void k_attn_decode_wv(AttnArgs a) {
+    constexpr int DS = 64 / HPW, NS = HD / DS, G = PF / 4;
+    static_assert(DS * HPW == 64 && NS * DS == HD && PF % 4 == 0 && 3 * HD * 4 < 4096, "shape");
+    const int lane = threadIdx.x, r = lane / DS, dd = lane - r * DS;
+    const int n_rep = a.n_head / a.n_kv_head, n_hg = n_rep / HPW;
+    const int s = blockIdx.x % NS, hg = (blockIdx.x / NS) % n_hg, g = blockIdx.x / (NS * n_hg);
+    const int h0 = g * n_rep + hg * HPW, d = s * DS + dd;
+    const int n = a.step[1] + 1;
+    // Buffer reads, range-checked on the lane offset (plus the instruction's constant offset): V rows
+    // at or past n and weights past the last head's row read as 0 and are never used.
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc(a.v_cache + g * a.head_stride, (short)0, n * HD * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(a.scores + (size_t)h0 * a.max_kv, (short)0,
+                                                                        HPW * a.max_kv * 4, 0x00020000);
+    // position j of the group at lane offset o: V row j + k at o + k * HD * 4 (constant offsets)
+    auto ldv = [&](uint32_t o, int k) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rv, o + k * HD * 4, 0, 0));
+    };
+    auto ldw = [&](uint32_t o) { return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, 0)); };
+    uint32_t ov = d * 4, ow = r * a.max_kv * 4;  // the next refill's group 0 (V row, weight)
+    float vr[PF];
+    f32x4 wr[G];  // wr[q][k] and vr[4q + k] hold position j + 4q + k
+#pragma unroll
+    for (int q = 0; q < G; q++) {
+        wr[q] = ldw(ow + q * 16);
+#pragma unroll
+        for (int k = 0; k < 4; k++) vr[4 * q + k] = ldv(ov + q * 4 * HD * 4, k);
+        __builtin_amdgcn_sched_barrier(0);  // issued in position order
+    }
+    ov += PF * HD * 4;
+    ow += PF * 4;
+    float acc = 0.0f;
+    int j = 0;
+    for (; j + PF <= n; j += PF) {
+#pragma unroll
+        for (int q = 0; q < G; q++) {
+            const f32x4 w = wr[q];
+#pragma unroll
+            for (int k = 0; k < 4; k++) acc = fmaf(w[k], vr[4 * q + k], acc);
+            // an opaque zero that depends on acc: the group's refill cannot be issued before its
+            // slots are read, so each refill reuses its slot's registers
+            uint32_t z;
+            asm volatile("s_mov_b32 %0, 0" : "=s"(z) : "v"(acc));
+            const uint32_t oq = ov + q * 4 * HD * 4 + z;
+            wr[q] = ldw(ow + q * 16 + z);
+#pragma unroll
+            for (int k = 0; k < 4; k++) vr[4 * q + k] = ldv(oq, k);
+        }
+        ov += PF * HD * 4;
+        ow += PF * 4;
+    }
+#pragma unroll
+    for (int u = 0; u < PF; u++)  // the last n - j < PF positions, already in the ring
+        if (j + u < n) acc = fmaf(wr[u / 4][u % 4], vr[u], acc);
+    a.out[(size_t)(h0 + r) * HD + d] = acc;
 }
 
 // Any head_dim (hd % 4 == 0 is not required): the same arithmetic with runtime loops and scalar LDS
@@ -436,14 +583,12 @@ __global__ __launch_bounds__(256) void k_attn_softmax_pv_any(AttnArgs a, int hd)
     const int n_rep = a.n_head / a.n_kv_head, g = h / n_rep;
     const int n = DECODE ? a.step[1] + 1 : a.n_kv0 + t;
     const float *row = a.scores + ((size_t)t * a.n_head + h) * a.max_kv;
-    float m = -INFINITY;
-    for (int j = tid; j < n; j += 256) m = fmaxf(m, row[j]);
+    float m = row_max(row, tid, 256, n);
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     if (lane == 0) redf[wave] = m;
     __syncthreads();
     m = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
-    double sum = 0.0;
-    for (int j = tid; j < n; j += 256) sum += (double)sdy_expf(row[j] - m);
+    double sum = row_expsum(row, tid, 256, n, m);
     for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
     if (lane == 0) redd[wave] = sum;
     __syncthreads();
@@ -456,7 +601,7 @@ __global__ __launch_bounds__(256) void k_attn_softmax_pv_any(AttnArgs a, int hd)
         for (int jb = 0; jb < n; jb += PW) {
             const int je = jb + PW < n ? jb + PW : n;
             __syncthreads();
-            for (int j = jb + tid; j < je; j += 256) pw[j - jb] = sdy_expf(row[j] - m) * inv;
+            row_weights(row, jb + tid, 256, je, m, inv, pw, jb, 1);
             __syncthreads();
             if (d < hd)
                 for (int j = jb; j < je; j++) acc = fmaf(pw[j - jb], vg[(size_t)j * hd + d], acc);
@@ -470,7 +615,7 @@ __global__ __launch_bounds__(256) void k_attn_softmax_pv_any(AttnArgs a, int hd)
 // =============================================================================== launchers
 
 extern "C" size_t sdy_attn_scores_floats(int n_tok, int n_head, int max_kv) {
-    return (size_t)n_tok * n_head * max_kv;
+    return (size_t)n_tok * n_head * ((max_kv + 3) & ~3);
 }
 
 static int head_dim_ok(int n_head, int n_kv_head, int hd) {
@@ -518,8 +663,40 @@ static int launch_attn_any(AttnArgs &A, int hd, int nc, int n_tblk, hipStream_t 
     return 0;
 }
 
+// decode: k_attn_scores, k_attn_decode_softmax, k_attn_decode_wv (four heads of a KV group per wave
+// when n_rep allows, else one), then the Q8_K row of the output when asked for.
+template <int HD>
+static int launch_attn_decode(AttnArgs &A, int nc, hipStream_t st) {
+    const int n_rep = A.n_head / A.n_kv_head;
+    const size_t lds = scores_lds(HD, n_rep);
+    static size_t granted = 0;
+    int rc = sdy_lds_limit((const void *)k_attn_scores<HD, true>, lds, &granted);
+    if (rc) return rc;
+    hipLaunchKernelGGL((k_attn_scores<HD, true>), dim3(nc, A.n_kv_head, 1), dim3(256), lds, st, A);
+    if ((rc = sdy_check_launch("attention_scores"))) return rc;
+    hipLaunchKernelGGL(k_attn_decode_softmax, dim3(A.n_head), dim3(256), 0, st, A);
+    if ((rc = sdy_check_launch("attention_decode_softmax"))) return rc;
+    constexpr int HPW = 4;
+    if (n_rep % HPW) {
+        hipLaunchKernelGGL((k_attn_decode_wv<HD, 1, 32>), dim3(A.n_head * (HD / 64)), dim3(64), 0, st, A);
+    } else {
+        hipLaunchKernelGGL((k_attn_decode_wv<HD, HPW, 32>), dim3(A.n_head * HD / 64), dim3(64), 0, st, A);
+    }
+    if ((rc = sdy_check_launch("attention_decode_wv"))) return rc;
+    if (A.xq) return sdy_quantize(SDY_Q8_K, A.out, A.xq, A.n_head * HD, 1, (sdy_stream)st);
+    return 0;
+}
+
 template <bool DECODE>
 static int attn_dispatch(AttnArgs &A, int hd, int nc, int n_tblk, hipStream_t st) {
+    if constexpr (DECODE) {
+        switch (hd) {
+        case 64: return launch_attn_decode<64>(A, nc, st);
+        case 128: return launch_attn_decode<128>(A, nc, st);
+        case 256: return launch_attn_decode<256>(A, nc, st);
+        default: break;
+        }
+    }
     switch (hd) {
     case 32: return launch_attn<32, DECODE>(A, nc, n_tblk, st);
     case 64: return launch_attn<64, DECODE>(A, nc, n_tblk, st);
@@ -594,7 +771,7 @@ extern "C" int sdy_attn_decode(const float *q, const float *k, const float *v, c
     A.v_cache = v_cache;
     A.head_stride = head_stride;
     A.scores = scores;
-    A.max_kv = max_seq;
+    A.max_kv = (max_seq + 3) & ~3;  // score rows padded to whole 16-byte groups
     A.scale = 1.0f / sqrtf((float)hd);
     A.out = out;
     A.out_stride = (long)n_head * hd;

@@ -59,10 +59,9 @@ SDY_EXPF_QUAL uint64_t sdy_expf_double_to_bits(double d) {
 #endif
 }
 
+/* Branch-free: the main path runs for every x (its table index is in range for any input) and the
+ * special cases are selected at the end, so a device wave issues its table reads without branching. */
 SDY_EXPF_QUAL float sdy_expf(float x) {
-    if (x != x) return x + x;
-    if (x > 0x1.62e42ep6f) return __builtin_inff();
-    if (x < -0x1.9fe368p6f) return 0.0f;
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
                  c2 = 0x1.62e42ff0c52d6p-1 / 32;
@@ -79,7 +78,10 @@ SDY_EXPF_QUAL float sdy_expf(float x) {
     double y = c2 * r + 1.0;
     y = p * r2 + y;
     y = y * s;
-    return (float)y;
+    float res = (float)y;
+    res = x < -0x1.9fe368p6f ? 0.0f : res;
+    res = x > 0x1.62e42ep6f ? __builtin_inff() : res;
+    return x != x ? x + x : res;
 }
 
 #endif
