@@ -7,8 +7,9 @@ step streams its weights from HBM. value = algorithmic bytes per step / step tim
 
 Other workloads (--workload): q8_0_head (the Q8_0 matvec of the same shape), q4k_matvec (2048 x
 2048 Q4_K, measured as one launch over 448 stacked copies), decode_3b (Qwen2.5-3B-shaped Q4_K_M
-decode tok/s after a 512-token context), decode_moe (Qwen3-30B-A3B-shaped MoE decode after a
-1024-token context), prefill_3b (one 512-token prompt through the Qwen2.5-3B-shaped model).
+decode tok/s, 128 tokens after a 512-token context), decode_moe (Qwen3-30B-A3B-shaped MoE decode,
+128 tokens after a 1024-token context), prefill_3b (one 512-token prompt through the
+Qwen2.5-3B-shaped model).
 
 Every line carries:
   roofline      the dominant kernel's algorithmic bytes / its average duration (HIP events on the
@@ -71,26 +72,22 @@ class Events:
 
 
 def per_launch_ms(stream, launch, n):
-    """Average duration (ms) of n launches, each bracketed by its own pair of HIP events recorded
-    on `stream` (the stream the kernel runs on)."""
+    """Average duration (ms) of n back-to-back launches on `stream` (the stream the kernel runs on):
+    one HIP event before the first and one after the last, so the figure is the kernels' own time
+    plus the (small) gaps between consecutive dispatches, without per-launch event overhead."""
     L = capi.lib()
-    evs = []
-    for _ in range(2 * n):
-        e = ctypes.c_void_p()
-        capi.check(L.sdy_event_new(ctypes.byref(e)))
-        evs.append(e)
+    e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+    capi.check(L.sdy_event_new(ctypes.byref(e0)))
+    capi.check(L.sdy_event_new(ctypes.byref(e1)))
+    capi.check(L.sdy_event_record(e0, stream))
     for i in range(n):
-        capi.check(L.sdy_event_record(evs[2 * i], stream))
         launch(i)
-        capi.check(L.sdy_event_record(evs[2 * i + 1], stream))
-    total = 0.0
+    capi.check(L.sdy_event_record(e1, stream))
     ms = ctypes.c_float()
-    for i in range(n):
-        capi.check(L.sdy_event_elapsed(ctypes.byref(ms), evs[2 * i], evs[2 * i + 1]))
-        total += ms.value
-    for e in evs:
+    capi.check(L.sdy_event_elapsed(ctypes.byref(ms), e0, e1))
+    for e in (e0, e1):
         capi.check(L.sdy_event_free(e))
-    return total / n
+    return ms.value / n
 
 
 def profiled_traffic(name):
@@ -535,7 +532,8 @@ def prefill_line(args, spec, label, n_prompt, desc):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default: 50; decode workloads: 128 generated tokens)")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="q6k_head",
                     choices=["q6k_head", "q8_0_head", "q4k_matvec", "decode_3b", "decode_moe", "prefill_3b"])
@@ -547,6 +545,8 @@ def main():
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
               "(the multi-GPU sharding of this path is a design note, not an implementation)", file=sys.stderr)
         sys.exit(2)
+    if args.steps is None:
+        args.steps = 128 if args.workload.startswith("decode") else 50
     capi.check(capi.lib().sdy_init())
     if args.workload == "q6k_head":
         line = bench_matvec(args, Q6_K, 151936, 2048, 8, stacked=False)
