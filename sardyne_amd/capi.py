@@ -137,6 +137,9 @@ _DEVICE_SIGNATURES = {
     "sdy_dequant_rows": (_int, [ctypes.POINTER(SdyMat), ctypes.c_long, ctypes.c_long, _vp, _vp]),
     "sdy_quantize": (_int, [_int, _vp, _vp, _int, _int, _vp]),
     "sdy_matvec": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp]),
+    "sdy_matvec_pair_ok": (_int, [ctypes.POINTER(SdyMat), _int, ctypes.POINTER(SdyMat), _int]),
+    "sdy_matvec_pair": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), ctypes.POINTER(SdyMat),
+                               ctypes.POINTER(SdyMvArgs), _vp]),
     "sdy_matvec_float": (_int, [_int, _vp, _int, ctypes.POINTER(SdyMvArgs), _vp]),
     "sdy_matvec_grouped": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp, _int, ctypes.c_long,
                                   ctypes.c_long, ctypes.c_long, _vp]),

@@ -153,6 +153,26 @@ static int norm_for(engine_ctx *c, const float *x, const float *wn, const dmat *
     return 0;
 }
 
+/* One token through two K-quant matrices in one launch (q|k and a v of another type): the Q8_K row
+ * of x is the one norm_for just wrote. */
+static int mm1_pair(engine_ctx *c, float *out1, const dmat *w1, const float *b1, float *out2, const dmat *w2,
+                    const float *b2) {
+    sdy_mv_args a1, a2;
+    memset(&a1, 0, sizeof a1);
+    memset(&a2, 0, sizeof a2);
+    a1.xq = a2.xq = c->xq[1];
+    a1.n_tok = a2.n_tok = 1;
+    a1.out = out1;
+    a1.out_stride = w1->n_out;
+    a1.bias = b1;
+    a1.row1 = w1->n_out;
+    a2.out = out2;
+    a2.out_stride = w2->n_out;
+    a2.bias = b2;
+    a2.row1 = w2->n_out;
+    return sdy_matvec_pair(&w1->m, &a1, &w2->m, &a2, c->st);
+}
+
 /* hb[t][i] = silu(gate_i . x) * (up_i . x) for n rows of x (gate/up fused and interleaved, or apart). */
 static int ffn_gate_up(engine_ctx *c, const float *x, int n, int new_input, const dmat *gate_up, const dmat *gate,
                        const dmat *up, int ffn) {
@@ -308,7 +328,10 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
             const int bias_fused = !in->qkv_bias ||
                                    (L->bk == L->bq + q_dim && (L->qkv_parts < 3 || L->bv == L->bk + kv_dim));
             TRY(norm_for(c, c->x, L->attn_norm, L->qkv_parts >= 2 ? &L->wqkv : &L->wq, 1));
-            if (L->qkv_parts >= 2 && bias_fused) {
+            if (L->qkv_parts == 2 && bias_fused &&
+                sdy_matvec_pair_ok(&L->wqkv.m, SDY_EPI_NONE, &L->wv.m, SDY_EPI_NONE)) {
+                TRY(mm1_pair(c, q, &L->wqkv, L->bq, v, &L->wv, L->bv)); /* q|k and v in one launch */
+            } else if (L->qkv_parts >= 2 && bias_fused) {
                 TRY(mm(c, q, c->xb, &L->wqkv, 1, L->bq, NULL, 0));
                 if (L->qkv_parts == 2) TRY(mm(c, v, c->xb, &L->wv, 1, L->bv, NULL, 0));
             } else {

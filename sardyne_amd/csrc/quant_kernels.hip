@@ -657,8 +657,9 @@ __global__ __launch_bounds__(THREADS) void k_matvec(MvArgs a) {
 // f32 order), so no LDS round trip is needed. 32-element types sum their unit terms with a fixed
 // butterfly over the row's T lanes (T a power of two). Waves stride over the iterations and load
 // the next iteration's weights while they compute the current one.
+// (the body of k_matvec_rl for workgroup bx of a grid of G, routed-expert slot `slot`)
 template <int WT, int MT, bool YREG>
-__global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
+SDY_DEV void matvec_rl_body(const MvArgs &a, long G, long bx, int slot) {
     extern __shared__ uint8_t lds[];
     // One token of Q8_K activations in memory: every lane reads the 64 activation bytes of its unit
     // (and the unit's bsums and block scale) straight into registers; no LDS staging, no barrier.
@@ -678,7 +679,6 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
     const uint8_t *xq = a.xq;
     float *out = a.out;
     if (a.slot_expert) {
-        const int slot = blockIdx.y;
         int e = a.slot_expert[slot];
         e = e < 0 ? 0 : (e >= a.n_slot_exp ? a.n_slot_exp - 1 : e);
         poff = (long)e * a.slot_rows;
@@ -689,7 +689,6 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
     const long n_it = (n_rows + rpi - 1) / rpi;
     // Workgroups are dealt round-robin over the 8 XCDs; renumber them so that consecutive work
     // (neighbouring rows) stays on one XCD and its L2.
-    const long G = gridDim.x, bx = blockIdx.x;
     const long vblk = (G % 8 == 0) ? (bx % 8) * (G / 8) + bx / 8 : bx;  // a bijection of [0, G)
     const long n_waves = G * WAVES, wid = vblk * WAVES + wave;
     // grid-stride: at any moment the waves of the grid read neighbouring rows, so the whole GPU
@@ -802,6 +801,20 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
         if (itx + 2 * S < n_it) load_it(itx + 2 * S, A);
         body(B, itx + S);
     }
+}
+
+template <int WT, int MT, bool YREG>
+__global__ __launch_bounds__(THREADS) void k_matvec_rl(MvArgs a) {
+    matvec_rl_body<WT, MT, YREG>(a, gridDim.x, blockIdx.x, blockIdx.y);
+}
+
+// Two one-token matvecs on the same Q8_K activations in one launch (q|k and v of a layer when v has
+// another type): workgroups [0, g1) run the first, [g1, gridDim.x) the second. g1 is a multiple of 8,
+// so each part keeps its own XCD-aware numbering.
+template <int WT1, int WT2>
+__global__ __launch_bounds__(THREADS) void k_matvec_rl_pair(MvArgs a, MvArgs b, int g1) {
+    if ((int)blockIdx.x < g1) matvec_rl_body<WT1, 1, true>(a, g1, blockIdx.x, 0);
+    else matvec_rl_body<WT2, 1, true>(b, (long)gridDim.x - g1, (long)blockIdx.x - g1, 0);
 }
 
 // Long rows, one token (K-quants with T > 64 units, e.g. n_in = 11008 with 172 units): a wave owns
@@ -1362,6 +1375,38 @@ static int launch_mv_rl(MvArgs &A, size_t lds, hipStream_t st, int n_slot = 1) {
     return sdy_check_launch("matvec");
 }
 
+// one-token K-quant matvecs of rows that fit k_matvec_rl's lanes: T <= 64, an even rows-per-iteration
+// count with the SwiGLU epilogue
+static bool rl_one_token_ok(const sdy_mat *m, int epilogue) {
+    const int T = m->n_units;
+    return (m->type == SDY_Q4_K || m->type == SDY_Q6_K) && T <= 64 &&
+           (epilogue != SDY_EPI_SWIGLU || (64 / T) % 2 == 0);
+}
+
+static long rl_wgs(const MvArgs &A, int per_cu) {
+    const int rpi = 64 / A.P.T;
+    const long n_it = (A.row1 - A.row0 + rpi - 1) / rpi;
+    long wgs = (n_it + WAVES - 1) / WAVES;
+    long cap = (long)(g_n_cu ? g_n_cu : 256) * per_cu;
+    if (cap < 8) cap = 8;
+    return wgs > cap ? cap : wgs;
+}
+
+template <int WT1, int WT2>
+static int launch_mv_pair(MvArgs &A, MvArgs &B, hipStream_t st) {
+    static int per_cu = 0;
+    if (per_cu == 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)k_matvec_rl_pair<WT1, WT2>, THREADS, 0) !=
+                hipSuccess || n < 1)
+            n = 1;
+        per_cu = n;
+    }
+    const long g1 = (rl_wgs(A, per_cu) + 7) / 8 * 8, g2 = rl_wgs(B, per_cu);
+    hipLaunchKernelGGL((k_matvec_rl_pair<WT1, WT2>), dim3((unsigned)(g1 + g2)), dim3(THREADS), 0, st, A, B, (int)g1);
+    return sdy_check_launch("matvec_pair");
+}
+
 template <int WT, int NI>
 static int launch_mv_lr_ni(MvArgs &A, size_t lds, hipStream_t st) {
     static int per_cu = 0;
@@ -1454,6 +1499,59 @@ static int mv_type(const sdy_mat *m, const sdy_mv_args *a, hipStream_t st) {
         t0 += n;
     }
     return 0;
+}
+
+static int check_mv_rows(const sdy_mat *m, const sdy_mv_args *a) {
+    if (a->row0 < 0 || a->row1 > m->n_rows || a->row0 > a->row1)
+        return sdy_fail(-1, "matvec rows [%ld, %ld) outside %ld", a->row0, a->row1, m->n_rows);
+    if (a->epilogue == SDY_EPI_SWIGLU && (((a->row1 - a->row0) | a->row0) & 1 || a->bias || a->resid))
+        return sdy_fail(-1, "matvec: the SwiGLU epilogue needs an even row range starting at an even row, no bias "
+                            "and no residual");
+    return 0;
+}
+
+static MvArgs rl_args(const sdy_mat *m, const sdy_mv_args *a) {
+    MvArgs A = {};
+    A.P = planes_of(m);
+    A.xq = (const uint8_t *)a->xq;
+    A.n_tok = 1;
+    A.out = a->out;
+    A.out_stride = a->out_stride;
+    A.bias = a->bias;
+    A.resid = a->resid;
+    A.row0 = a->row0;
+    A.row1 = a->row1;
+    A.swiglu = a->epilogue == SDY_EPI_SWIGLU;
+    A.nterm = A.P.nb;
+    return A;
+}
+
+extern "C" int sdy_matvec_pair_ok(const sdy_mat *m1, int epilogue1, const sdy_mat *m2, int epilogue2) {
+    return rl_one_token_ok(m1, epilogue1) && rl_one_token_ok(m2, epilogue2);
+}
+
+extern "C" int sdy_matvec_pair(const sdy_mat *m1, const sdy_mv_args *a1, const sdy_mat *m2, const sdy_mv_args *a2,
+                               sdy_stream s) {
+    if (!sdy_matvec_pair_ok(m1, a1->epilogue, m2, a2->epilogue))
+        return sdy_fail(-1, "matvec_pair: two Q4_K / Q6_K matrices of at most 4096-element rows (64 units) needed");
+    if (a1->n_tok != 1 || a2->n_tok != 1) return sdy_fail(-1, "matvec_pair: one token only");
+    int rc;
+    if ((rc = check_mv_rows(m1, a1)) || (rc = check_mv_rows(m2, a2))) return rc;
+    if (!g_n_cu) {
+        int n_cu = 0;
+        size_t mem = 0;
+        sdy_device_info(&n_cu, &mem);
+        g_n_cu = n_cu;
+    }
+    if (a1->row0 == a1->row1) return sdy_matvec(m2, a2, s);
+    if (a2->row0 == a2->row1) return sdy_matvec(m1, a1, s);
+    MvArgs A = rl_args(m1, a1), B = rl_args(m2, a2);
+    hipStream_t st = (hipStream_t)s;
+    const bool q4a = m1->type == SDY_Q4_K, q4b = m2->type == SDY_Q4_K;
+    if (q4a && q4b) return launch_mv_pair<SDY_Q4_K, SDY_Q4_K>(A, B, st);
+    if (q4a) return launch_mv_pair<SDY_Q4_K, SDY_Q6_K>(A, B, st);
+    if (q4b) return launch_mv_pair<SDY_Q6_K, SDY_Q4_K>(A, B, st);
+    return launch_mv_pair<SDY_Q6_K, SDY_Q6_K>(A, B, st);
 }
 
 extern "C" int sdy_matvec(const sdy_mat *m, const sdy_mv_args *a, sdy_stream s) {

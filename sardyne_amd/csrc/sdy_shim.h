@@ -100,6 +100,11 @@ typedef struct {
 enum { SDY_EPI_NONE = 0, SDY_EPI_SWIGLU = 1 };
 /* out = W · x for rows [row0, row1) and n_tok tokens. */
 int sdy_matvec(const sdy_mat *m, const sdy_mv_args *a, sdy_stream s);
+/* Two one-token matvecs in one launch (each with the bits of sdy_matvec): Q4_K / Q6_K matrices of
+ * at most 4096-element rows, e.g. a layer's q|k and a v of another type on the same Q8_K row. */
+int sdy_matvec_pair_ok(const sdy_mat *m1, int epilogue1, const sdy_mat *m2, int epilogue2);
+int sdy_matvec_pair(const sdy_mat *m1, const sdy_mv_args *a1, const sdy_mat *m2, const sdy_mv_args *a2,
+                    sdy_stream s);
 /* Grouped one-token matvec over routed experts: m stacks experts of slot_rows rows; for each of
  * n_slot slots, rows [row0, row1) of expert slot_expert[slot] (device array) times the slot's
  * Q8_K activation row (a->xq + slot * xq_slot bytes) go to a->out + slot * out_slot. Q4_K / Q6_K,

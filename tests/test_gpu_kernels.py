@@ -309,6 +309,56 @@ def test_norm_quant_equals_rmsnorm_then_quantize(vt, n, n_rows):
         assert np.array_equal(q2, O.quantize(exp, vt).reshape(-1))
 
 
+@pytest.mark.parametrize("k1,k2", [("Q4_K", "Q6_K"), ("Q6_K", "Q4_K"), ("Q4_K", "Q4_K"), ("Q6_K", "Q6_K")])
+@pytest.mark.parametrize("n_in,n1,n2,swiglu", [(2048, 2560, 256, False), (768, 70, 33, False), (2048, 40, 96, True),
+                                               (4096, 40, 96, False), (256, 17, 1000, False)])
+def test_matvec_pair(k1, k2, n_in, n1, n2, swiglu):
+    """Two one-token matvecs on one Q8_K row in one launch (a layer's q|k and v): each output has
+    the bits of its own sdy_matvec call (bias on the first, residual or SwiGLU on the second)."""
+    L = lib()
+    rng = np.random.default_rng(n_in + n1 + n2)
+    w1 = random_blocks(k1, n1 * n_in // 256, rng).reshape(n1, -1)
+    w2 = random_blocks(k2, n2 * n_in // 256, rng).reshape(n2, -1)
+    m1, m2 = capi.DeviceMatrix(TYPES[k1], n_in, n1, w1), capi.DeviceMatrix(TYPES[k2], n_in, n2, w2)
+    x = rng.standard_normal((1, n_in)).astype(np.float32)
+    dq = capi.DeviceBuffer.from_array(O.quantize(x, O.Q8_K))
+    bias = capi.DeviceBuffer.from_array(rng.standard_normal(n1).astype(np.float32))
+    o2 = n2 // 2 if swiglu else n2
+    resid = capi.DeviceBuffer.from_array(rng.standard_normal(o2).astype(np.float32))
+    epi2 = capi.EPI_SWIGLU if swiglu else capi.EPI_NONE
+    assert L.sdy_matvec_pair_ok(ctypes.byref(m1.m), capi.EPI_NONE, ctypes.byref(m2.m), epi2) == 1
+    outs = [capi.DeviceBuffer.from_array(np.full(n, np.nan, np.float32)) for n in (n1, o2, n1, o2)]
+    args = []
+    for i in (0, 2):
+        a1 = capi.SdyMvArgs(xq=dq.ptr, n_tok=1, out=outs[i].ptr, out_stride=n1, bias=bias.ptr, row0=0, row1=n1)
+        a2 = capi.SdyMvArgs(xq=dq.ptr, n_tok=1, out=outs[i + 1].ptr, out_stride=o2, resid=None if swiglu else resid.ptr,
+                            row0=0, row1=n2, epilogue=epi2)
+        args.append((a1, a2))
+    capi.check(L.sdy_matvec_pair(ctypes.byref(m1.m), ctypes.byref(args[0][0]), ctypes.byref(m2.m),
+                                 ctypes.byref(args[0][1]), None))
+    capi.check(L.sdy_matvec(ctypes.byref(m1.m), ctypes.byref(args[1][0]), None))
+    capi.check(L.sdy_matvec(ctypes.byref(m2.m), ctypes.byref(args[1][1]), None))
+    got = [outs[i].to_array(np.float32, n) for i, n in enumerate((n1, o2, n1, o2))]
+    assert np.array_equal(bits(got[0]), bits(got[2]))
+    assert np.array_equal(bits(got[1]), bits(got[3]))
+    assert not np.isnan(got[0]).any() and not np.isnan(got[1]).any()
+
+
+def test_matvec_pair_rejects_unsupported():
+    """The paired launch is for Q4_K / Q6_K rows of at most 64 units and one token."""
+    L = lib()
+    rng = np.random.default_rng(5)
+    a = capi.DeviceMatrix(O.Q4_K, 11008, 4, random_blocks("Q4_K", 4 * 43, rng).reshape(4, -1))
+    b = capi.DeviceMatrix(O.Q8_0, 256, 4, random_blocks("Q8_0", 4 * 8, rng).reshape(4, -1))
+    c = capi.DeviceMatrix(O.Q6_K, 256, 4, random_blocks("Q6_K", 4, rng).reshape(4, -1))
+    assert L.sdy_matvec_pair_ok(ctypes.byref(a.m), capi.EPI_NONE, ctypes.byref(c.m), capi.EPI_NONE) == 0
+    assert L.sdy_matvec_pair_ok(ctypes.byref(c.m), capi.EPI_NONE, ctypes.byref(b.m), capi.EPI_NONE) == 0
+    out = capi.DeviceBuffer(64)
+    x = capi.DeviceBuffer(292)
+    a1 = capi.SdyMvArgs(xq=x.ptr, n_tok=2, out=out.ptr, out_stride=4, row0=0, row1=4)
+    assert L.sdy_matvec_pair(ctypes.byref(c.m), ctypes.byref(a1), ctypes.byref(c.m), ctypes.byref(a1), None) != 0
+
+
 @pytest.mark.parametrize("kind", ["Q4_K", "Q6_K", "Q8_0", "Q5_0"])
 @pytest.mark.parametrize("n_in,ffn,n_tok", [(2048, 96, 1), (1024, 40, 3), (11008, 8, 2), (768, 20, 1)])
 def test_swiglu_epilogue(kind, n_in, ffn, n_tok):
