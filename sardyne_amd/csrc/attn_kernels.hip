@@ -467,6 +467,93 @@ __global__ __launch_bounds__(64) void k_attn_decode_wv(AttnArgs a) {
     a.out[(size_t)(h0 + r) * HD + d] = acc;
 }
 
+// Decode weighted V, four heads of a KV group per wave (n_rep % 4 == 0): lane (r, c) owns dim
+// s*16 + c of head h0 + r and runs its FMA chain out = fma(p_j, v_j[d], out) over j = 0..pos in order
+// (the reference's in-order axpy), exactly as k_attn_decode_wv, with fewer instructions per
+// position. Per block of 16 positions the wave issues four V loads, lane (r, c) reading V[j + r][d]
+// (four positions x 16 dims per instruction), and one weight load, lane (r, c) reading p[h0 + r][j + c].
+// Both go through wave-private LDS buffers ([c][position] and [r][position]), so one 16-byte read
+// gives a lane four positions of its dim, and one (a broadcast within the head's 16 lanes) four
+// of its weights. R blocks of loads stay in flight in registers; LDS is double-buffered by block
+// parity (block b + 1 is staged while block b is consumed).
+template <int HD, int R>
+__global__ __launch_bounds__(64) void k_attn_decode_wv4(AttnArgs a) {
+    constexpr int NS = HD / 16;
+    static_assert(NS * 16 == HD && R % 2 == 0, "shape");
+    __shared__ __align__(16) float tv[2][4][64];  // [block parity][group][c * 4 + position in group]
+    __shared__ __align__(16) float tw[2][64];     // [block parity][r * 16 + position in block]
+    const int lane = threadIdx.x, r = lane >> 4, c = lane & 15;
+    const int n_rep = a.n_head / a.n_kv_head, n_hg = n_rep / 4;
+    const int s = blockIdx.x % NS, hg = (blockIdx.x / NS) % n_hg, g = blockIdx.x / (NS * n_hg);
+    const int h0 = g * n_rep + hg * 4, d = s * 16 + c;
+    const int n = a.step[1] + 1, nbk = (n + 15) / 16;
+    // Buffer reads, range-checked on the lane offset: V rows at or past n, and weights past the
+    // last head's row, read as 0; positions past n are never used.
+    const __amdgpu_buffer_rsrc_t rsv =
+        __builtin_amdgcn_make_buffer_rsrc(a.v_cache + g * a.head_stride, (short)0, n * HD * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(a.scores + (size_t)h0 * a.max_kv, (short)0,
+                                                                         4 * a.max_kv * 4, 0x00020000);
+    const uint32_t ov = (uint32_t)(r * HD + d) * 4, ow = (uint32_t)(r * a.max_kv + c) * 4;
+    float rv[R][4], rw[R];  // ring slot t holds the loads of a block b with b % R == t
+    auto issue = [&](int t, uint32_t b) {
+        const uint32_t vb = ov + b * 16u * HD * 4;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            rv[t][q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsv, vb + q * 4 * HD * 4, 0, 0));
+        rw[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsw, ow + b * 64u, 0, 0));
+    };
+    auto stage = [&](int t, int par) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) tv[par][q][c * 4 + r] = rv[t][q];
+        tw[par][lane] = rw[t];
+    };
+    float acc = 0.0f;
+    // block at position jb from LDS buffer par; full: all 16 positions are below n
+    auto consume = [&](int par, int jb, bool full) {
+        f32x4 vv[4], ww[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            vv[q] = *reinterpret_cast<const f32x4 *>(&tv[par][q][c * 4]);
+            ww[q] = *reinterpret_cast<const f32x4 *>(&tw[par][r * 16 + 4 * q]);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                if (full || jb + 4 * q + k < n) acc = fmaf(ww[q][k], vv[q][k], acc);
+    };
+#pragma unroll
+    for (int t = 0; t < R; t++) {
+        issue(t, t);
+        __builtin_amdgcn_sched_barrier(0);  // issued in block order
+    }
+    stage(0, 0);
+    // rounds of R blocks that lie wholly below n: straight-line code, so the loads in flight are the
+    // same on every path (a block staged past n reads zeros and is never consumed)
+    int b0 = 0;
+    for (; 16 * (b0 + R) <= n; b0 += R) {
+#pragma unroll
+        for (int t = 0; t < R; t++) {
+            stage((t + 1) % R, (t + 1) & 1);
+            consume(t & 1, 16 * (b0 + t), true);
+            // an opaque zero that depends on acc: the refill of slot t cannot be issued before the
+            // slot's weights are read, so it reuses the slot's registers
+            uint32_t z;
+            asm volatile("s_mov_b32 %0, 0" : "=s"(z) : "v"(acc));
+            issue(t, (uint32_t)(b0 + t + R) + z);
+        }
+    }
+    // the last (fewer than R) blocks, already in flight
+#pragma unroll
+    for (int t = 0; t < R; t++) {
+        const int b = b0 + t;
+        if (b >= nbk) break;
+        if (b + 1 < nbk) stage((t + 1) % R, (t + 1) & 1);
+        consume(t & 1, 16 * b, false);
+    }
+    a.out[(size_t)(h0 + r) * HD + d] = acc;
+}
+
 // Any head_dim (hd % 4 == 0 is not required): the same arithmetic with runtime loops and scalar LDS
 // reads. Scores: as k_attn_scores (prefill or decode), K rows at an odd stride (hd | 1).
 SDY_DEV float dot_avx2_order_any(const float *q, const float *k, int hd) {
@@ -663,8 +750,9 @@ static int launch_attn_any(AttnArgs &A, int hd, int nc, int n_tblk, hipStream_t 
     return 0;
 }
 
-// decode: k_attn_scores, k_attn_decode_softmax, k_attn_decode_wv (four heads of a KV group per wave
-// when n_rep allows, else one), then the Q8_K row of the output when asked for.
+// decode: k_attn_scores, k_attn_decode_softmax, k_attn_decode_wv4 (four heads of a KV group per wave)
+// or, when 4 does not divide n_rep, k_attn_decode_wv (one head per wave), then the Q8_K row of the
+// output when asked for.
 template <int HD>
 static int launch_attn_decode(AttnArgs &A, int nc, hipStream_t st) {
     const int n_rep = A.n_head / A.n_kv_head;
@@ -676,11 +764,10 @@ static int launch_attn_decode(AttnArgs &A, int nc, hipStream_t st) {
     if ((rc = sdy_check_launch("attention_scores"))) return rc;
     hipLaunchKernelGGL(k_attn_decode_softmax, dim3(A.n_head), dim3(256), 0, st, A);
     if ((rc = sdy_check_launch("attention_decode_softmax"))) return rc;
-    constexpr int HPW = 4;
-    if (n_rep % HPW) {
+    if (n_rep % 4) {
         hipLaunchKernelGGL((k_attn_decode_wv<HD, 1, 32>), dim3(A.n_head * (HD / 64)), dim3(64), 0, st, A);
     } else {
-        hipLaunchKernelGGL((k_attn_decode_wv<HD, HPW, 32>), dim3(A.n_head * HD / 64), dim3(64), 0, st, A);
+        hipLaunchKernelGGL((k_attn_decode_wv4<HD, 8>), dim3(A.n_head * HD / 64), dim3(64), 0, st, A);
     }
     if ((rc = sdy_check_launch("attention_decode_wv"))) return rc;
     if (A.xq) return sdy_quantize(SDY_Q8_K, A.out, A.xq, A.n_head * HD, 1, (sdy_stream)st);
