@@ -508,19 +508,22 @@ __global__ __launch_bounds__(64) void k_attn_decode_wv4(AttnArgs a) {
         tw[par][lane] = rw[t];
     };
     float acc = 0.0f;
-    // block at position jb from LDS buffer par; full: all 16 positions are below n
-    auto consume = [&](int par, int jb, bool full) {
-        f32x4 vv[4], ww[4];
+    // a block's operands out of LDS buffer par into registers set e (read one block ahead of use)
+    f32x4 vv[2][4], ww[2][4];
+    auto fetch = [&](int e, int par) {
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            vv[q] = *reinterpret_cast<const f32x4 *>(&tv[par][q][c * 4]);
-            ww[q] = *reinterpret_cast<const f32x4 *>(&tw[par][r * 16 + 4 * q]);
+            vv[e][q] = *reinterpret_cast<const f32x4 *>(&tv[par][q][c * 4]);
+            ww[e][q] = *reinterpret_cast<const f32x4 *>(&tw[par][r * 16 + 4 * q]);
         }
+    };
+    // the chain over the block at position jb in registers set e; full: all 16 positions below n
+    auto consume = [&](int e, int jb, bool full) {
 #pragma unroll
         for (int q = 0; q < 4; q++)
 #pragma unroll
             for (int k = 0; k < 4; k++)
-                if (full || jb + 4 * q + k < n) acc = fmaf(ww[q][k], vv[q][k], acc);
+                if (full || jb + 4 * q + k < n) acc = fmaf(ww[e][q][k], vv[e][q][k], acc);
     };
 #pragma unroll
     for (int t = 0; t < R; t++) {
@@ -528,13 +531,18 @@ __global__ __launch_bounds__(64) void k_attn_decode_wv4(AttnArgs a) {
         __builtin_amdgcn_sched_barrier(0);  // issued in block order
     }
     stage(0, 0);
+    fetch(0, 0);
     // rounds of R blocks that lie wholly below n: straight-line code, so the loads in flight are the
-    // same on every path (a block staged past n reads zeros and is never consumed)
+    // same on every path (a block staged past n reads zeros and is never consumed). Iteration t
+    // stages block t + 1 and reads it back (a wave's LDS operations run in order), then runs the
+    // chain over block t, whose operands were read in the previous iteration.
     int b0 = 0;
     for (; 16 * (b0 + R) <= n; b0 += R) {
 #pragma unroll
         for (int t = 0; t < R; t++) {
             stage((t + 1) % R, (t + 1) & 1);
+            fetch((t + 1) & 1, (t + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);  // the reads of block t + 1 go out before block t's chain
             consume(t & 1, 16 * (b0 + t), true);
             // an opaque zero that depends on acc: the refill of slot t cannot be issued before the
             // slot's weights are read, so it reuses the slot's registers
@@ -548,7 +556,10 @@ __global__ __launch_bounds__(64) void k_attn_decode_wv4(AttnArgs a) {
     for (int t = 0; t < R; t++) {
         const int b = b0 + t;
         if (b >= nbk) break;
-        if (b + 1 < nbk) stage((t + 1) % R, (t + 1) & 1);
+        if (b + 1 < nbk) {
+            stage((t + 1) % R, (t + 1) & 1);
+            fetch((t + 1) & 1, (t + 1) & 1);
+        }
         consume(t & 1, 16 * b, false);
     }
     a.out[(size_t)(h0 + r) * HD + d] = acc;
