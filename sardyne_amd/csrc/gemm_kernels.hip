@@ -643,10 +643,25 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) isum[mt][nt] = float16v{};
+        // the activation fragments of step st = 4 un + s (16-element chunk 8 un + 2 s + h of each token
+        // tile), read from LDS one step ahead of their MFMAs
+        half8 bf[2][NT];
+        auto read_b = [&](int st, half8 (&dst)[NT]) {
+            const int c = 8 * (st >> 2) + 2 * (st & 3) + h;
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const int t = 32 * nt + lr;
+                dst[nt] = *reinterpret_cast<const half8 *>(bbuf + 16 * (t * 32 + (c ^ (t & 7))));
+            }
+        };
+        read_b(0, bf[0]);
 #pragma unroll
         for (int un = 0; un < 4; un++) {
 #pragma unroll
             for (int s = 0; s < 4; s++) {
+                const int st = 4 * un + s;
+                if (st + 1 < 16) read_b(st + 1, bf[(st + 1) & 1]);
+                __builtin_amdgcn_sched_barrier(0);  // the next step's reads go out before this step's work
                 half8 a[MT];
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
@@ -669,14 +684,11 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
                         a[mt] = frag_scaled(lo | hi, off6, half2v{f, f});
                     }
                 }
-                const int c = 8 * un + 2 * s + h;
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) {
-                    const int t = 32 * nt + lr;
-                    const half8 b = *reinterpret_cast<const half8 *>(bbuf + 16 * (t * 32 + (c ^ (t & 7))));
 #pragma unroll
                     for (int mt = 0; mt < MT; mt++)
-                        isum[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt], b, isum[mt][nt], 0, 0, 0);
+                        isum[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt], bf[st & 1][nt], isum[mt][nt], 0, 0, 0);
                 }
             }
         }
