@@ -977,7 +977,18 @@ __global__ __launch_bounds__(THREADS) void k_matvec_float_dot(const uint8_t *__r
     float acc = 0.0f;
     const int n32 = n_in & ~31, n8 = n_in & ~7;
     int i = L;
-    for (; i + 32 * 7 < n32; i += 32 * 8) {  // 8 steps' loads first, then their chain in order
+    constexpr int B = 32;  // steps whose loads go out together before their chain runs in order
+    for (; i + 32 * (B - 1) < n32; i += 32 * B) {
+        float wv[B], xv[B];
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            wv[j] = welem<WT>(wr, i + 32 * j);
+            xv[j] = xr[i + 32 * j];
+        }
+#pragma unroll
+        for (int j = 0; j < B; j++) acc = fmaf(wv[j], xv[j], acc);
+    }
+    for (; i + 32 * 7 < n32; i += 32 * 8) {
         float wv[8], xv[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
