@@ -23,14 +23,22 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
     const int t = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const float *xr = x + (size_t)t * n;
     float4 keep[NREG];
+    // the norm weights of the lane's first NREG super-blocks, requested before the row's reduction
+    float4 wk[NREG];
+    if constexpr (VT == SDY_Q8_K) {
+        const int nb = n / 256;
+#pragma unroll
+        for (int k = 0; k < NREG; k++) {
+            const int s = wave + 4 * k < nb ? wave + 4 * k : nb - 1;
+            wk[k] = s >= 0 ? *reinterpret_cast<const float4 *>(w + 256 * s + 4 * lane) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
     const double ss = sdy_row_sumsq<VT == SDY_Q8_K ? NREG : 0>(xr, n, keep, sh);
     const float scale = (float)(1.0 / sqrt(ss / (double)n + (double)eps));
     if constexpr (VT == SDY_Q8_K) {
         const int nb = n / 256;
         const bool in_regs = sdy_rows_vec4(xr, n);
-        auto values = [&](int s, const float4 &v) {
-            const int e0 = 256 * s + 4 * lane;
-            const float4 wv = *reinterpret_cast<const float4 *>(w + e0);
+        auto values = [&](int s, const float4 &v, const float4 &wv) {
             float4 o;
             o.x = (v.x * scale) * wv.x;
             o.y = (v.y * scale) * wv.y;
@@ -51,7 +59,7 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
 #pragma unroll
         for (int k = 0; k < NREG; k++) {
             const int s = wave + 4 * k < nb ? wave + 4 * k : nb - 1;
-            const float4 o = values(s, in_regs ? keep[k] : from_mem(s));
+            const float4 o = values(s, in_regs ? keep[k] : from_mem(s), wk[k]);
             xs[k][0] = o.x;
             xs[k][1] = o.y;
             xs[k][2] = o.z;
@@ -69,7 +77,7 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
                 if (lane == 0) *reinterpret_cast<float *>(ob) = r[k].d;
             }
         for (int s = wave + 4 * NREG; s < nb; s += 4) {
-            const float4 o = values(s, from_mem(s));
+            const float4 o = values(s, from_mem(s), *reinterpret_cast<const float4 *>(w + 256 * s + 4 * lane));
             const float x1[4] = {o.x, o.y, o.z, o.w};
             store_xb(s, x1);
             sdy_q8k_block(x1, lane, xq + ((size_t)t * nb + s) * 292);

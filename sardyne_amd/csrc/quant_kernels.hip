@@ -817,6 +817,126 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl_pair(MvArgs a, MvArgs b, 
     else matvec_rl_body<WT2, 1, true>(b, (long)gridDim.x - g1, (long)blockIdx.x - g1, 0);
 }
 
+// The row sum of one K-quant unit term per lane (one token, activations in registers): the quad
+// reduction leaves super-block s of row rl in lane rl*T + 4s, and lane rl*T folds the terms in
+// super-block order from the reference's initial 0.0f. All the lane reads are issued before the
+// first add (one LDS round trip), for up to 16 super-blocks (T <= 64).
+template <int WT>
+SDY_DEV float rl_row_sum(const WRegs<WT> &cur, const uint4 (&Yr)[4], uint2 bsr, float ydr, int u, int lane, int T) {
+    int isum, msum;
+    float term = 0.0f;
+    unit_dot<WT>(cur, Yr, bsr, u, isum, msum, term, make_float2(0.f, 0.f), make_int2(0, 0));
+    isum = sdy_quad_sum(isum);
+    if constexpr (WT == SDY_Q4_K) {
+        msum = sdy_quad_sum(msum);
+        const float d = sdy_h2f((uint16_t)(cur.c.x & 0xFFFFu)), dmin = sdy_h2f((uint16_t)(cur.c.x >> 16));
+        const float dall = ydr * d, dmn = ydr * dmin;
+        const float t1 = dall * (float)isum, t2 = dmn * (float)msum;
+        term = t1 - t2;
+    } else {
+        const float d = sdy_h2f((uint16_t)cur.g);
+        const float ydd = ydr * d;
+        term = ydd * (float)isum;
+    }
+    const int nsb = T >> 2;
+    float tv[16];
+#pragma unroll
+    for (int s = 1; s < 16; s++) tv[s] = __shfl(term, (lane + 4 * s) & 63);
+    float acc = 0.0f + term;
+#pragma unroll
+    for (int s = 1; s < 16; s++)
+        if (s < nsb) acc = acc + tv[s];
+    return acc;
+}
+
+// One token, K-quants with at most 64 units per row (every one-token matvec of a decode step but
+// the output head): wave w of the S waves of the grid takes the NIT iterations w, w + S, ...,
+// w + (NIT - 1) S of 64/T rows each, and issues every load it needs (the weights of all its
+// iterations, its unit's activations, the bias and residual of its rows) before its first
+// computation, so the wave waits for one memory round trip; the results are stored at the end.
+// Same lane layout and arithmetic as k_matvec_rl, so the bits are the same.
+// (the body of k_matvec_1t for workgroup bx of a grid of G, routed-expert slot `slot`)
+template <int WT, int NIT>
+SDY_DEV void matvec_1t_body(const MvArgs &a, long G, long bx, int slot) {
+    const int T = a.P.T;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rpi = 64 / T;
+    const int rl_ = lane / T, u = lane - rl_ * T;
+    const bool lane_on = rl_ < rpi;
+    const int rl = lane_on ? rl_ : 0;
+    long poff = 0;
+    const uint8_t *xq = a.xq;
+    float *out = a.out;
+    if (a.slot_expert) {
+        int e = a.slot_expert[slot];
+        e = e < 0 ? 0 : (e >= a.n_slot_exp ? a.n_slot_exp - 1 : e);
+        poff = (long)e * a.slot_rows;
+        xq += (size_t)slot * a.xq_slot;
+        out += (size_t)slot * a.out_slot;
+    }
+    const long n_rows = a.row1 - a.row0;
+    const long n_it = (n_rows + rpi - 1) / rpi;
+    const long vblk = (G % 8 == 0) ? (bx % 8) * (G / 8) + bx / 8 : bx;  // XCD-aware renumbering
+    const long S = G * WAVES, wid = vblk * WAVES + wave;
+    if (wid >= n_it) return;
+    WRegs<WT> R[NIT];
+    long row[NIT];
+#pragma unroll
+    for (int k = 0; k < NIT; k++) {
+        row[k] = a.row0 + (wid + k * S) * rpi + rl;
+        load_w<WT>(a.P, (uint32_t)((row[k] < a.row1 ? row[k] : a.row0) + poff), (uint32_t)u, R[k]);
+    }
+    uint4 Yr[4];
+    const uint8_t *blk = xq + (size_t)(u >> 2) * 292;
+    const uint8_t *yb = blk + 4 + 64 * (u & 3);
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        Yr[q] = make_uint4(ld4(yb + 16 * q), ld4(yb + 16 * q + 4), ld4(yb + 16 * q + 8), ld4(yb + 16 * q + 12));
+    const uint2 bsr = make_uint2(ld4(blk + 260 + 8 * (u & 3)), ld4(blk + 264 + 8 * (u & 3)));
+    const float ydr = *reinterpret_cast<const float *>(blk);
+    // the bias and residual of the rows this lane stores
+    float bv[NIT], rv[NIT];
+    const bool st_lane = u == 0 && lane_on && !a.swiglu;
+#pragma unroll
+    for (int k = 0; k < NIT; k++) {
+        bv[k] = 0.0f;
+        rv[k] = 0.0f;
+        if (st_lane && row[k] < a.row1) {
+            if (a.bias) bv[k] = a.bias[row[k]];
+            if (a.resid) rv[k] = a.resid[row[k]];
+        }
+    }
+    float acc[NIT];
+#pragma unroll
+    for (int k = 0; k < NIT; k++) acc[k] = rl_row_sum<WT>(R[k], Yr, bsr, ydr, u, lane, T);
+#pragma unroll
+    for (int k = 0; k < NIT; k++) {
+        const bool valid = lane_on && row[k] < a.row1;
+        if (a.swiglu) {
+            // rows per iteration is even and row0 is even: lane (rl+1)*T holds the up row
+            const float up = __shfl(acc[k], (lane + T) & 63);
+            if (u == 0 && (rl & 1) == 0 && valid) out[(row[k] - a.row0) >> 1] = sdy_silu_mul1(acc[k], up);
+        } else if (u == 0 && valid) {
+            float v = acc[k];
+            if (a.bias) v = v + bv[k];
+            if (a.resid) v = rv[k] + v;
+            out[row[k]] = v;
+        }
+    }
+}
+
+template <int WT, int NIT>
+__global__ __launch_bounds__(THREADS) void k_matvec_1t(MvArgs a) {
+    matvec_1t_body<WT, NIT>(a, gridDim.x, blockIdx.x, blockIdx.y);
+}
+
+// k_matvec_1t's pair form (see k_matvec_rl_pair), one iteration per wave
+template <int WT1, int WT2>
+__global__ __launch_bounds__(THREADS) void k_matvec_1t_pair(MvArgs a, MvArgs b, int g1) {
+    if ((int)blockIdx.x < g1) matvec_1t_body<WT1, 1>(a, g1, blockIdx.x, 0);
+    else matvec_1t_body<WT2, 1>(b, (long)gridDim.x - g1, (long)blockIdx.x - g1, 0);
+}
+
 // Long rows, one token (K-quants with T > 64 units, e.g. n_in = 11008 with 172 units): a wave owns
 // whole rows, lane l handles units l, l + 64, ..., l + 64 (NI - 1) of a row. After the quad
 // reduction the term of super-block s = 16k + q sits in lane 4q of pass k, and the row sum folds the
@@ -841,6 +961,15 @@ __global__ __launch_bounds__(THREADS) void k_matvec_lr(MvArgs a) {
     WRegs<WT> A[NI];
     if (wid >= n_rows) return;
     load_row(wid, A);
+    // the bias and residual of the row, requested with its weights (lane 0 stores)
+    float bv = 0.0f, rv = 0.0f;
+    auto load_br = [&](long r) {
+        if (lane == 0) {
+            if (a.bias) bv = a.bias[a.row0 + r];
+            if (a.resid) rv = a.resid[a.row0 + r];
+        }
+    };
+    load_br(wid);
     // the lane's activations (the 64 Q8_K bytes of its unit in each pass, their bsums and the block
     // scale) straight from memory into registers, requested with the first row's weights: no LDS
     // staging, no barrier
@@ -893,16 +1022,18 @@ __global__ __launch_bounds__(THREADS) void k_matvec_lr(MvArgs a) {
                 }
             }
         if (lane == 0) {
-            const long row = a.row0 + r;
-            if (a.bias) acc = acc + a.bias[row];
-            if (a.resid) acc = a.resid[row] + acc;
-            a.out[row] = acc;
+            if (a.bias) acc = acc + bv;
+            if (a.resid) acc = rv + acc;
+            a.out[a.row0 + r] = acc;
         }
     };
     // one row in registers per wave: the waves resident on a SIMD overlap each other's loads
     for (long r = wid; r < n_rows; r += S) {
         body(A, r);
-        if (r + S < n_rows) load_row(r + S, A);
+        if (r + S < n_rows) {
+            load_row(r + S, A);
+            load_br(r + S);
+        }
     }
 }
 
@@ -1365,8 +1496,50 @@ static int launch_mv_k(MvArgs &A, size_t lds, hipStream_t st) {
 
 static size_t mv_lds_bytes_rl(int T, int MT) { return (size_t)MT * 4 * T * 16 + (size_t)MT * T * 16; }
 
+// Workgroups of a THREADS-thread kernel without dynamic LDS that the GPU holds at once.
+static long resident_wgs(const void *fn, int &per_cu) {
+    if (per_cu == 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, THREADS, 0) != hipSuccess || n < 1) n = 1;
+        per_cu = n;
+    }
+    return (long)(g_n_cu ? g_n_cu : 256) * per_cu;
+}
+
+template <int WT, int NIT>
+static long cap_1t() {
+    static int per_cu = 0;
+    return resident_wgs((const void *)k_matvec_1t<WT, NIT>, per_cu);
+}
+
+// One token on k_matvec_1t with the smallest NIT (iterations per wave, at most 4) whose grid the GPU
+// holds at once, so that every wave's loads go out at the start; 1 when no NIT fits (the caller
+// then runs the persistent k_matvec_rl).
+template <int WT>
+static int launch_mv_1t(MvArgs &A, hipStream_t st, int n_slot) {
+    const int rpi = 64 / A.P.T;
+    const long n_it = (A.row1 - A.row0 + rpi - 1) / rpi;
+    auto wgs = [&](int nit) { return (n_it + (long)WAVES * nit - 1) / ((long)WAVES * nit); };
+#define SDY_1T(NIT)                                                                                                  \
+    if (wgs(NIT) * n_slot <= cap_1t<WT, NIT>()) {                                                                    \
+        hipLaunchKernelGGL((k_matvec_1t<WT, NIT>), dim3((unsigned)wgs(NIT), (unsigned)n_slot), dim3(THREADS), 0, st, \
+                           A);                                                                                       \
+        return sdy_check_launch("matvec");                                                                           \
+    }
+    SDY_1T(1)
+    SDY_1T(2)
+    SDY_1T(3)
+    SDY_1T(4)
+#undef SDY_1T
+    return 1;
+}
+
 template <int WT, int MT, bool YREG>
 static int launch_mv_rl(MvArgs &A, size_t lds, hipStream_t st, int n_slot = 1) {
+    if constexpr (MT == 1 && YREG && is_k(WT)) {
+        const int rc = launch_mv_1t<WT>(A, st, n_slot);
+        if (rc <= 0) return rc;
+    }
     static int per_cu = 0;
     static size_t per_cu_lds = 0;
     const void *fn = (const void *)k_matvec_rl<WT, MT, YREG>;
@@ -1405,6 +1578,20 @@ static long rl_wgs(const MvArgs &A, int per_cu) {
 
 template <int WT1, int WT2>
 static int launch_mv_pair(MvArgs &A, MvArgs &B, hipStream_t st) {
+    {
+        static int per_cu_1t = 0;
+        const long cap = resident_wgs((const void *)k_matvec_1t_pair<WT1, WT2>, per_cu_1t);
+        auto wgs1 = [](const MvArgs &M) {
+            const int rpi = 64 / M.P.T;
+            return ((M.row1 - M.row0 + rpi - 1) / rpi + WAVES - 1) / WAVES;
+        };
+        const long g1 = (wgs1(A) + 7) / 8 * 8, g2 = wgs1(B);
+        if (g1 + g2 <= cap) {
+            hipLaunchKernelGGL((k_matvec_1t_pair<WT1, WT2>), dim3((unsigned)(g1 + g2)), dim3(THREADS), 0, st, A, B,
+                               (int)g1);
+            return sdy_check_launch("matvec_pair");
+        }
+    }
     static int per_cu = 0;
     if (per_cu == 0) {
         int n = 0;
