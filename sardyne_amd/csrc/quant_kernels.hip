@@ -291,6 +291,9 @@ struct MvArgs {
     long slot_rows;
     int n_slot_exp;
     long xq_slot, out_slot;
+    // k_matvec_1t: rows per iteration 64/T, (lane * tmag) >> 16 == lane / T for lane < 64, and the
+    // iteration count
+    int rpi, tmag, n_it;
 };
 
 constexpr bool is_k(int wt) { return wt == SDY_Q4_K || wt == SDY_Q6_K; }
@@ -366,6 +369,25 @@ struct WRegs {
     uint32_t f, g;
 };
 
+// Loads one unit of a K-quant row given its unit index iu = row * T + u and super-block index
+// is = row * nb + u / 4 in the planes.
+template <int WT>
+SDY_DEV void load_w_at(const Planes &P, uint32_t iu, uint32_t is, uint32_t u, WRegs<WT> &r) {
+    const uint32_t ou = iu * 16u;
+    if constexpr (WT == SDY_Q4_K) {
+        r.a = ldw16(P.p[0] + ou);
+        r.b = ldw16(P.p[1] + ou);
+        r.c = ldw16(P.p[2] + is * 16u);
+    } else {
+        static_assert(WT == SDY_Q6_K, "K-quants only");
+        r.a = ldw16(P.p[0] + ou);
+        r.b = ldw16(P.p[1] + ou);
+        r.c = ldw16(P.p[2] + ou);
+        r.f = ldw4(P.p[3] + is * 16u + 4u * (u & 3u));
+        r.g = ldw2(P.p[4] + is * 2u);
+    }
+}
+
 // Loads one unit of one row (row and unit given as indices into the planes).
 template <int WT>
 SDY_DEV void load_w(const Planes &P, uint32_t row, uint32_t u, WRegs<WT> &r) {
@@ -402,18 +424,15 @@ SDY_DEV void load_w(const Planes &P, uint32_t row, uint32_t u, WRegs<WT> &r) {
 SDY_DEV uint32_t w4(const uint4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
 // Scales and mins of the Q4_K sub-block pair (2j, 2j+1) from the 12 scale bytes held in the
-// dwords A (bytes 0-3), B (4-7), C (8-11) (csrc/quant.h:72-80), with shifts and masks only.
+// dwords A (bytes 0-3), B (4-7), C (8-11) (csrc/quant.h:72-80), with shifts and masks only (both
+// forms computed and one selected: the four lanes of a super-block differ in j, so a branch would
+// run both sides anyway).
 SDY_DEV void q4k_pair(uint32_t A, uint32_t B, uint32_t C, int j, int &sc0, int &sc1, int &m0, int &m1) {
     const uint32_t sh = (j & 1) ? 16u : 0u;
     const uint32_t a = (A >> sh) & 0xFFFFu, b = (B >> sh) & 0xFFFFu, c = (C >> sh) & 0xFFFFu;
-    uint32_t sc, m;
-    if (j < 2) {
-        sc = a & 0x3F3Fu;
-        m = b & 0x3F3Fu;
-    } else {
-        sc = (c & 0x0F0Fu) | ((a >> 2) & 0x3030u);
-        m = ((c >> 4) & 0x0F0Fu) | ((b >> 2) & 0x3030u);
-    }
+    const uint32_t sc_lo = a & 0x3F3Fu, m_lo = b & 0x3F3Fu;
+    const uint32_t sc_hi = (c & 0x0F0Fu) | ((a >> 2) & 0x3030u), m_hi = ((c >> 4) & 0x0F0Fu) | ((b >> 2) & 0x3030u);
+    const uint32_t sc = j < 2 ? sc_lo : sc_hi, m = j < 2 ? m_lo : m_hi;
     sc0 = (int)(sc & 255u);
     sc1 = (int)(sc >> 8);
     m0 = (int)(m & 255u);
@@ -440,8 +459,10 @@ SDY_DEV void unit_dot(const WRegs<WT> &r, const uint4 *Y, uint2 bsp, int u, int 
         q4k_pair(r.c.y, r.c.z, r.c.w, u & 3, sc0, sc1, m0, m1);
         const int b0 = (int)(int16_t)(bsp.x & 0xFFFFu), b1 = (int)(int16_t)(bsp.x >> 16);
         const int b2 = (int)(int16_t)(bsp.y & 0xFFFFu), b3 = (int)(int16_t)(bsp.y >> 16);
-        isum = sc0 * slo + sc1 * shi;
-        msum = m0 * (b0 + b1) + m1 * (b2 + b3);
+        // 24-bit multiplies (full rate): |slo|, |shi| <= 32 * 15 * 128, scales and mins < 64,
+        // |b0 + b1| <= 32 * 128
+        isum = __mul24(sc0, slo) + __mul24(sc1, shi);
+        msum = __mul24(m0, b0 + b1) + __mul24(m1, b2 + b3);
     } else if constexpr (WT == SDY_Q6_K) {
         int acc0 = -32 * (int)(int16_t)(bsp.x & 0xFFFFu), acc1 = -32 * (int)(int16_t)(bsp.x >> 16);
         int acc2 = -32 * (int)(int16_t)(bsp.y & 0xFFFFu), acc3 = -32 * (int)(int16_t)(bsp.y >> 16);
@@ -459,7 +480,8 @@ SDY_DEV void unit_dot(const WRegs<WT> &r, const uint4 *Y, uint2 bsp, int u, int 
         }
         int s0 = (int)(int8_t)(r.f & 255u), s1 = (int)(int8_t)((r.f >> 8) & 255u);
         int s2 = (int)(int8_t)((r.f >> 16) & 255u), s3 = (int)(int8_t)(r.f >> 24);
-        isum = s0 * acc0 + s1 * acc1 + s2 * acc2 + s3 * acc3;
+        // 24-bit multiplies: |acc| <= 16 * 63 * 128 + 32 * 16 * 128, |s| <= 128
+        isum = __mul24(s0, acc0) + __mul24(s1, acc1) + __mul24(s2, acc2) + __mul24(s3, acc3);
         msum = 0;
     } else {
         int s[2];
@@ -817,11 +839,24 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl_pair(MvArgs a, MvArgs b, 
     else matvec_rl_body<WT2, 1, true>(b, (long)gridDim.x - g1, (long)blockIdx.x - g1, 0);
 }
 
+// Lane rl*T's sequential fold of the row's nsb <= N super-block terms (lanes rl*T + 4s).
+template <int N>
+SDY_DEV float rl_fold(float term, int lane, int nsb) {
+    float tv[N];
+#pragma unroll
+    for (int s = 1; s < N; s++) tv[s] = __shfl(term, (lane + 4 * s) & 63);
+    float acc = 0.0f + term;
+#pragma unroll
+    for (int s = 1; s < N; s++)
+        if (s < nsb) acc = acc + tv[s];
+    return acc;
+}
+
 // The row sum of one K-quant unit term per lane (one token, activations in registers): the quad
 // reduction leaves super-block s of row rl in lane rl*T + 4s, and lane rl*T folds the terms in
 // super-block order from the reference's initial 0.0f. All the lane reads are issued before the
-// first add (one LDS round trip), for up to 16 super-blocks (T <= 64).
-template <int WT>
+// first add (one LDS round trip), for up to 16 super-blocks (T <= 64); NSB > 0: exactly NSB.
+template <int WT, int NSB>
 SDY_DEV float rl_row_sum(const WRegs<WT> &cur, const uint4 (&Yr)[4], uint2 bsr, float ydr, int u, int lane, int T) {
     int isum, msum;
     float term = 0.0f;
@@ -838,15 +873,8 @@ SDY_DEV float rl_row_sum(const WRegs<WT> &cur, const uint4 (&Yr)[4], uint2 bsr, 
         const float ydd = ydr * d;
         term = ydd * (float)isum;
     }
-    const int nsb = T >> 2;
-    float tv[16];
-#pragma unroll
-    for (int s = 1; s < 16; s++) tv[s] = __shfl(term, (lane + 4 * s) & 63);
-    float acc = 0.0f + term;
-#pragma unroll
-    for (int s = 1; s < 16; s++)
-        if (s < nsb) acc = acc + tv[s];
-    return acc;
+    if constexpr (NSB > 0) return rl_fold<NSB>(term, lane, NSB);
+    else return rl_fold<16>(term, lane, T >> 2);
 }
 
 // One token, K-quants with at most 64 units per row (every one-token matvec of a decode step but
@@ -856,12 +884,12 @@ SDY_DEV float rl_row_sum(const WRegs<WT> &cur, const uint4 (&Yr)[4], uint2 bsr, 
 // computation, so the wave waits for one memory round trip; the results are stored at the end.
 // Same lane layout and arithmetic as k_matvec_rl, so the bits are the same.
 // (the body of k_matvec_1t for workgroup bx of a grid of G, routed-expert slot `slot`)
-template <int WT, int NIT>
-SDY_DEV void matvec_1t_body(const MvArgs &a, long G, long bx, int slot) {
+template <int WT, int NIT, int NSB>
+SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
     const int T = a.P.T;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int rpi = 64 / T;
-    const int rl_ = lane / T, u = lane - rl_ * T;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int rpi = a.rpi;
+    const int rl_ = __mul24(lane, a.tmag) >> 16, u = lane - __mul24(rl_, T);
     const bool lane_on = rl_ < rpi;
     const int rl = lane_on ? rl_ : 0;
     long poff = 0;
@@ -874,49 +902,78 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, long G, long bx, int slot) {
         xq += (size_t)slot * a.xq_slot;
         out += (size_t)slot * a.out_slot;
     }
-    const long n_rows = a.row1 - a.row0;
-    const long n_it = (n_rows + rpi - 1) / rpi;
-    const long vblk = (G % 8 == 0) ? (bx % 8) * (G / 8) + bx / 8 : bx;  // XCD-aware renumbering
-    const long S = G * WAVES, wid = vblk * WAVES + wave;
-    if (wid >= n_it) return;
+    const int vblk = (G & 7) == 0 ? (bx & 7) * (G >> 3) + (bx >> 3) : bx;  // XCD-aware renumbering
+    const int S = G * WAVES, wid = vblk * WAVES + wave;
+    if (wid >= a.n_it) return;
+    // load order: the first iteration's weights, the activations, the bias and residual, then the
+    // other iterations' weights, so that iteration k waits only for the loads it uses (every load
+    // is unconditional, which keeps the compiler's wait counts exact)
     WRegs<WT> R[NIT];
     long row[NIT];
 #pragma unroll
-    for (int k = 0; k < NIT; k++) {
-        row[k] = a.row0 + (wid + k * S) * rpi + rl;
-        load_w<WT>(a.P, (uint32_t)((row[k] < a.row1 ? row[k] : a.row0) + poff), (uint32_t)u, R[k]);
-    }
+    for (int k = 0; k < NIT; k++) row[k] = a.row0 + (long)((wid + k * S) * rpi + rl);
+    // unit and super-block indices: the row base is uniform over the wave (scalar arithmetic) and
+    // rl * T + u = lane; rows past the end read row0 instead
+    const uint32_t le = lane_on ? lane : u, nb = a.P.nb;
+    auto load_k = [&](int k) {
+        const uint32_t base = (uint32_t)(a.row0 + (long)(wid + k * S) * rpi + poff);
+        const uint32_t r0 = (uint32_t)(a.row0 + poff);
+        const bool ok = row[k] < a.row1;
+        const uint32_t iu = ok ? base * (uint32_t)T + le : r0 * (uint32_t)T + u;
+        const uint32_t is = ok ? base * nb + (le >> 2) : r0 * nb + (u >> 2);
+        load_w_at<WT>(a.P, iu, is, (uint32_t)u, R[k]);
+    };
+    load_k(0);
+    const uint32_t etab = sdy_expf_tab_lane(lane);  // the SwiGLU epilogue's exponential table
     uint4 Yr[4];
-    const uint8_t *blk = xq + (size_t)(u >> 2) * 292;
+    const uint8_t *blk = xq + __mul24(u >> 2, 292);
     const uint8_t *yb = blk + 4 + 64 * (u & 3);
 #pragma unroll
     for (int q = 0; q < 4; q++)
         Yr[q] = make_uint4(ld4(yb + 16 * q), ld4(yb + 16 * q + 4), ld4(yb + 16 * q + 8), ld4(yb + 16 * q + 12));
     const uint2 bsr = make_uint2(ld4(blk + 260 + 8 * (u & 3)), ld4(blk + 264 + 8 * (u & 3)));
     const float ydr = *reinterpret_cast<const float *>(blk);
-    // the bias and residual of the rows this lane stores
+    // the bias and residual of the lane's rows (an absent one reads a stand-in: the activation row)
+    const float *bsrc = a.bias ? a.bias : reinterpret_cast<const float *>(xq);
+    const float *rsrc = a.resid ? a.resid : reinterpret_cast<const float *>(xq);
     float bv[NIT], rv[NIT];
-    const bool st_lane = u == 0 && lane_on && !a.swiglu;
 #pragma unroll
     for (int k = 0; k < NIT; k++) {
-        bv[k] = 0.0f;
-        rv[k] = 0.0f;
-        if (st_lane && row[k] < a.row1) {
-            if (a.bias) bv[k] = a.bias[row[k]];
-            if (a.resid) rv[k] = a.resid[row[k]];
-        }
+        const int rc = (int)(row[k] < a.row1 ? row[k] : a.row0);
+        bv[k] = bsrc[a.bias ? rc : 0];
+        rv[k] = rsrc[a.resid ? rc : 0];
     }
+#pragma unroll
+    for (int k = 1; k < NIT; k++) load_k(k);
     float acc[NIT];
 #pragma unroll
-    for (int k = 0; k < NIT; k++) acc[k] = rl_row_sum<WT>(R[k], Yr, bsr, ydr, u, lane, T);
+    for (int k = 0; k < NIT; k++) acc[k] = rl_row_sum<WT, NSB>(R[k], Yr, bsr, ydr, u, lane, T);
+    if (a.swiglu) {
+        // rows per iteration and row0 are even: iteration k's output pair p has its gate row in lane
+        // 2p*T and its up row in lane (2p+1)*T. Lane j < NIT * rpi/2 gathers output j (iteration
+        // j / (rpi/2), pair j % (rpi/2)), so the wave evaluates SiLU once for all its outputs.
+        const int npair = rpi >> 1, nout = NIT * npair;
+        const int j = lane < nout ? lane : 0;
+        int kj = 0;
+#pragma unroll
+        for (int k = 1; k < NIT; k++)
+            if (j >= k * npair) kj = k;
+        const int p = j - kj * npair;
+        float g = 0.0f, up = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NIT; k++) {
+            const float gk = __shfl(acc[k], 2 * p * T), uk = __shfl(acc[k], (2 * p + 1) * T);
+            g = k == kj ? gk : g;
+            up = k == kj ? uk : up;
+        }
+        const long rowj = a.row0 + (long)((wid + kj * S) * rpi + 2 * p);
+        const float r = sdy_silu_mul1_reg(g, up, etab);
+        if (lane < nout && rowj < a.row1) out[(rowj - a.row0) >> 1] = r;
+        return;
+    }
 #pragma unroll
     for (int k = 0; k < NIT; k++) {
-        const bool valid = lane_on && row[k] < a.row1;
-        if (a.swiglu) {
-            // rows per iteration is even and row0 is even: lane (rl+1)*T holds the up row
-            const float up = __shfl(acc[k], (lane + T) & 63);
-            if (u == 0 && (rl & 1) == 0 && valid) out[(row[k] - a.row0) >> 1] = sdy_silu_mul1(acc[k], up);
-        } else if (u == 0 && valid) {
+        if (u == 0 && lane_on && row[k] < a.row1) {
             float v = acc[k];
             if (a.bias) v = v + bv[k];
             if (a.resid) v = rv[k] + v;
@@ -925,16 +982,16 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, long G, long bx, int slot) {
     }
 }
 
-template <int WT, int NIT>
+template <int WT, int NIT, int NSB>
 __global__ __launch_bounds__(THREADS) void k_matvec_1t(MvArgs a) {
-    matvec_1t_body<WT, NIT>(a, gridDim.x, blockIdx.x, blockIdx.y);
+    matvec_1t_body<WT, NIT, NSB>(a, (int)gridDim.x, (int)blockIdx.x, (int)blockIdx.y);
 }
 
 // k_matvec_1t's pair form (see k_matvec_rl_pair), one iteration per wave
-template <int WT1, int WT2>
+template <int WT1, int WT2, int NSB>
 __global__ __launch_bounds__(THREADS) void k_matvec_1t_pair(MvArgs a, MvArgs b, int g1) {
-    if ((int)blockIdx.x < g1) matvec_1t_body<WT1, 1>(a, g1, blockIdx.x, 0);
-    else matvec_1t_body<WT2, 1>(b, (long)gridDim.x - g1, (long)blockIdx.x - g1, 0);
+    if ((int)blockIdx.x < g1) matvec_1t_body<WT1, 1, NSB>(a, g1, (int)blockIdx.x, 0);
+    else matvec_1t_body<WT2, 1, NSB>(b, (int)gridDim.x - g1, (int)blockIdx.x - g1, 0);
 }
 
 // Long rows, one token (K-quants with T > 64 units, e.g. n_in = 11008 with 172 units): a wave owns
@@ -1506,24 +1563,29 @@ static long resident_wgs(const void *fn, int &per_cu) {
     return (long)(g_n_cu ? g_n_cu : 256) * per_cu;
 }
 
-template <int WT, int NIT>
+template <int WT, int NIT, int NSB>
 static long cap_1t() {
     static int per_cu = 0;
-    return resident_wgs((const void *)k_matvec_1t<WT, NIT>, per_cu);
+    return resident_wgs((const void *)k_matvec_1t<WT, NIT, NSB>, per_cu);
 }
 
 // One token on k_matvec_1t with the smallest NIT (iterations per wave, at most 4) whose grid the GPU
 // holds at once, so that every wave's loads go out at the start; 1 when no NIT fits (the caller
 // then runs the persistent k_matvec_rl).
-template <int WT>
-static int launch_mv_1t(MvArgs &A, hipStream_t st, int n_slot) {
-    const int rpi = 64 / A.P.T;
-    const long n_it = (A.row1 - A.row0 + rpi - 1) / rpi;
+static void prep_1t(MvArgs &A) {
+    A.rpi = 64 / A.P.T;
+    A.tmag = (65536 + A.P.T - 1) / A.P.T;
+    A.n_it = (int)((A.row1 - A.row0 + A.rpi - 1) / A.rpi);
+}
+
+template <int WT, int NSB>
+static int launch_mv_1t_nsb(MvArgs &A, hipStream_t st, int n_slot) {
+    const long n_it = A.n_it;
     auto wgs = [&](int nit) { return (n_it + (long)WAVES * nit - 1) / ((long)WAVES * nit); };
 #define SDY_1T(NIT)                                                                                                  \
-    if (wgs(NIT) * n_slot <= cap_1t<WT, NIT>()) {                                                                    \
-        hipLaunchKernelGGL((k_matvec_1t<WT, NIT>), dim3((unsigned)wgs(NIT), (unsigned)n_slot), dim3(THREADS), 0, st, \
-                           A);                                                                                       \
+    if (wgs(NIT) * n_slot <= cap_1t<WT, NIT, NSB>()) {                                                               \
+        hipLaunchKernelGGL((k_matvec_1t<WT, NIT, NSB>), dim3((unsigned)wgs(NIT), (unsigned)n_slot), dim3(THREADS), 0, \
+                           st, A);                                                                                   \
         return sdy_check_launch("matvec");                                                                           \
     }
     SDY_1T(1)
@@ -1532,6 +1594,18 @@ static int launch_mv_1t(MvArgs &A, hipStream_t st, int n_slot) {
     SDY_1T(4)
 #undef SDY_1T
     return 1;
+}
+
+// NSB: the row's super-block count when it is one of the common ones (n_in 768, 2048, 4096)
+template <int WT>
+static int launch_mv_1t(MvArgs &A, hipStream_t st, int n_slot) {
+    prep_1t(A);
+    switch (A.P.T) {
+    case 12: return launch_mv_1t_nsb<WT, 3>(A, st, n_slot);
+    case 32: return launch_mv_1t_nsb<WT, 8>(A, st, n_slot);
+    case 64: return launch_mv_1t_nsb<WT, 16>(A, st, n_slot);
+    default: return launch_mv_1t_nsb<WT, 0>(A, st, n_slot);
+    }
 }
 
 template <int WT, int MT, bool YREG>
@@ -1579,16 +1653,21 @@ static long rl_wgs(const MvArgs &A, int per_cu) {
 template <int WT1, int WT2>
 static int launch_mv_pair(MvArgs &A, MvArgs &B, hipStream_t st) {
     {
-        static int per_cu_1t = 0;
-        const long cap = resident_wgs((const void *)k_matvec_1t_pair<WT1, WT2>, per_cu_1t);
-        auto wgs1 = [](const MvArgs &M) {
-            const int rpi = 64 / M.P.T;
-            return ((M.row1 - M.row0 + rpi - 1) / rpi + WAVES - 1) / WAVES;
-        };
+        static int per_cu_8 = 0, per_cu_0 = 0;
+        prep_1t(A);
+        prep_1t(B);
+        const bool n8 = A.P.T == 32 && B.P.T == 32;  // both rows of 2048 elements: 8 super-blocks
+        const long cap = n8 ? resident_wgs((const void *)k_matvec_1t_pair<WT1, WT2, 8>, per_cu_8)
+                            : resident_wgs((const void *)k_matvec_1t_pair<WT1, WT2, 0>, per_cu_0);
+        auto wgs1 = [](const MvArgs &M) { return ((long)M.n_it + WAVES - 1) / WAVES; };
         const long g1 = (wgs1(A) + 7) / 8 * 8, g2 = wgs1(B);
         if (g1 + g2 <= cap) {
-            hipLaunchKernelGGL((k_matvec_1t_pair<WT1, WT2>), dim3((unsigned)(g1 + g2)), dim3(THREADS), 0, st, A, B,
-                               (int)g1);
+            if (n8)
+                hipLaunchKernelGGL((k_matvec_1t_pair<WT1, WT2, 8>), dim3((unsigned)(g1 + g2)), dim3(THREADS), 0, st, A,
+                                   B, (int)g1);
+            else
+                hipLaunchKernelGGL((k_matvec_1t_pair<WT1, WT2, 0>), dim3((unsigned)(g1 + g2)), dim3(THREADS), 0, st, A,
+                                   B, (int)g1);
             return sdy_check_launch("matvec_pair");
         }
     }

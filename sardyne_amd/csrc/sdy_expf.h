@@ -84,4 +84,38 @@ SDY_EXPF_QUAL float sdy_expf(float x) {
     return x != x ? x + x : res;
 }
 
+#ifdef __HIPCC__
+/* sdy_expf with the table in a register instead of memory: lane i of `tab` holds dword i of
+ * sdy_exp2_32_tab (sdy_expf_tab_lane loads it, with the kernel's other loads) and the lookup is two
+ * lane reads, so no memory round trip follows the argument. Every lane of the wave must be active. */
+__device__ static inline uint32_t sdy_expf_tab_lane(int lane) {
+    return reinterpret_cast<const uint32_t *>(sdy_exp2_32_tab)[lane & 63];
+}
+
+__device__ static inline float sdy_expf_reg(float x, uint32_t tab) {
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double)x;
+    const double z = inv_ln2_n * xd;
+    double kd = z + shift;
+    const uint64_t ki = sdy_expf_double_to_bits(kd);
+    kd -= shift;
+    const double r = SDY_EXPF_FMA(inv_ln2_n, xd, -kd);
+    const int i = (int)(ki % 32);
+    const uint32_t lo = (uint32_t)__shfl((int)tab, 2 * i), hi = (uint32_t)__shfl((int)tab, 2 * i + 1);
+    const uint64_t t = (((uint64_t)hi << 32) | lo) + (ki << 47);
+    const double s = sdy_expf_bits_to_double(t);
+    const double p = c0 * r + c1;
+    const double r2 = r * r;
+    double y = c2 * r + 1.0;
+    y = p * r2 + y;
+    y = y * s;
+    float res = (float)y;
+    res = x < -0x1.9fe368p6f ? 0.0f : res;
+    res = x > 0x1.62e42ep6f ? __builtin_inff() : res;
+    return x != x ? x + x : res;
+}
+#endif
+
 #endif

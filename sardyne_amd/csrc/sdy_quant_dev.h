@@ -150,3 +150,9 @@ SDY_DEV float sdy_silu_mul1(float g, float u) {
     const float s = g / (1.0f + sdy_expf(-g));
     return s * u;
 }
+
+// sdy_silu_mul1 with the exponential's table in a register (sdy_expf_reg; all lanes active)
+SDY_DEV float sdy_silu_mul1_reg(float g, float u, uint32_t tab) {
+    const float s = g / (1.0f + sdy_expf_reg(-g, tab));
+    return s * u;
+}

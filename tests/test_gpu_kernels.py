@@ -359,6 +359,66 @@ def test_matvec_pair_rejects_unsupported():
     assert L.sdy_matvec_pair(ctypes.byref(c.m), ctypes.byref(a1), ctypes.byref(c.m), ctypes.byref(a1), None) != 0
 
 
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("n_in,n_out", [(2048, 22016), (1024, 40000), (1024, 72000), (1024, 110000), (768, 30000),
+                                        (512, 151936)])
+def test_matvec_one_token_large(kind, n_in, n_out):
+    """One-token matvecs with enough rows that a wave takes several row iterations (up to the
+    persistent kernel at the largest): every row has the oracle's bits, also with a bias and a
+    residual over a row range whose ends are not iteration boundaries; rows outside stay untouched."""
+    L = lib()
+    t, w, xq = _matvec_case(kind, n_in, n_out, 1, seed=n_out)
+    exp = O.matmul_q(w, t, xq, n_in, simd=1)[0]
+    rng = np.random.default_rng(n_out + 1)
+    bias = rng.standard_normal(n_out).astype(np.float32)
+    resid = rng.standard_normal(n_out).astype(np.float32)
+    m = capi.DeviceMatrix(t, n_in, n_out, w)
+    dq, db, dr = capi.DeviceBuffer.from_array(xq), capi.DeviceBuffer.from_array(bias), capi.DeviceBuffer.from_array(resid)
+    for r0, r1, with_br in [(0, n_out, False), (3, n_out - 5, True)]:
+        dout = capi.DeviceBuffer.from_array(np.full(n_out, np.nan, np.float32))
+        a = capi.SdyMvArgs(xq=dq.ptr, n_tok=1, out=dout.ptr, out_stride=n_out, row0=r0, row1=r1,
+                           bias=db.ptr if with_br else None, resid=dr.ptr if with_br else None)
+        capi.check(L.sdy_matvec(ctypes.byref(m.m), ctypes.byref(a), None))
+        got = dout.to_array(np.float32, n_out)
+        e = exp.copy()
+        if with_br:
+            e = resid + (e + bias)  # the kernel's order: acc + bias, then resid + that
+        assert np.array_equal(bits(got[r0:r1]), bits(e[r0:r1]))
+        assert np.isnan(got[:r0]).all() and np.isnan(got[r1:]).all()
+    m.close()
+
+
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("n_in,ffn", [(2048, 11008), (1024, 20000), (1024, 36000), (256, 70000)])
+def test_swiglu_epilogue_large(kind, n_in, ffn):
+    """The one-token SwiGLU epilogue when a wave gathers the outputs of several row iterations (and
+    several (gate, up) pairs per iteration for short rows): the bits of the separate gate and up
+    matvecs followed by the SiLU op."""
+    t = TYPES[kind]
+    L = lib()
+    rng = np.random.default_rng(ffn)
+    nb = ffn * n_in // O.QK[t]
+    g = random_blocks(kind, nb, rng).reshape(ffn, -1)
+    u = random_blocks(kind, nb, rng).reshape(ffn, -1)
+    x = rng.standard_normal((1, n_in)).astype(np.float32)
+    xq = O.quantize(x, O.VEC_DOT[t])
+    m = capi.SdyMat()
+    capi.check(L.sdy_mat_alloc(ctypes.byref(m), t, n_in, 2 * ffn))
+    capi.check(L.sdy_mat_upload_map(ctypes.byref(m), 0, ffn, 2, ffn, 0, ptr(g), None))
+    capi.check(L.sdy_mat_upload_map(ctypes.byref(m), 1, ffn, 2, ffn, 0, ptr(u), None))
+    dq = capi.DeviceBuffer.from_array(xq)
+    dout = capi.DeviceBuffer(ffn * 4)
+    a = capi.SdyMvArgs(xq=dq.ptr, n_tok=1, out=dout.ptr, out_stride=ffn, row0=0, row1=2 * ffn,
+                       epilogue=capi.EPI_SWIGLU)
+    capi.check(L.sdy_matvec(ctypes.byref(m), ctypes.byref(a), None))
+    got = dout.to_array(np.float32, ffn)
+    eg, eu = O.matmul_q(g, t, xq, n_in, simd=1)[0], O.matmul_q(u, t, xq, n_in, simd=1)[0]
+    exp = eg.copy()
+    L.op_silu_mul(ptr(exp), ptr(eu), exp.size)
+    assert np.array_equal(bits(got), bits(exp))
+    L.sdy_mat_free(ctypes.byref(m))
+
+
 @pytest.mark.parametrize("kind", ["Q4_K", "Q6_K", "Q8_0", "Q5_0"])
 @pytest.mark.parametrize("n_in,ffn,n_tok", [(2048, 96, 1), (1024, 40, 3), (11008, 8, 2), (768, 20, 1)])
 def test_swiglu_epilogue(kind, n_in, ffn, n_tok):
