@@ -109,7 +109,7 @@ class SdyMat(ctypes.Structure):
 class SdyMvArgs(ctypes.Structure):
     _fields_ = [("xq", _vp), ("x", _vp), ("n_tok", _int), ("out", _vp), ("out_stride", ctypes.c_long),
                 ("bias", _vp), ("resid", _vp), ("row0", ctypes.c_long), ("row1", ctypes.c_long),
-                ("epilogue", _int)]
+                ("epilogue", _int), ("nw", _vp), ("eps", ctypes.c_float)]
 
 
 _DEVICE_SIGNATURES = {
@@ -138,6 +138,8 @@ _DEVICE_SIGNATURES = {
     "sdy_quantize": (_int, [_int, _vp, _vp, _int, _int, _vp]),
     "sdy_matvec": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp]),
     "sdy_matvec_pair_ok": (_int, [ctypes.POINTER(SdyMat), _int, ctypes.POINTER(SdyMat), _int]),
+    "sdy_matvec_fused_ok": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), ctypes.POINTER(SdyMat),
+                                   ctypes.POINTER(SdyMvArgs)]),
     "sdy_matvec_pair": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), ctypes.POINTER(SdyMat),
                                ctypes.POINTER(SdyMvArgs), _vp]),
     "sdy_matvec_float": (_int, [_int, _vp, _int, ctypes.POINTER(SdyMvArgs), _vp]),

@@ -511,6 +511,7 @@ engine_ctx *engine_ctx_new(const engine_model *m, int32_t max_seq, int32_t n_bat
     /* SARDYNE_NO_DEVICE_MOE: one-token MoE blocks group their experts on the host, as prefill does */
     c->moe_device = c->decode_fused && !getenv("SARDYNE_NO_DEVICE_MOE") && sdy_engine_moe_device_ok(c);
     c->use_graph = c->decode_fused && (!m->info.n_expert || c->moe_device) && !getenv("SARDYNE_NO_GRAPH");
+    c->fuse_act = c->decode_fused && !getenv("SARDYNE_NO_FUSED_ACT");
     return c;
 }
 

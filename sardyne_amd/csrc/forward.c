@@ -173,6 +173,35 @@ static int mm1_pair(engine_ctx *c, float *out1, const dmat *w1, const float *b1,
     return sdy_matvec_pair(&w1->m, &a1, &w2->m, &a2, c->st);
 }
 
+/* One-token arguments for a kernel that builds the Q8_K row of x itself (RMS-normalised with nw first
+ * when nw is set): the bytes norm_for / sdy_quantize would have written, without their launch. */
+static sdy_mv_args fused_args(const engine_ctx *c, float *out, const float *x, const float *nw, const dmat *w,
+                              const float *bias, const float *resid, int epilogue) {
+    sdy_mv_args a;
+    memset(&a, 0, sizeof a);
+    a.x = x;
+    a.nw = nw;
+    a.eps = c->m->info.norm_eps;
+    a.n_tok = 1;
+    a.out = out;
+    a.out_stride = epilogue == SDY_EPI_SWIGLU ? w->n_out / 2 : w->n_out;
+    a.bias = bias;
+    a.resid = resid;
+    a.row1 = w->n_out;
+    a.epilogue = epilogue;
+    return a;
+}
+
+/* out = W . x for one token through the in-kernel quantisation; 1 when it is not available for this
+ * matrix (the caller then quantises separately), 0 when done, < 0 on error. */
+static int mm1_fused(engine_ctx *c, float *out, const float *x, const float *nw, const dmat *w, const float *bias,
+                     const float *resid, int epilogue) {
+    sdy_mv_args a = fused_args(c, out, x, nw, w, bias, resid, epilogue);
+    if (!c->fuse_act || !sdy_matvec_fused_ok(&w->m, &a, NULL, NULL)) return 1;
+    c->xq_src[0] = c->xq_src[1] = NULL;
+    return sdy_matvec(&w->m, &a, c->st);
+}
+
 /* hb[t][i] = silu(gate_i . x) * (up_i . x) for n rows of x (gate/up fused and interleaved, or apart). */
 static int ffn_gate_up(engine_ctx *c, const float *x, int n, int new_input, const dmat *gate_up, const dmat *gate,
                        const dmat *up, int ffn) {
@@ -327,20 +356,37 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
             float *q = c->qkv, *k = q + q_dim, *v = k + kv_dim;
             const int bias_fused = !in->qkv_bias ||
                                    (L->bk == L->bq + q_dim && (L->qkv_parts < 3 || L->bv == L->bk + kv_dim));
-            TRY(norm_for(c, c->x, L->attn_norm, L->qkv_parts >= 2 ? &L->wqkv : &L->wq, 1));
-            if (L->qkv_parts == 2 && bias_fused &&
+            int qkv_done = 0;
+            if (c->fuse_act && L->qkv_parts == 2 && bias_fused &&
                 sdy_matvec_pair_ok(&L->wqkv.m, SDY_EPI_NONE, &L->wv.m, SDY_EPI_NONE)) {
-                TRY(mm1_pair(c, q, &L->wqkv, L->bq, v, &L->wv, L->bv)); /* q|k and v in one launch */
-            } else if (L->qkv_parts >= 2 && bias_fused) {
-                TRY(mm(c, q, c->xb, &L->wqkv, 1, L->bq, NULL, 0));
-                if (L->qkv_parts == 2) TRY(mm(c, v, c->xb, &L->wv, 1, L->bv, NULL, 0));
-            } else {
-                TRY(mm(c, q, c->xb, &L->wq, 1, L->bq, NULL, 0));
-                TRY(mm(c, k, c->xb, &L->wk, 1, L->bk, NULL, 0));
-                TRY(mm(c, v, c->xb, &L->wv, 1, L->bv, NULL, 0));
+                /* attention RMSNorm, quantisation, q|k and v in one launch */
+                sdy_mv_args a1 = fused_args(c, q, c->x, L->attn_norm, &L->wqkv, L->bq, NULL, SDY_EPI_NONE);
+                sdy_mv_args a2 = fused_args(c, v, c->x, L->attn_norm, &L->wv, L->bv, NULL, SDY_EPI_NONE);
+                if (sdy_matvec_fused_ok(&L->wqkv.m, &a1, &L->wv.m, &a2)) {
+                    c->xq_src[0] = c->xq_src[1] = NULL;
+                    TRY(sdy_matvec_pair(&L->wqkv.m, &a1, &L->wv.m, &a2, c->st));
+                    qkv_done = 1;
+                }
             }
-            /* attention into att (and, for a K-quant wo, its Q8_K row: mm then reuses it) */
-            const int q8k = vec_dot_type(L->wo.type) == SDY_Q8_K;
+            if (!qkv_done) {
+                TRY(norm_for(c, c->x, L->attn_norm, L->qkv_parts >= 2 ? &L->wqkv : &L->wq, 1));
+                if (L->qkv_parts == 2 && bias_fused &&
+                    sdy_matvec_pair_ok(&L->wqkv.m, SDY_EPI_NONE, &L->wv.m, SDY_EPI_NONE)) {
+                    TRY(mm1_pair(c, q, &L->wqkv, L->bq, v, &L->wv, L->bv)); /* q|k and v in one launch */
+                } else if (L->qkv_parts >= 2 && bias_fused) {
+                    TRY(mm(c, q, c->xb, &L->wqkv, 1, L->bq, NULL, 0));
+                    if (L->qkv_parts == 2) TRY(mm(c, v, c->xb, &L->wv, 1, L->bv, NULL, 0));
+                } else {
+                    TRY(mm(c, q, c->xb, &L->wq, 1, L->bq, NULL, 0));
+                    TRY(mm(c, k, c->xb, &L->wk, 1, L->bk, NULL, 0));
+                    TRY(mm(c, v, c->xb, &L->wv, 1, L->bv, NULL, 0));
+                }
+            }
+            /* attention into att (and, for a K-quant wo, its Q8_K row: mm then reuses it, unless wo
+               quantises att itself) */
+            sdy_mv_args awo = fused_args(c, c->x, c->att, NULL, &L->wo, NULL, c->x, SDY_EPI_NONE);
+            const int wo_fused = c->fuse_act && sdy_matvec_fused_ok(&L->wo.m, &awo, NULL, NULL);
+            const int q8k = !wo_fused && vec_dot_type(L->wo.type) == SDY_Q8_K;
             TRY(sdy_attn_decode(q, k, v, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos, c->rope_sin, c->step_dev,
                                 in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc, vc, head_stride, c->max_seq,
                                 c->part, c->att, q8k ? c->xq[1] : NULL, c->st));
@@ -350,7 +396,8 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
                 c->xq_n_tok[1] = 1;
                 c->xq_n_in[1] = q_dim;
             }
-            TRY(mm(c, c->x, c->att, &L->wo, 1, NULL, c->x, 0));
+            if (wo_fused) TRY(sdy_matvec(&L->wo.m, &awo, c->st));
+            else TRY(mm(c, c->x, c->att, &L->wo, 1, NULL, c->x, 0));
         } else {
             TRY(norm_for(c, c->x, L->attn_norm, L->qkv_parts >= 2 ? &L->wqkv : &L->wq, n));
             TRY(mm(c, c->q, c->xb, &L->wq, n, L->bq, NULL, 0));
@@ -369,8 +416,16 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
             TRY(moe(c, L, n));
             TRY(sdy_add(c->x, c->moe_sum, c->x, (long)n * dim, c->st));
         } else {
-            TRY(norm_for(c, c->x, L->ffn_norm, L->gu_fused ? &L->gate_up : &L->gate, n));
-            TRY(ffn_gate_up(c, c->xb, n, 0, L->gu_fused ? &L->gate_up : NULL, &L->gate, &L->up, in->ffn_dim));
+            /* one token: the FFN RMSNorm and quantisation inside gate|up (the hidden row keeps its own
+               quantiser: every workgroup of down re-reading the f32 row costs more than the launch) */
+            const int rc = decode && L->gu_fused
+                               ? mm1_fused(c, c->hb, c->x, L->ffn_norm, &L->gate_up, NULL, NULL, SDY_EPI_SWIGLU)
+                               : 1;
+            if (rc < 0) return rc;
+            if (rc) {
+                TRY(norm_for(c, c->x, L->ffn_norm, L->gu_fused ? &L->gate_up : &L->gate, n));
+                TRY(ffn_gate_up(c, c->xb, n, 0, L->gu_fused ? &L->gate_up : NULL, &L->gate, &L->up, in->ffn_dim));
+            }
             TRY(mm(c, c->x, c->hb, &L->down, n, NULL, c->x, 1));
         }
     }

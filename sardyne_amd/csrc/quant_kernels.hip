@@ -30,6 +30,7 @@
 #include "sdy_shim.h"
 #include "sdy_internal.h"
 #include "sdy_quant_dev.h"
+#include "sdy_norm_dev.h"
 
 namespace {
 
@@ -294,6 +295,10 @@ struct MvArgs {
     // k_matvec_1t: rows per iteration 64/T, (lane * tmag) >> 16 == lane / T for lane < 64, and the
     // iteration count
     int rpi, tmag, n_it;
+    // activations quantised by the kernel itself (one token, K-quants): the f32 row px, first
+    // RMS-normalised with the weights pnw and peps when pnw is set
+    const float *px, *pnw;
+    float peps;
 };
 
 constexpr bool is_k(int wt) { return wt == SDY_Q4_K || wt == SDY_Q6_K; }
@@ -839,6 +844,98 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl_pair(MvArgs a, MvArgs b, 
     else matvec_rl_body<WT2, 1, true>(b, (long)gridDim.x - g1, (long)blockIdx.x - g1, 0);
 }
 
+// The Q8_K row of a one-token matvec built in LDS by its 256-thread workgroup from the f32 row x (n
+// elements, a multiple of 256, x 16-byte aligned), RMS-normalised first when NORM (nb <= 4 NR): the
+// bytes that k_quant_q8k (k_norm_quant with NORM) writes — same sum order, same wave quantiser — in
+// an aligned layout: y [nb][256] int8, bsums [nb][16] int16, d [nb] f32 (nb * 292 bytes).
+// issue() requests the lane's inputs: super-blocks wave + 4k, k < NR (called before the weight loads,
+// so that these few bytes do not queue behind the weight stream); build() quantises them into LDS,
+// loading further rounds of NR super-blocks per wave when nb > 4 NR (without NORM only). Every thread
+// of the workgroup calls build(); it ends with a barrier.
+template <bool NORM, int NR>
+struct Q8kRow {
+    float4 xv[NR], wv[NR];
+
+    SDY_DEV void issue(const float *__restrict__ x, const float *__restrict__ nw, int n) {
+        const int nb = n >> 8, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+        for (int k = 0; k < NR; k++) {
+            const int sb = wave + 4 * k < nb ? wave + 4 * k : nb - 1;
+            xv[k] = *reinterpret_cast<const float4 *>(x + 256 * sb + 4 * lane);
+            if constexpr (NORM) wv[k] = *reinterpret_cast<const float4 *>(nw + 256 * sb + 4 * lane);
+        }
+    }
+
+    SDY_DEV void build(const float *__restrict__ x, float eps, int n, uint8_t *lds) {
+        const int nb = n >> 8, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        uint32_t *ly = reinterpret_cast<uint32_t *>(lds);
+        int16_t *lbs = reinterpret_cast<int16_t *>(lds + (size_t)nb * 256);
+        float *ld = reinterpret_cast<float *>(lds + (size_t)nb * 288);
+        float scale = 1.0f;
+        if constexpr (NORM) {
+            // sdy_row_sumsq's order: thread t adds the squares of its float4 chunks t, t + 256, ...
+            // (chunk t + 256 k is super-block wave + 4 k, the lane's four elements), then the tree
+            __shared__ double sh[4];
+            double ss = 0.0;
+#pragma unroll
+            for (int k = 0; k < NR; k++)
+                if (wave + 4 * k < nb) {
+                    const float4 v = xv[k];
+                    ss += (double)v.x * (double)v.x;
+                    ss += (double)v.y * (double)v.y;
+                    ss += (double)v.z * (double)v.z;
+                    ss += (double)v.w * (double)v.w;
+                }
+            ss = sdy_block_sum256(ss, sh);
+            scale = (float)(1.0 / sqrt(ss / (double)n + (double)eps));
+        }
+        for (int s0 = wave; s0 < nb; s0 += 4 * NR) {
+            if (s0 != wave) {  // a further round (long rows without NORM)
+#pragma unroll
+                for (int k = 0; k < NR; k++) {
+                    const int sb = s0 + 4 * k < nb ? s0 + 4 * k : nb - 1;
+                    xv[k] = *reinterpret_cast<const float4 *>(x + 256 * sb + 4 * lane);
+                }
+            }
+            float xs[NR][4];
+#pragma unroll
+            for (int k = 0; k < NR; k++) {
+                float4 v = xv[k];
+                if constexpr (NORM) {
+                    const float4 w = wv[k];
+                    v = make_float4((v.x * scale) * w.x, (v.y * scale) * w.y, (v.z * scale) * w.z, (v.w * scale) * w.w);
+                }
+                xs[k][0] = v.x;
+                xs[k][1] = v.y;
+                xs[k][2] = v.z;
+                xs[k][3] = v.w;
+            }
+            SdyQ8kLane r[NR];
+            sdy_q8k_lanes<NR>(xs, lane, r);
+#pragma unroll
+            for (int k = 0; k < NR; k++) {
+                const int sb = s0 + 4 * k;
+                if (sb < nb) {
+                    ly[sb * 64 + lane] = r[k].packed;
+                    if ((lane & 3) == 0) lbs[sb * 16 + (lane >> 2)] = (int16_t)r[k].gsum;
+                    if (lane == 0) ld[sb] = r[k].d;
+                }
+            }
+        }
+        __syncthreads();
+    }
+};
+
+// The lane's unit u of the activation row in LDS (Q8kRow layout): its 64 y bytes, the bsums of
+// its four 16-element groups and the block scale.
+SDY_DEV void q8k_unit_lds(const uint8_t *lds, int nb, int u, uint4 (&Yr)[4], uint2 &bsr, float &ydr) {
+    const uint8_t *y = lds + (u >> 2) * 256 + 64 * (u & 3);
+#pragma unroll
+    for (int q = 0; q < 4; q++) Yr[q] = *reinterpret_cast<const uint4 *>(y + 16 * q);
+    bsr = *reinterpret_cast<const uint2 *>(lds + (size_t)nb * 256 + (u >> 2) * 32 + 8 * (u & 3));
+    ydr = reinterpret_cast<const float *>(lds + (size_t)nb * 288)[u >> 2];
+}
+
 // Lane rl*T's sequential fold of the row's nsb <= N super-block terms (lanes rl*T + 4s).
 template <int N>
 SDY_DEV float rl_fold(float term, int lane, int nsb) {
@@ -884,8 +981,12 @@ SDY_DEV float rl_row_sum(const WRegs<WT> &cur, const uint4 (&Yr)[4], uint2 bsr, 
 // computation, so the wave waits for one memory round trip; the results are stored at the end.
 // Same lane layout and arithmetic as k_matvec_rl, so the bits are the same.
 // (the body of k_matvec_1t for workgroup bx of a grid of G, routed-expert slot `slot`)
-template <int WT, int NIT, int NSB>
+// PRO: 0 the Q8_K row a.xq in memory, 1 the f32 row a.px quantised by the workgroup (into LDS),
+// 2 a.px RMS-normalised with a.pnw, then quantised.
+template <int WT, int NIT, int NSB, int PRO = 0>
 SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
+    // super-blocks per wave of the workgroup's activation row (n_in 768: 3, 2048: 8, else up to 16)
+    constexpr int PRO_NR = NSB == 3 ? 1 : NSB == 8 ? 2 : 4;
     const int T = a.P.T;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int rpi = a.rpi;
@@ -904,7 +1005,15 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
     }
     const int vblk = (G & 7) == 0 ? (bx & 7) * (G >> 3) + (bx >> 3) : bx;  // XCD-aware renumbering
     const int S = G * WAVES, wid = vblk * WAVES + wave;
-    if (wid >= a.n_it) return;
+    extern __shared__ uint8_t lds_act[];
+    Q8kRow<PRO == 2, PRO_NR> arow;
+    // (with PRO, waves past the rows still take part in the workgroup's activation row: their rows
+    // are all >= row1, so they load row0 and store nothing)
+    if constexpr (PRO == 0) {
+        if (wid >= a.n_it) return;
+    } else {
+        arow.issue(a.px, a.pnw, a.P.n_in);
+    }
     // load order: the first iteration's weights, the activations, the bias and residual, then the
     // other iterations' weights, so that iteration k waits only for the loads it uses (every load
     // is unconditional, which keeps the compiler's wait counts exact)
@@ -926,16 +1035,27 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
     load_k(0);
     const uint32_t etab = sdy_expf_tab_lane(lane);  // the SwiGLU epilogue's exponential table
     uint4 Yr[4];
-    const uint8_t *blk = xq + __mul24(u >> 2, 292);
-    const uint8_t *yb = blk + 4 + 64 * (u & 3);
+    uint2 bsr;
+    float ydr;
+    if constexpr (PRO == 0) {
+        const uint8_t *blk = xq + __mul24(u >> 2, 292);
+        const uint8_t *yb = blk + 4 + 64 * (u & 3);
 #pragma unroll
-    for (int q = 0; q < 4; q++)
-        Yr[q] = make_uint4(ld4(yb + 16 * q), ld4(yb + 16 * q + 4), ld4(yb + 16 * q + 8), ld4(yb + 16 * q + 12));
-    const uint2 bsr = make_uint2(ld4(blk + 260 + 8 * (u & 3)), ld4(blk + 264 + 8 * (u & 3)));
-    const float ydr = *reinterpret_cast<const float *>(blk);
+        for (int q = 0; q < 4; q++)
+            Yr[q] = make_uint4(ld4(yb + 16 * q), ld4(yb + 16 * q + 4), ld4(yb + 16 * q + 8), ld4(yb + 16 * q + 12));
+        bsr = make_uint2(ld4(blk + 260 + 8 * (u & 3)), ld4(blk + 264 + 8 * (u & 3)));
+        ydr = *reinterpret_cast<const float *>(blk);
+    } else {
+        // every weight load goes out first; the workgroup quantises the row while they are in flight
+#pragma unroll
+        for (int k = 1; k < NIT; k++) load_k(k);
+        arow.build(a.px, a.peps, a.P.n_in, lds_act);
+        q8k_unit_lds(lds_act, a.P.nb, u, Yr, bsr, ydr);
+    }
     // the bias and residual of the lane's rows (an absent one reads a stand-in: the activation row)
-    const float *bsrc = a.bias ? a.bias : reinterpret_cast<const float *>(xq);
-    const float *rsrc = a.resid ? a.resid : reinterpret_cast<const float *>(xq);
+    const float *stand_in = PRO ? a.px : reinterpret_cast<const float *>(xq);
+    const float *bsrc = a.bias ? a.bias : stand_in;
+    const float *rsrc = a.resid ? a.resid : stand_in;
     float bv[NIT], rv[NIT];
 #pragma unroll
     for (int k = 0; k < NIT; k++) {
@@ -943,8 +1063,10 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
         bv[k] = bsrc[a.bias ? rc : 0];
         rv[k] = rsrc[a.resid ? rc : 0];
     }
+    if constexpr (PRO == 0) {
 #pragma unroll
-    for (int k = 1; k < NIT; k++) load_k(k);
+        for (int k = 1; k < NIT; k++) load_k(k);
+    }
     float acc[NIT];
 #pragma unroll
     for (int k = 0; k < NIT; k++) acc[k] = rl_row_sum<WT, NSB>(R[k], Yr, bsr, ydr, u, lane, T);
@@ -982,16 +1104,16 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
     }
 }
 
-template <int WT, int NIT, int NSB>
+template <int WT, int NIT, int NSB, int PRO>
 __global__ __launch_bounds__(THREADS) void k_matvec_1t(MvArgs a) {
-    matvec_1t_body<WT, NIT, NSB>(a, (int)gridDim.x, (int)blockIdx.x, (int)blockIdx.y);
+    matvec_1t_body<WT, NIT, NSB, PRO>(a, (int)gridDim.x, (int)blockIdx.x, (int)blockIdx.y);
 }
 
 // k_matvec_1t's pair form (see k_matvec_rl_pair), one iteration per wave
-template <int WT1, int WT2, int NSB>
+template <int WT1, int WT2, int NSB, int PRO>
 __global__ __launch_bounds__(THREADS) void k_matvec_1t_pair(MvArgs a, MvArgs b, int g1) {
-    if ((int)blockIdx.x < g1) matvec_1t_body<WT1, 1, NSB>(a, g1, (int)blockIdx.x, 0);
-    else matvec_1t_body<WT2, 1, NSB>(b, (int)gridDim.x - g1, (int)blockIdx.x - g1, 0);
+    if ((int)blockIdx.x < g1) matvec_1t_body<WT1, 1, NSB, PRO>(a, g1, (int)blockIdx.x, 0);
+    else matvec_1t_body<WT2, 1, NSB, PRO>(b, (int)gridDim.x - g1, (int)blockIdx.x - g1, 0);
 }
 
 // Long rows, one token (K-quants with T > 64 units, e.g. n_in = 11008 with 172 units): a wave owns
@@ -1000,8 +1122,11 @@ __global__ __launch_bounds__(THREADS) void k_matvec_1t_pair(MvArgs a, MvArgs b, 
 // terms in super-block order with lane reads (the reference's sequential f32 order). Each lane keeps
 // the activations of its units in registers (read from memory with the first row's weights). Each
 // wave walks its rows one at a time.
-template <int WT, int NI>
+// PRO = 1: the f32 row a.px is quantised by the workgroup into LDS (q8k_row_lds) instead of read
+// from a.xq.
+template <int WT, int NI, int PRO = 0>
 __global__ __launch_bounds__(THREADS) void k_matvec_lr(MvArgs a) {
+    constexpr int PRO_NR = 4 * NI < 12 ? 4 * NI : 12;  // the row's super-blocks per wave in one round (NI <= 3)
     const int T = a.P.T, nb = a.P.nb;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const long n_rows = a.row1 - a.row0;
@@ -1016,8 +1141,14 @@ __global__ __launch_bounds__(THREADS) void k_matvec_lr(MvArgs a) {
         }
     };
     WRegs<WT> A[NI];
-    if (wid >= n_rows) return;
-    load_row(wid, A);
+    extern __shared__ uint8_t lds_act[];
+    Q8kRow<false, PRO_NR> arow;
+    // (with PRO, waves past the rows still take part in the workgroup's activation row: they load
+    // row 0 and run no row)
+    if constexpr (PRO) arow.issue(a.px, nullptr, a.P.n_in);
+    else if (wid >= n_rows) return;
+    const long w0 = wid < n_rows ? wid : 0;
+    load_row(w0, A);
     // the bias and residual of the row, requested with its weights (lane 0 stores)
     float bv = 0.0f, rv = 0.0f;
     auto load_br = [&](long r) {
@@ -1026,16 +1157,21 @@ __global__ __launch_bounds__(THREADS) void k_matvec_lr(MvArgs a) {
             if (a.resid) rv = a.resid[a.row0 + r];
         }
     };
-    load_br(wid);
+    load_br(w0);
     // the lane's activations (the 64 Q8_K bytes of its unit in each pass, their bsums and the block
     // scale) straight from memory into registers, requested with the first row's weights: no LDS
     // staging, no barrier
     uint4 Yr[NI][4];
     uint2 bsr[NI];
     float ydr[NI];
+    if constexpr (PRO) arow.build(a.px, 0.0f, a.P.n_in, lds_act);
 #pragma unroll
     for (int k = 0; k < NI; k++) {
         const int u = 64 * k + lane, uu = u < T ? u : 0;
+        if constexpr (PRO) {
+            q8k_unit_lds(lds_act, nb, uu, Yr[k], bsr[k], ydr[k]);
+            continue;
+        }
         const uint8_t *blk = a.xq + (size_t)(uu >> 2) * 292;
         const uint8_t *yb = blk + 4 + 64 * (uu & 3);
 #pragma unroll
@@ -1553,39 +1689,49 @@ static int launch_mv_k(MvArgs &A, size_t lds, hipStream_t st) {
 
 static size_t mv_lds_bytes_rl(int T, int MT) { return (size_t)MT * 4 * T * 16 + (size_t)MT * T * 16; }
 
-// Workgroups of a THREADS-thread kernel without dynamic LDS that the GPU holds at once.
-static long resident_wgs(const void *fn, int &per_cu) {
-    if (per_cu == 0) {
+// Workgroups of a THREADS-thread kernel with `lds` bytes of dynamic LDS that the GPU holds at once
+// (the occupancy is cached per kernel and LDS size).
+static long resident_wgs(const void *fn, size_t lds, int &per_cu, size_t &per_cu_lds) {
+    if (per_cu == 0 || per_cu_lds != lds) {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, THREADS, 0) != hipSuccess || n < 1) n = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, THREADS, lds) != hipSuccess || n < 1) n = 1;
         per_cu = n;
+        per_cu_lds = lds;
     }
     return (long)(g_n_cu ? g_n_cu : 256) * per_cu;
 }
 
-template <int WT, int NIT, int NSB>
-static long cap_1t() {
+// LDS of the workgroup-quantised activation row (q8k_row_lds): 0 when the kernel reads a.xq
+static size_t pro_lds(const MvArgs &A) { return A.px ? (size_t)A.P.nb * 292 : 0; }
+static int pro_kind(const MvArgs &A) { return A.px ? (A.pnw ? 2 : 1) : 0; }
+
+template <int WT, int NIT, int NSB, int PRO>
+static long cap_1t(size_t lds) {
     static int per_cu = 0;
-    return resident_wgs((const void *)k_matvec_1t<WT, NIT, NSB>, per_cu);
+    static size_t per_cu_lds = 0;
+    return resident_wgs((const void *)k_matvec_1t<WT, NIT, NSB, PRO>, lds, per_cu, per_cu_lds);
 }
 
-// One token on k_matvec_1t with the smallest NIT (iterations per wave, at most 4) whose grid the GPU
-// holds at once, so that every wave's loads go out at the start; 1 when no NIT fits (the caller
-// then runs the persistent k_matvec_rl).
 static void prep_1t(MvArgs &A) {
     A.rpi = 64 / A.P.T;
     A.tmag = (65536 + A.P.T - 1) / A.P.T;
     A.n_it = (int)((A.row1 - A.row0 + A.rpi - 1) / A.rpi);
 }
 
-template <int WT, int NSB>
-static int launch_mv_1t_nsb(MvArgs &A, hipStream_t st, int n_slot) {
+// One token on k_matvec_1t with the smallest NIT (iterations per wave, at most 4) whose grid the GPU
+// holds at once, so that every wave's loads go out at the start; 1 when no NIT fits (the caller
+// then runs the persistent k_matvec_rl).
+// (dry: report whether some NIT fits, launch nothing)
+template <int WT, int NSB, int PRO>
+static int launch_mv_1t_nsb(MvArgs &A, hipStream_t st, int n_slot, bool dry) {
     const long n_it = A.n_it;
+    const size_t lds = pro_lds(A);
     auto wgs = [&](int nit) { return (n_it + (long)WAVES * nit - 1) / ((long)WAVES * nit); };
 #define SDY_1T(NIT)                                                                                                  \
-    if (wgs(NIT) * n_slot <= cap_1t<WT, NIT, NSB>()) {                                                               \
-        hipLaunchKernelGGL((k_matvec_1t<WT, NIT, NSB>), dim3((unsigned)wgs(NIT), (unsigned)n_slot), dim3(THREADS), 0, \
-                           st, A);                                                                                   \
+    if (wgs(NIT) * n_slot <= cap_1t<WT, NIT, NSB, PRO>(lds)) {                                                       \
+        if (dry) return 0;                                                                                           \
+        hipLaunchKernelGGL((k_matvec_1t<WT, NIT, NSB, PRO>), dim3((unsigned)wgs(NIT), (unsigned)n_slot), dim3(THREADS), \
+                           lds, st, A);                                                                              \
         return sdy_check_launch("matvec");                                                                           \
     }
     SDY_1T(1)
@@ -1596,15 +1742,23 @@ static int launch_mv_1t_nsb(MvArgs &A, hipStream_t st, int n_slot) {
     return 1;
 }
 
-// NSB: the row's super-block count when it is one of the common ones (n_in 768, 2048, 4096)
+template <int WT, int PRO>
+static int launch_mv_1t_pro(MvArgs &A, hipStream_t st, int n_slot, bool dry) {
+    switch (A.P.T) {  // NSB: the row's super-block count when it is a common one (n_in 768, 2048, 4096)
+    case 12: return launch_mv_1t_nsb<WT, 3, PRO>(A, st, n_slot, dry);
+    case 32: return launch_mv_1t_nsb<WT, 8, PRO>(A, st, n_slot, dry);
+    case 64: return launch_mv_1t_nsb<WT, 16, PRO>(A, st, n_slot, dry);
+    default: return launch_mv_1t_nsb<WT, 0, PRO>(A, st, n_slot, dry);
+    }
+}
+
 template <int WT>
-static int launch_mv_1t(MvArgs &A, hipStream_t st, int n_slot) {
+static int launch_mv_1t(MvArgs &A, hipStream_t st, int n_slot, bool dry = false) {
     prep_1t(A);
-    switch (A.P.T) {
-    case 12: return launch_mv_1t_nsb<WT, 3>(A, st, n_slot);
-    case 32: return launch_mv_1t_nsb<WT, 8>(A, st, n_slot);
-    case 64: return launch_mv_1t_nsb<WT, 16>(A, st, n_slot);
-    default: return launch_mv_1t_nsb<WT, 0>(A, st, n_slot);
+    switch (pro_kind(A)) {
+    case 1: return launch_mv_1t_pro<WT, 1>(A, st, n_slot, dry);
+    case 2: return launch_mv_1t_pro<WT, 2>(A, st, n_slot, dry);
+    default: return launch_mv_1t_pro<WT, 0>(A, st, n_slot, dry);
     }
 }
 
@@ -1650,26 +1804,40 @@ static long rl_wgs(const MvArgs &A, int per_cu) {
     return wgs > cap ? cap : wgs;
 }
 
+template <int WT1, int WT2, int NSB, int PRO>
+static int launch_mv_pair_1t(MvArgs &A, MvArgs &B, hipStream_t st, bool dry) {
+    static int per_cu = 0;
+    static size_t per_cu_lds = 0;
+    const size_t lds = pro_lds(A);
+    const long cap = resident_wgs((const void *)k_matvec_1t_pair<WT1, WT2, NSB, PRO>, lds, per_cu, per_cu_lds);
+    auto wgs1 = [](const MvArgs &M) { return ((long)M.n_it + WAVES - 1) / WAVES; };
+    const long g1 = (wgs1(A) + 7) / 8 * 8, g2 = wgs1(B);
+    if (g1 + g2 > cap) return 1;
+    if (dry) return 0;
+    hipLaunchKernelGGL((k_matvec_1t_pair<WT1, WT2, NSB, PRO>), dim3((unsigned)(g1 + g2)), dim3(THREADS), lds, st, A, B,
+                       (int)g1);
+    return sdy_check_launch("matvec_pair");
+}
+
+// the pair on k_matvec_1t_pair when its grid fits the GPU at once (1 when not)
+template <int WT1, int WT2, int PRO>
+static int launch_mv_pair_pro(MvArgs &A, MvArgs &B, hipStream_t st, bool dry = false) {
+    prep_1t(A);
+    prep_1t(B);
+    if (A.P.T == 32 && B.P.T == 32) return launch_mv_pair_1t<WT1, WT2, 8, PRO>(A, B, st, dry);  // 2048-element rows
+    return launch_mv_pair_1t<WT1, WT2, 0, PRO>(A, B, st, dry);
+}
+
 template <int WT1, int WT2>
 static int launch_mv_pair(MvArgs &A, MvArgs &B, hipStream_t st) {
     {
-        static int per_cu_8 = 0, per_cu_0 = 0;
-        prep_1t(A);
-        prep_1t(B);
-        const bool n8 = A.P.T == 32 && B.P.T == 32;  // both rows of 2048 elements: 8 super-blocks
-        const long cap = n8 ? resident_wgs((const void *)k_matvec_1t_pair<WT1, WT2, 8>, per_cu_8)
-                            : resident_wgs((const void *)k_matvec_1t_pair<WT1, WT2, 0>, per_cu_0);
-        auto wgs1 = [](const MvArgs &M) { return ((long)M.n_it + WAVES - 1) / WAVES; };
-        const long g1 = (wgs1(A) + 7) / 8 * 8, g2 = wgs1(B);
-        if (g1 + g2 <= cap) {
-            if (n8)
-                hipLaunchKernelGGL((k_matvec_1t_pair<WT1, WT2, 8>), dim3((unsigned)(g1 + g2)), dim3(THREADS), 0, st, A,
-                                   B, (int)g1);
-            else
-                hipLaunchKernelGGL((k_matvec_1t_pair<WT1, WT2, 0>), dim3((unsigned)(g1 + g2)), dim3(THREADS), 0, st, A,
-                                   B, (int)g1);
-            return sdy_check_launch("matvec_pair");
+        int rc;
+        switch (pro_kind(A)) {
+        case 1: return launch_mv_pair_pro<WT1, WT2, 1>(A, B, st);  // no other kernel for these
+        case 2: return launch_mv_pair_pro<WT1, WT2, 2>(A, B, st);
+        default: rc = launch_mv_pair_pro<WT1, WT2, 0>(A, B, st);
         }
+        if (rc <= 0) return rc;
     }
     static int per_cu = 0;
     if (per_cu == 0) {
@@ -1684,11 +1852,11 @@ static int launch_mv_pair(MvArgs &A, MvArgs &B, hipStream_t st) {
     return sdy_check_launch("matvec_pair");
 }
 
-template <int WT, int NI>
-static int launch_mv_lr_ni(MvArgs &A, size_t lds, hipStream_t st) {
+template <int WT, int NI, int PRO>
+static int launch_mv_lr_ni(MvArgs &A, size_t lds, hipStream_t st, bool dry) {
     static int per_cu = 0;
     static size_t per_cu_lds = 0, granted = 0;
-    const void *fn = (const void *)k_matvec_lr<WT, NI>;
+    const void *fn = (const void *)k_matvec_lr<WT, NI, PRO>;
     int rc = sdy_lds_limit(fn, lds, &granted);
     if (rc) return rc;
     if (per_cu == 0 || per_cu_lds != lds) {
@@ -1699,21 +1867,27 @@ static int launch_mv_lr_ni(MvArgs &A, size_t lds, hipStream_t st) {
     }
     long wgs = (A.row1 - A.row0 + WAVES - 1) / WAVES;
     long cap = (long)(g_n_cu ? g_n_cu : 256) * per_cu;
-    if (wgs > cap) wgs = cap;
-    hipLaunchKernelGGL((k_matvec_lr<WT, NI>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
+    if (wgs > cap) {
+        // the workgroup-quantised row needs every workgroup's waves at once (each quantises once)
+        if (PRO) return 1;
+        wgs = cap;
+    }
+    if (dry) return 0;
+    hipLaunchKernelGGL((k_matvec_lr<WT, NI, PRO>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
     return sdy_check_launch("matvec");
 }
 
 // one token, long rows: NI = ceil(T / 64) passes per row
-template <int WT>
-static int launch_mv_lr(MvArgs &A, size_t lds, hipStream_t st) {
+template <int WT, int PRO = 0>
+static int launch_mv_lr(MvArgs &A, size_t lds, hipStream_t st, bool dry = false) {
+    if (PRO) lds = pro_lds(A);
     switch ((A.P.T + 63) / 64) {
-    case 1: return launch_mv_lr_ni<WT, 1>(A, lds, st);
-    case 2: return launch_mv_lr_ni<WT, 2>(A, lds, st);
-    case 3: return launch_mv_lr_ni<WT, 3>(A, lds, st);
-    case 4: return launch_mv_lr_ni<WT, 4>(A, lds, st);
-    case 5: return launch_mv_lr_ni<WT, 5>(A, lds, st);
-    case 6: return launch_mv_lr_ni<WT, 6>(A, lds, st);
+    case 1: return launch_mv_lr_ni<WT, 1, PRO>(A, lds, st, dry);
+    case 2: return launch_mv_lr_ni<WT, 2, PRO>(A, lds, st, dry);
+    case 3: return launch_mv_lr_ni<WT, 3, PRO>(A, lds, st, dry);
+    case 4: return launch_mv_lr_ni<WT, 4, PRO>(A, lds, st, dry);
+    case 5: return launch_mv_lr_ni<WT, 5, PRO>(A, lds, st, dry);
+    case 6: return launch_mv_lr_ni<WT, 6, PRO>(A, lds, st, dry);
     default: return sdy_fail(-1, "matvec: rows of %d elements are above the one-token kernel's 24576", A.P.n_in);
     }
 }
@@ -1800,7 +1974,75 @@ static MvArgs rl_args(const sdy_mat *m, const sdy_mv_args *a) {
     A.row1 = a->row1;
     A.swiglu = a->epilogue == SDY_EPI_SWIGLU;
     A.nterm = A.P.nb;
+    if (!a->xq && a->x) {  // the workgroup quantises the f32 row
+        A.px = a->x;
+        A.pnw = a->nw;
+        A.peps = a->eps;
+    }
     return A;
+}
+
+static void ensure_n_cu() {
+    if (!g_n_cu) {
+        int n_cu = 0;
+        size_t mem = 0;
+        sdy_device_info(&n_cu, &mem);
+        g_n_cu = n_cu;
+    }
+}
+
+// The argument checks of a workgroup-quantised (xq = NULL, x set) one-token matvec; 0 when fine.
+static int fused_args_check(const sdy_mat *m, const sdy_mv_args *a) {
+    if (m->type != SDY_Q4_K && m->type != SDY_Q6_K) return sdy_fail(-1, "matvec: in-kernel quantisation needs Q4_K / Q6_K");
+    if (a->n_tok != 1) return sdy_fail(-1, "matvec: in-kernel quantisation of one token only");
+    if (m->n_in % 256 || ((uintptr_t)a->x & 15) || (a->nw && ((uintptr_t)a->nw & 15)))
+        return sdy_fail(-1, "matvec: in-kernel quantisation needs 256-element blocks and 16-byte aligned rows");
+    if (a->nw && m->n_in > 4096) return sdy_fail(-1, "matvec: in-kernel RMSNorm of rows above 4096 elements");
+    if (a->row0 < 0 || a->row1 > m->n_rows || a->row0 > a->row1)
+        return sdy_fail(-1, "matvec rows [%ld, %ld) outside %ld", a->row0, a->row1, m->n_rows);
+    if (m->n_units <= 64) {
+        if (!rl_one_token_ok(m, a->epilogue)) return sdy_fail(-1, "matvec: SwiGLU rows per iteration must be even");
+    } else if (a->nw || a->epilogue == SDY_EPI_SWIGLU) {
+        return sdy_fail(-1, "matvec: rows above 4096 elements are quantised in-kernel without RMSNorm or SwiGLU");
+    }
+    return 0;
+}
+
+// launch (or, dry, test) one workgroup-quantised matvec: 0 done, 1 no grid fits, < 0 error
+static int fused_launch(const sdy_mat *m, const sdy_mv_args *a, hipStream_t st, bool dry) {
+    int rc = fused_args_check(m, a);
+    if (rc) return rc;
+    ensure_n_cu();
+    MvArgs A = rl_args(m, a);
+    const bool q4 = m->type == SDY_Q4_K;
+    if (m->n_units <= 64) return q4 ? launch_mv_1t<SDY_Q4_K>(A, st, 1, dry) : launch_mv_1t<SDY_Q6_K>(A, st, 1, dry);
+    return q4 ? launch_mv_lr<SDY_Q4_K, 1>(A, 0, st, dry) : launch_mv_lr<SDY_Q6_K, 1>(A, 0, st, dry);
+}
+
+template <int WT1, int WT2>
+static int pair_fused_launch(MvArgs &A, MvArgs &B, hipStream_t st, bool dry) {
+    return A.pnw ? launch_mv_pair_pro<WT1, WT2, 2>(A, B, st, dry) : launch_mv_pair_pro<WT1, WT2, 1>(A, B, st, dry);
+}
+
+static int pair_fused(const sdy_mat *m1, const sdy_mv_args *a1, const sdy_mat *m2, const sdy_mv_args *a2, hipStream_t st,
+                      bool dry) {
+    int rc;
+    if ((rc = fused_args_check(m1, a1)) || (rc = fused_args_check(m2, a2))) return rc;
+    if (m1->n_units > 64 || m2->n_units > 64 || a1->x != a2->x || a1->nw != a2->nw || a1->eps != a2->eps)
+        return sdy_fail(-1, "matvec_pair: in-kernel quantisation needs rows of at most 4096 elements and one shared row");
+    ensure_n_cu();
+    MvArgs A = rl_args(m1, a1), B = rl_args(m2, a2);
+    const bool q4a = m1->type == SDY_Q4_K, q4b = m2->type == SDY_Q4_K;
+    if (q4a && q4b) return pair_fused_launch<SDY_Q4_K, SDY_Q4_K>(A, B, st, dry);
+    if (q4a) return pair_fused_launch<SDY_Q4_K, SDY_Q6_K>(A, B, st, dry);
+    if (q4b) return pair_fused_launch<SDY_Q6_K, SDY_Q4_K>(A, B, st, dry);
+    return pair_fused_launch<SDY_Q6_K, SDY_Q6_K>(A, B, st, dry);
+}
+
+extern "C" int sdy_matvec_fused_ok(const sdy_mat *m, const sdy_mv_args *a, const sdy_mat *m2, const sdy_mv_args *a2) {
+    if (!a || a->xq || !a->x || (m2 && (!a2 || a2->xq))) return 0;
+    const int rc = m2 ? pair_fused(m, a, m2, a2, nullptr, true) : fused_launch(m, a, nullptr, true);
+    return rc == 0;
 }
 
 extern "C" int sdy_matvec_pair_ok(const sdy_mat *m1, int epilogue1, const sdy_mat *m2, int epilogue2) {
@@ -1822,6 +2064,11 @@ extern "C" int sdy_matvec_pair(const sdy_mat *m1, const sdy_mv_args *a1, const s
     }
     if (a1->row0 == a1->row1) return sdy_matvec(m2, a2, s);
     if (a2->row0 == a2->row1) return sdy_matvec(m1, a1, s);
+    if (!a1->xq || !a2->xq) {
+        if (a1->xq || a2->xq) return sdy_fail(-1, "matvec_pair: both quantised rows or neither");
+        const int frc = pair_fused(m1, a1, m2, a2, (hipStream_t)s, false);
+        return frc > 0 ? sdy_fail(-1, "matvec_pair: no grid of the in-kernel quantisation fits these matrices") : frc;
+    }
     MvArgs A = rl_args(m1, a1), B = rl_args(m2, a2);
     hipStream_t st = (hipStream_t)s;
     const bool q4a = m1->type == SDY_Q4_K, q4b = m2->type == SDY_Q4_K;
@@ -1836,6 +2083,15 @@ extern "C" int sdy_matvec(const sdy_mat *m, const sdy_mv_args *a, sdy_stream s) 
     if (a->row0 < 0 || a->row1 > m->n_rows || a->row0 > a->row1)
         return sdy_fail(-1, "matvec rows [%ld, %ld) outside %ld", a->row0, a->row1, m->n_rows);
     if (a->row0 == a->row1 || a->n_tok <= 0) return 0;
+    if (!a->xq && m->type != SDY_F32 && m->type != SDY_F16 && m->type != SDY_BF16) {
+        if (!a->x) return sdy_fail(-1, "matvec: no activations (xq and x both null)");
+        if (a->epilogue == SDY_EPI_SWIGLU && (((a->row1 - a->row0) | a->row0) & 1 || a->bias || a->resid))
+            return sdy_fail(-1, "matvec: the SwiGLU epilogue needs an even row range starting at an even row, no "
+                                "bias and no residual");
+        const int rc = fused_launch(m, a, st, false);
+        return rc > 0 ? sdy_fail(-1, "matvec: no grid of the in-kernel quantisation fits %ld rows", a->row1 - a->row0)
+                      : rc;
+    }
     if (a->epilogue == SDY_EPI_SWIGLU && (((a->row1 - a->row0) | a->row0) & 1 || a->bias || a->resid))
         return sdy_fail(-1, "matvec: the SwiGLU epilogue needs an even row range starting at an even row, no bias "
                             "and no residual");

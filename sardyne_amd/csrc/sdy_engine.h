@@ -55,6 +55,7 @@ struct engine_ctx {
     int n_decode;               /* one-token evals so far (the first runs eagerly) */
     int decode_fused;           /* one-token steps use the fused decode kernels */
     int use_graph;              /* one-token steps are recorded once and replayed */
+    int fuse_act;               /* one-token matvecs quantise (and RMS-normalise) their f32 row in-kernel */
     int moe_device;             /* one-token MoE blocks route, run their experts and combine on the
                                    device (grouped matvec, no host round trip) */
     float *qkv;                 /* q | k | v of one token */

@@ -96,10 +96,18 @@ typedef struct {
     long row0, row1;     /* rows computed */
     int epilogue;        /* SDY_EPI_NONE, or SDY_EPI_SWIGLU: rows (2i, 2i+1) of [row0, row1) are the gate and
                             up rows of output i, out[t * out_stride + i] = silu(gate) * up */
+    const float *nw;     /* K-quant weights with xq = NULL and x set (one token): the kernel builds the Q8_K
+                            row of x itself, RMS-normalised first when nw is set (x / rms(x) * nw, eps), with
+                            the bytes sdy_quantize / sdy_norm_quant would write; see sdy_matvec_fused_ok */
+    float eps;
 } sdy_mv_args;
 enum { SDY_EPI_NONE = 0, SDY_EPI_SWIGLU = 1 };
 /* out = W · x for rows [row0, row1) and n_tok tokens. */
 int sdy_matvec(const sdy_mat *m, const sdy_mv_args *a, sdy_stream s);
+/* 1 when sdy_matvec (and, for two matrices, sdy_matvec_pair) can quantise the f32 row itself for these
+ * arguments: one token, Q4_K / Q6_K, 256-element blocks, x (and nw) 16-byte aligned, nw only for
+ * rows of at most 4096 elements, and a grid the GPU holds at once. m2/a2 may be NULL. */
+int sdy_matvec_fused_ok(const sdy_mat *m, const sdy_mv_args *a, const sdy_mat *m2, const sdy_mv_args *a2);
 /* Two one-token matvecs in one launch (each with the bits of sdy_matvec): Q4_K / Q6_K matrices of
  * at most 4096-element rows, e.g. a layer's q|k and a v of another type on the same Q8_K row. */
 int sdy_matvec_pair_ok(const sdy_mat *m1, int epilogue1, const sdy_mat *m2, int epilogue2);

@@ -388,6 +388,115 @@ def test_matvec_one_token_large(kind, n_in, n_out):
     m.close()
 
 
+Q8K_TYPE = 15
+
+
+def _fused_case(kind, n_in, n_out, seed):
+    t = TYPES[kind]
+    rng = np.random.default_rng(seed)
+    w = random_blocks(kind, n_out * n_in // O.QK[t], rng).reshape(n_out, -1)
+    x = (3.0 * rng.standard_normal(n_in)).astype(np.float32)
+    nw = (1.0 + 0.5 * rng.standard_normal(n_in)).astype(np.float32)
+    return t, w, x, nw
+
+
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("n_in,n_out,mode", [
+    (2048, 2560, "norm_bias"), (2048, 22016, "norm_swiglu"), (2048, 2048, "quant_resid"), (11008, 2048, "quant_resid"),
+    (768, 2048, "norm"), (4096, 2048, "quant_resid"), (4096, 512, "norm"), (1024, 40000, "quant_bias"),
+    (256, 300, "norm_swiglu"), (11008, 37, "quant"), (2048, 5, "norm")])
+def test_matvec_fused_activation(kind, n_in, n_out, mode):
+    """A one-token matvec whose workgroups build the Q8_K row of the f32 input themselves (RMS-
+    normalised first for 'norm') has the bits of sdy_norm_quant / sdy_quantize followed by
+    sdy_matvec, with a bias, a residual or the SwiGLU epilogue."""
+    L = lib()
+    t, w, x, nw = _fused_case(kind, n_in, n_out, n_in + n_out)
+    norm, swiglu = mode.startswith("norm"), mode.endswith("swiglu")
+    eps = 1e-6
+    m = capi.DeviceMatrix(t, n_in, n_out, w)
+    dx, dnw = capi.DeviceBuffer.from_array(x), capi.DeviceBuffer.from_array(nw)
+    rng = np.random.default_rng(n_out)
+    extra = capi.DeviceBuffer.from_array(rng.standard_normal(n_out).astype(np.float32))
+    dq = capi.DeviceBuffer(n_in // 256 * 292)
+    if norm:
+        capi.check(L.sdy_norm_quant(dx.ptr, dnw.ptr, eps, n_in, 1, None, Q8K_TYPE, dq.ptr, None))
+    else:
+        capi.check(L.sdy_quantize(Q8K_TYPE, dx.ptr, dq.ptr, n_in, 1, None))
+    n_res = n_out // 2 if swiglu else n_out
+    outs = []
+    for fused in (False, True):
+        dout = capi.DeviceBuffer.from_array(np.full(n_res, np.nan, np.float32))
+        a = capi.SdyMvArgs(n_tok=1, out=dout.ptr, out_stride=n_res, row0=0, row1=n_out,
+                           epilogue=capi.EPI_SWIGLU if swiglu else capi.EPI_NONE,
+                           bias=extra.ptr if mode.endswith("bias") else None,
+                           resid=extra.ptr if mode.endswith("resid") else None)
+        if fused:
+            a.x, a.nw, a.eps = dx.ptr, dnw.ptr if norm else None, eps
+            assert L.sdy_matvec_fused_ok(ctypes.byref(m.m), ctypes.byref(a), None, None) == 1
+        else:
+            a.xq = dq.ptr
+        capi.check(L.sdy_matvec(ctypes.byref(m.m), ctypes.byref(a), None))
+        outs.append(dout.to_array(np.float32, n_res))
+    assert not np.isnan(outs[0]).any()
+    assert np.array_equal(bits(outs[1]), bits(outs[0]))
+    m.close()
+
+
+@pytest.mark.parametrize("norm", [True, False])
+def test_matvec_pair_fused_activation(norm):
+    """The paired one-token matvec (q|k Q4_K and v Q6_K) building its own Q8_K row: the bits of the
+    pair on the row sdy_norm_quant / sdy_quantize wrote."""
+    L = lib()
+    n_in, n1, n2, eps = 2048, 2560, 256, 1e-6
+    _, w1, x, nw = _fused_case("Q4_K", n_in, n1, 5)
+    _, w2, _, _ = _fused_case("Q6_K", n_in, n2, 6)
+    m1, m2 = capi.DeviceMatrix(O.Q4_K, n_in, n1, w1), capi.DeviceMatrix(O.Q6_K, n_in, n2, w2)
+    dx, dnw = capi.DeviceBuffer.from_array(x), capi.DeviceBuffer.from_array(nw)
+    b1 = capi.DeviceBuffer.from_array(np.random.default_rng(1).standard_normal(n1).astype(np.float32))
+    b2 = capi.DeviceBuffer.from_array(np.random.default_rng(2).standard_normal(n2).astype(np.float32))
+    dq = capi.DeviceBuffer(n_in // 256 * 292)
+    if norm:
+        capi.check(L.sdy_norm_quant(dx.ptr, dnw.ptr, eps, n_in, 1, None, Q8K_TYPE, dq.ptr, None))
+    else:
+        capi.check(L.sdy_quantize(Q8K_TYPE, dx.ptr, dq.ptr, n_in, 1, None))
+    res = []
+    for fused in (False, True):
+        o1, o2 = capi.DeviceBuffer(n1 * 4), capi.DeviceBuffer(n2 * 4)
+        a1 = capi.SdyMvArgs(n_tok=1, out=o1.ptr, out_stride=n1, row0=0, row1=n1, bias=b1.ptr)
+        a2 = capi.SdyMvArgs(n_tok=1, out=o2.ptr, out_stride=n2, row0=0, row1=n2, bias=b2.ptr)
+        for a in (a1, a2):
+            if fused:
+                a.x, a.nw, a.eps = dx.ptr, dnw.ptr if norm else None, eps
+            else:
+                a.xq = dq.ptr
+        if fused:
+            assert L.sdy_matvec_fused_ok(ctypes.byref(m1.m), ctypes.byref(a1), ctypes.byref(m2.m), ctypes.byref(a2)) == 1
+        capi.check(L.sdy_matvec_pair(ctypes.byref(m1.m), ctypes.byref(a1), ctypes.byref(m2.m), ctypes.byref(a2), None))
+        res.append((o1.to_array(np.float32, n1), o2.to_array(np.float32, n2)))
+    for r0, r1 in zip(res[0], res[1]):
+        assert np.array_equal(bits(r0), bits(r1))
+
+
+def test_matvec_fused_activation_rejects():
+    """Arguments the in-kernel quantisation does not cover are refused (no launch): other weight
+    types, several tokens, a misaligned row, RMSNorm of rows above 4096 elements, SwiGLU on long rows."""
+    L = lib()
+    x = capi.DeviceBuffer.from_array(np.ones(8192 + 64, np.float32))
+    out = capi.DeviceBuffer(4 * 4096)
+    cases = [("Q8_0", 2048, 1, 0, False, capi.EPI_NONE), ("Q4_K", 2048, 2, 0, False, capi.EPI_NONE),
+             ("Q4_K", 2048, 1, 4, False, capi.EPI_NONE), ("Q4_K", 8192, 1, 0, True, capi.EPI_NONE),
+             ("Q6_K", 11008, 1, 0, False, capi.EPI_SWIGLU)]
+    for kind, n_in, n_tok, off, norm, epi in cases:
+        t = TYPES[kind]
+        w = random_blocks(kind, 8 * n_in // O.QK[t], np.random.default_rng(0)).reshape(8, -1)
+        m = capi.DeviceMatrix(t, n_in, 8, w)
+        a = capi.SdyMvArgs(x=x.ptr + off, nw=x.ptr if norm else None, eps=1e-6, n_tok=n_tok, out=out.ptr, out_stride=8,
+                           row0=0, row1=8, epilogue=epi)
+        assert L.sdy_matvec_fused_ok(ctypes.byref(m.m), ctypes.byref(a), None, None) == 0, (kind, n_in, n_tok, off)
+        assert L.sdy_matvec(ctypes.byref(m.m), ctypes.byref(a), None) != 0, (kind, n_in, n_tok, off)
+        m.close()
+
+
 @pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
 @pytest.mark.parametrize("n_in,ffn", [(2048, 11008), (1024, 20000), (1024, 36000), (256, 70000)])
 def test_swiglu_epilogue_large(kind, n_in, ffn):
