@@ -1116,6 +1116,74 @@ __global__ __launch_bounds__(THREADS) void k_matvec_1t_pair(MvArgs a, MvArgs b, 
     else matvec_1t_body<WT2, 1, NSB, PRO>(b, (int)gridDim.x - g1, (int)blockIdx.x - g1, 0);
 }
 
+// One token, K-quants with at most 64 units per row, when the rows are too many for k_matvec_1t
+// (the output head): a grid the GPU holds at once, wave w of S taking iterations w, w + S, ...
+// (64/T rows each) with NB iterations' weights in flight in a ring of registers. Every load is
+// unconditional (rows past the end read row0), so the code is straight-line per round of NB
+// iterations and the compiler's wait before each iteration's computation covers only that
+// iteration's loads; the slot is refilled right after its computation. Same lane layout and
+// arithmetic as k_matvec_1t (the same bits); no SwiGLU epilogue.
+template <int WT, int NB, int NSB>
+__global__ __launch_bounds__(THREADS) void k_matvec_ring(MvArgs a) {
+    const int T = a.P.T;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int rpi = a.rpi;
+    const int rl_ = __mul24(lane, a.tmag) >> 16, u = lane - __mul24(rl_, T);
+    const bool lane_on = rl_ < rpi;
+    const int rl = lane_on ? rl_ : 0;
+    const int G = (int)gridDim.x, bx = (int)blockIdx.x;
+    const int vblk = (G & 7) == 0 ? (bx & 7) * (G >> 3) + (bx >> 3) : bx;  // XCD-aware renumbering
+    const int S = G * WAVES, wid = vblk * WAVES + wave;
+    if (wid >= a.n_it) return;
+    const int n_my = (a.n_it - wid + S - 1) / S;  // this wave's iterations
+    const uint32_t le = lane_on ? lane : u, nb = a.P.nb, r0 = (uint32_t)a.row0;
+    WRegs<WT> R[NB];
+    // iteration i of this wave: rows row0 + (wid + i S) rpi + rl
+    auto load_i = [&](int t, int i) {
+        const uint32_t base = (uint32_t)(a.row0 + (long)(wid + i * S) * rpi);
+        const bool ok = (long)base + rl < a.row1;
+        const uint32_t iu = ok ? base * (uint32_t)T + le : r0 * (uint32_t)T + u;
+        const uint32_t is = ok ? base * nb + (le >> 2) : r0 * nb + (u >> 2);
+        load_w_at<WT>(a.P, iu, is, (uint32_t)u, R[t]);
+    };
+    load_i(0, 0);
+    uint4 Yr[4];
+    const uint8_t *blk = a.xq + __mul24(u >> 2, 292);
+    const uint8_t *yb = blk + 4 + 64 * (u & 3);
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        Yr[q] = make_uint4(ld4(yb + 16 * q), ld4(yb + 16 * q + 4), ld4(yb + 16 * q + 8), ld4(yb + 16 * q + 12));
+    const uint2 bsr = make_uint2(ld4(blk + 260 + 8 * (u & 3)), ld4(blk + 264 + 8 * (u & 3)));
+    const float ydr = *reinterpret_cast<const float *>(blk);
+#pragma unroll
+    for (int t = 1; t < NB; t++) load_i(t, t);
+    auto finish = [&](float acc, int i) {  // (no SwiGLU epilogue here)
+        const long row = a.row0 + (long)(wid + i * S) * rpi + rl;
+        const bool valid = lane_on && row < a.row1;
+        if (u == 0 && valid) {
+            if (a.bias) acc = acc + a.bias[row];
+            if (a.resid) acc = a.resid[row] + acc;
+            a.out[row] = acc;
+        }
+    };
+    int i0 = 0;
+    for (; i0 + NB <= n_my; i0 += NB) {
+#pragma unroll
+        for (int t = 0; t < NB; t++) {
+            const float acc = rl_row_sum<WT, NSB>(R[t], Yr, bsr, ydr, u, lane, T);
+            // an opaque zero that depends on acc: the refill of slot t cannot be issued before the
+            // slot's registers are read
+            int z;
+            asm volatile("s_mov_b32 %0, 0" : "=s"(z) : "v"(acc));
+            load_i(t, i0 + t + NB + z);
+            finish(acc, i0 + t);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NB; t++)  // the last n_my - i0 < NB iterations, already in flight
+        if (i0 + t < n_my) finish(rl_row_sum<WT, NSB>(R[t], Yr, bsr, ydr, u, lane, T), i0 + t);
+}
+
 // Long rows, one token (K-quants with T > 64 units, e.g. n_in = 11008 with 172 units): a wave owns
 // whole rows, lane l handles units l, l + 64, ..., l + 64 (NI - 1) of a row. After the quad
 // reduction the term of super-block s = 16k + q sits in lane 4q of pass k, and the row sum folds the
@@ -1762,11 +1830,37 @@ static int launch_mv_1t(MvArgs &A, hipStream_t st, int n_slot, bool dry = false)
     }
 }
 
+template <int WT, int NB, int NSB>
+static int launch_mv_ring_nsb(MvArgs &A, hipStream_t st) {
+    static int per_cu = 0;
+    static size_t per_cu_lds = 0;
+    long wgs = ((long)A.n_it + WAVES - 1) / WAVES;
+    const long cap = resident_wgs((const void *)k_matvec_ring<WT, NB, NSB>, 0, per_cu, per_cu_lds);
+    if (wgs > cap) wgs = cap;
+    if (wgs > 8) wgs &= ~7L;  // a multiple of 8: the XCD-aware numbering applies
+    hipLaunchKernelGGL((k_matvec_ring<WT, NB, NSB>), dim3((unsigned)wgs), dim3(THREADS), 0, st, A);
+    return sdy_check_launch("matvec");
+}
+
+// one token, one slot, no in-kernel quantisation: the persistent ring kernel (ring depth measured on
+// the 151936 x 2048 output head: Q6_K 3, Q4_K 2)
+template <int WT>
+static int launch_mv_ring(MvArgs &A, hipStream_t st) {
+    constexpr int NB = WT == SDY_Q6_K ? 3 : 2;
+    prep_1t(A);
+    switch (A.P.T) {
+    case 32: return launch_mv_ring_nsb<WT, NB, 8>(A, st);
+    case 64: return launch_mv_ring_nsb<WT, NB, 16>(A, st);
+    default: return launch_mv_ring_nsb<WT, NB, 0>(A, st);
+    }
+}
+
 template <int WT, int MT, bool YREG>
 static int launch_mv_rl(MvArgs &A, size_t lds, hipStream_t st, int n_slot = 1) {
     if constexpr (MT == 1 && YREG && is_k(WT)) {
         const int rc = launch_mv_1t<WT>(A, st, n_slot);
         if (rc <= 0) return rc;
+        if (n_slot == 1 && !A.px && !A.swiglu) return launch_mv_ring<WT>(A, st);
     }
     static int per_cu = 0;
     static size_t per_cu_lds = 0;
