@@ -140,6 +140,8 @@ _DEVICE_SIGNATURES = {
     "sdy_matvec_pair_ok": (_int, [ctypes.POINTER(SdyMat), _int, ctypes.POINTER(SdyMat), _int]),
     "sdy_matvec_fused_ok": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), ctypes.POINTER(SdyMat),
                                    ctypes.POINTER(SdyMvArgs)]),
+    "sdy_matvec_grouped_fused_ok": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _int, ctypes.c_long,
+                                           ctypes.c_long]),
     "sdy_matvec_pair": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), ctypes.POINTER(SdyMat),
                                ctypes.POINTER(SdyMvArgs), _vp]),
     "sdy_matvec_float": (_int, [_int, _vp, _int, ctypes.POINTER(SdyMvArgs), _vp]),

@@ -296,17 +296,24 @@ static int moe_decode(engine_ctx *c, const dlayer *L) {
         TRY(sdy_matvec_grouped(&L->up.m, &a, c->moe_top, k, fe, 0, fe, c->st));
         TRY(sdy_silu_mul(c->hb, c->hb2, (long)k * fe, c->st));
     }
-    /* the k SwiGLU rows, quantised for down (the Q8_K row of xb is no longer needed) */
+    /* down over the k SwiGLU rows: each slot's workgroups quantise its row themselves, or (when that
+       is not available) the rows are quantised first (the Q8_K row of xb is no longer needed) */
     c->xq_src[0] = c->xq_src[1] = NULL;
-    TRY(sdy_quantize(SDY_Q8_K, c->hb, c->xq[1], fe, k, c->st));
     memset(&a, 0, sizeof a);
     a.n_tok = 1;
-    a.xq = c->xq[1];
+    a.x = c->hb;
     a.out = c->moe_y;
     a.out_stride = dim;
     a.row0 = 0;
     a.row1 = dim;
-    TRY(sdy_matvec_grouped(&L->down.m, &a, c->moe_top, k, dim, (long)(fe / 256) * 292, dim, c->st));
+    long x_slot = fe;
+    if (!c->fuse_act || !sdy_matvec_grouped_fused_ok(&L->down.m, &a, k, dim, x_slot)) {
+        TRY(sdy_quantize(SDY_Q8_K, c->hb, c->xq[1], fe, k, c->st));
+        a.x = NULL;
+        a.xq = c->xq[1];
+        x_slot = (long)(fe / 256) * 292;
+    }
+    TRY(sdy_matvec_grouped(&L->down.m, &a, c->moe_top, k, dim, x_slot, dim, c->st));
     return sdy_moe_combine(c->moe_y, c->moe_top, c->moe_w, 1, k, dim, c->x, c->x, c->st);
 }
 

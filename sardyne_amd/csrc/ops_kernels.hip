@@ -147,6 +147,7 @@ __global__ __launch_bounds__(64) void k_moe_route(const float *logits, int n_exp
                                                   float *wts) {
     const int t = blockIdx.x, lane = threadIdx.x;
     const float *p = logits + (size_t)t * n_expert;
+    const uint32_t etab = sdy_expf_tab_lane(lane);  // the exponential's table, loaded with the logits
     float v[NPL];
     float m = -INFINITY;
 #pragma unroll
@@ -161,11 +162,10 @@ __global__ __launch_bounds__(64) void k_moe_route(const float *logits, int n_exp
     // n_expert (never chosen).
     double s = 0.0;
 #pragma unroll
-    for (int j = 0; j < NPL; j++)
-        if (lane + 64 * j < n_expert) {
-            v[j] = sdy_expf(v[j] - m);
-            s += (double)v[j];
-        }
+    for (int j = 0; j < NPL; j++) {
+        v[j] = sdy_expf_reg(v[j] - m, etab);  // every lane (the table lookup reads other lanes): 0 past n_expert
+        if (lane + 64 * j < n_expert) s += (double)v[j];
+    }
     for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
     const float inv = (float)(1.0 / s);
 #pragma unroll

@@ -295,10 +295,12 @@ struct MvArgs {
     // k_matvec_1t: rows per iteration 64/T, (lane * tmag) >> 16 == lane / T for lane < 64, and the
     // iteration count
     int rpi, tmag, n_it;
-    // activations quantised by the kernel itself (one token, K-quants): the f32 row px, first
-    // RMS-normalised with the weights pnw and peps when pnw is set
+    // activations quantised by the kernel itself (one token, K-quants): the f32 row px (slot s's at
+    // px + s * px_slot in a grouped launch), first RMS-normalised with the weights pnw and peps when
+    // pnw is set
     const float *px, *pnw;
     float peps;
+    long px_slot;
 };
 
 constexpr bool is_k(int wt) { return wt == SDY_Q4_K || wt == SDY_Q6_K; }
@@ -1007,12 +1009,13 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
     const int S = G * WAVES, wid = vblk * WAVES + wave;
     extern __shared__ uint8_t lds_act[];
     Q8kRow<PRO == 2, PRO_NR> arow;
+    const float *px = a.px + (PRO ? (size_t)slot * a.px_slot : 0);
     // (with PRO, waves past the rows still take part in the workgroup's activation row: their rows
     // are all >= row1, so they load row0 and store nothing)
     if constexpr (PRO == 0) {
         if (wid >= a.n_it) return;
     } else {
-        arow.issue(a.px, a.pnw, a.P.n_in);
+        arow.issue(px, a.pnw, a.P.n_in);
     }
     // load order: the first iteration's weights, the activations, the bias and residual, then the
     // other iterations' weights, so that iteration k waits only for the loads it uses (every load
@@ -1049,11 +1052,11 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
         // every weight load goes out first; the workgroup quantises the row while they are in flight
 #pragma unroll
         for (int k = 1; k < NIT; k++) load_k(k);
-        arow.build(a.px, a.peps, a.P.n_in, lds_act);
+        arow.build(px, a.peps, a.P.n_in, lds_act);
         q8k_unit_lds(lds_act, a.P.nb, u, Yr, bsr, ydr);
     }
     // the bias and residual of the lane's rows (an absent one reads a stand-in: the activation row)
-    const float *stand_in = PRO ? a.px : reinterpret_cast<const float *>(xq);
+    const float *stand_in = PRO ? px : reinterpret_cast<const float *>(xq);
     const float *bsrc = a.bias ? a.bias : stand_in;
     const float *rsrc = a.resid ? a.resid : stand_in;
     float bv[NIT], rv[NIT];
@@ -2211,7 +2214,7 @@ extern "C" int sdy_matvec(const sdy_mat *m, const sdy_mv_args *a, sdy_stream s) 
 
 template <int WT>
 static int mv_grouped(const sdy_mat *m, const sdy_mv_args *a, const int32_t *slot_expert, int n_slot, long slot_rows,
-                      long xq_slot, long out_slot, hipStream_t st) {
+                      long xq_slot, long out_slot, hipStream_t st, bool dry = false) {
     MvArgs A = {};
     A.P = planes_of(m);
     A.xq = (const uint8_t *)a->xq;
@@ -2226,12 +2229,20 @@ static int mv_grouped(const sdy_mat *m, const sdy_mv_args *a, const int32_t *slo
     A.n_slot_exp = (int)(m->n_rows / slot_rows);
     A.xq_slot = xq_slot;
     A.out_slot = out_slot;
+    if (!a->xq) {  // the workgroups quantise their slot's f32 row (a->x + slot * xq_slot floats)
+        A.xq_slot = 0;
+        A.px = a->x;
+        A.pnw = a->nw;
+        A.peps = a->eps;
+        A.px_slot = xq_slot;
+        const int rc = launch_mv_1t<WT>(A, st, n_slot, dry);
+        return rc > 0 ? sdy_fail(-1, "grouped matvec: no grid of the in-kernel quantisation fits") : rc;
+    }
     return launch_mv_rl<WT, 1, true>(A, 0, st, n_slot);
 }
 
-extern "C" int sdy_matvec_grouped(const sdy_mat *m, const sdy_mv_args *a, const int32_t *slot_expert, int n_slot,
-                                  long slot_rows, long xq_slot, long out_slot, sdy_stream s) {
-    hipStream_t st = (hipStream_t)s;
+// The argument checks of sdy_matvec_grouped; 0 when fine.
+static int grouped_check(const sdy_mat *m, const sdy_mv_args *a, int n_slot, long slot_rows, long xq_slot) {
     if (m->type != SDY_Q4_K && m->type != SDY_Q6_K)
         return sdy_fail(-1, "grouped matvec: K-quant weights only (type %d)", m->type);
     if (a->n_tok != 1 || a->bias || a->resid) return sdy_fail(-1, "grouped matvec: one token, no bias or residual");
@@ -2244,6 +2255,28 @@ extern "C" int sdy_matvec_grouped(const sdy_mat *m, const sdy_mv_args *a, const 
     if (T > 64) return sdy_fail(-1, "grouped matvec: rows of %d elements above 4096", m->n_in);
     if (a->epilogue == SDY_EPI_SWIGLU && ((64 / T) % 2 || ((a->row1 - a->row0) | a->row0) & 1))
         return sdy_fail(-1, "grouped matvec: SwiGLU needs an even number of rows per iteration and an even row range");
+    if (!a->xq) {
+        if (!a->x) return sdy_fail(-1, "grouped matvec: no activations");
+        if (m->n_in % 256 || ((uintptr_t)a->x & 15) || (xq_slot * 4) % 16 || (a->nw && ((uintptr_t)a->nw & 15)))
+            return sdy_fail(-1, "grouped matvec: in-kernel quantisation needs 256-element blocks and 16-byte aligned rows");
+    }
+    return 0;
+}
+
+extern "C" int sdy_matvec_grouped_fused_ok(const sdy_mat *m, const sdy_mv_args *a, int n_slot, long slot_rows,
+                                           long x_slot) {
+    if (!a || a->xq || !a->x || grouped_check(m, a, n_slot, slot_rows, x_slot)) return 0;
+    ensure_n_cu();
+    const int rc = m->type == SDY_Q4_K ? mv_grouped<SDY_Q4_K>(m, a, nullptr, n_slot, slot_rows, x_slot, 0, nullptr, true)
+                                       : mv_grouped<SDY_Q6_K>(m, a, nullptr, n_slot, slot_rows, x_slot, 0, nullptr, true);
+    return rc == 0;
+}
+
+extern "C" int sdy_matvec_grouped(const sdy_mat *m, const sdy_mv_args *a, const int32_t *slot_expert, int n_slot,
+                                  long slot_rows, long xq_slot, long out_slot, sdy_stream s) {
+    hipStream_t st = (hipStream_t)s;
+    int rc = grouped_check(m, a, n_slot, slot_rows, xq_slot);
+    if (rc) return rc;
     if (a->row0 == a->row1) return 0;
     if (!g_n_cu) {
         int n_cu = 0;

@@ -119,6 +119,9 @@ int sdy_matvec_pair(const sdy_mat *m1, const sdy_mv_args *a1, const sdy_mat *m2,
  * rows of at most 4096 elements; the SwiGLU epilogue as in sdy_matvec. */
 int sdy_matvec_grouped(const sdy_mat *m, const sdy_mv_args *a, const int32_t *slot_expert, int n_slot,
                        long slot_rows, long xq_slot, long out_slot, sdy_stream s);
+/* 1 when sdy_matvec_grouped can quantise each slot's f32 row itself (a->xq = NULL, a->x set; slot s's
+ * row at a->x + s * x_slot floats, passed as xq_slot; RMS-normalised first when a->nw is set) */
+int sdy_matvec_grouped_fused_ok(const sdy_mat *m, const sdy_mv_args *a, int n_slot, long slot_rows, long x_slot);
 
 /* The prefill GEMM (gemm_kernels.hip): the same outputs as sdy_matvec (bit for bit) for
  * n_tok >= 2 tokens of Q8_K activations a->xq on Q4_K / Q6_K matrices with gemm_ok, through

@@ -625,6 +625,51 @@ def test_grouped_matvec(kind, n_in, e_rows, swiglu, rows):
             np.testing.assert_allclose(got[s], g, rtol=1e-5, atol=1e-5 * float(np.abs(g).max()))
 
 
+@pytest.mark.parametrize("kind,n_in,e_rows,mode", [
+    ("Q6_K", 768, 2048, "quant"), ("Q4_K", 2048, 1536, "norm_swiglu"), ("Q4_K", 1024, 300, "quant"),
+    ("Q6_K", 2048, 96, "norm")])
+def test_grouped_matvec_fused_activation(kind, n_in, e_rows, mode):
+    """The grouped matvec whose workgroups quantise their slot's f32 row (one row per slot, or one
+    shared row RMS-normalised first): the bits of the grouped matvec on the rows sdy_quantize /
+    sdy_norm_quant wrote."""
+    t = TYPES[kind]
+    L = lib()
+    n_exp, eps = 10, 1e-6
+    top = np.array([7, 2, 9, 2, 0, 4, 5, 1], np.int32)
+    k = len(top)
+    norm, swiglu = mode.startswith("norm"), mode.endswith("swiglu")
+    rng = np.random.default_rng(n_in + e_rows)
+    w = random_blocks(kind, n_exp * e_rows * n_in // 256, rng).reshape(n_exp * e_rows, -1)
+    n_x = 1 if norm else k
+    x = (2.0 * rng.standard_normal((n_x, n_in))).astype(np.float32)
+    nw = (1.0 + 0.3 * rng.standard_normal(n_in)).astype(np.float32)
+    m = capi.DeviceMatrix(t, n_in, n_exp * e_rows, w)
+    dx, dnw, dtop = capi.DeviceBuffer.from_array(x), capi.DeviceBuffer.from_array(nw), capi.DeviceBuffer.from_array(top)
+    xrow = O.row_size(O.Q8_K, n_in)
+    dq = capi.DeviceBuffer(n_x * xrow)
+    if norm:
+        capi.check(L.sdy_norm_quant(dx.ptr, dnw.ptr, eps, n_in, 1, None, Q8K_TYPE, dq.ptr, None))
+    else:
+        capi.check(L.sdy_quantize(Q8K_TYPE, dx.ptr, dq.ptr, n_in, k, None))
+    n_out = e_rows // 2 if swiglu else e_rows
+    epi = capi.EPI_SWIGLU if swiglu else capi.EPI_NONE
+    res = []
+    for fused in (False, True):
+        dout = capi.DeviceBuffer.from_array(np.full((k, n_out), np.nan, np.float32))
+        a = capi.SdyMvArgs(n_tok=1, out=dout.ptr, out_stride=n_out, row0=0, row1=e_rows, epilogue=epi)
+        if fused:
+            a.x, a.nw, a.eps = dx.ptr, dnw.ptr if norm else None, eps
+            x_slot = 0 if norm else n_in
+            assert L.sdy_matvec_grouped_fused_ok(ctypes.byref(m.m), ctypes.byref(a), k, e_rows, x_slot) == 1
+        else:
+            a.xq = dq.ptr
+            x_slot = 0 if norm else xrow
+        capi.check(L.sdy_matvec_grouped(ctypes.byref(m.m), ctypes.byref(a), dtop.ptr, k, e_rows, x_slot, n_out, None))
+        res.append(dout.to_array(np.float32, (k, n_out)))
+    assert not np.isnan(res[0]).any()
+    assert np.array_equal(bits(res[1]), bits(res[0]))
+
+
 def test_grouped_matvec_rejects_bad_shapes():
     L = lib()
     w = random_blocks("Q4_K", 4 * 10 * 2048 // 256, np.random.default_rng(0)).reshape(40, -1)
