@@ -145,6 +145,7 @@ _DEVICE_SIGNATURES = {
     "sdy_matvec_pair": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), ctypes.POINTER(SdyMat),
                                ctypes.POINTER(SdyMvArgs), _vp]),
     "sdy_matvec_float": (_int, [_int, _vp, _int, ctypes.POINTER(SdyMvArgs), _vp]),
+    "sdy_matvec_float_norm": (_int, [_int, _vp, _int, ctypes.POINTER(SdyMvArgs), _vp, _vp]),
     "sdy_matvec_grouped": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp, _int, ctypes.c_long,
                                   ctypes.c_long, ctypes.c_long, _vp]),
     "sdy_mat_alloc": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long]),

@@ -275,8 +275,25 @@ static int moe(engine_ctx *c, const dlayer *L, int n) {
 static int moe_decode(engine_ctx *c, const dlayer *L) {
     const engine_model_info *in = &c->m->info;
     const int dim = in->dim, fe = in->ffn_exp_dim, ne = in->n_expert, k = in->n_expert_used;
-    TRY(norm_for(c, c->x, L->ffn_norm, L->gu_fused ? &L->gate_up : &L->gate, 1)); /* xb and its Q8_K row */
-    TRY(mm(c, c->moe_probs, c->xb, &L->gate_inp, 1, NULL, NULL, 0));
+    const dmat *first = L->gu_fused ? &L->gate_up : &L->gate;
+    if (c->fuse_act && vec_dot_type(first->type) == SDY_Q8_K && dim % 256 == 0 && dim <= 4096) {
+        /* the router reads the FFN-normalised row and writes its Q8_K bytes for gate|up */
+        sdy_mv_args r;
+        memset(&r, 0, sizeof r);
+        r.x = c->x;
+        r.nw = L->ffn_norm;
+        r.eps = in->norm_eps;
+        r.n_tok = 1;
+        r.out = c->moe_probs;
+        r.out_stride = ne;
+        r.row1 = ne;
+        c->xq_src[0] = c->xq_src[1] = NULL;
+        TRY(sdy_matvec_float_norm(L->gate_inp.type, (const uint8_t *)L->gate_inp.m.base + L->gate_inp.m.plane_off[0],
+                                  dim, &r, c->xq[1], c->st));
+    } else {
+        TRY(norm_for(c, c->x, L->ffn_norm, first, 1)); /* xb and its Q8_K row */
+        TRY(mm(c, c->moe_probs, c->xb, &L->gate_inp, 1, NULL, NULL, 0));
+    }
     TRY(sdy_moe_route(c->moe_probs, 1, ne, k, c->moe_top, c->moe_w, c->st));
     sdy_mv_args a;
     memset(&a, 0, sizeof a);

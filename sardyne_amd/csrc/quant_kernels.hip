@@ -1342,15 +1342,56 @@ SDY_DEV void float_store(float acc, long row, int t, float *out, long out_stride
     out[(size_t)t * out_stride + row] = acc;
 }
 
+// RMSNorm of a one-token row fused into the float matvec that reads it (NORM): the activation is
+// (x[i] * scale) * nw[i], scale = 1 / sqrt(mean(x^2) + eps) with k_norm_quant's sum order, and workgroup
+// b also writes super-block b of the normalised row's Q8_K bytes (when xq is set) — the bytes
+// k_norm_quant writes.
+struct FloatNorm {
+    const float *nw;
+    float eps;
+    uint8_t *xq;
+};
+
 // dot's order: one (row, token) per 32-lane half-wave. Items: with n_tok >= 4 the paired rows times
 // the tokens past the last group of four, then the unpaired last row times every token; with fewer
 // tokens every (row, token).
-template <int WT>
+template <int WT, bool NORM = false>
 __global__ __launch_bounds__(THREADS) void k_matvec_float_dot(const uint8_t *__restrict__ w, int n_in,
                                                               const float *__restrict__ x, int n_tok, float *out,
                                                               long out_stride, const float *bias, const float *resid,
-                                                              long row0, long row1) {
+                                                              long row0, long row1, FloatNorm fn = {}) {
     const int lane = threadIdx.x & 63, L = lane & 31, base = lane & 32;
+    // NORM: the normalised row in LDS, built by every thread (one token, n_in <= 4096, a multiple of 256)
+    __shared__ __align__(16) float xn[NORM ? 4096 : 4];
+    if constexpr (NORM) {
+        __shared__ double sh[4];
+        const int tid = threadIdx.x, wave = tid >> 6, n4 = n_in >> 2;
+        float4 keep[4], wk[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int c = tid + 256 * k < n4 ? tid + 256 * k : n4 - 1;
+            wk[k] = *reinterpret_cast<const float4 *>(fn.nw + 4 * c);
+        }
+        const double ss = sdy_row_sumsq<4>(x, n_in, keep, sh);  // keep[k]: the thread's chunk tid + 256k
+        const float scale = (float)(1.0 / sqrt(ss / (double)n_in + (double)fn.eps));
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (tid + 256 * k < n4)
+                *reinterpret_cast<float4 *>(&xn[4 * (tid + 256 * k)]) =
+                    make_float4((keep[k].x * scale) * wk[k].x, (keep[k].y * scale) * wk[k].y,
+                                (keep[k].z * scale) * wk[k].z, (keep[k].w * scale) * wk[k].w);
+        __syncthreads();
+        for (int sb = blockIdx.x + wave * gridDim.x; fn.xq && sb < (n_in >> 8); sb += 4 * gridDim.x) {
+            const float4 v = *reinterpret_cast<const float4 *>(&xn[256 * sb + 4 * lane]);
+            const float xs[4] = {v.x, v.y, v.z, v.w};
+            sdy_q8k_block(xs, lane, fn.xq + (size_t)sb * 292);
+        }
+    }
+    // the activation element i (from the normalised row in LDS when NORM)
+    auto xe = [&](const float *xr, int i) {
+        if constexpr (NORM) return xn[i];
+        else return xr[i];
+    };
     const long n_rows = row1 - row0, n_pr = n_tok >= 4 ? (n_rows & ~1L) : 0;
     const int n_gt = n_tok >= 4 ? (n_tok & ~3) : 0;
     const long n_a = n_pr * (n_tok - n_gt), n_items = n_a + (n_rows - n_pr) * n_tok;
@@ -1378,7 +1419,7 @@ __global__ __launch_bounds__(THREADS) void k_matvec_float_dot(const uint8_t *__r
 #pragma unroll
         for (int j = 0; j < B; j++) {
             wv[j] = welem<WT>(wr, i + 32 * j);
-            xv[j] = xr[i + 32 * j];
+            xv[j] = xe(xr, i + 32 * j);
         }
 #pragma unroll
         for (int j = 0; j < B; j++) acc = fmaf(wv[j], xv[j], acc);
@@ -1388,14 +1429,14 @@ __global__ __launch_bounds__(THREADS) void k_matvec_float_dot(const uint8_t *__r
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             wv[j] = welem<WT>(wr, i + 32 * j);
-            xv[j] = xr[i + 32 * j];
+            xv[j] = xe(xr, i + 32 * j);
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) acc = fmaf(wv[j], xv[j], acc);
     }
-    for (; i < n32; i += 32) acc = fmaf(welem<WT>(wr, i), xr[i], acc);
+    for (; i < n32; i += 32) acc = fmaf(welem<WT>(wr, i), xe(xr, i), acc);
     if (L < 8)
-        for (int i = n32 + L; i < n8; i += 8) acc = fmaf(welem<WT>(wr, i), xr[i], acc);
+        for (int i = n32 + L; i < n8; i += 8) acc = fmaf(welem<WT>(wr, i), xe(xr, i), acc);
     // lanes 0..7 of the half: v_l = (a0_l + a1_l) + (a2_l + a3_l)
     const float a1 = __shfl(acc, base + ((L + 8) & 31)), a2 = __shfl(acc, base + ((L + 16) & 31)),
                 a3 = __shfl(acc, base + ((L + 24) & 31));
@@ -2286,6 +2327,31 @@ extern "C" int sdy_matvec_grouped(const sdy_mat *m, const sdy_mv_args *a, const 
     }
     if (m->type == SDY_Q4_K) return mv_grouped<SDY_Q4_K>(m, a, slot_expert, n_slot, slot_rows, xq_slot, out_slot, st);
     return mv_grouped<SDY_Q6_K>(m, a, slot_expert, n_slot, slot_rows, xq_slot, out_slot, st);
+}
+
+extern "C" int sdy_matvec_float_norm(int wtype, const void *w, int n_in, const sdy_mv_args *a, void *xq_out,
+                                     sdy_stream s) {
+    hipStream_t st = (hipStream_t)s;
+    const long n_rows = a->row1 - a->row0;
+    if (wtype != SDY_F32 && wtype != SDY_F16 && wtype != SDY_BF16) return sdy_fail(-1, "float matvec: type %d", wtype);
+    if (a->n_tok != 1 || !a->x || !a->nw || n_in % 256 || n_in > 4096 || ((uintptr_t)a->x & 15) ||
+        ((uintptr_t)a->nw & 15))
+        return sdy_fail(-1, "float matvec with RMSNorm: one token, rows of 256..4096 elements (multiples of 256), "
+                            "16-byte aligned x and norm weights");
+    if (n_rows <= 0) return 0;
+    const dim3 grid((unsigned)((n_rows + 2 * WAVES - 1) / (2 * WAVES)));
+    const FloatNorm fn = {a->nw, a->eps, (uint8_t *)xq_out};
+    const uint8_t *wp = (const uint8_t *)w;
+    if (wtype == SDY_F32)
+        hipLaunchKernelGGL((k_matvec_float_dot<SDY_F32, true>), grid, dim3(THREADS), 0, st, wp, n_in, a->x, 1, a->out,
+                           a->out_stride, a->bias, a->resid, a->row0, a->row1, fn);
+    else if (wtype == SDY_F16)
+        hipLaunchKernelGGL((k_matvec_float_dot<SDY_F16, true>), grid, dim3(THREADS), 0, st, wp, n_in, a->x, 1, a->out,
+                           a->out_stride, a->bias, a->resid, a->row0, a->row1, fn);
+    else
+        hipLaunchKernelGGL((k_matvec_float_dot<SDY_BF16, true>), grid, dim3(THREADS), 0, st, wp, n_in, a->x, 1, a->out,
+                           a->out_stride, a->bias, a->resid, a->row0, a->row1, fn);
+    return sdy_check_launch("matvec_float_norm");
 }
 
 extern "C" int sdy_matvec_float(int wtype, const void *w, int n_in, const sdy_mv_args *a, sdy_stream s) {

@@ -134,6 +134,10 @@ int sdy_gemm_check_rows(const sdy_mat *m, long r0, long n, int *bad_host, sdy_st
 
 /* raw float-weight matrices (F32/F16/BF16, GGUF row-major layout kept as is) */
 int sdy_matvec_float(int wtype, const void *w, int n_in, const sdy_mv_args *a, sdy_stream s);
+/* The same for one token of the RMS-normalised row (x / rms(x) * a->nw, with a->eps): the bits of
+ * sdy_norm_quant's f32 row followed by sdy_matvec_float; with xq_out, also that row's Q8_K bytes (the
+ * ones sdy_norm_quant writes). n_in a multiple of 256, at most 4096; x and nw 16-byte aligned. */
+int sdy_matvec_float_norm(int wtype, const void *w, int n_in, const sdy_mv_args *a, void *xq_out, sdy_stream s);
 
 #ifdef __cplusplus
 }

@@ -670,6 +670,38 @@ def test_grouped_matvec_fused_activation(kind, n_in, e_rows, mode):
     assert np.array_equal(bits(res[1]), bits(res[0]))
 
 
+FLOAT_TYPES = {"F32": (0, np.float32), "F16": (1, np.float16), "BF16": (30, None)}
+
+
+@pytest.mark.parametrize("wname,n_in,n_rows", [("F32", 2048, 128), ("F16", 1024, 64), ("BF16", 4096, 17),
+                                               ("F32", 256, 3)])
+def test_matvec_float_norm(wname, n_in, n_rows):
+    """The float matvec of the RMS-normalised row (the MoE router reading the FFN norm's output):
+    the bits of sdy_norm_quant's f32 row followed by sdy_matvec_float, and the Q8_K bytes
+    sdy_norm_quant writes."""
+    L = lib()
+    wt, dt = FLOAT_TYPES[wname]
+    rng = np.random.default_rng(n_in + n_rows)
+    w32 = rng.standard_normal((n_rows, n_in)).astype(np.float32)
+    w = w32.astype(dt) if dt else (w32.view(np.uint32) >> 16).astype(np.uint16)
+    x = (2.0 * rng.standard_normal(n_in)).astype(np.float32)
+    nw = (1.0 + 0.3 * rng.standard_normal(n_in)).astype(np.float32)
+    eps = 1e-6
+    dw, dx, dnw = capi.DeviceBuffer.from_array(w), capi.DeviceBuffer.from_array(x), capi.DeviceBuffer.from_array(nw)
+    xrow = n_in // 256 * 292
+    # separate path: norm_quant (f32 row and Q8_K), then the float matvec of the f32 row
+    dxb, dq = capi.DeviceBuffer(n_in * 4), capi.DeviceBuffer(xrow)
+    capi.check(L.sdy_norm_quant(dx.ptr, dnw.ptr, eps, n_in, 1, dxb.ptr, Q8K_TYPE, dq.ptr, None))
+    d1 = capi.DeviceBuffer(n_rows * 4)
+    a = capi.SdyMvArgs(x=dxb.ptr, n_tok=1, out=d1.ptr, out_stride=n_rows, row0=0, row1=n_rows)
+    capi.check(L.sdy_matvec_float(wt, dw.ptr, n_in, ctypes.byref(a), None))
+    d2, dq2 = capi.DeviceBuffer(n_rows * 4), capi.DeviceBuffer(xrow)
+    a2 = capi.SdyMvArgs(x=dx.ptr, nw=dnw.ptr, eps=eps, n_tok=1, out=d2.ptr, out_stride=n_rows, row0=0, row1=n_rows)
+    capi.check(L.sdy_matvec_float_norm(wt, dw.ptr, n_in, ctypes.byref(a2), dq2.ptr, None))
+    assert np.array_equal(bits(d2.to_array(np.float32, n_rows)), bits(d1.to_array(np.float32, n_rows)))
+    assert np.array_equal(dq2.to_array(np.uint8, xrow), dq.to_array(np.uint8, xrow))
+
+
 def test_grouped_matvec_rejects_bad_shapes():
     L = lib()
     w = random_blocks("Q4_K", 4 * 10 * 2048 // 256, np.random.default_rng(0)).reshape(40, -1)
