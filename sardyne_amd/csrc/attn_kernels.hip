@@ -390,6 +390,43 @@ __global__ __launch_bounds__(256) void k_attn_decode_softmax(AttnArgs a) {
     __shared__ double red_s[4];
     const int tid = threadIdx.x, wave = tid >> 6, n = a.step[1] + 1;
     float *row = a.scores + (size_t)blockIdx.x * a.max_kv;
+    constexpr int KR = 8;  // up to 256 KR positions: each thread's scores stay in registers
+    if (n <= 256 * KR) {
+        // one read of the row, one exponential per score, one write: the same values and order as
+        // the three passes below
+        const uint32_t etab = sdy_expf_tab_lane(tid & 63);
+        float v[KR];
+#pragma unroll
+        for (int k = 0; k < KR; k++) {
+            const int j = tid + 256 * k;
+            v[k] = row[j < n ? j : n - 1];
+        }
+        float m = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < KR; k++)
+            if (tid + 256 * k < n) m = fmaxf(m, v[k]);
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if ((tid & 63) == 0) red_m[wave] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+        double sum = 0.0;
+#pragma unroll
+        for (int k = 0; k < KR; k++) {
+            v[k] = sdy_expf_reg(v[k] - m, etab);  // every lane (the table lookup reads other lanes)
+            if (tid + 256 * k < n) sum += (double)v[k];
+        }
+        for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+        if ((tid & 63) == 0) red_s[wave] = sum;
+        __syncthreads();
+        sum = (red_s[0] + red_s[1]) + (red_s[2] + red_s[3]);
+        const float inv = (float)(1.0 / sum);
+#pragma unroll
+        for (int k = 0; k < KR; k++) {
+            const int j = tid + 256 * k;
+            if (j < n) row[j] = v[k] * inv;
+        }
+        return;
+    }
     float m = row_max(row, tid, 256, n);
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     if ((tid & 63) == 0) red_m[wave] = m;
