@@ -213,6 +213,85 @@ SDY_DEV float dot_avx2_order(const float *q, const float *k) {
     return s;
 }
 
+// Decode q/k preparation with every input loaded at once (HD a multiple of 128, pairs (i, i + HD/2)):
+// lane l of a wave holds elements l + 64 e of a vector, so a RoPE pair sits in one lane and the
+// norm's sum has norm_rope_wave's per-lane order (elements l, l + 64, ...) and tree; the results go
+// to LDS (qs, kp) and, for the new k, to the KV cache. Returns false (nothing done) for other
+// shapes, which take norm_rope_wave.
+template <int HD>
+SDY_DEV bool decode_prep_regs(const AttnArgs &a, int g, int n_rep, int pos, bool has_pos, const float *cs,
+                              const float *sn, float *qs, float *kp, int wave, int lane) {
+    constexpr int E = HD / 64, EH = E / 2, RM = 4;  // elements per lane; vectors per wave
+    if constexpr (HD % 128 != 0) {
+        return false;
+    } else {
+        if (a.interleaved || n_rep + 1 > 4 * RM) return false;
+        float x[RM][E], qn[E], kn[E], vv[E], c[EH], sv[EH];
+        // every load first: the wave's vectors, the norm weights, cos/sin, the new v
+#pragma unroll
+        for (int i = 0; i < RM; i++) {
+            const int r = wave + 4 * i;
+            if (r <= n_rep) {
+                const float *src = r == n_rep ? a.k + (size_t)g * HD : a.q + (size_t)(g * n_rep + r) * HD;
+#pragma unroll
+                for (int e = 0; e < E; e++) x[i][e] = src[lane + 64 * e];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            qn[e] = a.q_norm ? a.q_norm[lane + 64 * e] : 1.0f;
+            kn[e] = a.k_norm ? a.k_norm[lane + 64 * e] : 1.0f;
+            vv[e] = a.v[(size_t)g * HD + lane + 64 * e];
+        }
+#pragma unroll
+        for (int e = 0; e < EH; e++) {
+            c[e] = cs[lane + 64 * e];
+            sv[e] = sn[lane + 64 * e];
+        }
+#pragma unroll
+        for (int i = 0; i < RM; i++) {
+            const int r = wave + 4 * i;
+            if (r > n_rep) break;
+            const bool is_k = r == n_rep;
+            float y[E];
+#pragma unroll
+            for (int e = 0; e < E; e++) y[e] = x[i][e];
+            if (is_k ? a.k_norm != nullptr : a.q_norm != nullptr) {
+                double ss = 0.0;
+#pragma unroll
+                for (int e = 0; e < E; e++) ss += (double)y[e] * (double)y[e];
+                for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+                const float sc = (float)(1.0 / sqrt(ss / (double)HD + (double)a.eps));
+#pragma unroll
+                for (int e = 0; e < E; e++) {
+                    const float tt = y[e] * sc;
+                    y[e] = tt * (is_k ? kn[e] : qn[e]);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < EH; e++) {  // the pair (l + 64 e, l + 64 e + HD/2)
+                const float av = y[e], bv = y[e + EH];
+                const float ac = av * c[e], bs = bv * sv[e], as = av * sv[e], bc = bv * c[e];
+                y[e] = ac - bs;
+                y[e + EH] = as + bc;
+            }
+            float *buf = is_k ? kp : qs + r * HD;
+#pragma unroll
+            for (int e = 0; e < E; e++) buf[lane + 64 * e] = y[e];
+            if (is_k && has_pos) {  // KV-cache write of the new position
+                float *kc = a.k_cache + g * a.head_stride + (size_t)pos * HD;
+                float *vc = a.v_cache + g * a.head_stride + (size_t)pos * HD;
+#pragma unroll
+                for (int e = 0; e < E; e++) {
+                    kc[lane + 64 * e] = y[e];
+                    vc[lane + 64 * e] = vv[e];
+                }
+            }
+        }
+        return true;
+    }
+}
+
 // Grid (n_chunk, n_kv_head, token blocks), 256 threads. Prefill: the block's tokens are
 // PAIRS / n_rep consecutive tokens (queries already rotated, K/V already in the cache). Decode: one
 // token at position step[1]; every workgroup normalises and rotates the group's queries and the
@@ -257,10 +336,11 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
     const int n_pairs = (t1 - t0) * n_rep;
     bool has_pos = false;
     if constexpr (DECODE) {
-        // q heads of the group and the new k: norm + RoPE in LDS (one wave per vector)
+        // q heads of the group and the new k: norm + RoPE (one wave per vector)
         has_pos = p0 + np_max == pos + 1;
         const float *cs = a.rope_cos + (size_t)pos * (HD / 2), *sn = a.rope_sin + (size_t)pos * (HD / 2);
-        for (int r = wave; r <= n_rep; r += 4) {
+        const bool done = decode_prep_regs<HD>(a, g, n_rep, pos, has_pos, cs, sn, qs, kp, wave, lane);
+        for (int r = wave; !done && r <= n_rep; r += 4) {
             const bool is_k = r == n_rep;
             float *buf = is_k ? kp : qs + r * HD;
             const float *src = is_k ? a.k + (size_t)g * HD : a.q + (size_t)(g * n_rep + r) * HD;
