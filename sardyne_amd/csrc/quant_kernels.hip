@@ -376,7 +376,7 @@ struct WRegs {
     uint32_t f, g;
 };
 
-// Loads one unit of a K-quant row given its unit index iu = row * T + u and super-block index
+// Loads one unit of a row given its unit index iu = row * T + u and (K-quants) super-block index
 // is = row * nb + u / 4 in the planes.
 template <int WT>
 SDY_DEV void load_w_at(const Planes &P, uint32_t iu, uint32_t is, uint32_t u, WRegs<WT> &r) {
@@ -385,13 +385,27 @@ SDY_DEV void load_w_at(const Planes &P, uint32_t iu, uint32_t is, uint32_t u, WR
         r.a = ldw16(P.p[0] + ou);
         r.b = ldw16(P.p[1] + ou);
         r.c = ldw16(P.p[2] + is * 16u);
-    } else {
-        static_assert(WT == SDY_Q6_K, "K-quants only");
+    } else if constexpr (WT == SDY_Q6_K) {
         r.a = ldw16(P.p[0] + ou);
         r.b = ldw16(P.p[1] + ou);
         r.c = ldw16(P.p[2] + ou);
         r.f = ldw4(P.p[3] + is * 16u + 4u * (u & 3u));
         r.g = ldw2(P.p[4] + is * 2u);
+    } else if constexpr (WT == SDY_Q8_0) {  // (is unused)
+        r.a = ldw16(P.p[0] + ou);
+        r.b = ldw16(P.p[1] + ou);
+        r.c = ldw16(P.p[2] + ou);
+        r.e = ldw16(P.p[3] + ou);
+        r.f = ldw4(P.p[4] + iu * 4u);
+    } else {
+        r.a = ldw16(P.p[0] + ou);
+        r.b = ldw16(P.p[1] + ou);
+        r.f = ldw4(P.p[4] + iu * 4u);
+        if constexpr (WT == SDY_Q5_0) {
+            const uint8_t *q = P.p[2] + iu * 8u;
+            r.c.x = ldw4(q);
+            r.c.y = ldw4(q + 4);
+        }
     }
 }
 
@@ -1119,8 +1133,10 @@ __global__ __launch_bounds__(THREADS) void k_matvec_1t_pair(MvArgs a, MvArgs b, 
     else matvec_1t_body<WT2, 1, NSB, PRO>(b, (int)gridDim.x - g1, (int)blockIdx.x - g1, 0);
 }
 
-// One token, K-quants with at most 64 units per row, when the rows are too many for k_matvec_1t
-// (the output head): a grid the GPU holds at once, wave w of S taking iterations w, w + S, ...
+// One token, rows of at most 64 units: K-quants when the rows are too many for k_matvec_1t (the
+// output head), and the 32-element types (whose activation row is staged in LDS, as in
+// k_matvec_rl, and whose unit terms are summed by k_matvec_rl's butterfly): a grid the GPU holds at
+// once, wave w of S taking iterations w, w + S, ...
 // (64/T rows each) with NB iterations' weights in flight in a ring of registers. Every load is
 // unconditional (rows past the end read row0), so the code is straight-line per round of NB
 // iterations and the compiler's wait before each iteration's computation covers only that
@@ -1128,6 +1144,7 @@ __global__ __launch_bounds__(THREADS) void k_matvec_1t_pair(MvArgs a, MvArgs b, 
 // arithmetic as k_matvec_1t (the same bits); no SwiGLU epilogue.
 template <int WT, int NB, int NSB>
 __global__ __launch_bounds__(THREADS) void k_matvec_ring(MvArgs a) {
+    extern __shared__ uint8_t lds[];
     const int T = a.P.T;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int rpi = a.rpi;
@@ -1137,6 +1154,10 @@ __global__ __launch_bounds__(THREADS) void k_matvec_ring(MvArgs a) {
     const int G = (int)gridDim.x, bx = (int)blockIdx.x;
     const int vblk = (G & 7) == 0 ? (bx & 7) * (G >> 3) + (bx >> 3) : bx;  // XCD-aware renumbering
     const int S = G * WAVES, wid = vblk * WAVES + wave;
+    if constexpr (!is_k(WT)) {  // the 32-element types' activation row in LDS (every thread)
+        stage_acts<WT, 1>(a, lds);
+        __syncthreads();
+    }
     if (wid >= a.n_it) return;
     const int n_my = (a.n_it - wid + S - 1) / S;  // this wave's iterations
     const uint32_t le = lane_on ? lane : u, nb = a.P.nb, r0 = (uint32_t)a.row0;
@@ -1151,13 +1172,36 @@ __global__ __launch_bounds__(THREADS) void k_matvec_ring(MvArgs a) {
     };
     load_i(0, 0);
     uint4 Yr[4];
-    const uint8_t *blk = a.xq + __mul24(u >> 2, 292);
-    const uint8_t *yb = blk + 4 + 64 * (u & 3);
+    uint2 bsr = make_uint2(0u, 0u);
+    float ydr = 0.0f;
+    float2 dxr = make_float2(0.f, 0.f);
+    int2 syr = make_int2(0, 0);
+    if constexpr (is_k(WT)) {
+        const uint8_t *blk = a.xq + __mul24(u >> 2, 292);
+        const uint8_t *yb = blk + 4 + 64 * (u & 3);
 #pragma unroll
-    for (int q = 0; q < 4; q++)
-        Yr[q] = make_uint4(ld4(yb + 16 * q), ld4(yb + 16 * q + 4), ld4(yb + 16 * q + 8), ld4(yb + 16 * q + 12));
-    const uint2 bsr = make_uint2(ld4(blk + 260 + 8 * (u & 3)), ld4(blk + 264 + 8 * (u & 3)));
-    const float ydr = *reinterpret_cast<const float *>(blk);
+        for (int q = 0; q < 4; q++)
+            Yr[q] = make_uint4(ld4(yb + 16 * q), ld4(yb + 16 * q + 4), ld4(yb + 16 * q + 8), ld4(yb + 16 * q + 12));
+        bsr = make_uint2(ld4(blk + 260 + 8 * (u & 3)), ld4(blk + 264 + 8 * (u & 3)));
+        ydr = *reinterpret_cast<const float *>(blk);
+    } else {  // k_matvec_rl's LDS layout (stage_acts)
+#pragma unroll
+        for (int q = 0; q < 4; q++) Yr[q] = *reinterpret_cast<const uint4 *>(lds + (q * T + u) * 16);
+        dxr = *reinterpret_cast<const float2 *>(lds + 4 * T * 16 + u * 8);
+        syr = *reinterpret_cast<const int2 *>(lds + 4 * T * 16 + T * 8 + u * 8);
+    }
+    // the iteration's row sum (K-quants: the in-order super-block fold; else the butterfly over T)
+    auto row_sum = [&](const WRegs<WT> &cur) -> float {
+        if constexpr (is_k(WT)) {
+            return rl_row_sum<WT, NSB>(cur, Yr, bsr, ydr, u, lane, T);
+        } else {
+            int isum, msum;
+            float acc = 0.0f;
+            unit_dot<WT>(cur, Yr, bsr, u, isum, msum, acc, dxr, syr);
+            for (int off = 1; off < T; off <<= 1) acc = acc + __shfl_xor(acc, off);
+            return acc;
+        }
+    };
 #pragma unroll
     for (int t = 1; t < NB; t++) load_i(t, t);
     auto finish = [&](float acc, int i) {  // (no SwiGLU epilogue here)
@@ -1173,7 +1217,7 @@ __global__ __launch_bounds__(THREADS) void k_matvec_ring(MvArgs a) {
     for (; i0 + NB <= n_my; i0 += NB) {
 #pragma unroll
         for (int t = 0; t < NB; t++) {
-            const float acc = rl_row_sum<WT, NSB>(R[t], Yr, bsr, ydr, u, lane, T);
+            const float acc = row_sum(R[t]);
             // an opaque zero that depends on acc: the refill of slot t cannot be issued before the
             // slot's registers are read
             int z;
@@ -1184,7 +1228,7 @@ __global__ __launch_bounds__(THREADS) void k_matvec_ring(MvArgs a) {
     }
 #pragma unroll
     for (int t = 0; t < NB; t++)  // the last n_my - i0 < NB iterations, already in flight
-        if (i0 + t < n_my) finish(rl_row_sum<WT, NSB>(R[t], Yr, bsr, ydr, u, lane, T), i0 + t);
+        if (i0 + t < n_my) finish(row_sum(R[t]), i0 + t);
 }
 
 // Long rows, one token (K-quants with T > 64 units, e.g. n_in = 11008 with 172 units): a wave owns
@@ -1878,11 +1922,12 @@ template <int WT, int NB, int NSB>
 static int launch_mv_ring_nsb(MvArgs &A, hipStream_t st) {
     static int per_cu = 0;
     static size_t per_cu_lds = 0;
+    const size_t lds = is_k(WT) ? 0 : mv_lds_bytes_rl(A.P.T, 1);
     long wgs = ((long)A.n_it + WAVES - 1) / WAVES;
-    const long cap = resident_wgs((const void *)k_matvec_ring<WT, NB, NSB>, 0, per_cu, per_cu_lds);
+    const long cap = resident_wgs((const void *)k_matvec_ring<WT, NB, NSB>, lds, per_cu, per_cu_lds);
     if (wgs > cap) wgs = cap;
     if (wgs > 8) wgs &= ~7L;  // a multiple of 8: the XCD-aware numbering applies
-    hipLaunchKernelGGL((k_matvec_ring<WT, NB, NSB>), dim3((unsigned)wgs), dim3(THREADS), 0, st, A);
+    hipLaunchKernelGGL((k_matvec_ring<WT, NB, NSB>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
     return sdy_check_launch("matvec");
 }
 
@@ -1890,7 +1935,7 @@ static int launch_mv_ring_nsb(MvArgs &A, hipStream_t st) {
 // the 151936 x 2048 output head: Q6_K 3, Q4_K 2)
 template <int WT>
 static int launch_mv_ring(MvArgs &A, hipStream_t st) {
-    constexpr int NB = WT == SDY_Q6_K ? 3 : 2;
+    constexpr int NB = WT == SDY_Q6_K || WT == SDY_Q8_0 ? 3 : 2;
     prep_1t(A);
     switch (A.P.T) {
     case 32: return launch_mv_ring_nsb<WT, NB, 8>(A, st);
@@ -1905,6 +1950,8 @@ static int launch_mv_rl(MvArgs &A, size_t lds, hipStream_t st, int n_slot = 1) {
         const int rc = launch_mv_1t<WT>(A, st, n_slot);
         if (rc <= 0) return rc;
         if (n_slot == 1 && !A.px && !A.swiglu) return launch_mv_ring<WT>(A, st);
+    } else if constexpr (MT == 1 && YREG) {
+        if (n_slot == 1 && !A.swiglu && 64 % A.P.T == 0) return launch_mv_ring<WT>(A, st);
     }
     static int per_cu = 0;
     static size_t per_cu_lds = 0;
