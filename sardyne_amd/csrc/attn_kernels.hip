@@ -17,6 +17,8 @@
 //                                 normalises and rotates q and the new k and writes the new K/V
 //   k_attn_softmax_pv<HD, DECODE> softmax and weighted V of 256 / HD heads of one token (the decode
 //                                 variant also quantises the 256 outputs to a Q8_K block)
+//   k_attn_prefill_pv<HD, TB>     the same for TB tokens at a time (prefill: each V element read once
+//                                 for the TB tokens' chains)
 //   k_attn_*_any                  the same for other head dims (runtime loops, scalar LDS reads)
 #include "sdy_device.h"
 #include "sdy_expf.h"
@@ -462,6 +464,100 @@ __global__ __launch_bounds__(256) void k_attn_softmax_pv(AttnArgs a) {
     }
 }
 
+// Prefill softmax and weighted V of 256 / HD heads for TB consecutive tokens per workgroup: the
+// arithmetic of k_attn_softmax_pv for each (token, head) (same maxima, double sums, weights and one
+// in-order FMA chain per output), but each V element is read once for the TB tokens, whose chains
+// advance together position by position (TB independent chains per thread). Tokens past n_tok
+// repeat the last one and store nothing.
+template <int HD, int TB>
+__global__ __launch_bounds__(256) void k_attn_prefill_pv(AttnArgs a) {
+    constexpr int HPB = 256 / HD, GW = HD < 64 ? HD : 64, NW = HD > 64 ? HD / 64 : 1;
+    constexpr int PB = PW / (HPB * TB);  // weights per (token, head) per pass
+    static_assert(HD * HPB == 256 && PB % 4 == 0, "head_dim divides 256");
+    __shared__ __align__(16) float pw[TB][HPB][PB];
+    __shared__ float redf[4][TB];
+    __shared__ double redd[4][TB];
+    const int tid = threadIdx.x, hl = tid / HD, d = tid - hl * HD, wave = tid >> 6;
+    const int t0 = blockIdx.y * TB;
+    const int h_raw = blockIdx.x * HPB + hl, h = h_raw < a.n_head ? h_raw : a.n_head - 1;
+    const int n_rep = a.n_head / a.n_kv_head, g = h / n_rep;
+    int nt[TB];
+    const float *rows[TB];
+#pragma unroll
+    for (int ti = 0; ti < TB; ti++) {
+        const int t = t0 + ti < a.n_tok ? t0 + ti : a.n_tok - 1;
+        nt[ti] = a.n_kv0 + t;
+        rows[ti] = a.scores + ((size_t)t * a.n_head + h) * a.max_kv;
+    }
+    float m[TB], inv[TB];
+#pragma unroll
+    for (int ti = 0; ti < TB; ti++) {
+        float mm = row_max(rows[ti], d, HD, nt[ti]);
+        for (int off = GW / 2; off >= 1; off >>= 1) mm = fmaxf(mm, __shfl_xor(mm, off));
+        m[ti] = mm;
+        if (HD > 64 && (tid & 63) == 0) redf[wave][ti] = mm;
+    }
+    if constexpr (HD > 64) {
+        __syncthreads();
+#pragma unroll
+        for (int ti = 0; ti < TB; ti++) {
+            float mm = -INFINITY;
+            for (int w = 0; w < NW; w++) mm = fmaxf(mm, redf[hl * NW + w][ti]);
+            m[ti] = mm;
+        }
+    }
+#pragma unroll
+    for (int ti = 0; ti < TB; ti++) {
+        double sum = row_expsum(rows[ti], d, HD, nt[ti], m[ti]);
+        for (int off = GW / 2; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+        if (HD > 64 && (tid & 63) == 0) redd[wave][ti] = sum;
+        inv[ti] = (float)(1.0 / sum);
+    }
+    if constexpr (HD > 64) {
+        __syncthreads();
+#pragma unroll
+        for (int ti = 0; ti < TB; ti++) {
+            double sum = 0.0;
+            for (int w = 0; w < NW; w++) sum += redd[hl * NW + w][ti];
+            inv[ti] = (float)(1.0 / sum);
+        }
+    }
+    const float *vg = a.v_cache + g * a.head_stride + d;
+    float acc[TB];
+#pragma unroll
+    for (int ti = 0; ti < TB; ti++) acc[ti] = 0.0f;
+    const int n_lo = nt[0], n_hi = nt[TB - 1];  // positions of the first and the last token
+    for (int jb = 0; jb < n_hi; jb += PB) {
+        __syncthreads();
+#pragma unroll
+        for (int ti = 0; ti < TB; ti++) {
+            const int je = jb + PB < nt[ti] ? jb + PB : nt[ti];
+            row_weights(rows[ti], jb + d, HD, je, m[ti], inv[ti], pw[ti][hl], jb, 1);
+        }
+        __syncthreads();
+        const int je_all = jb + PB < n_lo ? jb + PB : n_lo, je_any = jb + PB < n_hi ? jb + PB : n_hi;
+        int j = jb;
+        for (; j + 8 <= je_all; j += 8) {  // positions every token of the block sees
+            float vv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) vv[u] = vg[(size_t)(j + u) * HD];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+#pragma unroll
+                for (int ti = 0; ti < TB; ti++) acc[ti] = fmaf(pw[ti][hl][j + u - jb], vv[u], acc[ti]);
+        }
+        for (; j < je_any; j++) {
+            const float v = vg[(size_t)j * HD];
+#pragma unroll
+            for (int ti = 0; ti < TB; ti++)
+                if (j < nt[ti]) acc[ti] = fmaf(pw[ti][hl][j - jb], v, acc[ti]);
+        }
+    }
+#pragma unroll
+    for (int ti = 0; ti < TB; ti++)
+        if (h_raw < a.n_head && t0 + ti < a.n_tok) a.out[(size_t)(t0 + ti) * a.out_stride + (size_t)h * HD + d] = acc[ti];
+}
+
 // Decode softmax in place: one workgroup of 256 threads per query head turns the head's scores s_j
 // (j = 0..pos) into p_j = expf(s_j - m) * inv, m the maximum and inv = (float)(1 / sum expf(s_j - m))
 // with the sum in double. Each thread reads and rewrites only its own entries (j = tid mod 256).
@@ -856,8 +952,13 @@ static int launch_attn(AttnArgs &A, int nc, int n_tblk, hipStream_t st) {
     if (rc) return rc;
     hipLaunchKernelGGL((k_attn_scores<HD, DECODE>), dim3(nc, A.n_kv_head, n_tblk), dim3(256), lds, st, A);
     if ((rc = sdy_check_launch("attention_scores"))) return rc;
-    hipLaunchKernelGGL((k_attn_softmax_pv<HD, DECODE>), dim3((A.n_head * HD + 255) / 256, DECODE ? 1 : A.n_tok), dim3(256),
-                       0, st, A);
+    if constexpr (DECODE) {
+        hipLaunchKernelGGL((k_attn_softmax_pv<HD, DECODE>), dim3((A.n_head * HD + 255) / 256, 1), dim3(256), 0, st, A);
+    } else {  // four tokens per workgroup
+        constexpr int TB = 4;
+        hipLaunchKernelGGL((k_attn_prefill_pv<HD, TB>), dim3((A.n_head * HD + 255) / 256, (A.n_tok + TB - 1) / TB),
+                           dim3(256), 0, st, A);
+    }
     return sdy_check_launch("attention_softmax_pv");
 }
 
