@@ -16,85 +16,32 @@ struct SdyQ8kLane {
     float d;
 };
 
-SDY_DEV SdyQ8kLane sdy_q8k_lane(const float xs[4], int lane) {
-    float best = 0.0f, bval = 0.0f;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int e = 0; e < 4; e++)
-        if (fabsf(xs[e]) > best) {
-            best = fabsf(xs[e]);
-            bval = xs[e];
-            bi = 4 * lane + e;
-        }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        float ob_ = __shfl_xor(best, off), ov = __shfl_xor(bval, off);
-        int oi = __shfl_xor(bi, off);
-        if (ob_ > best || (ob_ == best && oi < bi)) {
-            best = ob_;
-            bval = ov;
-            bi = oi;
-        }
-    }
-    SdyQ8kLane r;
-    if (best == 0.0f) {
-        r.packed = 0u;
-        r.gsum = 0;
-        r.d = 0.0f;
-        return r;
-    }
-    const float iscale = -127.0f / bval;
-    uint32_t packed = 0;
-    int lsum = 0;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        int q = sdy_nearest_int(iscale * xs[e]);
-        q = q < 127 ? q : 127;
-        lsum += (int8_t)q;
-        packed |= (uint32_t)(uint8_t)(int8_t)q << (8 * e);
-    }
-    r.packed = packed;
-    r.gsum = sdy_quad_sum(lsum);
-    r.d = 1.0f / iscale;
-    return r;
-}
-
-// NB blocks at once (the same result per block as sdy_q8k_lane); their cross-lane reductions are
-// interleaved so that the latencies overlap.
+// NB blocks at once (each the same result as one block alone). The signed maximum: the magnitude is
+// reduced over the wave in any order (a maximum is order-free), then the first lane holding it (a
+// ballot) and that lane's first element of that magnitude give the element: the first one in index
+// order, as the reference's strict '>' picks. NaN never wins (fmaxf drops it; a block with no
+// finite nonzero element is all zero bytes, as in the reference).
 template <int NB>
 SDY_DEV void sdy_q8k_lanes(const float (&xs)[NB][4], int lane, SdyQ8kLane (&r)[NB]) {
-    float best[NB], bval[NB];
-    int bi[NB];
+    float lm[NB], amax[NB], bval[NB];
 #pragma unroll
     for (int b = 0; b < NB; b++) {
-        best[b] = 0.0f;
-        bval[b] = 0.0f;
-        bi[b] = 0x7fffffff;
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            if (fabsf(xs[b][e]) > best[b]) {
-                best[b] = fabsf(xs[b][e]);
-                bval[b] = xs[b][e];
-                bi[b] = 4 * lane + e;
-            }
+        lm[b] = fmaxf(fmaxf(fabsf(xs[b][0]), fabsf(xs[b][1])), fmaxf(fabsf(xs[b][2]), fabsf(xs[b][3])));
+        amax[b] = lm[b];
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        float ob_[NB], ov[NB];
-        int oi[NB];
+    for (int off = 32; off >= 1; off >>= 1)
 #pragma unroll
-        for (int b = 0; b < NB; b++) {
-            ob_[b] = __shfl_xor(best[b], off);
-            ov[b] = __shfl_xor(bval[b], off);
-            oi[b] = __shfl_xor(bi[b], off);
-        }
+        for (int b = 0; b < NB; b++) amax[b] = fmaxf(amax[b], __shfl_xor(amax[b], off));
 #pragma unroll
-        for (int b = 0; b < NB; b++)
-            if (ob_[b] > best[b] || (ob_[b] == best[b] && oi[b] < bi[b])) {
-                best[b] = ob_[b];
-                bval[b] = ov[b];
-                bi[b] = oi[b];
-            }
+    for (int b = 0; b < NB; b++) {
+        const unsigned long long holders = __ballot(lm[b] == amax[b]);
+        const int first = holders ? __builtin_ctzll(holders) : 0;
+        const float mine = fabsf(xs[b][0]) == amax[b]   ? xs[b][0]
+                           : fabsf(xs[b][1]) == amax[b] ? xs[b][1]
+                           : fabsf(xs[b][2]) == amax[b] ? xs[b][2]
+                                                        : xs[b][3];
+        bval[b] = __shfl(mine, first);
     }
     int lsum[NB];
 #pragma unroll
@@ -102,7 +49,7 @@ SDY_DEV void sdy_q8k_lanes(const float (&xs)[NB][4], int lane, SdyQ8kLane (&r)[N
         lsum[b] = 0;
         r[b].packed = 0u;
         r[b].d = 0.0f;
-        if (best[b] != 0.0f) {
+        if (amax[b] > 0.0f) {
             const float iscale = -127.0f / bval[b];
             uint32_t packed = 0;
 #pragma unroll
@@ -118,6 +65,13 @@ SDY_DEV void sdy_q8k_lanes(const float (&xs)[NB][4], int lane, SdyQ8kLane (&r)[N
     }
 #pragma unroll
     for (int b = 0; b < NB; b++) r[b].gsum = sdy_quad_sum(lsum[b]);
+}
+
+SDY_DEV SdyQ8kLane sdy_q8k_lane(const float xs[4], int lane) {
+    float x1[1][4] = {{xs[0], xs[1], xs[2], xs[3]}};
+    SdyQ8kLane r[1];
+    sdy_q8k_lanes<1>(x1, lane, r);
+    return r[0];
 }
 
 // The block in the reference layout (292 bytes at ob: f32 d, int8 qs[256], int16 bsums[16]).
