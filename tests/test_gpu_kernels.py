@@ -835,6 +835,58 @@ def test_prefill_attention_tokens_bit_identical(n_head, n_kv_head, hd, n_tok, n_
             np.testing.assert_allclose(got[t, h * hd:(h + 1) * hd], exp, rtol=1e-4, atol=1e-5)
 
 
+@pytest.mark.parametrize("n_head,n_kv_head,hd,qk_norm", [(16, 2, 128, False), (32, 4, 128, True), (6, 2, 64, False)])
+@pytest.mark.parametrize("pos", [0, 15, 16, 1000, 2047, 2048, 2110])
+def test_decode_attention_long_context(n_head, n_kv_head, hd, qk_norm, pos):
+    """One-token decode attention through sdy_attn_decode (q/k RMSNorm, RoPE, the KV write, scores,
+    softmax, weighted V and the output's Q8_K row) at positions up to the last slot of a 2111-position
+    cache: past the 2048 positions whose softmax stays in registers, and over a cache whose size is not
+    a multiple of 16 or 64. The output, the written cache rows and the Q8_K bytes have the bits of the
+    oracle's decode step (orc_model.c: norm, rope, cache write, orc_attention over pos + 1 positions)."""
+    L = lib()
+    max_seq, eps, half = 2111, 1e-6, hd // 2
+    assert L.sdy_attn_decode_ok(n_head, n_kv_head, hd, max_seq)
+    rng = np.random.default_rng(pos * 7 + n_head)
+    cs, sn = np.empty(max_seq * half, np.float32), np.empty(max_seq * half, np.float32)
+    O.lib().orc_rope_table(ptr(cs), ptr(sn), max_seq, hd, 1e6)
+    q = rng.standard_normal(n_head * hd).astype(np.float32)
+    k = rng.standard_normal(n_kv_head * hd).astype(np.float32)
+    v = rng.standard_normal(n_kv_head * hd).astype(np.float32)
+    kc = rng.standard_normal((n_kv_head, max_seq, hd)).astype(np.float32)
+    vc = rng.standard_normal((n_kv_head, max_seq, hd)).astype(np.float32)
+    qn = (1 + 0.2 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.2 * rng.standard_normal(hd)).astype(np.float32)
+    dev = {n: capi.DeviceBuffer.from_array(a) for n, a in
+           dict(q=q, k=k, v=v, kc=kc, vc=vc, cs=cs, sn=sn, qn=qn, kn=kn, step=np.array([0, pos], np.int32)).items()}
+    dscores = capi.DeviceBuffer(L.sdy_attn_scores_floats(1, n_head, max_seq) * 4)
+    dout = capi.DeviceBuffer(n_head * hd * 4)
+    with_q8k = n_head * hd % 256 == 0
+    dxq = capi.DeviceBuffer(n_head * hd // 256 * 292) if with_q8k else None
+    capi.check(L.sdy_attn_decode(dev["q"].ptr, dev["k"].ptr, dev["v"].ptr, dev["qn"].ptr if qk_norm else None,
+                                 dev["kn"].ptr if qk_norm else None, eps, dev["cs"].ptr, dev["sn"].ptr,
+                                 dev["step"].ptr, n_head, n_kv_head, hd, 0, dev["kc"].ptr, dev["vc"].ptr,
+                                 max_seq * hd, max_seq, dscores.ptr, dout.ptr, dxq.ptr if with_q8k else None, None))
+    got = dout.to_array(np.float32, n_head * hd)
+    qe, ke = q.copy(), k.copy()
+    if qk_norm:
+        for h in range(n_head):
+            O.lib().orc_rmsnorm(ptr(qe) + 4 * h * hd, ptr(qe) + 4 * h * hd, ptr(qn), hd, eps)
+        for h in range(n_kv_head):
+            O.lib().orc_rmsnorm(ptr(ke) + 4 * h * hd, ptr(ke) + 4 * h * hd, ptr(kn), hd, eps)
+    O.lib().orc_rope(ptr(qe), n_head, hd, ptr(cs) + 4 * pos * half, ptr(sn) + 4 * pos * half, 0)
+    O.lib().orc_rope(ptr(ke), n_kv_head, hd, ptr(cs) + 4 * pos * half, ptr(sn) + 4 * pos * half, 0)
+    kc[:, pos] = ke.reshape(n_kv_head, hd)
+    vc[:, pos] = v.reshape(n_kv_head, hd)
+    exp = np.empty(n_head * hd, np.float32)
+    scores = np.empty(max_seq, np.float32)
+    O.lib().orc_attention(ptr(exp), ptr(qe), ptr(kc), ptr(vc), n_head, n_kv_head, hd, pos + 1, max_seq, ptr(scores), 1)
+    assert np.array_equal(bits(got), bits(exp)), float(np.abs(got - exp).max())
+    assert np.array_equal(bits(dev["kc"].to_array(np.float32, kc.shape)), bits(kc))
+    assert np.array_equal(bits(dev["vc"].to_array(np.float32, vc.shape)), bits(vc))
+    if with_q8k:
+        assert dxq.to_array(np.uint8, n_head * hd // 256 * 292).tobytes() == O.quantize(exp, O.Q8_K).tobytes()
+
+
 def _gemm_case(kind, n_in, n_out, n_tok, seed, gen="workload"):
     t = TYPES[kind]
     rng = np.random.default_rng(seed)
