@@ -109,7 +109,7 @@ class SdyMat(ctypes.Structure):
 class SdyMvArgs(ctypes.Structure):
     _fields_ = [("xq", _vp), ("x", _vp), ("n_tok", _int), ("out", _vp), ("out_stride", ctypes.c_long),
                 ("bias", _vp), ("resid", _vp), ("row0", ctypes.c_long), ("row1", ctypes.c_long),
-                ("epilogue", _int), ("nw", _vp), ("eps", ctypes.c_float)]
+                ("epilogue", _int), ("nw", _vp), ("eps", ctypes.c_float), ("ws_ready", ctypes.c_int)]
 
 
 _DEVICE_SIGNATURES = {

@@ -100,11 +100,18 @@ void sdy_engine_release(engine_ctx *c) {
     for (size_t i = 0; i < sizeof host / sizeof *host; i++) sdy_host_free(host[i]);
 }
 
+/* Every write of c->xq[] comes with this call: the quantisation cache forgets its sources, and the GEMM
+ * workspace's f16 expansion of the activations (recorded with the epoch it was made in) goes stale. */
+static void xq_forget(engine_ctx *c) {
+    c->xq_src[0] = c->xq_src[1] = NULL;
+    c->xq_epoch++;
+}
+
 /* out[t][row] = W . x[t] for n_tok rows of x; new_input = 1 when x changed since the last call
  * (the quantized copy of x is then rebuilt), as matmul() in csrc/model_llama.c:592-611. */
 static int mm_epi(engine_ctx *c, float *out, const float *x, const dmat *w, int n_tok, const float *bias,
                   const float *resid, int new_input, int epilogue) {
-    if (new_input) c->xq_src[0] = c->xq_src[1] = NULL;
+    if (new_input) xq_forget(c);
     sdy_mv_args a;
     memset(&a, 0, sizeof a);
     a.n_tok = n_tok;
@@ -122,13 +129,26 @@ static int mm_epi(engine_ctx *c, float *out, const float *x, const dmat *w, int 
         int s = vt == SDY_Q8_0 ? 0 : 1;
         if (c->xq_src[s] != x || c->xq_n_tok[s] != n_tok || c->xq_n_in[s] != w->n_in) {
             TRY(sdy_quantize(vt, x, c->xq[s], w->n_in, n_tok, c->st));
+            c->xq_epoch++;
             c->xq_src[s] = x;
             c->xq_n_tok[s] = n_tok;
             c->xq_n_in[s] = w->n_in;
         }
         a.xq = c->xq[s];
         /* many tokens of a K-quant matrix: the MFMA GEMM (same bits as the matvec) */
-        if (n_tok >= GEMM_MIN_TOKENS && sdy_gemm_ok(&w->m, n_tok)) return sdy_gemm(&w->m, &a, c->gemm_ws, c->st);
+        if (n_tok >= GEMM_MIN_TOKENS && sdy_gemm_ok(&w->m, n_tok)) {
+            /* q, k and v (gate and up) read one quantised input: its f16 expansion is made once */
+            a.ws_ready = c->gemm_ready && c->gemm_epoch == c->xq_epoch && c->gemm_xq == a.xq &&
+                         c->gemm_n_tok == n_tok && c->gemm_n_in == w->n_in;
+            c->gemm_ready = 0;
+            TRY(sdy_gemm(&w->m, &a, c->gemm_ws, c->st));
+            c->gemm_ready = 1;
+            c->gemm_epoch = c->xq_epoch;
+            c->gemm_xq = a.xq;
+            c->gemm_n_tok = n_tok;
+            c->gemm_n_in = w->n_in;
+            return 0;
+        }
     }
     return sdy_matvec(&w->m, &a, c->st);
 }
@@ -143,7 +163,7 @@ static int mm(engine_ctx *c, float *out, const float *x, const dmat *w, int n_to
 static int norm_for(engine_ctx *c, const float *x, const float *wn, const dmat *next, int n) {
     const engine_model_info *in = &c->m->info;
     const int vt = vec_dot_type(next->type);
-    c->xq_src[0] = c->xq_src[1] = NULL;
+    xq_forget(c);
     if (vt == SDY_F32) return sdy_norm_quant(x, wn, in->norm_eps, in->dim, n, c->xb, SDY_F32, NULL, c->st);
     const int s = vt == SDY_Q8_0 ? 0 : 1;
     TRY(sdy_norm_quant(x, wn, in->norm_eps, in->dim, n, c->xb, vt, c->xq[s], c->st));
@@ -198,7 +218,7 @@ static int mm1_fused(engine_ctx *c, float *out, const float *x, const float *nw,
                      const float *resid, int epilogue) {
     sdy_mv_args a = fused_args(c, out, x, nw, w, bias, resid, epilogue);
     if (!c->fuse_act || !sdy_matvec_fused_ok(&w->m, &a, NULL, NULL)) return 1;
-    c->xq_src[0] = c->xq_src[1] = NULL;
+    xq_forget(c);
     return sdy_matvec(&w->m, &a, c->st);
 }
 
@@ -287,7 +307,7 @@ static int moe_decode(engine_ctx *c, const dlayer *L) {
         r.out = c->moe_probs;
         r.out_stride = ne;
         r.row1 = ne;
-        c->xq_src[0] = c->xq_src[1] = NULL;
+        xq_forget(c);
         TRY(sdy_matvec_float_norm(L->gate_inp.type, (const uint8_t *)L->gate_inp.m.base + L->gate_inp.m.plane_off[0],
                                   dim, &r, c->xq[1], c->st));
     } else {
@@ -315,7 +335,7 @@ static int moe_decode(engine_ctx *c, const dlayer *L) {
     }
     /* down over the k SwiGLU rows: each slot's workgroups quantise its row themselves, or (when that
        is not available) the rows are quantised first (the Q8_K row of xb is no longer needed) */
-    c->xq_src[0] = c->xq_src[1] = NULL;
+    xq_forget(c);
     memset(&a, 0, sizeof a);
     a.n_tok = 1;
     a.x = c->hb;
@@ -387,7 +407,7 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
                 sdy_mv_args a1 = fused_args(c, q, c->x, L->attn_norm, &L->wqkv, L->bq, NULL, SDY_EPI_NONE);
                 sdy_mv_args a2 = fused_args(c, v, c->x, L->attn_norm, &L->wv, L->bv, NULL, SDY_EPI_NONE);
                 if (sdy_matvec_fused_ok(&L->wqkv.m, &a1, &L->wv.m, &a2)) {
-                    c->xq_src[0] = c->xq_src[1] = NULL;
+                    xq_forget(c);
                     TRY(sdy_matvec_pair(&L->wqkv.m, &a1, &L->wv.m, &a2, c->st));
                     qkv_done = 1;
                 }
@@ -414,7 +434,7 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
             TRY(sdy_attn_decode(q, k, v, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos, c->rope_sin, c->step_dev,
                                 in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc, vc, head_stride, c->max_seq,
                                 c->part, c->att, q8k ? c->xq[1] : NULL, c->st));
-            c->xq_src[0] = c->xq_src[1] = NULL;
+            xq_forget(c);
             if (q8k) {
                 c->xq_src[1] = c->att;
                 c->xq_n_tok[1] = 1;

@@ -15,7 +15,8 @@
 //
 // Tiling: a wave owns 32 rows x 32*NT tokens (NT MFMA tiles sharing its dequantised weight
 // fragments); a workgroup is 4 waves on 4 consecutive row tiles, so they read the same activation
-// fragments (L1 hits). The activations are expanded once per call to f16 (k_gemm_prep).
+// fragments (L1 hits). The activations are expanded to f16 by k_gemm_prep, once per call unless the caller says
+// the workspace already holds them (ws_ready: q, k and v of one input).
 #include <stdlib.h>
 
 #include "sdy_device.h"
@@ -774,17 +775,30 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
         }
 }
 
-// Q8_K rows -> f16 values, f32 scales and f16 bsums for the GEMM. Grid (nb, n_tok), 64 threads.
-__global__ __launch_bounds__(64) void k_gemm_prep(const uint8_t *__restrict__ xq, int nb, _Float16 *__restrict__ y16,
-                                                  float *__restrict__ yd, _Float16 *__restrict__ bs16) {
-    const int sb = blockIdx.x, t = blockIdx.y, l = threadIdx.x;
-    const uint8_t *blk = xq + ((size_t)t * nb + sb) * 292;
-    const uint32_t v = *reinterpret_cast<const uint32_t *>(blk + 4 + 4 * l);
-    _Float16 *o = y16 + (size_t)t * nb * 256 + 256 * sb + 4 * l;
+// Q8_K rows -> f16 values, f32 scales and f16 bsums for the GEMM (all exact: |q| <= 127, |bsum| <=
+// 2032). One thread per 16 values of a super-block (n_sb = n_tok * nb super-blocks in a row): four
+// 4-byte loads, two 16-byte stores, and the super-block's bsum number `part`; 256 threads.
+__global__ __launch_bounds__(256) void k_gemm_prep(const uint8_t *__restrict__ xq, long n_sb,
+                                                   _Float16 *__restrict__ y16, float *__restrict__ yd,
+                                                   _Float16 *__restrict__ bs16) {
+    const long g = blockIdx.x * 256L + threadIdx.x, sbg = g >> 4;
+    const int part = (int)(g & 15);
+    if (sbg >= n_sb) return;
+    const uint8_t *blk = xq + sbg * 292;
+    const uint32_t *q4 = reinterpret_cast<const uint32_t *>(blk + 4 + 16 * part);
+    typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+    f16x8 o[2];
 #pragma unroll
-    for (int e = 0; e < 4; e++) o[e] = (_Float16)(float)(int8_t)((v >> (8 * e)) & 255u);
-    if (l < 16) bs16[((size_t)t * nb + sb) * 16 + l] = (_Float16)(float)reinterpret_cast<const int16_t *>(blk + 260)[l];
-    if (l == 0) yd[(size_t)t * nb + sb] = *reinterpret_cast<const float *>(blk);
+    for (int w = 0; w < 4; w++) {
+        const uint32_t v = q4[w];
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[w >> 1][4 * (w & 1) + e] = (_Float16)(float)(int8_t)((v >> (8 * e)) & 255u);
+    }
+    f16x8 *dst = reinterpret_cast<f16x8 *>(y16 + sbg * 256 + 16 * part);
+    dst[0] = o[0];
+    dst[1] = o[1];
+    bs16[sbg * 16 + part] = (_Float16)(float)reinterpret_cast<const int16_t *>(blk + 260)[part];
+    if (part == 0) yd[sbg] = *reinterpret_cast<const float *>(blk);
 }
 
 // Exactness check of a K-quant matrix for the GEMM: flags a row super-block whose
@@ -963,10 +977,13 @@ extern "C" int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_st
     g.yd = (const float *)w;
     w += ((size_t)n_tok * nb * 4 + 255) & ~(size_t)255;
     g.bs16 = (const _Float16 *)w;
-    hipLaunchKernelGGL(k_gemm_prep, dim3(nb, n_tok), dim3(64), 0, st, (const uint8_t *)a->xq, nb, (_Float16 *)g.y16,
-                       (float *)g.yd, (_Float16 *)g.bs16);
-    int rc = sdy_check_launch("gemm_prep");
-    if (rc) return rc;
+    int rc;
+    if (!a->ws_ready) {
+        const long n_sb = (long)n_tok * nb;
+        hipLaunchKernelGGL(k_gemm_prep, dim3((unsigned)((n_sb * 16 + 255) / 256)), dim3(256), 0, st,
+                           (const uint8_t *)a->xq, n_sb, (_Float16 *)g.y16, (float *)g.yd, (_Float16 *)g.bs16);
+        if ((rc = sdy_check_launch("gemm_prep"))) return rc;
+    }
     g.row0 = a->row0;
     g.n_rows = a->row1 - a->row0;
     g.n_tok = n_tok;

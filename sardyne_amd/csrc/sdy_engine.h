@@ -46,6 +46,11 @@ struct engine_ctx {
     void *xq[2];                /* quantized activations: [0] Q8_0, [1] Q8_K */
     const float *xq_src[2];
     int xq_n_tok[2], xq_n_in[2];
+    unsigned xq_epoch;          /* bumped at every write of xq[] */
+    int gemm_ready;             /* gemm_ws holds the f16 expansion of gemm_xq made in epoch gemm_epoch */
+    unsigned gemm_epoch;
+    const void *gemm_xq;
+    int gemm_n_tok, gemm_n_in;
     int32_t *tok_dev, *tok_host;
     /* one-token decode: step_dev = {token, position} read by the kernels, so the recorded graph
        replays for every position */

@@ -100,6 +100,9 @@ typedef struct {
                             row of x itself, RMS-normalised first when nw is set (x / rms(x) * nw, eps), with
                             the bytes sdy_quantize / sdy_norm_quant would write; see sdy_matvec_fused_ok */
     float eps;
+    int ws_ready;        /* sdy_gemm: ws already holds this xq's f16 expansion (same n_tok and n_in), written by
+                            the previous sdy_gemm on ws with nothing written to xq or ws since: it is not
+                            expanded again */
 } sdy_mv_args;
 enum { SDY_EPI_NONE = 0, SDY_EPI_SWIGLU = 1 };
 /* out = W · x for rows [row0, row1) and n_tok tokens. */

@@ -925,6 +925,40 @@ def test_gemm_bit_exact(kind, n_in, n_out, n_tok):
     assert np.array_equal(bits(got), bits(exp))
 
 
+@pytest.mark.parametrize("n_in,n_tok", [(2048, 512), (11008, 33), (256, 16)])
+def test_gemm_ws_ready_reuses_expansion(n_in, n_tok):
+    """ws_ready = 1 skips the f16 expansion of the activations: a Q6_K GEMM that reuses the workspace
+    a Q4_K GEMM on the same Q8_K input just filled gives the bits of its own full call and of the
+    oracle; after a different input has been expanded into the workspace, a full call is needed again."""
+    L = lib()
+    t4, w4, xq = _gemm_case("Q4_K", n_in, 96, n_tok, seed=n_in + n_tok)
+    t6, w6, _ = _gemm_case("Q6_K", n_in, 70, n_tok, seed=n_in + n_tok + 5)
+    m4, m6 = capi.DeviceMatrix(t4, n_in, 96, w4), capi.DeviceMatrix(t6, n_in, 70, w6)
+    assert L.sdy_gemm_ok(ctypes.byref(m4.m), n_tok) and L.sdy_gemm_ok(ctypes.byref(m6.m), n_tok)
+    dq = capi.DeviceBuffer.from_array(xq)
+    ws = capi.DeviceBuffer(L.sdy_gemm_ws_bytes(n_tok, n_in))
+    d4, d6 = capi.DeviceBuffer(n_tok * 96 * 4), capi.DeviceBuffer(n_tok * 70 * 4)
+
+    def run(m, dout, n_out, ready, xq_ptr=dq.ptr):
+        a = capi.SdyMvArgs(xq=xq_ptr, n_tok=n_tok, out=dout.ptr, out_stride=n_out, row0=0, row1=n_out,
+                           ws_ready=ready)
+        capi.check(L.sdy_gemm(ctypes.byref(m.m), ctypes.byref(a), ws.ptr, None))
+        return dout.to_array(np.float32, (n_tok, n_out))
+
+    got4 = run(m4, d4, 96, 0)
+    got6_reused = run(m6, d6, 70, 1)
+    exp6 = O.matmul_q(w6, t6, xq, n_in, simd=1)
+    assert np.array_equal(bits(got4), bits(O.matmul_q(w4, t4, xq, n_in, simd=1)))
+    assert np.array_equal(bits(got6_reused), bits(exp6))
+    assert np.array_equal(bits(run(m6, d6, 70, 0)), bits(exp6))
+    # another input expanded into the workspace: the reused result follows that input
+    xq2 = O.quantize(np.random.default_rng(n_in).standard_normal((n_tok, n_in)).astype(np.float32), O.Q8_K)
+    dq2 = capi.DeviceBuffer.from_array(xq2)
+    run(m4, d4, 96, 0, dq2.ptr)
+    assert np.array_equal(bits(run(m6, d6, 70, 1)), bits(O.matmul_q(w6, t6, xq2, n_in, simd=1)))
+    assert np.array_equal(bits(run(m6, d6, 70, 0)), bits(exp6))
+
+
 @pytest.mark.parametrize("variant", ["0", "3", "4", "5", "6", "11", "12", "13", "14", "15", "16"])
 @pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
 def test_gemm_tile_variants_bit_exact(kind, variant, monkeypatch):
