@@ -170,9 +170,22 @@ SDY_DEV void row_weights(const float *row, int i0, int stride, int n, float m, f
     }
 }
 
-// dot(q, k) in csrc/ops_avx2.c:61-74's order (x = q, w = k), both in LDS, q 16-byte aligned.
+// K operands of dot_avx2_order: a row in LDS (16-byte aligned), or a row held in registers
+struct KRowLds {
+    const float *p;
+    SDY_DEV float4 v4(int i) const { return *reinterpret_cast<const float4 *>(p + i); }
+    SDY_DEV float v1(int i) const { return p[i]; }
+};
 template <int HD>
-SDY_DEV float dot_avx2_order(const float *q, const float *k) {
+struct KRowReg {
+    f32x4 r[HD / 4];
+    SDY_DEV float4 v4(int i) const { return make_float4(r[i / 4][0], r[i / 4][1], r[i / 4][2], r[i / 4][3]); }
+    SDY_DEV float v1(int i) const { return r[i / 4][i % 4]; }
+};
+
+// dot(q, k) in csrc/ops_avx2.c:61-74's order (x = q, w = k), q in LDS (16-byte aligned).
+template <int HD, class K>
+SDY_DEV float dot_avx2_order(const float *q, const K &k) {
     constexpr int N32 = HD / 32 * 32, N8 = HD / 8 * 8;
     float a[4][8];
 #pragma unroll
@@ -185,8 +198,8 @@ SDY_DEV float dot_avx2_order(const float *q, const float *k) {
         for (int c = 0; c < 4; c++) {
             const float4 q0 = *reinterpret_cast<const float4 *>(q + i + 8 * c);
             const float4 q1 = *reinterpret_cast<const float4 *>(q + i + 8 * c + 4);
-            const float4 k0 = *reinterpret_cast<const float4 *>(k + i + 8 * c);
-            const float4 k1 = *reinterpret_cast<const float4 *>(k + i + 8 * c + 4);
+            const float4 k0 = k.v4(i + 8 * c);
+            const float4 k1 = k.v4(i + 8 * c + 4);
             a[c][0] = fmaf(k0.x, q0.x, a[c][0]);
             a[c][1] = fmaf(k0.y, q0.y, a[c][1]);
             a[c][2] = fmaf(k0.z, q0.z, a[c][2]);
@@ -199,7 +212,7 @@ SDY_DEV float dot_avx2_order(const float *q, const float *k) {
 #pragma unroll
     for (int i = N32; i < N8; i += 8)
 #pragma unroll
-        for (int l = 0; l < 8; l++) a[0][l] = fmaf(k[i + l], q[i + l], a[0][l]);
+        for (int l = 0; l < 8; l++) a[0][l] = fmaf(k.v1(i + l), q[i + l], a[0][l]);
     float v[8];
 #pragma unroll
     for (int l = 0; l < 8; l++) {
@@ -209,7 +222,7 @@ SDY_DEV float dot_avx2_order(const float *q, const float *k) {
     float s = ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]));
 #pragma unroll
     for (int i = N8; i < HD; i++) {
-        const float p = q[i] * k[i];
+        const float p = q[i] * k.v1(i);
         s = s + p;
     }
     return s;
@@ -382,14 +395,27 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
             for (int d = tid; d < HD; d += 256) ks[special * KS + d] = kp[d];
         __syncthreads();
     }
-    for (int pr = wave; pr < n_pairs; pr += 4) {
-        const int tl = pr / n_rep, r = pr - tl * n_rep, t = t0 + tl;
-        const int n_kv = DECODE ? pos + 1 : a.n_kv0 + t;
-        const int np = n_kv - p0 < CH ? n_kv - p0 : CH;
-        if (lane < np) {
-            const float s = dot_avx2_order<HD>(qs + pr * HD, ks + lane * KS) * a.scale;
-            a.scores[((size_t)t * a.n_head + g * n_rep + r) * a.max_kv + p0 + lane] = s;
+    // the scores of the wave's pairs; with K from kr (the lane's row) or from LDS
+    auto pairs = [&](const auto &kr) {
+        for (int pr = wave; pr < n_pairs; pr += 4) {
+            const int tl = pr / n_rep, r = pr - tl * n_rep, t = t0 + tl;
+            const int n_kv = DECODE ? pos + 1 : a.n_kv0 + t;
+            const int np = n_kv - p0 < CH ? n_kv - p0 : CH;
+            if (lane < np) {
+                const float s = dot_avx2_order<HD>(qs + pr * HD, kr) * a.scale;
+                a.scores[((size_t)t * a.n_head + g * n_rep + r) * a.max_kv + p0 + lane] = s;
+            }
         }
+    };
+    if constexpr (!DECODE && HD % 32 == 0 && HD <= 128) {
+        // prefill: the wave's many pairs share the lane's K row, read out of LDS into registers once
+        // (the LDS then serves only the pairs' q, a broadcast)
+        KRowReg<HD> kr;
+#pragma unroll
+        for (int i = 0; i < HD / 4; i++) kr.r[i] = *reinterpret_cast<const f32x4 *>(ks + lane * KS + 4 * i);
+        pairs(kr);
+    } else {
+        pairs(KRowLds{ks + lane * KS});
     }
 }
 
