@@ -156,6 +156,8 @@ _DEVICE_SIGNATURES = {
     "sdy_attn_scores_floats": (_sz, [_int, _int, _int]),
     "sdy_attention": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, ctypes.c_long, ctypes.c_long, _vp, _vp,
                              ctypes.c_long, _vp]),
+    "sdy_quantize_gemm": (_int, [_vp, _vp, _int, _int, _vp, _vp]),
+    "sdy_norm_quant_gemm": (_int, [_vp, _vp, ctypes.c_float, _int, _int, _vp, _vp, _vp, _vp]),
     "sdy_attn_decode_ok": (_int, [_int, _int, _int, _int]),
     "sdy_attn_decode": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _int, _int, _int, _int, _vp,
                                _vp, ctypes.c_long, _int, _vp, _vp, _vp, _vp]),

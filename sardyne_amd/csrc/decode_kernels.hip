@@ -11,13 +11,13 @@
 namespace {
 
 // VT = SDY_Q8_K, SDY_Q8_0 or SDY_F32 (normalise only). xb (f32 result) may be null for the
-// quantising variants. Grid: one 256-thread block per row. For Q8_K rows of up to 4096 elements
+// quantising variants; with e.y16 set, Q8_K also writes the GEMM's expansion of its blocks. Grid: one 256-thread block per row. For Q8_K rows of up to 4096 elements
 // the row is read once: the float4 chunks of the sum of squares are the elements each lane
 // quantises (superblock wave + 4k, elements 4 lane .. 4 lane + 3).
 template <int VT>
 __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x, const float *__restrict__ w,
                                                     float eps, int n, float *__restrict__ xb,
-                                                    uint8_t *__restrict__ xq) {
+                                                    uint8_t *__restrict__ xq, SdyGemmExp e) {
     constexpr int NREG = 4;
     __shared__ double sh[4];
     const int t = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -75,12 +75,18 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
                 *reinterpret_cast<uint32_t *>(ob + 4 + 4 * lane) = r[k].packed;
                 if ((lane & 3) == 0) *reinterpret_cast<int16_t *>(ob + 260 + 2 * (lane >> 2)) = (int16_t)r[k].gsum;
                 if (lane == 0) *reinterpret_cast<float *>(ob) = r[k].d;
+                if (e.y16) e.put(r[k], lane, (size_t)t * nb + wave + 4 * k);
             }
         for (int s = wave + 4 * NREG; s < nb; s += 4) {
             const float4 o = values(s, from_mem(s), *reinterpret_cast<const float4 *>(w + 256 * s + 4 * lane));
             const float x1[4] = {o.x, o.y, o.z, o.w};
             store_xb(s, x1);
-            sdy_q8k_block(x1, lane, xq + ((size_t)t * nb + s) * 292);
+            const SdyQ8kLane r1 = sdy_q8k_lane(x1, lane);
+            uint8_t *ob = xq + ((size_t)t * nb + s) * 292;
+            *reinterpret_cast<uint32_t *>(ob + 4 + 4 * lane) = r1.packed;
+            if ((lane & 3) == 0) *reinterpret_cast<int16_t *>(ob + 260 + 2 * (lane >> 2)) = (int16_t)r1.gsum;
+            if (lane == 0) *reinterpret_cast<float *>(ob) = r1.d;
+            if (e.y16) e.put(r1, lane, (size_t)t * nb + s);
         }
     } else if constexpr (VT == SDY_Q8_0) {
         const int nblk = n / 32, l = lane & 31;
@@ -110,18 +116,28 @@ extern "C" int sdy_norm_quant(const float *x, const float *w, float eps, int n, 
     switch (vtype) {
     case SDY_Q8_K:
         if (n % 256) return sdy_fail(-1, "norm_quant: Q8_K rows must be a multiple of 256 (got %d)", n);
-        hipLaunchKernelGGL(k_norm_quant<SDY_Q8_K>, dim3(n_rows), dim3(256), 0, st, x, w, eps, n, xb, q);
+        hipLaunchKernelGGL(k_norm_quant<SDY_Q8_K>, dim3(n_rows), dim3(256), 0, st, x, w, eps, n, xb, q, SdyGemmExp{});
         break;
     case SDY_Q8_0:
         if (n % 32) return sdy_fail(-1, "norm_quant: Q8_0 rows must be a multiple of 32 (got %d)", n);
-        hipLaunchKernelGGL(k_norm_quant<SDY_Q8_0>, dim3(n_rows), dim3(256), 0, st, x, w, eps, n, xb, q);
+        hipLaunchKernelGGL(k_norm_quant<SDY_Q8_0>, dim3(n_rows), dim3(256), 0, st, x, w, eps, n, xb, q, SdyGemmExp{});
         break;
     case SDY_F32:
         if (!xb) return sdy_fail(-1, "norm_quant: no output");
-        hipLaunchKernelGGL(k_norm_quant<SDY_F32>, dim3(n_rows), dim3(256), 0, st, x, w, eps, n, xb, q);
+        hipLaunchKernelGGL(k_norm_quant<SDY_F32>, dim3(n_rows), dim3(256), 0, st, x, w, eps, n, xb, q, SdyGemmExp{});
         break;
     default: return sdy_fail(-1, "norm_quant: activation type %d", vtype);
     }
+    return sdy_check_launch("norm_quant");
+}
+
+// sdy_norm_quant to Q8_K plus the GEMM's expansion of the rows in ws (the layout sdy_gemm reads)
+extern "C" int sdy_norm_quant_gemm(const float *x, const float *w, float eps, int n, int n_rows, float *xb, void *xq,
+                                   void *ws, sdy_stream s) {
+    if (n_rows <= 0) return 0;
+    if (n % 256) return sdy_fail(-1, "norm_quant: Q8_K rows must be a multiple of 256 (got %d)", n);
+    hipLaunchKernelGGL(k_norm_quant<SDY_Q8_K>, dim3(n_rows), dim3(256), 0, (hipStream_t)s, x, w, eps, n, xb,
+                       (uint8_t *)xq, sdy_gemm_exp(ws, n_rows, n));
     return sdy_check_launch("norm_quant");
 }
 

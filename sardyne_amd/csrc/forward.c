@@ -107,6 +107,18 @@ static void xq_forget(engine_ctx *c) {
     c->xq_epoch++;
 }
 
+/* gemm_ws now holds the f16 expansion of xq (n_tok rows of n_in), made after the last write of xq[] */
+static void gemm_record(engine_ctx *c, const void *xq, int n_tok, int n_in) {
+    c->gemm_ready = 1;
+    c->gemm_epoch = c->xq_epoch;
+    c->gemm_xq = xq;
+    c->gemm_n_tok = n_tok;
+    c->gemm_n_in = n_in;
+}
+
+/* Whether n_tok rows for w take the MFMA GEMM */
+static int use_gemm(const dmat *w, int n_tok) { return n_tok >= GEMM_MIN_TOKENS && sdy_gemm_ok(&w->m, n_tok); }
+
 /* out[t][row] = W . x[t] for n_tok rows of x; new_input = 1 when x changed since the last call
  * (the quantized copy of x is then rebuilt), as matmul() in csrc/model_llama.c:592-611. */
 static int mm_epi(engine_ctx *c, float *out, const float *x, const dmat *w, int n_tok, const float *bias,
@@ -128,25 +140,25 @@ static int mm_epi(engine_ctx *c, float *out, const float *x, const dmat *w, int 
     } else {
         int s = vt == SDY_Q8_0 ? 0 : 1;
         if (c->xq_src[s] != x || c->xq_n_tok[s] != n_tok || c->xq_n_in[s] != w->n_in) {
-            TRY(sdy_quantize(vt, x, c->xq[s], w->n_in, n_tok, c->st));
+            /* for the GEMM the quantiser also writes the f16 expansion it reads */
+            const int gemm = vt == SDY_Q8_K && use_gemm(w, n_tok);
+            if (gemm) TRY(sdy_quantize_gemm(x, c->xq[s], w->n_in, n_tok, c->gemm_ws, c->st));
+            else TRY(sdy_quantize(vt, x, c->xq[s], w->n_in, n_tok, c->st));
             c->xq_epoch++;
+            if (gemm) gemm_record(c, c->xq[s], n_tok, w->n_in);
             c->xq_src[s] = x;
             c->xq_n_tok[s] = n_tok;
             c->xq_n_in[s] = w->n_in;
         }
         a.xq = c->xq[s];
         /* many tokens of a K-quant matrix: the MFMA GEMM (same bits as the matvec) */
-        if (n_tok >= GEMM_MIN_TOKENS && sdy_gemm_ok(&w->m, n_tok)) {
+        if (use_gemm(w, n_tok)) {
             /* q, k and v (gate and up) read one quantised input: its f16 expansion is made once */
             a.ws_ready = c->gemm_ready && c->gemm_epoch == c->xq_epoch && c->gemm_xq == a.xq &&
                          c->gemm_n_tok == n_tok && c->gemm_n_in == w->n_in;
             c->gemm_ready = 0;
             TRY(sdy_gemm(&w->m, &a, c->gemm_ws, c->st));
-            c->gemm_ready = 1;
-            c->gemm_epoch = c->xq_epoch;
-            c->gemm_xq = a.xq;
-            c->gemm_n_tok = n_tok;
-            c->gemm_n_in = w->n_in;
+            gemm_record(c, a.xq, n_tok, w->n_in);
             return 0;
         }
     }
@@ -166,7 +178,12 @@ static int norm_for(engine_ctx *c, const float *x, const float *wn, const dmat *
     xq_forget(c);
     if (vt == SDY_F32) return sdy_norm_quant(x, wn, in->norm_eps, in->dim, n, c->xb, SDY_F32, NULL, c->st);
     const int s = vt == SDY_Q8_0 ? 0 : 1;
-    TRY(sdy_norm_quant(x, wn, in->norm_eps, in->dim, n, c->xb, vt, c->xq[s], c->st));
+    if (vt == SDY_Q8_K && use_gemm(next, n)) { /* with the GEMM's f16 expansion of the rows */
+        TRY(sdy_norm_quant_gemm(x, wn, in->norm_eps, in->dim, n, c->xb, c->xq[s], c->gemm_ws, c->st));
+        gemm_record(c, c->xq[s], n, in->dim);
+    } else {
+        TRY(sdy_norm_quant(x, wn, in->norm_eps, in->dim, n, c->xb, vt, c->xq[s], c->st));
+    }
     c->xq_src[s] = c->xb;
     c->xq_n_tok[s] = n;
     c->xq_n_in[s] = in->dim;

@@ -971,12 +971,10 @@ extern "C" int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_st
         return sdy_fail(-1, "gemm: the SwiGLU epilogue needs an even row range from an even row, no bias, no residual");
     GemmArgs g = gemm_args(m);
     const int nb = g.nb, n_tok = a->n_tok;
-    uint8_t *w = (uint8_t *)ws;
-    g.y16 = (const _Float16 *)w;
-    w += ((size_t)n_tok * g.n_in * 2 + 255) & ~(size_t)255;
-    g.yd = (const float *)w;
-    w += ((size_t)n_tok * nb * 4 + 255) & ~(size_t)255;
-    g.bs16 = (const _Float16 *)w;
+    const SdyGemmExp e = sdy_gemm_exp(ws, n_tok, g.n_in);
+    g.y16 = e.y16;
+    g.yd = e.yd;
+    g.bs16 = e.bs16;
     int rc;
     if (!a->ws_ready) {
         const long n_sb = (long)n_tok * nb;

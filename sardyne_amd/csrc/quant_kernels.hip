@@ -241,11 +241,17 @@ __global__ void k_dequant_float(const uint8_t *__restrict__ w, int n_in, const i
 // ------------------------------------------------------------------------ activation quantisers
 
 // Q8_K (csrc/quant.c:118-144): one wave per 256-element block, lane l holds elements 4l..4l+3.
-__global__ void k_quant_q8k(const float *__restrict__ x, uint8_t *__restrict__ out, int n_in) {
+// With e.y16 set, also the GEMM's expansion of the block.
+__global__ void k_quant_q8k(const float *__restrict__ x, uint8_t *__restrict__ out, int n_in, SdyGemmExp e) {
     const int nb = n_in / 256, s = blockIdx.x, t = blockIdx.y, l = threadIdx.x;
     const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)t * n_in + 256 * s + 4 * l);
     const float xs[4] = {v.x, v.y, v.z, v.w};
-    sdy_q8k_block(xs, l, out + ((size_t)t * nb + s) * 292);
+    const SdyQ8kLane r = sdy_q8k_lane(xs, l);
+    uint8_t *ob = out + ((size_t)t * nb + s) * 292;
+    *reinterpret_cast<uint32_t *>(ob + 4 + 4 * l) = r.packed;
+    if ((l & 3) == 0) *reinterpret_cast<int16_t *>(ob + 260 + 2 * (l >> 2)) = (int16_t)r.gsum;
+    if (l == 0) *reinterpret_cast<float *>(ob) = r.d;
+    if (e.y16) e.put(r, l, (size_t)t * nb + s);
 }
 
 // Q8_0 (csrc/quant.c:98-108): one wave per two 32-element blocks, one element per lane.
@@ -1780,7 +1786,8 @@ extern "C" int sdy_quantize(int vtype, const float *x, void *xq, int n_in, int n
     if (n_tok <= 0) return 0;
     if (vtype == SDY_Q8_K) {
         if (n_in % 256) return sdy_fail(-1, "Q8_K rows must be a multiple of 256 (got %d)", n_in);
-        hipLaunchKernelGGL(k_quant_q8k, dim3(n_in / 256, n_tok), dim3(64), 0, st, x, (uint8_t *)xq, n_in);
+        hipLaunchKernelGGL(k_quant_q8k, dim3(n_in / 256, n_tok), dim3(64), 0, st, x, (uint8_t *)xq, n_in,
+                           SdyGemmExp{nullptr, nullptr, nullptr});
         return sdy_check_launch("quant_q8k");
     }
     if (vtype == SDY_Q8_0) {
@@ -1790,6 +1797,15 @@ extern "C" int sdy_quantize(int vtype, const float *x, void *xq, int n_in, int n
         return sdy_check_launch("quant_q8_0");
     }
     return sdy_fail(-1, "activation type %d", vtype);
+}
+
+// Q8_K rows plus the GEMM's expansion of them in ws (the layout sdy_gemm reads)
+extern "C" int sdy_quantize_gemm(const float *x, void *xq, int n_in, int n_tok, void *ws, sdy_stream s) {
+    if (n_tok <= 0) return 0;
+    if (n_in % 256) return sdy_fail(-1, "Q8_K rows must be a multiple of 256 (got %d)", n_in);
+    hipLaunchKernelGGL(k_quant_q8k, dim3(n_in / 256, n_tok), dim3(64), 0, (hipStream_t)s, x, (uint8_t *)xq, n_in,
+                       sdy_gemm_exp(ws, n_tok, n_in));
+    return sdy_check_launch("quant_q8k");
 }
 
 static int g_n_cu = 0;

@@ -75,6 +75,36 @@ SDY_DEV SdyQ8kLane sdy_q8k_lane(const float xs[4], int lane) {
 }
 
 // The block in the reference layout (292 bytes at ob: f32 d, int8 qs[256], int16 bsums[16]).
+// The prefill GEMM's f16 expansion of a Q8_K row (the workspace of sdy_gemm; y16 null: none).
+struct SdyGemmExp {
+    _Float16 *y16;  // [super-block][256] the int8 values
+    float *yd;      // [super-block] the scales
+    _Float16 *bs16; // [super-block][16] the 16-element sums
+    // super-block sbg (of the row-major sequence) from the lane's quantiser result: the bits
+    // k_gemm_prep makes of the block's bytes (|q| <= 127 and |bsum| <= 2032 are exact in f16)
+    SDY_DEV void put(const SdyQ8kLane &r, int lane, size_t sbg) const {
+        typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+        f16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[e] = (_Float16)(float)(int8_t)((r.packed >> (8 * e)) & 255u);
+        *reinterpret_cast<f16x4 *>(y16 + sbg * 256 + 4 * lane) = o;
+        if ((lane & 3) == 0) bs16[sbg * 16 + (lane >> 2)] = (_Float16)(float)(int16_t)r.gsum;
+        if (lane == 0) yd[sbg] = r.d;
+    }
+};
+
+// sdy_gemm's workspace for n_tok rows of n_in: y16, then yd, then bs16, each 256-byte aligned
+inline SdyGemmExp sdy_gemm_exp(void *ws, int n_tok, int n_in) {
+    uint8_t *w = (uint8_t *)ws;
+    SdyGemmExp e;
+    e.y16 = (_Float16 *)w;
+    w += ((size_t)n_tok * n_in * 2 + 255) & ~(size_t)255;
+    e.yd = (float *)w;
+    w += ((size_t)n_tok * (n_in / 256) * 4 + 255) & ~(size_t)255;
+    e.bs16 = (_Float16 *)w;
+    return e;
+}
+
 SDY_DEV void sdy_q8k_block(const float xs[4], int lane, uint8_t *ob) {
     const SdyQ8kLane r = sdy_q8k_lane(xs, lane);
     *reinterpret_cast<uint32_t *>(ob + 4 + 4 * lane) = r.packed;

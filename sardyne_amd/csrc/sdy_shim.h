@@ -132,6 +132,12 @@ int sdy_matvec_grouped_fused_ok(const sdy_mat *m, const sdy_mv_args *a, int n_sl
 int sdy_gemm_ok(const sdy_mat *m, int n_tok);
 size_t sdy_gemm_ws_bytes(int n_tok, int n_in);
 int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_stream s);
+/* Q8_K activations for the GEMM in one launch: the bytes of sdy_quantize (of sdy_norm_quant, with xb
+ * as there) into xq, and their f16 expansion into ws, so that sdy_gemm on the same rows and ws runs
+ * with ws_ready = 1. */
+int sdy_quantize_gemm(const float *x, void *xq, int n_in, int n_tok, void *ws, sdy_stream s);
+int sdy_norm_quant_gemm(const float *x, const float *w, float eps, int n, int n_rows, float *xb, void *xq, void *ws,
+                        sdy_stream s);
 /* Exactness check of rows [r0, r0 + n) of m for the GEMM: *bad_host = 1 when some row fails. */
 int sdy_gemm_check_rows(const sdy_mat *m, long r0, long n, int *bad_host, sdy_stream s);
 

@@ -959,6 +959,47 @@ def test_gemm_ws_ready_reuses_expansion(n_in, n_tok):
     assert np.array_equal(bits(run(m6, d6, 70, 0)), bits(exp6))
 
 
+@pytest.mark.parametrize("norm", [False, True])
+@pytest.mark.parametrize("n_in,n_tok", [(2048, 512), (11008, 40), (4096, 17)])
+def test_quantize_gemm_expansion(norm, n_in, n_tok):
+    """sdy_quantize_gemm / sdy_norm_quant_gemm write the Q8_K bytes (and the normalised rows) of
+    sdy_quantize / sdy_norm_quant, plus the GEMM's expansion of them: a GEMM with ws_ready = 1 after
+    them gives the bits of a full GEMM on those bytes and of the oracle. Rows include all-zero ones."""
+    L = lib()
+    rng = np.random.default_rng(n_in + n_tok + norm)
+    x = rng.standard_normal((n_tok, n_in)).astype(np.float32)
+    x[1] = 0.0
+    wn = (1 + 0.3 * rng.standard_normal(n_in)).astype(np.float32)
+    t, w, _ = _gemm_case("Q4_K", n_in, 64, n_tok, seed=n_in + 3)
+    m = capi.DeviceMatrix(t, n_in, 64, w)
+    assert L.sdy_gemm_ok(ctypes.byref(m.m), n_tok)
+    dx, dw = capi.DeviceBuffer.from_array(x), capi.DeviceBuffer.from_array(wn)
+    qb = n_tok * n_in // 256 * 292
+    dq1, dq2 = capi.DeviceBuffer(qb), capi.DeviceBuffer(qb)
+    db1, db2 = capi.DeviceBuffer(x.nbytes), capi.DeviceBuffer(x.nbytes)
+    ws = capi.DeviceBuffer(L.sdy_gemm_ws_bytes(n_tok, n_in))
+    if norm:
+        capi.check(L.sdy_norm_quant(dx.ptr, dw.ptr, 1e-6, n_in, n_tok, db1.ptr, O.Q8_K, dq1.ptr, None))
+        capi.check(L.sdy_norm_quant_gemm(dx.ptr, dw.ptr, 1e-6, n_in, n_tok, db2.ptr, dq2.ptr, ws.ptr, None))
+        assert np.array_equal(bits(db2.to_array(np.float32, x.shape)), bits(db1.to_array(np.float32, x.shape)))
+    else:
+        capi.check(L.sdy_quantize(O.Q8_K, dx.ptr, dq1.ptr, n_in, n_tok, None))
+        capi.check(L.sdy_quantize_gemm(dx.ptr, dq2.ptr, n_in, n_tok, ws.ptr, None))
+    q1 = dq1.to_array(np.uint8, qb)
+    assert dq2.to_array(np.uint8, qb).tobytes() == q1.tobytes()
+    dout = capi.DeviceBuffer(n_tok * 64 * 4)
+
+    def gemm(ready):
+        a = capi.SdyMvArgs(xq=dq2.ptr, n_tok=n_tok, out=dout.ptr, out_stride=64, row0=0, row1=64, ws_ready=ready)
+        capi.check(L.sdy_gemm(ctypes.byref(m.m), ctypes.byref(a), ws.ptr, None))
+        return dout.to_array(np.float32, (n_tok, 64))
+
+    reused = gemm(1)
+    exp = O.matmul_q(w, t, q1.reshape(n_tok, -1), n_in, simd=1)
+    assert np.array_equal(bits(reused), bits(exp))
+    assert np.array_equal(bits(gemm(0)), bits(exp))
+
+
 @pytest.mark.parametrize("variant", ["0", "3", "4", "5", "6", "11", "12", "13", "14", "15", "16"])
 @pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
 def test_gemm_tile_variants_bit_exact(kind, variant, monkeypatch):
