@@ -62,17 +62,17 @@ SDY_DEV void norm_rope_wave(float *buf, const float *nw, float eps, const float 
     sdy_wave_sync();
 }
 
-// q/k norm + RoPE of the vectors of n_tok tokens and the KV-cache write at positions pos0 + t.
-// Grid (n_tok, n_head + n_kv_head), 64 threads.
-__global__ __launch_bounds__(64) void k_qk_rope_kv(float *q, float *k, const float *v, const float *qn, const float *kn,
-                                                   float eps, const float *rope_cos, const float *rope_sin, int pos0,
-                                                   int n_head, int n_kv_head, int hd, int interleaved, float *k_cache,
-                                                   float *v_cache, long head_stride) {
+// q/k norm + RoPE of the vectors of n_tok tokens and the KV-cache write at positions pos0 + t; token
+// t's q, k and v rows start at t * qs, t * ks, t * vs floats. Grid (n_tok, n_head + n_kv_head), 64 threads.
+__global__ __launch_bounds__(64) void k_qk_rope_kv(float *q, float *k, const float *v, long qs, long ks, long vs,
+                                                   const float *qn, const float *kn, float eps, const float *rope_cos,
+                                                   const float *rope_sin, int pos0, int n_head, int n_kv_head, int hd,
+                                                   int interleaved, float *k_cache, float *v_cache, long head_stride) {
     __shared__ float buf[512];
     const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const bool is_q = h < n_head;
     const int hh = is_q ? h : h - n_head;
-    float *vec = is_q ? q + ((size_t)t * n_head + hh) * hd : k + ((size_t)t * n_kv_head + hh) * hd;
+    float *vec = is_q ? q + (size_t)t * qs + (size_t)hh * hd : k + (size_t)t * ks + (size_t)hh * hd;
     for (int i = lane; i < hd; i += 64) buf[i] = vec[i];
     sdy_wave_sync();
     const int pos = pos0 + t;
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(64) void k_qk_rope_kv(float *q, float *k, const flo
     if (!is_q && k_cache) {
         float *kc = k_cache + hh * head_stride + (size_t)pos * hd;
         float *vc = v_cache + hh * head_stride + (size_t)pos * hd;
-        const float *vv = v + ((size_t)t * n_kv_head + hh) * hd;
+        const float *vv = v + (size_t)t * vs + (size_t)hh * hd;
         for (int i = lane; i < hd; i += 64) {
             kc[i] = buf[i];
             vc[i] = vv[i];
@@ -1052,9 +1052,20 @@ extern "C" int sdy_qk_rope_kv(float *q, float *k, const float *v, const float *q
                               const float *rope_cos, const float *rope_sin, int pos0, int n_tok, int n_head,
                               int n_kv_head, int hd, int interleaved, float *k_cache, float *v_cache,
                               long head_stride, sdy_stream s) {
+    return sdy_qk_rope_kv_strided(q, k, v, (long)n_head * hd, (long)n_kv_head * hd, (long)n_kv_head * hd, qn, kn, eps,
+                                  rope_cos, rope_sin, pos0, n_tok, n_head, n_kv_head, hd, interleaved, k_cache, v_cache,
+                                  head_stride, s);
+}
+
+extern "C" int sdy_qk_rope_kv_strided(float *q, float *k, const float *v, long q_stride, long k_stride, long v_stride,
+                                      const float *qn, const float *kn, float eps, const float *rope_cos,
+                                      const float *rope_sin, int pos0, int n_tok, int n_head, int n_kv_head, int hd,
+                                      int interleaved, float *k_cache, float *v_cache, long head_stride, sdy_stream s) {
     if (hd > 512) return sdy_fail(-1, "head_dim %d above 512", hd);
-    hipLaunchKernelGGL(k_qk_rope_kv, dim3(n_tok, n_head + n_kv_head), dim3(64), 0, (hipStream_t)s, q, k, v, qn, kn, eps,
-                       rope_cos, rope_sin, pos0, n_head, n_kv_head, hd, interleaved, k_cache, v_cache, head_stride);
+    if (n_tok <= 0) return 0;
+    hipLaunchKernelGGL(k_qk_rope_kv, dim3(n_tok, n_head + n_kv_head), dim3(64), 0, (hipStream_t)s, q, k, v, q_stride,
+                       k_stride, v_stride, qn, kn, eps, rope_cos, rope_sin, pos0, n_head, n_kv_head, hd, interleaved,
+                       k_cache, v_cache, head_stride);
     return sdy_check_launch("qk_rope_kv");
 }
 

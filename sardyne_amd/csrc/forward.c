@@ -63,7 +63,7 @@ int sdy_engine_alloc(engine_ctx *c) {
     TRY(dalloc(&c->xq[1], BR * ((max_in + 255) / 256 * 292)));
     TRY(dalloc((void **)&c->tok_dev, B * 4));
     TRY(sdy_host_alloc((void **)&c->tok_host, B * 4));
-    TRY(dalloc((void **)&c->qkv, (q_dim + 2 * kv_dim) * 4));
+    TRY(dalloc((void **)&c->qkv, B * (q_dim + 2 * kv_dim) * 4));
     TRY(dalloc((void **)&c->step_dev, 2 * 4));
     TRY(sdy_host_alloc((void **)&c->step_host, 2 * 4));
     TRY(dalloc(&c->gemm_ws, sdy_gemm_ws_bytes((int)B, (int)max_in)));
@@ -461,13 +461,32 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
             else TRY(mm(c, c->x, c->att, &L->wo, 1, NULL, c->x, 0));
         } else {
             TRY(norm_for(c, c->x, L->attn_norm, L->qkv_parts >= 2 ? &L->wqkv : &L->wq, n));
-            TRY(mm(c, c->q, c->xb, &L->wq, n, L->bq, NULL, 0));
-            TRY(mm(c, c->k, c->xb, &L->wk, n, L->bk, NULL, 0));
-            TRY(mm(c, c->v, c->xb, &L->wv, n, L->bv, NULL, 0));
-            TRY(sdy_qk_rope_kv(c->q, c->k, c->v, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos, c->rope_sin, pos0,
-                               n, in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc, vc, head_stride, c->st));
-            TRY(sdy_attention(c->q, kc, vc, n, in->n_head, in->n_kv_head, hd, pos0 + 1, head_stride, q_dim, c->part,
-                              c->att, q_dim, c->st));
+            const int bias_fused = !in->qkv_bias ||
+                                   (L->bk == L->bq + q_dim && (L->qkv_parts < 3 || L->bv == L->bk + kv_dim));
+            float *q = c->q, *k = c->k, *v = c->v;
+            long qs = q_dim, ks = kv_dim, vs = kv_dim;
+            if (L->qkv_parts >= 2 && bias_fused && use_gemm(&L->wqkv, n)) {
+                /* q | k (| v) of every token from one GEMM: rows of c->qkv, wqkv.n_out floats apart */
+                TRY(mm(c, c->qkv, c->xb, &L->wqkv, n, L->bq, NULL, 0));
+                q = c->qkv;
+                k = c->qkv + q_dim;
+                qs = ks = L->wqkv.n_out;
+                if (L->qkv_parts == 3) {
+                    v = c->qkv + q_dim + kv_dim;
+                    vs = L->wqkv.n_out;
+                } else {
+                    TRY(mm(c, c->v, c->xb, &L->wv, n, L->bv, NULL, 0));
+                }
+            } else {
+                TRY(mm(c, c->q, c->xb, &L->wq, n, L->bq, NULL, 0));
+                TRY(mm(c, c->k, c->xb, &L->wk, n, L->bk, NULL, 0));
+                TRY(mm(c, c->v, c->xb, &L->wv, n, L->bv, NULL, 0));
+            }
+            TRY(sdy_qk_rope_kv_strided(q, k, v, qs, ks, vs, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos,
+                                       c->rope_sin, pos0, n, in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc,
+                                       vc, head_stride, c->st));
+            TRY(sdy_attention(q, kc, vc, n, in->n_head, in->n_kv_head, hd, pos0 + 1, head_stride, qs, c->part, c->att,
+                              q_dim, c->st));
             TRY(mm(c, c->x, c->att, &L->wo, n, NULL, c->x, 1));
         }
         if (in->n_expert && decode && c->moe_device) {

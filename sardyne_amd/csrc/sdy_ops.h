@@ -14,6 +14,11 @@ int sdy_rmsnorm(const float *x, const float *w, float *out, int n, float eps, in
 int sdy_qk_rope_kv(float *q, float *k, const float *v, const float *qn, const float *kn, float eps,
                    const float *rope_cos, const float *rope_sin, int pos0, int n_tok, int n_head, int n_kv_head, int hd,
                    int interleaved, float *k_cache, float *v_cache, long head_stride, sdy_stream s);
+/* the same with token rows t * q_stride, t * k_stride, t * v_stride floats apart (q|k|v of one GEMM) */
+int sdy_qk_rope_kv_strided(float *q, float *k, const float *v, long q_stride, long k_stride, long v_stride,
+                           const float *qn, const float *kn, float eps, const float *rope_cos, const float *rope_sin,
+                           int pos0, int n_tok, int n_head, int n_kv_head, int hd, int interleaved, float *k_cache,
+                           float *v_cache, long head_stride, sdy_stream s);
 /* Causal attention of n_tok tokens at positions n_kv0 - 1 + t (q rotated, K/V in the cache) in the
  * reference's arithmetic; scores: sdy_attn_scores_floats(n_tok, n_head, n_kv0 + n_tok - 1) floats of
  * device scratch. head_dim 32, 64, 128 or 256. */
