@@ -240,10 +240,12 @@ __global__ void k_dequant_float(const uint8_t *__restrict__ w, int n_in, const i
 
 // ------------------------------------------------------------------------ activation quantisers
 
-// Q8_K (csrc/quant.c:118-144): one wave per 256-element block, lane l holds elements 4l..4l+3.
-// With e.y16 set, also the GEMM's expansion of the block.
-__global__ void k_quant_q8k(const float *__restrict__ x, uint8_t *__restrict__ out, int n_in, SdyGemmExp e) {
-    const int nb = n_in / 256, s = blockIdx.x, t = blockIdx.y, l = threadIdx.x;
+// Q8_K (csrc/quant.c:118-144): one wave per 256-element block (four blocks of a row per 256-thread
+// workgroup), lane l holds elements 4l..4l+3. With e.y16 set, also the GEMM's expansion of the block.
+__global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, uint8_t *__restrict__ out, int n_in,
+                                                   SdyGemmExp e) {
+    const int nb = n_in / 256, s = blockIdx.x * 4 + (threadIdx.x >> 6), t = blockIdx.y, l = threadIdx.x & 63;
+    if (s >= nb) return;  // uniform per wave
     const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)t * n_in + 256 * s + 4 * l);
     const float xs[4] = {v.x, v.y, v.z, v.w};
     const SdyQ8kLane r = sdy_q8k_lane(xs, l);
@@ -1786,7 +1788,7 @@ extern "C" int sdy_quantize(int vtype, const float *x, void *xq, int n_in, int n
     if (n_tok <= 0) return 0;
     if (vtype == SDY_Q8_K) {
         if (n_in % 256) return sdy_fail(-1, "Q8_K rows must be a multiple of 256 (got %d)", n_in);
-        hipLaunchKernelGGL(k_quant_q8k, dim3(n_in / 256, n_tok), dim3(64), 0, st, x, (uint8_t *)xq, n_in,
+        hipLaunchKernelGGL(k_quant_q8k, dim3((n_in / 256 + 3) / 4, n_tok), dim3(256), 0, st, x, (uint8_t *)xq, n_in,
                            SdyGemmExp{nullptr, nullptr, nullptr});
         return sdy_check_launch("quant_q8k");
     }
@@ -1803,8 +1805,8 @@ extern "C" int sdy_quantize(int vtype, const float *x, void *xq, int n_in, int n
 extern "C" int sdy_quantize_gemm(const float *x, void *xq, int n_in, int n_tok, void *ws, sdy_stream s) {
     if (n_tok <= 0) return 0;
     if (n_in % 256) return sdy_fail(-1, "Q8_K rows must be a multiple of 256 (got %d)", n_in);
-    hipLaunchKernelGGL(k_quant_q8k, dim3(n_in / 256, n_tok), dim3(64), 0, (hipStream_t)s, x, (uint8_t *)xq, n_in,
-                       sdy_gemm_exp(ws, n_tok, n_in));
+    hipLaunchKernelGGL(k_quant_q8k, dim3((n_in / 256 + 3) / 4, n_tok), dim3(256), 0, (hipStream_t)s, x, (uint8_t *)xq,
+                       n_in, sdy_gemm_exp(ws, n_tok, n_in));
     return sdy_check_launch("quant_q8k");
 }
 
