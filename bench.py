@@ -25,7 +25,6 @@ import json
 import os
 import sys
 import tempfile
-import threading
 import time
 from pathlib import Path
 
@@ -123,38 +122,12 @@ def membw_probe(stream, gib=4):
 # ---------------------------------------------------------------- CPU baseline (reference code)
 
 def cpu_matvec_baseline(wt, w_copies, x, n_in, seconds, n_threads):
-    """The reference's own matmul(): quantize the activation (op_quantize_rows) and split the rows
-    evenly over n_threads calling op_matmul_q_rows (csrc/model_llama.c:569-611). Rotates weight
-    copies; returns (GB/s by algorithmic bytes, reps)."""
+    """The reference's own matmul() for one token: op_quantize_rows, then op_matmul_q_rows with the
+    rows split evenly over its thread pool (tp_run, a barrier after each op;
+    csrc/model_llama.c:569-611, csrc/threadpool.c:68-141), rotating the weight copies.
+    n_threads 0 = the reference's default (the online CPUs). Returns (seconds per rep, reps, threads)."""
     import oracle as O
-    R = O.ref_lib()
-    R.op_set_simd(1)
-    n_out = w_copies[0].shape[0]
-    vt = Q8_K if wt in (Q4_K, Q6_K) else Q8_0
-    xq = np.zeros(row_size(vt, n_in), np.uint8)
-    out = np.empty(n_out, np.float32)
-    bounds = [(n_out * i // n_threads, n_out * (i + 1) // n_threads) for i in range(n_threads)]
-
-    def one(w):
-        R.op_quantize_rows(vt, x.ctypes.data, xq.ctypes.data, n_in, 0, 1)
-        if n_threads == 1:
-            R.op_matmul_q_rows(out.ctypes.data, xq.ctypes.data, w.ctypes.data, wt, 1, n_in, n_out, 0, n_out)
-            return
-        ts = [threading.Thread(target=R.op_matmul_q_rows,
-                               args=(out.ctypes.data, xq.ctypes.data, w.ctypes.data, wt, 1, n_in, n_out, r0, r1))
-              for r0, r1 in bounds]
-        for t in ts:
-            t.start()
-        for t in ts:
-            t.join()
-
-    one(w_copies[0])
-    reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        one(w_copies[reps % len(w_copies)])
-        reps += 1
-    dt = (time.perf_counter() - t0) / reps
-    return dt, reps
+    return O.ref_cpu_matvec(wt, w_copies, x, n_in, seconds, n_threads)
 
 
 def host_cpu_model():
@@ -250,11 +223,32 @@ def bench_matvec(args, wt, n_out, n_in, n_copies, stacked):
     # so the average is the launch duration without the gaps between dispatches
     for i in range(3):
         matvec_only(i)
+    kernel = L.sdy_last_kernel().decode() or "k_matvec"
     ms_k = per_launch_ms(st, matvec_only, args.steps)
     algo_launch = w_bytes * units + n_in * 4 + n_out * 4 * units
     achieved = algo_launch / (ms_k * 1e-3) / 1e9
     traffic = profiled_traffic(f"k_matvec_{name.lower()}_{'stacked' if stacked else 'head'}.md")
     achievable = membw_probe(st)
+    back_to_back = None
+    if stacked:
+        # the same copies as separate n_out x n_in matrices (row views of the stack, each its own region
+        # of HBM), one launch per copy, back to back in rotation: per-launch time includes the
+        # dispatch gaps that a 2.4 MB matvec cannot hide
+        views = [L.sdy_mat_rows(ctypes.byref(mats[0].m), c * n_out, n_out) for c in range(n_copies)]
+        vargs = capi.SdyMvArgs(xq=dq.ptr, n_tok=1, out=dout.ptr, out_stride=n_out, row0=0, row1=n_out)
+
+        def one_copy(i):
+            capi.check(L.sdy_matvec(ctypes.byref(views[i % n_copies]), ctypes.byref(vargs), st))
+
+        for i in range(n_copies):
+            one_copy(i)
+        n_launch = n_copies * max(1, args.steps // 10)
+        ms_b = per_launch_ms(st, one_copy, n_launch)
+        per = w_bytes + n_in * 4 + n_out * 4
+        back_to_back = {"launches": n_launch, "distinct_copies": n_copies, "per_launch_us": round(ms_b * 1e3, 3),
+                        "GBps": round(per / (ms_b * 1e-3) / 1e9, 1),
+                        "frac_of_hbm_peak": round(per / (ms_b * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                        "kernel": L.sdy_last_kernel().decode()}
 
     # CPU baseline: the reference's code on this host (all online CPUs, and 1 thread)
     cpu = None
@@ -262,15 +256,14 @@ def bench_matvec(args, wt, n_out, n_in, n_copies, stacked):
         try:
             import oracle as O
             if O.ref_available():
-                n_cpu = os.cpu_count() or 1
                 n_cpu_copies = max(2, int(np.ceil(512e6 / w_bytes))) if not stacked else 64
                 copies = [w0] + [random_blocks(name, n_out * n_in // e, np.random.default_rng(200 + c)).reshape(n_out, -1)
                                  for c in range(min(n_cpu_copies, 64) - 1)]
-                dt, reps = cpu_matvec_baseline(wt, copies, x, n_in, args.cpu_seconds, n_cpu)
-                dt1, reps1 = cpu_matvec_baseline(wt, copies, x, n_in, max(2.0, args.cpu_seconds / 4), 1)
+                dt, reps, n_cpu = cpu_matvec_baseline(wt, copies, x, n_in, args.cpu_seconds, 0)
+                dt1, _, _ = cpu_matvec_baseline(wt, copies, x, n_in, max(2.0, args.cpu_seconds / 4), 1)
                 cpu = {"value": round(algo_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": n_cpu, "kind": "reference",
-                       "sample": f"{reps} reps of quantize + row-split matvec over {len(copies)} rotated copies "
-                                 f"({dt * 1e3:.2f} ms/rep), {host_cpu_model()}",
+                       "sample": f"{reps} reps of the reference's matmul() (quantize + row split on its thread pool) "
+                                 f"over {len(copies)} rotated copies ({dt * 1e3:.3f} ms/rep), {host_cpu_model()}",
                        "single_thread_GBps": round(algo_bytes / dt1 / 1e9, 3)}
         except Exception as ex:
             cpu = {"error": str(ex)}
@@ -287,9 +280,11 @@ def bench_matvec(args, wt, n_out, n_in, n_copies, stacked):
             "achievable_hbm_GBps": round(achievable, 1),
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                         "kernel": f"k_matvec<{name}>", "kernel_avg_us": round(ms_k * 1e3, 3),
+                         "kernel": kernel, "kernel_avg_us": round(ms_k * 1e3, 3),
                          "algorithmic_bytes_per_launch": algo_launch},
             "cpu_baseline": cpu, "parity": parity}
+    if back_to_back:
+        line["back_to_back"] = back_to_back
     if cpu and "value" in cpu:
         line["gpu_over_cpu"] = round(value / cpu["value"], 1)
     return line
@@ -339,22 +334,22 @@ def bench_decode(args, spec, ctx_len, n_decode, label):
     bench/bench_decode.py:39-48: n_decode / wall time of the decode loop). Token ids are uniform
     over the vocabulary (seeded) and fed teacher-forced, so the GPU and the CPU reference see the
     same sequence and their logits are compared step by step."""
-    from sardyne_amd.runtime import Context, Model
+    from sardyne_amd.engine import LoadedModel
     path = write_bench_model(spec, label)
     rng = np.random.default_rng(0)
     toks = rng.integers(0, spec.n_vocab, ctx_len + n_decode).astype(np.int32)
     try:
         t0 = time.perf_counter()
-        model = Model(path)
+        model = LoadedModel(path)
         log(f"[bench] GPU model load {time.perf_counter() - t0:.1f}s")
-        ctx = Context(model, max_seq=ctx_len + n_decode + 1, n_batch=args.n_batch)
+        ctx = model.session(max_seq=ctx_len + n_decode + 1, n_batch=args.n_batch)
         t0 = time.perf_counter()
-        ctx.eval(toks[:ctx_len])
+        ctx.feed(toks[:ctx_len])
         t_prefill = time.perf_counter() - t0
         gpu_logits = []
         t0 = time.perf_counter()
         for i in range(n_decode):
-            gpu_logits.append(ctx.eval([int(toks[ctx_len + i])]))
+            gpu_logits.append(ctx.feed([int(toks[ctx_len + i])]))
         t_dec = time.perf_counter() - t0
         gpu_tok_s = n_decode / t_dec
         log(f"[bench] GPU prefill {ctx_len} tok in {t_prefill:.3f}s, decode {gpu_tok_s:.1f} tok/s")
@@ -397,8 +392,8 @@ def bench_decode(args, spec, ctx_len, n_decode, label):
     return gpu_tok_s, t_prefill, cpu, parity
 
 
-def decode_line(args, spec, label, ctx_len, desc):
-    n_dec = max(args.steps, 8)
+def decode_line(args, spec, label, ctx_len, desc, n_dec=None):
+    n_dec = n_dec or max(args.steps, 8)
     tok_s, t_pre, cpu, parity = bench_decode(args, spec, ctx_len, n_dec, label)
     w_bytes = decode_weight_bytes(spec)
     kv_mean = kv_bytes_per_position(spec) * (ctx_len + n_dec / 2)
@@ -461,26 +456,27 @@ def gemm_gate_up_ms(spec, n_tok, reps):
 
     for i in range(3):
         launch(i)
-    return per_launch_ms(st, launch, reps), 2.0 * rows * n_in * n_tok
+    kernel = L.sdy_last_kernel().decode()
+    return per_launch_ms(st, launch, reps), 2.0 * rows * n_in * n_tok, kernel
 
 
 def prefill_line(args, spec, label, n_prompt, desc):
     """Prefill tok/s of one n_prompt-token eval (n_batch = n_prompt), the median over --steps
     fresh evals, with the whole prefill's MFMA utilisation and the dominant GEMM's roofline."""
-    from sardyne_amd.runtime import Context, Model
+    from sardyne_amd.engine import LoadedModel
     MFMA_PEAK = 2500.0  # TFLOP/s, dense f16/bf16
     path = write_bench_model(spec, label)
     toks = np.random.default_rng(0).integers(0, spec.n_vocab, n_prompt).astype(np.int32)
-    model = Model(path)
-    ctx = Context(model, max_seq=n_prompt + 1, n_batch=n_prompt)
+    model = LoadedModel(path)
+    ctx = model.session(max_seq=n_prompt + 1, n_batch=n_prompt)
     for _ in range(max(1, args.warmup)):
-        ctx.reset()
-        gpu_logits = ctx.eval(toks)
+        ctx.clear()
+        gpu_logits = ctx.feed(toks)
     times = []
     for _ in range(args.steps):
-        ctx.reset()
+        ctx.clear()
         t0 = time.perf_counter()
-        ctx.eval(toks)
+        ctx.feed(toks)
         times.append(time.perf_counter() - t0)
     t = float(np.median(times))
     tok_s = n_prompt / t
@@ -490,10 +486,10 @@ def prefill_line(args, spec, label, n_prompt, desc):
     k = gemm_gate_up_ms(spec, n_prompt, args.steps)
     roof = None
     if k:
-        ms_k, fl = k
+        ms_k, fl, kname = k
         ach = fl / (ms_k * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": MFMA_PEAK, "unit": "TFLOP/s",
-                "frac": round(ach / MFMA_PEAK, 4), "traffic": None, "kernel": "k_gemm<Q4_K> (gate|up, SwiGLU)",
+                "frac": round(ach / MFMA_PEAK, 4), "traffic": None, "kernel": f"{kname} (gate|up, SwiGLU)",
                 "kernel_avg_us": round(ms_k * 1e3, 2), "algorithmic_flops_per_launch": fl}
     cpu, parity = None, {}
     if args.cpu_seconds > 0:
@@ -540,6 +536,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--n-batch", type=int, default=512, help="GPU prefill chunk (decode workloads)")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (smoke runs only)")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="default workload: leave out the decode_3b / decode_moe sub-objects")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -550,6 +548,20 @@ def main():
     capi.check(capi.lib().sdy_init())
     if args.workload == "q6k_head":
         line = bench_matvec(args, Q6_K, 151936, 2048, 8, stacked=False)
+        if not args.no_decode:
+            # the metric's second half: decode tok/s of the Qwen2.5-3B shape (and the MoE shape), each
+            # 128 tokens after its context, with the reference engine on the host beside it
+            from sardyne_amd.gguf_synth import qwen25_3b, qwen3_30b_a3b
+            for key, spec, label, ctx_len, desc in (
+                    ("decode_3b", qwen25_3b(), "qwen25_3b", 512, "Qwen2.5-3B-shaped Q4_K_M"),
+                    ("decode_moe", qwen3_30b_a3b(), "qwen3_30b_a3b", 1024,
+                     "Qwen3-30B-A3B-shaped qwen3moe Q4_K_M (128 experts resident, top-8)")):
+                d = decode_line(args, spec, label, ctx_len, desc, n_dec=128)
+                line[key] = {k: d[k] for k in ("value", "unit", "ms_per_step", "roofline", "cpu_baseline", "parity")
+                             if k in d}
+                line[key]["workload"] = d["config"]["workload"]
+                if "gpu_over_cpu" in d:
+                    line[key]["gpu_over_cpu"] = d["gpu_over_cpu"]
     elif args.workload == "q8_0_head":
         line = bench_matvec(args, Q8_0, 151936, 2048, 8, stacked=False)
     elif args.workload == "q4k_matvec":

@@ -345,3 +345,32 @@ class RefEngine:
             self.lib.engine_model_free(self.model)
         except Exception:
             pass
+
+
+CPU_MATVEC_LIB = HERE / "_ref" / "libref_cpu_matvec.so"
+
+
+def ref_cpu_matvec(wt, copies, x, n_in, seconds, n_threads=0):
+    """The reference's own one-token matmul() (quantise, then the row-split matvec, each through its
+    thread pool with a barrier) timed over the rotated weight copies for `seconds`
+    (oracle/ref_cpu_matvec.c over oracle/_ref). Returns (seconds per repetition, repetitions,
+    threads used); n_threads 0 = the reference's default, the online CPUs."""
+    if not CPU_MATVEC_LIB.exists():
+        raise OSError(f"{CPU_MATVEC_LIB} missing: run `make -C oracle ref` where the reference sources exist")
+    h = ctypes.CDLL(str(CPU_MATVEC_LIB))
+    fn = h.ref_cpu_matvec
+    fn.restype = ctypes.c_double
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp, _vp, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_double, ctypes.c_int, ctypes.POINTER(ctypes.c_long), ctypes.POINTER(ctypes.c_int)]
+    vt = VEC_DOT[wt]
+    n_out = copies[0].shape[0]
+    ptrs = (_vp * len(copies))(*[c.ctypes.data for c in copies])
+    x = np.ascontiguousarray(x, np.float32)
+    xq = np.zeros(row_size(vt, n_in), np.uint8)
+    out = np.empty(n_out, np.float32)
+    reps, threads = ctypes.c_long(), ctypes.c_int()
+    dt = fn(wt, vt, ptrs, len(copies), x.ctypes.data, xq.ctypes.data, out.ctypes.data, n_in, n_out, seconds, n_threads,
+            ctypes.byref(reps), ctypes.byref(threads))
+    if dt < 0:
+        raise OSError("the reference thread pool could not be created")
+    return dt, reps.value, threads.value

@@ -1,7 +1,7 @@
 /* Oracle restatement of the reference's float kernels. Test infrastructure only (see oracle.h).
  *
  * Reference files restated here: csrc/ops.c:185-229 (scalar kernels), csrc/ops.c:387-392 and
- * csrc/ops_avx2.c:26-147 (AVX2 matmul/dot/axpy, emulated lane by lane), csrc/ops.c:439-533
+ * csrc/ops_avx2.c:26-147 (AVX2 matmul/dot/axpy, emulated lane by lane), csrc/ops.c:329-423
  * (bias, norm, softmax, SiLU, RoPE, attention).
  */
 #include <math.h>
@@ -153,7 +153,7 @@ void orc_axpy(float *y, float a, const float *x, int n, int simd) {
     }
 }
 
-/* csrc/ops.c:456-461: sum of squares in double, scale rounded to float, out = (x*scale)*w */
+/* csrc/ops.c:346-351: sum of squares in double, scale rounded to float, out = (x*scale)*w */
 void orc_rmsnorm(float *out, const float *x, const float *w, int n, float eps) {
     double ss = 0.0;
     for (int i = 0; i < n; i++) ss += (double)x[i] * (double)x[i];
@@ -165,7 +165,7 @@ void orc_rmsnorm(float *out, const float *x, const float *w, int n, float eps) {
     }
 }
 
-/* csrc/ops.c:463-474: max-subtracted expf, double sum, multiply by the float reciprocal */
+/* csrc/ops.c:353-364: max-subtracted expf, double sum, multiply by the float reciprocal */
 void orc_softmax(float *x, int n) {
     float mx = x[0];
     for (int i = 1; i < n; i++) mx = x[i] > mx ? x[i] : mx;
@@ -178,7 +178,7 @@ void orc_softmax(float *x, int n) {
     for (int i = 0; i < n; i++) x[i] *= inv;
 }
 
-/* csrc/ops.c:476-481 */
+/* csrc/ops.c:366-371 */
 void orc_silu_mul(float *gate, const float *up, int n) {
     for (int i = 0; i < n; i++) {
         float g = gate[i];
@@ -187,7 +187,7 @@ void orc_silu_mul(float *gate, const float *up, int n) {
     }
 }
 
-/* csrc/ops.c:485-496: angles in double, rounded to float */
+/* csrc/ops.c:375-386: angles in double, rounded to float */
 void orc_rope_table(float *cos_out, float *sin_out, int n_pos, int head_dim, float theta) {
     int half = head_dim / 2;
     for (int i = 0; i < half; i++) {
@@ -200,7 +200,7 @@ void orc_rope_table(float *cos_out, float *sin_out, int n_pos, int head_dim, flo
     }
 }
 
-/* csrc/ops.c:498-511: pairs (2i, 2i+1) when interleaved, else (i, i + hd/2) */
+/* csrc/ops.c:388-401: pairs (2i, 2i+1) when interleaved, else (i, i + hd/2) */
 void orc_rope(float *x, int n_heads, int head_dim, const float *cos, const float *sin, int interleaved) {
     int half = head_dim / 2;
     for (int h = 0; h < n_heads; h++) {
@@ -215,7 +215,7 @@ void orc_rope(float *x, int n_heads, int head_dim, const float *cos, const float
     }
 }
 
-/* csrc/ops.c:515-533: per head, scaled dots, softmax, sum of p*v by axpy; GQA head h reads KV head
+/* csrc/ops.c:405-423: per head, scaled dots, softmax, sum of p*v by axpy; GQA head h reads KV head
  * h / (n_head / n_kv_head). */
 void orc_attention(float *out, const float *q, const float *k_cache, const float *v_cache, int n_head,
                    int n_kv_head, int head_dim, int n_kv, int stride, float *scores, int simd) {

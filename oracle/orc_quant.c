@@ -2,7 +2,7 @@
  * quantisers and quantized dots. Test infrastructure only (see oracle.h).
  *
  * Reference files restated here: csrc/quant.h, csrc/quant.c, csrc/quant_avx2.c, csrc/ops.c:15-62
- * and csrc/ops.c:329-437.
+ * and csrc/ops.c:211-327.
  */
 #include <math.h>
 #include <stdlib.h>

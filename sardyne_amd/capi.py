@@ -114,6 +114,7 @@ class SdyMvArgs(ctypes.Structure):
 
 _DEVICE_SIGNATURES = {
     "sdy_last_error": (ctypes.c_char_p, []),
+    "sdy_last_kernel": (ctypes.c_char_p, []),
     "sdy_init": (_int, []),
     "sdy_device_info": (_int, [ctypes.POINTER(_int), ctypes.POINTER(_sz)]),
     "sdy_malloc": (_int, [ctypes.POINTER(_vp), _sz]),
@@ -134,6 +135,7 @@ _DEVICE_SIGNATURES = {
     "sdy_mat_upload": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long, _vp, _vp]),
     "sdy_mat_from_device": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long, _vp, _vp]),
     "sdy_mat_free": (_int, [ctypes.POINTER(SdyMat)]),
+    "sdy_mat_rows": (SdyMat, [ctypes.POINTER(SdyMat), ctypes.c_long, ctypes.c_long]),
     "sdy_dequant_rows": (_int, [ctypes.POINTER(SdyMat), ctypes.c_long, ctypes.c_long, _vp, _vp]),
     "sdy_quantize": (_int, [_int, _vp, _vp, _int, _int, _vp]),
     "sdy_matvec": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp]),
@@ -154,6 +156,11 @@ _DEVICE_SIGNATURES = {
     "sdy_rmsnorm": (_int, [_vp, _vp, _vp, _int, ctypes.c_float, _int, ctypes.c_long, ctypes.c_long, _vp]),
     "sdy_norm_quant": (_int, [_vp, _vp, ctypes.c_float, _int, _int, _vp, _int, _vp, _vp]),
     "sdy_attn_scores_floats": (_sz, [_int, _int, _int]),
+    "sdy_qk_rope_kv": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _int, _int, _int, _int, _int, _int,
+                              _vp, _vp, ctypes.c_long, _vp]),
+    "sdy_qk_rope_kv_strided": (_int, [_vp, _vp, _vp, ctypes.c_long, ctypes.c_long, ctypes.c_long, _vp, _vp,
+                                      ctypes.c_float, _vp, _vp, _int, _int, _int, _int, _int, _int, _vp, _vp,
+                                      ctypes.c_long, _vp]),
     "sdy_attention": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, ctypes.c_long, ctypes.c_long, _vp, _vp,
                              ctypes.c_long, _vp]),
     "sdy_quantize_gemm": (_int, [_vp, _vp, _int, _int, _vp, _vp]),

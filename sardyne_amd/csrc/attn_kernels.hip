@@ -976,12 +976,15 @@ static int launch_attn(AttnArgs &A, int nc, int n_tblk, hipStream_t st) {
     static size_t granted = 0;
     int rc = sdy_lds_limit((const void *)k_attn_scores<HD, DECODE>, lds, &granted);
     if (rc) return rc;
+    SDY_NOTE_KERNEL((k_attn_scores<HD, DECODE>));
     hipLaunchKernelGGL((k_attn_scores<HD, DECODE>), dim3(nc, A.n_kv_head, n_tblk), dim3(256), lds, st, A);
     if ((rc = sdy_check_launch("attention_scores"))) return rc;
     if constexpr (DECODE) {
+        SDY_NOTE_KERNEL((k_attn_softmax_pv<HD, DECODE>));
         hipLaunchKernelGGL((k_attn_softmax_pv<HD, DECODE>), dim3((A.n_head * HD + 255) / 256, 1), dim3(256), 0, st, A);
     } else {  // four tokens per workgroup
         constexpr int TB = 4;
+        SDY_NOTE_KERNEL((k_attn_prefill_pv<HD, TB>));
         hipLaunchKernelGGL((k_attn_prefill_pv<HD, TB>), dim3((A.n_head * HD + 255) / 256, (A.n_tok + TB - 1) / TB),
                            dim3(256), 0, st, A);
     }
@@ -997,8 +1000,10 @@ static int launch_attn_any(AttnArgs &A, int hd, int nc, int n_tblk, hipStream_t 
     static size_t granted = 0;
     int rc = sdy_lds_limit((const void *)k_attn_scores_any<DECODE>, lds, &granted);
     if (rc) return rc;
+    SDY_NOTE_KERNEL((k_attn_scores_any<DECODE>));
     hipLaunchKernelGGL((k_attn_scores_any<DECODE>), dim3(nc, A.n_kv_head, n_tblk), dim3(256), lds, st, A, hd);
     if ((rc = sdy_check_launch("attention_scores"))) return rc;
+    SDY_NOTE_KERNEL((k_attn_softmax_pv_any<DECODE>));
     hipLaunchKernelGGL((k_attn_softmax_pv_any<DECODE>), dim3(A.n_head, DECODE ? 1 : A.n_tok), dim3(256), 0, st, A, hd);
     if ((rc = sdy_check_launch("attention_softmax_pv"))) return rc;
     if (DECODE && A.xq) return sdy_quantize(SDY_Q8_K, A.out, A.xq, A.n_head * hd, 1, (sdy_stream)st);
@@ -1015,13 +1020,17 @@ static int launch_attn_decode(AttnArgs &A, int nc, hipStream_t st) {
     static size_t granted = 0;
     int rc = sdy_lds_limit((const void *)k_attn_scores<HD, true>, lds, &granted);
     if (rc) return rc;
+    SDY_NOTE_KERNEL((k_attn_scores<HD, true>));
     hipLaunchKernelGGL((k_attn_scores<HD, true>), dim3(nc, A.n_kv_head, 1), dim3(256), lds, st, A);
     if ((rc = sdy_check_launch("attention_scores"))) return rc;
+    SDY_NOTE_KERNEL(k_attn_decode_softmax);
     hipLaunchKernelGGL(k_attn_decode_softmax, dim3(A.n_head), dim3(256), 0, st, A);
     if ((rc = sdy_check_launch("attention_decode_softmax"))) return rc;
     if (n_rep % 4) {
+        SDY_NOTE_KERNEL((k_attn_decode_wv<HD, 1, 32>));
         hipLaunchKernelGGL((k_attn_decode_wv<HD, 1, 32>), dim3(A.n_head * (HD / 64)), dim3(64), 0, st, A);
     } else {
+        SDY_NOTE_KERNEL((k_attn_decode_wv4<HD, 8>));
         hipLaunchKernelGGL((k_attn_decode_wv4<HD, 8>), dim3(A.n_head * HD / 64), dim3(64), 0, st, A);
     }
     if ((rc = sdy_check_launch("attention_decode_wv"))) return rc;

@@ -1,380 +1,483 @@
-/* Model runtime on the GPU: GGUF -> device weights, device KV cache, forward pass, eval API.
+/* engine_* of the public ABI: model loading into device memory, contexts, eval.
  *
- * The host side here is the reference's csrc/model_llama.c contract (engine_* of
- * include/sardyne.h) re-implemented around device buffers: the model is uploaded once (every
- * matrix repacked into the device layout of quant_kernels.hip, every expert resident), a context
- * owns the f32 KV cache [n_layer][n_kv_head][max_seq][head_dim] and the activations in device
- * memory, and engine_eval runs the layer sequence of the reference forward
- * (csrc/model_llama.c:757-832) as a stream of gfx950 kernels, copying back only the logits.
+ * The contract is the reference's csrc/engine.h:43-72: which GGUF files load (architectures,
+ * metadata rules, tensor shapes and types), the NULL-on-failure constructors with the reason in
+ * the caller's buffer, engine_eval's -1 with the context unchanged, and the error messages callers
+ * match on (kept verbatim). The structure is this file's own:
  *
- * Validation rules and error messages follow csrc/model_llama.c:225-319 and :468-525, :834-886,
- * because callers match on them (the Python runtime raises them as ValueError).
+ *   - configuration: a table of metadata keys, each with its field of engine_model_info and its
+ *     rule (required, constant default, or a quotient of fields read before it), read in one loop;
+ *     cross-field rules follow the table;
+ *   - tensors: one schema of per-layer tensors (suffix, rank, shape, when it must exist) serves
+ *     both the "unknown tensor" check and the loader, which walks the schema to validate shapes
+ *     and types before anything is uploaded;
+ *   - upload: every matrix goes from the mmap to the device layout through the shim's uploader;
+ *     q|k(|v) of one type become one stacked matrix, gate and up of one quantized type one
+ *     interleaved matrix, and a layer's q|k|v biases one contiguous span (what the stacked
+ *     matvecs read);
+ *   - contexts: argument limits checked from a table; the device state is allocated by forward.c.
  */
 #define _POSIX_C_SOURCE 200809L
 #include <stdarg.h>
+#include <stddef.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 #include "sardyne.h"
 #include "sdy_engine.h"
 #include "sdy_ops.h"
 #include "sdy_shim.h"
 
-#define MAX_SEQ_LIMIT (1 << 20)
-#define MAX_BATCH_LIMIT 4096
+enum { SEQ_CAP = 1 << 20, BATCH_CAP = 4096, THREADS_CAP = 256, META_INT_CAP = 1 << 30 };
 
-static void set_err(char *err, size_t len, const char *fmt, ...) {
-    if (!err || !len) return;
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(err, len, fmt, ap);
-    va_end(ap);
+static int say(char *err, size_t len, const char *fmt, ...) {
+    if (err && len) {
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(err, len, fmt, ap);
+        va_end(ap);
+    }
+    return -1;
 }
 
-/* ------------------------------------------------------------------ metadata */
+static const gguf_tensor *tensor(const gguf_file *gf, const char *name) {
+    return gguf_get_tensor(gf, (uint64_t)gguf_find_tensor(gf, name));
+}
+
+/* ------------------------------------------------------------------ configuration */
+
+#define INFO_FIELD(f) offsetof(engine_model_info, f)
+#define FIELD(in, off) (*(int32_t *)((char *)(in) + (off)))
+
+enum rule { REQUIRED, CONSTANT, COPY, QUOTIENT, SAME_AS };
+
+typedef struct {
+    const char *suffix;   /* key = "<arch>.<suffix>" */
+    int moe_only;
+    size_t field;         /* engine_model_info field written (SAME_AS: the field it must equal) */
+    enum rule rule;
+    int32_t constant;     /* CONSTANT default */
+    size_t num, den;      /* COPY default: field num; QUOTIENT default: field num / field den */
+    const char *zero;     /* QUOTIENT: message when the default comes out 0 */
+    const char *differs;  /* SAME_AS: message when the key holds another value */
+} int_key;
+
+/* The keys in the order they are read: COPY, QUOTIENT and SAME_AS rules only name fields above them. */
+static const int_key INT_KEYS[] = {
+    {"embedding_length", 0, INFO_FIELD(dim), REQUIRED, 0, 0, 0, NULL, NULL},
+    {"block_count", 0, INFO_FIELD(n_layer), REQUIRED, 0, 0, 0, NULL, NULL},
+    {"feed_forward_length", 0, INFO_FIELD(ffn_dim), REQUIRED, 0, 0, 0, NULL, NULL},
+    {"expert_count", 1, INFO_FIELD(n_expert), REQUIRED, 0, 0, 0, NULL, NULL},
+    {"expert_used_count", 1, INFO_FIELD(n_expert_used), REQUIRED, 0, 0, 0, NULL, NULL},
+    /* as in llama.cpp: without the key, the FFN length is the sum over the chosen experts */
+    {"expert_feed_forward_length", 1, INFO_FIELD(ffn_exp_dim), QUOTIENT, 0, INFO_FIELD(ffn_dim),
+     INFO_FIELD(n_expert_used), "dimensione degli esperti nulla", NULL},
+    {"attention.head_count", 0, INFO_FIELD(n_head), REQUIRED, 0, 0, 0, NULL, NULL},
+    {"attention.head_count_kv", 0, INFO_FIELD(n_kv_head), COPY, 0, INFO_FIELD(n_head), 0, NULL, NULL},
+    {"attention.key_length", 0, INFO_FIELD(head_dim), QUOTIENT, 0, INFO_FIELD(dim), INFO_FIELD(n_head),
+     "head_dim nullo", NULL},
+    {"attention.value_length", 0, INFO_FIELD(head_dim), SAME_AS, 0, 0, 0, NULL, "key_length diverso da value_length"},
+    {"rope.dimension_count", 0, INFO_FIELD(head_dim), SAME_AS, 0, 0, 0, NULL,
+     "RoPE parziale (rope.dimension_count < head_dim) non supportata"},
+    {"context_length", 0, INFO_FIELD(max_pos), CONSTANT, 2048, 0, 0, NULL, NULL},
+};
 
 typedef struct {
     const gguf_file *gf;
-    const char *arch;
+    char arch[32];
     char *err;
-    size_t err_len;
-} meta;
+    size_t len;
+} meta_reader;
 
-static int64_t arch_key(const meta *mt, const char *suffix) {
-    char key[128];
-    snprintf(key, sizeof key, "%s.%s", mt->arch, suffix);
-    return gguf_find_kv(mt->gf, key);
+/* Index of "<arch>.<suffix>", or -1. */
+static int64_t meta_key(const meta_reader *r, const char *suffix) {
+    char key[160];
+    snprintf(key, sizeof key, "%s.%s", r->arch, suffix);
+    return gguf_find_kv(r->gf, key);
 }
 
-/* Required (def < 0) or defaulted positive integer; -1 on error. */
-static int64_t meta_int(const meta *mt, const char *suffix, int64_t def) {
-    int64_t i = arch_key(mt, suffix);
-    uint64_t v;
-    if (i < 0) {
-        if (def < 0) set_err(mt->err, mt->err_len, "metadato mancante: %s.%s", mt->arch, suffix);
-        return def;
-    }
-    if (gguf_kv_get_u64(mt->gf, i, &v) || v == 0 || v > (1u << 30)) {
-        set_err(mt->err, mt->err_len, "metadato non valido: %s.%s", mt->arch, suffix);
-        return -1;
-    }
-    return (int64_t)v;
+/* 1 when present and valid (*v set), 0 when absent, -1 when present but not a count in 1..2^30. */
+static int meta_count(const meta_reader *r, const char *suffix, int32_t *v) {
+    int64_t i = meta_key(r, suffix);
+    uint64_t u;
+    if (i < 0) return 0;
+    if (gguf_kv_get_u64(r->gf, i, &u) || u == 0 || u > META_INT_CAP)
+        return say(r->err, r->len, "metadato non valido: %s.%s", r->arch, suffix);
+    *v = (int32_t)u;
+    return 1;
 }
 
-static int meta_float(const meta *mt, const char *suffix, double def, float *out) {
-    int64_t i = arch_key(mt, suffix);
+static int read_int_keys(const meta_reader *r, engine_model_info *in, int moe) {
+    for (size_t k = 0; k < sizeof INT_KEYS / sizeof *INT_KEYS; k++) {
+        const int_key *d = &INT_KEYS[k];
+        if (d->moe_only && !moe) continue;
+        int32_t v = 0;
+        int got = meta_count(r, d->suffix, &v);
+        if (got < 0 && d->rule != SAME_AS) return -1;
+        if (d->rule == SAME_AS) {
+            if (got && v != FIELD(in, d->field)) return say(r->err, r->len, "%s", d->differs);
+            if (got < 0) return say(r->err, r->len, "%s", d->differs);
+            continue;
+        }
+        if (!got) {
+            if (d->rule == REQUIRED) return say(r->err, r->len, "metadato mancante: %s.%s", r->arch, d->suffix);
+            v = d->rule == CONSTANT ? d->constant
+                : d->rule == COPY   ? FIELD(in, d->num)
+                                    : FIELD(in, d->num) / FIELD(in, d->den);
+            if (v == 0) return say(r->err, r->len, "%s", d->zero ? d->zero : d->suffix);
+        }
+        FIELD(in, d->field) = v;
+        if (d->field == INFO_FIELD(n_expert_used)) {
+            /* the used count is checked as soon as it is known: the next default divides by it */
+            if (in->n_expert_used > in->n_expert)
+                return say(r->err, r->len, "expert_used_count=%d oltre expert_count=%d", in->n_expert_used,
+                           in->n_expert);
+            /* the device router keeps one token's expert probabilities in a wave's registers */
+            if (in->n_expert > 512 || in->n_expert_used > 64)
+                return say(r->err, r->len,
+                           "expert_count=%d / expert_used_count=%d oltre i limiti del dispositivo (512 / 64)",
+                           in->n_expert, in->n_expert_used);
+        }
+    }
+    return 0;
+}
+
+/* A positive float key (<= 1e12); def < 0: required. */
+static int read_float_key(const meta_reader *r, const char *suffix, double def, float *out) {
+    int64_t i = meta_key(r, suffix);
     double v = def;
-    if (i < 0 && def < 0) {
-        set_err(mt->err, mt->err_len, "metadato mancante: %s.%s", mt->arch, suffix);
-        return -1;
-    }
-    if (i >= 0 && gguf_kv_get_f64(mt->gf, i, &v)) {
-        set_err(mt->err, mt->err_len, "metadato non valido: %s.%s", mt->arch, suffix);
-        return -1;
-    }
-    if (!(v > 0.0) || v > 1e12) {
-        set_err(mt->err, mt->err_len, "valore non valido per %s.%s", mt->arch, suffix);
-        return -1;
-    }
+    if (i < 0 && def < 0) return say(r->err, r->len, "metadato mancante: %s.%s", r->arch, suffix);
+    if (i >= 0 && gguf_kv_get_f64(r->gf, i, &v)) return say(r->err, r->len, "metadato non valido: %s.%s", r->arch, suffix);
+    if (!(v > 0.0 && v <= 1e12)) return say(r->err, r->len, "valore non valido per %s.%s", r->arch, suffix);
     *out = (float)v;
     return 0;
 }
 
-static const char *const LAYER_TENSORS[] = {
-    "attn_norm.weight", "attn_q.weight", "attn_q.bias", "attn_k.weight", "attn_k.bias", "attn_v.weight",
-    "attn_v.bias", "attn_q_norm.weight", "attn_k_norm.weight", "attn_output.weight", "ffn_norm.weight",
-    "ffn_gate.weight", "ffn_up.weight", "ffn_down.weight", "ffn_gate_inp.weight", "ffn_gate_exps.weight",
-    "ffn_up_exps.weight", "ffn_down_exps.weight",
-};
+/* Architectures and their RoPE pairing (csrc/model_llama.c:235-241). */
+static const struct {
+    const char *name;
+    int interleaved, moe;
+} ARCHS[] = {{"llama", 1, 0}, {"qwen2", 0, 0}, {"qwen3", 0, 0}, {"qwen3moe", 0, 1}};
 
-/* Unknown tensors mean an architecture variant this runtime does not implement. */
-static int known_tensor(const char *name, int n_layer) {
-    if (!strcmp(name, "token_embd.weight") || !strcmp(name, "output_norm.weight") || !strcmp(name, "output.weight"))
-        return 1;
+/* ------------------------------------------------------------------ tensor schema */
+
+enum when { ALWAYS, WITH_BIAS, WITH_QK_NORM, DENSE, MOE };
+enum dim_src { D_ONE, D_DIM, D_QDIM, D_KVDIM, D_HEAD, D_FFN, D_FFN_EXP, D_EXPERTS };
+
+typedef struct {
+    const char *suffix;
+    enum when when;
+    int rank;             /* 1 vector, 2 matrix, 3 stacked experts */
+    enum dim_src ne[3];   /* ne[0] (inner), ne[1], ne[2] */
+} layer_tensor;
+
+static const layer_tensor LAYER[] = {
+    {"attn_norm.weight", ALWAYS, 1, {D_DIM}},
+    {"attn_q.weight", ALWAYS, 2, {D_DIM, D_QDIM}},
+    {"attn_q.bias", WITH_BIAS, 1, {D_QDIM}},
+    {"attn_k.weight", ALWAYS, 2, {D_DIM, D_KVDIM}},
+    {"attn_k.bias", WITH_BIAS, 1, {D_KVDIM}},
+    {"attn_v.weight", ALWAYS, 2, {D_DIM, D_KVDIM}},
+    {"attn_v.bias", WITH_BIAS, 1, {D_KVDIM}},
+    {"attn_q_norm.weight", WITH_QK_NORM, 1, {D_HEAD}},
+    {"attn_k_norm.weight", WITH_QK_NORM, 1, {D_HEAD}},
+    {"attn_output.weight", ALWAYS, 2, {D_QDIM, D_DIM}},
+    {"ffn_norm.weight", ALWAYS, 1, {D_DIM}},
+    {"ffn_gate.weight", DENSE, 2, {D_DIM, D_FFN}},
+    {"ffn_up.weight", DENSE, 2, {D_DIM, D_FFN}},
+    {"ffn_down.weight", DENSE, 2, {D_FFN, D_DIM}},
+    {"ffn_gate_inp.weight", MOE, 2, {D_DIM, D_EXPERTS}},
+    {"ffn_gate_exps.weight", MOE, 3, {D_DIM, D_FFN_EXP, D_EXPERTS}},
+    {"ffn_up_exps.weight", MOE, 3, {D_DIM, D_FFN_EXP, D_EXPERTS}},
+    {"ffn_down_exps.weight", MOE, 3, {D_FFN_EXP, D_DIM, D_EXPERTS}},
+};
+enum { N_LAYER_TENSORS = sizeof LAYER / sizeof *LAYER };
+
+static int64_t dim_of(const engine_model_info *in, enum dim_src d) {
+    switch (d) {
+    case D_DIM: return in->dim;
+    case D_QDIM: return (int64_t)in->n_head * in->head_dim;
+    case D_KVDIM: return (int64_t)in->n_kv_head * in->head_dim;
+    case D_HEAD: return in->head_dim;
+    case D_FFN: return in->ffn_dim;
+    case D_FFN_EXP: return in->ffn_exp_dim;
+    case D_EXPERTS: return in->n_expert;
+    default: return 1;
+    }
+}
+
+static int needed(const engine_model_info *in, enum when w) {
+    switch (w) {
+    case WITH_BIAS: return in->qkv_bias;
+    case WITH_QK_NORM: return in->qk_norm;
+    case DENSE: return !in->n_expert;
+    case MOE: return in->n_expert > 0;
+    default: return 1;
+    }
+}
+
+/* Whether the runtime knows a tensor name: the model-level three, or blk.<l>.<schema suffix> with
+ * l < n_layer. Anything else is an architecture variant this runtime does not implement. */
+static int known_name(const char *name, int n_layer) {
+    static const char *const TOP[] = {"token_embd.weight", "output_norm.weight", "output.weight"};
+    for (size_t i = 0; i < 3; i++)
+        if (!strcmp(name, TOP[i])) return 1;
     if (strncmp(name, "blk.", 4)) return 0;
     const char *p = name + 4;
-    if (*p < '0' || *p > '9') return 0;
-    long idx = 0;
-    for (; *p >= '0' && *p <= '9'; p++)
-        if ((idx = idx * 10 + (*p - '0')) >= n_layer) return 0;
-    if (*p++ != '.') return 0;
-    for (size_t k = 0; k < sizeof LAYER_TENSORS / sizeof *LAYER_TENSORS; k++)
-        if (!strcmp(p, LAYER_TENSORS[k])) return 1;
+    long l = 0;
+    int digits = 0;
+    for (; *p >= '0' && *p <= '9'; p++, digits++)
+        if ((l = l * 10 + (*p - '0')) >= n_layer) return 0;
+    if (!digits || *p != '.') return 0;
+    for (int k = 0; k < N_LAYER_TENSORS; k++)
+        if (!strcmp(p + 1, LAYER[k].suffix)) return 1;
     return 0;
 }
 
-static const gguf_tensor *find(const gguf_file *gf, const char *name) {
-    int64_t i = gguf_find_tensor(gf, name);
-    return i < 0 ? NULL : gguf_get_tensor(gf, (uint64_t)i);
-}
-
-static int type_supported(uint32_t t) {
+static int runtime_type(uint32_t t) {
     return t == OP_F32 || t == OP_F16 || t == OP_BF16 || t == OP_Q8_0 || t == OP_Q4_0 || t == OP_Q5_0 ||
            t == OP_Q4_K || t == OP_Q6_K;
 }
 
-static int read_config(engine_model *m, char *err, size_t err_len) {
-    const gguf_file *gf = m->gf;
-    uint64_t len;
-    const char *arch = gguf_kv_get_str(gf, gguf_find_kv(gf, "general.architecture"), &len);
-    char ab[32];
-    if (!arch || len == 0 || len >= sizeof ab) {
-        set_err(err, err_len, "general.architecture mancante o non valido");
-        return -1;
-    }
-    memcpy(ab, arch, len);
-    ab[len] = '\0';
-    engine_model_info *in = &m->info;
-    if (!strcmp(ab, "llama")) in->rope_interleaved = 1;
-    else if (!strcmp(ab, "qwen2") || !strcmp(ab, "qwen3") || !strcmp(ab, "qwen3moe")) in->rope_interleaved = 0;
-    else {
-        set_err(err, err_len, "architettura %s non supportata", ab);
-        return -1;
-    }
-    meta mt = {gf, ab, err, err_len};
-    const char *scaling = gguf_kv_get_str(gf, arch_key(&mt, "rope.scaling.type"), &len);
-    if ((scaling && !(len == 4 && !memcmp(scaling, "none", 4))) || find(gf, "rope_freqs.weight")) {
-        set_err(err, err_len, "rope scaling (anche 'llama3' via rope_freqs.weight) non supportato");
-        return -1;
-    }
-    int64_t v;
-    if ((v = meta_int(&mt, "embedding_length", -1)) < 0) return -1;
-    in->dim = (int32_t)v;
-    if ((v = meta_int(&mt, "block_count", -1)) < 0) return -1;
-    in->n_layer = (int32_t)v;
-    if ((v = meta_int(&mt, "feed_forward_length", -1)) < 0) return -1;
-    in->ffn_dim = (int32_t)v;
-    if (!strcmp(ab, "qwen3moe")) {
-        if ((v = meta_int(&mt, "expert_count", -1)) < 0) return -1;
-        in->n_expert = (int32_t)v;
-        if ((v = meta_int(&mt, "expert_used_count", -1)) < 0) return -1;
-        in->n_expert_used = (int32_t)v;
-        if (in->n_expert_used > in->n_expert) {
-            set_err(err, err_len, "expert_used_count=%d oltre expert_count=%d", in->n_expert_used, in->n_expert);
-            return -1;
-        }
-        /* the device router keeps a token's expert probabilities in one wave's registers */
-        if (in->n_expert > 512 || in->n_expert_used < 1 || in->n_expert_used > 64) {
-            set_err(err, err_len, "expert_count=%d / expert_used_count=%d oltre i limiti del dispositivo (512 / 64)",
-                    in->n_expert, in->n_expert_used);
-            return -1;
-        }
-        if ((v = meta_int(&mt, "expert_feed_forward_length", in->ffn_dim / in->n_expert_used)) <= 0) {
-            if (v == 0) set_err(err, err_len, "dimensione degli esperti nulla");
-            return -1;
-        }
-        in->ffn_exp_dim = (int32_t)v;
-    }
-    if ((v = meta_int(&mt, "attention.head_count", -1)) < 0) return -1;
-    in->n_head = (int32_t)v;
-    if ((v = meta_int(&mt, "attention.head_count_kv", in->n_head)) < 0) return -1;
-    in->n_kv_head = (int32_t)v;
-    if ((v = meta_int(&mt, "attention.key_length", in->dim / in->n_head)) <= 0) {
-        if (v == 0) set_err(err, err_len, "head_dim nullo");
-        return -1;
-    }
-    in->head_dim = (int32_t)v;
-    if (meta_int(&mt, "attention.value_length", in->head_dim) != in->head_dim) {
-        set_err(err, err_len, "key_length diverso da value_length");
-        return -1;
-    }
-    if (meta_int(&mt, "rope.dimension_count", in->head_dim) != in->head_dim) {
-        set_err(err, err_len, "RoPE parziale (rope.dimension_count < head_dim) non supportata");
-        return -1;
-    }
-    if ((v = meta_int(&mt, "context_length", 2048)) < 0) return -1;
-    in->max_pos = (int32_t)v;
-    if (meta_float(&mt, "attention.layer_norm_rms_epsilon", -1.0, &in->norm_eps)) return -1;
-    if (meta_float(&mt, "rope.freq_base", 10000.0, &in->rope_theta)) return -1;
-    if (in->n_head % in->n_kv_head || in->head_dim % 2) {
-        set_err(err, err_len, "teste o head_dim non validi (n_head %% n_kv_head, head_dim pari)");
-        return -1;
-    }
-    const gguf_tensor *emb = find(gf, "token_embd.weight");
-    if (!emb || emb->n_dims != 2 || emb->ne[1] == 0 || emb->ne[1] > (1u << 30)) {
-        set_err(err, err_len, "token_embd.weight mancante o non valido");
-        return -1;
-    }
-    in->n_vocab = (int32_t)emb->ne[1];
-    in->tied_embeddings = find(gf, "output.weight") == NULL;
-    in->qkv_bias = find(gf, "blk.0.attn_q.bias") != NULL;
-    in->qk_norm = find(gf, "blk.0.attn_q_norm.weight") != NULL;
-    for (uint64_t i = 0; i < gguf_n_tensors(gf); i++) {
-        const char *name = gguf_get_tensor(gf, i)->name;
-        if (!known_tensor(name, in->n_layer)) {
-            set_err(err, err_len, "tensore non supportato: %s", name);
-            return -1;
-        }
-    }
-    return 0;
-}
-
-/* ------------------------------------------------------------------ upload */
-
-static int sdy_err(char *err, size_t err_len, const char *what) {
-    set_err(err, err_len, "%s: %s", what, sdy_last_error());
-    return -1;
-}
-
-/* Descriptor of a [n_expert][n_out][n_in] tensor (n_expert = 0: a matrix [n_out][n_in]) of a
- * supported type, or NULL with the reason in err. */
-static const gguf_tensor *check_tensor(engine_model *m, const char *name, int n_in, int n_out, int n_expert, char *err,
-                                       size_t err_len) {
-    const gguf_tensor *t = find(m->gf, name);
+/* Shape and type of one tensor against what the schema expects; NULL with the reason otherwise. */
+static const gguf_tensor *checked(const gguf_file *gf, const char *name, int rank, const int64_t want[3], char *err,
+                                  size_t len) {
+    const gguf_tensor *t = tensor(gf, name);
     if (!t) {
-        set_err(err, err_len, "tensore mancante: %s", name);
+        say(err, len, "tensore mancante: %s", name);
         return NULL;
     }
-    if (t->n_dims != (n_expert ? 3u : 2u) || t->ne[0] != (uint64_t)n_in || t->ne[1] != (uint64_t)n_out ||
-        (n_expert && t->ne[2] != (uint64_t)n_expert)) {
-        set_err(err, err_len, "%s: dimensioni [%llu, %llu, %llu], attese [%d, %d, %d]", name,
-                (unsigned long long)t->ne[0], (unsigned long long)t->ne[1], (unsigned long long)t->ne[2], n_in, n_out,
-                n_expert ? n_expert : 1);
+    int shape_ok = t->n_dims == (uint32_t)rank;
+    for (int d = 0; d < rank && shape_ok; d++) shape_ok = t->ne[d] == (uint64_t)want[d];
+    if (!shape_ok) {
+        if (rank == 1)
+            say(err, len, "%s: dimensione %llu, attesa %lld", name, (unsigned long long)t->ne[0], (long long)want[0]);
+        else
+            say(err, len, "%s: dimensioni [%llu, %llu, %llu], attese [%lld, %lld, %lld]", name,
+                (unsigned long long)t->ne[0], (unsigned long long)t->ne[1], (unsigned long long)t->ne[2],
+                (long long)want[0], (long long)want[1], (long long)(rank == 3 ? want[2] : 1));
         return NULL;
     }
-    if (!type_supported(t->type)) {
-        set_err(err, err_len,
-                "%s: tipo %s non supportato dal runtime (supportati: F32, F16, BF16, Q8_0, Q4_0, Q5_0, Q4_K, Q6_K)",
-                name, gguf_type_name(t->type));
+    if (!runtime_type(t->type)) {
+        if (rank == 1) say(err, len, "%s: tipo %s non supportato", name, gguf_type_name(t->type));
+        else
+            say(err, len, "%s: tipo %s non supportato dal runtime (supportati: F32, F16, BF16, Q8_0, Q4_0, Q5_0, "
+                "Q4_K, Q6_K)", name, gguf_type_name(t->type));
         return NULL;
     }
     return t;
 }
 
-static void set_dmat(dmat *d, int type, int n_in, int n_out) {
+static int read_config(engine_model *m, char *err, size_t len) {
+    const gguf_file *gf = m->gf;
+    engine_model_info *in = &m->info;
+    meta_reader r = {.gf = gf, .err = err, .len = len};
+    uint64_t n;
+    const char *arch = gguf_kv_get_str(gf, gguf_find_kv(gf, "general.architecture"), &n);
+    if (!arch || !n || n >= sizeof r.arch) return say(err, len, "general.architecture mancante o non valido");
+    memcpy(r.arch, arch, n);
+    r.arch[n] = '\0';
+    int moe = -1;
+    for (size_t a = 0; a < sizeof ARCHS / sizeof *ARCHS; a++)
+        if (!strcmp(r.arch, ARCHS[a].name)) {
+            in->rope_interleaved = ARCHS[a].interleaved;
+            moe = ARCHS[a].moe;
+        }
+    if (moe < 0) return say(err, len, "architettura %s non supportata", r.arch);
+    const char *scaling = gguf_kv_get_str(gf, meta_key(&r, "rope.scaling.type"), &n);
+    if ((scaling && !(n == 4 && !memcmp(scaling, "none", 4))) || tensor(gf, "rope_freqs.weight"))
+        return say(err, len, "rope scaling (anche 'llama3' via rope_freqs.weight) non supportato");
+    if (read_int_keys(&r, in, moe) || read_float_key(&r, "attention.layer_norm_rms_epsilon", -1.0, &in->norm_eps) ||
+        read_float_key(&r, "rope.freq_base", 10000.0, &in->rope_theta))
+        return -1;
+    if (in->n_head % in->n_kv_head || in->head_dim % 2)
+        return say(err, len, "teste o head_dim non validi (n_head %% n_kv_head, head_dim pari)");
+    const gguf_tensor *emb = tensor(gf, "token_embd.weight");
+    if (!emb || emb->n_dims != 2 || emb->ne[1] > META_INT_CAP) return say(err, len, "token_embd.weight mancante o non valido");
+    in->n_vocab = (int32_t)emb->ne[1];
+    in->tied_embeddings = !tensor(gf, "output.weight");
+    in->qkv_bias = tensor(gf, "blk.0.attn_q.bias") != NULL;
+    in->qk_norm = tensor(gf, "blk.0.attn_q_norm.weight") != NULL;
+    for (uint64_t i = 0; i < gguf_n_tensors(gf); i++) {
+        const char *name = gguf_get_tensor(gf, i)->name;
+        if (!known_name(name, in->n_layer)) return say(err, len, "tensore non supportato: %s", name);
+    }
+    return 0;
+}
+
+/* Every schema tensor of every layer, plus the model-level ones, checked before any upload. */
+static int validate_tensors(const engine_model *m, const gguf_tensor *lt[][N_LAYER_TENSORS], char *err, size_t len) {
+    const engine_model_info *in = &m->info;
+    char name[96];
+    const int64_t emb[3] = {in->dim, in->n_vocab, 1}, vec[3] = {in->dim, 1, 1};
+    if (!checked(m->gf, "token_embd.weight", 2, emb, err, len) || !checked(m->gf, "output_norm.weight", 1, vec, err, len))
+        return -1;
+    if (!in->tied_embeddings && !checked(m->gf, "output.weight", 2, emb, err, len)) return -1;
+    for (int l = 0; l < in->n_layer; l++)
+        for (int k = 0; k < N_LAYER_TENSORS; k++) {
+            lt[l][k] = NULL;
+            if (!needed(in, LAYER[k].when)) continue;
+            int64_t want[3];
+            for (int d = 0; d < 3; d++) want[d] = d < LAYER[k].rank ? dim_of(in, LAYER[k].ne[d]) : 1;
+            snprintf(name, sizeof name, "blk.%d.%s", l, LAYER[k].suffix);
+            if (!(lt[l][k] = checked(m->gf, name, LAYER[k].rank, want, err, len))) return -1;
+        }
+    return 0;
+}
+
+/* ------------------------------------------------------------------ upload */
+
+enum { T_ATTN_NORM, T_Q, T_QB, T_K, T_KB, T_V, T_VB, T_QN, T_KN, T_O, T_FFN_NORM, T_GATE, T_UP, T_DOWN, T_ROUTER,
+       T_GATE_X, T_UP_X, T_DOWN_X };
+
+typedef struct {
+    engine_model *m;
+    char *err;
+    size_t len;
+} loader;
+
+static int device_fail(loader *ld, const char *what) {
+    return say(ld->err, ld->len, "%s: %s", what, sdy_last_error());
+}
+
+static int is_quant(uint32_t t) { return t != OP_F32 && t != OP_F16 && t != OP_BF16; }
+
+static void describe(dmat *d, int type, int n_in, int n_out) {
     d->type = type;
     d->n_in = n_in;
     d->n_out = n_out;
 }
 
-static int get_tensor(engine_model *m, const char *name, int n_in, int n_out, int n_expert, dmat *out, char *err,
-                      size_t err_len) {
-    const gguf_tensor *t = check_tensor(m, name, n_in, n_out, n_expert, err, err_len);
-    if (!t) return -1;
-    if (sdy_mat_upload(&out->m, (int)t->type, n_in, (long)n_out * (n_expert ? n_expert : 1), t->data, m->st))
-        return sdy_err(err, err_len, name);
-    set_dmat(out, (int)t->type, n_in, n_out);
-    m->device_bytes += out->m.bytes;
-    return 0;
-}
-
-static int is_quant(uint32_t t) { return t != OP_F32 && t != OP_F16 && t != OP_BF16; }
-
-/* Row view of a fused matrix. */
-static dmat view(const dmat *w, long r0, int n_out) {
+static dmat row_view(const dmat *w, long r0, int n_out) {
     dmat d = *w;
     d.m = sdy_mat_rows(&w->m, r0, n_out);
     d.n_out = n_out;
     return d;
 }
 
-/* wq, wk, wv. When wq and wk (and wv) have one type they are stored as one matrix whose row ranges
- * are wq, wk (, wv), so that a single matvec computes them together. */
-static int get_qkv(engine_model *m, int l, dlayer *L, char *err, size_t err_len) {
-    const engine_model_info *in = &m->info;
-    const int dim = in->dim, q_dim = in->n_head * in->head_dim, kv_dim = in->n_kv_head * in->head_dim;
-    char nq[64], nk[64], nv[64];
-    snprintf(nq, sizeof nq, "blk.%d.attn_q.weight", l);
-    snprintf(nk, sizeof nk, "blk.%d.attn_k.weight", l);
-    snprintf(nv, sizeof nv, "blk.%d.attn_v.weight", l);
-    const gguf_tensor *tq = check_tensor(m, nq, dim, q_dim, 0, err, err_len);
-    const gguf_tensor *tk = tq ? check_tensor(m, nk, dim, kv_dim, 0, err, err_len) : NULL;
-    const gguf_tensor *tv = tk ? check_tensor(m, nv, dim, kv_dim, 0, err, err_len) : NULL;
-    if (!tv) return -1;
+/* One matrix (or expert stack) as it is in the file. */
+static int upload_matrix(loader *ld, const gguf_tensor *t, dmat *out) {
+    const long rows = (long)(t->nbytes / sdy_raw_row_bytes((int)t->type, (int)t->ne[0]));
+    if (sdy_mat_upload(&out->m, (int)t->type, (int)t->ne[0], rows, t->data, ld->m->st)) return device_fail(ld, t->name);
+    describe(out, (int)t->type, (int)t->ne[0], (int)t->ne[1]);
+    ld->m->device_bytes += out->m.bytes;
+    return 0;
+}
+
+/* q, k and v. With q and k of one type they are one matrix (and v too when it shares the type),
+ * whose row ranges are the three: one launch computes them all. */
+static int upload_qkv(loader *ld, const gguf_tensor *const *lt, dlayer *L) {
+    const gguf_tensor *tq = lt[T_Q], *tk = lt[T_K], *tv = lt[T_V];
+    const int n_in = (int)tq->ne[0], qd = (int)tq->ne[1], kvd = (int)tk->ne[1];
     if (tq->type != tk->type) {
         L->qkv_parts = 0;
-        return get_tensor(m, nq, dim, q_dim, 0, &L->wq, err, err_len) ||
-               get_tensor(m, nk, dim, kv_dim, 0, &L->wk, err, err_len) ||
-               get_tensor(m, nv, dim, kv_dim, 0, &L->wv, err, err_len) ? -1 : 0;
+        return upload_matrix(ld, tq, &L->wq) || upload_matrix(ld, tk, &L->wk) || upload_matrix(ld, tv, &L->wv) ? -1 : 0;
     }
     const int parts = tv->type == tq->type ? 3 : 2;
-    const long rows = (long)q_dim + kv_dim + (parts == 3 ? kv_dim : 0);
-    if (sdy_mat_alloc(&L->wqkv.m, (int)tq->type, dim, rows)) return sdy_err(err, err_len, nq);
-    set_dmat(&L->wqkv, (int)tq->type, dim, (int)rows);
+    const long rows = (long)qd + kvd + (parts == 3 ? kvd : 0);
+    sdy_stream st = ld->m->st;
+    if (sdy_mat_alloc(&L->wqkv.m, (int)tq->type, n_in, rows)) return device_fail(ld, tq->name);
+    describe(&L->wqkv, (int)tq->type, n_in, (int)rows);
     L->qkv_parts = parts;
-    m->device_bytes += L->wqkv.m.bytes;
-    if (sdy_mat_upload_rows(&L->wqkv.m, 0, 1, q_dim, tq->data, m->st)) return sdy_err(err, err_len, nq);
-    if (sdy_mat_upload_rows(&L->wqkv.m, q_dim, 1, kv_dim, tk->data, m->st)) return sdy_err(err, err_len, nk);
-    L->wq = view(&L->wqkv, 0, q_dim);
-    L->wk = view(&L->wqkv, q_dim, kv_dim);
-    if (parts == 3) {
-        if (sdy_mat_upload_rows(&L->wqkv.m, q_dim + kv_dim, 1, kv_dim, tv->data, m->st))
-            return sdy_err(err, err_len, nv);
-        L->wv = view(&L->wqkv, q_dim + kv_dim, kv_dim);
-        return 0;
+    ld->m->device_bytes += L->wqkv.m.bytes;
+    const gguf_tensor *src[3] = {tq, tk, tv};
+    long r0 = 0;
+    for (int p = 0; p < parts; p++) {
+        const int n = (int)src[p]->ne[1];
+        if (sdy_mat_upload_rows(&L->wqkv.m, r0, 1, n, src[p]->data, st)) return device_fail(ld, src[p]->name);
+        dmat *view = p == 0 ? &L->wq : p == 1 ? &L->wk : &L->wv;
+        *view = row_view(&L->wqkv, r0, n);
+        r0 += n;
     }
-    return get_tensor(m, nv, dim, kv_dim, 0, &L->wv, err, err_len);
+    return parts == 3 ? 0 : upload_matrix(ld, tv, &L->wv);
 }
 
-/* gate and up ([n_expert][ffn][dim]). With one quantized type they are stored interleaved, row
- * 2i = gate i and row 2i+1 = up i (per expert), for the SwiGLU matvec epilogue. */
-static int get_gate_up(engine_model *m, int l, dlayer *L, int ffn, int n_expert, char *err, size_t err_len) {
-    const int dim = m->info.dim;
-    char ng[64], nu[64];
-    snprintf(ng, sizeof ng, n_expert ? "blk.%d.ffn_gate_exps.weight" : "blk.%d.ffn_gate.weight", l);
-    snprintf(nu, sizeof nu, n_expert ? "blk.%d.ffn_up_exps.weight" : "blk.%d.ffn_up.weight", l);
-    const gguf_tensor *tg = check_tensor(m, ng, dim, ffn, n_expert, err, err_len);
-    const gguf_tensor *tu = tg ? check_tensor(m, nu, dim, ffn, n_expert, err, err_len) : NULL;
-    if (!tu) return -1;
+/* gate and up ([n_expert][ffn][dim]). With one quantized type they become one matrix with rows
+ * interleaved (2i = gate i, 2i+1 = up i, per expert) for the SwiGLU matvec epilogue. */
+static int upload_gate_up(loader *ld, const gguf_tensor *tg, const gguf_tensor *tu, dlayer *L) {
     if (tg->type != tu->type || !is_quant(tg->type)) {
         L->gu_fused = 0;
-        return get_tensor(m, ng, dim, ffn, n_expert, &L->gate, err, err_len) ||
-               get_tensor(m, nu, dim, ffn, n_expert, &L->up, err, err_len) ? -1 : 0;
+        return upload_matrix(ld, tg, &L->gate) || upload_matrix(ld, tu, &L->up) ? -1 : 0;
     }
-    const long ne = n_expert ? n_expert : 1, n = ne * ffn;
-    if (sdy_mat_alloc(&L->gate_up.m, (int)tg->type, dim, 2 * n)) return sdy_err(err, err_len, ng);
-    set_dmat(&L->gate_up, (int)tg->type, dim, 2 * ffn);
+    const int n_in = (int)tg->ne[0], ffn = (int)tg->ne[1];
+    const long experts = tg->n_dims == 3 ? (long)tg->ne[2] : 1, rows = experts * ffn;
+    if (sdy_mat_alloc(&L->gate_up.m, (int)tg->type, n_in, 2 * rows)) return device_fail(ld, tg->name);
+    describe(&L->gate_up, (int)tg->type, n_in, 2 * ffn);
     L->gu_fused = 1;
-    m->device_bytes += L->gate_up.m.bytes;
-    if (sdy_mat_upload_map(&L->gate_up.m, 0, n, 2, ffn, 2L * ffn, tg->data, m->st)) return sdy_err(err, err_len, ng);
-    if (sdy_mat_upload_map(&L->gate_up.m, 1, n, 2, ffn, 2L * ffn, tu->data, m->st)) return sdy_err(err, err_len, nu);
+    ld->m->device_bytes += L->gate_up.m.bytes;
+    sdy_stream st = ld->m->st;
+    if (sdy_mat_upload_map(&L->gate_up.m, 0, rows, 2, ffn, 2L * ffn, tg->data, st)) return device_fail(ld, tg->name);
+    if (sdy_mat_upload_map(&L->gate_up.m, 1, rows, 2, ffn, 2L * ffn, tu->data, st)) return device_fail(ld, tu->name);
     return 0;
 }
 
-/* Vector of n elements converted to f32 in device memory. */
-static int get_vector(engine_model *m, const char *name, int n, float **dst, char *err, size_t err_len) {
-    const gguf_tensor *t = find(m->gf, name);
-    if (!t) {
-        set_err(err, err_len, "tensore mancante: %s", name);
-        return -1;
+/* n f32 values from a vector tensor (converted on the device when it is F16/BF16/quantized) into
+ * device memory at dst. */
+static int upload_vector(loader *ld, const gguf_tensor *t, float *dst) {
+    const int n = (int)t->ne[0];
+    sdy_stream st = ld->m->st;
+    if (t->type == OP_F32) return sdy_h2d(dst, t->data, (size_t)n * 4, st) ? device_fail(ld, t->name) : 0;
+    sdy_mat tmp;
+    memset(&tmp, 0, sizeof tmp);
+    int rc = sdy_mat_upload(&tmp, (int)t->type, n, 1, t->data, st) || sdy_dequant_rows(&tmp, 0, 1, dst, st) ||
+             sdy_sync(st);
+    sdy_mat_free(&tmp);
+    return rc ? device_fail(ld, t->name) : 0;
+}
+
+/* Carves n floats from the model's vector block; spans start on 64-float boundaries. */
+static float *carve(engine_model *m, size_t n) {
+    float *p = m->vec_cursor;
+    m->vec_cursor += (n + 63) & ~(size_t)63;
+    return p;
+}
+
+static int upload_layer(loader *ld, const gguf_tensor *const *lt, dlayer *L) {
+    const engine_model_info *in = &ld->m->info;
+    const size_t dim = (size_t)in->dim, hd = (size_t)in->head_dim;
+    const size_t qd = in->n_head * hd, kvd = in->n_kv_head * hd;
+    L->attn_norm = carve(ld->m, dim);
+    L->ffn_norm = carve(ld->m, dim);
+    if (upload_vector(ld, lt[T_ATTN_NORM], L->attn_norm) || upload_vector(ld, lt[T_FFN_NORM], L->ffn_norm)) return -1;
+    if (in->qkv_bias) {
+        /* one contiguous span: the stacked q|k(|v) matvec adds it as a single bias vector */
+        L->bq = carve(ld->m, qd + 2 * kvd);
+        L->bk = L->bq + qd;
+        L->bv = L->bk + kvd;
+        if (upload_vector(ld, lt[T_QB], L->bq) || upload_vector(ld, lt[T_KB], L->bk) ||
+            upload_vector(ld, lt[T_VB], L->bv))
+            return -1;
     }
-    if (t->n_dims != 1 || t->ne[0] != (uint64_t)n) {
-        set_err(err, err_len, "%s: dimensione %llu, attesa %d", name, (unsigned long long)t->ne[0], n);
-        return -1;
+    if (in->qk_norm) {
+        L->q_norm = carve(ld->m, hd);
+        L->k_norm = carve(ld->m, hd);
+        if (upload_vector(ld, lt[T_QN], L->q_norm) || upload_vector(ld, lt[T_KN], L->k_norm)) return -1;
     }
-    if (!type_supported(t->type)) {
-        set_err(err, err_len, "%s: tipo %s non supportato", name, gguf_type_name(t->type));
-        return -1;
+    if (upload_qkv(ld, lt, L) || upload_matrix(ld, lt[T_O], &L->wo)) return -1;
+    if (in->n_expert) {
+        if (upload_matrix(ld, lt[T_ROUTER], &L->gate_inp) || upload_gate_up(ld, lt[T_GATE_X], lt[T_UP_X], L) ||
+            upload_matrix(ld, lt[T_DOWN_X], &L->down))
+            return -1;
+        L->down.n_out = in->dim; /* an expert's rows; the stack holds n_expert of them */
+        return 0;
     }
-    float *d = m->vec_cursor;
-    m->vec_cursor += (n + 63) & ~63;
-    if (t->type == OP_F32) {
-        if (sdy_h2d(d, t->data, (size_t)n * 4, m->st)) return sdy_err(err, err_len, name);
-    } else {
-        sdy_mat tmp;
-        if (sdy_mat_upload(&tmp, (int)t->type, n, 1, t->data, m->st) || sdy_dequant_rows(&tmp, 0, 1, d, m->st) ||
-            sdy_sync(m->st) || sdy_mat_free(&tmp))
-            return sdy_err(err, err_len, name);
-    }
-    *dst = d;
-    return 0;
+    return upload_gate_up(ld, lt[T_GATE], lt[T_UP], L) || upload_matrix(ld, lt[T_DOWN], &L->down) ? -1 : 0;
 }
 
 void engine_model_free(engine_model *m) {
     if (!m) return;
-    if (m->layers) {
-        for (int l = 0; l < m->info.n_layer; l++) {
-            dlayer *L = &m->layers[l];
-            /* row views of wqkv share its allocation */
-            if (L->qkv_parts < 2) sdy_mat_free(&L->wq.m);
-            if (L->qkv_parts < 2) sdy_mat_free(&L->wk.m);
-            if (L->qkv_parts < 3) sdy_mat_free(&L->wv.m);
-            dmat *mats[] = {&L->wqkv, &L->wo, &L->gate, &L->up, &L->gate_up, &L->down, &L->gate_inp};
-            for (size_t i = 0; i < sizeof mats / sizeof *mats; i++) sdy_mat_free(&mats[i]->m);
-        }
-        free(m->layers);
+    for (int l = 0; m->layers && l < m->info.n_layer; l++) {
+        dlayer *L = &m->layers[l];
+        /* row views of wqkv share its allocation */
+        dmat *own[] = {L->qkv_parts < 2 ? &L->wq : NULL, L->qkv_parts < 2 ? &L->wk : NULL,
+                       L->qkv_parts < 3 ? &L->wv : NULL, &L->wqkv, &L->wo, &L->gate, &L->up, &L->gate_up, &L->down,
+                       &L->gate_inp};
+        for (size_t i = 0; i < sizeof own / sizeof *own; i++)
+            if (own[i]) sdy_mat_free(&own[i]->m);
     }
+    free(m->layers);
     sdy_mat_free(&m->tok_embd.m);
     if (!m->info.tied_embeddings) sdy_mat_free(&m->output.m);
     sdy_free(m->vectors);
@@ -387,76 +490,54 @@ void engine_model_get_info(const engine_model *m, engine_model_info *out) {
     if (m && out) *out = m->info;
 }
 
+static int load(engine_model *m, const char *path, char *err, size_t len) {
+    if (!(m->gf = gguf_open(path, err, len)) || read_config(m, err, len)) return -1;
+    const engine_model_info *in = &m->info;
+    const gguf_tensor *(*lt)[N_LAYER_TENSORS] = calloc((size_t)in->n_layer, sizeof *lt);
+    m->layers = calloc((size_t)in->n_layer, sizeof *m->layers);
+    if (!lt || !m->layers) {
+        free(lt);
+        return say(err, len, "memoria esaurita");
+    }
+    loader ld = {m, err, len};
+    int rc = validate_tensors(m, lt, err, len);
+    if (!rc && (sdy_init() || sdy_stream_new(&m->st))) rc = device_fail(&ld, "GPU");
+    /* the f32 vectors of every layer: norms, biases, q/k norms, each span padded to 64 floats */
+    const size_t hd = (size_t)in->head_dim, qd = in->n_head * hd, kvd = in->n_kv_head * hd;
+    const size_t per_layer = 2 * ((size_t)in->dim + 63) + (in->qkv_bias ? qd + 2 * kvd + 63 : 0) +
+                             (in->qk_norm ? 2 * (hd + 63) : 0);
+    if (!rc && sdy_malloc((void **)&m->vectors, (((size_t)in->dim + 63) + per_layer * in->n_layer) * sizeof(float)))
+        rc = device_fail(&ld, "vettori");
+    m->vec_cursor = m->vectors;
+    if (!rc) {
+        const gguf_tensor *emb = tensor(m->gf, "token_embd.weight");
+        m->output_norm = carve(m, (size_t)in->dim);
+        rc = upload_matrix(&ld, emb, &m->tok_embd) || upload_vector(&ld, tensor(m->gf, "output_norm.weight"),
+                                                                    m->output_norm);
+        if (!rc && in->tied_embeddings) m->output = m->tok_embd;
+        else if (!rc) rc = upload_matrix(&ld, tensor(m->gf, "output.weight"), &m->output);
+    }
+    for (int l = 0; !rc && l < in->n_layer; l++) rc = upload_layer(&ld, lt[l], &m->layers[l]);
+    if (!rc && sdy_sync(m->st)) rc = device_fail(&ld, "upload");
+    free(lt);
+    return rc;
+}
+
 engine_model *engine_model_load(const char *path, char *err, size_t err_len) {
     if (err && err_len) err[0] = '\0';
     engine_model *m = calloc(1, sizeof *m);
     if (!m) {
-        set_err(err, err_len, "memoria esaurita");
+        say(err, err_len, "memoria esaurita");
         return NULL;
     }
-    if (!(m->gf = gguf_open(path, err, err_len)) || read_config(m, err, err_len)) goto fail;
-    if (sdy_init() || sdy_stream_new(&m->st)) {
-        sdy_err(err, err_len, "GPU");
-        goto fail;
-    }
-    const engine_model_info *in = &m->info;
-    int dim = in->dim, q_dim = in->n_head * in->head_dim, kv_dim = in->n_kv_head * in->head_dim;
-    size_t per_layer = 2 * (size_t)dim + (in->qkv_bias ? (size_t)q_dim + 2 * (size_t)kv_dim : 0) +
-                       (in->qk_norm ? 2 * (size_t)in->head_dim : 0) + 7 * 64;
-    size_t n_vec = (size_t)dim + 64 + per_layer * in->n_layer;
-    if (sdy_malloc((void **)&m->vectors, n_vec * sizeof(float))) {
-        sdy_err(err, err_len, "vettori");
-        goto fail;
-    }
-    m->vec_cursor = m->vectors;
-    m->layers = calloc((size_t)in->n_layer, sizeof(dlayer));
-    if (!m->layers) {
-        set_err(err, err_len, "memoria esaurita");
-        goto fail;
-    }
-    if (get_tensor(m, "token_embd.weight", dim, in->n_vocab, 0, &m->tok_embd, err, err_len) ||
-        get_vector(m, "output_norm.weight", dim, &m->output_norm, err, err_len))
-        goto fail;
-    if (in->tied_embeddings) m->output = m->tok_embd;
-    else if (get_tensor(m, "output.weight", dim, in->n_vocab, 0, &m->output, err, err_len)) goto fail;
-    for (int l = 0; l < in->n_layer; l++) {
-        dlayer *L = &m->layers[l];
-        char name[64];
-#define NAME(suffix) (snprintf(name, sizeof name, "blk.%d." suffix, l), name)
-        if (get_vector(m, NAME("attn_norm.weight"), dim, &L->attn_norm, err, err_len) ||
-            get_vector(m, NAME("ffn_norm.weight"), dim, &L->ffn_norm, err, err_len) || get_qkv(m, l, L, err, err_len) ||
-            get_tensor(m, NAME("attn_output.weight"), q_dim, dim, 0, &L->wo, err, err_len))
-            goto fail;
-        if (in->n_expert) {
-            int ne = in->n_expert, fe = in->ffn_exp_dim;
-            if (get_tensor(m, NAME("ffn_gate_inp.weight"), dim, ne, 0, &L->gate_inp, err, err_len) ||
-                get_gate_up(m, l, L, fe, ne, err, err_len) ||
-                get_tensor(m, NAME("ffn_down_exps.weight"), fe, dim, ne, &L->down, err, err_len))
-                goto fail;
-        } else if (get_gate_up(m, l, L, in->ffn_dim, 0, err, err_len) ||
-                   get_tensor(m, NAME("ffn_down.weight"), in->ffn_dim, dim, 0, &L->down, err, err_len)) {
-            goto fail;
-        }
-        if (in->qkv_bias && (get_vector(m, NAME("attn_q.bias"), q_dim, &L->bq, err, err_len) ||
-                             get_vector(m, NAME("attn_k.bias"), kv_dim, &L->bk, err, err_len) ||
-                             get_vector(m, NAME("attn_v.bias"), kv_dim, &L->bv, err, err_len)))
-            goto fail;
-        if (in->qk_norm && (get_vector(m, NAME("attn_q_norm.weight"), in->head_dim, &L->q_norm, err, err_len) ||
-                            get_vector(m, NAME("attn_k_norm.weight"), in->head_dim, &L->k_norm, err, err_len)))
-            goto fail;
-#undef NAME
-    }
-    if (sdy_sync(m->st)) {
-        sdy_err(err, err_len, "upload");
-        goto fail;
+    if (load(m, path, err, err_len)) {
+        engine_model_free(m);
+        return NULL;
     }
     return m;
-fail:
-    engine_model_free(m);
-    return NULL;
 }
 
-/* ------------------------------------------------------------------ context */
+/* ------------------------------------------------------------------ contexts */
 
 int32_t engine_ctx_n_threads(const engine_ctx *c) { return c ? c->n_threads : 0; }
 
@@ -468,86 +549,97 @@ void engine_ctx_free(engine_ctx *c) {
     free(c);
 }
 
+/* Reads an on/off switch from the environment: set and not "0" means on. */
+static int env_on(const char *name) {
+    const char *v = getenv(name);
+    return v && v[0] && strcmp(v, "0") != 0;
+}
+
 engine_ctx *engine_ctx_new(const engine_model *m, int32_t max_seq, int32_t n_batch, int32_t logits_all,
                            int32_t n_threads, char *err, size_t err_len) {
     if (err && err_len) err[0] = '\0';
     if (!m) {
-        set_err(err, err_len, "modello NULL");
+        say(err, err_len, "modello NULL");
         return NULL;
     }
-    if (max_seq < 1 || max_seq > MAX_SEQ_LIMIT || max_seq > m->info.max_pos) {
-        set_err(err, err_len, "max_seq=%d non valido (1..%d)", max_seq,
-                m->info.max_pos < MAX_SEQ_LIMIT ? m->info.max_pos : MAX_SEQ_LIMIT);
-        return NULL;
-    }
-    if (n_batch < 1 || n_batch > MAX_BATCH_LIMIT) {
-        set_err(err, err_len, "n_batch=%d non valido (1..%d)", n_batch, MAX_BATCH_LIMIT);
-        return NULL;
-    }
-    if (n_threads < 0 || n_threads > 256) {
-        set_err(err, err_len, "n_threads=%d non valido (0..256)", n_threads);
-        return NULL;
-    }
+    const struct {
+        const char *name;
+        int32_t v, lo, hi;
+    } limits[] = {
+        {"max_seq", max_seq, 1, m->info.max_pos < SEQ_CAP ? m->info.max_pos : SEQ_CAP},
+        {"n_batch", n_batch, 1, BATCH_CAP},
+        {"n_threads", n_threads, 0, THREADS_CAP},
+    };
+    for (size_t i = 0; i < sizeof limits / sizeof *limits; i++)
+        if (limits[i].v < limits[i].lo || limits[i].v > limits[i].hi) {
+            say(err, err_len, "%s=%d non valido (%d..%d)", limits[i].name, limits[i].v, limits[i].lo, limits[i].hi);
+            return NULL;
+        }
     engine_ctx *c = calloc(1, sizeof *c);
     if (!c) {
-        set_err(err, err_len, "memoria esaurita");
+        say(err, err_len, "memoria esaurita");
         return NULL;
     }
     c->m = m;
     c->max_seq = max_seq;
     c->n_batch = n_batch;
     c->logits_all = logits_all != 0;
-    c->n_threads = n_threads ? n_threads : 1;
-    size_t n_logit_rows = c->logits_all ? (size_t)n_batch : 1;
-    if (sdy_stream_new(&c->st) || sdy_host_alloc((void **)&c->logits, n_logit_rows * m->info.n_vocab * sizeof(float)) ||
-        sdy_engine_alloc(c)) {
-        set_err(err, err_len, "memoria GPU esaurita o errore del dispositivo: %s", sdy_last_error());
+    if (!n_threads) {
+        /* the reference's default, the online CPUs (csrc/threadpool.c:68-71); reported, never used
+           to split GPU work */
+        long online = sysconf(_SC_NPROCESSORS_ONLN);
+        n_threads = online < 1 ? 1 : online > THREADS_CAP ? THREADS_CAP : (int32_t)online;
+    }
+    c->n_threads = n_threads;
+    const size_t logit_bytes = (c->logits_all ? (size_t)n_batch : 1) * (size_t)m->info.n_vocab * sizeof(float);
+    if (sdy_stream_new(&c->st) || sdy_host_alloc((void **)&c->logits, logit_bytes) || sdy_engine_alloc(c)) {
+        say(err, err_len, "memoria GPU esaurita o errore del dispositivo: %s", sdy_last_error());
         engine_ctx_free(c);
         return NULL;
     }
-    /* SARDYNE_NO_FUSED_DECODE / SARDYNE_NO_GRAPH: run one-token steps with the unfused kernels, or
-       without recording them (the results are the same; used to compare the paths) */
-    c->decode_fused = !getenv("SARDYNE_NO_FUSED_DECODE") && sdy_engine_decode_fused_ok(c);
-    /* SARDYNE_NO_DEVICE_MOE: one-token MoE blocks group their experts on the host, as prefill does */
-    c->moe_device = c->decode_fused && !getenv("SARDYNE_NO_DEVICE_MOE") && sdy_engine_moe_device_ok(c);
-    c->use_graph = c->decode_fused && (!m->info.n_expert || c->moe_device) && !getenv("SARDYNE_NO_GRAPH");
-    c->fuse_act = c->decode_fused && !getenv("SARDYNE_NO_FUSED_ACT");
+    /* Switches that select between paths with identical results (used to compare them):
+       SARDYNE_NO_FUSED_DECODE  one-token steps on the unfused kernels;
+       SARDYNE_NO_DEVICE_MOE    one-token MoE blocks grouped on the host, as prefill does;
+       SARDYNE_NO_GRAPH         one-token steps issued eagerly instead of replayed;
+       SARDYNE_NO_FUSED_ACT     one-token matvecs read activations quantised by a separate launch. */
+    c->decode_fused = !env_on("SARDYNE_NO_FUSED_DECODE") && sdy_engine_decode_fused_ok(c);
+    c->moe_device = c->decode_fused && !env_on("SARDYNE_NO_DEVICE_MOE") && sdy_engine_moe_device_ok(c);
+    c->use_graph = c->decode_fused && (!m->info.n_expert || c->moe_device) && !env_on("SARDYNE_NO_GRAPH");
+    c->fuse_act = c->decode_fused && !env_on("SARDYNE_NO_FUSED_ACT");
     return c;
 }
 
 /* ------------------------------------------------------------------ eval */
 
+/* The reason n tokens cannot be evaluated now (written into c->err), or 0. */
+static int refuse(engine_ctx *c, const int32_t *tokens, int32_t n) {
+    const int vocab = c->m->info.n_vocab;
+    if (!tokens || n < 1) return say(c->err, sizeof c->err, "nessun token in ingresso");
+    if (c->logits_all && n > c->n_batch)
+        return say(c->err, sizeof c->err, "con logits_all servono al massimo n_batch=%d token per chiamata", c->n_batch);
+    if (n > c->max_seq - c->n_past)
+        return say(c->err, sizeof c->err, "contesto pieno: %d + %d > max_seq=%d", c->n_past, n, c->max_seq);
+    for (int32_t i = 0; i < n; i++)
+        if ((uint32_t)tokens[i] >= (uint32_t)vocab)
+            return say(c->err, sizeof c->err, "token %d fuori dal vocabolario [0, %d)", tokens[i], vocab);
+    return 0;
+}
+
 int engine_eval(engine_ctx *c, const int32_t *tokens, int32_t n) {
     if (!c) return -1;
     c->err[0] = '\0';
-    if (!tokens || n < 1) {
-        snprintf(c->err, sizeof c->err, "nessun token in ingresso");
-        return -1;
-    }
-    if (c->logits_all && n > c->n_batch) {
-        snprintf(c->err, sizeof c->err, "con logits_all servono al massimo n_batch=%d token per chiamata", c->n_batch);
-        return -1;
-    }
-    if (n > c->max_seq - c->n_past) {
-        snprintf(c->err, sizeof c->err, "contesto pieno: %d + %d > max_seq=%d", c->n_past, n, c->max_seq);
-        return -1;
-    }
-    for (int i = 0; i < n; i++)
-        if (tokens[i] < 0 || tokens[i] >= c->m->info.n_vocab) {
-            snprintf(c->err, sizeof c->err, "token %d fuori dal vocabolario [0, %d)", tokens[i], c->m->info.n_vocab);
-            return -1;
-        }
-    int n_past0 = c->n_past;
-    for (int done = 0; done < n;) {
-        int chunk = n - done < c->n_batch ? n - done : c->n_batch;
-        int last = done + chunk == n;
-        if (sdy_engine_forward(c, tokens + done, chunk, last ? (c->logits_all ? chunk : 1) : 0)) {
-            snprintf(c->err, sizeof c->err, "errore GPU: %s", sdy_last_error());
-            c->n_past = n_past0; /* positions after n_past are rewritten by the next eval */
+    if (refuse(c, tokens, n)) return -1;
+    const int start = c->n_past;
+    /* n_batch-token chunks; logits come from the last chunk only (all its rows with logits_all) */
+    for (int32_t at = 0; at < n; at += c->n_batch) {
+        const int32_t len = n - at < c->n_batch ? n - at : c->n_batch;
+        const int out_rows = at + len < n ? 0 : c->logits_all ? len : 1;
+        if (sdy_engine_forward(c, tokens + at, len, out_rows)) {
+            say(c->err, sizeof c->err, "errore GPU: %s", sdy_last_error());
+            c->n_past = start; /* positions past n_past are overwritten by the next eval */
             c->n_logits = 0;
             return -1;
         }
-        done += chunk;
     }
     c->n_logits = c->logits_all ? n : 1;
     return 0;
@@ -559,17 +651,12 @@ int32_t engine_n_past(const engine_ctx *c) { return c ? c->n_past : 0; }
 const char *engine_last_error(const engine_ctx *c) { return c ? c->err : "contesto NULL"; }
 
 void engine_reset(engine_ctx *c) {
-    if (!c) return;
-    c->n_past = 0;
-    c->n_logits = 0;
+    if (c) c->n_past = c->n_logits = 0;
 }
 
 int engine_truncate(engine_ctx *c, int32_t n) {
     if (!c) return -1;
-    if (n < 0 || n > c->n_past) {
-        snprintf(c->err, sizeof c->err, "posizione %d fuori da [0, %d]", n, c->n_past);
-        return -1;
-    }
+    if (n < 0 || n > c->n_past) return say(c->err, sizeof c->err, "posizione %d fuori da [0, %d]", n, c->n_past);
     c->n_past = n;
     c->n_logits = 0;
     return 0;

@@ -82,7 +82,17 @@ int sdy_engine_alloc(engine_ctx *c) {
         TRY(sdy_host_alloc((void **)&c->moe_gidx_host, chosen * 4));
         TRY(sdy_host_alloc((void **)&c->moe_gw_host, chosen * 4));
     }
-    TRY(sdy_rope_table(c->rope_cos, c->rope_sin, c->max_seq, in->head_dim, in->rope_theta, c->st));
+    {
+        /* RoPE table built on the host with libm (bit-identical to the reference's) and uploaded */
+        const size_t nt = S * (hd / 2);
+        float *tab = malloc(2 * nt * sizeof(float) + 1);
+        if (!tab) return -1;
+        sdy_rope_table_host(tab, tab + nt, c->max_seq, in->head_dim, in->rope_theta);
+        int rc = sdy_h2d(c->rope_cos, tab, nt * 4, c->st) || sdy_h2d(c->rope_sin, tab + nt, nt * 4, c->st) ||
+                 sdy_sync(c->st);
+        free(tab);
+        TRY(rc ? -1 : 0);
+    }
     TRY(sdy_memset(c->k_cache, 0, kv * 4, c->st));
     TRY(sdy_memset(c->v_cache, 0, kv * 4, c->st));
     return sdy_sync(c->st);

@@ -894,6 +894,7 @@ template <int WT, int NT>
 static int launch_gemm(GemmArgs &g, hipStream_t st) {
     const long row_tiles = (g.n_rows + 127) / 128;
     const int tok_groups = (g.n_tok + 32 * NT - 1) / (32 * NT);
+    SDY_NOTE_KERNEL((k_gemm<WT, NT>));
     hipLaunchKernelGGL((k_gemm<WT, NT>), dim3((unsigned)row_tiles, (unsigned)tok_groups), dim3(256), 0, st, g);
     return sdy_check_launch("gemm");
 }
@@ -907,6 +908,7 @@ static int launch_gemm2(GemmArgs &g, hipStream_t st) {
     int rc = sdy_lds_limit(fn, lds, &granted);
     if (rc) return rc;
     const unsigned tok_tiles = (unsigned)((g.n_tok + BN - 1) / BN), row_tiles = (unsigned)((g.n_rows + BM - 1) / BM);
+    SDY_NOTE_KERNEL((k_gemm2<WT, MT, NT, WM>));
     hipLaunchKernelGGL((k_gemm2<WT, MT, NT, WM>), dim3(tok_tiles, row_tiles), dim3(64 * WM), lds, st, g);
     return sdy_check_launch("gemm");
 }
@@ -920,6 +922,7 @@ static int launch_gemm3(GemmArgs &g, hipStream_t st) {
     int rc = sdy_lds_limit(fn, lds, &granted);
     if (rc) return rc;
     const unsigned tok_tiles = (unsigned)((g.n_tok + BN - 1) / BN), row_tiles = (unsigned)((g.n_rows + BM - 1) / BM);
+    SDY_NOTE_KERNEL((k_gemm3<WT, MT, NT, WM>));
     hipLaunchKernelGGL((k_gemm3<WT, MT, NT, WM>), dim3(tok_tiles, row_tiles), dim3(64 * WM), lds, st, g);
     return sdy_check_launch("gemm");
 }
@@ -978,6 +981,7 @@ extern "C" int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_st
     int rc;
     if (!a->ws_ready) {
         const long n_sb = (long)n_tok * nb;
+        SDY_NOTE_KERNEL(k_gemm_prep);
         hipLaunchKernelGGL(k_gemm_prep, dim3((unsigned)((n_sb * 16 + 255) / 256)), dim3(256), 0, st,
                            (const uint8_t *)a->xq, n_sb, (_Float16 *)g.y16, (float *)g.yd, (_Float16 *)g.bs16);
         if ((rc = sdy_check_launch("gemm_prep"))) return rc;

@@ -260,15 +260,10 @@ void op_silu_mul(float *gate, const float *up, int n) {
     sdy_free(du);
 }
 
+/* The table is host work: cos/sin in double through the host libm, as the reference computes it
+ * (csrc/ops.c:375-386), so its bits are the reference's. */
 void op_rope_table(float *cos_out, float *sin_out, int n_pos, int head_dim, float theta) {
-    size_t n = (size_t)n_pos * (head_dim / 2);
-    if (!n) return;
-    float *dc = dalloc(n * 4), *ds = dalloc(n * 4);
-    CK(sdy_rope_table(dc, ds, n_pos, head_dim, theta, stream()), "rope_table");
-    to_host(cos_out, dc, n * 4);
-    to_host(sin_out, ds, n * 4);
-    sdy_free(dc);
-    sdy_free(ds);
+    if (n_pos > 0 && head_dim > 1) sdy_rope_table_host(cos_out, sin_out, n_pos, head_dim, theta);
 }
 
 void op_rope(float *x, int n_heads, int head_dim, const float *cos, const float *sin, int interleaved) {

@@ -2,7 +2,7 @@
 // and rotation, MoE router (softmax + top-k) and the small elementwise ops of the kernel-level ABI
 // (attention: attn_kernels.hip).
 //
-// Numerics follow the reference (csrc/ops.c:456-533, csrc/model_llama.c:653-666) where it matters
+// Numerics follow the reference (csrc/ops.c:346-423, csrc/model_llama.c:653-666) where it matters
 // for parity: RMSNorm and softmax sum in double and round the scale once, RoPE angles are computed
 // in double, top-k keeps the lower expert index on ties and renormalises with a sequential float
 // sum. Reductions use fixed trees, so every result is reproducible run to run.
@@ -55,7 +55,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
 
 // ------------------------------------------------------------------------------ elementwise
 
-// gate = silu(gate) * up   (csrc/ops.c:476-481)
+// gate = silu(gate) * up   (csrc/ops.c:366-371)
 __global__ void k_silu_mul(float *gate, const float *up, long n) {
     long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void k_dot(const float *a, const float *b, int
     if (threadIdx.x == 0) *out = s;
 }
 
-// softmax over n values of each row (csrc/ops.c:463-474): max, expf, double sum, float reciprocal
+// softmax over n values of each row (csrc/ops.c:353-364): max, expf, double sum, float reciprocal
 __global__ __launch_bounds__(256) void k_softmax(float *x, int n, long stride) {
     __shared__ float shf[4];
     __shared__ double shd[4];
@@ -112,19 +112,7 @@ __global__ __launch_bounds__(256) void k_softmax(float *x, int n, long stride) {
     for (int i = threadIdx.x; i < n; i += 256) r[i] *= inv;
 }
 
-// RoPE tables in double (csrc/ops.c:485-496)
-__global__ void k_rope_table(float *cos_out, float *sin_out, int n_pos, int hd, float theta) {
-    long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
-    const int half = hd / 2;
-    if (i >= (long)n_pos * half) return;
-    int p = (int)(i / half), j = (int)(i - (long)p * half);
-    double inv_freq = 1.0 / pow((double)theta, (double)(2 * j) / (double)hd);
-    double ang = (double)p * inv_freq;
-    cos_out[i] = (float)cos(ang);
-    sin_out[i] = (float)sin(ang);
-}
-
-// rotate n_heads vectors by one row of the tables (csrc/ops.c:498-511)
+// rotate n_heads vectors by one row of the tables (csrc/ops.c:388-401)
 __global__ void k_rope(float *x, int n_heads, int hd, const float *cs, const float *sn, int interleaved) {
     long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
     const int half = hd / 2;
@@ -323,13 +311,6 @@ extern "C" int sdy_softmax(float *x, int n, int n_rows, long stride, sdy_stream 
     if (n_rows <= 0 || n <= 0) return 0;
     hipLaunchKernelGGL(k_softmax, dim3(n_rows), dim3(256), 0, (hipStream_t)s, x, n, stride);
     return sdy_check_launch("softmax");
-}
-
-extern "C" int sdy_rope_table(float *cos_out, float *sin_out, int n_pos, int hd, float theta, sdy_stream s) {
-    long n = (long)n_pos * (hd / 2);
-    if (n <= 0) return 0;
-    hipLaunchKernelGGL(k_rope_table, GRID1(n, 256), dim3(256), 0, (hipStream_t)s, cos_out, sin_out, n_pos, hd, theta);
-    return sdy_check_launch("rope_table");
 }
 
 extern "C" int sdy_rope(float *x, int n_heads, int hd, const float *cs, const float *sn, int interleaved, sdy_stream s) {

@@ -1857,6 +1857,7 @@ static int launch_mv_k(MvArgs &A, size_t lds, hipStream_t st) {
     long wgs = (n_batches + WAVES - 1) / WAVES;
     long cap = (long)(g_n_cu ? g_n_cu : 256) * per_cu;
     if (wgs > cap) wgs = cap;
+    SDY_NOTE_KERNEL((k_matvec<WT, MT, YREG>));
     hipLaunchKernelGGL((k_matvec<WT, MT, YREG>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
     return sdy_check_launch("matvec");
 }
@@ -1904,6 +1905,7 @@ static int launch_mv_1t_nsb(MvArgs &A, hipStream_t st, int n_slot, bool dry) {
 #define SDY_1T(NIT)                                                                                                  \
     if (wgs(NIT) * n_slot <= cap_1t<WT, NIT, NSB, PRO>(lds)) {                                                       \
         if (dry) return 0;                                                                                           \
+        SDY_NOTE_KERNEL((k_matvec_1t<WT, NIT, NSB, PRO>));                                                            \
         hipLaunchKernelGGL((k_matvec_1t<WT, NIT, NSB, PRO>), dim3((unsigned)wgs(NIT), (unsigned)n_slot), dim3(THREADS), \
                            lds, st, A);                                                                              \
         return sdy_check_launch("matvec");                                                                           \
@@ -1953,6 +1955,7 @@ static int launch_mv_ring_nsb(MvArgs &A, hipStream_t st) {
     const long cap = resident_wgs((const void *)k_matvec_ring<WT, NB, NSB>, lds, per_cu, per_cu_lds);
     if (wgs > cap) wgs = cap;
     if (wgs > 8) wgs &= ~7L;  // a multiple of 8: the XCD-aware numbering applies
+    SDY_NOTE_KERNEL((k_matvec_ring<WT, NB, NSB>));
     hipLaunchKernelGGL((k_matvec_ring<WT, NB, NSB>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
     return sdy_check_launch("matvec");
 }
@@ -1994,6 +1997,7 @@ static int launch_mv_rl(MvArgs &A, size_t lds, hipStream_t st, int n_slot = 1) {
     long cap = (long)(g_n_cu ? g_n_cu : 256) * per_cu / n_slot;
     if (cap < 8) cap = 8;
     if (wgs > cap) wgs = cap;
+    SDY_NOTE_KERNEL((k_matvec_rl<WT, MT, YREG>));
     hipLaunchKernelGGL((k_matvec_rl<WT, MT, YREG>), dim3((unsigned)wgs, (unsigned)n_slot), dim3(THREADS), lds, st, A);
     return sdy_check_launch("matvec");
 }
@@ -2025,6 +2029,7 @@ static int launch_mv_pair_1t(MvArgs &A, MvArgs &B, hipStream_t st, bool dry) {
     const long g1 = (wgs1(A) + 7) / 8 * 8, g2 = wgs1(B);
     if (g1 + g2 > cap) return 1;
     if (dry) return 0;
+    SDY_NOTE_KERNEL((k_matvec_1t_pair<WT1, WT2, NSB, PRO>));
     hipLaunchKernelGGL((k_matvec_1t_pair<WT1, WT2, NSB, PRO>), dim3((unsigned)(g1 + g2)), dim3(THREADS), lds, st, A, B,
                        (int)g1);
     return sdy_check_launch("matvec_pair");
@@ -2059,6 +2064,7 @@ static int launch_mv_pair(MvArgs &A, MvArgs &B, hipStream_t st) {
         per_cu = n;
     }
     const long g1 = (rl_wgs(A, per_cu) + 7) / 8 * 8, g2 = rl_wgs(B, per_cu);
+    SDY_NOTE_KERNEL((k_matvec_rl_pair<WT1, WT2>));
     hipLaunchKernelGGL((k_matvec_rl_pair<WT1, WT2>), dim3((unsigned)(g1 + g2)), dim3(THREADS), 0, st, A, B, (int)g1);
     return sdy_check_launch("matvec_pair");
 }
@@ -2084,6 +2090,7 @@ static int launch_mv_lr_ni(MvArgs &A, size_t lds, hipStream_t st, bool dry) {
         wgs = cap;
     }
     if (dry) return 0;
+    SDY_NOTE_KERNEL((k_matvec_lr<WT, NI, PRO>));
     hipLaunchKernelGGL((k_matvec_lr<WT, NI, PRO>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
     return sdy_check_launch("matvec");
 }

@@ -16,4 +16,8 @@ int sdy_lds_limit(const void *fn, size_t bytes, size_t *granted);
 size_t sdy_raw_row_bytes(int type, int n_in);
 #ifdef __cplusplus
 }
+/* The host function of the last matvec / GEMM / attention kernel launched by this thread (the name
+ * sdy_last_kernel reports). Set right before the launch: SDY_NOTE_KERNEL((k<A, B>)). */
+extern thread_local const void *sdy_last_kernel_fn;
+#define SDY_NOTE_KERNEL(k) (sdy_last_kernel_fn = reinterpret_cast<const void *>(&k))
 #endif

@@ -33,7 +33,8 @@ int sdy_dot(const float *a, const float *b, int n, float *out, sdy_stream s);
 int sdy_f16_to_f32(const uint16_t *x, float *out, long n, sdy_stream s);
 int sdy_f32_to_f16(const float *x, uint16_t *out, long n, sdy_stream s);
 int sdy_softmax(float *x, int n, int n_rows, long stride, sdy_stream s);
-int sdy_rope_table(float *cos_out, float *sin_out, int n_pos, int hd, float theta, sdy_stream s);
+/* RoPE cos/sin tables [n_pos][hd/2], computed on the host (libm, double) into host memory */
+void sdy_rope_table_host(float *cos_out, float *sin_out, int n_pos, int hd, float theta);
 int sdy_rope(float *x, int n_heads, int hd, const float *cs, const float *sn, int interleaved, sdy_stream s);
 int sdy_moe_route(float *probs, int n_tok, int n_expert, int k, int32_t *top, float *wts, sdy_stream s);
 int sdy_moe_combine(const float *y, const int32_t *top, const float *wts, int n_tok, int k, int dim, float *out,

@@ -1,7 +1,9 @@
 // Device management for the C host: device selection, allocations, copies, streams.
 // Errors are reported as negative return codes with a per-thread message (sdy_last_error).
+#include <cxxabi.h>
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -32,6 +34,23 @@ static int hip_fail(hipError_t e, const char *what) {
         hipError_t e_ = (call);                             \
         if (e_ != hipSuccess) return hip_fail(e_, what);    \
     } while (0)
+
+thread_local const void *sdy_last_kernel_fn = nullptr;
+
+// Demangled name of the kernel noted last by this thread (e.g. "void k_matvec_ring<14, 3, 8>(MvArgs)"),
+// or "" when none: benchmarks label their roofline with the kernel the dispatch actually chose.
+extern "C" const char *sdy_last_kernel(void) {
+    static thread_local char name[256];
+    name[0] = '\0';
+    if (!sdy_last_kernel_fn) return name;
+    const char *mangled = hipKernelNameRefByPtr(sdy_last_kernel_fn, nullptr);
+    if (!mangled) return name;
+    int status = -1;
+    char *d = abi::__cxa_demangle(mangled, nullptr, nullptr, &status);
+    snprintf(name, sizeof name, "%s", status == 0 && d ? d : mangled);
+    free(d);
+    return name;
+}
 
 extern "C" int sdy_check_launch(const char *what) {
     hipError_t e = hipGetLastError();

@@ -100,6 +100,15 @@ class GGUFBuilder:
         b = s.encode()
         self.kv.append((key, _VT_STR, struct.pack("<Q", len(b)) + b))
 
+    def add_raw(self, key, vt, payload: bytes):
+        """A metadata value of GGUF value type `vt` whose encoded bytes are `payload`."""
+        self.kv.append((key, vt, payload))
+
+    def add_str_array(self, key, items):
+        enc = [s.encode() for s in items]
+        self.kv.append((key, 9, struct.pack("<IQ", _VT_STR, len(enc)) + b"".join(struct.pack("<Q", len(e)) + e
+                                                                                for e in enc)))
+
     def add_tensor(self, name, ne, type_name, produce):
         tid = TYPE_ID[type_name]
         _, blk, size = GGML_TYPES[tid]
@@ -113,6 +122,10 @@ class GGUFBuilder:
         self.add_tensor(name, tuple(reversed(arr.shape)), tname, lambda a=arr: a.tobytes())
 
     def write(self):
+        align = ALIGN
+        for key, vt, payload in self.kv:
+            if key == "general.alignment" and vt == _VT_U32:
+                align = struct.unpack("<I", payload)[0]
         head = [b"GGUF", struct.pack("<IQQ", 3, len(self.tensors), len(self.kv))]
         for key, vt, payload in self.kv:
             k = key.encode()
@@ -122,12 +135,12 @@ class GGUFBuilder:
             nm = t.name.encode()
             head += [struct.pack("<Q", len(nm)), nm, struct.pack("<I", len(t.ne)),
                      struct.pack(f"<{len(t.ne)}Q", *t.ne), struct.pack("<IQ", t.type_id, off)]
-            off += -(-t.nbytes // ALIGN) * ALIGN
+            off += -(-t.nbytes // align) * align
         header = b"".join(head)
         tmp = Path(str(self.path) + ".tmp")
         with open(tmp, "wb") as f:
             f.write(header)
-            f.write(b"\0" * (-len(header) % ALIGN))
+            f.write(b"\0" * (-len(header) % align))
             for t in self.tensors:
                 start = f.tell()
                 res = t.produce()
@@ -138,7 +151,7 @@ class GGUFBuilder:
                 written = f.tell() - start
                 if written != t.nbytes:
                     raise ValueError(f"{t.name}: wrote {written} bytes, expected {t.nbytes}")
-                f.write(b"\0" * (-t.nbytes % ALIGN))
+                f.write(b"\0" * (-t.nbytes % align))
         os.replace(tmp, self.path)
         return self.path
 
@@ -174,6 +187,7 @@ class ModelSpec:
     norm_value: float = 1.0
     bias_std: float = 0.02
     type_fn: object = None  # optional name -> weight type override for quantized matrices
+    same_experts: bool = False  # every expert of a layer gets the blocks of expert 0 (the dense matrix of its seed)
 
 
 def qwen25_3b(n_layer=36) -> ModelSpec:
@@ -188,10 +202,15 @@ def qwen3_30b_a3b(n_layer=48) -> ModelSpec:
                      rope_theta=1e6)
 
 
-def _matrix_producer(type_name, n_out, n_in, seed, n_expert=0):
+def _matrix_producer(type_name, n_out, n_in, seed, n_expert=0, same=False):
+    """Random blocks of an n_out x n_in matrix (n_expert stacked ones). same: one matrix drawn from
+    the seed, repeated for every expert, so each expert equals the dense matrix of that seed."""
     def produce():
         rng = np.random.default_rng(seed)
         _, blk, _ = GGML_TYPES[TYPE_ID[type_name]]
+        if same:
+            one = random_blocks(type_name, n_out * (n_in // blk), rng)
+            return np.tile(one.reshape(1, -1), (max(1, n_expert), 1)).tobytes()
         rows = n_out * max(1, n_expert)
         nb = rows * (n_in // blk)
         return random_blocks(type_name, nb, rng).tobytes()
@@ -265,11 +284,11 @@ def write_model(path, spec: ModelSpec, seed: int = 0) -> Path:
             ne, fe = spec.n_expert, spec.ffn_exp_dim
             b.add_array(p + "ffn_gate_inp.weight", (rng.standard_normal((ne, dim)) * spec.router_std).astype(np.float32))
             b.add_tensor(p + "ffn_gate_exps.weight", (dim, fe, ne), spec.t_default,
-                         _matrix_producer(spec.t_default, fe, dim, nxt(), ne))
+                         _matrix_producer(spec.t_default, fe, dim, nxt(), ne, spec.same_experts))
             b.add_tensor(p + "ffn_up_exps.weight", (dim, fe, ne), spec.t_default,
-                         _matrix_producer(spec.t_default, fe, dim, nxt(), ne))
+                         _matrix_producer(spec.t_default, fe, dim, nxt(), ne, spec.same_experts))
             b.add_tensor(p + "ffn_down_exps.weight", (fe, dim, ne), spec.t_ffn_down,
-                         _matrix_producer(spec.t_ffn_down, dim, fe, nxt(), ne))
+                         _matrix_producer(spec.t_ffn_down, dim, fe, nxt(), ne, spec.same_experts))
         else:
             b.add_tensor(p + "ffn_gate.weight", (dim, spec.ffn_dim), spec.t_default,
                          _matrix_producer(spec.t_default, spec.ffn_dim, dim, nxt()))

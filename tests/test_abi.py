@@ -68,12 +68,12 @@ def gpu_present():
 @needs_lib
 @pytest.mark.skipif(gpu_present(), reason="checks the no-GPU error path")
 def test_engine_fails_loudly_without_gpu(tmp_path):
-    from sardyne_amd.runtime import Model
+    from sardyne_amd.engine import LoadedModel
     p = tmp_path / "m.gguf"
     write_model(p, ModelSpec(n_vocab=100, dim=256, n_layer=1, n_head=4, n_kv_head=2, head_dim=64, ffn_dim=256,
                              context=32), seed=1)
     with pytest.raises(ValueError, match="HIP device|gfx950"):
-        Model(p)
+        LoadedModel(p)
 
 
 # ---------------------------------------------------------------- GGUF reader (host code)
@@ -182,3 +182,132 @@ def test_gguf_rejections(tmp_path):
     b.add_u32("k", 1)
     b.add_u32("k", 2)
     assert "duplicato" in CGGUF(b.write()).err
+
+
+# ---------------------------------------------------------------- GGUF reader vs the reference's reader
+
+def _gguf_binding(path):
+    """ctypes view of the gguf_* functions of a library (this build's or the reference's)."""
+    h = ctypes.CDLL(str(path))
+    for name, (res, args) in capi._SIGNATURES.items():
+        if name.startswith("gguf_"):
+            fn = getattr(h, name)
+            fn.restype, fn.argtypes = res, args
+    return h
+
+
+def _summary(L, path):
+    """Everything a caller reads from an open file, or None when the reader rejects it."""
+    err = ctypes.create_string_buffer(256)
+    h = L.gguf_open(str(path).encode(), err, len(err))
+    if not h:
+        assert err.value, "rejected without a message"
+        return None
+    try:
+        kvs = []
+        for i in range(L.gguf_n_kv(h)):
+            kv = L.gguf_get_kv(h, i).contents
+            key = kv.key
+            assert L.gguf_find_kv(h, key) == i
+            u, f, n = ctypes.c_uint64(), ctypes.c_double(), ctypes.c_uint64()
+            val = (L.gguf_kv_get_u64(h, i, ctypes.byref(u)), u.value if L.gguf_kv_get_u64(h, i, ctypes.byref(u)) == 0
+                   else None, L.gguf_kv_get_f64(h, i, ctypes.byref(f)), f.value if kv.type in (6, 12) else None)
+            s = L.gguf_kv_get_str(h, i, ctypes.byref(n))
+            sv = ctypes.string_at(s, n.value) if s else None
+            arr = []
+            if kv.type == 9 and kv.arr_type == 8:
+                for j in range(min(kv.n, 8)):
+                    p = L.gguf_kv_get_arr_str(h, i, j, ctypes.byref(n))
+                    arr.append(ctypes.string_at(p, n.value))
+                assert not L.gguf_kv_get_arr_str(h, i, kv.n, ctypes.byref(n))
+            kvs.append((key, kv.type, kv.arr_type if kv.type == 9 else None, kv.n, val, sv, tuple(arr)))
+        ts = []
+        for i in range(L.gguf_n_tensors(h)):
+            t = L.gguf_get_tensor(h, i).contents
+            assert L.gguf_find_tensor(h, t.name) == i
+            ts.append((t.name, t.n_dims, t.type, tuple(t.ne), t.offset, t.nbytes,
+                       t.data - L.gguf_get_tensor(h, 0).contents.data if ts else 0))
+        return (L.gguf_version(h), L.gguf_alignment(h), L.gguf_data_offset(h), tuple(kvs), tuple(ts))
+    finally:
+        L.gguf_close(h)
+
+
+def _rich_file(path):
+    """A file that exercises every value kind: scalars of each width and sign, f32/f64, bool, a
+    string, scalar arrays and a string array (with a multi-byte UTF-8 element), and tensors of
+    several types and ranks."""
+    b = GGUFBuilder(path)
+    b.add_str("general.architecture", "qwen2")
+    b.add_raw("u8", 0, struct.pack("<B", 200))
+    b.add_raw("i8", 1, struct.pack("<b", -3))
+    b.add_raw("u16", 2, struct.pack("<H", 40000))
+    b.add_raw("i16", 3, struct.pack("<h", 1234))
+    b.add_raw("i32", 5, struct.pack("<i", -7))
+    b.add_raw("i64", 11, struct.pack("<q", 1 << 40))
+    b.add_raw("u64", 10, struct.pack("<Q", 1 << 62))
+    b.add_raw("f64", 12, struct.pack("<d", 2.5))
+    b.add_raw("ok", 7, b"\x01")
+    b.add_f32("f32", 0.125)
+    b.add_raw("arr.i32", 9, struct.pack("<IQ", 5, 3) + struct.pack("<3i", 1, -2, 3))
+    b.add_str_array("tokenizer.tokens", ["a", "bé", "", "€x"])
+    b.add_u32("general.alignment", 64)
+    b.add_tensor("t.f32", (64, 2), "F32", lambda: np.ones(128, np.float32).tobytes())
+    b.add_tensor("t.q4k", (256, 1), "Q4_K", lambda: bytes(144))
+    b.add_tensor("t.q8", (32, 2, 3), "Q8_0", lambda: bytes(6 * 34))
+    return b.write()
+
+
+needs_ref_gguf = pytest.mark.skipif(
+    not capi.available() or not (ROOT / "oracle" / "_ref" / "libsardyne_ref.so").exists(),
+    reason="needs build/libsardyne.so and the reference compiled into oracle/_ref")
+
+
+@needs_ref_gguf
+def test_gguf_reader_agrees_with_reference_reader(tmp_path):
+    """The reference's own parser (csrc/gguf.c, compiled from its sources) and this build's read
+    the same fields from a valid file, and accept or reject the same corrupted files: truncations
+    at every byte of the header and 1500 random header mutations (seed 42), the method of the
+    reference's tests/test_gguf.py:144-173 with its C parser as the other side."""
+    ours = _gguf_binding(capi.lib_path())
+    ref = _gguf_binding(ROOT / "oracle" / "_ref" / "libsardyne_ref.so")
+    path = _rich_file(tmp_path / "rich.gguf")
+    good = _summary(ref, path)
+    assert good is not None and _summary(ours, path) == good
+    data = path.read_bytes()
+    header_end = good[2]
+    bad = tmp_path / "bad.gguf"
+    for n in range(0, header_end + 1):
+        bad.write_bytes(data[:n])
+        assert _summary(ours, bad) == _summary(ref, bad), n
+    rng = np.random.default_rng(42)
+    accepted = 0
+    for _ in range(1500):
+        d = bytearray(data)
+        for pos in rng.integers(4, header_end, size=rng.integers(1, 4)):
+            d[pos] = int(rng.integers(0, 256))
+        bad.write_bytes(bytes(d))
+        r = _summary(ref, bad)
+        assert _summary(ours, bad) == r
+        accepted += r is not None
+    assert 0 < accepted < 1500
+
+
+@needs_ref_gguf
+@pytest.mark.parametrize("n_pos,hd,theta", [(640, 128, 1e6), (1152, 128, 1e6), (300, 64, 1e4), (50, 16, 10000.0)],
+                         ids=["qwen25-3b-ctx640", "qwen3-30b-a3b-ctx1152", "llama-hd64", "small"])
+def test_rope_table_bits_equal_reference(n_pos, hd, theta):
+    """op_rope_table (host libm in double, the table the engine uploads at context creation) has the
+    bits of the reference's op_rope_table (csrc/ops.c:375-386, compiled from its sources) at the
+    tables of the Qwen2.5-3B (640 positions) and Qwen3-30B-A3B (1152 positions) workloads."""
+    import oracle as O
+    got = [np.empty((n_pos, hd // 2), np.float32) for _ in range(2)]
+    exp = [np.empty((n_pos, hd // 2), np.float32) for _ in range(2)]
+    capi.lib().op_rope_table(got[0].ctypes.data, got[1].ctypes.data, n_pos, hd, theta)
+    O.ref_lib().op_rope_table(exp[0].ctypes.data, exp[1].ctypes.data, n_pos, hd, theta)
+    for g, e in zip(got, exp):
+        assert np.array_equal(g.view(np.uint32), e.view(np.uint32))
+    # the mathematics: position 0 is the identity rotation, and pair i turns by theta^(-2i/hd) per position
+    assert np.all(got[0][0] == 1.0) and np.all(got[1][0] == 0.0)
+    ang = np.arange(n_pos)[:, None] * theta ** (-np.arange(hd // 2) * 2.0 / hd)[None, :]
+    np.testing.assert_allclose(got[0], np.cos(ang), atol=2e-7)
+    np.testing.assert_allclose(got[1], np.sin(ang), atol=2e-7)

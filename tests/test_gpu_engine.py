@@ -8,7 +8,7 @@ import pytest
 
 import oracle as O
 from sardyne_amd.gguf_synth import ModelSpec, write_model
-from sardyne_amd.runtime import Context, Model, generate
+from sardyne_amd.engine import LoadedModel, greedy
 
 pytestmark = pytest.mark.gpu
 
@@ -21,6 +21,13 @@ def kquant_moe_types(name):
     if "ffn_down" in name:
         return "Q5_0"
     return "Q6_K" if "ffn_up" in name or "attn_output" in name else "Q4_K"
+
+
+def mixed_attn_v(name):
+    """attn_v Q4_K in even layers (three-part q|k|v stack), Q6_K (the spec's default) in odd ones."""
+    if name.endswith("attn_v.weight") and int(name.split(".")[1]) % 2 == 0:
+        return "Q4_K"
+    return None
 
 
 SPECS = {
@@ -43,6 +50,16 @@ SPECS = {
     "moe-16x4-ffn768": ModelSpec(arch="qwen3moe", n_vocab=300, dim=256, n_layer=2, n_head=4, n_kv_head=2,
                                  head_dim=64, ffn_dim=2048, context=64, n_expert=16, n_expert_used=4,
                                  ffn_exp_dim=768, qkv_bias=False, qk_norm=True, router_std=0.3),
+    # attn_v of q's type: q|k|v stacked as one matrix (three parts), on the GEMM in prefill chunks
+    "qwen2-kquant-v4k": ModelSpec(n_vocab=300, dim=256, n_layer=2, n_head=4, n_kv_head=2, head_dim=64, ffn_dim=512,
+                                  context=64, t_attn_v="Q4_K"),
+    # a published Q4_K_M mix: attn_v Q4_K in some layers and Q6_K in others
+    "qwen2-kquant-vmix": ModelSpec(n_vocab=300, dim=256, n_layer=3, n_head=4, n_kv_head=2, head_dim=64, ffn_dim=512,
+                                   context=64, type_fn=mixed_attn_v),
+    # kv_dim 32: the q|k|v biases are contiguous without 64-float padding between them
+    "qwen2-q8-kv32": ModelSpec(n_vocab=300, dim=128, n_layer=2, n_head=2, n_kv_head=1, head_dim=32, ffn_dim=256,
+                               context=64, t_default="Q8_0", t_attn_v="Q8_0", t_ffn_down="Q8_0", t_output="Q8_0",
+                               t_embd="Q8_0"),
     "moe-128x8": ModelSpec(arch="qwen3moe", n_vocab=300, dim=256, n_layer=2, n_head=4, n_kv_head=2, head_dim=64,
                            ffn_dim=2048, context=64, n_expert=128, n_expert_used=8, ffn_exp_dim=256, qkv_bias=False,
                            qk_norm=True, router_std=0.3),
@@ -64,30 +81,30 @@ def assert_close(got, ref):
 
 def test_forward_matches_oracle(model_path):
     ref = O.OracleContext(model_path, 32, n_batch=len(TOKENS), logits_all=True).eval(TOKENS)
-    got = Context(Model(model_path), max_seq=32, n_batch=len(TOKENS), logits_all=True).eval(TOKENS)
+    got = LoadedModel(model_path).session(max_seq=32, n_batch=len(TOKENS), logits_all=True).feed(TOKENS)
     assert_close(got, ref)
     assert np.mean(got.argmax(-1) == ref.argmax(-1)) == 1.0
 
 
 def test_kv_cache_and_batching(model_path):
-    model = Model(model_path)
-    full = Context(model, max_seq=32, n_batch=len(TOKENS), logits_all=True).eval(TOKENS)
-    chunked = Context(model, max_seq=32, n_batch=5, logits_all=True).eval(TOKENS)
+    model = LoadedModel(model_path)
+    full = model.session(max_seq=32, n_batch=len(TOKENS), logits_all=True).feed(TOKENS)
+    chunked = model.session(max_seq=32, n_batch=5, logits_all=True).feed(TOKENS)
     assert_close(chunked, full)
-    ctx = Context(model, max_seq=32, n_batch=4)
-    assert_close(ctx.eval(TOKENS[:7]), full[6])
+    ctx = model.session(max_seq=32, n_batch=4)
+    assert_close(ctx.feed(TOKENS[:7]), full[6])
     for i, t in enumerate(TOKENS[7:], start=7):
-        assert_close(ctx.eval([t]), full[i])
-    assert ctx.n_past == len(TOKENS)
-    ctx.reset()
-    assert ctx.n_past == 0
-    assert_close(ctx.eval(TOKENS), full[-1])
+        assert_close(ctx.feed([t]), full[i])
+    assert ctx.position == len(TOKENS)
+    ctx.clear()
+    assert ctx.position == 0
+    assert_close(ctx.feed(TOKENS), full[-1])
 
 
 def test_deterministic(model_path):
-    model = Model(model_path)
-    a = Context(model, max_seq=32, n_batch=len(TOKENS), logits_all=True).eval(TOKENS)
-    b = Context(model, max_seq=32, n_batch=len(TOKENS), logits_all=True, n_threads=7).eval(TOKENS)
+    model = LoadedModel(model_path)
+    a = model.session(max_seq=32, n_batch=len(TOKENS), logits_all=True).feed(TOKENS)
+    b = model.session(max_seq=32, n_batch=len(TOKENS), logits_all=True, n_threads=7).feed(TOKENS)
     assert np.array_equal(a, b)
 
 
@@ -99,46 +116,46 @@ def test_generate_matches_oracle(model_path):
         nxt = int(np.argmax(logits))
         out.append(nxt)
         logits = ref.eval([nxt])
-    assert generate(Context(Model(model_path), max_seq=32), TOKENS[:4], 12) == out
+    assert greedy(LoadedModel(model_path).session(max_seq=32), TOKENS[:4], 12) == out
 
 
 def test_truncate(model_path):
-    model = Model(model_path)
-    full = Context(model, max_seq=32, n_batch=len(TOKENS), logits_all=True).eval(TOKENS)
-    ctx = Context(model, max_seq=32, n_batch=4)
-    ctx.eval(TOKENS[:7])
-    ctx.truncate(3)
-    assert ctx.n_past == 3
-    ctx.eval([60, 61])
-    ctx.truncate(3)
-    assert_close(ctx.eval(TOKENS[3:]), full[-1])
+    model = LoadedModel(model_path)
+    full = model.session(max_seq=32, n_batch=len(TOKENS), logits_all=True).feed(TOKENS)
+    ctx = model.session(max_seq=32, n_batch=4)
+    ctx.feed(TOKENS[:7])
+    ctx.rewind(3)
+    assert ctx.position == 3
+    ctx.feed([60, 61])
+    ctx.rewind(3)
+    assert_close(ctx.feed(TOKENS[3:]), full[-1])
     for bad in (-1, len(TOKENS) + 1):
         with pytest.raises(ValueError, match="posizione"):
-            ctx.truncate(bad)
+            ctx.rewind(bad)
 
 
 def test_errors_leave_context_unchanged(model_path):
-    model = Model(model_path)
-    ctx = Context(model, max_seq=8, n_batch=4)
-    ctx.eval([1, 2, 3])
+    model = LoadedModel(model_path)
+    ctx = model.session(max_seq=8, n_batch=4)
+    ctx.feed([1, 2, 3])
     for bad, msg in [([1] * 6, "contesto pieno"), ([300], "vocabolario"), ([-1], "vocabolario"), ([], "nessun")]:
         with pytest.raises(ValueError, match=msg):
-            ctx.eval(bad)
-        assert ctx.n_past == 3
+            ctx.feed(bad)
+        assert ctx.position == 3
     with pytest.raises(ValueError, match="n_batch"):
-        Context(model, max_seq=8, n_batch=0)
+        model.session(max_seq=8, n_batch=0)
     with pytest.raises(ValueError, match="max_seq"):
-        Context(model, max_seq=0)
+        model.session(max_seq=0)
     with pytest.raises(ValueError, match="n_threads"):
-        Context(model, max_seq=8, n_threads=-1)
-    all_ctx = Context(model, max_seq=16, n_batch=2, logits_all=True)
-    assert all_ctx.eval([1, 2, 3, 4, 5]).shape == (5, model.info.n_vocab)
+        model.session(max_seq=8, n_threads=-1)
+    all_ctx = model.session(max_seq=16, n_batch=2, logits_all=True)
+    assert all_ctx.feed([1, 2, 3, 4, 5]).shape == (5, model.info.n_vocab)
 
 
 def test_info(model_path):
     from sardyne_amd.gguf_synth import read_tensors
     meta, tensors, _, _ = read_tensors(model_path)
-    i = Model(model_path).info
+    i = LoadedModel(model_path).info
     arch = meta["general.architecture"]
     assert i.dim == meta[f"{arch}.embedding_length"] and i.n_layer == meta[f"{arch}.block_count"]
     assert i.n_vocab == tensors["token_embd.weight"][0][1]
@@ -151,24 +168,24 @@ def _decode_run(model, env):
     saved = {k: os.environ.get(k) for k in env}
     os.environ.update(env)
     try:
-        ctx = Context(model, max_seq=32, n_batch=4)
+        ctx = model.session(max_seq=32, n_batch=4)
     finally:
         for k, v in saved.items():
             if v is None:
                 os.environ.pop(k, None)
             else:
                 os.environ[k] = v
-    out = [ctx.eval(TOKENS[:5])]
-    out += [ctx.eval([t]) for t in TOKENS[5:]]
-    ctx.truncate(6)
-    out += [ctx.eval([t]) for t in TOKENS[6:9]]
+    out = [ctx.feed(TOKENS[:5])]
+    out += [ctx.feed([t]) for t in TOKENS[5:]]
+    ctx.rewind(6)
+    out += [ctx.feed([t]) for t in TOKENS[6:9]]
     return np.stack(out)
 
 
 def test_decode_paths_bit_identical(model_path):
     """One-token steps through the fused decode kernels, replayed from a recorded graph, give the
     bits of the same steps run eagerly and of the unfused kernels (and these follow the oracle)."""
-    model = Model(model_path)
+    model = LoadedModel(model_path)
     fused_graph = _decode_run(model, {})
     fused_eager = _decode_run(model, {"SARDYNE_NO_GRAPH": "1"})
     host_moe = _decode_run(model, {"SARDYNE_NO_DEVICE_MOE": "1"})
@@ -187,7 +204,8 @@ def test_decode_paths_bit_identical(model_path):
     assert_close(fused_graph, np.stack(exp))
 
 
-KQUANT_SPECS = ["qwen2-kquant", "llama-kquant", "qwen2-gqa8-hd128", "moe-128x8", "moe-16x4-ffn768"]
+KQUANT_SPECS = ["qwen2-kquant", "llama-kquant", "qwen2-gqa8-hd128", "moe-128x8", "moe-16x4-ffn768",
+                "qwen2-kquant-v4k", "qwen2-kquant-vmix"]
 
 
 @pytest.mark.parametrize("spec", KQUANT_SPECS)
@@ -199,8 +217,8 @@ def test_logits_bit_identical_to_reference(spec, tmp_path):
     path = tmp_path / "m.gguf"
     write_model(path, dataclasses.replace(SPECS[spec], context=160), seed=7)
     toks = np.random.default_rng(8).integers(0, 300, 100).tolist()
-    ctx = Context(Model(path), max_seq=128, n_batch=32)
-    got = [ctx.eval(toks[:70])] + [ctx.eval([t]) for t in toks[70:100]]
+    ctx = LoadedModel(path).session(max_seq=128, n_batch=32)
+    got = [ctx.feed(toks[:70])] + [ctx.feed([t]) for t in toks[70:100]]
     ref = O.OracleContext(path, 128, n_batch=32, simd=1)
     exp = [ref.eval(toks[:70])] + [ref.eval([t]) for t in toks[70:100]]
     for i, (g, e) in enumerate(zip(got, exp)):
@@ -215,8 +233,8 @@ def test_long_context_decode(spec, tmp_path):
     write_model(path, dataclasses.replace(SPECS[spec], context=256), seed=5)
     rng = np.random.default_rng(3)
     toks = rng.integers(0, 300, 150).tolist()
-    ctx = Context(Model(path), max_seq=200, n_batch=64)
-    got = [ctx.eval(toks[:140])] + [ctx.eval([t]) for t in toks[140:]]
+    ctx = LoadedModel(path).session(max_seq=200, n_batch=64)
+    got = [ctx.feed(toks[:140])] + [ctx.feed([t]) for t in toks[140:]]
     ref = O.OracleContext(path, 200, n_batch=64, simd=0)
     exp = [ref.eval(toks[:140])] + [ref.eval([t]) for t in toks[140:]]
     assert_close(np.stack(got), np.stack(exp))

@@ -239,8 +239,7 @@ def test_rope(interleaved):
     lib().op_rope_table(ptr(cos), ptr(sin), n_pos, hd, theta)
     ec, es = np.empty_like(cos), np.empty_like(sin)
     O.lib().orc_rope_table(ptr(ec), ptr(es), n_pos, hd, theta)
-    np.testing.assert_allclose(cos, ec, atol=1e-7)
-    np.testing.assert_allclose(sin, es, atol=1e-7)
+    assert np.array_equal(bits(cos), bits(ec)) and np.array_equal(bits(sin), bits(es))
     x = np.random.default_rng(2).standard_normal((n_heads, hd)).astype(np.float32)
     e = x.copy()
     rc, rs = np.ascontiguousarray(ec[33]), np.ascontiguousarray(es[33])
@@ -1043,3 +1042,59 @@ def test_gemm_exactness_check_rejects_overflowing_rows():
     w2[5, 192:208] = np.uint8(0x80)  # scales -128: |-128 * (q - 32)| reaches 4096
     bad = capi.DeviceMatrix(O.Q6_K, 1024, 8, w2.reshape(8, -1))
     assert not L.sdy_gemm_ok(ctypes.byref(bad.m), 32)
+
+
+@pytest.mark.parametrize("interleaved", [0, 1], ids=["neox", "llama"])
+@pytest.mark.parametrize("qk_norm", [False, True], ids=["plain", "qknorm"])
+@pytest.mark.parametrize("v_in_stack", [True, False], ids=["v-stacked", "v-apart"])
+def test_qk_rope_kv_strided_equals_packed(interleaved, qk_norm, v_in_stack):
+    """The strided RoPE + KV write (token rows of q|k|v interleaved at the GEMM's stride
+    q_dim + 2 kv_dim, or v in a buffer of its own with another stride) gives the bits of the packed
+    form on contiguous copies: rotated q and k rows, and both caches."""
+    import ctypes
+    from sardyne_amd import capi
+    L = capi.lib()
+    capi.check(L.sdy_init())
+    n_tok, n_head, n_kv, hd, pos0, max_seq = 5, 4, 2, 64, 3, 16
+    qd, kvd = n_head * hd, n_kv * hd
+    rng = np.random.default_rng(9)
+    stack = rng.standard_normal((n_tok, qd + 2 * kvd)).astype(np.float32)
+    v_apart = rng.standard_normal((n_tok, kvd + 32)).astype(np.float32)  # stride kvd + 32
+    qn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    cs, sn = np.empty((max_seq, hd // 2), np.float32), np.empty((max_seq, hd // 2), np.float32)
+    L.op_rope_table(cs.ctypes.data, sn.ctypes.data, max_seq, hd, 1e6)
+    head_stride = max_seq * hd
+    D = capi.DeviceBuffer.from_array
+    dcs, dsn, dqn, dkn = D(cs), D(sn), D(qn), D(kn)
+    qn_p, kn_p = (dqn.ptr, dkn.ptr) if qk_norm else (None, None)
+    # strided: q, k (and v) in the stacked rows
+    dstack = D(stack)
+    dv_apart = D(v_apart)
+    kc1 = capi.DeviceBuffer.from_array(np.zeros(n_kv * head_stride, np.float32))
+    vc1 = capi.DeviceBuffer.from_array(np.zeros(n_kv * head_stride, np.float32))
+    row = qd + 2 * kvd
+    v_ptr, v_stride = ((dstack.ptr + 4 * (qd + kvd), row) if v_in_stack else (dv_apart.ptr, kvd + 32))
+    capi.check(L.sdy_qk_rope_kv_strided(dstack.ptr, dstack.ptr + 4 * qd, v_ptr, row, row, v_stride, qn_p, kn_p, 1e-6,
+                                        dcs.ptr, dsn.ptr, pos0, n_tok, n_head, n_kv, hd, interleaved, kc1.ptr,
+                                        vc1.ptr, head_stride, None))
+    # packed: contiguous copies
+    q = np.ascontiguousarray(stack[:, :qd])
+    k = np.ascontiguousarray(stack[:, qd:qd + kvd])
+    v = np.ascontiguousarray(stack[:, qd + kvd:] if v_in_stack else v_apart[:, :kvd])
+    dq, dk, dv = D(q), D(k), D(v)
+    kc2 = capi.DeviceBuffer.from_array(np.zeros(n_kv * head_stride, np.float32))
+    vc2 = capi.DeviceBuffer.from_array(np.zeros(n_kv * head_stride, np.float32))
+    capi.check(L.sdy_qk_rope_kv(dq.ptr, dk.ptr, dv.ptr, qn_p, kn_p, 1e-6, dcs.ptr, dsn.ptr, pos0, n_tok, n_head, n_kv,
+                                hd, interleaved, kc2.ptr, vc2.ptr, head_stride, None))
+    capi.check(L.sdy_sync(None))
+    got = dstack.to_array(np.float32, stack.size).reshape(stack.shape)
+    assert np.array_equal(bits(got[:, :qd]), bits(dq.to_array(np.float32, q.size).reshape(q.shape)))
+    assert np.array_equal(bits(got[:, qd:qd + kvd]), bits(dk.to_array(np.float32, k.size).reshape(k.shape)))
+    for a, b in ((kc1, kc2), (vc1, vc2)):
+        assert np.array_equal(bits(a.to_array(np.float32, n_kv * head_stride)),
+                              bits(b.to_array(np.float32, n_kv * head_stride)))
+    # the rotation did happen, and the cache rows outside [pos0, pos0 + n_tok) stayed zero
+    assert not np.array_equal(got[:, :qd], stack[:, :qd])
+    kc = kc1.to_array(np.float32, n_kv * head_stride).reshape(n_kv, max_seq, hd)
+    assert np.all(kc[:, :pos0] == 0) and np.all(kc[:, pos0 + n_tok:] == 0) and np.any(kc[:, pos0] != 0)

@@ -313,3 +313,38 @@ def test_rope_table_closed_form():
     ang = np.arange(64)[:, None] * inv[None, :]
     np.testing.assert_allclose(c, np.cos(ang), atol=1e-7)
     np.testing.assert_allclose(s, np.sin(ang), atol=1e-7)
+
+
+def test_oracle_moe_invariants(tmp_path):
+    """The oracle's MoE against what the mathematics fixes, with the same cases as the GPU tests
+    (tests/test_moe.py:147-157, 370-406 of the reference): NaN-poisoned unused experts change no bit;
+    identical experts equal the dense MLP within rounding; an all-zero router routes to the lowest k
+    experts (poisoning the others changes no bit), with the reference engine's bits."""
+    import dataclasses
+    from moe_cases import MOE, PROMPT, STEPS, poison_experts, used_experts
+    from sardyne_amd.gguf_synth import write_model
+
+    def run(p):
+        r = O.OracleContext(p, 48, n_batch=16)
+        return np.stack([r.eval(PROMPT)] + [r.eval([t]) for t in STEPS])
+
+    clean_p = write_model(tmp_path / "c.gguf", MOE, seed=3)
+    unused = [sorted(set(range(MOE.n_expert)) - u) for u in used_experts(clean_p)]
+    dirty_p = write_model(tmp_path / "d.gguf", MOE, seed=3)
+    poison_experts(dirty_p, unused)
+    a, b = run(clean_p), run(dirty_p)
+    assert np.all(np.isfinite(a)) and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    moe = dataclasses.replace(MOE, n_expert=8, n_expert_used=3, same_experts=True)
+    dense = dataclasses.replace(MOE, arch="qwen3", ffn_dim=MOE.ffn_exp_dim, n_expert=0, n_expert_used=0, ffn_exp_dim=0)
+    g, e = run(write_model(tmp_path / "m.gguf", moe, seed=4)), run(write_model(tmp_path / "n.gguf", dense, seed=4))
+    np.testing.assert_allclose(g, e, atol=1e-4 * max(1.0, float(np.abs(e).max())), rtol=0)
+    spec = dataclasses.replace(MOE, n_expert=16, n_expert_used=4, router_std=0.0)
+    z = write_model(tmp_path / "z.gguf", spec, seed=5)
+    h = write_model(tmp_path / "h.gguf", spec, seed=5)
+    poison_experts(h, [range(4, 16)] * spec.n_layer)
+    a, b = run(z), run(h)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    if O.ref_available():
+        R = O.RefEngine(z, 48, n_batch=16)
+        r = np.stack([R.eval(PROMPT)] + [R.eval([t]) for t in STEPS])
+        assert np.array_equal(a.view(np.uint32), r.view(np.uint32))
