@@ -606,6 +606,13 @@ engine_ctx *engine_ctx_new(const engine_model *m, int32_t max_seq, int32_t n_bat
     c->moe_device = c->decode_fused && !env_on("SARDYNE_NO_DEVICE_MOE") && sdy_engine_moe_device_ok(c);
     c->use_graph = c->decode_fused && (!m->info.n_expert || c->moe_device) && !env_on("SARDYNE_NO_GRAPH");
     c->fuse_act = c->decode_fused && !env_on("SARDYNE_NO_FUSED_ACT");
+    /* SARDYNE_ATTENTION=split: one-token attention in one launch split over positions (within
+       tolerance) instead of the bit-exact chain (the reference's softmax over all positions and its
+       in-order weighted sum), which is the default: measured in the decode step at 512-1152
+       positions, the chain is the faster of the two */
+    const char *attn = getenv("SARDYNE_ATTENTION");
+    c->split_attn = c->decode_fused && attn && !strcmp(attn, "split") &&
+                    sdy_attn_decode_split_ok(m->info.n_head, m->info.n_kv_head, m->info.head_dim);
     return c;
 }
 

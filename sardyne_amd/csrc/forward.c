@@ -67,6 +67,9 @@ int sdy_engine_alloc(engine_ctx *c) {
     TRY(dalloc((void **)&c->step_dev, 2 * 4));
     TRY(sdy_host_alloc((void **)&c->step_host, 2 * 4));
     TRY(dalloc(&c->gemm_ws, sdy_gemm_ws_bytes((int)B, (int)max_in)));
+    TRY(dalloc((void **)&c->attn_part, sdy_attn_decode_split_floats(in->n_head, in->head_dim, c->max_seq) * 4));
+    TRY(dalloc((void **)&c->attn_count, (size_t)in->n_kv_head * 4));
+    TRY(sdy_memset(c->attn_count, 0, (size_t)in->n_kv_head * 4, c->st));
     if (in->n_expert) {
         size_t chosen = B * in->n_expert_used;
         TRY(dalloc((void **)&c->moe_probs, B * in->n_expert * 4));
@@ -104,7 +107,7 @@ void sdy_engine_release(engine_ctx *c) {
     void *dev[] = {c->k_cache, c->v_cache, c->rope_cos, c->rope_sin, c->x, c->xb, c->q, c->k, c->v, c->att, c->hb,
                    c->hb2, c->logits_dev, c->part, c->xq[0], c->xq[1], c->tok_dev, c->moe_probs, c->moe_w,
                    c->moe_top, c->moe_x, c->moe_y, c->moe_sum, c->moe_gidx, c->moe_gw, c->qkv, c->step_dev,
-                   c->gemm_ws};
+                   c->gemm_ws, c->attn_part, c->attn_count};
     for (size_t i = 0; i < sizeof dev / sizeof *dev; i++) sdy_free(dev[i]);
     void *host[] = {c->tok_host, c->moe_top_host, c->moe_w_host, c->moe_gidx_host, c->moe_gw_host, c->step_host};
     for (size_t i = 0; i < sizeof host / sizeof *host; i++) sdy_host_free(host[i]);
@@ -456,11 +459,21 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
             /* attention into att (and, for a K-quant wo, its Q8_K row: mm then reuses it, unless wo
                quantises att itself) */
             sdy_mv_args awo = fused_args(c, c->x, c->att, NULL, &L->wo, NULL, c->x, SDY_EPI_NONE);
-            const int wo_fused = c->fuse_act && sdy_matvec_fused_ok(&L->wo.m, &awo, NULL, NULL);
-            const int q8k = !wo_fused && vec_dot_type(L->wo.type) == SDY_Q8_K;
-            TRY(sdy_attn_decode(q, k, v, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos, c->rope_sin, c->step_dev,
-                                in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc, vc, head_stride, c->max_seq,
-                                c->part, c->att, q8k ? c->xq[1] : NULL, c->st));
+            int wo_fused = c->fuse_act && sdy_matvec_fused_ok(&L->wo.m, &awo, NULL, NULL);
+            int q8k = !wo_fused && vec_dot_type(L->wo.type) == SDY_Q8_K;
+            if (c->split_attn) {
+                /* the split attention's merge writes wo's Q8_K row when wo does not quantise att
+                   itself (measured: wo quantising in its prologue is faster than reading the row) */
+                q8k = !wo_fused && vec_dot_type(L->wo.type) == SDY_Q8_K && in->n_head / in->n_kv_head * hd % 256 == 0;
+                TRY(sdy_attn_decode_split(q, k, v, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos, c->rope_sin,
+                                          c->step_dev, in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc, vc,
+                                          head_stride, c->max_seq, c->attn_part, c->attn_count, c->att,
+                                          q8k ? c->xq[1] : NULL, c->st));
+            } else {
+                TRY(sdy_attn_decode(q, k, v, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos, c->rope_sin,
+                                    c->step_dev, in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc, vc,
+                                    head_stride, c->max_seq, c->part, c->att, q8k ? c->xq[1] : NULL, c->st));
+            }
             xq_forget(c);
             if (q8k) {
                 c->xq_src[1] = c->att;

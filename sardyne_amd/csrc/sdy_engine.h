@@ -63,6 +63,10 @@ struct engine_ctx {
     int fuse_act;               /* one-token matvecs quantise (and RMS-normalise) their f32 row in-kernel */
     int moe_device;             /* one-token MoE blocks route, run their experts and combine on the
                                    device (grouped matvec, no host round trip) */
+    int split_attn;             /* one-token attention in one launch, split over positions (within
+                                   tolerance; SARDYNE_ATTENTION=split); 0: the bit-exact chain */
+    float *attn_part;           /* split attention: per-chunk partials */
+    unsigned *attn_count;       /* split attention: arrivals per kv head (zero between launches) */
     float *qkv;                 /* q | k | v of one token */
     void *gemm_ws;              /* scratch of the prefill GEMM (f16 activations of n_batch rows) */
     /* MoE */

@@ -53,6 +53,18 @@ int sdy_attn_decode(const float *q, const float *k, const float *v, const float 
                     float eps, const float *rope_cos, const float *rope_sin, const int32_t *step_dev, int n_head,
                     int n_kv_head, int hd, int interleaved, float *k_cache, float *v_cache, long head_stride,
                     int max_seq, float *scores, float *out, void *xq_q8k, sdy_stream s);
+/* One-token decode attention in one launch, split over 32-position chunks with a deterministic
+ * merge (within tolerance of the reference; sdy_attn_decode is the bit-exact form): the same
+ * inputs and outputs as sdy_attn_decode, with part (sdy_attn_decode_split_floats floats) and count
+ * (n_kv_head unsigned, zero before the first call; each call leaves them zero) as scratch. xq_q8k
+ * needs whole Q8_K blocks per kv group ((n_head / n_kv_head) * hd % 256 == 0). head_dim 64 or 128,
+ * at most 16 query heads per kv head. */
+int sdy_attn_decode_split_ok(int n_head, int n_kv_head, int hd);
+size_t sdy_attn_decode_split_floats(int n_head, int hd, int max_seq);
+int sdy_attn_decode_split(const float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
+                          float eps, const float *rope_cos, const float *rope_sin, const int32_t *step_dev, int n_head,
+                          int n_kv_head, int hd, int interleaved, float *k_cache, float *v_cache, long head_stride,
+                          int max_seq, float *part, unsigned *count, float *out, void *xq_q8k, sdy_stream s);
 #ifdef __cplusplus
 }
 #endif

@@ -9,3 +9,23 @@ for p in (ROOT, ROOT / "oracle"):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU; runs the HIP kernels")
+
+
+import contextlib
+import os
+
+
+@contextlib.contextmanager
+def engine_env(**values):
+    """Environment switches read by engine_ctx_new (e.g. SARDYNE_ATTENTION="split"), set while the
+    block creates its contexts and restored afterwards."""
+    saved = {k: os.environ.get(k) for k in values}
+    os.environ.update({k: str(v) for k, v in values.items()})
+    try:
+        yield
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v

@@ -7,10 +7,12 @@
       within rel-L2 1e-6 of both the reference's AVX2 and scalar orders).
   C3/C4  the Qwen2.5-3B-shaped Q4_K_M model: one 512-token prompt with n_batch 512 (the MFMA GEMM
       path), then one-token steps (replayed from the recorded decode graph after the first):
-      logits bit-identical to the reference engine compiled from its sources.
+      logits bit-identical to the reference engine compiled from its sources, and within 1e-4 of
+      the logit scale (same greedy tokens) with the one-launch split attention.
   C5  the Qwen3-30B-A3B-shaped qwen3moe model (128 experts resident, top-8): a 1024-token context
-      (two 512-token chunks), then one-token steps through the device router: logits
-      bit-identical to the reference engine.
+      (two 512-token chunks), then one-token steps through the device router: the exact chain
+      bit-identical, the split attention within 1e-2 of the logit scale (the spread between the
+      reference's own AVX2 and scalar engines here reaches 5.6e-3) with the same greedy tokens.
 
 The models are written to /dev/shm (2.2 GB and 19.8 GB) and deleted afterwards.
 """
@@ -24,6 +26,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+from conftest import engine_env
 from sardyne_amd import capi
 from sardyne_amd.engine import LoadedModel
 from sardyne_amd.gguf_synth import qwen25_3b, qwen3_30b_a3b, random_blocks, write_model
@@ -100,30 +103,46 @@ def qwen25_3b_path():
     p.unlink(missing_ok=True)
 
 
-def _run_and_compare(path, n_ctx, n_batch, n_steps, max_seq, seed):
+def _run_and_compare(path, n_ctx, n_batch, n_steps, max_seq, seed, tol):
+    """The engine (its exact attention chain) gives the reference's bits at every step; the split
+    attention (SARDYNE_ATTENTION=split) gives the prompt's bits (no decode step) and then logits
+    within tol of the logit scale, with the same greedy tokens."""
     toks = np.random.default_rng(seed).integers(0, 151936, n_ctx + n_steps).astype(np.int32)
     model = LoadedModel(path)
-    s = model.session(max_seq=max_seq, n_batch=n_batch)
-    got = [s.feed(toks[:n_ctx])] + [s.step(int(t)) for t in toks[n_ctx:]]
-    del s, model
+    runs = {}
+    for mode, env in (("exact", {}), ("split", {"SARDYNE_ATTENTION": "split"})):
+        with engine_env(**env):
+            s = model.session(max_seq=max_seq, n_batch=n_batch)
+        runs[mode] = [s.feed(toks[:n_ctx])] + [s.step(int(t)) for t in toks[n_ctx:]]
+        del s
+    del model
     ref = O.RefEngine(path, max_seq, n_batch=64)
     exp = [ref.eval(toks[:n_ctx])] + [ref.eval([int(t)]) for t in toks[n_ctx:]]
-    for i, (g, e) in enumerate(zip(got, exp)):
+    for i, (g, e) in enumerate(zip(runs["exact"], exp)):
         assert np.all(np.isfinite(g)), i
         assert np.array_equal(g.view(np.uint32), e.view(np.uint32)), (i, float(np.abs(g - e).max()))
-        assert int(g.argmax()) == int(e.argmax())
+    split, exp = np.stack(runs["split"]), np.stack(exp)
+    assert np.array_equal(split[0].view(np.uint32), exp[0].view(np.uint32))
+    scale = float(np.abs(exp).max())
+    assert float(np.abs(split - exp).max()) <= tol * scale, float(np.abs(split - exp).max()) / scale
+    assert np.array_equal(split.argmax(-1), exp.argmax(-1))
 
 
 @needs_ref
 def test_c3_c4_qwen25_3b_prefill_512_then_decode(qwen25_3b_path):
-    """512-token prompt in one 512-token batch (every projection on the GEMM), then 6 decode steps."""
-    _run_and_compare(qwen25_3b_path, 512, 512, 6, 640, seed=0)
+    """512-token prompt in one 512-token batch (every projection on the GEMM), then 6 decode steps;
+    the split attention within the reference tests' 1e-4 of the logit scale (tests/test_moe.py:297-299)."""
+    _run_and_compare(qwen25_3b_path, 512, 512, 6, 640, seed=0, tol=1e-4)
 
 
 @needs_ref
 def test_c5_qwen3_30b_a3b_context_1024_then_decode():
     p = _shm_model(qwen3_30b_a3b(), "qwen3_30b_a3b")
     try:
-        _run_and_compare(p, 1024, 512, 5, 1152, seed=1)
+        # 48 layers of int8 activation rounding and top-8 routing amplify any change of f32 rounding:
+        # the reference's own AVX2 and scalar engines (which differ only in float summation orders)
+        # differ by up to 5.6e-3 of the logit scale on this model and token sequence within five steps,
+        # with the same greedy tokens. The split attention is held to 1e-2 and the same greedy tokens.
+        _run_and_compare(p, 1024, 512, 5, 1152, seed=1, tol=1e-2)
     finally:
         p.unlink(missing_ok=True)

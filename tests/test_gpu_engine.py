@@ -7,6 +7,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+from conftest import engine_env
 from sardyne_amd.gguf_synth import ModelSpec, write_model
 from sardyne_amd.engine import LoadedModel, greedy
 
@@ -184,15 +185,21 @@ def _decode_run(model, env):
 
 def test_decode_paths_bit_identical(model_path):
     """One-token steps through the fused decode kernels, replayed from a recorded graph, give the
-    bits of the same steps run eagerly and of the unfused kernels (and these follow the oracle)."""
+    bits of the same steps run eagerly, with the MoE grouped on the host and through the unfused
+    kernels (and these follow the oracle); the split attention gives the same bits replayed and eager,
+    within tolerance of the exact chain."""
     model = LoadedModel(model_path)
     fused_graph = _decode_run(model, {})
     fused_eager = _decode_run(model, {"SARDYNE_NO_GRAPH": "1"})
     host_moe = _decode_run(model, {"SARDYNE_NO_DEVICE_MOE": "1"})
     unfused = _decode_run(model, {"SARDYNE_NO_FUSED_DECODE": "1"})
+    split_graph = _decode_run(model, {"SARDYNE_ATTENTION": "split"})
+    split_eager = _decode_run(model, {"SARDYNE_ATTENTION": "split", "SARDYNE_NO_GRAPH": "1"})
     assert np.array_equal(fused_graph.view(np.uint32), fused_eager.view(np.uint32))
     assert np.array_equal(fused_graph.view(np.uint32), host_moe.view(np.uint32))
     assert np.array_equal(fused_graph.view(np.uint32), unfused.view(np.uint32))
+    assert np.array_equal(split_graph.view(np.uint32), split_eager.view(np.uint32))
+    assert_close(split_graph, fused_graph)
     # the oracle's scalar kernels: its AVX2 Q8_0/Q4_0/Q5_0 order differs between one-token and
     # batched calls, and on this seed a resulting activation-quantisation flip moves one decode row
     # by 0.19 (the scalar kernels give identical bits either way)
@@ -217,12 +224,20 @@ def test_logits_bit_identical_to_reference(spec, tmp_path):
     path = tmp_path / "m.gguf"
     write_model(path, dataclasses.replace(SPECS[spec], context=160), seed=7)
     toks = np.random.default_rng(8).integers(0, 300, 100).tolist()
-    ctx = LoadedModel(path).session(max_seq=128, n_batch=32)
+    model = LoadedModel(path)
+    ctx = model.session(max_seq=128, n_batch=32)
     got = [ctx.feed(toks[:70])] + [ctx.feed([t]) for t in toks[70:100]]
     ref = O.OracleContext(path, 128, n_batch=32, simd=1)
     exp = [ref.eval(toks[:70])] + [ref.eval([t]) for t in toks[70:100]]
     for i, (g, e) in enumerate(zip(got, exp)):
         assert np.array_equal(g.view(np.uint32), e.view(np.uint32)), (i, float(np.abs(g - e).max()))
+    # the split one-token attention (SARDYNE_ATTENTION=split) within the reference tests' tolerance
+    with engine_env(SARDYNE_ATTENTION="split"):
+        ctx = model.session(max_seq=128, n_batch=32)
+    split = [ctx.feed(toks[:70])] + [ctx.feed([t]) for t in toks[70:100]]
+    assert np.array_equal(split[0].view(np.uint32), exp[0].view(np.uint32))  # the prompt: no decode step
+    assert_close(np.stack(split), np.stack(exp))
+    assert np.mean(np.stack(split).argmax(-1) == np.stack(exp).argmax(-1)) == 1.0
 
 
 @pytest.mark.parametrize("spec", ["qwen2-gqa8-hd128", "qwen2-kquant", "moe-kquant"])

@@ -1098,3 +1098,63 @@ def test_qk_rope_kv_strided_equals_packed(interleaved, qk_norm, v_in_stack):
     assert not np.array_equal(got[:, :qd], stack[:, :qd])
     kc = kc1.to_array(np.float32, n_kv * head_stride).reshape(n_kv, max_seq, hd)
     assert np.all(kc[:, :pos0] == 0) and np.all(kc[:, pos0 + n_tok:] == 0) and np.any(kc[:, pos0] != 0)
+
+
+@pytest.mark.parametrize("n_head,n_kv_head,hd,qk_norm,interleaved",
+                         [(16, 2, 128, False, 0), (32, 4, 128, True, 0), (6, 2, 64, False, 1), (4, 4, 64, True, 0),
+                          (32, 2, 128, False, 0)],
+                         ids=["qwen25-3b", "qwen3-30b-a3b", "llama-gqa3", "mha", "gqa16"])
+@pytest.mark.parametrize("pos", [0, 63, 64, 65, 640, 1151, 2110])
+def test_decode_attention_split(n_head, n_kv_head, hd, qk_norm, interleaved, pos):
+    """The one-launch split attention (32-position chunks, partials merged in chunk order by the last
+    workgroup of each kv group) against the oracle's exact decode step: output within 1e-5 of the
+    output scale, the new position's K/V rows bit-exact (the same norm and rotation), the Q8_K bytes
+    those of the output it wrote. Two calls in a row (the second at pos - 1 over a fresh copy of the
+    cache) check that each call leaves the arrival counters at zero for the next."""
+    L = lib()
+    max_seq, eps, half = 2111, 1e-6, hd // 2
+    assert L.sdy_attn_decode_split_ok(n_head, n_kv_head, hd)
+    rng = np.random.default_rng(pos * 11 + n_head)
+    cs, sn = np.empty(max_seq * half, np.float32), np.empty(max_seq * half, np.float32)
+    L.op_rope_table(ptr(cs), ptr(sn), max_seq, hd, 1e6)
+    kc0 = rng.standard_normal((n_kv_head, max_seq, hd)).astype(np.float32)
+    vc0 = rng.standard_normal((n_kv_head, max_seq, hd)).astype(np.float32)
+    qn = (1 + 0.2 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.2 * rng.standard_normal(hd)).astype(np.float32)
+    part = capi.DeviceBuffer(L.sdy_attn_decode_split_floats(n_head, hd, max_seq) * 4)
+    count = capi.DeviceBuffer.from_array(np.zeros(n_kv_head, np.uint32))
+    with_q8k = (n_head // n_kv_head) * hd % 256 == 0
+    for p in (pos, max(pos - 1, 0)):
+        q = rng.standard_normal(n_head * hd).astype(np.float32) * 3
+        k = rng.standard_normal(n_kv_head * hd).astype(np.float32) * 3
+        v = rng.standard_normal(n_kv_head * hd).astype(np.float32)
+        kc, vc = kc0.copy(), vc0.copy()
+        dev = {n: capi.DeviceBuffer.from_array(a) for n, a in
+               dict(q=q, k=k, v=v, kc=kc, vc=vc, cs=cs, sn=sn, qn=qn, kn=kn, step=np.array([0, p], np.int32)).items()}
+        dout = capi.DeviceBuffer(n_head * hd * 4)
+        dxq = capi.DeviceBuffer(n_head * hd // 256 * 292) if with_q8k else None
+        capi.check(L.sdy_attn_decode_split(dev["q"].ptr, dev["k"].ptr, dev["v"].ptr, dev["qn"].ptr if qk_norm else None,
+                                           dev["kn"].ptr if qk_norm else None, eps, dev["cs"].ptr, dev["sn"].ptr,
+                                           dev["step"].ptr, n_head, n_kv_head, hd, interleaved, dev["kc"].ptr,
+                                           dev["vc"].ptr, max_seq * hd, max_seq, part.ptr, count.ptr, dout.ptr,
+                                           dxq.ptr if with_q8k else None, None))
+        got = dout.to_array(np.float32, n_head * hd)
+        qe, ke = q.copy(), k.copy()
+        if qk_norm:
+            for h in range(n_head):
+                O.lib().orc_rmsnorm(ptr(qe) + 4 * h * hd, ptr(qe) + 4 * h * hd, ptr(qn), hd, eps)
+            for h in range(n_kv_head):
+                O.lib().orc_rmsnorm(ptr(ke) + 4 * h * hd, ptr(ke) + 4 * h * hd, ptr(kn), hd, eps)
+        O.lib().orc_rope(ptr(qe), n_head, hd, ptr(cs) + 4 * p * half, ptr(sn) + 4 * p * half, interleaved)
+        O.lib().orc_rope(ptr(ke), n_kv_head, hd, ptr(cs) + 4 * p * half, ptr(sn) + 4 * p * half, interleaved)
+        kc[:, p] = ke.reshape(n_kv_head, hd)
+        vc[:, p] = v.reshape(n_kv_head, hd)
+        exp = np.empty(n_head * hd, np.float32)
+        scores = np.empty(max_seq, np.float32)
+        O.lib().orc_attention(ptr(exp), ptr(qe), ptr(kc), ptr(vc), n_head, n_kv_head, hd, p + 1, max_seq, ptr(scores), 1)
+        np.testing.assert_allclose(got, exp, rtol=0, atol=1e-5 * float(np.abs(exp).max()))
+        assert np.array_equal(bits(dev["kc"].to_array(np.float32, kc.shape)), bits(kc))
+        assert np.array_equal(bits(dev["vc"].to_array(np.float32, vc.shape)), bits(vc))
+        if with_q8k:
+            assert dxq.to_array(np.uint8, n_head * hd // 256 * 292).tobytes() == O.quantize(got, O.Q8_K).tobytes()
+        assert np.all(count.to_array(np.uint32, n_kv_head) == 0)
