@@ -151,6 +151,22 @@ void op_rope(float *x, int n_heads, int head_dim, const float *cos, const float 
 void op_attention(float *out, const float *q, const float *k_cache, const float *v_cache, int n_head,
                   int n_kv_head, int head_dim, int n_kv, int stride, float *scores); /* csrc/ops.h:73-74 */
 
+/* ------------------------------------------------------------------ device-level, no allocation
+ * No counterpart in the reference. For callers that cannot allocate device memory: code recorded
+ * under graph capture, tight serving loops, harnesses that forbid hipMalloc. The one-token decode
+ * attention of the engine (q/k RMSNorm and RoPE, the K/V write at step_dev[1], attention over
+ * step_dev[1] + 1 positions split into 32-position chunks, and the Q8_K row of the output when
+ * xq_q8k is set), with its partials and counters in a fixed static device buffer instead of
+ * caller scratch: at most 1 048 576 floats of partials (n_head * ceil(max_seq / 32) * (head_dim + 4))
+ * and 256 kv heads; larger shapes are rejected with an error. It calls no allocator. Every call on a
+ * GPU shares that GPU's buffer: calls that overlap on one GPU race. Device pointers; returns 0 or a
+ * negative code (the message from the library's last-error call). */
+int sdy_attn_decode_split_noalloc(const float *q, const float *k, const float *v, const float *q_norm,
+                                  const float *k_norm, float eps, const float *rope_cos, const float *rope_sin,
+                                  const int32_t *step_dev, int n_head, int n_kv_head, int head_dim, int interleaved,
+                                  float *k_cache, float *v_cache, long head_stride, int max_seq, float *out,
+                                  void *xq_q8k, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

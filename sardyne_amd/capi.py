@@ -167,6 +167,8 @@ _DEVICE_SIGNATURES = {
     "sdy_norm_quant_gemm": (_int, [_vp, _vp, ctypes.c_float, _int, _int, _vp, _vp, _vp, _vp]),
     "sdy_attn_decode_ok": (_int, [_int, _int, _int, _int]),
     "sdy_attn_decode_split_ok": (_int, [_int, _int, _int]),
+    "sdy_attn_decode_split_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _int, _int, _int,
+                                             _int, _vp, _vp, ctypes.c_long, _int, _vp, _vp, _vp]),
     "sdy_attn_decode_split_floats": (_sz, [_int, _int, _int]),
     "sdy_attn_decode_split": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _int, _int, _int, _int,
                                      _vp, _vp, ctypes.c_long, _int, _vp, _vp, _vp, _vp, _vp]),

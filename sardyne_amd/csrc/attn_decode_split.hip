@@ -21,6 +21,10 @@
 // differ from the reference's in rounding only (exp of chunk-relative scores, f32 partial sums);
 // the engine's bit-exact path (k_attn_scores + k_attn_decode_softmax + k_attn_decode_wv) stays
 // available for comparisons.
+//
+// sdy_attn_decode_split_noalloc is the same computation for callers that cannot allocate (code
+// under graph capture, serving loops): its partials and counters live in this file's `scratch`
+// array, a static device array every GPU the library runs on holds until the process ends.
 #include "sdy_device.h"
 #include "sdy_internal.h"
 #include "sdy_ops.h"
@@ -321,7 +325,43 @@ int launch_split(const SplitArgs &A, hipStream_t st) {
     return sdy_check_launch("attn_decode_split");
 }
 
+__global__ void k_zero_u32(unsigned *p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
 }  // namespace
+
+// The no-alloc entry point's scratch: partials of at most SCRATCH_PART_FLOATS floats (4 MiB), then
+// SCRATCH_COUNTERS arrival counters. In host code the name is only a stand-in for the symbol: its
+// device address on the current GPU comes from hipGetSymbolAddress (scratch_dev below).
+constexpr size_t SCRATCH_PART_FLOATS = size_t(1) << 20;
+constexpr int SCRATCH_COUNTERS = 256;
+static __device__ __align__(256) float scratch[SCRATCH_PART_FLOATS + SCRATCH_COUNTERS];
+constexpr int SCRATCH_MAX_DEVICES = 64;
+static float *scratch_dev[SCRATCH_MAX_DEVICES];  // per device: the address of `scratch` there, once set up
+
+// Looks up `scratch` on the current device (once per device) and clears its counters. Called by
+// sdy_init for the device it selects, and by the no-alloc entry point's first call on another one.
+extern "C" int sdy_attn_split_scratch_setup(void) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return sdy_fail(-2, "scratch setup: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= SCRATCH_MAX_DEVICES)
+        return sdy_fail(-1, "scratch setup: device %d beyond the %d the table holds", dev, SCRATCH_MAX_DEVICES);
+    if (scratch_dev[dev]) return 0;
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+        return sdy_fail(-2, "scratch setup: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    float *base = static_cast<float *>(p);
+    hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(SCRATCH_COUNTERS), 0, 0,
+                       reinterpret_cast<unsigned *>(base + SCRATCH_PART_FLOATS), SCRATCH_COUNTERS);
+    if ((e = hipGetLastError()) != hipSuccess || (e = hipDeviceSynchronize()) != hipSuccess)
+        return sdy_fail(-2, "scratch setup: clearing the counters: %s", hipGetErrorString(e));
+    scratch_dev[dev] = base;
+    return 0;
+}
 
 extern "C" int sdy_attn_decode_split_ok(int n_head, int n_kv_head, int hd) {
     return (hd == 64 || hd == 128) && n_kv_head >= 1 && n_head % n_kv_head == 0 && n_head / n_kv_head <= MAX_REP;
@@ -367,3 +407,28 @@ extern "C" int sdy_attn_decode_split(const float *q, const float *k, const float
     return hd == 128 ? launch_split<128>(A, (hipStream_t)s) : launch_split<64>(A, (hipStream_t)s);
 }
 
+extern "C" int sdy_attn_decode_split_noalloc(const float *q, const float *k, const float *v, const float *q_norm,
+                                             const float *k_norm, float eps, const float *rope_cos,
+                                             const float *rope_sin, const int32_t *step_dev, int n_head, int n_kv_head,
+                                             int hd, int interleaved, float *k_cache, float *v_cache, long head_stride,
+                                             int max_seq, float *out, void *xq_q8k, sdy_stream s) {
+    if (!sdy_attn_decode_split_ok(n_head, n_kv_head, hd))
+        return sdy_fail(-1, "attn_decode_split_noalloc: head_dim %d with %d heads / %d kv heads not supported", hd,
+                        n_head, n_kv_head);
+    const size_t need = sdy_attn_decode_split_floats(n_head, hd, max_seq);
+    if (need > SCRATCH_PART_FLOATS || n_kv_head > SCRATCH_COUNTERS)
+        return sdy_fail(-1, "attn_decode_split_noalloc: %d heads x %d positions (head_dim %d) need %zu floats of "
+                        "partials and %d counters, beyond the fixed scratch of %zu floats and %d counters",
+                        n_head, max_seq, hd, need, n_kv_head, SCRATCH_PART_FLOATS, SCRATCH_COUNTERS);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SCRATCH_MAX_DEVICES)
+        return sdy_fail(-1, "attn_decode_split_noalloc: no usable current device");
+    if (!scratch_dev[dev]) {
+        const int rc = sdy_attn_split_scratch_setup();
+        if (rc) return rc;
+    }
+    float *base = scratch_dev[dev];
+    return sdy_attn_decode_split(q, k, v, q_norm, k_norm, eps, rope_cos, rope_sin, step_dev, n_head, n_kv_head, hd,
+                                 interleaved, k_cache, v_cache, head_stride, max_seq, base,
+                                 reinterpret_cast<unsigned *>(base + SCRATCH_PART_FLOATS), out, xq_q8k, s);
+}

@@ -12,6 +12,8 @@ int sdy_fail(int rc, const char *fmt, ...);
 int sdy_check_launch(const char *what);
 /* Raises kernel fn's dynamic-LDS limit to `bytes` if *granted (per call site) is below it. */
 int sdy_lds_limit(const void *fn, size_t bytes, size_t *granted);
+/* The no-alloc attention entry point's set-up on the current device (attn_decode_split.hip). */
+int sdy_attn_split_scratch_setup(void);
 /* Bytes of one row in the GGUF layout. */
 size_t sdy_raw_row_bytes(int type, int n_in);
 #ifdef __cplusplus

@@ -86,7 +86,7 @@ extern "C" int sdy_init(void) {
     g_n_cu = p.multiProcessorCount;
     g_mem = p.totalGlobalMem;
     g_inited = 1;
-    return 0;
+    return sdy_attn_split_scratch_setup();
 }
 
 extern "C" int sdy_device_info(int *n_cu, size_t *mem_total) {
