@@ -316,8 +316,14 @@ def decode_weight_bytes(spec):
     return spec.n_layer * layer + head + dim * 4 + row_bytes(spec.t_embd, dim)
 
 
+def engine_modes():
+    """The engine's one-token attention and KV-cache type, as engine_ctx_new reads them."""
+    return (os.environ.get("SARDYNE_ATTENTION") or "exact"), (os.environ.get("SARDYNE_KV") or "f32")
+
+
 def kv_bytes_per_position(spec):
-    return 2 * spec.n_layer * spec.n_kv_head * spec.head_dim * 4
+    elt = 2 if engine_modes()[1] == "f16" else 4
+    return 2 * spec.n_layer * spec.n_kv_head * spec.head_dim * elt
 
 
 def write_bench_model(spec, label):
@@ -400,7 +406,8 @@ def decode_line(args, spec, label, ctx_len, desc, n_dec=None):
     gbps = (w_bytes + kv_mean) * tok_s / 1e9
     cfg = {"workload": f"{desc} decode, batch 1, {n_dec} tokens after a {ctx_len}-token context",
            "n_layer": spec.n_layer, "dim": spec.dim, "heads": f"{spec.n_head}/{spec.n_kv_head}",
-           "vocab": spec.n_vocab, "weight_bytes_per_token": w_bytes, "mean_kv_bytes_per_token": int(kv_mean)}
+           "vocab": spec.n_vocab, "weight_bytes_per_token": w_bytes, "mean_kv_bytes_per_token": int(kv_mean),
+           "attention": engine_modes()[0], "kv_cache": engine_modes()[1]}
     if spec.n_expert:
         cfg.update({"experts": f"{spec.n_expert} (top-{spec.n_expert_used})", "expert_ffn": spec.ffn_exp_dim})
     else:

@@ -97,6 +97,7 @@ typedef struct orc_ctx orc_ctx;
 /* n_threads: OpenMP threads used for row loops (results never depend on it); simd as above. */
 orc_ctx *orc_ctx_new(const orc_model *m, int max_seq, int n_batch, int logits_all, int simd);
 void orc_ctx_free(orc_ctx *c);
+void orc_ctx_set_kv_f16(orc_ctx *c, int on);
 int orc_eval(orc_ctx *c, const int32_t *tokens, int n);
 const float *orc_logits(const orc_ctx *c);
 int orc_n_logits(const orc_ctx *c);

@@ -68,6 +68,7 @@ _SIG = {
     "orc_model_free": (None, [_vp]),
     "orc_ctx_new": (_vp, [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "orc_ctx_free": (None, [_vp]),
+    "orc_ctx_set_kv_f16": (None, [_vp, ctypes.c_int]),
     "orc_eval": (ctypes.c_int, [_vp, _vp, ctypes.c_int]),
     "orc_logits": (ctypes.POINTER(ctypes.c_float), [_vp]),
     "orc_n_logits": (ctypes.c_int, [_vp]),
@@ -259,13 +260,14 @@ def gguf_model(path, lib_=None):
 class OracleContext:
     """Oracle counterpart of the engine context: eval() returns logits like the reference runtime."""
 
-    def __init__(self, path, max_seq, n_batch=64, logits_all=False, simd=1):
+    def __init__(self, path, max_seq, n_batch=64, logits_all=False, simd=1, kv_f16=False):
         self.lib = lib()
         self.model, self._keep = gguf_model(path)
         self.info = self._keep[2]
         self.h = self.lib.orc_ctx_new(self.model, max_seq, n_batch, int(logits_all), simd)
         if not self.h:
             raise ValueError("oracle context rejected")
+        self.lib.orc_ctx_set_kv_f16(self.h, int(kv_f16))
         self.logits_all = logits_all
         self.n_batch = n_batch
 

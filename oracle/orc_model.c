@@ -23,6 +23,7 @@ struct orc_model {
 struct orc_ctx {
     const orc_model *m;
     int max_seq, n_batch, logits_all, simd, n_past, n_logits;
+    int kv_f16; /* the cache holds each K/V value rounded to f16 (orc_ctx_set_kv_f16) */
     float *k_cache, *v_cache, *rope_cos, *rope_sin;
     float *x, *xb, *q, *k, *v, *att, *hb, *hb2, *scores, *logits;
     float *moe_probs, *moe_w, *moe_x, *moe_y, *moe_sum;
@@ -127,6 +128,11 @@ orc_ctx *orc_ctx_new(const orc_model *m, int max_seq, int n_batch, int logits_al
     orc_rope_table(c->rope_cos, c->rope_sin, max_seq, in->head_dim, in->rope_theta);
     return c;
 }
+
+/* Not in the reference: a cache of f16 values, each K/V value rounded with the reference's
+ * f32 -> f16 conversion (csrc/ops.c:43-62) when it is written, the model otherwise unchanged. The
+ * f16-cache engine is checked against this. */
+void orc_ctx_set_kv_f16(orc_ctx *c, int on) { c->kv_f16 = on != 0; }
 
 void orc_ctx_free(orc_ctx *c) {
     if (!c) return;
@@ -247,8 +253,14 @@ static void forward(orc_ctx *c, const int32_t *tokens, int n, int out_rows) {
             orc_rope(qt, in->n_head, hd, cs, sn, in->rope_interleaved);
             orc_rope(kt, in->n_kv_head, hd, cs, sn, in->rope_interleaved);
             for (int h = 0; h < in->n_kv_head; h++) {
-                memcpy(kc + h * head_stride + (size_t)pos * hd, kt + (size_t)h * hd, sizeof(float) * hd);
-                memcpy(vc + h * head_stride + (size_t)pos * hd, vt + (size_t)h * hd, sizeof(float) * hd);
+                float *kd = kc + h * head_stride + (size_t)pos * hd, *vd = vc + h * head_stride + (size_t)pos * hd;
+                memcpy(kd, kt + (size_t)h * hd, sizeof(float) * hd);
+                memcpy(vd, vt + (size_t)h * hd, sizeof(float) * hd);
+                if (c->kv_f16)
+                    for (int i = 0; i < hd; i++) {
+                        kd[i] = orc_f16_to_f32(orc_f32_to_f16(kd[i]));
+                        vd[i] = orc_f16_to_f32(orc_f32_to_f16(vd[i]));
+                    }
             }
         }
         for (int t = 0; t < n; t++) /* token t sees positions 0..pos0+t */

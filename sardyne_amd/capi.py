@@ -156,13 +156,14 @@ _DEVICE_SIGNATURES = {
     "sdy_rmsnorm": (_int, [_vp, _vp, _vp, _int, ctypes.c_float, _int, ctypes.c_long, ctypes.c_long, _vp]),
     "sdy_norm_quant": (_int, [_vp, _vp, ctypes.c_float, _int, _int, _vp, _int, _vp, _vp]),
     "sdy_attn_scores_floats": (_sz, [_int, _int, _int]),
+    "sdy_kv_elt_bytes": (_sz, [_int]),
     "sdy_qk_rope_kv": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _int, _int, _int, _int, _int, _int,
-                              _vp, _vp, ctypes.c_long, _vp]),
+                              _vp, _vp, _int, ctypes.c_long, _vp]),
     "sdy_qk_rope_kv_strided": (_int, [_vp, _vp, _vp, ctypes.c_long, ctypes.c_long, ctypes.c_long, _vp, _vp,
-                                      ctypes.c_float, _vp, _vp, _int, _int, _int, _int, _int, _int, _vp, _vp,
+                                      ctypes.c_float, _vp, _vp, _int, _int, _int, _int, _int, _int, _vp, _vp, _int,
                                       ctypes.c_long, _vp]),
-    "sdy_attention": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, ctypes.c_long, ctypes.c_long, _vp, _vp,
-                             ctypes.c_long, _vp]),
+    "sdy_attention": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _int, ctypes.c_long, ctypes.c_long, _vp,
+                             _vp, ctypes.c_long, _vp]),
     "sdy_quantize_gemm": (_int, [_vp, _vp, _int, _int, _vp, _vp]),
     "sdy_norm_quant_gemm": (_int, [_vp, _vp, ctypes.c_float, _int, _int, _vp, _vp, _vp, _vp]),
     "sdy_attn_decode_ok": (_int, [_int, _int, _int, _int]),
@@ -173,7 +174,11 @@ _DEVICE_SIGNATURES = {
     "sdy_attn_decode_split": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _int, _int, _int, _int,
                                      _vp, _vp, ctypes.c_long, _int, _vp, _vp, _vp, _vp, _vp]),
     "sdy_attn_decode": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _int, _int, _int, _int, _vp,
-                               _vp, ctypes.c_long, _int, _vp, _vp, _vp, _vp]),
+                               _vp, _int, ctypes.c_long, _int, _vp, _vp, _vp, _vp]),
+    "sdy_attn_chunked_ok": (_int, [_int, _int, _int]),
+    "sdy_attn_chunked_floats": (_sz, [_int, _int, _int]),
+    "sdy_attn_decode_chunked": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _int, _int, _int, _int,
+                                       _vp, _vp, _int, ctypes.c_long, _int, _vp, _vp, _vp, _vp]),
     "sdy_moe_route": (_int, [_vp, _int, _int, _int, _vp, _vp, _vp]),
     "sdy_moe_combine": (_int, [_vp, _vp, _vp, _int, _int, _int, _vp, _vp, _vp]),
     "sdy_gemm_ok": (_int, [ctypes.POINTER(SdyMat), _int]),
@@ -182,6 +187,7 @@ _DEVICE_SIGNATURES = {
 }
 
 EPI_NONE, EPI_SWIGLU = 0, 1
+KV_F32, KV_F16 = 0, 1
 
 
 def lib_path() -> pathlib.Path:

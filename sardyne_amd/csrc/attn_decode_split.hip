@@ -25,6 +25,7 @@
 // sdy_attn_decode_split_noalloc is the same computation for callers that cannot allocate (code
 // under graph capture, serving loops): its partials and counters live in this file's `scratch`
 // array, a static device array every GPU the library runs on holds until the process ends.
+#include "sdy_attn_dev.h"
 #include "sdy_device.h"
 #include "sdy_internal.h"
 #include "sdy_ops.h"
@@ -52,33 +53,6 @@ struct SplitArgs {
     float *out;                      // [n_head][HD]
     uint8_t *xq;                     // Q8_K blocks of out (or null)
 };
-
-// RMSNorm (weights nw, when set) then RoPE at table row (cs, sn) of the HD-vector in LDS buf, by one
-// wave: the reference's per-head norm (double sum of squares, scale rounded once) and rotation.
-template <int HD>
-SDY_DEV void norm_rope(float *buf, const float *nw, float eps, const float *cs, const float *sn, int interleaved,
-                       int lane) {
-    if (nw) {
-        double ss = 0.0;
-        for (int i = lane; i < HD; i += 64) ss += (double)buf[i] * (double)buf[i];
-        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-        const float sc = (float)(1.0 / sqrt(ss / (double)HD + (double)eps));
-        for (int i = lane; i < HD; i += 64) {
-            const float t = buf[i] * sc;
-            buf[i] = t * nw[i];
-        }
-        sdy_wave_sync();
-    }
-    constexpr int H = HD / 2;
-    for (int i = lane; i < H; i += 64) {
-        const int ia = interleaved ? 2 * i : i, ib = interleaved ? 2 * i + 1 : i + H;
-        const float a = buf[ia], b = buf[ib];
-        const float ac = a * cs[i], bs = b * sn[i], as = a * sn[i], bc = b * cs[i];
-        buf[ia] = ac - bs;
-        buf[ib] = as + bc;
-    }
-    sdy_wave_sync();
-}
 
 // agent-scope relaxed float store / load: coherent across the XCDs without a fence
 SDY_DEV void st_agent(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
@@ -125,7 +99,7 @@ __global__ __launch_bounds__(256) void k_attn_decode_split(SplitArgs a) {
         const float *src = a.q + (size_t)(g * n_rep + r) * HD;
         for (int i = lane; i < HD; i += 64) qs[r * HD + i] = src[i];
         sdy_wave_sync();
-        norm_rope<HD>(qs + r * HD, a.q_norm, a.eps, cs, sn, a.interleaved, lane);
+        sdy_norm_rope<HD>(qs + r * HD, a.q_norm, a.eps, cs, sn, a.interleaved, lane);
     }
     if (own && wave == 3) {
         float *kn = ks + (np - 1) * KS;
@@ -135,7 +109,7 @@ __global__ __launch_bounds__(256) void k_attn_decode_split(SplitArgs a) {
             vs[(np - 1) * HD + i] = vsrc[i];
         }
         sdy_wave_sync();
-        norm_rope<HD>(kn, a.k_norm, a.eps, cs, sn, a.interleaved, lane);
+        sdy_norm_rope<HD>(kn, a.k_norm, a.eps, cs, sn, a.interleaved, lane);
         float *kw = a.k_cache + g * a.head_stride + (size_t)pos * HD;
         float *vw = a.v_cache + g * a.head_stride + (size_t)pos * HD;
         for (int i = lane; i < HD; i += 64) {

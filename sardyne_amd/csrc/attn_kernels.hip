@@ -1,6 +1,7 @@
 // gfx950 attention (the reference's op_attention_head over attention_worker's (token, head) pairs,
-// csrc/ops.c:405-414 and csrc/model_llama.c:619-634) over the f32 KV cache
-// [n_kv_head][max_seq][head_dim] of a layer, with the reference's arithmetic step by step:
+// csrc/ops.c:405-414 and csrc/model_llama.c:619-634) over the KV cache [n_kv_head][max_seq][head_dim]
+// of a layer (f32, or f16 rounded at the write: sdy_attn_dev.h), with the reference's arithmetic step
+// by step on the cache's f32 values:
 //   score_j = dot(q, k_j) * (1 / sqrtf(head_dim)), dot in the AVX2 order of csrc/ops_avx2.c:61-74
 //     (four 8-lane FMA chains over 32-element steps, 8-element steps into the first chain, the
 //     lane-wise (a0 + a1) + (a2 + a3), the 8-lane tree ((v0 + v4) + (v2 + v6)) + ((v1 + v5) +
@@ -20,6 +21,7 @@
 //   k_attn_prefill_pv<HD, TB>     the same for TB tokens at a time (prefill: each V element read once
 //                                 for the TB tokens' chains)
 //   k_attn_*_any                  the same for other head dims (runtime loops, scalar LDS reads)
+#include "sdy_attn_dev.h"
 #include "sdy_device.h"
 #include "sdy_expf.h"
 #include "sdy_internal.h"
@@ -34,7 +36,7 @@ constexpr int PAIRS = 64;    // (token, head) pairs per prefill scores workgroup
 constexpr int PW = 8192;     // weights held in LDS at a time by k_attn_softmax_pv (all its heads)
 
 // register arrays of 16-byte loads (an ext vector type: arrays of it stay in registers)
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef sdy_f32x4 f32x4;
 
 // One wave: optional per-head RMSNorm (qwen3 q/k norm: double sum, one rounding of the scale) then
 // RoPE (pairs (i, i + hd/2), or (2i, 2i+1) when interleaved) of the hd-vector in buf (LDS).
@@ -64,10 +66,11 @@ SDY_DEV void norm_rope_wave(float *buf, const float *nw, float eps, const float 
 
 // q/k norm + RoPE of the vectors of n_tok tokens and the KV-cache write at positions pos0 + t; token
 // t's q, k and v rows start at t * qs, t * ks, t * vs floats. Grid (n_tok, n_head + n_kv_head), 64 threads.
+template <class KT>
 __global__ __launch_bounds__(64) void k_qk_rope_kv(float *q, float *k, const float *v, long qs, long ks, long vs,
                                                    const float *qn, const float *kn, float eps, const float *rope_cos,
                                                    const float *rope_sin, int pos0, int n_head, int n_kv_head, int hd,
-                                                   int interleaved, float *k_cache, float *v_cache, long head_stride) {
+                                                   int interleaved, KT *k_cache, KT *v_cache, long head_stride) {
     __shared__ float buf[512];
     const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const bool is_q = h < n_head;
@@ -80,12 +83,12 @@ __global__ __launch_bounds__(64) void k_qk_rope_kv(float *q, float *k, const flo
                    interleaved, lane);
     for (int i = lane; i < hd; i += 64) vec[i] = buf[i];
     if (!is_q && k_cache) {
-        float *kc = k_cache + hh * head_stride + (size_t)pos * hd;
-        float *vc = v_cache + hh * head_stride + (size_t)pos * hd;
+        KT *kc = k_cache + hh * head_stride + (size_t)pos * hd;
+        KT *vc = v_cache + hh * head_stride + (size_t)pos * hd;
         const float *vv = v + (size_t)t * vs + (size_t)hh * hd;
         for (int i = lane; i < hd; i += 64) {
-            kc[i] = buf[i];
-            vc[i] = vv[i];
+            KvElt<KT>::st(kc, i, buf[i]);
+            KvElt<KT>::st(vc, i, vv[i]);
         }
     }
 }
@@ -99,7 +102,7 @@ struct AttnArgs {
     const int32_t *step;              // decode: step[1] = position of the token
     int n_head, n_kv_head, n_kv0, n_tok, interleaved;
     long q_stride;
-    float *k_cache, *v_cache;         // [n_kv_head][max_seq][HD]
+    void *k_cache, *v_cache;          // [n_kv_head][max_seq][HD] of the kernel's element type KT
     long head_stride;                 // max_seq * HD
     float *scores;                    // [n_tok][n_head][max_kv]
     int max_kv;
@@ -233,7 +236,7 @@ SDY_DEV float dot_avx2_order(const float *q, const K &k) {
 // norm's sum has norm_rope_wave's per-lane order (elements l, l + 64, ...) and tree; the results go
 // to LDS (qs, kp) and, for the new k, to the KV cache. Returns false (nothing done) for other
 // shapes, which take norm_rope_wave.
-template <int HD>
+template <int HD, class KT>
 SDY_DEV bool decode_prep_regs(const AttnArgs &a, int g, int n_rep, int pos, bool has_pos, const float *cs,
                               const float *sn, float *qs, float *kp, int wave, int lane) {
     constexpr int E = HD / 64, EH = E / 2, RM = 4;  // elements per lane; vectors per wave
@@ -294,12 +297,12 @@ SDY_DEV bool decode_prep_regs(const AttnArgs &a, int g, int n_rep, int pos, bool
 #pragma unroll
             for (int e = 0; e < E; e++) buf[lane + 64 * e] = y[e];
             if (is_k && has_pos) {  // KV-cache write of the new position
-                float *kc = a.k_cache + g * a.head_stride + (size_t)pos * HD;
-                float *vc = a.v_cache + g * a.head_stride + (size_t)pos * HD;
+                KT *kc = (KT *)a.k_cache + g * a.head_stride + (size_t)pos * HD;
+                KT *vc = (KT *)a.v_cache + g * a.head_stride + (size_t)pos * HD;
 #pragma unroll
                 for (int e = 0; e < E; e++) {
-                    kc[lane + 64 * e] = y[e];
-                    vc[lane + 64 * e] = vv[e];
+                    KvElt<KT>::st(kc, lane + 64 * e, y[e]);
+                    KvElt<KT>::st(vc, lane + 64 * e, vv[e]);
                 }
             }
         }
@@ -314,7 +317,7 @@ SDY_DEV bool decode_prep_regs(const AttnArgs &a, int g, int n_rep, int pos, bool
 // position's K comes from LDS. Lane p of a wave computes the score of position p0 + p for one
 // (token, head) pair; the waves share the staged K chunk ([CH][HD + 4]: 16-byte rows, 8
 // consecutive rows in distinct banks).
-template <int HD, bool DECODE>
+template <int HD, bool DECODE, class KT>
 __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
     constexpr int KS = HD + 4;
     constexpr int NV = CH * HD / 4 / 256 > 0 ? CH * HD / 4 / 256 : 1;  // float4 of K per thread
@@ -340,13 +343,13 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
     if (p0 >= n_kv_last) return;
     const int np_max = n_kv_last - p0 < CH ? n_kv_last - p0 : CH;
     // K chunk loads first (clamped indices, unconditional)
-    const float *kg = a.k_cache + g * a.head_stride + (size_t)p0 * HD;
+    const KT *kg = (const KT *)a.k_cache + g * a.head_stride + (size_t)p0 * HD;
     const int n4 = np_max * HD / 4;
     f32x4 kv[NV];
 #pragma unroll
     for (int j = 0; j < NV; j++) {
         const int i = tid + 256 * j < n4 ? tid + 256 * j : 0;
-        kv[j] = reinterpret_cast<const f32x4 *>(kg)[i];
+        kv[j] = KvElt<KT>::ld4(kg, (size_t)4 * i);
     }
     const int n_pairs = (t1 - t0) * n_rep;
     bool has_pos = false;
@@ -354,7 +357,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
         // q heads of the group and the new k: norm + RoPE (one wave per vector)
         has_pos = p0 + np_max == pos + 1;
         const float *cs = a.rope_cos + (size_t)pos * (HD / 2), *sn = a.rope_sin + (size_t)pos * (HD / 2);
-        const bool done = decode_prep_regs<HD>(a, g, n_rep, pos, has_pos, cs, sn, qs, kp, wave, lane);
+        const bool done = decode_prep_regs<HD, KT>(a, g, n_rep, pos, has_pos, cs, sn, qs, kp, wave, lane);
         for (int r = wave; !done && r <= n_rep; r += 4) {
             const bool is_k = r == n_rep;
             float *buf = is_k ? kp : qs + r * HD;
@@ -363,12 +366,12 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
             sdy_wave_sync();
             norm_rope_wave(buf, is_k ? a.k_norm : a.q_norm, a.eps, cs, sn, HD, a.interleaved, lane);
             if (is_k && has_pos) {  // KV-cache write of the new position
-                float *kc = a.k_cache + g * a.head_stride + (size_t)pos * HD;
-                float *vc = a.v_cache + g * a.head_stride + (size_t)pos * HD;
+                KT *kc = (KT *)a.k_cache + g * a.head_stride + (size_t)pos * HD;
+                KT *vc = (KT *)a.v_cache + g * a.head_stride + (size_t)pos * HD;
                 const float *vn = a.v + (size_t)g * HD;
                 for (int i = lane; i < HD; i += 64) {
-                    kc[i] = buf[i];
-                    vc[i] = vn[i];
+                    KvElt<KT>::st(kc, i, buf[i]);
+                    KvElt<KT>::st(vc, i, vn[i]);
                 }
             }
         }
@@ -390,9 +393,9 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
         *reinterpret_cast<f32x4 *>(ks + p * KS + d) = kv[j];
     }
     __syncthreads();
-    if constexpr (DECODE) {
+    if constexpr (DECODE) {  // the new position's K as the cache holds it
         if (special >= 0)
-            for (int d = tid; d < HD; d += 256) ks[special * KS + d] = kp[d];
+            for (int d = tid; d < HD; d += 256) ks[special * KS + d] = KvElt<KT>::round(kp[d]);
         __syncthreads();
     }
     // the scores of the wave's pairs; with K from kr (the lane's row) or from LDS
@@ -423,7 +426,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
 // Per head: max and the double sum of e_j over the token's positions (reductions across the head's
 // threads), then the weights in LDS (PW / HPB positions per head at a time) and out[d] = one FMA
 // chain over the positions in order. Decode: the 256 outputs (one Q8_K block) are also quantised to xq.
-template <int HD, bool DECODE>
+template <int HD, bool DECODE, class KT>
 __global__ __launch_bounds__(256) void k_attn_softmax_pv(AttnArgs a) {
     constexpr int HPB = 256 / HD, GW = HD < 64 ? HD : 64;  // heads per block, lanes per head in a wave
     constexpr int PB = PW / HPB;                           // weights per head per pass
@@ -459,7 +462,7 @@ __global__ __launch_bounds__(256) void k_attn_softmax_pv(AttnArgs a) {
     }
     const float inv = (float)(1.0 / sum);
     // weighted V, PB positions at a time
-    const float *vg = a.v_cache + g * a.head_stride + d;
+    const KT *vg = (const KT *)a.v_cache + g * a.head_stride + d;
     float acc = 0.0f;
     for (int jb = 0; jb < n; jb += PB) {
         const int je = jb + PB < n ? jb + PB : n;
@@ -470,11 +473,11 @@ __global__ __launch_bounds__(256) void k_attn_softmax_pv(AttnArgs a) {
         for (; j + 8 <= je; j += 8) {
             float vv[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) vv[u] = vg[(size_t)(j + u) * HD];
+            for (int u = 0; u < 8; u++) vv[u] = KvElt<KT>::ld(vg, (size_t)(j + u) * HD);
 #pragma unroll
             for (int u = 0; u < 8; u++) acc = fmaf(pw[hl][j + u - jb], vv[u], acc);
         }
-        for (; j < je; j++) acc = fmaf(pw[hl][j - jb], vg[(size_t)j * HD], acc);
+        for (; j < je; j++) acc = fmaf(pw[hl][j - jb], KvElt<KT>::ld(vg, (size_t)j * HD), acc);
     }
     if (h_raw < a.n_head) a.out[(size_t)t * a.out_stride + (size_t)h * HD + d] = acc;
     if constexpr (DECODE) {
@@ -495,7 +498,7 @@ __global__ __launch_bounds__(256) void k_attn_softmax_pv(AttnArgs a) {
 // in-order FMA chain per output), but each V element is read once for the TB tokens, whose chains
 // advance together position by position (TB independent chains per thread). Tokens past n_tok
 // repeat the last one and store nothing.
-template <int HD, int TB>
+template <int HD, int TB, class KT>
 __global__ __launch_bounds__(256) void k_attn_prefill_pv(AttnArgs a) {
     constexpr int HPB = 256 / HD, GW = HD < 64 ? HD : 64, NW = HD > 64 ? HD / 64 : 1;
     constexpr int PB = PW / (HPB * TB);  // weights per (token, head) per pass
@@ -548,7 +551,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill_pv(AttnArgs a) {
             inv[ti] = (float)(1.0 / sum);
         }
     }
-    const float *vg = a.v_cache + g * a.head_stride + d;
+    const KT *vg = (const KT *)a.v_cache + g * a.head_stride + d;
     float acc[TB];
 #pragma unroll
     for (int ti = 0; ti < TB; ti++) acc[ti] = 0.0f;
@@ -566,14 +569,14 @@ __global__ __launch_bounds__(256) void k_attn_prefill_pv(AttnArgs a) {
         for (; j + 8 <= je_all; j += 8) {  // positions every token of the block sees
             float vv[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) vv[u] = vg[(size_t)(j + u) * HD];
+            for (int u = 0; u < 8; u++) vv[u] = KvElt<KT>::ld(vg, (size_t)(j + u) * HD);
 #pragma unroll
             for (int u = 0; u < 8; u++)
 #pragma unroll
                 for (int ti = 0; ti < TB; ti++) acc[ti] = fmaf(pw[ti][hl][j + u - jb], vv[u], acc[ti]);
         }
         for (; j < je_any; j++) {
-            const float v = vg[(size_t)j * HD];
+            const float v = KvElt<KT>::ld(vg, (size_t)j * HD);
 #pragma unroll
             for (int ti = 0; ti < TB; ti++)
                 if (j < nt[ti]) acc[ti] = fmaf(pw[ti][hl][j - jb], v, acc[ti]);
@@ -648,9 +651,9 @@ __global__ __launch_bounds__(256) void k_attn_decode_softmax(AttnArgs a) {
 // floats (each by HPW lanes) and its weight loads read four positions of each head at once. The
 // chains are latency-bound, so the grid is n_kv_head * (n_rep / HPW) * (HD / DS) one-wave workgroups
 // (one per CU), each with PF positions in flight in registers.
-template <int HD, int HPW, int PF>
+template <int HD, int HPW, int PF, class KT>
 __global__ __launch_bounds__(64) void k_attn_decode_wv(AttnArgs a) {
-    constexpr int DS = 64 / HPW, NS = HD / DS, G = PF / 4;
+    constexpr int DS = 64 / HPW, NS = HD / DS, G = PF / 4, B = KvElt<KT>::BYTES;
     static_assert(DS * HPW == 64 && NS * DS == HD && PF % 4 == 0 && 3 * HD * 4 < 4096, "shape");
     const int lane = threadIdx.x, r = lane / DS, dd = lane - r * DS;
     const int n_rep = a.n_head / a.n_kv_head, n_hg = n_rep / HPW;
@@ -659,26 +662,24 @@ __global__ __launch_bounds__(64) void k_attn_decode_wv(AttnArgs a) {
     const int n = a.step[1] + 1;
     // Buffer reads, range-checked on the lane offset (plus the instruction's constant offset): V rows
     // at or past n and weights past the last head's row read as 0 and are never used.
-    const __amdgpu_buffer_rsrc_t rv =
-        __builtin_amdgcn_make_buffer_rsrc(a.v_cache + g * a.head_stride, (short)0, n * HD * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((KT *)a.v_cache + g * a.head_stride, (short)0,
+                                                                        n * HD * B, 0x00020000);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(a.scores + (size_t)h0 * a.max_kv, (short)0,
                                                                         HPW * a.max_kv * 4, 0x00020000);
-    // position j of the group at lane offset o: V row j + k at o + k * HD * 4 (constant offsets)
-    auto ldv = [&](uint32_t o, int k) {
-        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rv, o + k * HD * 4, 0, 0));
-    };
+    // position j of the group at lane offset o: V row j + k at o + k * HD * B (constant offsets)
+    auto ldv = [&](uint32_t o, int k) { return KvElt<KT>::ld_buf(rv, o + k * HD * B); };
     auto ldw = [&](uint32_t o) { return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, 0)); };
-    uint32_t ov = d * 4, ow = r * a.max_kv * 4;  // the next refill's group 0 (V row, weight)
+    uint32_t ov = d * B, ow = r * a.max_kv * 4;  // the next refill's group 0 (V row, weight)
     float vr[PF];
     f32x4 wr[G];  // wr[q][k] and vr[4q + k] hold position j + 4q + k
 #pragma unroll
     for (int q = 0; q < G; q++) {
         wr[q] = ldw(ow + q * 16);
 #pragma unroll
-        for (int k = 0; k < 4; k++) vr[4 * q + k] = ldv(ov + q * 4 * HD * 4, k);
+        for (int k = 0; k < 4; k++) vr[4 * q + k] = ldv(ov + q * 4 * HD * B, k);
         __builtin_amdgcn_sched_barrier(0);  // issued in position order
     }
-    ov += PF * HD * 4;
+    ov += PF * HD * B;
     ow += PF * 4;
     float acc = 0.0f;
     int j = 0;
@@ -692,12 +693,12 @@ __global__ __launch_bounds__(64) void k_attn_decode_wv(AttnArgs a) {
             // slots are read, so each refill reuses its slot's registers
             uint32_t z;
             asm volatile("s_mov_b32 %0, 0" : "=s"(z) : "v"(acc));
-            const uint32_t oq = ov + q * 4 * HD * 4 + z;
+            const uint32_t oq = ov + q * 4 * HD * B + z;
             wr[q] = ldw(ow + q * 16 + z);
 #pragma unroll
             for (int k = 0; k < 4; k++) vr[4 * q + k] = ldv(oq, k);
         }
-        ov += PF * HD * 4;
+        ov += PF * HD * B;
         ow += PF * 4;
     }
 #pragma unroll
@@ -715,9 +716,9 @@ __global__ __launch_bounds__(64) void k_attn_decode_wv(AttnArgs a) {
 // gives a lane four positions of its dim, and one (a broadcast within the head's 16 lanes) four
 // of its weights. R blocks of loads stay in flight in registers; LDS is double-buffered by block
 // parity (block b + 1 is staged while block b is consumed).
-template <int HD, int R>
+template <int HD, int R, class KT>
 __global__ __launch_bounds__(64) void k_attn_decode_wv4(AttnArgs a) {
-    constexpr int NS = HD / 16;
+    constexpr int NS = HD / 16, B = KvElt<KT>::BYTES;
     static_assert(NS * 16 == HD && R % 2 == 0, "shape");
     __shared__ __align__(16) float tv[2][4][64];  // [block parity][group][c * 4 + position in group]
     __shared__ __align__(16) float tw[2][64];     // [block parity][r * 16 + position in block]
@@ -728,17 +729,16 @@ __global__ __launch_bounds__(64) void k_attn_decode_wv4(AttnArgs a) {
     const int n = a.step[1] + 1, nbk = (n + 15) / 16;
     // Buffer reads, range-checked on the lane offset: V rows at or past n, and weights past the
     // last head's row, read as 0; positions past n are never used.
-    const __amdgpu_buffer_rsrc_t rsv =
-        __builtin_amdgcn_make_buffer_rsrc(a.v_cache + g * a.head_stride, (short)0, n * HD * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc((KT *)a.v_cache + g * a.head_stride, (short)0,
+                                                                         n * HD * B, 0x00020000);
     const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(a.scores + (size_t)h0 * a.max_kv, (short)0,
                                                                          4 * a.max_kv * 4, 0x00020000);
-    const uint32_t ov = (uint32_t)(r * HD + d) * 4, ow = (uint32_t)(r * a.max_kv + c) * 4;
+    const uint32_t ov = (uint32_t)(r * HD + d) * B, ow = (uint32_t)(r * a.max_kv + c) * 4;
     float rv[R][4], rw[R];  // ring slot t holds the loads of a block b with b % R == t
     auto issue = [&](int t, uint32_t b) {
-        const uint32_t vb = ov + b * 16u * HD * 4;
+        const uint32_t vb = ov + b * 16u * HD * B;
 #pragma unroll
-        for (int q = 0; q < 4; q++)
-            rv[t][q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsv, vb + q * 4 * HD * 4, 0, 0));
+        for (int q = 0; q < 4; q++) rv[t][q] = KvElt<KT>::ld_buf(rsv, vb + q * 4 * HD * B);
         rw[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsw, ow + b * 64u, 0, 0));
     };
     auto stage = [&](int t, int par) {
@@ -835,7 +835,7 @@ SDY_DEV float dot_avx2_order_any(const float *q, const float *k, int hd) {
     return s;
 }
 
-template <bool DECODE>
+template <bool DECODE, class KT>
 __global__ __launch_bounds__(256) void k_attn_scores_any(AttnArgs a, int hd) {
     extern __shared__ __align__(16) float sm[];
     const int KS = hd | 1;
@@ -872,11 +872,11 @@ __global__ __launch_bounds__(256) void k_attn_scores_any(AttnArgs a, int hd) {
             sdy_wave_sync();
             norm_rope_wave(buf, is_k ? a.k_norm : a.q_norm, a.eps, cs, sn, hd, a.interleaved, lane);
             if (is_k && has_pos) {
-                float *kc = a.k_cache + g * a.head_stride + (size_t)pos * hd;
-                float *vc = a.v_cache + g * a.head_stride + (size_t)pos * hd;
+                KT *kc = (KT *)a.k_cache + g * a.head_stride + (size_t)pos * hd;
+                KT *vc = (KT *)a.v_cache + g * a.head_stride + (size_t)pos * hd;
                 for (int i = lane; i < hd; i += 64) {
-                    kc[i] = buf[i];
-                    vc[i] = a.v[(size_t)g * hd + i];
+                    KvElt<KT>::st(kc, i, buf[i]);
+                    KvElt<KT>::st(vc, i, a.v[(size_t)g * hd + i]);
                 }
             }
         }
@@ -887,15 +887,15 @@ __global__ __launch_bounds__(256) void k_attn_scores_any(AttnArgs a, int hd) {
         }
     }
     const int special = DECODE && has_pos ? pos - p0 : -1;
-    const float *kg = a.k_cache + g * a.head_stride + (size_t)p0 * hd;
+    const KT *kg = (const KT *)a.k_cache + g * a.head_stride + (size_t)p0 * hd;
     for (int i = tid; i < np_max * hd; i += 256) {
         const int p = i / hd, d = i - p * hd;
-        if (p != special) ks[p * KS + d] = kg[i];
+        if (p != special) ks[p * KS + d] = KvElt<KT>::ld(kg, i);
     }
     __syncthreads();
-    if constexpr (DECODE) {
+    if constexpr (DECODE) {  // the new position's K as the cache holds it
         if (special >= 0)
-            for (int d = tid; d < hd; d += 256) ks[special * KS + d] = kp[d];
+            for (int d = tid; d < hd; d += 256) ks[special * KS + d] = KvElt<KT>::round(kp[d]);
         __syncthreads();
     }
     for (int pr = wave; pr < n_pairs; pr += 4) {
@@ -910,7 +910,7 @@ __global__ __launch_bounds__(256) void k_attn_scores_any(AttnArgs a, int hd) {
 
 // Softmax and weighted V of one head of one token per workgroup (256 threads; output elements
 // tid, tid + 256, ...), any head_dim. Decode: no Q8_K output (the caller quantises).
-template <bool DECODE>
+template <bool DECODE, class KT>
 __global__ __launch_bounds__(256) void k_attn_softmax_pv_any(AttnArgs a, int hd) {
     __shared__ float pw[PW];
     __shared__ float redf[4];
@@ -931,7 +931,7 @@ __global__ __launch_bounds__(256) void k_attn_softmax_pv_any(AttnArgs a, int hd)
     __syncthreads();
     sum = (redd[0] + redd[1]) + (redd[2] + redd[3]);
     const float inv = (float)(1.0 / sum);
-    const float *vg = a.v_cache + g * a.head_stride;
+    const KT *vg = (const KT *)a.v_cache + g * a.head_stride;
     for (int d0 = 0; d0 < hd; d0 += 256) {
         const int d = d0 + tid;
         float acc = 0.0f;
@@ -941,7 +941,7 @@ __global__ __launch_bounds__(256) void k_attn_softmax_pv_any(AttnArgs a, int hd)
             row_weights(row, jb + tid, 256, je, m, inv, pw, jb, 1);
             __syncthreads();
             if (d < hd)
-                for (int j = jb; j < je; j++) acc = fmaf(pw[j - jb], vg[(size_t)j * hd + d], acc);
+                for (int j = jb; j < je; j++) acc = fmaf(pw[j - jb], KvElt<KT>::ld(vg, (size_t)j * hd + d), acc);
         }
         if (d < hd) a.out[(size_t)t * a.out_stride + (size_t)h * hd + d] = acc;
     }
@@ -968,43 +968,45 @@ static size_t scores_lds(int hd, int n_pairs) {
     return sizeof(float) * ((size_t)CH * (hd + 4) + hd + (size_t)n_pairs * hd);
 }
 
-template <int HD, bool DECODE>
+template <int HD, bool DECODE, class KT>
 static int launch_attn(AttnArgs &A, int nc, int n_tblk, hipStream_t st) {
     const int n_rep = A.n_head / A.n_kv_head;
     const int n_pairs = DECODE ? n_rep : (PAIRS / n_rep > 0 ? PAIRS / n_rep : 1) * n_rep;
     const size_t lds = scores_lds(HD, n_pairs);
     static size_t granted = 0;
-    int rc = sdy_lds_limit((const void *)k_attn_scores<HD, DECODE>, lds, &granted);
+    int rc = sdy_lds_limit((const void *)k_attn_scores<HD, DECODE, KT>, lds, &granted);
     if (rc) return rc;
-    SDY_NOTE_KERNEL((k_attn_scores<HD, DECODE>));
-    hipLaunchKernelGGL((k_attn_scores<HD, DECODE>), dim3(nc, A.n_kv_head, n_tblk), dim3(256), lds, st, A);
+    SDY_NOTE_KERNEL((k_attn_scores<HD, DECODE, KT>));
+    hipLaunchKernelGGL((k_attn_scores<HD, DECODE, KT>), dim3(nc, A.n_kv_head, n_tblk), dim3(256), lds, st, A);
     if ((rc = sdy_check_launch("attention_scores"))) return rc;
     if constexpr (DECODE) {
-        SDY_NOTE_KERNEL((k_attn_softmax_pv<HD, DECODE>));
-        hipLaunchKernelGGL((k_attn_softmax_pv<HD, DECODE>), dim3((A.n_head * HD + 255) / 256, 1), dim3(256), 0, st, A);
+        SDY_NOTE_KERNEL((k_attn_softmax_pv<HD, DECODE, KT>));
+        hipLaunchKernelGGL((k_attn_softmax_pv<HD, DECODE, KT>), dim3((A.n_head * HD + 255) / 256, 1), dim3(256), 0, st,
+                           A);
     } else {  // four tokens per workgroup
         constexpr int TB = 4;
-        SDY_NOTE_KERNEL((k_attn_prefill_pv<HD, TB>));
-        hipLaunchKernelGGL((k_attn_prefill_pv<HD, TB>), dim3((A.n_head * HD + 255) / 256, (A.n_tok + TB - 1) / TB),
+        SDY_NOTE_KERNEL((k_attn_prefill_pv<HD, TB, KT>));
+        hipLaunchKernelGGL((k_attn_prefill_pv<HD, TB, KT>), dim3((A.n_head * HD + 255) / 256, (A.n_tok + TB - 1) / TB),
                            dim3(256), 0, st, A);
     }
     return sdy_check_launch("attention_softmax_pv");
 }
 
-template <bool DECODE>
+template <bool DECODE, class KT>
 static int launch_attn_any(AttnArgs &A, int hd, int nc, int n_tblk, hipStream_t st) {
     const int n_rep = A.n_head / A.n_kv_head;
     const int n_pairs = DECODE ? n_rep : (PAIRS / n_rep > 0 ? PAIRS / n_rep : 1) * n_rep;
     const size_t lds = sizeof(float) * ((size_t)CH * (hd | 1) + hd + (size_t)n_pairs * hd);
     if (lds > 160 * 1024) return sdy_fail(-1, "attention: head_dim %d needs %zu bytes of LDS", hd, lds);
     static size_t granted = 0;
-    int rc = sdy_lds_limit((const void *)k_attn_scores_any<DECODE>, lds, &granted);
+    int rc = sdy_lds_limit((const void *)k_attn_scores_any<DECODE, KT>, lds, &granted);
     if (rc) return rc;
-    SDY_NOTE_KERNEL((k_attn_scores_any<DECODE>));
-    hipLaunchKernelGGL((k_attn_scores_any<DECODE>), dim3(nc, A.n_kv_head, n_tblk), dim3(256), lds, st, A, hd);
+    SDY_NOTE_KERNEL((k_attn_scores_any<DECODE, KT>));
+    hipLaunchKernelGGL((k_attn_scores_any<DECODE, KT>), dim3(nc, A.n_kv_head, n_tblk), dim3(256), lds, st, A, hd);
     if ((rc = sdy_check_launch("attention_scores"))) return rc;
-    SDY_NOTE_KERNEL((k_attn_softmax_pv_any<DECODE>));
-    hipLaunchKernelGGL((k_attn_softmax_pv_any<DECODE>), dim3(A.n_head, DECODE ? 1 : A.n_tok), dim3(256), 0, st, A, hd);
+    SDY_NOTE_KERNEL((k_attn_softmax_pv_any<DECODE, KT>));
+    hipLaunchKernelGGL((k_attn_softmax_pv_any<DECODE, KT>), dim3(A.n_head, DECODE ? 1 : A.n_tok), dim3(256), 0, st, A,
+                       hd);
     if ((rc = sdy_check_launch("attention_softmax_pv"))) return rc;
     if (DECODE && A.xq) return sdy_quantize(SDY_Q8_K, A.out, A.xq, A.n_head * hd, 1, (sdy_stream)st);
     return 0;
@@ -1013,76 +1015,96 @@ static int launch_attn_any(AttnArgs &A, int hd, int nc, int n_tblk, hipStream_t 
 // decode: k_attn_scores, k_attn_decode_softmax, k_attn_decode_wv4 (four heads of a KV group per wave)
 // or, when 4 does not divide n_rep, k_attn_decode_wv (one head per wave), then the Q8_K row of the
 // output when asked for.
-template <int HD>
+template <int HD, class KT>
 static int launch_attn_decode(AttnArgs &A, int nc, hipStream_t st) {
     const int n_rep = A.n_head / A.n_kv_head;
     const size_t lds = scores_lds(HD, n_rep);
     static size_t granted = 0;
-    int rc = sdy_lds_limit((const void *)k_attn_scores<HD, true>, lds, &granted);
+    int rc = sdy_lds_limit((const void *)k_attn_scores<HD, true, KT>, lds, &granted);
     if (rc) return rc;
-    SDY_NOTE_KERNEL((k_attn_scores<HD, true>));
-    hipLaunchKernelGGL((k_attn_scores<HD, true>), dim3(nc, A.n_kv_head, 1), dim3(256), lds, st, A);
+    SDY_NOTE_KERNEL((k_attn_scores<HD, true, KT>));
+    hipLaunchKernelGGL((k_attn_scores<HD, true, KT>), dim3(nc, A.n_kv_head, 1), dim3(256), lds, st, A);
     if ((rc = sdy_check_launch("attention_scores"))) return rc;
     SDY_NOTE_KERNEL(k_attn_decode_softmax);
     hipLaunchKernelGGL(k_attn_decode_softmax, dim3(A.n_head), dim3(256), 0, st, A);
     if ((rc = sdy_check_launch("attention_decode_softmax"))) return rc;
     if (n_rep % 4) {
-        SDY_NOTE_KERNEL((k_attn_decode_wv<HD, 1, 32>));
-        hipLaunchKernelGGL((k_attn_decode_wv<HD, 1, 32>), dim3(A.n_head * (HD / 64)), dim3(64), 0, st, A);
+        SDY_NOTE_KERNEL((k_attn_decode_wv<HD, 1, 32, KT>));
+        hipLaunchKernelGGL((k_attn_decode_wv<HD, 1, 32, KT>), dim3(A.n_head * (HD / 64)), dim3(64), 0, st, A);
     } else {
-        SDY_NOTE_KERNEL((k_attn_decode_wv4<HD, 8>));
-        hipLaunchKernelGGL((k_attn_decode_wv4<HD, 8>), dim3(A.n_head * HD / 64), dim3(64), 0, st, A);
+        SDY_NOTE_KERNEL((k_attn_decode_wv4<HD, 8, KT>));
+        hipLaunchKernelGGL((k_attn_decode_wv4<HD, 8, KT>), dim3(A.n_head * HD / 64), dim3(64), 0, st, A);
     }
     if ((rc = sdy_check_launch("attention_decode_wv"))) return rc;
     if (A.xq) return sdy_quantize(SDY_Q8_K, A.out, A.xq, A.n_head * HD, 1, (sdy_stream)st);
     return 0;
 }
 
-template <bool DECODE>
+template <bool DECODE, class KT>
 static int attn_dispatch(AttnArgs &A, int hd, int nc, int n_tblk, hipStream_t st) {
     if constexpr (DECODE) {
         switch (hd) {
-        case 64: return launch_attn_decode<64>(A, nc, st);
-        case 128: return launch_attn_decode<128>(A, nc, st);
-        case 256: return launch_attn_decode<256>(A, nc, st);
+        case 64: return launch_attn_decode<64, KT>(A, nc, st);
+        case 128: return launch_attn_decode<128, KT>(A, nc, st);
+        case 256: return launch_attn_decode<256, KT>(A, nc, st);
         default: break;
         }
     }
     switch (hd) {
-    case 32: return launch_attn<32, DECODE>(A, nc, n_tblk, st);
-    case 64: return launch_attn<64, DECODE>(A, nc, n_tblk, st);
-    case 128: return launch_attn<128, DECODE>(A, nc, n_tblk, st);
-    case 256: return launch_attn<256, DECODE>(A, nc, n_tblk, st);
-    default: return launch_attn_any<DECODE>(A, hd, nc, n_tblk, st);
+    case 32: return launch_attn<32, DECODE, KT>(A, nc, n_tblk, st);
+    case 64: return launch_attn<64, DECODE, KT>(A, nc, n_tblk, st);
+    case 128: return launch_attn<128, DECODE, KT>(A, nc, n_tblk, st);
+    case 256: return launch_attn<256, DECODE, KT>(A, nc, n_tblk, st);
+    default: return launch_attn_any<DECODE, KT>(A, hd, nc, n_tblk, st);
     }
 }
 
+template <bool DECODE>
+static int attn_dispatch_kv(AttnArgs &A, int kv_type, int hd, int nc, int n_tblk, hipStream_t st) {
+    return kv_type == SDY_KV_F16 ? attn_dispatch<DECODE, uint16_t>(A, hd, nc, n_tblk, st)
+                                 : attn_dispatch<DECODE, float>(A, hd, nc, n_tblk, st);
+}
+
+extern "C" size_t sdy_kv_elt_bytes(int kv_type) {
+    return kv_type == SDY_KV_F32 ? 4 : kv_type == SDY_KV_F16 ? 2 : 0;
+}
+
+static int kv_type_fail(int kv_type) { return sdy_fail(-1, "KV cache element type %d not supported", kv_type); }
+
 extern "C" int sdy_qk_rope_kv(float *q, float *k, const float *v, const float *qn, const float *kn, float eps,
                               const float *rope_cos, const float *rope_sin, int pos0, int n_tok, int n_head,
-                              int n_kv_head, int hd, int interleaved, float *k_cache, float *v_cache,
+                              int n_kv_head, int hd, int interleaved, void *k_cache, void *v_cache, int kv_type,
                               long head_stride, sdy_stream s) {
     return sdy_qk_rope_kv_strided(q, k, v, (long)n_head * hd, (long)n_kv_head * hd, (long)n_kv_head * hd, qn, kn, eps,
                                   rope_cos, rope_sin, pos0, n_tok, n_head, n_kv_head, hd, interleaved, k_cache, v_cache,
-                                  head_stride, s);
+                                  kv_type, head_stride, s);
 }
 
 extern "C" int sdy_qk_rope_kv_strided(float *q, float *k, const float *v, long q_stride, long k_stride, long v_stride,
                                       const float *qn, const float *kn, float eps, const float *rope_cos,
                                       const float *rope_sin, int pos0, int n_tok, int n_head, int n_kv_head, int hd,
-                                      int interleaved, float *k_cache, float *v_cache, long head_stride, sdy_stream s) {
+                                      int interleaved, void *k_cache, void *v_cache, int kv_type, long head_stride,
+                                      sdy_stream s) {
     if (hd > 512) return sdy_fail(-1, "head_dim %d above 512", hd);
+    if (!sdy_kv_elt_bytes(kv_type)) return kv_type_fail(kv_type);
     if (n_tok <= 0) return 0;
-    hipLaunchKernelGGL(k_qk_rope_kv, dim3(n_tok, n_head + n_kv_head), dim3(64), 0, (hipStream_t)s, q, k, v, q_stride,
-                       k_stride, v_stride, qn, kn, eps, rope_cos, rope_sin, pos0, n_head, n_kv_head, hd, interleaved,
-                       k_cache, v_cache, head_stride);
+    if (kv_type == SDY_KV_F16)
+        hipLaunchKernelGGL(k_qk_rope_kv<uint16_t>, dim3(n_tok, n_head + n_kv_head), dim3(64), 0, (hipStream_t)s, q, k, v,
+                           q_stride, k_stride, v_stride, qn, kn, eps, rope_cos, rope_sin, pos0, n_head, n_kv_head, hd,
+                           interleaved, (uint16_t *)k_cache, (uint16_t *)v_cache, head_stride);
+    else
+        hipLaunchKernelGGL(k_qk_rope_kv<float>, dim3(n_tok, n_head + n_kv_head), dim3(64), 0, (hipStream_t)s, q, k, v,
+                           q_stride, k_stride, v_stride, qn, kn, eps, rope_cos, rope_sin, pos0, n_head, n_kv_head, hd,
+                           interleaved, (float *)k_cache, (float *)v_cache, head_stride);
     return sdy_check_launch("qk_rope_kv");
 }
 
-extern "C" int sdy_attention(const float *q, const float *k_cache, const float *v_cache, int n_tok, int n_head,
-                             int n_kv_head, int hd, int n_kv0, long head_stride, long q_stride, float *scores,
-                             float *out, long out_stride, sdy_stream s) {
+extern "C" int sdy_attention(const float *q, const void *k_cache, const void *v_cache, int kv_type, int n_tok,
+                             int n_head, int n_kv_head, int hd, int n_kv0, long head_stride, long q_stride,
+                             float *scores, float *out, long out_stride, sdy_stream s) {
     if (n_tok <= 0) return 0;
     if (!head_dim_ok(n_head, n_kv_head, hd)) return shape_fail(n_head, n_kv_head, hd);
+    if (!sdy_kv_elt_bytes(kv_type)) return kv_type_fail(kv_type);
     AttnArgs A = {};
     A.q = q;
     A.n_head = n_head;
@@ -1090,8 +1112,8 @@ extern "C" int sdy_attention(const float *q, const float *k_cache, const float *
     A.n_kv0 = n_kv0;
     A.n_tok = n_tok;
     A.q_stride = q_stride;
-    A.k_cache = (float *)k_cache;
-    A.v_cache = (float *)v_cache;
+    A.k_cache = (void *)k_cache;
+    A.v_cache = (void *)v_cache;
     A.head_stride = head_stride;
     A.scores = scores;
     A.max_kv = n_kv0 + n_tok - 1;
@@ -1100,7 +1122,7 @@ extern "C" int sdy_attention(const float *q, const float *k_cache, const float *
     A.out_stride = out_stride;
     const int n_rep = n_head / n_kv_head, tbs = PAIRS / n_rep > 0 ? PAIRS / n_rep : 1;
     const int nc = (A.max_kv + CH - 1) / CH;
-    return attn_dispatch<false>(A, hd, nc, (n_tok + tbs - 1) / tbs, (hipStream_t)s);
+    return attn_dispatch_kv<false>(A, kv_type, hd, nc, (n_tok + tbs - 1) / tbs, (hipStream_t)s);
 }
 
 extern "C" int sdy_attn_decode_ok(int n_head, int n_kv_head, int hd, int max_seq) {
@@ -1111,9 +1133,10 @@ extern "C" int sdy_attn_decode_ok(int n_head, int n_kv_head, int hd, int max_seq
 extern "C" int sdy_attn_decode(const float *q, const float *k, const float *v, const float *q_norm,
                                const float *k_norm, float eps, const float *rope_cos, const float *rope_sin,
                                const int32_t *step_dev, int n_head, int n_kv_head, int hd, int interleaved,
-                               float *k_cache, float *v_cache, long head_stride, int max_seq, float *scores,
-                               float *out, void *xq_q8k, sdy_stream s) {
+                               void *k_cache, void *v_cache, int kv_type, long head_stride, int max_seq,
+                               float *scores, float *out, void *xq_q8k, sdy_stream s) {
     if (!sdy_attn_decode_ok(n_head, n_kv_head, hd, max_seq)) return shape_fail(n_head, n_kv_head, hd);
+    if (!sdy_kv_elt_bytes(kv_type)) return kv_type_fail(kv_type);
     if (xq_q8k && (n_head * hd) % 256) return sdy_fail(-1, "attn_decode: %d outputs are not whole Q8_K blocks", n_head * hd);
     AttnArgs A = {};
     A.q = q;
@@ -1138,5 +1161,5 @@ extern "C" int sdy_attn_decode(const float *q, const float *k, const float *v, c
     A.out = out;
     A.out_stride = (long)n_head * hd;
     A.xq = (uint8_t *)xq_q8k;
-    return attn_dispatch<true>(A, hd, (max_seq + CH - 1) / CH, 1, (hipStream_t)s);
+    return attn_dispatch_kv<true>(A, kv_type, hd, (max_seq + CH - 1) / CH, 1, (hipStream_t)s);
 }

@@ -591,6 +591,33 @@ engine_ctx *engine_ctx_new(const engine_model *m, int32_t max_seq, int32_t n_bat
         n_threads = online < 1 ? 1 : online > THREADS_CAP ? THREADS_CAP : (int32_t)online;
     }
     c->n_threads = n_threads;
+    /* SARDYNE_KV: the KV cache's element type, f32 (the reference's; default) or f16 (each value
+       rounded to nearest even when written: half the cache's bytes and its reads) */
+    const char *kv = getenv("SARDYNE_KV");
+    if (!kv || !kv[0] || !strcmp(kv, "f32")) {
+        c->kv_type = SDY_KV_F32;
+    } else if (!strcmp(kv, "f16")) {
+        c->kv_type = SDY_KV_F16;
+    } else {
+        say(err, err_len, "SARDYNE_KV=%s not supported (f32, f16)", kv);
+        free(c);
+        return NULL;
+    }
+    /* SARDYNE_ATTENTION: the one-token attention. exact: the reference's softmax over every position
+       and its in-order weighted sum, bit for bit; chunked: split over spans of positions in two
+       launches, within tolerance; split: the same in one launch (f32 cache only) */
+    const char *attn = getenv("SARDYNE_ATTENTION");
+    if (!attn || !attn[0] || !strcmp(attn, "exact")) {
+        c->attn_mode = SDY_ATTN_EXACT;
+    } else if (!strcmp(attn, "chunked")) {
+        c->attn_mode = SDY_ATTN_CHUNKED;
+    } else if (!strcmp(attn, "split") && c->kv_type == SDY_KV_F32) {
+        c->attn_mode = SDY_ATTN_SPLIT;
+    } else {
+        say(err, err_len, "SARDYNE_ATTENTION=%s not supported (exact, chunked, split with an f32 cache)", attn);
+        free(c);
+        return NULL;
+    }
     const size_t logit_bytes = (c->logits_all ? (size_t)n_batch : 1) * (size_t)m->info.n_vocab * sizeof(float);
     if (sdy_stream_new(&c->st) || sdy_host_alloc((void **)&c->logits, logit_bytes) || sdy_engine_alloc(c)) {
         say(err, err_len, "memoria GPU esaurita o errore del dispositivo: %s", sdy_last_error());
@@ -606,13 +633,12 @@ engine_ctx *engine_ctx_new(const engine_model *m, int32_t max_seq, int32_t n_bat
     c->moe_device = c->decode_fused && !env_on("SARDYNE_NO_DEVICE_MOE") && sdy_engine_moe_device_ok(c);
     c->use_graph = c->decode_fused && (!m->info.n_expert || c->moe_device) && !env_on("SARDYNE_NO_GRAPH");
     c->fuse_act = c->decode_fused && !env_on("SARDYNE_NO_FUSED_ACT");
-    /* SARDYNE_ATTENTION=split: one-token attention in one launch split over positions (within
-       tolerance) instead of the bit-exact chain (the reference's softmax over all positions and its
-       in-order weighted sum), which is the default: measured in the decode step at 512-1152
-       positions, the chain is the faster of the two */
-    const char *attn = getenv("SARDYNE_ATTENTION");
-    c->split_attn = c->decode_fused && attn && !strcmp(attn, "split") &&
-                    sdy_attn_decode_split_ok(m->info.n_head, m->info.n_kv_head, m->info.head_dim);
+    /* the split forms take the fused one-token step and their head layouts; otherwise the exact chain */
+    const engine_model_info *in = &m->info;
+    if (!c->decode_fused || (c->attn_mode == SDY_ATTN_CHUNKED && !sdy_attn_chunked_ok(in->n_head, in->n_kv_head,
+                                                                                      in->head_dim)) ||
+        (c->attn_mode == SDY_ATTN_SPLIT && !sdy_attn_decode_split_ok(in->n_head, in->n_kv_head, in->head_dim)))
+        c->attn_mode = SDY_ATTN_EXACT;
     return c;
 }
 

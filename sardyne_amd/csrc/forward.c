@@ -45,8 +45,9 @@ int sdy_engine_alloc(engine_ctx *c) {
     size_t logit_rows = c->logits_all ? B : 1;
     /* rows of the FFN activations: n_batch tokens, or the k routed slots of one MoE token */
     size_t BR = in->n_expert && (size_t)in->n_expert_used > B ? (size_t)in->n_expert_used : B;
-    TRY(dalloc((void **)&c->k_cache, kv * 4));
-    TRY(dalloc((void **)&c->v_cache, kv * 4));
+    const size_t kv_bytes = kv * sdy_kv_elt_bytes(c->kv_type);
+    TRY(dalloc(&c->k_cache, kv_bytes));
+    TRY(dalloc(&c->v_cache, kv_bytes));
     TRY(dalloc((void **)&c->rope_cos, S * hd / 2 * 4));
     TRY(dalloc((void **)&c->rope_sin, S * hd / 2 * 4));
     TRY(dalloc((void **)&c->x, B * in->dim * 4));
@@ -67,7 +68,11 @@ int sdy_engine_alloc(engine_ctx *c) {
     TRY(dalloc((void **)&c->step_dev, 2 * 4));
     TRY(sdy_host_alloc((void **)&c->step_host, 2 * 4));
     TRY(dalloc(&c->gemm_ws, sdy_gemm_ws_bytes((int)B, (int)max_in)));
-    TRY(dalloc((void **)&c->attn_part, sdy_attn_decode_split_floats(in->n_head, in->head_dim, c->max_seq) * 4));
+    {
+        const size_t split = sdy_attn_decode_split_floats(in->n_head, in->head_dim, c->max_seq);
+        const size_t chunked = sdy_attn_chunked_floats(in->n_head, in->head_dim, c->max_seq);
+        TRY(dalloc((void **)&c->attn_part, (split > chunked ? split : chunked) * 4));
+    }
     TRY(dalloc((void **)&c->attn_count, (size_t)in->n_kv_head * 4));
     TRY(sdy_memset(c->attn_count, 0, (size_t)in->n_kv_head * 4, c->st));
     if (in->n_expert) {
@@ -96,8 +101,8 @@ int sdy_engine_alloc(engine_ctx *c) {
         free(tab);
         TRY(rc ? -1 : 0);
     }
-    TRY(sdy_memset(c->k_cache, 0, kv * 4, c->st));
-    TRY(sdy_memset(c->v_cache, 0, kv * 4, c->st));
+    TRY(sdy_memset(c->k_cache, 0, kv_bytes, c->st));
+    TRY(sdy_memset(c->v_cache, 0, kv_bytes, c->st));
     return sdy_sync(c->st);
 }
 
@@ -424,7 +429,8 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
     TRY(sdy_dequant_gather(&m->tok_embd.m, decode ? c->step_dev : c->tok_dev, n, c->x, c->st));
     for (int l = 0; l < in->n_layer; l++) {
         const dlayer *L = &m->layers[l];
-        float *kc = c->k_cache + l * layer_stride, *vc = c->v_cache + l * layer_stride;
+        const size_t kv_off = (size_t)l * layer_stride * sdy_kv_elt_bytes(c->kv_type);
+        void *kc = (char *)c->k_cache + kv_off, *vc = (char *)c->v_cache + kv_off;
         if (decode) {
             /* q | k | v of the token, contiguous in c->qkv */
             float *q = c->qkv, *k = q + q_dim, *v = k + kv_dim;
@@ -461,7 +467,12 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
             sdy_mv_args awo = fused_args(c, c->x, c->att, NULL, &L->wo, NULL, c->x, SDY_EPI_NONE);
             int wo_fused = c->fuse_act && sdy_matvec_fused_ok(&L->wo.m, &awo, NULL, NULL);
             int q8k = !wo_fused && vec_dot_type(L->wo.type) == SDY_Q8_K;
-            if (c->split_attn) {
+            if (c->attn_mode == SDY_ATTN_CHUNKED) {
+                TRY(sdy_attn_decode_chunked(q, k, v, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos, c->rope_sin,
+                                            c->step_dev, in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc, vc,
+                                            c->kv_type, head_stride, c->max_seq, c->attn_part, c->att,
+                                            q8k ? c->xq[1] : NULL, c->st));
+            } else if (c->attn_mode == SDY_ATTN_SPLIT) {
                 /* the split attention's merge writes wo's Q8_K row when wo does not quantise att
                    itself (measured: wo quantising in its prologue is faster than reading the row) */
                 q8k = !wo_fused && vec_dot_type(L->wo.type) == SDY_Q8_K && in->n_head / in->n_kv_head * hd % 256 == 0;
@@ -472,7 +483,8 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
             } else {
                 TRY(sdy_attn_decode(q, k, v, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos, c->rope_sin,
                                     c->step_dev, in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc, vc,
-                                    head_stride, c->max_seq, c->part, c->att, q8k ? c->xq[1] : NULL, c->st));
+                                    c->kv_type, head_stride, c->max_seq, c->part, c->att, q8k ? c->xq[1] : NULL,
+                                    c->st));
             }
             xq_forget(c);
             if (q8k) {
@@ -507,9 +519,9 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
             }
             TRY(sdy_qk_rope_kv_strided(q, k, v, qs, ks, vs, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos,
                                        c->rope_sin, pos0, n, in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc,
-                                       vc, head_stride, c->st));
-            TRY(sdy_attention(q, kc, vc, n, in->n_head, in->n_kv_head, hd, pos0 + 1, head_stride, qs, c->part, c->att,
-                              q_dim, c->st));
+                                       vc, c->kv_type, head_stride, c->st));
+            TRY(sdy_attention(q, kc, vc, c->kv_type, n, in->n_head, in->n_kv_head, hd, pos0 + 1, head_stride, qs,
+                              c->part, c->att, q_dim, c->st));
             TRY(mm(c, c->x, c->att, &L->wo, n, NULL, c->x, 1));
         }
         if (in->n_expert && decode && c->moe_device) {

@@ -285,8 +285,8 @@ void op_attention(float *out, const float *q, const float *k_cache, const float 
     float *dq = dup_to_dev(q, qn * 4), *dk = dup_to_dev(k_cache, kvn * 4), *dv = dup_to_dev(v_cache, kvn * 4);
     float *dout = dalloc(qn * 4);
     float *part = dalloc(sdy_attn_scores_floats(1, n_head, n_kv) * 4);
-    CK(sdy_attention(dq, dk, dv, 1, n_head, n_kv_head, head_dim, n_kv, (long)stride * head_dim, (long)qn, part, dout,
-                     (long)qn, stream()),
+    CK(sdy_attention(dq, dk, dv, SDY_KV_F32, 1, n_head, n_kv_head, head_dim, n_kv, (long)stride * head_dim, (long)qn,
+                     part, dout, (long)qn, stream()),
        "attention");
     to_host(out, dout, qn * 4);
     sdy_free(dq);

@@ -6,6 +6,8 @@
 #include "sardyne.h"
 #include "sdy_shim.h"
 
+enum { SDY_ATTN_EXACT = 0, SDY_ATTN_CHUNKED = 1, SDY_ATTN_SPLIT = 2 };
+
 typedef struct {
     sdy_mat m;  /* device layout; experts stacked as n_expert * n_out rows */
     int type, n_in, n_out;
@@ -41,7 +43,9 @@ struct engine_ctx {
     sdy_stream st;
     float *logits; /* host (pinned), [n_logits][n_vocab] */
     /* device state */
-    float *k_cache, *v_cache, *rope_cos, *rope_sin;
+    void *k_cache, *v_cache;    /* [n_layer][n_kv_head][max_seq][head_dim] of kv_type elements */
+    int kv_type;                /* SDY_KV_F32 (the reference's), or SDY_KV_F16 (SARDYNE_KV=f16) */
+    float *rope_cos, *rope_sin;
     float *x, *xb, *q, *k, *v, *att, *hb, *hb2, *logits_dev, *part;
     void *xq[2];                /* quantized activations: [0] Q8_0, [1] Q8_K */
     const float *xq_src[2];
@@ -63,9 +67,10 @@ struct engine_ctx {
     int fuse_act;               /* one-token matvecs quantise (and RMS-normalise) their f32 row in-kernel */
     int moe_device;             /* one-token MoE blocks route, run their experts and combine on the
                                    device (grouped matvec, no host round trip) */
-    int split_attn;             /* one-token attention in one launch, split over positions (within
-                                   tolerance; SARDYNE_ATTENTION=split); 0: the bit-exact chain */
-    float *attn_part;           /* split attention: per-chunk partials */
+    int attn_mode;              /* one-token attention: SDY_ATTN_EXACT (the reference's bits), or split
+                                   over positions within tolerance: SDY_ATTN_CHUNKED (two launches),
+                                   SDY_ATTN_SPLIT (one launch) */
+    float *attn_part;           /* chunked / split attention: per-span partials */
     unsigned *attn_count;       /* split attention: arrivals per kv head (zero between launches) */
     float *qkv;                 /* q | k | v of one token */
     void *gemm_ws;              /* scratch of the prefill GEMM (f16 activations of n_batch rows) */

@@ -11,21 +11,26 @@ extern "C" {
 #endif
 int sdy_rmsnorm(const float *x, const float *w, float *out, int n, float eps, int n_rows, long x_stride,
                 long out_stride, sdy_stream s);
+/* KV-cache element types (kv_type arguments): f32, or f16 with each value rounded to nearest even
+ * when written (the reference's f32 -> f16 rules). A layer's cache is [n_kv_head][max_seq][hd]
+ * elements; head_stride counts elements. */
+enum { SDY_KV_F32 = 0, SDY_KV_F16 = 1 };
+size_t sdy_kv_elt_bytes(int kv_type); /* 4, 2, or 0 for an unknown type */
 int sdy_qk_rope_kv(float *q, float *k, const float *v, const float *qn, const float *kn, float eps,
                    const float *rope_cos, const float *rope_sin, int pos0, int n_tok, int n_head, int n_kv_head, int hd,
-                   int interleaved, float *k_cache, float *v_cache, long head_stride, sdy_stream s);
+                   int interleaved, void *k_cache, void *v_cache, int kv_type, long head_stride, sdy_stream s);
 /* the same with token rows t * q_stride, t * k_stride, t * v_stride floats apart (q|k|v of one GEMM) */
 int sdy_qk_rope_kv_strided(float *q, float *k, const float *v, long q_stride, long k_stride, long v_stride,
                            const float *qn, const float *kn, float eps, const float *rope_cos, const float *rope_sin,
-                           int pos0, int n_tok, int n_head, int n_kv_head, int hd, int interleaved, float *k_cache,
-                           float *v_cache, long head_stride, sdy_stream s);
+                           int pos0, int n_tok, int n_head, int n_kv_head, int hd, int interleaved, void *k_cache,
+                           void *v_cache, int kv_type, long head_stride, sdy_stream s);
 /* Causal attention of n_tok tokens at positions n_kv0 - 1 + t (q rotated, K/V in the cache) in the
  * reference's arithmetic; scores: sdy_attn_scores_floats(n_tok, n_head, n_kv0 + n_tok - 1) floats of
  * device scratch. head_dim 32, 64, 128 or 256. */
 size_t sdy_attn_scores_floats(int n_tok, int n_head, int max_kv);
-int sdy_attention(const float *q, const float *k_cache, const float *v_cache, int n_tok, int n_head, int n_kv_head,
-                  int hd, int n_kv0, long head_stride, long q_stride, float *scores, float *out, long out_stride,
-                  sdy_stream s);
+int sdy_attention(const float *q, const void *k_cache, const void *v_cache, int kv_type, int n_tok, int n_head,
+                  int n_kv_head, int hd, int n_kv0, long head_stride, long q_stride, float *scores, float *out,
+                  long out_stride, sdy_stream s);
 int sdy_silu_mul(float *gate, const float *up, long n, sdy_stream s);
 int sdy_add(const float *a, const float *b, float *out, long n, sdy_stream s);
 int sdy_axpy(float *y, float a, const float *x, long n, sdy_stream s);
@@ -51,11 +56,23 @@ int sdy_norm_quant(const float *x, const float *w, float eps, int n, int n_rows,
 int sdy_attn_decode_ok(int n_head, int n_kv_head, int hd, int max_seq);
 int sdy_attn_decode(const float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
                     float eps, const float *rope_cos, const float *rope_sin, const int32_t *step_dev, int n_head,
-                    int n_kv_head, int hd, int interleaved, float *k_cache, float *v_cache, long head_stride,
-                    int max_seq, float *scores, float *out, void *xq_q8k, sdy_stream s);
+                    int n_kv_head, int hd, int interleaved, void *k_cache, void *v_cache, int kv_type,
+                    long head_stride, int max_seq, float *scores, float *out, void *xq_q8k, sdy_stream s);
+/* One-token decode attention in two launches, split over spans of positions (64, or more for
+ * caches beyond 8192 positions) with a deterministic merge in span order (within tolerance of the
+ * reference; sdy_attn_decode is the bit-exact form): the same inputs and outputs as
+ * sdy_attn_decode, with part (sdy_attn_chunked_floats floats) as scratch. xq_q8k needs
+ * n_head * hd % 256 == 0. head_dim 64, 128 or 256, at most 16 query heads per kv head. */
+int sdy_attn_chunked_ok(int n_head, int n_kv_head, int hd);
+size_t sdy_attn_chunked_floats(int n_head, int hd, int max_seq);
+int sdy_attn_decode_chunked(const float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
+                            float eps, const float *rope_cos, const float *rope_sin, const int32_t *step_dev,
+                            int n_head, int n_kv_head, int hd, int interleaved, void *k_cache, void *v_cache,
+                            int kv_type, long head_stride, int max_seq, float *part, float *out, void *xq_q8k,
+                            sdy_stream s);
 /* One-token decode attention in one launch, split over 32-position chunks with a deterministic
  * merge (within tolerance of the reference; sdy_attn_decode is the bit-exact form): the same
- * inputs and outputs as sdy_attn_decode, with part (sdy_attn_decode_split_floats floats) and count
+ * inputs and outputs as sdy_attn_decode (f32 cache only), with part (sdy_attn_decode_split_floats floats) and count
  * (n_kv_head unsigned, zero before the first call; each call leaves them zero) as scratch. xq_q8k
  * needs whole Q8_K blocks per kv group ((n_head / n_kv_head) * hd % 256 == 0). head_dim 64 or 128,
  * at most 16 query heads per kv head. */

@@ -104,13 +104,14 @@ def qwen25_3b_path():
 
 
 def _run_and_compare(path, n_ctx, n_batch, n_steps, max_seq, seed, tol):
-    """The engine (its exact attention chain) gives the reference's bits at every step; the split
-    attention (SARDYNE_ATTENTION=split) gives the prompt's bits (no decode step) and then logits
-    within tol of the logit scale, with the same greedy tokens."""
+    """The engine with the exact attention chain (SARDYNE_ATTENTION=exact) gives the reference's bits
+    at every step; the split attentions (chunked, split) give the prompt's bits (no decode step) and
+    then logits within tol of the logit scale, with the same greedy tokens."""
     toks = np.random.default_rng(seed).integers(0, 151936, n_ctx + n_steps).astype(np.int32)
     model = LoadedModel(path)
     runs = {}
-    for mode, env in (("exact", {}), ("split", {"SARDYNE_ATTENTION": "split"})):
+    for mode in ("exact", "chunked", "split"):
+        env = {"SARDYNE_ATTENTION": mode}
         with engine_env(**env):
             s = model.session(max_seq=max_seq, n_batch=n_batch)
         runs[mode] = [s.feed(toks[:n_ctx])] + [s.step(int(t)) for t in toks[n_ctx:]]
@@ -121,11 +122,13 @@ def _run_and_compare(path, n_ctx, n_batch, n_steps, max_seq, seed, tol):
     for i, (g, e) in enumerate(zip(runs["exact"], exp)):
         assert np.all(np.isfinite(g)), i
         assert np.array_equal(g.view(np.uint32), e.view(np.uint32)), (i, float(np.abs(g - e).max()))
-    split, exp = np.stack(runs["split"]), np.stack(exp)
-    assert np.array_equal(split[0].view(np.uint32), exp[0].view(np.uint32))
+    exp = np.stack(exp)
     scale = float(np.abs(exp).max())
-    assert float(np.abs(split - exp).max()) <= tol * scale, float(np.abs(split - exp).max()) / scale
-    assert np.array_equal(split.argmax(-1), exp.argmax(-1))
+    for mode in ("chunked", "split"):
+        split = np.stack(runs[mode])
+        assert np.array_equal(split[0].view(np.uint32), exp[0].view(np.uint32)), mode
+        assert float(np.abs(split - exp).max()) <= tol * scale, (mode, float(np.abs(split - exp).max()) / scale)
+        assert np.array_equal(split.argmax(-1), exp.argmax(-1)), mode
 
 
 @needs_ref

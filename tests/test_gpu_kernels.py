@@ -793,28 +793,36 @@ def test_moe_route_and_combine(n_expert, k):
 @pytest.mark.parametrize("n_head,n_kv_head,hd", [(16, 2, 128), (4, 2, 64), (32, 4, 128), (4, 4, 64), (6, 2, 64),
                                              (4, 2, 32), (2, 1, 256), (6, 3, 80)])
 @pytest.mark.parametrize("n_tok,n_kv0", [(16, 1), (40, 70), (77, 3)])
-def test_prefill_attention_tokens_bit_identical(n_head, n_kv_head, hd, n_tok, n_kv0):
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+def test_prefill_attention_tokens_bit_identical(n_head, n_kv_head, hd, n_tok, n_kv0, kv):
     """Causal attention of n_tok tokens in one call gives the bits of one call per token and those of
     the oracle's op_attention_head (the reference's AVX2 dot, libm expf, in-order axpy), and follows a
-    float64 softmax."""
+    float64 softmax. With an f16 cache, the oracle runs on the f32 values of the same f16 cache."""
     L = lib()
     rng = np.random.default_rng(n_head * 1000 + n_tok + hd)
     max_seq = 160
     q = rng.standard_normal((n_tok, n_head * hd)).astype(np.float32)
     kc = rng.standard_normal((n_kv_head, max_seq, hd)).astype(np.float32)
     vc = rng.standard_normal((n_kv_head, max_seq, hd)).astype(np.float32)
-    dq, dk, dv = capi.DeviceBuffer.from_array(q), capi.DeviceBuffer.from_array(kc), capi.DeviceBuffer.from_array(vc)
+    kv_type = capi.KV_F16 if kv == "f16" else capi.KV_F32
+    if kv == "f16":
+        kc16, vc16 = kc.astype(np.float16), vc.astype(np.float16)
+        dk, dv = capi.DeviceBuffer.from_array(kc16), capi.DeviceBuffer.from_array(vc16)
+        kc, vc = kc16.astype(np.float32), vc16.astype(np.float32)
+    else:
+        dk, dv = capi.DeviceBuffer.from_array(kc), capi.DeviceBuffer.from_array(vc)
+    dq = capi.DeviceBuffer.from_array(q)
     dpart = capi.DeviceBuffer(L.sdy_attn_scores_floats(n_tok, n_head, max_seq) * 4)
     dout = capi.DeviceBuffer(n_tok * n_head * hd * 4)
     q_dim = n_head * hd
-    capi.check(L.sdy_attention(dq.ptr, dk.ptr, dv.ptr, n_tok, n_head, n_kv_head, hd, n_kv0, max_seq * hd, q_dim,
-                               dpart.ptr, dout.ptr, q_dim, None))
+    capi.check(L.sdy_attention(dq.ptr, dk.ptr, dv.ptr, kv_type, n_tok, n_head, n_kv_head, hd, n_kv0, max_seq * hd,
+                               q_dim, dpart.ptr, dout.ptr, q_dim, None))
     got = dout.to_array(np.float32, (n_tok, q_dim))
     one = np.empty_like(got)
     d1 = capi.DeviceBuffer(q_dim * 4)
     for t in range(n_tok):
-        capi.check(L.sdy_attention(dq.ptr + 4 * t * q_dim, dk.ptr, dv.ptr, 1, n_head, n_kv_head, hd, n_kv0 + t,
-                                   max_seq * hd, q_dim, dpart.ptr, d1.ptr, q_dim, None))
+        capi.check(L.sdy_attention(dq.ptr + 4 * t * q_dim, dk.ptr, dv.ptr, kv_type, 1, n_head, n_kv_head, hd,
+                                   n_kv0 + t, max_seq * hd, q_dim, dpart.ptr, d1.ptr, q_dim, None))
         one[t] = d1.to_array(np.float32, q_dim)
     assert np.array_equal(bits(got), bits(one))
     exp_o = np.empty((n_tok, q_dim), np.float32)
@@ -836,12 +844,16 @@ def test_prefill_attention_tokens_bit_identical(n_head, n_kv_head, hd, n_tok, n_
 
 @pytest.mark.parametrize("n_head,n_kv_head,hd,qk_norm", [(16, 2, 128, False), (32, 4, 128, True), (6, 2, 64, False)])
 @pytest.mark.parametrize("pos", [0, 15, 16, 1000, 2047, 2048, 2110])
-def test_decode_attention_long_context(n_head, n_kv_head, hd, qk_norm, pos):
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+def test_decode_attention_long_context(n_head, n_kv_head, hd, qk_norm, pos, kv):
     """One-token decode attention through sdy_attn_decode (q/k RMSNorm, RoPE, the KV write, scores,
     softmax, weighted V and the output's Q8_K row) at positions up to the last slot of a 2111-position
     cache: past the 2048 positions whose softmax stays in registers, and over a cache whose size is not
     a multiple of 16 or 64. The output, the written cache rows and the Q8_K bytes have the bits of the
-    oracle's decode step (orc_model.c: norm, rope, cache write, orc_attention over pos + 1 positions)."""
+    oracle's decode step (orc_model.c: norm, rope, cache write, orc_attention over pos + 1 positions).
+    With an f16 cache: the new row is written as the f16 rounding of the oracle's (the reference's
+    f32 -> f16 rules, here numpy's, equal for these finite values) and the output has the oracle's
+    bits over the f32 values of the f16 cache."""
     L = lib()
     max_seq, eps, half = 2111, 1e-6, hd // 2
     assert L.sdy_attn_decode_ok(n_head, n_kv_head, hd, max_seq)
@@ -855,6 +867,8 @@ def test_decode_attention_long_context(n_head, n_kv_head, hd, qk_norm, pos):
     vc = rng.standard_normal((n_kv_head, max_seq, hd)).astype(np.float32)
     qn = (1 + 0.2 * rng.standard_normal(hd)).astype(np.float32)
     kn = (1 + 0.2 * rng.standard_normal(hd)).astype(np.float32)
+    ct = np.float16 if kv == "f16" else np.float32
+    kc, vc = kc.astype(ct), vc.astype(ct)
     dev = {n: capi.DeviceBuffer.from_array(a) for n, a in
            dict(q=q, k=k, v=v, kc=kc, vc=vc, cs=cs, sn=sn, qn=qn, kn=kn, step=np.array([0, pos], np.int32)).items()}
     dscores = capi.DeviceBuffer(L.sdy_attn_scores_floats(1, n_head, max_seq) * 4)
@@ -864,7 +878,8 @@ def test_decode_attention_long_context(n_head, n_kv_head, hd, qk_norm, pos):
     capi.check(L.sdy_attn_decode(dev["q"].ptr, dev["k"].ptr, dev["v"].ptr, dev["qn"].ptr if qk_norm else None,
                                  dev["kn"].ptr if qk_norm else None, eps, dev["cs"].ptr, dev["sn"].ptr,
                                  dev["step"].ptr, n_head, n_kv_head, hd, 0, dev["kc"].ptr, dev["vc"].ptr,
-                                 max_seq * hd, max_seq, dscores.ptr, dout.ptr, dxq.ptr if with_q8k else None, None))
+                                 capi.KV_F16 if kv == "f16" else capi.KV_F32, max_seq * hd, max_seq, dscores.ptr,
+                                 dout.ptr, dxq.ptr if with_q8k else None, None))
     got = dout.to_array(np.float32, n_head * hd)
     qe, ke = q.copy(), k.copy()
     if qk_norm:
@@ -876,12 +891,14 @@ def test_decode_attention_long_context(n_head, n_kv_head, hd, qk_norm, pos):
     O.lib().orc_rope(ptr(ke), n_kv_head, hd, ptr(cs) + 4 * pos * half, ptr(sn) + 4 * pos * half, 0)
     kc[:, pos] = ke.reshape(n_kv_head, hd)
     vc[:, pos] = v.reshape(n_kv_head, hd)
+    kc32, vc32 = np.ascontiguousarray(kc, np.float32), np.ascontiguousarray(vc, np.float32)
     exp = np.empty(n_head * hd, np.float32)
     scores = np.empty(max_seq, np.float32)
-    O.lib().orc_attention(ptr(exp), ptr(qe), ptr(kc), ptr(vc), n_head, n_kv_head, hd, pos + 1, max_seq, ptr(scores), 1)
+    O.lib().orc_attention(ptr(exp), ptr(qe), ptr(kc32), ptr(vc32), n_head, n_kv_head, hd, pos + 1, max_seq,
+                          ptr(scores), 1)
     assert np.array_equal(bits(got), bits(exp)), float(np.abs(got - exp).max())
-    assert np.array_equal(bits(dev["kc"].to_array(np.float32, kc.shape)), bits(kc))
-    assert np.array_equal(bits(dev["vc"].to_array(np.float32, vc.shape)), bits(vc))
+    assert dev["kc"].to_array(ct, kc.shape).tobytes() == kc.tobytes()
+    assert dev["vc"].to_array(ct, vc.shape).tobytes() == vc.tobytes()
     if with_q8k:
         assert dxq.to_array(np.uint8, n_head * hd // 256 * 292).tobytes() == O.quantize(exp, O.Q8_K).tobytes()
 
@@ -1077,7 +1094,7 @@ def test_qk_rope_kv_strided_equals_packed(interleaved, qk_norm, v_in_stack):
     v_ptr, v_stride = ((dstack.ptr + 4 * (qd + kvd), row) if v_in_stack else (dv_apart.ptr, kvd + 32))
     capi.check(L.sdy_qk_rope_kv_strided(dstack.ptr, dstack.ptr + 4 * qd, v_ptr, row, row, v_stride, qn_p, kn_p, 1e-6,
                                         dcs.ptr, dsn.ptr, pos0, n_tok, n_head, n_kv, hd, interleaved, kc1.ptr,
-                                        vc1.ptr, head_stride, None))
+                                        vc1.ptr, capi.KV_F32, head_stride, None))
     # packed: contiguous copies
     q = np.ascontiguousarray(stack[:, :qd])
     k = np.ascontiguousarray(stack[:, qd:qd + kvd])
@@ -1086,7 +1103,7 @@ def test_qk_rope_kv_strided_equals_packed(interleaved, qk_norm, v_in_stack):
     kc2 = capi.DeviceBuffer.from_array(np.zeros(n_kv * head_stride, np.float32))
     vc2 = capi.DeviceBuffer.from_array(np.zeros(n_kv * head_stride, np.float32))
     capi.check(L.sdy_qk_rope_kv(dq.ptr, dk.ptr, dv.ptr, qn_p, kn_p, 1e-6, dcs.ptr, dsn.ptr, pos0, n_tok, n_head, n_kv,
-                                hd, interleaved, kc2.ptr, vc2.ptr, head_stride, None))
+                                hd, interleaved, kc2.ptr, vc2.ptr, capi.KV_F32, head_stride, None))
     capi.check(L.sdy_sync(None))
     got = dstack.to_array(np.float32, stack.size).reshape(stack.shape)
     assert np.array_equal(bits(got[:, :qd]), bits(dq.to_array(np.float32, q.size).reshape(q.shape)))
@@ -1098,6 +1115,84 @@ def test_qk_rope_kv_strided_equals_packed(interleaved, qk_norm, v_in_stack):
     assert not np.array_equal(got[:, :qd], stack[:, :qd])
     kc = kc1.to_array(np.float32, n_kv * head_stride).reshape(n_kv, max_seq, hd)
     assert np.all(kc[:, :pos0] == 0) and np.all(kc[:, pos0 + n_tok:] == 0) and np.any(kc[:, pos0] != 0)
+
+
+def _decode_expected(q, k, v, kc, vc, qn, kn, cs, sn, p, n_head, n_kv_head, hd, qk_norm, interleaved, eps):
+    """The oracle's decode step (orc_model.c: q/k norm, RoPE, the cache write of position p, then
+    orc_attention over p + 1 positions) on copies of the caches kc / vc (f32 or f16: the new row is
+    rounded to the cache's type first). Returns (out, kc, vc) with the caches as written."""
+    half = hd // 2
+    qe, ke = q.copy(), k.copy()
+    if qk_norm:
+        for h in range(n_head):
+            O.lib().orc_rmsnorm(ptr(qe) + 4 * h * hd, ptr(qe) + 4 * h * hd, ptr(qn), hd, eps)
+        for h in range(n_kv_head):
+            O.lib().orc_rmsnorm(ptr(ke) + 4 * h * hd, ptr(ke) + 4 * h * hd, ptr(kn), hd, eps)
+    O.lib().orc_rope(ptr(qe), n_head, hd, ptr(cs) + 4 * p * half, ptr(sn) + 4 * p * half, interleaved)
+    O.lib().orc_rope(ptr(ke), n_kv_head, hd, ptr(cs) + 4 * p * half, ptr(sn) + 4 * p * half, interleaved)
+    kc, vc = kc.copy(), vc.copy()
+    kc[:, p] = ke.reshape(n_kv_head, hd)
+    vc[:, p] = v.reshape(n_kv_head, hd)
+    kc32, vc32 = np.ascontiguousarray(kc, np.float32), np.ascontiguousarray(vc, np.float32)
+    out = np.empty(n_head * hd, np.float32)
+    scores = np.empty(kc.shape[1], np.float32)
+    O.lib().orc_attention(ptr(out), ptr(qe), ptr(kc32), ptr(vc32), n_head, n_kv_head, hd, p + 1, kc.shape[1],
+                          ptr(scores), 1)
+    return out, kc, vc
+
+
+CHUNKED_LAYOUTS = [(16, 2, 128, False, 0), (32, 4, 128, True, 0), (6, 2, 64, False, 1), (4, 4, 64, True, 0),
+                   (32, 2, 128, False, 0), (8, 2, 256, True, 0)]
+CHUNKED_IDS = ["qwen25-3b", "qwen3-30b-a3b", "llama-gqa3", "mha", "gqa16", "hd256"]
+
+
+@pytest.mark.parametrize("n_head,n_kv_head,hd,qk_norm,interleaved", CHUNKED_LAYOUTS, ids=CHUNKED_IDS)
+@pytest.mark.parametrize("max_seq,pos", [(2111, p) for p in (0, 63, 64, 65, 640, 1151, 2110)] +
+                         [(9000, p) for p in (127, 128, 5000, 8999)])
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+def test_decode_attention_chunked(n_head, n_kv_head, hd, qk_norm, interleaved, max_seq, pos, kv):
+    """The two-launch chunked attention (64-position spans, or 128 for a 9000-position cache, partials
+    merged in span order) against the oracle's decode step on the same cache: output within 1e-5 of
+    the output scale, the new position's K/V rows bit-exact (f32), or the f16 rounding of the
+    oracle's (f16 cache, whose f32 values the oracle then attends over), the Q8_K bytes those of the
+    output it wrote. Two calls in a row (the second at pos - 1 over a fresh copy of the cache): the
+    partials of one call do not leak into the next."""
+    L = lib()
+    eps = 1e-6
+    assert L.sdy_attn_chunked_ok(n_head, n_kv_head, hd)
+    rng = np.random.default_rng(pos * 13 + n_head + hd)
+    cs, sn = np.empty(max_seq * hd // 2, np.float32), np.empty(max_seq * hd // 2, np.float32)
+    L.op_rope_table(ptr(cs), ptr(sn), max_seq, hd, 1e6)
+    ct = np.float16 if kv == "f16" else np.float32
+    kc0 = rng.standard_normal((n_kv_head, max_seq, hd)).astype(ct)
+    vc0 = rng.standard_normal((n_kv_head, max_seq, hd)).astype(ct)
+    qn = (1 + 0.2 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.2 * rng.standard_normal(hd)).astype(np.float32)
+    part = capi.DeviceBuffer(L.sdy_attn_chunked_floats(n_head, hd, max_seq) * 4)
+    with_q8k = n_head * hd % 256 == 0
+    for p in (pos, max(pos - 1, 0)):
+        q = rng.standard_normal(n_head * hd).astype(np.float32) * 3
+        k = rng.standard_normal(n_kv_head * hd).astype(np.float32) * 3
+        v = rng.standard_normal(n_kv_head * hd).astype(np.float32)
+        dev = {n: capi.DeviceBuffer.from_array(a) for n, a in
+               dict(q=q, k=k, v=v, kc=kc0, vc=vc0, cs=cs, sn=sn, qn=qn, kn=kn,
+                    step=np.array([0, p], np.int32)).items()}
+        dout = capi.DeviceBuffer(n_head * hd * 4)
+        dxq = capi.DeviceBuffer(n_head * hd // 256 * 292) if with_q8k else None
+        capi.check(L.sdy_attn_decode_chunked(dev["q"].ptr, dev["k"].ptr, dev["v"].ptr,
+                                             dev["qn"].ptr if qk_norm else None, dev["kn"].ptr if qk_norm else None,
+                                             eps, dev["cs"].ptr, dev["sn"].ptr, dev["step"].ptr, n_head, n_kv_head, hd,
+                                             interleaved, dev["kc"].ptr, dev["vc"].ptr,
+                                             capi.KV_F16 if kv == "f16" else capi.KV_F32, max_seq * hd, max_seq,
+                                             part.ptr, dout.ptr, dxq.ptr if with_q8k else None, None))
+        got = dout.to_array(np.float32, n_head * hd)
+        exp, kc, vc = _decode_expected(q, k, v, kc0, vc0, qn, kn, cs, sn, p, n_head, n_kv_head, hd, qk_norm,
+                                       interleaved, eps)
+        np.testing.assert_allclose(got, exp, rtol=0, atol=1e-5 * float(np.abs(exp).max()))
+        assert dev["kc"].to_array(ct, kc.shape).tobytes() == kc.tobytes()
+        assert dev["vc"].to_array(ct, vc.shape).tobytes() == vc.tobytes()
+        if with_q8k:
+            assert dxq.to_array(np.uint8, n_head * hd // 256 * 292).tobytes() == O.quantize(got, O.Q8_K).tobytes()
 
 
 @pytest.mark.parametrize("n_head,n_kv_head,hd,qk_norm,interleaved",
