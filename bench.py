@@ -318,7 +318,7 @@ def decode_weight_bytes(spec):
 
 def engine_modes():
     """The engine's one-token attention and KV-cache type, as engine_ctx_new reads them."""
-    return (os.environ.get("SARDYNE_ATTENTION") or "exact"), (os.environ.get("SARDYNE_KV") or "f32")
+    return (os.environ.get("SARDYNE_ATTENTION") or "chunked"), (os.environ.get("SARDYNE_KV") or "f32")
 
 
 def kv_bytes_per_position(spec):

@@ -5,8 +5,8 @@
 // s_j = q.k_j / sqrt(head_dim) over every cached position j, one softmax over all of them and the
 // weighted sum of the V rows. Here the positions are cut into spans of `span` (a multiple of 64):
 //
-//   k_attn_chunk<HD, KT>   grid (n_span_max, n_kv_head), 256 threads, one workgroup per (span, kv
-//                          head) for the group's n_rep query heads:
+//   k_attn_chunk<HD, HW, KT>  grid (n_span_max, n_kv_head * hsplit), 256 threads, one workgroup per
+//                          (span, kv head, share of the group's query heads):
 //     - q/k RMSNorm (qwen3) and RoPE of the group's queries, and of the new k when the span holds
 //       the token's own position (that workgroup writes the new K/V row to the cache);
 //     - the span's positions in sub-chunks of 64: K and V rows staged in LDS (the next sub-chunk's
@@ -43,6 +43,7 @@ struct ChunkArgs {
     const int32_t *step;             // step[1] = the token's position
     int n_head, n_kv_head, interleaved;
     int span, n_span_max;            // positions per workgroup (a multiple of SUB), spans per kv head
+    int hsplit;                      // workgroups sharing a kv group's heads (each takes n_rep / hsplit)
     void *k_cache, *v_cache;         // [n_kv_head][max_seq][HD] of KT
     long head_stride;                // max_seq * HD elements
     float scale;                     // 1 / sqrtf(HD)
@@ -81,7 +82,7 @@ SDY_DEV float wave_sum(float v) {
     return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 
-// HW: query heads per wave in the scores (n_rep <= 4 HW); wave w takes heads w, w + 4, ...
+// HW: query heads per wave in the scores (n_rep / hsplit <= 4 HW); wave w takes heads w, w + 4, ...
 template <int HD, int HW, class KT>
 __global__ __launch_bounds__(256) void k_attn_chunk(ChunkArgs a) {
     constexpr int KS = HD + 4;           // K rows in LDS: 16-byte aligned, consecutive rows on other banks
@@ -101,9 +102,11 @@ __global__ __launch_bounds__(256) void k_attn_chunk(ChunkArgs a) {
     float *es = vn + HD;               // [MAX_REP][SUB] exp(s - m) of the sub-chunk
     float *cs_l = es + MAX_REP * SUB;  // [MAX_REP] rescale of a head's old sums at this sub-chunk
 
-    const int sp = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int sp = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n_rep = a.n_head / a.n_kv_head;
+    const int n_rep = a.n_head / a.n_kv_head, g = blockIdx.y / a.hsplit, hs = blockIdx.y - g * a.hsplit;
+    const int nh = n_rep / a.hsplit;   // the workgroup's query heads: h0 .. h0 + nh - 1
+    const int h0 = g * n_rep + hs * nh;
     const int pos = a.step[1], n_kv = pos + 1;
     const int p_begin = sp * a.span;
     if (p_begin >= n_kv) return;  // beyond the token's position: no partial
@@ -130,13 +133,13 @@ __global__ __launch_bounds__(256) void k_attn_chunk(ChunkArgs a) {
     // by wave `wave`, lane l holding elements l + 64 e. Every input is loaded first (the K/V rows
     // above are in flight too), then the reference's per-head RMSNorm (qwen3) and rotation.
     {
-        const int n_vec = n_rep + (own ? 1 : 0);
+        const int n_vec = nh + (own ? 1 : 0);
         const float *cs = a.rope_cos + (size_t)pos * (HD / 2), *sn = a.rope_sin + (size_t)pos * (HD / 2);
         float x[RV][E], nq[E], nk[E], vnew[E], c[E], s[E];
 #pragma unroll
         for (int i = 0; i < RV; i++) {
             const int r = min(wave + 4 * i, n_vec - 1);
-            const float *src = r == n_rep ? a.k + (size_t)g * HD : a.q + (size_t)(g * n_rep + r) * HD;
+            const float *src = r == nh ? a.k + (size_t)g * HD : a.q + (size_t)(h0 + r) * HD;
 #pragma unroll
             for (int e = 0; e < E; e++) x[i][e] = src[lane + 64 * e];
         }
@@ -153,7 +156,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(ChunkArgs a) {
         for (int i = 0; i < RV; i++) {
             const int r = wave + 4 * i;
             if (r >= n_vec) break;
-            const bool is_k = r == n_rep;
+            const bool is_k = r == nh;
             float y[E];
 #pragma unroll
             for (int e = 0; e < E; e++) y[e] = x[i][e];
@@ -199,14 +202,16 @@ __global__ __launch_bounds__(256) void k_attn_chunk(ChunkArgs a) {
             float *buf = is_k ? kn : qs + r * HD;
 #pragma unroll
             for (int e = 0; e < E; e++) buf[lane + 64 * e] = o[e];
-            if (is_k) {  // the new K/V row of the cache
+            if (is_k) {  // the new K/V row (written to the cache by the group's first workgroup)
                 KT *kw = (KT *)a.k_cache + g * a.head_stride + (size_t)pos * HD;
                 KT *vw = (KT *)a.v_cache + g * a.head_stride + (size_t)pos * HD;
 #pragma unroll
                 for (int e = 0; e < E; e++) {
                     vn[lane + 64 * e] = vnew[e];
-                    KvElt<KT>::st(kw, lane + 64 * e, o[e]);
-                    KvElt<KT>::st(vw, lane + 64 * e, vnew[e]);
+                    if (hs == 0) {
+                        KvElt<KT>::st(kw, lane + 64 * e, o[e]);
+                        KvElt<KT>::st(vw, lane + 64 * e, vnew[e]);
+                    }
                 }
             }
         }
@@ -222,7 +227,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(ChunkArgs a) {
     const int slot = __builtin_amdgcn_readfirstlane(tid / HD), d = tid - slot * HD;
     int rc[NP];  // the weighted sum's heads, clamped to the group (extra ones are computed, not stored)
 #pragma unroll
-    for (int k = 0; k < NP; k++) rc[k] = min(slot + HPS * k, n_rep - 1);
+    for (int k = 0; k < NP; k++) rc[k] = min(slot + HPS * k, nh - 1);
     float acc[NP];
 #pragma unroll
     for (int k = 0; k < NP; k++) acc[k] = 0.0f;
@@ -283,7 +288,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(ChunkArgs a) {
 #pragma unroll
         for (int h = 0; h < HW; h++) {
             const int r = wave + 4 * h;
-            if (r >= n_rep) break;
+            if (r >= nh) break;
             const float m_new = fmaxf(m_run[h], wave_max(sc[h]));
             const float e = lane < np ? __expf(sc[h] - m_new) : 0.0f;
             const float cr = __expf(m_run[h] - m_new);  // 0 on the first sub-chunk (m_run = -inf)
@@ -321,14 +326,14 @@ __global__ __launch_bounds__(256) void k_attn_chunk(ChunkArgs a) {
 #pragma unroll
     for (int k = 0; k < NP; k++) {
         const int r = slot + HPS * k;
-        if (r < n_rep) a.part[((size_t)(g * n_rep + r) * a.n_span_max + sp) * (HD + 4) + 4 + d] = acc[k];
+        if (r < nh) a.part[((size_t)(h0 + r) * a.n_span_max + sp) * (HD + 4) + 4 + d] = acc[k];
     }
     if (lane == 0) {
 #pragma unroll
         for (int h = 0; h < HW; h++) {
             const int r = wave + 4 * h;
-            if (r < n_rep) {
-                float *pp = a.part + ((size_t)(g * n_rep + r) * a.n_span_max + sp) * (HD + 4);
+            if (r < nh) {
+                float *pp = a.part + ((size_t)(h0 + r) * a.n_span_max + sp) * (HD + 4);
                 pp[0] = m_run[h];
                 pp[1] = l_run[h];
             }
@@ -393,7 +398,8 @@ int launch_chunked(const ChunkArgs &A, hipStream_t st) {
     int rc = sdy_lds_limit((const void *)k_attn_chunk<HD, HW, KT>, lds, &granted);
     if (rc) return rc;
     SDY_NOTE_KERNEL((k_attn_chunk<HD, HW, KT>));
-    hipLaunchKernelGGL((k_attn_chunk<HD, HW, KT>), dim3(A.n_span_max, A.n_kv_head), dim3(256), lds, st, A);
+    hipLaunchKernelGGL((k_attn_chunk<HD, HW, KT>), dim3(A.n_span_max, A.n_kv_head * A.hsplit), dim3(256), lds, st,
+                       A);
     if ((rc = sdy_check_launch("attn_chunk"))) return rc;
     hipLaunchKernelGGL((k_attn_merge<HD>), dim3((A.n_head * HD + 255) / 256), dim3(256), 0, st, A);
     return sdy_check_launch("attn_merge");
@@ -406,10 +412,10 @@ int launch_chunked_kv(const ChunkArgs &A, int kv_type, hipStream_t st) {
 
 template <int HD>
 int launch_chunked_hw(const ChunkArgs &A, int kv_type, hipStream_t st) {
-    const int n_rep = A.n_head / A.n_kv_head;
-    return n_rep <= 4 ? launch_chunked_kv<HD, 1>(A, kv_type, st)
-           : n_rep <= 8 ? launch_chunked_kv<HD, 2>(A, kv_type, st)
-                        : launch_chunked_kv<HD, 4>(A, kv_type, st);
+    const int nh = A.n_head / A.n_kv_head / A.hsplit;
+    return nh <= 4 ? launch_chunked_kv<HD, 1>(A, kv_type, st)
+           : nh <= 8 ? launch_chunked_kv<HD, 2>(A, kv_type, st)
+                     : launch_chunked_kv<HD, 4>(A, kv_type, st);
 }
 
 // positions per span for a cache of max_seq positions: SUB, or a multiple of SUB that keeps the
@@ -457,6 +463,10 @@ extern "C" int sdy_attn_decode_chunked(const float *q, const float *k, const flo
     A.n_kv_head = n_kv_head;
     A.interleaved = interleaved;
     A.span = span_for(max_seq);
+    // two workgroups per (span, kv group), each with half the group's heads, when the group has four
+    // or more: twice the workgroups (the K/V rows are read by both), half the serial work in each
+    const int n_rep = n_head / n_kv_head;
+    A.hsplit = n_rep >= 4 && n_rep % 2 == 0 ? 2 : 1;
     A.n_span_max = (max_seq + A.span - 1) / A.span;
     A.k_cache = k_cache;
     A.v_cache = v_cache;

@@ -603,14 +603,15 @@ engine_ctx *engine_ctx_new(const engine_model *m, int32_t max_seq, int32_t n_bat
         free(c);
         return NULL;
     }
-    /* SARDYNE_ATTENTION: the one-token attention. exact: the reference's softmax over every position
-       and its in-order weighted sum, bit for bit; chunked: split over spans of positions in two
-       launches, within tolerance; split: the same in one launch (f32 cache only) */
+    /* SARDYNE_ATTENTION: the one-token attention. chunked (the default): split over spans of
+       positions in two launches, within tolerance of the reference (its f32 rounding only); exact: the
+       reference's softmax over every position and its in-order weighted sum, bit for bit; split: the
+       chunked form in one launch (f32 cache only) */
     const char *attn = getenv("SARDYNE_ATTENTION");
-    if (!attn || !attn[0] || !strcmp(attn, "exact")) {
-        c->attn_mode = SDY_ATTN_EXACT;
-    } else if (!strcmp(attn, "chunked")) {
+    if (!attn || !attn[0] || !strcmp(attn, "chunked")) {
         c->attn_mode = SDY_ATTN_CHUNKED;
+    } else if (!strcmp(attn, "exact")) {
+        c->attn_mode = SDY_ATTN_EXACT;
     } else if (!strcmp(attn, "split") && c->kv_type == SDY_KV_F32) {
         c->attn_mode = SDY_ATTN_SPLIT;
     } else {

@@ -184,15 +184,18 @@ def _decode_run(model, env):
 
 
 def test_decode_paths_bit_identical(model_path):
-    """One-token steps through the fused decode kernels, replayed from a recorded graph, give the
-    bits of the same steps run eagerly, with the MoE grouped on the host and through the unfused
-    kernels (and these follow the oracle); the split attention gives the same bits replayed and eager,
-    within tolerance of the exact chain."""
+    """One-token steps through the fused decode kernels with the exact attention, replayed from a
+    recorded graph, give the bits of the same steps run eagerly, with the MoE grouped on the host and
+    through the unfused kernels (and these follow the oracle); the chunked attention (the default)
+    and the split one give the same bits replayed and eager, within tolerance of the exact chain; the
+    f16 cache gives the same bits fused and unfused."""
     model = LoadedModel(model_path)
-    fused_graph = _decode_run(model, {})
-    fused_eager = _decode_run(model, {"SARDYNE_NO_GRAPH": "1"})
-    host_moe = _decode_run(model, {"SARDYNE_NO_DEVICE_MOE": "1"})
+    exact = {"SARDYNE_ATTENTION": "exact"}
+    fused_graph = _decode_run(model, exact)
+    fused_eager = _decode_run(model, {**exact, "SARDYNE_NO_GRAPH": "1"})
+    host_moe = _decode_run(model, {**exact, "SARDYNE_NO_DEVICE_MOE": "1"})
     unfused = _decode_run(model, {"SARDYNE_NO_FUSED_DECODE": "1"})
+    default = _decode_run(model, {})
     split_graph = _decode_run(model, {"SARDYNE_ATTENTION": "split"})
     split_eager = _decode_run(model, {"SARDYNE_ATTENTION": "split", "SARDYNE_NO_GRAPH": "1"})
     chunked_graph = _decode_run(model, {"SARDYNE_ATTENTION": "chunked"})
@@ -204,6 +207,7 @@ def test_decode_paths_bit_identical(model_path):
     assert np.array_equal(fused_graph.view(np.uint32), unfused.view(np.uint32))
     assert np.array_equal(split_graph.view(np.uint32), split_eager.view(np.uint32))
     assert np.array_equal(chunked_graph.view(np.uint32), chunked_eager.view(np.uint32))
+    assert np.array_equal(default.view(np.uint32), chunked_graph.view(np.uint32))  # the default attention
     assert np.array_equal(f16_graph.view(np.uint32), f16_unfused.view(np.uint32))
     assert_close(split_graph, fused_graph)
     assert_close(chunked_graph, fused_graph)
@@ -226,13 +230,14 @@ KQUANT_SPECS = ["qwen2-kquant", "llama-kquant", "qwen2-gqa8-hd128", "moe-128x8",
 def test_logits_bit_identical_to_reference(spec, tmp_path):
     """K-quant models (integer dots, the reference's f32 order for every float step: rmsnorm,
     RoPE, the AVX2 attention dot, libm expf in the softmaxes and SiLU, in-order axpys, the AVX2 router
-    matvec): prefill and one-token logits have the bits of the oracle's AVX2 forward (itself the
-    compiled reference's, tests/test_oracle.py)."""
+    matvec): with the exact attention, prefill and one-token logits have the bits of the oracle's AVX2
+    forward (itself the compiled reference's, tests/test_oracle.py)."""
     path = tmp_path / "m.gguf"
     write_model(path, dataclasses.replace(SPECS[spec], context=160), seed=7)
     toks = np.random.default_rng(8).integers(0, 300, 100).tolist()
     model = LoadedModel(path)
-    ctx = model.session(max_seq=128, n_batch=32)
+    with engine_env(SARDYNE_ATTENTION="exact"):
+        ctx = model.session(max_seq=128, n_batch=32)
     got = [ctx.feed(toks[:70])] + [ctx.feed([t]) for t in toks[70:100]]
     ref = O.OracleContext(path, 128, n_batch=32, simd=1)
     exp = [ref.eval(toks[:70])] + [ref.eval([t]) for t in toks[70:100]]

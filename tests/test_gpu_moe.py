@@ -22,10 +22,11 @@ from sardyne_amd.gguf_synth import write_model
 pytestmark = pytest.mark.gpu
 
 
-def run(path, n_batch=16, split=False):
-    """Prompt logits, then one-token steps' logits (stacked); split: the split one-launch attention."""
+def run(path, n_batch=16, mode="exact"):
+    """Prompt logits, then one-token steps' logits (stacked), with the one-token attention `mode`
+    (SARDYNE_ATTENTION: exact, chunked or split)."""
     model = LoadedModel(path)
-    with engine_env(**({"SARDYNE_ATTENTION": "split"} if split else {})):
+    with engine_env(SARDYNE_ATTENTION=mode):
         s = model.session(max_seq=48, n_batch=n_batch)
     return np.stack([s.feed(PROMPT)] + [s.step(t) for t in STEPS])
 
@@ -40,8 +41,9 @@ def test_unused_experts_poisoned_with_nan_change_nothing(tmp_path):
     clean, dirty = run(clean_p), run(dirty_p)
     assert np.all(np.isfinite(clean))
     assert np.array_equal(clean.view(np.uint32), dirty.view(np.uint32))
-    # the split attention reads only routed experts too
-    assert np.array_equal(run(clean_p, split=True).view(np.uint32), run(dirty_p, split=True).view(np.uint32))
+    # the split attentions read only routed experts too
+    for mode in ("chunked", "split"):
+        assert np.array_equal(run(clean_p, mode=mode).view(np.uint32), run(dirty_p, mode=mode).view(np.uint32))
     # a poisoned expert that is routed does reach the logits (the poisoning is effective). The Q8_K
     # activation quantiser of the next matvec takes its maximum over |x| with ordered comparisons, so
     # NaN rows quantise to zero blocks and the logits stay finite: the reference does exactly that,
