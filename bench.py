@@ -347,7 +347,8 @@ def bench_decode(args, spec, ctx_len, n_decode, label):
     try:
         t0 = time.perf_counter()
         model = LoadedModel(path)
-        log(f"[bench] GPU model load {time.perf_counter() - t0:.1f}s")
+        t_load = time.perf_counter() - t0
+        log(f"[bench] GPU model load {t_load:.2f}s")
         ctx = model.session(max_seq=ctx_len + n_decode + 1, n_batch=args.n_batch)
         t0 = time.perf_counter()
         ctx.feed(toks[:ctx_len])
@@ -391,16 +392,21 @@ def bench_decode(args, spec, ctx_len, n_decode, label):
                           "greedy_argmax_agreement": float(np.mean(g.argmax(-1) == c.argmax(-1)))}
         except Exception as ex:
             cpu = {"error": str(ex)}
+    size = path.stat().st_size
+    load = {"s": round(t_load, 3), "file_bytes": size, "gb_per_s": round(size / t_load / 1e9, 2),
+            "upload": "synchronous per tensor" if os.environ.get("SARDYNE_UPLOAD_SYNC", "0") not in ("", "0")
+            else "pipelined (4 x 64 MiB pinned slots)",
+            "file": "tmpfs" if str(path).startswith("/dev/shm") else "disk"}
     try:
         path.unlink()
     except OSError:
         pass
-    return gpu_tok_s, t_prefill, cpu, parity
+    return gpu_tok_s, t_prefill, cpu, parity, load
 
 
 def decode_line(args, spec, label, ctx_len, desc, n_dec=None):
     n_dec = n_dec or max(args.steps, 8)
-    tok_s, t_pre, cpu, parity = bench_decode(args, spec, ctx_len, n_dec, label)
+    tok_s, t_pre, cpu, parity, load = bench_decode(args, spec, ctx_len, n_dec, label)
     w_bytes = decode_weight_bytes(spec)
     kv_mean = kv_bytes_per_position(spec) * (ctx_len + n_dec / 2)
     gbps = (w_bytes + kv_mean) * tok_s / 1e9
@@ -420,7 +426,7 @@ def decode_line(args, spec, label, ctx_len, desc, n_dec=None):
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                          "kernel": "whole decode step (weights + mean KV bytes per token)"},
-            "cpu_baseline": cpu, "parity": parity}
+            "cpu_baseline": cpu, "parity": parity, "model_load": load}
     if cpu and "value" in cpu:
         line["gpu_over_cpu"] = round(tok_s / cpu["value"], 1)
     return line

@@ -151,6 +151,13 @@ _DEVICE_SIGNATURES = {
     "sdy_matvec_grouped": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp, _int, ctypes.c_long,
                                   ctypes.c_long, ctypes.c_long, _vp]),
     "sdy_mat_alloc": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long]),
+    "sdy_uploader_new": (_int, [ctypes.POINTER(_vp), _sz, _int, _int, _vp]),
+    "sdy_uploader_rows": (_int, [_vp, ctypes.POINTER(SdyMat), ctypes.c_long, ctypes.c_long, ctypes.c_long,
+                                 ctypes.c_long, ctypes.c_long, _vp]),
+    "sdy_uploader_finish": (_int, [_vp]),
+    "sdy_uploader_stats": (None, [_vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                                  ctypes.POINTER(ctypes.c_double)]),
+    "sdy_uploader_free": (_int, [_vp]),
     "sdy_mat_upload_map": (_int, [ctypes.POINTER(SdyMat), ctypes.c_long, ctypes.c_long, ctypes.c_long,
                                   ctypes.c_long, ctypes.c_long, _vp, _vp]),
     "sdy_rmsnorm": (_int, [_vp, _vp, _vp, _int, ctypes.c_float, _int, ctypes.c_long, ctypes.c_long, _vp]),

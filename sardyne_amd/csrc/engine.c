@@ -336,7 +336,14 @@ typedef struct {
     engine_model *m;
     char *err;
     size_t len;
+    sdy_uploader *up; /* pipelined uploads (NULL: one synchronous upload per tensor) */
 } loader;
+
+/* Rows of a tensor from the file mapping into an allocated matrix (the map of sdy_mat_upload_map). */
+static int load_rows(loader *ld, sdy_mat *m, long r0, long n, long step, long grp, long gstride, const void *data) {
+    return ld->up ? sdy_uploader_rows(ld->up, m, r0, n, step, grp, gstride, data)
+                  : sdy_mat_upload_map(m, r0, n, step, grp, gstride, data, ld->m->st);
+}
 
 static int device_fail(loader *ld, const char *what) {
     return say(ld->err, ld->len, "%s: %s", what, sdy_last_error());
@@ -360,7 +367,8 @@ static dmat row_view(const dmat *w, long r0, int n_out) {
 /* One matrix (or expert stack) as it is in the file. */
 static int upload_matrix(loader *ld, const gguf_tensor *t, dmat *out) {
     const long rows = (long)(t->nbytes / sdy_raw_row_bytes((int)t->type, (int)t->ne[0]));
-    if (sdy_mat_upload(&out->m, (int)t->type, (int)t->ne[0], rows, t->data, ld->m->st)) return device_fail(ld, t->name);
+    if (sdy_mat_alloc(&out->m, (int)t->type, (int)t->ne[0], rows)) return device_fail(ld, t->name);
+    if (load_rows(ld, &out->m, 0, rows, 1, rows, 0, t->data)) return device_fail(ld, t->name);
     describe(out, (int)t->type, (int)t->ne[0], (int)t->ne[1]);
     ld->m->device_bytes += out->m.bytes;
     return 0;
@@ -377,7 +385,6 @@ static int upload_qkv(loader *ld, const gguf_tensor *const *lt, dlayer *L) {
     }
     const int parts = tv->type == tq->type ? 3 : 2;
     const long rows = (long)qd + kvd + (parts == 3 ? kvd : 0);
-    sdy_stream st = ld->m->st;
     if (sdy_mat_alloc(&L->wqkv.m, (int)tq->type, n_in, rows)) return device_fail(ld, tq->name);
     describe(&L->wqkv, (int)tq->type, n_in, (int)rows);
     L->qkv_parts = parts;
@@ -386,7 +393,7 @@ static int upload_qkv(loader *ld, const gguf_tensor *const *lt, dlayer *L) {
     long r0 = 0;
     for (int p = 0; p < parts; p++) {
         const int n = (int)src[p]->ne[1];
-        if (sdy_mat_upload_rows(&L->wqkv.m, r0, 1, n, src[p]->data, st)) return device_fail(ld, src[p]->name);
+        if (load_rows(ld, &L->wqkv.m, r0, n, 1, n, 0, src[p]->data)) return device_fail(ld, src[p]->name);
         dmat *view = p == 0 ? &L->wq : p == 1 ? &L->wk : &L->wv;
         *view = row_view(&L->wqkv, r0, n);
         r0 += n;
@@ -407,9 +414,8 @@ static int upload_gate_up(loader *ld, const gguf_tensor *tg, const gguf_tensor *
     describe(&L->gate_up, (int)tg->type, n_in, 2 * ffn);
     L->gu_fused = 1;
     ld->m->device_bytes += L->gate_up.m.bytes;
-    sdy_stream st = ld->m->st;
-    if (sdy_mat_upload_map(&L->gate_up.m, 0, rows, 2, ffn, 2L * ffn, tg->data, st)) return device_fail(ld, tg->name);
-    if (sdy_mat_upload_map(&L->gate_up.m, 1, rows, 2, ffn, 2L * ffn, tu->data, st)) return device_fail(ld, tu->name);
+    if (load_rows(ld, &L->gate_up.m, 0, rows, 2, ffn, 2L * ffn, tg->data)) return device_fail(ld, tg->name);
+    if (load_rows(ld, &L->gate_up.m, 1, rows, 2, ffn, 2L * ffn, tu->data)) return device_fail(ld, tu->name);
     return 0;
 }
 
@@ -499,9 +505,17 @@ static int load(engine_model *m, const char *path, char *err, size_t len) {
         free(lt);
         return say(err, len, "memoria esaurita");
     }
-    loader ld = {m, err, len};
+    loader ld = {m, err, len, NULL};
     int rc = validate_tensors(m, lt, err, len);
     if (!rc && (sdy_init() || sdy_stream_new(&m->st))) rc = device_fail(&ld, "GPU");
+    /* weights go through a ring of four 64 MiB pinned/device slot pairs, the host copies split over
+       half the online CPUs; SARDYNE_UPLOAD_SYNC=1: one synchronous upload per tensor instead */
+    const char *sync_up = getenv("SARDYNE_UPLOAD_SYNC");
+    if (!rc && !(sync_up && sync_up[0] && strcmp(sync_up, "0"))) {
+        const long online = sysconf(_SC_NPROCESSORS_ONLN);
+        const int threads = online > 32 ? 16 : online > 2 ? (int)(online / 2) : 1;
+        if (sdy_uploader_new(&ld.up, (size_t)64 << 20, 4, threads, m->st)) rc = device_fail(&ld, "upload");
+    }
     /* the f32 vectors of every layer: norms, biases, q/k norms, each span padded to 64 floats */
     const size_t hd = (size_t)in->head_dim, qd = in->n_head * hd, kvd = in->n_kv_head * hd;
     const size_t per_layer = 2 * ((size_t)in->dim + 63) + (in->qkv_bias ? qd + 2 * kvd + 63 : 0) +
@@ -518,7 +532,22 @@ static int load(engine_model *m, const char *path, char *err, size_t len) {
         else if (!rc) rc = upload_matrix(&ld, tensor(m->gf, "output.weight"), &m->output);
     }
     for (int l = 0; !rc && l < in->n_layer; l++) rc = upload_layer(&ld, lt[l], &m->layers[l]);
+    if (!rc && ld.up && sdy_uploader_finish(ld.up)) rc = device_fail(&ld, "upload");
     if (!rc && sdy_sync(m->st)) rc = device_fail(&ld, "upload");
+    if (sdy_uploader_free(ld.up) && !rc) rc = device_fail(&ld, "upload");
+    if (!rc) {
+        /* views taken before the exactness checks ran: take them again (gemm_ok of the stack) */
+        for (int l = 0; l < in->n_layer; l++) {
+            dlayer *L = &m->layers[l];
+            if (L->qkv_parts >= 2) {
+                const int qd_l = L->wq.n_out, kvd_l = L->wk.n_out;
+                L->wq = row_view(&L->wqkv, 0, qd_l);
+                L->wk = row_view(&L->wqkv, qd_l, kvd_l);
+                if (L->qkv_parts == 3) L->wv = row_view(&L->wqkv, (long)qd_l + kvd_l, kvd_l);
+            }
+        }
+        if (in->tied_embeddings) m->output = m->tok_embd;
+    }
     free(lt);
     return rc;
 }

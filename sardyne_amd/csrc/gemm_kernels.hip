@@ -859,6 +859,17 @@ static GemmArgs gemm_args(const sdy_mat *m) {
 }
 
 // Flags (bad = 1) rows [r0, r0 + n) of m that the GEMM cannot multiply exactly. Synchronous.
+extern "C" int sdy_gemm_check_rows_async(const sdy_mat *m, long r0, long n, int *bad_dev, sdy_stream s) {
+    if (m->type != SDY_Q4_K && m->type != SDY_Q6_K) return 0;
+    sdy_mat v = sdy_mat_rows(m, r0, n);
+    GemmArgs g = gemm_args(&v);
+    const long total = n * (long)g.nb;
+    dim3 grid((unsigned)((total + 255) / 256));
+    if (m->type == SDY_Q4_K) hipLaunchKernelGGL(k_gemm_check<SDY_Q4_K>, grid, dim3(256), 0, (hipStream_t)s, g, bad_dev);
+    else hipLaunchKernelGGL(k_gemm_check<SDY_Q6_K>, grid, dim3(256), 0, (hipStream_t)s, g, bad_dev);
+    return sdy_check_launch("gemm_check");
+}
+
 extern "C" int sdy_gemm_check_rows(const sdy_mat *m, long r0, long n, int *bad_host, sdy_stream s) {
     *bad_host = 1;
     if (m->type != SDY_Q4_K && m->type != SDY_Q6_K) return 0;

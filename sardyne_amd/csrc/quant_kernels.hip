@@ -63,9 +63,15 @@ struct RowMap {
     long step, grp, gstride;
 };
 
+// The destination planes' row-0 addresses, passed by value.
+struct DstPlanes {
+    uint8_t *p[5];
+    SDY_DEV uint8_t *operator[](int i) const { return p[i]; }
+};
+
 template <int WT>
-__global__ void k_repack(const uint8_t *__restrict__ src, size_t src_row, Planes P, uint8_t *const *dst,
-                         long n_rows, RowMap map) {
+__global__ void k_repack(const uint8_t *__restrict__ src, size_t src_row, Planes P, DstPlanes dst, long n_rows,
+                         RowMap map) {
     long gid = blockIdx.x * (long)blockDim.x + threadIdx.x;
     long srow = gid / P.T;
     int u = (int)(gid - srow * P.T);
@@ -1640,8 +1646,9 @@ extern "C" int sdy_mat_alloc(sdy_mat *m, int type, int n_in, long n_rows) {
     return 0;
 }
 
-// Repacks n raw GGUF-layout rows (device memory) into rows r0 + map(i) of m (RowMap above).
-static int repack_rows(sdy_mat *m, long r0, RowMap map, long n, const void *dev_raw, sdy_stream s) {
+// Repacks n raw GGUF-layout rows (device memory) into rows r0 + map(i) of m (RowMap above),
+// queued on s (no allocation, no synchronisation).
+static int repack_rows_async(sdy_mat *m, long r0, RowMap map, long n, const void *dev_raw, sdy_stream s) {
     hipStream_t st = (hipStream_t)s;
     const int type = m->type;
     const size_t src_row = sdy_raw_row_bytes(type, m->n_in);
@@ -1652,31 +1659,45 @@ static int repack_rows(sdy_mat *m, long r0, RowMap map, long n, const void *dev_
     }
     size_t pb[5];
     plane_row_bytes(type, m->n_in, pb);
-    uint8_t *dst_h[5];
-    for (int i = 0; i < 5; i++) dst_h[i] = (uint8_t *)m->base + m->plane_off[i] + pb[i] * (size_t)r0;
-    uint8_t **dst_d = nullptr;
-    int rc;
-    if ((rc = sdy_malloc((void **)&dst_d, sizeof(dst_h)))) return rc;
-    if ((rc = sdy_h2d(dst_d, dst_h, sizeof(dst_h), s))) {
-        sdy_free(dst_d);
-        return rc;
-    }
+    DstPlanes dst;
+    for (int i = 0; i < 5; i++) dst.p[i] = (uint8_t *)m->base + m->plane_off[i] + pb[i] * (size_t)r0;
     Planes P = planes_of(m);
     long total = n * (long)m->n_units;
     dim3 grid((unsigned)((total + 255) / 256)), block(256);
     const uint8_t *src = (const uint8_t *)dev_raw;
     switch (type) {
-    case SDY_Q4_K: hipLaunchKernelGGL(k_repack<SDY_Q4_K>, grid, block, 0, st, src, src_row, P, dst_d, n, map); break;
-    case SDY_Q6_K: hipLaunchKernelGGL(k_repack<SDY_Q6_K>, grid, block, 0, st, src, src_row, P, dst_d, n, map); break;
-    case SDY_Q8_0: hipLaunchKernelGGL(k_repack<SDY_Q8_0>, grid, block, 0, st, src, src_row, P, dst_d, n, map); break;
-    case SDY_Q4_0: hipLaunchKernelGGL(k_repack<SDY_Q4_0>, grid, block, 0, st, src, src_row, P, dst_d, n, map); break;
-    case SDY_Q5_0: hipLaunchKernelGGL(k_repack<SDY_Q5_0>, grid, block, 0, st, src, src_row, P, dst_d, n, map); break;
+    case SDY_Q4_K: hipLaunchKernelGGL(k_repack<SDY_Q4_K>, grid, block, 0, st, src, src_row, P, dst, n, map); break;
+    case SDY_Q6_K: hipLaunchKernelGGL(k_repack<SDY_Q6_K>, grid, block, 0, st, src, src_row, P, dst, n, map); break;
+    case SDY_Q8_0: hipLaunchKernelGGL(k_repack<SDY_Q8_0>, grid, block, 0, st, src, src_row, P, dst, n, map); break;
+    case SDY_Q4_0: hipLaunchKernelGGL(k_repack<SDY_Q4_0>, grid, block, 0, st, src, src_row, P, dst, n, map); break;
+    case SDY_Q5_0: hipLaunchKernelGGL(k_repack<SDY_Q5_0>, grid, block, 0, st, src, src_row, P, dst, n, map); break;
     }
-    if ((rc = sdy_check_launch("repack")) || (rc = sdy_sync(s))) {
-        sdy_free(dst_d);
-        return rc;
-    }
-    return sdy_free(dst_d);
+    return sdy_check_launch("repack");
+}
+
+static int repack_rows(sdy_mat *m, long r0, RowMap map, long n, const void *dev_raw, sdy_stream s) {
+    int rc = repack_rows_async(m, r0, map, n, dev_raw, s);
+    return rc ? rc : sdy_sync(s);
+}
+
+// The last destination row and the end of the first group's span of an n-row map from r0 (or -1
+// with an error when they fall outside m).
+static int map_bounds(const sdy_mat *m, long r0, long n, long step, long grp, long gstride, long *span) {
+    if (n < 0 || r0 < 0 || step < 1 || grp < 1 || gstride < 0) return sdy_fail(-1, "upload: bad row map");
+    if (n == 0) return 0;
+    const long last = r0 + ((n - 1) / grp) * gstride + ((n - 1) % grp) * step;
+    *span = r0 + ((n - 1) / grp) * gstride + (grp - 1 < n - 1 ? grp - 1 : n - 1) * step;
+    if (last >= m->n_rows || *span >= m->n_rows)
+        return sdy_fail(-1, "upload of %ld rows from row %ld (step %ld) outside %ld rows", n, r0, step, m->n_rows);
+    return 0;
+}
+
+extern "C" int sdy_mat_repack_async(sdy_mat *m, long r0, long n, long step, long grp, long gstride,
+                                    const void *dev_raw, sdy_stream s) {
+    long span = 0;
+    const int rc = map_bounds(m, r0, n, step, grp, gstride, &span);
+    if (rc || n == 0) return rc;
+    return repack_rows_async(m, r0, RowMap{step, grp, gstride}, n, dev_raw, s);
 }
 
 extern "C" int sdy_mat_from_device(sdy_mat *m, int type, int n_in, long n_rows, const void *dev_raw, sdy_stream s) {
@@ -1696,15 +1717,11 @@ extern "C" int sdy_mat_from_device(sdy_mat *m, int type, int n_in, long n_rows, 
 
 extern "C" int sdy_mat_upload_map(sdy_mat *m, long r0, long n, long step, long grp, long gstride,
                                   const void *host_raw, sdy_stream s) {
-    if (n < 0 || r0 < 0 || step < 1 || grp < 1 || gstride < 0) return sdy_fail(-1, "upload: bad row map");
-    if (n == 0) return 0;
-    const long last = r0 + ((n - 1) / grp) * gstride + ((n - 1) % grp) * step;
-    const long span = r0 + ((n - 1) / grp) * gstride + (grp - 1 < n - 1 ? grp - 1 : n - 1) * step;
-    if (last >= m->n_rows || span >= m->n_rows)
-        return sdy_fail(-1, "upload of %ld rows from row %ld (step %ld) outside %ld rows", n, r0, step, m->n_rows);
+    long span = 0;
+    int rc = map_bounds(m, r0, n, step, grp, gstride, &span);
+    if (rc || n == 0) return rc;
     size_t raw = sdy_raw_row_bytes(m->type, m->n_in) * (size_t)n;
     void *tmp = nullptr;
-    int rc;
     if ((rc = sdy_malloc(&tmp, raw))) return rc;
     if (!(rc = sdy_h2d(tmp, host_raw, raw, s))) rc = repack_rows(m, r0, RowMap{step, grp, gstride}, n, tmp, s);
     if (!rc) rc = sdy_sync(s);

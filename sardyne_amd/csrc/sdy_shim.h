@@ -73,6 +73,26 @@ int sdy_mat_upload_map(sdy_mat *m, long r0, long n, long step, long grp, long gs
                        sdy_stream s);
 /* Same, from raw rows already in device memory. */
 int sdy_mat_from_device(sdy_mat *m, int type, int n_in, long n_rows, const void *dev_raw, sdy_stream s);
+/* The repack of sdy_mat_upload_map from raw rows in device memory, queued on s (no allocation, no
+ * synchronisation, no exactness check). */
+int sdy_mat_repack_async(sdy_mat *m, long r0, long n, long step, long grp, long gstride, const void *dev_raw,
+                         sdy_stream s);
+
+/* Pipelined uploads (upload.hip): a ring of pinned host slots and device slots. A host thread pool
+ * copies the next rows from the file mapping into a free pinned slot (advising the kernel to read
+ * the rows after them ahead), the DMA engine moves the slot to the device on a copy stream, and the
+ * repack runs on the work stream; the three overlap across slots. The GEMM exactness checks of the
+ * uploaded rows run at sdy_uploader_finish, which waits for everything and sets each matrix's
+ * gemm_ok. A matrix must stay at its address until then. */
+typedef struct sdy_uploader sdy_uploader;
+int sdy_uploader_new(sdy_uploader **u, size_t slot_bytes, int n_slots, int n_threads, sdy_stream work);
+/* Rows as sdy_mat_upload_map, from host memory (a GGUF mapping) */
+int sdy_uploader_rows(sdy_uploader *u, sdy_mat *m, long r0, long n, long step, long grp, long gstride,
+                      const void *host_raw);
+int sdy_uploader_finish(sdy_uploader *u); /* waits, runs the checks; the uploader stays usable */
+/* bytes uploaded so far, and seconds spent in the host copies and waiting for a free slot */
+void sdy_uploader_stats(const sdy_uploader *u, double *bytes, double *host_copy_s, double *slot_wait_s);
+int sdy_uploader_free(sdy_uploader *u); /* finishes, then releases the slots and the copy stream */
 int sdy_mat_free(sdy_mat *m);
 /* Sub-matrix view of rows [r0, r0+n) (e.g. one expert); no copy. */
 sdy_mat sdy_mat_rows(const sdy_mat *m, long r0, long n);
@@ -140,6 +160,8 @@ int sdy_norm_quant_gemm(const float *x, const float *w, float eps, int n, int n_
                         sdy_stream s);
 /* Exactness check of rows [r0, r0 + n) of m for the GEMM: *bad_host = 1 when some row fails. */
 int sdy_gemm_check_rows(const sdy_mat *m, long r0, long n, int *bad_host, sdy_stream s);
+/* The same, queued on s: sets *bad_dev (device int, zero beforehand) to nonzero when some row fails */
+int sdy_gemm_check_rows_async(const sdy_mat *m, long r0, long n, int *bad_dev, sdy_stream s);
 
 /* raw float-weight matrices (F32/F16/BF16, GGUF row-major layout kept as is) */
 int sdy_matvec_float(int wtype, const void *w, int n_in, const sdy_mv_args *a, sdy_stream s);

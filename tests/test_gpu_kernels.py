@@ -1253,3 +1253,53 @@ def test_decode_attention_split(n_head, n_kv_head, hd, qk_norm, interleaved, pos
         if with_q8k:
             assert dxq.to_array(np.uint8, n_head * hd // 256 * 292).tobytes() == O.quantize(got, O.Q8_K).tobytes()
         assert np.all(count.to_array(np.uint32, n_kv_head) == 0)
+
+
+def _mat_bytes(m):
+    L = lib()
+    out = np.empty(m.bytes, np.uint8)
+    capi.check(L.sdy_d2h(out.ctypes.data, m.base, m.bytes, None))
+    capi.check(L.sdy_sync(None))
+    return out
+
+
+@pytest.mark.parametrize("kind,n_in,grp,n_grp,bad_scale", [("Q4_K", 2048, 700, 2, False), ("Q6_K", 1024, 3000, 1, False),
+                                                           ("Q6_K", 1024, 900, 3, True), ("Q8_0", 2048, 1200, 1, False)])
+def test_pipelined_upload_equals_synchronous(kind, n_in, grp, n_grp, bad_scale):
+    """The pipelined uploader (1 MiB pinned/device slots, so a tensor spans several slots; the rows of
+    a per-group interleaved map, as the engine's per-expert gate|up, split at group boundaries) leaves
+    the same device bytes as the synchronous upload, and the deferred exactness check the same
+    gemm_ok (a Q6_K block with scale -128 fails it)."""
+    L = lib()
+    t = TYPES[kind]
+    rng = np.random.default_rng(grp + n_in)
+    n = grp * n_grp
+    w = [random_blocks(kind, n * n_in // O.QK[t], rng).reshape(n, -1) for _ in range(2)]
+    if bad_scale:
+        w[1][n - 1].reshape(-1, 210)[0, 192:208] = np.uint8(0x80)
+    rows = 2 * n
+    mats = [capi.SdyMat(), capi.SdyMat()]
+    for m in mats:
+        capi.check(L.sdy_mat_alloc(ctypes.byref(m), t, n_in, rows))
+    # synchronous: the two sources interleaved per group (step 2, group grp, group stride 2 grp)
+    for part in range(2):
+        capi.check(L.sdy_mat_upload_map(ctypes.byref(mats[0]), part, n, 2, grp, 2 * grp, w[part].ctypes.data, None))
+    up = ctypes.c_void_p()
+    capi.check(L.sdy_uploader_new(ctypes.byref(up), 1 << 20, 3, 4, None))
+    try:
+        for part in range(2):
+            capi.check(L.sdy_uploader_rows(up, ctypes.byref(mats[1]), part, n, 2, grp, 2 * grp, w[part].ctypes.data))
+        capi.check(L.sdy_uploader_finish(up))
+        b = ctypes.c_double()
+        L.sdy_uploader_stats(up, ctypes.byref(b), None, None)
+        assert b.value == 2 * w[0].nbytes
+    finally:
+        capi.check(L.sdy_uploader_free(up))
+    try:
+        assert _mat_bytes(mats[0]).tobytes() == _mat_bytes(mats[1]).tobytes()
+        assert mats[0].gemm_ok == mats[1].gemm_ok
+        if kind in ("Q4_K", "Q6_K"):
+            assert mats[1].gemm_ok == (0 if bad_scale else 1)
+    finally:
+        for m in mats:
+            L.sdy_mat_free(ctypes.byref(m))
