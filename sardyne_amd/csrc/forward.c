@@ -31,6 +31,14 @@ static int vec_dot_type(int wtype) {
 
 static int dalloc(void **p, size_t n) { return sdy_malloc(p, n ? n : 64); }
 
+/* an environment switch: set and not "0" */
+static int env_flag(const char *name) {
+    const char *v = getenv(name);
+    return v && v[0] && strcmp(v, "0") != 0;
+}
+
+static int moe_grouped_ok(const engine_ctx *c);
+
 /* Token count from which quantized matrices go through the MFMA GEMM instead of the matvec. */
 #define GEMM_MIN_TOKENS 16
 
@@ -43,8 +51,8 @@ int sdy_engine_alloc(engine_ctx *c) {
     size_t max_in = (size_t)in->dim > q_dim ? (size_t)in->dim : q_dim;
     if (ffn > max_in) max_in = ffn;
     size_t logit_rows = c->logits_all ? B : 1;
-    /* rows of the FFN activations: n_batch tokens, or the k routed slots of one MoE token */
-    size_t BR = in->n_expert && (size_t)in->n_expert_used > B ? (size_t)in->n_expert_used : B;
+    /* rows of the FFN activations: n_batch tokens, or for MoE the k routed slots of each of them */
+    size_t BR = in->n_expert ? B * (size_t)in->n_expert_used : B;
     const size_t kv_bytes = kv * sdy_kv_elt_bytes(c->kv_type);
     TRY(dalloc(&c->k_cache, kv_bytes));
     TRY(dalloc(&c->v_cache, kv_bytes));
@@ -67,7 +75,7 @@ int sdy_engine_alloc(engine_ctx *c) {
     TRY(dalloc((void **)&c->qkv, B * (q_dim + 2 * kv_dim) * 4));
     TRY(dalloc((void **)&c->step_dev, 2 * 4));
     TRY(sdy_host_alloc((void **)&c->step_host, 2 * 4));
-    TRY(dalloc(&c->gemm_ws, sdy_gemm_ws_bytes((int)B, (int)max_in)));
+    TRY(dalloc(&c->gemm_ws, sdy_gemm_ws_bytes((int)BR, (int)max_in)));
     {
         const size_t split = sdy_attn_decode_split_floats(in->n_head, in->head_dim, c->max_seq);
         const size_t chunked = sdy_attn_chunked_floats(in->n_head, in->head_dim, c->max_seq);
@@ -80,7 +88,11 @@ int sdy_engine_alloc(engine_ctx *c) {
         TRY(dalloc((void **)&c->moe_probs, B * in->n_expert * 4));
         TRY(dalloc((void **)&c->moe_w, chosen * 4));
         TRY(dalloc((void **)&c->moe_top, chosen * 4));
-        TRY(dalloc((void **)&c->moe_x, B * in->dim * 4));
+        TRY(dalloc((void **)&c->moe_x, BR * in->dim * 4));
+        TRY(dalloc((void **)&c->moe_grp_tok, ((size_t)in->n_expert + 1) * 4));
+        TRY(dalloc((void **)&c->moe_grp_tile, ((size_t)in->n_expert + 1) * 4));
+        TRY(dalloc((void **)&c->moe_src, BR * 4));
+        TRY(dalloc((void **)&c->moe_orow, BR * 4));
         TRY(dalloc((void **)&c->moe_y, BR * in->dim * 4));
         TRY(dalloc((void **)&c->moe_sum, B * in->dim * 4));
         TRY(dalloc((void **)&c->moe_gidx, chosen * 4));
@@ -101,6 +113,8 @@ int sdy_engine_alloc(engine_ctx *c) {
         free(tab);
         TRY(rc ? -1 : 0);
     }
+    /* SARDYNE_NO_GROUPED_MOE: many-token MoE blocks grouped on the host instead (same bits) */
+    c->moe_grouped_ok = moe_grouped_ok(c) && !env_flag("SARDYNE_NO_GROUPED_MOE");
     TRY(sdy_memset(c->k_cache, 0, kv_bytes, c->st));
     TRY(sdy_memset(c->v_cache, 0, kv_bytes, c->st));
     return sdy_sync(c->st);
@@ -112,7 +126,8 @@ void sdy_engine_release(engine_ctx *c) {
     void *dev[] = {c->k_cache, c->v_cache, c->rope_cos, c->rope_sin, c->x, c->xb, c->q, c->k, c->v, c->att, c->hb,
                    c->hb2, c->logits_dev, c->part, c->xq[0], c->xq[1], c->tok_dev, c->moe_probs, c->moe_w,
                    c->moe_top, c->moe_x, c->moe_y, c->moe_sum, c->moe_gidx, c->moe_gw, c->qkv, c->step_dev,
-                   c->gemm_ws, c->attn_part, c->attn_count};
+                   c->gemm_ws, c->attn_part, c->attn_count, c->moe_grp_tok, c->moe_grp_tile, c->moe_src,
+                   c->moe_orow};
     for (size_t i = 0; i < sizeof dev / sizeof *dev; i++) sdy_free(dev[i]);
     void *host[] = {c->tok_host, c->moe_top_host, c->moe_w_host, c->moe_gidx_host, c->moe_gw_host, c->step_host};
     for (size_t i = 0; i < sizeof host / sizeof *host; i++) sdy_host_free(host[i]);
@@ -327,6 +342,51 @@ static int moe(engine_ctx *c, const dlayer *L, int n) {
  * matvec, softmax + top-k, the k chosen experts' gate|up (SwiGLU) and down as grouped matvecs
  * indexed by the device-side top-k, then the weighted sum in ascending expert order plus the
  * residual. No host round trip, so the step can be recorded as a graph. */
+/* The MoE block of n tokens on the device, the residual included (x += the routed experts' sum):
+ * router, top-k, the routed pairs sorted by expert, their rows gathered and quantised once, then
+ * gate|up + SwiGLU and down as one grouped GEMM each over all routed experts, and the ascending-
+ * expert weighted sum (csrc/model_llama.c:724-751; the same bits as moe() below). */
+static int moe_grouped(engine_ctx *c, const dlayer *L, int n) {
+    const engine_model_info *in = &c->m->info;
+    const int dim = in->dim, fe = in->ffn_exp_dim, ne = in->n_expert, k = in->n_expert_used, R = n * k;
+    TRY(mm(c, c->moe_probs, c->xb, &L->gate_inp, n, NULL, NULL, 0));
+    TRY(sdy_moe_route(c->moe_probs, n, ne, k, c->moe_top, c->moe_w, c->st));
+    TRY(sdy_moe_sort(c->moe_top, n, k, ne, sdy_gemm_grouped_tile(), c->moe_grp_tok, c->moe_grp_tile, c->moe_src,
+                     c->moe_orow, c->st));
+    TRY(sdy_gather_rows(c->xb, c->moe_src, R, dim, c->moe_x, c->st));
+    xq_forget(c); /* xq[1] and the GEMM workspace now hold the routed rows */
+    c->gemm_ready = 0;
+    TRY(sdy_quantize_gemm(c->moe_x, c->xq[1], dim, R, c->gemm_ws, c->st));
+    sdy_mv_args a;
+    memset(&a, 0, sizeof a);
+    a.xq = c->xq[1];
+    a.n_tok = R;
+    a.out = c->hb;
+    a.out_stride = fe;
+    a.epilogue = SDY_EPI_SWIGLU;
+    a.ws_ready = 1;
+    TRY(sdy_gemm_grouped(&L->gate_up.m, 2L * fe, ne, c->moe_grp_tok, c->moe_grp_tile, NULL, &a, c->gemm_ws, c->st));
+    TRY(sdy_quantize_gemm(c->hb, c->xq[1], fe, R, c->gemm_ws, c->st));
+    a.out = c->moe_y;
+    a.out_stride = dim;
+    a.epilogue = SDY_EPI_NONE;
+    TRY(sdy_gemm_grouped(&L->down.m, dim, ne, c->moe_grp_tok, c->moe_grp_tile, c->moe_orow, &a, c->gemm_ws, c->st));
+    xq_forget(c);
+    return sdy_moe_combine(c->moe_y, c->moe_top, c->moe_w, n, k, dim, c->x, c->x, c->st);
+}
+
+/* Whether every MoE layer can take moe_grouped: gate|up stored fused and both expert stacks on the
+ * GEMM (K-quant, exactness check passed), an expert width that Q8_K blocks tile. */
+static int moe_grouped_ok(const engine_ctx *c) {
+    const engine_model_info *in = &c->m->info;
+    if (!in->n_expert || in->n_expert_used > 16 || in->n_expert > 512 || in->ffn_exp_dim % 256) return 0;
+    for (int l = 0; l < in->n_layer; l++) {
+        const dlayer *L = &c->m->layers[l];
+        if (!L->gu_fused || !sdy_gemm_ok(&L->gate_up.m, 2) || !sdy_gemm_ok(&L->down.m, 2)) return 0;
+    }
+    return 1;
+}
+
 static int moe_decode(engine_ctx *c, const dlayer *L) {
     const engine_model_info *in = &c->m->info;
     const int dim = in->dim, fe = in->ffn_exp_dim, ne = in->n_expert, k = in->n_expert_used;
@@ -526,6 +586,9 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
         }
         if (in->n_expert && decode && c->moe_device) {
             TRY(moe_decode(c, L));
+        } else if (in->n_expert && c->moe_grouped_ok && n * in->n_expert_used >= GEMM_MIN_TOKENS) {
+            TRY(norm_for(c, c->x, L->ffn_norm, &L->gate_inp, n));
+            TRY(moe_grouped(c, L, n));
         } else if (in->n_expert) {
             TRY(norm_for(c, c->x, L->ffn_norm, &L->gate_inp, n));
             TRY(moe(c, L, n));

@@ -45,6 +45,13 @@ struct GemmArgs {
     long out_stride;
     const float *bias, *resid;
     int swiglu;
+    // grouped launch (k_gemm3 only; grp_tile null: one matrix): group e (a routed expert) multiplies
+    // weight rows row0 + e * grp_rows + [0, n_rows) with activation rows grp_tok[e] .. grp_tok[e + 1]
+    // - 1; its token tiles are grp_tile[e] .. grp_tile[e + 1] - 1 of the grid. out_row (or null)
+    // sends activation row t's outputs to output row out_row[t].
+    const int *grp_tile, *grp_tok, *out_row;
+    long grp_rows;
+    int n_grp;
 };
 
 SDY_DEV u32x2 ld8(const uint8_t *p) { return *reinterpret_cast<const u32x2 *>(p); }
@@ -545,9 +552,24 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
         }
     }
     const long rt = rti * (32 * MT * WM) + 32 * MT * wave;
-    const int t0 = (int)tti * BN;
+    int t0 = (int)tti * BN, t_end = g.n_tok;
+    long row0 = g.row0;
+    if (g.grp_tile) {
+        // the group of this token tile: the last e with grp_tile[e] <= tti (empty groups share
+        // their successor's start, so the last one is the group that owns the tile)
+        if (tti >= g.grp_tile[g.n_grp]) return;  // past the routed tokens (uniform over the workgroup)
+        int lo = 0, hi = g.n_grp - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (g.grp_tile[mid] <= (int)tti) lo = mid;
+            else hi = mid - 1;
+        }
+        t0 = g.grp_tok[lo] + ((int)tti - g.grp_tile[lo]) * BN;
+        t_end = g.grp_tok[lo + 1];
+        row0 += (long)lo * g.grp_rows;
+    }
     const int nb = g.nb;
-    auto tok_of = [&](int t) { return t0 + t < g.n_tok ? t0 + t : g.n_tok - 1; };
+    auto tok_of = [&](int t) { return t0 + t < t_end ? t0 + t : t_end - 1; };
 
     // weight buffer resources and this lane's per-row offsets
     __amdgpu_buffer_rsrc_t rq[3], rh, rd;
@@ -559,7 +581,7 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         const long ri = rt + 32 * mt + lr;
-        const uint32_t row = (uint32_t)(g.row0 + (ri < g.n_rows ? ri : g.n_rows - 1));
+        const uint32_t row = (uint32_t)(row0 + (ri < g.n_rows ? ri : g.n_rows - 1));
         oq[mt] = row * (uint32_t)g.T * 16u + 8u * (uint32_t)h;
         oh[mt] = row * (uint32_t)nb * 16u;
         od[mt] = row * (uint32_t)nb * 2u;
@@ -756,20 +778,21 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const int tok = t0 + 32 * nt + lr;
-            if (tok >= g.n_tok) continue;
+            if (tok >= t_end) continue;
+            const size_t orow = g.out_row ? (size_t)g.out_row[tok] : (size_t)tok;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const long ri = rt + 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (ri >= g.n_rows) continue;
-                const long row = g.row0 + ri;
+                const long row = g.grp_tile ? ri : g.row0 + ri;
                 if (g.swiglu) {
                     if ((r & 1) == 0)
-                        g.out[(size_t)tok * g.out_stride + (ri >> 1)] = sdy_silu_mul1(acc[mt][nt][r], acc[mt][nt][r + 1]);
+                        g.out[orow * g.out_stride + (ri >> 1)] = sdy_silu_mul1(acc[mt][nt][r], acc[mt][nt][r + 1]);
                 } else {
                     float v = acc[mt][nt][r];
                     if (g.bias) v = v + g.bias[row];
-                    if (g.resid) v = g.resid[(size_t)tok * g.out_stride + row] + v;
-                    g.out[(size_t)tok * g.out_stride + row] = v;
+                    if (g.resid) v = g.resid[orow * g.out_stride + row] + v;
+                    g.out[orow * g.out_stride + row] = v;
                 }
             }
         }
@@ -938,6 +961,19 @@ static int launch_gemm3(GemmArgs &g, hipStream_t st) {
     return sdy_check_launch("gemm");
 }
 
+template <int WT, int MT, int NT, int WM>
+static int launch_gemm3_grid(GemmArgs &g, unsigned tok_tiles, unsigned row_tiles, hipStream_t st) {
+    constexpr int BN = 32 * NT, YDN = BN < 64 ? 64 : BN;
+    constexpr size_t lds = 2 * (size_t)(BN * 512 + YDN * 4 + BN * 32);
+    static size_t granted = 0;
+    const void *fn = (const void *)k_gemm3<WT, MT, NT, WM>;
+    int rc = sdy_lds_limit(fn, lds, &granted);
+    if (rc) return rc;
+    SDY_NOTE_KERNEL((k_gemm3<WT, MT, NT, WM>));
+    hipLaunchKernelGGL((k_gemm3<WT, MT, NT, WM>), dim3(tok_tiles, row_tiles), dim3(64 * WM), lds, st, g);
+    return sdy_check_launch("gemm");
+}
+
 template <int WT>
 static int gemm_type(GemmArgs &g, hipStream_t st) {
     // SARDYNE_GEMM_VARIANT picks one tile shape (tests and tuning); default: by shape
@@ -1007,4 +1043,53 @@ extern "C" int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_st
     g.swiglu = a->epilogue == SDY_EPI_SWIGLU;
     // with a row range the outputs are indexed by row - row0 only for SwiGLU (as in the matvec)
     return m->type == SDY_Q4_K ? gemm_type<SDY_Q4_K>(g, st) : gemm_type<SDY_Q6_K>(g, st);
+}
+
+extern "C" int sdy_gemm_grouped_tile(void) { return 32; }
+
+extern "C" int sdy_gemm_grouped(const sdy_mat *m, long grp_rows, int n_grp, const int *grp_tok, const int *grp_tile,
+                                const int *out_row, const sdy_mv_args *a, void *ws, sdy_stream s) {
+    hipStream_t st = (hipStream_t)s;
+    const int n_tok = a->n_tok;
+    if (n_tok <= 0) return 0;
+    if (!((m->type == SDY_Q4_K || m->type == SDY_Q6_K) && m->gemm_ok &&
+          (size_t)m->n_rows * m->n_units * 16 < 0xFFFFFFFFu))
+        return sdy_fail(-1, "gemm_grouped: matrix not eligible (type %d)", m->type);
+    if (n_grp < 1 || grp_rows < 1 || (long)n_grp * grp_rows > m->n_rows)
+        return sdy_fail(-1, "gemm_grouped: %d groups of %ld rows in %ld rows", n_grp, grp_rows, m->n_rows);
+    if (a->bias || a->resid || (a->epilogue == SDY_EPI_SWIGLU && (grp_rows & 1)))
+        return sdy_fail(-1, "gemm_grouped: no bias or residual; the SwiGLU epilogue needs an even row count per group");
+    GemmArgs g = gemm_args(m);
+    const SdyGemmExp e = sdy_gemm_exp(ws, n_tok, g.n_in);
+    g.y16 = e.y16;
+    g.yd = e.yd;
+    g.bs16 = e.bs16;
+    int rc;
+    if (!a->ws_ready) {
+        const long n_sb = (long)n_tok * g.nb;
+        SDY_NOTE_KERNEL(k_gemm_prep);
+        hipLaunchKernelGGL(k_gemm_prep, dim3((unsigned)((n_sb * 16 + 255) / 256)), dim3(256), 0, st,
+                           (const uint8_t *)a->xq, n_sb, (_Float16 *)g.y16, (float *)g.yd, (_Float16 *)g.bs16);
+        if ((rc = sdy_check_launch("gemm_prep"))) return rc;
+    }
+    g.row0 = 0;
+    g.n_rows = grp_rows;
+    g.n_tok = n_tok;
+    g.out = a->out;
+    g.out_stride = a->out_stride;
+    g.bias = a->bias;
+    g.resid = a->resid;
+    g.swiglu = a->epilogue == SDY_EPI_SWIGLU;
+    g.grp_tile = grp_tile;
+    g.grp_tok = grp_tok;
+    g.out_row = out_row;
+    g.grp_rows = grp_rows;
+    g.n_grp = n_grp;
+    // token tiles: at most one partial tile per group beyond the full ones (the grid's extra
+    // workgroups return at once)
+    constexpr int BN = 32;
+    const unsigned tok_tiles = (unsigned)((n_tok + BN - 1) / BN + n_grp - 1);
+    const unsigned row_tiles = (unsigned)((grp_rows + 127) / 128);
+    return m->type == SDY_Q4_K ? launch_gemm3_grid<SDY_Q4_K, 1, 1, 4>(g, tok_tiles, row_tiles, st)
+                               : launch_gemm3_grid<SDY_Q6_K, 1, 1, 4>(g, tok_tiles, row_tiles, st);
 }

@@ -341,6 +341,80 @@ extern "C" int sdy_moe_combine(const float *y, const int32_t *top, const float *
     return sdy_check_launch("moe_combine");
 }
 
+// The routed (token, slot) pairs grouped by expert for the grouped GEMM: a stable counting sort of
+// the n = n_tok * k expert ids in top (the reference groups a batch's tokens per expert the same
+// way, csrc/model_llama.c:676-700). Sorted row r holds pair out_row[r] = t * k + s, of token
+// src_tok[r] = t; rows grp_tok[e] .. grp_tok[e + 1] - 1 are expert e's, in (t, s) order;
+// grp_tile[e] is the number of bn-row tiles of the experts before e. One workgroup: SORT_SEG
+// threads count, then place, the pairs of their segment of the list; per (segment, expert) counts
+// in LDS make the placement stable.
+constexpr int SORT_SEG = 64;
+
+__global__ __launch_bounds__(256) void k_moe_sort(const int32_t *top, int n, int k, int ne, int bn, int *grp_tok,
+                                                  int *grp_tile, int32_t *src_tok, int32_t *out_row) {
+    extern __shared__ int sort_lds[];
+    int *cnt = sort_lds;              // [SORT_SEG][ne]: counts, then running offsets
+    int *base = cnt + SORT_SEG * ne;  // [ne + 1] first row of each expert
+    const int tid = threadIdx.x, seg_len = (n + SORT_SEG - 1) / SORT_SEG;
+    for (int i = tid; i < SORT_SEG * ne; i += 256) cnt[i] = 0;
+    __syncthreads();
+    auto expert_of = [&](int i) {
+        const int e = top[i];
+        return e < 0 ? 0 : e >= ne ? ne - 1 : e;
+    };
+    if (tid < SORT_SEG) {
+        const int b = tid * seg_len, end = b + seg_len < n ? b + seg_len : n;
+        for (int i = b; i < end; i++) cnt[tid * ne + expert_of(i)]++;
+    }
+    __syncthreads();
+    for (int e = tid; e < ne; e += 256) {  // offsets of each segment within its expert
+        int run = 0;
+        for (int sg = 0; sg < SORT_SEG; sg++) {
+            const int c = cnt[sg * ne + e];
+            cnt[sg * ne + e] = run;
+            run += c;
+        }
+        base[e] = run;  // the expert's total, for now
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int rows = 0, tiles = 0;
+        for (int e = 0; e < ne; e++) {
+            const int c = base[e];
+            base[e] = rows;
+            grp_tok[e] = rows;
+            grp_tile[e] = tiles;
+            rows += c;
+            tiles += (c + bn - 1) / bn;
+        }
+        base[ne] = rows;
+        grp_tok[ne] = rows;
+        grp_tile[ne] = tiles;
+    }
+    __syncthreads();
+    if (tid < SORT_SEG) {
+        const int b = tid * seg_len, end = b + seg_len < n ? b + seg_len : n;
+        for (int i = b; i < end; i++) {
+            const int e = expert_of(i), r = base[e] + cnt[tid * ne + e]++;
+            src_tok[r] = i / k;
+            out_row[r] = i;
+        }
+    }
+}
+
+extern "C" int sdy_moe_sort(const int32_t *top, int n_tok, int k, int n_expert, int bn, int *grp_tok, int *grp_tile,
+                            int32_t *src_tok, int32_t *out_row, sdy_stream s) {
+    if (n_expert < 1 || n_expert > 512 || k < 1 || n_tok < 1 || bn < 1)
+        return sdy_fail(-1, "moe_sort: %d tokens x %d of %d experts (at most 512), tiles of %d", n_tok, k, n_expert, bn);
+    const size_t lds = sizeof(int) * ((size_t)SORT_SEG * n_expert + n_expert + 1);
+    static size_t granted = 0;
+    int rc = sdy_lds_limit((const void *)k_moe_sort, lds, &granted);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(256), lds, (hipStream_t)s, top, n_tok * k, k, n_expert, bn, grp_tok,
+                       grp_tile, src_tok, out_row);
+    return sdy_check_launch("moe_sort");
+}
+
 extern "C" int sdy_gather_rows(const float *src, const int32_t *idx, int n, int dim, float *dst, sdy_stream s) {
     if (n <= 0) return 0;
     hipLaunchKernelGGL(k_gather_rows, dim3((dim + 255) / 256, n), dim3(256), 0, (hipStream_t)s, src, idx, dim, dst);

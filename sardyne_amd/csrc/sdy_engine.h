@@ -77,6 +77,10 @@ struct engine_ctx {
     /* MoE */
     float *moe_probs, *moe_w, *moe_x, *moe_y, *moe_sum, *moe_gw;
     int32_t *moe_top, *moe_gidx, *moe_top_host, *moe_gidx_host;
+    /* many-token MoE on the device: the routed pairs sorted by expert (sdy_moe_sort) */
+    int *moe_grp_tok, *moe_grp_tile;
+    int32_t *moe_src, *moe_orow;
+    int moe_grouped_ok;         /* every MoE layer's experts take the grouped GEMM */
     float *moe_w_host, *moe_gw_host;
     char err[256];
 };

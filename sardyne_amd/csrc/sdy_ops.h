@@ -42,6 +42,12 @@ int sdy_softmax(float *x, int n, int n_rows, long stride, sdy_stream s);
 void sdy_rope_table_host(float *cos_out, float *sin_out, int n_pos, int hd, float theta);
 int sdy_rope(float *x, int n_heads, int hd, const float *cs, const float *sn, int interleaved, sdy_stream s);
 int sdy_moe_route(float *probs, int n_tok, int n_expert, int k, int32_t *top, float *wts, sdy_stream s);
+/* The routed (token, slot) pairs of top ([n_tok][k] expert ids) grouped by expert, stably: sorted row
+ * r is pair out_row[r] = t * k + s of token src_tok[r]; expert e owns rows grp_tok[e] ..
+ * grp_tok[e + 1] - 1 and the bn-row tiles grp_tile[e] .. grp_tile[e + 1] - 1 (arrays of n_expert + 1). */
+int sdy_moe_sort(const int32_t *top, int n_tok, int k, int n_expert, int bn, int *grp_tok, int *grp_tile,
+                 int32_t *src_tok, int32_t *out_row, sdy_stream s);
+int sdy_gather_rows(const float *src, const int32_t *idx, int n, int dim, float *dst, sdy_stream s);
 int sdy_moe_combine(const float *y, const int32_t *top, const float *wts, int n_tok, int k, int dim, float *out,
                     const float *resid, sdy_stream s);
 /* RMSNorm of n_rows rows of n floats, then the activation quantiser vtype (SDY_Q8_K / SDY_Q8_0)

@@ -1303,3 +1303,61 @@ def test_pipelined_upload_equals_synchronous(kind, n_in, grp, n_grp, bad_scale):
     finally:
         for m in mats:
             L.sdy_mat_free(ctypes.byref(m))
+
+
+@pytest.mark.parametrize("kind,n_in,rows,n_exp,n_tok,k", [("Q4_K", 512, 96, 8, 45, 3), ("Q6_K", 768, 64, 16, 70, 4),
+                                                           ("Q4_K", 256, 128, 128, 33, 8)])
+def test_moe_sort_and_grouped_gemm_equal_per_expert_gemm(kind, n_in, rows, n_exp, n_tok, k):
+    """The expert sort (stable: each expert's pairs in (token, slot) order, tile counts per expert)
+    and the grouped GEMM over a stacked expert matrix: every routed (token, slot) row has the bits of
+    the per-expert GEMM of that token's row, through the SwiGLU epilogue (the gate|up form) and
+    through the output-row scatter (the down form). Some experts receive no token."""
+    L = lib()
+    t = TYPES[kind]
+    rng = np.random.default_rng(n_exp * 100 + n_tok)
+    w = random_blocks(kind, n_exp * rows * n_in // O.QK[t], rng).reshape(n_exp * rows, -1)
+    m = capi.DeviceMatrix(t, n_in, n_exp * rows, w)
+    assert L.sdy_gemm_ok(ctypes.byref(m.m), 2)
+    top = np.stack([rng.choice(n_exp // 2 + 1, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    x = rng.standard_normal((n_tok, n_in)).astype(np.float32)
+    bn = L.sdy_gemm_grouped_tile()
+    R = n_tok * k
+    D = capi.DeviceBuffer.from_array
+    dtop, dx = D(top), D(x)
+    grp_tok, grp_tile = capi.DeviceBuffer(4 * (n_exp + 1)), capi.DeviceBuffer(4 * (n_exp + 1))
+    src, orow = capi.DeviceBuffer(4 * R), capi.DeviceBuffer(4 * R)
+    capi.check(L.sdy_moe_sort(dtop.ptr, n_tok, k, n_exp, bn, grp_tok.ptr, grp_tile.ptr, src.ptr, orow.ptr, None))
+    gt = grp_tok.to_array(np.int32, n_exp + 1)
+    gl = grp_tile.to_array(np.int32, n_exp + 1)
+    s_src, s_orow = src.to_array(np.int32, R), orow.to_array(np.int32, R)
+    flat = top.reshape(-1)
+    exp_rows = [i for e in range(n_exp) for i in range(R) if flat[i] == e]
+    assert list(s_orow) == exp_rows and np.array_equal(s_src, s_orow // k)
+    cnt = np.bincount(flat, minlength=n_exp)
+    assert np.array_equal(gt, np.concatenate([[0], np.cumsum(cnt)]))
+    assert np.array_equal(gl, np.concatenate([[0], np.cumsum((cnt + bn - 1) // bn)]))
+    # routed rows, quantised with the GEMM expansion
+    xs = capi.DeviceBuffer(4 * R * n_in)
+    capi.check(L.sdy_gather_rows(dx.ptr, src.ptr, R, n_in, xs.ptr, None))
+    xq = capi.DeviceBuffer(R * O.row_size(O.Q8_K, n_in))
+    ws = capi.DeviceBuffer(L.sdy_gemm_ws_bytes(R, n_in))
+    capi.check(L.sdy_quantize_gemm(xs.ptr, xq.ptr, n_in, R, ws.ptr, None))
+    ref = O.matmul_q(w, t, O.quantize(x, O.Q8_K), n_in)  # [n_tok][n_exp * rows]: every expert's rows
+    # plain rows scattered back to (token, slot) order
+    out = capi.DeviceBuffer.from_array(np.full((R, rows), np.nan, np.float32))
+    a = capi.SdyMvArgs(xq=xq.ptr, n_tok=R, out=out.ptr, out_stride=rows, ws_ready=1)
+    capi.check(L.sdy_gemm_grouped(ctypes.byref(m.m), rows, n_exp, grp_tok.ptr, grp_tile.ptr, orow.ptr,
+                                  ctypes.byref(a), ws.ptr, None))
+    got = out.to_array(np.float32, (R, rows))
+    exp = np.stack([ref[i // k, flat[i] * rows:(flat[i] + 1) * rows] for i in range(R)])
+    assert np.array_equal(bits(got), bits(exp))
+    # SwiGLU pairs (rows 2i, 2i+1 of each expert), outputs in sorted order
+    sw = capi.DeviceBuffer.from_array(np.full((R, rows // 2), np.nan, np.float32))
+    a = capi.SdyMvArgs(xq=xq.ptr, n_tok=R, out=sw.ptr, out_stride=rows // 2, ws_ready=1, epilogue=capi.EPI_SWIGLU)
+    capi.check(L.sdy_gemm_grouped(ctypes.byref(m.m), rows, n_exp, grp_tok.ptr, grp_tile.ptr, None,
+                                  ctypes.byref(a), ws.ptr, None))
+    got = sw.to_array(np.float32, (R, rows // 2))
+    srt = exp[s_orow]
+    g, u = srt[:, 0::2].copy(), srt[:, 1::2].copy()
+    lib().op_silu_mul(ptr(g), ptr(u), g.size)
+    assert np.array_equal(bits(got), bits(g))
