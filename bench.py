@@ -20,6 +20,7 @@ Every line carries:
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import ctypes
 import json
 import os
@@ -451,7 +452,7 @@ def gemm_gate_up_ms(spec, n_tok, reps):
     capi.check(L.sdy_stream_new(ctypes.byref(stream)))
     st = stream.value
     rows, n_in = 2 * spec.ffn_dim, spec.dim
-    w = random_blocks("Q4_K", rows * n_in // 256, np.random.default_rng(3)).reshape(rows, -1)
+    w = random_blocks("Q4_K", rows * n_in // 256, np.random.default_rng(3), spec.scales).reshape(rows, -1)
     m = capi.DeviceMatrix(Q4_K, n_in, rows, w, st)
     if not L.sdy_gemm_ok(ctypes.byref(m.m), n_tok):
         return None
@@ -530,7 +531,8 @@ def prefill_line(args, spec, label, n_prompt, desc):
             "vs_baseline": None, "dtype": "int8 activations x Q4_K/Q6_K weights on f16 MFMA (exact integer sums)",
             "data": "synthetic (random-init Q4_K_M weights, uniform token ids)",
             "config": {"workload": f"{desc} prefill, one {n_prompt}-token prompt", "n_layer": spec.n_layer,
-                       "dim": spec.dim, "ffn": spec.ffn_dim, "vocab": spec.n_vocab, "flops": flops},
+                       "dim": spec.dim, "ffn": spec.ffn_dim, "vocab": spec.n_vocab, "flops": flops,
+                       "kquant_scales": spec.scales},
             "mfma_utilisation": round(flops / t / 1e12 / MFMA_PEAK, 4),
             "roofline": roof, "cpu_baseline": cpu, "parity": parity}
     if cpu and "value" in cpu:
@@ -549,6 +551,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--n-batch", type=int, default=512, help="GPU prefill chunk (decode workloads)")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (smoke runs only)")
+    ap.add_argument("--scales", default="workload", choices=["workload", "file"],
+                    help="K-quant scale distribution of the prefill model: the workload's, or the "
+                         "normalised scales of quantized model files (the GEMM's wide variant)")
     ap.add_argument("--no-decode", action="store_true",
                     help="default workload: leave out the decode_3b / decode_moe sub-objects")
     args = ap.parse_args()
@@ -588,7 +593,8 @@ def main():
                            "Qwen3-30B-A3B-shaped qwen3moe Q4_K_M (128 experts resident, top-8)")
     else:
         from sardyne_amd.gguf_synth import qwen25_3b
-        line = prefill_line(args, qwen25_3b(args.layers or 36), "qwen25_3b", 512, "Qwen2.5-3B-shaped Q4_K_M")
+        spec = dataclasses.replace(qwen25_3b(args.layers or 36), scales=args.scales)
+        line = prefill_line(args, spec, "qwen25_3b", 512, "Qwen2.5-3B-shaped Q4_K_M")
     print(json.dumps(line), flush=True)
 
 

@@ -8,15 +8,18 @@
 // sc * (q - 32) (Q6_K) — exact small integers — and multiplies them with the Q8_K activations as
 // f16 (exact int8 values) on v_mfma_f32_32x32x16_f16, accumulating one super-block at a time in
 // f32. The products are exact and every partial sum stays below 2^24 when
-// 127 * sum_k |w'_k| < 2^24 for each row and super-block (checked when the matrix is uploaded;
-// matrices that fail it take the matvec path), so the accumulator holds isum exactly. The Q4_K
-// min term is one more MFMA of the mins against the 16-element bsums. The f32 combine then follows
-// the reference's expression and super-block order, so each output has the reference's bits.
+// 127 * sum_k |w'_k| < 2^24 and |w'| <= 2048 for each row and super-block, so the accumulator
+// holds isum exactly. Matrices with a block beyond that (real Q6_K files store int8 scales down to
+// -128) take the wide variant, exact for every block the formats can hold: Q6_K splits each scale,
+// sc = 16 sh + sl with 0 <= sl < 16, into two fragments with two accumulators, isum = 16 ihi + ilo;
+// Q4_K centres its quants, isum = sum sc (q - 8) y + sum_j 8 sc_j bsum_j. Each part's partial sums
+// stay below 2^24 and the two are added in f32 with one rounding, that of (float)isum. The check
+// runs once per matrix at upload. The Q4_K min term is one more MFMA of the mins against
+// the 16-element bsums. The f32 combine then follows the reference's expression and super-block
+// order, so each output has the reference's bits.
 //
-// Tiling: a wave owns 32 rows x 32*NT tokens (NT MFMA tiles sharing its dequantised weight
-// fragments); a workgroup is 4 waves on 4 consecutive row tiles, so they read the same activation
-// fragments (L1 hits). The activations are expanded to f16 by k_gemm_prep, once per call unless the caller says
-// the workspace already holds them (ws_ready: q, k and v of one input).
+// The activations are expanded to f16 by k_gemm_prep, once per call unless the caller says the
+// workspace already holds them (ws_ready: q, k and v of one input).
 #include <stdlib.h>
 
 #include "sdy_device.h"
@@ -52,6 +55,7 @@ struct GemmArgs {
     const int *grp_tile, *grp_tok, *out_row;
     long grp_rows;
     int n_grp;
+    int wide;  // host-side: the wide variant is needed (k_gemm3 only)
 };
 
 SDY_DEV u32x2 ld8(const uint8_t *p) { return *reinterpret_cast<const u32x2 *>(p); }
@@ -106,137 +110,6 @@ SDY_DEV void load_unit(const GemmArgs &g, long row, int u, int h, u32x2 (&q)[3])
     }
 }
 
-template <int WT, int NT>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, lr = lane & 31;
-    const long rt = (long)blockIdx.x * 128 + 32 * wave;  // first row of the wave's tile
-    if (rt >= g.n_rows) return;
-    const int t0 = blockIdx.y * 32 * NT;
-    const long ra = g.row0 + (rt + lr < g.n_rows ? rt + lr : g.n_rows - 1);  // this lane's A row
-    int tb[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const int t = t0 + 32 * nt + lr;
-        tb[nt] = t < g.n_tok ? t : g.n_tok - 1;
-    }
-    float acc[NT][16];
-#pragma unroll
-    for (int nt = 0; nt < NT; nt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[nt][r] = 0.0f;
-    const half2v off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-    const half2v off6 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
-
-    for (int sb = 0; sb < g.nb; sb++) {
-        // this super-block's weights for the lane's A row, all requested up front
-        u32x2 q[4][3];
-#pragma unroll
-        for (int un = 0; un < 4; un++) load_unit<WT>(g, ra, 4 * sb + un, h, q[un]);
-        // scales of this lane's A row, and d (dmin) of that row (lanes 0..31 hold rows 0..31)
-        int sc[16];
-        int mn[8];
-        uint32_t dpair;
-        if constexpr (WT == SDY_Q4_K) {
-            const u32x4 hd = *reinterpret_cast<const u32x4 *>(g.p[2] + ((size_t)ra * g.nb + sb) * 16);
-            const uint32_t A = hd.y, B = hd.z, C = hd.w;
-            dpair = hd.x;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                sc[j] = (A >> (8 * j)) & 63;
-                mn[j] = (B >> (8 * j)) & 63;
-                sc[j + 4] = ((C >> (8 * j)) & 15) | (((A >> (8 * j + 6)) & 3) << 4);
-                mn[j + 4] = ((C >> (8 * j + 4)) & 15) | (((B >> (8 * j + 6)) & 3) << 4);
-            }
-        } else {
-            const u32x4 s4 = *reinterpret_cast<const u32x4 *>(g.p[3] + ((size_t)ra * g.nb + sb) * 16);
-#pragma unroll
-            for (int j = 0; j < 16; j++) sc[j] = (int)(int8_t)((s4[j >> 2] >> (8 * (j & 3))) & 255u);
-            dpair = *reinterpret_cast<const uint16_t *>(g.p[4] + ((size_t)ra * g.nb + sb) * 2);
-        }
-        float16v isum[NT];
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) isum[nt] = float16v{};
-#pragma unroll
-        for (int un = 0; un < 4; un++) {
-#pragma unroll
-            for (int s = 0; s < 4; s++) {
-                half8 a;
-                if constexpr (WT == SDY_Q4_K) {
-                    // s: 0 QA low, 1 QB low (sub-block 2un), 2 QA high, 3 QB high (sub-block 2un + 1)
-                    const u32x2 src = (s & 1) ? q[un][1] : q[un][0];
-                    const u32x2 nib = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
-                    const _Float16 f = (_Float16)(float)sc[2 * un + (s >> 1)];
-                    a = frag_scaled(nib, off, half2v{f, f});
-                } else {
-                    // s: 0 N0 low, 1 N1 low, 2 N0 high, 3 N1 high; high bits from HB >> 2s; group 4un + s
-                    const u32x2 src = (s & 1) ? q[un][1] : q[un][0];
-                    const u32x2 lo = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
-                    const u32x2 hi = ((q[un][2] >> (unsigned)(2 * s)) & 0x03030303u) << 4u;
-                    const _Float16 f = (_Float16)(float)sc[4 * un + s];
-                    a = frag_scaled(lo | hi, off6, half2v{f, f});
-                }
-                const int k = sb * 256 + 64 * un + 16 * s + 8 * h;
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++) {
-                    const half8 b = *reinterpret_cast<const half8 *>(g.y16 + (size_t)tb[nt] * g.n_in + k);
-                    isum[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, isum[nt], 0, 0, 0);
-                }
-            }
-        }
-        float16v msum[NT];
-        if constexpr (WT == SDY_Q4_K) {
-            half8 a2;
-#pragma unroll
-            for (int e = 0; e < 8; e++) a2[e] = (_Float16)(float)mn[4 * h + (e >> 1)];
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                const half8 b2 = *reinterpret_cast<const half8 *>(g.bs16 + ((size_t)tb[nt] * g.nb + sb) * 16 + 8 * h);
-                msum[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b2, float16v{}, 0, 0, 0);
-            }
-        }
-        // combine in the reference's order: acc + (yd*d*isum - yd*dmin*msum)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            // D row 8(r/4) + 4h + r%4 of the tile is the A row of lane 8(r/4) + 4h + r%4
-            const uint32_t dd = (uint32_t)__shfl((int)dpair, 8 * (r >> 2) + 4 * h + (r & 3));
-            const float d = sdy_h2f((uint16_t)(dd & 0xFFFFu));
-            const float dmin = WT == SDY_Q4_K ? sdy_h2f((uint16_t)(dd >> 16)) : 0.0f;
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                const float ydv = g.yd[(size_t)tb[nt] * g.nb + sb];
-                if constexpr (WT == SDY_Q4_K) {
-                    const float dall = ydv * d, dmn = ydv * dmin;
-                    const float t1 = dall * isum[nt][r], t2 = dmn * msum[nt][r];
-                    acc[nt][r] = acc[nt][r] + (t1 - t2);
-                } else {
-                    const float ydd = ydv * d;
-                    acc[nt][r] = acc[nt][r] + ydd * isum[nt][r];
-                }
-            }
-        }
-    }
-    // store (bias, residual, or the SwiGLU pair of rows 2i, 2i+1 held by this lane)
-#pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const int tok = t0 + 32 * nt + lr;
-        if (tok >= g.n_tok) continue;
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const long ri = rt + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (ri >= g.n_rows) continue;
-            const long row = g.row0 + ri;
-            if (g.swiglu) {
-                if ((r & 1) == 0) g.out[(size_t)tok * g.out_stride + (ri >> 1)] = sdy_silu_mul1(acc[nt][r], acc[nt][r + 1]);
-            } else {
-                float v = acc[nt][r];
-                if (g.bias) v = v + g.bias[row];
-                if (g.resid) v = g.resid[(size_t)tok * g.out_stride + row] + v;
-                g.out[(size_t)tok * g.out_stride + row] = v;
-            }
-        }
-    }
-}
-
 // The weights of one super-block for one lane: its A row's quants for k-half h of the 4 units, the
 // scale record (Q4_K: d, dmin and the 12 packed scale/min bytes; Q6_K: the 16 int8 scales) and
 // the Q6_K d.
@@ -257,232 +130,6 @@ SDY_DEV void load_sb(const GemmArgs &g, long row, int sb, int h, SbRegs &r) {
         r.hd = *reinterpret_cast<const u32x4 *>(g.p[3] + ((size_t)row * g.nb + sb) * 16);
         r.d6 = *reinterpret_cast<const uint16_t *>(g.p[4] + ((size_t)row * g.nb + sb) * 2);
     }
-}
-
-// LDS-staged GEMM. A workgroup of WM waves covers 32*MT*WM rows x 32*NT tokens; every wave owns
-// 32*MT rows (MT MFMA row tiles, dequantised in its registers from its own global loads) and all
-// the workgroup's tokens. The f16 activations of a super-block (32*NT tokens x 256 values) are
-// staged once per workgroup in LDS (rows padded to 528 bytes: the 16-byte fragment reads of 8
-// consecutive lanes fall in distinct banks), double-buffered: the loads of super-block s + 1
-// (activations into registers, then LDS; weights into registers) are in flight while s is
-// multiplied. One barrier per super-block. Integer sums and the f32 combine as in k_gemm.
-template <int WT, int MT, int NT, int WM>
-__global__ __launch_bounds__(64 * WM) void k_gemm2(GemmArgs g) {
-    constexpr int BN = 32 * NT, NTH = 64 * WM, ROWB = 528;
-    constexpr int BUF = BN * ROWB + BN * 4 + BN * 32;  // f16 rows, yd, 16 f16 bsums per token
-    constexpr int NCH = BN * 32 / NTH;                  // 16-byte activation chunks per thread
-    static_assert(BN <= NTH && (BN * 32) % NTH == 0, "tile");
-    extern __shared__ __align__(16) uint8_t lds[];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, lr = lane & 31;
-    // Workgroups are dealt round-robin to the 8 XCDs in launch order. Renumber them so that the
-    // token tiles of a row tile run on one XCD at about the same time: its weights then come from
-    // HBM once into that XCD's L2 instead of once per token tile.
-    const int n_tt = gridDim.x;
-    const long n_rt = gridDim.y, L = (long)blockIdx.y * n_tt + blockIdx.x;
-    long rti, tti;
-    {
-        const long grp = 8L * n_tt;                     // 8 row tiles x all token tiles
-        const long full = n_rt / 8 * grp;               // workgroups in complete groups
-        if (L < full) {
-            const long gq = L / grp, w = L - gq * grp;  // w % 8: the XCD
-            rti = gq * 8 + (w & 7);
-            tti = w >> 3;
-        } else {                                        // the last, partial group: row-major
-            const long w = L - full;
-            rti = n_rt / 8 * 8 + w / n_tt;
-            tti = w - (w / n_tt) * n_tt;
-        }
-    }
-    const long rt = rti * (32 * MT * WM) + 32 * MT * wave;  // first row of the wave
-    const int t0 = (int)tti * BN;
-    long ra[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        const long ri = rt + 32 * mt + lr;
-        ra[mt] = g.row0 + (ri < g.n_rows ? ri : g.n_rows - 1);
-    }
-    const int nb = g.nb;
-    auto tok_of = [&](int t) { return t0 + t < g.n_tok ? t0 + t : g.n_tok - 1; };
-    u32x4 bv[NCH];
-    float ydv = 0.0f;
-    u32x4 bs0 = {0u, 0u, 0u, 0u}, bs1 = {0u, 0u, 0u, 0u};
-    auto load_b = [&](int sb) {
-#pragma unroll
-        for (int j = 0; j < NCH; j++) {
-            const int q = tid + j * NTH;
-            bv[j] = *reinterpret_cast<const u32x4 *>(g.y16 + (size_t)tok_of(q >> 5) * g.n_in + 256 * sb + 8 * (q & 31));
-        }
-        if (tid < BN) {
-            const size_t tb = (size_t)tok_of(tid) * nb + sb;
-            ydv = g.yd[tb];
-            if constexpr (WT == SDY_Q4_K) {
-                bs0 = *reinterpret_cast<const u32x4 *>(g.bs16 + tb * 16);
-                bs1 = *reinterpret_cast<const u32x4 *>(g.bs16 + tb * 16 + 8);
-            }
-        }
-    };
-    auto store_b = [&](int buf) {
-        uint8_t *base = lds + buf * BUF;
-#pragma unroll
-        for (int j = 0; j < NCH; j++) {
-            const int q = tid + j * NTH;
-            *reinterpret_cast<u32x4 *>(base + (q >> 5) * ROWB + 16 * (q & 31)) = bv[j];
-        }
-        if (tid < BN) {
-            *reinterpret_cast<float *>(base + BN * ROWB + 4 * tid) = ydv;
-            if constexpr (WT == SDY_Q4_K) {
-                *reinterpret_cast<u32x4 *>(base + BN * ROWB + BN * 4 + 32 * tid) = bs0;
-                *reinterpret_cast<u32x4 *>(base + BN * ROWB + BN * 4 + 32 * tid + 16) = bs1;
-            }
-        }
-    };
-
-    float16v acc[MT][NT];
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) acc[mt][nt] = float16v{};
-    const half2v off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-    const half2v off6 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
-
-    // weights two super-blocks ahead (A: current, An: next, Ann: requested in this iteration);
-    // activations one ahead (registers, then the other LDS buffer)
-    SbRegs A[MT], An[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        load_sb<WT>(g, ra[mt], 0, h, A[mt]);
-        load_sb<WT>(g, ra[mt], nb > 1 ? 1 : 0, h, An[mt]);
-    }
-    load_b(0);
-    store_b(0);
-    __syncthreads();
-
-    for (int sb = 0; sb < nb; sb++) {
-        const int cur = sb & 1;
-        const int nx = sb + 1 < nb ? sb + 1 : sb;   // the last iterations reload their own super-block
-        const int nx2 = sb + 2 < nb ? sb + 2 : nb - 1;
-        SbRegs Ann[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) load_sb<WT>(g, ra[mt], nx2, h, Ann[mt]);
-        load_b(nx);
-
-        const uint8_t *bbuf = lds + cur * BUF;
-        float16v isum[MT][NT];
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) isum[mt][nt] = float16v{};
-#pragma unroll
-        for (int un = 0; un < 4; un++) {
-#pragma unroll
-            for (int s = 0; s < 4; s++) {
-                half8 a[MT];
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++) {
-                    if constexpr (WT == SDY_Q4_K) {
-                        // s: 0 QA low, 1 QB low (sub-block 2un), 2 QA high, 3 QB high (sub-block 2un + 1)
-                        const uint32_t Aw = A[mt].hd.y, Cw = A[mt].hd.w;
-                        const int j = 2 * un + (s >> 1);
-                        const int sc = j < 4 ? (int)((Aw >> (8 * j)) & 63)
-                                             : (int)(((Cw >> (8 * (j - 4))) & 15) | (((Aw >> (8 * (j - 4) + 6)) & 3) << 4));
-                        const u32x2 src = (s & 1) ? A[mt].q[un][1] : A[mt].q[un][0];
-                        const u32x2 nib = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
-                        const _Float16 f = (_Float16)(float)sc;
-                        a[mt] = frag_scaled(nib, off, half2v{f, f});
-                    } else {
-                        const int j = 4 * un + s;
-                        const int sc = (int)(int8_t)((A[mt].hd[j >> 2] >> (8 * (j & 3))) & 255u);
-                        const u32x2 src = (s & 1) ? A[mt].q[un][1] : A[mt].q[un][0];
-                        const u32x2 lo = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
-                        const u32x2 hi = ((A[mt].q[un][2] >> (unsigned)(2 * s)) & 0x03030303u) << 4u;
-                        const _Float16 f = (_Float16)(float)sc;
-                        a[mt] = frag_scaled(lo | hi, off6, half2v{f, f});
-                    }
-                }
-                const int koff = 2 * (64 * un + 16 * s + 8 * h);
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++) {
-                    const half8 b = *reinterpret_cast<const half8 *>(bbuf + (32 * nt + lr) * ROWB + koff);
-#pragma unroll
-                    for (int mt = 0; mt < MT; mt++)
-                        isum[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt], b, isum[mt][nt], 0, 0, 0);
-                }
-            }
-        }
-        // combine in the reference's order: acc + (yd*d*isum - yd*dmin*msum)
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            float16v msum[NT];
-            if constexpr (WT == SDY_Q4_K) {
-                const uint32_t Aw = A[mt].hd.y, Bw = A[mt].hd.z, Cw = A[mt].hd.w;
-                half8 a2;
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const int j = 4 * h + (e >> 1);  // sub-block of 16-group 8h + e
-                    const int m = j < 4 ? (int)((Bw >> (8 * j)) & 63)
-                                        : (int)(((Cw >> (8 * (j - 4) + 4)) & 15) | (((Bw >> (8 * (j - 4) + 6)) & 3) << 4));
-                    a2[e] = (_Float16)(float)m;
-                }
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++) {
-                    const half8 b2 = *reinterpret_cast<const half8 *>(bbuf + BN * ROWB + BN * 4 + 32 * (32 * nt + lr) + 16 * h);
-                    msum[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b2, float16v{}, 0, 0, 0);
-                }
-            }
-            const uint32_t dpair = WT == SDY_Q4_K ? A[mt].hd.x : A[mt].d6;
-            float ydn[NT];
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) ydn[nt] = *reinterpret_cast<const float *>(bbuf + BN * ROWB + 4 * (32 * nt + lr));
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                // D row 8(r/4) + 4h + r%4 of the tile is the A row of lane 8(r/4) + 4h + r%4
-                const uint32_t dd = (uint32_t)__shfl((int)dpair, 8 * (r >> 2) + 4 * h + (r & 3));
-                const float d = sdy_h2f((uint16_t)(dd & 0xFFFFu));
-                const float dmin = WT == SDY_Q4_K ? sdy_h2f((uint16_t)(dd >> 16)) : 0.0f;
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++) {
-                    if constexpr (WT == SDY_Q4_K) {
-                        const float dall = ydn[nt] * d, dmn = ydn[nt] * dmin;
-                        const float t1 = dall * isum[mt][nt][r], t2 = dmn * msum[nt][r];
-                        acc[mt][nt][r] = acc[mt][nt][r] + (t1 - t2);
-                    } else {
-                        const float ydd = ydn[nt] * d;
-                        acc[mt][nt][r] = acc[mt][nt][r] + ydd * isum[mt][nt][r];
-                    }
-                }
-            }
-        }
-        store_b(cur ^ 1);
-        __syncthreads();
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            A[mt] = An[mt];
-            An[mt] = Ann[mt];
-        }
-    }
-    // store (bias, residual, or the SwiGLU pair of rows 2i, 2i+1 held by this lane)
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const int tok = t0 + 32 * nt + lr;
-            if (tok >= g.n_tok) continue;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const long ri = rt + 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (ri >= g.n_rows) continue;
-                const long row = g.row0 + ri;
-                if (g.swiglu) {
-                    if ((r & 1) == 0)
-                        g.out[(size_t)tok * g.out_stride + (ri >> 1)] = sdy_silu_mul1(acc[mt][nt][r], acc[mt][nt][r + 1]);
-                } else {
-                    float v = acc[mt][nt][r];
-                    if (g.bias) v = v + g.bias[row];
-                    if (g.resid) v = g.resid[(size_t)tok * g.out_stride + row] + v;
-                    g.out[(size_t)tok * g.out_stride + row] = v;
-                }
-            }
-        }
 }
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
@@ -524,8 +171,8 @@ SDY_DEV __amdgpu_buffer_rsrc_t plane_rsrc(const uint8_t *p, uint32_t bytes) {
 // p / 32, chunk (p % 32) ^ (token % 8), so that the fragment reads of 8 consecutive lanes hit
 // distinct banks. Two stages: super-block s + 1 is in flight while s is multiplied; one
 // s_waitcnt + barrier per super-block. The per-row d (and dmin) are converted once per row into a
-// per-wave LDS table. Integer sums and the f32 combine as in k_gemm.
-template <int WT, int MT, int NT, int WM>
+// per-wave LDS table.
+template <int WT, int MT, int NT, int WM, bool WIDE>
 __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
     constexpr int BN = 32 * NT, NTH = 64 * WM;
     constexpr int YDN = BN < 64 ? 64 : BN;                  // yd slots (one DMA dword per lane)
@@ -636,6 +283,7 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
         for (int nt = 0; nt < NT; nt++) acc[mt][nt] = float16v{};
     const half2v off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
     const half2v off6 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+    const half2v off4c = {(_Float16)-1032.0f, (_Float16)-1032.0f};  // centred Q4_K quants q - 8
     // per-wave d[32 MT] then dmin[32 MT] as f32 (static LDS: a separate object from the DMA target,
     // so its reads need not wait for the activation loads in flight)
     __shared__ __align__(16) float dtab_all[WM * 64 * MT];
@@ -661,11 +309,24 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
             }
         }
         const uint8_t *bbuf = lds + cur * BUF;
-        float16v isum[MT][NT];
+        // WIDE (any block the formats can hold):
+        //   Q6_K: each scale sc = 16 sh + sl (sl in [0, 16), sh in [-8, 7]) is applied in two exact
+        //         fragments with their own integer sums, isum = 16 ihi + ilo; the partial sums stay
+        //         below 2^24 (127 * 256 * 32 * 15 and 127 * 256 * 32 * 8);
+        //   Q4_K: the quants are centred, isum = sum sc (q - 8) y + sum_j 8 sc_j bsum_j: the first sum
+        //         below 127 * 256 * 63 * 8 < 2^24, the second one more MFMA against the bsums.
+        constexpr bool SPLIT6 = WIDE && WT == SDY_Q6_K;
+        float16v isum[MT][NT], ihi[SPLIT6 ? MT : 1][SPLIT6 ? NT : 1];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) isum[mt][nt] = float16v{};
+        if constexpr (SPLIT6) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) ihi[mt][nt] = float16v{};
+        }
         // the activation fragments of step st = 4 un + s (16-element chunk 8 un + 2 s + h of each token
         // tile), read from LDS one step ahead of their MFMAs
         half8 bf[2][NT];
@@ -685,7 +346,7 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
                 const int st = 4 * un + s;
                 if (st + 1 < 16) read_b(st + 1, bf[(st + 1) & 1]);
                 __builtin_amdgcn_sched_barrier(0);  // the next step's reads go out before this step's work
-                half8 a[MT];
+                half8 a[MT], ah[SPLIT6 ? MT : 1];
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
                     if constexpr (WT == SDY_Q4_K) {
@@ -695,25 +356,51 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
                                              : (int)(((Cw >> (8 * (j - 4))) & 15) | (((Aw >> (8 * (j - 4) + 6)) & 3) << 4));
                         const u32x2 src = (s & 1) ? A[mt].q[un][1] : A[mt].q[un][0];
                         const u32x2 nib = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
-                        const _Float16 f = (_Float16)(float)sc, nf = (_Float16)(float)(-1024 * sc);
-                        a[mt] = frag_q4(nib, half2v{f, f}, half2v{nf, nf});
+                        if constexpr (WIDE) {
+                            const _Float16 f = (_Float16)(float)sc;
+                            a[mt] = frag_scaled(nib, off4c, half2v{f, f});
+                        } else {
+                            const _Float16 f = (_Float16)(float)sc, nf = (_Float16)(float)(-1024 * sc);
+                            a[mt] = frag_q4(nib, half2v{f, f}, half2v{nf, nf});
+                        }
                     } else {
                         const int j = 4 * un + s;
                         const int sc = (int)(int8_t)((A[mt].hd[j >> 2] >> (8 * (j & 3))) & 255u);
                         const u32x2 src = (s & 1) ? A[mt].q[un][1] : A[mt].q[un][0];
                         const u32x2 lo = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
                         const u32x2 hi = ((A[mt].q[un][2] >> (unsigned)(2 * s)) & 0x03030303u) << 4u;
-                        const _Float16 f = (_Float16)(float)sc;
-                        a[mt] = frag_scaled(lo | hi, off6, half2v{f, f});
+                        if constexpr (SPLIT6) {
+                            const int sl = sc & 15, sh = sc >> 4;
+                            const _Float16 fl = (_Float16)(float)sl, fh = (_Float16)(float)sh;
+                            a[mt] = frag_scaled(lo | hi, off6, half2v{fl, fl});
+                            ah[mt] = frag_scaled(lo | hi, off6, half2v{fh, fh});
+                        } else {
+                            const _Float16 f = (_Float16)(float)sc;
+                            a[mt] = frag_scaled(lo | hi, off6, half2v{f, f});
+                        }
                     }
                 }
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) {
 #pragma unroll
-                    for (int mt = 0; mt < MT; mt++)
+                    for (int mt = 0; mt < MT; mt++) {
                         isum[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt], bf[st & 1][nt], isum[mt][nt], 0, 0, 0);
+                        if constexpr (SPLIT6)
+                            ihi[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[mt], bf[st & 1][nt], ihi[mt][nt], 0, 0, 0);
+                    }
                 }
             }
+        }
+        if constexpr (SPLIT6) {  // isum = 16 ihi + ilo: 16 ihi exact, one rounding of the sum (that of (float)isum)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const float hi = 16.0f * ihi[mt][nt][r];
+                        isum[mt][nt][r] = hi + isum[mt][nt][r];
+                    }
         }
         // combine in the reference's order: acc + (yd*d*isum - yd*dmin*msum)
         float ydn[NT];
@@ -723,19 +410,29 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
         for (int mt = 0; mt < MT; mt++) {
             float16v msum[NT];
             if constexpr (WT == SDY_Q4_K) {
-                const uint32_t Bw = A[mt].hd.z, Cw = A[mt].hd.w;
-                half8 a2;
+                const uint32_t Aw = A[mt].hd.y, Bw = A[mt].hd.z, Cw = A[mt].hd.w;
+                half8 a2, a3;
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
                     const int j = 4 * h + (e >> 1);  // sub-block of 16-group 8h + e
                     const int m = j < 4 ? (int)((Bw >> (8 * j)) & 63)
                                         : (int)(((Cw >> (8 * (j - 4) + 4)) & 15) | (((Bw >> (8 * (j - 4) + 6)) & 3) << 4));
                     a2[e] = (_Float16)(float)m;
+                    if constexpr (WIDE) {
+                        const int sc = j < 4 ? (int)((Aw >> (8 * j)) & 63)
+                                             : (int)(((Cw >> (8 * (j - 4))) & 15) | (((Aw >> (8 * (j - 4) + 6)) & 3) << 4));
+                        a3[e] = (_Float16)(float)(8 * sc);
+                    }
                 }
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) {
                     const half8 b2 = *reinterpret_cast<const half8 *>(bbuf + BSOFF + 32 * (32 * nt + lr) + 16 * h);
                     msum[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b2, float16v{}, 0, 0, 0);
+                    if constexpr (WIDE) {  // + sum_j 8 sc_j bsum_j (below 16 * 504 * 2032 < 2^24): one rounding
+                        const float16v c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a3, b2, float16v{}, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 16; r++) isum[mt][nt][r] = isum[mt][nt][r] + c[r];
+                    }
                 }
             }
             // rows 8q + 4h .. 8q + 4h + 3 of the tile (D registers 4q .. 4q + 3): d, then dmin
@@ -824,8 +521,9 @@ __global__ __launch_bounds__(256) void k_gemm_prep(const uint8_t *__restrict__ x
     if (part == 0) yd[sbg] = *reinterpret_cast<const float *>(blk);
 }
 
-// Exactness check of a K-quant matrix for the GEMM: flags a row super-block whose
-// 127 * sum |w'| reaches 2^24 or (Q6_K) whose |sc * (q - 32)| exceeds 2048. One thread per
+// Which variant of the GEMM multiplies a K-quant matrix exactly: flags a row super-block whose
+// 127 * sum |w'| reaches 2^24 or (Q6_K) whose |sc * (q - 32)| exceeds 2048, which the one-fragment
+// scheme would round; the wide variant multiplies every block exactly. One thread per
 // (row, super-block) of rows [0, n_rows) of the planes.
 template <int WT>
 __global__ void k_gemm_check(GemmArgs g, int *bad) {
@@ -878,6 +576,7 @@ static GemmArgs gemm_args(const sdy_mat *m) {
     const size_t sz[5] = {unit, unit, m->type == SDY_Q4_K ? sbk * 16 : unit, m->type == SDY_Q4_K ? 0 : sbk * 16,
                           m->type == SDY_Q4_K ? 0 : sbk * 2};
     for (int i = 0; i < 5; i++) g.psz[i] = sz[i] < 0xFFFFFFFFu ? (uint32_t)sz[i] : 0xFFFFFFFFu;
+    g.wide = m->gemm_ok == 2;
     return g;
 }
 
@@ -924,54 +623,43 @@ extern "C" int sdy_gemm_ok(const sdy_mat *m, int n_tok) {
            (size_t)m->n_rows * m->n_units * 16 < 0xFFFFFFFFu;
 }
 
-template <int WT, int NT>
-static int launch_gemm(GemmArgs &g, hipStream_t st) {
-    const long row_tiles = (g.n_rows + 127) / 128;
-    const int tok_groups = (g.n_tok + 32 * NT - 1) / (32 * NT);
-    SDY_NOTE_KERNEL((k_gemm<WT, NT>));
-    hipLaunchKernelGGL((k_gemm<WT, NT>), dim3((unsigned)row_tiles, (unsigned)tok_groups), dim3(256), 0, st, g);
-    return sdy_check_launch("gemm");
-}
-
-template <int WT, int MT, int NT, int WM>
-static int launch_gemm2(GemmArgs &g, hipStream_t st) {
-    constexpr int BN = 32 * NT, BM = 32 * MT * WM;
-    constexpr size_t lds = 2 * (size_t)(BN * 528 + BN * 4 + BN * 32);
-    static size_t granted = 0;
-    const void *fn = (const void *)k_gemm2<WT, MT, NT, WM>;
-    int rc = sdy_lds_limit(fn, lds, &granted);
-    if (rc) return rc;
-    const unsigned tok_tiles = (unsigned)((g.n_tok + BN - 1) / BN), row_tiles = (unsigned)((g.n_rows + BM - 1) / BM);
-    SDY_NOTE_KERNEL((k_gemm2<WT, MT, NT, WM>));
-    hipLaunchKernelGGL((k_gemm2<WT, MT, NT, WM>), dim3(tok_tiles, row_tiles), dim3(64 * WM), lds, st, g);
-    return sdy_check_launch("gemm");
-}
-
-template <int WT, int MT, int NT, int WM>
-static int launch_gemm3(GemmArgs &g, hipStream_t st) {
+template <int WT, int MT, int NT, int WM, bool WIDE>
+static int launch_gemm3_s(GemmArgs &g, hipStream_t st) {
     constexpr int BN = 32 * NT, BM = 32 * MT * WM, YDN = BN < 64 ? 64 : BN;
     constexpr size_t lds = 2 * (size_t)(BN * 512 + YDN * 4 + BN * 32);
     static size_t granted = 0;
-    const void *fn = (const void *)k_gemm3<WT, MT, NT, WM>;
+    const void *fn = (const void *)k_gemm3<WT, MT, NT, WM, WIDE>;
     int rc = sdy_lds_limit(fn, lds, &granted);
     if (rc) return rc;
     const unsigned tok_tiles = (unsigned)((g.n_tok + BN - 1) / BN), row_tiles = (unsigned)((g.n_rows + BM - 1) / BM);
-    SDY_NOTE_KERNEL((k_gemm3<WT, MT, NT, WM>));
-    hipLaunchKernelGGL((k_gemm3<WT, MT, NT, WM>), dim3(tok_tiles, row_tiles), dim3(64 * WM), lds, st, g);
+    SDY_NOTE_KERNEL((k_gemm3<WT, MT, NT, WM, WIDE>));
+    hipLaunchKernelGGL((k_gemm3<WT, MT, NT, WM, WIDE>), dim3(tok_tiles, row_tiles), dim3(64 * WM), lds, st, g);
+    return sdy_check_launch("gemm");
+}
+
+// g.wide: the matrix has blocks that the one-fragment scheme cannot multiply exactly
+template <int WT, int MT, int NT, int WM>
+static int launch_gemm3(GemmArgs &g, hipStream_t st) {
+    return g.wide ? launch_gemm3_s<WT, MT, NT, WM, true>(g, st) : launch_gemm3_s<WT, MT, NT, WM, false>(g, st);
+}
+
+template <int WT, int MT, int NT, int WM, bool WIDE>
+static int launch_gemm3_grid_s(GemmArgs &g, unsigned tok_tiles, unsigned row_tiles, hipStream_t st) {
+    constexpr int BN = 32 * NT, YDN = BN < 64 ? 64 : BN;
+    constexpr size_t lds = 2 * (size_t)(BN * 512 + YDN * 4 + BN * 32);
+    static size_t granted = 0;
+    const void *fn = (const void *)k_gemm3<WT, MT, NT, WM, WIDE>;
+    int rc = sdy_lds_limit(fn, lds, &granted);
+    if (rc) return rc;
+    SDY_NOTE_KERNEL((k_gemm3<WT, MT, NT, WM, WIDE>));
+    hipLaunchKernelGGL((k_gemm3<WT, MT, NT, WM, WIDE>), dim3(tok_tiles, row_tiles), dim3(64 * WM), lds, st, g);
     return sdy_check_launch("gemm");
 }
 
 template <int WT, int MT, int NT, int WM>
 static int launch_gemm3_grid(GemmArgs &g, unsigned tok_tiles, unsigned row_tiles, hipStream_t st) {
-    constexpr int BN = 32 * NT, YDN = BN < 64 ? 64 : BN;
-    constexpr size_t lds = 2 * (size_t)(BN * 512 + YDN * 4 + BN * 32);
-    static size_t granted = 0;
-    const void *fn = (const void *)k_gemm3<WT, MT, NT, WM>;
-    int rc = sdy_lds_limit(fn, lds, &granted);
-    if (rc) return rc;
-    SDY_NOTE_KERNEL((k_gemm3<WT, MT, NT, WM>));
-    hipLaunchKernelGGL((k_gemm3<WT, MT, NT, WM>), dim3(tok_tiles, row_tiles), dim3(64 * WM), lds, st, g);
-    return sdy_check_launch("gemm");
+    return g.wide ? launch_gemm3_grid_s<WT, MT, NT, WM, true>(g, tok_tiles, row_tiles, st)
+                   : launch_gemm3_grid_s<WT, MT, NT, WM, false>(g, tok_tiles, row_tiles, st);
 }
 
 template <int WT>
@@ -979,34 +667,21 @@ static int gemm_type(GemmArgs &g, hipStream_t st) {
     // SARDYNE_GEMM_VARIANT picks one tile shape (tests and tuning); default: by shape
     const char *ev = getenv("SARDYNE_GEMM_VARIANT");
     const int variant = ev ? atoi(ev) : 1;
-    if (variant == 1) {
-        // 128-row workgroup tiles (4 waves of 32 rows); 64 tokens per tile when there are enough
-        // row tiles to fill the GPU twice over with them, else 32 (measured on the 2048- to
-        // 22016-row matrices of a 512-token prefill)
-        const long r128 = (g.n_rows + 127) / 128, t64 = (g.n_tok + 63) / 64;
-        if (r128 * t64 >= 1024) return launch_gemm3<WT, 1, 2, 4>(g, st);
-        return launch_gemm3<WT, 1, 1, 4>(g, st);
+    switch (variant) {
+    case 11: return launch_gemm3<WT, 1, 4, 8>(g, st);
+    case 12: return launch_gemm3<WT, 1, 2, 4>(g, st);
+    case 13: return launch_gemm3<WT, 1, 2, 8>(g, st);
+    case 14: return launch_gemm3<WT, 1, 1, 4>(g, st);
+    case 15: return launch_gemm3<WT, 1, 4, 4>(g, st);
+    case 16: return launch_gemm3<WT, 2, 2, 4>(g, st);
+    default: break;
     }
-    if (variant == 2) return launch_gemm2<WT, 2, 4, 4>(g, st);
-    if (variant == 3) return launch_gemm2<WT, 1, 4, 4>(g, st);
-    if (variant == 4) return launch_gemm2<WT, 1, 2, 4>(g, st);
-    if (variant == 5) return launch_gemm2<WT, 1, 2, 2>(g, st);
-    if (variant == 6) return launch_gemm2<WT, 2, 2, 4>(g, st);
-    if (variant == 11) return launch_gemm3<WT, 1, 4, 8>(g, st);
-    if (variant == 12) return launch_gemm3<WT, 1, 2, 4>(g, st);
-    if (variant == 13) return launch_gemm3<WT, 1, 2, 8>(g, st);
-    if (variant == 14) return launch_gemm3<WT, 1, 1, 4>(g, st);
-    if (variant == 15) return launch_gemm3<WT, 1, 4, 4>(g, st);
-    if (variant == 16) return launch_gemm3<WT, 2, 2, 4>(g, st);
-    // variant 0: the register-only kernel (activation fragments from global memory)
-    // token tiles per wave: the largest of 4, 2, 1 that still gives a few waves per SIMD
-    const long waves_at = [&](int nt) { return (g.n_rows + 31) / 32 * ((g.n_tok + 32 * nt - 1) / (32 * nt)); }(4);
-    int n_cu = 256;
-    size_t mem = 0;
-    sdy_device_info(&n_cu, &mem);
-    if (waves_at >= 4L * n_cu && g.n_tok > 64) return launch_gemm<WT, 4>(g, st);
-    if (g.n_tok > 32) return launch_gemm<WT, 2>(g, st);
-    return launch_gemm<WT, 1>(g, st);
+    // 128-row workgroup tiles (4 waves of 32 rows); 64 tokens per tile when there are enough row
+    // tiles to fill the GPU twice over with them, else 32 (measured on the 2048- to 22016-row
+    // matrices of a 512-token prefill)
+    const long r128 = (g.n_rows + 127) / 128, t64 = (g.n_tok + 63) / 64;
+    if (r128 * t64 >= 1024) return launch_gemm3<WT, 1, 2, 4>(g, st);
+    return launch_gemm3<WT, 1, 1, 4>(g, st);
 }
 
 // out[t][row] for rows [a->row0, a->row1) and a->n_tok tokens of Q8_K activations a->xq, through

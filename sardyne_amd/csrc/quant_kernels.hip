@@ -1710,7 +1710,7 @@ extern "C" int sdy_mat_from_device(sdy_mat *m, int type, int n_in, long n_rows, 
     if (m->gemm_ok) {
         int bad = 1;
         if ((rc = sdy_gemm_check_rows(m, 0, n_rows, &bad, s))) return rc;
-        if (bad) m->gemm_ok = 0;
+        if (bad) m->gemm_ok = 2;
     }
     return 0;
 }
@@ -1729,7 +1729,7 @@ extern "C" int sdy_mat_upload_map(sdy_mat *m, long r0, long n, long step, long g
     if (!rc && m->gemm_ok) {
         int bad = 1;
         rc = sdy_gemm_check_rows(m, r0, span - r0 + 1, &bad, s);
-        if (!rc && bad) m->gemm_ok = 0;
+        if (!rc && bad) m->gemm_ok = 2;
     }
     return rc;
 }

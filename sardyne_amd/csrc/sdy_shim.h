@@ -55,7 +55,8 @@ typedef struct {
     long n_rows;    /* rows (experts stacked: n_expert * n_out) */
     int n_units;    /* 64-element units per row (quantized types) */
     size_t plane_off[5];
-    int gemm_ok;    /* K-quant rows the MFMA GEMM multiplies exactly (every row passes its check) */
+    int gemm_ok;    /* Q4_K / Q6_K: 1 when the GEMM's one-fragment scheme is exact for every block,
+                       2 when some block needs the wide variant (Q6_K: twice the MFMA work); 0 other types */
 } sdy_mat;
 
 /* Bytes of the device layout for a matrix. */
@@ -81,7 +82,7 @@ int sdy_mat_repack_async(sdy_mat *m, long r0, long n, long step, long grp, long 
 /* Pipelined uploads (upload.hip): a ring of pinned host slots and device slots. A host thread pool
  * copies the next rows from the file mapping into a free pinned slot (advising the kernel to read
  * the rows after them ahead), the DMA engine moves the slot to the device on a copy stream, and the
- * repack runs on the work stream; the three overlap across slots. The GEMM exactness checks of the
+ * repack runs on the work stream; the three overlap across slots. The GEMM variant checks of the
  * uploaded rows run at sdy_uploader_finish, which waits for everything and sets each matrix's
  * gemm_ok. A matrix must stay at its address until then. */
 typedef struct sdy_uploader sdy_uploader;
@@ -166,9 +167,10 @@ int sdy_norm_quant_gemm(const float *x, const float *w, float eps, int n, int n_
 int sdy_gemm_grouped_tile(void);
 int sdy_gemm_grouped(const sdy_mat *m, long grp_rows, int n_grp, const int *grp_tok, const int *grp_tile,
                      const int *out_row, const sdy_mv_args *a, void *ws, sdy_stream s);
-/* Exactness check of rows [r0, r0 + n) of m for the GEMM: *bad_host = 1 when some row fails. */
+/* Variant check of rows [r0, r0 + n) of m for the GEMM: *bad_host = 1 when some row has a block
+ * that only the wide variant multiplies exactly. */
 int sdy_gemm_check_rows(const sdy_mat *m, long r0, long n, int *bad_host, sdy_stream s);
-/* The same, queued on s: sets *bad_dev (device int, zero beforehand) to nonzero when some row fails */
+/* The same, queued on s: sets *bad_dev (device int, zero beforehand) to nonzero for such a row */
 int sdy_gemm_check_rows_async(const sdy_mat *m, long r0, long n, int *bad_dev, sdy_stream s);
 
 /* raw float-weight matrices (F32/F16/BF16, GGUF row-major layout kept as is) */

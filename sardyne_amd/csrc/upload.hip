@@ -196,7 +196,7 @@ extern "C" int sdy_uploader_finish(sdy_uploader *u) {
     if (flags) sdy_free(flags);
     if (rc) return rc;
     for (size_t i = 0; i < nc; i++)
-        if (bad[i]) u->checks[i].m->gemm_ok = 0;
+        if (bad[i]) u->checks[i].m->gemm_ok = 2;
     u->checks.clear();
     for (int k = 0; k < u->n_slots; k++) u->busy[k] = false;
     return 0;

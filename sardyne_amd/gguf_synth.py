@@ -12,6 +12,11 @@ distributions of the benchmark workloads:
 - Q8_0: f16 scale = |N(0, 0.01)|, int8 quants uniform in [-127, 127];
 - Q4_0 / Q5_0: f16 scale = |N(0, 0.01)|, uniform quant bytes.
 
+``scales="file"`` gives the K-quant scales the shape they have in quantized model files, where each
+super-block's scales are normalised to the largest one: Q6_K int8 scales with the sub-block of
+largest amplitude at -128 and the others in [-128, 127] by their signed amplitude; Q4_K 6-bit scales
+and minima with the largest at 63. Sub-block amplitudes are the maxima of 16 |N(0, 1)| draws.
+
 Everything is produced block-row by block-row from a seeded ``numpy.random.Generator``, so a
 model of several GB is written without holding it in memory.
 """
@@ -43,15 +48,45 @@ def _f16_abs_normal(rng, std, n):
     return np.abs(rng.standard_normal(n) * std).astype(np.float16).view(np.uint8).reshape(n, 2)
 
 
-def random_blocks(type_name: str, n_blocks: int, rng: np.random.Generator) -> np.ndarray:
-    """[n_blocks, block_bytes] uint8 with the workload distributions above."""
+def _amplitudes(rng, n_blocks, n_sub):
+    """[n_blocks, n_sub] sub-block amplitudes: the largest |N(0, 1)| of 16 draws."""
+    return np.abs(rng.standard_normal((n_blocks, n_sub, 16))).max(axis=2)
+
+
+def _q4k_pack(sc, mn):
+    """The 12 scale bytes of Q4_K from 8 six-bit scales and minima per block: bytes 0-3 hold
+    scales 0-3 (low 6 bits) and the top 2 bits of scales 4-7; bytes 4-7 minima 0-3 and the top bits
+    of minima 4-7; bytes 8-11 the low 4 bits of scales 4-7 and (high nibble) of minima 4-7."""
+    sc, mn = sc.astype(np.uint8), mn.astype(np.uint8)
+    out = np.empty((sc.shape[0], 12), np.uint8)
+    out[:, 0:4] = sc[:, 0:4] | ((sc[:, 4:8] >> 4) << 6)
+    out[:, 4:8] = mn[:, 0:4] | ((mn[:, 4:8] >> 4) << 6)
+    out[:, 8:12] = (sc[:, 4:8] & 15) | ((mn[:, 4:8] & 15) << 4)
+    return out
+
+
+def random_blocks(type_name: str, n_blocks: int, rng: np.random.Generator, scales: str = "workload") -> np.ndarray:
+    """[n_blocks, block_bytes] uint8 with the workload distributions above (K-quant scales as in
+    model files with scales="file")."""
     _, _, size = GGML_TYPES[TYPE_ID[type_name]]
     b = np.frombuffer(rng.bytes(n_blocks * size), np.uint8).reshape(n_blocks, size).copy()
+    if scales not in ("workload", "file"):
+        raise ValueError(scales)
     if type_name == "Q4_K":
         b[:, 0:2] = _f16_abs_normal(rng, 0.02, n_blocks)
         b[:, 2:4] = _f16_abs_normal(rng, 0.02, n_blocks)
+        if scales == "file":
+            a, m = _amplitudes(rng, n_blocks, 8), _amplitudes(rng, n_blocks, 8)
+            sc = np.rint(63 * a / a.max(axis=1, keepdims=True))
+            mn = np.rint(63 * m / m.max(axis=1, keepdims=True))
+            b[:, 4:16] = _q4k_pack(sc, mn)
     elif type_name == "Q6_K":
-        b[:, 192:208] = rng.integers(-32, 32, (n_blocks, 16), dtype=np.int8).view(np.uint8)
+        if scales == "file":
+            a = _amplitudes(rng, n_blocks, 16) * rng.choice([-1.0, 1.0], (n_blocks, 16))
+            top = a[np.arange(n_blocks), np.abs(a).argmax(axis=1)][:, None]
+            b[:, 192:208] = np.minimum(127, np.rint(-128 * a / top)).astype(np.int8).view(np.uint8)
+        else:
+            b[:, 192:208] = rng.integers(-32, 32, (n_blocks, 16), dtype=np.int8).view(np.uint8)
         b[:, 208:210] = _f16_abs_normal(rng, 0.01, n_blocks)
     elif type_name == "Q8_0":
         b[:, 0:2] = _f16_abs_normal(rng, 0.01, n_blocks)
@@ -188,6 +223,7 @@ class ModelSpec:
     bias_std: float = 0.02
     type_fn: object = None  # optional name -> weight type override for quantized matrices
     same_experts: bool = False  # every expert of a layer gets the blocks of expert 0 (the dense matrix of its seed)
+    scales: str = "workload"  # K-quant scale distribution: "workload" or "file" (random_blocks)
 
 
 def qwen25_3b(n_layer=36) -> ModelSpec:
@@ -202,18 +238,18 @@ def qwen3_30b_a3b(n_layer=48) -> ModelSpec:
                      rope_theta=1e6)
 
 
-def _matrix_producer(type_name, n_out, n_in, seed, n_expert=0, same=False):
+def _matrix_producer(type_name, n_out, n_in, seed, n_expert=0, same=False, scales="workload"):
     """Random blocks of an n_out x n_in matrix (n_expert stacked ones). same: one matrix drawn from
     the seed, repeated for every expert, so each expert equals the dense matrix of that seed."""
     def produce():
         rng = np.random.default_rng(seed)
         _, blk, _ = GGML_TYPES[TYPE_ID[type_name]]
         if same:
-            one = random_blocks(type_name, n_out * (n_in // blk), rng)
+            one = random_blocks(type_name, n_out * (n_in // blk), rng, scales)
             return np.tile(one.reshape(1, -1), (max(1, n_expert), 1)).tobytes()
         rows = n_out * max(1, n_expert)
         nb = rows * (n_in // blk)
-        return random_blocks(type_name, nb, rng).tobytes()
+        return random_blocks(type_name, nb, rng, scales).tobytes()
     return produce
 
 
@@ -253,26 +289,26 @@ def write_model(path, spec: ModelSpec, seed: int = 0) -> Path:
         t = spec.type_fn(name) if spec.type_fn else None
         if t and t != tname and tname not in ("F32", "F16", "BF16"):
             n_out = int(np.prod(ne[1:]))
-            produce = _matrix_producer(t, n_out, ne[0], nxt())
+            produce = _matrix_producer(t, n_out, ne[0], nxt(), scales=spec.scales)
             tname = t
         orig_add(name, ne, tname, produce)
 
     b.add_tensor = add_matrix
     b.add_tensor("token_embd.weight", (dim, spec.n_vocab), spec.t_embd,
-                 _matrix_producer(spec.t_embd, spec.n_vocab, dim, nxt()))
+                 _matrix_producer(spec.t_embd, spec.n_vocab, dim, nxt(), scales=spec.scales))
     b.add_array("output_norm.weight", norm(dim))
     if not spec.tied:
         b.add_tensor("output.weight", (dim, spec.n_vocab), spec.t_output,
-                     _matrix_producer(spec.t_output, spec.n_vocab, dim, nxt()))
+                     _matrix_producer(spec.t_output, spec.n_vocab, dim, nxt(), scales=spec.scales))
     for l in range(spec.n_layer):
         p = f"blk.{l}."
         b.add_array(p + "attn_norm.weight", norm(dim))
         b.add_array(p + "ffn_norm.weight", norm(dim))
-        b.add_tensor(p + "attn_q.weight", (dim, q_dim), spec.t_default, _matrix_producer(spec.t_default, q_dim, dim, nxt()))
-        b.add_tensor(p + "attn_k.weight", (dim, kv_dim), spec.t_default, _matrix_producer(spec.t_default, kv_dim, dim, nxt()))
-        b.add_tensor(p + "attn_v.weight", (dim, kv_dim), spec.t_attn_v, _matrix_producer(spec.t_attn_v, kv_dim, dim, nxt()))
+        b.add_tensor(p + "attn_q.weight", (dim, q_dim), spec.t_default, _matrix_producer(spec.t_default, q_dim, dim, nxt(), scales=spec.scales))
+        b.add_tensor(p + "attn_k.weight", (dim, kv_dim), spec.t_default, _matrix_producer(spec.t_default, kv_dim, dim, nxt(), scales=spec.scales))
+        b.add_tensor(p + "attn_v.weight", (dim, kv_dim), spec.t_attn_v, _matrix_producer(spec.t_attn_v, kv_dim, dim, nxt(), scales=spec.scales))
         b.add_tensor(p + "attn_output.weight", (q_dim, dim), spec.t_default,
-                     _matrix_producer(spec.t_default, dim, q_dim, nxt()))
+                     _matrix_producer(spec.t_default, dim, q_dim, nxt(), scales=spec.scales))
         if spec.qkv_bias:
             b.add_array(p + "attn_q.bias", (rng.standard_normal(q_dim) * spec.bias_std).astype(np.float32))
             b.add_array(p + "attn_k.bias", (rng.standard_normal(kv_dim) * spec.bias_std).astype(np.float32))
@@ -284,18 +320,18 @@ def write_model(path, spec: ModelSpec, seed: int = 0) -> Path:
             ne, fe = spec.n_expert, spec.ffn_exp_dim
             b.add_array(p + "ffn_gate_inp.weight", (rng.standard_normal((ne, dim)) * spec.router_std).astype(np.float32))
             b.add_tensor(p + "ffn_gate_exps.weight", (dim, fe, ne), spec.t_default,
-                         _matrix_producer(spec.t_default, fe, dim, nxt(), ne, spec.same_experts))
+                         _matrix_producer(spec.t_default, fe, dim, nxt(), ne, spec.same_experts, spec.scales))
             b.add_tensor(p + "ffn_up_exps.weight", (dim, fe, ne), spec.t_default,
-                         _matrix_producer(spec.t_default, fe, dim, nxt(), ne, spec.same_experts))
+                         _matrix_producer(spec.t_default, fe, dim, nxt(), ne, spec.same_experts, spec.scales))
             b.add_tensor(p + "ffn_down_exps.weight", (fe, dim, ne), spec.t_ffn_down,
-                         _matrix_producer(spec.t_ffn_down, dim, fe, nxt(), ne, spec.same_experts))
+                         _matrix_producer(spec.t_ffn_down, dim, fe, nxt(), ne, spec.same_experts, spec.scales))
         else:
             b.add_tensor(p + "ffn_gate.weight", (dim, spec.ffn_dim), spec.t_default,
-                         _matrix_producer(spec.t_default, spec.ffn_dim, dim, nxt()))
+                         _matrix_producer(spec.t_default, spec.ffn_dim, dim, nxt(), scales=spec.scales))
             b.add_tensor(p + "ffn_up.weight", (dim, spec.ffn_dim), spec.t_default,
-                         _matrix_producer(spec.t_default, spec.ffn_dim, dim, nxt()))
+                         _matrix_producer(spec.t_default, spec.ffn_dim, dim, nxt(), scales=spec.scales))
             b.add_tensor(p + "ffn_down.weight", (spec.ffn_dim, dim), spec.t_ffn_down,
-                         _matrix_producer(spec.t_ffn_down, dim, spec.ffn_dim, nxt()))
+                         _matrix_producer(spec.t_ffn_down, dim, spec.ffn_dim, nxt(), scales=spec.scales))
     return b.write()
 
 

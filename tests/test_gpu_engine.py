@@ -254,6 +254,24 @@ def test_logits_bit_identical_to_reference(spec, tmp_path):
         assert np.mean(np.stack(split).argmax(-1) == np.stack(exp).argmax(-1)) == 1.0, mode
 
 
+@pytest.mark.parametrize("spec", ["qwen2-kquant", "moe-128x8", "qwen2-kquant-v4k", "llama-kquant"])
+def test_file_scales_logits_bit_identical(spec, tmp_path):
+    """K-quant scales as quantized model files hold them (Q6_K int8 scales down to -128, Q4_K
+    scales normalised to 63): the prefill GEMMs take the wide variant and the logits keep the
+    oracle's bits, prompt chunks and one-token steps alike."""
+    path = tmp_path / "m.gguf"
+    write_model(path, dataclasses.replace(SPECS[spec], context=160, scales="file"), seed=11)
+    toks = np.random.default_rng(12).integers(0, 300, 90).tolist()
+    model = LoadedModel(path)
+    with engine_env(SARDYNE_ATTENTION="exact"):
+        ctx = model.session(max_seq=128, n_batch=64)
+    got = [ctx.feed(toks[:80])] + [ctx.feed([t]) for t in toks[80:90]]
+    ref = O.OracleContext(path, 128, n_batch=64, simd=1)
+    exp = [ref.eval(toks[:80])] + [ref.eval([t]) for t in toks[80:90]]
+    for i, (g, e) in enumerate(zip(got, exp)):
+        assert np.array_equal(g.view(np.uint32), e.view(np.uint32)), (i, float(np.abs(g - e).max()))
+
+
 @pytest.mark.parametrize("spec", ["qwen2-kquant", "qwen2-gqa8-hd128", "moe-128x8", "qwen2-kquant-vmix"])
 def test_f16_kv_cache(spec, tmp_path):
     """The f16 KV cache (SARDYNE_KV=f16): with the exact attention, prefill and one-token logits have

@@ -1016,17 +1016,22 @@ def test_quantize_gemm_expansion(norm, n_in, n_tok):
     assert np.array_equal(bits(gemm(0)), bits(exp))
 
 
-@pytest.mark.parametrize("variant", ["0", "3", "4", "5", "6", "11", "12", "13", "14", "15", "16"])
+@pytest.mark.parametrize("variant", ["11", "12", "13", "14", "15", "16"])
 @pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
 def test_gemm_tile_variants_bit_exact(kind, variant, monkeypatch):
     """Every workgroup tile shape of the GEMM (forced through SARDYNE_GEMM_VARIANT) gives the
-    reference's bits, with partial row and token tiles."""
+    reference's bits, with partial row and token tiles, in its one-fragment and wide forms."""
     monkeypatch.setenv("SARDYNE_GEMM_VARIANT", variant)
     for n_in, n_out, n_tok in [(2048, 300, 200), (768, 40, 17), (11008, 70, 130)]:
         t, w, xq = _gemm_case(kind, n_in, n_out, n_tok, seed=n_in + n_out + n_tok + 1)
         got = _gemm_run(t, w, xq, n_in, n_out, n_tok)
         exp = O.matmul_q(w, t, xq, n_in, simd=1)
         assert np.array_equal(bits(got), bits(exp)), (n_in, n_out, n_tok)
+    n_in, n_out, n_tok = 1024, 200, 150
+    w = _full_range_blocks(kind, n_out, n_in, 11)
+    xq = O.quantize(np.random.default_rng(12).standard_normal((n_tok, n_in)).astype(np.float32), O.Q8_K)
+    got = _gemm_run(t, w, xq, n_in, n_out, n_tok)
+    assert np.array_equal(bits(got), bits(O.matmul_q(w, t, xq, n_in, simd=1)))
 
 
 @pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
@@ -1048,17 +1053,61 @@ def test_gemm_bias_resid_rows_swiglu(kind):
     assert np.array_equal(bits(sw), bits(g))
 
 
-def test_gemm_exactness_check_rejects_overflowing_rows():
-    """Q6_K rows whose scaled values exceed what f16 holds exactly are flagged (they take the
-    matvec path); ordinary rows are accepted."""
+def _full_range_blocks(kind, n_out, n_in, seed):
+    """Blocks with scales over the whole range the format stores: Q6_K int8 scales in [-128, 127]
+    (row 0 all -128 with quants 0, i.e. values -32; row 1 all 127 with quants 63), Q4_K 6-bit scales
+    and minima in [0, 63] (rows 0 and 1 all 63 with quants 15)."""
+    rng = np.random.default_rng(seed)
+    w = random_blocks(kind, n_out * n_in // 256, rng).reshape(n_out, n_in // 256, -1)
+    if kind == "Q6_K":
+        w[:, :, 192:208] = rng.integers(-128, 128, w.shape[:2] + (16,)).astype(np.int8).view(np.uint8)
+        w[0, :, 0:192], w[0, :, 192:208] = 0, np.uint8(0x80)
+        w[1, :, 0:192], w[1, :, 192:208] = 0xFF, 127
+    else:
+        w[:, :, 4:16] = rng.integers(0, 256, w.shape[:2] + (12,), dtype=np.uint8)
+        w[0:2, :, 4:144] = 0xFF
+    return w.reshape(n_out, -1)
+
+
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("n_in,n_out,n_tok", [(2048, 96, 40), (1024, 37, 129), (256, 64, 2)])
+def test_gemm_wide_variant_bit_exact(kind, n_in, n_out, n_tok):
+    """Matrices whose blocks the one-fragment scheme would round (Q6_K |sc * (q - 32)| above 2048,
+    partial sums of 2^24 and more) are flagged for the wide variant (gemm_ok 2), which keeps
+    the oracle's bits for every row and token: scales over the whole stored range, a token of one
+    sign (Q8_K values all -127) that drives the extreme rows' sums to their bounds. The same shapes
+    with the workload's scales take the one-fragment variant (gemm_ok 1)."""
+    L = lib()
+    t = TYPES[kind]
+    w = _full_range_blocks(kind, n_out, n_in, n_in + n_out)
+    x = np.random.default_rng(n_tok).standard_normal((n_tok, n_in)).astype(np.float32)
+    x[0] = 1.0
+    xq = O.quantize(x, O.Q8_K)
+    m = capi.DeviceMatrix(t, n_in, n_out, w)
+    assert m.m.gemm_ok == 2
+    got = _gemm_run(t, w, xq, n_in, n_out, n_tok)
+    exp = O.matmul_q(w, t, xq, n_in, simd=1)
+    assert np.array_equal(bits(got), bits(exp))
+    if n_out % 2 == 0:
+        sw = _gemm_run(t, w, xq, n_in, n_out, n_tok, epilogue=capi.EPI_SWIGLU)
+        g, u = exp[:, 0::2].copy(), exp[:, 1::2].copy()
+        lib().op_silu_mul(ptr(g), ptr(u), g.size)
+        assert np.array_equal(bits(sw), bits(g))
+    _, w1, _ = _gemm_case(kind, n_in, n_out, n_tok, seed=n_in + n_out)
+    assert capi.DeviceMatrix(t, n_in, n_out, w1).m.gemm_ok == 1
+
+
+def test_gemm_variant_check_flags_rows():
+    """One Q6_K block with scales -128 anywhere in the matrix selects the wide variant;
+    ordinary rows keep the one-fragment one."""
     L = lib()
     w = random_blocks("Q6_K", 8 * 4, np.random.default_rng(3)).reshape(8, -1)
     ok = capi.DeviceMatrix(O.Q6_K, 1024, 8, w)
-    assert L.sdy_gemm_ok(ctypes.byref(ok.m), 32)
+    assert L.sdy_gemm_ok(ctypes.byref(ok.m), 32) and ok.m.gemm_ok == 1
     w2 = w.copy().reshape(-1, 210)
     w2[5, 192:208] = np.uint8(0x80)  # scales -128: |-128 * (q - 32)| reaches 4096
-    bad = capi.DeviceMatrix(O.Q6_K, 1024, 8, w2.reshape(8, -1))
-    assert not L.sdy_gemm_ok(ctypes.byref(bad.m), 32)
+    split = capi.DeviceMatrix(O.Q6_K, 1024, 8, w2.reshape(8, -1))
+    assert L.sdy_gemm_ok(ctypes.byref(split.m), 32) and split.m.gemm_ok == 2
 
 
 @pytest.mark.parametrize("interleaved", [0, 1], ids=["neox", "llama"])
@@ -1268,8 +1317,8 @@ def _mat_bytes(m):
 def test_pipelined_upload_equals_synchronous(kind, n_in, grp, n_grp, bad_scale):
     """The pipelined uploader (1 MiB pinned/device slots, so a tensor spans several slots; the rows of
     a per-group interleaved map, as the engine's per-expert gate|up, split at group boundaries) leaves
-    the same device bytes as the synchronous upload, and the deferred exactness check the same
-    gemm_ok (a Q6_K block with scale -128 fails it)."""
+    the same device bytes as the synchronous upload, and the deferred variant check the same
+    gemm_ok (a Q6_K block with scale -128 selects the wide variant)."""
     L = lib()
     t = TYPES[kind]
     rng = np.random.default_rng(grp + n_in)
@@ -1299,7 +1348,7 @@ def test_pipelined_upload_equals_synchronous(kind, n_in, grp, n_grp, bad_scale):
         assert _mat_bytes(mats[0]).tobytes() == _mat_bytes(mats[1]).tobytes()
         assert mats[0].gemm_ok == mats[1].gemm_ok
         if kind in ("Q4_K", "Q6_K"):
-            assert mats[1].gemm_ok == (0 if bad_scale else 1)
+            assert mats[1].gemm_ok == (2 if bad_scale else 1)
     finally:
         for m in mats:
             L.sdy_mat_free(ctypes.byref(m))
