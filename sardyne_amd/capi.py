@@ -171,6 +171,9 @@ _DEVICE_SIGNATURES = {
                                       ctypes.c_long, _vp]),
     "sdy_attention": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _int, ctypes.c_long, ctypes.c_long, _vp,
                              _vp, ctypes.c_long, _vp]),
+    "sdy_attention_flash_ok": (_int, [_int, _int, _int]),
+    "sdy_attention_flash": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _int, ctypes.c_long, ctypes.c_long,
+                                   _vp, ctypes.c_long, _vp]),
     "sdy_quantize_gemm": (_int, [_vp, _vp, _int, _int, _vp, _vp]),
     "sdy_norm_quant_gemm": (_int, [_vp, _vp, ctypes.c_float, _int, _int, _vp, _vp, _vp, _vp]),
     "sdy_attn_decode_ok": (_int, [_int, _int, _int, _int]),

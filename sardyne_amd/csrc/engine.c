@@ -634,8 +634,9 @@ engine_ctx *engine_ctx_new(const engine_model *m, int32_t max_seq, int32_t n_bat
     }
     /* SARDYNE_ATTENTION: the one-token attention. chunked (the default): split over spans of
        positions in two launches, within tolerance of the reference (its f32 rounding only); exact: the
-       reference's softmax over every position and its in-order weighted sum, bit for bit; split: the
-       chunked form in one launch (f32 cache only) */
+       reference's softmax over every position and its in-order weighted sum, bit for bit, for the
+       one-token steps and the prompt alike; split: the chunked form in one launch (f32 cache only).
+       Except with exact, the prompt's attention runs in flash form (also within tolerance). */
     const char *attn = getenv("SARDYNE_ATTENTION");
     if (!attn || !attn[0] || !strcmp(attn, "chunked")) {
         c->attn_mode = SDY_ATTN_CHUNKED;
@@ -663,8 +664,11 @@ engine_ctx *engine_ctx_new(const engine_model *m, int32_t max_seq, int32_t n_bat
     c->moe_device = c->decode_fused && !env_on("SARDYNE_NO_DEVICE_MOE") && sdy_engine_moe_device_ok(c);
     c->use_graph = c->decode_fused && (!m->info.n_expert || c->moe_device) && !env_on("SARDYNE_NO_GRAPH");
     c->fuse_act = c->decode_fused && !env_on("SARDYNE_NO_FUSED_ACT");
-    /* the split forms take the fused one-token step and their head layouts; otherwise the exact chain */
     const engine_model_info *in = &m->info;
+    /* the prompt's attention: in flash form on the matrix cores unless the reference's bits are asked
+       for (SARDYNE_ATTENTION=exact) */
+    c->prefill_flash = c->attn_mode != SDY_ATTN_EXACT && sdy_attention_flash_ok(in->n_head, in->n_kv_head, in->head_dim);
+    /* the split forms take the fused one-token step and their head layouts; otherwise the exact chain */
     if (!c->decode_fused || (c->attn_mode == SDY_ATTN_CHUNKED && !sdy_attn_chunked_ok(in->n_head, in->n_kv_head,
                                                                                       in->head_dim)) ||
         (c->attn_mode == SDY_ATTN_SPLIT && !sdy_attn_decode_split_ok(in->n_head, in->n_kv_head, in->head_dim)))

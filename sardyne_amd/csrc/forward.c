@@ -580,8 +580,12 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
             TRY(sdy_qk_rope_kv_strided(q, k, v, qs, ks, vs, L->q_norm, L->k_norm, in->norm_eps, c->rope_cos,
                                        c->rope_sin, pos0, n, in->n_head, in->n_kv_head, hd, in->rope_interleaved, kc,
                                        vc, c->kv_type, head_stride, c->st));
-            TRY(sdy_attention(q, kc, vc, c->kv_type, n, in->n_head, in->n_kv_head, hd, pos0 + 1, head_stride, qs,
-                              c->part, c->att, q_dim, c->st));
+            if (c->prefill_flash && (qs & 3) == 0)
+                TRY(sdy_attention_flash(q, kc, vc, c->kv_type, n, in->n_head, in->n_kv_head, hd, pos0 + 1, head_stride,
+                                        qs, c->att, q_dim, c->st));
+            else
+                TRY(sdy_attention(q, kc, vc, c->kv_type, n, in->n_head, in->n_kv_head, hd, pos0 + 1, head_stride, qs,
+                                  c->part, c->att, q_dim, c->st));
             TRY(mm(c, c->x, c->att, &L->wo, n, NULL, c->x, 1));
         }
         if (in->n_expert && decode && c->moe_device) {

@@ -19,6 +19,8 @@ struct KvElt<float> {
     SDY_DEV static float ld(const float *p, size_t i) { return p[i]; }
     // four consecutive elements from i (i a multiple of 4)
     SDY_DEV static sdy_f32x4 ld4(const float *p, size_t i) { return *reinterpret_cast<const sdy_f32x4 *>(p + i); }
+    // two consecutive elements from i (i even)
+    SDY_DEV static float2 ld2(const float *p, size_t i) { return *reinterpret_cast<const float2 *>(p + i); }
     SDY_DEV static void st(float *p, size_t i, float v) { p[i] = v; }
     // the value a write then a read of v gives
     SDY_DEV static float round(float v) { return v; }
@@ -40,6 +42,10 @@ struct KvElt<uint16_t> {
         r[2] = sdy_h2f((uint16_t)(u.y & 0xFFFFu));
         r[3] = sdy_h2f((uint16_t)(u.y >> 16));
         return r;
+    }
+    SDY_DEV static float2 ld2(const uint16_t *p, size_t i) {
+        const uint32_t u = *reinterpret_cast<const uint32_t *>(p + i);
+        return make_float2(sdy_h2f((uint16_t)(u & 0xFFFFu)), sdy_h2f((uint16_t)(u >> 16)));
     }
     SDY_DEV static void st(uint16_t *p, size_t i, float v) { p[i] = sdy_f2h(v); }
     SDY_DEV static float round(float v) { return sdy_h2f(sdy_f2h(v)); }

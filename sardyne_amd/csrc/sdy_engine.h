@@ -70,6 +70,7 @@ struct engine_ctx {
     int attn_mode;              /* one-token attention: SDY_ATTN_EXACT (the reference's bits), or split
                                    over positions within tolerance: SDY_ATTN_CHUNKED (two launches),
                                    SDY_ATTN_SPLIT (one launch) */
+    int prefill_flash;          /* many-token attention in flash form (sdy_attention_flash), within tolerance */
     float *attn_part;           /* chunked / split attention: per-span partials */
     unsigned *attn_count;       /* split attention: arrivals per kv head (zero between launches) */
     float *qkv;                 /* q | k | v of one token */

@@ -31,6 +31,12 @@ size_t sdy_attn_scores_floats(int n_tok, int n_head, int max_kv);
 int sdy_attention(const float *q, const void *k_cache, const void *v_cache, int kv_type, int n_tok, int n_head,
                   int n_kv_head, int hd, int n_kv0, long head_stride, long q_stride, float *scores, float *out,
                   long out_stride, sdy_stream s);
+/* The same attention in flash form on the f32 matrix cores (attn_flash.hip): within tolerance of the
+ * reference, not its bits; no scratch. head_dim 64 or 128; q rows and both strides 16-byte aligned. */
+int sdy_attention_flash_ok(int n_head, int n_kv_head, int hd);
+int sdy_attention_flash(const float *q, const void *k_cache, const void *v_cache, int kv_type, int n_tok,
+                        int n_head, int n_kv_head, int hd, int n_kv0, long head_stride, long q_stride, float *out,
+                        long out_stride, sdy_stream s);
 int sdy_silu_mul(float *gate, const float *up, long n, sdy_stream s);
 int sdy_add(const float *a, const float *b, float *out, long n, sdy_stream s);
 int sdy_axpy(float *y, float a, const float *x, long n, sdy_stream s);

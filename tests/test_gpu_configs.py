@@ -105,8 +105,8 @@ def qwen25_3b_path():
 
 def _run_and_compare(path, n_ctx, n_batch, n_steps, max_seq, seed, tol):
     """The engine with the exact attention chain (SARDYNE_ATTENTION=exact) gives the reference's bits
-    at every step; the split attentions (chunked, split) give the prompt's bits (no decode step) and
-    then logits within tol of the logit scale, with the same greedy tokens."""
+    at every step; with the split one-token attentions (chunked, split), whose prompt runs through
+    the flash attention, the logits are within tol of the logit scale, with the same greedy tokens."""
     toks = np.random.default_rng(seed).integers(0, 151936, n_ctx + n_steps).astype(np.int32)
     model = LoadedModel(path)
     runs = {}
@@ -126,7 +126,6 @@ def _run_and_compare(path, n_ctx, n_batch, n_steps, max_seq, seed, tol):
     scale = float(np.abs(exp).max())
     for mode in ("chunked", "split"):
         split = np.stack(runs[mode])
-        assert np.array_equal(split[0].view(np.uint32), exp[0].view(np.uint32)), mode
         assert float(np.abs(split - exp).max()) <= tol * scale, (mode, float(np.abs(split - exp).max()) / scale)
         assert np.array_equal(split.argmax(-1), exp.argmax(-1)), mode
 

@@ -187,21 +187,21 @@ def test_decode_paths_bit_identical(model_path):
     """One-token steps through the fused decode kernels with the exact attention, replayed from a
     recorded graph, give the bits of the same steps run eagerly, with the MoE grouped on the host and
     through the unfused kernels (and these follow the oracle); the chunked attention (the default)
-    and the split one give the same bits replayed and eager, within tolerance of the exact chain; the
-    f16 cache gives the same bits fused and unfused."""
+    and the split one, with the prompt's flash attention, give the same bits replayed and eager,
+    within tolerance of the exact chain; the f16 cache gives the same bits fused and unfused."""
     model = LoadedModel(model_path)
     exact = {"SARDYNE_ATTENTION": "exact"}
     fused_graph = _decode_run(model, exact)
     fused_eager = _decode_run(model, {**exact, "SARDYNE_NO_GRAPH": "1"})
     host_moe = _decode_run(model, {**exact, "SARDYNE_NO_DEVICE_MOE": "1"})
-    unfused = _decode_run(model, {"SARDYNE_NO_FUSED_DECODE": "1"})
+    unfused = _decode_run(model, {**exact, "SARDYNE_NO_FUSED_DECODE": "1"})
     default = _decode_run(model, {})
     split_graph = _decode_run(model, {"SARDYNE_ATTENTION": "split"})
     split_eager = _decode_run(model, {"SARDYNE_ATTENTION": "split", "SARDYNE_NO_GRAPH": "1"})
     chunked_graph = _decode_run(model, {"SARDYNE_ATTENTION": "chunked"})
     chunked_eager = _decode_run(model, {"SARDYNE_ATTENTION": "chunked", "SARDYNE_NO_GRAPH": "1"})
     f16_graph = _decode_run(model, {"SARDYNE_ATTENTION": "exact", "SARDYNE_KV": "f16"})
-    f16_unfused = _decode_run(model, {"SARDYNE_KV": "f16", "SARDYNE_NO_FUSED_DECODE": "1"})
+    f16_unfused = _decode_run(model, {**exact, "SARDYNE_KV": "f16", "SARDYNE_NO_FUSED_DECODE": "1"})
     assert np.array_equal(fused_graph.view(np.uint32), fused_eager.view(np.uint32))
     assert np.array_equal(fused_graph.view(np.uint32), host_moe.view(np.uint32))
     assert np.array_equal(fused_graph.view(np.uint32), unfused.view(np.uint32))
@@ -243,15 +243,19 @@ def test_logits_bit_identical_to_reference(spec, tmp_path):
     exp = [ref.eval(toks[:70])] + [ref.eval([t]) for t in toks[70:100]]
     for i, (g, e) in enumerate(zip(got, exp)):
         assert np.array_equal(g.view(np.uint32), e.view(np.uint32)), (i, float(np.abs(g - e).max()))
-    # the split one-token attentions (SARDYNE_ATTENTION=split / chunked) within the reference tests'
-    # tolerance
+    # the split one-token attentions (SARDYNE_ATTENTION=split / chunked), with the prompt's flash
+    # attention, within the reference tests' tolerance. With a router, a rounding-level change can
+    # reorder two nearly tied experts of a token and every later position follows that token's
+    # other expert: those models are held to 1e-2 of the logit scale and 90 % of the greedy tokens,
+    # the bound the 30B-A3B-shaped test applies
+    moe = SPECS[spec].n_expert > 0
     for mode in ("split", "chunked"):
         with engine_env(SARDYNE_ATTENTION=mode):
             ctx = model.session(max_seq=128, n_batch=32)
         split = [ctx.feed(toks[:70])] + [ctx.feed([t]) for t in toks[70:100]]
-        assert np.array_equal(split[0].view(np.uint32), exp[0].view(np.uint32))  # the prompt: no decode step
-        assert_close(np.stack(split), np.stack(exp))
-        assert np.mean(np.stack(split).argmax(-1) == np.stack(exp).argmax(-1)) == 1.0, mode
+        assert_close(np.stack(split), np.stack(exp), tol=1e-2 if moe else 1e-4)
+        agree = np.mean(np.stack(split).argmax(-1) == np.stack(exp).argmax(-1))
+        assert agree >= (0.9 if moe else 1.0), (mode, agree)
 
 
 @pytest.mark.parametrize("spec", ["qwen2-kquant", "moe-128x8", "qwen2-kquant-v4k", "llama-kquant"])
@@ -276,7 +280,7 @@ def test_file_scales_logits_bit_identical(spec, tmp_path):
 def test_f16_kv_cache(spec, tmp_path):
     """The f16 KV cache (SARDYNE_KV=f16): with the exact attention, prefill and one-token logits have
     the bits of the oracle whose cache rounds every K/V value to f16 when it is written; the chunked
-    attention is within tolerance of it. Against the f32 cache the rounding is a real change: on these
+    attention (and the prompt's flash attention) is within tolerance of it. Against the f32 cache the rounding is a real change: on these
     random-weight models the oracle's own f16 and f32 caches differ by 0.6-2.4 % in relative L2 (up to
     7 % of the logit scale in one logit) with 97-100 % of the greedy tokens equal, so that comparison
     is held to 5 % relative L2 and 90 % agreement."""
@@ -295,7 +299,6 @@ def test_f16_kv_cache(spec, tmp_path):
         if mode == "exact":
             assert np.array_equal(got.view(np.uint32), exp16.view(np.uint32)), float(np.abs(got - exp16).max())
         else:
-            assert np.array_equal(got[0].view(np.uint32), exp16[0].view(np.uint32))
             assert_close(got, exp16)
         rel = float(np.linalg.norm(got - exp) / np.linalg.norm(exp))
         assert rel < 5e-2, (mode, rel)

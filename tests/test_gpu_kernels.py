@@ -842,6 +842,48 @@ def test_prefill_attention_tokens_bit_identical(n_head, n_kv_head, hd, n_tok, n_
             np.testing.assert_allclose(got[t, h * hd:(h + 1) * hd], exp, rtol=1e-4, atol=1e-5)
 
 
+@pytest.mark.parametrize("n_head,n_kv_head,hd", [(16, 2, 128), (32, 4, 128), (4, 2, 64), (4, 4, 64), (6, 2, 64)])
+@pytest.mark.parametrize("n_tok,n_kv0", [(16, 1), (40, 70), (77, 3), (512, 1), (100, 900)])
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+def test_prefill_attention_flash(n_head, n_kv_head, hd, n_tok, n_kv0, kv):
+    """The flash-form prompt attention (f32 matrix cores, eight waves per 32 queries over key tiles
+    of 32, merged in wave order) is within 1e-5 of the output scale of the reference's arithmetic
+    (sdy_attention, bit-exact with the oracle), for partial query blocks and key tiles, q rows at a
+    stride wider than the heads (the engine's q|k|v rows) and both cache types; it is deterministic."""
+    L = lib()
+    assert L.sdy_attention_flash_ok(n_head, n_kv_head, hd)
+    rng = np.random.default_rng(n_head * 7 + n_tok + n_kv0 + hd)
+    max_seq = n_kv0 + n_tok + 5
+    q_dim = n_head * hd
+    q_stride = q_dim + 2 * n_kv_head * hd
+    q = rng.standard_normal((n_tok, q_stride)).astype(np.float32)
+    ct = np.float16 if kv == "f16" else np.float32
+    kc = rng.standard_normal((n_kv_head, max_seq, hd)).astype(ct)
+    vc = rng.standard_normal((n_kv_head, max_seq, hd)).astype(ct)
+    kv_type = capi.KV_F16 if kv == "f16" else capi.KV_F32
+    dq, dk, dv = (capi.DeviceBuffer.from_array(a) for a in (q, kc, vc))
+    dpart = capi.DeviceBuffer(L.sdy_attn_scores_floats(n_tok, n_head, max_seq) * 4)
+    dexp, dgot = capi.DeviceBuffer(n_tok * q_dim * 4), capi.DeviceBuffer(n_tok * q_dim * 4)
+    capi.check(L.sdy_attention(dq.ptr, dk.ptr, dv.ptr, kv_type, n_tok, n_head, n_kv_head, hd, n_kv0, max_seq * hd,
+                               q_stride, dpart.ptr, dexp.ptr, q_dim, None))
+    exp = dexp.to_array(np.float32, (n_tok, q_dim))
+    outs = []
+    for _ in range(2):
+        capi.check(L.sdy_attention_flash(dq.ptr, dk.ptr, dv.ptr, kv_type, n_tok, n_head, n_kv_head, hd, n_kv0,
+                                         max_seq * hd, q_stride, dgot.ptr, q_dim, None))
+        outs.append(dgot.to_array(np.float32, (n_tok, q_dim)))
+    assert np.array_equal(bits(outs[0]), bits(outs[1]))
+    np.testing.assert_allclose(outs[0], exp, rtol=0, atol=1e-5 * float(np.abs(exp).max()))
+
+
+def test_prefill_attention_flash_rejects_layouts():
+    """head_dim other than 64 / 128, GQA groups that do not divide, unaligned q rows: an error, no launch."""
+    L = lib()
+    assert not L.sdy_attention_flash_ok(4, 2, 32) and not L.sdy_attention_flash_ok(6, 4, 64)
+    assert L.sdy_attention_flash(None, None, None, capi.KV_F32, 4, 4, 2, 32, 1, 64, 128, None, 128, None) != 0
+    assert L.sdy_attention_flash(None, None, None, capi.KV_F32, 4, 4, 2, 64, 1, 64, 258, None, 256, None) != 0
+
+
 @pytest.mark.parametrize("n_head,n_kv_head,hd,qk_norm", [(16, 2, 128, False), (32, 4, 128, True), (6, 2, 64, False)])
 @pytest.mark.parametrize("pos", [0, 15, 16, 1000, 2047, 2048, 2110])
 @pytest.mark.parametrize("kv", ["f32", "f16"])
