@@ -366,14 +366,102 @@ extern "C" int sdy_moe_combine(const float *y, const int32_t *top, const float *
     return sdy_check_launch("moe_combine");
 }
 
-// The routed (token, slot) pairs grouped by expert for the grouped GEMM: a stable counting sort of
-// the n = n_tok * k expert ids in top (the reference groups a batch's tokens per expert the same
-// way, csrc/model_llama.c:676-700). Sorted row r holds pair out_row[r] = t * k + s, of token
+// The routed (token, slot) pairs grouped by expert for the grouped GEMM: a stable sort of the
+// n = n_tok * k expert ids in top (the reference groups a batch's tokens per expert the same way,
+// csrc/model_llama.c:676-700). Sorted row r holds pair out_row[r] = t * k + s, of token
 // src_tok[r] = t; rows grp_tok[e] .. grp_tok[e + 1] - 1 are expert e's, in (t, s) order;
-// grp_tile[e] is the number of bn-row tiles of the experts before e. One workgroup: SORT_SEG
-// threads count, then place, the pairs of their segment of the list; per (segment, expert) counts
-// in LDS make the placement stable.
+// grp_tile[e] is the number of bn-row tiles of the experts before e.
+//
+// k_moe_sort_rank (when its per-chunk counts fit in LDS): one workgroup of 16 waves. The list is cut
+// into chunks of 64 pairs (one per lane); in a chunk, the lanes holding the same expert are found
+// with one ballot per bit of the expert id, so a pair's rank among them is a popcount of the lower
+// lanes. Each chunk's count per expert goes to LDS; one thread per expert turns its column into
+// offsets over the chunks (in chunk order), the experts' first rows and tile offsets are exclusive
+// scans, and each pair lands at its expert's first row + its chunk's offset + its rank.
+// k_moe_sort (lists whose chunk counts do not fit): SORT_SEG threads count, then place, the pairs of
+// their segment of the list; per (segment, expert) counts in LDS make the placement stable.
 constexpr int SORT_SEG = 64;
+constexpr int SORT_RANK_LDS = 128 * 1024;  // bytes of per-chunk counts k_moe_sort_rank may use
+
+__global__ __launch_bounds__(1024) void k_moe_sort_rank(const int32_t *top, int n, int k, int ne, int bn,
+                                                        int *grp_tok, int *grp_tile, int32_t *src_tok,
+                                                        int32_t *out_row) {
+    extern __shared__ uint16_t ccnt[];  // [n_chunk][ne]: counts, then offsets within the expert
+    __shared__ int first[513];          // each expert's first row, [ne] = n
+    __shared__ int wsum[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n_chunk = (n + 63) >> 6;
+    for (int i = tid; i < n_chunk * ne; i += 1024) ccnt[i] = 0;
+    __syncthreads();
+    // lanes of the wave holding the same expert (ids up to 511; past the list: the id ne)
+    auto peers = [&](int e) {
+        uint64_t m = ~0ull;
+#pragma unroll
+        for (int b = 0; b < 10; b++) {
+            const uint64_t v = __ballot((e >> b) & 1);
+            m &= ((e >> b) & 1) ? v : ~v;
+        }
+        return m;
+    };
+    auto expert_of = [&](int i) {
+        if (i >= n) return ne;
+        const int e = top[i];
+        return e < 0 ? 0 : e >= ne ? ne - 1 : e;
+    };
+    const uint64_t below = (1ull << lane) - 1;  // lanes under this one
+    for (int c = wave; c < n_chunk; c += 16) {
+        const int i = 64 * c + lane, e = expert_of(i);
+        const uint64_t m = peers(e);
+        if (e < ne && (m & below) == 0) ccnt[c * ne + e] = (uint16_t)__popcll(m);
+    }
+    __syncthreads();
+    for (int e = tid; e < ne; e += 1024) {  // chunk offsets within the expert, in chunk order
+        int run = 0;
+        for (int c = 0; c < n_chunk; c++) {
+            const int v = ccnt[c * ne + e];
+            ccnt[c * ne + e] = (uint16_t)run;
+            run += v;
+        }
+        first[e] = run;  // the expert's total, for now
+    }
+    __syncthreads();
+    // experts' first rows and tile offsets: exclusive scans over the experts (ne <= 512: waves 0-7)
+    const int cnt_e = tid < ne ? first[tid] : 0, tiles = (cnt_e + bn - 1) / bn;
+    int inc_r = cnt_e, inc_t = tiles;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int vr = __shfl_up(inc_r, off), vt = __shfl_up(inc_t, off);
+        if (lane >= off) {
+            inc_r += vr;
+            inc_t += vt;
+        }
+    }
+    if (lane == 63) wsum[wave] = inc_r;
+    __syncthreads();
+    int before_r = 0;
+    for (int w = 0; w < wave; w++) before_r += wsum[w];
+    __syncthreads();
+    if (lane == 63) wsum[wave] = inc_t;
+    __syncthreads();
+    int before_t = 0;
+    for (int w = 0; w < wave; w++) before_t += wsum[w];
+    __syncthreads();  // every thread has read the totals of the experts' counts
+    if (tid <= ne) {
+        const int row = before_r + inc_r - cnt_e;  // (tid == ne: cnt_e = 0, the total n)
+        first[tid] = row;
+        grp_tok[tid] = row;
+        grp_tile[tid] = before_t + inc_t - tiles;
+    }
+    __syncthreads();
+    for (int c = wave; c < n_chunk; c += 16) {
+        const int i = 64 * c + lane, e = expert_of(i);
+        const uint64_t m = peers(e);
+        if (e < ne) {
+            const int r = first[e] + ccnt[c * ne + e] + __popcll(m & below);
+            src_tok[r] = i / k;
+            out_row[r] = i;
+        }
+    }
+}
 
 __global__ __launch_bounds__(256) void k_moe_sort(const int32_t *top, int n, int k, int ne, int bn, int *grp_tok,
                                                   int *grp_tile, int32_t *src_tok, int32_t *out_row) {
@@ -431,11 +519,22 @@ extern "C" int sdy_moe_sort(const int32_t *top, int n_tok, int k, int n_expert, 
                             int32_t *src_tok, int32_t *out_row, sdy_stream s) {
     if (n_expert < 1 || n_expert > 512 || k < 1 || n_tok < 1 || bn < 1)
         return sdy_fail(-1, "moe_sort: %d tokens x %d of %d experts (at most 512), tiles of %d", n_tok, k, n_expert, bn);
+    const int n = n_tok * k;
+    int rc;
+    const size_t rank_lds = sizeof(uint16_t) * (size_t)((n + 63) / 64) * n_expert;
+    if (rank_lds <= SORT_RANK_LDS && n <= 65535) {
+        static size_t granted_rank = 0;
+        if ((rc = sdy_lds_limit((const void *)k_moe_sort_rank, rank_lds, &granted_rank))) return rc;
+        SDY_NOTE_KERNEL(k_moe_sort_rank);
+        hipLaunchKernelGGL(k_moe_sort_rank, dim3(1), dim3(1024), rank_lds, (hipStream_t)s, top, n, k, n_expert, bn,
+                           grp_tok, grp_tile, src_tok, out_row);
+        return sdy_check_launch("moe_sort");
+    }
     const size_t lds = sizeof(int) * ((size_t)SORT_SEG * n_expert + n_expert + 1);
     static size_t granted = 0;
-    int rc = sdy_lds_limit((const void *)k_moe_sort, lds, &granted);
-    if (rc) return rc;
-    hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(256), lds, (hipStream_t)s, top, n_tok * k, k, n_expert, bn, grp_tok,
+    if ((rc = sdy_lds_limit((const void *)k_moe_sort, lds, &granted))) return rc;
+    SDY_NOTE_KERNEL(k_moe_sort);
+    hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(256), lds, (hipStream_t)s, top, n, k, n_expert, bn, grp_tok,
                        grp_tile, src_tok, out_row);
     return sdy_check_launch("moe_sort");
 }

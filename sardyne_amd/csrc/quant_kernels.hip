@@ -1538,6 +1538,135 @@ __global__ __launch_bounds__(THREADS) void k_matvec_float_block(const uint8_t *_
     if (l == 0) float_store<WT>(float_tail<WT>(wr, xr, n_in, sum), row, t, out, out_stride, bias, resid);
 }
 
+// block_2x4's order for many rows and tokens (the MoE router over a prompt's tokens): a workgroup of
+// 32 groups of 8 lanes owns 16 rows x 16 tokens; group g computes the 2 x 4 (row, token) pairs of
+// rows 2 (g / 4) + {0, 1}, tokens 4 (g % 4) + {0..3}, lane l carrying chain l (elements l, l + 8, ...
+// in order) of all eight, from row and token tiles of FT_K elements staged in LDS (as f32) that the
+// whole workgroup shares, the next tile's loads in flight while the current one is multiplied. In
+// LDS a row's chain l is contiguous (element 8 s + l at [row][l][s]), so a lane reads four steps of
+// a row with one 16-byte read. The chains, the hsum tree and the tail are k_matvec_float_block's,
+// so the bits are the same; an element is read from memory once per workgroup instead of once per
+// pair.
+typedef float ft_f32x4 __attribute__((ext_vector_type(4)));
+constexpr int FT_ROWS = 16, FT_TOKS = 16, FT_K = 256;
+constexpr int FT_SP = FT_K / 8 + 4;  // floats per (row, chain) in LDS: the 8 chains' 16-byte reads in distinct banks
+
+template <int WT>
+__global__ __launch_bounds__(256) void k_matvec_float_tile(const uint8_t *__restrict__ w, int n_in,
+                                                          const float *__restrict__ x, int n_tok, float *out,
+                                                          long out_stride, const float *bias, const float *resid,
+                                                          long row0, long row1) {
+    constexpr int NTH = 256, NW = FT_ROWS * FT_K / NTH / 4, NX = FT_TOKS * FT_K / NTH / 4;  // 4-element loads
+    __shared__ __align__(16) float ws[FT_ROWS * 8 * FT_SP], xs[FT_TOKS * 8 * FT_SP];
+    const int tid = threadIdx.x, l = tid & 7, g = tid >> 3, rb = g >> 2, tb = g & 3;
+    const int base = (tid & 63) & 56;
+    const long n_pr = (row1 - row0) & ~1L;
+    const int n_gt = n_tok & ~3;
+    const long r_tile = row0 + (long)blockIdx.y * FT_ROWS;
+    const int t_tile = blockIdx.x * FT_TOKS;
+    const int n8 = n_in & ~7;
+    float acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = 0.0f;
+    // a chunk's elements in 4-element loads, all requested before any is used (elements i .. i + 3,
+    // i = 4 (tid + u NTH): row i / FT_K of the tile, columns i % FT_K ...; clamped rows and columns
+    // past the chunk read in bounds; kn is a multiple of 8, so a load is wholly in or out)
+    ft_f32x4 wv[NW], xv[NX];
+    auto fetch = [&](int k0, int kn) {
+#pragma unroll
+        for (int u = 0; u < NW; u++) {
+            const int i = 4 * (tid + u * NTH), r = i / FT_K, e = i - r * FT_K;
+            const long row = r_tile + r < row0 + n_pr ? r_tile + r : row0;
+            const size_t o = (size_t)row * n_in + k0 + (e < kn ? e : 0);
+            if constexpr (WT == SDY_F32) {
+                wv[u] = *reinterpret_cast<const ft_f32x4 *>(reinterpret_cast<const float *>(w) + o);
+            } else {
+                const uint2 h = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(w) + o);
+                const uint16_t hv[4] = {(uint16_t)(h.x & 0xFFFFu), (uint16_t)(h.x >> 16), (uint16_t)(h.y & 0xFFFFu),
+                                        (uint16_t)(h.y >> 16)};
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    wv[u][c] = WT == SDY_F16 ? sdy_h2f(hv[c]) : __uint_as_float((uint32_t)hv[c] << 16);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NX; u++) {
+            const int i = 4 * (tid + u * NTH), t = i / FT_K, e = i - t * FT_K;
+            const int tk = t_tile + t < n_gt ? t_tile + t : 0;
+            xv[u] = *reinterpret_cast<const ft_f32x4 *>(x + (size_t)tk * n_in + k0 + (e < kn ? e : 0));
+        }
+    };
+    const float *wr = ws + (2 * rb * 8 + l) * FT_SP, *xr = xs + (4 * tb * 8 + l) * FT_SP;
+    // steps 4 q .. 4 q + 3 of the lane's chain (elements 8 (4q + c) + l)
+    auto step4 = [&](int q) {
+        ft_f32x4 a[2], b[4];
+#pragma unroll
+        for (int i = 0; i < 2; i++) a[i] = *reinterpret_cast<const ft_f32x4 *>(wr + i * 8 * FT_SP + 4 * q);
+#pragma unroll
+        for (int j = 0; j < 4; j++) b[j] = *reinterpret_cast<const ft_f32x4 *>(xr + j * 8 * FT_SP + 4 * q);
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = fmaf(a[i][c], b[j][c], acc[i][j]);
+    };
+    auto step1 = [&](int st) {  // one step (a chunk's last steps, when they are not a multiple of 4)
+        float a[2], b[4];
+#pragma unroll
+        for (int i = 0; i < 2; i++) a[i] = wr[i * 8 * FT_SP + st];
+#pragma unroll
+        for (int j = 0; j < 4; j++) b[j] = xr[j * 8 * FT_SP + st];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    };
+    if (n8 > 0) fetch(0, n8 < FT_K ? n8 : FT_K);
+    for (int k0 = 0; k0 < n8; k0 += FT_K) {
+        const int kn = n8 - k0 < FT_K ? n8 - k0 : FT_K;  // a multiple of 8
+        __syncthreads();  // the previous chunk's reads are done
+#pragma unroll
+        for (int u = 0; u < NW; u++) {
+            const int i = 4 * (tid + u * NTH), r = i / FT_K, e = i - r * FT_K;
+#pragma unroll
+            for (int c = 0; c < 4; c++) ws[(r * 8 + ((e + c) & 7)) * FT_SP + (e >> 3)] = wv[u][c];
+        }
+#pragma unroll
+        for (int u = 0; u < NX; u++) {
+            const int i = 4 * (tid + u * NTH), t = i / FT_K, e = i - t * FT_K;
+#pragma unroll
+            for (int c = 0; c < 4; c++) xs[(t * 8 + ((e + c) & 7)) * FT_SP + (e >> 3)] = xv[u][c];
+        }
+        __syncthreads();
+        if (k0 + FT_K < n8) fetch(k0 + FT_K, n8 - k0 - FT_K < FT_K ? n8 - k0 - FT_K : FT_K);
+        const int ns = kn >> 3;  // steps of the chunk
+        if (ns == FT_K / 8) {
+#pragma unroll
+            for (int q = 0; q < FT_K / 32; q++) step4(q);
+        } else {
+            int st = 0;
+            for (; st + 4 <= ns; st += 4) step4(st >> 2);
+            for (; st < ns; st++) step1(st);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float sum = hsum8_group(acc[i][j], base);
+            const long row = r_tile + 2 * rb + i;
+            const int t = t_tile + 4 * tb + j;
+            if (l == 0 && row < row0 + n_pr && t < n_gt) {
+                const uint8_t *wrow = w + (size_t)row * n_in * (WT == SDY_F32 ? 4 : 2);
+                float_store<WT>(float_tail<WT>(wrow, x + (size_t)t * n_in, n_in, sum), row, t, out, out_stride, bias,
+                                resid);
+            }
+        }
+}
+
 }  // namespace
 
 // =============================================================================== host launchers
@@ -2474,7 +2603,23 @@ extern "C" int sdy_matvec_float(int wtype, const void *w, int n_in, const sdy_mv
             hipLaunchKernelGGL(KERNEL<SDY_BF16>, grid, dim3(THREADS), 0, st, wp, n_in, a->x, n_tok, a->out,           \
                                a->out_stride, a->bias, a->resid, a->row0, a->row1);                                  \
     }
-    SDY_FLOAT_LAUNCH(k_matvec_float_block, n_block, 8)
+    if (n_pr >= FT_ROWS && n_gt >= FT_TOKS && n_in % 4 == 0 && ((uintptr_t)wp & 15) == 0 &&
+        ((uintptr_t)a->x & 15) == 0) {
+        // many rows and tokens: the block-order pairs from tiles staged in LDS (4-element loads)
+        const dim3 grid((unsigned)((n_gt + FT_TOKS - 1) / FT_TOKS), (unsigned)((n_pr + FT_ROWS - 1) / FT_ROWS));
+        const dim3 block(256);
+        if (wtype == SDY_F32)
+            hipLaunchKernelGGL(k_matvec_float_tile<SDY_F32>, grid, block, 0, st, wp, n_in, a->x, n_tok, a->out,
+                               a->out_stride, a->bias, a->resid, a->row0, a->row1);
+        else if (wtype == SDY_F16)
+            hipLaunchKernelGGL(k_matvec_float_tile<SDY_F16>, grid, block, 0, st, wp, n_in, a->x, n_tok, a->out,
+                               a->out_stride, a->bias, a->resid, a->row0, a->row1);
+        else
+            hipLaunchKernelGGL(k_matvec_float_tile<SDY_BF16>, grid, block, 0, st, wp, n_in, a->x, n_tok, a->out,
+                               a->out_stride, a->bias, a->resid, a->row0, a->row1);
+    } else {
+        SDY_FLOAT_LAUNCH(k_matvec_float_block, n_block, 8)
+    }
     SDY_FLOAT_LAUNCH(k_matvec_float_dot, n_dot, 2)
 #undef SDY_FLOAT_LAUNCH
     return sdy_check_launch("matvec_float");

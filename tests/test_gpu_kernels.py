@@ -717,11 +717,13 @@ def test_grouped_matvec_rejects_bad_shapes():
 @pytest.mark.parametrize("wtype", [O.F32, O.F16, O.BF16], ids=["f32", "f16", "bf16"])
 @pytest.mark.parametrize("n_in,n_out,n_tok,r0,r1", [(2048, 128, 1, 0, 128), (2340, 45, 9, 0, 45),
                                                   (67, 45, 4, 3, 42), (768, 33, 17, 0, 33), (96, 10, 3, 1, 10),
-                                                  (2048, 128, 1024, 0, 128)])
+                                                  (2048, 128, 1024, 0, 128), (2048, 128, 512, 0, 128),
+                                                  (2340, 45, 37, 0, 45), (300, 35, 19, 1, 34), (16, 16, 16, 0, 16)])
 def test_float_matmul_reference_order_bit_exact(wtype, n_in, n_out, n_tok, r0, r1):
     """F32/F16/BF16 weights (the MoE router) in the reference's AVX2 order: block_2x4 for paired
     rows x groups of four tokens, dot for the rest, with the hsum tree and the scalar tail; the
-    bits of the oracle's restatement of csrc/ops_avx2.c."""
+    bits of the oracle's restatement of csrc/ops_avx2.c. Blocks of at least 16 rows and tokens run
+    on the LDS-tiled kernel (partial tiles and a partial last 256-element chunk included)."""
     rng = np.random.default_rng(n_in + n_tok + r0)
     x = rng.standard_normal((n_tok, n_in)).astype(np.float32)
     w32 = (rng.standard_normal((n_out, n_in)) * 0.02).astype(np.float32)
@@ -1394,6 +1396,35 @@ def test_pipelined_upload_equals_synchronous(kind, n_in, grp, n_grp, bad_scale):
     finally:
         for m in mats:
             L.sdy_mat_free(ctypes.byref(m))
+
+
+@pytest.mark.parametrize("n_tok,k,n_exp,bn", [(1, 1, 1, 32), (3, 2, 8, 32), (512, 8, 128, 32), (700, 6, 60, 32),
+                                            (2048, 8, 128, 32), (2100, 8, 512, 16), (333, 4, 512, 64)])
+def test_moe_sort_stable_grouping(n_tok, k, n_exp, bn):
+    """The expert sort against numpy's stable argsort of the expert ids: rows grouped by expert in
+    (token, slot) order, each expert's first row and tile offset (tiles of bn rows), for the
+    in-LDS sorting network (up to 16384 pairs) and the segmented counting sort beyond it; skewed
+    routings (a few experts take most pairs, some none) included."""
+    L = lib()
+    rng = np.random.default_rng(n_tok * 31 + n_exp)
+    hot = rng.choice(n_exp, max(1, n_exp // 8), replace=False)
+    top = np.empty((n_tok, k), np.int32)
+    for t in range(n_tok):
+        pool = hot if rng.random() < 0.5 and len(hot) >= k else np.arange(n_exp)
+        top[t] = rng.choice(pool, k, replace=False) if len(pool) >= k else rng.choice(pool, k)
+    n = n_tok * k
+    dtop = capi.DeviceBuffer.from_array(top)
+    grp_tok, grp_tile = capi.DeviceBuffer(4 * (n_exp + 1)), capi.DeviceBuffer(4 * (n_exp + 1))
+    src, orow = capi.DeviceBuffer(4 * n), capi.DeviceBuffer(4 * n)
+    capi.check(L.sdy_moe_sort(dtop.ptr, n_tok, k, n_exp, bn, grp_tok.ptr, grp_tile.ptr, src.ptr, orow.ptr, None))
+    flat = top.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    counts = np.bincount(flat, minlength=n_exp)
+    assert np.array_equal(orow.to_array(np.int32, n), order)
+    assert np.array_equal(src.to_array(np.int32, n), order // k)
+    assert np.array_equal(grp_tok.to_array(np.int32, n_exp + 1), np.concatenate([[0], np.cumsum(counts)]))
+    tiles = (counts + bn - 1) // bn
+    assert np.array_equal(grp_tile.to_array(np.int32, n_exp + 1), np.concatenate([[0], np.cumsum(tiles)]))
 
 
 @pytest.mark.parametrize("kind,n_in,rows,n_exp,n_tok,k", [("Q4_K", 512, 96, 8, 45, 3), ("Q6_K", 768, 64, 16, 70, 4),
