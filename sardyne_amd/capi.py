@@ -195,7 +195,7 @@ _DEVICE_SIGNATURES = {
     "sdy_gemm_ws_bytes": (_sz, [_int, _int]),
     "sdy_gemm": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp, _vp]),
     "sdy_gemm_grouped_tile": (_int, []),
-    "sdy_gemm_grouped": (_int, [ctypes.POINTER(SdyMat), ctypes.c_long, _int, _vp, _vp, _vp,
+    "sdy_gemm_grouped": (_int, [ctypes.POINTER(SdyMat), ctypes.c_long, _int, _vp, _vp, _vp, _vp, _int,
                                 ctypes.POINTER(SdyMvArgs), _vp, _vp]),
     "sdy_moe_sort": (_int, [_vp, _int, _int, _int, _int, _vp, _vp, _vp, _vp, _vp]),
     "sdy_gather_rows": (_int, [_vp, _vp, _int, _int, _vp, _vp]),

@@ -353,10 +353,9 @@ static int moe_grouped(engine_ctx *c, const dlayer *L, int n) {
     TRY(sdy_moe_route(c->moe_probs, n, ne, k, c->moe_top, c->moe_w, c->st));
     TRY(sdy_moe_sort(c->moe_top, n, k, ne, sdy_gemm_grouped_tile(), c->moe_grp_tok, c->moe_grp_tile, c->moe_src,
                      c->moe_orow, c->st));
-    TRY(sdy_gather_rows(c->xb, c->moe_src, R, dim, c->moe_x, c->st));
-    xq_forget(c); /* xq[1] and the GEMM workspace now hold the routed rows */
+    xq_forget(c); /* xq[1] and the GEMM workspace now hold the n normalised rows */
     c->gemm_ready = 0;
-    TRY(sdy_quantize_gemm(c->moe_x, c->xq[1], dim, R, c->gemm_ws, c->st));
+    TRY(sdy_quantize_gemm(c->xb, c->xq[1], dim, n, c->gemm_ws, c->st));
     sdy_mv_args a;
     memset(&a, 0, sizeof a);
     a.xq = c->xq[1];
@@ -365,12 +364,15 @@ static int moe_grouped(engine_ctx *c, const dlayer *L, int n) {
     a.out_stride = fe;
     a.epilogue = SDY_EPI_SWIGLU;
     a.ws_ready = 1;
-    TRY(sdy_gemm_grouped(&L->gate_up.m, 2L * fe, ne, c->moe_grp_tok, c->moe_grp_tile, NULL, &a, c->gemm_ws, c->st));
+    /* sorted row r reads token moe_src[r]'s row: no gathered copy of the routed rows */
+    TRY(sdy_gemm_grouped(&L->gate_up.m, 2L * fe, ne, c->moe_grp_tok, c->moe_grp_tile, NULL, c->moe_src, n, &a,
+                         c->gemm_ws, c->st));
     TRY(sdy_quantize_gemm(c->hb, c->xq[1], fe, R, c->gemm_ws, c->st));
     a.out = c->moe_y;
     a.out_stride = dim;
     a.epilogue = SDY_EPI_NONE;
-    TRY(sdy_gemm_grouped(&L->down.m, dim, ne, c->moe_grp_tok, c->moe_grp_tile, c->moe_orow, &a, c->gemm_ws, c->st));
+    TRY(sdy_gemm_grouped(&L->down.m, dim, ne, c->moe_grp_tok, c->moe_grp_tile, c->moe_orow, NULL, 0, &a, c->gemm_ws,
+                         c->st));
     xq_forget(c);
     return sdy_moe_combine(c->moe_y, c->moe_top, c->moe_w, n, k, dim, c->x, c->x, c->st);
 }

@@ -53,6 +53,7 @@ struct GemmArgs {
     // - 1; its token tiles are grp_tile[e] .. grp_tile[e + 1] - 1 of the grid. out_row (or null)
     // sends activation row t's outputs to output row out_row[t].
     const int *grp_tile, *grp_tok, *out_row;
+    const int *act_row;  // or null: the activation (expansion) row of row t of the tile
     long grp_rows;
     int n_grp;
     int wide;  // host-side: the wide variant is needed (k_gemm3 only)
@@ -217,6 +218,15 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
     }
     const int nb = g.nb;
     auto tok_of = [&](int t) { return t0 + t < t_end ? t0 + t : t_end - 1; };
+    // the expansion rows the stages read: this lane's rows of the tile, looked up once
+    auto act_of = [&](int t) { return g.act_row ? g.act_row[tok_of(t)] : tok_of(t); };
+    int ar_st[NI], ar_yd[YDN / 64], ar_bs[BN / 32 > 0 ? BN / 32 : 1];
+#pragma unroll
+    for (int j = 0; j < NI; j++) ar_st[j] = act_of(((j * WM + wave) * 64 + lane) >> 5);
+#pragma unroll
+    for (int i = 0; i < YDN / 64; i++) ar_yd[i] = act_of(64 * i + lane);
+#pragma unroll
+    for (int i = 0; i < BN / 32; i++) ar_bs[i] = act_of(32 * i + (lane >> 1));
 
     // weight buffer resources and this lane's per-row offsets
     __amdgpu_buffer_rsrc_t rq[3], rh, rd;
@@ -254,13 +264,13 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
         for (int j = 0; j < NI; j++) {
             const int blk = j * WM + wave;  // 64-chunk block written by this wave instruction
             const int p = blk * 64 + lane, t = p >> 5, c = (p & 31) ^ (t & 7);
-            __builtin_amdgcn_global_load_lds((const void *)(g.y16 + (size_t)tok_of(t) * g.n_in + 256 * sb + 8 * c),
+            __builtin_amdgcn_global_load_lds((const void *)(g.y16 + (size_t)ar_st[j] * g.n_in + 256 * sb + 8 * c),
                                              (lds_ptr_t)(base + blk * 1024), 16, 0, 0);
         }
         if (wave == 0) {
 #pragma unroll
             for (int i = 0; i < YDN / 64; i++)
-                __builtin_amdgcn_global_load_lds((const void *)(g.yd + (size_t)tok_of(64 * i + lane) * nb + sb),
+                __builtin_amdgcn_global_load_lds((const void *)(g.yd + (size_t)ar_yd[i] * nb + sb),
                                                  (lds_ptr_t)(base + YDOFF + 256 * i), 4, 0, 0);
         }
         if constexpr (WT == SDY_Q4_K) {
@@ -268,7 +278,7 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
 #pragma unroll
                 for (int i = 0; i < BN / 32; i++)
                     __builtin_amdgcn_global_load_lds(
-                        (const void *)(g.bs16 + ((size_t)tok_of(32 * i + (lane >> 1)) * nb + sb) * 16 + 8 * (lane & 1)),
+                        (const void *)(g.bs16 + ((size_t)ar_bs[i] * nb + sb) * 16 + 8 * (lane & 1)),
                         (lds_ptr_t)(base + BSOFF + 1024 * i), 16, 0, 0);
             }
         }
@@ -723,7 +733,8 @@ extern "C" int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_st
 extern "C" int sdy_gemm_grouped_tile(void) { return 32; }
 
 extern "C" int sdy_gemm_grouped(const sdy_mat *m, long grp_rows, int n_grp, const int *grp_tok, const int *grp_tile,
-                                const int *out_row, const sdy_mv_args *a, void *ws, sdy_stream s) {
+                                const int *out_row, const int *act_row, int n_act, const sdy_mv_args *a, void *ws,
+                                sdy_stream s) {
     hipStream_t st = (hipStream_t)s;
     const int n_tok = a->n_tok;
     if (n_tok <= 0) return 0;
@@ -734,8 +745,11 @@ extern "C" int sdy_gemm_grouped(const sdy_mat *m, long grp_rows, int n_grp, cons
         return sdy_fail(-1, "gemm_grouped: %d groups of %ld rows in %ld rows", n_grp, grp_rows, m->n_rows);
     if (a->bias || a->resid || (a->epilogue == SDY_EPI_SWIGLU && (grp_rows & 1)))
         return sdy_fail(-1, "gemm_grouped: no bias or residual; the SwiGLU epilogue needs an even row count per group");
+    if (act_row && (!a->ws_ready || n_act < 1))
+        return sdy_fail(-1, "gemm_grouped: activation rows by index read an expansion of n_act >= 1 rows that the "
+                            "caller made (ws_ready)");
     GemmArgs g = gemm_args(m);
-    const SdyGemmExp e = sdy_gemm_exp(ws, n_tok, g.n_in);
+    const SdyGemmExp e = sdy_gemm_exp(ws, act_row ? n_act : n_tok, g.n_in);
     g.y16 = e.y16;
     g.yd = e.yd;
     g.bs16 = e.bs16;
@@ -758,6 +772,7 @@ extern "C" int sdy_gemm_grouped(const sdy_mat *m, long grp_rows, int n_grp, cons
     g.grp_tile = grp_tile;
     g.grp_tok = grp_tok;
     g.out_row = out_row;
+    g.act_row = act_row;
     g.grp_rows = grp_rows;
     g.n_grp = n_grp;
     // token tiles: at most one partial tile per group beyond the full ones (the grid's extra

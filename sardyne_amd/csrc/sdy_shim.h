@@ -159,14 +159,17 @@ int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_stream s);
 int sdy_quantize_gemm(const float *x, void *xq, int n_in, int n_tok, void *ws, sdy_stream s);
 int sdy_norm_quant_gemm(const float *x, const float *w, float eps, int n, int n_rows, float *xb, void *xq, void *ws,
                         sdy_stream s);
-/* The GEMM over routed experts in one launch: m stacks n_grp experts of grp_rows rows; activation
- * rows grp_tok[e] .. grp_tok[e + 1] - 1 (Q8_K in a->xq, a->n_tok rows in all) multiply expert e,
- * and the results of row t go to output row out_row[t] (or t). grp_tile: the tiles of
- * sdy_gemm_grouped_tile() rows per expert, as sdy_moe_sort writes them. a->epilogue may be SwiGLU
- * (even grp_rows); no bias or residual. The same bits as sdy_gemm per expert. */
+/* The GEMM over routed experts in one launch: m stacks n_grp experts of grp_rows rows; rows
+ * grp_tok[e] .. grp_tok[e + 1] - 1 (a->n_tok rows in all) multiply expert e, and the results of row
+ * t go to output row out_row[t] (or t). Row t's activations are row act_row[t] (or t) of the
+ * quantised input (Q8_K in a->xq); with act_row the caller has made the expansion of those n_act
+ * rows in ws (sdy_quantize_gemm, a->ws_ready = 1), so the routed rows need no gathered copy. grp_tile: the
+ * tiles of sdy_gemm_grouped_tile() rows per expert, as sdy_moe_sort writes them. a->epilogue may be
+ * SwiGLU (even grp_rows); no bias or residual. The same bits as sdy_gemm per expert. */
 int sdy_gemm_grouped_tile(void);
 int sdy_gemm_grouped(const sdy_mat *m, long grp_rows, int n_grp, const int *grp_tok, const int *grp_tile,
-                     const int *out_row, const sdy_mv_args *a, void *ws, sdy_stream s);
+                     const int *out_row, const int *act_row, int n_act, const sdy_mv_args *a, void *ws,
+                     sdy_stream s);
 /* Variant check of rows [r0, r0 + n) of m for the GEMM: *bad_host = 1 when some row has a block
  * that only the wide variant multiplies exactly. */
 int sdy_gemm_check_rows(const sdy_mat *m, long r0, long n, int *bad_host, sdy_stream s);

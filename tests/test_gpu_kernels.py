@@ -1468,15 +1468,27 @@ def test_moe_sort_and_grouped_gemm_equal_per_expert_gemm(kind, n_in, rows, n_exp
     # plain rows scattered back to (token, slot) order
     out = capi.DeviceBuffer.from_array(np.full((R, rows), np.nan, np.float32))
     a = capi.SdyMvArgs(xq=xq.ptr, n_tok=R, out=out.ptr, out_stride=rows, ws_ready=1)
-    capi.check(L.sdy_gemm_grouped(ctypes.byref(m.m), rows, n_exp, grp_tok.ptr, grp_tile.ptr, orow.ptr,
+    capi.check(L.sdy_gemm_grouped(ctypes.byref(m.m), rows, n_exp, grp_tok.ptr, grp_tile.ptr, orow.ptr, None, 0,
                                   ctypes.byref(a), ws.ptr, None))
     got = out.to_array(np.float32, (R, rows))
     exp = np.stack([ref[i // k, flat[i] * rows:(flat[i] + 1) * rows] for i in range(R)])
     assert np.array_equal(bits(got), bits(exp))
+    # the same rows read by index from the n_tok token rows, quantised once (no gathered copy)
+    xq1 = capi.DeviceBuffer(n_tok * O.row_size(O.Q8_K, n_in))
+    ws1 = capi.DeviceBuffer(L.sdy_gemm_ws_bytes(n_tok, n_in))
+    capi.check(L.sdy_quantize_gemm(dx.ptr, xq1.ptr, n_in, n_tok, ws1.ptr, None))
+    out1 = capi.DeviceBuffer.from_array(np.full((R, rows), np.nan, np.float32))
+    a1 = capi.SdyMvArgs(xq=xq1.ptr, n_tok=R, out=out1.ptr, out_stride=rows, ws_ready=1)
+    capi.check(L.sdy_gemm_grouped(ctypes.byref(m.m), rows, n_exp, grp_tok.ptr, grp_tile.ptr, orow.ptr, src.ptr, n_tok,
+                                  ctypes.byref(a1), ws1.ptr, None))
+    assert np.array_equal(bits(out1.to_array(np.float32, (R, rows))), bits(exp))
+    a1.ws_ready = 0  # an index needs the caller's expansion
+    assert L.sdy_gemm_grouped(ctypes.byref(m.m), rows, n_exp, grp_tok.ptr, grp_tile.ptr, orow.ptr, src.ptr, n_tok,
+                              ctypes.byref(a1), ws1.ptr, None) != 0
     # SwiGLU pairs (rows 2i, 2i+1 of each expert), outputs in sorted order
     sw = capi.DeviceBuffer.from_array(np.full((R, rows // 2), np.nan, np.float32))
     a = capi.SdyMvArgs(xq=xq.ptr, n_tok=R, out=sw.ptr, out_stride=rows // 2, ws_ready=1, epilogue=capi.EPI_SWIGLU)
-    capi.check(L.sdy_gemm_grouped(ctypes.byref(m.m), rows, n_exp, grp_tok.ptr, grp_tile.ptr, None,
+    capi.check(L.sdy_gemm_grouped(ctypes.byref(m.m), rows, n_exp, grp_tok.ptr, grp_tile.ptr, None, None, 0,
                                   ctypes.byref(a), ws.ptr, None))
     got = sw.to_array(np.float32, (R, rows // 2))
     srt = exp[s_orow]
