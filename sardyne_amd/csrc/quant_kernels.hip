@@ -1063,11 +1063,18 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
         const uint32_t is = ok ? base * nb + (le >> 2) : r0 * nb + (u >> 2);
         load_w_at<WT>(a.P, iu, is, (uint32_t)u, R[k]);
     };
-    load_k(0);
-    const uint32_t etab = sdy_expf_tab_lane(lane);  // the SwiGLU epilogue's exponential table
     uint4 Yr[4];
     uint2 bsr;
     float ydr;
+    if constexpr (PRO != 0) {
+        // the workgroup's activation row first: requested before any weight, its loads do not
+        // return behind this workgroup's weight stream (measured on the 22016 x 2048 gate|up with
+        // the FFN norm: 9.5 -> 8.9 us against building the row while the weights are in flight)
+        arow.build(px, a.peps, a.P.n_in, lds_act);
+        q8k_unit_lds(lds_act, a.P.nb, u, Yr, bsr, ydr);
+    }
+    load_k(0);
+    const uint32_t etab = sdy_expf_tab_lane(lane);  // the SwiGLU epilogue's exponential table
     if constexpr (PRO == 0) {
         const uint8_t *blk = xq + __mul24(u >> 2, 292);
         const uint8_t *yb = blk + 4 + 64 * (u & 3);
@@ -1077,11 +1084,8 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
         bsr = make_uint2(ld4(blk + 260 + 8 * (u & 3)), ld4(blk + 264 + 8 * (u & 3)));
         ydr = *reinterpret_cast<const float *>(blk);
     } else {
-        // every weight load goes out first; the workgroup quantises the row while they are in flight
 #pragma unroll
         for (int k = 1; k < NIT; k++) load_k(k);
-        arow.build(px, a.peps, a.P.n_in, lds_act);
-        q8k_unit_lds(lds_act, a.P.nb, u, Yr, bsr, ydr);
     }
     // the bias and residual of the lane's rows (an absent one reads a stand-in: the activation row)
     const float *stand_in = PRO ? px : reinterpret_cast<const float *>(xq);
