@@ -1278,8 +1278,14 @@ __global__ __launch_bounds__(THREADS) void k_matvec_lr(MvArgs a) {
     Q8kRow<false, PRO_NR> arow;
     // (with PRO, waves past the rows still take part in the workgroup's activation row: they load
     // row 0 and run no row)
-    if constexpr (PRO) arow.issue(a.px, nullptr, a.P.n_in);
-    else if (wid >= n_rows) return;
+    if constexpr (PRO) {
+        // the workgroup's activation row before any weight is requested (its loads would otherwise
+        // return behind the weight stream)
+        arow.issue(a.px, nullptr, a.P.n_in);
+        arow.build(a.px, 0.0f, a.P.n_in, lds_act);
+    } else if (wid >= n_rows) {
+        return;
+    }
     const long w0 = wid < n_rows ? wid : 0;
     load_row(w0, A);
     // the bias and residual of the row, requested with its weights (lane 0 stores)
@@ -1297,7 +1303,6 @@ __global__ __launch_bounds__(THREADS) void k_matvec_lr(MvArgs a) {
     uint4 Yr[NI][4];
     uint2 bsr[NI];
     float ydr[NI];
-    if constexpr (PRO) arow.build(a.px, 0.0f, a.P.n_in, lds_act);
 #pragma unroll
     for (int k = 0; k < NI; k++) {
         const int u = 64 * k + lane, uu = u < T ? u : 0;
