@@ -133,6 +133,14 @@ SDY_DEV void load_sb(const GemmArgs &g, long row, int sb, int h, SbRegs &r) {
     }
 }
 
+// k_gemm3's weights of one super-block for one lane: the quants of its units (all 16 bytes of each
+// plane's record: both k-halves), the scale record and the Q6_K d.
+struct SbRegs3 {
+    u32x4 q[2][3];
+    u32x4 hd;
+    uint32_t d6;
+};
+
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -160,6 +168,24 @@ SDY_DEV void lds_read8(uint32_t a, uint32_t b, f32x4 &a0, f32x4 &a1, f32x4 &a2, 
         : "memory");
 }
 
+// Two 16-byte LDS reads at a, a + 32 and two at b, b + 32, as lds_read8.
+SDY_DEV void lds_read4(uint32_t a, uint32_t b, f32x4 &a0, f32x4 &a1, f32x4 &b0, f32x4 &b1) {
+    __asm__ volatile(
+        "ds_read_b128 %0, %4\n"
+        "ds_read_b128 %1, %4 offset:32\n"
+        "ds_read_b128 %2, %5\n"
+        "ds_read_b128 %3, %5 offset:32\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(a0), "=&v"(a1), "=&v"(b0), "=&v"(b1)
+        : "v"(a), "v"(b)
+        : "memory");
+}
+
+// The s_waitcnt immediate that waits for at most n (< 64) vector memory operations outstanding and
+// lgkm (0 or 15: every LDS access, or none) LDS and scalar ones (vmcnt in bits 3:0 and 15:14,
+// expcnt at its maximum, lgkmcnt in bits 11:8).
+constexpr int sdy_vmcnt_imm(int n, int lgkm = 0) { return (n & 15) | (((n >> 4) & 3) << 14) | (7 << 4) | (lgkm << 8); }
+
 SDY_DEV __amdgpu_buffer_rsrc_t plane_rsrc(const uint8_t *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)bytes, 0x00020000);
 }
@@ -167,22 +193,46 @@ SDY_DEV __amdgpu_buffer_rsrc_t plane_rsrc(const uint8_t *p, uint32_t bytes) {
 // The MFMA GEMM with the activations staged by LDS DMA. A workgroup of WM waves covers 32*MT*WM
 // rows x 32*NT tokens; each wave owns 32*MT rows (MT MFMA row tiles, dequantised in registers
 // from buffer loads whose per-super-block advance is a scalar offset) and shares the staged
-// activations of all the workgroup's tokens. Per super-block and stage the activations are
+// activations of all the workgroup's tokens. The two lanes of a row split its units, each loading
+// whole 16-byte records (lane half h: units 2h, 2h+1), so that a load instruction reads 32 bytes
+// of each of its 32 rows (the vector L1 looks up a cache line per row and instruction); a step's
+// MFMA k-slots are then the lane halves' own units, and the activation fragments are read to
+// match (the integer sums do not depend on the k order). Per super-block and stage the activations are
 // copied global -> LDS with global_load_lds (no registers): LDS chunk p (16 bytes) holds token
 // p / 32, chunk (p % 32) ^ (token % 8), so that the fragment reads of 8 consecutive lanes hit
 // distinct banks. Two stages: super-block s + 1 is in flight while s is multiplied; one
 // s_waitcnt + barrier per super-block. The per-row d (and dmin) are converted once per row into a
 // per-wave LDS table.
-template <int WT, int MT, int NT, int WM, bool WIDE>
+//
+// KS = 2 splits each super-block's four 64-element units between the two waves of a pair that own
+// the same rows (units 0-1 and 2-3): each wave sums its units' integer products, the pair exchanges
+// half of its accumulator through LDS at the super-block's barrier, and each wave completes and
+// combines its half of the tile (D registers 0-7 or 8-15). Integer partial sums add exactly, so the
+// bits are KS 1's; a grid has twice the waves (for shapes with one wave per SIMD otherwise: the
+// 2048-row down and attention projections of a prompt).
+//
+// PF = 2 keeps two super-blocks in flight (three register sets and three stage buffers): the wave
+// waits by count for the loads of the next super-block only, and the workgroup barrier orders LDS
+// alone. For grids of one wave per SIMD, whose super-blocks otherwise each wait a full memory round
+// trip.
+template <int WT, int MT, int NT, int WM, bool WIDE, int KS = 1, int PF = 1>
 __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
+    static_assert(KS == 1 || (KS == 2 && WM % 2 == 0), "unit split");
+    static_assert(PF == 1 || PF == 2, "prefetch depth");
+    constexpr int UN = 4 / KS, PAIRS = WM / KS;  // units per wave, row tiles per workgroup
     constexpr int BN = 32 * NT, NTH = 64 * WM;
     constexpr int YDN = BN < 64 ? 64 : BN;                  // yd slots (one DMA dword per lane)
-    constexpr int YDOFF = BN * 512, BSOFF = YDOFF + YDN * 4;
+    // PF 2: every wave issues the same loads (so that its waits can be counted): each copies the yd
+    // row into a slot of its own and a 1/WM share of the bsums, as dwords
+    constexpr int YDOFF = BN * 512, BSOFF = YDOFF + (PF == 2 ? WM : 1) * YDN * 4;
     constexpr int BUF = BSOFF + BN * 32;                    // bytes of one stage
+    constexpr int NBSW = BN * 8 / (64 * WM);                // PF 2: bsum dword loads per wave
+    static_assert(PF == 1 || (BN * 8) % (64 * WM) == 0, "PF 2: the bsums in whole dword loads per wave");
     constexpr int NI = BN * 32 / NTH;                       // activation DMA chunks per lane per stage
     static_assert((BN * 32) % NTH == 0 && NI >= 1, "tile");
     extern __shared__ __align__(16) uint8_t lds[];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, lr = lane & 31;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, h = lane >> 5,
+              lr = lane & 31;
     // token tiles of a row tile on one XCD (workgroups are dealt round-robin to the 8 XCDs)
     const int n_tt = gridDim.x;
     const long n_rt = gridDim.y, L = (long)blockIdx.y * n_tt + blockIdx.x;
@@ -199,7 +249,9 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
             tti = w - (w / n_tt) * n_tt;
         }
     }
-    const long rt = rti * (32 * MT * WM) + 32 * MT * wave;
+    const int pw = __builtin_amdgcn_readfirstlane(wave / KS);  // the wave's row tile
+    const int ks = __builtin_amdgcn_readfirstlane(wave - pw * KS);  // and unit share
+    const long rt = rti * (32 * MT * PAIRS) + 32 * MT * pw;
     int t0 = (int)tti * BN, t_end = g.n_tok;
     long row0 = g.row0;
     if (g.grp_tile) {
@@ -220,13 +272,17 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
     auto tok_of = [&](int t) { return t0 + t < t_end ? t0 + t : t_end - 1; };
     // the expansion rows the stages read: this lane's rows of the tile, looked up once
     auto act_of = [&](int t) { return g.act_row ? g.act_row[tok_of(t)] : tok_of(t); };
-    int ar_st[NI], ar_yd[YDN / 64], ar_bs[BN / 32 > 0 ? BN / 32 : 1];
+    int ar_st[NI], ar_yd[YDN / 64], ar_bs[BN / 32 > 0 ? BN / 32 : 1], ar_b2[PF == 2 && NBSW > 0 ? NBSW : 1];
 #pragma unroll
     for (int j = 0; j < NI; j++) ar_st[j] = act_of(((j * WM + wave) * 64 + lane) >> 5);
 #pragma unroll
     for (int i = 0; i < YDN / 64; i++) ar_yd[i] = act_of(64 * i + lane);
 #pragma unroll
     for (int i = 0; i < BN / 32; i++) ar_bs[i] = act_of(32 * i + (lane >> 1));
+    if constexpr (PF == 2 && WT == SDY_Q4_K) {
+#pragma unroll
+        for (int i = 0; i < NBSW; i++) ar_b2[i] = act_of(((i * WM + wave) * 64 + lane) >> 3);
+    }
 
     // weight buffer resources and this lane's per-row offsets
     __amdgpu_buffer_rsrc_t rq[3], rh, rd;
@@ -234,24 +290,27 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
     for (int i = 0; i < 3; i++) rq[i] = plane_rsrc(g.p[i], g.psz[i]);
     rh = plane_rsrc(g.p[WT == SDY_Q4_K ? 2 : 3], g.psz[WT == SDY_Q4_K ? 2 : 3]);
     rd = plane_rsrc(g.p[4], g.psz[4]);
+    // the lane's units of each super-block: ub + uu, uu < UN / 2
+    constexpr int UL = UN / 2;
+    const int ub = ks * UN + h * UL;
     uint32_t oq[MT], oh[MT], od[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         const long ri = rt + 32 * mt + lr;
         const uint32_t row = (uint32_t)(row0 + (ri < g.n_rows ? ri : g.n_rows - 1));
-        oq[mt] = row * (uint32_t)g.T * 16u + 8u * (uint32_t)h;
+        oq[mt] = row * (uint32_t)g.T * 16u + 16u * (uint32_t)(h * UL);
         oh[mt] = row * (uint32_t)nb * 16u;
         od[mt] = row * (uint32_t)nb * 2u;
     }
-    auto load_sb3 = [&](int sb, SbRegs (&R)[MT]) {
+    auto load_sb3 = [&](int sb, SbRegs3 (&R)[MT]) {
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
 #pragma unroll
-            for (int un = 0; un < 4; un++) {
-                const int so = (4 * sb + un) * 16;
-                R[mt].q[un][0] = __builtin_amdgcn_raw_buffer_load_b64(rq[0], oq[mt], so, 0);
-                R[mt].q[un][1] = __builtin_amdgcn_raw_buffer_load_b64(rq[1], oq[mt], so, 0);
-                if constexpr (WT == SDY_Q6_K) R[mt].q[un][2] = __builtin_amdgcn_raw_buffer_load_b64(rq[2], oq[mt], so, 0);
+            for (int uu = 0; uu < UL; uu++) {  // units ub + uu (h UL in the lane's offset)
+                const int so = (4 * sb + ks * UN + uu) * 16;
+                R[mt].q[uu][0] = __builtin_amdgcn_raw_buffer_load_b128(rq[0], oq[mt], so, 0);
+                R[mt].q[uu][1] = __builtin_amdgcn_raw_buffer_load_b128(rq[1], oq[mt], so, 0);
+                if constexpr (WT == SDY_Q6_K) R[mt].q[uu][2] = __builtin_amdgcn_raw_buffer_load_b128(rq[2], oq[mt], so, 0);
             }
             R[mt].hd = __builtin_amdgcn_raw_buffer_load_b128(rh, oh[mt], sb * 16, 0);
             R[mt].d6 = WT == SDY_Q6_K ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rd, od[mt], sb * 2, 0) : 0u;
@@ -267,13 +326,30 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
             __builtin_amdgcn_global_load_lds((const void *)(g.y16 + (size_t)ar_st[j] * g.n_in + 256 * sb + 8 * c),
                                              (lds_ptr_t)(base + blk * 1024), 16, 0, 0);
         }
-        if (wave == 0) {
+        if constexpr (PF == 2) {
 #pragma unroll
             for (int i = 0; i < YDN / 64; i++)
                 __builtin_amdgcn_global_load_lds((const void *)(g.yd + (size_t)ar_yd[i] * nb + sb),
-                                                 (lds_ptr_t)(base + YDOFF + 256 * i), 4, 0, 0);
+                                                 (lds_ptr_t)(base + YDOFF + wave * (YDN * 4) + 256 * i), 4, 0, 0);
+            if constexpr (WT == SDY_Q4_K) {
+#pragma unroll
+                for (int i = 0; i < NBSW; i++) {
+                    const int p = (i * WM + wave) * 64 + lane;  // bsum dword p: token p / 8, bytes 4 (p % 8)
+                    __builtin_amdgcn_global_load_lds(
+                        (const void *)(reinterpret_cast<const uint8_t *>(g.bs16) + ((size_t)ar_b2[i] * nb + sb) * 32 +
+                                       4 * (p & 7)),
+                        (lds_ptr_t)(base + BSOFF + 256 * (i * WM + wave)), 4, 0, 0);
+                }
+            }
+        } else {
+            if (wave == 0) {
+#pragma unroll
+                for (int i = 0; i < YDN / 64; i++)
+                    __builtin_amdgcn_global_load_lds((const void *)(g.yd + (size_t)ar_yd[i] * nb + sb),
+                                                     (lds_ptr_t)(base + YDOFF + 256 * i), 4, 0, 0);
+            }
         }
-        if constexpr (WT == SDY_Q4_K) {
+        if constexpr (WT == SDY_Q4_K && PF == 1) {
             if (wave == (WM > 1 ? 1 : 0)) {
 #pragma unroll
                 for (int i = 0; i < BN / 32; i++)
@@ -283,14 +359,33 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
             }
         }
     };
-    // the barrier's release fence waits for every load of the wave, the DMA of the stage included
-    auto wait_stage = [&]() { __syncthreads(); };
+    // PF 1: the barrier's release fence waits for every load of the wave, the DMA of the stage included.
+    // PF 2: the loads of the iteration's super-block sb + 2 stay in flight: wait until at most as
+    // many as the wave issued for it are outstanding (loads complete in order), then a barrier that
+    // orders the LDS accesses (the activations DMA'd by every wave, the exchange)
+    constexpr int NWL = MT * (UL * (WT == SDY_Q6_K ? 3 : 2) + (WT == SDY_Q6_K ? 2 : 1));  // load_sb3's loads
+    constexpr int NSL = NI + YDN / 64 + (WT == SDY_Q4_K ? NBSW : 0);                     // PF 2: stage()'s
+    static_assert(PF == 1 || NWL + NSL < 64, "wait count");
+    auto wait_stage = [&]() {
+        if constexpr (PF == 1) {
+            __syncthreads();
+        } else {
+            // s_waitcnt vmcnt(NWL + NSL) lgkmcnt(0) (the compiler's own wait tracking sees it), then the
+            // barrier as a compiler memory barrier too (a fence would wait for the DMA in flight: it
+            // writes LDS)
+            __builtin_amdgcn_s_waitcnt(sdy_vmcnt_imm(NWL + NSL));
+            __asm__ volatile("s_barrier" ::: "memory");
+        }
+    };
 
-    float16v acc[MT][NT];
+    constexpr int RH = 16 / KS;  // D registers (of 16) that a wave completes: RH ks .. RH ks + RH - 1
+    float acc[MT][NT][RH];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) acc[mt][nt] = float16v{};
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int i = 0; i < RH; i++) acc[mt][nt][i] = 0.0f;
     const half2v off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
     const half2v off6 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
     const half2v off4c = {(_Float16)-1032.0f, (_Float16)-1032.0f};  // centred Q4_K quants q - 8
@@ -298,17 +393,26 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
     // so its reads need not wait for the activation loads in flight)
     __shared__ __align__(16) float dtab_all[WM * 64 * MT];
     float *dtab = dtab_all + wave * (64 * MT);
+    // KS 2: the half accumulators a wave hands its partner, [parity][wave][sum][mt][nt][8][64]
+    constexpr int NXS = WIDE && WT == SDY_Q6_K ? 2 : 1;
+    __shared__ float xch[KS == 2 ? 2 * WM * NXS * MT * NT * 8 * 64 : 1];
 
-    SbRegs A[MT];
-    load_sb3(0, A);
-    stage(0, 0);
-    wait_stage();
-
-    for (int sb = 0; sb < nb; sb++) {
+    constexpr int NBUF = PF + 1;  // stage buffers
+    // one super-block: sb's weights in A, the loads of sb + PF issued into An (clamped to the last
+    // super-block, so that every iteration issues the same weight loads)
+    auto iter = [&](int sb, SbRegs3(&A)[MT], SbRegs3(&An)[MT]) {
         const int cur = sb & 1;
-        SbRegs An[MT];
-        load_sb3(sb + 1 < nb ? sb + 1 : sb, An);
-        if (sb + 1 < nb) stage(sb + 1, cur ^ 1);
+        load_sb3(sb + PF < nb ? sb + PF : nb - 1, An);
+        // PF 2 stages the last super-block again past the end (into the buffer of sb - 1, which is
+        // read no more), so that every iteration issues the same loads
+        if constexpr (PF == 2) {
+            stage(sb + PF < nb ? sb + PF : nb - 1, (sb + PF) % NBUF);
+            // already true (the previous iteration waited for sb's loads): stated so that the
+            // compiler's wait tracking, which loses count at the loop head, knows A complete
+            __builtin_amdgcn_s_waitcnt(sdy_vmcnt_imm(2 * (NWL + NSL), 15));
+        } else if (sb + PF < nb) {
+            stage(sb + PF, (sb + PF) % NBUF);
+        }
         // d (and dmin) of the wave's rows as f32
         if (h == 0) {
 #pragma unroll
@@ -318,7 +422,7 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
                 if constexpr (WT == SDY_Q4_K) dtab[32 * MT + 32 * mt + lr] = sdy_h2f((uint16_t)(dp >> 16));
             }
         }
-        const uint8_t *bbuf = lds + cur * BUF;
+        const uint8_t *bbuf = lds + (sb % NBUF) * BUF;
         // WIDE (any block the formats can hold):
         //   Q6_K: each scale sc = 16 sh + sl (sl in [0, 16), sh in [-8, 7]) is applied in two exact
         //         fragments with their own integer sums, isum = 16 ihi + ilo; the partial sums stay
@@ -337,11 +441,30 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) ihi[mt][nt] = float16v{};
         }
-        // the activation fragments of step st = 4 un + s (16-element chunk 8 un + 2 s + h of each token
-        // tile), read from LDS one step ahead of their MFMAs
+        // the lane's scales for its units, once per super-block. Q4_K: the 6-bit scales of sub-blocks
+        // 2 ub .. 2 ub + 2 UL - 1 as bytes (sub-blocks 0-3 from the low bits of the first word, 4-7
+        // from the third word and the top bits of the first); Q6_K: the int8 scale words of units ub + uu
+        uint32_t scw[MT][UL];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            if constexpr (WT == SDY_Q4_K) {
+                const uint32_t Aw = A[mt].hd.y, Cw = A[mt].hd.w;
+                const uint32_t f1 = Aw & 0x3F3F3F3Fu, f2 = (Cw & 0x0F0F0F0Fu) | ((Aw >> 2) & 0x30303030u);
+                scw[mt][0] = (ub >= 2 ? f2 : f1) >> (16 * (ub & 1));
+            } else {
+#pragma unroll
+                for (int uu = 0; uu < UL; uu++) {
+                    const int w = ub + uu;
+                    const uint32_t lo = (w & 1) ? A[mt].hd.y : A[mt].hd.x, hi2 = (w & 1) ? A[mt].hd.w : A[mt].hd.z;
+                    scw[mt][uu] = (w & 2) ? hi2 : lo;
+                }
+            }
+        }
+        // step sl = 8 uu + 4 hh + s of the lane: k-half hh of unit ub + uu, quarter s (its 16-element
+        // chunk 8 (ub + uu) + 2 s + hh of each token), read from LDS one step ahead of its MFMAs
         half8 bf[2][NT];
-        auto read_b = [&](int st, half8 (&dst)[NT]) {
-            const int c = 8 * (st >> 2) + 2 * (st & 3) + h;
+        auto read_b = [&](int sl, half8 (&dst)[NT]) {
+            const int c = 8 * (ub + (sl >> 3)) + 2 * (sl & 3) + ((sl >> 2) & 1);
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 const int t = 32 * nt + lr;
@@ -350,21 +473,22 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
         };
         read_b(0, bf[0]);
 #pragma unroll
-        for (int un = 0; un < 4; un++) {
+        for (int uu = 0; uu < UL; uu++) {
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++)
 #pragma unroll
             for (int s = 0; s < 4; s++) {
-                const int st = 4 * un + s;
-                if (st + 1 < 16) read_b(st + 1, bf[(st + 1) & 1]);
+                const int sl = 8 * uu + 4 * hh + s;  // the lane's step
+                if (sl + 1 < 4 * UN) read_b(sl + 1, bf[(sl + 1) & 1]);
                 __builtin_amdgcn_sched_barrier(0);  // the next step's reads go out before this step's work
                 half8 a[MT], ah[SPLIT6 ? MT : 1];
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
+                    auto half_of = [&](const u32x4 &v) { return hh ? u32x2{v.z, v.w} : u32x2{v.x, v.y}; };
                     if constexpr (WT == SDY_Q4_K) {
-                        const uint32_t Aw = A[mt].hd.y, Cw = A[mt].hd.w;
-                        const int j = 2 * un + (s >> 1);
-                        const int sc = j < 4 ? (int)((Aw >> (8 * j)) & 63)
-                                             : (int)(((Cw >> (8 * (j - 4))) & 15) | (((Aw >> (8 * (j - 4) + 6)) & 3) << 4));
-                        const u32x2 src = (s & 1) ? A[mt].q[un][1] : A[mt].q[un][0];
+                        // sub-block 2 (ub + uu) + s / 2
+                        const int sc = (int)((scw[mt][0] >> (8 * (2 * uu + (s >> 1)))) & 255u);
+                        const u32x2 src = half_of((s & 1) ? A[mt].q[uu][1] : A[mt].q[uu][0]);
                         const u32x2 nib = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
                         if constexpr (WIDE) {
                             const _Float16 f = (_Float16)(float)sc;
@@ -374,14 +498,13 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
                             a[mt] = frag_q4(nib, half2v{f, f}, half2v{nf, nf});
                         }
                     } else {
-                        const int j = 4 * un + s;
-                        const int sc = (int)(int8_t)((A[mt].hd[j >> 2] >> (8 * (j & 3))) & 255u);
-                        const u32x2 src = (s & 1) ? A[mt].q[un][1] : A[mt].q[un][0];
+                        const int sc = (int)(int8_t)((scw[mt][uu] >> (8 * s)) & 255u);
+                        const u32x2 src = half_of((s & 1) ? A[mt].q[uu][1] : A[mt].q[uu][0]);
                         const u32x2 lo = (s & 2) ? ((src >> 4u) & 0x0F0F0F0Fu) : (src & 0x0F0F0F0Fu);
-                        const u32x2 hi = ((A[mt].q[un][2] >> (unsigned)(2 * s)) & 0x03030303u) << 4u;
+                        const u32x2 hi = ((half_of(A[mt].q[uu][2]) >> (unsigned)(2 * s)) & 0x03030303u) << 4u;
                         if constexpr (SPLIT6) {
-                            const int sl = sc & 15, sh = sc >> 4;
-                            const _Float16 fl = (_Float16)(float)sl, fh = (_Float16)(float)sh;
+                            const int sl6 = sc & 15, sh = sc >> 4;
+                            const _Float16 fl = (_Float16)(float)sl6, fh = (_Float16)(float)sh;
                             a[mt] = frag_scaled(lo | hi, off6, half2v{fl, fl});
                             ah[mt] = frag_scaled(lo | hi, off6, half2v{fh, fh});
                         } else {
@@ -394,61 +517,48 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
                 for (int nt = 0; nt < NT; nt++) {
 #pragma unroll
                     for (int mt = 0; mt < MT; mt++) {
-                        isum[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt], bf[st & 1][nt], isum[mt][nt], 0, 0, 0);
+                        isum[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt], bf[sl & 1][nt], isum[mt][nt], 0, 0, 0);
                         if constexpr (SPLIT6)
-                            ihi[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[mt], bf[st & 1][nt], ihi[mt][nt], 0, 0, 0);
+                            ihi[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[mt], bf[sl & 1][nt], ihi[mt][nt], 0, 0, 0);
                     }
                 }
             }
-        }
-        if constexpr (SPLIT6) {  // isum = 16 ihi + ilo: 16 ihi exact, one rounding of the sum (that of (float)isum)
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const float hi = 16.0f * ihi[mt][nt][r];
-                        isum[mt][nt][r] = hi + isum[mt][nt][r];
-                    }
         }
         // combine in the reference's order: acc + (yd*d*isum - yd*dmin*msum)
         float ydn[NT];
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) ydn[nt] = *reinterpret_cast<const float *>(bbuf + YDOFF + 4 * (32 * nt + lr));
+        for (int nt = 0; nt < NT; nt++)
+            ydn[nt] = *reinterpret_cast<const float *>(bbuf + YDOFF + (PF == 2 ? wave * (YDN * 4) : 0) + 4 * (32 * nt + lr));
+        // Q4_K, row tile mt: msum = sum_j m_j bsum_j and, WIDE, cw = sum_j 8 sc_j bsum_j (below 16 * 504 *
+        // 2032 < 2^24), both exact, from the staged bsums
+        auto bsum_mfma = [&](int mt, float16v(&msum)[NT], float16v(&cw)[NT]) {
+            const uint32_t Aw = A[mt].hd.y, Bw = A[mt].hd.z, Cw = A[mt].hd.w;
+            half8 a2, a3;
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            float16v msum[NT];
-            if constexpr (WT == SDY_Q4_K) {
-                const uint32_t Aw = A[mt].hd.y, Bw = A[mt].hd.z, Cw = A[mt].hd.w;
-                half8 a2, a3;
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const int j = 4 * h + (e >> 1);  // sub-block of 16-group 8h + e
-                    const int m = j < 4 ? (int)((Bw >> (8 * j)) & 63)
-                                        : (int)(((Cw >> (8 * (j - 4) + 4)) & 15) | (((Bw >> (8 * (j - 4) + 6)) & 3) << 4));
-                    a2[e] = (_Float16)(float)m;
-                    if constexpr (WIDE) {
-                        const int sc = j < 4 ? (int)((Aw >> (8 * j)) & 63)
-                                             : (int)(((Cw >> (8 * (j - 4))) & 15) | (((Aw >> (8 * (j - 4) + 6)) & 3) << 4));
-                        a3[e] = (_Float16)(float)(8 * sc);
-                    }
-                }
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++) {
-                    const half8 b2 = *reinterpret_cast<const half8 *>(bbuf + BSOFF + 32 * (32 * nt + lr) + 16 * h);
-                    msum[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b2, float16v{}, 0, 0, 0);
-                    if constexpr (WIDE) {  // + sum_j 8 sc_j bsum_j (below 16 * 504 * 2032 < 2^24): one rounding
-                        const float16v c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a3, b2, float16v{}, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 16; r++) isum[mt][nt][r] = isum[mt][nt][r] + c[r];
-                    }
+            for (int e = 0; e < 8; e++) {
+                const int j = 4 * h + (e >> 1);  // sub-block of 16-group 8h + e
+                const int m = j < 4 ? (int)((Bw >> (8 * j)) & 63)
+                                    : (int)(((Cw >> (8 * (j - 4) + 4)) & 15) | (((Bw >> (8 * (j - 4) + 6)) & 3) << 4));
+                a2[e] = (_Float16)(float)m;
+                if constexpr (WIDE) {
+                    const int sc = j < 4 ? (int)((Aw >> (8 * j)) & 63)
+                                         : (int)(((Cw >> (8 * (j - 4))) & 15) | (((Aw >> (8 * (j - 4) + 6)) & 3) << 4));
+                    a3[e] = (_Float16)(float)(8 * sc);
                 }
             }
-            // rows 8q + 4h .. 8q + 4h + 3 of the tile (D registers 4q .. 4q + 3): d, then dmin
-            float dv[16], dm[16];
-            {
-                const uint32_t da = lds_addr(dtab + 32 * mt + 4 * h);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const half8 b2 = *reinterpret_cast<const half8 *>(bbuf + BSOFF + 32 * (32 * nt + lr) + 16 * h);
+                msum[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b2, float16v{}, 0, 0, 0);
+                if constexpr (WIDE) cw[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a3, b2, float16v{}, 0, 0, 0);
+            }
+        };
+        // acc += yd d isum - yd dmin msum over the wave's D registers of row tile mt: register RH ks + i
+        // holds row 8 q + 4 h + (i & 3) of the tile, q = (RH ks + i) / 4
+        auto combine = [&](int mt, const float(&tot)[NT][RH], const float(&ms)[NT][RH]) {
+            float dv[RH], dm[RH];
+            const uint32_t da = lds_addr(dtab + 32 * mt + 4 * h + 8 * (RH / 4) * ks);
+            if constexpr (KS == 1) {
                 f32x4 d0, d1, d2, d3, m0, m1, m2, m3;
                 lds_read8(da, da + 4 * 32 * MT, d0, d1, d2, d3, m0, m1, m2, m3);
                 const f32x4 dq[4] = {d0, d1, d2, d3}, mq[4] = {m0, m1, m2, m3};
@@ -459,47 +569,202 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
                         dv[4 * q + i] = dq[q][i];
                         dm[4 * q + i] = WT == SDY_Q4_K ? mq[q][i] : 0.0f;
                     }
+            } else {
+                f32x4 d0, d1, m0, m1;
+                lds_read4(da, da + 4 * 32 * MT, d0, d1, m0, m1);
+                const f32x4 dq[2] = {d0, d1}, mq[2] = {m0, m1};
+#pragma unroll
+                for (int q = 0; q < 2; q++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        dv[4 * q + i] = dq[q][i];
+                        dm[4 * q + i] = WT == SDY_Q4_K ? mq[q][i] : 0.0f;
+                    }
             }
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
+            for (int i = 0; i < RH; i++) {
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) {
                     if constexpr (WT == SDY_Q4_K) {
-                        const float dall = ydn[nt] * dv[r], dmn = ydn[nt] * dm[r];
-                        const float t1 = dall * isum[mt][nt][r], t2 = dmn * msum[nt][r];
-                        acc[mt][nt][r] = acc[mt][nt][r] + (t1 - t2);
+                        const float dall = ydn[nt] * dv[i], dmn = ydn[nt] * dm[i];
+                        const float t1 = dall * tot[nt][i], t2 = dmn * ms[nt][i];
+                        acc[mt][nt][i] = acc[mt][nt][i] + (t1 - t2);
                     } else {
-                        const float ydd = ydn[nt] * dv[r];
-                        acc[mt][nt][r] = acc[mt][nt][r] + ydd * isum[mt][nt][r];
+                        const float ydd = ydn[nt] * dv[i];
+                        acc[mt][nt][i] = acc[mt][nt][i] + ydd * tot[nt][i];
                     }
                 }
             }
-        }
-        wait_stage();
+        };
+        if constexpr (KS == 1) {
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) A[mt] = An[mt];
+            for (int mt = 0; mt < MT; mt++) {
+                float16v msum[NT], cw[NT];
+                if constexpr (WT == SDY_Q4_K) bsum_mfma(mt, msum, cw);
+                float tot[NT][16], ms[NT][16];
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        float v = isum[mt][nt][r];
+                        // SPLIT6: isum = 16 ihi + ilo, 16 ihi exact, one rounding of the sum (that of (float)isum)
+                        if constexpr (SPLIT6) v = 16.0f * ihi[mt][nt][r] + v;
+                        if constexpr (WT == SDY_Q4_K && WIDE) v = v + cw[nt][r];  // one rounding
+                        tot[nt][r] = v;
+                        ms[nt][r] = WT == SDY_Q4_K ? msum[nt][r] : 0.0f;
+                    }
+                combine(mt, tot, ms);
+            }
+            wait_stage();
+        } else {
+            // before the barrier (after it the stage buffer is refilled): the bsum products, and the half
+            // of the integer sums that the partner completes into its slot
+            float ms[MT][NT][RH], cws[MT][NT][RH];
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                float16v msum[NT], cw[NT];
+                if constexpr (WT == SDY_Q4_K) {
+                    bsum_mfma(mt, msum, cw);
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                        for (int i = 0; i < RH; i++) {
+                            ms[mt][nt][i] = ks ? msum[nt][RH + i] : msum[nt][i];
+                            if constexpr (WIDE) cws[mt][nt][i] = ks ? cw[nt][RH + i] : cw[nt][i];
+                        }
+                }
+            }
+            float *xw = xch + (size_t)(cur * WM + wave) * (NXS * MT * NT * 512);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                    for (int i = 0; i < RH; i++) {
+                        const int o = ((mt * NT + nt) * 8 + i) * 64 + lane;
+                        xw[o] = ks ? isum[mt][nt][i] : isum[mt][nt][RH + i];
+                        if constexpr (SPLIT6) xw[MT * NT * 512 + o] = ks ? ihi[mt][nt][i] : ihi[mt][nt][RH + i];
+                    }
+            wait_stage();
+            const float *xr = xch + (size_t)(cur * WM + (wave ^ 1)) * (NXS * MT * NT * 512);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                float tot[NT][RH], msh[NT][RH];
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                    for (int i = 0; i < RH; i++) {
+                        const int o = ((mt * NT + nt) * 8 + i) * 64 + lane;
+                        // the unit halves' sums are integers below 2^24: their sum is isum exactly
+                        float v = (ks ? isum[mt][nt][RH + i] : isum[mt][nt][i]) + xr[o];
+                        if constexpr (SPLIT6) {
+                            const float hi = (ks ? ihi[mt][nt][RH + i] : ihi[mt][nt][i]) + xr[MT * NT * 512 + o];
+                            v = 16.0f * hi + v;
+                        }
+                        if constexpr (WT == SDY_Q4_K && WIDE) v = v + cws[mt][nt][i];
+                        tot[nt][i] = v;
+                        msh[nt][i] = WT == SDY_Q4_K ? ms[mt][nt][i] : 0.0f;
+                    }
+                combine(mt, tot, msh);
+            }
+        }
+    };
+    if constexpr (PF == 1) {
+        SbRegs3 A[MT];
+        load_sb3(0, A);
+        stage(0, 0);
+        __syncthreads();
+        for (int sb = 0; sb < nb; sb++) {
+            SbRegs3 An[MT];
+            iter(sb, A, An);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) A[mt] = An[mt];
+        }
+    } else {
+        // a ring of three register sets, rotated by name
+        SbRegs3 S0[MT], S1[MT], S2[MT];
+        load_sb3(0, S0);
+        stage(0, 0);
+        load_sb3(nb > 1 ? 1 : 0, S1);
+        if (nb > 1) stage(1, 1);
+        __syncthreads();
+        // whole rounds of three, then the rest (no exit inside a round: the compiler's wait tracking
+        // would merge such exits into the loop's back edge, with the next set still pending)
+        int sb = 0;
+        for (; sb + 3 <= nb; sb += 3) {
+            iter(sb, S0, S2);
+            iter(sb + 1, S1, S0);
+            iter(sb + 2, S2, S1);
+        }
+        if (sb < nb) {
+            iter(sb, S0, S2);
+            if (sb + 1 < nb) iter(sb + 1, S1, S0);
+        }
     }
-    // store (bias, residual, or the SwiGLU pair of rows 2i, 2i+1 held by this lane)
+    // store (bias, residual, or the SwiGLU pair of rows 2i, 2i+1 held by this lane). The output rows,
+    // bias and residual values are all requested before the first store (one memory round trip);
+    // tokens and rows past the ends read the last valid ones and store nothing.
+    int orow[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int tok = t0 + 32 * nt + lr;
+        orow[nt] = tok < t_end ? tok : t_end - 1;
+    }
+    if (g.out_row) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) orow[nt] = g.out_row[orow[nt]];
+    }
+    auto row_of = [&](int mt, int i) {  // the matrix row of D register RH ks + i of row tile mt (clamped)
+        const int r = RH * ks + i;
+        const long ri = rt + 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
+        return ri < g.n_rows ? ri : g.n_rows - 1;
+    };
+    // the SwiGLU exponential's table in a register (its lane reads need every lane: the values are
+    // computed before the stores' branches)
+    const uint32_t etab = sdy_expf_tab_lane(lane);
+    float bv[MT][RH], rv[MT][NT][RH];
+    if (g.bias) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int i = 0; i < RH; i++) bv[mt][i] = g.bias[g.row0 + row_of(mt, i)];
+    }
+    if (g.resid) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                for (int i = 0; i < RH; i++) rv[mt][nt][i] = g.resid[(size_t)orow[nt] * g.out_stride + g.row0 + row_of(mt, i)];
+    }
+    if (g.swiglu) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                for (int i = 0; i < RH; i += 2)
+                    acc[mt][nt][i] = sdy_silu_mul1_reg(acc[mt][nt][i], acc[mt][nt][i + 1], etab);
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
-            const int tok = t0 + 32 * nt + lr;
-            if (tok >= t_end) continue;
-            const size_t orow = g.out_row ? (size_t)g.out_row[tok] : (size_t)tok;
+            if (t0 + 32 * nt + lr >= t_end) continue;
+            float *orp = g.out + (size_t)orow[nt] * g.out_stride;
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
+            for (int i = 0; i < RH; i++) {
+                const int r = RH * ks + i;  // the D register
                 const long ri = rt + 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (ri >= g.n_rows) continue;
                 const long row = g.grp_tile ? ri : g.row0 + ri;
                 if (g.swiglu) {
-                    if ((r & 1) == 0)
-                        g.out[orow * g.out_stride + (ri >> 1)] = sdy_silu_mul1(acc[mt][nt][r], acc[mt][nt][r + 1]);
+                    if ((i & 1) == 0) orp[ri >> 1] = acc[mt][nt][i];
                 } else {
-                    float v = acc[mt][nt][r];
-                    if (g.bias) v = v + g.bias[row];
-                    if (g.resid) v = g.resid[orow * g.out_stride + row] + v;
-                    g.out[orow * g.out_stride + row] = v;
+                    float v = acc[mt][nt][i];
+                    if (g.bias) v = v + bv[mt][i];
+                    if (g.resid) v = rv[mt][nt][i] + v;
+                    orp[row] = v;
                 }
             }
         }
@@ -633,24 +898,25 @@ extern "C" int sdy_gemm_ok(const sdy_mat *m, int n_tok) {
            (size_t)m->n_rows * m->n_units * 16 < 0xFFFFFFFFu;
 }
 
-template <int WT, int MT, int NT, int WM, bool WIDE>
+template <int WT, int MT, int NT, int WM, bool WIDE, int KS, int PF>
 static int launch_gemm3_s(GemmArgs &g, hipStream_t st) {
-    constexpr int BN = 32 * NT, BM = 32 * MT * WM, YDN = BN < 64 ? 64 : BN;
-    constexpr size_t lds = 2 * (size_t)(BN * 512 + YDN * 4 + BN * 32);
+    constexpr int BN = 32 * NT, BM = 32 * MT * WM / KS, YDN = BN < 64 ? 64 : BN;
+    constexpr size_t lds = (PF + 1) * (size_t)(BN * 512 + (PF == 2 ? WM : 1) * YDN * 4 + BN * 32);
     static size_t granted = 0;
-    const void *fn = (const void *)k_gemm3<WT, MT, NT, WM, WIDE>;
+    const void *fn = (const void *)k_gemm3<WT, MT, NT, WM, WIDE, KS, PF>;
     int rc = sdy_lds_limit(fn, lds, &granted);
     if (rc) return rc;
     const unsigned tok_tiles = (unsigned)((g.n_tok + BN - 1) / BN), row_tiles = (unsigned)((g.n_rows + BM - 1) / BM);
-    SDY_NOTE_KERNEL((k_gemm3<WT, MT, NT, WM, WIDE>));
-    hipLaunchKernelGGL((k_gemm3<WT, MT, NT, WM, WIDE>), dim3(tok_tiles, row_tiles), dim3(64 * WM), lds, st, g);
+    SDY_NOTE_KERNEL((k_gemm3<WT, MT, NT, WM, WIDE, KS, PF>));
+    hipLaunchKernelGGL((k_gemm3<WT, MT, NT, WM, WIDE, KS, PF>), dim3(tok_tiles, row_tiles), dim3(64 * WM), lds, st, g);
     return sdy_check_launch("gemm");
 }
 
 // g.wide: the matrix has blocks that the one-fragment scheme cannot multiply exactly
-template <int WT, int MT, int NT, int WM>
+template <int WT, int MT, int NT, int WM, int KS = 1, int PF = 1>
 static int launch_gemm3(GemmArgs &g, hipStream_t st) {
-    return g.wide ? launch_gemm3_s<WT, MT, NT, WM, true>(g, st) : launch_gemm3_s<WT, MT, NT, WM, false>(g, st);
+    return g.wide ? launch_gemm3_s<WT, MT, NT, WM, true, KS, PF>(g, st)
+                  : launch_gemm3_s<WT, MT, NT, WM, false, KS, PF>(g, st);
 }
 
 template <int WT, int MT, int NT, int WM, bool WIDE>
@@ -684,6 +950,10 @@ static int gemm_type(GemmArgs &g, hipStream_t st) {
     case 14: return launch_gemm3<WT, 1, 1, 4>(g, st);
     case 15: return launch_gemm3<WT, 1, 4, 4>(g, st);
     case 16: return launch_gemm3<WT, 2, 2, 4>(g, st);
+    case 17: return launch_gemm3<WT, 1, 1, 4, 2>(g, st);
+    case 18: return launch_gemm3<WT, 1, 1, 8, 2>(g, st);
+    case 19: return launch_gemm3<WT, 1, 1, 4, 1, 2>(g, st);
+    case 20: return launch_gemm3<WT, 1, 1, 4, 2, 2>(g, st);
     default: break;
     }
     // 128-row workgroup tiles (4 waves of 32 rows); 64 tokens per tile when there are enough row

@@ -1060,17 +1060,25 @@ def test_quantize_gemm_expansion(norm, n_in, n_tok):
     assert np.array_equal(bits(gemm(0)), bits(exp))
 
 
-@pytest.mark.parametrize("variant", ["11", "12", "13", "14", "15", "16"])
+@pytest.mark.parametrize("variant", ["11", "12", "13", "14", "15", "16", "17", "18", "19", "20"])
 @pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
 def test_gemm_tile_variants_bit_exact(kind, variant, monkeypatch):
-    """Every workgroup tile shape of the GEMM (forced through SARDYNE_GEMM_VARIANT) gives the
-    reference's bits, with partial row and token tiles, in its one-fragment and wide forms."""
+    """Every workgroup tile shape of the GEMM (forced through SARDYNE_GEMM_VARIANT; 17, 18 and 20 split
+    each super-block's units between two waves, 19 and 20 keep two super-blocks in flight) gives the
+    reference's bits, with partial row and token tiles (1 to 43 super-blocks: every remainder of the
+    rounds of three), in its one-fragment and wide forms, and with the SwiGLU and residual epilogues."""
     monkeypatch.setenv("SARDYNE_GEMM_VARIANT", variant)
-    for n_in, n_out, n_tok in [(2048, 300, 200), (768, 40, 17), (11008, 70, 130)]:
+    for n_in, n_out, n_tok in [(256, 64, 40), (512, 96, 33), (2048, 300, 200), (768, 40, 17), (11008, 70, 130)]:
         t, w, xq = _gemm_case(kind, n_in, n_out, n_tok, seed=n_in + n_out + n_tok + 1)
         got = _gemm_run(t, w, xq, n_in, n_out, n_tok)
         exp = O.matmul_q(w, t, xq, n_in, simd=1)
         assert np.array_equal(bits(got), bits(exp)), (n_in, n_out, n_tok)
+    sw = _gemm_run(t, w, xq, n_in, n_out, n_tok, epilogue=capi.EPI_SWIGLU)
+    g, u = exp[:, 0::2].copy(), exp[:, 1::2].copy()
+    lib().op_silu_mul(ptr(g), ptr(u), g.size)
+    assert np.array_equal(bits(sw), bits(g))
+    resid = np.random.default_rng(5).standard_normal((n_tok, n_out)).astype(np.float32)
+    assert np.array_equal(bits(_gemm_run(t, w, xq, n_in, n_out, n_tok, resid=resid)), bits(resid + exp))
     n_in, n_out, n_tok = 1024, 200, 150
     w = _full_range_blocks(kind, n_out, n_in, 11)
     xq = O.quantize(np.random.default_rng(12).standard_normal((n_tok, n_in)).astype(np.float32), O.Q8_K)
