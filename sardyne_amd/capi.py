@@ -103,7 +103,8 @@ _SIGNATURES = {
 class SdyMat(ctypes.Structure):
     """Device-layout matrix descriptor (sdy_mat in sardyne_amd/csrc/sdy_shim.h)."""
     _fields_ = [("base", _vp), ("bytes", _sz), ("type", _int), ("n_in", _int), ("n_rows", ctypes.c_long),
-                ("n_units", _int), ("plane_off", _sz * 5), ("gemm_ok", _int)]
+                ("n_units", _int), ("plane_off", _sz * 5), ("gemm_ok", _int), ("gbase", _vp), ("gbytes", _sz),
+                ("grow0", ctypes.c_long), ("grows", ctypes.c_long)]
 
 
 class SdyMvArgs(ctypes.Structure):
@@ -133,12 +134,14 @@ _DEVICE_SIGNATURES = {
     "sdy_membw_read": (_int, [_vp, _sz, _vp, _vp]),
     "sdy_mat_bytes": (_sz, [_int, _int, ctypes.c_long]),
     "sdy_mat_upload": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long, _vp, _vp]),
+    "sdy_mat_upload_rows": (_int, [ctypes.POINTER(SdyMat), ctypes.c_long, ctypes.c_long, ctypes.c_long, _vp, _vp]),
     "sdy_mat_from_device": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long, _vp, _vp]),
     "sdy_mat_free": (_int, [ctypes.POINTER(SdyMat)]),
     "sdy_mat_rows": (SdyMat, [ctypes.POINTER(SdyMat), ctypes.c_long, ctypes.c_long]),
     "sdy_dequant_rows": (_int, [ctypes.POINTER(SdyMat), ctypes.c_long, ctypes.c_long, _vp, _vp]),
     "sdy_quantize": (_int, [_int, _vp, _vp, _int, _int, _vp]),
     "sdy_matvec": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp]),
+    "sdy_mat_gemm_layout": (_int, [ctypes.POINTER(SdyMat), _vp]),
     "sdy_matvec_pair_ok": (_int, [ctypes.POINTER(SdyMat), _int, ctypes.POINTER(SdyMat), _int]),
     "sdy_matvec_fused_ok": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), ctypes.POINTER(SdyMat),
                                    ctypes.POINTER(SdyMvArgs)]),
@@ -290,10 +293,12 @@ class DeviceBuffer:
 class DeviceMatrix:
     """A quantized (or float) weight matrix in the device layout."""
 
-    def __init__(self, type_id: int, n_in: int, n_rows: int, raw: np.ndarray, stream=None):
+    def __init__(self, type_id: int, n_in: int, n_rows: int, raw: np.ndarray, stream=None, gemm_layout=True):
         self.m = SdyMat()
         raw = np.ascontiguousarray(raw).view(np.uint8)
         check(lib().sdy_mat_upload(ctypes.byref(self.m), type_id, n_in, n_rows, raw.ctypes.data, stream))
+        if gemm_layout:  # the prefill GEMM's copy (Q4_K / Q6_K), as the engine makes it after loading
+            check(lib().sdy_mat_gemm_layout(ctypes.byref(self.m), stream))
         self.type, self.n_in, self.n_rows = type_id, n_in, n_rows
 
     def close(self):

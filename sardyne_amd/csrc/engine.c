@@ -536,6 +536,22 @@ static int load(engine_model *m, const char *path, char *err, size_t len) {
     if (!rc && sdy_sync(m->st)) rc = device_fail(&ld, "upload");
     if (sdy_uploader_free(ld.up) && !rc) rc = device_fail(&ld, "upload");
     if (!rc) {
+        /* the prefill GEMM's copies of the layer matrices (Q4_K / Q6_K; others: no-op), made from the
+           loaded planes: a second copy of those weights, rows in tiles of 32 */
+        for (int l = 0; !rc && l < in->n_layer; l++) {
+            dlayer *L = &m->layers[l];
+            dmat *own[] = {L->qkv_parts < 2 ? &L->wq : NULL, L->qkv_parts < 2 ? &L->wk : NULL,
+                           L->qkv_parts < 3 ? &L->wv : NULL, L->qkv_parts >= 2 ? &L->wqkv : NULL, &L->wo,
+                           &L->gate, &L->up, &L->gate_up, &L->down};
+            for (size_t i = 0; !rc && i < sizeof own / sizeof *own; i++) {
+                if (!own[i] || !own[i]->m.base) continue;
+                if (sdy_mat_gemm_layout(&own[i]->m, m->st)) rc = device_fail(&ld, "gemm layout");
+                else m->device_bytes += own[i]->m.gbytes;
+            }
+        }
+        if (!rc && sdy_sync(m->st)) rc = device_fail(&ld, "gemm layout");
+    }
+    if (!rc) {
         /* views taken before the exactness checks ran: take them again (gemm_ok of the stack) */
         for (int l = 0; l < in->n_layer; l++) {
             dlayer *L = &m->layers[l];

@@ -57,6 +57,10 @@ struct GemmArgs {
     long grp_rows;
     int n_grp;
     int wide;  // host-side: the wide variant is needed (k_gemm3 only)
+    // k_gemm3: p holds the GEMM's copy of the planes (sdy_mat_gemm_layout: rows in tiles of 32,
+    // records unit- or super-block-major within a tile); row r of the matrix is row grow0 + r there
+    int blk;
+    long grow0;
 };
 
 SDY_DEV u32x2 ld8(const uint8_t *p) { return *reinterpret_cast<const u32x2 *>(p); }
@@ -293,27 +297,38 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
     // the lane's units of each super-block: ub + uu, uu < UN / 2
     constexpr int UL = UN / 2;
     const int ub = ks * UN + h * UL;
+    // per-lane offsets of the row's records, and the scalar strides of a unit and a super-block:
+    // planes row-major, or the GEMM copy (tiles of 32 rows, the tile's 32 records of one unit or
+    // super-block adjacent: a load instruction reads 512 contiguous bytes per half-wave)
     uint32_t oq[MT], oh[MT], od[MT];
+    const uint32_t ust = g.blk ? 512u : 16u, hst = g.blk ? 512u : 16u, dst2 = g.blk ? 64u : 2u;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         const long ri = rt + 32 * mt + lr;
         const uint32_t row = (uint32_t)(row0 + (ri < g.n_rows ? ri : g.n_rows - 1));
-        oq[mt] = row * (uint32_t)g.T * 16u + 16u * (uint32_t)(h * UL);
-        oh[mt] = row * (uint32_t)nb * 16u;
-        od[mt] = row * (uint32_t)nb * 2u;
+        if (g.blk) {
+            const uint32_t R = (uint32_t)g.grow0 + row, tb = R >> 5, r = R & 31u;
+            oq[mt] = (tb * (uint32_t)g.T * 32u + r) * 16u + 512u * (uint32_t)(h * UL);
+            oh[mt] = (tb * (uint32_t)nb * 32u + r) * 16u;
+            od[mt] = (tb * (uint32_t)nb * 32u + r) * 2u;
+        } else {
+            oq[mt] = row * (uint32_t)g.T * 16u + 16u * (uint32_t)(h * UL);
+            oh[mt] = row * (uint32_t)nb * 16u;
+            od[mt] = row * (uint32_t)nb * 2u;
+        }
     }
     auto load_sb3 = [&](int sb, SbRegs3 (&R)[MT]) {
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
 #pragma unroll
             for (int uu = 0; uu < UL; uu++) {  // units ub + uu (h UL in the lane's offset)
-                const int so = (4 * sb + ks * UN + uu) * 16;
+                const int so = (4 * sb + ks * UN + uu) * (int)ust;
                 R[mt].q[uu][0] = __builtin_amdgcn_raw_buffer_load_b128(rq[0], oq[mt], so, 0);
                 R[mt].q[uu][1] = __builtin_amdgcn_raw_buffer_load_b128(rq[1], oq[mt], so, 0);
                 if constexpr (WT == SDY_Q6_K) R[mt].q[uu][2] = __builtin_amdgcn_raw_buffer_load_b128(rq[2], oq[mt], so, 0);
             }
-            R[mt].hd = __builtin_amdgcn_raw_buffer_load_b128(rh, oh[mt], sb * 16, 0);
-            R[mt].d6 = WT == SDY_Q6_K ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rd, od[mt], sb * 2, 0) : 0u;
+            R[mt].hd = __builtin_amdgcn_raw_buffer_load_b128(rh, oh[mt], sb * (int)hst, 0);
+            R[mt].d6 = WT == SDY_Q6_K ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rd, od[mt], sb * (int)dst2, 0) : 0u;
         }
     };
     // activation stage of super-block sb into buffer buf (asynchronous; completes at s_waitcnt)
@@ -839,7 +854,23 @@ __global__ void k_gemm_check(GemmArgs g, int *bad) {
 
 // =============================================================================== host
 
-static GemmArgs gemm_args(const sdy_mat *m) {
+// Offsets and sizes of the planes of the GEMM's copy of a matrix of `rows` rows (tiles of 32 rows:
+// the 16-byte unit records [tile][unit][32], the per-super-block records [tile][super-block][32]).
+static size_t gemm_layout_planes(int type, int n_in, long rows, size_t off[5], size_t sz[5]) {
+    const size_t tiles = (size_t)(rows + 31) / 32, T = (size_t)n_in / 64, nb = (size_t)n_in / 256;
+    const size_t unit = tiles * T * 512, sbk = tiles * nb * 32;
+    const size_t s4[5] = {unit, unit, sbk * 16, 0, 0}, s6[5] = {unit, unit, unit, sbk * 16, sbk * 2};
+    size_t o = 0;
+    for (int i = 0; i < 5; i++) {
+        sz[i] = type == SDY_Q4_K ? s4[i] : s6[i];
+        off[i] = o;
+        o += (sz[i] + 255) & ~(size_t)255;
+    }
+    return o;
+}
+
+// The kernel arguments of m; with its GEMM copy (k_gemm3) when it has one and `layout` is set.
+static GemmArgs gemm_args(const sdy_mat *m, bool layout = false) {
     GemmArgs g;
     memset(&g, 0, sizeof(g));
     for (int i = 0; i < 5; i++) g.p[i] = (const uint8_t *)m->base + m->plane_off[i];
@@ -848,11 +879,59 @@ static GemmArgs gemm_args(const sdy_mat *m) {
     g.nb = m->n_in / 256;
     g.n_rows = m->n_rows;
     const size_t rows = (size_t)m->n_rows, unit = rows * g.T * 16, sbk = rows * g.nb;
-    const size_t sz[5] = {unit, unit, m->type == SDY_Q4_K ? sbk * 16 : unit, m->type == SDY_Q4_K ? 0 : sbk * 16,
-                          m->type == SDY_Q4_K ? 0 : sbk * 2};
+    size_t sz[5] = {unit, unit, m->type == SDY_Q4_K ? sbk * 16 : unit, m->type == SDY_Q4_K ? 0 : sbk * 16,
+                    m->type == SDY_Q4_K ? 0 : sbk * 2};
+    if (layout && m->gbase) {
+        size_t off[5];
+        gemm_layout_planes(m->type, m->n_in, m->grows, off, sz);
+        for (int i = 0; i < 5; i++) g.p[i] = (const uint8_t *)m->gbase + off[i];
+        g.blk = 1;
+        g.grow0 = m->grow0;
+    }
     for (int i = 0; i < 5; i++) g.psz[i] = sz[i] < 0xFFFFFFFFu ? (uint32_t)sz[i] : 0xFFFFFFFFu;
     g.wide = m->gemm_ok == 2;
     return g;
+}
+
+// Plane record r = row * n_rec + j (rs bytes, rs 16 or 2) into the tiled copy: [row / 32][j][row % 32].
+__global__ __launch_bounds__(256) void k_gemm_layout(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                     long n_rows, int n_rec, int rs) {
+    const long i = blockIdx.x * 256L + threadIdx.x;
+    if (i >= n_rows * (long)n_rec) return;
+    const long row = i / n_rec;
+    const int j = (int)(i - row * n_rec);
+    const size_t o = (((size_t)(row >> 5) * n_rec + j) * 32 + (row & 31)) * rs;
+    if (rs == 16) *reinterpret_cast<uint4 *>(dst + o) = *reinterpret_cast<const uint4 *>(src + (size_t)i * 16);
+    else *reinterpret_cast<uint16_t *>(dst + o) = *reinterpret_cast<const uint16_t *>(src + (size_t)i * 2);
+}
+
+extern "C" int sdy_mat_gemm_layout(sdy_mat *m, sdy_stream s) {
+    if (!m || !m->base || (m->type != SDY_Q4_K && m->type != SDY_Q6_K) || !m->gemm_ok) return 0;
+    if (m->grow0 != 0 || (m->gbase && m->grows != m->n_rows))
+        return sdy_fail(-1, "gemm_layout: made for a whole matrix, not a row view");
+    size_t off[5], sz[5];
+    const size_t bytes = gemm_layout_planes(m->type, m->n_in, m->n_rows, off, sz);
+    int rc;
+    if (!m->gbase) {
+        if ((rc = sdy_malloc(&m->gbase, bytes))) return rc;
+        m->gbytes = bytes;
+        m->grows = m->n_rows;
+        // the padding rows of the last tile: zero (never read: the GEMM clamps its rows)
+        if ((rc = sdy_memset(m->gbase, 0, bytes, s))) return rc;
+    }
+    const int T = m->n_units, nb = m->n_in / 256;
+    const int nrec[5] = {T, T, m->type == SDY_Q4_K ? nb : T, nb, nb};
+    const int rsz[5] = {16, 16, 16, 16, 2};
+    for (int i = 0; i < 5; i++) {
+        if (!sz[i]) continue;
+        const long total = m->n_rows * (long)nrec[i];
+        SDY_NOTE_KERNEL(k_gemm_layout);
+        hipLaunchKernelGGL(k_gemm_layout, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)s,
+                           (const uint8_t *)m->base + m->plane_off[i], (uint8_t *)m->gbase + off[i], m->n_rows,
+                           nrec[i], rsz[i]);
+        if ((rc = sdy_check_launch("gemm_layout"))) return rc;
+    }
+    return 0;
 }
 
 // Flags (bad = 1) rows [r0, r0 + n) of m that the GEMM cannot multiply exactly. Synchronous.
@@ -974,7 +1053,7 @@ extern "C" int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_st
     if (a->row0 == a->row1) return 0;
     if (a->epilogue == SDY_EPI_SWIGLU && (((a->row1 - a->row0) | a->row0) & 1 || a->bias || a->resid))
         return sdy_fail(-1, "gemm: the SwiGLU epilogue needs an even row range from an even row, no bias, no residual");
-    GemmArgs g = gemm_args(m);
+    GemmArgs g = gemm_args(m, true);
     const int nb = g.nb, n_tok = a->n_tok;
     const SdyGemmExp e = sdy_gemm_exp(ws, n_tok, g.n_in);
     g.y16 = e.y16;
@@ -1018,7 +1097,7 @@ extern "C" int sdy_gemm_grouped(const sdy_mat *m, long grp_rows, int n_grp, cons
     if (act_row && (!a->ws_ready || n_act < 1))
         return sdy_fail(-1, "gemm_grouped: activation rows by index read an expansion of n_act >= 1 rows that the "
                             "caller made (ws_ready)");
-    GemmArgs g = gemm_args(m);
+    GemmArgs g = gemm_args(m, true);
     const SdyGemmExp e = sdy_gemm_exp(ws, act_row ? n_act : n_tok, g.n_in);
     g.y16 = e.y16;
     g.yd = e.yd;

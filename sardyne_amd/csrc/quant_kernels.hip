@@ -1784,10 +1784,20 @@ extern "C" int sdy_mat_alloc(sdy_mat *m, int type, int n_in, long n_rows) {
     return 0;
 }
 
+// The GEMM's copy of m, stale once rows change: freed (the GEMM then reads the planes).
+static int drop_gemm_layout(sdy_mat *m) {
+    if (!m->gbase) return 0;
+    const int rc = sdy_free(m->gbase);
+    m->gbase = nullptr;
+    m->gbytes = 0;
+    return rc;
+}
+
 // Repacks n raw GGUF-layout rows (device memory) into rows r0 + map(i) of m (RowMap above),
 // queued on s (no allocation, no synchronisation).
 static int repack_rows_async(sdy_mat *m, long r0, RowMap map, long n, const void *dev_raw, sdy_stream s) {
     hipStream_t st = (hipStream_t)s;
+    if (int rc = drop_gemm_layout(m)) return rc;
     const int type = m->type;
     const size_t src_row = sdy_raw_row_bytes(type, m->n_in);
     if (is_float_type(type)) {
@@ -1885,9 +1895,10 @@ extern "C" int sdy_mat_upload(sdy_mat *m, int type, int n_in, long n_rows, const
 
 extern "C" int sdy_mat_free(sdy_mat *m) {
     if (!m || !m->base) return 0;
-    int rc = sdy_free(m->base);
+    int rc = drop_gemm_layout(m);
+    const int rc2 = sdy_free(m->base);
     m->base = nullptr;
-    return rc;
+    return rc ? rc : rc2;
 }
 
 extern "C" sdy_mat sdy_mat_rows(const sdy_mat *m, long r0, long n) {
@@ -1897,6 +1908,7 @@ extern "C" sdy_mat sdy_mat_rows(const sdy_mat *m, long r0, long n) {
     size_t pb[5];
     plane_row_bytes(m->type, m->n_in, pb);
     for (int i = 0; i < 5; i++) v.plane_off[i] = m->plane_off[i] + pb[i] * (size_t)r0;
+    v.grow0 = m->grow0 + r0;  // the GEMM's copy (shared) is addressed by rows of the whole matrix
     v.n_rows = n;
     return v;
 }

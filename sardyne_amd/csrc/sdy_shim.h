@@ -57,6 +57,12 @@ typedef struct {
     size_t plane_off[5];
     int gemm_ok;    /* Q4_K / Q6_K: 1 when the GEMM's one-fragment scheme is exact for every block,
                        2 when some block needs the wide variant (Q6_K: twice the MFMA work); 0 other types */
+    void *gbase;    /* the GEMM's copy of the planes (sdy_mat_gemm_layout) or NULL: rows in tiles of 32,
+                       each tile's records unit-major ([tile][unit][32 rows][16 bytes], the per-super-block
+                       records [tile][super-block][32 rows]) */
+    size_t gbytes;
+    long grow0;     /* the first row of a row view in that copy */
+    long grows;     /* rows of the matrix the copy was made from */
 } sdy_mat;
 
 /* Bytes of the device layout for a matrix. */
@@ -78,6 +84,10 @@ int sdy_mat_from_device(sdy_mat *m, int type, int n_in, long n_rows, const void 
  * synchronisation, no exactness check). */
 int sdy_mat_repack_async(sdy_mat *m, long r0, long n, long step, long grp, long gstride, const void *dev_raw,
                          sdy_stream s);
+/* The GEMM's copy of a Q4_K / Q6_K matrix (gbase), made from its planes after the last upload, for
+ * the prefill GEMM's loads (a load instruction then reads whole cache lines). Another upload into
+ * the matrix frees it (the GEMM reads the planes until it is made again). Other types: no-op. */
+int sdy_mat_gemm_layout(sdy_mat *m, sdy_stream s);
 
 /* Pipelined uploads (upload.hip): a ring of pinned host slots and device slots. A host thread pool
  * copies the next rows from the file mapping into a free pinned slot (advising the kernel to read

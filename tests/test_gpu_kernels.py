@@ -1060,6 +1060,38 @@ def test_quantize_gemm_expansion(norm, n_in, n_tok):
     assert np.array_equal(bits(gemm(0)), bits(exp))
 
 
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
+def test_gemm_layout_copy_and_planes_same_bits(kind):
+    """The GEMM reads the tiled copy that sdy_mat_gemm_layout makes (the default of DeviceMatrix and
+    of the engine) or, without one, the planes: the same bits, the oracle's, with a row count that
+    is not a multiple of the 32-row tile and a row range; an upload into the matrix drops the copy
+    (it would be stale) and the GEMM goes on with the planes."""
+    L = lib()
+    n_in, n_out, n_tok = 1024, 77, 45
+    t, w, xq = _gemm_case(kind, n_in, n_out, n_tok, seed=21)
+    exp = O.matmul_q(w, t, xq, n_in, simd=1)
+    dq = capi.DeviceBuffer.from_array(xq)
+    ws = capi.DeviceBuffer(L.sdy_gemm_ws_bytes(n_tok, n_in))
+
+    def run(m, row0=0, row1=n_out):
+        dout = capi.DeviceBuffer.from_array(np.full((n_tok, n_out), np.nan, np.float32))
+        a = capi.SdyMvArgs(xq=dq.ptr, n_tok=n_tok, out=dout.ptr, out_stride=n_out, row0=row0, row1=row1)
+        capi.check(L.sdy_gemm(ctypes.byref(m.m), ctypes.byref(a), ws.ptr, None))
+        return dout.to_array(np.float32, (n_tok, n_out))
+
+    tiled = capi.DeviceMatrix(t, n_in, n_out, w)
+    assert tiled.m.gbase and tiled.m.grows == n_out
+    planes = capi.DeviceMatrix(t, n_in, n_out, w, gemm_layout=False)
+    assert not planes.m.gbase
+    assert np.array_equal(bits(run(tiled)), bits(exp))
+    assert np.array_equal(bits(run(planes)), bits(exp))
+    assert np.array_equal(bits(run(tiled, 33, 70)[:, 33:70]), bits(exp[:, 33:70]))
+    raw = np.ascontiguousarray(w[5:6]).view(np.uint8)
+    capi.check(L.sdy_mat_upload_rows(ctypes.byref(tiled.m), 5, 1, 1, raw.ctypes.data, None))
+    assert not tiled.m.gbase
+    assert np.array_equal(bits(run(tiled)), bits(exp))
+
+
 @pytest.mark.parametrize("variant", ["11", "12", "13", "14", "15", "16", "17", "18", "19", "20"])
 @pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
 def test_gemm_tile_variants_bit_exact(kind, variant, monkeypatch):
