@@ -998,23 +998,23 @@ static int launch_gemm3(GemmArgs &g, hipStream_t st) {
                   : launch_gemm3_s<WT, MT, NT, WM, false, KS, PF>(g, st);
 }
 
-template <int WT, int MT, int NT, int WM, bool WIDE>
+template <int WT, int MT, int NT, int WM, bool WIDE, int KS>
 static int launch_gemm3_grid_s(GemmArgs &g, unsigned tok_tiles, unsigned row_tiles, hipStream_t st) {
     constexpr int BN = 32 * NT, YDN = BN < 64 ? 64 : BN;
     constexpr size_t lds = 2 * (size_t)(BN * 512 + YDN * 4 + BN * 32);
     static size_t granted = 0;
-    const void *fn = (const void *)k_gemm3<WT, MT, NT, WM, WIDE>;
+    const void *fn = (const void *)k_gemm3<WT, MT, NT, WM, WIDE, KS>;
     int rc = sdy_lds_limit(fn, lds, &granted);
     if (rc) return rc;
-    SDY_NOTE_KERNEL((k_gemm3<WT, MT, NT, WM, WIDE>));
-    hipLaunchKernelGGL((k_gemm3<WT, MT, NT, WM, WIDE>), dim3(tok_tiles, row_tiles), dim3(64 * WM), lds, st, g);
+    SDY_NOTE_KERNEL((k_gemm3<WT, MT, NT, WM, WIDE, KS>));
+    hipLaunchKernelGGL((k_gemm3<WT, MT, NT, WM, WIDE, KS>), dim3(tok_tiles, row_tiles), dim3(64 * WM), lds, st, g);
     return sdy_check_launch("gemm");
 }
 
-template <int WT, int MT, int NT, int WM>
+template <int WT, int MT, int NT, int WM, int KS>
 static int launch_gemm3_grid(GemmArgs &g, unsigned tok_tiles, unsigned row_tiles, hipStream_t st) {
-    return g.wide ? launch_gemm3_grid_s<WT, MT, NT, WM, true>(g, tok_tiles, row_tiles, st)
-                   : launch_gemm3_grid_s<WT, MT, NT, WM, false>(g, tok_tiles, row_tiles, st);
+    return g.wide ? launch_gemm3_grid_s<WT, MT, NT, WM, true, KS>(g, tok_tiles, row_tiles, st)
+                   : launch_gemm3_grid_s<WT, MT, NT, WM, false, KS>(g, tok_tiles, row_tiles, st);
 }
 
 template <int WT>
@@ -1035,12 +1035,13 @@ static int gemm_type(GemmArgs &g, hipStream_t st) {
     case 20: return launch_gemm3<WT, 1, 1, 4, 2, 2>(g, st);
     default: break;
     }
-    // 128-row workgroup tiles (4 waves of 32 rows); 64 tokens per tile when there are enough row
-    // tiles to fill the GPU twice over with them, else 32 (measured on the 2048- to 22016-row
-    // matrices of a 512-token prefill)
+    // 128-row workgroup tiles (4 waves of 32 rows) of 64 tokens when there are enough row tiles to
+    // fill the GPU twice over with them; else 64-row tiles of 32 tokens, two waves to a row tile
+    // splitting each super-block's units (twice the waves for the grids of one wave per SIMD).
+    // Measured on the 256- to 22016-row matrices of a 512-token prefill.
     const long r128 = (g.n_rows + 127) / 128, t64 = (g.n_tok + 63) / 64;
     if (r128 * t64 >= 1024) return launch_gemm3<WT, 1, 2, 4>(g, st);
-    return launch_gemm3<WT, 1, 1, 4>(g, st);
+    return launch_gemm3<WT, 1, 1, 4, 2>(g, st);
 }
 
 // out[t][row] for rows [a->row0, a->row1) and a->n_tok tokens of Q8_K activations a->xq, through
@@ -1126,9 +1127,11 @@ extern "C" int sdy_gemm_grouped(const sdy_mat *m, long grp_rows, int n_grp, cons
     g.n_grp = n_grp;
     // token tiles: at most one partial tile per group beyond the full ones (the grid's extra
     // workgroups return at once)
+    // (128-row tiles, one wave to a row tile: the unit split of the dense GEMM's small grids measured
+    // slower here, 38.5 against 36.3 ms for the 30B-A3B-shaped 1024-token prefill)
     constexpr int BN = 32;
     const unsigned tok_tiles = (unsigned)((n_tok + BN - 1) / BN + n_grp - 1);
     const unsigned row_tiles = (unsigned)((grp_rows + 127) / 128);
-    return m->type == SDY_Q4_K ? launch_gemm3_grid<SDY_Q4_K, 1, 1, 4>(g, tok_tiles, row_tiles, st)
-                               : launch_gemm3_grid<SDY_Q6_K, 1, 1, 4>(g, tok_tiles, row_tiles, st);
+    return m->type == SDY_Q4_K ? launch_gemm3_grid<SDY_Q4_K, 1, 1, 4, 1>(g, tok_tiles, row_tiles, st)
+                               : launch_gemm3_grid<SDY_Q6_K, 1, 1, 4, 1>(g, tok_tiles, row_tiles, st);
 }
