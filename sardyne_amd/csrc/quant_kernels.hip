@@ -1066,10 +1066,10 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
     uint4 Yr[4];
     uint2 bsr;
     float ydr;
-    if constexpr (PRO != 0) {
-        // the workgroup's activation row first: requested before any weight, its loads do not
-        // return behind this workgroup's weight stream (measured on the 22016 x 2048 gate|up with
-        // the FFN norm: 9.5 -> 8.9 us against building the row while the weights are in flight)
+    if constexpr (PRO == 2) {
+        // the normalised row first: requested before any weight, its loads do not return behind
+        // this workgroup's weight stream (measured on the 22016 x 2048 gate|up with the FFN norm:
+        // 9.5 -> 8.9 us against building the row while the weights are in flight)
         arow.build(px, a.peps, a.P.n_in, lds_act);
         q8k_unit_lds(lds_act, a.P.nb, u, Yr, bsr, ydr);
     }
@@ -1086,6 +1086,13 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
     } else {
 #pragma unroll
         for (int k = 1; k < NIT; k++) load_k(k);
+        if constexpr (PRO == 1) {
+            // the quantiser alone (no norm): every weight load goes out first and the workgroup
+            // quantises the row while they are in flight (3B decode 637 -> 646 tok/s against building
+            // it first, with the 2048 x 2048 wo)
+            arow.build(px, a.peps, a.P.n_in, lds_act);
+            q8k_unit_lds(lds_act, a.P.nb, u, Yr, bsr, ydr);
+        }
     }
     // the bias and residual of the lane's rows (an absent one reads a stand-in: the activation row)
     const float *stand_in = PRO ? px : reinterpret_cast<const float *>(xq);
