@@ -61,6 +61,7 @@ struct GemmArgs {
     // records unit- or super-block-major within a tile); row r of the matrix is row grow0 + r there
     int blk;
     long grow0;
+    int exp_rows;  // rows of the activations' expansion (y16, yd, bs16)
 };
 
 SDY_DEV u32x2 ld8(const uint8_t *p) { return *reinterpret_cast<const u32x2 *>(p); }
@@ -190,6 +191,17 @@ SDY_DEV void lds_read4(uint32_t a, uint32_t b, f32x4 &a0, f32x4 &a1, f32x4 &b0, 
 // expcnt at its maximum, lgkmcnt in bits 11:8).
 constexpr int sdy_vmcnt_imm(int n, int lgkm = 0) { return (n & 15) | (((n >> 4) & 3) << 14) | (7 << 4) | (lgkm << 8); }
 
+// SIZE bytes per lane from buffer r at vo + so into LDS at dst + SIZE * lane (the host pass of this
+// file does not know the builtin: it has no body there)
+template <int SIZE>
+SDY_DEV void buf_to_lds(__amdgpu_buffer_rsrc_t r, lds_ptr_t dst, uint32_t vo, int so) {
+    static_assert(SIZE == 4 || SIZE == 16, "dword or dwordx4");
+#if __HIP_DEVICE_COMPILE__
+    if constexpr (SIZE == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, vo, so, 0, 0);
+    else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 4, vo, so, 0, 0);
+#endif
+}
+
 SDY_DEV __amdgpu_buffer_rsrc_t plane_rsrc(const uint8_t *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)bytes, 0x00020000);
 }
@@ -287,6 +299,25 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < NBSW; i++) ar_b2[i] = act_of(((i * WM + wave) * 64 + lane) >> 3);
     }
+    // the stage's loads as buffer loads to LDS: the lanes' byte offsets are fixed, the super-block
+    // advance is a scalar offset (no per-super-block address arithmetic)
+    const __amdgpu_buffer_rsrc_t ry = plane_rsrc(reinterpret_cast<const uint8_t *>(g.y16), (uint32_t)g.exp_rows * g.n_in * 2u),
+                                 ryd = plane_rsrc(reinterpret_cast<const uint8_t *>(g.yd), (uint32_t)g.exp_rows * nb * 4u),
+                                 rbs = plane_rsrc(reinterpret_cast<const uint8_t *>(g.bs16), (uint32_t)g.exp_rows * nb * 32u);
+    uint32_t vst[NI], vyd[YDN / 64], vbs[BN / 32 > 0 ? BN / 32 : 1], vb2[PF == 2 && NBSW > 0 ? NBSW : 1];
+#pragma unroll
+    for (int j = 0; j < NI; j++) {
+        const int p = (j * WM + wave) * 64 + lane, t = p >> 5, c = (p & 31) ^ (t & 7);
+        vst[j] = ((uint32_t)ar_st[j] * (uint32_t)g.n_in + 8u * (uint32_t)c) * 2u;
+    }
+#pragma unroll
+    for (int i = 0; i < YDN / 64; i++) vyd[i] = (uint32_t)ar_yd[i] * (uint32_t)nb * 4u;
+#pragma unroll
+    for (int i = 0; i < BN / 32; i++) vbs[i] = (uint32_t)ar_bs[i] * (uint32_t)nb * 32u + 16u * (uint32_t)(lane & 1);
+    if constexpr (PF == 2 && WT == SDY_Q4_K) {
+#pragma unroll
+        for (int i = 0; i < NBSW; i++) vb2[i] = (uint32_t)ar_b2[i] * (uint32_t)nb * 32u + 4u * (uint32_t)(lane & 7);
+    }
 
     // weight buffer resources and this lane's per-row offsets
     __amdgpu_buffer_rsrc_t rq[3], rh, rd;
@@ -297,6 +328,10 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
     // the lane's units of each super-block: ub + uu, uu < UN / 2
     constexpr int UL = UN / 2;
     const int ub = ks * UN + h * UL;
+    // the lane's LDS byte offsets in a stage of its activation fragments' chunks k = 2 s + hh of unit ub
+    uint32_t rbo[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) rbo[k] = 16u * (uint32_t)(lr * 32 + 8 * ub + (k ^ (lr & 7)));
     // per-lane offsets of the row's records, and the scalar strides of a unit and a super-block:
     // planes row-major, or the GEMM copy (tiles of 32 rows, the tile's 32 records of one unit or
     // super-block adjacent: a load instruction reads 512 contiguous bytes per half-wave)
@@ -337,40 +372,29 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < NI; j++) {
             const int blk = j * WM + wave;  // 64-chunk block written by this wave instruction
-            const int p = blk * 64 + lane, t = p >> 5, c = (p & 31) ^ (t & 7);
-            __builtin_amdgcn_global_load_lds((const void *)(g.y16 + (size_t)ar_st[j] * g.n_in + 256 * sb + 8 * c),
-                                             (lds_ptr_t)(base + blk * 1024), 16, 0, 0);
+            buf_to_lds<16>(ry, (lds_ptr_t)(base + blk * 1024), vst[j], sb * 512);
         }
         if constexpr (PF == 2) {
 #pragma unroll
             for (int i = 0; i < YDN / 64; i++)
-                __builtin_amdgcn_global_load_lds((const void *)(g.yd + (size_t)ar_yd[i] * nb + sb),
-                                                 (lds_ptr_t)(base + YDOFF + wave * (YDN * 4) + 256 * i), 4, 0, 0);
+                buf_to_lds<4>(ryd, (lds_ptr_t)(base + YDOFF + wave * (YDN * 4) + 256 * i), vyd[i], sb * 4);
             if constexpr (WT == SDY_Q4_K) {
 #pragma unroll
-                for (int i = 0; i < NBSW; i++) {
-                    const int p = (i * WM + wave) * 64 + lane;  // bsum dword p: token p / 8, bytes 4 (p % 8)
-                    __builtin_amdgcn_global_load_lds(
-                        (const void *)(reinterpret_cast<const uint8_t *>(g.bs16) + ((size_t)ar_b2[i] * nb + sb) * 32 +
-                                       4 * (p & 7)),
-                        (lds_ptr_t)(base + BSOFF + 256 * (i * WM + wave)), 4, 0, 0);
-                }
+                for (int i = 0; i < NBSW; i++)  // bsum dword p = (i WM + wave) 64 + lane: token p / 8, bytes 4 (p % 8)
+                    buf_to_lds<4>(rbs, (lds_ptr_t)(base + BSOFF + 256 * (i * WM + wave)), vb2[i], sb * 32);
             }
         } else {
             if (wave == 0) {
 #pragma unroll
                 for (int i = 0; i < YDN / 64; i++)
-                    __builtin_amdgcn_global_load_lds((const void *)(g.yd + (size_t)ar_yd[i] * nb + sb),
-                                                     (lds_ptr_t)(base + YDOFF + 256 * i), 4, 0, 0);
+                    buf_to_lds<4>(ryd, (lds_ptr_t)(base + YDOFF + 256 * i), vyd[i], sb * 4);
             }
         }
         if constexpr (WT == SDY_Q4_K && PF == 1) {
             if (wave == (WM > 1 ? 1 : 0)) {
 #pragma unroll
                 for (int i = 0; i < BN / 32; i++)
-                    __builtin_amdgcn_global_load_lds(
-                        (const void *)(g.bs16 + ((size_t)ar_bs[i] * nb + sb) * 16 + 8 * (lane & 1)),
-                        (lds_ptr_t)(base + BSOFF + 1024 * i), 16, 0, 0);
+                    buf_to_lds<16>(rbs, (lds_ptr_t)(base + BSOFF + 1024 * i), vbs[i], sb * 32);
             }
         }
     };
@@ -401,7 +425,6 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
         for (int nt = 0; nt < NT; nt++)
 #pragma unroll
             for (int i = 0; i < RH; i++) acc[mt][nt][i] = 0.0f;
-    const half2v off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
     const half2v off6 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
     const half2v off4c = {(_Float16)-1032.0f, (_Float16)-1032.0f};  // centred Q4_K quants q - 8
     // per-wave d[32 MT] then dmin[32 MT] as f32 (static LDS: a separate object from the DMA target,
@@ -478,13 +501,15 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
         // step sl = 8 uu + 4 hh + s of the lane: k-half hh of unit ub + uu, quarter s (its 16-element
         // chunk 8 (ub + uu) + 2 s + hh of each token), read from LDS one step ahead of its MFMAs
         half8 bf[2][NT];
-        auto read_b = [&](int sl, half8 (&dst)[NT]) {
-            const int c = 8 * (ub + (sl >> 3)) + 2 * (sl & 3) + ((sl >> 2) & 1);
+        // chunk 8 (ub + uu) + k of token 32 nt + lr sits at bbuf + rbo[k] + 128 uu + 16384 nt (the swizzle
+        // only permutes the low three bits of the chunk index: k ^ (lr & 7))
+        const uint8_t *rbp[8];
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                const int t = 32 * nt + lr;
-                dst[nt] = *reinterpret_cast<const half8 *>(bbuf + 16 * (t * 32 + (c ^ (t & 7))));
-            }
+        for (int k = 0; k < 8; k++) rbp[k] = bbuf + rbo[k];
+        auto read_b = [&](int sl, half8 (&dst)[NT]) {
+            const int k = 2 * (sl & 3) + ((sl >> 2) & 1), uu = sl >> 3;
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) dst[nt] = *reinterpret_cast<const half8 *>(rbp[k] + 128 * uu + 16384 * nt);
         };
         read_b(0, bf[0]);
 #pragma unroll
@@ -1057,6 +1082,7 @@ extern "C" int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_st
     GemmArgs g = gemm_args(m, true);
     const int nb = g.nb, n_tok = a->n_tok;
     const SdyGemmExp e = sdy_gemm_exp(ws, n_tok, g.n_in);
+    g.exp_rows = n_tok;
     g.y16 = e.y16;
     g.yd = e.yd;
     g.bs16 = e.bs16;
@@ -1100,6 +1126,7 @@ extern "C" int sdy_gemm_grouped(const sdy_mat *m, long grp_rows, int n_grp, cons
                             "caller made (ws_ready)");
     GemmArgs g = gemm_args(m, true);
     const SdyGemmExp e = sdy_gemm_exp(ws, act_row ? n_act : n_tok, g.n_in);
+    g.exp_rows = act_row ? n_act : n_tok;
     g.y16 = e.y16;
     g.yd = e.yd;
     g.bs16 = e.bs16;
