@@ -142,6 +142,8 @@ _DEVICE_SIGNATURES = {
     "sdy_quantize": (_int, [_int, _vp, _vp, _int, _int, _vp]),
     "sdy_matvec": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp]),
     "sdy_mat_gemm_layout": (_int, [ctypes.POINTER(SdyMat), _vp]),
+    "sdy_gemm2": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), ctypes.POINTER(SdyMat),
+                         ctypes.POINTER(SdyMvArgs), _vp, _vp]),
     "sdy_matvec_pair_ok": (_int, [ctypes.POINTER(SdyMat), _int, ctypes.POINTER(SdyMat), _int]),
     "sdy_matvec_fused_ok": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), ctypes.POINTER(SdyMat),
                                    ctypes.POINTER(SdyMvArgs)]),

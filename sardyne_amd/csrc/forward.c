@@ -203,6 +203,41 @@ static int mm(engine_ctx *c, float *out, const float *x, const dmat *w, int n_to
     return mm_epi(c, out, x, w, n_tok, bias, resid, new_input, SDY_EPI_NONE);
 }
 
+/* out1 = W1 . x and out2 = W2 . x (+ biases) for n_tok rows of x, which the previous matmul (or norm)
+ * quantised already: a layer's q|k and its v. When both take the GEMM on the same quantised rows,
+ * one launch multiplies both (sdy_gemm2); otherwise two matmuls. */
+static int mm_pair(engine_ctx *c, float *out1, const dmat *w1, const float *b1, float *out2, const dmat *w2,
+                   const float *b2, const float *x, int n_tok) {
+    const int s = 1;  /* the Q8_K copy */
+    if (!(use_gemm(w1, n_tok) && use_gemm(w2, n_tok) && w1->n_in == w2->n_in &&
+          vec_dot_type(w1->type) == SDY_Q8_K && vec_dot_type(w2->type) == SDY_Q8_K && c->xq_src[s] == x &&
+          c->xq_n_tok[s] == n_tok && c->xq_n_in[s] == w1->n_in)) {
+        TRY(mm(c, out1, x, w1, n_tok, b1, NULL, 0));
+        return mm(c, out2, x, w2, n_tok, b2, NULL, 0);
+    }
+    sdy_mv_args a[2];
+    const dmat *w[2] = {w1, w2};
+    float *out[2] = {out1, out2};
+    const float *b[2] = {b1, b2};
+    for (int i = 0; i < 2; i++) {
+        memset(&a[i], 0, sizeof a[i]);
+        a[i].xq = c->xq[s];
+        a[i].n_tok = n_tok;
+        a[i].out = out[i];
+        a[i].out_stride = w[i]->n_out;
+        a[i].bias = b[i];
+        a[i].row0 = 0;
+        a[i].row1 = w[i]->n_out;
+        a[i].epilogue = SDY_EPI_NONE;
+    }
+    a[0].ws_ready = c->gemm_ready && c->gemm_epoch == c->xq_epoch && c->gemm_xq == a[0].xq &&
+                    c->gemm_n_tok == n_tok && c->gemm_n_in == w1->n_in;
+    c->gemm_ready = 0;
+    TRY(sdy_gemm2(&w1->m, &a[0], &w2->m, &a[1], c->gemm_ws, c->st));
+    gemm_record(c, a[0].xq, n_tok, w1->n_in);
+    return 0;
+}
+
 /* xb = RMSNorm(x) * wn for n rows, quantized for the matrix `next` in the same launch; the copy
  * is registered in the activation-quantisation cache, so mm(next, xb, new_input = 0) reuses it. */
 static int norm_for(engine_ctx *c, const float *x, const float *wn, const dmat *next, int n) {
@@ -563,16 +598,17 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
             float *q = c->q, *k = c->k, *v = c->v;
             long qs = q_dim, ks = kv_dim, vs = kv_dim;
             if (L->qkv_parts >= 2 && bias_fused && use_gemm(&L->wqkv, n)) {
-                /* q | k (| v) of every token from one GEMM: rows of c->qkv, wqkv.n_out floats apart */
-                TRY(mm(c, c->qkv, c->xb, &L->wqkv, n, L->bq, NULL, 0));
+                /* q | k (| v) of every token from one GEMM: rows of c->qkv, wqkv.n_out floats apart; a v of
+                   another type in the same launch */
                 q = c->qkv;
                 k = c->qkv + q_dim;
                 qs = ks = L->wqkv.n_out;
                 if (L->qkv_parts == 3) {
+                    TRY(mm(c, c->qkv, c->xb, &L->wqkv, n, L->bq, NULL, 0));
                     v = c->qkv + q_dim + kv_dim;
                     vs = L->wqkv.n_out;
                 } else {
-                    TRY(mm(c, c->v, c->xb, &L->wv, n, L->bv, NULL, 0));
+                    TRY(mm_pair(c, c->qkv, &L->wqkv, L->bq, c->v, &L->wv, L->bv, c->xb, n));
                 }
             } else {
                 TRY(mm(c, c->q, c->xb, &L->wq, n, L->bq, NULL, 0));

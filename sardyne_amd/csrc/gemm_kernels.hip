@@ -231,8 +231,18 @@ SDY_DEV __amdgpu_buffer_rsrc_t plane_rsrc(const uint8_t *p, uint32_t bytes) {
 // waits by count for the loads of the next super-block only, and the workgroup barrier orders LDS
 // alone. For grids of one wave per SIMD, whose super-blocks otherwise each wait a full memory round
 // trip.
-template <int WT, int MT, int NT, int WM, bool WIDE, int KS = 1, int PF = 1>
-__global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
+//
+// The body below takes the workgroup's place in its grid (bx, by of gx, gy: a pair launch gives
+// each matrix a part of one grid) and its LDS: the stages (dynamic), the per-wave d table and the
+// KS 2 exchange (static objects of the kernel, sized by gemm3_dtab_floats / gemm3_xch_floats).
+template <int MT, int WM>
+constexpr int gemm3_dtab_floats() { return WM * 64 * MT; }
+template <int WT, int MT, int NT, int WM, bool WIDE, int KS>
+constexpr int gemm3_xch_floats() { return KS == 2 ? 2 * WM * (WIDE && WT == SDY_Q6_K ? 2 : 1) * MT * NT * 8 * 64 : 1; }
+
+template <int WT, int MT, int NT, int WM, bool WIDE, int KS, int PF>
+SDY_DEV void gemm3_body(const GemmArgs &g, int bx, int by, int gx, int gy, uint8_t *lds, float *dtab_all,
+                        float *xch) {
     static_assert(KS == 1 || (KS == 2 && WM % 2 == 0), "unit split");
     static_assert(PF == 1 || PF == 2, "prefetch depth");
     constexpr int UN = 4 / KS, PAIRS = WM / KS;  // units per wave, row tiles per workgroup
@@ -246,12 +256,11 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
     static_assert(PF == 1 || (BN * 8) % (64 * WM) == 0, "PF 2: the bsums in whole dword loads per wave");
     constexpr int NI = BN * 32 / NTH;                       // activation DMA chunks per lane per stage
     static_assert((BN * 32) % NTH == 0 && NI >= 1, "tile");
-    extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, h = lane >> 5,
               lr = lane & 31;
     // token tiles of a row tile on one XCD (workgroups are dealt round-robin to the 8 XCDs)
-    const int n_tt = gridDim.x;
-    const long n_rt = gridDim.y, L = (long)blockIdx.y * n_tt + blockIdx.x;
+    const int n_tt = gx;
+    const long n_rt = gy, L = (long)by * n_tt + bx;
     long rti, tti;
     {
         const long grp = 8L * n_tt, full = n_rt / 8 * grp;
@@ -429,11 +438,9 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
     const half2v off4c = {(_Float16)-1032.0f, (_Float16)-1032.0f};  // centred Q4_K quants q - 8
     // per-wave d[32 MT] then dmin[32 MT] as f32 (static LDS: a separate object from the DMA target,
     // so its reads need not wait for the activation loads in flight)
-    __shared__ __align__(16) float dtab_all[WM * 64 * MT];
     float *dtab = dtab_all + wave * (64 * MT);
-    // KS 2: the half accumulators a wave hands its partner, [parity][wave][sum][mt][nt][8][64]
+    // KS 2: the half accumulators a wave hands its partner (xch), [parity][wave][sum][mt][nt][8][64]
     constexpr int NXS = WIDE && WT == SDY_Q6_K ? 2 : 1;
-    __shared__ float xch[KS == 2 ? 2 * WM * NXS * MT * NT * 8 * 64 : 1];
 
     constexpr int NBUF = PF + 1;  // stage buffers
     // one super-block: sb's weights in A, the loads of sb + PF issued into An (clamped to the last
@@ -810,6 +817,32 @@ __global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
         }
 }
 
+template <int WT, int MT, int NT, int WM, bool WIDE, int KS = 1, int PF = 1>
+__global__ __launch_bounds__(64 * WM) void k_gemm3(GemmArgs g) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ __align__(16) float dtab_all[gemm3_dtab_floats<MT, WM>()];
+    __shared__ float xch[gemm3_xch_floats<WT, MT, NT, WM, WIDE, KS>()];
+    gemm3_body<WT, MT, NT, WM, WIDE, KS, PF>(g, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.x, (int)gridDim.y, lds,
+                                             dtab_all, xch);
+}
+
+// Two GEMMs on the same activations in one launch (a layer's q|k and a v of another type): row
+// tiles [0, gy1) of the grid multiply g1, the rest g2; both take the <MT, NT, WM, KS> tile form.
+template <int WT1, bool WIDE1, int WT2, bool WIDE2, int MT, int NT, int WM, int KS>
+__global__ __launch_bounds__(64 * WM) void k_gemm3_pair(GemmArgs g1, GemmArgs g2, int gy1) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int X1 = gemm3_xch_floats<WT1, MT, NT, WM, WIDE1, KS>(), X2 = gemm3_xch_floats<WT2, MT, NT, WM, WIDE2, KS>();
+    __shared__ __align__(16) float dtab_all[gemm3_dtab_floats<MT, WM>()];
+    __shared__ float xch[X1 > X2 ? X1 : X2];
+    if ((int)blockIdx.y < gy1)
+        gemm3_body<WT1, MT, NT, WM, WIDE1, KS, 1>(g1, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.x, gy1, lds,
+                                                  dtab_all, xch);
+    else
+        gemm3_body<WT2, MT, NT, WM, WIDE2, KS, 1>(g2, (int)blockIdx.x, (int)blockIdx.y - gy1, (int)gridDim.x,
+                                                  (int)gridDim.y - gy1, lds, dtab_all, xch);
+}
+
+
 // Q8_K rows -> f16 values, f32 scales and f16 bsums for the GEMM (all exact: |q| <= 127, |bsum| <=
 // 2032). One thread per 16 values of a super-block (n_sb = n_tok * nb super-blocks in a row): four
 // 4-byte loads, two 16-byte stores, and the super-block's bsum number `part`; 256 threads.
@@ -1071,28 +1104,32 @@ static int gemm_type(GemmArgs &g, hipStream_t st) {
 
 // out[t][row] for rows [a->row0, a->row1) and a->n_tok tokens of Q8_K activations a->xq, through
 // the MFMA GEMM; ws: sdy_gemm_ws_bytes(n_tok, n_in) bytes of device scratch.
-extern "C" int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_stream s) {
-    hipStream_t st = (hipStream_t)s;
+// The checks and kernel arguments of one sdy_gemm call; the activations' expansion is made first
+// unless ws_ready. *empty: an empty row range (nothing to launch).
+static int gemm_setup(const sdy_mat *m, const sdy_mv_args *a, void *ws, hipStream_t st, GemmArgs &g, bool *empty) {
+    *empty = false;
     if (!sdy_gemm_ok(m, a->n_tok)) return sdy_fail(-1, "gemm: matrix not eligible (type %d)", m->type);
     if (a->row0 < 0 || a->row1 > m->n_rows || a->row0 > a->row1)
         return sdy_fail(-1, "gemm rows [%ld, %ld) outside %ld", a->row0, a->row1, m->n_rows);
-    if (a->row0 == a->row1) return 0;
     if (a->epilogue == SDY_EPI_SWIGLU && (((a->row1 - a->row0) | a->row0) & 1 || a->bias || a->resid))
         return sdy_fail(-1, "gemm: the SwiGLU epilogue needs an even row range from an even row, no bias, no residual");
-    GemmArgs g = gemm_args(m, true);
+    if (a->row0 == a->row1) {
+        *empty = true;
+        return 0;
+    }
+    g = gemm_args(m, true);
     const int nb = g.nb, n_tok = a->n_tok;
     const SdyGemmExp e = sdy_gemm_exp(ws, n_tok, g.n_in);
     g.exp_rows = n_tok;
     g.y16 = e.y16;
     g.yd = e.yd;
     g.bs16 = e.bs16;
-    int rc;
     if (!a->ws_ready) {
         const long n_sb = (long)n_tok * nb;
         SDY_NOTE_KERNEL(k_gemm_prep);
         hipLaunchKernelGGL(k_gemm_prep, dim3((unsigned)((n_sb * 16 + 255) / 256)), dim3(256), 0, st,
                            (const uint8_t *)a->xq, n_sb, (_Float16 *)g.y16, (float *)g.yd, (_Float16 *)g.bs16);
-        if ((rc = sdy_check_launch("gemm_prep"))) return rc;
+        if (int rc = sdy_check_launch("gemm_prep")) return rc;
     }
     g.row0 = a->row0;
     g.n_rows = a->row1 - a->row0;
@@ -1103,7 +1140,66 @@ extern "C" int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_st
     g.resid = a->resid;
     g.swiglu = a->epilogue == SDY_EPI_SWIGLU;
     // with a row range the outputs are indexed by row - row0 only for SwiGLU (as in the matvec)
+    return 0;
+}
+
+extern "C" int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_stream s) {
+    hipStream_t st = (hipStream_t)s;
+    GemmArgs g;
+    bool empty;
+    if (int rc = gemm_setup(m, a, ws, st, g, &empty)) return rc;
+    if (empty) return 0;
     return m->type == SDY_Q4_K ? gemm_type<SDY_Q4_K>(g, st) : gemm_type<SDY_Q6_K>(g, st);
+}
+
+// the small-grid tile form of gemm_type (64-row tiles of 32 tokens, the unit split)
+static bool gemm_small_grid(long n_rows, int n_tok) {
+    return ((n_rows + 127) / 128) * (long)((n_tok + 63) / 64) < 1024;
+}
+
+template <int WT1, bool WIDE1, int WT2, bool WIDE2>
+static int launch_gemm3_pair_s(GemmArgs &g1, GemmArgs &g2, hipStream_t st) {
+    constexpr int NT = 1, BN = 32 * NT, YDN = 64, BM = 64;
+    constexpr size_t lds = 2 * (size_t)(BN * 512 + YDN * 4 + BN * 32);
+    static size_t granted = 0;
+    const void *fn = (const void *)k_gemm3_pair<WT1, WIDE1, WT2, WIDE2, 1, NT, 4, 2>;
+    int rc = sdy_lds_limit(fn, lds, &granted);
+    if (rc) return rc;
+    const unsigned tok_tiles = (unsigned)((g1.n_tok + BN - 1) / BN);
+    const int gy1 = (int)((g1.n_rows + BM - 1) / BM), gy2 = (int)((g2.n_rows + BM - 1) / BM);
+    SDY_NOTE_KERNEL((k_gemm3_pair<WT1, WIDE1, WT2, WIDE2, 1, NT, 4, 2>));
+    hipLaunchKernelGGL((k_gemm3_pair<WT1, WIDE1, WT2, WIDE2, 1, NT, 4, 2>), dim3(tok_tiles, (unsigned)(gy1 + gy2)),
+                       dim3(256), lds, st, g1, g2, gy1);
+    return sdy_check_launch("gemm2");
+}
+
+// Two GEMMs over the same activations (a layer's q|k and its v): one launch when the first matrix
+// is Q4_K and the second Q6_K, each on the small-grid tile form (the bits of two sdy_gemm calls);
+// otherwise, or with SARDYNE_GEMM_VARIANT set, two sdy_gemm calls.
+extern "C" int sdy_gemm2(const sdy_mat *m1, const sdy_mv_args *a1, const sdy_mat *m2, const sdy_mv_args *a2, void *ws,
+                         sdy_stream s) {
+    hipStream_t st = (hipStream_t)s;
+    if (a2->xq != a1->xq || a2->n_tok != a1->n_tok || m2->n_in != m1->n_in)
+        return sdy_fail(-1, "gemm2: the two GEMMs must read the same activation rows");
+    const bool pair = m1->type == SDY_Q4_K && m2->type == SDY_Q6_K && !getenv("SARDYNE_GEMM_VARIANT") &&
+                      a1->row1 > a1->row0 && a2->row1 > a2->row0 && gemm_small_grid(a1->row1 - a1->row0, a1->n_tok) &&
+                      gemm_small_grid(a2->row1 - a2->row0, a2->n_tok);
+    if (!pair) {
+        if (int rc = sdy_gemm(m1, a1, ws, s)) return rc;
+        sdy_mv_args b = *a2;
+        b.ws_ready = 1;  // the expansion the first call made (or found)
+        return sdy_gemm(m2, &b, ws, s);
+    }
+    GemmArgs g1, g2;
+    bool e1, e2;
+    sdy_mv_args b = *a2;
+    b.ws_ready = 1;
+    if (int rc = gemm_setup(m1, a1, ws, st, g1, &e1)) return rc;  // (both ranges non-empty here)
+    if (int rc = gemm_setup(m2, &b, ws, st, g2, &e2)) return rc;
+    if (g1.wide) return g2.wide ? launch_gemm3_pair_s<SDY_Q4_K, true, SDY_Q6_K, true>(g1, g2, st)
+                                : launch_gemm3_pair_s<SDY_Q4_K, true, SDY_Q6_K, false>(g1, g2, st);
+    return g2.wide ? launch_gemm3_pair_s<SDY_Q4_K, false, SDY_Q6_K, true>(g1, g2, st)
+                   : launch_gemm3_pair_s<SDY_Q4_K, false, SDY_Q6_K, false>(g1, g2, st);
 }
 
 extern "C" int sdy_gemm_grouped_tile(void) { return 32; }

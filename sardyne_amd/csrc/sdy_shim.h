@@ -163,6 +163,11 @@ int sdy_matvec_grouped_fused_ok(const sdy_mat *m, const sdy_mv_args *a, int n_sl
 int sdy_gemm_ok(const sdy_mat *m, int n_tok);
 size_t sdy_gemm_ws_bytes(int n_tok, int n_in);
 int sdy_gemm(const sdy_mat *m, const sdy_mv_args *a, void *ws, sdy_stream s);
+/* Two GEMMs over the same activations (a1->xq == a2->xq, the same n_tok and n_in; a layer's q|k and
+ * its v): one launch when m1 is Q4_K and m2 Q6_K on small grids, else two sdy_gemm calls. The bits of
+ * sdy_gemm(m1, a1) then sdy_gemm(m2, a2 with ws_ready). */
+int sdy_gemm2(const sdy_mat *m1, const sdy_mv_args *a1, const sdy_mat *m2, const sdy_mv_args *a2, void *ws,
+              sdy_stream s);
 /* Q8_K activations for the GEMM in one launch: the bytes of sdy_quantize (of sdy_norm_quant, with xb
  * as there) into xq, and their f16 expansion into ws, so that sdy_gemm on the same rows and ws runs
  * with ws_ready = 1. */

@@ -1060,6 +1060,38 @@ def test_quantize_gemm_expansion(norm, n_in, n_tok):
     assert np.array_equal(bits(gemm(0)), bits(exp))
 
 
+@pytest.mark.parametrize("wide1,wide2", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("n_in,rows1,rows2,n_tok", [(2048, 2304, 256, 512), (1024, 200, 77, 45)])
+def test_gemm2_pair_launch_bit_exact(n_in, rows1, rows2, n_tok, wide1, wide2):
+    """sdy_gemm2 (a layer's Q4_K q|k and Q6_K v on the same activations, one launch) gives each matrix
+    the oracle's bits, bias included, in the one-fragment and wide forms of either matrix, and with
+    row counts that do not fill the 64-row tiles."""
+    L = lib()
+    rng = np.random.default_rng(rows1 + rows2 + n_tok)
+    def mat(kind, rows, wide, seed):
+        if wide:
+            return _full_range_blocks(kind, rows, n_in, seed)
+        return _gemm_case(kind, n_in, rows, n_tok, seed=seed)[1]
+    w1, w2 = mat("Q4_K", rows1, wide1, 3), mat("Q6_K", rows2, wide2, 4)
+    x = rng.standard_normal((n_tok, n_in)).astype(np.float32)
+    xq = O.quantize(x, O.Q8_K)
+    b1 = rng.standard_normal(rows1).astype(np.float32)
+    b2 = rng.standard_normal(rows2).astype(np.float32)
+    m1, m2 = capi.DeviceMatrix(O.Q4_K, n_in, rows1, w1), capi.DeviceMatrix(O.Q6_K, n_in, rows2, w2)
+    assert m1.m.gemm_ok == (2 if wide1 else 1) and m2.m.gemm_ok == (2 if wide2 else 1)
+    dq = capi.DeviceBuffer.from_array(xq)
+    ws = capi.DeviceBuffer(L.sdy_gemm_ws_bytes(n_tok, n_in))
+    d1 = capi.DeviceBuffer.from_array(np.full((n_tok, rows1), np.nan, np.float32))
+    d2 = capi.DeviceBuffer.from_array(np.full((n_tok, rows2), np.nan, np.float32))
+    db1, db2 = capi.DeviceBuffer.from_array(b1), capi.DeviceBuffer.from_array(b2)
+    a1 = capi.SdyMvArgs(xq=dq.ptr, n_tok=n_tok, out=d1.ptr, out_stride=rows1, row0=0, row1=rows1, bias=db1.ptr)
+    a2 = capi.SdyMvArgs(xq=dq.ptr, n_tok=n_tok, out=d2.ptr, out_stride=rows2, row0=0, row1=rows2, bias=db2.ptr)
+    capi.check(L.sdy_gemm2(ctypes.byref(m1.m), ctypes.byref(a1), ctypes.byref(m2.m), ctypes.byref(a2), ws.ptr, None))
+    got1, got2 = d1.to_array(np.float32, (n_tok, rows1)), d2.to_array(np.float32, (n_tok, rows2))
+    assert np.array_equal(bits(got1), bits(O.matmul_q(w1, O.Q4_K, xq, n_in, simd=1) + b1))
+    assert np.array_equal(bits(got2), bits(O.matmul_q(w2, O.Q6_K, xq, n_in, simd=1) + b2))
+
+
 @pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
 def test_gemm_layout_copy_and_planes_same_bits(kind):
     """The GEMM reads the tiled copy that sdy_mat_gemm_layout makes (the default of DeviceMatrix and
