@@ -44,10 +44,12 @@ struct FlashArgs {
 };
 
 // LDS: Q^T of the block as [2][32][QS] (element (query q, dim half * HD/2 + s) at [half][q][s]),
-// then, after the key tiles, the merge area: the waves' O as [FW][32][OS] and their m, l as [2][FW][32].
-template <int HD>
+// then, after the key tiles, the merge area: the waves' O dims, 1/MS of them at a time, as
+// [FW][32][OS] and their m, l as [2][FW][32] (HD 128: 134 KB for MS 1, one workgroup per CU;
+// 68 KB for MS 2, two).
+template <int HD, int MS>
 struct FlashLds {
-    static constexpr int HH = HD / 2, QS = HH + 4, OS = HD + 1;
+    static constexpr int HH = HD / 2, QS = HH + 4, OS = HD / MS + 1;
     static constexpr size_t q_floats = 2 * 32 * QS;
     static constexpr size_t merge_floats = (size_t)FW * 32 * OS + 2 * FW * 32;
     static constexpr size_t bytes = 4 * (q_floats > merge_floats ? q_floats : merge_floats);
@@ -69,9 +71,9 @@ struct VLoad<2, KT> {
     SDY_DEV static float at(const T &v, int j) { return j ? v.y : v.x; }
 };
 
-template <int HD, class KT>
+template <int HD, class KT, int MS>
 __global__ __launch_bounds__(64 * FW) void k_attn_flash(FlashArgs a) {
-    using LY = FlashLds<HD>;
+    using LY = FlashLds<HD, MS>;
     constexpr int HH = HD / 2, ND = HD / 32;
     using VL = VLoad<ND, KT>;
     extern __shared__ __align__(16) float lds[];
@@ -161,54 +163,72 @@ __global__ __launch_bounds__(64 * FW) void k_attn_flash(FlashArgs a) {
                 o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(VL::at(vv[r], dt), p[r], o[dt], 0, 0, 0);
     }
 
-    // merge of the waves' partials in wave order (the Q^T area is reused)
-    __syncthreads();
-    float *om = lds + (size_t)wave * 32 * LY::OS;
+    // merge of the waves' partials in wave order (the Q^T area is reused), in MS parts of the dims:
+    // part x holds the O columns dt in [x NDH, (x + 1) NDH), dims ND * row + dt, at NDH * row + dt - x NDH
+    constexpr int NDH = ND / MS;
     float *ml = lds + (size_t)FW * 32 * LY::OS;  // m [FW][32], then l [FW][32]
 #pragma unroll
-    for (int dt = 0; dt < ND; dt++)
+    for (int x = 0; x < MS; x++) {
+        __syncthreads();
+        float *om = lds + (size_t)wave * 32 * LY::OS;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int row = 8 * (r >> 2) + 4 * hh + (r & 3);  // D row: dim ND * row + dt
-            om[ql * LY::OS + ND * row + dt] = o[dt][r];
+        for (int dt = x * NDH; dt < (x + 1) * NDH; dt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = 8 * (r >> 2) + 4 * hh + (r & 3);  // D row: dim ND * row + dt
+                om[ql * LY::OS + NDH * row + dt - x * NDH] = o[dt][r];
+            }
+        if (x == 0 && hh == 0) {
+            ml[wave * 32 + ql] = m_run;
+            ml[FW * 32 + wave * 32 + ql] = l_run;
         }
-    if (hh == 0) {
-        ml[wave * 32 + ql] = m_run;
-        ml[FW * 32 + wave * 32 + ql] = l_run;
-    }
-    __syncthreads();
-    for (int i = tid; i < QB * HD; i += 64 * FW) {
-        const int q = i / HD, d = i - q * HD;
-        if (q0 + q >= a.n_tok) continue;
-        float M = -INFINITY;
+        __syncthreads();
+        for (int i = tid; i < QB * (HD / MS); i += 64 * FW) {
+            const int q = i / (HD / MS), dl = i - q * (HD / MS);
+            if (q0 + q >= a.n_tok) continue;
+            const int d = ND * (dl / NDH) + x * NDH + dl % NDH;
+            float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < FW; w++) M = fmaxf(M, ml[w * 32 + q]);
-        float ls = 0.0f, os = 0.0f;
+            for (int w = 0; w < FW; w++) M = fmaxf(M, ml[w * 32 + q]);
+            float ls = 0.0f, os = 0.0f;
 #pragma unroll
-        for (int w = 0; w < FW; w++) {
-            const float e = __expf(ml[w * 32 + q] - M);  // a wave without keys: m = -inf, e = 0
-            ls += ml[FW * 32 + w * 32 + q] * e;
-            os += lds[((size_t)w * 32 + q) * LY::OS + d] * e;
+            for (int w = 0; w < FW; w++) {
+                const float e = __expf(ml[w * 32 + q] - M);  // a wave without keys: m = -inf, e = 0
+                ls += ml[FW * 32 + w * 32 + q] * e;
+                os += lds[((size_t)w * 32 + q) * LY::OS + dl] * e;
+            }
+            a.out[(size_t)(q0 + q) * a.out_stride + (size_t)h * HD + d] = os / ls;
         }
-        a.out[(size_t)(q0 + q) * a.out_stride + (size_t)h * HD + d] = os / ls;
     }
 }
 
-template <int HD, class KT>
+template <int HD, class KT, int MS>
 int launch_flash(const FlashArgs &A, hipStream_t st) {
     static size_t granted = 0;
-    const void *fn = (const void *)k_attn_flash<HD, KT>;
-    int rc = sdy_lds_limit(fn, FlashLds<HD>::bytes, &granted);
+    const void *fn = (const void *)k_attn_flash<HD, KT, MS>;
+    int rc = sdy_lds_limit(fn, FlashLds<HD, MS>::bytes, &granted);
     if (rc) return rc;
-    SDY_NOTE_KERNEL((k_attn_flash<HD, KT>));
-    hipLaunchKernelGGL((k_attn_flash<HD, KT>), dim3((unsigned)((A.n_tok + QB - 1) / QB), (unsigned)A.n_head),
-                       dim3(64 * FW), FlashLds<HD>::bytes, st, A);
+    SDY_NOTE_KERNEL((k_attn_flash<HD, KT, MS>));
+    hipLaunchKernelGGL((k_attn_flash<HD, KT, MS>), dim3((unsigned)((A.n_tok + QB - 1) / QB), (unsigned)A.n_head),
+                       dim3(64 * FW), (FlashLds<HD, MS>::bytes), st, A);
     return sdy_check_launch("attn_flash");
+}
+
+// The merge in two parts (two workgroups per CU) when the grid has more workgroups than the GPU
+// has CUs: the 30B-A3B's 32 heads x 16 blocks, 36.0 -> 34.2 ms for its 1024-token prefill; the 3B's
+// 16 x 16 fill the CUs once, and a second merge round only costs (53.8k against 53.4k tok/s).
+template <int HD, class KT>
+int launch_flash_ms(const FlashArgs &A, hipStream_t st) {
+    int n_cu = 0;
+    size_t mem = 0;
+    if (sdy_device_info(&n_cu, &mem) || n_cu <= 0) n_cu = 256;
+    const long wgs = (long)((A.n_tok + QB - 1) / QB) * A.n_head;
+    return wgs > n_cu ? launch_flash<HD, KT, 2>(A, st) : launch_flash<HD, KT, 1>(A, st);
 }
 
 template <int HD>
 int launch_flash_kv(const FlashArgs &A, int kv_type, hipStream_t st) {
-    return kv_type == SDY_KV_F16 ? launch_flash<HD, uint16_t>(A, st) : launch_flash<HD, float>(A, st);
+    return kv_type == SDY_KV_F16 ? launch_flash_ms<HD, uint16_t>(A, st) : launch_flash_ms<HD, float>(A, st);
 }
 
 }  // namespace
