@@ -196,6 +196,7 @@ _DEVICE_SIGNATURES = {
                                        _vp, _vp, _int, ctypes.c_long, _int, _vp, _vp, _vp, _vp]),
     "sdy_moe_route": (_int, [_vp, _int, _int, _int, _vp, _vp, _vp]),
     "sdy_moe_combine": (_int, [_vp, _vp, _vp, _int, _int, _int, _vp, _vp, _vp]),
+    "sdy_moe_down_combine": (_int, [ctypes.POINTER(SdyMat), _vp, _vp, _vp, _int, ctypes.c_long, _vp, _vp, _vp]),
     "sdy_gemm_ok": (_int, [ctypes.POINTER(SdyMat), _int]),
     "sdy_gemm_ws_bytes": (_sz, [_int, _int]),
     "sdy_gemm": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp, _vp]),

@@ -476,7 +476,10 @@ static int moe_decode(engine_ctx *c, const dlayer *L) {
     a.row0 = 0;
     a.row1 = dim;
     long x_slot = fe;
-    if (!c->fuse_act || !sdy_matvec_grouped_fused_ok(&L->down.m, &a, k, dim, x_slot)) {
+    const int fused = c->fuse_act && sdy_matvec_grouped_fused_ok(&L->down.m, &a, k, dim, x_slot);
+    if (fused && k <= 8) /* the k down projections and their combine in one launch */
+        return sdy_moe_down_combine(&L->down.m, c->hb, c->moe_top, c->moe_w, k, dim, c->x, c->x, c->st);
+    if (!fused) {
         TRY(sdy_quantize(SDY_Q8_K, c->hb, c->xq[1], fe, k, c->st));
         a.x = NULL;
         a.xq = c->xq[1];

@@ -882,15 +882,16 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl_pair(MvArgs a, MvArgs b, 
 // so that these few bytes do not queue behind the weight stream); build() quantises them into LDS,
 // loading further rounds of NR super-blocks per wave when nb > 4 NR (without NORM only). Every thread
 // of the workgroup calls build(); it ends with a barrier.
-template <bool NORM, int NR>
+template <bool NORM, int NR, int WV = 4>
 struct Q8kRow {
+    static_assert(!NORM || WV == 4, "the norm's block sum takes four waves");
     float4 xv[NR], wv[NR];
 
     SDY_DEV void issue(const float *__restrict__ x, const float *__restrict__ nw, int n) {
         const int nb = n >> 8, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
         for (int k = 0; k < NR; k++) {
-            const int sb = wave + 4 * k < nb ? wave + 4 * k : nb - 1;
+            const int sb = wave + WV * k < nb ? wave + WV * k : nb - 1;
             xv[k] = *reinterpret_cast<const float4 *>(x + 256 * sb + 4 * lane);
             if constexpr (NORM) wv[k] = *reinterpret_cast<const float4 *>(nw + 256 * sb + 4 * lane);
         }
@@ -919,11 +920,11 @@ struct Q8kRow {
             ss = sdy_block_sum256(ss, sh);
             scale = (float)(1.0 / sqrt(ss / (double)n + (double)eps));
         }
-        for (int s0 = wave; s0 < nb; s0 += 4 * NR) {
+        for (int s0 = wave; s0 < nb; s0 += WV * NR) {
             if (s0 != wave) {  // a further round (long rows without NORM)
 #pragma unroll
                 for (int k = 0; k < NR; k++) {
-                    const int sb = s0 + 4 * k < nb ? s0 + 4 * k : nb - 1;
+                    const int sb = s0 + WV * k < nb ? s0 + WV * k : nb - 1;
                     xv[k] = *reinterpret_cast<const float4 *>(x + 256 * sb + 4 * lane);
                 }
             }
@@ -944,7 +945,7 @@ struct Q8kRow {
             sdy_q8k_lanes<NR>(xs, lane, r);
 #pragma unroll
             for (int k = 0; k < NR; k++) {
-                const int sb = s0 + 4 * k;
+                const int sb = s0 + WV * k;
                 if (sb < nb) {
                     ly[sb * 64 + lane] = r[k].packed;
                     if ((lane & 3) == 0) lbs[sb * 16 + (lane >> 2)] = (int16_t)r[k].gsum;
@@ -1156,6 +1157,83 @@ template <int WT1, int WT2, int NSB, int PRO>
 __global__ __launch_bounds__(THREADS) void k_matvec_1t_pair(MvArgs a, MvArgs b, int g1) {
     if ((int)blockIdx.x < g1) matvec_1t_body<WT1, 1, NSB, PRO>(a, g1, (int)blockIdx.x, 0);
     else matvec_1t_body<WT2, 1, NSB, PRO>(b, (int)gridDim.x - g1, (int)blockIdx.x - g1, 0);
+}
+
+// The routed experts' down projections of one token and their combine in one launch. Workgroup of
+// KMAX waves over rpi rows: wave s computes slot s's dots with expert slot_expert[s] as
+// k_matvec_1t's grouped form does (the same bits: lane (rl, u) holds unit u of row rl), the
+// workgroup exchanges them through LDS, and wave 0 sums the k slots in ascending expert id with the
+// weights wts (k_moe_combine's order, op_axpy's per-element form), plus resid, into out. The k
+// slots' f32 rows (px, n_in apart: contiguous) are quantised by the workgroup as one row of
+// k * n_in elements into LDS (slot s's units follow slot s - 1's).
+template <int WT, int NSB, int KMAX>
+__global__ __launch_bounds__(64 * KMAX) void k_moe_down_combine(MvArgs a, const float *__restrict__ wts, int k,
+                                                                float *out, const float *resid) {
+    const int T = a.P.T, n_in = a.P.n_in;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int rpi = a.rpi;
+    const int rl_ = __mul24(lane, a.tmag) >> 16, u = lane - __mul24(rl_, T);
+    const bool lane_on = rl_ < rpi;
+    const int rl = lane_on ? rl_ : 0;
+    const int G = (int)gridDim.x, bx = (int)blockIdx.x;
+    const int vblk = (G & 7) == 0 ? (bx & 7) * (G >> 3) + (bx >> 3) : bx;  // XCD-aware renumbering
+    const long row = a.row0 + (long)vblk * rpi + rl;
+    const long rowc = row < a.row1 ? row : a.row0;  // (rows past the end read row0 and store nothing)
+    extern __shared__ uint8_t lds_act[];
+    // (eight rows of 768: 24 super-blocks, three per wave)
+    Q8kRow<false, NSB == 3 ? 3 : 4, KMAX> arow;
+    arow.issue(a.px, nullptr, k * n_in);
+    const int sl = wave < k ? wave : k - 1;
+    int e = a.slot_expert[sl];
+    e = e < 0 ? 0 : (e >= a.n_slot_exp ? a.n_slot_exp - 1 : e);
+    WRegs<WT> R;
+    const uint32_t nb = a.P.nb, base = (uint32_t)((long)e * a.slot_rows + rowc);
+    load_w_at<WT>(a.P, base * (uint32_t)T + (uint32_t)u, base * nb + ((uint32_t)u >> 2), (uint32_t)u, R);
+    const float rv = resid ? resid[rowc] : 0.0f;
+    // the combine's expert ids and weights, requested with the other loads
+    int ids[KMAX];
+    float wv[KMAX], yv[KMAX];
+#pragma unroll
+    for (int i = 0; i < KMAX; i++) {
+        const int ii = i < k ? i : 0;
+        const int id = a.slot_expert[ii];  // (unconditional loads: the slots past k read slot 0)
+        ids[i] = i < k ? id : 0x7fffffff;
+        wv[i] = wts[ii];
+    }
+    arow.build(a.px, 0.0f, k * n_in, lds_act);
+    uint4 Yr[4];
+    uint2 bsr;
+    float ydr;
+    q8k_unit_lds(lds_act, k * (int)nb, sl * T + u, Yr, bsr, ydr);
+    const float acc = rl_row_sum<WT, NSB>(R, Yr, bsr, ydr, u, lane, T);
+    float *xacc = reinterpret_cast<float *>(lds_act + (size_t)k * nb * 292);  // [KMAX][64]
+    if (u == 0) xacc[wave * 64 + rl_] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int i = 0; i < KMAX; i++) yv[i] = xacc[(i < k ? i : 0) * 64 + rl];
+    // ascending expert id (the same order k_moe_combine sorts the triples into)
+#pragma unroll
+    for (int i = 0; i < KMAX; i++)
+#pragma unroll
+        for (int j = 0; j + 1 < KMAX - i; j++)
+            if (ids[j] > ids[j + 1]) {
+                const int ti = ids[j];
+                ids[j] = ids[j + 1];
+                ids[j + 1] = ti;
+                const float tw = wv[j];
+                wv[j] = wv[j + 1];
+                wv[j + 1] = tw;
+                const float ty = yv[j];
+                yv[j] = yv[j + 1];
+                yv[j + 1] = ty;
+            }
+    const long dim = a.row1 - a.row0, d = rowc - a.row0;
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KMAX; i++)
+        if (i < k) tot = d < (dim & ~7L) ? fmaf(wv[i], yv[i], tot) : tot + wv[i] * yv[i];
+    if (u == 0 && lane_on && row < a.row1) out[row] = resid ? rv + tot : tot;
 }
 
 // One token, rows of at most 64 units: K-quants when the rows are too many for k_matvec_1t (the
@@ -2581,6 +2659,48 @@ extern "C" int sdy_matvec_grouped(const sdy_mat *m, const sdy_mv_args *a, const 
     }
     if (m->type == SDY_Q4_K) return mv_grouped<SDY_Q4_K>(m, a, slot_expert, n_slot, slot_rows, xq_slot, out_slot, st);
     return mv_grouped<SDY_Q6_K>(m, a, slot_expert, n_slot, slot_rows, xq_slot, out_slot, st);
+}
+
+// The routed experts' down projections of one token (the k slots' f32 rows x, n_in apart, through
+// expert slot_expert[s] of the stack m, dim rows each) and their combine: out = resid + sum over the
+// slots in ascending expert id of wts[s] * y_s. The bits of sdy_matvec_grouped (quantising the
+// rows in the kernel) then sdy_moe_combine.
+extern "C" int sdy_moe_down_combine(const sdy_mat *m, const float *x, const int32_t *slot_expert, const float *wts,
+                                    int k, long dim, float *out, const float *resid, sdy_stream s) {
+    if (m->type != SDY_Q4_K && m->type != SDY_Q6_K) return sdy_fail(-1, "moe_down_combine: K-quant weights only");
+    if (k < 1 || k > 8 || dim < 1 || m->n_rows % dim || m->n_units > 64 || m->n_in % 256 || ((uintptr_t)x & 15))
+        return sdy_fail(-1, "moe_down_combine: 1..8 slots, a stack of %ld-row experts, rows of 256..4096 elements, "
+                            "16-byte aligned activations", dim);
+    MvArgs A = {};
+    A.P = planes_of(m);
+    A.n_tok = 1;
+    A.row0 = 0;
+    A.row1 = dim;
+    A.slot_expert = slot_expert;
+    A.slot_rows = dim;
+    A.n_slot_exp = (int)(m->n_rows / dim);
+    A.px = x;
+    prep_1t(A);
+    const size_t lds = (size_t)k * (m->n_in / 256) * 292 + 8 * 64 * sizeof(float);
+    const unsigned wgs = (unsigned)A.n_it;
+    hipStream_t st = (hipStream_t)s;
+#define SDY_MDC(WT, NSB)                                                                                             \
+    {                                                                                                                \
+        SDY_NOTE_KERNEL((k_moe_down_combine<WT, NSB, 8>));                                                           \
+        hipLaunchKernelGGL((k_moe_down_combine<WT, NSB, 8>), dim3(wgs), dim3(512), lds, st, A, wts, k, out,           \
+                           resid);                                                                                   \
+        return sdy_check_launch("moe_down_combine");                                                                 \
+    }
+    const int nsb = m->n_in / 256;
+    if (m->type == SDY_Q6_K) {
+        if (nsb == 3) SDY_MDC(SDY_Q6_K, 3)
+        if (nsb == 8) SDY_MDC(SDY_Q6_K, 8)
+        SDY_MDC(SDY_Q6_K, 0)
+    }
+    if (nsb == 3) SDY_MDC(SDY_Q4_K, 3)
+    if (nsb == 8) SDY_MDC(SDY_Q4_K, 8)
+    SDY_MDC(SDY_Q4_K, 0)
+#undef SDY_MDC
 }
 
 extern "C" int sdy_matvec_float_norm(int wtype, const void *w, int n_in, const sdy_mv_args *a, void *xq_out,

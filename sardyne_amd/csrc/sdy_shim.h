@@ -156,6 +156,12 @@ int sdy_matvec_grouped(const sdy_mat *m, const sdy_mv_args *a, const int32_t *sl
 /* 1 when sdy_matvec_grouped can quantise each slot's f32 row itself (a->xq = NULL, a->x set; slot s's
  * row at a->x + s * x_slot floats, passed as xq_slot; RMS-normalised first when a->nw is set) */
 int sdy_matvec_grouped_fused_ok(const sdy_mat *m, const sdy_mv_args *a, int n_slot, long slot_rows, long x_slot);
+/* The routed experts' down projections of one token and their combine in one launch: slot s's f32
+ * row x + s * n_in through expert slot_expert[s] of the stack m (dim rows each), then
+ * out = resid + sum over the k <= 8 slots in ascending expert id of wts[s] * y_s (resid may be NULL,
+ * or out itself). The bits of sdy_matvec_grouped with in-kernel quantisation, then sdy_moe_combine. */
+int sdy_moe_down_combine(const sdy_mat *m, const float *x, const int32_t *slot_expert, const float *wts, int k,
+                         long dim, float *out, const float *resid, sdy_stream s);
 
 /* The prefill GEMM (gemm_kernels.hip): the same outputs as sdy_matvec (bit for bit) for
  * n_tok >= 2 tokens of Q8_K activations a->xq on Q4_K / Q6_K matrices with gemm_ok, through

@@ -669,6 +669,45 @@ def test_grouped_matvec_fused_activation(kind, n_in, e_rows, mode):
     assert np.array_equal(bits(res[1]), bits(res[0]))
 
 
+@pytest.mark.parametrize("kind,n_in,dim,k,resid", [
+    ("Q6_K", 768, 2048, 8, "inplace"), ("Q4_K", 768, 2050, 8, "sep"), ("Q6_K", 2048, 300, 5, "none"),
+    ("Q4_K", 512, 77, 1, "inplace"), ("Q6_K", 4096, 130, 3, "sep"), ("Q4_K", 1280, 1000, 7, "inplace")])
+def test_moe_down_combine_bit_exact(kind, n_in, dim, k, resid):
+    """The routed experts' down projections and their combine in one launch: the bits of the grouped
+    matvec (each slot's f32 row quantised in the kernel) followed by sdy_moe_combine, with the
+    residual separate, absent or the output itself."""
+    t = TYPES[kind]
+    L = lib()
+    n_exp = 11
+    rng = np.random.default_rng(n_in + dim + k)
+    top = rng.permutation(n_exp)[:k].astype(np.int32)
+    wts = rng.random(k).astype(np.float32)
+    w = random_blocks(kind, n_exp * dim * n_in // 256, rng).reshape(n_exp * dim, -1)
+    x = (2.0 * rng.standard_normal((k, n_in))).astype(np.float32)
+    r = rng.standard_normal(dim).astype(np.float32)
+    m = capi.DeviceMatrix(t, n_in, n_exp * dim, w)
+    dx, dtop, dw = capi.DeviceBuffer.from_array(x), capi.DeviceBuffer.from_array(top), capi.DeviceBuffer.from_array(wts)
+    # separate: grouped matvec into y [k][dim], then the combine
+    dy = capi.DeviceBuffer.from_array(np.full((k, dim), np.nan, np.float32))
+    a = capi.SdyMvArgs(n_tok=1, x=dx.ptr, out=dy.ptr, out_stride=dim, row0=0, row1=dim)
+    assert L.sdy_matvec_grouped_fused_ok(ctypes.byref(m.m), ctypes.byref(a), k, dim, n_in) == 1
+    capi.check(L.sdy_matvec_grouped(ctypes.byref(m.m), ctypes.byref(a), dtop.ptr, k, dim, n_in, dim, None))
+    dr = capi.DeviceBuffer.from_array(r)
+    de = capi.DeviceBuffer.from_array(np.full(dim, np.nan, np.float32))
+    capi.check(L.sdy_moe_combine(dy.ptr, dtop.ptr, dw.ptr, 1, k, dim, de.ptr, None if resid == "none" else dr.ptr,
+                                 None))
+    exp = de.to_array(np.float32, dim)
+    assert not np.isnan(exp).any()
+    if resid == "inplace":
+        dout = capi.DeviceBuffer.from_array(r)
+        rp = dout.ptr
+    else:
+        dout = capi.DeviceBuffer.from_array(np.full(dim, np.nan, np.float32))
+        rp = dr.ptr if resid == "sep" else None
+    capi.check(L.sdy_moe_down_combine(ctypes.byref(m.m), dx.ptr, dtop.ptr, dw.ptr, k, dim, dout.ptr, rp, None))
+    assert np.array_equal(bits(dout.to_array(np.float32, dim)), bits(exp))
+
+
 FLOAT_TYPES = {"F32": (0, np.float32), "F16": (1, np.float16), "BF16": (30, None)}
 
 
