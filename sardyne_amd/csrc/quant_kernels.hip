@@ -2682,7 +2682,9 @@ extern "C" int sdy_moe_down_combine(const sdy_mat *m, const float *x, const int3
     A.px = x;
     prep_1t(A);
     const size_t lds = (size_t)k * (m->n_in / 256) * 292 + 8 * 64 * sizeof(float);
-    const unsigned wgs = (unsigned)A.n_it;
+    // a multiple of 8 workgroups: the kernel's XCD-aware renumbering then keeps neighbouring rows
+    // (whose plane segments share cache lines) on one XCD (the extra workgroups store nothing)
+    const unsigned wgs = (unsigned)((A.n_it + 7) & ~7L);
     hipStream_t st = (hipStream_t)s;
 #define SDY_MDC(WT, NSB)                                                                                             \
     {                                                                                                                \
