@@ -349,30 +349,32 @@ __global__ __launch_bounds__(256) void k_attn_merge(ChunkArgs a) {
     const int h_raw = blockIdx.x * HPS + slot, h = h_raw < a.n_head ? h_raw : a.n_head - 1;
     const int n_span = a.step[1] / a.span + 1;
     const float *pb = a.part + (size_t)h * a.n_span_max * (HD + 4);
-    // rounds of MERGE_ROUND spans whose loads are issued before use, folded with the running maximum
+    // rounds of MERGE_ROUND spans whose loads are issued before use, folded with the running maximum.
+    // The head is uniform over a wave (HD >= 64): lane u loads span s0 + u's m and l and computes its
+    // weight, which the fold reads by lane; a thread loads only its own dimension of each span's o.
+    const int lane = tid & 63;
     float M = -INFINITY, L = 0.0f, o = 0.0f;
     for (int s0 = 0; s0 < n_span; s0 += MERGE_ROUND) {
-        float mv[MERGE_ROUND], lv[MERGE_ROUND], ov[MERGE_ROUND];
+        const int lu = lane < MERGE_ROUND ? lane : 0;
+        const bool lu_ok = lane < MERGE_ROUND && s0 + lu < n_span;
+        const float *pl = pb + (size_t)(lu_ok ? s0 + lu : s0) * (HD + 4);
+        const float m_l = pl[0], l_l = pl[1];
+        float ov[MERGE_ROUND];
 #pragma unroll
         for (int u = 0; u < MERGE_ROUND; u++) {
             const int s = s0 + u < n_span ? s0 + u : s0;
-            const float *pc = pb + (size_t)s * (HD + 4);
-            mv[u] = pc[0];
-            lv[u] = pc[1];
-            ov[u] = pc[4 + d];
+            ov[u] = pb[(size_t)s * (HD + 4) + 4 + d];
         }
-        float Mr = M;
-#pragma unroll
-        for (int u = 0; u < MERGE_ROUND; u++)
-            if (s0 + u < n_span) Mr = fmaxf(Mr, mv[u]);
+        const float Mr = fmaxf(M, wave_max(lu_ok ? m_l : -INFINITY));
         const float sc = __expf(M - Mr);  // 0 on the first round (M = -inf)
         L *= sc;
         o *= sc;
+        const float w_l = __expf(m_l - Mr);
 #pragma unroll
         for (int u = 0; u < MERGE_ROUND; u++) {
             if (s0 + u < n_span) {
-                const float w = __expf(mv[u] - Mr);
-                L = fmaf(lv[u], w, L);
+                const float w = lane_f(w_l, u);
+                L = fmaf(lane_f(l_l, u), w, L);
                 o = fmaf(ov[u], w, o);
             }
         }
