@@ -1513,6 +1513,12 @@ __global__ __launch_bounds__(THREADS) void k_matvec_float_dot(const uint8_t *__r
                                                               long out_stride, const float *bias, const float *resid,
                                                               long row0, long row1, FloatNorm fn = {}) {
     const int lane = threadIdx.x & 63, L = lane & 31, base = lane & 32;
+    constexpr int B = 32;  // steps whose loads go out together before their chain runs in order
+    // NORM (one token): the half-wave's first B steps of weights are requested right after the
+    // prologue's own loads, before its computation (they do not depend on it); half-waves past the
+    // rows read row0's
+    float wv0[NORM ? B : 1];
+    const bool pre = NORM && (n_in & ~31) >= 32 * B;
     // NORM: the normalised row in LDS, built by every thread (one token, n_in <= 4096, a multiple of 256)
     __shared__ __align__(16) float xn[NORM ? 4096 : 4];
     if constexpr (NORM) {
@@ -1522,9 +1528,31 @@ __global__ __launch_bounds__(THREADS) void k_matvec_float_dot(const uint8_t *__r
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const int c = tid + 256 * k < n4 ? tid + 256 * k : n4 - 1;
+            keep[k] = *reinterpret_cast<const float4 *>(x + 4 * c);
             wk[k] = *reinterpret_cast<const float4 *>(fn.nw + 4 * c);
         }
-        const double ss = sdy_row_sumsq<4>(x, n_in, keep, sh);  // keep[k]: the thread's chunk tid + 256k
+        __builtin_amdgcn_sched_barrier(0);  // (the prologue's loads stay ahead of the weights')
+        {
+            const long it = ((long)blockIdx.x * THREADS + threadIdx.x) >> 5;
+            const long rr = it < row1 - row0 ? row0 + it : row0;
+            const uint8_t *wr0 = w + (size_t)rr * n_in * (WT == SDY_F32 ? 4 : 2);
+            // (unconditional, indices clamped to the row, so that the compiler's wait counts stay
+            // exact; used only when pre)
+#pragma unroll
+            for (int j = 0; j < B; j++) wv0[j] = welem<WT>(wr0, min(L + 32 * j, n_in - 1));
+        }
+        // sdy_row_sumsq's order (x is 16-byte aligned and n_in <= 4096: the four chunks tid + 256 k)
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (tid + 256 * k < n4) {
+                const float4 v = keep[k];
+                ss += (double)v.x * (double)v.x;
+                ss += (double)v.y * (double)v.y;
+                ss += (double)v.z * (double)v.z;
+                ss += (double)v.w * (double)v.w;
+            }
+        ss = sdy_block_sum256(ss, sh);
         const float scale = (float)(1.0 / sqrt(ss / (double)n_in + (double)fn.eps));
 #pragma unroll
         for (int k = 0; k < 4; k++)
@@ -1565,7 +1593,13 @@ __global__ __launch_bounds__(THREADS) void k_matvec_float_dot(const uint8_t *__r
     float acc = 0.0f;
     const int n32 = n_in & ~31, n8 = n_in & ~7;
     int i = L;
-    constexpr int B = 32;  // steps whose loads go out together before their chain runs in order
+    if constexpr (NORM) {
+        if (pre) {  // the first B steps, whose weights are in wv0
+#pragma unroll
+            for (int j = 0; j < B; j++) acc = fmaf(wv0[j], xe(xr, i + 32 * j), acc);
+            i += 32 * B;
+        }
+    }
     for (; i + 32 * (B - 1) < n32; i += 32 * B) {
         float wv[B], xv[B];
 #pragma unroll
