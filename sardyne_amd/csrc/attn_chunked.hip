@@ -117,21 +117,22 @@ __global__ __launch_bounds__(256) void k_attn_chunk(ChunkArgs a) {
     const KT *vc = (const KT *)a.v_cache + g * a.head_stride;
 
     sdy_f32x4 kr[PER], vr[PER];
+    // every load unconditional (rows past the cached ones read row 0, never stored to LDS), so that
+    // the compiler's wait counts stay exact
     auto issue = [&](int p0) {
 #pragma unroll
         for (int i = 0; i < PER; i++) {
             const int f = tid + 256 * i, row = f / L4, col = f - row * L4, p = p0 + row;
-            if (p < cached_end) {
-                kr[i] = KvElt<KT>::ld4(kc, (size_t)p * HD + 4 * col);
-                vr[i] = KvElt<KT>::ld4(vc, (size_t)p * HD + 4 * col);
-            }
+            const int pl = p < cached_end ? p : 0;
+            kr[i] = KvElt<KT>::ld4(kc, (size_t)pl * HD + 4 * col);
+            vr[i] = KvElt<KT>::ld4(vc, (size_t)pl * HD + 4 * col);
         }
     };
-    issue(p_begin);
 
     // The group's queries and, in the span of the token's position, the new k: vector r = wave + 4 i
-    // by wave `wave`, lane l holding elements l + 64 e. Every input is loaded first (the K/V rows
-    // above are in flight too), then the reference's per-head RMSNorm (qwen3) and rotation.
+    // by wave `wave`, lane l holding elements l + 64 e. Every input is loaded first, then the span's
+    // first K/V rows are requested (loads complete in order: the rotation below waits only for its
+    // own inputs, not for the K/V tile), then the reference's per-head RMSNorm (qwen3) and rotation.
     {
         const int n_vec = nh + (own ? 1 : 0);
         const float *cs = a.rope_cos + (size_t)pos * (HD / 2), *sn = a.rope_sin + (size_t)pos * (HD / 2);
@@ -152,6 +153,8 @@ __global__ __launch_bounds__(256) void k_attn_chunk(ChunkArgs a) {
             c[e] = cs[ci];
             s[e] = sn[ci];
         }
+        __builtin_amdgcn_sched_barrier(0);
+        issue(p_begin);
 #pragma unroll
         for (int i = 0; i < RV; i++) {
             const int r = wave + 4 * i;
