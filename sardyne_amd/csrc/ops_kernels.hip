@@ -130,28 +130,21 @@ __global__ void k_rope(float *x, int n_heads, int hd, const float *cs, const flo
 // One wave per token: softmax over the expert logits (max, expf, double sum, float reciprocal),
 // then top-k by repeated arg-max with ties to the lower index (the order moe_select produces,
 // csrc/model_llama.c:653-666) and weights renormalised by their sequential float sum.
-// The maximum of a 64-bit value over the wave, in every lane: DPP within rows of 16 lanes (quad
+// The maximum of a 32-bit value over the wave, in every lane: DPP within rows of 16 lanes (quad
 // perms, row rotations), then the four rows' maxima by readlane.
-template <int CTRL>
-SDY_DEV uint64_t dpp_u64(uint64_t v) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
-    return ((uint64_t)hi << 32) | lo;
-}
-SDY_DEV uint64_t wave_max_u64(uint64_t v) {
-    uint64_t o = dpp_u64<0xB1>(v);  // quad_perm [1, 0, 3, 2]
+SDY_DEV uint32_t wave_max_u32(uint32_t v) {
+    uint32_t o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
     v = o > v ? o : v;
-    o = dpp_u64<0x4E>(v);           // quad_perm [2, 3, 0, 1]
+    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
     v = o > v ? o : v;
-    o = dpp_u64<0x124>(v);          // row_ror 4
+    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, false);  // row_ror 4
     v = o > v ? o : v;
-    o = dpp_u64<0x128>(v);          // row_ror 8
+    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);  // row_ror 8
     v = o > v ? o : v;
-    uint64_t r = 0;
+    uint32_t r = 0;
 #pragma unroll
     for (int row = 0; row < 4; row++) {
-        const uint64_t x = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 16 * row) << 32) |
-                           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 16 * row);
+        const uint32_t x = (uint32_t)__builtin_amdgcn_readlane((int)v, 16 * row);
         r = x > r ? x : r;
     }
     return r;
@@ -188,23 +181,29 @@ __global__ __launch_bounds__(64) void k_moe_route(const float *logits, int n_exp
     // moe_select (csrc/model_llama.c:653-666): k times the largest remaining probability, ties to
     // the lowest expert; chosen ones are marked -2. The weights divide by the sum of the chosen
     // probabilities taken in rank order.
-    // Each round's arg-max as the maximum of a 64-bit key: high word the probability's bits plus one
-    // (probabilities are >= 0, so their bits order as unsigned; the -1 / -2 marks map to 0), low word
-    // the complemented expert id (the lower id wins a tie). The wave maximum runs through DPP within
-    // rows of 16 lanes and readlane across the four rows, with no LDS round trip.
+    // Each round's arg-max: the wave maximum of a 32-bit key, the probability's bits plus one
+    // (probabilities are >= 0, so their bits order as unsigned; the -1 / -2 marks map to 0), through
+    // DPP within rows of 16 lanes and readlane across the four rows (no LDS round trip); then the
+    // lowest expert id holding it from ballots (the lower id wins a tie).
     float chosen_sum = 0.0f, my_p = 0.0f;
     int my_e = 0;
     for (int i = 0; i < k; i++) {
-        uint64_t key = 0;
+        // the largest key (the probability's bits plus one; 0 for the marks) over the wave, then the
+        // lowest expert holding it: the first slot j whose ballot has a lane, its lowest lane
+        uint32_t hk[NPL], key = 0;
 #pragma unroll
         for (int j = 0; j < NPL; j++) {
-            const uint32_t hi = v[j] >= 0.0f ? __float_as_uint(fabsf(v[j])) + 1u : 0u;
-            const uint64_t kj = ((uint64_t)hi << 32) | (uint32_t)~(uint32_t)(lane + 64 * j);
-            key = kj > key ? kj : key;
+            hk[j] = v[j] >= 0.0f ? __float_as_uint(fabsf(v[j])) + 1u : 0u;
+            key = hk[j] > key ? hk[j] : key;
         }
-        key = wave_max_u64(key);
-        const float best = __uint_as_float((uint32_t)(key >> 32) - 1u);
-        const int bi = (int)~(uint32_t)key;
+        key = wave_max_u32(key);
+        int bi = -1;
+#pragma unroll
+        for (int j = NPL - 1; j >= 0; j--) {
+            const uint64_t bal = __ballot(hk[j] == key);
+            if (bal) bi = 64 * j + (int)__builtin_ctzll(bal);
+        }
+        const float best = __uint_as_float(key - 1u);
 #pragma unroll
         for (int j = 0; j < NPL; j++)
             if (bi == lane + 64 * j) v[j] = -2.0f;
