@@ -2196,13 +2196,14 @@ static int launch_mv_1t_nsb(MvArgs &A, hipStream_t st, int n_slot, bool dry) {
                            lds, st, A);                                                                              \
         return sdy_check_launch("matvec");                                                                           \
     }
-    if (PRO) {
+    if (PRO || n_slot > 1) {
         // the workgroup-quantised row is built once per workgroup: fewer, fuller workgroups while
-        // every CU still gets three (measured on the 22016 x 2048 gate|up: NIT 3)
+        // every CU still gets three (measured on the 22016 x 2048 gate|up: NIT 3); the same for the
+        // grouped launches, counting every slot's workgroups
         const long want = 3L * (g_n_cu ? g_n_cu : 256);
-        if (wgs(4) >= want) { SDY_1T(4) }
-        if (wgs(3) >= want) { SDY_1T(3) }
-        if (wgs(2) >= want) { SDY_1T(2) }
+        if (wgs(4) * n_slot >= want) { SDY_1T(4) }
+        if (wgs(3) * n_slot >= want) { SDY_1T(3) }
+        if (wgs(2) * n_slot >= want) { SDY_1T(2) }
     }
     SDY_1T(1)
     SDY_1T(2)
