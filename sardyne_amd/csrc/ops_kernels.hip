@@ -150,6 +150,27 @@ SDY_DEV uint32_t wave_max_u32(uint32_t v) {
     return r;
 }
 
+// lane l's value from the DPP source of control CTRL within its row of 16 lanes (both words)
+template <int CTRL>
+SDY_DEV double dpp_f64(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)b, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+SDY_DEV float wave_max_f32(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false)));
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 template <int NPL>  // experts held per lane: n_expert <= 64 * NPL
 __global__ __launch_bounds__(64) void k_moe_route(const float *logits, int n_expert, int k, int32_t *top,
                                                   float *wts) {
@@ -164,7 +185,7 @@ __global__ __launch_bounds__(64) void k_moe_route(const float *logits, int n_exp
         v[j] = e < n_expert ? p[e] : -INFINITY;
         m = fmaxf(m, v[j]);
     }
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    m = wave_max_f32(m);  // (a maximum: the same value in any order)
     // op_softmax (csrc/ops.c:353-364): expf(x - max) (the host libm's expf, bit for bit), the sum
     // in double, times (float)(1 / sum). The probabilities stay in registers; -1 marks lanes past
     // n_expert (never chosen).
@@ -174,7 +195,17 @@ __global__ __launch_bounds__(64) void k_moe_route(const float *logits, int n_exp
         v[j] = sdy_expf_reg(v[j] - m, etab);  // every lane (the table lookup reads other lanes): 0 past n_expert
         if (lane + 64 * j < n_expert) s += (double)v[j];
     }
-    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    // the butterfly over lane ^ 32, 16, 8, 4, 2, 1 (each lane adds its partner's sum): the last four
+    // steps by DPP (row_ror 8; row_shl / row_shr 4 by the lane's bit 2; quad perms), the same pairs
+    s += __shfl_xor(s, 32);
+    s += __shfl_xor(s, 16);
+    s += dpp_f64<0x128>(s);
+    {
+        const double up = dpp_f64<0x104>(s), down = dpp_f64<0x114>(s);
+        s += (lane & 4) ? down : up;
+    }
+    s += dpp_f64<0x4E>(s);
+    s += dpp_f64<0xB1>(s);
     const float inv = (float)(1.0 / s);
 #pragma unroll
     for (int j = 0; j < NPL; j++) v[j] = lane + 64 * j < n_expert ? v[j] * inv : -1.0f;
