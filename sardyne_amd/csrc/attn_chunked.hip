@@ -24,6 +24,7 @@
 #include "sdy_attn_dev.h"
 #include "sdy_device.h"
 #include "sdy_internal.h"
+#include "sdy_norm_dev.h"
 #include "sdy_ops.h"
 #include "sdy_quant_dev.h"
 #include "sdy_shim.h"
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(ChunkArgs a) {
                 double ss = 0.0;
 #pragma unroll
                 for (int e = 0; e < E; e++) ss += (double)y[e] * (double)y[e];
-                for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+                ss = sdy_wave_sum_f64(ss);  // (the butterfly over lane ^ 32, ..., 1; the branch is uniform)
                 const float sc = (float)(1.0 / sqrt(ss / (double)HD + (double)a.eps));
 #pragma unroll
                 for (int e = 0; e < E; e++) {

@@ -150,15 +150,6 @@ SDY_DEV uint32_t wave_max_u32(uint32_t v) {
     return r;
 }
 
-// lane l's value from the DPP source of control CTRL within its row of 16 lanes (both words)
-template <int CTRL>
-SDY_DEV double dpp_f64(double v) {
-    const uint64_t b = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)b, CTRL, 0xF, 0xF, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
-    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
-
 SDY_DEV float wave_max_f32(float v) {
     v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
     v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
@@ -195,17 +186,7 @@ __global__ __launch_bounds__(64) void k_moe_route(const float *logits, int n_exp
         v[j] = sdy_expf_reg(v[j] - m, etab);  // every lane (the table lookup reads other lanes): 0 past n_expert
         if (lane + 64 * j < n_expert) s += (double)v[j];
     }
-    // the butterfly over lane ^ 32, 16, 8, 4, 2, 1 (each lane adds its partner's sum): the last four
-    // steps by DPP (row_ror 8; row_shl / row_shr 4 by the lane's bit 2; quad perms), the same pairs
-    s += __shfl_xor(s, 32);
-    s += __shfl_xor(s, 16);
-    s += dpp_f64<0x128>(s);
-    {
-        const double up = dpp_f64<0x104>(s), down = dpp_f64<0x114>(s);
-        s += (lane & 4) ? down : up;
-    }
-    s += dpp_f64<0x4E>(s);
-    s += dpp_f64<0xB1>(s);
+    s = sdy_wave_sum_f64(s);  // the butterfly over lane ^ 32, 16, ..., 1
     const float inv = (float)(1.0 / s);
 #pragma unroll
     for (int j = 0; j < NPL; j++) v[j] = lane + 64 * j < n_expert ? v[j] * inv : -1.0f;

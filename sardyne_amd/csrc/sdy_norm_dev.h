@@ -5,8 +5,32 @@
 #pragma once
 #include "sdy_device.h"
 
+// lane l's double from the DPP source of control CTRL within its row of 16 lanes (both words)
+template <int CTRL>
+SDY_DEV double sdy_dpp_f64(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)b, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// The wave's sum by the butterfly over lane ^ 32, 16, 8, 4, 2, 1 (each lane adds its partner's
+// value; every lane ends with the same sum): the last four steps by DPP (row_ror 8; row_shl or
+// row_shr 4 by the lane's bit 2; quad perms), the same pairs in the same order as __shfl_xor.
+SDY_DEV double sdy_wave_sum_f64(double v) {
+    const int lane = threadIdx.x & 63;
+    v += __shfl_xor(v, 32);
+    v += __shfl_xor(v, 16);
+    v += sdy_dpp_f64<0x128>(v);
+    const double up = sdy_dpp_f64<0x104>(v), down = sdy_dpp_f64<0x114>(v);
+    v += (lane & 4) ? down : up;
+    v += sdy_dpp_f64<0x4E>(v);
+    v += sdy_dpp_f64<0xB1>(v);
+    return v;
+}
+
 SDY_DEV double sdy_block_sum256(double v, double *sh) {
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    v = sdy_wave_sum_f64(v);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     __syncthreads();
     if (lane == 0) sh[wave] = v;
