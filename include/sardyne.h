@@ -151,6 +151,18 @@ void op_rope(float *x, int n_heads, int head_dim, const float *cos, const float 
 void op_attention(float *out, const float *q, const float *k_cache, const float *v_cache, int n_head,
                   int n_kv_head, int head_dim, int n_kv, int stride, float *scores); /* csrc/ops.h:73-74 */
 
+/* ------------------------------------------------------------------ model memory
+ * No counterpart in the reference. The device memory a loaded model holds: its weights (the planes
+ * of every matrix, the same bytes as the file's tensors) and the prefill GEMM's tiled copies made at
+ * load, with the number of matrices that got a copy and that were left without one because the
+ * device had no room (the GEMM then reads the planes, with the same results). Returns 0, or -1 for
+ * a NULL model. */
+int sdy_model_memory(const engine_model *m, size_t *weight_bytes, size_t *gemm_copy_bytes, int *n_copies,
+                     int *n_skipped);
+/* Free and total device memory now (hipMemGetInfo); 0 or a negative code. No counterpart in the
+ * reference. */
+int sdy_mem_info(size_t *free_bytes, size_t *total_bytes);
+
 /* ------------------------------------------------------------------ device-level, no allocation
  * No counterpart in the reference. For callers that cannot allocate device memory: code recorded
  * under graph capture, tight serving loops, harnesses that forbid hipMalloc. The one-token decode
@@ -159,8 +171,11 @@ void op_attention(float *out, const float *q, const float *k_cache, const float 
  * xq_q8k is set), with its partials and counters in a fixed static device buffer instead of
  * caller scratch: at most 1 048 576 floats of partials (n_head * ceil(max_seq / 32) * (head_dim + 4))
  * and 256 kv heads; larger shapes are rejected with an error. It calls no allocator. Every call on a
- * GPU shares that GPU's buffer: calls that overlap on one GPU race. Device pointers; returns 0 or a
- * negative code (the message from the library's last-error call). */
+ * GPU shares that GPU's buffer: calls that overlap on one GPU race. sdy_init sets the buffer up on the
+ * device it selects; on another device the first call does (a launch and a wait on the null stream),
+ * and returns an error instead when the stream is being captured. A position step_dev[1] outside
+ * [0, max_seq) leaves out and the caches untouched. Device pointers; returns 0 or a negative code
+ * (the message from the library's last-error call). */
 int sdy_attn_decode_split_noalloc(const float *q, const float *k, const float *v, const float *q_norm,
                                   const float *k_norm, float eps, const float *rope_cos, const float *rope_sin,
                                   const int32_t *step_dev, int n_head, int n_kv_head, int head_dim, int interleaved,

@@ -118,6 +118,9 @@ _DEVICE_SIGNATURES = {
     "sdy_last_kernel": (ctypes.c_char_p, []),
     "sdy_init": (_int, []),
     "sdy_device_info": (_int, [ctypes.POINTER(_int), ctypes.POINTER(_sz)]),
+    "sdy_mem_info": (_int, [ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
+    "sdy_model_memory": (_int, [_vp, ctypes.POINTER(_sz), ctypes.POINTER(_sz), ctypes.POINTER(_int),
+                                ctypes.POINTER(_int)]),
     "sdy_malloc": (_int, [ctypes.POINTER(_vp), _sz]),
     "sdy_free": (_int, [_vp]),
     "sdy_h2d": (_int, [_vp, _vp, _sz, _vp]),

@@ -496,6 +496,52 @@ void engine_model_get_info(const engine_model *m, engine_model_info *out) {
     if (m && out) *out = m->info;
 }
 
+/* The prefill GEMM's tiled copies of the layer matrices (Q4_K / Q6_K, sdy_mat_gemm_layout): a second
+ * copy of those weights, from which the GEMM's loads read whole cache lines. They only make prompts
+ * faster (without one the GEMM reads the planes, with the same results), so they are made where the
+ * device has room: the attention and dense FFN matrices of every layer first, then the expert stacks
+ * (the bulk of a MoE file), each only if it leaves the reserve free for the contexts (KV caches, work
+ * buffers): SARDYNE_GEMM_RESERVE_MB, by default an eighth of the device memory and at least 2 GiB. An
+ * allocation that fails all the same skips that copy. SARDYNE_GEMM_COPY_MB caps the copies' total
+ * (MiB, fractions allowed; 0: no copies). */
+static int gemm_copies(loader *ld) {
+    engine_model *m = ld->m;
+    const engine_model_info *in = &m->info;
+    size_t free_b = 0, total = 0;
+    if (sdy_mem_info(&free_b, &total)) return device_fail(ld, "gemm layout");
+    size_t reserve = total / 8 > ((size_t)2 << 30) ? total / 8 : ((size_t)2 << 30);
+    const char *r = getenv("SARDYNE_GEMM_RESERVE_MB");
+    if (r && r[0]) reserve = (size_t)(strtod(r, NULL) * 1048576.0);
+    size_t cap = (size_t)-1;
+    const char *c = getenv("SARDYNE_GEMM_COPY_MB");
+    if (c && c[0]) cap = (size_t)(strtod(c, NULL) * 1048576.0);
+    for (int experts = 0; experts < 2; experts++) {
+        for (int l = 0; l < in->n_layer; l++) {
+            dlayer *L = &m->layers[l];
+            dmat *own[] = {L->qkv_parts < 2 ? &L->wq : NULL, L->qkv_parts < 2 ? &L->wk : NULL,
+                           L->qkv_parts < 3 ? &L->wv : NULL, L->qkv_parts >= 2 ? &L->wqkv : NULL, &L->wo,
+                           &L->gate, &L->up, &L->gate_up, &L->down};
+            for (size_t i = 0; i < sizeof own / sizeof *own; i++) {
+                if (!own[i] || !own[i]->m.base) continue;
+                if ((in->n_expert && i >= 5) != experts) continue; /* (i >= 5: the FFN matrices) */
+                const size_t need = sdy_mat_gemm_layout_bytes(&own[i]->m);
+                if (!need) continue;
+                if (sdy_mem_info(&free_b, NULL)) return device_fail(ld, "gemm layout");
+                const int room = free_b >= need + reserve && m->gemm_bytes + need <= cap;
+                const int rc = room ? sdy_mat_gemm_layout(&own[i]->m, m->st) : SDY_ERR_ALLOC;
+                if (rc == SDY_ERR_ALLOC) {
+                    m->gemm_skipped++;
+                    continue;
+                }
+                if (rc) return device_fail(ld, "gemm layout");
+                m->gemm_bytes += own[i]->m.gbytes;
+                m->gemm_copies++;
+            }
+        }
+    }
+    return sdy_sync(m->st) ? device_fail(ld, "gemm layout") : 0;
+}
+
 static int load(engine_model *m, const char *path, char *err, size_t len) {
     if (!(m->gf = gguf_open(path, err, len)) || read_config(m, err, len)) return -1;
     const engine_model_info *in = &m->info;
@@ -535,22 +581,7 @@ static int load(engine_model *m, const char *path, char *err, size_t len) {
     if (!rc && ld.up && sdy_uploader_finish(ld.up)) rc = device_fail(&ld, "upload");
     if (!rc && sdy_sync(m->st)) rc = device_fail(&ld, "upload");
     if (sdy_uploader_free(ld.up) && !rc) rc = device_fail(&ld, "upload");
-    if (!rc) {
-        /* the prefill GEMM's copies of the layer matrices (Q4_K / Q6_K; others: no-op), made from the
-           loaded planes: a second copy of those weights, rows in tiles of 32 */
-        for (int l = 0; !rc && l < in->n_layer; l++) {
-            dlayer *L = &m->layers[l];
-            dmat *own[] = {L->qkv_parts < 2 ? &L->wq : NULL, L->qkv_parts < 2 ? &L->wk : NULL,
-                           L->qkv_parts < 3 ? &L->wv : NULL, L->qkv_parts >= 2 ? &L->wqkv : NULL, &L->wo,
-                           &L->gate, &L->up, &L->gate_up, &L->down};
-            for (size_t i = 0; !rc && i < sizeof own / sizeof *own; i++) {
-                if (!own[i] || !own[i]->m.base) continue;
-                if (sdy_mat_gemm_layout(&own[i]->m, m->st)) rc = device_fail(&ld, "gemm layout");
-                else m->device_bytes += own[i]->m.gbytes;
-            }
-        }
-        if (!rc && sdy_sync(m->st)) rc = device_fail(&ld, "gemm layout");
-    }
+    if (!rc) rc = gemm_copies(&ld);
     if (!rc) {
         /* views taken before the exactness checks ran: take them again (gemm_ok of the stack) */
         for (int l = 0; l < in->n_layer; l++) {
@@ -566,6 +597,16 @@ static int load(engine_model *m, const char *path, char *err, size_t len) {
     }
     free(lt);
     return rc;
+}
+
+int sdy_model_memory(const engine_model *m, size_t *weight_bytes, size_t *gemm_copy_bytes, int *n_copies,
+                     int *n_skipped) {
+    if (!m) return -1;
+    if (weight_bytes) *weight_bytes = m->device_bytes;
+    if (gemm_copy_bytes) *gemm_copy_bytes = m->gemm_bytes;
+    if (n_copies) *n_copies = m->gemm_copies;
+    if (n_skipped) *n_skipped = m->gemm_skipped;
+    return 0;
 }
 
 engine_model *engine_model_load(const char *path, char *err, size_t err_len) {
@@ -672,23 +713,24 @@ engine_ctx *engine_ctx_new(const engine_model *m, int32_t max_seq, int32_t n_bat
         return NULL;
     }
     /* Switches that select between paths with identical results (used to compare them):
-       SARDYNE_NO_FUSED_DECODE  one-token steps on the unfused kernels;
        SARDYNE_NO_DEVICE_MOE    one-token MoE blocks grouped on the host, as prefill does;
        SARDYNE_NO_GRAPH         one-token steps issued eagerly instead of replayed;
-       SARDYNE_NO_FUSED_ACT     one-token matvecs read activations quantised by a separate launch. */
+       SARDYNE_NO_FUSED_ACT     one-token matvecs read activations quantised by a separate launch.
+       SARDYNE_NO_FUSED_DECODE  one-token steps on the unfused kernels: they take the exact attention
+                                chain, and so does the prompt (the results of SARDYNE_ATTENTION=exact). */
     c->decode_fused = !env_on("SARDYNE_NO_FUSED_DECODE") && sdy_engine_decode_fused_ok(c);
     c->moe_device = c->decode_fused && !env_on("SARDYNE_NO_DEVICE_MOE") && sdy_engine_moe_device_ok(c);
     c->use_graph = c->decode_fused && (!m->info.n_expert || c->moe_device) && !env_on("SARDYNE_NO_GRAPH");
     c->fuse_act = c->decode_fused && !env_on("SARDYNE_NO_FUSED_ACT");
     const engine_model_info *in = &m->info;
-    /* the prompt's attention: in flash form on the matrix cores unless the reference's bits are asked
-       for (SARDYNE_ATTENTION=exact) */
-    c->prefill_flash = c->attn_mode != SDY_ATTN_EXACT && sdy_attention_flash_ok(in->n_head, in->n_kv_head, in->head_dim);
     /* the split forms take the fused one-token step and their head layouts; otherwise the exact chain */
     if (!c->decode_fused || (c->attn_mode == SDY_ATTN_CHUNKED && !sdy_attn_chunked_ok(in->n_head, in->n_kv_head,
                                                                                       in->head_dim)) ||
         (c->attn_mode == SDY_ATTN_SPLIT && !sdy_attn_decode_split_ok(in->n_head, in->n_kv_head, in->head_dim)))
         c->attn_mode = SDY_ATTN_EXACT;
+    /* the prompt's attention: in flash form on the matrix cores with the split one-token forms; with
+       the exact chain the prompt keeps the reference's bits too */
+    c->prefill_flash = c->attn_mode != SDY_ATTN_EXACT && sdy_attention_flash_ok(in->n_head, in->n_kv_head, in->head_dim);
     return c;
 }
 

@@ -963,6 +963,12 @@ __global__ __launch_bounds__(256) void k_gemm_layout(const uint8_t *__restrict__
     else *reinterpret_cast<uint16_t *>(dst + o) = *reinterpret_cast<const uint16_t *>(src + (size_t)i * 2);
 }
 
+extern "C" size_t sdy_mat_gemm_layout_bytes(const sdy_mat *m) {
+    if (!m || !m->base || (m->type != SDY_Q4_K && m->type != SDY_Q6_K) || !m->gemm_ok || m->gbase) return 0;
+    size_t off[5], sz[5];
+    return gemm_layout_planes(m->type, m->n_in, m->n_rows, off, sz);
+}
+
 extern "C" int sdy_mat_gemm_layout(sdy_mat *m, sdy_stream s) {
     if (!m || !m->base || (m->type != SDY_Q4_K && m->type != SDY_Q6_K) || !m->gemm_ok) return 0;
     if (m->grow0 != 0 || (m->gbase && m->grows != m->n_rows))

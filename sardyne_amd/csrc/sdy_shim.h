@@ -21,6 +21,8 @@ typedef struct sdy_stream_s *sdy_stream; /* hipStream_t */
 
 const char *sdy_last_error(void);
 int sdy_init(void);                       /* selects the device, checks it is gfx950 */
+/* the code sdy_malloc returns when the device has no room */
+#define SDY_ERR_ALLOC (-4)
 int sdy_malloc(void **p, size_t n);
 int sdy_free(void *p);
 int sdy_h2d(void *dst, const void *src, size_t n, sdy_stream s);
@@ -33,6 +35,8 @@ int sdy_stream_free(sdy_stream s);
 int sdy_host_alloc(void **p, size_t n); /* pinned host memory */
 int sdy_host_free(void *p);
 int sdy_device_info(int *n_cu, size_t *mem_total);
+/* Free and total device memory now (hipMemGetInfo). */
+int sdy_mem_info(size_t *free_bytes, size_t *total_bytes);
 int sdy_event_new(void **ev);
 int sdy_event_record(void *ev, sdy_stream s);
 int sdy_event_elapsed(float *ms, void *e0, void *e1); /* waits for e1 */
@@ -88,6 +92,8 @@ int sdy_mat_repack_async(sdy_mat *m, long r0, long n, long step, long grp, long 
  * the prefill GEMM's loads (a load instruction then reads whole cache lines). Another upload into
  * the matrix frees it (the GEMM reads the planes until it is made again). Other types: no-op. */
 int sdy_mat_gemm_layout(sdy_mat *m, sdy_stream s);
+/* Bytes sdy_mat_gemm_layout would allocate for m (0: no copy for this type or matrix). */
+size_t sdy_mat_gemm_layout_bytes(const sdy_mat *m);
 
 /* Pipelined uploads (upload.hip): a ring of pinned host slots and device slots. A host thread pool
  * copies the next rows from the file mapping into a free pinned slot (advising the kernel to read

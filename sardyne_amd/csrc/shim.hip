@@ -97,6 +97,16 @@ extern "C" int sdy_device_info(int *n_cu, size_t *mem_total) {
     return 0;
 }
 
+extern "C" int sdy_mem_info(size_t *free_bytes, size_t *total_bytes) {
+    int rc = sdy_init();
+    if (rc) return rc;
+    size_t f = 0, t = 0;
+    HIPCK(hipMemGetInfo(&f, &t), "hipMemGetInfo");
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return 0;
+}
+
 extern "C" int sdy_malloc(void **p, size_t n) {
     int rc = sdy_init();
     if (rc) return rc;
@@ -105,7 +115,7 @@ extern "C" int sdy_malloc(void **p, size_t n) {
     hipError_t e = hipMalloc(p, n);
     if (e != hipSuccess) {
         (void)hipGetLastError();
-        return sdy_fail(-4, "device allocation of %.1f MB failed: %s", n / 1e6, hipGetErrorString(e));
+        return sdy_fail(SDY_ERR_ALLOC, "device allocation of %.1f MB failed: %s", n / 1e6, hipGetErrorString(e));
     }
     return 0;
 }
@@ -236,20 +246,34 @@ extern "C" int sdy_graph_free(void *exec) {
     return 0;
 }
 
-// ---- HBM read-bandwidth probe: every byte of buf read once with 16-byte loads (a grid-stride
-// sweep), an XOR of the data kept live so the loads are not removed.
-__global__ void k_membw_read(const uint4 *__restrict__ p, size_t n16, unsigned *sink) {
-    size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x, stride = (size_t)gridDim.x * blockDim.x;
+// ---- HBM read-bandwidth probe: every byte of buf read once, in the streaming weight kernels' load
+// pattern: non-temporal 16-byte loads, one 1 KiB contiguous span per wave and load instruction, eight
+// loads of a lane in flight before their data is used, over a grid the GPU holds at once (8
+// workgroups of 256 threads per CU). An XOR of the data is kept live so the loads are not removed.
+typedef unsigned int membw_u32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void k_membw_read(const membw_u32x4 *__restrict__ p, size_t n16, unsigned *sink) {
+    constexpr int U = 8;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     unsigned acc = 0;
+    for (; i + (U - 1) * stride < n16; i += U * stride) {
+        membw_u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = __builtin_nontemporal_load(p + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
     for (; i < n16; i += stride) {
-        uint4 v = p[i];
+        const membw_u32x4 v = __builtin_nontemporal_load(p + i);
         acc ^= v.x ^ v.y ^ v.z ^ v.w;
     }
     if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
 extern "C" int sdy_membw_read(const void *buf, size_t bytes, void *sink, sdy_stream s) {
-    hipLaunchKernelGGL(k_membw_read, dim3(2048), dim3(256), 0, (hipStream_t)s, (const uint4 *)buf, bytes / 16,
-                       (unsigned *)sink);
+    int rc = sdy_init();
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_membw_read, dim3((unsigned)(g_n_cu * 8)), dim3(256), 0, (hipStream_t)s,
+                       (const membw_u32x4 *)buf, bytes / 16, (unsigned *)sink);
     return sdy_check_launch("membw_read");
 }

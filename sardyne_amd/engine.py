@@ -42,6 +42,15 @@ class LoadedModel:
     def n_vocab(self) -> int:
         return self.info.n_vocab
 
+    def memory(self) -> dict:
+        """Device memory the model holds (sdy_model_memory): weight bytes, the prefill GEMM's tiled
+        copies, and how many matrices got a copy / were left without one."""
+        w, g, nc, ns = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_int(), ctypes.c_int()
+        capi.check(self._lib.sdy_model_memory(self._h, ctypes.byref(w), ctypes.byref(g), ctypes.byref(nc),
+                                              ctypes.byref(ns)))
+        return {"weight_bytes": w.value, "gemm_copy_bytes": g.value, "gemm_copies": nc.value,
+                "gemm_copies_skipped": ns.value}
+
     def session(self, max_seq: int = 2048, n_batch: int = 64, logits_all: bool = False,
                 n_threads: int = 0) -> "Session":
         return Session(self, max_seq, n_batch, logits_all, n_threads)

@@ -11,8 +11,9 @@
       the logit scale (same greedy tokens) with the one-launch split attention.
   C5  the Qwen3-30B-A3B-shaped qwen3moe model (128 experts resident, top-8): a 1024-token context
       (two 512-token chunks), then one-token steps through the device router: the exact chain
-      bit-identical, the split attention within 1e-2 of the logit scale (the spread between the
-      reference's own AVX2 and scalar engines here reaches 5.6e-3) with the same greedy tokens.
+      bit-identical, the chunked and split attentions within twice the spread between the
+      reference's own AVX2 and scalar engines on the same model and tokens (golden/c5_simd_spread.npz),
+      with the same greedy tokens.
 
 The models are written to /dev/shm (2.2 GB and 19.8 GB) and deleted afterwards.
 """
@@ -137,14 +138,65 @@ def test_c3_c4_qwen25_3b_prefill_512_then_decode(qwen25_3b_path):
     _run_and_compare(qwen25_3b_path, 512, 512, 6, 640, seed=0, tol=1e-4)
 
 
+def test_c3_loads_under_memory_pressure(qwen25_3b_path):
+    """The Qwen2.5-3B-shaped model on a device with little room: a ballast allocation leaves free only
+    the weights, half of the prefill GEMM's tiled copies and 512 MiB, so the weights are more than
+    half of the memory left to the model. It loads, the copies are made for what fits (a 256 MiB
+    reserve), and the 512-token prompt on the GEMM and two decode steps give the logits bits of the
+    load with every copy (the exact attention chain in both)."""
+    L = capi.lib()
+    capi.check(L.sdy_init())
+    toks = np.random.default_rng(3).integers(0, 151936, 514).astype(np.int32)
+
+    def run():
+        with engine_env(SARDYNE_ATTENTION="exact", SARDYNE_GEMM_RESERVE_MB="256"):
+            model = LoadedModel(qwen25_3b_path)
+            s = model.session(max_seq=640, n_batch=512)
+        out = np.stack([s.feed(toks[:512]), s.step(int(toks[512])), s.step(int(toks[513]))])
+        return out, model.memory()
+
+    base, mem = run()
+    assert mem["gemm_copies"] > 0 and mem["gemm_copies_skipped"] == 0
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    capi.check(L.sdy_mem_info(ctypes.byref(free), ctypes.byref(total)))
+    room = mem["weight_bytes"] + mem["gemm_copy_bytes"] // 2 + (512 << 20)
+    assert free.value > room
+    ballast = capi.DeviceBuffer(free.value - room)
+    try:
+        got, mem2 = run()
+    finally:
+        ballast.close()
+    assert mem2["weight_bytes"] == mem["weight_bytes"] and mem2["weight_bytes"] > room // 2
+    assert mem2["gemm_copies_skipped"] > 0 and 0 < mem2["gemm_copy_bytes"] < mem["gemm_copy_bytes"]
+    assert np.all(np.isfinite(base))
+    assert np.array_equal(base.view(np.uint32), got.view(np.uint32))
+
+
+# How far the reference's own AVX2 and scalar engines drift apart on the C5 model and tokens (they
+# differ only in float summation orders): written by golden/make_c5_spread.py from the reference
+# compiled from its sources. The split one-token attentions change f32 rounding only, and are held to
+# SPREAD_MULTIPLE times the largest of that spread.
+SPREAD_MULTIPLE = 2.0
+
+
+def c5_tolerance():
+    g = np.load(GOLDEN / "c5_simd_spread.npz")
+    toks = np.random.default_rng(1).integers(0, 151936, 1024 + 5).astype(np.int32)
+    assert str(g["tok_sha"]) == sha(toks), "the fixture was made for other tokens"
+    assert int(g["n_ctx"]) == 1024 and int(g["n_steps"]) == 5 and int(g["model_seed"]) == 0
+    assert bool(np.all(g["argmax_equal"]))
+    return SPREAD_MULTIPLE * float(g["spread"].max()) / float(g["scale"])
+
+
 @needs_ref
 def test_c5_qwen3_30b_a3b_context_1024_then_decode():
+    """48 layers of int8 activation rounding and top-8 routing amplify any change of f32 rounding: the
+    exact chain gives the reference's bits, the chunked and split attentions stay within twice the
+    reference's own AVX2-vs-scalar spread on this model and token sequence, with the same greedy
+    tokens."""
+    tol = c5_tolerance()
     p = _shm_model(qwen3_30b_a3b(), "qwen3_30b_a3b")
     try:
-        # 48 layers of int8 activation rounding and top-8 routing amplify any change of f32 rounding:
-        # the reference's own AVX2 and scalar engines (which differ only in float summation orders)
-        # differ by up to 5.6e-3 of the logit scale on this model and token sequence within five steps,
-        # with the same greedy tokens. The split attention is held to 1e-2 and the same greedy tokens.
-        _run_and_compare(p, 1024, 512, 5, 1152, seed=1, tol=1e-2)
+        _run_and_compare(p, 1024, 512, 5, 1152, seed=1, tol=tol)
     finally:
         p.unlink(missing_ok=True)

@@ -318,3 +318,40 @@ def test_long_context_decode(spec, tmp_path):
     ref = O.OracleContext(path, 200, n_batch=64, simd=0)
     exp = [ref.eval(toks[:140])] + [ref.eval([t]) for t in toks[140:]]
     assert_close(np.stack(got), np.stack(exp))
+
+
+
+def _memory(model):
+    m = model.memory()
+    return m["weight_bytes"], m["gemm_copy_bytes"], m["gemm_copies"], m["gemm_copies_skipped"]
+
+
+@pytest.mark.parametrize("copies", ["all", "none", "some"])
+def test_gemm_copies_are_optional(tmp_path, copies):
+    """The prefill GEMM's tiled weight copies only change where its loads read from: a model loaded
+    with every copy, with none (SARDYNE_GEMM_COPY_MB=0) or with the copies that half their bytes
+    leave room for gives the same logits bits for a prompt on the GEMM and the steps after it."""
+    spec = dataclasses.replace(SPECS["qwen2-kquant-vmix"], n_layer=4)
+    p = tmp_path / "m.gguf"
+    write_model(p, spec, seed=7)
+    prompt = list(np.random.default_rng(8).integers(0, 300, 40))
+
+    def logits(**env):
+        with engine_env(SARDYNE_ATTENTION="exact", **env):
+            model = LoadedModel(p)
+            s = model.session(max_seq=64, n_batch=32)
+        return np.stack([s.feed(prompt)] + [s.step(t) for t in (4, 99, 250)]), _memory(model)
+
+    base, (w, g, nc, ns) = logits()
+    assert nc > 0 and ns == 0 and g > 0 and w > 0
+    if copies == "none":
+        got, mem = logits(SARDYNE_GEMM_COPY_MB="0")
+        assert mem == (w, 0, 0, nc)
+    elif copies == "some":
+        got, (w2, g2, nc2, ns2) = logits(SARDYNE_GEMM_COPY_MB=repr(g / 2 / 1048576))
+        assert w2 == w and 0 < nc2 < nc and nc2 + ns2 == nc and 0 < g2 <= g / 2
+    else:
+        got, mem = logits()
+        assert mem == (w, g, nc, ns)
+    assert np.all(np.isfinite(base))
+    assert np.array_equal(base.view(np.uint32), got.view(np.uint32))

@@ -1,7 +1,8 @@
 """MoE edge cases of the reference's tests (tests/test_moe.py:147-157, 370-406), through the engine ABI on
-the GPU, on both MoE paths: the prompt's prefill chunk (experts grouped on the host, GEMM or multi-token
-matvecs) and one-token decode steps (device router, grouped matvec over the routed experts, replayed
-from the recorded decode graph).
+the GPU, on both MoE paths: the prompt's prefill chunk (16 tokens x top-2 = 32 routed rows: the router,
+sort and grouped GEMMs on the device; SARDYNE_NO_GROUPED_MOE=1 groups the experts on the host instead)
+and one-token decode steps (device router, grouped matvec over the routed experts, replayed from the
+recorded decode graph).
 
   - unused experts poisoned with NaN scales change no bit of the logits: only routed experts are read;
   - identical experts equal the dense MLP of the same weights (the renormalised weights sum to 1);
@@ -22,13 +23,25 @@ from sardyne_amd.gguf_synth import write_model
 pytestmark = pytest.mark.gpu
 
 
-def run(path, n_batch=16, mode="exact"):
+def run(path, n_batch=16, mode="exact", **switches):
     """Prompt logits, then one-token steps' logits (stacked), with the one-token attention `mode`
-    (SARDYNE_ATTENTION: exact, chunked or split)."""
-    model = LoadedModel(path)
-    with engine_env(SARDYNE_ATTENTION=mode):
+    (SARDYNE_ATTENTION: exact, chunked or split) and the environment switches given, set while the
+    model loads and the context is made."""
+    with engine_env(SARDYNE_ATTENTION=mode, **switches):
+        model = LoadedModel(path)
         s = model.session(max_seq=48, n_batch=n_batch)
     return np.stack([s.feed(PROMPT)] + [s.step(t) for t in STEPS])
+
+
+@pytest.mark.parametrize("switch", ["SARDYNE_UPLOAD_SYNC", "SARDYNE_NO_GROUPED_MOE", "SARDYNE_GEMM_COPY_MB"])
+def test_load_and_prefill_switches_keep_the_bits(tmp_path, switch):
+    """The synchronous per-tensor upload, the host-grouped MoE prefill and a load without the GEMM's
+    tiled weight copies give the default run's logits bit for bit."""
+    p = write_model(tmp_path / "m.gguf", MOE, seed=3)
+    base = run(p)
+    got = run(p, **{switch: "0" if switch == "SARDYNE_GEMM_COPY_MB" else "1"})
+    assert np.all(np.isfinite(base))
+    assert np.array_equal(base.view(np.uint32), got.view(np.uint32))
 
 
 def test_unused_experts_poisoned_with_nan_change_nothing(tmp_path):
