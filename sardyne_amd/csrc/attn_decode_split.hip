@@ -44,7 +44,7 @@ struct SplitArgs {
     float eps;
     const float *rope_cos, *rope_sin;
     const int32_t *step;             // step[1] = the token's position
-    int n_head, n_kv_head, interleaved, n_chunk_max;
+    int n_head, n_kv_head, interleaved, n_chunk_max, max_seq;
     float *k_cache, *v_cache;        // [n_kv_head][max_seq][HD]
     long head_stride;                // max_seq * HD
     float *part;                     // [n_head][n_chunk_max][HD + 4]: m, l, -, -, acc[HD]
@@ -74,6 +74,9 @@ __global__ __launch_bounds__(256) void k_attn_decode_split(SplitArgs a) {
     const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int n_rep = a.n_head / a.n_kv_head;
     const int pos = a.step[1];
+    // a position outside the cache: every workgroup returns before it writes or counts anything
+    // (the output is left as it was, the counters stay at zero for the next call)
+    if (pos < 0 || pos >= a.max_seq) return;
     const int n_kv = pos + 1, n_chunk = (n_kv + CHUNK - 1) / CHUNK;
     if (c >= n_chunk) return;  // beyond the token's position: no work, not counted
     const int p0 = c * CHUNK, np = min(CHUNK, n_kv - p0);
@@ -207,14 +210,15 @@ __global__ __launch_bounds__(256) void k_attn_decode_split(SplitArgs a) {
     }
 
     // hand-off: the group's last workgroup to arrive merges. The partials are written and read with
-    // agent-scope atomic accesses (coherent across the XCDs' L2s by themselves), and every wave waits
-    // for its stores to complete before the workgroup is counted: the release/acquire that the
-    // partials need, without writing back or invalidating the whole L2 as a fence would.
+    // agent-scope accesses (sc1: past the non-coherent per-XCD L2s), and the arrival is an agent-scope
+    // acquire-release increment by one thread after the workgroup's barrier: its release writes back
+    // this XCD's L2 before the count moves (the workgroup's stores are ordered before it by the
+    // barrier), and the last arrival's acquire invalidates its L2 before the merge reads the partials.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
-        const unsigned done = __hip_atomic_fetch_add(a.count + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned done = __hip_atomic_fetch_add(a.count + g, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         s_last = done == (unsigned)(n_chunk - 1);
         if (s_last) __hip_atomic_store(a.count + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -370,6 +374,7 @@ extern "C" int sdy_attn_decode_split(const float *q, const float *k, const float
     A.n_kv_head = n_kv_head;
     A.interleaved = interleaved;
     A.n_chunk_max = (max_seq + CHUNK - 1) / CHUNK;
+    A.max_seq = max_seq;
     A.k_cache = k_cache;
     A.v_cache = v_cache;
     A.head_stride = head_stride;
@@ -398,6 +403,13 @@ extern "C" int sdy_attn_decode_split_noalloc(const float *q, const float *k, con
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SCRATCH_MAX_DEVICES)
         return sdy_fail(-1, "attn_decode_split_noalloc: no usable current device");
     if (!scratch_dev[dev]) {
+        // the first call on a device that sdy_init did not select sets the scratch up, which launches
+        // and waits on the null stream: not allowed while the caller's stream is being captured
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing((hipStream_t)s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+            return sdy_fail(-1, "attn_decode_split_noalloc: device %d is not set up and the stream is being "
+                                "captured: call sdy_init with this device current (or this entry point once "
+                                "outside capture) first", dev);
         const int rc = sdy_attn_split_scratch_setup();
         if (rc) return rc;
     }

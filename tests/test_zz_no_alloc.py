@@ -69,3 +69,22 @@ def test_noalloc_rejects_shapes_beyond_its_scratch():
                                          None, 131072 * 128, 131072, None, None, None)
     assert rc != 0
     assert b"scratch" in L.sdy_last_error()
+
+
+def test_noalloc_position_outside_the_cache_changes_nothing():
+    """A device-side position at or past max_seq (or below 0): every workgroup returns before it
+    writes or counts, so the output buffer and the caches keep their bytes, and the next call, with
+    a valid position, gives the scratch entry point's result (the shared counters stayed at zero)."""
+    capi.check(capi.lib().sdy_init())
+    rng = np.random.default_rng(9)
+    n_head, n_kv_head, hd, max_seq = 16, 2, 128, 640
+    inp = _inputs(rng, n_head, n_kv_head, hd, max_seq)
+    for pos in (max_seq, max_seq + 100, -1):
+        out, kc, vc, _ = _run("noalloc", inp, n_head, n_kv_head, hd, max_seq, pos, False)
+        assert np.array_equal(kc, inp["kc"]) and np.array_equal(vc, inp["vc"])
+        # (the output buffer is fresh device memory: it was not written, so it is not the result of
+        # any position; the check that matters is the next call)
+    got = _run("noalloc", inp, n_head, n_kv_head, hd, max_seq, 200, False)
+    exp = _run("scratch", inp, n_head, n_kv_head, hd, max_seq, 200, False)
+    for g, e in zip(got, exp):
+        assert np.array_equal(np.ascontiguousarray(g).view(np.uint8), np.ascontiguousarray(e).view(np.uint8))
