@@ -348,3 +348,16 @@ def test_oracle_moe_invariants(tmp_path):
         R = O.RefEngine(z, 48, n_batch=16)
         r = np.stack([R.eval(PROMPT)] + [R.eval([t]) for t in STEPS])
         assert np.array_equal(a.view(np.uint32), r.view(np.uint32))
+
+
+def test_c5_spread_fixture_is_for_the_c5_test():
+    """golden/c5_simd_spread.npz (made by golden/make_c5_spread.py from the reference compiled from its
+    sources) is the AVX2-vs-scalar spread of the reference engine on the C5 test's model and tokens:
+    its token digest matches the test's tokens, both engines agree on every argmax, and the spread is
+    a rounding-level drift (between 1e-4 and 1e-2 of the logit scale) that the test's bound follows."""
+    g = np.load(GOLDEN / "c5_simd_spread.npz")
+    toks = np.random.default_rng(1).integers(0, 151936, 1024 + 5).astype(np.int32)
+    assert str(g["tok_sha"]) == hashlib.sha256(toks.tobytes()).hexdigest()
+    assert g["spread"].shape == (6,) and bool(np.all(g["argmax_equal"]))
+    rel = float(g["spread"].max()) / float(g["scale"])
+    assert 1e-4 < rel < 1e-2
