@@ -9,7 +9,8 @@ Other workloads (--workload): q8_0_head (the Q8_0 matvec of the same shape), q4k
 2048 Q4_K, measured as one launch over 448 stacked copies), decode_3b (Qwen2.5-3B-shaped Q4_K_M
 decode tok/s, 128 tokens after a 512-token context), decode_moe (Qwen3-30B-A3B-shaped MoE decode,
 128 tokens after a 1024-token context), prefill_3b (one 512-token prompt through the
-Qwen2.5-3B-shaped model).
+Qwen2.5-3B-shaped model), grid_barrier (the per-phase synchronisation a persistent decode kernel
+would pay, against the kernel boundary).
 
 Every line carries:
   roofline      the dominant kernel's algorithmic bytes / its average duration (HIP events on the
@@ -91,12 +92,12 @@ def per_launch_ms(stream, launch, n):
 
 
 def profiled_traffic(name):
-    """HBM bytes per launch of a kernel, from the PMC summary committed under profiles/
-    (FETCH_SIZE and WRITE_SIZE scaled by copy-kernel calibration); None when absent."""
+    """HBM bytes per launch of a kernel (or per decode token of a step), from the PMC summary committed
+    under profiles/ (FETCH_SIZE and WRITE_SIZE scaled by copy-kernel calibration); None when absent."""
     p = ROOT / "profiles" / name
     try:
         for line in p.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
+            if line.startswith(("traffic_bytes_per_launch:", "traffic_bytes_per_token:")):
                 return int(line.split(":", 1)[1])
     except OSError:
         pass
@@ -129,6 +130,31 @@ def cpu_matvec_baseline(wt, w_copies, x, n_in, seconds, n_threads):
     n_threads 0 = the reference's default (the online CPUs). Returns (seconds per rep, reps, threads)."""
     import oracle as O
     return O.ref_cpu_matvec(wt, w_copies, x, n_in, seconds, n_threads)
+
+
+def host_membw(max_threads=None):
+    """Host read bandwidth from the reference's own tool (tools/membw.c with its thread pool, built
+    into oracle/_ref/membw): a 512 MB buffer summed with AVX2 by 1..N threads, best of 5 each.
+    Returns {"1": GB/s at one thread, "best": GB/s, "best_threads": n, "threads_swept": N} or None."""
+    import subprocess
+    exe = ROOT / "oracle" / "_ref" / "membw"
+    if not exe.exists():
+        return None
+    n = max_threads or min(os.cpu_count() or 1, 64)
+    try:
+        out = subprocess.run([str(exe), "512", str(n)], capture_output=True, text=True, timeout=120).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    rows = {}
+    for line in out.splitlines():
+        f = line.split()
+        if len(f) == 2 and f[0].isdigit():
+            rows[int(f[0])] = float(f[1])
+    if not rows:
+        return None
+    bt = max(rows, key=rows.get)
+    return {"1": rows.get(1), "best": rows[bt], "best_threads": bt, "threads_swept": n,
+            "tool": "the reference's tools/membw.c (AVX2 read, 512 MB)"}
 
 
 def host_cpu_model():
@@ -257,9 +283,10 @@ def bench_matvec(args, wt, n_out, n_in, n_copies, stacked):
         try:
             import oracle as O
             if O.ref_available():
-                n_cpu_copies = max(2, int(np.ceil(512e6 / w_bytes))) if not stacked else 64
+                # at least 2 GB of distinct copies, beyond the host's last-level cache
+                n_cpu_copies = min(max(2, int(np.ceil(2e9 / w_bytes))), 1024)
                 copies = [w0] + [random_blocks(name, n_out * n_in // e, np.random.default_rng(200 + c)).reshape(n_out, -1)
-                                 for c in range(min(n_cpu_copies, 64) - 1)]
+                                 for c in range(n_cpu_copies - 1)]
                 dt, reps, n_cpu = cpu_matvec_baseline(wt, copies, x, n_in, args.cpu_seconds, 0)
                 dt1, _, _ = cpu_matvec_baseline(wt, copies, x, n_in, max(2.0, args.cpu_seconds / 4), 1)
                 cpu = {"value": round(algo_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": n_cpu, "kind": "reference",
@@ -327,52 +354,85 @@ def kv_bytes_per_position(spec):
     return 2 * spec.n_layer * spec.n_kv_head * spec.head_dim * elt
 
 
+def keep_models():
+    """SARDYNE_BENCH_KEEP=1: model files are kept after the run and reused by the next one (several
+    profiler passes over one workload write the file once)."""
+    return os.environ.get("SARDYNE_BENCH_KEEP", "0") not in ("", "0")
+
+
 def write_bench_model(spec, label):
     from sardyne_amd.gguf_synth import write_model
     tmpdir = Path(os.environ.get("SARDYNE_BENCH_DIR", "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()))
-    path = tmpdir / f"sardyne_bench_{label}.gguf"
+    path = tmpdir / f"sardyne_bench_{label}_{spec.n_layer}l_{spec.scales}.gguf"
+    if keep_models() and path.exists():
+        log(f"[bench] reusing {path}")
+        return path
     t0 = time.perf_counter()
     write_model(path, spec, seed=0)
     log(f"[bench] wrote {path} ({path.stat().st_size / 1e9:.2f} GB) in {time.perf_counter() - t0:.1f}s")
     return path
 
-def bench_decode(args, spec, ctx_len, n_decode, label):
+
+def drop_bench_model(path):
+    if not keep_models():
+        path.unlink(missing_ok=True)
+
+def bench_decode(args, spec, ctx_len, n_decode, label, path=None):
     """Decode tok/s after a ctx_len-token context at batch 1 (the method of the reference's
     bench/bench_decode.py:39-48: n_decode / wall time of the decode loop). Token ids are uniform
     over the vocabulary (seeded) and fed teacher-forced, so the GPU and the CPU reference see the
-    same sequence and their logits are compared step by step."""
+    same sequence and their logits are compared step by step. The same steps with the f16 KV cache
+    (SARDYNE_KV=f16) are compared with the f32 reference too. path: a model file written already
+    (kept), else one is written and deleted."""
     from sardyne_amd.engine import LoadedModel
-    path = write_bench_model(spec, label)
+    own_file = path is None
+    if own_file:
+        path = write_bench_model(spec, label)
     rng = np.random.default_rng(0)
     toks = rng.integers(0, spec.n_vocab, ctx_len + n_decode).astype(np.int32)
-    try:
-        t0 = time.perf_counter()
-        model = LoadedModel(path)
-        t_load = time.perf_counter() - t0
-        log(f"[bench] GPU model load {t_load:.2f}s")
-        ctx = model.session(max_seq=ctx_len + n_decode + 1, n_batch=args.n_batch)
-        ctx.feed(toks[:ctx_len])  # the prompt kernels' first launches (code loading), untimed
-        ctx.clear()
-        t0 = time.perf_counter()
+    t0 = time.perf_counter()
+    model = LoadedModel(path)
+    t_load = time.perf_counter() - t0
+    mem = model.memory()
+    log(f"[bench] GPU model load {t_load:.2f}s")
+    ctx = model.session(max_seq=ctx_len + n_decode + 1, n_batch=args.n_batch)
+    ctx.feed(toks[:ctx_len])  # the prompt kernels' first launches (code loading), untimed
+    ctx.clear()
+    t0 = time.perf_counter()
+    ctx.feed(toks[:ctx_len])
+    t_prefill = time.perf_counter() - t0
+    gpu_logits = []
+    t0 = time.perf_counter()
+    for i in range(n_decode):
+        gpu_logits.append(ctx.feed([int(toks[ctx_len + i])]))
+    t_dec = time.perf_counter() - t0
+    gpu_tok_s = n_decode / t_dec
+    log(f"[bench] GPU prefill {ctx_len} tok in {t_prefill:.3f}s, decode {gpu_tok_s:.1f} tok/s")
+    del ctx
+    # the same prompt and steps with the f16 cache (untimed: its drift from the f32 reference)
+    f16_logits = []
+    # (only when the reference runs beside it: the drift is measured against its logits; the split
+    # form has no f16 cache)
+    if args.cpu_seconds > 0 and engine_modes() in (("chunked", "f32"), ("exact", "f32")):
+        saved = os.environ.get("SARDYNE_KV")
+        os.environ["SARDYNE_KV"] = "f16"
+        try:
+            ctx = model.session(max_seq=ctx_len + n_decode + 1, n_batch=args.n_batch)
+        finally:
+            if saved is None:
+                os.environ.pop("SARDYNE_KV", None)
+            else:
+                os.environ["SARDYNE_KV"] = saved
         ctx.feed(toks[:ctx_len])
-        t_prefill = time.perf_counter() - t0
-        gpu_logits = []
-        t0 = time.perf_counter()
-        for i in range(n_decode):
-            gpu_logits.append(ctx.feed([int(toks[ctx_len + i])]))
-        t_dec = time.perf_counter() - t0
-        gpu_tok_s = n_decode / t_dec
-        log(f"[bench] GPU prefill {ctx_len} tok in {t_prefill:.3f}s, decode {gpu_tok_s:.1f} tok/s")
-        del ctx, model
-    finally:
-        pass
+        f16_logits = [ctx.feed([int(toks[ctx_len + i])]) for i in range(n_decode)]
+        del ctx
+    del model
     cpu = None
     parity = {}
     if args.cpu_seconds > 0:
         try:
             import oracle as O
             if O.ref_available():
-                n_cpu = os.cpu_count() or 1
                 eng = O.RefEngine(path, ctx_len + n_decode + 1, n_batch=64, n_threads=0)
                 t0 = time.perf_counter()
                 eng.eval(toks[:ctx_len])
@@ -383,33 +443,58 @@ def bench_decode(args, spec, ctx_len, n_decode, label):
                     cpu_logits.append(eng.eval([int(toks[ctx_len + n_cpu_steps])]))
                     n_cpu_steps += 1
                 t_cpu = time.perf_counter() - t0
-                cpu = {"value": round(n_cpu_steps / t_cpu, 3), "unit": "tok/s", "cores": eng.n_threads,
+                n_thr = eng.n_threads
+                del eng
+                # one thread (bounded: a 16-token context, then a few steps)
+                eng1 = O.RefEngine(path, 64, n_batch=16, n_threads=1)
+                eng1.eval(toks[:16])
+                n1 = 0
+                t0 = time.perf_counter()
+                while n1 < 32 and (time.perf_counter() - t0 < max(2.0, args.cpu_seconds / 4) or n1 < 2):
+                    eng1.eval([int(toks[16 + n1])])
+                    n1 += 1
+                t1 = time.perf_counter() - t0
+                del eng1
+                cpu = {"value": round(n_cpu_steps / t_cpu, 3), "unit": "tok/s", "cores": n_thr,
                        "kind": "reference",
                        "sample": f"reference engine, {n_cpu_steps} decode steps after a {ctx_len}-token prefill "
-                                 f"(prefill {ctx_len / t_pre_cpu:.1f} tok/s, n_batch 64), {host_cpu_model()}"}
+                                 f"(prefill {ctx_len / t_pre_cpu:.1f} tok/s, n_batch 64), {host_cpu_model()}",
+                       "single_thread": {"value": round(n1 / t1, 3), "unit": "tok/s",
+                                         "sample": f"{n1} decode steps after a 16-token context (one thread)"}}
+                hb = host_membw()
+                if hb:
+                    cpu["host_read_GBps"] = hb
                 g = np.stack(gpu_logits[:n_cpu_steps])
                 c = np.stack(cpu_logits)
+                scale = float(np.abs(c).max())
                 maxabs = float(np.abs(g - c).max())
                 parity = {"steps_compared": n_cpu_steps, "logits_max_abs": maxabs,
-                          "logits_max_abs_over_max_ref": maxabs / float(np.abs(c).max()),
+                          "logits_max_abs_over_max_ref": maxabs / scale,
                           "greedy_argmax_agreement": float(np.mean(g.argmax(-1) == c.argmax(-1)))}
+                if f16_logits:
+                    h = np.stack(f16_logits[:n_cpu_steps])
+                    d = float(np.abs(h - c).max())
+                    parity["kv_f16_vs_f32_reference"] = {
+                        "logits_max_abs": d, "logits_max_abs_over_max_ref": d / scale,
+                        "rel_l2": float(np.linalg.norm(h - c) / np.linalg.norm(c)),
+                        "greedy_argmax_agreement": float(np.mean(h.argmax(-1) == c.argmax(-1)))}
         except Exception as ex:
             cpu = {"error": str(ex)}
     size = path.stat().st_size
     load = {"s": round(t_load, 3), "file_bytes": size, "gb_per_s": round(size / t_load / 1e9, 2),
+            "device_weight_bytes": mem["weight_bytes"], "gemm_copy_bytes": mem["gemm_copy_bytes"],
+            "gemm_copies": mem["gemm_copies"], "gemm_copies_skipped": mem["gemm_copies_skipped"],
             "upload": "synchronous per tensor" if os.environ.get("SARDYNE_UPLOAD_SYNC", "0") not in ("", "0")
             else "pipelined (4 x 64 MiB pinned slots)",
             "file": "tmpfs" if str(path).startswith("/dev/shm") else "disk"}
-    try:
-        path.unlink()
-    except OSError:
-        pass
+    if own_file:
+        drop_bench_model(path)
     return gpu_tok_s, t_prefill, cpu, parity, load
 
 
-def decode_line(args, spec, label, ctx_len, desc, n_dec=None):
+def decode_line(args, spec, label, ctx_len, desc, n_dec=None, path=None):
     n_dec = n_dec or max(args.steps, 8)
-    tok_s, t_pre, cpu, parity, load = bench_decode(args, spec, ctx_len, n_dec, label)
+    tok_s, t_pre, cpu, parity, load = bench_decode(args, spec, ctx_len, n_dec, label, path)
     w_bytes = decode_weight_bytes(spec)
     kv_mean = kv_bytes_per_position(spec) * (ctx_len + n_dec / 2)
     gbps = (w_bytes + kv_mean) * tok_s / 1e9
@@ -427,7 +512,8 @@ def decode_line(args, spec, label, ctx_len, desc, n_dec=None):
             "data": "synthetic (random-init Q4_K_M weights, uniform token ids)", "config": cfg,
             f"prefill_{ctx_len}_s": round(t_pre, 4),
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(f"decode_{label}.md"),
+                         "traffic_unit": "HBM bytes per decode token (PMC, profiles/)",
                          "kernel": "whole decode step (weights + mean KV bytes per token)"},
             "cpu_baseline": cpu, "parity": parity, "model_load": load}
     if cpu and "value" in cpu:
@@ -478,12 +564,15 @@ def gemm_gate_up_ms(spec, n_tok, reps):
     return per_launch_ms(st, launch, reps), 2.0 * rows * n_in * n_tok, kernel
 
 
-def prefill_line(args, spec, label, n_prompt, desc):
+def prefill_line(args, spec, label, n_prompt, desc, path=None):
     """Prefill tok/s of one n_prompt-token eval (n_batch = n_prompt), the median over --steps
-    fresh evals, with the whole prefill's MFMA utilisation and the dominant GEMM's roofline."""
+    fresh evals, with the whole prefill's MFMA utilisation and the dominant GEMM's roofline. path: a
+    model file written already (kept), else one is written and deleted."""
     from sardyne_amd.engine import LoadedModel
     MFMA_PEAK = 2500.0  # TFLOP/s, dense f16/bf16
-    path = write_bench_model(spec, label)
+    own_file = path is None
+    if own_file:
+        path = write_bench_model(spec, label)
     toks = np.random.default_rng(0).integers(0, spec.n_vocab, n_prompt).astype(np.int32)
     model = LoadedModel(path)
     ctx = model.session(max_seq=n_prompt + 1, n_batch=n_prompt)
@@ -526,10 +615,8 @@ def prefill_line(args, spec, label, n_prompt, desc):
                           "greedy_argmax_agreement": float(gpu_logits.argmax() == c.argmax())}
         except Exception as ex:
             cpu = {"error": str(ex)}
-    try:
-        path.unlink()
-    except OSError:
-        pass
+    if own_file:
+        drop_bench_model(path)
     line = {"metric": METRIC, "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(t * 1e3, 3), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "int8 activations x Q4_K/Q6_K weights on f16 MFMA (exact integer sums)",
@@ -544,6 +631,41 @@ def prefill_line(args, spec, label, n_prompt, desc):
     return line
 
 
+def barrier_line(args):
+    """What a persistent decode kernel would pay per phase: grid barriers over co-resident grids of
+    256 and 512 workgroups (one and two per CU), flat, two-level (per XCD, then the grid) and two-level
+    with the XCD leaders' release/acquire fences, each publishing data that is read back and checked;
+    idle and while the other waves stream 4 GiB from HBM (four passes). Beside them, the kernel
+    boundary they would replace: empty kernels back to back from a replayed graph and eagerly."""
+    L = capi.lib()
+    rounds = 2000
+    forms = ((0, "flat"), (1, "two_level"), (2, "two_level_fenced"))
+    results = []
+    for n_wg in (256, 512):
+        for mode, name in forms:
+            for stream_mb in (0, 4096):
+                st = capi.SdyBarrierStats()
+                capi.check(L.sdy_grid_barrier_probe(n_wg, rounds, mode, stream_mb, ctypes.byref(st)))
+                r = {"workgroups": n_wg, "form": name, "hbm_stream": bool(stream_mb),
+                     "us_median": round(st.us_median, 3), "us_mean": round(st.us_mean, 3),
+                     "rounds": st.rounds_done, "timeouts": st.timeouts, "mismatches": st.mismatches}
+                if stream_mb:
+                    r.update({"us_mean_while_streaming": round(st.us_mean_streaming, 3),
+                              "rounds_while_streaming": st.rounds_streaming})
+                results.append(r)
+                log(f"[bench] barrier {n_wg} {name} stream={bool(stream_mb)}: {r}")
+    ug, ue = ctypes.c_float(), ctypes.c_float()
+    capi.check(L.sdy_kernel_boundary_us(2000, ctypes.byref(ug), ctypes.byref(ue)))
+    best = next(r for r in results if r["workgroups"] == 256 and r["form"] == "two_level_fenced" and not r["hbm_stream"])
+    return {"metric": METRIC, "value": best["us_median"], "unit": "us per grid barrier (256 workgroups, idle)",
+            "n_gpus": 1, "steps": rounds, "warmup": 0, "ms_per_step": round(best["us_median"] / 1e3, 6),
+            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "n/a (synchronisation)",
+            "data": "synthetic (64 floats per workgroup per round, checked)",
+            "config": {"workload": "grid barrier of a persistent kernel vs the kernel boundary"},
+            "kernel_boundary_us": {"graph_replay": round(ug.value, 3), "eager": round(ue.value, 3)},
+            "barriers": results, "roofline": None, "cpu_baseline": None}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -551,7 +673,8 @@ def main():
                     help="timed steps (default: 50; decode workloads: 128 generated tokens)")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="q6k_head",
-                    choices=["q6k_head", "q8_0_head", "q4k_matvec", "decode_3b", "decode_moe", "prefill_3b"])
+                    choices=["q6k_head", "q8_0_head", "q4k_matvec", "decode_3b", "decode_moe", "prefill_3b",
+                             "grid_barrier"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--n-batch", type=int, default=512, help="GPU prefill chunk (decode workloads)")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (smoke runs only)")
@@ -572,18 +695,29 @@ def main():
         line = bench_matvec(args, Q6_K, 151936, 2048, 8, stacked=False)
         if not args.no_decode:
             # the metric's second half: decode tok/s of the Qwen2.5-3B shape (and the MoE shape), each
-            # 128 tokens after its context, with the reference engine on the host beside it
+            # 128 tokens after its context, with the reference engine on the host beside it; and the
+            # 3B model's 512-token prefill on the GEMM (configuration 4)
             from sardyne_amd.gguf_synth import qwen25_3b, qwen3_30b_a3b
-            for key, spec, label, ctx_len, desc in (
-                    ("decode_3b", qwen25_3b(), "qwen25_3b", 512, "Qwen2.5-3B-shaped Q4_K_M"),
-                    ("decode_moe", qwen3_30b_a3b(), "qwen3_30b_a3b", 1024,
-                     "Qwen3-30B-A3B-shaped qwen3moe Q4_K_M (128 experts resident, top-8)")):
-                d = decode_line(args, spec, label, ctx_len, desc, n_dec=128)
-                line[key] = {k: d[k] for k in ("value", "unit", "ms_per_step", "roofline", "cpu_baseline", "parity")
-                             if k in d}
-                line[key]["workload"] = d["config"]["workload"]
-                if "gpu_over_cpu" in d:
-                    line[key]["gpu_over_cpu"] = d["gpu_over_cpu"]
+            sub = ("value", "unit", "ms_per_step", "roofline", "cpu_baseline", "parity", "model_load",
+                   "mfma_utilisation", "gpu_over_cpu")
+            p3b = write_bench_model(qwen25_3b(), "qwen25_3b")
+            try:
+                d = decode_line(args, qwen25_3b(), "qwen25_3b", 512, "Qwen2.5-3B-shaped Q4_K_M", n_dec=128,
+                                path=p3b)
+                line["decode_3b"] = {k: d[k] for k in sub if k in d}
+                line["decode_3b"]["workload"] = d["config"]["workload"]
+                pargs = argparse.Namespace(**{**vars(args), "steps": 20, "warmup": 2})
+                d = prefill_line(pargs, qwen25_3b(), "qwen25_3b", 512, "Qwen2.5-3B-shaped Q4_K_M", path=p3b)
+                line["prefill_3b"] = {k: d[k] for k in sub if k in d}
+                line["prefill_3b"]["workload"] = d["config"]["workload"]
+            finally:
+                drop_bench_model(p3b)
+            d = decode_line(args, qwen3_30b_a3b(), "qwen3_30b_a3b", 1024,
+                            "Qwen3-30B-A3B-shaped qwen3moe Q4_K_M (128 experts resident, top-8)", n_dec=128)
+            line["decode_moe"] = {k: d[k] for k in sub if k in d}
+            line["decode_moe"]["workload"] = d["config"]["workload"]
+    elif args.workload == "grid_barrier":
+        line = barrier_line(args)
     elif args.workload == "q8_0_head":
         line = bench_matvec(args, Q8_0, 151936, 2048, 8, stacked=False)
     elif args.workload == "q4k_matvec":

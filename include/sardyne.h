@@ -163,6 +163,28 @@ int sdy_model_memory(const engine_model *m, size_t *weight_bytes, size_t *gemm_c
  * reference. */
 int sdy_mem_info(size_t *free_bytes, size_t *total_bytes);
 
+/* ------------------------------------------------------------------ measurement
+ * No counterpart in the reference: what a persistent decode kernel would pay per phase, against the
+ * kernel boundary it would replace (the benchmark's grid_barrier workload).
+ *
+ * sdy_grid_barrier_probe: a co-resident grid of n_wg workgroups (cooperative launch) runs `rounds`
+ * grid barriers of the given form, each publishing 64 floats per workgroup that another workgroup
+ * reads back and checks; with stream_mb > 0 the other waves stream that many MiB (four passes) from
+ * HBM meanwhile. Every wait is bounded: a timeout ends the grid and is counted. Times come from the
+ * GPU's wall clock per round of workgroup 0. */
+enum { SDY_BARRIER_FLAT = 0, SDY_BARRIER_TWO_LEVEL = 1, SDY_BARRIER_FENCED = 2 };
+typedef struct {
+    float us_median, us_mean;   /* per barrier round, over all rounds done */
+    float us_mean_streaming;    /* mean over the rounds that ended while the stream still ran */
+    float kernel_ms;            /* the whole launch (HIP events) */
+    int rounds_done, rounds_streaming;
+    unsigned timeouts, mismatches;  /* bounded waits that gave up; data values read back wrong */
+} sdy_barrier_stats;
+int sdy_grid_barrier_probe(int n_wg, int rounds, int mode, int stream_mb, sdy_barrier_stats *out);
+/* n empty kernels back to back on one stream, recorded as a graph and replayed, and issued eagerly:
+ * the mean microseconds per kernel of each. */
+int sdy_kernel_boundary_us(int n, float *us_graph, float *us_eager);
+
 /* ------------------------------------------------------------------ device-level, no allocation
  * No counterpart in the reference. For callers that cannot allocate device memory: code recorded
  * under graph capture, tight serving loops, harnesses that forbid hipMalloc. The one-token decode

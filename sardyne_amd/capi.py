@@ -107,6 +107,13 @@ class SdyMat(ctypes.Structure):
                 ("grow0", ctypes.c_long), ("grows", ctypes.c_long)]
 
 
+class SdyBarrierStats(ctypes.Structure):
+    """sdy_barrier_stats (include/sardyne.h)."""
+    _fields_ = [("us_median", ctypes.c_float), ("us_mean", ctypes.c_float), ("us_mean_streaming", ctypes.c_float),
+                ("kernel_ms", ctypes.c_float), ("rounds_done", _int), ("rounds_streaming", _int),
+                ("timeouts", ctypes.c_uint), ("mismatches", ctypes.c_uint)]
+
+
 class SdyMvArgs(ctypes.Structure):
     _fields_ = [("xq", _vp), ("x", _vp), ("n_tok", _int), ("out", _vp), ("out_stride", ctypes.c_long),
                 ("bias", _vp), ("resid", _vp), ("row0", ctypes.c_long), ("row1", ctypes.c_long),
@@ -118,6 +125,8 @@ _DEVICE_SIGNATURES = {
     "sdy_last_kernel": (ctypes.c_char_p, []),
     "sdy_init": (_int, []),
     "sdy_device_info": (_int, [ctypes.POINTER(_int), ctypes.POINTER(_sz)]),
+    "sdy_grid_barrier_probe": (_int, [_int, _int, _int, _int, ctypes.POINTER(SdyBarrierStats)]),
+    "sdy_kernel_boundary_us": (_int, [_int, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]),
     "sdy_mem_info": (_int, [ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "sdy_model_memory": (_int, [_vp, ctypes.POINTER(_sz), ctypes.POINTER(_sz), ctypes.POINTER(_int),
                                 ctypes.POINTER(_int)]),

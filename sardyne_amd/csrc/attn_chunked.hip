@@ -5,8 +5,8 @@
 // s_j = q.k_j / sqrt(head_dim) over every cached position j, one softmax over all of them and the
 // weighted sum of the V rows. Here the positions are cut into spans of `span` (a multiple of 64):
 //
-//   k_attn_chunk<HD, HW, KT>  grid (n_span_max, n_kv_head * hsplit), 256 threads, one workgroup per
-//                          (span, kv head, share of the group's query heads):
+//   k_attn_chunk<HD, HW, KT>  256 threads, one workgroup per (span, kv head, share of the group's
+//                          query heads; the shares of one span and head on one XCD):
 //     - q/k RMSNorm (qwen3) and RoPE of the group's queries, and of the new k when the span holds
 //       the token's own position (that workgroup writes the new K/V row to the cache);
 //     - the span's positions in sub-chunks of 64: K and V rows staged in LDS (the next sub-chunk's
@@ -103,9 +103,17 @@ __global__ __launch_bounds__(256) void k_attn_chunk(ChunkArgs a) {
     float *es = vn + HD;               // [MAX_REP][SUB] exp(s - m) of the sub-chunk
     float *cs_l = es + MAX_REP * SUB;  // [MAX_REP] rescale of a head's old sums at this sub-chunk
 
-    const int sp = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n_rep = a.n_head / a.n_kv_head, g = blockIdx.y / a.hsplit, hs = blockIdx.y - g * a.hsplit;
+    // workgroup -> (span, kv group, share of its heads). With two shares, the two workgroups of one
+    // (span, group) are 8 apart in the launch order: workgroups are dealt to the 8 XCDs in turn, so
+    // they run on one XCD and the span's K/V rows are fetched from HBM into its L2 once (apart, on
+    // two XCDs, every row came from HBM twice: 2.2x the K/V bytes, PMC)
+    const int wg = blockIdx.x;
+    const int j = a.hsplit == 2 ? ((wg >> 4) << 3) | (wg & 7) : wg, hs = a.hsplit == 2 ? (wg >> 3) & 1 : 0;
+    if (j >= a.n_span_max * a.n_kv_head) return;  // (padding of the launch to whole groups of 16)
+    const int g = j / a.n_span_max, sp = j - g * a.n_span_max;
+    const int n_rep = a.n_head / a.n_kv_head;
     const int nh = n_rep / a.hsplit;   // the workgroup's query heads: h0 .. h0 + nh - 1
     const int h0 = g * n_rep + hs * nh;
     const int pos = a.step[1], n_kv = pos + 1;
@@ -404,8 +412,9 @@ int launch_chunked(const ChunkArgs &A, hipStream_t st) {
     int rc = sdy_lds_limit((const void *)k_attn_chunk<HD, HW, KT>, lds, &granted);
     if (rc) return rc;
     SDY_NOTE_KERNEL((k_attn_chunk<HD, HW, KT>));
-    hipLaunchKernelGGL((k_attn_chunk<HD, HW, KT>), dim3(A.n_span_max, A.n_kv_head * A.hsplit), dim3(256), lds, st,
-                       A);
+    const int pairs = A.n_span_max * A.n_kv_head;
+    const int n_wg = A.hsplit == 2 ? (pairs + 7) / 8 * 16 : pairs;
+    hipLaunchKernelGGL((k_attn_chunk<HD, HW, KT>), dim3(n_wg), dim3(256), lds, st, A);
     if ((rc = sdy_check_launch("attn_chunk"))) return rc;
     hipLaunchKernelGGL((k_attn_merge<HD>), dim3((A.n_head * HD + 255) / 256), dim3(256), 0, st, A);
     return sdy_check_launch("attn_merge");
