@@ -130,6 +130,10 @@ enum { OP_F32 = 0, OP_F16 = 1, OP_Q4_0 = 2, OP_Q5_0 = 6, OP_Q8_0 = 8, OP_Q4_K = 
  * their Q4_K/Q6_K results equal both of the reference's kernel sets, which agree bit for bit. */
 int op_simd(void);
 int op_set_simd(int enable);
+/* No counterpart in the reference (its op_* cannot fail): the message of this thread's last op_*
+ * call that failed on the GPU or rejected its arguments, "" after one that succeeded. A failed call
+ * frees what it allocated and fills its float outputs with NaN; the process goes on. */
+const char *op_last_error(void);
 void op_f16_to_f32_n(const uint16_t *x, float *out, size_t n);                     /* csrc/ops.h:36 */
 void op_matmul_rows(float *out, const float *x, const void *w, int wtype, int n_tok, int n_in, int n_out,
                     int row0, int row1);                                          /* csrc/ops.h:42-43 */

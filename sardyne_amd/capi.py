@@ -122,6 +122,7 @@ class SdyMvArgs(ctypes.Structure):
 
 _DEVICE_SIGNATURES = {
     "sdy_last_error": (ctypes.c_char_p, []),
+    "op_last_error": (ctypes.c_char_p, []),
     "sdy_last_kernel": (ctypes.c_char_p, []),
     "sdy_init": (_int, []),
     "sdy_device_info": (_int, [ctypes.POINTER(_int), ctypes.POINTER(_sz)]),

@@ -76,6 +76,38 @@ def test_engine_fails_loudly_without_gpu(tmp_path):
         LoadedModel(p)
 
 
+@needs_lib
+def test_op_rejects_bad_arguments_without_aborting():
+    """A host-pointer op_* that cannot run (here a weight type the kernels do not take, checked before
+    any GPU work) returns instead of ending the process: its outputs are NaN and op_last_error names
+    the call; the next call clears the message."""
+    L = capi.lib()
+    out = np.zeros(4, np.float32)
+    w = np.zeros(64, np.uint8)
+    x = np.zeros(256, np.float32)
+    L.op_matmul_rows(out.ctypes.data, x.ctypes.data, w.ctypes.data, 12, 1, 256, 4, 0, 4)  # Q4_K: not a float type
+    assert np.all(np.isnan(out))
+    assert b"op_matmul_rows" in L.op_last_error() and b"float type" in L.op_last_error()
+    out = np.zeros(256, np.float32)
+    L.op_row_to_f32(w.ctypes.data, 99, out.ctypes.data, 256)  # no such type
+    assert np.all(np.isnan(out)) and b"op_row_to_f32" in L.op_last_error()
+
+
+@needs_lib
+@pytest.mark.skipif(gpu_present(), reason="checks the no-GPU error path")
+def test_op_without_gpu_reports_instead_of_aborting():
+    """Without a GPU the host-pointer op_* report the failure (NaN outputs, op_last_error) and the
+    process goes on, where they used to abort."""
+    L = capi.lib()
+    x = np.ones(64, np.float32)
+    out = np.zeros(64, np.float32)
+    L.op_rmsnorm(out.ctypes.data, x.ctypes.data, x.ctypes.data, 64, ctypes.c_float(1e-6))
+    assert np.all(np.isnan(out))
+    assert b"op_rmsnorm" in L.op_last_error() and b"GPU" in L.op_last_error()
+    r = L.op_dot_f32(x.ctypes.data, x.ctypes.data, 64)
+    assert np.isnan(r)
+
+
 # ---------------------------------------------------------------- GGUF reader (host code)
 
 class CGGUF:
