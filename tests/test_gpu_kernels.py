@@ -1606,3 +1606,20 @@ def test_moe_sort_and_grouped_gemm_equal_per_expert_gemm(kind, n_in, rows, n_exp
     g, u = srt[:, 0::2].copy(), srt[:, 1::2].copy()
     lib().op_silu_mul(ptr(g), ptr(u), g.size)
     assert np.array_equal(bits(got), bits(g))
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2], ids=["flat", "two_level", "two_level_fenced"])
+def test_grid_barrier_probe_publishes_every_value(mode):
+    """The persistent-kernel barrier measurement (sdy_grid_barrier_probe): over 300 rounds of a
+    256-workgroup co-resident grid, every workgroup reads back another's data of that round, with and
+    without the other waves streaming HBM meanwhile; no value is stale and no bounded wait gives up."""
+    L = capi.lib()
+    capi.check(L.sdy_init())
+    for stream_mb in (0, 256):
+        st = capi.SdyBarrierStats()
+        capi.check(L.sdy_grid_barrier_probe(256, 300, mode, stream_mb, ctypes.byref(st)))
+        assert st.timeouts == 0 and st.mismatches == 0, (stream_mb, st.timeouts, st.mismatches)
+        assert st.rounds_done == 300 and 0 < st.us_median < 100
+    ug, ue = ctypes.c_float(), ctypes.c_float()
+    capi.check(L.sdy_kernel_boundary_us(200, ctypes.byref(ug), ctypes.byref(ue)))
+    assert 0 < ug.value < 50 and 0 < ue.value < 50
