@@ -492,6 +492,10 @@ def bench_decode(args, spec, ctx_len, n_decode, label, path=None):
     return gpu_tok_s, t_prefill, cpu, parity, load
 
 
+# the decode profiles under profiles/ (their per-token PMC traffic), by workload label
+DECODE_PROFILE = {"qwen25_3b": "decode_qwen25_3b.md", "qwen3_30b_a3b": "decode_qwen3_30b_a3b_moe.md"}
+
+
 def decode_line(args, spec, label, ctx_len, desc, n_dec=None, path=None):
     n_dec = n_dec or max(args.steps, 8)
     tok_s, t_pre, cpu, parity, load = bench_decode(args, spec, ctx_len, n_dec, label, path)
@@ -512,7 +516,7 @@ def decode_line(args, spec, label, ctx_len, desc, n_dec=None, path=None):
             "data": "synthetic (random-init Q4_K_M weights, uniform token ids)", "config": cfg,
             f"prefill_{ctx_len}_s": round(t_pre, 4),
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(f"decode_{label}.md"),
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(DECODE_PROFILE.get(label, f"decode_{label}.md")),
                          "traffic_unit": "HBM bytes per decode token (PMC, profiles/)",
                          "kernel": "whole decode step (weights + mean KV bytes per token)"},
             "cpu_baseline": cpu, "parity": parity, "model_load": load}
