@@ -272,10 +272,26 @@ def bench_matvec(args, wt, n_out, n_in, n_copies, stacked):
         n_launch = n_copies * max(1, args.steps // 10)
         ms_b = per_launch_ms(st, one_copy, n_launch)
         per = w_bytes + n_in * 4 + n_out * 4
+        # the same launches recorded once as a graph and replayed (no host work between them: what a
+        # caller that replays its step, as the engine does, pays per launch)
+        ms_g = None
+        ex = ctypes.c_void_p()
+        if L.sdy_graph_begin(st) == 0:
+            for i in range(n_copies):
+                one_copy(i)
+            if L.sdy_graph_end(st, ctypes.byref(ex)) == 0:
+                capi.check(L.sdy_graph_launch(ex, st))
+                reps = max(1, args.steps // 10)
+                ms_g = per_launch_ms(st, lambda _: capi.check(L.sdy_graph_launch(ex, st)), reps) / n_copies
+                capi.check(L.sdy_graph_free(ex))
         back_to_back = {"launches": n_launch, "distinct_copies": n_copies, "per_launch_us": round(ms_b * 1e3, 3),
                         "GBps": round(per / (ms_b * 1e-3) / 1e9, 1),
                         "frac_of_hbm_peak": round(per / (ms_b * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
                         "kernel": L.sdy_last_kernel().decode()}
+        if ms_g:
+            back_to_back["graph_replay"] = {"per_launch_us": round(ms_g * 1e3, 3),
+                                            "GBps": round(per / (ms_g * 1e-3) / 1e9, 1),
+                                            "frac_of_hbm_peak": round(per / (ms_g * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
 
     # CPU baseline: the reference's code on this host (all online CPUs, and 1 thread)
     cpu = None

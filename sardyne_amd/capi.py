@@ -144,6 +144,10 @@ _DEVICE_SIGNATURES = {
     "sdy_event_record": (_int, [_vp, _vp]),
     "sdy_event_elapsed": (_int, [ctypes.POINTER(ctypes.c_float), _vp, _vp]),
     "sdy_event_free": (_int, [_vp]),
+    "sdy_graph_begin": (_int, [_vp]),
+    "sdy_graph_end": (_int, [_vp, ctypes.POINTER(_vp)]),
+    "sdy_graph_launch": (_int, [_vp, _vp]),
+    "sdy_graph_free": (_int, [_vp]),
     "sdy_membw_read": (_int, [_vp, _sz, _vp, _vp]),
     "sdy_mat_bytes": (_sz, [_int, _int, ctypes.c_long]),
     "sdy_mat_upload": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long, _vp, _vp]),
