@@ -500,6 +500,7 @@ def bench_decode(args, spec, ctx_len, n_decode, label, path=None):
     load = {"s": round(t_load, 3), "file_bytes": size, "gb_per_s": round(size / t_load / 1e9, 2),
             "device_weight_bytes": mem["weight_bytes"], "gemm_copy_bytes": mem["gemm_copy_bytes"],
             "gemm_copies": mem["gemm_copies"], "gemm_copies_skipped": mem["gemm_copies_skipped"],
+            "host_expert_bytes": mem["host_expert_bytes"], "host_expert_layers": mem["host_expert_layers"],
             "upload": "synchronous per tensor" if os.environ.get("SARDYNE_UPLOAD_SYNC", "0") not in ("", "0")
             else "pipelined (4 x 64 MiB pinned slots)",
             "file": "tmpfs" if str(path).startswith("/dev/shm") else "disk"}

@@ -163,6 +163,12 @@ void op_attention(float *out, const float *q, const float *k_cache, const float 
  * a NULL model. */
 int sdy_model_memory(const engine_model *m, size_t *weight_bytes, size_t *gemm_copy_bytes, int *n_copies,
                      int *n_skipped);
+/* The expert stacks a loaded model keeps in pinned host memory, read in place by the kernels over
+ * the host link (the layers whose experts did not fit the device, or those SARDYNE_HOST_EXPERTS
+ * names): their bytes and the number of layers. Stands where the reference reads its weights from
+ * the file mapping and prefetches the chosen experts (csrc/model_llama.c:703-721). Returns 0, or
+ * -1 for a NULL model. */
+int sdy_model_host_weights(const engine_model *m, size_t *host_bytes, int *host_layers);
 /* Free and total device memory now (hipMemGetInfo); 0 or a negative code. No counterpart in the
  * reference. */
 int sdy_mem_info(size_t *free_bytes, size_t *total_bytes);

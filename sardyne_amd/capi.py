@@ -104,7 +104,7 @@ class SdyMat(ctypes.Structure):
     """Device-layout matrix descriptor (sdy_mat in sardyne_amd/csrc/sdy_shim.h)."""
     _fields_ = [("base", _vp), ("bytes", _sz), ("type", _int), ("n_in", _int), ("n_rows", ctypes.c_long),
                 ("n_units", _int), ("plane_off", _sz * 5), ("gemm_ok", _int), ("gbase", _vp), ("gbytes", _sz),
-                ("grow0", ctypes.c_long), ("grows", ctypes.c_long)]
+                ("grow0", ctypes.c_long), ("grows", ctypes.c_long), ("hbase", _vp)]
 
 
 class SdyBarrierStats(ctypes.Structure):
@@ -131,6 +131,7 @@ _DEVICE_SIGNATURES = {
     "sdy_mem_info": (_int, [ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "sdy_model_memory": (_int, [_vp, ctypes.POINTER(_sz), ctypes.POINTER(_sz), ctypes.POINTER(_int),
                                 ctypes.POINTER(_int)]),
+    "sdy_model_host_weights": (_int, [_vp, ctypes.POINTER(_sz), ctypes.POINTER(_int)]),
     "sdy_malloc": (_int, [ctypes.POINTER(_vp), _sz]),
     "sdy_free": (_int, [_vp]),
     "sdy_h2d": (_int, [_vp, _vp, _sz, _vp]),
@@ -173,6 +174,8 @@ _DEVICE_SIGNATURES = {
     "sdy_matvec_grouped": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp, _int, ctypes.c_long,
                                   ctypes.c_long, ctypes.c_long, _vp]),
     "sdy_mat_alloc": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long]),
+    "sdy_mat_alloc_host": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long]),
+    "sdy_host_alloc_mapped": (_int, [ctypes.POINTER(_vp), ctypes.POINTER(_vp), _sz]),
     "sdy_uploader_new": (_int, [ctypes.POINTER(_vp), _sz, _int, _int, _vp]),
     "sdy_uploader_rows": (_int, [_vp, ctypes.POINTER(SdyMat), ctypes.c_long, ctypes.c_long, ctypes.c_long,
                                  ctypes.c_long, ctypes.c_long, _vp]),

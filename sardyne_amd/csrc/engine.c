@@ -14,7 +14,9 @@
  *   - upload: every matrix goes from the mmap to the device layout through the shim's uploader;
  *     q|k(|v) of one type become one stacked matrix, gate and up of one quantized type one
  *     interleaved matrix, and a layer's q|k|v biases one contiguous span (what the stacked
- *     matvecs read);
+ *     matvecs read). Expert stacks are uploaded last, each layer's into device memory while it
+ *     leaves room for the contexts and otherwise into pinned host memory, which the same kernels
+ *     read in place (so a model larger than the device still loads);
  *   - contexts: argument limits checked from a table; the device state is allocated by forward.c.
  */
 #define _POSIX_C_SOURCE 200809L
@@ -332,11 +334,16 @@ static int validate_tensors(const engine_model *m, const gguf_tensor *lt[][N_LAY
 enum { T_ATTN_NORM, T_Q, T_QB, T_K, T_KB, T_V, T_VB, T_QN, T_KN, T_O, T_FFN_NORM, T_GATE, T_UP, T_DOWN, T_ROUTER,
        T_GATE_X, T_UP_X, T_DOWN_X };
 
+enum { HOST_AUTO, HOST_NONE, HOST_ALL, HOST_LAST };
+
 typedef struct {
     engine_model *m;
     char *err;
     size_t len;
     sdy_uploader *up; /* pipelined uploads (NULL: one synchronous upload per tensor) */
+    int host_mode;    /* where expert stacks go (HOST_*; HOST_LAST: the last host_last layers' in host memory) */
+    int host_last;
+    size_t reserve;   /* device memory the load leaves free for the contexts (HOST_AUTO) */
 } loader;
 
 /* Rows of a tensor from the file mapping into an allocated matrix (the map of sdy_mat_upload_map). */
@@ -364,15 +371,28 @@ static dmat row_view(const dmat *w, long r0, int n_out) {
     return d;
 }
 
-/* One matrix (or expert stack) as it is in the file. */
-static int upload_matrix(loader *ld, const gguf_tensor *t, dmat *out) {
-    const long rows = (long)(t->nbytes / sdy_raw_row_bytes((int)t->type, (int)t->ne[0]));
-    if (sdy_mat_alloc(&out->m, (int)t->type, (int)t->ne[0], rows)) return device_fail(ld, t->name);
-    if (load_rows(ld, &out->m, 0, rows, 1, rows, 0, t->data)) return device_fail(ld, t->name);
-    describe(out, (int)t->type, (int)t->ne[0], (int)t->ne[1]);
-    ld->m->device_bytes += out->m.bytes;
+/* A matrix allocated in device memory, or (host) in pinned host memory, and counted. */
+static int alloc_matrix(loader *ld, sdy_mat *m, int type, int n_in, long rows, int host) {
+    if (host ? sdy_mat_alloc_host(m, type, n_in, rows) : sdy_mat_alloc(m, type, n_in, rows)) return -1;
+    if (host) ld->m->host_bytes += m->bytes;
+    else ld->m->device_bytes += m->bytes;
     return 0;
 }
+
+static long file_rows(const gguf_tensor *t) {
+    return (long)(t->nbytes / sdy_raw_row_bytes((int)t->type, (int)t->ne[0]));
+}
+
+/* One matrix (or expert stack) as it is in the file; host: in pinned host memory. */
+static int upload_matrix_in(loader *ld, const gguf_tensor *t, dmat *out, int host) {
+    const long rows = file_rows(t);
+    if (alloc_matrix(ld, &out->m, (int)t->type, (int)t->ne[0], rows, host)) return device_fail(ld, t->name);
+    if (load_rows(ld, &out->m, 0, rows, 1, rows, 0, t->data)) return device_fail(ld, t->name);
+    describe(out, (int)t->type, (int)t->ne[0], (int)t->ne[1]);
+    return 0;
+}
+
+static int upload_matrix(loader *ld, const gguf_tensor *t, dmat *out) { return upload_matrix_in(ld, t, out, 0); }
 
 /* q, k and v. With q and k of one type they are one matrix (and v too when it shares the type),
  * whose row ranges are the three: one launch computes them all. */
@@ -385,10 +405,9 @@ static int upload_qkv(loader *ld, const gguf_tensor *const *lt, dlayer *L) {
     }
     const int parts = tv->type == tq->type ? 3 : 2;
     const long rows = (long)qd + kvd + (parts == 3 ? kvd : 0);
-    if (sdy_mat_alloc(&L->wqkv.m, (int)tq->type, n_in, rows)) return device_fail(ld, tq->name);
+    if (alloc_matrix(ld, &L->wqkv.m, (int)tq->type, n_in, rows, 0)) return device_fail(ld, tq->name);
     describe(&L->wqkv, (int)tq->type, n_in, (int)rows);
     L->qkv_parts = parts;
-    ld->m->device_bytes += L->wqkv.m.bytes;
     const gguf_tensor *src[3] = {tq, tk, tv};
     long r0 = 0;
     for (int p = 0; p < parts; p++) {
@@ -402,18 +421,18 @@ static int upload_qkv(loader *ld, const gguf_tensor *const *lt, dlayer *L) {
 }
 
 /* gate and up ([n_expert][ffn][dim]). With one quantized type they become one matrix with rows
- * interleaved (2i = gate i, 2i+1 = up i, per expert) for the SwiGLU matvec epilogue. */
-static int upload_gate_up(loader *ld, const gguf_tensor *tg, const gguf_tensor *tu, dlayer *L) {
+ * interleaved (2i = gate i, 2i+1 = up i, per expert) for the SwiGLU matvec epilogue. host: in
+ * pinned host memory. */
+static int upload_gate_up(loader *ld, const gguf_tensor *tg, const gguf_tensor *tu, dlayer *L, int host) {
     if (tg->type != tu->type || !is_quant(tg->type)) {
         L->gu_fused = 0;
-        return upload_matrix(ld, tg, &L->gate) || upload_matrix(ld, tu, &L->up) ? -1 : 0;
+        return upload_matrix_in(ld, tg, &L->gate, host) || upload_matrix_in(ld, tu, &L->up, host) ? -1 : 0;
     }
     const int n_in = (int)tg->ne[0], ffn = (int)tg->ne[1];
     const long experts = tg->n_dims == 3 ? (long)tg->ne[2] : 1, rows = experts * ffn;
-    if (sdy_mat_alloc(&L->gate_up.m, (int)tg->type, n_in, 2 * rows)) return device_fail(ld, tg->name);
+    if (alloc_matrix(ld, &L->gate_up.m, (int)tg->type, n_in, 2 * rows, host)) return device_fail(ld, tg->name);
     describe(&L->gate_up, (int)tg->type, n_in, 2 * ffn);
     L->gu_fused = 1;
-    ld->m->device_bytes += L->gate_up.m.bytes;
     if (load_rows(ld, &L->gate_up.m, 0, rows, 2, ffn, 2L * ffn, tg->data)) return device_fail(ld, tg->name);
     if (load_rows(ld, &L->gate_up.m, 1, rows, 2, ffn, 2L * ffn, tu->data)) return device_fail(ld, tu->name);
     return 0;
@@ -462,14 +481,37 @@ static int upload_layer(loader *ld, const gguf_tensor *const *lt, dlayer *L) {
         if (upload_vector(ld, lt[T_QN], L->q_norm) || upload_vector(ld, lt[T_KN], L->k_norm)) return -1;
     }
     if (upload_qkv(ld, lt, L) || upload_matrix(ld, lt[T_O], &L->wo)) return -1;
-    if (in->n_expert) {
-        if (upload_matrix(ld, lt[T_ROUTER], &L->gate_inp) || upload_gate_up(ld, lt[T_GATE_X], lt[T_UP_X], L) ||
-            upload_matrix(ld, lt[T_DOWN_X], &L->down))
-            return -1;
-        L->down.n_out = in->dim; /* an expert's rows; the stack holds n_expert of them */
-        return 0;
+    if (in->n_expert) return upload_matrix(ld, lt[T_ROUTER], &L->gate_inp); /* the experts: upload_experts */
+    return upload_gate_up(ld, lt[T_GATE], lt[T_UP], L, 0) || upload_matrix(ld, lt[T_DOWN], &L->down) ? -1 : 0;
+}
+
+/* Whether layer l's expert stacks (need bytes) go to pinned host memory: SARDYNE_HOST_EXPERTS=auto
+ * (the default) while the device would keep less than the reserve free after them, all, none, or
+ * a count n of the last layers. */
+static int experts_on_host(loader *ld, int l, size_t need) {
+    switch (ld->host_mode) {
+    case HOST_NONE: return 0;
+    case HOST_ALL: return 1;
+    case HOST_LAST: return l >= ld->m->info.n_layer - ld->host_last;
+    default: {
+        size_t free_b = 0;
+        if (sdy_mem_info(&free_b, NULL)) return 0; /* (the allocation then reports the device's state) */
+        return free_b < need + ld->reserve;
     }
-    return upload_gate_up(ld, lt[T_GATE], lt[T_UP], L) || upload_matrix(ld, lt[T_DOWN], &L->down) ? -1 : 0;
+    }
+}
+
+/* A MoE layer's expert stacks (gate|up and down), in device memory or in pinned host memory. */
+static int upload_experts(loader *ld, const gguf_tensor *const *lt, dlayer *L, int l) {
+    const gguf_tensor *tg = lt[T_GATE_X], *tu = lt[T_UP_X], *td = lt[T_DOWN_X];
+    const size_t need = sdy_mat_bytes((int)tg->type, (int)tg->ne[0], file_rows(tg)) +
+                        sdy_mat_bytes((int)tu->type, (int)tu->ne[0], file_rows(tu)) +
+                        sdy_mat_bytes((int)td->type, (int)td->ne[0], file_rows(td));
+    const int host = experts_on_host(ld, l, need);
+    if (upload_gate_up(ld, tg, tu, L, host) || upload_matrix_in(ld, td, &L->down, host)) return -1;
+    L->down.n_out = ld->m->info.dim; /* an expert's rows; the stack holds n_expert of them */
+    ld->m->host_layers += host;
+    return 0;
 }
 
 void engine_model_free(engine_model *m) {
@@ -496,20 +538,49 @@ void engine_model_get_info(const engine_model *m, engine_model_info *out) {
     if (m && out) *out = m->info;
 }
 
+/* Device memory a load leaves free for the contexts (KV caches, work buffers): SARDYNE_RESERVE_MB,
+ * by default an eighth of the device and at least 2 GiB. */
+static size_t context_reserve(size_t total) {
+    const char *r = getenv("SARDYNE_RESERVE_MB");
+    if (r && r[0]) return (size_t)(strtod(r, NULL) * 1048576.0);
+    return total / 8 > ((size_t)2 << 30) ? total / 8 : ((size_t)2 << 30);
+}
+
+/* The expert placement switch (SARDYNE_HOST_EXPERTS: auto, none, all, or a count of last layers)
+ * and the reserve. */
+static int placement(loader *ld) {
+    size_t total = 0;
+    if (sdy_mem_info(NULL, &total)) return device_fail(ld, "GPU");
+    ld->reserve = context_reserve(total);
+    const char *h = getenv("SARDYNE_HOST_EXPERTS");
+    char *end = NULL;
+    if (!h || !h[0] || !strcmp(h, "auto")) ld->host_mode = HOST_AUTO;
+    else if (!strcmp(h, "none")) ld->host_mode = HOST_NONE;
+    else if (!strcmp(h, "all")) ld->host_mode = HOST_ALL;
+    else {
+        const long n = strtol(h, &end, 10);
+        if (*end || n < 0) return say(ld->err, ld->len, "SARDYNE_HOST_EXPERTS=%s not supported (auto, none, all, or a "
+                                                        "count of layers)", h);
+        ld->host_mode = HOST_LAST;
+        ld->host_last = (int)n;
+    }
+    return 0;
+}
+
 /* The prefill GEMM's tiled copies of the layer matrices (Q4_K / Q6_K, sdy_mat_gemm_layout): a second
  * copy of those weights, from which the GEMM's loads read whole cache lines. They only make prompts
  * faster (without one the GEMM reads the planes, with the same results), so they are made where the
  * device has room: the attention and dense FFN matrices of every layer first, then the expert stacks
- * (the bulk of a MoE file), each only if it leaves the reserve free for the contexts (KV caches, work
- * buffers): SARDYNE_GEMM_RESERVE_MB, by default an eighth of the device memory and at least 2 GiB. An
- * allocation that fails all the same skips that copy. SARDYNE_GEMM_COPY_MB caps the copies' total
- * (MiB, fractions allowed; 0: no copies). */
+ * (the bulk of a MoE file) in device memory, each only if it leaves the reserve free for the
+ * contexts (SARDYNE_GEMM_RESERVE_MB, else the load's reserve). An allocation that fails all the same
+ * skips that copy. SARDYNE_GEMM_COPY_MB caps the copies' total (MiB, fractions allowed; 0: no
+ * copies). Expert stacks in host memory have none. */
 static int gemm_copies(loader *ld) {
     engine_model *m = ld->m;
     const engine_model_info *in = &m->info;
-    size_t free_b = 0, total = 0;
-    if (sdy_mem_info(&free_b, &total)) return device_fail(ld, "gemm layout");
-    size_t reserve = total / 8 > ((size_t)2 << 30) ? total / 8 : ((size_t)2 << 30);
+    size_t free_b = 0;
+    if (sdy_mem_info(&free_b, NULL)) return device_fail(ld, "gemm layout");
+    size_t reserve = ld->reserve;
     const char *r = getenv("SARDYNE_GEMM_RESERVE_MB");
     if (r && r[0]) reserve = (size_t)(strtod(r, NULL) * 1048576.0);
     size_t cap = (size_t)-1;
@@ -522,7 +593,7 @@ static int gemm_copies(loader *ld) {
                            L->qkv_parts < 3 ? &L->wv : NULL, L->qkv_parts >= 2 ? &L->wqkv : NULL, &L->wo,
                            &L->gate, &L->up, &L->gate_up, &L->down};
             for (size_t i = 0; i < sizeof own / sizeof *own; i++) {
-                if (!own[i] || !own[i]->m.base) continue;
+                if (!own[i] || !own[i]->m.base || own[i]->m.hbase) continue;
                 if ((in->n_expert && i >= 5) != experts) continue; /* (i >= 5: the FFN matrices) */
                 const size_t need = sdy_mat_gemm_layout_bytes(&own[i]->m);
                 if (!need) continue;
@@ -551,9 +622,10 @@ static int load(engine_model *m, const char *path, char *err, size_t len) {
         free(lt);
         return say(err, len, "memoria esaurita");
     }
-    loader ld = {m, err, len, NULL};
+    loader ld = {m, err, len, NULL, HOST_AUTO, 0, 0};
     int rc = validate_tensors(m, lt, err, len);
     if (!rc && (sdy_init() || sdy_stream_new(&m->st))) rc = device_fail(&ld, "GPU");
+    if (!rc) rc = placement(&ld);
     /* weights go through a ring of four 64 MiB pinned/device slot pairs, the host copies split over
        half the online CPUs; SARDYNE_UPLOAD_SYNC=1: one synchronous upload per tensor instead */
     const char *sync_up = getenv("SARDYNE_UPLOAD_SYNC");
@@ -578,6 +650,7 @@ static int load(engine_model *m, const char *path, char *err, size_t len) {
         else if (!rc) rc = upload_matrix(&ld, tensor(m->gf, "output.weight"), &m->output);
     }
     for (int l = 0; !rc && l < in->n_layer; l++) rc = upload_layer(&ld, lt[l], &m->layers[l]);
+    for (int l = 0; !rc && in->n_expert && l < in->n_layer; l++) rc = upload_experts(&ld, lt[l], &m->layers[l], l);
     if (!rc && ld.up && sdy_uploader_finish(ld.up)) rc = device_fail(&ld, "upload");
     if (!rc && sdy_sync(m->st)) rc = device_fail(&ld, "upload");
     if (sdy_uploader_free(ld.up) && !rc) rc = device_fail(&ld, "upload");
@@ -597,6 +670,13 @@ static int load(engine_model *m, const char *path, char *err, size_t len) {
     }
     free(lt);
     return rc;
+}
+
+int sdy_model_host_weights(const engine_model *m, size_t *host_bytes, int *host_layers) {
+    if (!m) return -1;
+    if (host_bytes) *host_bytes = m->host_bytes;
+    if (host_layers) *host_layers = m->host_layers;
+    return 0;
 }
 
 int sdy_model_memory(const engine_model *m, size_t *weight_bytes, size_t *gemm_copy_bytes, int *n_copies,

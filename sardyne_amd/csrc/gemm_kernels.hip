@@ -964,13 +964,15 @@ __global__ __launch_bounds__(256) void k_gemm_layout(const uint8_t *__restrict__
 }
 
 extern "C" size_t sdy_mat_gemm_layout_bytes(const sdy_mat *m) {
-    if (!m || !m->base || (m->type != SDY_Q4_K && m->type != SDY_Q6_K) || !m->gemm_ok || m->gbase) return 0;
+    if (!m || !m->base || m->hbase || (m->type != SDY_Q4_K && m->type != SDY_Q6_K) || !m->gemm_ok || m->gbase)
+        return 0;
     size_t off[5], sz[5];
     return gemm_layout_planes(m->type, m->n_in, m->n_rows, off, sz);
 }
 
 extern "C" int sdy_mat_gemm_layout(sdy_mat *m, sdy_stream s) {
-    if (!m || !m->base || (m->type != SDY_Q4_K && m->type != SDY_Q6_K) || !m->gemm_ok) return 0;
+    // (a matrix in host memory keeps no copy: the GEMM reads its planes in place)
+    if (!m || !m->base || m->hbase || (m->type != SDY_Q4_K && m->type != SDY_Q6_K) || !m->gemm_ok) return 0;
     if (m->grow0 != 0 || (m->gbase && m->grows != m->n_rows))
         return sdy_fail(-1, "gemm_layout: made for a whole matrix, not a row view");
     size_t off[5], sz[5];
@@ -1000,7 +1002,7 @@ extern "C" int sdy_mat_gemm_layout(sdy_mat *m, sdy_stream s) {
 
 // Flags (bad = 1) rows [r0, r0 + n) of m that the GEMM cannot multiply exactly. Synchronous.
 extern "C" int sdy_gemm_check_rows_async(const sdy_mat *m, long r0, long n, int *bad_dev, sdy_stream s) {
-    if (m->type != SDY_Q4_K && m->type != SDY_Q6_K) return 0;
+    if ((m->type != SDY_Q4_K && m->type != SDY_Q6_K) || m->hbase) return 0;  // (host memory: wide, unchecked)
     sdy_mat v = sdy_mat_rows(m, r0, n);
     GemmArgs g = gemm_args(&v);
     const long total = n * (long)g.nb;
@@ -1012,7 +1014,7 @@ extern "C" int sdy_gemm_check_rows_async(const sdy_mat *m, long r0, long n, int 
 
 extern "C" int sdy_gemm_check_rows(const sdy_mat *m, long r0, long n, int *bad_host, sdy_stream s) {
     *bad_host = 1;
-    if (m->type != SDY_Q4_K && m->type != SDY_Q6_K) return 0;
+    if ((m->type != SDY_Q4_K && m->type != SDY_Q6_K) || m->hbase) return 0;
     sdy_mat v = sdy_mat_rows(m, r0, n);
     GemmArgs g = gemm_args(&v);
     int *bad = nullptr, rc;

@@ -69,6 +69,19 @@ struct DstPlanes {
     SDY_DEV uint8_t *operator[](int i) const { return p[i]; }
 };
 
+// Whole-record stores of bytes assembled in registers (a matrix in host memory takes the stores over
+// the host link, where single-byte writes would each be a transaction of their own).
+template <int N>
+SDY_DEV void st_bytes(uint8_t *dst, const uint8_t (&b)[N]) {
+    uint32_t w[N / 4];
+#pragma unroll
+    for (int k = 0; k < N / 4; k++)
+        w[k] = b[4 * k] | (uint32_t)b[4 * k + 1] << 8 | (uint32_t)b[4 * k + 2] << 16 | (uint32_t)b[4 * k + 3] << 24;
+    if constexpr (N == 16) *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+    else if constexpr (N == 8) *reinterpret_cast<uint2 *>(dst) = make_uint2(w[0], w[1]);
+    else *reinterpret_cast<uint32_t *>(dst) = w[0];
+}
+
 template <int WT>
 __global__ void k_repack(const uint8_t *__restrict__ src, size_t src_row, Planes P, DstPlanes dst, long n_rows,
                          RowMap map) {
@@ -81,14 +94,19 @@ __global__ void k_repack(const uint8_t *__restrict__ src, size_t src_row, Planes
     if constexpr (WT == SDY_Q4_K) {
         int s = u >> 2, j = u & 3;
         const uint8_t *sb = r + 144 * s;
-        uint8_t *qa = dst[0] + (row * P.T + u) * 16, *qb = dst[1] + (row * P.T + u) * 16;
+        uint8_t a[16], b[16];
+#pragma unroll
         for (int i = 0; i < 16; i++) {
-            qa[i] = sb[16 + 32 * j + i];
-            qb[i] = sb[16 + 32 * j + 16 + i];
+            a[i] = sb[16 + 32 * j + i];
+            b[i] = sb[16 + 32 * j + 16 + i];
         }
+        st_bytes(dst[0] + (row * P.T + u) * 16, a);
+        st_bytes(dst[1] + (row * P.T + u) * 16, b);
         if (j == 0) {
-            uint8_t *h = dst[2] + (row * P.nb + s) * 16;
+            uint8_t h[16];
+#pragma unroll
             for (int i = 0; i < 16; i++) h[i] = sb[i];
+            st_bytes(dst[2] + (row * P.nb + s) * 16, h);
         }
     } else if constexpr (WT == SDY_Q6_K) {
         int s = u >> 2, j = u & 3;
@@ -104,31 +122,36 @@ __global__ void k_repack(const uint8_t *__restrict__ src, size_t src_row, Planes
             return (sb[128 + 32 * half + l] >> (2 * k)) & 3;
         };
         int base = 64 * j;
-        uint8_t *n0 = dst[0] + (row * P.T + u) * 16, *n1 = dst[1] + (row * P.T + u) * 16;
-        uint8_t *hb = dst[2] + (row * P.T + u) * 16;
+        uint8_t n0[16], n1[16], hb[16];
+#pragma unroll
         for (int i = 0; i < 32; i++) {
             uint8_t v = (uint8_t)(lo4(base + i) | (lo4(base + i + 32) << 4));
             if (i < 16) n0[i] = v;
             else n1[i - 16] = v;
         }
+#pragma unroll
         for (int i = 0; i < 16; i++) {
             int v = 0;
             for (int k = 0; k < 4; k++) v |= hi2(base + i + 16 * k) << (2 * k);
             hb[i] = (uint8_t)v;
         }
+        st_bytes(dst[0] + (row * P.T + u) * 16, n0);
+        st_bytes(dst[1] + (row * P.T + u) * 16, n1);
+        st_bytes(dst[2] + (row * P.T + u) * 16, hb);
         if (j == 0) {
-            uint8_t *sc = dst[3] + (row * P.nb + s) * 16;
+            uint8_t sc[16];
+#pragma unroll
             for (int i = 0; i < 16; i++) sc[i] = sb[192 + i];
-            uint8_t *d = dst[4] + (row * P.nb + s) * 2;
-            d[0] = sb[208];
-            d[1] = sb[209];
+            st_bytes(dst[3] + (row * P.nb + s) * 16, sc);
+            *reinterpret_cast<uint16_t *>(dst[4] + (row * P.nb + s) * 2) = (uint16_t)(sb[208] | sb[209] << 8);
         }
     } else {
         // 32-element types: blocks 2u and 2u+1 (the second may be absent when the row has an odd
         // number of blocks: zero quants and zero scale).
         constexpr int BB = WT == SDY_Q8_0 ? 34 : WT == SDY_Q4_0 ? 18 : 22;
         constexpr int QOFF = WT == SDY_Q8_0 ? 2 : WT == SDY_Q4_0 ? 2 : 6;
-        uint8_t *d = dst[4] + (row * P.T + u) * 4;
+        uint8_t d[4];
+#pragma unroll
         for (int h = 0; h < 2; h++) {
             int b = 2 * u + h;
             bool ok = b < P.nb;
@@ -136,20 +159,28 @@ __global__ void k_repack(const uint8_t *__restrict__ src, size_t src_row, Planes
             d[2 * h] = ok ? blk[0] : 0;
             d[2 * h + 1] = ok ? blk[1] : 0;
             if constexpr (WT == SDY_Q8_0) {
-                uint8_t *q0 = dst[2 * h] + (row * P.T + u) * 16, *q1 = dst[2 * h + 1] + (row * P.T + u) * 16;
+                uint8_t q0[16], q1[16];
+#pragma unroll
                 for (int i = 0; i < 16; i++) {
                     q0[i] = ok ? blk[QOFF + i] : 0;
                     q1[i] = ok ? blk[QOFF + 16 + i] : 0;
                 }
+                st_bytes(dst[2 * h] + (row * P.T + u) * 16, q0);
+                st_bytes(dst[2 * h + 1] + (row * P.T + u) * 16, q1);
             } else {
-                uint8_t *q = dst[h] + (row * P.T + u) * 16;
+                uint8_t q[16];
+#pragma unroll
                 for (int i = 0; i < 16; i++) q[i] = ok ? blk[QOFF + i] : 0;
+                st_bytes(dst[h] + (row * P.T + u) * 16, q);
                 if constexpr (WT == SDY_Q5_0) {
-                    uint8_t *qh = dst[2] + (row * P.T + u) * 8 + 4 * h;
+                    uint8_t qh[4];
+#pragma unroll
                     for (int i = 0; i < 4; i++) qh[i] = ok ? blk[2 + i] : 0;
+                    st_bytes(dst[2] + (row * P.T + u) * 8 + 4 * h, qh);
                 }
             }
         }
+        st_bytes(dst[4] + (row * P.T + u) * 4, d);
     }
 }
 
@@ -1880,7 +1911,7 @@ static int check_shape(int type, int n_in, long n_rows) {
     return 0;
 }
 
-extern "C" int sdy_mat_alloc(sdy_mat *m, int type, int n_in, long n_rows) {
+static int mat_alloc(sdy_mat *m, int type, int n_in, long n_rows, bool host) {
     int rc = check_shape(type, n_in, n_rows);
     if (rc) return rc;
     memset(m, 0, sizeof(*m));
@@ -1889,18 +1920,30 @@ extern "C" int sdy_mat_alloc(sdy_mat *m, int type, int n_in, long n_rows) {
     m->n_rows = n_rows;
     m->n_units = n_units(type, n_in);
     m->bytes = sdy_mat_bytes(type, n_in, n_rows);
-    if ((rc = sdy_malloc(&m->base, m->bytes))) return rc;
+    if ((rc = host ? sdy_host_alloc_mapped(&m->hbase, &m->base, m->bytes) : sdy_malloc(&m->base, m->bytes))) return rc;
     size_t pb[5], off = 0;
     plane_row_bytes(type, n_in, pb);
     for (int i = 0; i < 5; i++) {
         m->plane_off[i] = off;
         if (pb[i]) off += align256(pb[i] * (size_t)n_rows);
     }
-    // zero rows pass the GEMM check, so a matrix filled in several uploads is checked piecewise
-    m->gemm_ok = type == SDY_Q4_K || type == SDY_Q6_K;
-    // (completed before returning: the uploads run on other, non-blocking streams)
+    // zero rows pass the GEMM check, so a matrix filled in several uploads is checked piecewise. A
+    // matrix in host memory is not checked (the check's reads would cross the host link) and takes
+    // the GEMM's wide variant, exact for every block
+    m->gemm_ok = type == SDY_Q4_K || type == SDY_Q6_K ? (host ? 2 : 1) : 0;
+    // (zeroed by the GPU for host memory too: its pages are mapped to the device at allocation, and the
+    // CPU's first touch of each would fault. Completed before returning: the uploads run on other,
+    // non-blocking streams)
     if (m->gemm_ok && ((rc = sdy_memset(m->base, 0, m->bytes, nullptr)) || (rc = sdy_sync(nullptr)))) return rc;
     return 0;
+}
+
+extern "C" int sdy_mat_alloc(sdy_mat *m, int type, int n_in, long n_rows) {
+    return mat_alloc(m, type, n_in, n_rows, false);
+}
+
+extern "C" int sdy_mat_alloc_host(sdy_mat *m, int type, int n_in, long n_rows) {
+    return mat_alloc(m, type, n_in, n_rows, true);
 }
 
 // The GEMM's copy of m, stale once rows change: freed (the GEMM then reads the planes).
@@ -2015,8 +2058,8 @@ extern "C" int sdy_mat_upload(sdy_mat *m, int type, int n_in, long n_rows, const
 extern "C" int sdy_mat_free(sdy_mat *m) {
     if (!m || !m->base) return 0;
     int rc = drop_gemm_layout(m);
-    const int rc2 = sdy_free(m->base);
-    m->base = nullptr;
+    const int rc2 = m->hbase ? sdy_host_free(m->hbase) : sdy_free(m->base);
+    m->base = m->hbase = nullptr;
     return rc ? rc : rc2;
 }
 

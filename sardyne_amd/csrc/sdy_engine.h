@@ -34,7 +34,9 @@ struct engine_model {
     dlayer *layers;
     float *vectors, *vec_cursor; /* one device allocation for every f32 vector */
     sdy_stream st;
-    size_t device_bytes;       /* the uploaded weights (the planes of every matrix) */
+    size_t device_bytes;       /* the uploaded weights in device memory (the planes of every matrix) */
+    size_t host_bytes;         /* expert stacks kept in pinned host memory (read in place by the kernels) */
+    int host_layers;           /* layers whose expert stacks are in host memory */
     size_t gemm_bytes;         /* the prefill GEMM's tiled copies made at load */
     int gemm_copies, gemm_skipped;
 };

@@ -33,6 +33,9 @@ int sdy_sync(sdy_stream s);
 int sdy_stream_new(sdy_stream *s);
 int sdy_stream_free(sdy_stream s);
 int sdy_host_alloc(void **p, size_t n); /* pinned host memory */
+/* pinned host memory that kernels read in place: host the allocation (for sdy_host_free), dev its
+ * device address; SDY_ERR_ALLOC when the host has no room */
+int sdy_host_alloc_mapped(void **host, void **dev, size_t n);
 int sdy_host_free(void *p);
 int sdy_device_info(int *n_cu, size_t *mem_total);
 /* Free and total device memory now (hipMemGetInfo). */
@@ -67,6 +70,8 @@ typedef struct {
     size_t gbytes;
     long grow0;     /* the first row of a row view in that copy */
     long grows;     /* rows of the matrix the copy was made from */
+    void *hbase;    /* a matrix in pinned host memory (sdy_mat_alloc_host): the allocation, whose device
+                       address is base; NULL for a matrix in device memory */
 } sdy_mat;
 
 /* Bytes of the device layout for a matrix. */
@@ -75,6 +80,9 @@ size_t sdy_mat_bytes(int type, int n_in, long n_rows);
 int sdy_mat_upload(sdy_mat *m, int type, int n_in, long n_rows, const void *host_raw, sdy_stream s);
 /* Allocate a matrix in the device layout (contents undefined until rows are uploaded). */
 int sdy_mat_alloc(sdy_mat *m, int type, int n_in, long n_rows);
+/* The same layout in pinned host memory that the kernels read in place over the host link (every
+ * sdy_mat entry point takes it; no GEMM copy is made of it). */
+int sdy_mat_alloc_host(sdy_mat *m, int type, int n_in, long n_rows);
 /* Upload n raw rows from host memory into rows r0, r0 + step, ... of an allocated matrix: step 1
  * fills a range (concatenated matrices), step 2 interleaves two matrices row by row. */
 int sdy_mat_upload_rows(sdy_mat *m, long r0, long step, long n, const void *host_raw, sdy_stream s);

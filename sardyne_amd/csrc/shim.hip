@@ -133,6 +133,26 @@ extern "C" int sdy_host_alloc(void **p, size_t n) {
     return 0;
 }
 
+extern "C" int sdy_host_alloc_mapped(void **host, void **dev, size_t n) {
+    int rc = sdy_init();
+    if (rc) return rc;
+    *host = *dev = nullptr;
+    // coarse-grained (non-coherent): the GPU may keep the lines in its caches, which suits weights
+    // written once at load and then only read
+    hipError_t e = hipHostMalloc(host, n ? n : 64, hipHostMallocMapped | hipHostMallocNonCoherent);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        *host = nullptr;
+        return sdy_fail(SDY_ERR_ALLOC, "pinned host allocation of %.1f MB failed: %s", n / 1e6, hipGetErrorString(e));
+    }
+    if ((e = hipHostGetDevicePointer(dev, *host, 0)) != hipSuccess) {
+        (void)hipHostFree(*host);
+        *host = *dev = nullptr;
+        return sdy_fail(-2, "hipHostGetDevicePointer: %s", hipGetErrorString(e));
+    }
+    return 0;
+}
+
 extern "C" int sdy_host_free(void *p) {
     if (!p) return 0;
     HIPCK(hipHostFree(p), "hipHostFree");

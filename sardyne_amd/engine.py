@@ -43,13 +43,16 @@ class LoadedModel:
         return self.info.n_vocab
 
     def memory(self) -> dict:
-        """Device memory the model holds (sdy_model_memory): weight bytes, the prefill GEMM's tiled
-        copies, and how many matrices got a copy / were left without one."""
+        """Memory the model holds (sdy_model_memory, sdy_model_host_weights): weight bytes in device
+        memory, the prefill GEMM's tiled copies and how many matrices got a copy / were left without
+        one, and the expert stacks kept in pinned host memory (bytes, layers)."""
         w, g, nc, ns = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_int(), ctypes.c_int()
         capi.check(self._lib.sdy_model_memory(self._h, ctypes.byref(w), ctypes.byref(g), ctypes.byref(nc),
                                               ctypes.byref(ns)))
+        hb, hl = ctypes.c_size_t(), ctypes.c_int()
+        capi.check(self._lib.sdy_model_host_weights(self._h, ctypes.byref(hb), ctypes.byref(hl)))
         return {"weight_bytes": w.value, "gemm_copy_bytes": g.value, "gemm_copies": nc.value,
-                "gemm_copies_skipped": ns.value}
+                "gemm_copies_skipped": ns.value, "host_expert_bytes": hb.value, "host_expert_layers": hl.value}
 
     def session(self, max_seq: int = 2048, n_batch: int = 64, logits_all: bool = False,
                 n_threads: int = 0) -> "Session":

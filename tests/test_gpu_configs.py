@@ -13,7 +13,8 @@
       (two 512-token chunks), then one-token steps through the device router: the exact chain
       bit-identical, the chunked and split attentions within twice the spread between the
       reference's own AVX2 and scalar engines on the same model and tokens (golden/c5_simd_spread.npz),
-      with the same greedy tokens.
+      with the same greedy tokens. On a device with room for half its experts, the rest in pinned
+      host memory: the bits of the load with every expert on the device.
 
 The models are written to /dev/shm (2.2 GB and 19.8 GB) and deleted afterwards.
 """
@@ -188,15 +189,53 @@ def c5_tolerance():
     return SPREAD_MULTIPLE * float(g["spread"].max()) / float(g["scale"])
 
 
+@pytest.fixture(scope="module")
+def qwen3_30b_a3b_path():
+    p = _shm_model(qwen3_30b_a3b(), "qwen3_30b_a3b")
+    yield p
+    p.unlink(missing_ok=True)
+
+
 @needs_ref
-def test_c5_qwen3_30b_a3b_context_1024_then_decode():
+def test_c5_qwen3_30b_a3b_context_1024_then_decode(qwen3_30b_a3b_path):
     """48 layers of int8 activation rounding and top-8 routing amplify any change of f32 rounding: the
     exact chain gives the reference's bits, the chunked and split attentions stay within twice the
     reference's own AVX2-vs-scalar spread on this model and token sequence, with the same greedy
     tokens."""
-    tol = c5_tolerance()
-    p = _shm_model(qwen3_30b_a3b(), "qwen3_30b_a3b")
+    _run_and_compare(qwen3_30b_a3b_path, 1024, 512, 5, 1152, seed=1, tol=c5_tolerance())
+
+
+def test_c5_experts_beyond_the_device_memory(qwen3_30b_a3b_path):
+    """The Qwen3-30B-A3B-shaped model on a device that holds about half of its expert stacks: a
+    ballast allocation leaves free the attention and embedding weights, half the experts and a
+    2 GiB reserve. The loader places each layer's experts on the device while the reserve stays
+    free and the rest in pinned host memory, which the grouped GEMM and the device-routed decode
+    read in place; a 512-token prompt and three decode steps give the logits bits of the load with
+    every expert on the device (the exact attention chain in both)."""
+    L = capi.lib()
+    capi.check(L.sdy_init())
+    toks = np.random.default_rng(4).integers(0, 151936, 515).astype(np.int32)
+
+    def run():
+        with engine_env(SARDYNE_ATTENTION="exact", SARDYNE_RESERVE_MB="2048", SARDYNE_GEMM_COPY_MB="0"):
+            model = LoadedModel(qwen3_30b_a3b_path)
+            s = model.session(max_seq=640, n_batch=512)
+        out = np.stack([s.feed(toks[:512])] + [s.step(int(t)) for t in toks[512:]])
+        return out, model.memory()
+
+    base, mem = run()
+    assert mem["host_expert_layers"] == 0 and mem["host_expert_bytes"] == 0
+    spec = qwen3_30b_a3b()
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    capi.check(L.sdy_mem_info(ctypes.byref(free), ctypes.byref(total)))
+    room = mem["weight_bytes"] // 2 + (2048 << 20) + (256 << 20)
+    assert free.value > room
+    ballast = capi.DeviceBuffer(free.value - room)
     try:
-        _run_and_compare(p, 1024, 512, 5, 1152, seed=1, tol=tol)
+        got, mem2 = run()
     finally:
-        p.unlink(missing_ok=True)
+        ballast.close()
+    assert 0 < mem2["host_expert_layers"] < spec.n_layer, mem2
+    assert mem2["weight_bytes"] + mem2["host_expert_bytes"] == mem["weight_bytes"]
+    assert np.all(np.isfinite(base))
+    assert np.array_equal(base.view(np.uint32), got.view(np.uint32))

@@ -321,6 +321,39 @@ def test_long_context_decode(spec, tmp_path):
 
 
 
+@pytest.mark.parametrize("spec,where", [("moe-128x8", "all"), ("moe-kquant", "all"), ("moe-16x4-ffn768", "1")])
+def test_host_experts_keep_the_bits(tmp_path, spec, where):
+    """Expert stacks in pinned host memory (SARDYNE_HOST_EXPERTS=all, or 1: the last layer's), read in
+    place by the kernels: prompt chunks on the grouped GEMM and one-token steps through the device
+    router, replayed and eager, give the bits of the load with every expert on the device (the
+    exact chain and the default attention). moe-kquant has gate and up of two types (separate
+    stacks) and Q5_0 down projections."""
+    path = tmp_path / "m.gguf"
+    write_model(path, dataclasses.replace(SPECS[spec], context=160), seed=9)
+    toks = np.random.default_rng(10).integers(0, 300, 60).tolist()
+
+    def run(**env):
+        model = LoadedModel(path)
+        out = []
+        for mode in ("exact", "chunked"):
+            for graph in ("0", "1"):
+                sw = {"SARDYNE_ATTENTION": mode, **({"SARDYNE_NO_GRAPH": "1"} if graph == "1" else {})}
+                with engine_env(**sw, **env):
+                    ctx = model.session(max_seq=128, n_batch=32)
+                out += [ctx.feed(toks[:50])] + [ctx.feed([t]) for t in toks[50:]]
+                del ctx
+        return np.stack(out), model.memory()
+
+    with engine_env(SARDYNE_HOST_EXPERTS="none"):
+        base, mem = run()
+    with engine_env(SARDYNE_HOST_EXPERTS=where):
+        got, mem2 = run()
+    n_layer = SPECS[spec].n_layer
+    assert mem["host_expert_layers"] == 0 and mem2["host_expert_layers"] == (n_layer if where == "all" else 1)
+    assert mem2["host_expert_bytes"] > 0 and mem2["weight_bytes"] + mem2["host_expert_bytes"] == mem["weight_bytes"]
+    assert np.array_equal(base.view(np.uint32), got.view(np.uint32)), float(np.abs(base - got).max())
+
+
 def _memory(model):
     m = model.memory()
     return m["weight_bytes"], m["gemm_copy_bytes"], m["gemm_copies"], m["gemm_copies_skipped"]

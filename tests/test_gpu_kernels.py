@@ -1163,6 +1163,59 @@ def test_gemm_layout_copy_and_planes_same_bits(kind):
     assert np.array_equal(bits(run(tiled)), bits(exp))
 
 
+@pytest.mark.parametrize("kind", list(TYPES))
+def test_matrix_in_host_memory_same_bits(kind):
+    """A matrix in pinned host memory (sdy_mat_alloc_host, read in place by the kernels over the host
+    link, as the engine keeps expert stacks the device has no room for): its dequantised rows, its
+    one-token and 40-token matvecs and, for the K-quants, the GEMM (the wide variant: a host matrix is
+    not checked, and keeps no tiled copy) have the bits of the same matrix in device memory."""
+    L = lib()
+    n_in, n_out, n_tok = 2048, 70, 40
+    t, w, xq = _matvec_case(kind, n_in, n_out, n_tok, seed=31)
+    dev = capi.DeviceMatrix(t, n_in, n_out, w, gemm_layout=False)
+    host = capi.SdyMat()
+    capi.check(L.sdy_mat_alloc_host(ctypes.byref(host), t, n_in, n_out))
+    try:
+        assert host.hbase and host.base
+        raw = np.ascontiguousarray(w).view(np.uint8)
+        capi.check(L.sdy_mat_upload_rows(ctypes.byref(host), 0, 1, n_out, raw.ctypes.data, None))
+        capi.check(L.sdy_mat_gemm_layout(ctypes.byref(host), None))
+        assert not host.gbase
+        kq = t in (O.Q4_K, O.Q6_K)
+        assert host.gemm_ok == (2 if kq else 0)
+
+        def dequant(m):
+            d = capi.DeviceBuffer(n_out * n_in * 4)
+            capi.check(L.sdy_dequant_rows(ctypes.byref(m), 0, n_out, d.ptr, None))
+            return d.to_array(np.float32, (n_out, n_in))
+
+        def matvec(m, n, gemm=False):
+            q = capi.DeviceBuffer.from_array(xq[:n] if not gemm else O.quantize(
+                np.random.default_rng(32).standard_normal((n, n_in)).astype(np.float32), O.Q8_K))
+            out = capi.DeviceBuffer.from_array(np.full((n, n_out), np.nan, np.float32))
+            a = capi.SdyMvArgs(xq=q.ptr, n_tok=n, out=out.ptr, out_stride=n_out, row0=0, row1=n_out)
+            if gemm:
+                ws = capi.DeviceBuffer(L.sdy_gemm_ws_bytes(n, n_in))
+                capi.check(L.sdy_gemm(ctypes.byref(m), ctypes.byref(a), ws.ptr, None))
+            else:
+                capi.check(L.sdy_matvec(ctypes.byref(m), ctypes.byref(a), None))
+            capi.check(L.sdy_sync(None))
+            return out.to_array(np.float32, (n, n_out))
+
+        assert np.array_equal(bits(dequant(host)), bits(dequant(dev.m)))
+        for n in (1, n_tok):
+            got = matvec(host, n)
+            assert np.all(np.isfinite(got))
+            assert np.array_equal(bits(got), bits(matvec(dev.m, n))), n
+        if kq:
+            got = matvec(host, n_tok, gemm=True)
+            assert np.array_equal(bits(got), bits(matvec(dev.m, n_tok, gemm=True)))
+            assert np.array_equal(bits(got), bits(O.matmul_q(w, t, O.quantize(
+                np.random.default_rng(32).standard_normal((n_tok, n_in)).astype(np.float32), O.Q8_K), n_in, simd=1)))
+    finally:
+        L.sdy_mat_free(ctypes.byref(host))
+
+
 @pytest.mark.parametrize("variant", ["11", "12", "13", "14", "15", "16", "17", "18", "19", "20"])
 @pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
 def test_gemm_tile_variants_bit_exact(kind, variant, monkeypatch):
