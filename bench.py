@@ -8,7 +8,8 @@ step streams its weights from HBM. value = algorithmic bytes per step / step tim
 Other workloads (--workload): q8_0_head (the Q8_0 matvec of the same shape), q4k_matvec (2048 x
 2048 Q4_K, measured as one launch over 448 stacked copies), decode_3b (Qwen2.5-3B-shaped Q4_K_M
 decode tok/s, 128 tokens after a 512-token context), decode_moe (Qwen3-30B-A3B-shaped MoE decode,
-128 tokens after a 1024-token context), prefill_3b (one 512-token prompt through the
+128 tokens after a 1024-token context), decode_moe_host (the same with the expert stacks in pinned
+host memory, the placement of a model larger than the device), prefill_3b (one 512-token prompt through the
 Qwen2.5-3B-shaped model), grid_barrier (the per-phase synchronisation a persistent decode kernel
 would pay, against the kernel boundary).
 
@@ -41,6 +42,7 @@ from sardyne_amd.gguf_synth import random_blocks  # noqa: E402
 
 METRIC = "Q4_K/Q6_K matvec GB/s (% of HBM peak); decode tok/s, Qwen2.5-3B shape"
 HBM_PEAK_GBPS = 8000.0
+PCIE5_X16_GBPS = 64.0  # the host link, one direction (PCIe 5.0 x16)
 Q4_K, Q6_K, Q8_0, Q8_K = 12, 14, 8, 15
 BLOCK = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34), Q8_K: (256, 292)}
 
@@ -358,6 +360,36 @@ def decode_weight_bytes(spec):
         layer += 2 * spec.ffn_dim * row_bytes(td, dim) + dim * row_bytes(spec.t_ffn_down, spec.ffn_dim)
     head = spec.n_vocab * row_bytes(spec.t_embd if spec.tied else spec.t_output, dim)
     return spec.n_layer * layer + head + dim * 4 + row_bytes(spec.t_embd, dim)
+
+
+def routed_expert_bytes(spec):
+    """Weight bytes of the k routed experts one decode token reads (gate, up and down, every layer)."""
+    from sardyne_amd.gguf_synth import row_bytes
+    fe = spec.ffn_exp_dim
+    return spec.n_layer * spec.n_expert_used * (2 * fe * row_bytes(spec.t_default, spec.dim)
+                                                + spec.dim * row_bytes(spec.t_ffn_down, fe))
+
+
+def host_link_read_GBps(stream, gib=4):
+    """The GPU's read rate of pinned host memory: the HBM probe kernel over a buffer the engine would
+    hold host-resident experts in (sdy_host_alloc_mapped), best of 3."""
+    L = capi.lib()
+    h, d = ctypes.c_void_p(), ctypes.c_void_p()
+    n = gib << 30
+    capi.check(L.sdy_host_alloc_mapped(ctypes.byref(h), ctypes.byref(d), n))
+    sink = capi.DeviceBuffer(64)
+    try:
+        capi.check(L.sdy_memset(d, 0, n, stream))
+        ev = Events(stream)
+        best = 0.0
+        for _ in range(3):
+            ev.start()
+            capi.check(L.sdy_membw_read(d, n, sink.ptr, stream))
+            best = max(best, n / (ev.stop_ms() * 1e-3) / 1e9)
+        return best
+    finally:
+        capi.check(L.sdy_sync(stream))
+        capi.check(L.sdy_host_free(h))
 
 
 def engine_modes():
@@ -694,8 +726,8 @@ def main():
                     help="timed steps (default: 50; decode workloads: 128 generated tokens)")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="q6k_head",
-                    choices=["q6k_head", "q8_0_head", "q4k_matvec", "decode_3b", "decode_moe", "prefill_3b",
-                             "grid_barrier"])
+                    choices=["q6k_head", "q8_0_head", "q4k_matvec", "decode_3b", "decode_moe", "decode_moe_host",
+                             "prefill_3b", "grid_barrier"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--n-batch", type=int, default=512, help="GPU prefill chunk (decode workloads)")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (smoke runs only)")
@@ -750,6 +782,22 @@ def main():
         from sardyne_amd.gguf_synth import qwen3_30b_a3b
         line = decode_line(args, qwen3_30b_a3b(args.layers or 48), "qwen3_30b_a3b", 1024,
                            "Qwen3-30B-A3B-shaped qwen3moe Q4_K_M (128 experts resident, top-8)")
+    elif args.workload == "decode_moe_host":
+        # the same decode with every expert stack in pinned host memory (a model larger than the
+        # device): the routed experts' weights cross the host link each token
+        from sardyne_amd.gguf_synth import qwen3_30b_a3b
+        os.environ["SARDYNE_HOST_EXPERTS"] = os.environ.get("SARDYNE_HOST_EXPERTS") or "all"
+        spec = qwen3_30b_a3b(args.layers or 48)
+        line = decode_line(args, spec, "qwen3_30b_a3b_host", 1024,
+                           "Qwen3-30B-A3B-shaped qwen3moe Q4_K_M (experts in pinned host memory, top-8)")
+        eb = routed_expert_bytes(spec)
+        gbps = eb * line["value"] / 1e9
+        line["roofline"] = {"bound": "host_link", "achieved": round(gbps, 1), "peak": PCIE5_X16_GBPS,
+                            "unit": "GB/s", "frac": round(gbps / PCIE5_X16_GBPS, 4), "traffic": None,
+                            "kernel": "routed experts' weights read in place from pinned host memory",
+                            "routed_expert_bytes_per_token": eb,
+                            "achievable_GBps": round(host_link_read_GBps(None), 1),
+                            "host_expert_layers": line["model_load"]["host_expert_layers"]}
     else:
         from sardyne_amd.gguf_synth import qwen25_3b
         spec = dataclasses.replace(qwen25_3b(args.layers or 36), scales=args.scales)

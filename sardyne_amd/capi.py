@@ -176,6 +176,7 @@ _DEVICE_SIGNATURES = {
     "sdy_mat_alloc": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long]),
     "sdy_mat_alloc_host": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long]),
     "sdy_host_alloc_mapped": (_int, [ctypes.POINTER(_vp), ctypes.POINTER(_vp), _sz]),
+    "sdy_host_free": (_int, [_vp]),
     "sdy_uploader_new": (_int, [ctypes.POINTER(_vp), _sz, _int, _int, _vp]),
     "sdy_uploader_rows": (_int, [_vp, ctypes.POINTER(SdyMat), ctypes.c_long, ctypes.c_long, ctypes.c_long,
                                  ctypes.c_long, ctypes.c_long, _vp]),
