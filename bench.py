@@ -107,6 +107,7 @@ def profiled_traffic(name):
 
 
 def membw_probe(stream, gib=4):
+    """The GPU's HBM read rate for a pure read stream (sdy_membw_read) over a gib-GiB buffer, GB/s."""
     L = capi.lib()
     n = gib << 30
     buf = capi.DeviceBuffer(n)
@@ -258,6 +259,20 @@ def bench_matvec(args, wt, n_out, n_in, n_copies, stacked):
     achieved = algo_launch / (ms_k * 1e-3) / 1e9
     traffic = profiled_traffic(f"k_matvec_{name.lower()}_{'stacked' if stacked else 'head'}.md")
     achievable = membw_probe(st)
+    # the read probes over the matrices themselves, one launch per copy in rotation, back to back: a
+    # pure read stream of this launch size, with the per-launch ramp and tail the matvec also pays
+    # (the faster of the two read orders)
+    sink = capi.DeviceBuffer(64)
+    achievable_launch = 0.0
+    for probe in (L.sdy_membw_read, L.sdy_membw_read_strided):
+        def read_copy(i, probe=probe):
+            m = mats[i % len(mats)]
+            capi.check(probe(ctypes.c_void_p(m.m.base), m.m.bytes, sink.ptr, st))
+
+        for i in range(len(mats)):
+            read_copy(i)
+        ms_r = per_launch_ms(st, read_copy, max(args.steps, 8 * len(mats)))
+        achievable_launch = max(achievable_launch, mats[0].m.bytes / (ms_r * 1e-3) / 1e9)
     back_to_back = None
     if stacked:
         # the same copies as separate n_out x n_in matrices (row views of the stack, each its own region
@@ -324,6 +339,7 @@ def bench_matvec(args, wt, n_out, n_in, n_copies, stacked):
             if wt == Q6_K else "int8", "data": "synthetic (seeded random quantized blocks, x ~ N(0,1))",
             "config": cfg, "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2),
             "achievable_hbm_GBps": round(achievable, 1),
+            "achievable_hbm_GBps_at_launch_size": round(achievable_launch, 1),
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                          "kernel": kernel, "kernel_avg_us": round(ms_k * 1e3, 3),

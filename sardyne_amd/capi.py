@@ -150,6 +150,7 @@ _DEVICE_SIGNATURES = {
     "sdy_graph_launch": (_int, [_vp, _vp]),
     "sdy_graph_free": (_int, [_vp]),
     "sdy_membw_read": (_int, [_vp, _sz, _vp, _vp]),
+    "sdy_membw_read_strided": (_int, [_vp, _sz, _vp, _vp]),
     "sdy_mat_bytes": (_sz, [_int, _int, ctypes.c_long]),
     "sdy_mat_upload": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long, _vp, _vp]),
     "sdy_mat_upload_rows": (_int, [ctypes.POINTER(SdyMat), ctypes.c_long, ctypes.c_long, ctypes.c_long, _vp, _vp]),

@@ -50,8 +50,10 @@ int sdy_graph_end(sdy_stream s, void **exec);
 void sdy_graph_abort(sdy_stream s);
 int sdy_graph_launch(void *exec, sdy_stream s);
 int sdy_graph_free(void *exec);
-/* reads every byte of buf once (HBM bandwidth probe); sink: 4 bytes of device memory */
+/* reads every byte of buf once (HBM bandwidth probe); sink: 4 bytes of device memory. _strided: the
+ * same in a grid-strided order over fewer workgroups (the faster one on buffers of a few hundred MB) */
 int sdy_membw_read(const void *buf, size_t bytes, void *sink, sdy_stream s);
+int sdy_membw_read_strided(const void *buf, size_t bytes, void *sink, sdy_stream s);
 
 /* ---- weight matrices in the device layout (planes, see quant_kernels.hip) */
 typedef struct {

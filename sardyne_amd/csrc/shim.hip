@@ -266,13 +266,42 @@ extern "C" int sdy_graph_free(void *exec) {
     return 0;
 }
 
-// ---- HBM read-bandwidth probe: every byte of buf read once, in the streaming weight kernels' load
-// pattern: non-temporal 16-byte loads, one 1 KiB contiguous span per wave and load instruction, eight
-// loads of a lane in flight before their data is used, over a grid the GPU holds at once (8
-// workgroups of 256 threads per CU). An XOR of the data is kept live so the loads are not removed.
+// ---- HBM read-bandwidth probe: every byte of buf read once, as fast as a pure read stream goes:
+// each workgroup reads a contiguous slice (n16 / grid 16-byte elements) with non-temporal 16-byte
+// loads, 4 KiB per workgroup and load instruction, eight loads of a lane in flight before their data
+// is used, over 8 workgroups of 256 threads per CU; the last workgroup also reads the remainder. A
+// sweep of read patterns over 4 GiB on MI355X put this one (slices per workgroup: 7.0-7.2 TB/s) above
+// the grid-strided form of the weight kernels (consecutive waves on consecutive KiB, every wave's
+// loads in flight a grid apart: 5.9-6.8 TB/s by grid size). An XOR of the data is kept live so the
+// loads are not removed.
 typedef unsigned int membw_u32x4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(256) void k_membw_read(const membw_u32x4 *__restrict__ p, size_t n16, unsigned *sink) {
     constexpr int U = 8;
+    const size_t per = n16 / gridDim.x, stride = blockDim.x;
+    const membw_u32x4 *q = p + blockIdx.x * per;
+    const size_t end = blockIdx.x + 1 == gridDim.x ? n16 - blockIdx.x * per : per;
+    size_t i = threadIdx.x;
+    unsigned acc = 0;
+    for (; i + (U - 1) * stride < end; i += U * stride) {
+        membw_u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = __builtin_nontemporal_load(q + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < end; i += stride) {
+        const membw_u32x4 v = __builtin_nontemporal_load(q + i);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+// The same read stream grid-strided (consecutive waves on consecutive KiB, four loads of a lane in
+// flight a grid apart) over 2 workgroups of 256 threads per CU: on buffers of a few hundred MB read
+// back to back, where each launch's ramp and tail weigh more, the faster of the two.
+__global__ __launch_bounds__(256) void k_membw_read_strided(const membw_u32x4 *__restrict__ p, size_t n16,
+                                                            unsigned *sink) {
+    constexpr int U = 4;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     unsigned acc = 0;
@@ -288,6 +317,14 @@ __global__ __launch_bounds__(256) void k_membw_read(const membw_u32x4 *__restric
         acc ^= v.x ^ v.y ^ v.z ^ v.w;
     }
     if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+extern "C" int sdy_membw_read_strided(const void *buf, size_t bytes, void *sink, sdy_stream s) {
+    int rc = sdy_init();
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_membw_read_strided, dim3((unsigned)(g_n_cu * 2)), dim3(256), 0, (hipStream_t)s,
+                       (const membw_u32x4 *)buf, bytes / 16, (unsigned *)sink);
+    return sdy_check_launch("membw_read_strided");
 }
 
 extern "C" int sdy_membw_read(const void *buf, size_t bytes, void *sink, sdy_stream s) {
