@@ -45,7 +45,9 @@ const char *engine_version(void);
 void engine_add_f32(const float *a, const float *b, float *out, size_t n);
 
 /* csrc/engine.h:49-51. Loads a llama / qwen2 / qwen3 / qwen3moe GGUF and uploads every weight to
- * device memory (all experts resident). NULL on error, with the reason in err. */
+ * device memory; the expert stacks of layers the device has no room for go to pinned host memory,
+ * read in place by the kernels (SARDYNE_HOST_EXPERTS, sdy_model_host_weights). NULL on error, with
+ * the reason in err. */
 engine_model *engine_model_load(const char *path, char *err, size_t err_len);
 void engine_model_free(engine_model *m);
 void engine_model_get_info(const engine_model *m, engine_model_info *out);
