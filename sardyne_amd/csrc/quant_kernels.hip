@@ -1372,16 +1372,22 @@ __global__ __launch_bounds__(THREADS) void k_matvec_ring(MvArgs a) {
 // the activations of its units in registers (read from memory with the first row's weights). Each
 // wave walks its rows one at a time.
 // PRO = 1: the f32 row a.px is quantised by the workgroup into LDS (q8k_row_lds) instead of read
-// from a.xq.
-template <int WT, int NI, int PRO = 0>
-__global__ __launch_bounds__(THREADS) void k_matvec_lr(MvArgs a) {
-    constexpr int PRO_NR = 4 * NI < 12 ? 4 * NI : 12;  // the row's super-blocks per wave in one round (NI <= 3)
+// from a.xq. WV waves per workgroup: with 4 the row is built before any weight is requested; with
+// 8 (half the workgroups, each quantising the row once) the row's loads go out first, then every
+// wave's weights, and the workgroup builds the row while the weights stream (its loads, issued
+// first, complete first). Measured on the 3B's 2048 x 11008 down: 8 waves 677 tok/s, 4 waves
+// 630-635, 16 waves (128 VGPRs: spills) 611, the quantiser's own launch 659-661.
+template <int WT, int NI, int PRO = 0, int WV = WAVES>
+__global__ __launch_bounds__(64 * WV) void k_matvec_lr(MvArgs a) {
+    // the row's super-blocks per wave in one round: up to 16 NI super-blocks over the WV waves
+    constexpr int PRO_NR = (16 * NI + WV - 1) / WV < 12 ? (16 * NI + WV - 1) / WV : 12;
+    constexpr bool WFIRST = WV > 4;
     const int T = a.P.T, nb = a.P.nb;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const long n_rows = a.row1 - a.row0;
     const long G = gridDim.x, bx = blockIdx.x;
     const long vblk = (G % 8 == 0) ? (bx % 8) * (G / 8) + bx / 8 : bx;  // XCD-aware renumbering
-    const long S = G * WAVES, wid = vblk * WAVES + wave;
+    const long S = G * WV, wid = vblk * WV + wave;
     auto load_row = [&](long r, WRegs<WT> (&R)[NI]) {
 #pragma unroll
         for (int k = 0; k < NI; k++) {
@@ -1391,16 +1397,14 @@ __global__ __launch_bounds__(THREADS) void k_matvec_lr(MvArgs a) {
     };
     WRegs<WT> A[NI];
     extern __shared__ uint8_t lds_act[];
-    Q8kRow<false, PRO_NR> arow;
+    Q8kRow<false, PRO_NR, WV> arow;
     // (with PRO, waves past the rows still take part in the workgroup's activation row: they load
     // row 0 and run no row)
     if constexpr (PRO) {
-        // the workgroup's activation row before any weight is requested (its loads would otherwise
-        // return behind the weight stream)
         arow.issue(a.px, nullptr, a.P.n_in);
-        arow.build(a.px, 0.0f, a.P.n_in, lds_act);
-    } else if (wid >= n_rows) {
-        return;
+        if constexpr (!WFIRST) arow.build(a.px, 0.0f, a.P.n_in, lds_act);
+    } else {
+        if (wid >= n_rows) return;
     }
     const long w0 = wid < n_rows ? wid : 0;
     load_row(w0, A);
@@ -1413,6 +1417,7 @@ __global__ __launch_bounds__(THREADS) void k_matvec_lr(MvArgs a) {
         }
     };
     load_br(w0);
+    if constexpr (PRO && WFIRST) arow.build(a.px, 0.0f, a.P.n_in, lds_act);
     // the lane's activations (the 64 Q8_K bytes of its unit in each pass, their bsums and the block
     // scale) straight from memory into registers, requested with the first row's weights: no LDS
     // staging, no barrier
@@ -2401,18 +2406,20 @@ static int launch_mv_pair(MvArgs &A, MvArgs &B, hipStream_t st) {
 
 template <int WT, int NI, int PRO>
 static int launch_mv_lr_ni(MvArgs &A, size_t lds, hipStream_t st, bool dry) {
+    // the workgroup-quantised row: 8-wave workgroups, the row built while the weights stream
+    constexpr int WV = PRO ? 8 : WAVES;
     static int per_cu = 0;
     static size_t per_cu_lds = 0, granted = 0;
-    const void *fn = (const void *)k_matvec_lr<WT, NI, PRO>;
+    const void *fn = (const void *)k_matvec_lr<WT, NI, PRO, WV>;
     int rc = sdy_lds_limit(fn, lds, &granted);
     if (rc) return rc;
     if (per_cu == 0 || per_cu_lds != lds) {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, THREADS, lds) != hipSuccess || n < 1) n = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, 64 * WV, lds) != hipSuccess || n < 1) n = 1;
         per_cu = n;
         per_cu_lds = lds;
     }
-    long wgs = (A.row1 - A.row0 + WAVES - 1) / WAVES;
+    long wgs = (A.row1 - A.row0 + WV - 1) / WV;
     long cap = (long)(g_n_cu ? g_n_cu : 256) * per_cu;
     if (wgs > cap) {
         // the workgroup-quantised row needs every workgroup's waves at once (each quantises once)
@@ -2420,8 +2427,8 @@ static int launch_mv_lr_ni(MvArgs &A, size_t lds, hipStream_t st, bool dry) {
         wgs = cap;
     }
     if (dry) return 0;
-    SDY_NOTE_KERNEL((k_matvec_lr<WT, NI, PRO>));
-    hipLaunchKernelGGL((k_matvec_lr<WT, NI, PRO>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
+    SDY_NOTE_KERNEL((k_matvec_lr<WT, NI, PRO, WV>));
+    hipLaunchKernelGGL((k_matvec_lr<WT, NI, PRO, WV>), dim3((unsigned)wgs), dim3(64 * WV), lds, st, A);
     return sdy_check_launch("matvec");
 }
 
