@@ -905,17 +905,17 @@ __global__ __launch_bounds__(THREADS) void k_matvec_rl_pair(MvArgs a, MvArgs b, 
     else matvec_rl_body<WT2, 1, true>(b, (long)gridDim.x - g1, (long)blockIdx.x - g1, 0);
 }
 
-// The Q8_K row of a one-token matvec built in LDS by its 256-thread workgroup from the f32 row x (n
-// elements, a multiple of 256, x 16-byte aligned), RMS-normalised first when NORM (nb <= 4 NR): the
+// The Q8_K row of a one-token matvec built in LDS by its workgroup of WV waves from the f32 row x (n
+// elements, a multiple of 256, x 16-byte aligned), RMS-normalised first when NORM (nb <= WV NR): the
 // bytes that k_quant_q8k (k_norm_quant with NORM) writes — same sum order, same wave quantiser — in
 // an aligned layout: y [nb][256] int8, bsums [nb][16] int16, d [nb] f32 (nb * 292 bytes).
-// issue() requests the lane's inputs: super-blocks wave + 4k, k < NR (called before the weight loads,
-// so that these few bytes do not queue behind the weight stream); build() quantises them into LDS,
-// loading further rounds of NR super-blocks per wave when nb > 4 NR (without NORM only). Every thread
-// of the workgroup calls build(); it ends with a barrier.
+// issue() requests the lane's inputs: super-blocks wave + WV k, k < NR (called before the weight
+// loads, so that these few bytes do not queue behind the weight stream); build() quantises them into
+// LDS, loading further rounds of NR super-blocks per wave when nb > WV NR (without NORM only). Every
+// thread of the workgroup calls build(); it ends with a barrier.
 template <bool NORM, int NR, int WV = 4>
 struct Q8kRow {
-    static_assert(!NORM || WV == 4, "the norm's block sum takes four waves");
+    static_assert(!NORM || WV == 4 || WV == 8, "the norm's sum order is that of 256 threads");
     float4 xv[NR], wv[NR];
 
     SDY_DEV void issue(const float *__restrict__ x, const float *__restrict__ nw, int n) {
@@ -939,16 +939,40 @@ struct Q8kRow {
             // (chunk t + 256 k is super-block wave + 4 k, the lane's four elements), then the tree
             __shared__ double sh[4];
             double ss = 0.0;
+            auto add = [&](const float4 &v) {
+                ss += (double)v.x * (double)v.x;
+                ss += (double)v.y * (double)v.y;
+                ss += (double)v.z * (double)v.z;
+                ss += (double)v.w * (double)v.w;
+            };
+            if constexpr (WV == 4) {
 #pragma unroll
-            for (int k = 0; k < NR; k++)
-                if (wave + 4 * k < nb) {
-                    const float4 v = xv[k];
-                    ss += (double)v.x * (double)v.x;
-                    ss += (double)v.y * (double)v.y;
-                    ss += (double)v.z * (double)v.z;
-                    ss += (double)v.w * (double)v.w;
+                for (int k = 0; k < NR; k++)
+                    if (wave + 4 * k < nb) add(xv[k]);
+                ss = sdy_block_sum256(ss, sh);
+            } else {
+                // eight waves: thread t of the 256-thread order (wave w = t / 64 < 4) takes super-blocks
+                // w, w + 4, w + 8, ... in turn; w + 8 k is wave w's k-th, w + 4 + 8 k the k-th of wave
+                // w + 4, which passes its chunks through LDS. Waves 0-3 add in that order, then the
+                // same tree over their four wave sums
+                __shared__ float4 xch[4][NR][64];
+                if (wave >= 4) {
+#pragma unroll
+                    for (int k = 0; k < NR; k++) xch[wave - 4][k][lane] = xv[k];
                 }
-            ss = sdy_block_sum256(ss, sh);
+                __syncthreads();
+                if (wave < 4) {
+#pragma unroll
+                    for (int k = 0; k < NR; k++) {
+                        if (wave + 8 * k < nb) add(xv[k]);
+                        if (wave + 4 + 8 * k < nb) add(xch[wave][k][lane]);
+                    }
+                }
+                const double v = sdy_wave_sum_f64(ss);
+                if (lane == 0 && wave < 4) sh[wave] = v;
+                __syncthreads();
+                ss = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+            }
             scale = (float)(1.0 / sqrt(ss / (double)n + (double)eps));
         }
         for (int s0 = wave; s0 < nb; s0 += WV * NR) {
@@ -1045,10 +1069,14 @@ SDY_DEV float rl_row_sum(const WRegs<WT> &cur, const uint4 (&Yr)[4], uint2 bsr, 
 // (the body of k_matvec_1t for workgroup bx of a grid of G, routed-expert slot `slot`)
 // PRO: 0 the Q8_K row a.xq in memory, 1 the f32 row a.px quantised by the workgroup (into LDS),
 // 2 a.px RMS-normalised with a.pnw, then quantised.
-template <int WT, int NIT, int NSB, int PRO = 0>
+// WV waves per workgroup: 4, or 8 for the RMS-normalised row (PRO 2), whose row is then built after
+// the weights are requested (with 4 it is built before them; its sum of squares keeps the 256-thread
+// order either way).
+template <int WT, int NIT, int NSB, int PRO = 0, int WV = WAVES>
 SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
     // super-blocks per wave of the workgroup's activation row (n_in 768: 3, 2048: 8, else up to 16)
-    constexpr int PRO_NR = NSB == 3 ? 1 : NSB == 8 ? 2 : 4;
+    constexpr int PRO_NR = WV == 4 ? (NSB == 3 ? 1 : NSB == 8 ? 2 : 4) : (NSB == 3 || NSB == 8 ? 1 : 2);
+    constexpr bool NORM_FIRST = PRO == 2 && WV == 4;  // the normalised row built before the weight loads
     const int T = a.P.T;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int rpi = a.rpi;
@@ -1066,9 +1094,9 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
         out += (size_t)slot * a.out_slot;
     }
     const int vblk = (G & 7) == 0 ? (bx & 7) * (G >> 3) + (bx >> 3) : bx;  // XCD-aware renumbering
-    const int S = G * WAVES, wid = vblk * WAVES + wave;
+    const int S = G * WV, wid = vblk * WV + wave;
     extern __shared__ uint8_t lds_act[];
-    Q8kRow<PRO == 2, PRO_NR> arow;
+    Q8kRow<PRO == 2, PRO_NR, WV> arow;
     const float *px = a.px + (PRO ? (size_t)slot * a.px_slot : 0);
     // (with PRO, waves past the rows still take part in the workgroup's activation row: their rows
     // are all >= row1, so they load row0 and store nothing)
@@ -1098,10 +1126,11 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
     uint4 Yr[4];
     uint2 bsr;
     float ydr;
-    if constexpr (PRO == 2) {
+    if constexpr (NORM_FIRST) {
         // the normalised row first: requested before any weight, its loads do not return behind
-        // this workgroup's weight stream (measured on the 22016 x 2048 gate|up with the FFN norm:
-        // 9.5 -> 8.9 us against building the row while the weights are in flight)
+        // this workgroup's weight stream (measured on the 22016 x 2048 gate|up with the FFN norm
+        // and 4-wave workgroups: 9.5 -> 8.9 us against building the row while the weights are in
+        // flight)
         arow.build(px, a.peps, a.P.n_in, lds_act);
         q8k_unit_lds(lds_act, a.P.nb, u, Yr, bsr, ydr);
     }
@@ -1118,10 +1147,10 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
     } else {
 #pragma unroll
         for (int k = 1; k < NIT; k++) load_k(k);
-        if constexpr (PRO == 1) {
+        if constexpr (PRO == 1 || (PRO == 2 && !NORM_FIRST)) {
             // the quantiser alone (no norm): every weight load goes out first and the workgroup
             // quantises the row while they are in flight (3B decode 637 -> 646 tok/s against building
-            // it first, with the 2048 x 2048 wo)
+            // it first, with the 2048 x 2048 wo); the same for the norm with 8-wave workgroups
             arow.build(px, a.peps, a.P.n_in, lds_act);
             q8k_unit_lds(lds_act, a.P.nb, u, Yr, bsr, ydr);
         }
@@ -1178,16 +1207,16 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
     }
 }
 
-template <int WT, int NIT, int NSB, int PRO>
-__global__ __launch_bounds__(THREADS) void k_matvec_1t(MvArgs a) {
-    matvec_1t_body<WT, NIT, NSB, PRO>(a, (int)gridDim.x, (int)blockIdx.x, (int)blockIdx.y);
+template <int WT, int NIT, int NSB, int PRO, int WV = WAVES>
+__global__ __launch_bounds__(64 * WV) void k_matvec_1t(MvArgs a) {
+    matvec_1t_body<WT, NIT, NSB, PRO, WV>(a, (int)gridDim.x, (int)blockIdx.x, (int)blockIdx.y);
 }
 
 // k_matvec_1t's pair form (see k_matvec_rl_pair), one iteration per wave
-template <int WT1, int WT2, int NSB, int PRO>
-__global__ __launch_bounds__(THREADS) void k_matvec_1t_pair(MvArgs a, MvArgs b, int g1) {
-    if ((int)blockIdx.x < g1) matvec_1t_body<WT1, 1, NSB, PRO>(a, g1, (int)blockIdx.x, 0);
-    else matvec_1t_body<WT2, 1, NSB, PRO>(b, (int)gridDim.x - g1, (int)blockIdx.x - g1, 0);
+template <int WT1, int WT2, int NSB, int PRO, int WV = WAVES>
+__global__ __launch_bounds__(64 * WV) void k_matvec_1t_pair(MvArgs a, MvArgs b, int g1) {
+    if ((int)blockIdx.x < g1) matvec_1t_body<WT1, 1, NSB, PRO, WV>(a, g1, (int)blockIdx.x, 0);
+    else matvec_1t_body<WT2, 1, NSB, PRO, WV>(b, (int)gridDim.x - g1, (int)blockIdx.x - g1, 0);
 }
 
 // The routed experts' down projections of one token and their combine in one launch. Workgroup of
@@ -2200,10 +2229,10 @@ static size_t mv_lds_bytes_rl(int T, int MT) { return (size_t)MT * 4 * T * 16 + 
 
 // Workgroups of a THREADS-thread kernel with `lds` bytes of dynamic LDS that the GPU holds at once
 // (the occupancy is cached per kernel and LDS size).
-static long resident_wgs(const void *fn, size_t lds, int &per_cu, size_t &per_cu_lds) {
+static long resident_wgs(const void *fn, size_t lds, int &per_cu, size_t &per_cu_lds, int threads = THREADS) {
     if (per_cu == 0 || per_cu_lds != lds) {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, THREADS, lds) != hipSuccess || n < 1) n = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess || n < 1) n = 1;
         per_cu = n;
         per_cu_lds = lds;
     }
@@ -2214,12 +2243,13 @@ static long resident_wgs(const void *fn, size_t lds, int &per_cu, size_t &per_cu
 static size_t pro_lds(const MvArgs &A) { return A.px ? (size_t)A.P.nb * 292 : 0; }
 static int pro_kind(const MvArgs &A) { return A.px ? (A.pnw ? 2 : 1) : 0; }
 
-template <int WT, int NIT, int NSB, int PRO>
+template <int WT, int NIT, int NSB, int PRO, int WV>
 static long cap_1t(size_t lds) {
     static int per_cu = 0;
     static size_t per_cu_lds = 0;
-    return resident_wgs((const void *)k_matvec_1t<WT, NIT, NSB, PRO>, lds, per_cu, per_cu_lds);
+    return resident_wgs((const void *)k_matvec_1t<WT, NIT, NSB, PRO, WV>, lds, per_cu, per_cu_lds, 64 * WV);
 }
+
 
 static void prep_1t(MvArgs &A) {
     A.rpi = 64 / A.P.T;
@@ -2231,24 +2261,24 @@ static void prep_1t(MvArgs &A) {
 // holds at once, so that every wave's loads go out at the start; 1 when no NIT fits (the caller
 // then runs the persistent k_matvec_rl).
 // (dry: report whether some NIT fits, launch nothing)
-template <int WT, int NSB, int PRO>
+template <int WT, int NSB, int PRO, int WV = WAVES>
 static int launch_mv_1t_nsb(MvArgs &A, hipStream_t st, int n_slot, bool dry) {
     const long n_it = A.n_it;
     const size_t lds = pro_lds(A);
-    auto wgs = [&](int nit) { return (n_it + (long)WAVES * nit - 1) / ((long)WAVES * nit); };
+    auto wgs = [&](int nit) { return (n_it + (long)WV * nit - 1) / ((long)WV * nit); };
 #define SDY_1T(NIT)                                                                                                  \
-    if (wgs(NIT) * n_slot <= cap_1t<WT, NIT, NSB, PRO>(lds)) {                                                       \
+    if (wgs(NIT) * n_slot <= cap_1t<WT, NIT, NSB, PRO, WV>(lds)) {                                                   \
         if (dry) return 0;                                                                                           \
-        SDY_NOTE_KERNEL((k_matvec_1t<WT, NIT, NSB, PRO>));                                                            \
-        hipLaunchKernelGGL((k_matvec_1t<WT, NIT, NSB, PRO>), dim3((unsigned)wgs(NIT), (unsigned)n_slot), dim3(THREADS), \
-                           lds, st, A);                                                                              \
+        SDY_NOTE_KERNEL((k_matvec_1t<WT, NIT, NSB, PRO, WV>));                                                        \
+        hipLaunchKernelGGL((k_matvec_1t<WT, NIT, NSB, PRO, WV>), dim3((unsigned)wgs(NIT), (unsigned)n_slot),           \
+                           dim3(64 * WV), lds, st, A);                                                               \
         return sdy_check_launch("matvec");                                                                           \
     }
     if (PRO || n_slot > 1) {
         // the workgroup-quantised row is built once per workgroup: fewer, fuller workgroups while
         // every CU still gets three (measured on the 22016 x 2048 gate|up: NIT 3); the same for the
         // grouped launches, counting every slot's workgroups
-        const long want = 3L * (g_n_cu ? g_n_cu : 256);
+        const long want = 3L * (g_n_cu ? g_n_cu : 256) * WAVES / WV;
         if (wgs(4) * n_slot >= want) { SDY_1T(4) }
         if (wgs(3) * n_slot >= want) { SDY_1T(3) }
         if (wgs(2) * n_slot >= want) { SDY_1T(2) }
@@ -2261,14 +2291,24 @@ static int launch_mv_1t_nsb(MvArgs &A, hipStream_t st, int n_slot, bool dry) {
     return 1;
 }
 
+template <int WT, int PRO, int WV = WAVES>
+static int launch_mv_1t_wv(MvArgs &A, hipStream_t st, int n_slot, bool dry) {
+    switch (A.P.T) {  // NSB: the row's super-block count when it is a common one (n_in 768, 2048, 4096)
+    case 12: return launch_mv_1t_nsb<WT, 3, PRO, WV>(A, st, n_slot, dry);
+    case 32: return launch_mv_1t_nsb<WT, 8, PRO, WV>(A, st, n_slot, dry);
+    case 64: return launch_mv_1t_nsb<WT, 16, PRO, WV>(A, st, n_slot, dry);
+    default: return launch_mv_1t_nsb<WT, 0, PRO, WV>(A, st, n_slot, dry);
+    }
+}
+
+// The RMS-normalised row (PRO 2) on 8-wave workgroups that build it while the weights stream: 3B
+// decode 682-685 against 674-676 tok/s with 4-wave workgroups building it before requesting them
+// (30B-A3B: 453 against 452). The quantiser alone (PRO 1) stays on 4 waves (8: 682-688 against
+// 687-690).
 template <int WT, int PRO>
 static int launch_mv_1t_pro(MvArgs &A, hipStream_t st, int n_slot, bool dry) {
-    switch (A.P.T) {  // NSB: the row's super-block count when it is a common one (n_in 768, 2048, 4096)
-    case 12: return launch_mv_1t_nsb<WT, 3, PRO>(A, st, n_slot, dry);
-    case 32: return launch_mv_1t_nsb<WT, 8, PRO>(A, st, n_slot, dry);
-    case 64: return launch_mv_1t_nsb<WT, 16, PRO>(A, st, n_slot, dry);
-    default: return launch_mv_1t_nsb<WT, 0, PRO>(A, st, n_slot, dry);
-    }
+    if constexpr (PRO == 2) return launch_mv_1t_wv<WT, PRO, 8>(A, st, n_slot, dry);
+    return launch_mv_1t_wv<WT, PRO>(A, st, n_slot, dry);
 }
 
 template <int WT>
@@ -2354,19 +2394,20 @@ static long rl_wgs(const MvArgs &A, int per_cu) {
     return wgs > cap ? cap : wgs;
 }
 
-template <int WT1, int WT2, int NSB, int PRO>
+template <int WT1, int WT2, int NSB, int PRO, int WV = WAVES>
 static int launch_mv_pair_1t(MvArgs &A, MvArgs &B, hipStream_t st, bool dry) {
     static int per_cu = 0;
     static size_t per_cu_lds = 0;
     const size_t lds = pro_lds(A);
-    const long cap = resident_wgs((const void *)k_matvec_1t_pair<WT1, WT2, NSB, PRO>, lds, per_cu, per_cu_lds);
-    auto wgs1 = [](const MvArgs &M) { return ((long)M.n_it + WAVES - 1) / WAVES; };
+    const long cap =
+        resident_wgs((const void *)k_matvec_1t_pair<WT1, WT2, NSB, PRO, WV>, lds, per_cu, per_cu_lds, 64 * WV);
+    auto wgs1 = [](const MvArgs &M) { return ((long)M.n_it + WV - 1) / WV; };
     const long g1 = (wgs1(A) + 7) / 8 * 8, g2 = wgs1(B);
     if (g1 + g2 > cap) return 1;
     if (dry) return 0;
-    SDY_NOTE_KERNEL((k_matvec_1t_pair<WT1, WT2, NSB, PRO>));
-    hipLaunchKernelGGL((k_matvec_1t_pair<WT1, WT2, NSB, PRO>), dim3((unsigned)(g1 + g2)), dim3(THREADS), lds, st, A, B,
-                       (int)g1);
+    SDY_NOTE_KERNEL((k_matvec_1t_pair<WT1, WT2, NSB, PRO, WV>));
+    hipLaunchKernelGGL((k_matvec_1t_pair<WT1, WT2, NSB, PRO, WV>), dim3((unsigned)(g1 + g2)), dim3(64 * WV), lds, st, A,
+                       B, (int)g1);
     return sdy_check_launch("matvec_pair");
 }
 
@@ -2375,8 +2416,9 @@ template <int WT1, int WT2, int PRO>
 static int launch_mv_pair_pro(MvArgs &A, MvArgs &B, hipStream_t st, bool dry = false) {
     prep_1t(A);
     prep_1t(B);
-    if (A.P.T == 32 && B.P.T == 32) return launch_mv_pair_1t<WT1, WT2, 8, PRO>(A, B, st, dry);  // 2048-element rows
-    return launch_mv_pair_1t<WT1, WT2, 0, PRO>(A, B, st, dry);
+    constexpr int WV = PRO == 2 ? 8 : WAVES;  // (as launch_mv_1t_pro)
+    if (A.P.T == 32 && B.P.T == 32) return launch_mv_pair_1t<WT1, WT2, 8, PRO, WV>(A, B, st, dry);  // 2048-element rows
+    return launch_mv_pair_1t<WT1, WT2, 0, PRO, WV>(A, B, st, dry);
 }
 
 template <int WT1, int WT2>
