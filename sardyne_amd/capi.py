@@ -174,6 +174,8 @@ _DEVICE_SIGNATURES = {
     "sdy_matvec_float_norm": (_int, [_int, _vp, _int, ctypes.POINTER(SdyMvArgs), _vp, _vp]),
     "sdy_matvec_grouped": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp, _int, ctypes.c_long,
                                   ctypes.c_long, ctypes.c_long, _vp]),
+    "sdy_matvec_grouped_route": (_int, [ctypes.POINTER(SdyMat), ctypes.POINTER(SdyMvArgs), _vp, _int, _int, _vp, _vp,
+                                        ctypes.c_long, ctypes.c_long, ctypes.c_long, _vp]),
     "sdy_mat_alloc": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long]),
     "sdy_mat_alloc_host": (_int, [ctypes.POINTER(SdyMat), _int, _int, ctypes.c_long]),
     "sdy_host_alloc_mapped": (_int, [ctypes.POINTER(_vp), ctypes.POINTER(_vp), _sz]),

@@ -446,7 +446,6 @@ static int moe_decode(engine_ctx *c, const dlayer *L) {
         TRY(norm_for(c, c->x, L->ffn_norm, first, 1)); /* xb and its Q8_K row */
         TRY(mm(c, c->moe_probs, c->xb, &L->gate_inp, 1, NULL, NULL, 0));
     }
-    TRY(sdy_moe_route(c->moe_probs, 1, ne, k, c->moe_top, c->moe_w, c->st));
     sdy_mv_args a;
     memset(&a, 0, sizeof a);
     a.n_tok = 1;
@@ -454,16 +453,29 @@ static int moe_decode(engine_ctx *c, const dlayer *L) {
     a.out = c->hb;
     a.out_stride = fe;
     a.row0 = 0;
-    if (L->gu_fused) {
+    /* gate|up selects its experts from the router's logits itself (writing moe_top / moe_w for down),
+       else the route kernel runs first */
+    int routed = 1;
+    if (L->gu_fused && c->fuse_act && ne <= 128) {
         a.row1 = 2 * fe;
         a.epilogue = SDY_EPI_SWIGLU;
-        TRY(sdy_matvec_grouped(&L->gate_up.m, &a, c->moe_top, k, 2L * fe, 0, fe, c->st));
-    } else {
-        a.row1 = fe;
-        TRY(sdy_matvec_grouped(&L->gate.m, &a, c->moe_top, k, fe, 0, fe, c->st));
-        a.out = c->hb2;
-        TRY(sdy_matvec_grouped(&L->up.m, &a, c->moe_top, k, fe, 0, fe, c->st));
-        TRY(sdy_silu_mul(c->hb, c->hb2, (long)k * fe, c->st));
+        routed = sdy_matvec_grouped_route(&L->gate_up.m, &a, c->moe_probs, ne, k, c->moe_top, c->moe_w, 2L * fe, 0,
+                                          fe, c->st);
+        if (routed < 0) return routed;
+    }
+    if (routed) {
+        TRY(sdy_moe_route(c->moe_probs, 1, ne, k, c->moe_top, c->moe_w, c->st));
+        if (L->gu_fused) {
+            a.row1 = 2 * fe;
+            a.epilogue = SDY_EPI_SWIGLU;
+            TRY(sdy_matvec_grouped(&L->gate_up.m, &a, c->moe_top, k, 2L * fe, 0, fe, c->st));
+        } else {
+            a.row1 = fe;
+            TRY(sdy_matvec_grouped(&L->gate.m, &a, c->moe_top, k, fe, 0, fe, c->st));
+            a.out = c->hb2;
+            TRY(sdy_matvec_grouped(&L->up.m, &a, c->moe_top, k, fe, 0, fe, c->st));
+            TRY(sdy_silu_mul(c->hb, c->hb2, (long)k * fe, c->st));
+        }
     }
     /* down over the k SwiGLU rows: each slot's workgroups quantise its row themselves, or (when that
        is not available) the rows are quantised first (the Q8_K row of xb is no longer needed) */

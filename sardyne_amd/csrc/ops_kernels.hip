@@ -11,6 +11,7 @@
 #include "sdy_internal.h"
 #include "sdy_norm_dev.h"
 #include "sdy_ops.h"
+#include "sdy_route_dev.h"
 #include "sdy_shim.h"
 
 namespace {
@@ -129,102 +130,16 @@ __global__ void k_rope(float *x, int n_heads, int hd, const float *cs, const flo
 // ---------------------------------------------------------------------------------- MoE router
 // One wave per token: softmax over the expert logits (max, expf, double sum, float reciprocal),
 // then top-k by repeated arg-max with ties to the lower index (the order moe_select produces,
-// csrc/model_llama.c:653-666) and weights renormalised by their sequential float sum.
-// The maximum of a 32-bit value over the wave, in every lane: DPP within rows of 16 lanes (quad
-// perms, row rotations), then the four rows' maxima by readlane.
-SDY_DEV uint32_t wave_max_u32(uint32_t v) {
-    uint32_t o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
-    v = o > v ? o : v;
-    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
-    v = o > v ? o : v;
-    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, false);  // row_ror 4
-    v = o > v ? o : v;
-    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);  // row_ror 8
-    v = o > v ? o : v;
-    uint32_t r = 0;
-#pragma unroll
-    for (int row = 0; row < 4; row++) {
-        const uint32_t x = (uint32_t)__builtin_amdgcn_readlane((int)v, 16 * row);
-        r = x > r ? x : r;
-    }
-    return r;
-}
-
-SDY_DEV float wave_max_f32(float v) {
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false)));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false)));
-    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
-
+// csrc/model_llama.c:653-666) and weights renormalised by their sequential float sum
+// (sdy_moe_route_wave).
 template <int NPL>  // experts held per lane: n_expert <= 64 * NPL
 __global__ __launch_bounds__(64) void k_moe_route(const float *logits, int n_expert, int k, int32_t *top,
                                                   float *wts) {
     const int t = blockIdx.x, lane = threadIdx.x;
-    const float *p = logits + (size_t)t * n_expert;
     const uint32_t etab = sdy_expf_tab_lane(lane);  // the exponential's table, loaded with the logits
-    float v[NPL];
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < NPL; j++) {
-        const int e = lane + 64 * j;
-        v[j] = e < n_expert ? p[e] : -INFINITY;
-        m = fmaxf(m, v[j]);
-    }
-    m = wave_max_f32(m);  // (a maximum: the same value in any order)
-    // op_softmax (csrc/ops.c:353-364): expf(x - max) (the host libm's expf, bit for bit), the sum
-    // in double, times (float)(1 / sum). The probabilities stay in registers; -1 marks lanes past
-    // n_expert (never chosen).
-    double s = 0.0;
-#pragma unroll
-    for (int j = 0; j < NPL; j++) {
-        v[j] = sdy_expf_reg(v[j] - m, etab);  // every lane (the table lookup reads other lanes): 0 past n_expert
-        if (lane + 64 * j < n_expert) s += (double)v[j];
-    }
-    s = sdy_wave_sum_f64(s);  // the butterfly over lane ^ 32, 16, ..., 1
-    const float inv = (float)(1.0 / s);
-#pragma unroll
-    for (int j = 0; j < NPL; j++) v[j] = lane + 64 * j < n_expert ? v[j] * inv : -1.0f;
-    // moe_select (csrc/model_llama.c:653-666): k times the largest remaining probability, ties to
-    // the lowest expert; chosen ones are marked -2. The weights divide by the sum of the chosen
-    // probabilities taken in rank order.
-    // Each round's arg-max: the wave maximum of a 32-bit key, the probability's bits plus one
-    // (probabilities are >= 0, so their bits order as unsigned; the -1 / -2 marks map to 0), through
-    // DPP within rows of 16 lanes and readlane across the four rows (no LDS round trip); then the
-    // lowest expert id holding it from ballots (the lower id wins a tie).
-    float chosen_sum = 0.0f, my_p = 0.0f;
-    int my_e = 0;
-    for (int i = 0; i < k; i++) {
-        // the largest key (the probability's bits plus one; 0 for the marks) over the wave, then the
-        // lowest expert holding it: the first slot j whose ballot has a lane, its lowest lane
-        uint32_t hk[NPL], key = 0;
-#pragma unroll
-        for (int j = 0; j < NPL; j++) {
-            hk[j] = v[j] >= 0.0f ? __float_as_uint(fabsf(v[j])) + 1u : 0u;
-            key = hk[j] > key ? hk[j] : key;
-        }
-        key = wave_max_u32(key);
-        int bi = -1;
-#pragma unroll
-        for (int j = NPL - 1; j >= 0; j--) {
-            const uint64_t bal = __ballot(hk[j] == key);
-            if (bal) bi = 64 * j + (int)__builtin_ctzll(bal);
-        }
-        const float best = __uint_as_float(key - 1u);
-#pragma unroll
-        for (int j = 0; j < NPL; j++)
-            if (bi == lane + 64 * j) v[j] = -2.0f;
-        if (lane == i) {
-            my_p = best;
-            my_e = bi;
-        }
-        chosen_sum = chosen_sum + best;
-    }
+    int my_e;
+    float my_p, chosen_sum;
+    sdy_moe_route_wave<NPL>(logits + (size_t)t * n_expert, n_expert, k, lane, etab, my_e, my_p, chosen_sum);
     if (lane < k) {
         top[(size_t)t * k + lane] = my_e;
         wts[(size_t)t * k + lane] = my_p / chosen_sum;

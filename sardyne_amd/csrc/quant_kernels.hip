@@ -31,6 +31,7 @@
 #include "sdy_internal.h"
 #include "sdy_quant_dev.h"
 #include "sdy_norm_dev.h"
+#include "sdy_route_dev.h"
 
 namespace {
 
@@ -346,6 +347,12 @@ struct MvArgs {
     const float *px, *pnw;
     float peps;
     long px_slot;
+    // a grouped launch that selects its experts itself: the router's route_ne logits of the token,
+    // route_k choices; the choices and their weights are written to route_top / route_wts
+    const float *route_logits;
+    int route_ne, route_k;
+    int32_t *route_top;
+    float *route_wts;
 };
 
 constexpr bool is_k(int wt) { return wt == SDY_Q4_K || wt == SDY_Q6_K; }
@@ -1060,6 +1067,22 @@ SDY_DEV float rl_row_sum(const WRegs<WT> &cur, const uint4 (&Yr)[4], uint2 bsr, 
     else return rl_fold<16>(term, lane, T >> 2);
 }
 
+// A grouped one-token matvec that routes its token itself (k_matvec_1t with PRO 3): one wave of each
+// workgroup runs the router's softmax and top-k over the route_ne logits (the bits of k_moe_route,
+// at most 128 experts) and takes slot `slot`'s expert; the writer wave (one in the grid) stores the
+// route_k choices and their weights for the kernels that follow.
+SDY_DEV int routed_expert(const MvArgs &a, int slot, int lane, bool writer) {
+    int my_e;
+    float my_p, chosen_sum;
+    sdy_moe_route_wave<2>(a.route_logits, a.route_ne, a.route_k, lane, sdy_expf_tab_lane(lane), my_e, my_p,
+                          chosen_sum);
+    if (writer && lane < a.route_k) {
+        a.route_top[lane] = my_e;
+        a.route_wts[lane] = my_p / chosen_sum;
+    }
+    return __builtin_amdgcn_readlane(my_e, slot);
+}
+
 // One token, K-quants with at most 64 units per row (every one-token matvec of a decode step but
 // the output head): wave w of the S waves of the grid takes the NIT iterations w, w + S, ...,
 // w + (NIT - 1) S of 64/T rows each, and issues every load it needs (the weights of all its
@@ -1068,7 +1091,8 @@ SDY_DEV float rl_row_sum(const WRegs<WT> &cur, const uint4 (&Yr)[4], uint2 bsr, 
 // Same lane layout and arithmetic as k_matvec_rl, so the bits are the same.
 // (the body of k_matvec_1t for workgroup bx of a grid of G, routed-expert slot `slot`)
 // PRO: 0 the Q8_K row a.xq in memory, 1 the f32 row a.px quantised by the workgroup (into LDS),
-// 2 a.px RMS-normalised with a.pnw, then quantised.
+// 2 a.px RMS-normalised with a.pnw, then quantised; 3 as 0 in a grouped launch whose workgroups
+// select their slot's expert from the router's logits (routed_expert).
 // WV waves per workgroup: 4, or 8 for the RMS-normalised row (PRO 2), whose row is then built after
 // the weights are requested (with 4 it is built before them; its sum of squares keeps the 256-thread
 // order either way).
@@ -1076,35 +1100,51 @@ template <int WT, int NIT, int NSB, int PRO = 0, int WV = WAVES>
 SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
     // super-blocks per wave of the workgroup's activation row (n_in 768: 3, 2048: 8, else up to 16)
     constexpr int PRO_NR = WV == 4 ? (NSB == 3 ? 1 : NSB == 8 ? 2 : 4) : (NSB == 3 || NSB == 8 ? 1 : 2);
-    constexpr bool NORM_FIRST = PRO == 2 && WV == 4;  // the normalised row built before the weight loads
+    constexpr bool ROUTE = PRO == 3;
+    constexpr int PK = ROUTE ? 0 : PRO;  // the activation row's kind
+    constexpr bool NORM_FIRST = PK == 2 && WV == 4;  // the normalised row built before the weight loads
     const int T = a.P.T;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int rpi = a.rpi;
     const int rl_ = __mul24(lane, a.tmag) >> 16, u = lane - __mul24(rl_, T);
     const bool lane_on = rl_ < rpi;
     const int rl = lane_on ? rl_ : 0;
+    const int vblk = (G & 7) == 0 ? (bx & 7) * (G >> 3) + (bx >> 3) : bx;  // XCD-aware renumbering
+    const int S = G * WV, wid = vblk * WV + wave;
+    int e_routed = 0;
+    if constexpr (ROUTE) {
+        // wave 0 routes the token and hands its slot's expert to the workgroup (before any wave
+        // leaves: the barrier counts them all); one wave per workgroup reading the logits instead of
+        // every wave: 30B-A3B decode 465-467 against 461-463 tok/s
+        __shared__ int sh_e;
+        if (wave == 0) {
+            const int e0 = routed_expert(a, slot, lane, bx == 0 && slot == 0);
+            if (lane == 0) sh_e = e0;
+        }
+        __syncthreads();
+        e_routed = __builtin_amdgcn_readfirstlane(sh_e);
+    }
+    if constexpr (PK == 0) {
+        if (wid >= a.n_it) return;
+    }
     long poff = 0;
     const uint8_t *xq = a.xq;
     float *out = a.out;
     if (a.slot_expert) {
-        int e = a.slot_expert[slot];
+        int e;
+        if constexpr (ROUTE) e = e_routed;
+        else e = a.slot_expert[slot];
         e = e < 0 ? 0 : (e >= a.n_slot_exp ? a.n_slot_exp - 1 : e);
         poff = (long)e * a.slot_rows;
         xq += (size_t)slot * a.xq_slot;
         out += (size_t)slot * a.out_slot;
     }
-    const int vblk = (G & 7) == 0 ? (bx & 7) * (G >> 3) + (bx >> 3) : bx;  // XCD-aware renumbering
-    const int S = G * WV, wid = vblk * WV + wave;
     extern __shared__ uint8_t lds_act[];
-    Q8kRow<PRO == 2, PRO_NR, WV> arow;
-    const float *px = a.px + (PRO ? (size_t)slot * a.px_slot : 0);
+    Q8kRow<PK == 2, PRO_NR, WV> arow;
+    const float *px = a.px + (PK ? (size_t)slot * a.px_slot : 0);
     // (with PRO, waves past the rows still take part in the workgroup's activation row: their rows
     // are all >= row1, so they load row0 and store nothing)
-    if constexpr (PRO == 0) {
-        if (wid >= a.n_it) return;
-    } else {
-        arow.issue(px, a.pnw, a.P.n_in);
-    }
+    if constexpr (PK != 0) arow.issue(px, a.pnw, a.P.n_in);
     // load order: the first iteration's weights, the activations, the bias and residual, then the
     // other iterations' weights, so that iteration k waits only for the loads it uses (every load
     // is unconditional, which keeps the compiler's wait counts exact)
@@ -1136,7 +1176,7 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
     }
     load_k(0);
     const uint32_t etab = sdy_expf_tab_lane(lane);  // the SwiGLU epilogue's exponential table
-    if constexpr (PRO == 0) {
+    if constexpr (PK == 0) {
         const uint8_t *blk = xq + __mul24(u >> 2, 292);
         const uint8_t *yb = blk + 4 + 64 * (u & 3);
 #pragma unroll
@@ -1147,7 +1187,7 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
     } else {
 #pragma unroll
         for (int k = 1; k < NIT; k++) load_k(k);
-        if constexpr (PRO == 1 || (PRO == 2 && !NORM_FIRST)) {
+        if constexpr (PK == 1 || (PK == 2 && !NORM_FIRST)) {
             // the quantiser alone (no norm): every weight load goes out first and the workgroup
             // quantises the row while they are in flight (3B decode 637 -> 646 tok/s against building
             // it first, with the 2048 x 2048 wo); the same for the norm with 8-wave workgroups
@@ -1156,7 +1196,7 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
         }
     }
     // the bias and residual of the lane's rows (an absent one reads a stand-in: the activation row)
-    const float *stand_in = PRO ? px : reinterpret_cast<const float *>(xq);
+    const float *stand_in = PK ? px : reinterpret_cast<const float *>(xq);
     const float *bsrc = a.bias ? a.bias : stand_in;
     const float *rsrc = a.resid ? a.resid : stand_in;
     float bv[NIT], rv[NIT];
@@ -1166,7 +1206,7 @@ SDY_DEV void matvec_1t_body(const MvArgs &a, int G, int bx, int slot) {
         bv[k] = bsrc[a.bias ? rc : 0];
         rv[k] = rsrc[a.resid ? rc : 0];
     }
-    if constexpr (PRO == 0) {
+    if constexpr (PK == 0) {
 #pragma unroll
         for (int k = 1; k < NIT; k++) load_k(k);
     }
@@ -2241,7 +2281,7 @@ static long resident_wgs(const void *fn, size_t lds, int &per_cu, size_t &per_cu
 
 // LDS of the workgroup-quantised activation row (q8k_row_lds): 0 when the kernel reads a.xq
 static size_t pro_lds(const MvArgs &A) { return A.px ? (size_t)A.P.nb * 292 : 0; }
-static int pro_kind(const MvArgs &A) { return A.px ? (A.pnw ? 2 : 1) : 0; }
+static int pro_kind(const MvArgs &A) { return A.px ? (A.pnw ? 2 : 1) : A.route_logits ? 3 : 0; }
 
 template <int WT, int NIT, int NSB, int PRO, int WV>
 static long cap_1t(size_t lds) {
@@ -2317,6 +2357,7 @@ static int launch_mv_1t(MvArgs &A, hipStream_t st, int n_slot, bool dry = false)
     switch (pro_kind(A)) {
     case 1: return launch_mv_1t_pro<WT, 1>(A, st, n_slot, dry);
     case 2: return launch_mv_1t_pro<WT, 2>(A, st, n_slot, dry);
+    case 3: return launch_mv_1t_pro<WT, 3>(A, st, n_slot, dry);
     default: return launch_mv_1t_pro<WT, 0>(A, st, n_slot, dry);
     }
 }
@@ -2712,9 +2753,8 @@ extern "C" int sdy_matvec(const sdy_mat *m, const sdy_mv_args *a, sdy_stream s) 
     }
 }
 
-template <int WT>
-static int mv_grouped(const sdy_mat *m, const sdy_mv_args *a, const int32_t *slot_expert, int n_slot, long slot_rows,
-                      long xq_slot, long out_slot, hipStream_t st, bool dry = false) {
+static MvArgs grouped_args(const sdy_mat *m, const sdy_mv_args *a, const int32_t *slot_expert, long slot_rows,
+                           long xq_slot, long out_slot) {
     MvArgs A = {};
     A.P = planes_of(m);
     A.xq = (const uint8_t *)a->xq;
@@ -2729,6 +2769,13 @@ static int mv_grouped(const sdy_mat *m, const sdy_mv_args *a, const int32_t *slo
     A.n_slot_exp = (int)(m->n_rows / slot_rows);
     A.xq_slot = xq_slot;
     A.out_slot = out_slot;
+    return A;
+}
+
+template <int WT>
+static int mv_grouped(const sdy_mat *m, const sdy_mv_args *a, const int32_t *slot_expert, int n_slot, long slot_rows,
+                      long xq_slot, long out_slot, hipStream_t st, bool dry = false) {
+    MvArgs A = grouped_args(m, a, slot_expert, slot_rows, xq_slot, out_slot);
     if (!a->xq) {  // the workgroups quantise their slot's f32 row (a->x + slot * xq_slot floats)
         A.xq_slot = 0;
         A.px = a->x;
@@ -2786,6 +2833,35 @@ extern "C" int sdy_matvec_grouped(const sdy_mat *m, const sdy_mv_args *a, const 
     }
     if (m->type == SDY_Q4_K) return mv_grouped<SDY_Q4_K>(m, a, slot_expert, n_slot, slot_rows, xq_slot, out_slot, st);
     return mv_grouped<SDY_Q6_K>(m, a, slot_expert, n_slot, slot_rows, xq_slot, out_slot, st);
+}
+
+// sdy_matvec_grouped over the k slots of one token whose experts the kernel selects itself from
+// the router's n_expert logits (softmax, top k, renormalised weights: the bits of sdy_moe_route,
+// which it also writes to top and wts), saving the route launch. The Q8_K row in memory (a->xq),
+// n_expert <= 128, k <= 64. Returns 1, launching nothing, when no one-token grid fits: the caller
+// then runs sdy_moe_route and sdy_matvec_grouped.
+extern "C" int sdy_matvec_grouped_route(const sdy_mat *m, const sdy_mv_args *a, const float *logits, int n_expert,
+                                        int k, int32_t *top, float *wts, long slot_rows, long xq_slot, long out_slot,
+                                        sdy_stream s) {
+    int rc = grouped_check(m, a, k, slot_rows, xq_slot);
+    if (rc) return rc;
+    if (!a->xq) return sdy_fail(-1, "routed grouped matvec: needs the Q8_K row (xq)");
+    if (!logits || !top || !wts || n_expert < 1 || n_expert > 128 || k < 1 || k > 64 || k > n_expert)
+        return sdy_fail(-1, "routed grouped matvec: %d of %d experts (at most 64 of 128), logits and outputs set", k,
+                        n_expert);
+    if (m->n_rows / slot_rows < n_expert)
+        return sdy_fail(-1, "routed grouped matvec: a stack of %ld experts for %d logits", m->n_rows / slot_rows,
+                        n_expert);
+    if (a->row0 == a->row1) return 1;  // no workgroup would write the choices
+    ensure_n_cu();
+    MvArgs A = grouped_args(m, a, top, slot_rows, xq_slot, out_slot);
+    A.route_logits = logits;
+    A.route_ne = n_expert;
+    A.route_k = k;
+    A.route_top = top;
+    A.route_wts = wts;
+    hipStream_t st = (hipStream_t)s;
+    return m->type == SDY_Q4_K ? launch_mv_1t<SDY_Q4_K>(A, st, k) : launch_mv_1t<SDY_Q6_K>(A, st, k);
 }
 
 // The routed experts' down projections of one token (the k slots' f32 rows x, n_in apart, through

@@ -169,6 +169,12 @@ int sdy_matvec_pair(const sdy_mat *m1, const sdy_mv_args *a1, const sdy_mat *m2,
  * rows of at most 4096 elements; the SwiGLU epilogue as in sdy_matvec. */
 int sdy_matvec_grouped(const sdy_mat *m, const sdy_mv_args *a, const int32_t *slot_expert, int n_slot,
                        long slot_rows, long xq_slot, long out_slot, sdy_stream s);
+/* sdy_matvec_grouped over the k slots of one token whose experts the kernel selects from the
+ * router's n_expert <= 128 logits (device array): the choices and weights of sdy_moe_route, which it
+ * also writes to top and wts (k entries each), so no route launch precedes it. The Q8_K row in memory
+ * (a->xq), k <= 64. Returns 1, launching nothing, when no one-token grid fits. */
+int sdy_matvec_grouped_route(const sdy_mat *m, const sdy_mv_args *a, const float *logits, int n_expert, int k,
+                             int32_t *top, float *wts, long slot_rows, long xq_slot, long out_slot, sdy_stream s);
 /* 1 when sdy_matvec_grouped can quantise each slot's f32 row itself (a->xq = NULL, a->x set; slot s's
  * row at a->x + s * x_slot floats, passed as xq_slot; RMS-normalised first when a->nw is set) */
 int sdy_matvec_grouped_fused_ok(const sdy_mat *m, const sdy_mv_args *a, int n_slot, long slot_rows, long x_slot);

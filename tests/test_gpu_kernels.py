@@ -624,6 +624,63 @@ def test_grouped_matvec(kind, n_in, e_rows, swiglu, rows):
             np.testing.assert_allclose(got[s], g, rtol=1e-5, atol=1e-5 * float(np.abs(g).max()))
 
 
+@pytest.mark.parametrize("kind,n_in,e_rows,swiglu,n_exp,k,case", [
+    ("Q4_K", 2048, 96, True, 128, 8, "normal"), ("Q4_K", 2048, 96, True, 128, 8, "ties"),
+    ("Q4_K", 2048, 64, True, 128, 16, "equal"), ("Q6_K", 768, 40, False, 60, 4, "normal"),
+    ("Q6_K", 256, 24, True, 8, 8, "ties"), ("Q4_K", 4096, 32, False, 100, 64, "normal")])
+def test_grouped_matvec_routes_itself(kind, n_in, e_rows, swiglu, n_exp, k, case):
+    """The grouped matvec that selects its experts from the router's logits: its choices and weights
+    are sdy_moe_route's bit for bit (exact ties, all-equal logits: the lowest experts), and its
+    outputs are sdy_matvec_grouped's on those choices."""
+    t = TYPES[kind]
+    L = lib()
+    rng = np.random.default_rng(n_in + n_exp + k)
+    w = random_blocks(kind, n_exp * e_rows * n_in // 256, rng).reshape(n_exp * e_rows, -1)
+    x = rng.standard_normal((1, n_in)).astype(np.float32)
+    xq = O.quantize(x, O.Q8_K)
+    logits = (rng.standard_normal(n_exp) * 2).astype(np.float32)
+    if case == "ties":
+        logits[1:n_exp:3] = logits.max()
+    elif case == "equal":
+        logits[:] = -0.25
+    n_out = e_rows // 2 if swiglu else e_rows
+    epi = capi.EPI_SWIGLU if swiglu else capi.EPI_NONE
+    m = capi.DeviceMatrix(t, n_in, n_exp * e_rows, w)
+    dq, dl = capi.DeviceBuffer.from_array(xq), capi.DeviceBuffer.from_array(logits)
+    outs = []
+    for routed in (False, True):
+        dtop = capi.DeviceBuffer.from_array(np.full(k, -7, np.int32))
+        dw = capi.DeviceBuffer.from_array(np.full(k, np.nan, np.float32))
+        dout = capi.DeviceBuffer.from_array(np.full((k, n_out), np.nan, np.float32))
+        a = capi.SdyMvArgs(xq=dq.ptr, n_tok=1, out=dout.ptr, out_stride=n_out, row0=0, row1=e_rows, epilogue=epi)
+        if routed:
+            capi.check(L.sdy_matvec_grouped_route(ctypes.byref(m.m), ctypes.byref(a), dl.ptr, n_exp, k, dtop.ptr, dw.ptr,
+                                                  e_rows, 0, n_out, None))
+        else:
+            capi.check(L.sdy_moe_route(dl.ptr, 1, n_exp, k, dtop.ptr, dw.ptr, None))
+            capi.check(L.sdy_matvec_grouped(ctypes.byref(m.m), ctypes.byref(a), dtop.ptr, k, e_rows, 0, n_out, None))
+        outs.append((dtop.to_array(np.int32, k), dw.to_array(np.float32, k), dout.to_array(np.float32, (k, n_out))))
+    (t0, w0, y0), (t1, w1, y1) = outs
+    assert t1.tolist() == t0.tolist()
+    assert np.array_equal(bits(w1), bits(w0)) and np.array_equal(bits(y1), bits(y0))
+    p = logits.copy()
+    O.lib().orc_softmax(ptr(p), n_exp)
+    assert t1.tolist() == np.argsort(-p, kind="stable")[:k].tolist()
+    if case == "equal":
+        assert t1.tolist() == list(range(k))
+    assert not np.isnan(y1).any()
+    # the checks of the entry point: more than 128 experts, more than 64 choices, no Q8_K row
+    a = capi.SdyMvArgs(xq=dq.ptr, n_tok=1, out=dout.ptr, out_stride=n_out, row0=0, row1=e_rows, epilogue=epi)
+    assert L.sdy_matvec_grouped_route(ctypes.byref(m.m), ctypes.byref(a), dl.ptr, 129, k, dtop.ptr, dw.ptr, e_rows, 0,
+                                      n_out, None) < 0
+    assert L.sdy_matvec_grouped_route(ctypes.byref(m.m), ctypes.byref(a), dl.ptr, n_exp, 65, dtop.ptr, dw.ptr, e_rows,
+                                      0, n_out, None) < 0
+    a.xq = None
+    a.x = dq.ptr
+    assert L.sdy_matvec_grouped_route(ctypes.byref(m.m), ctypes.byref(a), dl.ptr, n_exp, k, dtop.ptr, dw.ptr, e_rows, 0,
+                                      n_out, None) < 0
+
+
 @pytest.mark.parametrize("kind,n_in,e_rows,mode", [
     ("Q6_K", 768, 2048, "quant"), ("Q4_K", 2048, 1536, "norm_swiglu"), ("Q4_K", 1024, 300, "quant"),
     ("Q6_K", 2048, 96, "norm")])
