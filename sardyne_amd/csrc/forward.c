@@ -456,7 +456,7 @@ static int moe_decode(engine_ctx *c, const dlayer *L) {
     /* gate|up selects its experts from the router's logits itself (writing moe_top / moe_w for down),
        else the route kernel runs first */
     int routed = 1;
-    if (L->gu_fused && c->fuse_act && ne <= 128) {
+    if (L->gu_fused && c->fuse_act && ne <= 128 && k <= 64) {
         a.row1 = 2 * fe;
         a.epilogue = SDY_EPI_SWIGLU;
         routed = sdy_matvec_grouped_route(&L->gate_up.m, &a, c->moe_probs, ne, k, c->moe_top, c->moe_w, 2L * fe, 0,

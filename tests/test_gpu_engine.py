@@ -64,6 +64,12 @@ SPECS = {
     "moe-128x8": ModelSpec(arch="qwen3moe", n_vocab=300, dim=256, n_layer=2, n_head=4, n_kv_head=2, head_dim=64,
                            ffn_dim=2048, context=64, n_expert=128, n_expert_used=8, ffn_exp_dim=256, qkv_bias=False,
                            qk_norm=True, router_std=0.3),
+    # more experts than the routed gate|up selects itself (128): the decode routes in its own launch.
+    # (With 160 experts and these seeds token 5 of TOKENS has two nearly tied experts, which the
+    # reference's own AVX2 and scalar engines order differently.)
+    "moe-192x6": ModelSpec(arch="qwen3moe", n_vocab=300, dim=256, n_layer=2, n_head=4, n_kv_head=2, head_dim=64,
+                           ffn_dim=2048, context=64, n_expert=192, n_expert_used=6, ffn_exp_dim=256, qkv_bias=False,
+                           qk_norm=True, router_std=0.3),
 }
 
 
@@ -222,7 +228,7 @@ def test_decode_paths_bit_identical(model_path):
     assert_close(fused_graph, np.stack(exp))
 
 
-KQUANT_SPECS = ["qwen2-kquant", "llama-kquant", "qwen2-gqa8-hd128", "moe-128x8", "moe-16x4-ffn768",
+KQUANT_SPECS = ["qwen2-kquant", "llama-kquant", "qwen2-gqa8-hd128", "moe-128x8", "moe-16x4-ffn768", "moe-192x6",
                 "qwen2-kquant-v4k", "qwen2-kquant-vmix"]
 
 
