@@ -20,7 +20,10 @@ The models are written to /dev/shm (2.2 GB and 19.8 GB) and deleted afterwards.
 """
 import ctypes
 import hashlib
+import json
 import os
+import subprocess
+import sys
 import tempfile
 from pathlib import Path
 
@@ -35,7 +38,8 @@ from sardyne_amd.gguf_synth import qwen25_3b, qwen3_30b_a3b, random_blocks, writ
 
 pytestmark = pytest.mark.gpu
 
-GOLDEN = Path(__file__).resolve().parent / "golden"
+TESTS = Path(__file__).resolve().parent
+GOLDEN = TESTS / "golden"
 needs_ref = pytest.mark.skipif(not O.ref_available(), reason="the reference compiled into oracle/_ref is missing")
 
 
@@ -156,32 +160,59 @@ def fill_device_to(room):
     return ballast
 
 
-def test_c3_loads_under_memory_pressure(qwen25_3b_path):
+def _pressure_child(path, room, toks_path, env, out_path):
+    """The pressured load of a memory-pressure test, run in a process of its own: a ballast leaves
+    `room` bytes free, then the model is loaded with the engine switches `env` (JSON) and fed the
+    512-token prompt and one-token steps of toks_path; its logits and memory figures go to out_path.
+    A fresh process because the runtime keeps device memory freed by earlier loads for its own
+    reuse and reports it as used: a ballast sized in the same process leaves the next load more room
+    than it measures."""
+    L = capi.lib()
+    capi.check(L.sdy_init())
+    toks = np.load(toks_path)
+    ballast = fill_device_to(int(room))
+    with engine_env(**json.loads(env)):
+        model = LoadedModel(path)
+        s = model.session(max_seq=640, n_batch=512)
+    out = np.stack([s.feed(toks[:512])] + [s.step(int(t)) for t in toks[512:]])
+    np.savez(out_path, logits=out, **{k: np.int64(v) for k, v in model.memory().items()})
+    del s, model, ballast
+
+
+def run_pressured(path, room, toks, env, tmp):
+    """_pressure_child in a child process; returns its logits and memory figures."""
+    tp, op = Path(tmp) / "toks.npy", Path(tmp) / "pressured.npz"
+    np.save(tp, toks)
+    # (conftest puts the repository and the oracle's module directory on the path, as under pytest)
+    code = ("import sys; sys.path.insert(0, sys.argv[1]); import conftest; import test_gpu_configs as t; "
+            "t._pressure_child(*sys.argv[2:])")
+    r = subprocess.run([sys.executable, "-c", code, str(TESTS), str(path), str(room), str(tp), json.dumps(env),
+                        str(op)], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, (r.returncode, r.stdout[-3000:], r.stderr[-3000:])
+    d = np.load(op)
+    return d["logits"], {k: int(d[k]) for k in d.files if k != "logits"}
+
+
+def test_c3_loads_under_memory_pressure(qwen25_3b_path, tmp_path):
     """The Qwen2.5-3B-shaped model on a device with little room: a ballast allocation leaves free only
     the weights, half of the prefill GEMM's tiled copies and 512 MiB, so the weights are more than
     half of the memory left to the model. It loads, the copies are made for what fits (a 256 MiB
     reserve), and the 512-token prompt on the GEMM and two decode steps give the logits bits of the
-    load with every copy (the exact attention chain in both)."""
+    load with every copy (the exact attention chain in both; the pressured load in a process of
+    its own, _pressure_child)."""
     L = capi.lib()
     capi.check(L.sdy_init())
     toks = np.random.default_rng(3).integers(0, 151936, 514).astype(np.int32)
-
-    def run():
-        with engine_env(SARDYNE_ATTENTION="exact", SARDYNE_GEMM_RESERVE_MB="256"):
-            model = LoadedModel(qwen25_3b_path)
-            s = model.session(max_seq=640, n_batch=512)
-        out = np.stack([s.feed(toks[:512]), s.step(int(toks[512])), s.step(int(toks[513]))])
-        return out, model.memory()
-
-    base, mem = run()
+    env = {"SARDYNE_ATTENTION": "exact", "SARDYNE_GEMM_RESERVE_MB": "256"}
+    with engine_env(**env):
+        model = LoadedModel(qwen25_3b_path)
+        s = model.session(max_seq=640, n_batch=512)
+    base = np.stack([s.feed(toks[:512]), s.step(int(toks[512])), s.step(int(toks[513]))])
+    mem = model.memory()
+    del s, model
     assert mem["gemm_copies"] > 0 and mem["gemm_copies_skipped"] == 0
     room = mem["weight_bytes"] + mem["gemm_copy_bytes"] // 2 + (512 << 20)
-    ballast = fill_device_to(room)
-    try:
-        got, mem2 = run()
-    finally:
-        for b in ballast:
-            b.close()
+    got, mem2 = run_pressured(qwen25_3b_path, room, toks, env, tmp_path)
     assert mem2["weight_bytes"] == mem["weight_bytes"] and mem2["weight_bytes"] > room // 2
     assert mem2["gemm_copies_skipped"] > 0 and 0 < mem2["gemm_copy_bytes"] < mem["gemm_copy_bytes"]
     assert np.all(np.isfinite(base))
@@ -220,34 +251,28 @@ def test_c5_qwen3_30b_a3b_context_1024_then_decode(qwen3_30b_a3b_path):
     _run_and_compare(qwen3_30b_a3b_path, 1024, 512, 5, 1152, seed=1, tol=c5_tolerance())
 
 
-def test_c5_experts_beyond_the_device_memory(qwen3_30b_a3b_path):
+def test_c5_experts_beyond_the_device_memory(qwen3_30b_a3b_path, tmp_path):
     """The Qwen3-30B-A3B-shaped model on a device that holds about half of its expert stacks: a
     ballast allocation leaves free the attention and embedding weights, half the experts and a
     2 GiB reserve. The loader places each layer's experts on the device while the reserve stays
     free and the rest in pinned host memory, which the grouped GEMM and the device-routed decode
     read in place; a 512-token prompt and three decode steps give the logits bits of the load with
-    every expert on the device (the exact attention chain in both)."""
+    every expert on the device (the exact attention chain in both; the pressured load in a process
+    of its own, _pressure_child)."""
     L = capi.lib()
     capi.check(L.sdy_init())
     toks = np.random.default_rng(4).integers(0, 151936, 515).astype(np.int32)
-
-    def run():
-        with engine_env(SARDYNE_ATTENTION="exact", SARDYNE_RESERVE_MB="2048", SARDYNE_GEMM_COPY_MB="0"):
-            model = LoadedModel(qwen3_30b_a3b_path)
-            s = model.session(max_seq=640, n_batch=512)
-        out = np.stack([s.feed(toks[:512])] + [s.step(int(t)) for t in toks[512:]])
-        return out, model.memory()
-
-    base, mem = run()
+    env = {"SARDYNE_ATTENTION": "exact", "SARDYNE_RESERVE_MB": "2048", "SARDYNE_GEMM_COPY_MB": "0"}
+    with engine_env(**env):
+        model = LoadedModel(qwen3_30b_a3b_path)
+        s = model.session(max_seq=640, n_batch=512)
+    base = np.stack([s.feed(toks[:512])] + [s.step(int(t)) for t in toks[512:]])
+    mem = model.memory()
+    del s, model
     assert mem["host_expert_layers"] == 0 and mem["host_expert_bytes"] == 0
     spec = qwen3_30b_a3b()
     room = mem["weight_bytes"] // 2 + (2048 << 20) + (256 << 20)
-    ballast = fill_device_to(room)
-    try:
-        got, mem2 = run()
-    finally:
-        for b in ballast:
-            b.close()
+    got, mem2 = run_pressured(qwen3_30b_a3b_path, room, toks, env, tmp_path)
     assert 0 < mem2["host_expert_layers"] < spec.n_layer, mem2
     assert mem2["weight_bytes"] + mem2["host_expert_bytes"] == mem["weight_bytes"]
     assert np.all(np.isfinite(base))
