@@ -459,7 +459,8 @@ def bench_decode(args, spec, ctx_len, n_decode, label, path=None):
     t_load = time.perf_counter() - t0
     mem = model.memory()
     log(f"[bench] GPU model load {t_load:.2f}s")
-    ctx = model.session(max_seq=ctx_len + n_decode + 1, n_batch=args.n_batch)
+    n_batch = args.n_batch or ctx_len
+    ctx = model.session(max_seq=ctx_len + n_decode + 1, n_batch=n_batch)
     ctx.feed(toks[:ctx_len])  # the prompt kernels' first launches (code loading), untimed
     ctx.clear()
     t0 = time.perf_counter()
@@ -481,7 +482,7 @@ def bench_decode(args, spec, ctx_len, n_decode, label, path=None):
         saved = os.environ.get("SARDYNE_KV")
         os.environ["SARDYNE_KV"] = "f16"
         try:
-            ctx = model.session(max_seq=ctx_len + n_decode + 1, n_batch=args.n_batch)
+            ctx = model.session(max_seq=ctx_len + n_decode + 1, n_batch=n_batch)
         finally:
             if saved is None:
                 os.environ.pop("SARDYNE_KV", None)
@@ -745,7 +746,8 @@ def main():
                     choices=["q6k_head", "q8_0_head", "q4k_matvec", "decode_3b", "decode_moe", "decode_moe_host",
                              "prefill_3b", "grid_barrier"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--n-batch", type=int, default=512, help="GPU prefill chunk (decode workloads)")
+    ap.add_argument("--n-batch", type=int, default=0,
+                    help="GPU prefill chunk (decode workloads; 0: the whole context in one batch)")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (smoke runs only)")
     ap.add_argument("--scales", default="workload", choices=["workload", "file"],
                     help="K-quant scale distribution of the prefill model: the workload's, or the "
