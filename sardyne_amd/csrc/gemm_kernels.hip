@@ -30,6 +30,7 @@
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x32 __attribute__((ext_vector_type(32)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
@@ -465,13 +466,25 @@ SDY_DEV void gemm3_body(const GemmArgs &g, int bx, int by, int gx, int gy, uint8
             stage(sb + PF, (sb + PF) % NBUF);
         }
         __builtin_amdgcn_s_setprio(1);
-        // d (and dmin) of the wave's rows as f32
-        if (h == 0) {
+        // d (and dmin) of the lane's row (lr, the same in both lane halves) as f32
+        float drow[MT], mrow[MT];
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++) {
-                const uint32_t dp = WT == SDY_Q4_K ? A[mt].hd.x : A[mt].d6;
-                dtab[32 * mt + lr] = sdy_h2f((uint16_t)(dp & 0xFFFFu));
-                if constexpr (WT == SDY_Q4_K) dtab[32 * MT + 32 * mt + lr] = sdy_h2f((uint16_t)(dp >> 16));
+        for (int mt = 0; mt < MT; mt++) {
+            const uint32_t dp = WT == SDY_Q4_K ? A[mt].hd.x : A[mt].d6;
+            drow[mt] = sdy_h2f((uint16_t)(dp & 0xFFFFu));
+            mrow[mt] = WT == SDY_Q4_K ? sdy_h2f((uint16_t)(dp >> 16)) : 0.0f;
+        }
+        // KS 1: the combine's scale products from the matrix cores (outer products, below); KS 2 keeps
+        // them on the VALU from a per-wave LDS table (the MFMA form's registers cost the unit split's
+        // grids an occupancy step)
+        constexpr bool OUTER = KS == 1;
+        if constexpr (!OUTER) {
+            if (h == 0) {
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    dtab[32 * mt + lr] = drow[mt];
+                    if constexpr (WT == SDY_Q4_K) dtab[32 * MT + 32 * mt + lr] = mrow[mt];
+                }
             }
         }
         const uint8_t *bbuf = lds + (sb % NBUF) * BUF;
@@ -611,6 +624,39 @@ SDY_DEV void gemm3_body(const GemmArgs &g, int bx, int by, int gx, int gy, uint8
         // acc += yd d isum - yd dmin msum over the wave's D registers of row tile mt: register RH ks + i
         // holds row 8 q + 4 h + (i & 3) of the tile, q = (RH ks + i) / 4
         auto combine = [&](int mt, const float(&tot)[NT][RH], const float(&ms)[NT][RH]) {
+            if constexpr (OUTER) {
+                // yd*d and yd*dmin of the tile's (row, token) pairs as the outer products of an f32 MFMA
+                // with k = 1: one rounding of a single product, the bits of the VALU's multiply (a zero
+                // product may come out +0 where the multiply gives -0; acc starts at +0 and sums of
+                // zeros of either sign keep it +0, so the results are the same). Two blocks: token
+                // tiles 2p and 2p + 1 from lane halves 0 and 1 (past the last tile, block 1 repeats it
+                // and is not read); the D register r of block b holds the row and token that isum's
+                // register r holds.
+#pragma unroll
+                for (int pr = 0; pr < (NT + 1) / 2; pr++) {
+                    const float ydb = h && 2 * pr + 1 < NT ? ydn[2 * pr + 1] : ydn[2 * pr];
+                    const f32x32 da = __builtin_amdgcn_mfma_f32_32x32x1f32(drow[mt], ydb, f32x32{}, 0, 0, 0);
+                    f32x32 dmv = {};
+                    if constexpr (WT == SDY_Q4_K)
+                        dmv = __builtin_amdgcn_mfma_f32_32x32x1f32(mrow[mt], ydb, f32x32{}, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < RH; i++) {
+#pragma unroll
+                        for (int b = 0; b < 2; b++) {
+                            const int nt = 2 * pr + b;
+                            if (nt >= NT) continue;
+                            const int r = 16 * b + RH * ks + i;
+                            if constexpr (WT == SDY_Q4_K) {
+                                const float t1 = da[r] * tot[nt][i], t2 = dmv[r] * ms[nt][i];
+                                acc[mt][nt][i] = acc[mt][nt][i] + (t1 - t2);
+                            } else {
+                                acc[mt][nt][i] = acc[mt][nt][i] + da[r] * tot[nt][i];
+                            }
+                        }
+                    }
+                }
+                return;
+            }
             float dv[RH], dm[RH];
             const uint32_t da = lds_addr(dtab + 32 * mt + 4 * h + 8 * (RH / 4) * ks);
             if constexpr (KS == 1) {
