@@ -1,4 +1,4 @@
-// Prefill attention in flash form on the matrix cores (within tolerance of the reference, not
+// Prefill attention in flash form on the f32 matrix cores (within tolerance of the reference, not
 // its bits; the reference's own arithmetic is sdy_attention in attn_kernels.hip).
 //
 // For each prompt token t and query head, the reference (csrc/ops.c:405-414, called per token from
@@ -8,16 +8,10 @@
 //   k_attn_flash<HD, KT>  grid (ceil(n_tok / 32), n_head), 512 threads: one workgroup per 32
 //   consecutive queries of one head (the blocks with the most keys first), its eight waves sharing
 //   the key tiles of 32 positions (wave w: tiles w, w + 8, ...). Per tile a wave computes
-//   S^T = K Q^T (keys as rows, so a lane holds its own query's 16 scores of the tile), masks the
-//   positions at or past each query's causal limit, and keeps the running maximum m, the sum l of
-//   exp(s - m) and O^T = V^T P (HD / 32 tiles of 32 dims), rescaled by exp(m_old - m_new) when m
-//   grows. The queries' rows sit in LDS, read by all eight waves.
-//
-//   Both products run on the f16 matrix cores (v_mfma_f32_32x32x16_f16, sixteen times the f32
-//   MFMA's rate) in three passes: each f32 operand x is split as hi = x rounded toward zero to f16
-//   and lo = (x - hi) rounded toward zero to f16 (x - hi is exact in f32), and a product is
-//   hi*hi + hi*lo + lo*hi with f32 accumulation, the dropped lo*lo and lo's rounding being below
-//   2^-21 of it. Operands must stay below 65504 in magnitude (hi saturates there).
+//   S^T = K Q^T on v_mfma_f32_32x32x2_f32 (keys as rows, so a lane holds its own query's 16 scores
+//   of the tile), masks the positions at or past each query's causal limit, and keeps the running
+//   maximum m, the sum l of exp(s - m) and O^T = V^T P (HD / 32 tiles of 32 dims), rescaled by
+//   exp(m_old - m_new) when m grows. The queries' Q^T rows sit in LDS, read by all eight waves.
 //   The waves' (m, l, O) are then merged through LDS in wave order:
 //   out = sum_w O_w exp(m_w - M) / sum_w l_w exp(m_w - M), M = max_w m_w.
 //
@@ -49,15 +43,14 @@ struct FlashArgs {
     long out_stride;
 };
 
-// LDS: the block's queries split in f16 hi and lo parts, [2][32][QR] halves (query q, dim d at
-// [part][q][d]; rows padded to QR = HD + 8 halves so that the 16-byte reads of eight consecutive
-// queries hit distinct banks), then, after the key tiles, the merge area: the waves' O dims, 1/MS
-// of them at a time, as [FW][32][OS] and their m, l as [2][FW][32] (HD 128: 134 KB for MS 1, one
-// workgroup per CU; 68 KB for MS 2, two).
+// LDS: Q^T of the block as [2][32][QS] (element (query q, dim half * HD/2 + s) at [half][q][s]),
+// then, after the key tiles, the merge area: the waves' O dims, 1/MS of them at a time, as
+// [FW][32][OS] and their m, l as [2][FW][32] (HD 128: 134 KB for MS 1, one workgroup per CU;
+// 68 KB for MS 2, two).
 template <int HD, int MS>
 struct FlashLds {
-    static constexpr int QR = HD + 8, OS = HD / MS + 1;
-    static constexpr size_t q_floats = 2 * 32 * QR / 2;
+    static constexpr int HH = HD / 2, QS = HH + 4, OS = HD / MS + 1;
+    static constexpr size_t q_floats = 2 * 32 * QS;
     static constexpr size_t merge_floats = (size_t)FW * 32 * OS + 2 * FW * 32;
     static constexpr size_t bytes = 4 * (q_floats > merge_floats ? q_floats : merge_floats);
 };
@@ -78,36 +71,10 @@ struct VLoad<2, KT> {
     SDY_DEV static float at(const T &v, int j) { return j ? v.y : v.x; }
 };
 
-typedef _Float16 half8f __attribute__((ext_vector_type(8)));
-typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
-
-// x = hi + lo (+ below 2^-21 of x): hi = x rounded toward zero to f16, lo = (x - hi) likewise
-SDY_DEV void split_f16(const float (&x)[8], half8f &hi, half8f &lo) {
-    uint32_t hw[4], lw[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const fp16x2 h2 = __builtin_amdgcn_cvt_pkrtz(x[2 * e], x[2 * e + 1]);
-        const float r0 = x[2 * e] - (float)h2[0], r1 = x[2 * e + 1] - (float)h2[1];
-        hw[e] = __builtin_bit_cast(uint32_t, h2);
-        lw[e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
-    }
-    hi = __builtin_bit_cast(half8f, make_uint4(hw[0], hw[1], hw[2], hw[3]));
-    lo = __builtin_bit_cast(half8f, make_uint4(lw[0], lw[1], lw[2], lw[3]));
-}
-
-// c += a b in three f16 passes (hi*lo and lo*hi first, the largest term last); A_EXACT: a is f16
-// already (an f16 K/V cache), its lo part zero and its pass left out
-template <bool A_EXACT>
-SDY_DEV f32x16 mfma3(const half8f &ah, const half8f &al, const half8f &bh, const half8f &bl, f32x16 c) {
-    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, c, 0, 0, 0);
-    if constexpr (!A_EXACT) c = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, c, 0, 0, 0);
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, c, 0, 0, 0);
-}
-
 template <int HD, class KT, int MS>
 __global__ __launch_bounds__(64 * FW) void k_attn_flash(FlashArgs a) {
     using LY = FlashLds<HD, MS>;
-    constexpr int ND = HD / 32;
+    constexpr int HH = HD / 2, ND = HD / 32;
     using VL = VLoad<ND, KT>;
     extern __shared__ __align__(16) float lds[];
     const int tid = threadIdx.x, lane = tid & 63, hh = lane >> 5, ql = lane & 31;
@@ -119,17 +86,12 @@ __global__ __launch_bounds__(64 * FW) void k_attn_flash(FlashArgs a) {
     const int n_kv_max = a.n_kv0 + t_last;  // positions of the block's last query
     const int n_kt = (n_kv_max + KB - 1) / KB;
 
-    _Float16 *qlds = reinterpret_cast<_Float16 *>(lds);  // [2][32][QR]: hi, then lo
-    for (int i = tid; i < QB * HD / 8; i += 64 * FW) {
-        const int q = i / (HD / 8), d = 8 * (i - q * (HD / 8));
+    for (int i = tid; i < QB * HD / 4; i += 64 * FW) {
+        const int q = i / (HD / 4), d = 4 * (i - q * (HD / 4));
         const int t = q0 + q < a.n_tok ? q0 + q : a.n_tok - 1;
-        const float *src = a.q + (size_t)t * a.q_stride + (size_t)h * HD + d;
-        const float4 v0 = *reinterpret_cast<const float4 *>(src), v1 = *reinterpret_cast<const float4 *>(src + 4);
-        const float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        half8f hi, lo;
-        split_f16(x, hi, lo);
-        *reinterpret_cast<half8f *>(qlds + q * LY::QR + d) = hi;
-        *reinterpret_cast<half8f *>(qlds + (32 + q) * LY::QR + d) = lo;
+        const float4 v = *reinterpret_cast<const float4 *>(a.q + (size_t)t * a.q_stride + (size_t)h * HD + d);
+        const int part = d / HH, s = d - part * HH;
+        *reinterpret_cast<float4 *>(lds + (part * 32 + q) * LY::QS + s) = v;
     }
     __syncthreads();
 
@@ -137,42 +99,34 @@ __global__ __launch_bounds__(64 * FW) void k_attn_flash(FlashArgs a) {
     const int lim = t < a.n_tok ? a.n_kv0 + t : 0;  // this lane's query sees positions < lim
     const KT *kb = (const KT *)a.k_cache + (size_t)g * a.head_stride;
     const KT *vb = (const KT *)a.v_cache + (size_t)g * a.head_stride;
-    const _Float16 *qh = qlds + ql * LY::QR + 8 * hh, *qlo = qlds + (32 + ql) * LY::QR + 8 * hh;
+    const float *qs = lds + (hh * 32 + ql) * LY::QS;
     f32x16 o[ND];
 #pragma unroll
     for (int dt = 0; dt < ND; dt++) o[dt] = f32x16{};
     float m_run = -INFINITY, l_run = 0.0f;
     for (int kt = wave; kt < n_kt; kt += FW) {
         const int k0 = kt * KB;
-        // K: lane (key ql of the tile), dims 16 i + 8 hh .. + 7 of step i (the MFMA's k-slots of the
-        // lane half); V of the PV step r: key 8 (r / 4) + 4 hh + r % 4 of the tile (the key of the
-        // lane's score register r), dims ND * ql ... (positions past the block's last one read its
-        // row: masked below)
+        // K: lane (key ql of the tile, dims hh * HH ...); V of the PV step r: key
+        // 8 (r / 4) + 4 hh + r % 4 of the tile (the key of the lane's score register r), dims
+        // ND * ql ... (positions past the block's last one read its row: masked below)
         const int kr = k0 + ql < n_kv_max ? k0 + ql : n_kv_max - 1;
-        sdy_f32x4 kv[HD / 8];
+        sdy_f32x4 kv[HH / 4];
 #pragma unroll
-        for (int i = 0; i < HD / 16; i++) {
-            kv[2 * i] = KvElt<KT>::ld4(kb, (size_t)kr * HD + 16 * i + 8 * hh);
-            kv[2 * i + 1] = KvElt<KT>::ld4(kb, (size_t)kr * HD + 16 * i + 8 * hh + 4);
-        }
+        for (int i = 0; i < HH / 4; i++) kv[i] = KvElt<KT>::ld4(kb, (size_t)kr * HD + hh * HH + 4 * i);
         typename VL::T vv[16];
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int key = k0 + 8 * (r >> 2) + 4 * hh + (r & 3);
             vv[r] = VL::ld(vb, (size_t)(key < n_kv_max ? key : n_kv_max - 1) * HD + ND * ql);
         }
-        // S^T[key][query] = sum over dims of K[key][d] Q[query][d]: step i takes dims 16 i .. 16 i + 15,
-        // lane half hh its k-slots 8 hh .. 8 hh + 7 (the same dims in K and Q)
+        // S^T[key][query] = sum over dims of K[key][d] Q[query][d]: step (i, j) pairs dim 4i + j
+        // (lanes 0-31) with dim HH + 4i + j (lanes 32-63)
         f32x16 s = f32x16{};
 #pragma unroll
-        for (int i = 0; i < HD / 16; i++) {
-            const float x[8] = {kv[2 * i][0], kv[2 * i][1], kv[2 * i][2], kv[2 * i][3],
-                                kv[2 * i + 1][0], kv[2 * i + 1][1], kv[2 * i + 1][2], kv[2 * i + 1][3]};
-            half8f khi, klo;
-            split_f16(x, khi, klo);
-            const half8f qhv = *reinterpret_cast<const half8f *>(qh + 16 * i);
-            const half8f qlv = *reinterpret_cast<const half8f *>(qlo + 16 * i);
-            s = mfma3<sizeof(KT) == 2>(khi, klo, qhv, qlv, s);
+        for (int i = 0; i < HH / 4; i++) {
+            const sdy_f32x4 qv = *reinterpret_cast<const sdy_f32x4 *>(qs + 4 * i);
+#pragma unroll
+            for (int j = 0; j < 4; j++) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[i][j], qv[j], s, 0, 0, 0);
         }
         // scores of the lane's query (register r: key 8 (r / 4) + 4 hh + r % 4), running maximum
         // and sum; the other half of the tile's keys is in lane ^ 32
@@ -201,25 +155,12 @@ __global__ __launch_bounds__(64 * FW) void k_attn_flash(FlashArgs a) {
         for (int dt = 0; dt < ND; dt++)
 #pragma unroll
             for (int e = 0; e < 16; e++) o[dt][e] = o[dt][e] * corr;
-        // O^T[dim][query] += V^T[dim][key] P[key][query] over the tile's keys, sixteen per step: step
-        // s2, k-slot 8 hh + j is the key of score register 8 s2 + j (in V^T the lane's row of that
-        // key, in P the lane's own register)
+        // O^T[dim][query] += V^T[dim][key] P[key][query] over the tile's keys, two per step
 #pragma unroll
-        for (int s2 = 0; s2 < 2; s2++) {
-            const float px[8] = {p[8 * s2], p[8 * s2 + 1], p[8 * s2 + 2], p[8 * s2 + 3],
-                                 p[8 * s2 + 4], p[8 * s2 + 5], p[8 * s2 + 6], p[8 * s2 + 7]};
-            half8f phi, plo;
-            split_f16(px, phi, plo);
+        for (int r = 0; r < 16; r++)
 #pragma unroll
-            for (int dt = 0; dt < ND; dt++) {
-                float y[8];
-#pragma unroll
-                for (int j = 0; j < 8; j++) y[j] = VL::at(vv[8 * s2 + j], dt);
-                half8f vhi, vlo;
-                split_f16(y, vhi, vlo);
-                o[dt] = mfma3<sizeof(KT) == 2>(vhi, vlo, phi, plo, o[dt]);
-            }
-        }
+            for (int dt = 0; dt < ND; dt++)
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(VL::at(vv[r], dt), p[r], o[dt], 0, 0, 0);
     }
 
     // merge of the waves' partials in wave order (the Q^T area is reused), in MS parts of the dims:

@@ -944,7 +944,7 @@ def test_prefill_attention_tokens_bit_identical(n_head, n_kv_head, hd, n_tok, n_
 @pytest.mark.parametrize("n_tok,n_kv0", [(16, 1), (40, 70), (77, 3), (512, 1), (100, 900)])
 @pytest.mark.parametrize("kv", ["f32", "f16"])
 def test_prefill_attention_flash(n_head, n_kv_head, hd, n_tok, n_kv0, kv):
-    """The flash-form prompt attention (f32 products as three f16 matrix-core passes, eight waves per 32 queries over key tiles
+    """The flash-form prompt attention (f32 matrix cores, eight waves per 32 queries over key tiles
     of 32, merged in wave order) is within 1e-5 of the output scale of the reference's arithmetic
     (sdy_attention, bit-exact with the oracle), for partial query blocks and key tiles, q rows at a
     stride wider than the heads (the engine's q|k|v rows) and both cache types; it is deterministic."""
