@@ -143,6 +143,30 @@ def test_c3_c4_qwen25_3b_prefill_512_then_decode(qwen25_3b_path):
     _run_and_compare(qwen25_3b_path, 512, 512, 6, 640, seed=0, tol=1e-4)
 
 
+@needs_ref
+def test_c3_default_engine_over_the_decode_benchmark(qwen25_3b_path):
+    """The default engine (the flash prompt attention, the chunked one-token attention) over the
+    decode benchmark's own sequence: a 512-token prompt of uniform token ids (seed 0), then 128
+    one-token steps, each within 1e-4 of the logit scale of the reference engine with the same greedy
+    token. Over this many steps a rounding-level change of the prompt's attention can flip one
+    activation's int8 rounding in a later layer and move a step's logits far past that bar, which
+    six steps do not show."""
+    n_ctx, n_steps = 512, 128
+    toks = np.random.default_rng(0).integers(0, 151936, n_ctx + n_steps).astype(np.int32)
+    model = LoadedModel(qwen25_3b_path)
+    s = model.session(max_seq=n_ctx + n_steps + 1, n_batch=n_ctx)
+    s.feed(toks[:n_ctx])
+    got = np.stack([s.step(int(t)) for t in toks[n_ctx:]])
+    del s, model
+    ref = O.RefEngine(qwen25_3b_path, n_ctx + n_steps + 1, n_batch=64)
+    ref.eval(toks[:n_ctx])
+    exp = np.stack([ref.eval([int(t)]) for t in toks[n_ctx:]])
+    scale = float(np.abs(exp).max())
+    err = np.abs(got - exp).max(axis=1) / scale
+    assert float(err.max()) <= 1e-4, (int(err.argmax()), float(err.max()))
+    assert np.array_equal(got.argmax(-1), exp.argmax(-1))
+
+
 def fill_device_to(room):
     """Ballast allocations that leave about `room` bytes of device memory free (within 64 MiB): the
     free figure after an allocation can exceed the request's complement (allocation granularity,
