@@ -1081,6 +1081,31 @@ def test_gemm_bit_exact(kind, n_in, n_out, n_tok):
     assert np.array_equal(bits(got), bits(exp))
 
 
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
+def test_gemm_bit_exact_with_subnormal_scale_products(kind):
+    """Tokens whose activations are scaled by 2^-80 .. 2^-119: their Q8_K scales yd reach 2^-127, and
+    the combine's products yd*d and yd*dmin (formed on the matrix cores for one wave per row tile)
+    and the sums after them run through f32 subnormals. The bits stay the oracle's."""
+    n_in, n_out, n_tok = 512, 96, 40
+    t = TYPES[kind]
+    rng = np.random.default_rng(77)
+    w = random_blocks(kind, n_out * n_in // O.QK[t], rng).reshape(n_out, -1)
+    x = np.random.default_rng(78).standard_normal((n_tok, n_in)).astype(np.float32)
+    x *= np.float32(2.0) ** -(80 + np.arange(n_tok, dtype=np.float32))[:, None]
+    xq = O.quantize(x, O.Q8_K)
+    got = _gemm_run(t, w, xq, n_in, n_out, n_tok)
+    exp = O.matmul_q(w, t, xq, n_in, simd=1)
+    # the smallest tokens' yd times the rows' d scales (an f16 at byte 0 of a Q4_K block, 208 of a
+    # Q6_K one) are f32 subnormals: the case reaches the range it is about
+    yd = np.ascontiguousarray(xq.reshape(n_tok, -1)[:, :4]).view(np.float32)[:, 0]
+    off = 0 if kind == "Q4_K" else 208
+    d = np.ascontiguousarray(w.reshape(-1, w.shape[1] // (n_in // 256))[:, off:off + 2]).view(np.float16)[:, 0]
+    prods = np.abs(yd[-1]).astype(np.float64) * np.abs(d.astype(np.float64))
+    assert np.any((prods > 0) & (prods < np.finfo(np.float32).tiny))
+    assert np.all(np.isfinite(exp))
+    assert np.array_equal(bits(got), bits(exp))
+
+
 @pytest.mark.parametrize("n_in,n_tok", [(2048, 512), (11008, 33), (256, 16)])
 def test_gemm_ws_ready_reuses_expansion(n_in, n_tok):
     """ws_ready = 1 skips the f16 expansion of the activations: a Q6_K GEMM that reuses the workspace
