@@ -15,6 +15,8 @@
       reference's own AVX2 and scalar engines on the same model and tokens (golden/c5_simd_spread.npz),
       with the same greedy tokens. On a device with room for half its experts, the rest in pinned
       host memory: the bits of the load with every expert on the device.
+  C3 and C5 over the decode benchmark's own sequence (its context, then 128 one-token steps): the
+      default engine within the same tolerances at every step, with the same greedy tokens.
 
 The models are written to /dev/shm (2.2 GB and 19.8 GB) and deleted afterwards.
 """
@@ -143,28 +145,33 @@ def test_c3_c4_qwen25_3b_prefill_512_then_decode(qwen25_3b_path):
     _run_and_compare(qwen25_3b_path, 512, 512, 6, 640, seed=0, tol=1e-4)
 
 
-@needs_ref
-def test_c3_default_engine_over_the_decode_benchmark(qwen25_3b_path):
-    """The default engine (the flash prompt attention, the chunked one-token attention) over the
-    decode benchmark's own sequence: a 512-token prompt of uniform token ids (seed 0), then 128
-    one-token steps, each within 1e-4 of the logit scale of the reference engine with the same greedy
-    token. Over this many steps a rounding-level change of the prompt's attention can flip one
-    activation's int8 rounding in a later layer and move a step's logits far past that bar, which
-    six steps do not show."""
-    n_ctx, n_steps = 512, 128
+def _default_engine_over_the_decode_benchmark(path, n_ctx, n_steps, tol):
+    """The default engine over the decode benchmark's own sequence (bench.py's decode workloads: the
+    model written with seed 0, uniform token ids from seed 0, the context in one batch, then n_steps
+    one-token steps): each step within tol of the logit scale of the reference engine, with the same
+    greedy token."""
     toks = np.random.default_rng(0).integers(0, 151936, n_ctx + n_steps).astype(np.int32)
-    model = LoadedModel(qwen25_3b_path)
+    model = LoadedModel(path)
     s = model.session(max_seq=n_ctx + n_steps + 1, n_batch=n_ctx)
     s.feed(toks[:n_ctx])
     got = np.stack([s.step(int(t)) for t in toks[n_ctx:]])
     del s, model
-    ref = O.RefEngine(qwen25_3b_path, n_ctx + n_steps + 1, n_batch=64)
+    ref = O.RefEngine(path, n_ctx + n_steps + 1, n_batch=64)
     ref.eval(toks[:n_ctx])
     exp = np.stack([ref.eval([int(t)]) for t in toks[n_ctx:]])
     scale = float(np.abs(exp).max())
     err = np.abs(got - exp).max(axis=1) / scale
-    assert float(err.max()) <= 1e-4, (int(err.argmax()), float(err.max()))
+    assert float(err.max()) <= tol, (int(err.argmax()), float(err.max()), tol)
     assert np.array_equal(got.argmax(-1), exp.argmax(-1))
+
+
+@needs_ref
+def test_c3_default_engine_over_the_decode_benchmark(qwen25_3b_path):
+    """The 3B default engine (the flash prompt attention, the chunked one-token attention) over the
+    benchmark's 512-token prompt and 128 steps, each within 1e-4 of the logit scale. Over this many
+    steps a rounding-level change of the prompt's attention can flip one activation's int8 rounding
+    in a later layer and move a step's logits far past that bar, which six steps do not show."""
+    _default_engine_over_the_decode_benchmark(qwen25_3b_path, 512, 128, 1e-4)
 
 
 def fill_device_to(room):
@@ -273,6 +280,14 @@ def test_c5_qwen3_30b_a3b_context_1024_then_decode(qwen3_30b_a3b_path):
     reference's own AVX2-vs-scalar spread on this model and token sequence, with the same greedy
     tokens."""
     _run_and_compare(qwen3_30b_a3b_path, 1024, 512, 5, 1152, seed=1, tol=c5_tolerance())
+
+
+@needs_ref
+def test_c5_default_engine_over_the_decode_benchmark(qwen3_30b_a3b_path):
+    """The 30B-A3B default engine (the flash prompt attention, the chunked one-token attention, the
+    gate|up that routes each token itself) over the benchmark's 1024-token context and 128 steps,
+    each within the tolerance derived from the reference's own AVX2-vs-scalar spread."""
+    _default_engine_over_the_decode_benchmark(qwen3_30b_a3b_path, 1024, 128, c5_tolerance())
 
 
 def test_c5_experts_beyond_the_device_memory(qwen3_30b_a3b_path, tmp_path):
