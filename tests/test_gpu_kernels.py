@@ -769,11 +769,12 @@ FLOAT_TYPES = {"F32": (0, np.float32), "F16": (1, np.float16), "BF16": (30, None
 
 
 @pytest.mark.parametrize("wname,n_in,n_rows", [("F32", 2048, 128), ("F16", 1024, 64), ("BF16", 4096, 17),
-                                               ("F32", 256, 3)])
+                                               ("F32", 256, 3), ("F32", 4096, 13), ("F32", 1024, 70),
+                                               ("F32", 2048, 5)])
 def test_matvec_float_norm(wname, n_in, n_rows):
     """The float matvec of the RMS-normalised row (the MoE router reading the FFN norm's output):
     the bits of sdy_norm_quant's f32 row followed by sdy_matvec_float, and the Q8_K bytes
-    sdy_norm_quant writes."""
+    sdy_norm_quant writes (row counts that leave the last workgroup partial among them)."""
     L = lib()
     wt, dt = FLOAT_TYPES[wname]
     rng = np.random.default_rng(n_in + n_rows)
