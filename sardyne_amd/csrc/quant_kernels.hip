@@ -1283,13 +1283,17 @@ __global__ __launch_bounds__(64 * KMAX) void k_moe_down_combine(MvArgs a, const 
     // (eight rows of 768: 24 super-blocks, three per wave)
     Q8kRow<false, NSB == 3 ? 3 : 4, KMAX> arow;
     arow.issue(a.px, nullptr, k * n_in);
+    __builtin_amdgcn_sched_barrier(0);  // (the row's loads stay ahead of the weights')
     const int sl = wave < k ? wave : k - 1;
     int e = a.slot_expert[sl];
     e = e < 0 ? 0 : (e >= a.n_slot_exp ? a.n_slot_exp - 1 : e);
     WRegs<WT> R;
     const uint32_t nb = a.P.nb, base = (uint32_t)((long)e * a.slot_rows + rowc);
     load_w_at<WT>(a.P, base * (uint32_t)T + (uint32_t)u, base * nb + ((uint32_t)u >> 2), (uint32_t)u, R);
-    const float rv = resid ? resid[rowc] : 0.0f;
+    // (an unconditional load, from a stand-in when there is no residual: a load under a pointer
+    // test makes the compiler's wait before the activation row count the weight loads issued ahead
+    // of it)
+    const float rv = (resid ? resid : a.px)[resid ? rowc : 0];
     // the combine's expert ids and weights, requested with the other loads
     int ids[KMAX];
     float wv[KMAX], yv[KMAX];
@@ -1471,19 +1475,26 @@ __global__ __launch_bounds__(64 * WV) void k_matvec_lr(MvArgs a) {
     // row 0 and run no row)
     if constexpr (PRO) {
         arow.issue(a.px, nullptr, a.P.n_in);
+        // (the row's loads stay ahead of the weights': the wait before the row is built then
+        // covers only them)
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (!WFIRST) arow.build(a.px, 0.0f, a.P.n_in, lds_act);
     } else {
         if (wid >= n_rows) return;
     }
     const long w0 = wid < n_rows ? wid : 0;
     load_row(w0, A);
-    // the bias and residual of the row, requested with its weights (lane 0 stores)
+    // the bias and residual of the row, requested with its weights (lane 0 stores). Every lane
+    // loads (an absent one reads a stand-in: the activation row): a load under a lane or pointer
+    // test makes the compiler's wait before the activation row also count the weight loads issued
+    // ahead of it, and the row then waited for the first weights (2048 x 11008 Q6_K down with
+    // its quantiser: the row built at 5.5 us into the kernel instead of 1.3 us after its loads)
+    const float *stand_in = PRO ? a.px : reinterpret_cast<const float *>(a.xq);
+    const float *bsrc = a.bias ? a.bias : stand_in, *rsrc = a.resid ? a.resid : stand_in;
     float bv = 0.0f, rv = 0.0f;
     auto load_br = [&](long r) {
-        if (lane == 0) {
-            if (a.bias) bv = a.bias[a.row0 + r];
-            if (a.resid) rv = a.resid[a.row0 + r];
-        }
+        bv = bsrc[a.bias ? a.row0 + r : 0];
+        rv = rsrc[a.resid ? a.row0 + r : 0];
     };
     load_br(w0);
     if constexpr (PRO && WFIRST) arow.build(a.px, 0.0f, a.P.n_in, lds_act);

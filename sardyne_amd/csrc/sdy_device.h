@@ -36,6 +36,26 @@ SDY_DEV uint16_t sdy_f2h(float f) {
 // Σ of four int8 products plus acc (v_dot4c_i32_i8): exact.
 SDY_DEV int sdy_dot4(int a, int b, int acc) { return __builtin_amdgcn_sdot4(a, b, acc, false); }
 
+// The maximum of a 32-bit unsigned value over the wave, in every lane (all lanes active): DPP
+// within rows of 16 lanes (quad perms, row rotations), then the four rows' maxima by readlane.
+SDY_DEV uint32_t wave_max_u32(uint32_t v) {
+    uint32_t o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
+    v = o > v ? o : v;
+    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
+    v = o > v ? o : v;
+    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, false);  // row_ror 4
+    v = o > v ? o : v;
+    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);  // row_ror 8
+    v = o > v ? o : v;
+    uint32_t r = 0;
+#pragma unroll
+    for (int row = 0; row < 4; row++) {
+        const uint32_t x = (uint32_t)__builtin_amdgcn_readlane((int)v, 16 * row);
+        r = x > r ? x : r;
+    }
+    return r;
+}
+
 // Sum over the 4 lanes of a quad (lanes 4k..4k+3), result in every lane of the quad: exact for ints.
 SDY_DEV int sdy_quad_sum(int v) {
     v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]

@@ -19,29 +19,50 @@ struct SdyQ8kLane {
 // NB blocks at once (each the same result as one block alone). The signed maximum: the magnitude is
 // reduced over the wave in any order (a maximum is order-free), then the first lane holding it (a
 // ballot) and that lane's first element of that magnitude give the element: the first one in index
-// order, as the reference's strict '>' picks. NaN never wins (fmaxf drops it; a block with no
-// finite nonzero element is all zero bytes, as in the reference).
+// order, as the reference's strict '>' picks. NaN never wins (fmaxf drops it within the lane, and a
+// lane whose four elements are all NaN enters the wave maximum as 0); a block with no finite nonzero
+// element is all zero bytes, as in the reference. The wave maximum runs on the magnitudes' bits
+// (non-negative floats order as their bits) through DPP and readlane, and the element is read with
+// readlane from the uniform first holder: no LDS permutes. With NB > 1 the blocks' two divisions
+// (-127/max and 1/iscale, correctly rounded) run once for all blocks, block b's operand in lane b.
 template <int NB>
 SDY_DEV void sdy_q8k_lanes(const float (&xs)[NB][4], int lane, SdyQ8kLane (&r)[NB]) {
-    float lm[NB], amax[NB], bval[NB];
+    float lm[NB], bval[NB];
+    uint32_t mb[NB];
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         lm[b] = fmaxf(fmaxf(fabsf(xs[b][0]), fabsf(xs[b][1])), fmaxf(fabsf(xs[b][2]), fabsf(xs[b][3])));
-        amax[b] = lm[b];
+        const uint32_t u = __float_as_uint(lm[b]);
+        mb[b] = u > 0x7F800000u ? 0u : u;
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-#pragma unroll
-        for (int b = 0; b < NB; b++) amax[b] = fmaxf(amax[b], __shfl_xor(amax[b], off));
+    for (int b = 0; b < NB; b++) mb[b] = wave_max_u32(mb[b]);
 #pragma unroll
     for (int b = 0; b < NB; b++) {
-        const unsigned long long holders = __ballot(lm[b] == amax[b]);
+        const float amax = __uint_as_float(mb[b]);
+        const unsigned long long holders = __ballot(lm[b] == amax);
         const int first = holders ? __builtin_ctzll(holders) : 0;
-        const float mine = fabsf(xs[b][0]) == amax[b]   ? xs[b][0]
-                           : fabsf(xs[b][1]) == amax[b] ? xs[b][1]
-                           : fabsf(xs[b][2]) == amax[b] ? xs[b][2]
-                                                        : xs[b][3];
-        bval[b] = __shfl(mine, first);
+        const float mine = fabsf(xs[b][0]) == amax   ? xs[b][0]
+                           : fabsf(xs[b][1]) == amax ? xs[b][1]
+                           : fabsf(xs[b][2]) == amax ? xs[b][2]
+                                                     : xs[b][3];
+        bval[b] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), first));
+    }
+    float iscale[NB], dinv[NB];
+    if constexpr (NB == 1) {
+        iscale[0] = -127.0f / bval[0];
+        dinv[0] = 1.0f / iscale[0];
+    } else {
+        float bv = bval[0];
+#pragma unroll
+        for (int b = 1; b < NB; b++) bv = lane == b ? bval[b] : bv;
+        const float is = -127.0f / bv;
+        const float dv = 1.0f / is;
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            iscale[b] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, is), b));
+            dinv[b] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, dv), b));
+        }
     }
     int lsum[NB];
 #pragma unroll
@@ -49,18 +70,17 @@ SDY_DEV void sdy_q8k_lanes(const float (&xs)[NB][4], int lane, SdyQ8kLane (&r)[N
         lsum[b] = 0;
         r[b].packed = 0u;
         r[b].d = 0.0f;
-        if (amax[b] > 0.0f) {
-            const float iscale = -127.0f / bval[b];
+        if (mb[b] > 0u) {
             uint32_t packed = 0;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                int q = sdy_nearest_int(iscale * xs[b][e]);
+                int q = sdy_nearest_int(iscale[b] * xs[b][e]);
                 q = q < 127 ? q : 127;
                 lsum[b] += (int8_t)q;
                 packed |= (uint32_t)(uint8_t)(int8_t)q << (8 * e);
             }
             r[b].packed = packed;
-            r[b].d = 1.0f / iscale;
+            r[b].d = dinv[b];
         }
     }
 #pragma unroll
@@ -114,9 +134,10 @@ SDY_DEV void sdy_q8k_block(const float xs[4], int lane, uint8_t *ob) {
 
 // One 32-element Q8_0 block (csrc/quant.c:98-108) held by a half-wave, one element per lane l
 // (0..31 within the half): d = amax/127 stored as f16, q = roundf(x/d) computed with the unrounded
-// reciprocal. ob points at the 34-byte block.
+// reciprocal. The maximum starts from 0 in every lane, as the reference's does, so that NaN never
+// enters it (a block of NaN has d = 0). ob points at the 34-byte block.
 SDY_DEV void sdy_q8_0_block(float xv, int l, uint8_t *ob) {
-    float amax = fabsf(xv);
+    float amax = fmaxf(0.0f, fabsf(xv));
 #pragma unroll
     for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
     const float d = amax / 127.0f;

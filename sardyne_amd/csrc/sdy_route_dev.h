@@ -5,26 +5,7 @@
 #include "sdy_expf.h"
 #include "sdy_norm_dev.h"
 
-// The maximum of a 32-bit value over the wave, in every lane: DPP within rows of 16 lanes (quad
-// perms, row rotations), then the four rows' maxima by readlane.
-SDY_DEV uint32_t wave_max_u32(uint32_t v) {
-    uint32_t o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
-    v = o > v ? o : v;
-    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
-    v = o > v ? o : v;
-    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, false);  // row_ror 4
-    v = o > v ? o : v;
-    o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);  // row_ror 8
-    v = o > v ? o : v;
-    uint32_t r = 0;
-#pragma unroll
-    for (int row = 0; row < 4; row++) {
-        const uint32_t x = (uint32_t)__builtin_amdgcn_readlane((int)v, 16 * row);
-        r = x > r ? x : r;
-    }
-    return r;
-}
-
+// The maximum of a float over the wave, in every lane (wave_max_u32's DPP and readlane pattern)
 SDY_DEV float wave_max_f32(float v) {
     v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
     v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));

@@ -90,10 +90,33 @@ def test_activation_quantization_byte_exact(vt):
     x[2, 7] = 1e4  # one dominant value
     x[3, 10], x[3, 20] = -4.0, 4.0  # equal magnitudes: the first one sets the sign
     x[3, 300] = 2.5
+    x = np.concatenate([x, _quant_edge_rows(512, np.random.default_rng(6))])
     n_rows, n = x.shape
     out = np.zeros(O.row_size(vt, n) * n_rows, np.uint8)
     lib().op_quantize_rows(vt, ptr(x), ptr(out), n, 0, n_rows)
     assert out.tobytes() == O.quantize(x, vt).tobytes()
+    if O.ref_available():
+        assert out.tobytes() == O.quantize(x, vt, use_ref=True).tobytes()
+
+
+def _quant_edge_rows(n, rng):
+    """Rows whose 256-element blocks hold the quantisers' edge cases: NaN elements beside finite
+    ones (NaN never sets the scale), a block of NaN but one finite element, an all-NaN block (all
+    zero bytes), equal magnitudes of opposite sign in one lane and across lanes (the first one in
+    index order sets the sign), infinities (the scale from an infinite maximum), a block holding
+    only a value of the smallest subnormal magnitude."""
+    x = rng.standard_normal((4, n)).astype(np.float32)
+    x[0, [3, 100, 255]] = np.nan
+    x[0, 256:512] = np.nan
+    x[0, 256 + 77] = -3.0
+    x[1, 0:256] = np.nan
+    x[1, 256 + 8], x[1, 256 + 10] = -5.0, 5.0  # one lane (elements 8..11)
+    x[1, 256 + 40], x[1, 256 + 200] = 5.0, -5.0  # later lanes, the same magnitude
+    x[2, 50] = np.inf
+    x[2, 256 + 4], x[2, 256 + 9] = -np.inf, np.inf
+    x[3, 0:256] = 0.0
+    x[3, 17] = -1e-45
+    return x
 
 
 def _matvec_case(kind, n_in, n_out, n_tok, seed, gen="workload"):
@@ -438,6 +461,42 @@ def test_matvec_fused_activation(kind, n_in, n_out, mode):
         outs.append(dout.to_array(np.float32, n_res))
     assert not np.isnan(outs[0]).any()
     assert np.array_equal(bits(outs[1]), bits(outs[0]))
+    m.close()
+
+
+@pytest.mark.parametrize("kind,n_in", [("Q6_K", 11008), ("Q4_K", 2048), ("Q4_K", 768)])
+def test_matvec_fused_quantiser_edge_cases(kind, n_in):
+    """The workgroup quantisers of the fused one-token matvecs (several blocks per wave in one set
+    of cross-lane reductions and divisions) write the bytes of the one-block quantiser on rows of
+    NaN elements, all-NaN blocks, equal magnitudes of opposite sign, infinities and subnormals: the
+    matvec outputs through both carry the same bits (NaN where an infinite scale makes them NaN)."""
+    L = lib()
+    t = TYPES[kind]
+    n_out = 2048
+    rng = np.random.default_rng(n_in)
+    w = random_blocks(kind, n_out * n_in // O.QK[t], rng).reshape(n_out, -1)
+    rows = _quant_edge_rows(n_in, rng)
+    m = capi.DeviceMatrix(t, n_in, n_out, w)
+    for xr in rows:
+        x = np.ascontiguousarray(xr)
+        dx = capi.DeviceBuffer.from_array(x)
+        dq = capi.DeviceBuffer(n_in // 256 * 292)
+        capi.check(L.sdy_quantize(Q8K_TYPE, dx.ptr, dq.ptr, n_in, 1, None))
+        assert dq.to_array(np.uint8, n_in // 256 * 292).tobytes() == O.quantize(x[None], O.Q8_K).tobytes()
+        outs = []
+        for fused in (False, True):
+            dout = capi.DeviceBuffer.from_array(np.full(n_out, 7.0, np.float32))
+            a = capi.SdyMvArgs(n_tok=1, out=dout.ptr, out_stride=n_out, row0=0, row1=n_out, epilogue=capi.EPI_NONE)
+            if fused:
+                a.x, a.nw, a.eps = dx.ptr, None, 1e-6
+                assert L.sdy_matvec_fused_ok(ctypes.byref(m.m), ctypes.byref(a), None, None) == 1
+            else:
+                a.xq = dq.ptr
+            capi.check(L.sdy_matvec(ctypes.byref(m.m), ctypes.byref(a), None))
+            outs.append(dout.to_array(np.float32, n_out))
+        nan = np.isnan(outs[0])
+        assert np.array_equal(np.isnan(outs[1]), nan)
+        assert np.array_equal(bits(outs[1])[~nan], bits(outs[0])[~nan])
     m.close()
 
 
