@@ -1541,17 +1541,19 @@ __global__ __launch_bounds__(64 * WV) void k_matvec_lr(MvArgs a) {
                 term[k] = ydd * (float)isum;
             }
         }
-        // fold in super-block order: super-block 16k + q is in lane 4q of pass k
+        // fold in super-block order: super-block 16k + q is in lane 4q of pass k. The lanes past
+        // the row's super-blocks hold +0 and are folded too, with no test per step: the sum starts
+        // at +0, so it is never -0, and adding +0 leaves it as it is
+#pragma unroll
+        for (int k = 0; k < NI; k++)
+            if (16 * k + (lane >> 2) >= nb) term[k] = 0.0f;
         float acc = 0.0f;
 #pragma unroll
         for (int k = 0; k < NI; k++)
 #pragma unroll
             for (int q = 0; q < 16; q++) {
-                const int sb = 16 * k + q;
-                if (sb < nb) {
-                    const float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(term[k]), 4 * q));
-                    acc = acc + t;
-                }
+                const float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(term[k]), 4 * q));
+                acc = acc + t;
             }
         if (lane == 0) {
             if (a.bias) acc = acc + bv;
