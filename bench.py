@@ -443,9 +443,10 @@ def drop_bench_model(path):
 
 def bench_decode(args, spec, ctx_len, n_decode, label, path=None):
     """Decode tok/s after a ctx_len-token context at batch 1 (the method of the reference's
-    bench/bench_decode.py:39-48: n_decode / wall time of the decode loop). Token ids are uniform
-    over the vocabulary (seeded) and fed teacher-forced, so the GPU and the CPU reference see the
-    same sequence and their logits are compared step by step. The same steps with the f16 KV cache
+    bench/bench_decode.py:39-48: n_decode / wall time of the decode loop, each step's logits
+    returned as a fresh array and dropped). Token ids are uniform over the vocabulary (seeded) and
+    fed teacher-forced, so the GPU and the CPU reference see the same sequence; an untimed rerun of
+    the same steps keeps the logits, which are compared step by step. The same steps with the f16 KV cache
     (SARDYNE_KV=f16) are compared with the f32 reference too. path: a model file written already
     (kept), else one is written and deleted."""
     from sardyne_amd.engine import LoadedModel
@@ -466,13 +467,23 @@ def bench_decode(args, spec, ctx_len, n_decode, label, path=None):
     t0 = time.perf_counter()
     ctx.feed(toks[:ctx_len])
     t_prefill = time.perf_counter() - t0
-    gpu_logits = []
+    # the timed loop drops each step's logits, as the reference's loop does (bench/bench_decode.py:
+    # 44-45: every call still returns a fresh copy); kept, the 128 arrays of 608 KB (3B) would add
+    # the first-touch faults of fresh memory to every step
     t0 = time.perf_counter()
     for i in range(n_decode):
-        gpu_logits.append(ctx.feed([int(toks[ctx_len + i])]))
+        last = ctx.feed([int(toks[ctx_len + i])])
     t_dec = time.perf_counter() - t0
     gpu_tok_s = n_decode / t_dec
     log(f"[bench] GPU prefill {ctx_len} tok in {t_prefill:.3f}s, decode {gpu_tok_s:.1f} tok/s")
+    # the same prompt and steps again, untimed, keeping every step's logits for the comparison with
+    # the reference; the timed run's last step must carry the same bits
+    ctx.clear()
+    ctx.feed(toks[:ctx_len])
+    gpu_logits = [ctx.feed([int(toks[ctx_len + i])]) for i in range(n_decode)]
+    rerun_same_bits = bool(np.array_equal(gpu_logits[-1].view(np.uint32), last.view(np.uint32)))
+    if not rerun_same_bits:
+        log("[bench] decode: the untimed rerun's last logits differ from the timed run's")
     del ctx
     # the same prompt and steps with the f16 cache (untimed: its drift from the f32 reference)
     f16_logits = []
@@ -533,7 +544,8 @@ def bench_decode(args, spec, ctx_len, n_decode, label, path=None):
                 c = np.stack(cpu_logits)
                 scale = float(np.abs(c).max())
                 maxabs = float(np.abs(g - c).max())
-                parity = {"steps_compared": n_cpu_steps, "logits_max_abs": maxabs,
+                parity = {"steps_compared": n_cpu_steps, "timed_run_last_step_same_bits": rerun_same_bits,
+                          "logits_max_abs": maxabs,
                           "logits_max_abs_over_max_ref": maxabs / scale,
                           "greedy_argmax_agreement": float(np.mean(g.argmax(-1) == c.argmax(-1)))}
                 if f16_logits:
