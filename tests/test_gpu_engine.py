@@ -115,6 +115,19 @@ def test_deterministic(model_path):
     assert np.array_equal(a, b)
 
 
+def test_decode_rerun_same_bits(model_path):
+    """One-token decode steps replayed after ctx.clear() and the same prompt give the same bits
+    (the decode benchmark compares an untimed rerun of its timed steps with the reference)."""
+    model = LoadedModel(model_path)
+    ctx = model.session(max_seq=32, n_batch=8)
+    runs = []
+    for _ in range(2):
+        ctx.clear()
+        ctx.feed(TOKENS[:8])
+        runs.append(np.stack([ctx.feed([t]) for t in TOKENS[8:14]]))
+    assert np.array_equal(runs[0].view(np.uint32), runs[1].view(np.uint32))
+
+
 def test_generate_matches_oracle(model_path):
     ref = O.OracleContext(model_path, 32, n_batch=64)
     toks, out = list(TOKENS[:4]), []
