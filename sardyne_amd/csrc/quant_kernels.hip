@@ -1636,7 +1636,7 @@ __global__ __launch_bounds__(THREADS) void k_matvec_float_dot(const uint8_t *__r
     // prologue's own loads, before its computation (they do not depend on it); half-waves past the
     // rows read row0's
     float wv0[NORM ? B : 1];
-    const bool pre = NORM && (n_in & ~31) >= 32 * B;
+    const bool pre = NORM && (n_in & ~31) >= 32 * 2 * B;
     // NORM: the normalised row in LDS, built by every thread (one token, n_in <= 4096, a multiple of 256)
     __shared__ __align__(16) float xn[NORM ? 4096 : 4];
     if constexpr (NORM) {
@@ -1712,10 +1712,18 @@ __global__ __launch_bounds__(THREADS) void k_matvec_float_dot(const uint8_t *__r
     const int n32 = n_in & ~31, n8 = n_in & ~7;
     int i = L;
     if constexpr (NORM) {
-        if (pre) {  // the first B steps, whose weights are in wv0
+        if (pre) {
+            // the first B steps, whose weights are in wv0; the next B steps' weights are requested
+            // before their chain runs, so that their loads are in flight during it (n_in = 2048:
+            // the whole row)
+            float wv1[B];
+#pragma unroll
+            for (int j = 0; j < B; j++) wv1[j] = welem<WT>(wr, i + 32 * (B + j));
 #pragma unroll
             for (int j = 0; j < B; j++) acc = fmaf(wv0[j], xe(xr, i + 32 * j), acc);
-            i += 32 * B;
+#pragma unroll
+            for (int j = 0; j < B; j++) acc = fmaf(wv1[j], xe(xr, i + 32 * (B + j)), acc);
+            i += 32 * 2 * B;
         }
     }
     for (; i + 32 * (B - 1) < n32; i += 32 * B) {
