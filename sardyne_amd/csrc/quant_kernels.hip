@@ -1487,8 +1487,7 @@ __global__ __launch_bounds__(64 * WV) void k_matvec_lr(MvArgs a) {
     // the bias and residual of the row, requested with its weights (lane 0 stores). Every lane
     // loads (an absent one reads a stand-in: the activation row): a load under a lane or pointer
     // test makes the compiler's wait before the activation row also count the weight loads issued
-    // ahead of it, and the row then waited for the first weights (2048 x 11008 Q6_K down with
-    // its quantiser: the row built at 5.5 us into the kernel instead of 1.3 us after its loads)
+    // ahead of it, so that the row would wait for the first weights to land
     const float *stand_in = PRO ? a.px : reinterpret_cast<const float *>(a.xq);
     const float *bsrc = a.bias ? a.bias : stand_in, *rsrc = a.resid ? a.resid : stand_in;
     float bv = 0.0f, rv = 0.0f;
