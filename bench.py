@@ -207,14 +207,31 @@ def bench_matvec(args, wt, n_out, n_in, n_copies, stacked):
     out_rows = n_out * (n_copies if stacked else 1)
     dout = capi.DeviceBuffer(out_rows * 4)
 
+    def fused_args(m):
+        a = capi.SdyMvArgs(n_tok=1, out=dout.ptr, out_stride=out_rows, row0=0, row1=m.n_rows)
+        a.x, a.eps = dx.ptr, 0.0
+        return a
+
+    # K-quant weights: one launch whose workgroups quantise the f32 row themselves (the reference's
+    # matmul() quantises the activation, then runs the dots); Q8_0: the quantiser's launch, then the
+    # matvec on its bytes
+    fused = wt in (Q4_K, Q6_K) and L.sdy_matvec_fused_ok(ctypes.byref(mats[0].m), ctypes.byref(fused_args(mats[0])),
+                                                          None, None) == 1
+
     def step(i):
-        capi.check(L.sdy_quantize(vt, dx.ptr, dq.ptr, n_in, 1, st))
         m = mats[0] if stacked else mats[i % len(mats)]
+        if fused:
+            capi.check(L.sdy_matvec(ctypes.byref(m.m), ctypes.byref(fused_args(m)), st))
+            return
+        capi.check(L.sdy_quantize(vt, dx.ptr, dq.ptr, n_in, 1, st))
         a = capi.SdyMvArgs(xq=dq.ptr, n_tok=1, out=dout.ptr, out_stride=out_rows, row0=0, row1=m.n_rows)
         capi.check(L.sdy_matvec(ctypes.byref(m.m), ctypes.byref(a), st))
 
     def matvec_only(i):
         m = mats[0] if stacked else mats[i % len(mats)]
+        if fused:
+            capi.check(L.sdy_matvec(ctypes.byref(m.m), ctypes.byref(fused_args(m)), st))
+            return
         a = capi.SdyMvArgs(xq=dq.ptr, n_tok=1, out=dout.ptr, out_stride=out_rows, row0=0, row1=m.n_rows)
         capi.check(L.sdy_matvec(ctypes.byref(m.m), ctypes.byref(a), st))
 
@@ -278,6 +295,7 @@ def bench_matvec(args, wt, n_out, n_in, n_copies, stacked):
         # the same copies as separate n_out x n_in matrices (row views of the stack, each its own region
         # of HBM), one launch per copy, back to back in rotation: per-launch time includes the
         # dispatch gaps that a 2.4 MB matvec cannot hide
+        capi.check(L.sdy_quantize(vt, dx.ptr, dq.ptr, n_in, 1, st))  # (the views read the quantised row)
         views = [L.sdy_mat_rows(ctypes.byref(mats[0].m), c * n_out, n_out) for c in range(n_copies)]
         vargs = capi.SdyMvArgs(xq=dq.ptr, n_tok=1, out=dout.ptr, out_stride=n_out, row0=0, row1=n_out)
 
@@ -332,7 +350,8 @@ def bench_matvec(args, wt, n_out, n_in, n_copies, stacked):
     cfg = {"workload": f"{name} matvec, batch 1, W {n_out}x{n_in}" + (f" x {n_copies} stacked copies" if stacked else
                                                                        f", {n_copies} rotated copies"),
            "weight_type": name, "n_out": n_out, "n_in": n_in, "copies": n_copies,
-           "algorithmic_bytes_per_matvec": algo_bytes}
+           "algorithmic_bytes_per_matvec": algo_bytes,
+           "step": "one launch quantising the f32 row in its workgroups" if fused else "quantiser launch + matvec"}
     line = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "int8 (Q8_K activations x 6-bit weights, int32 dots, f32 combine)"

@@ -674,8 +674,16 @@ static int layers(engine_ctx *c, int n, int out_rows, int decode) {
     }
     if (out_rows > 0) {
         const float *xs = c->x + (size_t)(n - out_rows) * dim;
-        TRY(norm_for(c, xs, m->output_norm, &m->output, out_rows));
-        TRY(mm(c, c->logits_dev, c->xb, &m->output, out_rows, NULL, NULL, 0));
+        /* one row of logits: the head's workgroups normalise and quantise the row themselves (the
+           persistent ring matvec with its norm prologue, the bits of the norm launch + matvec) */
+        const int hrc = out_rows == 1 ? mm1_fused(c, c->logits_dev, xs, m->output_norm, &m->output, NULL, NULL,
+                                                  SDY_EPI_NONE)
+                                      : 1;
+        if (hrc < 0) return hrc;
+        if (hrc) {
+            TRY(norm_for(c, xs, m->output_norm, &m->output, out_rows));
+            TRY(mm(c, c->logits_dev, c->xb, &m->output, out_rows, NULL, NULL, 0));
+        }
     }
     return 0;
 }

@@ -1349,7 +1349,10 @@ __global__ __launch_bounds__(64 * KMAX) void k_moe_down_combine(MvArgs a, const 
 // iterations and the compiler's wait before each iteration's computation covers only that
 // iteration's loads; the slot is refilled right after its computation. Same lane layout and
 // arithmetic as k_matvec_1t (the same bits); no SwiGLU epilogue.
-template <int WT, int NB, int NSB>
+// PRO 1 / 2 (K-quants): the workgroup builds the Q8_K row of the f32 input a.px in LDS
+// (RMS-normalised first for 2: Q8kRow, the bytes k_quant_q8k / k_norm_quant write) after its waves
+// have requested their first NB iterations' weights, which stream meanwhile.
+template <int WT, int NB, int NSB, int PRO = 0>
 __global__ __launch_bounds__(THREADS) void k_matvec_ring(MvArgs a) {
     extern __shared__ uint8_t lds[];
     const int T = a.P.T;
@@ -1365,8 +1368,17 @@ __global__ __launch_bounds__(THREADS) void k_matvec_ring(MvArgs a) {
         stage_acts<WT, 1>(a, lds);
         __syncthreads();
     }
-    if (wid >= a.n_it) return;
-    const int n_my = (a.n_it - wid + S - 1) / S;  // this wave's iterations
+    static_assert(PRO == 0 || is_k(WT), "in-kernel quantisation of K-quant activations only");
+    constexpr int PRO_NR = NSB == 3 ? 1 : NSB == 8 ? 2 : 4;  // the row's super-blocks per wave (nb <= 16)
+    Q8kRow<PRO == 2, PRO_NR, WAVES> arow;
+    if constexpr (PRO) {
+        arow.issue(a.px, a.pnw, a.P.n_in);
+        __builtin_amdgcn_sched_barrier(0);  // (the row's loads stay ahead of the weights')
+    } else {
+        if (wid >= a.n_it) return;
+    }
+    // this wave's iterations (with PRO, waves past them still build the row with the workgroup)
+    const int n_my = wid < a.n_it ? (a.n_it - wid + S - 1) / S : 0;
     const uint32_t le = lane_on ? lane : u, nb = a.P.nb, r0 = (uint32_t)a.row0;
     WRegs<WT> R[NB];
     // iteration i of this wave: rows row0 + (wid + i S) rpi + rl
@@ -1383,7 +1395,12 @@ __global__ __launch_bounds__(THREADS) void k_matvec_ring(MvArgs a) {
     float ydr = 0.0f;
     float2 dxr = make_float2(0.f, 0.f);
     int2 syr = make_int2(0, 0);
-    if constexpr (is_k(WT)) {
+    if constexpr (PRO) {
+#pragma unroll
+        for (int t = 1; t < NB; t++) load_i(t, t);
+        arow.build(a.px, a.peps, a.P.n_in, lds);
+        q8k_unit_lds(lds, nb, u, Yr, bsr, ydr);
+    } else if constexpr (is_k(WT)) {
         const uint8_t *blk = a.xq + __mul24(u >> 2, 292);
         const uint8_t *yb = blk + 4 + 64 * (u & 3);
 #pragma unroll
@@ -1409,8 +1426,10 @@ __global__ __launch_bounds__(THREADS) void k_matvec_ring(MvArgs a) {
             return acc;
         }
     };
+    if constexpr (!PRO) {
 #pragma unroll
-    for (int t = 1; t < NB; t++) load_i(t, t);
+        for (int t = 1; t < NB; t++) load_i(t, t);
+    }
     auto finish = [&](float acc, int i) {  // (no SwiGLU epilogue here)
         const long row = a.row0 + (long)(wid + i * S) * rpi + rl;
         const bool valid = lane_on && row < a.row1;
@@ -2382,30 +2401,31 @@ static int launch_mv_1t(MvArgs &A, hipStream_t st, int n_slot, bool dry = false)
     }
 }
 
-template <int WT, int NB, int NSB>
-static int launch_mv_ring_nsb(MvArgs &A, hipStream_t st) {
+template <int WT, int NB, int NSB, int PRO = 0>
+static int launch_mv_ring_nsb(MvArgs &A, hipStream_t st, bool dry = false) {
     static int per_cu = 0;
     static size_t per_cu_lds = 0;
-    const size_t lds = is_k(WT) ? 0 : mv_lds_bytes_rl(A.P.T, 1);
+    const size_t lds = PRO ? pro_lds(A) : is_k(WT) ? 0 : mv_lds_bytes_rl(A.P.T, 1);
     long wgs = ((long)A.n_it + WAVES - 1) / WAVES;
-    const long cap = resident_wgs((const void *)k_matvec_ring<WT, NB, NSB>, lds, per_cu, per_cu_lds);
+    const long cap = resident_wgs((const void *)k_matvec_ring<WT, NB, NSB, PRO>, lds, per_cu, per_cu_lds);
     if (wgs > cap) wgs = cap;
     if (wgs > 8) wgs &= ~7L;  // a multiple of 8: the XCD-aware numbering applies
-    SDY_NOTE_KERNEL((k_matvec_ring<WT, NB, NSB>));
-    hipLaunchKernelGGL((k_matvec_ring<WT, NB, NSB>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
+    if (dry) return 0;
+    SDY_NOTE_KERNEL((k_matvec_ring<WT, NB, NSB, PRO>));
+    hipLaunchKernelGGL((k_matvec_ring<WT, NB, NSB, PRO>), dim3((unsigned)wgs), dim3(THREADS), lds, st, A);
     return sdy_check_launch("matvec");
 }
 
-// one token, one slot, no in-kernel quantisation: the persistent ring kernel (ring depth measured on
-// the 151936 x 2048 output head: Q6_K 3, Q4_K 2)
-template <int WT>
-static int launch_mv_ring(MvArgs &A, hipStream_t st) {
+// one token, one slot: the persistent ring kernel (ring depth measured on the 151936 x 2048 output
+// head: Q6_K 3, Q4_K 2); PRO 1 / 2 (K-quants): the workgroups quantise the f32 row a.px themselves
+template <int WT, int PRO = 0>
+static int launch_mv_ring(MvArgs &A, hipStream_t st, bool dry = false) {
     constexpr int NB = WT == SDY_Q6_K || WT == SDY_Q8_0 ? 3 : 2;
     prep_1t(A);
     switch (A.P.T) {
-    case 32: return launch_mv_ring_nsb<WT, NB, 8>(A, st);
-    case 64: return launch_mv_ring_nsb<WT, NB, 16>(A, st);
-    default: return launch_mv_ring_nsb<WT, NB, 0>(A, st);
+    case 32: return launch_mv_ring_nsb<WT, NB, 8, PRO>(A, st, dry);
+    case 64: return launch_mv_ring_nsb<WT, NB, 16, PRO>(A, st, dry);
+    default: return launch_mv_ring_nsb<WT, NB, 0, PRO>(A, st, dry);
     }
 }
 
@@ -2673,7 +2693,14 @@ static int fused_launch(const sdy_mat *m, const sdy_mv_args *a, hipStream_t st, 
     ensure_n_cu();
     MvArgs A = rl_args(m, a);
     const bool q4 = m->type == SDY_Q4_K;
-    if (m->n_units <= 64) return q4 ? launch_mv_1t<SDY_Q4_K>(A, st, 1, dry) : launch_mv_1t<SDY_Q6_K>(A, st, 1, dry);
+    if (m->n_units <= 64) {
+        const int rc = q4 ? launch_mv_1t<SDY_Q4_K>(A, st, 1, dry) : launch_mv_1t<SDY_Q6_K>(A, st, 1, dry);
+        if (rc != 1 || A.swiglu) return rc;
+        // too many rows for a grid the GPU holds at once (the output head): the persistent ring
+        // kernel, its workgroups quantising the row themselves
+        if (A.pnw) return q4 ? launch_mv_ring<SDY_Q4_K, 2>(A, st, dry) : launch_mv_ring<SDY_Q6_K, 2>(A, st, dry);
+        return q4 ? launch_mv_ring<SDY_Q4_K, 1>(A, st, dry) : launch_mv_ring<SDY_Q6_K, 1>(A, st, dry);
+    }
     return q4 ? launch_mv_lr<SDY_Q4_K, 1>(A, 0, st, dry) : launch_mv_lr<SDY_Q6_K, 1>(A, 0, st, dry);
 }
 

@@ -535,6 +535,43 @@ def test_matvec_pair_fused_activation(norm):
         assert np.array_equal(bits(r0), bits(r1))
 
 
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("norm", [False, True], ids=["quant", "norm"])
+def test_matvec_ring_fused_activation(kind, norm):
+    """Rows too many for a one-token grid the GPU holds at once (an output head) on the persistent
+    ring kernel whose workgroups build the Q8_K row of the f32 input themselves: the bits of
+    sdy_quantize / sdy_norm_quant followed by sdy_matvec, with a residual."""
+    L = lib()
+    n_in, n_out = 2048, 100003
+    t, w, x, nw = _fused_case(kind, n_in, n_out, 17)
+    eps = 1e-6
+    m = capi.DeviceMatrix(t, n_in, n_out, w)
+    dx, dnw = capi.DeviceBuffer.from_array(x), capi.DeviceBuffer.from_array(nw)
+    extra = capi.DeviceBuffer.from_array(np.random.default_rng(3).standard_normal(n_out).astype(np.float32))
+    dq = capi.DeviceBuffer(n_in // 256 * 292)
+    if norm:
+        capi.check(L.sdy_norm_quant(dx.ptr, dnw.ptr, eps, n_in, 1, None, Q8K_TYPE, dq.ptr, None))
+    else:
+        capi.check(L.sdy_quantize(Q8K_TYPE, dx.ptr, dq.ptr, n_in, 1, None))
+    outs = []
+    for fused in (False, True):
+        dout = capi.DeviceBuffer.from_array(np.full(n_out, np.nan, np.float32))
+        a = capi.SdyMvArgs(n_tok=1, out=dout.ptr, out_stride=n_out, row0=0, row1=n_out, epilogue=capi.EPI_NONE,
+                           resid=extra.ptr)
+        if fused:
+            a.x, a.nw, a.eps = dx.ptr, dnw.ptr if norm else None, eps
+            assert L.sdy_matvec_fused_ok(ctypes.byref(m.m), ctypes.byref(a), None, None) == 1
+        else:
+            a.xq = dq.ptr
+        capi.check(L.sdy_matvec(ctypes.byref(m.m), ctypes.byref(a), None))
+        if fused:
+            assert "k_matvec_ring" in L.sdy_last_kernel().decode()
+        outs.append(dout.to_array(np.float32, n_out))
+    assert not np.isnan(outs[0]).any()
+    assert np.array_equal(bits(outs[1]), bits(outs[0]))
+    m.close()
+
+
 def test_matvec_fused_activation_rejects():
     """Arguments the in-kernel quantisation does not cover are refused (no launch): other weight
     types, several tokens, a misaligned row, RMSNorm of rows above 4096 elements, SwiGLU on long rows."""
