@@ -156,7 +156,9 @@ enum { SDY_EPI_NONE = 0, SDY_EPI_SWIGLU = 1 };
 int sdy_matvec(const sdy_mat *m, const sdy_mv_args *a, sdy_stream s);
 /* 1 when sdy_matvec (and, for two matrices, sdy_matvec_pair) can quantise the f32 row itself for these
  * arguments: one token, Q4_K / Q6_K, 256-element blocks, x (and nw) 16-byte aligned, nw only for
- * rows of at most 4096 elements, and a grid the GPU holds at once. m2/a2 may be NULL. */
+ * rows of at most 4096 elements; a single matrix with more rows than a one-token grid holds at once
+ * (an output head) runs on the persistent ring kernel, except with the SwiGLU epilogue; a pair needs
+ * a grid the GPU holds at once. m2/a2 may be NULL. */
 int sdy_matvec_fused_ok(const sdy_mat *m, const sdy_mv_args *a, const sdy_mat *m2, const sdy_mv_args *a2);
 /* Two one-token matvecs in one launch (each with the bits of sdy_matvec): Q4_K / Q6_K matrices of
  * at most 4096-element rows, e.g. a layer's q|k and a v of another type on the same Q8_K row. */
